@@ -1,0 +1,89 @@
+"""bindcraft2_amd -- MI355X-native AlphaFold2 trunk for BindCraft2.
+
+The product is the C-ABI library ``libbc2n.so`` (declared in
+``include/bc2n.h``), built from the HIP sources in ``csrc/`` for gfx950.
+This package loads it with ctypes and exposes thin torch-tensor wrappers
+(``bindcraft2_amd.ops``) in the shape of the reference's module interface.
+There is no CPU fallback: if the library is missing every op raises.
+"""
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libbc2n.so")
+_lib = None
+
+
+class NativeError(RuntimeError):
+    """A bc2n C-ABI call returned a non-zero status."""
+
+
+def lib():
+    """The loaded libbc2n.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise NativeError(
+                f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'`"
+                " (there is no CPU fallback)")
+        _lib = ctypes.CDLL(LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+def _declare(L):
+    c = ctypes
+    vp, i, f, u32, sz, cs = c.c_void_p, c.c_int, c.c_float, c.c_uint32, c.c_size_t, c.c_char_p
+    L.bc2n_last_error.restype = cs
+    L.bc2n_abi_version.restype = i
+    sigs = {
+        "bc2n_triattn_save_bytes": (sz, [i, i, i]),
+        "bc2n_triattn_fwd": (i, [vp, cs, cs, i, i, vp, vp, vp, vp, vp]),
+        "bc2n_triattn_bwd": (i, [vp, cs, cs, i, i, vp, vp, vp, vp, vp, vp]),
+        "bc2n_dropout_table": (i, [vp, vp, i, i, u32, u32, f]),
+        "bc2n_bernoulli_bits": (i, [vp, vp, c.c_long, u32, u32, f]),
+        "bc2n_stack_keys": (i, [vp, vp, i, vp]),
+        "bc2n_prof_enable": (i, [i]),
+        "bc2n_prof_read": (i, [vp, i, vp, vp, i]),
+        "bc2n_probe_gemm": (i, [vp, i, i, i, vp, vp, vp]),
+        "bc2n_probe_layernorm": (i, [vp, c.c_long, i, vp, vp, vp, i, vp, vp, vp]),
+    }
+    for name, (res, args) in sigs.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+def check(status):
+    """Raise NativeError with the library's message for a non-zero status."""
+    if status != 0:
+        msg = lib().bc2n_last_error().decode(errors="replace")
+        raise NativeError(msg or f"bc2n call failed with status {status}")
+
+
+def exported_symbols():
+    """Names declared in include/bc2n.h (the C ABI)."""
+    import re
+    hdr = os.path.join(os.path.dirname(_HERE), "include", "bc2n.h")
+    with open(hdr) as fh:
+        txt = fh.read()
+    return sorted(set(re.findall(r"\b(bc2n_[a-z0-9_]+)\s*\(", txt)))
+
+
+def prof_enable(on=True):
+    check(lib().bc2n_prof_enable(int(on)))
+
+
+def prof_read(cap=128, name_len=64):
+    """{kernel name: (total ms, launches)} since the last read."""
+    names = ctypes.create_string_buffer(cap * name_len)
+    ms = (ctypes.c_double * cap)()
+    cnt = (ctypes.c_int * cap)()
+    n = lib().bc2n_prof_read(names, name_len, ms, cnt, cap)
+    if n < 0:
+        check(1)
+    out = {}
+    for i in range(n):
+        nm = names.raw[i * name_len:(i + 1) * name_len].split(b"\0", 1)[0].decode()
+        out[nm] = (ms[i], cnt[i])
+    return out

@@ -1,0 +1,106 @@
+// Shared device/host helpers for the gfx950 (CDNA4) trunk kernels.
+//
+// Everything here is written for wave64 and the gfx950 MFMA set; there is no
+// other target.  bf16 is the storage type of GEMM operands, f32 the type of
+// every accumulation, residual carry and softmax statistic.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+namespace bc2n {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr float LN_EPS = 1e-5f;
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float LN2 = 0.6931471805599453f;
+// AF2's attention clip (accel.py LOGIT_CLIP) and mask bias magnitude.
+constexpr float LOGIT_CLIP = 1e8f;
+constexpr float MASK_BIAS = 1e9f;
+
+__device__ __forceinline__ float bf2f(bf16 v) { return (float)v; }
+__device__ __forceinline__ bf16 f2bf(float v) { return (bf16)v; }
+
+__device__ __forceinline__ float sigmoidf_(float x) {
+  return 1.f / (1.f + __expf(-x));
+}
+
+// D += A(16x32) * B(32x16), bf16 operands, f32 accumulation.
+// Lane l: A row l%16, B column l%16, 8 K-slots per lane; D lane l holds
+// column l%16, rows 4*(l/16)+r.  The K-slot -> k mapping is the same for A
+// and B, so any bijection of the 32 k values over (lane group, element) that
+// is applied identically to both operands yields the exact product.
+__device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Wave-level butterfly reductions over groups of lanes.
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+template <int W>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+  for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// 16-byte vector load/store of 8 bf16 values.
+__device__ __forceinline__ bf16x8 ld8(const bf16* p) {
+  return *reinterpret_cast<const bf16x8*>(p);
+}
+__device__ __forceinline__ void st8(bf16* p, bf16x8 v) {
+  *reinterpret_cast<bf16x8*>(p) = v;
+}
+
+// ---------------------------------------------------------------------------
+// JAX threefry2x32-20 (Salmon et al. 2011, Random123), the block cipher under
+// jax.random; used for dropout masks that equal jax.random.bernoulli's.
+__host__ __device__ __forceinline__ uint32_t rotl32(uint32_t v, int d) {
+  return (v << d) | (v >> (32 - d));
+}
+
+__host__ __device__ __forceinline__ void threefry2x32(uint32_t k0, uint32_t k1,
+                                                      uint32_t& x0,
+                                                      uint32_t& x1) {
+  const uint32_t k2 = k0 ^ k1 ^ 0x1BD11BDAu;
+  const uint32_t ks[3] = {k0, k1, k2};
+  x0 += k0;
+  x1 += k1;
+#pragma unroll
+  for (int g = 0; g < 5; ++g) {
+    const int r0 = (g & 1) ? 17 : 13, r1 = (g & 1) ? 29 : 15;
+    const int r2 = (g & 1) ? 16 : 26, r3 = (g & 1) ? 24 : 6;
+    x0 += x1; x1 = rotl32(x1, r0); x1 ^= x0;
+    x0 += x1; x1 = rotl32(x1, r1); x1 ^= x0;
+    x0 += x1; x1 = rotl32(x1, r2); x1 ^= x0;
+    x0 += x1; x1 = rotl32(x1, r3); x1 ^= x0;
+    x0 += ks[(g + 1) % 3];
+    x1 += ks[(g + 2) % 3] + (uint32_t)(g + 1);
+  }
+}
+
+// jax.random.uniform(key, shape, float32) element `idx` (partitionable
+// counters: element i is enciphered as the pair (hi32(i), lo32(i)); the two
+// output words are XORed to one 32-bit draw; 23 mantissa bits make a float in
+// [1,2) from which 1 is subtracted).
+__host__ __device__ __forceinline__ float jax_uniform01(uint32_t k0, uint32_t k1,
+                                                        uint64_t idx) {
+  uint32_t x0 = (uint32_t)(idx >> 32), x1 = (uint32_t)(idx & 0xffffffffu);
+  threefry2x32(k0, k1, x0, x1);
+  const uint32_t bits = x0 ^ x1;
+  const uint32_t fb = (bits >> 9) | 0x3F800000u;
+  float f;
+  __builtin_memcpy(&f, &fb, 4);
+  return f - 1.0f;
+}
+
+}  // namespace bc2n

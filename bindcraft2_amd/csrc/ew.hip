@@ -1,0 +1,129 @@
+// Small elementwise kernels: dropout tables from JAX keys, the JAX key chain of
+// the Evoformer stack, residual/dropout glue of the backward passes.
+#include "kernels.h"
+
+namespace bc2n {
+
+// -------------------------------------------------------------- dropout
+// tbl[b*C+c] = keep ? 1/keep_rate : 0 where keep = uniform(key, (B,C)) < keep_rate
+// and the key (k0,k1) / enable flag are read on the device.
+__global__ void dropout_table_kernel(float* __restrict__ tbl, int B, int C,
+                                     const uint32_t* __restrict__ key,
+                                     const uint32_t* __restrict__ enabled,
+                                     float keep_rate) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long)B * C) return;
+  const bool on = enabled == nullptr || enabled[0] != 0u;
+  if (!on) { tbl[i] = 1.f; return; }
+  const float u = jax_uniform01(key[0], key[1], (uint64_t)i);
+  tbl[i] = (u < keep_rate) ? 1.f / keep_rate : 0.f;
+}
+
+void dropout_table_dev(hipStream_t st, float* tbl, int B, int C,
+                       const uint32_t* key, const uint32_t* enabled, float keep_rate) {
+  const long n = (long)B * C;
+  hipLaunchKernelGGL(dropout_table_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                     tbl, B, C, key, enabled, keep_rate);
+}
+
+__global__ void dropout_table_host_key_kernel(float* __restrict__ tbl, int B, int C,
+                                              uint32_t k0, uint32_t k1, float keep_rate) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long)B * C) return;
+  const float u = jax_uniform01(k0, k1, (uint64_t)i);
+  tbl[i] = (u < keep_rate) ? 1.f / keep_rate : 0.f;
+}
+
+void dropout_table(hipStream_t st, float* tbl, int B, int C, uint32_t k0,
+                   uint32_t k1, float keep_rate) {
+  const long n = (long)B * C;
+  hipLaunchKernelGGL(dropout_table_host_key_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256),
+                     0, st, tbl, B, C, k0, k1, keep_rate);
+}
+
+// Raw keep bits (1 keep, 0 drop) of jax.random.bernoulli(key, keep_rate, (n,)).
+__global__ void bernoulli_bits_kernel(uint8_t* __restrict__ out, long n, uint32_t k0,
+                                      uint32_t k1, float keep_rate) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  out[i] = jax_uniform01(k0, k1, (uint64_t)i) < keep_rate ? 1 : 0;
+}
+
+void bernoulli_bits(hipStream_t st, uint8_t* out, long n, uint32_t k0, uint32_t k1,
+                    float keep_rate) {
+  hipLaunchKernelGGL(bernoulli_bits_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                     out, n, k0, k1, keep_rate);
+}
+
+// -------------------------------------------------------------- key chain
+// The Evoformer stack's per-module keys (modules_multimer.py evoformer_fn and
+// modules.py EvoformerIteration): for each layer, (carry, sub) = split(carry);
+// the block splits `sub` into 10 and hands keys 1..9 to its modules in order.
+// out[(layer*9 + module)*2 + {0,1}].
+// jax.random.split (partitionable): key i = threefry(key, counter (0, i)).
+__device__ __host__ inline void split_key(uint32_t k0, uint32_t k1, int i,
+                                          uint32_t* o0, uint32_t* o1) {
+  uint32_t x0 = 0u, x1 = (uint32_t)i;
+  threefry2x32(k0, k1, x0, x1);
+  *o0 = x0;
+  *o1 = x1;
+}
+
+__global__ void stack_keys_kernel(const uint32_t* __restrict__ seed, int depth,
+                                  uint32_t* __restrict__ out) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  uint32_t c0 = seed[0], c1 = seed[1];
+  for (int l = 0; l < depth; ++l) {
+    uint32_t s0, s1, n0, n1;
+    split_key(c0, c1, 1, &s0, &s1);
+    split_key(c0, c1, 0, &n0, &n1);
+    for (int m = 0; m < 9; ++m) {
+      uint32_t a, b;
+      split_key(s0, s1, m + 1, &a, &b);
+      out[(l * 9 + m) * 2 + 0] = a;
+      out[(l * 9 + m) * 2 + 1] = b;
+    }
+    c0 = n0;
+    c1 = n1;
+  }
+}
+
+void stack_keys(hipStream_t st, const uint32_t* seed, int depth, uint32_t* out) {
+  hipLaunchKernelGGL(stack_keys_kernel, dim3(1), dim3(64), 0, st, seed, depth, out);
+}
+
+// -------------------------------------------------------------- residual glue
+// dd[m][c] = bf16(dy[src(m)][c] * tbl[(m % nt)*C + c])   (tbl may be null)
+__global__ void scale_rows_bf16_kernel(const float* __restrict__ dy, long M, int C,
+                                       int nt, bool transpose,
+                                       const float* __restrict__ tbl,
+                                       bf16* __restrict__ out) {
+  const long i8 = ((long)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  if (i8 >= M * C) return;
+  const long m = i8 / C;
+  const int c0 = (int)(i8 % C);
+  long src = m;
+  if (transpose) src = (m % nt) * nt + m / nt;
+  const float4 a = *reinterpret_cast<const float4*>(dy + src * C + c0);
+  const float4 b = *reinterpret_cast<const float4*>(dy + src * C + c0 + 4);
+  float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  bf16x8 o;
+  if (tbl) {
+    const float* t = tbl + (m % nt) * C + c0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = (bf16)(v[e] * t[e]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = (bf16)v[e];
+  }
+  st8(out + m * C + c0, o);
+}
+
+void scale_rows_bf16(hipStream_t st, const float* dy, long M, int C, int nt,
+                     bool transpose, const float* tbl, bf16* out) {
+  const long n8 = M * C / 8;
+  hipLaunchKernelGGL(scale_rows_bf16_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, st,
+                     dy, M, C, nt, transpose, tbl, out);
+}
+
+}  // namespace bc2n

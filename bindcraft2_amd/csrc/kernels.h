@@ -1,0 +1,82 @@
+// Host-side launchers of the non-template kernels (defined in *.hip files).
+#pragma once
+#include "common.h"
+#include <stdexcept>
+
+namespace bc2n {
+
+// ---------------------------------------------------------------- LayerNorm
+// y[m] = LN(x[src(m)]) with src(m) = m, or (q*nt+p) for m = p*nt+q when nt>0.
+// When H>0, bias_out[h*M+m] = bias_scale * sum_c LN(x)[m][c] * wb[c*H+h].
+void ln_fwd_f32(hipStream_t st, const float* x, long M, int C, int nt,
+                const float* gamma, const float* beta, bf16* y, float* mean,
+                float* rstd, bool fast, int H, const float* wb, float* bias_out,
+                float bias_scale = 1.f);
+// dx[src(m)] (+)= LN-backward(dy[m] + sum_h dbias[h*M+m] * wb[c*H+h]).
+void ln_bwd_f32(hipStream_t st, const float* dy, const float* x, long M, int C,
+                int nt, const float* gamma, const float* mean, const float* rstd,
+                float* dx, bool acc, int H, const float* dbias, const float* wb);
+// Channel-major ([C][M]) input forms used by the triangle multiplication.
+void ln_fwd_cm(hipStream_t st, const float* x, long M, int C, const float* gamma,
+               const float* beta, bf16* y, float* mean, float* rstd, bool fast);
+void ln_bwd_cm(hipStream_t st, const float* dy, const float* x, long M, int C,
+               const float* gamma, const float* mean, const float* rstd, bf16* dx);
+
+// ---------------------------------------------------------------- attention
+// Gated multi-head attention over R independent rows of N tokens, H heads of
+// width D, keys = queries = the N tokens of the row (AF2 Attention with a
+// per-(row,key) mask and an optional per-head [H][N][N] bias shared by rows).
+struct AttnArgs {
+  int R = 0, H = 0, N = 0, D = 32;
+  // q|k|v|g for token t = r*N+i live in row t of `qkvg` (row stride ld):
+  // q at column h*D (pre-scaled by D^-1/2 * log2 e), k at H*D+h*D,
+  // v at 2*H*D+h*D, gate pre-activation at 3*H*D+h*D.
+  const bf16* qkvg = nullptr;
+  long ld = 0;
+  const float* mask = nullptr;  // mask[r*mask_sr + k*mask_sk], binary 0/1
+  long mask_sr = 0, mask_sk = 0;
+  const float* bias = nullptr;  // [H][N][N], log2 domain, or null
+  bf16* o = nullptr;            // ungated output [R*N][H*D]
+  bf16* og = nullptr;           // sigmoid(g) * o   [R*N][H*D]
+  long ldo = 0;
+  float* lse = nullptr;         // [R][H][N], log2 domain
+};
+void attn_fwd(hipStream_t st, const AttnArgs& a);
+
+struct AttnBwdArgs {
+  AttnArgs f;                  // forward operands (o, lse read back)
+  const bf16* dog = nullptr;   // upstream gradient of og [R*N][H*D]
+  bf16* dO = nullptr;          // scratch: dL/do [R*N][H*D]
+  float* Dsum = nullptr;       // scratch: [R][H][N] rowsum(dO*o)
+  bf16* dqkvg = nullptr;       // out: dq|dk|dv|dg with the layout of qkvg
+  float* dbias_part = nullptr; // scratch: [nchunk][H][N][N]
+  float* dbias = nullptr;      // out: [H][N][N] (natural units), or null
+  float scale = 1.f;           // D^-1/2 (q scaling applied in the forward)
+  int rows_per_chunk = 8;
+};
+void attn_bwd(hipStream_t st, const AttnBwdArgs& a);
+int attn_bwd_nchunk(int R, int rows_per_chunk);
+
+// ---------------------------------------------------------------- dropout
+// Shared-dropout keep/scale table for one module: tbl[b*C+c] = keep/keep_rate
+// (0 where dropped), with keep = jax.random.uniform(key,(B,C)) < keep_rate.
+void dropout_table(hipStream_t st, float* tbl, int B, int C, uint32_t k0,
+                   uint32_t k1, float keep_rate);
+// Same with the key (2 x u32) and the enable flag (u32, may be null) in device
+// memory; a disabled flag gives an all-ones table (rate 0).
+void dropout_table_dev(hipStream_t st, float* tbl, int B, int C,
+                       const uint32_t* key, const uint32_t* enabled, float keep_rate);
+// out[i] = jax.random.bernoulli(key, keep_rate, (n,))[i].
+void bernoulli_bits(hipStream_t st, uint8_t* out, long n, uint32_t k0, uint32_t k1,
+                    float keep_rate);
+// Per-module keys of a `depth`-layer Evoformer stack from the stack key
+// seed[0..1]: out[(layer*9+module)*2 + {0,1}].
+void stack_keys(hipStream_t st, const uint32_t* seed, int depth, uint32_t* out);
+
+// ---------------------------------------------------------------- glue
+// out[m][c] = bf16(dy[src(m)][c] * tbl[(m % nt)*C + c]); src transposes the
+// N x N grid when `transpose`; tbl may be null (no dropout).
+void scale_rows_bf16(hipStream_t st, const float* dy, long M, int C, int nt,
+                     bool transpose, const float* tbl, bf16* out);
+
+}  // namespace bc2n

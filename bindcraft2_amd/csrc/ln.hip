@@ -1,0 +1,326 @@
+// LayerNorm forward/backward over the channel axis, bandwidth kernels.
+//
+// A row of C channels is held by C/8 consecutive lanes, 8 channels each, so a
+// 256-thread block normalises 2048/C rows with no LDS and no block barrier;
+// both reductions are butterflies inside the lane group.  Variance is either
+// two-pass (mean of squared deviations; haiku's default) or the "fast" form
+// E[x^2]-E[x]^2 that AF2's fused triangle multiplication asks for.
+//
+// Options used by the trunk:
+//  * transposed read: output row (p,q) normalises input row (q,p) of an
+//    N x N grid -- the "ending node"/"per column" orientation without a copy;
+//  * fused pair-bias projection: bias[h][row] = sum_c y[c] * W[c][h] from the
+//    f32 normalised row (triangle attention / MSA row attention bias);
+//  * channel-major input (trimul's centre norm), staged through LDS.
+#include "kernels.h"
+
+namespace bc2n {
+
+template <int C>
+struct LnGeom {
+  static constexpr int TPR = C / 8;         // lanes per row
+  static constexpr int RPB = 256 / TPR;     // rows per block
+};
+
+template <class T>
+__device__ __forceinline__ void load8f(const T* p, float (&v)[8]);
+template <>
+__device__ __forceinline__ void load8f<float>(const float* p, float (&v)[8]) {
+  const float4 a = reinterpret_cast<const float4*>(p)[0];
+  const float4 b = reinterpret_cast<const float4*>(p)[1];
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+template <>
+__device__ __forceinline__ void load8f<bf16>(const bf16* p, float (&v)[8]) {
+  const bf16x8 a = ld8(p);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = (float)a[e];
+}
+
+__device__ __forceinline__ long ln_src_row(long m, int nt) {
+  if (nt <= 0) return m;
+  const long p = m / nt, q = m % nt;
+  return q * nt + p;
+}
+
+template <int C, bool FAST, class InT>
+__global__ __launch_bounds__(256) void ln_fwd_kernel(
+    const InT* __restrict__ x, long M, int nt, const float* __restrict__ gamma,
+    const float* __restrict__ beta, bf16* __restrict__ y,
+    float* __restrict__ mean_out, float* __restrict__ rstd_out, int H,
+    const float* __restrict__ wb, float* __restrict__ bias_out, float bias_scale) {
+  using G = LnGeom<C>;
+  const int t = threadIdx.x;
+  const long m = (long)blockIdx.x * G::RPB + t / G::TPR;
+  const int c0 = (t % G::TPR) * 8;
+  if (m >= M) return;  // whole lane groups exit together
+  float v[8];
+  load8f<InT>(x + ln_src_row(m, nt) * C + c0, v);
+  float s = 0.f, s2 = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) { s += v[e]; s2 += v[e] * v[e]; }
+  s = group_sum<G::TPR>(s);
+  const float mu = s / C;
+  float var;
+  if (FAST) {
+    s2 = group_sum<G::TPR>(s2);
+    var = s2 / C - mu * mu;
+  } else {
+    float d2 = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) { const float d = v[e] - mu; d2 += d * d; }
+    var = group_sum<G::TPR>(d2) / C;
+  }
+  const float r = rsqrtf(var + LN_EPS);
+  float o[8];
+  bf16x8 ob;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    o[e] = (v[e] - mu) * r * gamma[c0 + e] + beta[c0 + e];
+    ob[e] = (bf16)o[e];
+  }
+  if (y) st8(y + m * C + c0, ob);
+  if (t % G::TPR == 0) {
+    if (mean_out) mean_out[m] = mu;
+    if (rstd_out) rstd_out[m] = r;
+  }
+  for (int h = 0; h < H; ++h) {
+    float p = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) p += o[e] * wb[(c0 + e) * H + h];
+    p = group_sum<G::TPR>(p);
+    if (t % G::TPR == 0) bias_out[(long)h * M + m] = p * bias_scale;
+  }
+}
+
+// dx[src(m)] (+)= LN'(dy[m] + sum_h dbias[h][m] W[c][h])
+template <int C, class InT, bool ACC>
+__global__ __launch_bounds__(256) void ln_bwd_kernel(
+    const float* __restrict__ dy, const InT* __restrict__ x, long M, int nt,
+    const float* __restrict__ gamma, const float* __restrict__ mean,
+    const float* __restrict__ rstd, float* __restrict__ dx, int H,
+    const float* __restrict__ dbias, const float* __restrict__ wb) {
+  using G = LnGeom<C>;
+  const int t = threadIdx.x;
+  const long m = (long)blockIdx.x * G::RPB + t / G::TPR;
+  const int c0 = (t % G::TPR) * 8;
+  if (m >= M) return;
+  const long src = ln_src_row(m, nt);
+  float xv[8], g[8];
+  load8f<InT>(x + src * C + c0, xv);
+  load8f<float>(dy + m * C + c0, g);
+  for (int h = 0; h < H; ++h) {
+    const float db = dbias[(long)h * M + m];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) g[e] += db * wb[(c0 + e) * H + h];
+  }
+  const float mu = mean[m], r = rstd[m];
+  float sg = 0.f, sgx = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    xv[e] = (xv[e] - mu) * r;
+    g[e] *= gamma[c0 + e];
+    sg += g[e];
+    sgx += g[e] * xv[e];
+  }
+  sg = group_sum<G::TPR>(sg) / C;
+  sgx = group_sum<G::TPR>(sgx) / C;
+  float* out = dx + src * C + c0;
+  float4 a, b;
+  float res[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) res[e] = r * (g[e] - sg - xv[e] * sgx);
+  if (ACC) {
+    a = reinterpret_cast<float4*>(out)[0];
+    b = reinterpret_cast<float4*>(out)[1];
+    a.x += res[0]; a.y += res[1]; a.z += res[2]; a.w += res[3];
+    b.x += res[4]; b.y += res[5]; b.z += res[6]; b.w += res[7];
+  } else {
+    a = make_float4(res[0], res[1], res[2], res[3]);
+    b = make_float4(res[4], res[5], res[6], res[7]);
+  }
+  reinterpret_cast<float4*>(out)[0] = a;
+  reinterpret_cast<float4*>(out)[1] = b;
+}
+
+// Channel-major input: x is [C][M] (one plane per channel).  A block of 64
+// rows stages the [C][64] tile through LDS and then runs the row-wise
+// normaliser on it; the output is row-major [M][C] bf16.
+template <int C, bool FAST>
+__global__ __launch_bounds__(256) void ln_fwd_cm_kernel(
+    const float* __restrict__ x, long M, const float* __restrict__ gamma,
+    const float* __restrict__ beta, bf16* __restrict__ y,
+    float* __restrict__ mean_out, float* __restrict__ rstd_out) {
+  constexpr int R = 64;
+  __shared__ float tile[R][C + 1];
+  const int t = threadIdx.x;
+  const long m0 = (long)blockIdx.x * R;
+  for (int i = t; i < C * R; i += 256) {
+    const int c = i / R, r = i % R;
+    const long m = m0 + r;
+    tile[r][c] = (m < M) ? x[(long)c * M + m] : 0.f;
+  }
+  __syncthreads();
+  // 4 lanes per row, C/4 channels per lane
+  constexpr int CPL = C / 4;
+  const int r = t / 4, part = t % 4;
+  const long m = m0 + r;
+  float v[CPL];
+  float s = 0.f, s2 = 0.f;
+#pragma unroll
+  for (int e = 0; e < CPL; ++e) {
+    v[e] = tile[r][part * CPL + e];
+    s += v[e];
+    s2 += v[e] * v[e];
+  }
+  s = group_sum<4>(s);
+  const float mu = s / C;
+  float var;
+  if (FAST) {
+    var = group_sum<4>(s2) / C - mu * mu;
+  } else {
+    float d2 = 0.f;
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) { const float d = v[e] - mu; d2 += d * d; }
+    var = group_sum<4>(d2) / C;
+  }
+  const float rs = rsqrtf(var + LN_EPS);
+  if (m < M) {
+#pragma unroll
+    for (int e0 = 0; e0 < CPL; e0 += 8) {
+      bf16x8 ob;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int c = part * CPL + e0 + e;
+        ob[e] = (bf16)((v[e0 + e] - mu) * rs * gamma[c] + beta[c]);
+      }
+      st8(y + m * C + part * CPL + e0, ob);
+    }
+    if (part == 0) { mean_out[m] = mu; rstd_out[m] = rs; }
+  }
+}
+
+// Backward of the channel-major norm: dy row-major [M][C] f32, x channel-major
+// [C][M] f32; writes dx channel-major [C][M] as bf16 (a GEMM operand).
+template <int C>
+__global__ __launch_bounds__(256) void ln_bwd_cm_kernel(
+    const float* __restrict__ dy, const float* __restrict__ x, long M,
+    const float* __restrict__ gamma, const float* __restrict__ mean,
+    const float* __restrict__ rstd, bf16* __restrict__ dx) {
+  constexpr int R = 64;
+  __shared__ float tile[R][C + 1];
+  const int t = threadIdx.x;
+  const long m0 = (long)blockIdx.x * R;
+  for (int i = t; i < C * R; i += 256) {
+    const int c = i / R, r = i % R;
+    const long m = m0 + r;
+    tile[r][c] = (m < M) ? x[(long)c * M + m] : 0.f;
+  }
+  __syncthreads();
+  constexpr int CPL = C / 4;
+  const int r = t / 4, part = t % 4;
+  const long m = m0 + r;
+  const float mu = (m < M) ? mean[m] : 0.f, rs = (m < M) ? rstd[m] : 0.f;
+  float xh[CPL], g[CPL];
+  float sg = 0.f, sgx = 0.f;
+#pragma unroll
+  for (int e = 0; e < CPL; ++e) {
+    const int c = part * CPL + e;
+    xh[e] = (tile[r][c] - mu) * rs;
+    g[e] = (m < M) ? dy[m * C + c] * gamma[c] : 0.f;
+    sg += g[e];
+    sgx += g[e] * xh[e];
+  }
+  sg = group_sum<4>(sg) / C;
+  sgx = group_sum<4>(sgx) / C;
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < CPL; ++e) {
+    const int c = part * CPL + e;
+    tile[r][c] = rs * (g[e] - sg - xh[e] * sgx);
+  }
+  __syncthreads();
+  for (int i = t; i < C * R; i += 256) {
+    const int c = i / R, rr = i % R;
+    const long mm = m0 + rr;
+    if (mm < M) dx[(long)c * M + mm] = (bf16)tile[rr][c];
+  }
+}
+
+// ------------------------------------------------------------------ launchers
+
+template <int C, class InT>
+static void ln_fwd_dispatch(hipStream_t st, const InT* x, long M, int nt,
+                            const float* gamma, const float* beta, bf16* y,
+                            float* mean, float* rstd, bool fast, int H,
+                            const float* wb, float* bias_out, float bs) {
+  const int grid = (int)((M + LnGeom<C>::RPB - 1) / LnGeom<C>::RPB);
+  if (fast)
+    hipLaunchKernelGGL((ln_fwd_kernel<C, true, InT>), dim3(grid), dim3(256), 0, st,
+                       x, M, nt, gamma, beta, y, mean, rstd, H, wb, bias_out, bs);
+  else
+    hipLaunchKernelGGL((ln_fwd_kernel<C, false, InT>), dim3(grid), dim3(256), 0, st,
+                       x, M, nt, gamma, beta, y, mean, rstd, H, wb, bias_out, bs);
+}
+
+void ln_fwd_f32(hipStream_t st, const float* x, long M, int C, int nt,
+                const float* gamma, const float* beta, bf16* y, float* mean,
+                float* rstd, bool fast, int H, const float* wb, float* bias_out,
+                float bs) {
+  switch (C) {
+    case 64: ln_fwd_dispatch<64>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, H, wb, bias_out, bs); break;
+    case 128: ln_fwd_dispatch<128>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, H, wb, bias_out, bs); break;
+    case 256: ln_fwd_dispatch<256>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, H, wb, bias_out, bs); break;
+    default: throw std::runtime_error("ln_fwd: unsupported channel count");
+  }
+}
+
+template <int C>
+static void ln_bwd_dispatch(hipStream_t st, const float* dy, const float* x, long M,
+                            int nt, const float* gamma, const float* mean,
+                            const float* rstd, float* dx, bool acc, int H,
+                            const float* dbias, const float* wb) {
+  const int grid = (int)((M + LnGeom<C>::RPB - 1) / LnGeom<C>::RPB);
+  if (acc)
+    hipLaunchKernelGGL((ln_bwd_kernel<C, float, true>), dim3(grid), dim3(256), 0, st,
+                       dy, x, M, nt, gamma, mean, rstd, dx, H, dbias, wb);
+  else
+    hipLaunchKernelGGL((ln_bwd_kernel<C, float, false>), dim3(grid), dim3(256), 0, st,
+                       dy, x, M, nt, gamma, mean, rstd, dx, H, dbias, wb);
+}
+
+void ln_bwd_f32(hipStream_t st, const float* dy, const float* x, long M, int C,
+                int nt, const float* gamma, const float* mean, const float* rstd,
+                float* dx, bool acc, int H, const float* dbias, const float* wb) {
+  switch (C) {
+    case 64: ln_bwd_dispatch<64>(st, dy, x, M, nt, gamma, mean, rstd, dx, acc, H, dbias, wb); break;
+    case 128: ln_bwd_dispatch<128>(st, dy, x, M, nt, gamma, mean, rstd, dx, acc, H, dbias, wb); break;
+    case 256: ln_bwd_dispatch<256>(st, dy, x, M, nt, gamma, mean, rstd, dx, acc, H, dbias, wb); break;
+    default: throw std::runtime_error("ln_bwd: unsupported channel count");
+  }
+}
+
+void ln_fwd_cm(hipStream_t st, const float* x, long M, int C, const float* gamma,
+               const float* beta, bf16* y, float* mean, float* rstd, bool fast) {
+  const int grid = (int)((M + 63) / 64);
+  if (C == 128) {
+    if (fast) hipLaunchKernelGGL((ln_fwd_cm_kernel<128, true>), dim3(grid), dim3(256), 0, st, x, M, gamma, beta, y, mean, rstd);
+    else hipLaunchKernelGGL((ln_fwd_cm_kernel<128, false>), dim3(grid), dim3(256), 0, st, x, M, gamma, beta, y, mean, rstd);
+  } else if (C == 64) {
+    if (fast) hipLaunchKernelGGL((ln_fwd_cm_kernel<64, true>), dim3(grid), dim3(256), 0, st, x, M, gamma, beta, y, mean, rstd);
+    else hipLaunchKernelGGL((ln_fwd_cm_kernel<64, false>), dim3(grid), dim3(256), 0, st, x, M, gamma, beta, y, mean, rstd);
+  } else {
+    throw std::runtime_error("ln_fwd_cm: unsupported channel count");
+  }
+}
+
+void ln_bwd_cm(hipStream_t st, const float* dy, const float* x, long M, int C,
+               const float* gamma, const float* mean, const float* rstd, bf16* dx) {
+  const int grid = (int)((M + 63) / 64);
+  if (C == 128) hipLaunchKernelGGL((ln_bwd_cm_kernel<128>), dim3(grid), dim3(256), 0, st, dy, x, M, gamma, mean, rstd, dx);
+  else if (C == 64) hipLaunchKernelGGL((ln_bwd_cm_kernel<64>), dim3(grid), dim3(256), 0, st, dy, x, M, gamma, mean, rstd, dx);
+  else throw std::runtime_error("ln_bwd_cm: unsupported channel count");
+}
+
+}  // namespace bc2n

@@ -1,0 +1,141 @@
+// Host runtime: weights manifests, device weight forms, scratch arena and the
+// status-code error channel of the C ABI.
+#pragma once
+#include "common.h"
+#include <map>
+#include <memory>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+namespace bc2n {
+
+struct HipError : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+
+void hip_check(hipError_t e, const char* what);
+#define BC2N_HIP(x) ::bc2n::hip_check((x), #x)
+
+// One tensor of a weights manifest: `name file ndim d0 d1 ...` + raw LE f32.
+struct HostTensor {
+  std::vector<int> shape;
+  std::vector<float> data;
+  size_t size() const { return data.size(); }
+};
+
+// A weights directory as written by the reference's manifest writer
+// (bindcraft/af/native.py weights_from_params): manifest.txt plus one .f32
+// file per parameter, names param/block{b}/<module path>/<param>.  Device
+// forms (f32 copies, transposed bf16 GEMM operands) are built on first use
+// and kept for the life of the process.
+class WeightStore {
+ public:
+  explicit WeightStore(const std::string& dir);
+  bool has(const std::string& name) const { return host_.count(name) != 0; }
+  const HostTensor& host(const std::string& name) const;
+  // f32 copy on the device.
+  const float* f32(const std::string& name);
+  // A device buffer built once from host data by `make` under cache key `key`.
+  template <class T, class F>
+  const T* derived(const std::string& key, F make) {
+    std::lock_guard<std::mutex> lk(mu_);
+    auto it = dev_.find(key);
+    if (it != dev_.end()) return reinterpret_cast<const T*>(it->second);
+    std::vector<T> h = make();
+    void* d = upload(h.data(), h.size() * sizeof(T));
+    dev_[key] = d;
+    return reinterpret_cast<const T*>(d);
+  }
+  const std::string& dir() const { return dir_; }
+
+ private:
+  void* upload(const void* src, size_t bytes);
+  std::string dir_;
+  std::map<std::string, HostTensor> host_;
+  std::map<std::string, void*> dev_;
+  std::mutex mu_;
+};
+
+// Process-wide cache of weight stores keyed by directory.
+WeightStore& weights(const std::string& dir);
+
+// Host-side conversions used to build GEMM operands.
+std::vector<bf16> to_bf16(const std::vector<float>& v);
+// [rows][cols] f32 -> [cols][rows] bf16
+std::vector<bf16> transpose_bf16(const float* src, int rows, int cols);
+
+// Grow-only device scratch arena, carved by bump allocation per call.  One
+// arena per device; callers hold `lock()` for the duration of a call.
+class Arena {
+ public:
+  void reset(hipStream_t st, size_t need);
+  void* take(size_t bytes);
+  template <class T>
+  T* take_n(size_t n) { return reinterpret_cast<T*>(take(n * sizeof(T))); }
+  std::recursive_mutex& lock() { return mu_; }
+
+ private:
+  char* base_ = nullptr;
+  size_t cap_ = 0, off_ = 0;
+  std::recursive_mutex mu_;
+};
+Arena& arena();
+
+// Per-kernel device timing: when enabled, every launch site wrapped in
+// KTimed records a HIP event pair on its own stream; kprof_read() syncs the
+// events and returns per-name totals.  Off by default (no events recorded).
+void kprof_enable(bool on);
+bool kprof_on();
+void kprof_record(const char* name, hipEvent_t a, hipEvent_t b);
+hipEvent_t kprof_event();
+// Fills names/ms/counts (up to cap entries), returns the number of entries,
+// and clears the records.
+int kprof_read(char* names, int name_len, double* ms, int* counts, int cap);
+
+struct KTimed {
+  const char* name;
+  hipStream_t st;
+  hipEvent_t a = nullptr;
+  KTimed(const char* n, hipStream_t s) : name(n), st(s) {
+    if (kprof_on()) {
+      a = kprof_event();
+      hip_check(hipEventRecord(a, st), "hipEventRecord");
+    }
+  }
+  ~KTimed() {
+    if (a) {
+      hipEvent_t b = kprof_event();
+      if (hipEventRecord(b, st) == hipSuccess) kprof_record(name, a, b);
+    }
+  }
+};
+
+// Thread-local last error message of the C ABI.
+void set_error(const std::string& msg);
+const char* last_error();
+
+// Sequential carve of a caller-owned buffer (save-sets).
+struct Carver {
+  char* p;
+  size_t off = 0;
+  explicit Carver(void* base) : p(reinterpret_cast<char*>(base)) {}
+  template <class T>
+  T* take(size_t n) {
+    T* r = reinterpret_cast<T*>(p + off);
+    off += (n * sizeof(T) + 255) & ~size_t(255);
+    return r;
+  }
+};
+// The same walk, counting bytes only.
+struct Sizer {
+  size_t off = 0;
+  template <class T>
+  T* take(size_t n) {
+    off += (n * sizeof(T) + 255) & ~size_t(255);
+    return nullptr;
+  }
+};
+
+}  // namespace bc2n

@@ -1,0 +1,252 @@
+// Triangle attention (starting / ending node), forward and backward.
+//
+// Forward, in the module's frame (the transposed pair for the ending node):
+//   LN (two-pass) + fused pair-bias projection  -> xn bf16, bias[H][M] (log2 e)
+//   GEMM xn . [Wq|Wk|Wv|Wg]  (q scaled by D^-1/2 log2 e, +gating_b)  -> qkvg
+//   flash attention (mask per row/key, bias per head)               -> o, og, lse
+//   GEMM og . Wo + bo, fused residual + shared dropout (+ transposed write)
+// Backward replays nothing: the save-set holds LN stats, bias, qkvg, o, lse.
+//   dd = tbl * dout                       (transposed read for ending node)
+//   GEMM dd . Wo^T                        -> d(og)
+//   attention backward                    -> dq|dk|dv|dg, d(bias)
+//   GEMM dqkvg . [Wq|Wk|Wv|Wg]^T          -> d(xn)
+//   LN backward (+ d(bias) . W2d^T) accumulated into din
+// Reference: modules.py:675-734 (TriangleAttention), :313-400 (Attention),
+// accel.py:13-24 (logit clip); native/triattn_body.cuh:647-1488 (TriAttn).
+#include "gemm.h"
+#include "modules.h"
+#include <cmath>
+
+namespace bc2n {
+
+namespace {
+
+// qkvg epilogue: bf16 store with per-column bias and the q-column scale.
+struct EpiQKVG {
+  bf16* C;
+  long ldc;
+  const float* bias;
+  float qscale;
+  int qcols, N;
+  template <int TN>
+  __device__ __forceinline__ void apply(int, int m, int n, const float (&v)[TN]) const {
+    bf16* row = C + (long)m * ldc;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int c = n + 16 * j;
+      if (c >= N) continue;
+      float x = v[j] + bias[c];
+      if (c < qcols) x *= qscale;
+      row[c] = (bf16)x;
+    }
+  }
+};
+
+// out[src(m)] = in[src(m)] + tbl[(m % nt)*C + c] * (acc + bias[c])
+struct EpiResidual {
+  const float* in;
+  float* out;
+  const float* bias;
+  const float* tbl;  // may be null
+  int nt, C;
+  bool transpose;
+  template <int TN>
+  __device__ __forceinline__ void apply(int, int m, int n, const float (&v)[TN]) const {
+    const long src = transpose ? (long)(m % nt) * nt + m / nt : m;
+    const float* t = tbl ? tbl + (long)(m % nt) * C : nullptr;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int c = n + 16 * j;
+      if (c >= C) continue;
+      float x = v[j] + bias[c];
+      if (t) x *= t[c];
+      out[src * C + c] = in[src * C + c] + x;
+    }
+  }
+};
+
+template <class A>
+struct TriAttnSave {
+  float *mean, *rstd, *bias, *lse;
+  bf16 *qkvg, *o;
+  TriAttnSave(A& a, int N, int C, int H) {
+    const size_t M = (size_t)N * N;
+    mean = a.template take<float>(M);
+    rstd = a.template take<float>(M);
+    bias = a.template take<float>((size_t)H * M);
+    lse = a.template take<float>((size_t)H * M);
+    qkvg = a.template take<bf16>(M * 4 * C);
+    o = a.template take<bf16>(M * C);
+  }
+};
+
+}  // namespace
+
+TriAttnW triattn_weights(WeightStore& ws, const std::string& P) {
+  TriAttnW w;
+  const HostTensor& qw = ws.host(P + "attention/query_w");
+  if (qw.shape.size() != 3) throw std::runtime_error("triattn: query_w must be [C,H,D]");
+  w.C = qw.shape[0];
+  w.H = qw.shape[1];
+  w.D = qw.shape[2];
+  const int C = w.C, HD = w.H * w.D;
+  if (HD != C) throw std::runtime_error("triattn: H*D must equal C");
+  w.ln_g = ws.f32(P + "query_norm/scale");
+  w.ln_b = ws.f32(P + "query_norm/offset");
+  w.w2d = ws.f32(P + "feat_2d_weights");
+  const char* parts[4] = {"attention/query_w", "attention/key_w", "attention/value_w",
+                          "attention/gating_w"};
+  auto cat = [&]() {
+    std::vector<float> c((size_t)C * 4 * HD);
+    for (int p = 0; p < 4; ++p) {
+      const HostTensor& t = ws.host(P + parts[p]);
+      for (int r = 0; r < C; ++r)
+        for (int j = 0; j < HD; ++j) c[(size_t)r * 4 * HD + p * HD + j] = t.data[(size_t)r * HD + j];
+    }
+    return c;
+  };
+  w.wqkvg = ws.derived<bf16>("triattn.wqkvg:" + P, [&] { return to_bf16(cat()); });
+  w.wqkvg_t = ws.derived<bf16>("triattn.wqkvg_t:" + P, [&] {
+    std::vector<float> c = cat();
+    return transpose_bf16(c.data(), C, 4 * HD);
+  });
+  w.bqkvg = ws.derived<float>("triattn.bqkvg:" + P, [&] {
+    std::vector<float> b((size_t)4 * HD, 0.f);
+    const HostTensor& gb = ws.host(P + "attention/gating_b");
+    for (int j = 0; j < HD; ++j) b[3 * HD + j] = gb.data[j];
+    return b;
+  });
+  const HostTensor& ow = ws.host(P + "attention/output_w");  // [H,D,C]
+  w.wo = ws.derived<bf16>("triattn.wo:" + P, [&] { return to_bf16(ow.data); });
+  w.wo_t = ws.derived<bf16>("triattn.wo_t:" + P, [&] { return transpose_bf16(ow.data.data(), HD, C); });
+  w.bo = ws.f32(P + "attention/output_b");
+  return w;
+}
+
+size_t triattn_save_bytes(int N, int C, int H) {
+  Sizer s;
+  TriAttnSave<Sizer> plan(s, N, C, H);
+  (void)plan;
+  return s.off;
+}
+
+static void triattn_check(const TriAttnW& w, int N) {
+  if (N <= 0 || N % 32 != 0) throw std::runtime_error("triattn: N must be a positive multiple of 32");
+  if (w.D != 32) throw std::runtime_error("triattn: head width 32 only");
+}
+
+void triattn_fwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
+                 const float* pair_in, const float* mask, const float* tbl,
+                 float* pair_out, void* save) {
+  triattn_check(w, N);
+  const int C = w.C, H = w.H, HD = w.H * w.D;
+  const long M = (long)N * N;
+  Carver cv(save);
+  TriAttnSave<Carver> sv(cv, N, C, H);
+  Arena& ar = arena();
+  std::lock_guard<std::recursive_mutex> lk(ar.lock());
+  ar.reset(st, (size_t)M * C * 2 + (size_t)M * HD * 2 + 1024);
+  bf16* xn = ar.take_n<bf16>((size_t)M * C);
+  bf16* og = ar.take_n<bf16>((size_t)M * HD);
+
+  {
+    KTimed kt("triattn.ln_fwd", st);
+    ln_fwd_f32(st, pair_in, M, C, per_column ? N : 0, w.ln_g, w.ln_b, xn, sv.mean, sv.rstd,
+               false, H, w.w2d, sv.bias, LOG2E);
+  }
+  GemmArgs g1;
+  g1.M = (int)M; g1.N = 4 * HD; g1.K = C;
+  g1.A = xn; g1.a_sm = C; g1.a_sk = 1;
+  g1.B = w.wqkvg_t; g1.b_sn = C; g1.b_sk = 1;
+  const float qscale = LOG2E / std::sqrt((float)w.D);
+  gemm<128, 128>(st, g1, EpiQKVG{sv.qkvg, 4L * HD, w.bqkvg, qscale, HD, 4 * HD},
+                 "triattn.gemm_qkvg");
+
+  AttnArgs a;
+  a.R = N; a.H = H; a.N = N; a.D = w.D;
+  a.qkvg = sv.qkvg; a.ld = 4L * HD;
+  a.mask = mask;
+  a.mask_sr = per_column ? 1 : N;
+  a.mask_sk = per_column ? N : 1;
+  a.bias = sv.bias;
+  a.o = sv.o; a.og = og; a.ldo = HD;
+  a.lse = sv.lse;
+  attn_fwd(st, a);
+
+  GemmArgs g2;
+  g2.M = (int)M; g2.N = C; g2.K = HD;
+  g2.A = og; g2.a_sm = HD; g2.a_sk = 1;
+  g2.B = w.wo_t; g2.b_sn = HD; g2.b_sk = 1;
+  gemm<128, 128>(st, g2, EpiResidual{pair_in, pair_out, w.bo, tbl, N, C, per_column},
+                 "triattn.gemm_out");
+}
+
+void triattn_bwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
+                 const float* pair_in, const float* mask, const float* tbl,
+                 const void* save, const float* dout, float* din) {
+  triattn_check(w, N);
+  const int C = w.C, H = w.H, HD = w.H * w.D;
+  const long M = (long)N * N;
+  Carver cv(const_cast<void*>(save));
+  TriAttnSave<Carver> sv(cv, N, C, H);
+  AttnBwdArgs b;
+  b.rows_per_chunk = 8;
+  const int nch = attn_bwd_nchunk(N, b.rows_per_chunk);
+  Arena& ar = arena();
+  std::lock_guard<std::recursive_mutex> lk(ar.lock());
+  Sizer need;
+  need.take<bf16>((size_t)M * C);            // dd
+  need.take<bf16>((size_t)M * HD);           // dog
+  need.take<bf16>((size_t)M * HD);           // dO
+  need.take<float>((size_t)H * M);           // Dsum
+  need.take<bf16>((size_t)M * 4 * HD);       // dqkvg
+  need.take<float>((size_t)nch * H * M);     // dbias partials
+  need.take<float>((size_t)H * M);           // dbias
+  need.take<float>((size_t)M * C);           // dxn
+  ar.reset(st, need.off);
+  bf16* dd = ar.take_n<bf16>((size_t)M * C);
+  bf16* dog = ar.take_n<bf16>((size_t)M * HD);
+  b.dO = ar.take_n<bf16>((size_t)M * HD);
+  b.Dsum = ar.take_n<float>((size_t)H * M);
+  b.dqkvg = ar.take_n<bf16>((size_t)M * 4 * HD);
+  b.dbias_part = ar.take_n<float>((size_t)nch * H * M);
+  b.dbias = ar.take_n<float>((size_t)H * M);
+  float* dxn = ar.take_n<float>((size_t)M * C);
+
+  {
+    KTimed kt("triattn.dropout_bwd", st);
+    scale_rows_bf16(st, dout, M, C, N, per_column, tbl, dd);
+  }
+  GemmArgs g1;
+  g1.M = (int)M; g1.N = HD; g1.K = C;
+  g1.A = dd; g1.a_sm = C; g1.a_sk = 1;
+  g1.B = w.wo; g1.b_sn = C; g1.b_sk = 1;
+  gemm<128, 128>(st, g1, EpiStore<bf16>{dog, HD, 0, nullptr, HD}, "triattn.gemm_dout");
+
+  AttnArgs& a = b.f;
+  a.R = N; a.H = H; a.N = N; a.D = w.D;
+  a.qkvg = sv.qkvg; a.ld = 4L * HD;
+  a.mask = mask;
+  a.mask_sr = per_column ? 1 : N;
+  a.mask_sk = per_column ? N : 1;
+  a.bias = sv.bias;
+  a.o = sv.o; a.og = nullptr; a.ldo = HD;
+  a.lse = sv.lse;
+  b.dog = dog;
+  b.scale = 1.f / std::sqrt((float)w.D);
+  attn_bwd(st, b);
+
+  GemmArgs g2;
+  g2.M = (int)M; g2.N = C; g2.K = 4 * HD;
+  g2.A = b.dqkvg; g2.a_sm = 4L * HD; g2.a_sk = 1;
+  g2.B = w.wqkvg; g2.b_sn = 4L * HD; g2.b_sk = 1;
+  gemm<128, 128>(st, g2, EpiStore<float>{dxn, C, 0, nullptr, C}, "triattn.gemm_dx");
+
+  if (din != dout)
+    BC2N_HIP(hipMemcpyAsync(din, dout, (size_t)M * C * 4, hipMemcpyDeviceToDevice, st));
+  KTimed kt("triattn.ln_bwd", st);
+  ln_bwd_f32(st, dxn, pair_in, M, C, per_column ? N : 0, w.ln_g, sv.mean, sv.rstd, din, true,
+             H, b.dbias, w.w2d);
+}
+
+}  // namespace bc2n

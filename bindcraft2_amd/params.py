@@ -1,0 +1,143 @@
+"""Random-init AF2 trunk parameters and the weights-manifest writer.
+
+Parameter names and shapes are those of the AF2 multimer Evoformer haiku
+modules (bindcraft/af/alphafold/model/modules.py), flattened into the
+manifest naming the reference's native loader reads,
+``param/block{b}/<module>/<sub>/<param>`` (bindcraft/af/native.py:171-226).
+The manifest format is kept identical on purpose so a directory written by
+the reference's ``weights_from_params`` loads here unchanged: one line
+``name file ndim d0 d1 ...`` per tensor, raw little-endian float32 files.
+"""
+import os
+
+import numpy as np
+
+# AF2 multimer widths (config.py:386-460)
+C_Z, C_M, C_E, C_T = 128, 256, 64, 64
+
+
+def _shapes_attention(c_in, h, d, c_out, gating=True):
+    s = {
+        "attention/query_w": (c_in, h, d),
+        "attention/key_w": (c_in, h, d),
+        "attention/value_w": (c_in, h, d),
+        "attention/output_w": (h, d, c_out),
+        "attention/output_b": (c_out,),
+    }
+    if gating:
+        s["attention/gating_w"] = (c_in, h, d)
+        s["attention/gating_b"] = (h, d)
+    return s
+
+
+def module_shapes(c_z=C_Z, c_m=C_M, tri_heads=4, trimul_hidden=None, opm_c=32,
+                  row_heads=8, col_heads=8):
+    """{module: {param: shape}} of one EvoformerIteration."""
+    ti = trimul_hidden or c_z
+    sh = {}
+    for n in ("triangle_attention_starting_node", "triangle_attention_ending_node"):
+        s = {"query_norm/scale": (c_z,), "query_norm/offset": (c_z,),
+             "feat_2d_weights": (c_z, tri_heads)}
+        s.update(_shapes_attention(c_z, tri_heads, c_z // tri_heads, c_z))
+        sh[n] = s
+    for n in ("triangle_multiplication_outgoing", "triangle_multiplication_incoming"):
+        sh[n] = {
+            "left_norm_input/scale": (c_z,), "left_norm_input/offset": (c_z,),
+            "projection/weights": (c_z, 2 * ti), "projection/bias": (2 * ti,),
+            "gate/weights": (c_z, 2 * ti), "gate/bias": (2 * ti,),
+            "center_norm/scale": (ti,), "center_norm/offset": (ti,),
+            "output_projection/weights": (ti, c_z), "output_projection/bias": (c_z,),
+            "gating_linear/weights": (c_z, c_z), "gating_linear/bias": (c_z,),
+        }
+    for n, c in (("pair_transition", c_z), ("msa_transition", c_m)):
+        sh[n] = {"input_layer_norm/scale": (c,), "input_layer_norm/offset": (c,),
+                 "transition1/weights": (c, 4 * c), "transition1/bias": (4 * c,),
+                 "transition2/weights": (4 * c, c), "transition2/bias": (c,)}
+    sh["outer_product_mean"] = {
+        "layer_norm_input/scale": (c_m,), "layer_norm_input/offset": (c_m,),
+        "left_projection/weights": (c_m, opm_c), "left_projection/bias": (opm_c,),
+        "right_projection/weights": (c_m, opm_c), "right_projection/bias": (opm_c,),
+        "output_w": (opm_c, opm_c, c_z), "output_b": (c_z,),
+    }
+    s = {"query_norm/scale": (c_m,), "query_norm/offset": (c_m,),
+         "feat_2d_norm/scale": (c_z,), "feat_2d_norm/offset": (c_z,),
+         "feat_2d_weights": (c_z, row_heads)}
+    s.update(_shapes_attention(c_m, row_heads, c_m // row_heads, c_m))
+    sh["msa_row_attention_with_pair_bias"] = s
+    s = {"query_norm/scale": (c_m,), "query_norm/offset": (c_m,)}
+    s.update(_shapes_attention(c_m, col_heads, c_m // col_heads, c_m))
+    sh["msa_column_attention"] = s
+    return sh
+
+
+def _fan_in(pname, shape):
+    if pname.endswith("output_w") and len(shape) == 3 and not pname.startswith("output_w"):
+        return shape[0] * shape[1]      # attention output [H, D, C]
+    if pname == "output_w":
+        return shape[0] * shape[1]      # OPM [c, e, f]
+    return shape[0]
+
+
+def init_module(shapes, rng, gates="zero", ln="identity"):
+    """LeCun-normal weights (std 1/sqrt(fan_in)), zero biases.  gates='zero'
+    gives AF2's gate init (weights 0, bias 1); gates='random' draws them like
+    any weight (bias N(0,1)) so the gate paths carry signal in tests.
+    ln='identity' -> scale 1, offset 0; 'random' -> 1+N(0,.1), N(0,.1)."""
+    out = {}
+    for pname, shape in shapes.items():
+        leaf = pname.split("/")[-1]
+        is_gate = ("gating" in pname) or pname.startswith("gate/")
+        if leaf == "scale":
+            v = np.ones(shape) if ln == "identity" else 1.0 + 0.1 * rng.standard_normal(shape)
+        elif leaf == "offset":
+            v = np.zeros(shape) if ln == "identity" else 0.1 * rng.standard_normal(shape)
+        elif leaf in ("bias", "output_b", "gating_b"):
+            if is_gate:
+                v = np.ones(shape) if gates == "zero" else rng.standard_normal(shape)
+            else:
+                v = np.zeros(shape) if gates == "zero" else 0.1 * rng.standard_normal(shape)
+        else:
+            if is_gate and gates == "zero":
+                v = np.zeros(shape)
+            else:
+                v = rng.standard_normal(shape) / np.sqrt(_fan_in(pname, shape))
+        out[pname] = np.asarray(v, np.float32)
+    return out
+
+
+def init_block_params(block, rng, modules=None, gates="zero", ln="identity", **shape_kw):
+    """Flat {manifest name: array} for one Evoformer block."""
+    sh = module_shapes(**shape_kw)
+    out = {}
+    for mod, shapes in sh.items():
+        if modules is not None and mod not in modules:
+            continue
+        for pname, arr in init_module(shapes, rng, gates, ln).items():
+            out[f"param/block{block}/{mod}/{pname}"] = arr
+    return out
+
+
+def write_manifest(out_dir, params):
+    """Write {name: array} as a weights directory (manifest.txt + .f32)."""
+    os.makedirs(out_dir, exist_ok=True)
+    with open(os.path.join(out_dir, "manifest.txt"), "w") as fh:
+        for name in sorted(params):
+            arr = np.ascontiguousarray(params[name], dtype=np.float32)
+            fn = name.replace("/", "__") + ".f32"
+            arr.tofile(os.path.join(out_dir, fn))
+            fh.write(f"{name} {fn} {arr.ndim} {' '.join(str(x) for x in arr.shape)}\n")
+    return out_dir
+
+
+def read_manifest(in_dir):
+    """Inverse of write_manifest (numpy only; nothing is unpickled)."""
+    out = {}
+    with open(os.path.join(in_dir, "manifest.txt")) as fh:
+        for line in fh:
+            parts = line.split()
+            if not parts:
+                continue
+            name, fn, nd = parts[0], parts[1], int(parts[2])
+            shape = tuple(int(x) for x in parts[3:3 + nd])
+            out[name] = np.fromfile(os.path.join(in_dir, fn), dtype="<f4").reshape(shape)
+    return out

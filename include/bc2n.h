@@ -1,0 +1,105 @@
+/*
+ * bc2n -- MI355X-native AlphaFold2 trunk for BindCraft2, C ABI.
+ *
+ * Every entry point is plain C: device pointers, sizes, an opaque HIP stream
+ * (hipStream_t passed as void*; NULL = the null stream) and an int status
+ * (0 = success; otherwise call bc2n_last_error() for the message).  Nothing
+ * here exits the process.  All work of one call is enqueued on `stream`; no
+ * call synchronises the host unless its scratch arena has to grow.
+ *
+ * Weights are not arguments: as in the reference, they come from a weights
+ * directory (manifest.txt + raw little-endian f32 files, names
+ * "param/block{b}/<module path>/<param>") loaded once per process.
+ *
+ * Calls are serialised by one process-wide lock and share one scratch arena,
+ * so all calls of a process must use the same stream.
+ *
+ * Lengths: N (residues) must be a multiple of 32 -- the reference's caller
+ * pads to 32 outside the custom VJP (bindcraft/af/native.py:950-972).
+ */
+#ifndef BC2N_H
+#define BC2N_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* bc2n_last_error(void);
+/* ABI version of this library. */
+int bc2n_abi_version(void);
+
+/* ------------------------------------------------------------------------
+ * Module entry points: one AF2 layer wrapped in dropout_wrapper
+ * (reference: bindcraft/af/alphafold/model/modules.py:46-76), i.e.
+ *     pair_out = pair + drop_tbl * module(pair)
+ * and its VJP
+ *     dpair_in = dpair_out + J^T (drop_tbl * dpair_out).
+ * `prefix` names the module inside the weights directory, e.g.
+ * "param/block0/triangle_attention_starting_node/".  `drop_tbl` is the
+ * shared-dropout scale table [N][C] (1/keep or 0; see bc2n_dropout_table) or
+ * NULL for no dropout.  `save` is a caller-owned device buffer of
+ * bc2n_*_save_bytes() bytes written by the forward and read by the backward.
+ * dpair_in may alias dpair_out.
+ * ---------------------------------------------------------------------- */
+
+/* Triangle attention, starting node (per_column=0) or ending node
+ * (per_column=1).  pair f32 [N,N,C], pair_mask f32 [N,N] (binary).
+ * Replaces native/triattn_body.cuh TriAttn::forward (:1090) / backward
+ * (:1228); semantics of modules.py:675-734. */
+size_t bc2n_triattn_save_bytes(int N, int C, int H);
+int bc2n_triattn_fwd(void* stream, const char* weights_dir, const char* prefix,
+                     int per_column, int N, const float* pair,
+                     const float* pair_mask, const float* drop_tbl,
+                     float* pair_out, void* save);
+int bc2n_triattn_bwd(void* stream, const char* weights_dir, const char* prefix,
+                     int per_column, int N, const float* pair,
+                     const float* pair_mask, const float* drop_tbl,
+                     const void* save, const float* dpair_out, float* dpair_in);
+
+/* ------------------------------------------------------------------------
+ * Dropout with JAX's own bits.  tbl[b*C+c] = keep/keep_rate where
+ * keep = jax.random.bernoulli(key, keep_rate, (B, C)), keep_rate =
+ * float32(1) - float32(rate); key = (k0, k1) = jax.random.key_data(key).
+ * Reference semantics: modules.py:37-44 (apply_dropout).
+ * ---------------------------------------------------------------------- */
+int bc2n_dropout_table(void* stream, float* tbl, int B, int C, uint32_t k0,
+                       uint32_t k1, float rate);
+/* keep bits (uint8 0/1) of jax.random.bernoulli(key, 1-rate, (n,)). */
+int bc2n_bernoulli_bits(void* stream, uint8_t* out, long n, uint32_t k0,
+                        uint32_t k1, float rate);
+/* Per-module dropout keys of an Evoformer stack, derived on the device from
+ * the stack key seed[0..1] (modules_multimer.py:622-641, modules.py:1308):
+ * out[(layer*9 + module)*2 + {0,1}]. */
+int bc2n_stack_keys(void* stream, const uint32_t* seed, int depth, uint32_t* out);
+
+/* ------------------------------------------------------------------------
+ * Per-kernel device timing (the reference's BLK_PROF/PROF_STEP counterpart,
+ * native/common.cuh:842-900): when enabled each kernel launch is bracketed
+ * by a HIP event pair on its stream.  bc2n_prof_read synchronises, writes
+ * up to `cap` (name, total ms, launch count) entries -- names as
+ * NUL-terminated strings at names + i*name_len -- clears the records and
+ * returns the entry count (-1 on error).
+ * ---------------------------------------------------------------------- */
+int bc2n_prof_enable(int on);
+int bc2n_prof_read(char* names, int name_len, double* ms, int* counts, int cap);
+
+/* ------------------------------------------------------------------------
+ * Kernel probes (test hooks; no reference counterpart beyond the module
+ * gates of native/*.cu).
+ * ---------------------------------------------------------------------- */
+/* C[M,N] = A[M,K] . B[N,K]^T, bf16 (uint16 bits) in, f32 out. */
+int bc2n_probe_gemm(void* stream, int M, int N, int K, const uint16_t* A,
+                    const uint16_t* B, float* C);
+/* y = LN(x) over C channels, bf16 out + mean/rstd. fast = E[x^2]-E[x]^2. */
+int bc2n_probe_layernorm(void* stream, long M, int C, const float* x,
+                         const float* gamma, const float* beta, int fast,
+                         uint16_t* y, float* mean, float* rstd);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* BC2N_H */

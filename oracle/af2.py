@@ -1,0 +1,279 @@
+"""CPU restatement of the reference's JAX AlphaFold2 trunk (fp64/fp32 torch).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py as the checker.  The product never routes
+through this module.
+
+Every function follows one function of the reference, cited by file:line
+(paths under bindcraft/af/alphafold/model/ unless noted), einsum by einsum, so
+autograd of this code is the reference's VJP.  Parameters are a flat dict in
+the weights-manifest naming ``param/block{b}/<module>/<param>`` (the names
+bindcraft/af/native.py:205-226 writes), values numpy float32 arrays.
+
+Pinning (tests/test_oracle_*.py): LayerNorm/Linear/attention against textbook
+closed forms and torch.nn.functional at fp64; attention against a pure-Python
+loop on tiny inputs; triangle attention ending == starting on the transposed
+pair; incoming == outgoing with swapped operands; OPM against its direct
+4-index sum and the mask==0 constant; S=1 column attention against its
+softmax==1 closed form; gradients against central finite differences.
+"""
+import math
+
+import numpy as np
+import torch
+
+from . import jax_prng
+
+LOGIT_CLIP = 1e8  # bindcraft/af/accel.py:6
+
+
+class Params:
+    """Prefix view over a flat parameter dict, converting to torch."""
+
+    def __init__(self, params, prefix, dtype=torch.float64):
+        self.params, self.prefix, self.dtype = params, prefix, dtype
+
+    def __call__(self, name):
+        return torch.as_tensor(np.asarray(self.params[self.prefix + name]), dtype=self.dtype)
+
+    def sub(self, name):
+        return Params(self.params, self.prefix + name, self.dtype)
+
+
+def layer_norm(x, scale, offset, fast=False, eps=1e-5):
+    """common_modules.py:127-183 (haiku LayerNorm); fast=True is the
+    use_fast_variance form of modules.py:909-919."""
+    mean = x.mean(-1, keepdim=True)
+    if fast:
+        var = (x * x).mean(-1, keepdim=True) - mean * mean
+    else:
+        var = ((x - mean) ** 2).mean(-1, keepdim=True)
+    return (x - mean) * (torch.rsqrt(var + eps) * scale) + offset
+
+
+def linear(x, p):
+    """common_modules.py:52-118 (Linear: '...c,cd->...d' + bias)."""
+    return torch.einsum("...c,cd->...d", x, p("weights")) + p("bias")
+
+
+def attention(q_data, m_data, bias, nonbatched_bias, p, gating=True):
+    """modules.py:313-400 (Attention) with accel.py:13-22 (_attend_stock:
+    logits + bias + nonbatched bias, clipped to +-LOGIT_CLIP, softmax)."""
+    qw, kw, vw = p("attention/query_w"), p("attention/key_w"), p("attention/value_w")
+    key_dim = qw.shape[-1]
+    q = torch.einsum("bqa,ahc->bqhc", q_data, qw) * key_dim ** (-0.5)
+    k = torch.einsum("bka,ahc->bkhc", m_data, kw)
+    v = torch.einsum("bka,ahc->bkhc", m_data, vw)
+    logits = torch.einsum("bqhc,bkhc->bhqk", q, k) + bias
+    if nonbatched_bias is not None:
+        logits = logits + nonbatched_bias[None]
+    logits = torch.clamp(logits, -LOGIT_CLIP, LOGIT_CLIP)
+    weights = torch.softmax(logits, dim=-1)
+    wa = torch.einsum("bhqk,bkhc->bqhc", weights, v)
+    if gating:
+        gate = torch.einsum("bqc,chv->bqhv", q_data, p("attention/gating_w")) + p("attention/gating_b")
+        wa = wa * torch.sigmoid(gate)
+    return torch.einsum("bqhc,hco->bqo", wa, p("attention/output_w")) + p("attention/output_b")
+
+
+def global_attention(q_data, m_data, q_mask, p, gating=True):
+    """modules.py:403-497 (GlobalAttention)."""
+    qw, kw, vw = p("attention/query_w"), p("attention/key_w"), p("attention/value_w")
+    key_dim = qw.shape[-1]
+    v = torch.einsum("bka,ac->bkc", m_data, vw)
+    q_avg = (q_mask * q_data).sum(1) / (q_mask.sum(1) + 1e-10)  # utils.mask_mean
+    q = torch.einsum("ba,ahc->bhc", q_avg, qw) * key_dim ** (-0.5)
+    k = torch.einsum("bka,ac->bkc", m_data, kw)
+    bias = 1e9 * (q_mask[:, None, :, 0] - 1.0)
+    logits = torch.einsum("bhc,bkc->bhk", q, k) + bias
+    weights = torch.softmax(logits, dim=-1)
+    wa = torch.einsum("bhk,bkc->bhc", weights, v)
+    ow, ob = p("attention/output_w"), p("attention/output_b")
+    if gating:
+        gate = torch.sigmoid(torch.einsum("bqc,chv->bqhv", q_data, p("attention/gating_w"))
+                             + p("attention/gating_b"))
+        wa = wa[:, None] * gate
+        return torch.einsum("bqhc,hco->bqo", wa, ow) + ob
+    return (torch.einsum("bhc,hco->bo", wa, ow) + ob)[:, None]
+
+
+def triangle_attention(pair, mask, p, per_column):
+    """modules.py:675-734 (TriangleAttention); per_column = ending node."""
+    if per_column:
+        pair = pair.transpose(0, 1)
+        mask = mask.transpose(0, 1)
+    bias = (1e9 * (mask - 1.0))[:, None, None, :]
+    x = layer_norm(pair, p("query_norm/scale"), p("query_norm/offset"))
+    nb = torch.einsum("qkc,ch->hqk", x, p("feat_2d_weights"))
+    out = attention(x, x, bias, nb, p)
+    if per_column:
+        out = out.transpose(0, 1)
+    return out
+
+
+def triangle_multiplication(pair, mask, p, outgoing):
+    """modules.py:1044-1088 (_fused_triangle_multiplication); equations
+    'ikc,jkc->ijc' (outgoing) / 'kjc,kic->ijc' (incoming), config.py:440-453."""
+    m = mask[..., None]
+    x = layer_norm(pair, p("left_norm_input/scale"), p("left_norm_input/offset"), fast=True)
+    proj = m * linear(x, p.sub("projection/"))
+    proj = proj * torch.sigmoid(linear(x, p.sub("gate/")))
+    nI = proj.shape[-1] // 2
+    left, right = proj[..., :nI], proj[..., nI:]
+    eq = "ikc,jkc->ijc" if outgoing else "kjc,kic->ijc"
+    act = torch.einsum(eq, left, right)
+    act = layer_norm(act, p("center_norm/scale"), p("center_norm/offset"), fast=True)
+    act = linear(act, p.sub("output_projection/"))
+    return act * torch.sigmoid(linear(x, p.sub("gating_linear/")))
+
+
+def transition(act, mask, p):
+    """modules.py:252-305 (Transition): LN -> Linear+relu -> Linear."""
+    x = layer_norm(act, p("input_layer_norm/scale"), p("input_layer_norm/offset"))
+    h = torch.relu(linear(x, p.sub("transition1/")))
+    return linear(h, p.sub("transition2/"))
+
+
+def outer_product_mean(msa, mask, p):
+    """modules.py:1128-1212 (OuterProductMean)."""
+    m = mask[..., None]
+    x = layer_norm(msa, p("layer_norm_input/scale"), p("layer_norm_input/offset"))
+    left = m * linear(x, p.sub("left_projection/"))
+    right = m * linear(x, p.sub("right_projection/"))
+    act = torch.einsum("abc,ade->bdce", left, right)
+    act = torch.einsum("bdce,cef->bdf", act, p("output_w")) + p("output_b")
+    norm = torch.einsum("abc,adc->bdc", m, m)
+    return act / (1e-3 + norm)
+
+
+def msa_row_attention(msa, msa_mask, pair, p):
+    """modules.py:500-563 (MSARowAttentionWithPairBias)."""
+    bias = (1e9 * (msa_mask - 1.0))[:, None, None, :]
+    x = layer_norm(msa, p("query_norm/scale"), p("query_norm/offset"))
+    z = layer_norm(pair, p("feat_2d_norm/scale"), p("feat_2d_norm/offset"))
+    nb = torch.einsum("qkc,ch->hqk", z, p("feat_2d_weights"))
+    return attention(x, x, bias, nb, p)
+
+
+def msa_column_attention(msa, msa_mask, p):
+    """modules.py:566-616 (MSAColumnAttention)."""
+    msa = msa.transpose(0, 1)
+    msa_mask = msa_mask.transpose(0, 1)
+    bias = (1e9 * (msa_mask - 1.0))[:, None, None, :]
+    x = layer_norm(msa, p("query_norm/scale"), p("query_norm/offset"))
+    return attention(x, x, bias, None, p).transpose(0, 1)
+
+
+def msa_column_global_attention(msa, msa_mask, p):
+    """modules.py:619-672 (MSAColumnGlobalAttention)."""
+    msa = msa.transpose(0, 1)
+    msa_mask = msa_mask.transpose(0, 1)
+    x = layer_norm(msa, p("query_norm/scale"), p("query_norm/offset"))
+    out = global_attention(x, x, msa_mask[..., None], p)
+    return out.transpose(0, 1)
+
+
+# ------------------------------------------------------------------ dropout
+
+def dropout_keep(key, rate, shape):
+    """The keep mask of apply_dropout (modules.py:37-44) as float64 0/1."""
+    keep = jax_prng.bernoulli(key, jax_prng.keep_rate(rate), shape)
+    return torch.as_tensor(keep.astype(np.float64))
+
+
+def apply_dropout(tensor, key, rate, broadcast_dim):
+    """modules.py:37-44: keep * tensor / keep_rate, keep shared over
+    broadcast_dim."""
+    if rate == 0.0 or key is None:
+        return tensor
+    shape = list(tensor.shape)
+    if broadcast_dim is not None:
+        shape[broadcast_dim] = 1
+    keep = dropout_keep(key, rate, tuple(shape)).to(tensor.dtype)
+    return keep * tensor / float(jax_prng.keep_rate(rate))
+
+
+def dropout_table(key, rate, rows, channels):
+    """The [rows, C] scale table the native path consumes for a shared mask
+    of shape (1, rows, C) or (rows, 1, C): keep / keep_rate."""
+    keep = jax_prng.bernoulli(key, jax_prng.keep_rate(rate), (rows, channels))
+    return keep.astype(np.float32) / np.float32(jax_prng.keep_rate(rate))
+
+
+# Module configuration of the multimer Evoformer (config.py:386-460):
+# (name, dropout rate, orientation).
+EVO_MODULES = (
+    ("outer_product_mean", 0.0, "per_row"),
+    ("msa_row_attention_with_pair_bias", 0.15, "per_row"),
+    ("msa_column_attention", 0.0, "per_column"),
+    ("msa_transition", 0.0, "per_row"),
+    ("triangle_multiplication_outgoing", 0.25, "per_row"),
+    ("triangle_multiplication_incoming", 0.25, "per_row"),
+    ("triangle_attention_starting_node", 0.25, "per_row"),
+    ("triangle_attention_ending_node", 0.25, "per_column"),
+    ("pair_transition", 0.0, "per_row"),
+)
+
+
+def dropout_wrapper(residual, output_act, key, rate, orientation, use_dropout):
+    """modules.py:46-76: output_act + apply_dropout(residual) with the shared
+    mask's broadcast dim 0 for 'per_row' and 1 for 'per_column'."""
+    bd = 0 if orientation == "per_row" else 1
+    r = rate if use_dropout else 0.0
+    return output_act + apply_dropout(residual, key, r, bd)
+
+
+def evoformer_iteration(msa, pair, msa_mask, pair_mask, params, prefix, key,
+                        use_dropout, is_extra_msa=False, dtype=torch.float64):
+    """modules.py:1278-1391 (EvoformerIteration) with outer_product_mean.first
+    (config.py:414).  `key` is the block's SafeKey value: split into 10, keys
+    1..9 go to the 9 modules in order (modules.py:1308-1309)."""
+    P = Params(params, prefix, dtype)
+    sub = jax_prng.split(key, 10)[1:] if key is not None else [None] * 9
+    cfg = {n: (r, o) for n, r, o in EVO_MODULES}
+
+    def wrap(name, residual, out_act, k):
+        r, o = cfg[name]
+        return dropout_wrapper(residual, out_act, k, r, o, use_dropout)
+
+    pair = wrap("outer_product_mean",
+                outer_product_mean(msa, msa_mask, P.sub("outer_product_mean/")), pair, sub[0])
+    msa = wrap("msa_row_attention_with_pair_bias",
+               msa_row_attention(msa, msa_mask, pair, P.sub("msa_row_attention_with_pair_bias/")),
+               msa, sub[1])
+    if is_extra_msa:
+        col = msa_column_global_attention(msa, msa_mask, P.sub("msa_column_global_attention/"))
+    else:
+        col = msa_column_attention(msa, msa_mask, P.sub("msa_column_attention/"))
+    msa = wrap("msa_column_attention", col, msa, sub[2])
+    msa = wrap("msa_transition", transition(msa, msa_mask, P.sub("msa_transition/")), msa, sub[3])
+    pair = wrap("triangle_multiplication_outgoing",
+                triangle_multiplication(pair, pair_mask, P.sub("triangle_multiplication_outgoing/"), True),
+                pair, sub[4])
+    pair = wrap("triangle_multiplication_incoming",
+                triangle_multiplication(pair, pair_mask, P.sub("triangle_multiplication_incoming/"), False),
+                pair, sub[5])
+    pair = wrap("triangle_attention_starting_node",
+                triangle_attention(pair, pair_mask, P.sub("triangle_attention_starting_node/"), False),
+                pair, sub[6])
+    pair = wrap("triangle_attention_ending_node",
+                triangle_attention(pair, pair_mask, P.sub("triangle_attention_ending_node/"), True),
+                pair, sub[7])
+    pair = wrap("pair_transition", transition(pair, pair_mask, P.sub("pair_transition/")), pair, sub[8])
+    return msa, pair
+
+
+def evoformer_stack(msa, pair, msa_mask, pair_mask, params, depth, stack_key,
+                    use_dropout, is_extra_msa=False, dtype=torch.float64):
+    """modules_multimer.py:610-641 (layer_stack scan of evoformer_fn): per
+    layer (carry, sub) = split(carry); the block gets `sub`."""
+    carry = stack_key
+    for b in range(depth):
+        if carry is not None:
+            carry, sub = jax_prng.split(carry, 2)
+        else:
+            sub = None
+        msa, pair = evoformer_iteration(msa, pair, msa_mask, pair_mask, params,
+                                        f"param/block{b}/", sub, use_dropout,
+                                        is_extra_msa, dtype)
+    return msa, pair
