@@ -16,9 +16,15 @@
 // second product; the first product's result already sits in exactly that
 // order.  Scores are kept in the log2 domain: q is pre-scaled by
 // D^-1/2 * log2(e) and the pair bias by log2(e) upstream, so a score is one
-// MFMA plus one add.  A masked key takes the value -1e8*log2(e), which is what
-// AF2's clip(-1e9-ish, -1e8, 1e8) produces: a fully masked query row attends
-// uniformly, exactly as in the reference, and masked keys carry no gradient.
+// MFMA plus one add.  A masked key takes one shared constant score, as AF2's
+// clip(-1e9 + x, -1e8, 1e8) gives every masked key the same -1e8: a fully
+// masked row attends uniformly, partially masked rows give masked keys zero
+// weight, and masked keys carry no gradient (the clip's derivative is 0).
+// The constant is -2^13 rather than -1e8*log2(e): only score differences
+// matter, 2^13 log2-units (5678 natural units) is far beyond any unmasked
+// logit, and at that magnitude f32 still resolves the row's log-sum-exp
+// (lse = -2^13 + log2 N) to ~1e-3, so the backward's exp2(s - lse) = 1/N
+// on a fully masked row is exact to bf16 precision.
 //
 // The bias gradient sum over rows is accumulated in registers over a chunk of
 // rows and written once per chunk; a second pass adds the chunks in a fixed
@@ -29,7 +35,7 @@
 namespace bc2n {
 
 constexpr int AD = 32;             // head width handled here
-constexpr float NEG_LOGIT = -1e8f * LOG2E;
+constexpr float NEG_LOGIT = -8192.0f;
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
