@@ -40,6 +40,9 @@ def _declare(L):
         "bc2n_triattn_save_bytes": (sz, [i, i, i]),
         "bc2n_triattn_fwd": (i, [vp, cs, cs, i, i, vp, vp, vp, vp, vp]),
         "bc2n_triattn_bwd": (i, [vp, cs, cs, i, i, vp, vp, vp, vp, vp, vp]),
+        "bc2n_trimul_save_bytes": (sz, [i, i, i]),
+        "bc2n_trimul_fwd": (i, [vp, cs, cs, i, i, vp, vp, vp, vp, vp]),
+        "bc2n_trimul_bwd": (i, [vp, cs, cs, i, i, vp, vp, vp, vp, vp, vp]),
         "bc2n_dropout_table": (i, [vp, vp, i, i, u32, u32, f]),
         "bc2n_bernoulli_bits": (i, [vp, vp, c.c_long, u32, u32, f]),
         "bc2n_stack_keys": (i, [vp, vp, i, vp]),

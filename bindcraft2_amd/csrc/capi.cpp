@@ -38,6 +38,17 @@ const TriAttnW& triattn_w(const char* dir, const char* prefix) {
   return g_triattn.emplace(key, w).first->second;
 }
 
+std::map<std::pair<std::string, std::string>, TriMulW> g_trimul;
+
+const TriMulW& trimul_w(const char* dir, const char* prefix) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto key = std::make_pair(std::string(dir), std::string(prefix));
+  auto it = g_trimul.find(key);
+  if (it != g_trimul.end()) return it->second;
+  TriMulW w = trimul_weights(weights(dir), prefix);
+  return g_trimul.emplace(key, w).first->second;
+}
+
 void need(bool ok, const char* msg) {
   if (!ok) throw std::invalid_argument(msg);
 }
@@ -57,6 +68,7 @@ int bc2n_triattn_fwd(void* stream, const char* weights_dir, const char* prefix, 
   return guarded([&] {
     need(weights_dir && prefix, "weights_dir/prefix required");
     need(pair && pair_mask && pair_out && save, "null operand");
+    need(pair_out != pair, "triattn: pair_out must not alias pair");
     const TriAttnW& w = triattn_w(weights_dir, prefix);
     triattn_fwd(as_stream(stream), w, per_column != 0, N, pair, pair_mask, drop_tbl, pair_out,
                 save);
@@ -72,6 +84,32 @@ int bc2n_triattn_bwd(void* stream, const char* weights_dir, const char* prefix, 
     const TriAttnW& w = triattn_w(weights_dir, prefix);
     triattn_bwd(as_stream(stream), w, per_column != 0, N, pair, pair_mask, drop_tbl, save,
                 dpair_out, dpair_in);
+  });
+}
+
+size_t bc2n_trimul_save_bytes(int N, int C, int I) { return trimul_save_bytes(N, C, I); }
+
+int bc2n_trimul_fwd(void* stream, const char* weights_dir, const char* prefix, int outgoing,
+                    int N, const float* pair, const float* pair_mask, const float* drop_tbl,
+                    float* pair_out, void* save) {
+  return guarded([&] {
+    need(weights_dir && prefix, "weights_dir/prefix required");
+    need(pair && pair_mask && pair_out && save, "null operand");
+    need(pair_out != pair, "trimul: pair_out must not alias pair");
+    const TriMulW& w = trimul_w(weights_dir, prefix);
+    trimul_fwd(as_stream(stream), w, outgoing != 0, N, pair, pair_mask, drop_tbl, pair_out, save);
+  });
+}
+
+int bc2n_trimul_bwd(void* stream, const char* weights_dir, const char* prefix, int outgoing,
+                    int N, const float* pair, const float* pair_mask, const float* drop_tbl,
+                    const void* save, const float* dpair_out, float* dpair_in) {
+  return guarded([&] {
+    need(weights_dir && prefix, "weights_dir/prefix required");
+    need(pair && pair_mask && save && dpair_out && dpair_in, "null operand");
+    const TriMulW& w = trimul_w(weights_dir, prefix);
+    trimul_bwd(as_stream(stream), w, outgoing != 0, N, pair, pair_mask, drop_tbl, save, dpair_out,
+               dpair_in);
   });
 }
 

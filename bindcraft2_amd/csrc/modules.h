@@ -33,4 +33,23 @@ void triattn_bwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
                  const float* pair_in, const float* mask, const float* tbl,
                  const void* save, const float* dout, float* din);
 
+// ------------------------------------------------------ triangle multiplication
+// modules.py:1044-1088 (fused projection weights).
+struct TriMulW {
+  int C = 0, I = 0;
+  const float *ln_g = nullptr, *ln_b = nullptr, *cn_g = nullptr, *cn_b = nullptr;
+  const float *bp = nullptr, *bg = nullptr, *bgl = nullptr, *bo = nullptr;
+  const bf16* wcat = nullptr;    // [C][4I+C]  (GEMM column order)
+  const bf16* wcat_t = nullptr;  // [4I+C][C]
+  const bf16* wo = nullptr;      // [I][C]
+  const bf16* wo_t = nullptr;    // [C][I]
+};
+TriMulW trimul_weights(WeightStore& ws, const std::string& prefix);
+size_t trimul_save_bytes(int N, int C, int I);
+void trimul_fwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const float* pair_in,
+                const float* mask, const float* tbl, float* pair_out, void* save);
+void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const float* pair_in,
+                const float* mask, const float* tbl, const void* save, const float* dout,
+                float* din);
+
 }  // namespace bc2n

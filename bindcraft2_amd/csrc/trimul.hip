@@ -1,0 +1,358 @@
+// Triangle multiplication (outgoing 'ikc,jkc->ijc' / incoming 'kjc,kic->ijc'),
+// AF2's fused-projection form, forward and backward.
+//
+// Forward:
+//   LN (fast variance) -> xn bf16
+//   GEMM xn . Wcat  (Wcat = [proj|gate] channel pairs interleaved in 16-wide
+//        blocks, then gating_linear), fused epilogue:
+//          a = mask * proj * sigmoid(gate)   -> left/right planes [I][N*N] bf16
+//          proj, gate pre-activations kept (channel-major) for the backward
+//          g_out = sigmoid(gating_linear)  -> [M][C] bf16
+//   batched MFMA GEMM over the I channels (plane layouts pick out/in)  -> T f32
+//   centre LN (fast variance) reading the channel-major T            -> Tn bf16
+//   GEMM Tn . Wo + bo, fused: o kept, out = in + tbl * (o * g_out)
+// Backward: the exact reverse with the contraction's two transposed GEMMs.
+// Reference: modules.py:1044-1088 (_fused_triangle_multiplication), :909-919
+// (fast-variance LN); native/trimul_body.cuh:1183-1796 (TriMul).
+#include "gemm.h"
+#include "modules.h"
+
+namespace bc2n {
+
+namespace {
+
+// GEMM column of projection channel ch (0..2I) and of its gate.
+__host__ __device__ inline int col_proj(int ch) { return (ch / 16) * 32 + ch % 16; }
+__host__ __device__ inline int col_gate(int ch) { return (ch / 16) * 32 + 16 + ch % 16; }
+
+struct EpiTrimulProj {
+  bf16 *left, *right;   // [I][M]
+  bf16 *psave, *gsave;  // [2I][M] pre-activations
+  bf16* gout;           // [M][C]
+  const float *bp, *bg, *bgl, *mask;
+  long M;
+  int I, C;
+  template <int TN>
+  __device__ __forceinline__ void apply(int, int m, int n, const float (&v)[TN]) const {
+    static_assert(TN == 4, "wave tile must span 64 columns");
+    const int two_i4 = 4 * I;
+    if (n < two_i4) {
+      const float mk = mask[m];
+      const int base = n - (n % 16);  // lane column is base + fr
+      const int fr = n % 16;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int cb = (base + 32 * j) / 32;
+        const int ch = cb * 16 + fr;
+        const float p = v[2 * j] + bp[ch];
+        const float g = v[2 * j + 1] + bg[ch];
+        psave[(long)ch * M + m] = (bf16)p;
+        gsave[(long)ch * M + m] = (bf16)g;
+        const float a = mk * p * sigmoidf_(g);
+        if (ch < I) left[(long)ch * M + m] = (bf16)a;
+        else right[(long)(ch - I) * M + m] = (bf16)a;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int c = n + 16 * j - two_i4;
+        if (c >= C) continue;
+        gout[(long)m * C + c] = (bf16)sigmoidf_(v[j] + bgl[c]);
+      }
+    }
+  }
+};
+
+// o = acc + bo (kept, bf16); out[m] = in[m] + tbl[(m%nt)*C+c] * o * g_out
+struct EpiTrimulOut {
+  const float* in;
+  float* out;
+  const float* bo;
+  const bf16* gout;
+  bf16* osave;
+  const float* tbl;
+  int nt, C;
+  template <int TN>
+  __device__ __forceinline__ void apply(int, int m, int n, const float (&v)[TN]) const {
+    const float* t = tbl ? tbl + (long)(m % nt) * C : nullptr;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int c = n + 16 * j;
+      if (c >= C) continue;
+      const long o = (long)m * C + c;
+      const float ov = v[j] + bo[c];
+      osave[o] = (bf16)ov;
+      float x = ov * (float)gout[o];
+      if (t) x *= t[c];
+      out[o] = in[o] + x;
+    }
+  }
+};
+
+template <class A>
+struct TriMulSave {
+  float *mean, *rstd, *cmean, *crstd, *T;
+  bf16 *left, *right, *psave, *gsave, *gout, *osave;
+  TriMulSave(A& a, int N, int C, int I) {
+    const size_t M = (size_t)N * N;
+    mean = a.template take<float>(M);
+    rstd = a.template take<float>(M);
+    cmean = a.template take<float>(M);
+    crstd = a.template take<float>(M);
+    T = a.template take<float>(M * I);
+    left = a.template take<bf16>(M * I);
+    right = a.template take<bf16>(M * I);
+    psave = a.template take<bf16>(M * 2 * I);
+    gsave = a.template take<bf16>(M * 2 * I);
+    gout = a.template take<bf16>(M * C);
+    osave = a.template take<bf16>(M * C);
+  }
+};
+
+// dd = tbl*dout; do = dd*g_out (bf16, GEMM operand);
+// dcat[m][4I + c] = dd * o * g(1-g)   (gating_linear pre-activation grad)
+__global__ void trimul_out_bwd_kernel(const float* __restrict__ dout, const float* __restrict__ tbl,
+                                      const bf16* __restrict__ gout, const bf16* __restrict__ osave,
+                                      bf16* __restrict__ dob, bf16* __restrict__ dcat, long M,
+                                      int C, int ldcat, int off, int nt) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= M * C) return;
+  const long m = i / C;
+  const int c = (int)(i % C);
+  float d = dout[i];
+  if (tbl) d *= tbl[(m % nt) * C + c];
+  const float g = (float)gout[i], o = (float)osave[i];
+  dob[i] = (bf16)(d * g);
+  dcat[m * ldcat + off + c] = (bf16)(d * o * g * (1.f - g));
+}
+
+// From channel-major dleft/dright and the kept pre-activations, write the
+// row-major [M][4I] gradient of the projection GEMM's output columns:
+//   dproj = da * mask * s,  dgate = da * mask * p * s(1-s),  s = sigmoid(gate)
+// A block handles 32 rows: reads are coalesced along m, the transposed
+// writes go through LDS.
+__global__ __launch_bounds__(256) void trimul_proj_bwd_kernel(
+    const bf16* __restrict__ dl, const bf16* __restrict__ dr, const bf16* __restrict__ psave,
+    const bf16* __restrict__ gsave, const float* __restrict__ mask, bf16* __restrict__ dcat,
+    long M, int I, int ldcat) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
+  constexpr int R = 32;
+  const int W = 4 * I;                 // columns of the tile
+  const int LD = W + 8;
+  bf16* tile = reinterpret_cast<bf16*>(smem_raw);  // [R][LD]
+  const long m0 = (long)blockIdx.x * R;
+  const int t = threadIdx.x;
+  for (int idx = t; idx < 2 * I * R; idx += 256) {
+    const int ch = idx / R, r = idx % R;
+    const long m = m0 + r;
+    float dp = 0.f, dg = 0.f;
+    if (m < M) {
+      const float da = (float)(ch < I ? dl[(long)ch * M + m] : dr[(long)(ch - I) * M + m]);
+      const float mk = mask[m];
+      const float s = sigmoidf_((float)gsave[(long)ch * M + m]);
+      const float p = (float)psave[(long)ch * M + m];
+      dp = da * mk * s;
+      dg = da * mk * p * s * (1.f - s);
+    }
+    tile[r * LD + col_proj(ch)] = (bf16)dp;
+    tile[r * LD + col_gate(ch)] = (bf16)dg;
+  }
+  __syncthreads();
+  const int chunks = W / 8;
+  for (int idx = t; idx < R * chunks; idx += 256) {
+    const int r = idx / chunks, c8 = (idx % chunks) * 8;
+    const long m = m0 + r;
+    if (m < M) st8(dcat + m * ldcat + c8, ld8(&tile[r * LD + c8]));
+  }
+}
+
+}  // namespace
+
+TriMulW trimul_weights(WeightStore& ws, const std::string& P) {
+  TriMulW w;
+  const HostTensor& pw = ws.host(P + "projection/weights");  // [C, 2I]
+  w.C = pw.shape[0];
+  w.I = pw.shape[1] / 2;
+  const int C = w.C, I = w.I, NC = 4 * I + C;
+  if (I % 16 != 0 || C % 64 != 0) throw std::runtime_error("trimul: widths must be multiples of 16/64");
+  w.ln_g = ws.f32(P + "left_norm_input/scale");
+  w.ln_b = ws.f32(P + "left_norm_input/offset");
+  w.cn_g = ws.f32(P + "center_norm/scale");
+  w.cn_b = ws.f32(P + "center_norm/offset");
+  w.bp = ws.f32(P + "projection/bias");
+  w.bg = ws.f32(P + "gate/bias");
+  w.bgl = ws.f32(P + "gating_linear/bias");
+  w.bo = ws.f32(P + "output_projection/bias");
+  // Wcat [C][NC] in GEMM column order
+  auto cat = [&]() {
+    const HostTensor& gw = ws.host(P + "gate/weights");
+    const HostTensor& lw = ws.host(P + "gating_linear/weights");
+    std::vector<float> c((size_t)C * NC);
+    for (int r = 0; r < C; ++r) {
+      for (int ch = 0; ch < 2 * I; ++ch) {
+        c[(size_t)r * NC + col_proj(ch)] = pw.data[(size_t)r * 2 * I + ch];
+        c[(size_t)r * NC + col_gate(ch)] = gw.data[(size_t)r * 2 * I + ch];
+      }
+      for (int j = 0; j < C; ++j) c[(size_t)r * NC + 4 * I + j] = lw.data[(size_t)r * C + j];
+    }
+    return c;
+  };
+  w.wcat = ws.derived<bf16>("trimul.wcat:" + P, [&] { return to_bf16(cat()); });
+  w.wcat_t = ws.derived<bf16>("trimul.wcat_t:" + P, [&] {
+    std::vector<float> c = cat();
+    return transpose_bf16(c.data(), C, NC);
+  });
+  const HostTensor& ow = ws.host(P + "output_projection/weights");  // [I, C]
+  w.wo = ws.derived<bf16>("trimul.wo:" + P, [&] { return to_bf16(ow.data); });
+  w.wo_t = ws.derived<bf16>("trimul.wo_t:" + P, [&] { return transpose_bf16(ow.data.data(), I, C); });
+  return w;
+}
+
+size_t trimul_save_bytes(int N, int C, int I) {
+  Sizer s;
+  TriMulSave<Sizer> plan(s, N, C, I);
+  (void)plan;
+  return s.off;
+}
+
+static void trimul_check(int N) {
+  if (N <= 0 || N % 32 != 0) throw std::runtime_error("trimul: N must be a positive multiple of 32");
+}
+
+// Contraction operand layouts for one channel plane (row-major N x N).
+static void contraction_fwd(hipStream_t st, bool outgoing, int N, int I, const bf16* L,
+                            const bf16* R, float* T) {
+  const long M = (long)N * N;
+  GemmArgs g;
+  g.M = N; g.N = N; g.K = N; g.batch = I;
+  if (outgoing) {  // T[i][j] = sum_k L[i][k] R[j][k]
+    g.A = L; g.a_sm = N; g.a_sk = 1;
+    g.B = R; g.b_sn = N; g.b_sk = 1;
+  } else {         // T[i][j] = sum_k R[k][i] L[k][j]
+    g.A = R; g.a_sm = 1; g.a_sk = N;
+    g.B = L; g.b_sn = 1; g.b_sk = N;
+  }
+  g.a_sb = M; g.b_sb = M;
+  gemm<64, 64>(st, g, EpiStore<float>{T, N, M, nullptr, N}, "trimul.contract_fwd");
+}
+
+void trimul_fwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const float* pair_in,
+                const float* mask, const float* tbl, float* pair_out, void* save) {
+  trimul_check(N);
+  const int C = w.C, I = w.I, NC = 4 * I + C;
+  const long M = (long)N * N;
+  Carver cv(save);
+  TriMulSave<Carver> sv(cv, N, C, I);
+  Arena& ar = arena();
+  std::lock_guard<std::recursive_mutex> lk(ar.lock());
+  ar.reset(st, (size_t)M * C * 2 + (size_t)M * I * 2 + 1024);
+  bf16* xn = ar.take_n<bf16>((size_t)M * C);
+  bf16* tn = ar.take_n<bf16>((size_t)M * I);
+  {
+    KTimed kt("trimul.ln_fwd", st);
+    ln_fwd_f32(st, pair_in, M, C, 0, w.ln_g, w.ln_b, xn, sv.mean, sv.rstd, true, 0, nullptr,
+               nullptr);
+  }
+  GemmArgs g1;
+  g1.M = (int)M; g1.N = NC; g1.K = C;
+  g1.A = xn; g1.a_sm = C; g1.a_sk = 1;
+  g1.B = w.wcat_t; g1.b_sn = C; g1.b_sk = 1;
+  gemm<128, 128>(st, g1,
+                 EpiTrimulProj{sv.left, sv.right, sv.psave, sv.gsave, sv.gout, w.bp, w.bg, w.bgl,
+                               mask, M, I, C},
+                 "trimul.gemm_proj");
+  contraction_fwd(st, outgoing, N, I, sv.left, sv.right, sv.T);
+  {
+    KTimed kt("trimul.ln_center", st);
+    ln_fwd_cm(st, sv.T, M, I, w.cn_g, w.cn_b, tn, sv.cmean, sv.crstd, true);
+  }
+  GemmArgs g2;
+  g2.M = (int)M; g2.N = C; g2.K = I;
+  g2.A = tn; g2.a_sm = I; g2.a_sk = 1;
+  g2.B = w.wo_t; g2.b_sn = I; g2.b_sk = 1;
+  gemm<128, 128>(st, g2, EpiTrimulOut{pair_in, pair_out, w.bo, sv.gout, sv.osave, tbl, N, C},
+                 "trimul.gemm_out");
+}
+
+void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const float* pair_in,
+                const float* mask, const float* tbl, const void* save, const float* dout,
+                float* din) {
+  trimul_check(N);
+  const int C = w.C, I = w.I, NC = 4 * I + C;
+  const long M = (long)N * N;
+  Carver cv(const_cast<void*>(save));
+  TriMulSave<Carver> sv(cv, N, C, I);
+  Arena& ar = arena();
+  std::lock_guard<std::recursive_mutex> lk(ar.lock());
+  Sizer need;
+  need.take<bf16>((size_t)M * C);   // do
+  need.take<bf16>((size_t)M * NC);  // dcat
+  need.take<float>((size_t)M * I);  // dTn
+  need.take<bf16>((size_t)M * I);   // dT
+  need.take<bf16>((size_t)M * I);   // dL
+  need.take<bf16>((size_t)M * I);   // dR
+  need.take<float>((size_t)M * C);  // dxn
+  ar.reset(st, need.off);
+  bf16* dob = ar.take_n<bf16>((size_t)M * C);
+  bf16* dcat = ar.take_n<bf16>((size_t)M * NC);
+  float* dtn = ar.take_n<float>((size_t)M * I);
+  bf16* dT = ar.take_n<bf16>((size_t)M * I);
+  bf16* dL = ar.take_n<bf16>((size_t)M * I);
+  bf16* dR = ar.take_n<bf16>((size_t)M * I);
+  float* dxn = ar.take_n<float>((size_t)M * C);
+
+  {
+    KTimed kt("trimul.out_bwd", st);
+    const long n = M * C;
+    hipLaunchKernelGGL(trimul_out_bwd_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                       dout, tbl, sv.gout, sv.osave, dob, dcat, M, C, NC, 4 * I, N);
+  }
+  GemmArgs g1;
+  g1.M = (int)M; g1.N = I; g1.K = C;
+  g1.A = dob; g1.a_sm = C; g1.a_sk = 1;
+  g1.B = w.wo; g1.b_sn = C; g1.b_sk = 1;
+  gemm<128, 128>(st, g1, EpiStore<float>{dtn, I, 0, nullptr, I}, "trimul.gemm_dout");
+  {
+    KTimed kt("trimul.ln_center_bwd", st);
+    ln_bwd_cm(st, dtn, sv.T, M, I, w.cn_g, sv.cmean, sv.crstd, dT);
+  }
+  {
+    GemmArgs a, b;
+    a.M = N; a.N = N; a.K = N; a.batch = I; a.a_sb = M; a.b_sb = M;
+    b = a;
+    if (outgoing) {
+      // dL[i][k] = sum_j dT[i][j] R[j][k]
+      a.A = dT; a.a_sm = N; a.a_sk = 1;
+      a.B = sv.right; a.b_sn = 1; a.b_sk = N;
+      // dR[j][k] = sum_i dT[i][j] L[i][k]
+      b.A = dT; b.a_sm = 1; b.a_sk = N;
+      b.B = sv.left; b.b_sn = 1; b.b_sk = N;
+    } else {
+      // dL[k][j] = sum_i R[k][i] dT[i][j]
+      a.A = sv.right; a.a_sm = N; a.a_sk = 1;
+      a.B = dT; a.b_sn = 1; a.b_sk = N;
+      // dR[k][i] = sum_j L[k][j] dT[i][j]
+      b.A = sv.left; b.a_sm = N; b.a_sk = 1;
+      b.B = dT; b.b_sn = N; b.b_sk = 1;
+    }
+    gemm<64, 64>(st, a, EpiStore<bf16>{dL, N, M, nullptr, N}, "trimul.contract_bwd");
+    gemm<64, 64>(st, b, EpiStore<bf16>{dR, N, M, nullptr, N}, "trimul.contract_bwd");
+  }
+  {
+    KTimed kt("trimul.proj_bwd", st);
+    const size_t lds = (size_t)32 * (4 * I + 8) * 2;
+    hipLaunchKernelGGL(trimul_proj_bwd_kernel, dim3((unsigned)((M + 31) / 32)), dim3(256), lds, st,
+                       dL, dR, sv.psave, sv.gsave, mask, dcat, M, I, NC);
+  }
+  GemmArgs g2;
+  g2.M = (int)M; g2.N = C; g2.K = NC;
+  g2.A = dcat; g2.a_sm = NC; g2.a_sk = 1;
+  g2.B = w.wcat; g2.b_sn = NC; g2.b_sk = 1;
+  gemm<128, 128>(st, g2, EpiStore<float>{dxn, C, 0, nullptr, C}, "trimul.gemm_dx");
+  if (din != dout)
+    BC2N_HIP(hipMemcpyAsync(din, dout, (size_t)M * C * 4, hipMemcpyDeviceToDevice, st));
+  KTimed kt("trimul.ln_bwd", st);
+  ln_bwd_f32(st, dxn, pair_in, M, C, 0, w.ln_g, sv.mean, sv.rstd, din, true, 0, nullptr, nullptr);
+}
+
+}  // namespace bc2n

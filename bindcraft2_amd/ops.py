@@ -68,6 +68,43 @@ class TriangleAttention:
         return din
 
 
+class TriangleMultiplication:
+    """modules.py TriangleMultiplication (fused projections) + dropout_wrapper,
+    outgoing or incoming."""
+
+    def __init__(self, weights_dir, prefix, outgoing, c=128, hidden=128):
+        self.dir = weights_dir.encode()
+        self.prefix = prefix.encode()
+        self.outgoing = int(bool(outgoing))
+        self.c, self.i = c, hidden
+
+    def save_bytes(self, n):
+        return lib().bc2n_trimul_save_bytes(n, self.c, self.i)
+
+    def forward(self, pair, mask, drop_tbl=None, out=None, save=None):
+        n = pair.shape[0]
+        _f32(pair, (n, n, self.c), "pair")
+        _f32(mask, (n, n), "pair_mask")
+        if out is None:
+            out = torch.empty_like(pair)
+        if save is None:
+            save = torch.empty(self.save_bytes(n), dtype=torch.uint8, device=pair.device)
+        check(lib().bc2n_trimul_fwd(_stream(), self.dir, self.prefix, self.outgoing, n,
+                                    _ptr(pair), _ptr(mask), _ptr(drop_tbl), _ptr(out),
+                                    _ptr(save)))
+        return out, save
+
+    def backward(self, pair, mask, drop_tbl, save, dout, din=None):
+        n = pair.shape[0]
+        _f32(dout, (n, n, self.c), "dpair_out")
+        if din is None:
+            din = torch.empty_like(dout)
+        check(lib().bc2n_trimul_bwd(_stream(), self.dir, self.prefix, self.outgoing, n,
+                                    _ptr(pair), _ptr(mask), _ptr(drop_tbl), _ptr(save),
+                                    _ptr(dout), _ptr(din)))
+        return din
+
+
 def dropout_table(rows, channels, key, rate, device="cuda"):
     """[rows, channels] keep/keep_rate table from a JAX key (k0, k1)."""
     tbl = torch.empty(rows, channels, dtype=torch.float32, device=device)

@@ -43,6 +43,7 @@ int bc2n_abi_version(void);
  * shared-dropout scale table [N][C] (1/keep or 0; see bc2n_dropout_table) or
  * NULL for no dropout.  `save` is a caller-owned device buffer of
  * bc2n_*_save_bytes() bytes written by the forward and read by the backward.
+ * pair_out must not alias pair (the backward reads the module input);
  * dpair_in may alias dpair_out.
  * ---------------------------------------------------------------------- */
 
@@ -59,6 +60,21 @@ int bc2n_triattn_bwd(void* stream, const char* weights_dir, const char* prefix,
                      int per_column, int N, const float* pair,
                      const float* pair_mask, const float* drop_tbl,
                      const void* save, const float* dpair_out, float* dpair_in);
+
+/* Triangle multiplication, outgoing (outgoing=1, 'ikc,jkc->ijc') or incoming
+ * (outgoing=0, 'kjc,kic->ijc'), AF2's fused-projection form with
+ * fast-variance LayerNorms.  pair f32 [N,N,C]; pair_out must not alias pair.
+ * Replaces native/trimul_body.cuh TriMul::forward (:1572) / backward
+ * (:1680); semantics of modules.py:1044-1088. */
+size_t bc2n_trimul_save_bytes(int N, int C, int I);
+int bc2n_trimul_fwd(void* stream, const char* weights_dir, const char* prefix,
+                    int outgoing, int N, const float* pair,
+                    const float* pair_mask, const float* drop_tbl,
+                    float* pair_out, void* save);
+int bc2n_trimul_bwd(void* stream, const char* weights_dir, const char* prefix,
+                    int outgoing, int N, const float* pair,
+                    const float* pair_mask, const float* drop_tbl,
+                    const void* save, const float* dpair_out, float* dpair_in);
 
 /* ------------------------------------------------------------------------
  * Dropout with JAX's own bits.  tbl[b*C+c] = keep/keep_rate where
