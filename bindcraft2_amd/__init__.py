@@ -43,6 +43,23 @@ def _declare(L):
         "bc2n_trimul_save_bytes": (sz, [i, i, i]),
         "bc2n_trimul_fwd": (i, [vp, cs, cs, i, i, vp, vp, vp, vp, vp]),
         "bc2n_trimul_bwd": (i, [vp, cs, cs, i, i, vp, vp, vp, vp, vp, vp]),
+        "bc2n_transition_save_bytes": (sz, [c.c_long, i, i]),
+        "bc2n_transition_fwd": (i, [vp, cs, cs, c.c_long, i, vp, vp, vp, vp]),
+        "bc2n_transition_bwd": (i, [vp, cs, cs, c.c_long, i, vp, vp, vp, vp, vp]),
+        "bc2n_opm_save_bytes": (sz, [i, i, i, i]),
+        "bc2n_opm_fwd": (i, [vp, cs, cs, i, i, vp, vp, vp, vp, vp, vp]),
+        "bc2n_opm_bwd": (i, [vp, cs, cs, i, i, vp, vp, vp, vp, vp, vp, vp]),
+        "bc2n_msarow_save_bytes": (sz, [i, i, i, i]),
+        "bc2n_msarow_fwd": (i, [vp, cs, cs, i, i, vp, vp, vp, vp, vp, vp]),
+        "bc2n_msarow_bwd": (i, [vp, cs, cs, i, i, vp, vp, vp, vp, vp, vp, vp, vp]),
+        "bc2n_msacol_save_bytes": (sz, [i, i, i, i]),
+        "bc2n_msacol_fwd": (i, [vp, cs, cs, i, i, vp, vp, vp, vp, vp]),
+        "bc2n_msacol_bwd": (i, [vp, cs, cs, i, i, vp, vp, vp, vp, vp, vp]),
+        "bc2n_evoformer_save_bytes": (sz, [cs, i, i, c.c_int64, c.c_int64]),
+        "bc2n_evoformer_fwd": (i, [vp, vp, vp, vp, vp, vp, i, i, i, i, c.c_int64, c.c_int64,
+                                   c.c_int64, c.c_int64, c.c_int64, c.c_int64, cs, vp, vp, vp, vp]),
+        "bc2n_evoformer_bwd": (i, [vp, vp, vp, vp, vp, vp, vp, vp, i, i, i, i, c.c_int64,
+                                   c.c_int64, c.c_int64, c.c_int64, c.c_int64, cs, vp, vp]),
         "bc2n_dropout_table": (i, [vp, vp, i, i, u32, u32, f]),
         "bc2n_bernoulli_bits": (i, [vp, vp, c.c_long, u32, u32, f]),
         "bc2n_stack_keys": (i, [vp, vp, i, vp]),

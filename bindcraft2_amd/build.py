@@ -12,7 +12,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libbc2n.so")
-SOURCES = ["runtime.cpp", "ln.hip", "flash.hip", "ew.hip", "triattn.hip", "trimul.hip", "capi.cpp"]
+SOURCES = ["runtime.cpp", "ln.hip", "flash.hip", "ew.hip", "triattn.hip", "trimul.hip", "transition.hip",
+           "msa.hip", "opm.hip", "evoformer.hip", "capi.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 FLAGS = [

@@ -1,5 +1,6 @@
 // The C ABI (include/bc2n.h): argument checks, weight lookup, error channel.
 #include "../../include/bc2n.h"
+#include "evoformer.h"
 #include "gemm.h"
 #include "modules.h"
 
@@ -48,6 +49,48 @@ const TriMulW& trimul_w(const char* dir, const char* prefix) {
   TriMulW w = trimul_weights(weights(dir), prefix);
   return g_trimul.emplace(key, w).first->second;
 }
+
+template <class W, class F>
+const W& cached(std::map<std::pair<std::string, std::string>, W>& m, const char* dir,
+                const char* prefix, F make) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto key = std::make_pair(std::string(dir), std::string(prefix));
+  auto it = m.find(key);
+  if (it != m.end()) return it->second;
+  W w = make(weights(dir), std::string(prefix));
+  return m.emplace(key, w).first->second;
+}
+std::map<std::pair<std::string, std::string>, TransW> g_trans;
+std::map<std::pair<std::string, std::string>, OpmW> g_opm;
+std::map<std::pair<std::string, std::string>, MsaRowW> g_row;
+std::map<std::pair<std::string, std::string>, MsaColW> g_col;
+std::map<std::pair<std::string, std::string>, StackW> g_stack;
+
+const StackW& stack_w(const char* dir, int depth, bool pair_only) {
+  const std::string tag = std::to_string(depth) + (pair_only ? ":pair_only" : ":full");
+  return cached(g_stack, dir, tag.c_str(), [&](WeightStore& ws, const std::string&) {
+    return stack_weights(ws, depth, pair_only);
+  });
+}
+
+// Library-owned save-set for detached forwards (save=0) and own_save=1.
+struct OwnSave {
+  void* p = nullptr;
+  size_t n = 0;
+  void* get(hipStream_t st, size_t need) {
+    if (need > n) {
+      if (p) {
+        BC2N_HIP(hipStreamSynchronize(st));
+        BC2N_HIP(hipFree(p));
+        p = nullptr;
+      }
+      BC2N_HIP(hipMalloc(&p, need));
+      n = need;
+    }
+    return p;
+  }
+};
+OwnSave g_own;
 
 void need(bool ok, const char* msg) {
   if (!ok) throw std::invalid_argument(msg);
@@ -110,6 +153,178 @@ int bc2n_trimul_bwd(void* stream, const char* weights_dir, const char* prefix, i
     const TriMulW& w = trimul_w(weights_dir, prefix);
     trimul_bwd(as_stream(stream), w, outgoing != 0, N, pair, pair_mask, drop_tbl, save, dpair_out,
                dpair_in);
+  });
+}
+
+size_t bc2n_transition_save_bytes(long rows, int C, int factor) {
+  return transition_save_bytes(rows, C, factor);
+}
+
+int bc2n_transition_fwd(void* stream, const char* weights_dir, const char* prefix, long rows,
+                        int N, const float* act, const float* drop_tbl, float* act_out,
+                        void* save) {
+  return guarded([&] {
+    need(weights_dir && prefix && act && act_out && save, "null operand");
+    need(act_out != act, "transition: act_out must not alias act");
+    need(rows > 0 && N > 0 && rows % N == 0, "transition: rows must be a multiple of N");
+    const TransW& w = cached(g_trans, weights_dir, prefix, transition_weights);
+    transition_fwd(as_stream(stream), w, rows, N, act, drop_tbl, act_out, save);
+  });
+}
+
+int bc2n_transition_bwd(void* stream, const char* weights_dir, const char* prefix, long rows,
+                        int N, const float* act, const float* drop_tbl, const void* save,
+                        const float* dact_out, float* dact_in) {
+  return guarded([&] {
+    need(weights_dir && prefix && act && save && dact_out && dact_in, "null operand");
+    const TransW& w = cached(g_trans, weights_dir, prefix, transition_weights);
+    transition_bwd(as_stream(stream), w, rows, N, act, drop_tbl, save, dact_out, dact_in);
+  });
+}
+
+size_t bc2n_opm_save_bytes(int S, int N, int O, int C) { return opm_save_bytes(S, N, O, C); }
+
+int bc2n_opm_fwd(void* stream, const char* weights_dir, const char* prefix, int S, int N,
+                 const float* msa, const float* msa_mask, const float* pair,
+                 const float* drop_tbl, float* pair_out, void* save) {
+  return guarded([&] {
+    need(weights_dir && prefix && msa && msa_mask && pair && pair_out && save, "null operand");
+    need(pair_out != pair, "opm: pair_out must not alias pair");
+    const OpmW& w = cached(g_opm, weights_dir, prefix, opm_weights);
+    opm_fwd(as_stream(stream), w, S, N, msa, msa_mask, pair, drop_tbl, pair_out, save);
+  });
+}
+
+int bc2n_opm_bwd(void* stream, const char* weights_dir, const char* prefix, int S, int N,
+                 const float* msa, const float* msa_mask, const float* drop_tbl, const void* save,
+                 const float* dpair, const float* dmsa_out, float* dmsa_in) {
+  return guarded([&] {
+    need(weights_dir && prefix && msa && msa_mask && save && dpair && dmsa_out && dmsa_in,
+         "null operand");
+    const OpmW& w = cached(g_opm, weights_dir, prefix, opm_weights);
+    opm_bwd(as_stream(stream), w, S, N, msa, msa_mask, drop_tbl, save, dpair, dmsa_out, dmsa_in);
+  });
+}
+
+size_t bc2n_msarow_save_bytes(int S, int N, int Cm, int H) { return msarow_save_bytes(S, N, Cm, H); }
+
+int bc2n_msarow_fwd(void* stream, const char* weights_dir, const char* prefix, int S, int N,
+                    const float* msa, const float* msa_mask, const float* pair,
+                    const float* drop_tbl, float* msa_out, void* save) {
+  return guarded([&] {
+    need(weights_dir && prefix && msa && msa_mask && pair && msa_out && save, "null operand");
+    need(msa_out != msa, "msarow: msa_out must not alias msa");
+    const MsaRowW& w = cached(g_row, weights_dir, prefix, msarow_weights);
+    msarow_fwd(as_stream(stream), w, S, N, msa, msa_mask, pair, drop_tbl, msa_out, save);
+  });
+}
+
+int bc2n_msarow_bwd(void* stream, const char* weights_dir, const char* prefix, int S, int N,
+                    const float* msa, const float* msa_mask, const float* pair,
+                    const float* drop_tbl, const void* save, const float* dmsa_out,
+                    float* dmsa_in, float* dpair) {
+  return guarded([&] {
+    need(weights_dir && prefix && msa && msa_mask && pair && save && dmsa_out && dmsa_in && dpair,
+         "null operand");
+    const MsaRowW& w = cached(g_row, weights_dir, prefix, msarow_weights);
+    msarow_bwd(as_stream(stream), w, S, N, msa, msa_mask, pair, drop_tbl, save, dmsa_out, dmsa_in,
+               dpair);
+  });
+}
+
+size_t bc2n_msacol_save_bytes(int S, int N, int Cm, int H) { return msacol_save_bytes(S, N, Cm, H); }
+
+int bc2n_msacol_fwd(void* stream, const char* weights_dir, const char* prefix, int S, int N,
+                    const float* msa, const float* msa_mask, const float* drop_tbl,
+                    float* msa_out, void* save) {
+  return guarded([&] {
+    need(weights_dir && prefix && msa && msa_mask && msa_out && save, "null operand");
+    need(msa_out != msa, "msacol: msa_out must not alias msa");
+    const MsaColW& w = cached(g_col, weights_dir, prefix, msacol_weights);
+    msacol_fwd(as_stream(stream), w, S, N, msa, msa_mask, drop_tbl, msa_out, save);
+  });
+}
+
+int bc2n_msacol_bwd(void* stream, const char* weights_dir, const char* prefix, int S, int N,
+                    const float* msa, const float* msa_mask, const float* drop_tbl,
+                    const void* save, const float* dmsa_out, float* dmsa_in) {
+  return guarded([&] {
+    need(weights_dir && prefix && msa && msa_mask && save && dmsa_out && dmsa_in, "null operand");
+    const MsaColW& w = cached(g_col, weights_dir, prefix, msacol_weights);
+    msacol_bwd(as_stream(stream), w, S, N, msa, msa_mask, drop_tbl, save, dmsa_out, dmsa_in);
+  });
+}
+
+// ------------------------------------------------------------ the stack
+
+size_t bc2n_evoformer_save_bytes(const char* weights_dir, int N, int S, int64_t depth,
+                                 int64_t pair_only) {
+  size_t n = 0;
+  if (guarded([&] {
+        need(weights_dir != nullptr, "weights_dir required");
+        const StackW& w = stack_w(weights_dir, (int)depth, pair_only != 0);
+        n = stack_save_bytes(w, N, S, (int)depth) + 256;
+      }) != 0)
+    return 0;
+  return n;
+}
+
+static const uint32_t* stack_key(hipStream_t st, const uint32_t* seed, int seed_len,
+                                 uint32_t* scratch) {
+  if (seed_len == 3) return seed;  // [k0, k1, enabled]: jax.random.key_data
+  key_from_bits(st, seed, scratch);  // [bits, enabled]: PRNGKey(bits)
+  return scratch;
+}
+
+int bc2n_evoformer_fwd(void* stream, const float* pair, const float* msa, const float* pair_mask,
+                       const float* msa_mask, const uint32_t* seed, int seed_len, int N, int S,
+                       int Cm, int64_t depth, int64_t save, int64_t pair_only, int64_t own_save,
+                       int64_t opm_first, int64_t dropout, const char* weights_dir,
+                       float* pair_out, float* msa_out, void* psave, void* msave) {
+  (void)msave;
+  return guarded([&] {
+    hipStream_t st = as_stream(stream);
+    need(weights_dir && pair && pair_mask && pair_out, "null operand");
+    need(opm_first == 1, "evoformer: only outer_product_mean.first=True (AF2-multimer) is built");
+    need(seed_len == 2 || seed_len == 3, "evoformer: seed must be u32[2] or u32[3]");
+    need(!dropout || seed, "evoformer: dropout needs the seed operand");
+    need(pair_only || (msa && msa_mask && msa_out), "evoformer: msa operands required");
+    need(pair_out != pair && (pair_only || msa_out != msa), "evoformer: outputs must not alias inputs");
+    const StackW& w = stack_w(weights_dir, (int)depth, pair_only != 0);
+    if (!pair_only) need(Cm == w.blocks[0].row.a.Cin, "evoformer: msa channel width mismatch");
+    const size_t bytes = stack_save_bytes(w, N, S, (int)depth) + 256;
+    void* sv = (save == 0 || own_save != 0 || psave == nullptr) ? g_own.get(st, bytes) : psave;
+    uint32_t* keyslot = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(sv) + bytes - 256);
+    const uint32_t* key = dropout ? stack_key(st, seed, seed_len, keyslot) : nullptr;
+    const uint32_t* enabled = dropout ? seed + (seed_len - 1) : nullptr;
+    stack_fwd(st, w, N, S, (int)depth, pair, msa, pair_mask, msa_mask, key, enabled, dropout != 0,
+              pair_out, msa_out, sv);
+    if (pair_only && msa && msa_out && msa_out != msa && Cm > 0)
+      BC2N_HIP(hipMemcpyAsync(msa_out, msa, (size_t)S * N * Cm * 4, hipMemcpyDeviceToDevice, st));
+  });
+}
+
+int bc2n_evoformer_bwd(void* stream, const float* ct_pair, const float* ct_msa,
+                       const float* pair_mask, const float* msa_mask, const void* psave,
+                       const void* msave, const uint32_t* seed, int seed_len, int N, int S,
+                       int Cm, int64_t depth, int64_t pair_only, int64_t own_save,
+                       int64_t opm_first, int64_t dropout, const char* weights_dir,
+                       float* dpair, float* dmsa) {
+  (void)msave;
+  (void)seed;
+  (void)seed_len;
+  return guarded([&] {
+    hipStream_t st = as_stream(stream);
+    need(weights_dir && ct_pair && pair_mask && dpair, "null operand");
+    need(opm_first == 1, "evoformer: only outer_product_mean.first=True (AF2-multimer) is built");
+    need(pair_only || (ct_msa && msa_mask && dmsa), "evoformer: msa operands required");
+    const StackW& w = stack_w(weights_dir, (int)depth, pair_only != 0);
+    const size_t bytes = stack_save_bytes(w, N, S, (int)depth) + 256;
+    const void* sv = (own_save != 0 || psave == nullptr) ? g_own.get(st, bytes) : psave;
+    stack_bwd(st, w, N, S, (int)depth, pair_mask, msa_mask, dropout != 0, sv, ct_pair, ct_msa,
+              dpair, dmsa);
+    if (pair_only && dmsa && ct_msa && dmsa != ct_msa && Cm > 0)
+      BC2N_HIP(hipMemcpyAsync(dmsa, ct_msa, (size_t)S * N * Cm * 4, hipMemcpyDeviceToDevice, st));
   });
 }
 

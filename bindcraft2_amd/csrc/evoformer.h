@@ -1,0 +1,45 @@
+// Evoformer block / stack (host orchestration over the module kernels).
+#pragma once
+#include "modules.h"
+#include <vector>
+
+namespace bc2n {
+
+struct BlockW {
+  OpmW opm;
+  MsaRowW row;
+  MsaColW col;
+  TransW mtr;
+  TriMulW tmo, tmi;
+  TriAttnW tas, tae;
+  TransW ptr;
+  const float* opm_b = nullptr;  // outer_product_mean/output_b (pair_only constant)
+};
+
+struct StackW {
+  bool pair_only = false;
+  std::vector<BlockW> blocks;
+};
+
+BlockW block_weights(WeightStore& ws, const std::string& prefix, bool pair_only);
+// Blocks param/block0 .. param/block{depth-1} of a weights directory.
+StackW stack_weights(WeightStore& ws, int depth, bool pair_only,
+                     const std::string& root = "param/");
+
+// Bytes of the save-set a forward with these shapes writes and the backward
+// reads (every block's carries and module save-sets, the dropout tables).
+size_t stack_save_bytes(const StackW& w, int N, int S, int depth);
+
+// Forward of `depth` blocks.  key = stack key (2 x u32, device), enabled =
+// device u32 flag (may be null = on); dropout=false skips every mask.
+void stack_fwd(hipStream_t st, const StackW& w, int N, int S, int depth, const float* pair,
+               const float* msa, const float* pmask, const float* mmask, const uint32_t* key,
+               const uint32_t* enabled, bool dropout, float* pair_out, float* msa_out,
+               void* save);
+// Backward: cotangents of the stack outputs in, of the stack inputs out.
+// Everything else it needs (inputs, carries, dropout tables) is in `save`.
+void stack_bwd(hipStream_t st, const StackW& w, int N, int S, int depth, const float* pmask,
+               const float* mmask, bool dropout, const void* save, const float* ct_pair,
+               const float* ct_msa, float* dpair, float* dmsa);
+
+}  // namespace bc2n

@@ -1,0 +1,274 @@
+// Evoformer block and stack, forward and backward, with JAX-exact dropout.
+//
+// Block order (modules.py:1278-1391, outer_product_mean.first=True):
+//   pair += OPM(msa)               msa += RowAttn(msa, pair)
+//   msa  += ColAttn(msa)           msa += MsaTransition(msa)
+//   pair += TriMulOut, TriMulIn, TriAttnStart, TriAttnEnd, PairTransition
+// each wrapped in dropout_wrapper with the shared per-row/per-column mask of
+// its config (config.py:386-460).  pair_only blocks (the extra-MSA stack with
+// its MSA mask all zero, native/block.cuh:79-91) reduce the MSA side to OPM's
+// constant output_b/1e-3 and skip the MSA modules.
+//
+// The stack keeps every block's carries and module save-sets (no replay):
+// 288 GB of HBM holds them at the lengths the configs use.  Dropout keys are
+// derived on the device from the stack key by JAX's split chain
+// (modules_multimer.py:622-641), turned into shared-mask tables once per
+// forward and kept in the save-set, so the backward applies the identical
+// masks and a reseed is a new value in the seed operand, not a recompile.
+#include "evoformer.h"
+
+namespace bc2n {
+
+namespace {
+
+// module indices of a block's 9 dropout keys (modules.py:1308-1390 order)
+enum { K_OPM = 0, K_ROW, K_COL, K_MTR, K_TMO, K_TMI, K_TAS, K_TAE, K_PTR };
+
+size_t al256(size_t n) { return (n + 255) & ~size_t(255); }
+
+struct Layout {
+  int N = 0, S = 0, Cz = 0, Cm = 0, depth = 0;
+  bool pair_only = false;
+  size_t opm = 0, row = 0, col = 0, mtr = 0, tmo = 0, tmi = 0, tas = 0, tae = 0, ptr = 0;
+  size_t pair_bytes = 0, msa_bytes = 0, block_bytes = 0;
+  size_t tbl_per_block = 0;  // floats
+  // offsets of the save-set regions
+  size_t off_carry_p = 0, off_carry_m = 0, off_msa_in = 0, off_tbl = 0, off_keys = 0, total = 0;
+};
+
+Layout layout(const StackW& w, int N, int S, int depth) {
+  Layout L;
+  L.N = N; L.S = S; L.depth = depth; L.pair_only = w.pair_only;
+  const BlockW& b = w.blocks[0];
+  L.Cz = b.tmo.C;
+  L.Cm = w.pair_only ? 0 : b.row.a.Cin;
+  const long M = (long)N * N;
+  L.tmo = trimul_save_bytes(N, b.tmo.C, b.tmo.I);
+  L.tmi = trimul_save_bytes(N, b.tmi.C, b.tmi.I);
+  L.tas = triattn_save_bytes(N, b.tas.C, b.tas.H);
+  L.tae = triattn_save_bytes(N, b.tae.C, b.tae.H);
+  L.ptr = transition_save_bytes(M, b.ptr.C, b.ptr.F);
+  if (!w.pair_only) {
+    L.opm = opm_save_bytes(S, N, b.opm.O, b.opm.C);
+    L.row = msarow_save_bytes(S, N, b.row.a.Cin, b.row.a.H);
+    L.col = msacol_save_bytes(S, N, b.col.a.Cin, b.col.a.H);
+    L.mtr = transition_save_bytes((long)S * N, b.mtr.C, b.mtr.F);
+  }
+  L.pair_bytes = al256((size_t)M * L.Cz * 4);
+  L.msa_bytes = w.pair_only ? 0 : al256((size_t)S * N * L.Cm * 4);
+  // per block: module save-sets + the pair after opm, tmo, tmi, tas, tae and
+  // the msa after row and col attention
+  L.block_bytes = L.opm + L.row + L.col + L.mtr + L.tmo + L.tmi + L.tas + L.tae + L.ptr +
+                  5 * L.pair_bytes + 2 * L.msa_bytes;
+  L.tbl_per_block = (size_t)N * L.Cm + 4 * (size_t)N * L.Cz;
+  L.off_carry_p = (size_t)depth * L.block_bytes;
+  L.off_carry_m = L.off_carry_p + (size_t)(depth - 1) * L.pair_bytes;
+  // the stack's msa input, kept for the backward of block 0
+  L.off_msa_in = L.off_carry_m + (size_t)(depth - 1) * L.msa_bytes;
+  L.off_tbl = L.off_msa_in + L.msa_bytes;
+  L.off_keys = L.off_tbl + al256((size_t)depth * L.tbl_per_block * 4);
+  L.total = L.off_keys + al256((size_t)depth * 9 * 2 * 4);
+  return L;
+}
+
+struct BlockPtrs {
+  char *opm, *row, *col, *mtr, *tmo, *tmi, *tas, *tae, *ptr;
+  float *p1, *p2, *p3, *p4, *p5;  // pair after opm, tmo, tmi, tas, tae
+  float *m1, *m2;                 // msa after row, col
+};
+
+BlockPtrs carve(const Layout& L, char* base) {
+  BlockPtrs p{};
+  char* c = base;
+  auto take = [&](size_t n) { char* r = c; c += n; return r; };
+  p.opm = take(L.opm); p.row = take(L.row); p.col = take(L.col); p.mtr = take(L.mtr);
+  p.tmo = take(L.tmo); p.tmi = take(L.tmi); p.tas = take(L.tas); p.tae = take(L.tae);
+  p.ptr = take(L.ptr);
+  p.p1 = reinterpret_cast<float*>(take(L.pair_bytes));
+  p.p2 = reinterpret_cast<float*>(take(L.pair_bytes));
+  p.p3 = reinterpret_cast<float*>(take(L.pair_bytes));
+  p.p4 = reinterpret_cast<float*>(take(L.pair_bytes));
+  p.p5 = reinterpret_cast<float*>(take(L.pair_bytes));
+  p.m1 = reinterpret_cast<float*>(take(L.msa_bytes));
+  p.m2 = reinterpret_cast<float*>(take(L.msa_bytes));
+  return p;
+}
+
+// pair_out = pair_in + c with the per-channel constant c = output_b / 1e-3
+// (OPM of a fully masked MSA: left = right = 0, norm = 0).  OPM's dropout
+// rate is 0, and its backward on the pair is the identity.
+__global__ void add_const_kernel(const float* __restrict__ in, float* __restrict__ out,
+                                 const float* __restrict__ b, long M, int C) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= M * C) return;
+  out[i] = in[i] + b[i % C] / 1e-3f;
+}
+
+struct Tables {
+  const float* base = nullptr;
+  const Layout* L = nullptr;
+  const float* row(int b) const { return base ? base + b * L->tbl_per_block : nullptr; }
+  const float* pair(int b, int k) const {
+    return base ? base + b * L->tbl_per_block + (size_t)L->N * L->Cm + (size_t)k * L->N * L->Cz
+                : nullptr;
+  }
+};
+
+struct Frame {
+  const float *pin, *min;
+  float *pout, *mout;
+};
+
+Frame frame(const Layout& L, char* save, int b, const float* pair, const float* msa,
+            float* pair_out, float* msa_out) {
+  Frame f;
+  auto cp = [&](int k) { return reinterpret_cast<float*>(save + L.off_carry_p + (size_t)k * L.pair_bytes); };
+  auto cm = [&](int k) { return reinterpret_cast<float*>(save + L.off_carry_m + (size_t)k * L.msa_bytes); };
+  f.pin = b == 0 ? pair : cp(b - 1);
+  f.pout = b == L.depth - 1 ? pair_out : cp(b);
+  if (L.pair_only) {
+    f.min = msa;
+    f.mout = nullptr;
+  } else {
+    // msa == nullptr: the backward, which reads block 0's input from the save-set
+    f.min = b == 0 ? (msa ? msa : reinterpret_cast<float*>(save + L.off_msa_in)) : cm(b - 1);
+    f.mout = b == L.depth - 1 ? msa_out : cm(b);
+  }
+  return f;
+}
+
+void block_fwd(hipStream_t st, const BlockW& B, const Layout& L, int b, const Tables& t,
+               const Frame& f, const float* pmask, const float* mmask, char* save) {
+  BlockPtrs p = carve(L, save);
+  const int N = L.N, S = L.S;
+  const long M = (long)N * N;
+  if (L.pair_only) {
+    KTimed kt("block.opm_const", st);
+    hipLaunchKernelGGL(add_const_kernel, dim3((unsigned)((M * L.Cz + 255) / 256)), dim3(256), 0,
+                       st, f.pin, p.p1, B.opm_b, M, L.Cz);
+  } else {
+    opm_fwd(st, B.opm, S, N, f.min, mmask, f.pin, nullptr, p.p1, p.opm);
+    msarow_fwd(st, B.row, S, N, f.min, mmask, p.p1, t.row(b), p.m1, p.row);
+    msacol_fwd(st, B.col, S, N, p.m1, mmask, nullptr, p.m2, p.col);
+    transition_fwd(st, B.mtr, (long)S * N, N, p.m2, nullptr, f.mout, p.mtr);
+  }
+  trimul_fwd(st, B.tmo, true, N, p.p1, pmask, t.pair(b, 0), p.p2, p.tmo);
+  trimul_fwd(st, B.tmi, false, N, p.p2, pmask, t.pair(b, 1), p.p3, p.tmi);
+  triattn_fwd(st, B.tas, false, N, p.p3, pmask, t.pair(b, 2), p.p4, p.tas);
+  triattn_fwd(st, B.tae, true, N, p.p4, pmask, t.pair(b, 3), p.p5, p.tae);
+  transition_fwd(st, B.ptr, M, N, p.p5, nullptr, f.pout, p.ptr);
+}
+
+// dpair / dmsa: cotangents of the block outputs on entry, of its inputs on
+// exit (updated in place).
+void block_bwd(hipStream_t st, const BlockW& B, const Layout& L, int b, const Tables& t,
+               const Frame& f, const float* pmask, const float* mmask, char* save, float* dpair,
+               float* dmsa) {
+  BlockPtrs p = carve(L, save);
+  const int N = L.N, S = L.S;
+  const long M = (long)N * N;
+  transition_bwd(st, B.ptr, M, N, p.p5, nullptr, p.ptr, dpair, dpair);
+  triattn_bwd(st, B.tae, true, N, p.p4, pmask, t.pair(b, 3), p.tae, dpair, dpair);
+  triattn_bwd(st, B.tas, false, N, p.p3, pmask, t.pair(b, 2), p.tas, dpair, dpair);
+  trimul_bwd(st, B.tmi, false, N, p.p2, pmask, t.pair(b, 1), p.tmi, dpair, dpair);
+  trimul_bwd(st, B.tmo, true, N, p.p1, pmask, t.pair(b, 0), p.tmo, dpair, dpair);
+  if (!L.pair_only) {
+    transition_bwd(st, B.mtr, (long)S * N, N, p.m2, nullptr, p.mtr, dmsa, dmsa);
+    msacol_bwd(st, B.col, S, N, p.m1, mmask, nullptr, p.col, dmsa, dmsa);
+    msarow_bwd(st, B.row, S, N, f.min, mmask, p.p1, t.row(b), p.row, dmsa, dmsa, dpair);
+    opm_bwd(st, B.opm, S, N, f.min, mmask, nullptr, p.opm, dpair, dmsa, dmsa);
+  }
+}
+
+void stack_check(const StackW& w, int N, int S, int depth) {
+  if (depth <= 0 || depth > (int)w.blocks.size()) throw std::runtime_error("stack: bad depth");
+  if (N <= 0 || N % 32 != 0) throw std::runtime_error("stack: N must be a positive multiple of 32");
+  if (!w.pair_only && (S <= 0 || S > 32)) throw std::runtime_error("stack: S must be in 1..32");
+}
+
+}  // namespace
+
+BlockW block_weights(WeightStore& ws, const std::string& P, bool pair_only) {
+  BlockW b;
+  b.tmo = trimul_weights(ws, P + "triangle_multiplication_outgoing/");
+  b.tmi = trimul_weights(ws, P + "triangle_multiplication_incoming/");
+  b.tas = triattn_weights(ws, P + "triangle_attention_starting_node/");
+  b.tae = triattn_weights(ws, P + "triangle_attention_ending_node/");
+  b.ptr = transition_weights(ws, P + "pair_transition/");
+  b.opm_b = ws.f32(P + "outer_product_mean/output_b");
+  if (!pair_only) {
+    b.opm = opm_weights(ws, P + "outer_product_mean/");
+    b.row = msarow_weights(ws, P + "msa_row_attention_with_pair_bias/");
+    b.col = msacol_weights(ws, P + "msa_column_attention/");
+    b.mtr = transition_weights(ws, P + "msa_transition/");
+  }
+  return b;
+}
+
+StackW stack_weights(WeightStore& ws, int depth, bool pair_only, const std::string& root) {
+  StackW s;
+  s.pair_only = pair_only;
+  for (int b = 0; b < depth; ++b)
+    s.blocks.push_back(block_weights(ws, root + "block" + std::to_string(b) + "/", pair_only));
+  return s;
+}
+
+size_t stack_save_bytes(const StackW& w, int N, int S, int depth) {
+  stack_check(w, N, S, depth);
+  return layout(w, N, S, depth).total;
+}
+
+void stack_fwd(hipStream_t st, const StackW& w, int N, int S, int depth, const float* pair,
+               const float* msa, const float* pmask, const float* mmask, const uint32_t* key,
+               const uint32_t* enabled, bool dropout, float* pair_out, float* msa_out,
+               void* save) {
+  stack_check(w, N, S, depth);
+  const Layout L = layout(w, N, S, depth);
+  char* sv = reinterpret_cast<char*>(save);
+  Tables t;
+  t.L = &L;
+  if (dropout) {
+    if (!key) throw std::runtime_error("stack: dropout needs a key");
+    float* tbl = reinterpret_cast<float*>(sv + L.off_tbl);
+    uint32_t* keys = reinterpret_cast<uint32_t*>(sv + L.off_keys);
+    KTimed kt("stack.dropout_tables", st);
+    stack_keys(st, key, depth, keys);
+    const int pm[4] = {K_TMO, K_TMI, K_TAS, K_TAE};
+    for (int b = 0; b < depth; ++b) {
+      float* tb = tbl + b * L.tbl_per_block;
+      if (!L.pair_only)
+        dropout_table_dev(st, tb, N, L.Cm, keys + (b * 9 + K_ROW) * 2, enabled, 1.0f - 0.15f);
+      for (int k = 0; k < 4; ++k)
+        dropout_table_dev(st, tb + (size_t)N * L.Cm + (size_t)k * N * L.Cz, N, L.Cz,
+                          keys + (b * 9 + pm[k]) * 2, enabled, 1.0f - 0.25f);
+    }
+    t.base = tbl;
+  }
+  if (!L.pair_only)
+    BC2N_HIP(hipMemcpyAsync(sv + L.off_msa_in, msa, (size_t)S * N * L.Cm * 4,
+                            hipMemcpyDeviceToDevice, st));
+  for (int b = 0; b < depth; ++b)
+    block_fwd(st, w.blocks[b], L, b, t, frame(L, sv, b, pair, msa, pair_out, msa_out), pmask,
+              mmask, sv + (size_t)b * L.block_bytes);
+}
+
+void stack_bwd(hipStream_t st, const StackW& w, int N, int S, int depth, const float* pmask,
+               const float* mmask, bool dropout, const void* save, const float* ct_pair,
+               const float* ct_msa, float* dpair, float* dmsa) {
+  stack_check(w, N, S, depth);
+  const Layout L = layout(w, N, S, depth);
+  char* sv = const_cast<char*>(reinterpret_cast<const char*>(save));
+  Tables t;
+  t.L = &L;
+  if (dropout) t.base = reinterpret_cast<const float*>(sv + L.off_tbl);
+  const long M = (long)N * N;
+  if (dpair != ct_pair)
+    BC2N_HIP(hipMemcpyAsync(dpair, ct_pair, (size_t)M * L.Cz * 4, hipMemcpyDeviceToDevice, st));
+  if (!L.pair_only && dmsa != ct_msa)
+    BC2N_HIP(hipMemcpyAsync(dmsa, ct_msa, (size_t)S * N * L.Cm * 4, hipMemcpyDeviceToDevice, st));
+  for (int b = depth - 1; b >= 0; --b)
+    block_bwd(st, w.blocks[b], L, b, t, frame(L, sv, b, nullptr, nullptr, nullptr, nullptr),
+              pmask, mmask, sv + (size_t)b * L.block_bytes, dpair, dmsa);
+}
+
+}  // namespace bc2n

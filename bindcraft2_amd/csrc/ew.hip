@@ -88,6 +88,19 @@ __global__ void stack_keys_kernel(const uint32_t* __restrict__ seed, int depth,
   }
 }
 
+// jax.random.PRNGKey(bits) = (0, bits) for the reference's 2-word seed
+// operand [bits, enabled] (modules_multimer.py:660-667).
+__global__ void key_from_bits_kernel(const uint32_t* __restrict__ seed, uint32_t* __restrict__ out) {
+  if (threadIdx.x == 0) {
+    out[0] = 0u;
+    out[1] = seed[0];
+  }
+}
+
+void key_from_bits(hipStream_t st, const uint32_t* seed, uint32_t* out) {
+  hipLaunchKernelGGL(key_from_bits_kernel, dim3(1), dim3(64), 0, st, seed, out);
+}
+
 void stack_keys(hipStream_t st, const uint32_t* seed, int depth, uint32_t* out) {
   hipLaunchKernelGGL(stack_keys_kernel, dim3(1), dim3(64), 0, st, seed, depth, out);
 }

@@ -72,6 +72,8 @@ void bernoulli_bits(hipStream_t st, uint8_t* out, long n, uint32_t k0, uint32_t 
 // Per-module keys of a `depth`-layer Evoformer stack from the stack key
 // seed[0..1]: out[(layer*9+module)*2 + {0,1}].
 void stack_keys(hipStream_t st, const uint32_t* seed, int depth, uint32_t* out);
+// out[0..1] = (0, seed[0]): PRNGKey of a 32-bit seed word, on the device.
+void key_from_bits(hipStream_t st, const uint32_t* seed, uint32_t* out);
 
 // ---------------------------------------------------------------- glue
 // out[m][c] = bf16(dy[src(m)][c] * tbl[(m % nt)*C + c]); src transposes the

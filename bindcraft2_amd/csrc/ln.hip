@@ -109,7 +109,12 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(
   const long src = ln_src_row(m, nt);
   float xv[8], g[8];
   load8f<InT>(x + src * C + c0, xv);
-  load8f<float>(dy + m * C + c0, g);
+  if (dy) {
+    load8f<float>(dy + m * C + c0, g);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) g[e] = 0.f;
+  }
   for (int h = 0; h < H; ++h) {
     const float db = dbias[(long)h * M + m];
 #pragma unroll

@@ -52,4 +52,65 @@ void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
                 const float* mask, const float* tbl, const void* save, const float* dout,
                 float* din);
 
+// ----------------------------------------------------------------- transition
+// modules.py:252-305; pair (rows = N*N) and MSA (rows = S*N) alike.  `nt` is
+// the residue count: the shared dropout table row of act row m is m % nt.
+struct TransW {
+  int C = 0, F = 0;
+  const float *ln_g = nullptr, *ln_b = nullptr, *b1 = nullptr, *b2 = nullptr;
+  const bf16 *w1 = nullptr, *w1_t = nullptr, *w2 = nullptr, *w2_t = nullptr;
+};
+TransW transition_weights(WeightStore& ws, const std::string& prefix);
+size_t transition_save_bytes(long rows, int C, int F);
+void transition_fwd(hipStream_t st, const TransW& w, long rows, int nt, const float* act_in,
+                    const float* tbl, float* act_out, void* save);
+void transition_bwd(hipStream_t st, const TransW& w, long rows, int nt, const float* act_in,
+                    const float* tbl, const void* save, const float* dout, float* din);
+
+// ------------------------------------------------------------- MSA attention
+struct AttnW {
+  int Cin = 0, Cout = 0, H = 0, D = 0;
+  const float *ln_g = nullptr, *ln_b = nullptr, *bqkvg = nullptr, *bo = nullptr;
+  const bf16 *wqkvg = nullptr, *wqkvg_t = nullptr, *wo = nullptr, *wo_t = nullptr;
+};
+struct MsaRowW {
+  AttnW a;
+  int Cz = 0;
+  const float *pn_g = nullptr, *pn_b = nullptr, *w2d = nullptr;
+};
+struct MsaColW {
+  AttnW a;
+};
+MsaRowW msarow_weights(WeightStore& ws, const std::string& prefix);
+MsaColW msacol_weights(WeightStore& ws, const std::string& prefix);
+size_t msarow_save_bytes(int S, int N, int Cm, int H);
+size_t msacol_save_bytes(int S, int N, int Cm, int H);
+void msarow_fwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa_in,
+                const float* msa_mask, const float* pair, const float* tbl, float* msa_out,
+                void* save);
+// dpair is accumulated (+=), dmsa_in = dmsa_out + J^T(...)
+void msarow_bwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa_in,
+                const float* msa_mask, const float* pair, const float* tbl, const void* save,
+                const float* dmsa_out, float* dmsa_in, float* dpair);
+void msacol_fwd(hipStream_t st, const MsaColW& w, int S, int N, const float* msa_in,
+                const float* msa_mask, const float* tbl, float* msa_out, void* save);
+void msacol_bwd(hipStream_t st, const MsaColW& w, int S, int N, const float* msa_in,
+                const float* msa_mask, const float* tbl, const void* save,
+                const float* dmsa_out, float* dmsa_in);
+
+// --------------------------------------------------------- outer product mean
+struct OpmW {
+  int Cm = 0, O = 0, C = 0;
+  const float *ln_g = nullptr, *ln_b = nullptr, *blr = nullptr, *bo = nullptr;
+  const bf16 *wlr = nullptr, *wlr_t = nullptr, *wt = nullptr, *wt2 = nullptr;
+};
+OpmW opm_weights(WeightStore& ws, const std::string& prefix);
+size_t opm_save_bytes(int S, int N, int O, int C);
+void opm_fwd(hipStream_t st, const OpmW& w, int S, int N, const float* msa, const float* msa_mask,
+             const float* pair_in, const float* tbl, float* pair_out, void* save);
+// dmsa_in = dmsa_out + J^T(tbl * dpair)
+void opm_bwd(hipStream_t st, const OpmW& w, int S, int N, const float* msa, const float* msa_mask,
+             const float* tbl, const void* save, const float* dpair, const float* dmsa_out,
+             float* dmsa_in);
+
 }  // namespace bc2n

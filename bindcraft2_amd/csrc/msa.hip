@@ -1,0 +1,505 @@
+// MSA row attention with pair bias and MSA column attention, fwd + bwd.
+//
+// Row attention (H=8, D=32 over the N residues of each of the S rows):
+//   LN(msa) -> xn;  LN(pair) fused with the [C_z -> H] bias projection;
+//   GEMM qkvg; flash attention (rows = S, mask = msa_mask[s][k]); GEMM out +
+//   residual (+ shared per-row dropout).  The backward returns both d(msa)
+//   and d(pair) (through the bias projection and the pair LN).
+// Column attention (H=8, D=32 over the S rows of each residue): same
+//   projections; the S x S attention per (residue, head) is tiny (S <= 32)
+//   and runs one wave per (residue, head) in registers.
+// Reference: modules.py:500-563 (MSARowAttentionWithPairBias), :566-616
+// (MSAColumnAttention); native/msarow.cuh:208-441, native/msacol.cuh:247-361.
+#include "gemm.h"
+#include "modules.h"
+#include <cmath>
+
+namespace bc2n {
+
+namespace {
+
+struct EpiQKVG2 {
+  bf16* C;
+  long ldc;
+  const float* bias;
+  float qscale;
+  int qcols, N;
+  template <int TN>
+  __device__ __forceinline__ void apply(int, int m, int n, const float (&v)[TN]) const {
+    bf16* row = C + (long)m * ldc;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int c = n + 16 * j;
+      if (c >= N) continue;
+      float x = v[j] + bias[c];
+      if (c < qcols) x *= qscale;
+      row[c] = (bf16)x;
+    }
+  }
+};
+
+struct EpiAddRows2 {
+  const float* in;
+  float* out;
+  const float* bias;
+  const float* tbl;
+  int nt, C;
+  template <int TN>
+  __device__ __forceinline__ void apply(int, int m, int n, const float (&v)[TN]) const {
+    const float* t = tbl ? tbl + (long)(m % nt) * C : nullptr;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int c = n + 16 * j;
+      if (c >= C) continue;
+      float x = v[j] + bias[c];
+      if (t) x *= t[c];
+      const long o = (long)m * C + c;
+      out[o] = in[o] + x;
+    }
+  }
+};
+
+// Gated-attention weights shared by the row and column modules:
+// [Wq|Wk|Wv|Wg] (C_in x 4HD) in both orientations, gate bias, output.
+void attn_weights(WeightStore& ws, const std::string& P, AttnW& w) {
+  const HostTensor& qw = ws.host(P + "attention/query_w");
+  w.Cin = qw.shape[0];
+  w.H = qw.shape[1];
+  w.D = qw.shape[2];
+  const int C = w.Cin, HD = w.H * w.D;
+  const HostTensor& ow = ws.host(P + "attention/output_w");  // [H, D, Cout]
+  w.Cout = ow.shape[2];
+  const char* parts[4] = {"attention/query_w", "attention/key_w", "attention/value_w",
+                          "attention/gating_w"};
+  auto cat = [&]() {
+    std::vector<float> c((size_t)C * 4 * HD);
+    for (int p = 0; p < 4; ++p) {
+      const HostTensor& t = ws.host(P + parts[p]);
+      for (int r = 0; r < C; ++r)
+        for (int j = 0; j < HD; ++j) c[(size_t)r * 4 * HD + p * HD + j] = t.data[(size_t)r * HD + j];
+    }
+    return c;
+  };
+  w.wqkvg = ws.derived<bf16>("attn.wqkvg:" + P, [&] { return to_bf16(cat()); });
+  w.wqkvg_t = ws.derived<bf16>("attn.wqkvg_t:" + P, [&] {
+    std::vector<float> c = cat();
+    return transpose_bf16(c.data(), C, 4 * HD);
+  });
+  w.bqkvg = ws.derived<float>("attn.bqkvg:" + P, [&] {
+    std::vector<float> b((size_t)4 * HD, 0.f);
+    const HostTensor& gb = ws.host(P + "attention/gating_b");
+    for (int j = 0; j < HD; ++j) b[3 * HD + j] = gb.data[j];
+    return b;
+  });
+  w.wo = ws.derived<bf16>("attn.wo:" + P, [&] { return to_bf16(ow.data); });
+  w.wo_t = ws.derived<bf16>("attn.wo_t:" + P, [&] { return transpose_bf16(ow.data.data(), HD, w.Cout); });
+  w.bo = ws.f32(P + "attention/output_b");
+  w.ln_g = ws.f32(P + "query_norm/scale");
+  w.ln_b = ws.f32(P + "query_norm/offset");
+}
+
+// ------------------------------------------------- small-S column attention
+// One wave per (residue j, head h); lane s_q < S owns one query row over all
+// S keys (S <= 32).  q already carries D^-1/2 (no log2 scale here: scores
+// are in natural units, clipped as the reference does); the mask of key row
+// s is msa_mask[s][j].
+constexpr int SA_D = 32;
+
+__global__ __launch_bounds__(64) void small_attn_fwd_kernel(
+    const bf16* __restrict__ qkvg, long ld, int S, int N, int H,
+    const float* __restrict__ mask, bf16* __restrict__ o, bf16* __restrict__ og, long ldo,
+    float* __restrict__ lse) {
+  const int j = blockIdx.x / H, h = blockIdx.x % H;
+  const int lane = threadIdx.x;
+  const int HD = H * SA_D;
+  // every lane handles one query row (lane < S) over all keys
+  if (lane >= S) return;
+  const int sq = lane;
+  const bf16* q = qkvg + ((long)sq * N + j) * ld + h * SA_D;
+  float qv[SA_D];
+#pragma unroll
+  for (int d = 0; d < SA_D; ++d) qv[d] = (float)q[d];
+  float mx = -INFINITY;
+  float sc[32];
+  for (int sk = 0; sk < S; ++sk) {
+    const bf16* k = qkvg + ((long)sk * N + j) * ld + HD + h * SA_D;
+    float s = 0.f;
+#pragma unroll
+    for (int d = 0; d < SA_D; ++d) s += qv[d] * (float)k[d];
+    const float mb = MASK_BIAS * (mask[(long)sk * N + j] - 1.f);
+    s = fminf(fmaxf(s + mb, -LOGIT_CLIP), LOGIT_CLIP);
+    sc[sk] = s;
+    mx = fmaxf(mx, s);
+  }
+  float sum = 0.f;
+  for (int sk = 0; sk < S; ++sk) {
+    sc[sk] = __expf(sc[sk] - mx);
+    sum += sc[sk];
+  }
+  const float inv = 1.f / sum;
+  float acc[SA_D];
+#pragma unroll
+  for (int d = 0; d < SA_D; ++d) acc[d] = 0.f;
+  for (int sk = 0; sk < S; ++sk) {
+    const bf16* v = qkvg + ((long)sk * N + j) * ld + 2 * HD + h * SA_D;
+    const float p = sc[sk] * inv;
+#pragma unroll
+    for (int d = 0; d < SA_D; ++d) acc[d] += p * (float)v[d];
+  }
+  const long row = (long)sq * N + j;
+  const bf16* g = qkvg + row * ld + 3 * HD + h * SA_D;
+#pragma unroll
+  for (int d = 0; d < SA_D; ++d) {
+    o[row * ldo + h * SA_D + d] = (bf16)acc[d];
+    og[row * ldo + h * SA_D + d] = (bf16)(acc[d] * sigmoidf_((float)g[d]));
+  }
+  lse[((long)j * H + h) * S + sq] = mx + __logf(sum);
+}
+
+// Backward, same decomposition; lane = query row.  dK/dV sums over queries
+// go through LDS atomics of the one wave that owns the (j,h) pair.
+__global__ __launch_bounds__(64) void small_attn_bwd_kernel(
+    const bf16* __restrict__ qkvg, long ld, int S, int N, int H,
+    const float* __restrict__ mask, const bf16* __restrict__ o, const bf16* __restrict__ dog,
+    long ldo, float qscale, bf16* __restrict__ dqkvg) {
+  __shared__ float dk_s[32][SA_D + 1];
+  __shared__ float dv_s[32][SA_D + 1];
+  const int j = blockIdx.x / H, h = blockIdx.x % H;
+  const int lane = threadIdx.x;
+  const int HD = H * SA_D;
+  for (int i = lane; i < 32 * (SA_D + 1); i += 64) {
+    (&dk_s[0][0])[i] = 0.f;
+    (&dv_s[0][0])[i] = 0.f;
+  }
+  __syncthreads();
+  if (lane < S) {
+    const int sq = lane;
+    const long row = (long)sq * N + j;
+    const bf16* q = qkvg + row * ld + h * SA_D;
+    const bf16* g = qkvg + row * ld + 3 * HD + h * SA_D;
+    float qv[SA_D], dO[SA_D];
+    float Dsum = 0.f;
+#pragma unroll
+    for (int d = 0; d < SA_D; ++d) {
+      qv[d] = (float)q[d];
+      const float sg = sigmoidf_((float)g[d]);
+      const float dgo = (float)dog[row * ldo + h * SA_D + d];
+      const float ov = (float)o[row * ldo + h * SA_D + d];
+      dO[d] = dgo * sg;
+      Dsum += dO[d] * ov;
+      dqkvg[row * ld + 3 * HD + h * SA_D + d] = (bf16)(dgo * ov * sg * (1.f - sg));
+    }
+    // softmax recomputed in full (S is small): exact even for a fully masked
+    // column, where every clipped logit is -1e8 and f32 cannot carry an lse
+    float sc[32], mx = -INFINITY;
+    bool live[32];
+    for (int sk = 0; sk < S; ++sk) {
+      const bf16* k = qkvg + ((long)sk * N + j) * ld + HD + h * SA_D;
+      float s = 0.f;
+#pragma unroll
+      for (int d = 0; d < SA_D; ++d) s += qv[d] * (float)k[d];
+      const float raw = s + MASK_BIAS * (mask[(long)sk * N + j] - 1.f);
+      live[sk] = raw > -LOGIT_CLIP && raw < LOGIT_CLIP;
+      sc[sk] = fminf(fmaxf(raw, -LOGIT_CLIP), LOGIT_CLIP);
+      mx = fmaxf(mx, sc[sk]);
+    }
+    float sum = 0.f;
+    for (int sk = 0; sk < S; ++sk) {
+      sc[sk] = __expf(sc[sk] - mx);
+      sum += sc[sk];
+    }
+    const float inv = 1.f / sum;
+    float dq[SA_D];
+#pragma unroll
+    for (int d = 0; d < SA_D; ++d) dq[d] = 0.f;
+    for (int sk = 0; sk < S; ++sk) {
+      const long krow = (long)sk * N + j;
+      const bf16* k = qkvg + krow * ld + HD + h * SA_D;
+      const bf16* v = qkvg + krow * ld + 2 * HD + h * SA_D;
+      float dp = 0.f;
+#pragma unroll
+      for (int d = 0; d < SA_D; ++d) dp += dO[d] * (float)v[d];
+      const float p = sc[sk] * inv;
+      const float ds = live[sk] ? p * (dp - Dsum) : 0.f;
+#pragma unroll
+      for (int d = 0; d < SA_D; ++d) {
+        dq[d] += ds * (float)k[d];
+        atomicAdd(&dk_s[sk][d], ds * qv[d]);
+        atomicAdd(&dv_s[sk][d], p * dO[d]);
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < SA_D; ++d) dqkvg[row * ld + h * SA_D + d] = (bf16)(dq[d] * qscale);
+  }
+  __syncthreads();
+  for (int i = lane; i < S * SA_D; i += 64) {
+    const int sk = i / SA_D, d = i % SA_D;
+    const long krow = (long)sk * N + j;
+    // q was scaled by qscale: dK (unscaled k) = sum ds * q_scaled
+    dqkvg[krow * ld + HD + h * SA_D + d] = (bf16)dk_s[sk][d];
+    dqkvg[krow * ld + 2 * HD + h * SA_D + d] = (bf16)dv_s[sk][d];
+  }
+}
+
+template <class A>
+struct MsaRowSave {
+  float *mean, *rstd, *pmean, *prstd, *bias, *lse;
+  bf16 *qkvg, *o;
+  MsaRowSave(A& a, int S, int N, int Cm, int H) {
+    const size_t R = (size_t)S * N, M = (size_t)N * N;
+    mean = a.template take<float>(R);
+    rstd = a.template take<float>(R);
+    pmean = a.template take<float>(M);
+    prstd = a.template take<float>(M);
+    bias = a.template take<float>((size_t)H * M);
+    lse = a.template take<float>((size_t)S * H * N);
+    qkvg = a.template take<bf16>(R * 4 * Cm);
+    o = a.template take<bf16>(R * Cm);
+  }
+};
+
+template <class A>
+struct MsaColSave {
+  float *mean, *rstd, *lse;
+  bf16 *qkvg, *o;
+  MsaColSave(A& a, int S, int N, int Cm, int H) {
+    const size_t R = (size_t)S * N;
+    mean = a.template take<float>(R);
+    rstd = a.template take<float>(R);
+    lse = a.template take<float>((size_t)N * H * S);
+    qkvg = a.template take<bf16>(R * 4 * Cm);
+    o = a.template take<bf16>(R * Cm);
+  }
+};
+
+void qkvg_gemm(hipStream_t st, const AttnW& w, long rows, const bf16* xn, bf16* qkvg, float qscale,
+               const char* name) {
+  const int HD = w.H * w.D;
+  GemmArgs g;
+  g.M = (int)rows; g.N = 4 * HD; g.K = w.Cin;
+  g.A = xn; g.a_sm = w.Cin; g.a_sk = 1;
+  g.B = w.wqkvg_t; g.b_sn = w.Cin; g.b_sk = 1;
+  gemm<128, 128>(st, g, EpiQKVG2{qkvg, 4L * HD, w.bqkvg, qscale, HD, 4 * HD}, name);
+}
+
+void out_gemm(hipStream_t st, const AttnW& w, long rows, const bf16* og, const float* in,
+              float* out, const float* tbl, int nt, const char* name) {
+  const int HD = w.H * w.D;
+  GemmArgs g;
+  g.M = (int)rows; g.N = w.Cout; g.K = HD;
+  g.A = og; g.a_sm = HD; g.a_sk = 1;
+  g.B = w.wo_t; g.b_sn = HD; g.b_sk = 1;
+  gemm<128, 128>(st, g, EpiAddRows2{in, out, w.bo, tbl, nt, w.Cout}, name);
+}
+
+// d(og) = dd . Wo^T and, after the attention backward, d(xn) = dqkvg . Wcat^T
+void dout_gemm(hipStream_t st, const AttnW& w, long rows, const bf16* dd, bf16* dog,
+               const char* name) {
+  const int HD = w.H * w.D;
+  GemmArgs g;
+  g.M = (int)rows; g.N = HD; g.K = w.Cout;
+  g.A = dd; g.a_sm = w.Cout; g.a_sk = 1;
+  g.B = w.wo; g.b_sn = w.Cout; g.b_sk = 1;
+  gemm<128, 128>(st, g, EpiStore<bf16>{dog, HD, 0, nullptr, HD}, name);
+}
+
+void dx_gemm(hipStream_t st, const AttnW& w, long rows, const bf16* dqkvg, float* dxn,
+             const char* name) {
+  const int HD = w.H * w.D;
+  GemmArgs g;
+  g.M = (int)rows; g.N = w.Cin; g.K = 4 * HD;
+  g.A = dqkvg; g.a_sm = 4L * HD; g.a_sk = 1;
+  g.B = w.wqkvg; g.b_sn = 4L * HD; g.b_sk = 1;
+  gemm<128, 128>(st, g, EpiStore<float>{dxn, w.Cin, 0, nullptr, w.Cin}, name);
+}
+
+}  // namespace
+
+MsaRowW msarow_weights(WeightStore& ws, const std::string& P) {
+  MsaRowW w;
+  attn_weights(ws, P, w.a);
+  w.pn_g = ws.f32(P + "feat_2d_norm/scale");
+  w.pn_b = ws.f32(P + "feat_2d_norm/offset");
+  w.w2d = ws.f32(P + "feat_2d_weights");
+  w.Cz = ws.host(P + "feat_2d_weights").shape[0];
+  return w;
+}
+
+MsaColW msacol_weights(WeightStore& ws, const std::string& P) {
+  MsaColW w;
+  attn_weights(ws, P, w.a);
+  return w;
+}
+
+size_t msarow_save_bytes(int S, int N, int Cm, int H) {
+  Sizer s;
+  MsaRowSave<Sizer> p(s, S, N, Cm, H);
+  (void)p;
+  return s.off;
+}
+
+size_t msacol_save_bytes(int S, int N, int Cm, int H) {
+  Sizer s;
+  MsaColSave<Sizer> p(s, S, N, Cm, H);
+  (void)p;
+  return s.off;
+}
+
+void msarow_fwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa_in,
+                const float* msa_mask, const float* pair, const float* tbl, float* msa_out,
+                void* save) {
+  const AttnW& a = w.a;
+  if (a.D != 32 || a.Cin != a.Cout || a.H * a.D != a.Cin)
+    throw std::runtime_error("msarow: unsupported widths");
+  if (N % 32 != 0) throw std::runtime_error("msarow: N must be a multiple of 32");
+  const int Cm = a.Cin, H = a.H, HD = H * a.D;
+  const long R = (long)S * N, M = (long)N * N;
+  Carver cv(save);
+  MsaRowSave<Carver> sv(cv, S, N, Cm, H);
+  Arena& ar = arena();
+  std::lock_guard<std::recursive_mutex> lk(ar.lock());
+  ar.reset(st, (size_t)R * Cm * 2 + (size_t)R * HD * 2 + 1024);
+  bf16* xn = ar.take_n<bf16>((size_t)R * Cm);
+  bf16* og = ar.take_n<bf16>((size_t)R * HD);
+  {
+    KTimed kt("msarow.ln", st);
+    ln_fwd_f32(st, msa_in, R, Cm, 0, a.ln_g, a.ln_b, xn, sv.mean, sv.rstd, false, 0, nullptr,
+               nullptr);
+    ln_fwd_f32(st, pair, M, w.Cz, 0, w.pn_g, w.pn_b, nullptr, sv.pmean, sv.prstd, false, H, w.w2d,
+               sv.bias, LOG2E);
+  }
+  qkvg_gemm(st, a, R, xn, sv.qkvg, LOG2E / std::sqrt((float)a.D), "msarow.gemm_qkvg");
+  AttnArgs at;
+  at.R = S; at.H = H; at.N = N; at.D = a.D;
+  at.qkvg = sv.qkvg; at.ld = 4L * HD;
+  at.mask = msa_mask; at.mask_sr = N; at.mask_sk = 1;
+  at.bias = sv.bias;
+  at.o = sv.o; at.og = og; at.ldo = HD;
+  at.lse = sv.lse;
+  attn_fwd(st, at);
+  out_gemm(st, a, R, og, msa_in, msa_out, tbl, N, "msarow.gemm_out");
+}
+
+void msarow_bwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa_in,
+                const float* msa_mask, const float* pair, const float* tbl, const void* save,
+                const float* dmsa_out, float* dmsa_in, float* dpair) {
+  const AttnW& a = w.a;
+  const int Cm = a.Cin, H = a.H, HD = H * a.D;
+  const long R = (long)S * N, M = (long)N * N;
+  Carver cv(const_cast<void*>(save));
+  MsaRowSave<Carver> sv(cv, S, N, Cm, H);
+  AttnBwdArgs b;
+  b.rows_per_chunk = 8;
+  const int nch = attn_bwd_nchunk(S, b.rows_per_chunk);
+  Arena& ar = arena();
+  std::lock_guard<std::recursive_mutex> lk(ar.lock());
+  Sizer need;
+  need.take<bf16>((size_t)R * Cm);
+  need.take<bf16>((size_t)R * HD);
+  need.take<bf16>((size_t)R * HD);
+  need.take<float>((size_t)S * H * N);
+  need.take<bf16>((size_t)R * 4 * HD);
+  need.take<float>((size_t)nch * H * M);
+  need.take<float>((size_t)H * M);
+  need.take<float>((size_t)R * Cm);
+  ar.reset(st, need.off);
+  bf16* dd = ar.take_n<bf16>((size_t)R * Cm);
+  bf16* dog = ar.take_n<bf16>((size_t)R * HD);
+  b.dO = ar.take_n<bf16>((size_t)R * HD);
+  b.Dsum = ar.take_n<float>((size_t)S * H * N);
+  b.dqkvg = ar.take_n<bf16>((size_t)R * 4 * HD);
+  b.dbias_part = ar.take_n<float>((size_t)nch * H * M);
+  b.dbias = ar.take_n<float>((size_t)H * M);
+  float* dxn = ar.take_n<float>((size_t)R * Cm);
+  {
+    KTimed kt("msarow.dropout_bwd", st);
+    scale_rows_bf16(st, dmsa_out, R, Cm, N, false, tbl, dd);
+  }
+  dout_gemm(st, a, R, dd, dog, "msarow.gemm_dout");
+  AttnArgs& at = b.f;
+  at.R = S; at.H = H; at.N = N; at.D = a.D;
+  at.qkvg = sv.qkvg; at.ld = 4L * HD;
+  at.mask = msa_mask; at.mask_sr = N; at.mask_sk = 1;
+  at.bias = sv.bias;
+  at.o = sv.o; at.og = nullptr; at.ldo = HD;
+  at.lse = sv.lse;
+  b.dog = dog;
+  b.scale = 1.f / std::sqrt((float)a.D);
+  attn_bwd(st, b);
+  dx_gemm(st, a, R, b.dqkvg, dxn, "msarow.gemm_dx");
+  if (dmsa_in != dmsa_out)
+    BC2N_HIP(hipMemcpyAsync(dmsa_in, dmsa_out, (size_t)R * Cm * 4, hipMemcpyDeviceToDevice, st));
+  KTimed kt("msarow.ln_bwd", st);
+  ln_bwd_f32(st, dxn, msa_in, R, Cm, 0, a.ln_g, sv.mean, sv.rstd, dmsa_in, true, 0, nullptr,
+             nullptr);
+  // pair gradient: only through the bias projection
+  ln_bwd_f32(st, nullptr, pair, M, w.Cz, 0, w.pn_g, sv.pmean, sv.prstd, dpair, true, H, b.dbias,
+             w.w2d);
+}
+
+void msacol_fwd(hipStream_t st, const MsaColW& w, int S, int N, const float* msa_in,
+                const float* msa_mask, const float* tbl, float* msa_out, void* save) {
+  const AttnW& a = w.a;
+  if (a.D != 32 || S > 32) throw std::runtime_error("msacol: D must be 32 and S <= 32");
+  const int Cm = a.Cin, H = a.H, HD = H * a.D;
+  const long R = (long)S * N;
+  Carver cv(save);
+  MsaColSave<Carver> sv(cv, S, N, Cm, H);
+  Arena& ar = arena();
+  std::lock_guard<std::recursive_mutex> lk(ar.lock());
+  ar.reset(st, (size_t)R * Cm * 2 + (size_t)R * HD * 2 + 1024);
+  bf16* xn = ar.take_n<bf16>((size_t)R * Cm);
+  bf16* og = ar.take_n<bf16>((size_t)R * HD);
+  {
+    KTimed kt("msacol.ln", st);
+    ln_fwd_f32(st, msa_in, R, Cm, 0, a.ln_g, a.ln_b, xn, sv.mean, sv.rstd, false, 0, nullptr,
+               nullptr);
+  }
+  qkvg_gemm(st, a, R, xn, sv.qkvg, 1.f / std::sqrt((float)a.D), "msacol.gemm_qkvg");
+  {
+    KTimed kt("msacol.attn", st);
+    hipLaunchKernelGGL(small_attn_fwd_kernel, dim3(N * H), dim3(64), 0, st, sv.qkvg, 4L * HD, S, N,
+                       H, msa_mask, sv.o, og, (long)HD, sv.lse);
+  }
+  out_gemm(st, a, R, og, msa_in, msa_out, tbl, N, "msacol.gemm_out");
+}
+
+void msacol_bwd(hipStream_t st, const MsaColW& w, int S, int N, const float* msa_in,
+                const float* msa_mask, const float* tbl, const void* save,
+                const float* dmsa_out, float* dmsa_in) {
+  const AttnW& a = w.a;
+  const int Cm = a.Cin, H = a.H, HD = H * a.D;
+  const long R = (long)S * N;
+  Carver cv(const_cast<void*>(save));
+  MsaColSave<Carver> sv(cv, S, N, Cm, H);
+  Arena& ar = arena();
+  std::lock_guard<std::recursive_mutex> lk(ar.lock());
+  Sizer need;
+  need.take<bf16>((size_t)R * Cm);
+  need.take<bf16>((size_t)R * HD);
+  need.take<bf16>((size_t)R * 4 * HD);
+  need.take<float>((size_t)R * Cm);
+  ar.reset(st, need.off);
+  bf16* dd = ar.take_n<bf16>((size_t)R * Cm);
+  bf16* dog = ar.take_n<bf16>((size_t)R * HD);
+  bf16* dqkvg = ar.take_n<bf16>((size_t)R * 4 * HD);
+  float* dxn = ar.take_n<float>((size_t)R * Cm);
+  {
+    KTimed kt("msacol.dropout_bwd", st);
+    scale_rows_bf16(st, dmsa_out, R, Cm, N, false, tbl, dd);
+  }
+  dout_gemm(st, a, R, dd, dog, "msacol.gemm_dout");
+  {
+    KTimed kt("msacol.attn_bwd", st);
+    hipLaunchKernelGGL(small_attn_bwd_kernel, dim3(N * H), dim3(64), 0, st, sv.qkvg, 4L * HD, S, N,
+                       H, msa_mask, sv.o, dog, (long)HD, 1.f / std::sqrt((float)a.D), dqkvg);
+  }
+  dx_gemm(st, a, R, dqkvg, dxn, "msacol.gemm_dx");
+  if (dmsa_in != dmsa_out)
+    BC2N_HIP(hipMemcpyAsync(dmsa_in, dmsa_out, (size_t)R * Cm * 4, hipMemcpyDeviceToDevice, st));
+  KTimed kt("msacol.ln_bwd", st);
+  ln_bwd_f32(st, dxn, msa_in, R, Cm, 0, a.ln_g, sv.mean, sv.rstd, dmsa_in, true, 0, nullptr,
+             nullptr);
+}
+
+}  // namespace bc2n

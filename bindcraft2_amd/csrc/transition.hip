@@ -1,0 +1,135 @@
+// Transition (pair and MSA), forward and backward.
+//   LN -> GEMM (C -> F*C) + bias + relu (hidden kept, bf16)
+//      -> GEMM (F*C -> C) + bias, fused residual (+ shared dropout table)
+// Backward: dd = tbl*dout; dh = (dd . W2^T) * (h > 0); dxn = dh . W1^T;
+// LN backward accumulated into din.
+// Reference: modules.py:252-305 (Transition); native/transition.cuh:313-675.
+#include "gemm.h"
+#include "modules.h"
+
+namespace bc2n {
+
+namespace {
+
+// out[m] = in[m] + tbl[(m%nt)*C + c] * (acc + bias[c])
+struct EpiAddRows {
+  const float* in;
+  float* out;
+  const float* bias;
+  const float* tbl;
+  int nt, C;
+  template <int TN>
+  __device__ __forceinline__ void apply(int, int m, int n, const float (&v)[TN]) const {
+    const float* t = tbl ? tbl + (long)(m % nt) * C : nullptr;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int c = n + 16 * j;
+      if (c >= C) continue;
+      float x = v[j] + bias[c];
+      if (t) x *= t[c];
+      const long o = (long)m * C + c;
+      out[o] = in[o] + x;
+    }
+  }
+};
+
+template <class A>
+struct TransSave {
+  float *mean, *rstd;
+  bf16* h;
+  TransSave(A& a, long rows, int C, int F) {
+    mean = a.template take<float>(rows);
+    rstd = a.template take<float>(rows);
+    h = a.template take<bf16>((size_t)rows * C * F);
+  }
+};
+
+}  // namespace
+
+TransW transition_weights(WeightStore& ws, const std::string& P) {
+  TransW w;
+  const HostTensor& w1 = ws.host(P + "transition1/weights");  // [C, F*C]
+  w.C = w1.shape[0];
+  w.F = w1.shape[1] / w.C;
+  const int C = w.C, H = w.C * w.F;
+  w.ln_g = ws.f32(P + "input_layer_norm/scale");
+  w.ln_b = ws.f32(P + "input_layer_norm/offset");
+  w.b1 = ws.f32(P + "transition1/bias");
+  w.b2 = ws.f32(P + "transition2/bias");
+  const HostTensor& w2 = ws.host(P + "transition2/weights");  // [F*C, C]
+  w.w1 = ws.derived<bf16>("trans.w1:" + P, [&] { return to_bf16(w1.data); });
+  w.w1_t = ws.derived<bf16>("trans.w1_t:" + P, [&] { return transpose_bf16(w1.data.data(), C, H); });
+  w.w2 = ws.derived<bf16>("trans.w2:" + P, [&] { return to_bf16(w2.data); });
+  w.w2_t = ws.derived<bf16>("trans.w2_t:" + P, [&] { return transpose_bf16(w2.data.data(), H, C); });
+  return w;
+}
+
+size_t transition_save_bytes(long rows, int C, int F) {
+  Sizer s;
+  TransSave<Sizer> plan(s, rows, C, F);
+  (void)plan;
+  return s.off;
+}
+
+void transition_fwd(hipStream_t st, const TransW& w, long rows, int nt, const float* act_in,
+                    const float* tbl, float* act_out, void* save) {
+  const int C = w.C, H = w.C * w.F;
+  Carver cv(save);
+  TransSave<Carver> sv(cv, rows, C, w.F);
+  Arena& ar = arena();
+  std::lock_guard<std::recursive_mutex> lk(ar.lock());
+  ar.reset(st, (size_t)rows * C * 2 + 256);
+  bf16* xn = ar.take_n<bf16>((size_t)rows * C);
+  {
+    KTimed kt("trans.ln_fwd", st);
+    ln_fwd_f32(st, act_in, rows, C, 0, w.ln_g, w.ln_b, xn, sv.mean, sv.rstd, false, 0, nullptr,
+               nullptr);
+  }
+  GemmArgs g1;
+  g1.M = (int)rows; g1.N = H; g1.K = C;
+  g1.A = xn; g1.a_sm = C; g1.a_sk = 1;
+  g1.B = w.w1_t; g1.b_sn = C; g1.b_sk = 1;
+  gemm<128, 128>(st, g1, EpiStore<bf16, true>{sv.h, H, 0, w.b1, H}, "trans.gemm1");
+  GemmArgs g2;
+  g2.M = (int)rows; g2.N = C; g2.K = H;
+  g2.A = sv.h; g2.a_sm = H; g2.a_sk = 1;
+  g2.B = w.w2_t; g2.b_sn = H; g2.b_sk = 1;
+  gemm<128, 128>(st, g2, EpiAddRows{act_in, act_out, w.b2, tbl, nt, C}, "trans.gemm2");
+}
+
+void transition_bwd(hipStream_t st, const TransW& w, long rows, int nt, const float* act_in,
+                    const float* tbl, const void* save, const float* dout, float* din) {
+  const int C = w.C, H = w.C * w.F;
+  Carver cv(const_cast<void*>(save));
+  TransSave<Carver> sv(cv, rows, C, w.F);
+  Arena& ar = arena();
+  std::lock_guard<std::recursive_mutex> lk(ar.lock());
+  Sizer need;
+  need.take<bf16>((size_t)rows * C);
+  need.take<bf16>((size_t)rows * H);
+  need.take<float>((size_t)rows * C);
+  ar.reset(st, need.off);
+  bf16* dd = ar.take_n<bf16>((size_t)rows * C);
+  bf16* dh = ar.take_n<bf16>((size_t)rows * H);
+  float* dxn = ar.take_n<float>((size_t)rows * C);
+  {
+    KTimed kt("trans.dropout_bwd", st);
+    scale_rows_bf16(st, dout, rows, C, nt, false, tbl, dd);
+  }
+  GemmArgs g1;
+  g1.M = (int)rows; g1.N = H; g1.K = C;
+  g1.A = dd; g1.a_sm = C; g1.a_sk = 1;
+  g1.B = w.w2; g1.b_sn = C; g1.b_sk = 1;
+  gemm<128, 128>(st, g1, EpiReluMask{dh, sv.h, H, H}, "trans.gemm_dh");
+  GemmArgs g2;
+  g2.M = (int)rows; g2.N = C; g2.K = H;
+  g2.A = dh; g2.a_sm = H; g2.a_sk = 1;
+  g2.B = w.w1; g2.b_sn = H; g2.b_sk = 1;
+  gemm<128, 128>(st, g2, EpiStore<float>{dxn, C, 0, nullptr, C}, "trans.gemm_dx");
+  if (din != dout)
+    BC2N_HIP(hipMemcpyAsync(din, dout, (size_t)rows * C * 4, hipMemcpyDeviceToDevice, st));
+  KTimed kt("trans.ln_bwd", st);
+  ln_bwd_f32(st, dxn, act_in, rows, C, 0, w.ln_g, sv.mean, sv.rstd, din, true, 0, nullptr, nullptr);
+}
+
+}  // namespace bc2n

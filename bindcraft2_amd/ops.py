@@ -105,6 +105,156 @@ class TriangleMultiplication:
         return din
 
 
+class Transition:
+    """modules.py Transition + dropout_wrapper over act [B, N, C] (pair:
+    B = N; MSA: B = S)."""
+
+    def __init__(self, weights_dir, prefix, c, factor=4):
+        self.dir, self.prefix, self.c, self.f = weights_dir.encode(), prefix.encode(), c, factor
+
+    def forward(self, act, drop_tbl=None):
+        b, n, c = act.shape
+        rows = b * n
+        out = torch.empty_like(act)
+        save = torch.empty(lib().bc2n_transition_save_bytes(rows, c, self.f), dtype=torch.uint8,
+                           device=act.device)
+        check(lib().bc2n_transition_fwd(_stream(), self.dir, self.prefix, rows, n, _ptr(act),
+                                        _ptr(drop_tbl), _ptr(out), _ptr(save)))
+        return out, save
+
+    def backward(self, act, drop_tbl, save, dout):
+        b, n, c = act.shape
+        din = torch.empty_like(dout)
+        check(lib().bc2n_transition_bwd(_stream(), self.dir, self.prefix, b * n, n, _ptr(act),
+                                        _ptr(drop_tbl), _ptr(save), _ptr(dout), _ptr(din)))
+        return din
+
+
+class OuterProductMean:
+    """modules.py OuterProductMean added into the pair (dropout_wrapper)."""
+
+    def __init__(self, weights_dir, prefix, outer=32, c_z=128):
+        self.dir, self.prefix, self.o, self.cz = weights_dir.encode(), prefix.encode(), outer, c_z
+
+    def forward(self, msa, msa_mask, pair, drop_tbl=None):
+        s, n, _ = msa.shape
+        out = torch.empty_like(pair)
+        save = torch.empty(lib().bc2n_opm_save_bytes(s, n, self.o, self.cz), dtype=torch.uint8,
+                           device=msa.device)
+        check(lib().bc2n_opm_fwd(_stream(), self.dir, self.prefix, s, n, _ptr(msa), _ptr(msa_mask),
+                                 _ptr(pair), _ptr(drop_tbl), _ptr(out), _ptr(save)))
+        return out, save
+
+    def backward(self, msa, msa_mask, drop_tbl, save, dpair, dmsa_out=None):
+        s, n, _ = msa.shape
+        if dmsa_out is None:
+            dmsa_out = torch.zeros_like(msa)
+        dmsa = torch.empty_like(msa)
+        check(lib().bc2n_opm_bwd(_stream(), self.dir, self.prefix, s, n, _ptr(msa), _ptr(msa_mask),
+                                 _ptr(drop_tbl), _ptr(save), _ptr(dpair), _ptr(dmsa_out),
+                                 _ptr(dmsa)))
+        return dmsa
+
+
+class MSARowAttentionWithPairBias:
+    def __init__(self, weights_dir, prefix, c_m=256, heads=8):
+        self.dir, self.prefix, self.cm, self.h = weights_dir.encode(), prefix.encode(), c_m, heads
+
+    def forward(self, msa, msa_mask, pair, drop_tbl=None):
+        s, n, _ = msa.shape
+        out = torch.empty_like(msa)
+        save = torch.empty(lib().bc2n_msarow_save_bytes(s, n, self.cm, self.h), dtype=torch.uint8,
+                           device=msa.device)
+        check(lib().bc2n_msarow_fwd(_stream(), self.dir, self.prefix, s, n, _ptr(msa),
+                                    _ptr(msa_mask), _ptr(pair), _ptr(drop_tbl), _ptr(out),
+                                    _ptr(save)))
+        return out, save
+
+    def backward(self, msa, msa_mask, pair, drop_tbl, save, dout, dpair=None):
+        s, n, _ = msa.shape
+        din = torch.empty_like(dout)
+        if dpair is None:
+            dpair = torch.zeros_like(pair)
+        check(lib().bc2n_msarow_bwd(_stream(), self.dir, self.prefix, s, n, _ptr(msa),
+                                    _ptr(msa_mask), _ptr(pair), _ptr(drop_tbl), _ptr(save),
+                                    _ptr(dout), _ptr(din), _ptr(dpair)))
+        return din, dpair
+
+
+class MSAColumnAttention:
+    def __init__(self, weights_dir, prefix, c_m=256, heads=8):
+        self.dir, self.prefix, self.cm, self.h = weights_dir.encode(), prefix.encode(), c_m, heads
+
+    def forward(self, msa, msa_mask, drop_tbl=None):
+        s, n, _ = msa.shape
+        out = torch.empty_like(msa)
+        save = torch.empty(lib().bc2n_msacol_save_bytes(s, n, self.cm, self.h), dtype=torch.uint8,
+                           device=msa.device)
+        check(lib().bc2n_msacol_fwd(_stream(), self.dir, self.prefix, s, n, _ptr(msa),
+                                    _ptr(msa_mask), _ptr(drop_tbl), _ptr(out), _ptr(save)))
+        return out, save
+
+    def backward(self, msa, msa_mask, drop_tbl, save, dout):
+        s, n, _ = msa.shape
+        din = torch.empty_like(dout)
+        check(lib().bc2n_msacol_bwd(_stream(), self.dir, self.prefix, s, n, _ptr(msa),
+                                    _ptr(msa_mask), _ptr(drop_tbl), _ptr(save), _ptr(dout),
+                                    _ptr(din)))
+        return din
+
+
+def seed_tensor(key, enabled=True, device="cuda"):
+    """The stack's seed operand u32[3] = [k0, k1, enabled] (key_data of the
+    stack's JAX key plus the use_dropout flag)."""
+    t = torch.tensor([int(key[0]), int(key[1]), int(bool(enabled))], dtype=torch.int64)
+    return t.to(torch.uint32).to(device)
+
+
+class EvoformerStack:
+    """The drop-in for the reference's native_evoformer_fwd/bwd FFI pair
+    (native/ffi.cu:942-982): `depth` Evoformer blocks from a weights
+    directory, pure forward/backward with the save-set crossing as data."""
+
+    def __init__(self, weights_dir, depth, pair_only=False, c_m=256):
+        self.dir, self.depth, self.pair_only, self.cm = weights_dir.encode(), depth, pair_only, c_m
+
+    def save_bytes(self, n, s):
+        b = lib().bc2n_evoformer_save_bytes(self.dir, n, s, self.depth, int(self.pair_only))
+        if b == 0:
+            check(1)
+        return b
+
+    def forward(self, pair, msa, pair_mask, msa_mask, seed=None, dropout=True, save=None,
+                pair_out=None, msa_out=None):
+        n = pair.shape[0]
+        s, _, cm = msa.shape
+        if pair_out is None:
+            pair_out = torch.empty_like(pair)
+        if msa_out is None:
+            msa_out = torch.empty_like(msa)
+        if save is None:
+            save = torch.empty(self.save_bytes(n, s), dtype=torch.uint8, device=pair.device)
+        seed_len = 0 if seed is None else seed.numel()
+        check(lib().bc2n_evoformer_fwd(_stream(), _ptr(pair), _ptr(msa), _ptr(pair_mask),
+                                       _ptr(msa_mask), _ptr(seed), max(seed_len, 3), n, s, cm,
+                                       self.depth, 1, int(self.pair_only), 0, 1, int(dropout),
+                                       self.dir, _ptr(pair_out), _ptr(msa_out), _ptr(save), None))
+        return pair_out, msa_out, save
+
+    def backward(self, ct_pair, ct_msa, pair_mask, msa_mask, save, seed=None, dropout=True):
+        n = ct_pair.shape[0]
+        s, _, cm = ct_msa.shape
+        dpair = torch.empty_like(ct_pair)
+        dmsa = torch.empty_like(ct_msa)
+        seed_len = 0 if seed is None else seed.numel()
+        check(lib().bc2n_evoformer_bwd(_stream(), _ptr(ct_pair), _ptr(ct_msa), _ptr(pair_mask),
+                                       _ptr(msa_mask), _ptr(save), None, _ptr(seed),
+                                       max(seed_len, 3), n, s, cm, self.depth,
+                                       int(self.pair_only), 0, 1, int(dropout), self.dir,
+                                       _ptr(dpair), _ptr(dmsa)))
+        return dpair, dmsa
+
+
 def dropout_table(rows, channels, key, rate, device="cuda"):
     """[rows, channels] keep/keep_rate table from a JAX key (k0, k1)."""
     tbl = torch.empty(rows, channels, dtype=torch.float32, device=device)

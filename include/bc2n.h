@@ -76,6 +76,96 @@ int bc2n_trimul_bwd(void* stream, const char* weights_dir, const char* prefix,
                     const float* pair_mask, const float* drop_tbl,
                     const void* save, const float* dpair_out, float* dpair_in);
 
+/* Transition (pair or MSA): act f32 [B, N, C] as rows = B*N; the shared
+ * dropout table row of act row m is m % N.  AF2 passes a mask it does not
+ * use; none is taken here.  Replaces native/transition.cuh Trans::forward
+ * (:569) / backward (:619); semantics of modules.py:252-305. */
+size_t bc2n_transition_save_bytes(long rows, int C, int factor);
+int bc2n_transition_fwd(void* stream, const char* weights_dir, const char* prefix,
+                        long rows, int N, const float* act, const float* drop_tbl,
+                        float* act_out, void* save);
+int bc2n_transition_bwd(void* stream, const char* weights_dir, const char* prefix,
+                        long rows, int N, const float* act, const float* drop_tbl,
+                        const void* save, const float* dact_out, float* dact_in);
+
+/* Outer product mean added into the pair: msa f32 [S,N,Cm], msa_mask f32
+ * [S,N], pair f32 [N,N,C].  The backward returns the MSA cotangent:
+ * dmsa_in = dmsa_out + J^T(drop_tbl * dpair) (the pair's own cotangent passes
+ * through the residual unchanged).  Replaces native/opm.cuh Opm::forward
+ * (:271) / backward (:293); semantics of modules.py:1128-1212. */
+size_t bc2n_opm_save_bytes(int S, int N, int O, int C);
+int bc2n_opm_fwd(void* stream, const char* weights_dir, const char* prefix, int S,
+                 int N, const float* msa, const float* msa_mask, const float* pair,
+                 const float* drop_tbl, float* pair_out, void* save);
+int bc2n_opm_bwd(void* stream, const char* weights_dir, const char* prefix, int S,
+                 int N, const float* msa, const float* msa_mask,
+                 const float* drop_tbl, const void* save, const float* dpair,
+                 const float* dmsa_out, float* dmsa_in);
+
+/* MSA row attention with pair bias: msa [S,N,Cm], msa_mask [S,N], pair
+ * [N,N,Cz].  The backward also accumulates (+=) the pair cotangent of the
+ * bias path into dpair.  Replaces native/msarow.cuh MsaRow::forward (:363) /
+ * backward (:385); semantics of modules.py:500-563. */
+size_t bc2n_msarow_save_bytes(int S, int N, int Cm, int H);
+int bc2n_msarow_fwd(void* stream, const char* weights_dir, const char* prefix,
+                    int S, int N, const float* msa, const float* msa_mask,
+                    const float* pair, const float* drop_tbl, float* msa_out,
+                    void* save);
+int bc2n_msarow_bwd(void* stream, const char* weights_dir, const char* prefix,
+                    int S, int N, const float* msa, const float* msa_mask,
+                    const float* pair, const float* drop_tbl, const void* save,
+                    const float* dmsa_out, float* dmsa_in, float* dpair);
+
+/* MSA column attention (S <= 32).  Replaces native/msacol.cuh
+ * MsaCol (:247-361); semantics of modules.py:566-616. */
+size_t bc2n_msacol_save_bytes(int S, int N, int Cm, int H);
+int bc2n_msacol_fwd(void* stream, const char* weights_dir, const char* prefix,
+                    int S, int N, const float* msa, const float* msa_mask,
+                    const float* drop_tbl, float* msa_out, void* save);
+int bc2n_msacol_bwd(void* stream, const char* weights_dir, const char* prefix,
+                    int S, int N, const float* msa, const float* msa_mask,
+                    const float* drop_tbl, const void* save,
+                    const float* dmsa_out, float* dmsa_in);
+
+/* ------------------------------------------------------------------------
+ * The Evoformer stack: the drop-in for the reference's XLA FFI pair
+ * NativeEvoformerFwd / NativeEvoformerBwd (native/ffi.cu:942-982, impl
+ * FwdImpl :183-331, BwdImpl :333-371), same operands and attributes:
+ *   fwd(pair f32[N,N,128], msa f32[S,N,Cm], pair_mask f32[N,N],
+ *       msa_mask f32[S,N], seed u32[seed_len]; depth, save, pair_only,
+ *       own_save, opm_first, dropout, weights_dir)
+ *     -> (pair_out, msa_out, psave, msave)
+ *   bwd(ct_pair, ct_msa, pair_mask, msa_mask, psave, msave, seed; depth,
+ *       pair_only, own_save, opm_first, dropout, weights_dir) -> (dpair, dmsa)
+ * Shapes cross as N, S, Cm.  psave is one opaque byte buffer of
+ * bc2n_evoformer_save_bytes() (every block's carries and module save-sets:
+ * the backward replays nothing); msave is accepted and unused (may be NULL).
+ * save=0 or own_save=1 use a library-owned save-set instead.
+ * seed: seed_len=3 -> [k0, k1, enabled] with (k0,k1) = key_data of the
+ * stack's JAX key: dropout masks are bit-identical to jax.random.bernoulli
+ * through AF2's key chain.  seed_len=2 -> the reference's [bits, enabled]
+ * operand (modules_multimer.py:660-667), taken as PRNGKey(bits).
+ * opm_first must be 1 (AF2-multimer, config.py:414).  pair_only=1 is the
+ * reference's extra-MSA specialisation (MSA mask all zero: OPM adds
+ * output_b/1e-3, the MSA modules are skipped, msa passes through).
+ * ---------------------------------------------------------------------- */
+size_t bc2n_evoformer_save_bytes(const char* weights_dir, int N, int S,
+                                 int64_t depth, int64_t pair_only);
+int bc2n_evoformer_fwd(void* stream, const float* pair, const float* msa,
+                       const float* pair_mask, const float* msa_mask,
+                       const uint32_t* seed, int seed_len, int N, int S, int Cm,
+                       int64_t depth, int64_t save, int64_t pair_only,
+                       int64_t own_save, int64_t opm_first, int64_t dropout,
+                       const char* weights_dir, float* pair_out, float* msa_out,
+                       void* psave, void* msave);
+int bc2n_evoformer_bwd(void* stream, const float* ct_pair, const float* ct_msa,
+                       const float* pair_mask, const float* msa_mask,
+                       const void* psave, const void* msave,
+                       const uint32_t* seed, int seed_len, int N, int S, int Cm,
+                       int64_t depth, int64_t pair_only, int64_t own_save,
+                       int64_t opm_first, int64_t dropout,
+                       const char* weights_dir, float* dpair, float* dmsa);
+
 /* ------------------------------------------------------------------------
  * Dropout with JAX's own bits.  tbl[b*C+c] = keep/keep_rate where
  * keep = jax.random.bernoulli(key, keep_rate, (B, C)), keep_rate =
