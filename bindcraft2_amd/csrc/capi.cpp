@@ -66,12 +66,14 @@ std::map<std::pair<std::string, std::string>, MsaRowW> g_row;
 std::map<std::pair<std::string, std::string>, MsaColW> g_col;
 std::map<std::pair<std::string, std::string>, StackW> g_stack;
 
-const StackW& stack_w(const char* dir, int depth, bool pair_only) {
-  const std::string tag = std::to_string(depth) + (pair_only ? ":pair_only" : ":full");
+const StackW& stack_w(const char* dir, int depth, StackKind kind) {
+  const char* kn = kind == StackKind::EVO ? ":evo" : kind == StackKind::PAIR_ONLY ? ":pair_only" : ":tpl";
+  const std::string tag = std::to_string(depth) + kn;
   return cached(g_stack, dir, tag.c_str(), [&](WeightStore& ws, const std::string&) {
-    return stack_weights(ws, depth, pair_only);
+    return stack_weights(ws, depth, kind);
   });
 }
+StackKind evo_kind(int64_t pair_only) { return pair_only ? StackKind::PAIR_ONLY : StackKind::EVO; }
 
 // Library-owned save-set for detached forwards (save=0) and own_save=1.
 struct OwnSave {
@@ -262,7 +264,7 @@ size_t bc2n_evoformer_save_bytes(const char* weights_dir, int N, int S, int64_t 
   size_t n = 0;
   if (guarded([&] {
         need(weights_dir != nullptr, "weights_dir required");
-        const StackW& w = stack_w(weights_dir, (int)depth, pair_only != 0);
+        const StackW& w = stack_w(weights_dir, (int)depth, evo_kind(pair_only));
         n = stack_save_bytes(w, N, S, (int)depth) + 256;
       }) != 0)
     return 0;
@@ -290,7 +292,7 @@ int bc2n_evoformer_fwd(void* stream, const float* pair, const float* msa, const 
     need(!dropout || seed, "evoformer: dropout needs the seed operand");
     need(pair_only || (msa && msa_mask && msa_out), "evoformer: msa operands required");
     need(pair_out != pair && (pair_only || msa_out != msa), "evoformer: outputs must not alias inputs");
-    const StackW& w = stack_w(weights_dir, (int)depth, pair_only != 0);
+    const StackW& w = stack_w(weights_dir, (int)depth, evo_kind(pair_only));
     if (!pair_only) need(Cm == w.blocks[0].row.a.Cin, "evoformer: msa channel width mismatch");
     const size_t bytes = stack_save_bytes(w, N, S, (int)depth) + 256;
     void* sv = (save == 0 || own_save != 0 || psave == nullptr) ? g_own.get(st, bytes) : psave;
@@ -318,13 +320,58 @@ int bc2n_evoformer_bwd(void* stream, const float* ct_pair, const float* ct_msa,
     need(weights_dir && ct_pair && pair_mask && dpair, "null operand");
     need(opm_first == 1, "evoformer: only outer_product_mean.first=True (AF2-multimer) is built");
     need(pair_only || (ct_msa && msa_mask && dmsa), "evoformer: msa operands required");
-    const StackW& w = stack_w(weights_dir, (int)depth, pair_only != 0);
+    const StackW& w = stack_w(weights_dir, (int)depth, evo_kind(pair_only));
     const size_t bytes = stack_save_bytes(w, N, S, (int)depth) + 256;
     const void* sv = (own_save != 0 || psave == nullptr) ? g_own.get(st, bytes) : psave;
     stack_bwd(st, w, N, S, (int)depth, pair_mask, msa_mask, dropout != 0, sv, ct_pair, ct_msa,
               dpair, dmsa);
     if (pair_only && dmsa && ct_msa && dmsa != ct_msa && Cm > 0)
       BC2N_HIP(hipMemcpyAsync(dmsa, ct_msa, (size_t)S * N * Cm * 4, hipMemcpyDeviceToDevice, st));
+  });
+}
+
+// ------------------------------------------------------ template pair stack
+
+size_t bc2n_tplstack_save_bytes(const char* weights_dir, int N, int64_t depth) {
+  size_t n = 0;
+  if (guarded([&] {
+        need(weights_dir != nullptr, "weights_dir required");
+        const StackW& w = stack_w(weights_dir, (int)depth, StackKind::TEMPLATE);
+        n = stack_save_bytes(w, N, 1, (int)depth) + 256;
+      }) != 0)
+    return 0;
+  return n;
+}
+
+int bc2n_tplstack_fwd(void* stream, const float* pair, const float* pair_mask,
+                      const uint32_t* seed, int seed_len, int N, int64_t depth, int64_t dropout,
+                      const char* weights_dir, float* out, void* save) {
+  return guarded([&] {
+    hipStream_t st = as_stream(stream);
+    need(weights_dir && pair && pair_mask && out && save, "null operand");
+    need(out != pair, "tplstack: out must not alias pair");
+    need(seed_len == 2 || seed_len == 3, "tplstack: seed must be u32[2] or u32[3]");
+    need(!dropout || seed, "tplstack: dropout needs the seed operand");
+    const StackW& w = stack_w(weights_dir, (int)depth, StackKind::TEMPLATE);
+    const size_t bytes = stack_save_bytes(w, N, 1, (int)depth) + 256;
+    uint32_t* keyslot = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(save) + bytes - 256);
+    const uint32_t* key = dropout ? stack_key(st, seed, seed_len, keyslot) : nullptr;
+    const uint32_t* enabled = dropout ? seed + (seed_len - 1) : nullptr;
+    stack_fwd(st, w, N, 1, (int)depth, pair, nullptr, pair_mask, nullptr, key, enabled,
+              dropout != 0, out, nullptr, save);
+  });
+}
+
+int bc2n_tplstack_bwd(void* stream, const float* ct, const float* pair_mask, const void* save,
+                      const uint32_t* seed, int seed_len, int N, int64_t depth, int64_t dropout,
+                      const char* weights_dir, float* dpair) {
+  (void)seed;
+  (void)seed_len;
+  return guarded([&] {
+    need(weights_dir && ct && pair_mask && save && dpair, "null operand");
+    const StackW& w = stack_w(weights_dir, (int)depth, StackKind::TEMPLATE);
+    stack_bwd(as_stream(stream), w, N, 1, (int)depth, pair_mask, nullptr, dropout != 0, save, ct,
+              nullptr, dpair, nullptr);
   });
 }
 

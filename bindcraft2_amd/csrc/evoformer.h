@@ -16,14 +16,20 @@ struct BlockW {
   const float* opm_b = nullptr;  // outer_product_mean/output_b (pair_only constant)
 };
 
+// EVO: full Evoformer blocks.  PAIR_ONLY: the extra-MSA specialisation
+// (OPM constant + pair modules).  TEMPLATE: TemplateEmbeddingIteration
+// (modules_multimer.py:1008-1077: tmo, tmi, tas, tae, transition).
+enum class StackKind { EVO, PAIR_ONLY, TEMPLATE };
+
 struct StackW {
-  bool pair_only = false;
+  StackKind kind = StackKind::EVO;
+  bool pair_only = false;  // no MSA track (PAIR_ONLY or TEMPLATE)
   std::vector<BlockW> blocks;
 };
 
-BlockW block_weights(WeightStore& ws, const std::string& prefix, bool pair_only);
+BlockW block_weights(WeightStore& ws, const std::string& prefix, StackKind kind);
 // Blocks param/block0 .. param/block{depth-1} of a weights directory.
-StackW stack_weights(WeightStore& ws, int depth, bool pair_only,
+StackW stack_weights(WeightStore& ws, int depth, StackKind kind,
                      const std::string& root = "param/");
 
 // Bytes of the save-set a forward with these shapes writes and the backward

@@ -23,22 +23,26 @@ namespace {
 
 // module indices of a block's 9 dropout keys (modules.py:1308-1390 order)
 enum { K_OPM = 0, K_ROW, K_COL, K_MTR, K_TMO, K_TMI, K_TAS, K_TAE, K_PTR };
+// ... and of the template iteration's 5 (modules_multimer.py:1039-1075)
+enum { T_TMO = 0, T_TMI, T_TAS, T_TAE, T_PTR };
 
 size_t al256(size_t n) { return (n + 255) & ~size_t(255); }
 
 struct Layout {
   int N = 0, S = 0, Cz = 0, Cm = 0, depth = 0;
-  bool pair_only = false;
+  bool pair_only = false, tpl = false;
   size_t opm = 0, row = 0, col = 0, mtr = 0, tmo = 0, tmi = 0, tas = 0, tae = 0, ptr = 0;
   size_t pair_bytes = 0, msa_bytes = 0, block_bytes = 0;
   size_t tbl_per_block = 0;  // floats
   // offsets of the save-set regions
-  size_t off_carry_p = 0, off_carry_m = 0, off_msa_in = 0, off_tbl = 0, off_keys = 0, total = 0;
+  size_t off_carry_p = 0, off_carry_m = 0, off_msa_in = 0, off_pair_in = 0, off_tbl = 0,
+         off_keys = 0, total = 0;
 };
 
 Layout layout(const StackW& w, int N, int S, int depth) {
   Layout L;
   L.N = N; L.S = S; L.depth = depth; L.pair_only = w.pair_only;
+  L.tpl = (w.kind == StackKind::TEMPLATE);
   const BlockW& b = w.blocks[0];
   L.Cz = b.tmo.C;
   L.Cm = w.pair_only ? 0 : b.row.a.Cin;
@@ -65,9 +69,13 @@ Layout layout(const StackW& w, int N, int S, int depth) {
   L.off_carry_m = L.off_carry_p + (size_t)(depth - 1) * L.pair_bytes;
   // the stack's msa input, kept for the backward of block 0
   L.off_msa_in = L.off_carry_m + (size_t)(depth - 1) * L.msa_bytes;
-  L.off_tbl = L.off_msa_in + L.msa_bytes;
+  // the template iteration's first module reads the block input itself: the
+  // stack's pair input is kept for block 0's backward
+  L.off_pair_in = L.off_msa_in + L.msa_bytes;
+  L.off_tbl = L.off_pair_in + (L.tpl ? L.pair_bytes : 0);
   L.off_keys = L.off_tbl + al256((size_t)depth * L.tbl_per_block * 4);
   L.total = L.off_keys + al256((size_t)depth * 9 * 2 * 4);
+  (void)K_OPM; (void)K_COL; (void)K_MTR; (void)K_PTR; (void)T_PTR;
   return L;
 }
 
@@ -124,7 +132,9 @@ Frame frame(const Layout& L, char* save, int b, const float* pair, const float* 
   Frame f;
   auto cp = [&](int k) { return reinterpret_cast<float*>(save + L.off_carry_p + (size_t)k * L.pair_bytes); };
   auto cm = [&](int k) { return reinterpret_cast<float*>(save + L.off_carry_m + (size_t)k * L.msa_bytes); };
-  f.pin = b == 0 ? pair : cp(b - 1);
+  // pair == nullptr: the backward, which reads block 0's input from the save-set
+  f.pin = b == 0 ? (pair ? pair : (L.tpl ? reinterpret_cast<float*>(save + L.off_pair_in) : nullptr))
+                 : cp(b - 1);
   f.pout = b == L.depth - 1 ? pair_out : cp(b);
   if (L.pair_only) {
     f.min = msa;
@@ -142,7 +152,10 @@ void block_fwd(hipStream_t st, const BlockW& B, const Layout& L, int b, const Ta
   BlockPtrs p = carve(L, save);
   const int N = L.N, S = L.S;
   const long M = (long)N * N;
-  if (L.pair_only) {
+  // the template iteration starts at the triangle multiplications
+  const float* p1 = L.tpl ? f.pin : p.p1;
+  if (L.tpl) {
+  } else if (L.pair_only) {
     KTimed kt("block.opm_const", st);
     hipLaunchKernelGGL(add_const_kernel, dim3((unsigned)((M * L.Cz + 255) / 256)), dim3(256), 0,
                        st, f.pin, p.p1, B.opm_b, M, L.Cz);
@@ -152,7 +165,7 @@ void block_fwd(hipStream_t st, const BlockW& B, const Layout& L, int b, const Ta
     msacol_fwd(st, B.col, S, N, p.m1, mmask, nullptr, p.m2, p.col);
     transition_fwd(st, B.mtr, (long)S * N, N, p.m2, nullptr, f.mout, p.mtr);
   }
-  trimul_fwd(st, B.tmo, true, N, p.p1, pmask, t.pair(b, 0), p.p2, p.tmo);
+  trimul_fwd(st, B.tmo, true, N, p1, pmask, t.pair(b, 0), p.p2, p.tmo);
   trimul_fwd(st, B.tmi, false, N, p.p2, pmask, t.pair(b, 1), p.p3, p.tmi);
   triattn_fwd(st, B.tas, false, N, p.p3, pmask, t.pair(b, 2), p.p4, p.tas);
   triattn_fwd(st, B.tae, true, N, p.p4, pmask, t.pair(b, 3), p.p5, p.tae);
@@ -171,7 +184,7 @@ void block_bwd(hipStream_t st, const BlockW& B, const Layout& L, int b, const Ta
   triattn_bwd(st, B.tae, true, N, p.p4, pmask, t.pair(b, 3), p.tae, dpair, dpair);
   triattn_bwd(st, B.tas, false, N, p.p3, pmask, t.pair(b, 2), p.tas, dpair, dpair);
   trimul_bwd(st, B.tmi, false, N, p.p2, pmask, t.pair(b, 1), p.tmi, dpair, dpair);
-  trimul_bwd(st, B.tmo, true, N, p.p1, pmask, t.pair(b, 0), p.tmo, dpair, dpair);
+  trimul_bwd(st, B.tmo, true, N, L.tpl ? f.pin : p.p1, pmask, t.pair(b, 0), p.tmo, dpair, dpair);
   if (!L.pair_only) {
     transition_bwd(st, B.mtr, (long)S * N, N, p.m2, nullptr, p.mtr, dmsa, dmsa);
     msacol_bwd(st, B.col, S, N, p.m1, mmask, nullptr, p.col, dmsa, dmsa);
@@ -188,14 +201,15 @@ void stack_check(const StackW& w, int N, int S, int depth) {
 
 }  // namespace
 
-BlockW block_weights(WeightStore& ws, const std::string& P, bool pair_only) {
+BlockW block_weights(WeightStore& ws, const std::string& P, StackKind kind) {
+  const bool pair_only = kind != StackKind::EVO;
   BlockW b;
   b.tmo = trimul_weights(ws, P + "triangle_multiplication_outgoing/");
   b.tmi = trimul_weights(ws, P + "triangle_multiplication_incoming/");
   b.tas = triattn_weights(ws, P + "triangle_attention_starting_node/");
   b.tae = triattn_weights(ws, P + "triangle_attention_ending_node/");
   b.ptr = transition_weights(ws, P + "pair_transition/");
-  b.opm_b = ws.f32(P + "outer_product_mean/output_b");
+  if (kind != StackKind::TEMPLATE) b.opm_b = ws.f32(P + "outer_product_mean/output_b");
   if (!pair_only) {
     b.opm = opm_weights(ws, P + "outer_product_mean/");
     b.row = msarow_weights(ws, P + "msa_row_attention_with_pair_bias/");
@@ -205,11 +219,12 @@ BlockW block_weights(WeightStore& ws, const std::string& P, bool pair_only) {
   return b;
 }
 
-StackW stack_weights(WeightStore& ws, int depth, bool pair_only, const std::string& root) {
+StackW stack_weights(WeightStore& ws, int depth, StackKind kind, const std::string& root) {
   StackW s;
-  s.pair_only = pair_only;
+  s.kind = kind;
+  s.pair_only = kind != StackKind::EVO;
   for (int b = 0; b < depth; ++b)
-    s.blocks.push_back(block_weights(ws, root + "block" + std::to_string(b) + "/", pair_only));
+    s.blocks.push_back(block_weights(ws, root + "block" + std::to_string(b) + "/", kind));
   return s;
 }
 
@@ -232,20 +247,26 @@ void stack_fwd(hipStream_t st, const StackW& w, int N, int S, int depth, const f
     float* tbl = reinterpret_cast<float*>(sv + L.off_tbl);
     uint32_t* keys = reinterpret_cast<uint32_t*>(sv + L.off_keys);
     KTimed kt("stack.dropout_tables", st);
-    stack_keys(st, key, depth, keys);
-    const int pm[4] = {K_TMO, K_TMI, K_TAS, K_TAE};
+    const int nk = L.tpl ? 5 : 9;
+    stack_keys(st, key, depth, keys, nk);
+    const int pm_evo[4] = {K_TMO, K_TMI, K_TAS, K_TAE};
+    const int pm_tpl[4] = {T_TMO, T_TMI, T_TAS, T_TAE};
+    const int* pm = L.tpl ? pm_tpl : pm_evo;
     for (int b = 0; b < depth; ++b) {
       float* tb = tbl + b * L.tbl_per_block;
       if (!L.pair_only)
-        dropout_table_dev(st, tb, N, L.Cm, keys + (b * 9 + K_ROW) * 2, enabled, 1.0f - 0.15f);
+        dropout_table_dev(st, tb, N, L.Cm, keys + (b * nk + K_ROW) * 2, enabled, 1.0f - 0.15f);
       for (int k = 0; k < 4; ++k)
         dropout_table_dev(st, tb + (size_t)N * L.Cm + (size_t)k * N * L.Cz, N, L.Cz,
-                          keys + (b * 9 + pm[k]) * 2, enabled, 1.0f - 0.25f);
+                          keys + (b * nk + pm[k]) * 2, enabled, 1.0f - 0.25f);
     }
     t.base = tbl;
   }
   if (!L.pair_only)
     BC2N_HIP(hipMemcpyAsync(sv + L.off_msa_in, msa, (size_t)S * N * L.Cm * 4,
+                            hipMemcpyDeviceToDevice, st));
+  if (L.tpl)
+    BC2N_HIP(hipMemcpyAsync(sv + L.off_pair_in, pair, (size_t)N * N * L.Cz * 4,
                             hipMemcpyDeviceToDevice, st));
   for (int b = 0; b < depth; ++b)
     block_fwd(st, w.blocks[b], L, b, t, frame(L, sv, b, pair, msa, pair_out, msa_out), pmask,

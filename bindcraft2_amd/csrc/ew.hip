@@ -56,10 +56,12 @@ void bernoulli_bits(hipStream_t st, uint8_t* out, long n, uint32_t k0, uint32_t 
 }
 
 // -------------------------------------------------------------- key chain
-// The Evoformer stack's per-module keys (modules_multimer.py evoformer_fn and
-// modules.py EvoformerIteration): for each layer, (carry, sub) = split(carry);
-// the block splits `sub` into 10 and hands keys 1..9 to its modules in order.
-// out[(layer*9 + module)*2 + {0,1}].
+// A layer_stack's per-module keys: for each layer, (carry, sub) =
+// split(carry); the block splits `sub` into n_split and hands keys
+// 1..n_used to its modules in order -- (10, 9) for the Evoformer
+// (modules_multimer.py:622-641, modules.py:1308-1309), (20, 5) for the
+// template pair stack (modules_multimer.py:957-966, :1036-1037).
+// out[(layer*n_used + module)*2 + {0,1}].
 // jax.random.split (partitionable): key i = threefry(key, counter (0, i)).
 __device__ __host__ inline void split_key(uint32_t k0, uint32_t k1, int i,
                                           uint32_t* o0, uint32_t* o1) {
@@ -69,7 +71,7 @@ __device__ __host__ inline void split_key(uint32_t k0, uint32_t k1, int i,
   *o1 = x1;
 }
 
-__global__ void stack_keys_kernel(const uint32_t* __restrict__ seed, int depth,
+__global__ void stack_keys_kernel(const uint32_t* __restrict__ seed, int depth, int n_used,
                                   uint32_t* __restrict__ out) {
   if (threadIdx.x != 0 || blockIdx.x != 0) return;
   uint32_t c0 = seed[0], c1 = seed[1];
@@ -77,11 +79,11 @@ __global__ void stack_keys_kernel(const uint32_t* __restrict__ seed, int depth,
     uint32_t s0, s1, n0, n1;
     split_key(c0, c1, 1, &s0, &s1);
     split_key(c0, c1, 0, &n0, &n1);
-    for (int m = 0; m < 9; ++m) {
+    for (int m = 0; m < n_used; ++m) {
       uint32_t a, b;
       split_key(s0, s1, m + 1, &a, &b);
-      out[(l * 9 + m) * 2 + 0] = a;
-      out[(l * 9 + m) * 2 + 1] = b;
+      out[(l * n_used + m) * 2 + 0] = a;
+      out[(l * n_used + m) * 2 + 1] = b;
     }
     c0 = n0;
     c1 = n1;
@@ -101,8 +103,8 @@ void key_from_bits(hipStream_t st, const uint32_t* seed, uint32_t* out) {
   hipLaunchKernelGGL(key_from_bits_kernel, dim3(1), dim3(64), 0, st, seed, out);
 }
 
-void stack_keys(hipStream_t st, const uint32_t* seed, int depth, uint32_t* out) {
-  hipLaunchKernelGGL(stack_keys_kernel, dim3(1), dim3(64), 0, st, seed, depth, out);
+void stack_keys(hipStream_t st, const uint32_t* seed, int depth, uint32_t* out, int n_used) {
+  hipLaunchKernelGGL(stack_keys_kernel, dim3(1), dim3(64), 0, st, seed, depth, n_used, out);
 }
 
 // -------------------------------------------------------------- residual glue

@@ -69,9 +69,11 @@ void dropout_table_dev(hipStream_t st, float* tbl, int B, int C,
 // out[i] = jax.random.bernoulli(key, keep_rate, (n,))[i].
 void bernoulli_bits(hipStream_t st, uint8_t* out, long n, uint32_t k0, uint32_t k1,
                     float keep_rate);
-// Per-module keys of a `depth`-layer Evoformer stack from the stack key
-// seed[0..1]: out[(layer*9+module)*2 + {0,1}].
-void stack_keys(hipStream_t st, const uint32_t* seed, int depth, uint32_t* out);
+// Per-module keys of a `depth`-layer stack from the stack key seed[0..1]:
+// out[(layer*n_used+module)*2 + {0,1}] = split(sub_layer)[1 + module]
+// (n_used = 9: Evoformer; 5: template pair stack).
+void stack_keys(hipStream_t st, const uint32_t* seed, int depth, uint32_t* out,
+                int n_used = 9);
 // out[0..1] = (0, seed[0]): PRNGKey of a 32-bit seed word, on the device.
 void key_from_bits(hipStream_t st, const uint32_t* seed, uint32_t* out);
 

@@ -348,6 +348,8 @@ size_t msacol_save_bytes(int S, int N, int Cm, int H) {
 void msarow_fwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa_in,
                 const float* msa_mask, const float* pair, const float* tbl, float* msa_out,
                 void* save) {
+  nonnull(msa_in, "msarow msa"); nonnull(msa_mask, "msarow mask"); nonnull(pair, "msarow pair");
+  nonnull(msa_out, "msarow out"); nonnull(save, "msarow save");
   const AttnW& a = w.a;
   if (a.D != 32 || a.Cin != a.Cout || a.H * a.D != a.Cin)
     throw std::runtime_error("msarow: unsupported widths");
@@ -383,6 +385,9 @@ void msarow_fwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa
 void msarow_bwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa_in,
                 const float* msa_mask, const float* pair, const float* tbl, const void* save,
                 const float* dmsa_out, float* dmsa_in, float* dpair) {
+  nonnull(msa_in, "msarow msa"); nonnull(msa_mask, "msarow mask"); nonnull(pair, "msarow pair");
+  nonnull(save, "msarow save"); nonnull(dmsa_out, "msarow dout"); nonnull(dmsa_in, "msarow din");
+  nonnull(dpair, "msarow dpair");
   const AttnW& a = w.a;
   const int Cm = a.Cin, H = a.H, HD = H * a.D;
   const long R = (long)S * N, M = (long)N * N;
@@ -439,6 +444,8 @@ void msarow_bwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa
 
 void msacol_fwd(hipStream_t st, const MsaColW& w, int S, int N, const float* msa_in,
                 const float* msa_mask, const float* tbl, float* msa_out, void* save) {
+  nonnull(msa_in, "msacol msa"); nonnull(msa_mask, "msacol mask"); nonnull(msa_out, "msacol out");
+  nonnull(save, "msacol save");
   const AttnW& a = w.a;
   if (a.D != 32 || S > 32) throw std::runtime_error("msacol: D must be 32 and S <= 32");
   const int Cm = a.Cin, H = a.H, HD = H * a.D;
@@ -467,6 +474,8 @@ void msacol_fwd(hipStream_t st, const MsaColW& w, int S, int N, const float* msa
 void msacol_bwd(hipStream_t st, const MsaColW& w, int S, int N, const float* msa_in,
                 const float* msa_mask, const float* tbl, const void* save,
                 const float* dmsa_out, float* dmsa_in) {
+  nonnull(msa_in, "msacol msa"); nonnull(msa_mask, "msacol mask"); nonnull(save, "msacol save");
+  nonnull(dmsa_out, "msacol dout"); nonnull(dmsa_in, "msacol din");
   const AttnW& a = w.a;
   const int Cm = a.Cin, H = a.H, HD = H * a.D;
   const long R = (long)S * N;

@@ -209,6 +209,8 @@ size_t opm_save_bytes(int S, int N, int O, int C) {
 
 void opm_fwd(hipStream_t st, const OpmW& w, int S, int N, const float* msa, const float* msa_mask,
              const float* pair_in, const float* tbl, float* pair_out, void* save) {
+  nonnull(msa, "opm msa"); nonnull(msa_mask, "opm mask"); nonnull(pair_in, "opm pair");
+  nonnull(pair_out, "opm out"); nonnull(save, "opm save");
   const int Cm = w.Cm, O = w.O, C = w.C;
   if ((S * O) % 32 != 0 || N % 32 != 0) throw std::runtime_error("opm: S*O and N must be multiples of 32");
   const long R = (long)S * N;
@@ -246,6 +248,8 @@ void opm_fwd(hipStream_t st, const OpmW& w, int S, int N, const float* msa, cons
 void opm_bwd(hipStream_t st, const OpmW& w, int S, int N, const float* msa, const float* msa_mask,
              const float* tbl, const void* save, const float* dpair, const float* dmsa_out,
              float* dmsa_in) {
+  nonnull(msa, "opm msa"); nonnull(msa_mask, "opm mask"); nonnull(save, "opm save");
+  nonnull(dpair, "opm dpair"); nonnull(dmsa_out, "opm dout"); nonnull(dmsa_in, "opm din");
   const int Cm = w.Cm, O = w.O, C = w.C;
   const long R = (long)S * N, NC = (long)N * C;
   Carver cv(const_cast<void*>(save));

@@ -112,6 +112,12 @@ struct KTimed {
   }
 };
 
+// Host-side operand check before any launch: a null device pointer becomes
+// an error status, never a kernel reading address 0.
+inline void nonnull(const void* p, const char* what) {
+  if (p == nullptr) throw std::invalid_argument(std::string("null operand: ") + what);
+}
+
 // Thread-local last error message of the C ABI.
 void set_error(const std::string& msg);
 const char* last_error();

@@ -73,6 +73,7 @@ size_t transition_save_bytes(long rows, int C, int F) {
 
 void transition_fwd(hipStream_t st, const TransW& w, long rows, int nt, const float* act_in,
                     const float* tbl, float* act_out, void* save) {
+  nonnull(act_in, "transition act"); nonnull(act_out, "transition out"); nonnull(save, "transition save");
   const int C = w.C, H = w.C * w.F;
   Carver cv(save);
   TransSave<Carver> sv(cv, rows, C, w.F);
@@ -99,6 +100,8 @@ void transition_fwd(hipStream_t st, const TransW& w, long rows, int nt, const fl
 
 void transition_bwd(hipStream_t st, const TransW& w, long rows, int nt, const float* act_in,
                     const float* tbl, const void* save, const float* dout, float* din) {
+  nonnull(act_in, "transition act"); nonnull(save, "transition save");
+  nonnull(dout, "transition dout"); nonnull(din, "transition din");
   const int C = w.C, H = w.C * w.F;
   Carver cv(const_cast<void*>(save));
   TransSave<Carver> sv(cv, rows, C, w.F);

@@ -132,13 +132,15 @@ size_t triattn_save_bytes(int N, int C, int H) {
 
 static void triattn_check(const TriAttnW& w, int N) {
   if (N <= 0 || N % 32 != 0) throw std::runtime_error("triattn: N must be a positive multiple of 32");
-  if (w.D != 32) throw std::runtime_error("triattn: head width 32 only");
+  if (w.D != 32 && w.D != 16) throw std::runtime_error("triattn: head width 16 or 32 only");
 }
 
 void triattn_fwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
                  const float* pair_in, const float* mask, const float* tbl,
                  float* pair_out, void* save) {
   triattn_check(w, N);
+  nonnull(pair_in, "triattn pair_in"); nonnull(mask, "triattn mask");
+  nonnull(pair_out, "triattn pair_out"); nonnull(save, "triattn save");
   const int C = w.C, H = w.H, HD = w.H * w.D;
   const long M = (long)N * N;
   Carver cv(save);
@@ -185,6 +187,8 @@ void triattn_bwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
                  const float* pair_in, const float* mask, const float* tbl,
                  const void* save, const float* dout, float* din) {
   triattn_check(w, N);
+  nonnull(pair_in, "triattn pair_in"); nonnull(mask, "triattn mask"); nonnull(save, "triattn save");
+  nonnull(dout, "triattn dout"); nonnull(din, "triattn din");
   const int C = w.C, H = w.H, HD = w.H * w.D;
   const long M = (long)N * N;
   Carver cv(const_cast<void*>(save));

@@ -239,6 +239,8 @@ static void contraction_fwd(hipStream_t st, bool outgoing, int N, int I, const b
 void trimul_fwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const float* pair_in,
                 const float* mask, const float* tbl, float* pair_out, void* save) {
   trimul_check(N);
+  nonnull(pair_in, "trimul pair_in"); nonnull(mask, "trimul mask");
+  nonnull(pair_out, "trimul pair_out"); nonnull(save, "trimul save");
   const int C = w.C, I = w.I, NC = 4 * I + C;
   const long M = (long)N * N;
   Carver cv(save);
@@ -278,6 +280,8 @@ void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
                 const float* mask, const float* tbl, const void* save, const float* dout,
                 float* din) {
   trimul_check(N);
+  nonnull(pair_in, "trimul pair_in"); nonnull(mask, "trimul mask"); nonnull(save, "trimul save");
+  nonnull(dout, "trimul dout"); nonnull(din, "trimul din");
   const int C = w.C, I = w.I, NC = 4 * I + C;
   const long M = (long)N * N;
   Carver cv(const_cast<void*>(save));

@@ -255,6 +255,40 @@ class EvoformerStack:
         return dpair, dmsa
 
 
+class TemplatePairStack:
+    """The drop-in for TemplatePairStackFwd/Bwd (native/ffi.cu:983-1008)."""
+
+    def __init__(self, weights_dir, depth):
+        self.dir, self.depth = weights_dir.encode(), depth
+
+    def save_bytes(self, n):
+        b = lib().bc2n_tplstack_save_bytes(self.dir, n, self.depth)
+        if b == 0:
+            check(1)
+        return b
+
+    def forward(self, pair, pair_mask, seed=None, dropout=True, out=None, save=None):
+        n = pair.shape[0]
+        if out is None:
+            out = torch.empty_like(pair)
+        if save is None:
+            save = torch.empty(self.save_bytes(n), dtype=torch.uint8, device=pair.device)
+        seed_len = 3 if seed is None else seed.numel()
+        check(lib().bc2n_tplstack_fwd(_stream(), _ptr(pair), _ptr(pair_mask), _ptr(seed),
+                                      seed_len, n, self.depth, int(dropout), self.dir, _ptr(out),
+                                      _ptr(save)))
+        return out, save
+
+    def backward(self, ct, pair_mask, save, seed=None, dropout=True):
+        n = ct.shape[0]
+        dpair = torch.empty_like(ct)
+        seed_len = 3 if seed is None else seed.numel()
+        check(lib().bc2n_tplstack_bwd(_stream(), _ptr(ct), _ptr(pair_mask), _ptr(save),
+                                      _ptr(seed), seed_len, n, self.depth, int(dropout), self.dir,
+                                      _ptr(dpair)))
+        return dpair
+
+
 def dropout_table(rows, channels, key, rate, device="cuda"):
     """[rows, channels] keep/keep_rate table from a JAX key (k0, k1)."""
     tbl = torch.empty(rows, channels, dtype=torch.float32, device=device)

@@ -105,6 +105,25 @@ def init_module(shapes, rng, gates="zero", ln="identity"):
     return out
 
 
+TEMPLATE_MODULES = ("triangle_multiplication_outgoing", "triangle_multiplication_incoming",
+                    "triangle_attention_starting_node", "triangle_attention_ending_node",
+                    "pair_transition")
+
+
+def init_template_block_params(block, rng, gates="zero", ln="identity"):
+    """One TemplateEmbeddingIteration (c_t=64, 4 heads, trimul hidden 64,
+    transition factor 2 -- config.py template_pair_stack)."""
+    sh = module_shapes(c_z=C_T, tri_heads=4, trimul_hidden=64)
+    sh["pair_transition"] = {"input_layer_norm/scale": (C_T,), "input_layer_norm/offset": (C_T,),
+                             "transition1/weights": (C_T, 2 * C_T), "transition1/bias": (2 * C_T,),
+                             "transition2/weights": (2 * C_T, C_T), "transition2/bias": (C_T,)}
+    out = {}
+    for mod in TEMPLATE_MODULES:
+        for pname, arr in init_module(sh[mod], rng, gates, ln).items():
+            out[f"param/block{block}/{mod}/{pname}"] = arr
+    return out
+
+
 def init_block_params(block, rng, modules=None, gates="zero", ln="identity", **shape_kw):
     """Flat {manifest name: array} for one Evoformer block."""
     sh = module_shapes(**shape_kw)

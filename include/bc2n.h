@@ -167,6 +167,27 @@ int bc2n_evoformer_bwd(void* stream, const float* ct_pair, const float* ct_msa,
                        const char* weights_dir, float* dpair, float* dmsa);
 
 /* ------------------------------------------------------------------------
+ * The template pair stack: the drop-in for TemplatePairStackFwd / Bwd
+ * (native/ffi.cu:983-1008, impl TplFwdImpl :403-430, TplBwdImpl :432-456):
+ *   fwd(pair f32[N,N,64], pair_mask f32[N,N], seed; depth, dropout,
+ *       weights_dir) -> (out f32[N,N,64], save)
+ *   bwd(ct f32[N,N,64], pair_mask, save, seed; ...) -> dpair
+ * Blocks are TemplateEmbeddingIteration (modules_multimer.py:1008-1077:
+ * tmo, tmi, tas, tae at C=64 with 4 heads of 16, transition x2), dropout
+ * keys split(sub, 20)[1..5].  save holds bc2n_tplstack_save_bytes() bytes;
+ * seed as for the Evoformer stack.
+ * ---------------------------------------------------------------------- */
+size_t bc2n_tplstack_save_bytes(const char* weights_dir, int N, int64_t depth);
+int bc2n_tplstack_fwd(void* stream, const float* pair, const float* pair_mask,
+                      const uint32_t* seed, int seed_len, int N, int64_t depth,
+                      int64_t dropout, const char* weights_dir, float* out,
+                      void* save);
+int bc2n_tplstack_bwd(void* stream, const float* ct, const float* pair_mask,
+                      const void* save, const uint32_t* seed, int seed_len, int N,
+                      int64_t depth, int64_t dropout, const char* weights_dir,
+                      float* dpair);
+
+/* ------------------------------------------------------------------------
  * Dropout with JAX's own bits.  tbl[b*C+c] = keep/keep_rate where
  * keep = jax.random.bernoulli(key, keep_rate, (B, C)), keep_rate =
  * float32(1) - float32(rate); key = (k0, k1) = jax.random.key_data(key).

@@ -277,3 +277,43 @@ def evoformer_stack(msa, pair, msa_mask, pair_mask, params, depth, stack_key,
                                         f"param/block{b}/", sub, use_dropout,
                                         is_extra_msa, dtype)
     return msa, pair
+
+
+# Template pair stack (modules_multimer.py:1008-1077), rates/orientations of
+# config.py template_pair_stack.
+TPL_MODULES = (
+    ("triangle_multiplication_outgoing", 0.25, "per_row"),
+    ("triangle_multiplication_incoming", 0.25, "per_row"),
+    ("triangle_attention_starting_node", 0.25, "per_row"),
+    ("triangle_attention_ending_node", 0.25, "per_column"),
+    ("pair_transition", 0.0, "per_row"),
+)
+
+
+def template_iteration(act, pair_mask, params, prefix, key, use_dropout, dtype=torch.float64):
+    """modules_multimer.py:1017-1077 (TemplateEmbeddingIteration): the block
+    key is split into 20; keys 1..5 go to the five modules in order."""
+    P = Params(params, prefix, dtype)
+    sub = jax_prng.split(key, 20)[1:6] if key is not None else [None] * 5
+    for (name, rate, orient), k in zip(TPL_MODULES, sub):
+        p = P.sub(name + "/")
+        if name.startswith("triangle_multiplication"):
+            res = triangle_multiplication(act, pair_mask, p, name.endswith("outgoing"))
+        elif name.startswith("triangle_attention"):
+            res = triangle_attention(act, pair_mask, p, name.endswith("ending_node"))
+        else:
+            res = transition(act, pair_mask, p)
+        act = dropout_wrapper(res, act, k, rate, orient, use_dropout)
+    return act
+
+
+def template_stack(act, pair_mask, params, depth, stack_key, use_dropout, dtype=torch.float64):
+    """modules_multimer.py:957-975 (layer_stack of template_iteration_fn)."""
+    carry = stack_key
+    for b in range(depth):
+        if carry is not None:
+            carry, sub = jax_prng.split(carry, 2)
+        else:
+            sub = None
+        act = template_iteration(act, pair_mask, params, f"param/block{b}/", sub, use_dropout, dtype)
+    return act
