@@ -1,17 +1,27 @@
-"""Benchmark of the trunk hot path on one MI355X.
+"""Benchmark of the AF2 trunk hot path on one MI355X.
 
-Workload: flash triangle attention forward +
-backward, pair [224, 224, 128], H=4 x D=32, starting AND ending node, pair
-bias projected from the same tensor, sigmoid gating, 10% of residues masked
-(seeded), upstream gradient N(0,1).  One step = both orientations, forward
-and backward, through the C ABI; inputs and weights are resident in HBM
-before the timed region starts.
+Default workload (the metric's own config): the
+trunk of one design gradient step at L=224 -- forward AND backward of
+  * the template pair stack: 2 blocks, c_t=64 (native_tplstack_fwd/bwd),
+  * the extra-MSA stack: 4 blocks in the reference's pair-only form
+    (extra_msa_mask == 0 in the design step),
+  * the main Evoformer stack: 48 blocks, N_seq=1, c_m=256, c_z=128
+    (native_evoformer_fwd/bwd),
+with dropout on (JAX-exact masks from a stack key), random-init weights
+(LeCun normal, AF2 gate init) and N(0,1) synthetic activations resident in
+HBM, 10% of residues masked.  The embedder, template-feature embedding,
+structure module and losses around the trunk are not part of the timed
+step (they are ~1% of the reference's step and not built yet).
 
-Prints ONE JSON line (the driver's contract).  `roofline` is the dominant
-kernel's achieved MFMA rate (its algorithmic FLOPs per launch / its mean
-launch time from HIP events on its own stream) against the MI355X bf16 dense
-peak; `cpu_baseline` times the oracle (the fp32 torch-CPU restatement of the
-reference's JAX module) on this host on a bounded sample.
+`--workload triattn` times BASELINE configs[1] instead (flash triangle
+attention fwd+bwd, both orientations, L=224).
+
+Prints ONE JSON line.  `roofline` is the dominant kernel's achieved rate
+(its algorithmic work per launch / its mean launch time, HIP events on its
+own stream, recorded in a second pass of the same K steps) against the
+MI355X dense bf16 MFMA peak or the HBM peak; `cpu_baseline` times the
+oracle (fp32 torch-CPU restatement of the reference's JAX modules) on this
+host on a bounded sample and extrapolates to one step.
 """
 import argparse
 import json
@@ -28,37 +38,111 @@ PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0
 
 
+# ----------------------------------------------------------- algorithmic work
 def triattn_flops(n, c=128, h=4):
-    """Algorithmic FLOPs of one triangle-attention module, forward+backward,
-    split by kernel (projection GEMMs, flash core, bias projection)."""
+    """Algorithmic FLOPs of one triangle-attention module, forward+backward."""
     m = n * n
-    return {
-        "gemm_qkvg_fwd": 2 * m * c * 4 * c,
-        "bias_fwd": 2 * m * c * h,
+    return (2 * m * c * 4 * c + 2 * m * c * h + 4 * n ** 3 * c + 2 * m * c * c      # fwd
+            + 2 * m * c * c + 10 * n ** 3 * c + 2 * m * 4 * c * c + 2 * m * c * h)  # bwd
+
+
+def trimul_flops(n, c=128, i=128):
+    """Forward: projections (4I+C outputs) + contraction + output; backward:
+    output dX, two contractions, projection dX."""
+    m = n * n
+    fwd = 2 * m * c * (4 * i + c) + 2 * i * n ** 3 + 2 * m * i * c
+    bwd = 2 * m * c * i + 4 * i * n ** 3 + 2 * m * (4 * i + c) * c
+    return fwd + bwd
+
+
+# executed MFMA work per launch of the kernels the roofline may name
+def kernel_work(name, n):
+    c = 128
+    flops = {
         "attn_fwd": 4 * n ** 3 * c,
-        "gemm_out_fwd": 2 * m * c * c,
-        "gemm_dout_bwd": 2 * m * c * c,
-        "attn_bwd": 10 * n ** 3 * c,
-        "gemm_dx_bwd": 2 * m * 4 * c * c,
-        "bias_bwd": 2 * m * c * h,
-    }
-
-
-# executed MFMA work per launch of each flash kernel (for the roofline line)
-def kernel_flops(name, n, c=128):
-    return {
-        "attn_fwd": 4 * n ** 3 * c,          # S = QK^T, O = PV
-        "attn_bwd_dq": 6 * n ** 3 * c,       # S, dP, dQ
-        "attn_bwd_dkv": 8 * n ** 3 * c,      # S, dP, dV, dK
+        "attn_bwd_dq": 6 * n ** 3 * c,
+        "attn_bwd_dkv": 8 * n ** 3 * c,
         "triattn.gemm_qkvg": 2 * n * n * c * 4 * c,
         "triattn.gemm_dx": 2 * n * n * 4 * c * c,
-        "triattn.gemm_out": 2 * n * n * c * c,
-        "triattn.gemm_dout": 2 * n * n * c * c,
-    }.get(name)
+        "trimul.gemm_proj": 2 * n * n * c * (4 * c + c),
+        "trimul.gemm_dx": 2 * n * n * (4 * c + c) * c,
+        "trimul.contract_fwd": 2 * c * n ** 3,
+        "trimul.contract_bwd": 2 * c * n ** 3,
+        "trans.gemm1": 2 * n * n * c * 4 * c,
+        "trans.gemm2": 2 * n * n * 4 * c * c,
+        "trans.gemm_dh": 2 * n * n * c * 4 * c,
+        "trans.gemm_dx": 2 * n * n * 4 * c * c,
+    }
+    return flops.get(name)
 
 
-def cpu_baseline(n, seconds=12.0):
-    """fp32 oracle triangle attention fwd+bwd (starting node) on the host."""
+# --------------------------------------------------------------- CPU baseline
+def cpu_trunk_baseline(n, budget_s=20.0):
+    """fp32 torch-CPU oracle: one Evoformer block, one pair-only block and one
+    template block forward+backward at length n, scaled to 48 + 4 + 2 blocks."""
+    import numpy as np
+    import torch
+    from bindcraft2_amd import params as bparams
+    from oracle import af2, jax_prng
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    rng = np.random.default_rng(0)
+    f32 = torch.float32
+    prm = bparams.init_block_params(0, rng, gates="zero")
+    tprm = bparams.init_template_block_params(0, rng, gates="zero")
+    m1 = np.ones(n, np.float32)
+    m1[rng.choice(n, int(round(0.1 * n)), replace=False)] = 0
+    pmask = torch.as_tensor(np.outer(m1, m1))
+    mmask = torch.as_tensor(m1[None])
+    key = jax_prng.prng_key(1)
+
+    def evo_block():
+        pair = torch.randn(n, n, 128, requires_grad=True)
+        msa = torch.randn(1, n, 256, requires_grad=True)
+        mo, po = af2.evoformer_iteration(msa, pair, mmask, pmask, prm, "param/block0/", key, True,
+                                         dtype=f32)
+        torch.autograd.grad((po, mo), (pair, msa), (torch.randn_like(po), torch.randn_like(mo)))
+
+    def pair_only_block():
+        # the pair track of an Evoformer block (OPM constant + 5 pair modules)
+        pair = torch.randn(n, n, 128, requires_grad=True)
+        P = af2.Params(prm, "param/block0/", f32)
+        x = pair + P("outer_product_mean/output_b") / 1e-3
+        for name, fn in (("triangle_multiplication_outgoing", lambda a, p: af2.triangle_multiplication(a, pmask, p, True)),
+                         ("triangle_multiplication_incoming", lambda a, p: af2.triangle_multiplication(a, pmask, p, False)),
+                         ("triangle_attention_starting_node", lambda a, p: af2.triangle_attention(a, pmask, p, False)),
+                         ("triangle_attention_ending_node", lambda a, p: af2.triangle_attention(a, pmask, p, True)),
+                         ("pair_transition", lambda a, p: af2.transition(a, pmask, p))):
+            x = x + fn(x, P.sub(name + "/"))
+        torch.autograd.grad(x, pair, torch.randn_like(x))
+
+    def tpl_block():
+        pair = torch.randn(n, n, 64, requires_grad=True)
+        out = af2.template_iteration(pair, pmask, tprm, "param/block0/", key, True, dtype=f32)
+        torch.autograd.grad(out, pair, torch.randn_like(out))
+
+    times = {}
+    spent = 0.0
+    for name, fn in (("evo", evo_block), ("pair_only", pair_only_block), ("tpl", tpl_block)):
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            reps += 1
+            el = time.perf_counter() - t0
+            if el > budget_s / 3 or reps >= 3:
+                break
+        times[name] = el / reps
+        spent += el
+    step_ms = (48 * times["evo"] + 4 * times["pair_only"] + 2 * times["tpl"]) * 1e3
+    return {"value": round(step_ms, 1), "unit": "ms", "cores": threads, "kind": "port",
+            "sample": (f"oracle fp32 torch-CPU, one block each fwd+bwd at L={n}: Evoformer "
+                       f"{times['evo']:.2f} s, pair-only {times['pair_only']:.2f} s, template "
+                       f"{times['tpl']:.2f} s ({spent:.1f} s of CPU work on {threads} threads); "
+                       f"step = 48 x Evoformer + 4 x pair-only + 2 x template (extrapolated)")}
+
+
+def cpu_triattn_baseline(n, seconds=12.0):
     import numpy as np
     import torch
     from bindcraft2_amd import params as bparams
@@ -78,28 +162,57 @@ def cpu_baseline(n, seconds=12.0):
     reps, t0 = 0, time.perf_counter()
     while True:
         out = af2.triangle_attention(pair, mask, P, False)
-        (g,) = torch.autograd.grad(out, pair, dout)
+        torch.autograd.grad(out, pair, dout)
         reps += 1
         el = time.perf_counter() - t0
         if el >= seconds or reps >= 50:
             break
-    flops = sum(triattn_flops(n).values())
-    return {"value": round(flops * reps / el / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
-            "kind": "port",
-            "sample": f"oracle fp32 torch-CPU triangle attention (starting node) fwd+bwd at L={n}, "
-                      f"{reps} reps in {el:.1f} s on {threads} host threads"}
+    return {"value": round(triattn_flops(n) * reps / el / 1e12, 4), "unit": "TFLOP/s",
+            "cores": threads, "kind": "port",
+            "sample": f"oracle fp32 torch-CPU triangle attention (starting node) fwd+bwd at "
+                      f"L={n}, {reps} reps in {el:.1f} s on {threads} host threads"}
+
+
+# ------------------------------------------------------------------- roofline
+def roofline_from(prof, n):
+    cand = {k: v for k, v in prof.items() if kernel_work(k, n) is not None}
+    dom = max(cand, key=lambda k: cand[k][0])
+    tot, cnt = cand[dom]
+    achieved = kernel_work(dom, n) / (tot / cnt * 1e-3) / 1e12
+    return {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2),
+            "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+            "launch_us": round(tot / cnt * 1e3, 2)}
+
+
+def kernel_table(prof):
+    return {k: {"ms_total": round(t, 3), "launches": c, "us_mean": round(t / c * 1e3, 2)}
+            for k, (t, c) in sorted(prof.items(), key=lambda kv: -kv[1][0])}
+
+
+def timed(step, steps, warmup):
+    import torch
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps * 1e3
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--n", type=int, default=224)
+    ap.add_argument("--workload", choices=["trunk", "triattn"], default="trunk")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py: this build measures one GPU only (the hot path runs on one MI355X; "
+        print("bench.py: this build measures one GPU only (the trunk runs on one MI355X; "
               "multi-GPU sharding is a design note, not built)", file=sys.stderr)
         sys.exit(2)
 
@@ -111,79 +224,119 @@ def main():
     dev = torch.device("cuda:0")
     n = args.n
     rng = np.random.default_rng(0)
-    mods = ["triangle_attention_starting_node", "triangle_attention_ending_node"]
-    prm = bparams.init_block_params(0, rng, modules=mods, gates="zero")
-    wdir = bparams.write_manifest(tempfile.mkdtemp(prefix="bc2n_bench_"), prm)
-    pair = torch.randn(n, n, 128, device=dev)
-    m = np.ones(n, np.float32)
-    m[rng.choice(n, int(round(0.1 * n)), replace=False)] = 0
-    mask = torch.as_tensor(np.outer(m, m), device=dev)
-    dout = torch.randn(n, n, 128, device=dev)
-    layers = [ops.TriangleAttention(wdir, f"param/block0/{mods[i]}/", per_column=bool(i))
-              for i in range(2)]
-    outs = [torch.empty_like(pair) for _ in layers]
-    dins = [torch.empty_like(pair) for _ in layers]
-    saves = [torch.empty(l.save_bytes(n), dtype=torch.uint8, device=dev) for l in layers]
+    m1 = np.ones(n, np.float32)
+    m1[rng.choice(n, int(round(0.1 * n)), replace=False)] = 0
+    pmask = torch.as_tensor(np.outer(m1, m1), device=dev)
+    mmask = torch.as_tensor(m1[None], device=dev)
 
-    def step():
-        for l, o, s, d in zip(layers, outs, saves, dins):
-            l.forward(pair, mask, None, out=o, save=s)
-            l.backward(pair, mask, None, s, dout, din=d)
+    if args.workload == "triattn":
+        mods = ["triangle_attention_starting_node", "triangle_attention_ending_node"]
+        prm = bparams.init_block_params(0, rng, modules=mods, gates="zero")
+        wdir = bparams.write_manifest(tempfile.mkdtemp(prefix="bc2n_bench_"), prm)
+        pair = torch.randn(n, n, 128, device=dev)
+        dout = torch.randn(n, n, 128, device=dev)
+        layers = [ops.TriangleAttention(wdir, f"param/block0/{mods[i]}/", per_column=bool(i))
+                  for i in range(2)]
+        outs = [torch.empty_like(pair) for _ in layers]
+        dins = [torch.empty_like(pair) for _ in layers]
+        saves = [torch.empty(l.save_bytes(n), dtype=torch.uint8, device=dev) for l in layers]
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    el = time.perf_counter() - t0
-    ms = el / args.steps * 1e3
-    flops = 2 * sum(triattn_flops(n).values())
-    value = flops / (ms * 1e-3) / 1e12
+        def step():
+            for l, o, s, d in zip(layers, outs, saves, dins):
+                l.forward(pair, pmask, None, out=o, save=s)
+                l.backward(pair, pmask, None, s, dout, din=d)
 
-    # per-kernel durations from HIP events on the launch stream, same K steps
-    b.prof_enable(True)
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    prof = b.prof_read()
-    b.prof_enable(False)
-    kern = {}
-    for name, (tot, cnt) in prof.items():
-        kern[name] = {"ms_total": round(tot, 4), "launches": cnt, "us_mean": round(tot / cnt * 1e3, 2)}
-    flash = {k: v for k, v in prof.items() if kernel_flops(k, n) is not None}
-    dom = max(flash, key=lambda k: flash[k][0])
-    tot, cnt = flash[dom]
-    achieved = kernel_flops(dom, n) / (tot / cnt * 1e-3) / 1e12
-    roofline = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2),
-                "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None}
+        ms = timed(step, args.steps, args.warmup)
+        flops = 2 * triattn_flops(n)
+        b.prof_enable(True)
+        for _ in range(args.steps):
+            step()
+        prof = b.prof_read()
+        b.prof_enable(False)
+        line = {"metric": METRIC, "value": round(flops / (ms * 1e-3) / 1e12, 3),
+                "unit": "TFLOP/s", "higher_is_better": True,
+                "config": {"workload": "triangle attention fwd+bwd, starting+ending node "
+                                       "(BASELINE configs[1])", "L": n, "c_z": 128, "heads": 4,
+                           "head_dim": 32, "masked_residues": 0.1, "flops_per_step": flops}}
+        cpu = None if args.no_cpu_baseline else cpu_triattn_baseline(n)
+    else:
+        # weights: 48 Evoformer blocks, 4 pair-only extra blocks, 2 template blocks
+        evo = {}
+        for blk in range(48):
+            evo.update(bparams.init_block_params(blk, rng, gates="zero"))
+        extra = {}
+        for blk in range(4):
+            extra.update(bparams.init_block_params(
+                blk, rng, gates="zero",
+                modules=["outer_product_mean", "triangle_multiplication_outgoing",
+                         "triangle_multiplication_incoming", "triangle_attention_starting_node",
+                         "triangle_attention_ending_node", "pair_transition"]))
+        tpl = {}
+        for blk in range(2):
+            tpl.update(bparams.init_template_block_params(blk, rng, gates="zero"))
+        root = tempfile.mkdtemp(prefix="bc2n_bench_")
+        d_evo = bparams.write_manifest(os.path.join(root, "evo"), evo)
+        d_extra = bparams.write_manifest(os.path.join(root, "extra"), extra)
+        d_tpl = bparams.write_manifest(os.path.join(root, "tpl"), tpl)
+        main_stack = ops.EvoformerStack(d_evo, 48)
+        extra_stack = ops.EvoformerStack(d_extra, 4, pair_only=True, c_m=64)
+        tpl_stack = ops.TemplatePairStack(d_tpl, 2)
 
-    cpu = None
-    if not args.no_cpu_baseline:
-        cpu = cpu_baseline(n)
+        pair0 = torch.randn(n, n, 128, device=dev)
+        msa0 = torch.randn(1, n, 256, device=dev)
+        emsa0 = torch.randn(1, n, 64, device=dev)
+        emask = torch.zeros(1, n, device=dev)       # the design step's extra MSA mask
+        tpl0 = torch.randn(n, n, 64, device=dev)
+        ct_pair = torch.randn(n, n, 128, device=dev)
+        ct_msa = torch.randn(1, n, 256, device=dev)
+        ct_tpl = torch.randn(n, n, 64, device=dev)
+        keys = [ops.seed_tensor((0, 11 + i), True, dev) for i in range(3)]
+        s_main = torch.empty(main_stack.save_bytes(n, 1), dtype=torch.uint8, device=dev)
+        s_extra = torch.empty(extra_stack.save_bytes(n, 1), dtype=torch.uint8, device=dev)
+        s_tpl = torch.empty(tpl_stack.save_bytes(n), dtype=torch.uint8, device=dev)
+        pe, me = torch.empty_like(pair0), torch.empty_like(emsa0)
+        pm, mm = torch.empty_like(pair0), torch.empty_like(msa0)
+        to = torch.empty_like(tpl0)
 
-    print(json.dumps({
-        "metric": METRIC,
-        "value": round(value, 3),
-        "unit": "TFLOP/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic",
-        "config": {"workload": "triangle attention fwd+bwd, starting+ending node (BASELINE configs[1])",
-                   "L": n, "c_z": 128, "heads": 4, "head_dim": 32, "masked_residues": 0.1,
-                   "flops_per_step": flops},
-        "roofline": roofline,
-        "cpu_baseline": cpu,
-        "kernels": kern,
-    }))
+        def step():
+            tpl_stack.forward(tpl0, pmask, keys[0], out=to, save=s_tpl)
+            extra_stack.forward(pair0, emsa0, pmask, emask, keys[1], save=s_extra,
+                                pair_out=pe, msa_out=me)
+            main_stack.forward(pe, msa0, pmask, mmask, keys[2], save=s_main, pair_out=pm,
+                               msa_out=mm)
+            dp, _ = main_stack.backward(ct_pair, ct_msa, pmask, mmask, s_main, keys[2])
+            extra_stack.backward(dp, torch.zeros_like(emsa0), pmask, emask, s_extra, keys[1])
+            tpl_stack.backward(ct_tpl, pmask, s_tpl, keys[0])
+
+        ms = timed(step, args.steps, args.warmup)
+        b.prof_enable(True)
+        for _ in range(args.steps):
+            step()
+        prof = b.prof_read()
+        b.prof_enable(False)
+        tri = sum(v[0] for k, v in prof.items() if k.startswith("attn_") or k.startswith("triattn."))
+        tm = sum(v[0] for k, v in prof.items() if k.startswith("trimul."))
+        n_tri = 2 * (48 + 4) * args.steps
+        line = {"metric": METRIC, "value": round(ms, 2), "unit": "ms", "higher_is_better": False,
+                "config": {"workload": "design-step trunk fwd+bwd at L=224: 48 Evoformer + 4 "
+                                       "extra-MSA (pair-only) + 2 template blocks "
+                                       "(BASELINE configs[3])",
+                           "L": n, "n_seq": 1, "c_m": 256, "c_z": 128, "c_t": 64,
+                           "dropout": [0.15, 0.25], "masked_residues": 0.1},
+                "triattn_tflops": round(n_tri * triattn_flops(n) / (tri * 1e-3) / 1e12, 2),
+                "trimul_tflops": round(n_tri * trimul_flops(n) / (tm * 1e-3) / 1e12, 2),
+                "save_set_gb": round((s_main.numel() + s_extra.numel() + s_tpl.numel()) / 1e9, 2)}
+        cpu = None if args.no_cpu_baseline else cpu_trunk_baseline(n)
+
+    out = {"metric": line.pop("metric"), "value": line.pop("value"), "unit": line.pop("unit"),
+           "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": round(ms, 3), "higher_is_better": line.pop("higher_is_better"),
+           "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+           "config": line.pop("config"), "roofline": roofline_from(prof, n),
+           "cpu_baseline": cpu}
+    out.update(line)
+    out["kernels"] = kernel_table(prof)
+    print(json.dumps(out))
 
 
 if __name__ == "__main__":
