@@ -10,10 +10,12 @@
 // v_mfma_f32_16x16x32_bf16.  K is walked in BK steps with two LDS buffers and
 // a register prefetch of the next step's tile.
 //
-// The epilogue is called once per (batch, output row, lane column) with the
-// lane's TN accumulator values, which sit 16 columns apart.  Epilogues that
-// need two logically paired columns (a projection and its gate) get them in
-// one call by ordering the weight rows so the pair lands 16 columns apart.
+// Epilogue: the f32 accumulator tile is staged through LDS (reusing the
+// operand buffers, half a tile per pass) and handed to the epilogue as
+// vectors of 8, either 8 consecutive columns of one row (`row`, the default)
+// or 8 consecutive rows of one column (`col`, when `col_mode(n0)` says so for
+// the tile starting at column n0 -- channel-major outputs).  Every global
+// store of an epilogue is therefore a 16- or 32-byte vector.
 #pragma once
 #include "common.h"
 #include "runtime.h"
@@ -30,16 +32,69 @@ struct GemmArgs {
   long b_sn = 0, b_sk = 0, b_sb = 0;  // element strides; b_sn==1 or b_sk==1
 };
 
+// ------------------------------------------------------------ vector helpers
+__device__ __forceinline__ void ld_f8(const float* p, float (&v)[8]) {
+  const float4 a = reinterpret_cast<const float4*>(p)[0];
+  const float4 b = reinterpret_cast<const float4*>(p)[1];
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+__device__ __forceinline__ void st_f8(float* p, const float (&v)[8]) {
+  reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
+  reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
+}
+__device__ __forceinline__ void ld_b8f(const bf16* p, float (&v)[8]) {
+  const bf16x8 a = ld8(p);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = (float)a[e];
+}
+__device__ __forceinline__ void st_b8f(bf16* p, const float (&v)[8]) {
+  bf16x8 a;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) a[e] = (bf16)v[e];
+  st8(p, a);
+}
+template <class T>
+__device__ __forceinline__ void st_any8(T* p, const float (&v)[8]);
+template <>
+__device__ __forceinline__ void st_any8<float>(float* p, const float (&v)[8]) { st_f8(p, v); }
+template <>
+__device__ __forceinline__ void st_any8<bf16>(bf16* p, const float (&v)[8]) { st_b8f(p, v); }
+template <class T>
+__device__ __forceinline__ void ld_any8(const T* p, float (&v)[8]);
+template <>
+__device__ __forceinline__ void ld_any8<float>(const float* p, float (&v)[8]) { ld_f8(p, v); }
+template <>
+__device__ __forceinline__ void ld_any8<bf16>(const bf16* p, float (&v)[8]) { ld_b8f(p, v); }
+
+// Base of every epilogue: row mode only.
+struct EpiRows {
+  static constexpr bool kHasCol = false;
+  __device__ __forceinline__ bool col_mode(int) const { return false; }
+  __device__ __forceinline__ void col(int, int, int, const float (&)[8], const float*, int) const {}
+};
+
+template <int BM, int BN, int BK>
+struct GemmSmem {
+  static constexpr int LDK = BK + 8;
+  static constexpr int AB = 2 * (BM + BN) * LDK * 2;   // bytes of the operand buffers
+  static constexpr int LDT = BN + 4;
+  static constexpr int T = (BM / 2) * LDT * 4;          // bytes of one epilogue pass
+  static constexpr int BYTES = AB > T ? AB : T;
+};
+
 template <int BM, int BN, int BK, bool AK, bool BKC, class Epi>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi) {
+  using SM = GemmSmem<BM, BN, BK>;
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int TM = WM / 16, TN = WN / 16;
-  constexpr int LDK = BK + 8;
+  constexpr int LDK = SM::LDK;
   constexpr int A_CH = BM * BK / 8 / 256;
   constexpr int B_CH = BN * BK / 8 / 256;
   static_assert(A_CH >= 1 && B_CH >= 1, "tile too small for 256 threads");
-  __shared__ __attribute__((aligned(16))) bf16 As[2][BM * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 Bs[2][BN * LDK];
+  __shared__ __attribute__((aligned(16))) unsigned char smem[SM::BYTES];
+  bf16* As = reinterpret_cast<bf16*>(smem);            // [2][BM * LDK]
+  bf16* Bs = As + 2 * BM * LDK;                        // [2][BN * LDK]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -83,16 +138,18 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi) {
     }
   };
   auto sstore = [&](int buf) {
+    bf16* as = As + buf * BM * LDK;
+    bf16* bs = Bs + buf * BN * LDK;
 #pragma unroll
     for (int p = 0; p < A_CH; ++p) {
       const int c = tid + 256 * p;
       if constexpr (AK) {
         const int row = c / (BK / 8), kc = (c % (BK / 8)) * 8;
-        st8(&As[buf][row * LDK + kc], ra[p]);
+        st8(&as[row * LDK + kc], ra[p]);
       } else {
         const int k = c / (BM / 8), mc = (c % (BM / 8)) * 8;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) As[buf][(mc + e) * LDK + k] = ra[p][e];
+        for (int e = 0; e < 8; ++e) as[(mc + e) * LDK + k] = ra[p][e];
       }
     }
 #pragma unroll
@@ -100,11 +157,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi) {
       const int c = tid + 256 * p;
       if constexpr (BKC) {
         const int row = c / (BK / 8), kc = (c % (BK / 8)) * 8;
-        st8(&Bs[buf][row * LDK + kc], rb[p]);
+        st8(&bs[row * LDK + kc], rb[p]);
       } else {
         const int k = c / (BN / 8), nc = (c % (BN / 8)) * 8;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) Bs[buf][(nc + e) * LDK + k] = rb[p][e];
+        for (int e = 0; e < 8; ++e) bs[(nc + e) * LDK + k] = rb[p][e];
       }
     }
   };
@@ -122,16 +179,18 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi) {
   const int fr = lane & 15, fk = (lane >> 4) * 8;
   for (int kt = 0; kt < nk; ++kt) {
     const int buf = kt & 1;
+    const bf16* as = As + buf * BM * LDK;
+    const bf16* bs = Bs + buf * BN * LDK;
     if (kt + 1 < nk) gload((kt + 1) * BK);
 #pragma unroll
     for (int kk = 0; kk < BK / 32; ++kk) {
       bf16x8 af[TM], bfr[TN];
 #pragma unroll
       for (int i = 0; i < TM; ++i)
-        af[i] = ld8(&As[buf][(wm * WM + i * 16 + fr) * LDK + kk * 32 + fk]);
+        af[i] = ld8(&as[(wm * WM + i * 16 + fr) * LDK + kk * 32 + fk]);
 #pragma unroll
       for (int j = 0; j < TN; ++j)
-        bfr[j] = ld8(&Bs[buf][(wn * WN + j * 16 + fr) * LDK + kk * 32 + fk]);
+        bfr[j] = ld8(&bs[(wn * WN + j * 16 + fr) * LDK + kk * 32 + fk]);
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -141,17 +200,44 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi) {
     __syncthreads();
   }
 
-  const int ncol = n0 + wn * WN + fr;
+  // ---- epilogue: stage half a tile (the rows of one wave row) per pass
+  constexpr int LDT = SM::LDT;
+  float* T = reinterpret_cast<float*>(smem);
+  const bool colm = epi.col_mode(n0);
+#pragma unroll 1
+  for (int pass = 0; pass < 2; ++pass) {
+    if (pass) __syncthreads();  // previous pass consumed
+    if (wm == pass) {
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = m0 + wm * WM + i * 16 + (lane >> 4) * 4 + r;
-      if (m >= M) continue;
-      float v[TN];
+        for (int j = 0; j < TN; ++j)
 #pragma unroll
-      for (int j = 0; j < TN; ++j) v[j] = acc[i][j][r];
-      epi.template apply<TN>(b, m, ncol, v);
+          for (int r = 0; r < 4; ++r)
+            T[(i * 16 + (lane >> 4) * 4 + r) * LDT + wn * WN + j * 16 + fr] = acc[i][j][r];
+    }
+    __syncthreads();
+    const int mb = m0 + pass * WM;
+    if (colm) {
+      for (int it = tid; it < BN * (WM / 8); it += 256) {
+        const int c = it % BN, rg = it / BN;
+        const int m = mb + rg * 8, n = n0 + c;
+        if (m >= M || n >= N) continue;
+        const float* tp = T + (rg * 8) * LDT + c;
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = tp[e * LDT];
+        epi.col(b, m, n, v, tp, LDT);
+      }
+    } else {
+      for (int it = tid; it < WM * (BN / 8); it += 256) {
+        const int r = it / (BN / 8), c8 = (it % (BN / 8)) * 8;
+        const int m = mb + r, n = n0 + c8;
+        if (m >= M || n >= N) continue;
+        float v[8];
+        ld_f8(T + r * LDT + c8, v);
+        epi.row(b, m, n, v);
+      }
     }
   }
 }
@@ -166,15 +252,17 @@ template <int BM, int BN, class Epi>
 void gemm(hipStream_t st, const GemmArgs& g, const Epi& epi, const char* name = "gemm") {
   gemm_check(g.M > 0 && g.N > 0 && g.K > 0 && g.batch > 0, "empty shape");
   gemm_check(g.K % 32 == 0, "K must be a multiple of 32");
+  gemm_check(g.N % 8 == 0, "N must be a multiple of 8 (vector epilogue)");
+  gemm_check(!Epi::kHasCol || g.M % 8 == 0, "M must be a multiple of 8 (column epilogue)");
   const bool ak = (g.a_sk == 1), bk = (g.b_sk == 1);
   gemm_check(ak || g.a_sm == 1, "A needs a unit stride");
   gemm_check(bk || g.b_sn == 1, "B needs a unit stride");
   auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
   gemm_check(al16(g.A) && al16(g.B), "operands must be 16-byte aligned");
   if (ak) gemm_check(g.a_sm % 8 == 0, "A row stride must be a multiple of 8");
-  else gemm_check(g.a_sk % 8 == 0 && g.M % 8 == 0, "A(T) stride/M must be multiples of 8");
+  else gemm_check(g.a_sk % 8 == 0, "A(T) stride must be a multiple of 8");
   if (bk) gemm_check(g.b_sn % 8 == 0, "B row stride must be a multiple of 8");
-  else gemm_check(g.b_sk % 8 == 0 && g.N % 8 == 0, "B(T) stride/N must be multiples of 8");
+  else gemm_check(g.b_sk % 8 == 0, "B(T) stride must be a multiple of 8");
   gemm_check(g.batch == 1 || (g.a_sb % 8 == 0 && g.b_sb % 8 == 0), "batch strides");
   const int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
   dim3 grid(tiles, 1, g.batch), block(256);
@@ -200,58 +288,101 @@ void gemm(hipStream_t st, const GemmArgs& g, const Epi& epi, const char* name = 
 
 // C[b][m][n] = act(acc + bias[n]) (+= existing when ACC), OutT in {float, bf16}.
 template <class OutT, bool RELU = false, bool ACC = false>
-struct EpiStore {
+struct EpiStore : EpiRows {
   OutT* C;
   long ldc, sb;
   const float* bias;  // may be null
   int N;
-  template <int TN>
-  __device__ __forceinline__ void apply(int b, int m, int n, const float (&v)[TN]) const {
-    OutT* row = C + (long)b * sb + (long)m * ldc;
+  EpiStore(OutT* c, long l, long s, const float* bi, int n) : C(c), ldc(l), sb(s), bias(bi), N(n) {}
+  __device__ __forceinline__ void row(int b, int m, int n, const float (&v)[8]) const {
+    OutT* p = C + (long)b * sb + (long)m * ldc + n;
+    float x[8];
+    if (bias) {
+      float bb[8];
+      ld_f8(bias + n, bb);
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int c = n + 16 * j;
-      if (c >= N) continue;
-      float x = v[j] + (bias ? bias[c] : 0.f);
-      if (RELU) x = fmaxf(x, 0.f);
-      if (ACC) x += (float)row[c];
-      row[c] = (OutT)x;
+      for (int e = 0; e < 8; ++e) x[e] = v[e] + bb[e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = v[e];
     }
+    if (RELU) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = fmaxf(x[e], 0.f);
+    }
+    if (ACC) {
+      float o[8];
+      ld_any8<OutT>(p, o);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] += o[e];
+    }
+    st_any8<OutT>(p, x);
   }
 };
 
-// Transposed store: C[b][n][m] (channel-major planes), bf16 or f32.
-template <class OutT>
-struct EpiStoreT {
-  OutT* C;
-  long ldc, sb;  // plane stride (per n) and batch stride
-  int N;
-  template <int TN>
-  __device__ __forceinline__ void apply(int b, int m, int n, const float (&v)[TN]) const {
+// bf16 store of acc + bias[n], columns n < qcols additionally scaled by
+// qscale (attention projections: q carries D^-1/2 log2 e).
+struct EpiScaledCols : EpiRows {
+  bf16* C;
+  long ldc;
+  const float* bias;
+  float qscale;
+  int qcols;
+  EpiScaledCols(bf16* c, long l, const float* b, float q, int qc)
+      : C(c), ldc(l), bias(b), qscale(q), qcols(qc) {}
+  __device__ __forceinline__ void row(int, int m, int n, const float (&v)[8]) const {
+    float bb[8], x[8];
+    ld_f8(bias + n, bb);
+    const float s = n < qcols ? qscale : 1.f;  // qcols is a multiple of 8
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int c = n + 16 * j;
-      if (c >= N) continue;
-      C[(long)b * sb + (long)c * ldc + m] = (OutT)v[j];
+    for (int e = 0; e < 8; ++e) x[e] = (v[e] + bb[e]) * s;
+    st_b8f(C + (long)m * ldc + n, x);
+  }
+};
+
+// out[src(m)][n] = in[src(m)][n] + tbl[(m % nt)*C + n] * (acc + bias[n]);
+// src(m) transposes the nt x nt grid when `transpose` (ending-node frame).
+struct EpiResidualRows : EpiRows {
+  const float* in;
+  float* out;
+  const float* bias;
+  const float* tbl;  // may be null
+  int nt, C;
+  bool transpose;
+  EpiResidualRows(const float* i, float* o, const float* b, const float* t, int n, int c, bool tr)
+      : in(i), out(o), bias(b), tbl(t), nt(n), C(c), transpose(tr) {}
+  __device__ __forceinline__ void row(int, int m, int n, const float (&v)[8]) const {
+    const long src = transpose ? (long)(m % nt) * nt + m / nt : m;
+    float bb[8], x[8], r[8];
+    ld_f8(bias + n, bb);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = v[e] + bb[e];
+    if (tbl) {
+      float tt[8];
+      ld_f8(tbl + (long)(m % nt) * C + n, tt);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] *= tt[e];
     }
+    ld_f8(in + src * C + n, r);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] += x[e];
+    st_f8(out + src * C + n, r);
   }
 };
 
 // dH = acc * (H > 0): backward through a ReLU whose output H is kept (bf16).
-struct EpiReluMask {
+struct EpiReluMask : EpiRows {
   bf16* C;
   const bf16* H;
   long ldc;
-  int N;
-  template <int TN>
-  __device__ __forceinline__ void apply(int, int m, int n, const float (&v)[TN]) const {
+  EpiReluMask(bf16* c, const bf16* h, long l) : C(c), H(h), ldc(l) {}
+  __device__ __forceinline__ void row(int, int m, int n, const float (&v)[8]) const {
+    const long o = (long)m * ldc + n;
+    const bf16x8 h = ld8(H + o);
+    float x[8];
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int c = n + 16 * j;
-      if (c >= N) continue;
-      const long o = (long)m * ldc + c;
-      C[o] = (float)H[o] > 0.f ? (bf16)v[j] : (bf16)0.f;
-    }
+    for (int e = 0; e < 8; ++e) x[e] = (float)h[e] > 0.f ? v[e] : 0.f;
+    st_b8f(C + o, x);
   }
 };
 

@@ -44,19 +44,63 @@ __device__ __forceinline__ long ln_src_row(long m, int nt) {
   return q * nt + p;
 }
 
-template <int C, bool FAST, class InT>
+// Sum each of the H values v[0..H) over the TPR-lane group by halving
+// exchanges (reduce-scatter, H/2 + H/4 + ... shuffles instead of H full
+// butterflies); on return v[0] holds the group total of head `h`, the same in
+// every lane whose bits below the last exchanged bit differ.
+template <int TPR, int H>
+__device__ __forceinline__ float reduce_scatter(float (&v)[H], int lane, int& h) {
+  static_assert(H >= 1 && (H & (H - 1)) == 0 && H <= TPR, "H: power of two <= TPR");
+  int base = 0;
+  int bit = TPR / 2;
+#pragma unroll
+  for (int width = H; width > 1; width /= 2) {
+    const bool upper = (lane & bit) != 0;
+#pragma unroll
+    for (int j = 0; j < width / 2; ++j) {
+      const float send = upper ? v[j] : v[j + width / 2];
+      const float keep = upper ? v[j + width / 2] : v[j];
+      v[j] = keep + __shfl_xor(send, bit, 64);
+    }
+    base += upper ? width / 2 : 0;
+    bit /= 2;
+  }
+#pragma unroll
+  for (int b = bit; b >= 1; b /= 2) v[0] += __shfl_xor(v[0], b, 64);
+  h = base;
+  return v[0];
+}
+
+template <int H>
+__device__ __forceinline__ void load_w(const float* __restrict__ wb, int c0, float (&w)[8][H]) {
+  const float4* p = reinterpret_cast<const float4*>(wb + c0 * H);
+#pragma unroll
+  for (int i = 0; i < 2 * H; ++i) {
+    const float4 q = p[i];
+    const float f[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) w[(4 * i + k) / H][(4 * i + k) % H] = f[k];
+  }
+}
+
+// H = 0: plain LayerNorm.  H in {4, 8}: also the pair-bias projection
+// bias_out[h][m] = bias_scale * sum_c y[m][c] W[c][h], from the f32 row.
+template <int C, bool FAST, class InT, int H>
 __global__ __launch_bounds__(256) void ln_fwd_kernel(
     const InT* __restrict__ x, long M, int nt, const float* __restrict__ gamma,
     const float* __restrict__ beta, bf16* __restrict__ y,
-    float* __restrict__ mean_out, float* __restrict__ rstd_out, int H,
+    float* __restrict__ mean_out, float* __restrict__ rstd_out,
     const float* __restrict__ wb, float* __restrict__ bias_out, float bias_scale) {
   using G = LnGeom<C>;
   const int t = threadIdx.x;
   const long m = (long)blockIdx.x * G::RPB + t / G::TPR;
-  const int c0 = (t % G::TPR) * 8;
+  const int gl = t % G::TPR;
+  const int c0 = gl * 8;
   if (m >= M) return;  // whole lane groups exit together
-  float v[8];
+  float v[8], gm[8], bt[8];
   load8f<InT>(x + ln_src_row(m, nt) * C + c0, v);
+  load8f<float>(gamma + c0, gm);
+  load8f<float>(beta + c0, bt);
   float s = 0.f, s2 = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) { s += v[e]; s2 += v[e] * v[e]; }
@@ -77,29 +121,38 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(
   bf16x8 ob;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    o[e] = (v[e] - mu) * r * gamma[c0 + e] + beta[c0 + e];
+    o[e] = (v[e] - mu) * r * gm[e] + bt[e];
     ob[e] = (bf16)o[e];
   }
   if (y) st8(y + m * C + c0, ob);
-  if (t % G::TPR == 0) {
+  if (gl == 0) {
     if (mean_out) mean_out[m] = mu;
     if (rstd_out) rstd_out[m] = r;
   }
-  for (int h = 0; h < H; ++h) {
-    float p = 0.f;
+  if constexpr (H > 0) {
+    float w[8][H], p[H];
+    load_w<H>(wb, c0, w);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) p += o[e] * wb[(c0 + e) * H + h];
-    p = group_sum<G::TPR>(p);
-    if (t % G::TPR == 0) bias_out[(long)h * M + m] = p * bias_scale;
+    for (int h = 0; h < H; ++h) {
+      p[h] = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) p[h] += o[e] * w[e][h];
+    }
+    int h;
+    const float tot = reduce_scatter<G::TPR, H>(p, gl, h);
+    // the lanes that ended with the same head hold the same value; the one
+    // with the lowest index among them writes
+    constexpr int SPAN = G::TPR / H;  // lanes per head after the exchange
+    if ((gl % SPAN) == 0) bias_out[(long)h * M + m] = tot * bias_scale;
   }
 }
 
-// dx[src(m)] (+)= LN'(dy[m] + sum_h dbias[h][m] W[c][h])
-template <int C, class InT, bool ACC>
+// dx[src(m)] (+)= LN'(dy[m] + sum_h dbias[h][m] W[c][h])   (dy may be null)
+template <int C, class InT, bool ACC, int H>
 __global__ __launch_bounds__(256) void ln_bwd_kernel(
     const float* __restrict__ dy, const InT* __restrict__ x, long M, int nt,
     const float* __restrict__ gamma, const float* __restrict__ mean,
-    const float* __restrict__ rstd, float* __restrict__ dx, int H,
+    const float* __restrict__ rstd, float* __restrict__ dx,
     const float* __restrict__ dbias, const float* __restrict__ wb) {
   using G = LnGeom<C>;
   const int t = threadIdx.x;
@@ -107,25 +160,31 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(
   const int c0 = (t % G::TPR) * 8;
   if (m >= M) return;
   const long src = ln_src_row(m, nt);
-  float xv[8], g[8];
+  float xv[8], g[8], gm[8];
   load8f<InT>(x + src * C + c0, xv);
+  load8f<float>(gamma + c0, gm);
   if (dy) {
     load8f<float>(dy + m * C + c0, g);
   } else {
 #pragma unroll
     for (int e = 0; e < 8; ++e) g[e] = 0.f;
   }
-  for (int h = 0; h < H; ++h) {
-    const float db = dbias[(long)h * M + m];
+  if constexpr (H > 0) {
+    float w[8][H];
+    load_w<H>(wb, c0, w);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) g[e] += db * wb[(c0 + e) * H + h];
+    for (int h = 0; h < H; ++h) {
+      const float db = dbias[(long)h * M + m];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) g[e] += db * w[e][h];
+    }
   }
   const float mu = mean[m], r = rstd[m];
   float sg = 0.f, sgx = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     xv[e] = (xv[e] - mu) * r;
-    g[e] *= gamma[c0 + e];
+    g[e] *= gm[e];
     sg += g[e];
     sgx += g[e] * xv[e];
   }
@@ -150,8 +209,9 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(
 }
 
 // Channel-major input: x is [C][M] (one plane per channel).  A block of 64
-// rows stages the [C][64] tile through LDS and then runs the row-wise
-// normaliser on it; the output is row-major [M][C] bf16.
+// rows stages the [C][64] tile through LDS (float4 loads along m) and then
+// normalises it 4 lanes per row; the output is row-major [M][C] bf16.
+// Requires M % 4 == 0.
 template <int C, bool FAST>
 __global__ __launch_bounds__(256) void ln_fwd_cm_kernel(
     const float* __restrict__ x, long M, const float* __restrict__ gamma,
@@ -161,13 +221,17 @@ __global__ __launch_bounds__(256) void ln_fwd_cm_kernel(
   __shared__ float tile[R][C + 1];
   const int t = threadIdx.x;
   const long m0 = (long)blockIdx.x * R;
-  for (int i = t; i < C * R; i += 256) {
-    const int c = i / R, r = i % R;
-    const long m = m0 + r;
-    tile[r][c] = (m < M) ? x[(long)c * M + m] : 0.f;
+  for (int i = t; i < C * (R / 4); i += 256) {
+    const int c = i / (R / 4), q = (i % (R / 4)) * 4;
+    const long m = m0 + q;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (m < M) v = *reinterpret_cast<const float4*>(x + (long)c * M + m);
+    tile[q + 0][c] = v.x;
+    tile[q + 1][c] = v.y;
+    tile[q + 2][c] = v.z;
+    tile[q + 3][c] = v.w;
   }
   __syncthreads();
-  // 4 lanes per row, C/4 channels per lane
   constexpr int CPL = C / 4;
   const int r = t / 4, part = t % 4;
   const long m = m0 + r;
@@ -217,25 +281,37 @@ __global__ __launch_bounds__(256) void ln_bwd_cm_kernel(
   __shared__ float tile[R][C + 1];
   const int t = threadIdx.x;
   const long m0 = (long)blockIdx.x * R;
-  for (int i = t; i < C * R; i += 256) {
-    const int c = i / R, r = i % R;
-    const long m = m0 + r;
-    tile[r][c] = (m < M) ? x[(long)c * M + m] : 0.f;
+  for (int i = t; i < C * (R / 4); i += 256) {
+    const int c = i / (R / 4), q = (i % (R / 4)) * 4;
+    const long m = m0 + q;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (m < M) v = *reinterpret_cast<const float4*>(x + (long)c * M + m);
+    tile[q + 0][c] = v.x;
+    tile[q + 1][c] = v.y;
+    tile[q + 2][c] = v.z;
+    tile[q + 3][c] = v.w;
   }
   __syncthreads();
   constexpr int CPL = C / 4;
   const int r = t / 4, part = t % 4;
   const long m = m0 + r;
-  const float mu = (m < M) ? mean[m] : 0.f, rs = (m < M) ? rstd[m] : 0.f;
+  const bool live = m < M;
+  const float mu = live ? mean[m] : 0.f, rs = live ? rstd[m] : 0.f;
   float xh[CPL], g[CPL];
   float sg = 0.f, sgx = 0.f;
 #pragma unroll
-  for (int e = 0; e < CPL; ++e) {
-    const int c = part * CPL + e;
-    xh[e] = (tile[r][c] - mu) * rs;
-    g[e] = (m < M) ? dy[m * C + c] * gamma[c] : 0.f;
-    sg += g[e];
-    sgx += g[e] * xh[e];
+  for (int e0 = 0; e0 < CPL; e0 += 4) {
+    float4 d = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (live) d = *reinterpret_cast<const float4*>(dy + m * C + part * CPL + e0);
+    const float dv[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int e = e0 + k, c = part * CPL + e;
+      xh[e] = (tile[r][c] - mu) * rs;
+      g[e] = dv[k] * gamma[c];
+      sg += g[e];
+      sgx += g[e] * xh[e];
+    }
   }
   sg = group_sum<4>(sg) / C;
   sgx = group_sum<4>(sgx) / C;
@@ -246,27 +322,45 @@ __global__ __launch_bounds__(256) void ln_bwd_cm_kernel(
     tile[r][c] = rs * (g[e] - sg - xh[e] * sgx);
   }
   __syncthreads();
-  for (int i = t; i < C * R; i += 256) {
-    const int c = i / R, rr = i % R;
-    const long mm = m0 + rr;
-    if (mm < M) dx[(long)c * M + mm] = (bf16)tile[rr][c];
+  for (int i = t; i < C * (R / 4); i += 256) {
+    const int c = i / (R / 4), q = (i % (R / 4)) * 4;
+    const long mm = m0 + q;
+    if (mm < M) {
+      bf16x4 o;
+      o[0] = (bf16)tile[q + 0][c];
+      o[1] = (bf16)tile[q + 1][c];
+      o[2] = (bf16)tile[q + 2][c];
+      o[3] = (bf16)tile[q + 3][c];
+      *reinterpret_cast<bf16x4*>(dx + (long)c * M + mm) = o;
+    }
   }
 }
 
 // ------------------------------------------------------------------ launchers
 
-template <int C, class InT>
-static void ln_fwd_dispatch(hipStream_t st, const InT* x, long M, int nt,
-                            const float* gamma, const float* beta, bf16* y,
-                            float* mean, float* rstd, bool fast, int H,
-                            const float* wb, float* bias_out, float bs) {
+template <int C, int H>
+static void ln_fwd_launch(hipStream_t st, const float* x, long M, int nt, const float* gamma,
+                          const float* beta, bf16* y, float* mean, float* rstd, bool fast,
+                          const float* wb, float* bias_out, float bs) {
   const int grid = (int)((M + LnGeom<C>::RPB - 1) / LnGeom<C>::RPB);
   if (fast)
-    hipLaunchKernelGGL((ln_fwd_kernel<C, true, InT>), dim3(grid), dim3(256), 0, st,
-                       x, M, nt, gamma, beta, y, mean, rstd, H, wb, bias_out, bs);
+    hipLaunchKernelGGL((ln_fwd_kernel<C, true, float, H>), dim3(grid), dim3(256), 0, st, x, M, nt,
+                       gamma, beta, y, mean, rstd, wb, bias_out, bs);
   else
-    hipLaunchKernelGGL((ln_fwd_kernel<C, false, InT>), dim3(grid), dim3(256), 0, st,
-                       x, M, nt, gamma, beta, y, mean, rstd, H, wb, bias_out, bs);
+    hipLaunchKernelGGL((ln_fwd_kernel<C, false, float, H>), dim3(grid), dim3(256), 0, st, x, M, nt,
+                       gamma, beta, y, mean, rstd, wb, bias_out, bs);
+}
+
+template <int C>
+static void ln_fwd_dispatch(hipStream_t st, const float* x, long M, int nt, const float* gamma,
+                            const float* beta, bf16* y, float* mean, float* rstd, bool fast, int H,
+                            const float* wb, float* bias_out, float bs) {
+  switch (H) {
+    case 0: ln_fwd_launch<C, 0>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, wb, bias_out, bs); break;
+    case 4: ln_fwd_launch<C, 4>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, wb, bias_out, bs); break;
+    case 8: ln_fwd_launch<C, 8>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, wb, bias_out, bs); break;
+    default: throw std::runtime_error("ln_fwd: bias heads must be 0, 4 or 8");
+  }
 }
 
 void ln_fwd_f32(hipStream_t st, const float* x, long M, int C, int nt,
@@ -281,18 +375,29 @@ void ln_fwd_f32(hipStream_t st, const float* x, long M, int C, int nt,
   }
 }
 
-template <int C>
-static void ln_bwd_dispatch(hipStream_t st, const float* dy, const float* x, long M,
-                            int nt, const float* gamma, const float* mean,
-                            const float* rstd, float* dx, bool acc, int H,
-                            const float* dbias, const float* wb) {
+template <int C, int H>
+static void ln_bwd_launch(hipStream_t st, const float* dy, const float* x, long M, int nt,
+                          const float* gamma, const float* mean, const float* rstd, float* dx,
+                          bool acc, const float* dbias, const float* wb) {
   const int grid = (int)((M + LnGeom<C>::RPB - 1) / LnGeom<C>::RPB);
   if (acc)
-    hipLaunchKernelGGL((ln_bwd_kernel<C, float, true>), dim3(grid), dim3(256), 0, st,
-                       dy, x, M, nt, gamma, mean, rstd, dx, H, dbias, wb);
+    hipLaunchKernelGGL((ln_bwd_kernel<C, float, true, H>), dim3(grid), dim3(256), 0, st, dy, x, M,
+                       nt, gamma, mean, rstd, dx, dbias, wb);
   else
-    hipLaunchKernelGGL((ln_bwd_kernel<C, float, false>), dim3(grid), dim3(256), 0, st,
-                       dy, x, M, nt, gamma, mean, rstd, dx, H, dbias, wb);
+    hipLaunchKernelGGL((ln_bwd_kernel<C, float, false, H>), dim3(grid), dim3(256), 0, st, dy, x, M,
+                       nt, gamma, mean, rstd, dx, dbias, wb);
+}
+
+template <int C>
+static void ln_bwd_dispatch(hipStream_t st, const float* dy, const float* x, long M, int nt,
+                            const float* gamma, const float* mean, const float* rstd, float* dx,
+                            bool acc, int H, const float* dbias, const float* wb) {
+  switch (H) {
+    case 0: ln_bwd_launch<C, 0>(st, dy, x, M, nt, gamma, mean, rstd, dx, acc, dbias, wb); break;
+    case 4: ln_bwd_launch<C, 4>(st, dy, x, M, nt, gamma, mean, rstd, dx, acc, dbias, wb); break;
+    case 8: ln_bwd_launch<C, 8>(st, dy, x, M, nt, gamma, mean, rstd, dx, acc, dbias, wb); break;
+    default: throw std::runtime_error("ln_bwd: bias heads must be 0, 4 or 8");
+  }
 }
 
 void ln_bwd_f32(hipStream_t st, const float* dy, const float* x, long M, int C,
@@ -308,6 +413,7 @@ void ln_bwd_f32(hipStream_t st, const float* dy, const float* x, long M, int C,
 
 void ln_fwd_cm(hipStream_t st, const float* x, long M, int C, const float* gamma,
                const float* beta, bf16* y, float* mean, float* rstd, bool fast) {
+  if (M % 4 != 0) throw std::runtime_error("ln_fwd_cm: M must be a multiple of 4");
   const int grid = (int)((M + 63) / 64);
   if (C == 128) {
     if (fast) hipLaunchKernelGGL((ln_fwd_cm_kernel<128, true>), dim3(grid), dim3(256), 0, st, x, M, gamma, beta, y, mean, rstd);
@@ -322,6 +428,7 @@ void ln_fwd_cm(hipStream_t st, const float* x, long M, int C, const float* gamma
 
 void ln_bwd_cm(hipStream_t st, const float* dy, const float* x, long M, int C,
                const float* gamma, const float* mean, const float* rstd, bf16* dx) {
+  if (M % 4 != 0) throw std::runtime_error("ln_bwd_cm: M must be a multiple of 4");
   const int grid = (int)((M + 63) / 64);
   if (C == 128) hipLaunchKernelGGL((ln_bwd_cm_kernel<128>), dim3(grid), dim3(256), 0, st, dy, x, M, gamma, mean, rstd, dx);
   else if (C == 64) hipLaunchKernelGGL((ln_bwd_cm_kernel<64>), dim3(grid), dim3(256), 0, st, dy, x, M, gamma, mean, rstd, dx);

@@ -18,47 +18,6 @@ namespace bc2n {
 
 namespace {
 
-struct EpiQKVG2 {
-  bf16* C;
-  long ldc;
-  const float* bias;
-  float qscale;
-  int qcols, N;
-  template <int TN>
-  __device__ __forceinline__ void apply(int, int m, int n, const float (&v)[TN]) const {
-    bf16* row = C + (long)m * ldc;
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int c = n + 16 * j;
-      if (c >= N) continue;
-      float x = v[j] + bias[c];
-      if (c < qcols) x *= qscale;
-      row[c] = (bf16)x;
-    }
-  }
-};
-
-struct EpiAddRows2 {
-  const float* in;
-  float* out;
-  const float* bias;
-  const float* tbl;
-  int nt, C;
-  template <int TN>
-  __device__ __forceinline__ void apply(int, int m, int n, const float (&v)[TN]) const {
-    const float* t = tbl ? tbl + (long)(m % nt) * C : nullptr;
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int c = n + 16 * j;
-      if (c >= C) continue;
-      float x = v[j] + bias[c];
-      if (t) x *= t[c];
-      const long o = (long)m * C + c;
-      out[o] = in[o] + x;
-    }
-  }
-};
-
 // Gated-attention weights shared by the row and column modules:
 // [Wq|Wk|Wv|Wg] (C_in x 4HD) in both orientations, gate bias, output.
 void attn_weights(WeightStore& ws, const std::string& P, AttnW& w) {
@@ -279,7 +238,7 @@ void qkvg_gemm(hipStream_t st, const AttnW& w, long rows, const bf16* xn, bf16* 
   g.M = (int)rows; g.N = 4 * HD; g.K = w.Cin;
   g.A = xn; g.a_sm = w.Cin; g.a_sk = 1;
   g.B = w.wqkvg_t; g.b_sn = w.Cin; g.b_sk = 1;
-  gemm<128, 128>(st, g, EpiQKVG2{qkvg, 4L * HD, w.bqkvg, qscale, HD, 4 * HD}, name);
+  gemm<128, 128>(st, g, EpiScaledCols(qkvg, 4L * HD, w.bqkvg, qscale, HD), name);
 }
 
 void out_gemm(hipStream_t st, const AttnW& w, long rows, const bf16* og, const float* in,
@@ -289,7 +248,7 @@ void out_gemm(hipStream_t st, const AttnW& w, long rows, const bf16* og, const f
   g.M = (int)rows; g.N = w.Cout; g.K = HD;
   g.A = og; g.a_sm = HD; g.a_sk = 1;
   g.B = w.wo_t; g.b_sn = HD; g.b_sk = 1;
-  gemm<128, 128>(st, g, EpiAddRows2{in, out, w.bo, tbl, nt, w.Cout}, name);
+  gemm<128, 128>(st, g, EpiResidualRows(in, out, w.bo, tbl, nt, w.Cout, false), name);
 }
 
 // d(og) = dd . Wo^T and, after the attention backward, d(xn) = dqkvg . Wcat^T

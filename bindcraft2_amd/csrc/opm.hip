@@ -18,77 +18,75 @@ namespace bc2n {
 namespace {
 
 // lr = (acc + b) * mask -> left_t [N][S][O] and right [S*N][O] (bf16)
-struct EpiOpmLR {
+struct EpiOpmLR : EpiRows {
   bf16 *left_t, *right;
   const float *b, *mask;
   int S, N, O;
-  template <int TN>
-  __device__ __forceinline__ void apply(int, int m, int n, const float (&v)[TN]) const {
+  EpiOpmLR(bf16* l, bf16* r, const float* bb, const float* mk, int s, int n, int o)
+      : left_t(l), right(r), b(bb), mask(mk), S(s), N(n), O(o) {}
+  __device__ __forceinline__ void row(int, int m, int n, const float (&v)[8]) const {
     const int s = m / N, r = m % N;
     const float mk = mask[m];
+    float bb[8], x[8];
+    ld_f8(b + n, bb);
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int e = n + 16 * j;
-      if (e >= 2 * O) continue;
-      const float x = (v[j] + b[e]) * mk;
-      if (e < O) left_t[((long)r * S + s) * O + e] = (bf16)x;
-      else right[(long)m * O + (e - O)] = (bf16)x;
-    }
+    for (int e = 0; e < 8; ++e) x[e] = (v[e] + bb[e]) * mk;
+    if (n < O) st_b8f(left_t + ((long)r * S + s) * O + n, x);
+    else st_b8f(right + (long)m * O + (n - O), x);
   }
 };
 
 // R'[(s,j)][(c,f)] -> Rp[(j,f)][(s,c)]  (the main GEMM's K-contiguous B)
-struct EpiOpmR {
+struct EpiOpmR : EpiRows {
   bf16* rp;
   int S, N, O, C;
-  template <int TN>
-  __device__ __forceinline__ void apply(int, int m, int n, const float (&v)[TN]) const {
+  EpiOpmR(bf16* r, int s, int n, int o, int c) : rp(r), S(s), N(n), O(o), C(c) {}
+  __device__ __forceinline__ void row(int, int m, int n, const float (&v)[8]) const {
     const int s = m / N, jj = m % N;
+    const int c = n / C, f0 = n % C;  // 8 columns share c (C % 8 == 0)
 #pragma unroll
-    for (int t = 0; t < TN; ++t) {
-      const int col = n + 16 * t;
-      if (col >= O * C) continue;
-      const int c = col / C, f = col % C;
-      rp[(((long)jj * C + f) * S + s) * O + c] = (bf16)v[t];
-    }
+    for (int e = 0; e < 8; ++e) rp[(((long)jj * C + f0 + e) * S + s) * O + c] = (bf16)v[e];
   }
 };
 
 // pair_out[i][j][f] = pair_in + tbl[j][f] * (acc + b[f]) * normf[i][j]
-struct EpiOpmOut {
+struct EpiOpmOut : EpiRows {
   const float* in;
   float* out;
   const float *b, *normf, *tbl;
   int N, C;
-  template <int TN>
-  __device__ __forceinline__ void apply(int, int i, int n, const float (&v)[TN]) const {
+  EpiOpmOut(const float* i, float* o, const float* bb, const float* nf, const float* t, int n, int c)
+      : in(i), out(o), b(bb), normf(nf), tbl(t), N(n), C(c) {}
+  __device__ __forceinline__ void row(int, int i, int n, const float (&v)[8]) const {
+    const int jj = n / C, f0 = n % C;
+    const float nf = normf[(long)i * N + jj];
+    float bb[8], x[8], r[8];
+    ld_f8(b + f0, bb);
 #pragma unroll
-    for (int t = 0; t < TN; ++t) {
-      const int col = n + 16 * t;
-      if (col >= N * C) continue;
-      const int jj = col / C, f = col % C;
-      float x = (v[t] + b[f]) * normf[(long)i * N + jj];
-      if (tbl) x *= tbl[(long)jj * C + f];
-      const long o = (long)i * N * C + col;
-      out[o] = in[o] + x;
+    for (int e = 0; e < 8; ++e) x[e] = (v[e] + bb[e]) * nf;
+    if (tbl) {
+      float tt[8];
+      ld_f8(tbl + (long)jj * C + f0, tt);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] *= tt[e];
     }
+    const long o = (long)i * N * C + n;
+    ld_f8(in + o, r);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] += x[e];
+    st_f8(out + o, r);
   }
 };
 
 // dR'[(s,c)][(j,f)] -> dRp2[(s,j)][(c,f)] (bf16)
-struct EpiOpmDR {
+struct EpiOpmDR : EpiRows {
   bf16* d;
   int S, N, O, C;
-  template <int TN>
-  __device__ __forceinline__ void apply(int, int m, int n, const float (&v)[TN]) const {
+  EpiOpmDR(bf16* dd, int s, int n, int o, int c) : d(dd), S(s), N(n), O(o), C(c) {}
+  __device__ __forceinline__ void row(int, int m, int n, const float (&v)[8]) const {
     const int s = m / O, c = m % O;
-#pragma unroll
-    for (int t = 0; t < TN; ++t) {
-      const int col = n + 16 * t;
-      if (col >= N * C) continue;
-      const int jj = col / C, f = col % C;
-      d[((long)s * N + jj) * O * C + (long)c * C + f] = (bf16)v[t];
-    }
+    const int jj = n / C, f0 = n % C;
+    st_b8f(d + ((long)s * N + jj) * O * C + (long)c * C + f0, v);
   }
 };
 
@@ -232,17 +230,17 @@ void opm_fwd(hipStream_t st, const OpmW& w, int S, int N, const float* msa, cons
   g1.M = (int)R; g1.N = 2 * O; g1.K = Cm;
   g1.A = xn; g1.a_sm = Cm; g1.a_sk = 1;
   g1.B = w.wlr_t; g1.b_sn = Cm; g1.b_sk = 1;
-  gemm<64, 64>(st, g1, EpiOpmLR{sv.left_t, right, w.blr, msa_mask, S, N, O}, "opm.gemm_lr");
+  gemm<64, 64>(st, g1, EpiOpmLR(sv.left_t, right, w.blr, msa_mask, S, N, O), "opm.gemm_lr");
   GemmArgs g2;
   g2.M = (int)R; g2.N = O * C; g2.K = O;
   g2.A = right; g2.a_sm = O; g2.a_sk = 1;
   g2.B = w.wt; g2.b_sn = O; g2.b_sk = 1;
-  gemm<64, 64>(st, g2, EpiOpmR{sv.rp, S, N, O, C}, "opm.gemm_r");
+  gemm<64, 64>(st, g2, EpiOpmR(sv.rp, S, N, O, C), "opm.gemm_r");
   GemmArgs g3;
   g3.M = N; g3.N = N * C; g3.K = S * O;
   g3.A = sv.left_t; g3.a_sm = (long)S * O; g3.a_sk = 1;
   g3.B = sv.rp; g3.b_sn = (long)S * O; g3.b_sk = 1;
-  gemm<128, 128>(st, g3, EpiOpmOut{pair_in, pair_out, w.bo, sv.normf, tbl, N, C}, "opm.gemm_out");
+  gemm<128, 128>(st, g3, EpiOpmOut(pair_in, pair_out, w.bo, sv.normf, tbl, N, C), "opm.gemm_out");
 }
 
 void opm_bwd(hipStream_t st, const OpmW& w, int S, int N, const float* msa, const float* msa_mask,
@@ -298,7 +296,7 @@ void opm_bwd(hipStream_t st, const OpmW& w, int S, int N, const float* msa, cons
     g.M = S * O; g.N = (int)NC; g.K = N;
     g.A = sv.left_t; g.a_sm = 1; g.a_sk = (long)S * O;
     g.B = dact; g.b_sn = 1; g.b_sk = NC;
-    gemm<64, 64>(st, g, EpiOpmDR{drp, S, N, O, C}, "opm.gemm_drp");
+    gemm<64, 64>(st, g, EpiOpmDR(drp, S, N, O, C), "opm.gemm_drp");
   }
   {  // dright partials: [chunk][(s,j)][e]
     GemmArgs g;

@@ -11,28 +11,6 @@ namespace bc2n {
 
 namespace {
 
-// out[m] = in[m] + tbl[(m%nt)*C + c] * (acc + bias[c])
-struct EpiAddRows {
-  const float* in;
-  float* out;
-  const float* bias;
-  const float* tbl;
-  int nt, C;
-  template <int TN>
-  __device__ __forceinline__ void apply(int, int m, int n, const float (&v)[TN]) const {
-    const float* t = tbl ? tbl + (long)(m % nt) * C : nullptr;
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int c = n + 16 * j;
-      if (c >= C) continue;
-      float x = v[j] + bias[c];
-      if (t) x *= t[c];
-      const long o = (long)m * C + c;
-      out[o] = in[o] + x;
-    }
-  }
-};
-
 template <class A>
 struct TransSave {
   float *mean, *rstd;
@@ -95,7 +73,7 @@ void transition_fwd(hipStream_t st, const TransW& w, long rows, int nt, const fl
   g2.M = (int)rows; g2.N = C; g2.K = H;
   g2.A = sv.h; g2.a_sm = H; g2.a_sk = 1;
   g2.B = w.w2_t; g2.b_sn = H; g2.b_sk = 1;
-  gemm<128, 128>(st, g2, EpiAddRows{act_in, act_out, w.b2, tbl, nt, C}, "trans.gemm2");
+  gemm<128, 128>(st, g2, EpiResidualRows(act_in, act_out, w.b2, tbl, nt, C, false), "trans.gemm2");
 }
 
 void transition_bwd(hipStream_t st, const TransW& w, long rows, int nt, const float* act_in,
@@ -123,7 +101,7 @@ void transition_bwd(hipStream_t st, const TransW& w, long rows, int nt, const fl
   g1.M = (int)rows; g1.N = H; g1.K = C;
   g1.A = dd; g1.a_sm = C; g1.a_sk = 1;
   g1.B = w.w2; g1.b_sn = C; g1.b_sk = 1;
-  gemm<128, 128>(st, g1, EpiReluMask{dh, sv.h, H, H}, "trans.gemm_dh");
+  gemm<128, 128>(st, g1, EpiReluMask(dh, sv.h, H), "trans.gemm_dh");
   GemmArgs g2;
   g2.M = (int)rows; g2.N = C; g2.K = H;
   g2.A = dh; g2.a_sm = H; g2.a_sk = 1;

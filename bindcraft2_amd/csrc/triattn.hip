@@ -21,50 +21,6 @@ namespace bc2n {
 
 namespace {
 
-// qkvg epilogue: bf16 store with per-column bias and the q-column scale.
-struct EpiQKVG {
-  bf16* C;
-  long ldc;
-  const float* bias;
-  float qscale;
-  int qcols, N;
-  template <int TN>
-  __device__ __forceinline__ void apply(int, int m, int n, const float (&v)[TN]) const {
-    bf16* row = C + (long)m * ldc;
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int c = n + 16 * j;
-      if (c >= N) continue;
-      float x = v[j] + bias[c];
-      if (c < qcols) x *= qscale;
-      row[c] = (bf16)x;
-    }
-  }
-};
-
-// out[src(m)] = in[src(m)] + tbl[(m % nt)*C + c] * (acc + bias[c])
-struct EpiResidual {
-  const float* in;
-  float* out;
-  const float* bias;
-  const float* tbl;  // may be null
-  int nt, C;
-  bool transpose;
-  template <int TN>
-  __device__ __forceinline__ void apply(int, int m, int n, const float (&v)[TN]) const {
-    const long src = transpose ? (long)(m % nt) * nt + m / nt : m;
-    const float* t = tbl ? tbl + (long)(m % nt) * C : nullptr;
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int c = n + 16 * j;
-      if (c >= C) continue;
-      float x = v[j] + bias[c];
-      if (t) x *= t[c];
-      out[src * C + c] = in[src * C + c] + x;
-    }
-  }
-};
-
 template <class A>
 struct TriAttnSave {
   float *mean, *rstd, *bias, *lse;
@@ -161,7 +117,7 @@ void triattn_fwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
   g1.A = xn; g1.a_sm = C; g1.a_sk = 1;
   g1.B = w.wqkvg_t; g1.b_sn = C; g1.b_sk = 1;
   const float qscale = LOG2E / std::sqrt((float)w.D);
-  gemm<128, 128>(st, g1, EpiQKVG{sv.qkvg, 4L * HD, w.bqkvg, qscale, HD, 4 * HD},
+  gemm<128, 128>(st, g1, EpiScaledCols(sv.qkvg, 4L * HD, w.bqkvg, qscale, HD),
                  "triattn.gemm_qkvg");
 
   AttnArgs a;
@@ -179,7 +135,7 @@ void triattn_fwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
   g2.M = (int)M; g2.N = C; g2.K = HD;
   g2.A = og; g2.a_sm = HD; g2.a_sk = 1;
   g2.B = w.wo_t; g2.b_sn = HD; g2.b_sk = 1;
-  gemm<128, 128>(st, g2, EpiResidual{pair_in, pair_out, w.bo, tbl, N, C, per_column},
+  gemm<128, 128>(st, g2, EpiResidualRows(pair_in, pair_out, w.bo, tbl, N, C, per_column),
                  "triattn.gemm_out");
 }
 

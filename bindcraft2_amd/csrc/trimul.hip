@@ -25,46 +25,53 @@ namespace {
 __host__ __device__ inline int col_proj(int ch) { return (ch / 16) * 32 + ch % 16; }
 __host__ __device__ inline int col_gate(int ch) { return (ch / 16) * 32 + 16 + ch % 16; }
 
+// Projection epilogue.  Tiles of the [proj|gate] columns (n0 < 4I) run in
+// column mode: the thread of a proj column reads its gate column (16 to the
+// right, same tile) from LDS and writes 8 consecutive m of the channel-major
+// planes: a = mask * proj * sigmoid(gate) into left/right, proj and gate
+// pre-activations into psave/gsave.  Tiles of gating_linear columns run in
+// row mode: g_out[m][c] = sigmoid(acc + b).
 struct EpiTrimulProj {
+  static constexpr bool kHasCol = true;
   bf16 *left, *right;   // [I][M]
   bf16 *psave, *gsave;  // [2I][M] pre-activations
   bf16* gout;           // [M][C]
   const float *bp, *bg, *bgl, *mask;
   long M;
   int I, C;
-  template <int TN>
-  __device__ __forceinline__ void apply(int, int m, int n, const float (&v)[TN]) const {
-    static_assert(TN == 4, "wave tile must span 64 columns");
-    const int two_i4 = 4 * I;
-    if (n < two_i4) {
-      const float mk = mask[m];
-      const int base = n - (n % 16);  // lane column is base + fr
-      const int fr = n % 16;
+  __device__ __forceinline__ bool col_mode(int n0) const { return n0 < 4 * I; }
+  __device__ __forceinline__ void col(int, int m, int n, const float (&v)[8], const float* tp,
+                                      int ldt) const {
+    if ((n & 31) >= 16) return;  // gate column: done by its projection column
+    const int ch = (n >> 5) * 16 + (n & 15);
+    const float bpv = bp[ch], bgv = bg[ch];
+    float mk[8];
+    ld_f8(mask + m, mk);
+    float pv[8], gv[8], av[8];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int cb = (base + 32 * j) / 32;
-        const int ch = cb * 16 + fr;
-        const float p = v[2 * j] + bp[ch];
-        const float g = v[2 * j + 1] + bg[ch];
-        psave[(long)ch * M + m] = (bf16)p;
-        gsave[(long)ch * M + m] = (bf16)g;
-        const float a = mk * p * sigmoidf_(g);
-        if (ch < I) left[(long)ch * M + m] = (bf16)a;
-        else right[(long)(ch - I) * M + m] = (bf16)a;
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int c = n + 16 * j - two_i4;
-        if (c >= C) continue;
-        gout[(long)m * C + c] = (bf16)sigmoidf_(v[j] + bgl[c]);
-      }
+    for (int e = 0; e < 8; ++e) {
+      pv[e] = v[e] + bpv;
+      gv[e] = tp[e * ldt + 16] + bgv;
+      av[e] = mk[e] * pv[e] * sigmoidf_(gv[e]);
     }
+    st_b8f(psave + (long)ch * M + m, pv);
+    st_b8f(gsave + (long)ch * M + m, gv);
+    if (ch < I) st_b8f(left + (long)ch * M + m, av);
+    else st_b8f(right + (long)(ch - I) * M + m, av);
+  }
+  __device__ __forceinline__ void row(int, int m, int n, const float (&v)[8]) const {
+    const int c = n - 4 * I;
+    if (c < 0 || c >= C) return;
+    float bb[8], x[8];
+    ld_f8(bgl + c, bb);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = sigmoidf_(v[e] + bb[e]);
+    st_b8f(gout + (long)m * C + c, x);
   }
 };
 
 // o = acc + bo (kept, bf16); out[m] = in[m] + tbl[(m%nt)*C+c] * o * g_out
-struct EpiTrimulOut {
+struct EpiTrimulOut : EpiRows {
   const float* in;
   float* out;
   const float* bo;
@@ -72,20 +79,29 @@ struct EpiTrimulOut {
   bf16* osave;
   const float* tbl;
   int nt, C;
-  template <int TN>
-  __device__ __forceinline__ void apply(int, int m, int n, const float (&v)[TN]) const {
-    const float* t = tbl ? tbl + (long)(m % nt) * C : nullptr;
+  EpiTrimulOut(const float* i, float* o, const float* b, const bf16* g, bf16* os, const float* t,
+               int n, int c)
+      : in(i), out(o), bo(b), gout(g), osave(os), tbl(t), nt(n), C(c) {}
+  __device__ __forceinline__ void row(int, int m, int n, const float (&v)[8]) const {
+    const long o = (long)m * C + n;
+    float bb[8], ov[8], gv[8], r[8];
+    ld_f8(bo + n, bb);
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int c = n + 16 * j;
-      if (c >= C) continue;
-      const long o = (long)m * C + c;
-      const float ov = v[j] + bo[c];
-      osave[o] = (bf16)ov;
-      float x = ov * (float)gout[o];
-      if (t) x *= t[c];
-      out[o] = in[o] + x;
+    for (int e = 0; e < 8; ++e) ov[e] = v[e] + bb[e];
+    st_b8f(osave + o, ov);
+    ld_b8f(gout + o, gv);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) gv[e] *= ov[e];
+    if (tbl) {
+      float tt[8];
+      ld_f8(tbl + (long)(m % nt) * C + n, tt);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) gv[e] *= tt[e];
     }
+    ld_f8(in + o, r);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] += gv[e];
+    st_f8(out + o, r);
   }
 };
 
@@ -127,10 +143,10 @@ __global__ void trimul_out_bwd_kernel(const float* __restrict__ dout, const floa
 }
 
 // From channel-major dleft/dright and the kept pre-activations, write the
-// row-major [M][4I] gradient of the projection GEMM's output columns:
+// row-major [M][4I+C] gradient of the projection GEMM's output columns:
 //   dproj = da * mask * s,  dgate = da * mask * p * s(1-s),  s = sigmoid(gate)
-// A block handles 32 rows: reads are coalesced along m, the transposed
-// writes go through LDS.
+// A block handles 32 rows: each thread reads 8 consecutive rows of one channel
+// (16-byte loads), the transposed writes go through LDS.  Requires M % 8 == 0.
 __global__ __launch_bounds__(256) void trimul_proj_bwd_kernel(
     const bf16* __restrict__ dl, const bf16* __restrict__ dr, const bf16* __restrict__ psave,
     const bf16* __restrict__ gsave, const float* __restrict__ mask, bf16* __restrict__ dcat,
@@ -142,20 +158,30 @@ __global__ __launch_bounds__(256) void trimul_proj_bwd_kernel(
   bf16* tile = reinterpret_cast<bf16*>(smem_raw);  // [R][LD]
   const long m0 = (long)blockIdx.x * R;
   const int t = threadIdx.x;
-  for (int idx = t; idx < 2 * I * R; idx += 256) {
-    const int ch = idx / R, r = idx % R;
-    const long m = m0 + r;
-    float dp = 0.f, dg = 0.f;
+  for (int idx = t; idx < 2 * I * (R / 8); idx += 256) {
+    const int ch = idx / (R / 8), r0 = (idx % (R / 8)) * 8;
+    const long m = m0 + r0;
+    bf16x8 dp8 = {}, dg8 = {};
     if (m < M) {
-      const float da = (float)(ch < I ? dl[(long)ch * M + m] : dr[(long)(ch - I) * M + m]);
-      const float mk = mask[m];
-      const float s = sigmoidf_((float)gsave[(long)ch * M + m]);
-      const float p = (float)psave[(long)ch * M + m];
-      dp = da * mk * s;
-      dg = da * mk * p * s * (1.f - s);
+      const bf16x8 da = ld8((ch < I ? dl + (long)ch * M : dr + (long)(ch - I) * M) + m);
+      const bf16x8 gv = ld8(gsave + (long)ch * M + m);
+      const bf16x8 pv = ld8(psave + (long)ch * M + m);
+      const float4 mk0 = *reinterpret_cast<const float4*>(mask + m);
+      const float4 mk1 = *reinterpret_cast<const float4*>(mask + m + 4);
+      const float mk[8] = {mk0.x, mk0.y, mk0.z, mk0.w, mk1.x, mk1.y, mk1.z, mk1.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float s = sigmoidf_((float)gv[e]);
+        const float a = (float)da[e] * mk[e];
+        dp8[e] = (bf16)(a * s);
+        dg8[e] = (bf16)(a * (float)pv[e] * s * (1.f - s));
+      }
     }
-    tile[r * LD + col_proj(ch)] = (bf16)dp;
-    tile[r * LD + col_gate(ch)] = (bf16)dg;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      tile[(r0 + e) * LD + col_proj(ch)] = dp8[e];
+      tile[(r0 + e) * LD + col_gate(ch)] = dg8[e];
+    }
   }
   __syncthreads();
   const int chunks = W / 8;
@@ -272,7 +298,7 @@ void trimul_fwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
   g2.M = (int)M; g2.N = C; g2.K = I;
   g2.A = tn; g2.a_sm = I; g2.a_sk = 1;
   g2.B = w.wo_t; g2.b_sn = I; g2.b_sk = 1;
-  gemm<128, 128>(st, g2, EpiTrimulOut{pair_in, pair_out, w.bo, sv.gout, sv.osave, tbl, N, C},
+  gemm<128, 128>(st, g2, EpiTrimulOut(pair_in, pair_out, w.bo, sv.gout, sv.osave, tbl, N, C),
                  "trimul.gemm_out");
 }
 
