@@ -208,7 +208,7 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--n", type=int, default=224)
-    ap.add_argument("--workload", choices=["trunk", "triattn"], default="trunk")
+    ap.add_argument("--workload", choices=["trunk", "triattn", "copy"], default="trunk")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -229,6 +229,20 @@ def main():
     pmask = torch.as_tensor(np.outer(m1, m1), device=dev)
     mmask = torch.as_tensor(m1[None], device=dev)
 
+    if args.workload == "copy":
+        # calibration for the HBM byte counters: one device-to-device copy of
+        # a known size per step (FETCH_SIZE / WRITE_SIZE of this kernel,
+        # divided by 256 MiB, is the counters' scale factor)
+        nbytes = 256 << 20
+        src = torch.randn(nbytes // 4, device=dev)
+        dst = torch.empty_like(src)
+        ms = timed(lambda: dst.copy_(src), args.steps, args.warmup)
+        out = {"metric": "device copy bandwidth (read+write)", "value":
+               round(2 * nbytes / (ms * 1e-3) / 1e9, 1), "unit": "GB/s", "n_gpus": 1,
+               "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+               "higher_is_better": True, "config": {"workload": "copy", "bytes": nbytes}}
+        print(json.dumps(out))
+        return
     if args.workload == "triattn":
         mods = ["triangle_attention_starting_node", "triangle_attention_ending_node"]
         prm = bparams.init_block_params(0, rng, modules=mods, gates="zero")

@@ -26,8 +26,25 @@ constexpr float MASK_BIAS = 1e9f;
 __device__ __forceinline__ float bf2f(bf16 v) { return (float)v; }
 __device__ __forceinline__ bf16 f2bf(float v) { return (bf16)v; }
 
+// 1/(1+e^-x) with the hardware reciprocal (v_rcp_f32, 1 ulp) instead of an
+// IEEE division: the results feed bf16 operands or f32 sums far coarser than
+// that.  exp(-x) = 2^(-x log2 e).
 __device__ __forceinline__ float sigmoidf_(float x) {
-  return 1.f / (1.f + __expf(-x));
+  return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
+}
+
+// Workgroups are handed to the 8 XCDs round-robin (workgroup b runs on XCD
+// b % 8) and every XCD has its own L2.  A kernel launched on xcd_grid(G)
+// workgroups that takes its logical index from xcd_block(G) gives each XCD
+// one contiguous range of the logical order, so workgroups that share
+// operands (neighbours in that order) share an L2.  Indices >= G are padding
+// and must exit before any barrier.
+constexpr int NUM_XCD = 8;
+__host__ __device__ inline long xcd_per(long G) { return (G + NUM_XCD - 1) / NUM_XCD; }
+inline unsigned xcd_grid(long G) { return (unsigned)(xcd_per(G) * NUM_XCD); }
+__device__ __forceinline__ long xcd_block(long G) {
+  const long b = blockIdx.x;
+  return (b % NUM_XCD) * xcd_per(G) + b / NUM_XCD;
 }
 
 // D += A(16x32) * B(32x16), bf16 operands, f32 accumulation.

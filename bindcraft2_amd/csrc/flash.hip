@@ -1,6 +1,6 @@
 // Flash attention forward/backward for AF2's gated attention with pair bias,
 // written for wave64 and gfx950 MFMA, head width D = 32 (Evoformer) or 16
-// (template stack).
+// (template stack), N <= 256 keys per row.
 //
 // Every product is arranged so that the lane -> query (or lane -> key)
 // assignment of the MFMA result is the one the next MFMA needs as its B
@@ -17,7 +17,10 @@
 // queries) always uses the x32 form.  For that second product the 8 K-slots
 // of lane group g=l/16 are mapped to positions {4g..4g+3, 16+4g..16+4g+3}
 // of the 32-block, for both operands; the first product's result already
-// sits in exactly that order.
+// sits in exactly that order.  All operands live in LDS row-major (token x
+// head width); the second product's transposed operand (V^T, K^T, Q^T, dO^T)
+// is read with ds_read_b64_tr_b16, which hands each lane a column of a 4 x 16
+// block, so nothing is ever staged transposed.
 //
 // Scores are kept in the log2 domain: q is pre-scaled by D^-1/2 * log2(e)
 // and the pair bias by log2(e) upstream, so a score is one MFMA plus one add.
@@ -43,14 +46,42 @@ constexpr float NEG_LOGIT = -8192.0f;
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// 8 bf16 from two runs of 4 contiguous elements (positions p and p+16).
-__device__ __forceinline__ bf16x8 ld_slots(const bf16* p) {
-  const bf16x4 a = *reinterpret_cast<const bf16x4*>(p);
-  const bf16x4 b = *reinterpret_cast<const bf16x4*>(p + 16);
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// Column read of a row-major bf16 LDS tile T[row][ld] (ld % 4 == 0):
+// returns, for lane l (column c = l%16, group g = l/16), the four values
+// T[r0 + 4g + j][c0 + c], j = 0..3.  One ds_read_b64_tr_b16: within each
+// 16-lane group, lane m addresses the 8-byte chunk T[r0 + 4g + m/4][c0 + 4(m%4)
+// .. +3] and the instruction returns to lane 4a + c element c of the chunks
+// of lanes a, a+4, a+8, a+12.
+__device__ __forceinline__ bf16x4 ld_tr4(const bf16* T, int ld, int r0, int c0, int lane) {
+  const int g = lane >> 4, m = lane & 15;
+  const bf16* p = T + (r0 + 4 * g + (m >> 2)) * ld + c0 + 4 * (m & 3);
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p);
+  return __builtin_bit_cast(bf16x4, v);
+}
+
+// x32 operand over a 32-block at row r0 (slots {4g..4g+3, 16+4g..16+4g+3}),
+// column c0 + l%16 of a row-major LDS tile.
+__device__ __forceinline__ bf16x8 ld_tr8(const bf16* T, int ld, int r0, int c0, int lane) {
+  const bf16x4 a = ld_tr4(T, ld, r0, c0, lane);
+  const bf16x4 b = ld_tr4(T, ld, r0 + 16, c0, lane);
   bf16x8 r;
   r[0] = a[0]; r[1] = a[1]; r[2] = a[2]; r[3] = a[3];
   r[4] = b[0]; r[5] = b[1]; r[6] = b[2]; r[7] = b[3];
   return r;
+}
+
+// Row-major copy of the n x D head slice at src (row stride ld) into
+// dst[n][D + 8]: 16-byte loads and stores.
+template <int D>
+__device__ __forceinline__ void stage_rows(bf16* dst, const bf16* src, long ld, int n, int tid,
+                                           int nthr) {
+  for (int c = tid; c < n * (D / 8); c += nthr) {
+    const int t = c / (D / 8), dc = (c % (D / 8)) * 8;
+    st8(&dst[t * (D + 8) + dc], ld8(src + (long)t * ld + dc));
+  }
 }
 
 // Operand fragment of the head-width contraction for lane group g.
@@ -77,91 +108,115 @@ struct HFrag<16> {
 
 // ------------------------------------------------------------------ forward
 // Workgroup = (row r, head h, 64 queries); 4 waves x 16 queries.  The row's
-// K (row-major) and V (transposed) for head h are staged once in LDS.
-template <int D>
+// K and V for head h are staged once in LDS.  N is at most 32*NKB, so a lane
+// keeps its query's whole score row (8 keys of every 32-key block) in
+// registers: the pair-bias row is fetched with all loads in flight at once,
+// the row maximum is taken once and every score costs one exponent -- no
+// running rescale of the output accumulator.
+template <int D, int NKB>
 __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   constexpr int DT = D / 16;
+  constexpr int LD = D + 8;
   const int N = a.N, H = a.H;
-  const int KLD = D + 8, VLD = N + 8;
-  bf16* Ks = reinterpret_cast<bf16*>(smem_raw);          // [N][KLD]
-  bf16* Vt = Ks + N * KLD;                               // [D][VLD]
-  float* Ms = reinterpret_cast<float*>(Vt + D * VLD);    // [N]
+  bf16* Ks = reinterpret_cast<bf16*>(smem_raw);          // [N][LD]
+  bf16* Vs = Ks + N * LD;                                // [N][LD]
+  float* Mm = reinterpret_cast<float*>(Vs + N * LD);     // [N] 1 / 0 per key
+  float* Ma = Mm + N;                                    // [N] 0 / NEG_LOGIT
 
   const int nqb = (N + 63) / 64;
-  const int qb = blockIdx.x % nqb;
-  const int h = (blockIdx.x / nqb) % H;
-  const int r = blockIdx.x / (nqb * H);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const long G = (long)a.R * H * nqb;
+  const int bid = (int)xcd_block(G);  // (r, h, qb): the qb blocks of (r, h) share K, V
+  if (bid >= G) return;
+  const int qb = bid % nqb;
+  const int h = (bid / nqb) % H;
+  const int r = bid / (nqb * H);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const long tok0 = (long)r * N;
-  const bf16* Kg = a.qkvg + tok0 * a.ld + H * D + h * D;
-  const bf16* Vg = a.qkvg + tok0 * a.ld + 2 * H * D + h * D;
-  for (int c = tid; c < N * (D / 8); c += 256) {
-    const int k = c / (D / 8), dc = (c % (D / 8)) * 8;
-    st8(&Ks[k * KLD + dc], ld8(Kg + (long)k * a.ld + dc));
-    const bf16x8 v = ld8(Vg + (long)k * a.ld + dc);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) Vt[(dc + e) * VLD + k] = v[e];
+  stage_rows<D>(Ks, a.qkvg + tok0 * a.ld + H * D + h * D, a.ld, N, tid, 256);
+  stage_rows<D>(Vs, a.qkvg + tok0 * a.ld + 2 * H * D + h * D, a.ld, N, tid, 256);
+  for (int k = tid; k < N; k += 256) {
+    const bool on = a.mask[r * a.mask_sr + k * a.mask_sk] != 0.f;
+    Mm[k] = on ? 1.f : 0.f;
+    Ma[k] = on ? 0.f : NEG_LOGIT;
   }
-  for (int k = tid; k < N; k += 256) Ms[k] = a.mask[r * a.mask_sr + k * a.mask_sk];
-  __syncthreads();
 
   const int q0 = qb * 64 + wave * 16;
-  if (q0 >= N) return;  // no barrier follows
   const int lq = lane & 15, g = lane >> 4;
-  const int q = q0 + lq;
+  const int q = min(q0, N - 16) + lq;  // idle waves read in bounds, store nothing
+  const int nkb = N / 32;
   HFrag<D> qf;
   qf.load(a.qkvg + (tok0 + q) * a.ld + h * D, g);
+  float sv[NKB][8];
   const float* brow = a.bias ? a.bias + ((long)h * N + q) * N : nullptr;
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) {
+    if (kb < nkb) {
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh) {
+        const float4 bb = brow ? *reinterpret_cast<const float4*>(brow + kb * 32 + kh * 16 + 4 * g)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+        sv[kb][kh * 4 + 0] = bb.x;
+        sv[kb][kh * 4 + 1] = bb.y;
+        sv[kb][kh * 4 + 2] = bb.z;
+        sv[kb][kh * 4 + 3] = bb.w;
+      }
+    }
+  }
+  __syncthreads();
+  if (q0 >= N) return;  // no barrier follows
 
-  float mrun = -INFINITY, lrun = 0.f;
   const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+  float mx = -INFINITY;
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) {
+    if (kb < nkb) {
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh) {
+        HFrag<D> kf;
+        kf.load(&Ks[(kb * 32 + kh * 16 + lq) * LD], g);
+        const f32x4 s = HFrag<D>::mma(kf, qf, z4);
+        const int k0 = kb * 32 + kh * 16 + 4 * g;
+        const float4 mm = *reinterpret_cast<const float4*>(Mm + k0);
+        const float4 ma = *reinterpret_cast<const float4*>(Ma + k0);
+        const float mv[4] = {mm.x, mm.y, mm.z, mm.w};
+        const float av[4] = {ma.x, ma.y, ma.z, ma.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          // unmasked: s + bias; masked: exactly NEG_LOGIT
+          float& x = sv[kb][kh * 4 + i];
+          x = __builtin_fmaf(s[i] + x, mv[i], av[i]);
+          mx = fmaxf(mx, x);
+        }
+      }
+    }
+  }
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+
+  float lsum = 0.f;
   f32x4 acc[DT];
 #pragma unroll
   for (int i = 0; i < DT; ++i) acc[i] = z4;
-  for (int kb = 0; kb < N; kb += 32) {
-    float sv[8];
 #pragma unroll
-    for (int kh = 0; kh < 2; ++kh) {
-      HFrag<D> kf;
-      kf.load(&Ks[(kb + kh * 16 + lq) * KLD], g);
-      const f32x4 s = HFrag<D>::mma(kf, qf, z4);
-      const int key0 = kb + kh * 16 + 4 * g;
-      float4 bb = brow ? *reinterpret_cast<const float4*>(brow + key0)
-                       : make_float4(0.f, 0.f, 0.f, 0.f);
-      const float4 mm = *reinterpret_cast<const float4*>(Ms + key0);
-      sv[kh * 4 + 0] = mm.x != 0.f ? s[0] + bb.x : NEG_LOGIT;
-      sv[kh * 4 + 1] = mm.y != 0.f ? s[1] + bb.y : NEG_LOGIT;
-      sv[kh * 4 + 2] = mm.z != 0.f ? s[2] + bb.z : NEG_LOGIT;
-      sv[kh * 4 + 3] = mm.w != 0.f ? s[3] + bb.w : NEG_LOGIT;
-    }
-    float bm = sv[0];
+  for (int kb = 0; kb < NKB; ++kb) {
+    if (kb < nkb) {
+      bf16x8 pf;
 #pragma unroll
-    for (int e = 1; e < 8; ++e) bm = fmaxf(bm, sv[e]);
-    bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
-    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-    const float mnew = fmaxf(mrun, bm);
-    const float alpha = fast_exp2(mrun - mnew);
-    bf16x8 pf;
-    float ps = 0.f;
+      for (int e = 0; e < 8; ++e) {
+        const float p = fast_exp2(sv[kb][e] - mx);
+        lsum += p;
+        pf[e] = (bf16)p;
+      }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float p = fast_exp2(sv[e] - mnew);
-      ps += p;
-      pf[e] = (bf16)p;
-    }
-    lrun = lrun * alpha + ps;
-    mrun = mnew;
-#pragma unroll
-    for (int dh = 0; dh < DT; ++dh) {
-      acc[dh] *= alpha;
-      const bf16x8 vf = ld_slots(&Vt[(dh * 16 + lq) * VLD + kb + 4 * g]);
-      acc[dh] = mfma16x16x32(vf, pf, acc[dh]);
+      for (int dh = 0; dh < DT; ++dh)
+        acc[dh] = mfma16x16x32(ld_tr8(Vs, LD, kb * 32, dh * 16, lane), pf, acc[dh]);
     }
   }
-  lrun += __shfl_xor(lrun, 16, 64);
-  lrun += __shfl_xor(lrun, 32, 64);
-  const float inv = 1.f / lrun;
+  lsum += __shfl_xor(lsum, 16, 64);
+  lsum += __shfl_xor(lsum, 32, 64);
+  const float inv = __builtin_amdgcn_rcpf(lsum);
   const long orow = (tok0 + q) * a.ldo + h * D;
   const bf16* grow = a.qkvg + (tok0 + q) * a.ld + 3 * H * D + h * D;
 #pragma unroll
@@ -178,7 +233,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
     *reinterpret_cast<bf16x4*>(a.o + orow + d0) = ov;
     *reinterpret_cast<bf16x4*>(a.og + orow + d0) = gov;
   }
-  if (g == 0) a.lse[((long)r * H + h) * N + q] = mrun + __log2f(lrun);
+  if (g == 0) a.lse[((long)r * H + h) * N + q] = mx + __log2f(lsum);
 }
 
 // ------------------------------------------------------- backward: gate + D
@@ -220,78 +275,103 @@ __global__ __launch_bounds__(256) void attn_gate_bwd_kernel(AttnBwdArgs b) {
 }
 
 // ----------------------------------------------------------- backward: dQ
-// Same decomposition as the forward: (row, head, 64 queries), 4 waves.
-template <int D>
+// Same decomposition as the forward: (row, head, 64 queries), 4 waves; the
+// lane's pair-bias row (minus lse, with -inf at masked keys so p = dS = 0
+// there) is fetched up front, all loads in flight at once.
+template <int D, int NKB>
 __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs b) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   constexpr int DT = D / 16;
+  constexpr int LD = D + 8;
   const AttnArgs& a = b.f;
   const int N = a.N, H = a.H;
-  const int KLD = D + 8, TLD = N + 8;
-  bf16* Ks = reinterpret_cast<bf16*>(smem_raw);   // [N][KLD]
-  bf16* Vs = Ks + N * KLD;                        // [N][KLD]
-  bf16* Kt = Vs + N * KLD;                        // [D][TLD]
-  float* Ms = reinterpret_cast<float*>(Kt + D * TLD);
+  bf16* Ks = reinterpret_cast<bf16*>(smem_raw);   // [N][LD]
+  bf16* Vs = Ks + N * LD;                         // [N][LD]
+  float* Ms = reinterpret_cast<float*>(Vs + N * LD);
 
   const int nqb = (N + 63) / 64;
-  const int qb = blockIdx.x % nqb;
-  const int h = (blockIdx.x / nqb) % H;
-  const int r = blockIdx.x / (nqb * H);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const long G = (long)a.R * H * nqb;
+  const int bid = (int)xcd_block(G);  // (r, h, qb): the qb blocks of (r, h) share K, V
+  if (bid >= G) return;
+  const int qb = bid % nqb;
+  const int h = (bid / nqb) % H;
+  const int r = bid / (nqb * H);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const long tok0 = (long)r * N;
-  const bf16* Kg = a.qkvg + tok0 * a.ld + H * D + h * D;
-  const bf16* Vg = a.qkvg + tok0 * a.ld + 2 * H * D + h * D;
-  for (int c = tid; c < N * (D / 8); c += 256) {
-    const int k = c / (D / 8), dc = (c % (D / 8)) * 8;
-    const bf16x8 kv = ld8(Kg + (long)k * a.ld + dc);
-    st8(&Ks[k * KLD + dc], kv);
-    st8(&Vs[k * KLD + dc], ld8(Vg + (long)k * a.ld + dc));
-#pragma unroll
-    for (int e = 0; e < 8; ++e) Kt[(dc + e) * TLD + k] = kv[e];
-  }
-  for (int k = tid; k < N; k += 256) Ms[k] = a.mask[r * a.mask_sr + k * a.mask_sk];
-  __syncthreads();
+  stage_rows<D>(Ks, a.qkvg + tok0 * a.ld + H * D + h * D, a.ld, N, tid, 256);
+  stage_rows<D>(Vs, a.qkvg + tok0 * a.ld + 2 * H * D + h * D, a.ld, N, tid, 256);
+  // additive key mask: a masked key's exponent becomes -inf, so p = dS = 0
+  for (int k = tid; k < N; k += 256)
+    Ms[k] = a.mask[r * a.mask_sr + k * a.mask_sk] != 0.f ? 0.f : -INFINITY;
 
   const int q0 = qb * 64 + wave * 16;
-  if (q0 >= N) return;
   const int lq = lane & 15, g = lane >> 4;
-  const int q = q0 + lq;
+  const int q = min(q0, N - 16) + lq;  // idle waves read in bounds, store nothing
+  const int nkb = N / 32;
   HFrag<D> qf, dof;
   qf.load(a.qkvg + (tok0 + q) * a.ld + h * D, g);
   dof.load(b.dO + (tok0 + q) * a.ldo + h * D, g);
   const float lse = a.lse[((long)r * H + h) * N + q];
   const float Dq = b.Dsum[((long)r * H + h) * N + q];
+  float bsv[NKB][8];
   const float* brow = a.bias ? a.bias + ((long)h * N + q) * N : nullptr;
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) {
+    if (kb < nkb) {
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh) {
+        const float4 bb = brow ? *reinterpret_cast<const float4*>(brow + kb * 32 + kh * 16 + 4 * g)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+        bsv[kb][kh * 4 + 0] = bb.x - lse;
+        bsv[kb][kh * 4 + 1] = bb.y - lse;
+        bsv[kb][kh * 4 + 2] = bb.z - lse;
+        bsv[kb][kh * 4 + 3] = bb.w - lse;
+      }
+    }
+  }
+  __syncthreads();
+  if (q0 >= N) return;  // no barrier follows
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) {
+    if (kb < nkb) {
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh) {
+        const float4 mm = *reinterpret_cast<const float4*>(Ms + kb * 32 + kh * 16 + 4 * g);
+        bsv[kb][kh * 4 + 0] += mm.x;
+        bsv[kb][kh * 4 + 1] += mm.y;
+        bsv[kb][kh * 4 + 2] += mm.z;
+        bsv[kb][kh * 4 + 3] += mm.w;
+      }
+    }
+  }
+
   const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+  const f32x4 nD = {-Dq, -Dq, -Dq, -Dq};
   f32x4 acc[DT];
 #pragma unroll
   for (int i = 0; i < DT; ++i) acc[i] = z4;
-  for (int kb = 0; kb < N; kb += 32) {
-    bf16x8 dsf;
 #pragma unroll
-    for (int kh = 0; kh < 2; ++kh) {
-      const int krow = (kb + kh * 16 + lq) * KLD;
-      HFrag<D> kf, vf;
-      kf.load(&Ks[krow], g);
-      vf.load(&Vs[krow], g);
-      const f32x4 s = HFrag<D>::mma(kf, qf, z4);
-      const f32x4 dp = HFrag<D>::mma(vf, dof, z4);
-      const int key0 = kb + kh * 16 + 4 * g;
-      float4 bb = brow ? *reinterpret_cast<const float4*>(brow + key0)
-                       : make_float4(0.f, 0.f, 0.f, 0.f);
-      const float4 mm = *reinterpret_cast<const float4*>(Ms + key0);
-      const float bv[4] = {bb.x, bb.y, bb.z, bb.w};
-      const float mv[4] = {mm.x, mm.y, mm.z, mm.w};
+  for (int kb = 0; kb < NKB; ++kb) {
+    if (kb < nkb) {
+      bf16x8 dsf;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float p = fast_exp2(s[i] + bv[i] - lse);
-        dsf[kh * 4 + i] = (bf16)(mv[i] != 0.f ? p * (dp[i] - Dq) : 0.f);
+      for (int kh = 0; kh < 2; ++kh) {
+        const int krow = (kb * 32 + kh * 16 + lq) * LD;
+        HFrag<D> kf, vf;
+        kf.load(&Ks[krow], g);
+        vf.load(&Vs[krow], g);
+        f32x4 cs;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) cs[i] = bsv[kb][kh * 4 + i];
+        const f32x4 s = HFrag<D>::mma(kf, qf, cs);    // S + bias - lse
+        const f32x4 dp = HFrag<D>::mma(vf, dof, nD);  // dP - Dsum
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dsf[kh * 4 + i] = (bf16)(fast_exp2(s[i]) * dp[i]);
       }
-    }
 #pragma unroll
-    for (int dh = 0; dh < DT; ++dh) {
-      const bf16x8 kt = ld_slots(&Kt[(dh * 16 + lq) * TLD + kb + 4 * g]);
-      acc[dh] = mfma16x16x32(kt, dsf, acc[dh]);
+      for (int dh = 0; dh < DT; ++dh)
+        acc[dh] = mfma16x16x32(ld_tr8(Ks, LD, kb * 32, dh * 16, lane), dsf, acc[dh]);
     }
   }
   bf16* out = b.dqkvg + (tok0 + q) * a.ld + h * D;
@@ -305,107 +385,130 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs b) {
 }
 
 // ------------------------------------------------------ backward: dK, dV, dB
-// Workgroup = (head h, 32 keys, chunk of rows), 4 waves: wave w owns key
+// Workgroup = (chunk of rows, head h, 32 keys), 4 waves: wave w owns key
 // tile w&1 (16 keys) and the 32-query blocks ib with ib%2 == w>>1, so the
-// bias-gradient tile it keeps in registers is ceil(N/64) x 8 floats per lane.
-// Per row, Q^T and dO^T (head h) are staged in LDS; the two query halves'
-// dK/dV partials are combined through LDS before the write.  NQ_MAX bounds N.
+// bias-gradient tile it keeps in registers is ceil(N/64) x 8 floats per lane;
+// the pair bias is row-independent and is read once per workgroup into a
+// register tile of the same shape.  Per row, Q and dO (head h) are staged in
+// LDS; the two query halves' dK/dV partials are combined through LDS before
+// the write.  NQ_MAX bounds N.
+//
+// Per score the MFMA accumulators start at (bias - lse) and -Dsum, so
+// p = exp2(S) and dS = p * dP' need no further adds.  A masked key gets
+// exponent -inf (p = dS = 0) -- exact for a row with any unmasked key, where
+// AF2's masked weight exp(-1e8 - lse) underflows to 0.  A fully masked row is
+// the uniform distribution (p = 1/N, dS = 0), handled as its own case.
 template <int D, int NQ_MAX>
 __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   constexpr int DT = D / 16;
+  constexpr int LD = D + 8;
   constexpr int NB = (NQ_MAX / 32 + 1) / 2;  // query blocks per wave
   const AttnArgs& a = b.f;
   const int N = a.N, H = a.H;
-  const int TLD = N + 8;
-  bf16* Qt = reinterpret_cast<bf16*>(smem_raw);         // [D][TLD]
-  bf16* Dt = Qt + D * TLD;                              // [D][TLD]
-  float* Ls = reinterpret_cast<float*>(Dt + D * TLD);   // [N] lse
-  float* Ds = Ls + N;                                   // [N] Dsum
+  bf16* Qs = reinterpret_cast<bf16*>(smem_raw);         // [N][LD]
+  bf16* Os = Qs + N * LD;                               // [N][LD] dO
+  float* Ls = reinterpret_cast<float*>(Os + N * LD);    // [N] -lse
+  float* Ds = Ls + N;                                   // [N] -Dsum
   float* Xs = Ds + N;                                   // [2 tiles][K,V][DT*4][64]
 
   const int nkb = (N + 31) / 32;
-  const int kb32 = blockIdx.x % nkb;
-  const int h = (blockIdx.x / nkb) % H;
-  const int ch = blockIdx.x / (nkb * H);
+  const long G = (long)((a.R + b.rows_per_chunk - 1) / b.rows_per_chunk) * H * nkb;
+  const int bid = (int)xcd_block(G);  // (chunk, h, kb): the kb blocks share Q, dO
+  if (bid >= G) return;
+  const int kb32 = bid % nkb;
+  const int h = (bid / nkb) % H;
+  const int ch = bid / (nkb * H);
   const int r0 = ch * b.rows_per_chunk;
   const int r1 = min(a.R, r0 + b.rows_per_chunk);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int kt_ = wave & 1, half = wave >> 1;
   const int lk = lane & 15, g = lane >> 4;
   const int k = kb32 * 32 + kt_ * 16 + lk;
   const int nqblk = N / 32;
-  float dbias[NB][8];
-#pragma unroll
-  for (int i = 0; i < NB; ++i)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) dbias[i][e] = 0.f;
-  const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
   const long HD = (long)H * D;
   float* xk = Xs + (kt_ * 2 + 0) * DT * 4 * 64;
   float* xv = Xs + (kt_ * 2 + 1) * DT * 4 * 64;
 
+  // bias column k at this wave's queries; bias-gradient accumulators
+  float bsl[NB][8], dbias[NB][8];
+  const float* bcol = a.bias ? a.bias + (long)h * N * N + k : nullptr;
+#pragma unroll
+  for (int ib = 0; ib < NB; ++ib) {
+    const int qb = (ib * 2 + half) * 32;
+    const bool have = bcol && qb < N;  // wave-uniform
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      bsl[ib][e] = 0.f;
+      dbias[ib][e] = 0.f;
+    }
+    if (have) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        bsl[ib][e] = bcol[(long)(qb + (e / 4) * 16 + 4 * g + (e % 4)) * N];
+    }
+  }
+  const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+
   for (int r = r0; r < r1; ++r) {
     const long tok0 = (long)r * N;
     __syncthreads();  // previous row's LDS readers are done
-    for (int c = tid; c < N * (D / 8); c += 256) {
-      const int qq = c / (D / 8), dc = (c % (D / 8)) * 8;
-      const bf16x8 qv = ld8(a.qkvg + (tok0 + qq) * a.ld + h * D + dc);
-      const bf16x8 dv = ld8(b.dO + (tok0 + qq) * a.ldo + h * D + dc);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        Qt[(dc + e) * TLD + qq] = qv[e];
-        Dt[(dc + e) * TLD + qq] = dv[e];
-      }
-    }
+    stage_rows<D>(Qs, a.qkvg + tok0 * a.ld + h * D, a.ld, N, tid, 256);
+    stage_rows<D>(Os, b.dO + tok0 * a.ldo + h * D, a.ldo, N, tid, 256);
+    int on = 0;
     for (int qq = tid; qq < N; qq += 256) {
-      Ls[qq] = a.lse[((long)r * H + h) * N + qq];
-      Ds[qq] = b.Dsum[((long)r * H + h) * N + qq];
+      Ls[qq] = -a.lse[((long)r * H + h) * N + qq];
+      Ds[qq] = -b.Dsum[((long)r * H + h) * N + qq];
+      on |= a.mask[r * a.mask_sr + qq * a.mask_sk] != 0.f;
     }
-    __syncthreads();
     HFrag<D> kf, vf;
     kf.load(a.qkvg + (tok0 + k) * a.ld + HD + h * D, g);
     vf.load(a.qkvg + (tok0 + k) * a.ld + 2 * HD + h * D, g);
     const bool mk = a.mask[r * a.mask_sr + k * a.mask_sk] != 0.f;
+    const bool live = __syncthreads_or(on);  // the row has an unmasked key
     f32x4 accK[DT], accV[DT];
 #pragma unroll
     for (int i = 0; i < DT; ++i) { accK[i] = z4; accV[i] = z4; }
+    // exponent of a masked key: -inf (weight 0) in a live row, -log2 N
+    // (weight 1/N) in a fully masked one; either way its dS is 0
+    const float xm = live ? -INFINITY : -__log2f((float)N);
 #pragma unroll
     for (int ib = 0; ib < NB; ++ib) {
       const int blk = ib * 2 + half;
-      if (blk >= nqblk) break;
-      const int qb = blk * 32;
-      bf16x8 pf, dsf;
+      if (blk < nqblk) {
+        const int qb = blk * 32;
+        bf16x8 pf, dsf;
 #pragma unroll
-      for (int qh = 0; qh < 2; ++qh) {
-        const long qrow = tok0 + qb + qh * 16 + lk;
-        HFrag<D> qa, da;
-        qa.load(a.qkvg + qrow * a.ld + h * D, g);
-        da.load(b.dO + qrow * a.ldo + h * D, g);
-        const f32x4 s = HFrag<D>::mma(qa, kf, z4);
-        const f32x4 dp = HFrag<D>::mma(da, vf, z4);
-        const int qi0 = qb + qh * 16 + 4 * g;
-        const float4 lv = *reinterpret_cast<const float4*>(Ls + qi0);
-        const float4 dv = *reinterpret_cast<const float4*>(Ds + qi0);
-        const float lsv[4] = {lv.x, lv.y, lv.z, lv.w};
-        const float dsv[4] = {dv.x, dv.y, dv.z, dv.w};
+        for (int qh = 0; qh < 2; ++qh) {
+          const int qrow = qb + qh * 16;
+          HFrag<D> qa, da;
+          qa.load(&Qs[(qrow + lk) * LD], g);
+          da.load(&Os[(qrow + lk) * LD], g);
+          const float4 lv = *reinterpret_cast<const float4*>(Ls + qrow + 4 * g);
+          const float4 dv = *reinterpret_cast<const float4*>(Ds + qrow + 4 * g);
+          f32x4 cs, cd;
+          cs[0] = bsl[ib][qh * 4 + 0] + lv.x;
+          cs[1] = bsl[ib][qh * 4 + 1] + lv.y;
+          cs[2] = bsl[ib][qh * 4 + 2] + lv.z;
+          cs[3] = bsl[ib][qh * 4 + 3] + lv.w;
+          cd[0] = dv.x; cd[1] = dv.y; cd[2] = dv.z; cd[3] = dv.w;
+          const f32x4 s = HFrag<D>::mma(qa, kf, cs);   // S + bias - lse
+          const f32x4 dp = HFrag<D>::mma(da, vf, cd);  // dP - Dsum
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float bb = a.bias ? a.bias[((long)h * N + qi0 + i) * N + k] : 0.f;
-          const float sc = mk ? s[i] + bb : NEG_LOGIT;
-          const float p = fast_exp2(sc - lsv[i]);
-          const float ds = mk ? p * (dp[i] - dsv[i]) : 0.f;
-          pf[qh * 4 + i] = (bf16)p;
-          dsf[qh * 4 + i] = (bf16)ds;
-          dbias[ib][qh * 4 + i] += ds;
+          for (int i = 0; i < 4; ++i) {
+            const float p = fast_exp2(mk ? s[i] : xm);
+            const float ds = mk ? p * dp[i] : 0.f;
+            pf[qh * 4 + i] = (bf16)p;
+            dsf[qh * 4 + i] = (bf16)ds;
+            dbias[ib][qh * 4 + i] += ds;
+          }
         }
-      }
 #pragma unroll
-      for (int dh = 0; dh < DT; ++dh) {
-        const bf16x8 dot = ld_slots(&Dt[(dh * 16 + lk) * TLD + qb + 4 * g]);
-        accV[dh] = mfma16x16x32(dot, pf, accV[dh]);
-        const bf16x8 qt = ld_slots(&Qt[(dh * 16 + lk) * TLD + qb + 4 * g]);
-        accK[dh] = mfma16x16x32(qt, dsf, accK[dh]);
+        for (int dh = 0; dh < DT; ++dh) {
+          accV[dh] = mfma16x16x32(ld_tr8(Os, LD, qb, dh * 16, lane), pf, accV[dh]);
+          accK[dh] = mfma16x16x32(ld_tr8(Qs, LD, qb, dh * 16, lane), dsf, accK[dh]);
+        }
       }
     }
     // combine the two query halves: half 1 parks its partials in LDS
@@ -477,9 +580,9 @@ static void attn_check(const AttnArgs& a) {
 template <int D>
 static void attn_fwd_t(hipStream_t st, const AttnArgs& a) {
   const int nqb = (a.N + 63) / 64;
-  const size_t lds = (size_t)a.N * (D + 8) * 2 + (size_t)D * (a.N + 8) * 2 + (size_t)a.N * 4;
+  const size_t lds = (size_t)a.N * (D + 8) * 2 * 2 + (size_t)a.N * 8;
   KTimed kt("attn_fwd", st);
-  hipLaunchKernelGGL((attn_fwd_kernel<D>), dim3(a.R * a.H * nqb), dim3(256), lds, st, a);
+  hipLaunchKernelGGL((attn_fwd_kernel<D, 8>), dim3(xcd_grid((long)a.R * a.H * nqb)), dim3(256), lds, st, a);
 }
 
 void attn_fwd(hipStream_t st, const AttnArgs& a) {
@@ -500,18 +603,18 @@ static void attn_bwd_t(hipStream_t st, const AttnBwdArgs& b) {
                        dim3(256), 0, st, b);
   }
   const int nqb = (a.N + 63) / 64;
-  const size_t lds_q = (size_t)a.N * (D + 8) * 2 * 2 + (size_t)D * (a.N + 8) * 2 + (size_t)a.N * 4;
+  const size_t lds_q = (size_t)a.N * (D + 8) * 2 * 2 + (size_t)a.N * 4;
   {
     KTimed kt("attn_bwd_dq", st);
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<D>), dim3(a.R * a.H * nqb), dim3(256), lds_q, st, b);
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<D, 8>), dim3(xcd_grid((long)a.R * a.H * nqb)), dim3(256), lds_q, st, b);
   }
   const int nch = attn_bwd_nchunk(a.R, b.rows_per_chunk);
   const int nkb = (a.N + 31) / 32;
-  const size_t lds_k = (size_t)D * (a.N + 8) * 2 * 2 + (size_t)a.N * 4 * 2 +
+  const size_t lds_k = (size_t)a.N * (D + 8) * 2 * 2 + (size_t)a.N * 4 * 2 +
                        (size_t)2 * 2 * (D / 16) * 4 * 64 * 4;
   {
     KTimed kt("attn_bwd_dkv", st);
-    hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, 256>), dim3(nch * a.H * nkb), dim3(256), lds_k, st,
+    hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, 256>), dim3(xcd_grid((long)nch * a.H * nkb)), dim3(256), lds_k, st,
                        b);
   }
   if (b.dbias && a.bias) {

@@ -98,10 +98,15 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
+  // logical order (batch, m tile, n tile): the n tiles of one m tile, and
+  // the tiles of one batch entry, run on one XCD and share its L2
   const int tiles_n = (g.N + BN - 1) / BN;
-  const int m0 = (blockIdx.x / tiles_n) * BM;
-  const int n0 = (blockIdx.x % tiles_n) * BN;
-  const int b = blockIdx.z;
+  const int tiles = ((g.M + BM - 1) / BM) * tiles_n;
+  const long bid = xcd_block((long)tiles * g.batch);
+  if (bid >= (long)tiles * g.batch) return;
+  const int b = (int)(bid / tiles), t = (int)(bid % tiles);
+  const int m0 = (t / tiles_n) * BM;
+  const int n0 = (t % tiles_n) * BN;
   const bf16* __restrict__ A = g.A + (long)b * g.a_sb;
   const bf16* __restrict__ B = g.B + (long)b * g.b_sb;
   const int M = g.M, N = g.N;
@@ -265,7 +270,7 @@ void gemm(hipStream_t st, const GemmArgs& g, const Epi& epi, const char* name = 
   else gemm_check(g.b_sk % 8 == 0, "B(T) stride must be a multiple of 8");
   gemm_check(g.batch == 1 || (g.a_sb % 8 == 0 && g.b_sb % 8 == 0), "batch strides");
   const int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
-  dim3 grid(tiles, 1, g.batch), block(256);
+  dim3 grid(xcd_grid((long)tiles * g.batch)), block(256);
   const bool k64 = (g.K % 64 == 0);
   KTimed kt(name, st);
 #define BC2N_GEMM_LAUNCH(BKV, AKV, BKCV) \
