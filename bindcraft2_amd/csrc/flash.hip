@@ -37,6 +37,8 @@
 // The bias gradient (a sum over rows) is accumulated in registers over a
 // chunk of rows and written once per chunk; a second pass adds the chunks in
 // a fixed order, so the result is deterministic (no float atomics anywhere).
+#include <type_traits>
+
 #include "kernels.h"
 #include "runtime.h"
 
@@ -108,8 +110,10 @@ struct HFrag<16> {
 
 // ------------------------------------------------------------------ forward
 // Workgroup = (row r, head h, 64 queries); 4 waves x 16 queries.  The row's
-// K and V for head h are staged once in LDS.  N is at most 32*NKB, so a lane
-// keeps its query's whole score row (8 keys of every 32-key block) in
+// K and V for head h are staged once in LDS.  N = 32*NKB exactly (one
+// instantiation per block count, so every loop over key blocks unrolls
+// without guards and the scheduler can overlap one block's MFMAs with the
+// previous block's softmax), and a lane keeps its query's whole score row (8 keys of every 32-key block) in
 // registers: the pair-bias row is fetched with all loads in flight at once,
 // the row maximum is taken once and every score costs one exponent -- no
 // running rescale of the output accumulator.
@@ -145,14 +149,13 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   const int q0 = qb * 64 + wave * 16;
   const int lq = lane & 15, g = lane >> 4;
   const int q = min(q0, N - 16) + lq;  // idle waves read in bounds, store nothing
-  const int nkb = N / 32;
   HFrag<D> qf;
   qf.load(a.qkvg + (tok0 + q) * a.ld + h * D, g);
   float sv[NKB][8];
   const float* brow = a.bias ? a.bias + ((long)h * N + q) * N : nullptr;
 #pragma unroll
   for (int kb = 0; kb < NKB; ++kb) {
-    if (kb < nkb) {
+    {
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh) {
         const float4 bb = brow ? *reinterpret_cast<const float4*>(brow + kb * 32 + kh * 16 + 4 * g)
@@ -171,7 +174,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   float mx = -INFINITY;
 #pragma unroll
   for (int kb = 0; kb < NKB; ++kb) {
-    if (kb < nkb) {
+    {
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh) {
         HFrag<D> kf;
@@ -201,7 +204,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   for (int i = 0; i < DT; ++i) acc[i] = z4;
 #pragma unroll
   for (int kb = 0; kb < NKB; ++kb) {
-    if (kb < nkb) {
+    {
       bf16x8 pf;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -308,7 +311,6 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs b) {
   const int q0 = qb * 64 + wave * 16;
   const int lq = lane & 15, g = lane >> 4;
   const int q = min(q0, N - 16) + lq;  // idle waves read in bounds, store nothing
-  const int nkb = N / 32;
   HFrag<D> qf, dof;
   qf.load(a.qkvg + (tok0 + q) * a.ld + h * D, g);
   dof.load(b.dO + (tok0 + q) * a.ldo + h * D, g);
@@ -318,7 +320,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs b) {
   const float* brow = a.bias ? a.bias + ((long)h * N + q) * N : nullptr;
 #pragma unroll
   for (int kb = 0; kb < NKB; ++kb) {
-    if (kb < nkb) {
+    {
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh) {
         const float4 bb = brow ? *reinterpret_cast<const float4*>(brow + kb * 32 + kh * 16 + 4 * g)
@@ -334,7 +336,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs b) {
   if (q0 >= N) return;  // no barrier follows
 #pragma unroll
   for (int kb = 0; kb < NKB; ++kb) {
-    if (kb < nkb) {
+    {
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh) {
         const float4 mm = *reinterpret_cast<const float4*>(Ms + kb * 32 + kh * 16 + 4 * g);
@@ -353,7 +355,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs b) {
   for (int i = 0; i < DT; ++i) acc[i] = z4;
 #pragma unroll
   for (int kb = 0; kb < NKB; ++kb) {
-    if (kb < nkb) {
+    {
       bf16x8 dsf;
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh) {
@@ -391,19 +393,19 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs b) {
 // the pair bias is row-independent and is read once per workgroup into a
 // register tile of the same shape.  Per row, Q and dO (head h) are staged in
 // LDS; the two query halves' dK/dV partials are combined through LDS before
-// the write.  NQ_MAX bounds N.
+// the write.  N = 32*NQB exactly.
 //
 // Per score the MFMA accumulators start at (bias - lse) and -Dsum, so
 // p = exp2(S) and dS = p * dP' need no further adds.  A masked key gets
 // exponent -inf (p = dS = 0) -- exact for a row with any unmasked key, where
 // AF2's masked weight exp(-1e8 - lse) underflows to 0.  A fully masked row is
 // the uniform distribution (p = 1/N, dS = 0), handled as its own case.
-template <int D, int NQ_MAX>
+template <int D, int NQB>
 __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   constexpr int DT = D / 16;
   constexpr int LD = D + 8;
-  constexpr int NB = (NQ_MAX / 32 + 1) / 2;  // query blocks per wave
+  constexpr int NB = (NQB + 1) / 2;  // query blocks per wave (at most)
   const AttnArgs& a = b.f;
   const int N = a.N, H = a.H;
   bf16* Qs = reinterpret_cast<bf16*>(smem_raw);         // [N][LD]
@@ -423,10 +425,9 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
   const int r1 = min(a.R, r0 + b.rows_per_chunk);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
-  const int kt_ = wave & 1, half = wave >> 1;
+  const int kt_ = wave & 1, half = (wave >> 1) & 1;
   const int lk = lane & 15, g = lane >> 4;
   const int k = kb32 * 32 + kt_ * 16 + lk;
-  const int nqblk = N / 32;
   const long HD = (long)H * D;
   float* xk = Xs + (kt_ * 2 + 0) * DT * 4 * 64;
   float* xv = Xs + (kt_ * 2 + 1) * DT * 4 * 64;
@@ -476,7 +477,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
 #pragma unroll
     for (int ib = 0; ib < NB; ++ib) {
       const int blk = ib * 2 + half;
-      if (blk < nqblk) {
+      if (blk < NQB) {
         const int qb = blk * 32;
         bf16x8 pf, dsf;
 #pragma unroll
@@ -544,7 +545,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
 #pragma unroll
   for (int ib = 0; ib < NB; ++ib) {
     const int blk = ib * 2 + half;
-    if (blk >= nqblk) break;
+    if (blk >= NQB) break;
     const int qb = blk * 32;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -569,6 +570,23 @@ int attn_bwd_nchunk(int R, int rows_per_chunk) {
   return (R + rows_per_chunk - 1) / rows_per_chunk;
 }
 
+// Calls f(std::integral_constant<int, nb>) for nb = N/32 in 1..8: every
+// kernel is instantiated for its exact number of 32-blocks.
+template <class F>
+static void with_blocks(int nb, F&& f) {
+  switch (nb) {
+    case 1: f(std::integral_constant<int, 1>()); break;
+    case 2: f(std::integral_constant<int, 2>()); break;
+    case 3: f(std::integral_constant<int, 3>()); break;
+    case 4: f(std::integral_constant<int, 4>()); break;
+    case 5: f(std::integral_constant<int, 5>()); break;
+    case 6: f(std::integral_constant<int, 6>()); break;
+    case 7: f(std::integral_constant<int, 7>()); break;
+    case 8: f(std::integral_constant<int, 8>()); break;
+    default: throw std::runtime_error("attention: N/32 out of range");
+  }
+}
+
 static void attn_check(const AttnArgs& a) {
   if (a.D != 32 && a.D != 16) throw std::runtime_error("attention: head width must be 16 or 32");
   if (a.N <= 0 || a.N % 32 != 0) throw std::runtime_error("attention: N must be a positive multiple of 32");
@@ -582,7 +600,10 @@ static void attn_fwd_t(hipStream_t st, const AttnArgs& a) {
   const int nqb = (a.N + 63) / 64;
   const size_t lds = (size_t)a.N * (D + 8) * 2 * 2 + (size_t)a.N * 8;
   KTimed kt("attn_fwd", st);
-  hipLaunchKernelGGL((attn_fwd_kernel<D, 8>), dim3(xcd_grid((long)a.R * a.H * nqb)), dim3(256), lds, st, a);
+  const dim3 grid(xcd_grid((long)a.R * a.H * nqb));
+  with_blocks(a.N / 32, [&](auto nb) {
+    hipLaunchKernelGGL((attn_fwd_kernel<D, decltype(nb)::value>), grid, dim3(256), lds, st, a);
+  });
 }
 
 void attn_fwd(hipStream_t st, const AttnArgs& a) {
@@ -606,7 +627,10 @@ static void attn_bwd_t(hipStream_t st, const AttnBwdArgs& b) {
   const size_t lds_q = (size_t)a.N * (D + 8) * 2 * 2 + (size_t)a.N * 4;
   {
     KTimed kt("attn_bwd_dq", st);
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<D, 8>), dim3(xcd_grid((long)a.R * a.H * nqb)), dim3(256), lds_q, st, b);
+    const dim3 grid(xcd_grid((long)a.R * a.H * nqb));
+    with_blocks(a.N / 32, [&](auto nb) {
+      hipLaunchKernelGGL((attn_bwd_dq_kernel<D, decltype(nb)::value>), grid, dim3(256), lds_q, st, b);
+    });
   }
   const int nch = attn_bwd_nchunk(a.R, b.rows_per_chunk);
   const int nkb = (a.N + 31) / 32;
@@ -614,8 +638,10 @@ static void attn_bwd_t(hipStream_t st, const AttnBwdArgs& b) {
                        (size_t)2 * 2 * (D / 16) * 4 * 64 * 4;
   {
     KTimed kt("attn_bwd_dkv", st);
-    hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, 256>), dim3(xcd_grid((long)nch * a.H * nkb)), dim3(256), lds_k, st,
-                       b);
+    const dim3 grid(xcd_grid((long)nch * a.H * nkb));
+    with_blocks(a.N / 32, [&](auto nb) {
+      hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, decltype(nb)::value>), grid, dim3(256), lds_k, st, b);
+    });
   }
   if (b.dbias && a.bias) {
     if (!b.dbias_part) throw std::runtime_error("attention bwd: missing dbias scratch");
