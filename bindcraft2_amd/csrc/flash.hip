@@ -75,14 +75,31 @@ __device__ __forceinline__ bf16x8 ld_tr8(const bf16* T, int ld, int r0, int c0, 
   return r;
 }
 
-// Row-major copy of the n x D head slice at src (row stride ld) into
-// dst[n][D + 8]: 16-byte loads and stores.
-template <int D>
-__device__ __forceinline__ void stage_rows(bf16* dst, const bf16* src, long ld, int n, int tid,
-                                           int nthr) {
-  for (int c = tid; c < n * (D / 8); c += nthr) {
-    const int t = c / (D / 8), dc = (c % (D / 8)) * 8;
-    st8(&dst[t * (D + 8) + dc], ld8(src + (long)t * ld + dc));
+// Row-major copies of two N x D head slices (row strides lda, ldb) into
+// LDS tiles [N][D + 8], by 256 threads: every 16-byte load is issued before
+// the first store, so one memory latency covers the whole tile.
+template <int D, int N>
+__device__ __forceinline__ void stage_rows2(bf16* dA, const bf16* sA, long lda, bf16* dB,
+                                            const bf16* sB, long ldb, int tid) {
+  constexpr int CPR = D / 8;  // 16-byte chunks per row
+  constexpr int ITEMS = N * CPR;
+  constexpr int IT = (ITEMS + 255) / 256;
+  bf16x8 va[IT], vb[IT];
+#pragma unroll
+  for (int i = 0; i < IT; ++i) {
+    const int c = tid + 256 * i;
+    if (ITEMS % 256 == 0 || c < ITEMS) {
+      va[i] = ld8(sA + (long)(c / CPR) * lda + (c % CPR) * 8);
+      vb[i] = ld8(sB + (long)(c / CPR) * ldb + (c % CPR) * 8);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < IT; ++i) {
+    const int c = tid + 256 * i;
+    if (ITEMS % 256 == 0 || c < ITEMS) {
+      st8(&dA[(c / CPR) * (D + 8) + (c % CPR) * 8], va[i]);
+      st8(&dB[(c / CPR) * (D + 8) + (c % CPR) * 8], vb[i]);
+    }
   }
 }
 
@@ -122,7 +139,8 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   constexpr int DT = D / 16;
   constexpr int LD = D + 8;
-  const int N = a.N, H = a.H;
+  constexpr int N = 32 * NKB;  // == a.N (dispatch)
+  const int H = a.H;
   bf16* Ks = reinterpret_cast<bf16*>(smem_raw);          // [N][LD]
   bf16* Vs = Ks + N * LD;                                // [N][LD]
   float* Mm = reinterpret_cast<float*>(Vs + N * LD);     // [N] 1 / 0 per key
@@ -138,8 +156,8 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const long tok0 = (long)r * N;
-  stage_rows<D>(Ks, a.qkvg + tok0 * a.ld + H * D + h * D, a.ld, N, tid, 256);
-  stage_rows<D>(Vs, a.qkvg + tok0 * a.ld + 2 * H * D + h * D, a.ld, N, tid, 256);
+  stage_rows2<D, NKB * 32>(Ks, a.qkvg + tok0 * a.ld + H * D + h * D, a.ld, Vs,
+                           a.qkvg + tok0 * a.ld + 2 * H * D + h * D, a.ld, tid);
   for (int k = tid; k < N; k += 256) {
     const bool on = a.mask[r * a.mask_sr + k * a.mask_sk] != 0.f;
     Mm[k] = on ? 1.f : 0.f;
@@ -151,6 +169,10 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   const int q = min(q0, N - 16) + lq;  // idle waves read in bounds, store nothing
   HFrag<D> qf;
   qf.load(a.qkvg + (tok0 + q) * a.ld + h * D, g);
+  const bf16* grow = a.qkvg + (tok0 + q) * a.ld + 3 * H * D + h * D;
+  bf16x4 gv[DT];
+#pragma unroll
+  for (int dh = 0; dh < DT; ++dh) gv[dh] = *reinterpret_cast<const bf16x4*>(grow + dh * 16 + 4 * g);
   float sv[NKB][8];
   const float* brow = a.bias ? a.bias + ((long)h * N + q) * N : nullptr;
 #pragma unroll
@@ -221,17 +243,15 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   lsum += __shfl_xor(lsum, 32, 64);
   const float inv = __builtin_amdgcn_rcpf(lsum);
   const long orow = (tok0 + q) * a.ldo + h * D;
-  const bf16* grow = a.qkvg + (tok0 + q) * a.ld + 3 * H * D + h * D;
 #pragma unroll
   for (int dh = 0; dh < DT; ++dh) {
     const int d0 = dh * 16 + 4 * g;
-    const bf16x4 gv = *reinterpret_cast<const bf16x4*>(grow + d0);
     bf16x4 ov, gov;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float o = acc[dh][i] * inv;
       ov[i] = (bf16)o;
-      gov[i] = (bf16)(o * sigmoidf_((float)gv[i]));
+      gov[i] = (bf16)(o * sigmoidf_((float)gv[dh][i]));
     }
     *reinterpret_cast<bf16x4*>(a.o + orow + d0) = ov;
     *reinterpret_cast<bf16x4*>(a.og + orow + d0) = gov;
@@ -287,7 +307,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs b) {
   constexpr int DT = D / 16;
   constexpr int LD = D + 8;
   const AttnArgs& a = b.f;
-  const int N = a.N, H = a.H;
+  constexpr int N = 32 * NKB;  // == a.N (dispatch)
+  const int H = a.H;
   bf16* Ks = reinterpret_cast<bf16*>(smem_raw);   // [N][LD]
   bf16* Vs = Ks + N * LD;                         // [N][LD]
   float* Ms = reinterpret_cast<float*>(Vs + N * LD);
@@ -302,8 +323,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs b) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const long tok0 = (long)r * N;
-  stage_rows<D>(Ks, a.qkvg + tok0 * a.ld + H * D + h * D, a.ld, N, tid, 256);
-  stage_rows<D>(Vs, a.qkvg + tok0 * a.ld + 2 * H * D + h * D, a.ld, N, tid, 256);
+  stage_rows2<D, NKB * 32>(Ks, a.qkvg + tok0 * a.ld + H * D + h * D, a.ld, Vs,
+                           a.qkvg + tok0 * a.ld + 2 * H * D + h * D, a.ld, tid);
   // additive key mask: a masked key's exponent becomes -inf, so p = dS = 0
   for (int k = tid; k < N; k += 256)
     Ms[k] = a.mask[r * a.mask_sr + k * a.mask_sk] != 0.f ? 0.f : -INFINITY;
@@ -407,7 +428,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
   constexpr int LD = D + 8;
   constexpr int NB = (NQB + 1) / 2;  // query blocks per wave (at most)
   const AttnArgs& a = b.f;
-  const int N = a.N, H = a.H;
+  constexpr int N = 32 * NQB;  // == a.N (dispatch)
+  const int H = a.H;
   bf16* Qs = reinterpret_cast<bf16*>(smem_raw);         // [N][LD]
   bf16* Os = Qs + N * LD;                               // [N][LD] dO
   float* Ls = reinterpret_cast<float*>(Os + N * LD);    // [N] -lse
@@ -455,8 +477,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
   for (int r = r0; r < r1; ++r) {
     const long tok0 = (long)r * N;
     __syncthreads();  // previous row's LDS readers are done
-    stage_rows<D>(Qs, a.qkvg + tok0 * a.ld + h * D, a.ld, N, tid, 256);
-    stage_rows<D>(Os, b.dO + tok0 * a.ldo + h * D, a.ldo, N, tid, 256);
+    stage_rows2<D, NQB * 32>(Qs, a.qkvg + tok0 * a.ld + h * D, a.ld, Os,
+                             b.dO + tok0 * a.ldo + h * D, a.ldo, tid);
     int on = 0;
     for (int qq = tid; qq < N; qq += 256) {
       Ls[qq] = -a.lse[((long)r * H + h) * N + qq];
