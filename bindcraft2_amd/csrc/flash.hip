@@ -75,20 +75,22 @@ __device__ __forceinline__ bf16x8 ld_tr8(const bf16* T, int ld, int r0, int c0, 
   return r;
 }
 
-// Row-major copies of two N x D head slices (row strides lda, ldb) into
-// LDS tiles [N][D + 8], by 256 threads: every 16-byte load is issued before
-// the first store, so one memory latency covers the whole tile.
+// Row-major copies of the first `rows` (<= N) rows of two head slices (row
+// strides lda, ldb) into LDS tiles [N][D + 8], by 256 threads: every 16-byte
+// load is issued before the first store, so one memory latency covers the
+// whole tile.
 template <int D, int N>
 __device__ __forceinline__ void stage_rows2(bf16* dA, const bf16* sA, long lda, bf16* dB,
-                                            const bf16* sB, long ldb, int tid) {
+                                            const bf16* sB, long ldb, int tid, int rows = N) {
   constexpr int CPR = D / 8;  // 16-byte chunks per row
   constexpr int ITEMS = N * CPR;
   constexpr int IT = (ITEMS + 255) / 256;
+  const int items = rows * CPR;
   bf16x8 va[IT], vb[IT];
 #pragma unroll
   for (int i = 0; i < IT; ++i) {
     const int c = tid + 256 * i;
-    if (ITEMS % 256 == 0 || c < ITEMS) {
+    if (c < items) {
       va[i] = ld8(sA + (long)(c / CPR) * lda + (c % CPR) * 8);
       vb[i] = ld8(sB + (long)(c / CPR) * ldb + (c % CPR) * 8);
     }
@@ -96,7 +98,7 @@ __device__ __forceinline__ void stage_rows2(bf16* dA, const bf16* sA, long lda, 
 #pragma unroll
   for (int i = 0; i < IT; ++i) {
     const int c = tid + 256 * i;
-    if (ITEMS % 256 == 0 || c < ITEMS) {
+    if (c < items) {
       st8(&dA[(c / CPR) * (D + 8) + (c % CPR) * 8], va[i]);
       st8(&dB[(c / CPR) * (D + 8) + (c % CPR) * 8], vb[i]);
     }
@@ -126,24 +128,28 @@ struct HFrag<16> {
 };
 
 // ------------------------------------------------------------------ forward
-// Workgroup = (row r, head h, 64 queries); 4 waves x 16 queries.  The row's
-// K and V for head h are staged once in LDS.  N = 32*NKB exactly (one
-// instantiation per block count, so every loop over key blocks unrolls
-// without guards and the scheduler can overlap one block's MFMAs with the
-// previous block's softmax), and a lane keeps its query's whole score row (8 keys of every 32-key block) in
-// registers: the pair-bias row is fetched with all loads in flight at once,
-// the row maximum is taken once and every score costs one exponent -- no
-// running rescale of the output accumulator.
+// Workgroup = (row r, head h, 64 queries); 4 waves x 16 queries.  N = 32*NKB
+// exactly (one instantiation per block count, so every loop over key blocks
+// unrolls without guards and the scheduler can overlap one block's MFMAs
+// with the previous block's softmax).  Keys are processed in chunks of up to
+// 256 (8 blocks) whose K and V are staged in LDS; within a chunk a lane
+// keeps its query's scores (8 keys of every block) in registers, so the
+// chunk's maximum is taken once and every score costs one exponent.  For
+// N <= 256 there is one chunk and no rescale at all; beyond that the output
+// accumulator is rescaled once per chunk (online softmax over chunks).
 template <int D, int NKB>
 __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   constexpr int DT = D / 16;
   constexpr int LD = D + 8;
   constexpr int N = 32 * NKB;  // == a.N (dispatch)
+  constexpr int CB = NKB < 8 ? NKB : 8;  // key blocks per chunk
+  constexpr int NCH = (NKB + CB - 1) / CB;
+  constexpr int CN = 32 * CB;            // keys per chunk
   const int H = a.H;
-  bf16* Ks = reinterpret_cast<bf16*>(smem_raw);          // [N][LD]
-  bf16* Vs = Ks + N * LD;                                // [N][LD]
-  float* Mm = reinterpret_cast<float*>(Vs + N * LD);     // [N] 1 / 0 per key
+  bf16* Ks = reinterpret_cast<bf16*>(smem_raw);          // [CN][LD]
+  bf16* Vs = Ks + CN * LD;                               // [CN][LD]
+  float* Mm = reinterpret_cast<float*>(Vs + CN * LD);    // [N] 1 / 0 per key
   float* Ma = Mm + N;                                    // [N] 0 / NEG_LOGIT
 
   const int nqb = (N + 63) / 64;
@@ -156,8 +162,9 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const long tok0 = (long)r * N;
-  stage_rows2<D, NKB * 32>(Ks, a.qkvg + tok0 * a.ld + H * D + h * D, a.ld, Vs,
-                           a.qkvg + tok0 * a.ld + 2 * H * D + h * D, a.ld, tid);
+  const bf16* Kg = a.qkvg + tok0 * a.ld + H * D + h * D;
+  const bf16* Vg = a.qkvg + tok0 * a.ld + 2 * H * D + h * D;
+  stage_rows2<D, CN>(Ks, Kg, a.ld, Vs, Vg, a.ld, tid);
   for (int k = tid; k < N; k += 256) {
     const bool on = a.mask[r * a.mask_sr + k * a.mask_sk] != 0.f;
     Mm[k] = on ? 1.f : 0.f;
@@ -173,72 +180,92 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   bf16x4 gv[DT];
 #pragma unroll
   for (int dh = 0; dh < DT; ++dh) gv[dh] = *reinterpret_cast<const bf16x4*>(grow + dh * 16 + 4 * g);
-  float sv[NKB][8];
   const float* brow = a.bias ? a.bias + ((long)h * N + q) * N : nullptr;
-#pragma unroll
-  for (int kb = 0; kb < NKB; ++kb) {
-    {
-#pragma unroll
-      for (int kh = 0; kh < 2; ++kh) {
-        const float4 bb = brow ? *reinterpret_cast<const float4*>(brow + kb * 32 + kh * 16 + 4 * g)
-                               : make_float4(0.f, 0.f, 0.f, 0.f);
-        sv[kb][kh * 4 + 0] = bb.x;
-        sv[kb][kh * 4 + 1] = bb.y;
-        sv[kb][kh * 4 + 2] = bb.z;
-        sv[kb][kh * 4 + 3] = bb.w;
-      }
-    }
-  }
-  __syncthreads();
-  if (q0 >= N) return;  // no barrier follows
-
   const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
-  float mx = -INFINITY;
-#pragma unroll
-  for (int kb = 0; kb < NKB; ++kb) {
-    {
-#pragma unroll
-      for (int kh = 0; kh < 2; ++kh) {
-        HFrag<D> kf;
-        kf.load(&Ks[(kb * 32 + kh * 16 + lq) * LD], g);
-        const f32x4 s = HFrag<D>::mma(kf, qf, z4);
-        const int k0 = kb * 32 + kh * 16 + 4 * g;
-        const float4 mm = *reinterpret_cast<const float4*>(Mm + k0);
-        const float4 ma = *reinterpret_cast<const float4*>(Ma + k0);
-        const float mv[4] = {mm.x, mm.y, mm.z, mm.w};
-        const float av[4] = {ma.x, ma.y, ma.z, ma.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          // unmasked: s + bias; masked: exactly NEG_LOGIT
-          float& x = sv[kb][kh * 4 + i];
-          x = __builtin_fmaf(s[i] + x, mv[i], av[i]);
-          mx = fmaxf(mx, x);
-        }
-      }
-    }
-  }
-  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-
-  float lsum = 0.f;
+  float mx = -INFINITY, lsum = 0.f;
   f32x4 acc[DT];
 #pragma unroll
   for (int i = 0; i < DT; ++i) acc[i] = z4;
+
 #pragma unroll
-  for (int kb = 0; kb < NKB; ++kb) {
-    {
-      bf16x8 pf;
+  for (int c = 0; c < NCH; ++c) {
+    const int k0c = c * CN;
+    float sv[CB][8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float p = fast_exp2(sv[kb][e] - mx);
-        lsum += p;
-        pf[e] = (bf16)p;
+    for (int kb = 0; kb < CB; ++kb) {
+      if (c * CB + kb < NKB) {
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) {
+          const float4 bb = brow ? *reinterpret_cast<const float4*>(brow + k0c + kb * 32 + kh * 16 + 4 * g)
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+          sv[kb][kh * 4 + 0] = bb.x;
+          sv[kb][kh * 4 + 1] = bb.y;
+          sv[kb][kh * 4 + 2] = bb.z;
+          sv[kb][kh * 4 + 3] = bb.w;
+        }
       }
+    }
+    if (c > 0) {
+      __syncthreads();  // every wave is done with the previous chunk
+      stage_rows2<D, CN>(Ks, Kg + (long)k0c * a.ld, a.ld, Vs, Vg + (long)k0c * a.ld, a.ld, tid,
+                         min(CN, N - k0c));
+    }
+    __syncthreads();
+    if (NCH == 1 && q0 >= N) return;  // idle wave, no barrier follows
+
+    float mc = -INFINITY;
 #pragma unroll
-      for (int dh = 0; dh < DT; ++dh)
-        acc[dh] = mfma16x16x32(ld_tr8(Vs, LD, kb * 32, dh * 16, lane), pf, acc[dh]);
+    for (int kb = 0; kb < CB; ++kb) {
+      if (c * CB + kb < NKB) {
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) {
+          HFrag<D> kf;
+          kf.load(&Ks[(kb * 32 + kh * 16 + lq) * LD], g);
+          const f32x4 s = HFrag<D>::mma(kf, qf, z4);
+          const int kk = k0c + kb * 32 + kh * 16 + 4 * g;
+          const float4 mm = *reinterpret_cast<const float4*>(Mm + kk);
+          const float4 ma = *reinterpret_cast<const float4*>(Ma + kk);
+          const float mv[4] = {mm.x, mm.y, mm.z, mm.w};
+          const float av[4] = {ma.x, ma.y, ma.z, ma.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            // unmasked: s + bias; masked: exactly NEG_LOGIT
+            float& x = sv[kb][kh * 4 + i];
+            x = __builtin_fmaf(s[i] + x, mv[i], av[i]);
+            mc = fmaxf(mc, x);
+          }
+        }
+      }
+    }
+    mc = fmaxf(mc, __shfl_xor(mc, 16, 64));
+    mc = fmaxf(mc, __shfl_xor(mc, 32, 64));
+    if (c > 0) {
+      const float mn = fmaxf(mx, mc);
+      const float alpha = fast_exp2(mx - mn);
+      lsum *= alpha;
+#pragma unroll
+      for (int dh = 0; dh < DT; ++dh) acc[dh] *= alpha;
+      mx = mn;
+    } else {
+      mx = mc;
+    }
+#pragma unroll
+    for (int kb = 0; kb < CB; ++kb) {
+      if (c * CB + kb < NKB) {
+        bf16x8 pf;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float p = fast_exp2(sv[kb][e] - mx);
+          lsum += p;
+          pf[e] = (bf16)p;
+        }
+#pragma unroll
+        for (int dh = 0; dh < DT; ++dh)
+          acc[dh] = mfma16x16x32(ld_tr8(Vs, LD, kb * 32, dh * 16, lane), pf, acc[dh]);
+      }
     }
   }
+  if (q0 >= N) return;
   lsum += __shfl_xor(lsum, 16, 64);
   lsum += __shfl_xor(lsum, 32, 64);
   const float inv = __builtin_amdgcn_rcpf(lsum);
@@ -298,9 +325,10 @@ __global__ __launch_bounds__(256) void attn_gate_bwd_kernel(AttnBwdArgs b) {
 }
 
 // ----------------------------------------------------------- backward: dQ
-// Same decomposition as the forward: (row, head, 64 queries), 4 waves; the
-// lane's pair-bias row (minus lse, with -inf at masked keys so p = dS = 0
-// there) is fetched up front, all loads in flight at once.
+// Same decomposition as the forward: (row, head, 64 queries), 4 waves, keys
+// in chunks of up to 256 staged in LDS.  Per chunk the lane's pair-bias row
+// (minus lse, with -inf at masked keys so p = dS = 0 there) is fetched up
+// front, all loads in flight at once.
 template <int D, int NKB>
 __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs b) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
@@ -308,10 +336,13 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs b) {
   constexpr int LD = D + 8;
   const AttnArgs& a = b.f;
   constexpr int N = 32 * NKB;  // == a.N (dispatch)
+  constexpr int CB = NKB < 8 ? NKB : 8;  // key blocks per chunk
+  constexpr int NCH = (NKB + CB - 1) / CB;
+  constexpr int CN = 32 * CB;
   const int H = a.H;
-  bf16* Ks = reinterpret_cast<bf16*>(smem_raw);   // [N][LD]
-  bf16* Vs = Ks + N * LD;                         // [N][LD]
-  float* Ms = reinterpret_cast<float*>(Vs + N * LD);
+  bf16* Ks = reinterpret_cast<bf16*>(smem_raw);   // [CN][LD]
+  bf16* Vs = Ks + CN * LD;                        // [CN][LD]
+  float* Ms = reinterpret_cast<float*>(Vs + CN * LD);  // [N]
 
   const int nqb = (N + 63) / 64;
   const long G = (long)a.R * H * nqb;
@@ -323,8 +354,9 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs b) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const long tok0 = (long)r * N;
-  stage_rows2<D, NKB * 32>(Ks, a.qkvg + tok0 * a.ld + H * D + h * D, a.ld, Vs,
-                           a.qkvg + tok0 * a.ld + 2 * H * D + h * D, a.ld, tid);
+  const bf16* Kg = a.qkvg + tok0 * a.ld + H * D + h * D;
+  const bf16* Vg = a.qkvg + tok0 * a.ld + 2 * H * D + h * D;
+  stage_rows2<D, CN>(Ks, Kg, a.ld, Vs, Vg, a.ld, tid);
   // additive key mask: a masked key's exponent becomes -inf, so p = dS = 0
   for (int k = tid; k < N; k += 256)
     Ms[k] = a.mask[r * a.mask_sr + k * a.mask_sk] != 0.f ? 0.f : -INFINITY;
@@ -337,66 +369,76 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs b) {
   dof.load(b.dO + (tok0 + q) * a.ldo + h * D, g);
   const float lse = a.lse[((long)r * H + h) * N + q];
   const float Dq = b.Dsum[((long)r * H + h) * N + q];
-  float bsv[NKB][8];
   const float* brow = a.bias ? a.bias + ((long)h * N + q) * N : nullptr;
-#pragma unroll
-  for (int kb = 0; kb < NKB; ++kb) {
-    {
-#pragma unroll
-      for (int kh = 0; kh < 2; ++kh) {
-        const float4 bb = brow ? *reinterpret_cast<const float4*>(brow + kb * 32 + kh * 16 + 4 * g)
-                               : make_float4(0.f, 0.f, 0.f, 0.f);
-        bsv[kb][kh * 4 + 0] = bb.x - lse;
-        bsv[kb][kh * 4 + 1] = bb.y - lse;
-        bsv[kb][kh * 4 + 2] = bb.z - lse;
-        bsv[kb][kh * 4 + 3] = bb.w - lse;
-      }
-    }
-  }
-  __syncthreads();
-  if (q0 >= N) return;  // no barrier follows
-#pragma unroll
-  for (int kb = 0; kb < NKB; ++kb) {
-    {
-#pragma unroll
-      for (int kh = 0; kh < 2; ++kh) {
-        const float4 mm = *reinterpret_cast<const float4*>(Ms + kb * 32 + kh * 16 + 4 * g);
-        bsv[kb][kh * 4 + 0] += mm.x;
-        bsv[kb][kh * 4 + 1] += mm.y;
-        bsv[kb][kh * 4 + 2] += mm.z;
-        bsv[kb][kh * 4 + 3] += mm.w;
-      }
-    }
-  }
-
   const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
   const f32x4 nD = {-Dq, -Dq, -Dq, -Dq};
   f32x4 acc[DT];
 #pragma unroll
   for (int i = 0; i < DT; ++i) acc[i] = z4;
+
 #pragma unroll
-  for (int kb = 0; kb < NKB; ++kb) {
-    {
-      bf16x8 dsf;
+  for (int c = 0; c < NCH; ++c) {
+    const int k0c = c * CN;
+    float bsv[CB][8];
 #pragma unroll
-      for (int kh = 0; kh < 2; ++kh) {
-        const int krow = (kb * 32 + kh * 16 + lq) * LD;
-        HFrag<D> kf, vf;
-        kf.load(&Ks[krow], g);
-        vf.load(&Vs[krow], g);
-        f32x4 cs;
+    for (int kb = 0; kb < CB; ++kb) {
+      if (c * CB + kb < NKB) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) cs[i] = bsv[kb][kh * 4 + i];
-        const f32x4 s = HFrag<D>::mma(kf, qf, cs);    // S + bias - lse
-        const f32x4 dp = HFrag<D>::mma(vf, dof, nD);  // dP - Dsum
-#pragma unroll
-        for (int i = 0; i < 4; ++i) dsf[kh * 4 + i] = (bf16)(fast_exp2(s[i]) * dp[i]);
+        for (int kh = 0; kh < 2; ++kh) {
+          const float4 bb = brow ? *reinterpret_cast<const float4*>(brow + k0c + kb * 32 + kh * 16 + 4 * g)
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+          bsv[kb][kh * 4 + 0] = bb.x - lse;
+          bsv[kb][kh * 4 + 1] = bb.y - lse;
+          bsv[kb][kh * 4 + 2] = bb.z - lse;
+          bsv[kb][kh * 4 + 3] = bb.w - lse;
+        }
       }
+    }
+    if (c > 0) {
+      __syncthreads();  // every wave is done with the previous chunk
+      stage_rows2<D, CN>(Ks, Kg + (long)k0c * a.ld, a.ld, Vs, Vg + (long)k0c * a.ld, a.ld, tid,
+                         min(CN, N - k0c));
+    }
+    __syncthreads();
+    if (NCH == 1 && q0 >= N) return;  // idle wave, no barrier follows
 #pragma unroll
-      for (int dh = 0; dh < DT; ++dh)
-        acc[dh] = mfma16x16x32(ld_tr8(Ks, LD, kb * 32, dh * 16, lane), dsf, acc[dh]);
+    for (int kb = 0; kb < CB; ++kb) {
+      if (c * CB + kb < NKB) {
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) {
+          const float4 mm = *reinterpret_cast<const float4*>(Ms + k0c + kb * 32 + kh * 16 + 4 * g);
+          bsv[kb][kh * 4 + 0] += mm.x;
+          bsv[kb][kh * 4 + 1] += mm.y;
+          bsv[kb][kh * 4 + 2] += mm.z;
+          bsv[kb][kh * 4 + 3] += mm.w;
+        }
+      }
+    }
+#pragma unroll
+    for (int kb = 0; kb < CB; ++kb) {
+      if (c * CB + kb < NKB) {
+        bf16x8 dsf;
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) {
+          const int krow = (kb * 32 + kh * 16 + lq) * LD;
+          HFrag<D> kf, vf;
+          kf.load(&Ks[krow], g);
+          vf.load(&Vs[krow], g);
+          f32x4 cs;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) cs[i] = bsv[kb][kh * 4 + i];
+          const f32x4 s = HFrag<D>::mma(kf, qf, cs);    // S + bias - lse
+          const f32x4 dp = HFrag<D>::mma(vf, dof, nD);  // dP - Dsum
+#pragma unroll
+          for (int i = 0; i < 4; ++i) dsf[kh * 4 + i] = (bf16)(fast_exp2(s[i]) * dp[i]);
+        }
+#pragma unroll
+        for (int dh = 0; dh < DT; ++dh)
+          acc[dh] = mfma16x16x32(ld_tr8(Ks, LD, kb * 32, dh * 16, lane), dsf, acc[dh]);
+      }
     }
   }
+  if (q0 >= N) return;
   bf16* out = b.dqkvg + (tok0 + q) * a.ld + h * D;
 #pragma unroll
   for (int dh = 0; dh < DT; ++dh) {
@@ -408,58 +450,63 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs b) {
 }
 
 // ------------------------------------------------------ backward: dK, dV, dB
-// Workgroup = (chunk of rows, head h, 32 keys), 4 waves: wave w owns key
-// tile w&1 (16 keys) and the 32-query blocks ib with ib%2 == w>>1, so the
-// bias-gradient tile it keeps in registers is ceil(N/64) x 8 floats per lane;
-// the pair bias is row-independent and is read once per workgroup into a
-// register tile of the same shape.  Per row, Q and dO (head h) are staged in
-// LDS; the two query halves' dK/dV partials are combined through LDS before
-// the write.  N = 32*NQB exactly.
+// Workgroup = (chunk of rows, head h, KT*16 keys), 4 waves = KT key tiles x
+// QS query groups (KT=2, QS=2 for N <= 256; KT=1, QS=4 beyond).  Wave
+// (kt, qs) owns key tile kt and the 32-query blocks blk = ib*QS + qs, so the
+// bias-gradient tile it keeps in registers is ceil(N/(32*QS)) x 8 floats per
+// lane; the pair bias is row-independent and is read once per workgroup into
+// a register tile of the same shape.  Per row, Q and dO (head h) are staged
+// in LDS (in chunks of up to 256 rows); the QS query groups' dK/dV partials
+// are added through LDS in a fixed order before the write.  N = 32*NQB.
 //
 // Per score the MFMA accumulators start at (bias - lse) and -Dsum, so
 // p = exp2(S) and dS = p * dP' need no further adds.  A masked key gets
 // exponent -inf (p = dS = 0) -- exact for a row with any unmasked key, where
 // AF2's masked weight exp(-1e8 - lse) underflows to 0.  A fully masked row is
-// the uniform distribution (p = 1/N, dS = 0), handled as its own case.
+// the uniform distribution (p = 1/N, dS = 0).
 template <int D, int NQB>
 __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   constexpr int DT = D / 16;
   constexpr int LD = D + 8;
-  constexpr int NB = (NQB + 1) / 2;  // query blocks per wave (at most)
+  constexpr int N = 32 * NQB;            // == a.N (dispatch)
+  constexpr int QS = NQB > 8 ? 4 : 2;    // query groups per key tile
+  constexpr int KT = 4 / QS;             // 16-key tiles per workgroup
+  constexpr int NB = (NQB + QS - 1) / QS;  // query blocks per wave (at most)
+  constexpr int CQB = NQB < 8 ? NQB : 8;   // query blocks per staged chunk
+  constexpr int NCH = (NQB + CQB - 1) / CQB;
+  constexpr int CN = 32 * CQB;
+  static_assert(NCH == 1 || CQB % QS == 0, "chunk must hold whole rounds of query groups");
   const AttnArgs& a = b.f;
-  constexpr int N = 32 * NQB;  // == a.N (dispatch)
   const int H = a.H;
-  bf16* Qs = reinterpret_cast<bf16*>(smem_raw);         // [N][LD]
-  bf16* Os = Qs + N * LD;                               // [N][LD] dO
-  float* Ls = reinterpret_cast<float*>(Os + N * LD);    // [N] -lse
+  bf16* Qs = reinterpret_cast<bf16*>(smem_raw);         // [CN][LD]
+  bf16* Os = Qs + CN * LD;                              // [CN][LD] dO
+  float* Ls = reinterpret_cast<float*>(Os + CN * LD);   // [N] -lse
   float* Ds = Ls + N;                                   // [N] -Dsum
-  float* Xs = Ds + N;                                   // [2 tiles][K,V][DT*4][64]
+  float* Xs = Ds + N;                                   // [QS-1][KT][K,V][DT*4][64]
 
-  const int nkb = (N + 31) / 32;
-  const long G = (long)((a.R + b.rows_per_chunk - 1) / b.rows_per_chunk) * H * nkb;
-  const int bid = (int)xcd_block(G);  // (chunk, h, kb): the kb blocks share Q, dO
+  constexpr int NKW = N / (16 * KT);  // key groups per (chunk, head)
+  const long G = (long)((a.R + b.rows_per_chunk - 1) / b.rows_per_chunk) * H * NKW;
+  const int bid = (int)xcd_block(G);  // (chunk, h, kw): the kw groups share Q, dO
   if (bid >= G) return;
-  const int kb32 = bid % nkb;
-  const int h = (bid / nkb) % H;
-  const int ch = bid / (nkb * H);
+  const int kw = bid % NKW;
+  const int h = (bid / NKW) % H;
+  const int ch = bid / (NKW * H);
   const int r0 = ch * b.rows_per_chunk;
   const int r1 = min(a.R, r0 + b.rows_per_chunk);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
-  const int kt_ = wave & 1, half = (wave >> 1) & 1;
+  const int kt_ = wave % KT, qs = (wave / KT) % QS;
   const int lk = lane & 15, g = lane >> 4;
-  const int k = kb32 * 32 + kt_ * 16 + lk;
+  const int k = kw * 16 * KT + kt_ * 16 + lk;
   const long HD = (long)H * D;
-  float* xk = Xs + (kt_ * 2 + 0) * DT * 4 * 64;
-  float* xv = Xs + (kt_ * 2 + 1) * DT * 4 * 64;
 
   // bias column k at this wave's queries; bias-gradient accumulators
   float bsl[NB][8], dbias[NB][8];
   const float* bcol = a.bias ? a.bias + (long)h * N * N + k : nullptr;
 #pragma unroll
   for (int ib = 0; ib < NB; ++ib) {
-    const int qb = (ib * 2 + half) * 32;
+    const int qb = (ib * QS + qs) * 32;
     const bool have = bcol && qb < N;  // wave-uniform
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -476,9 +523,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
 
   for (int r = r0; r < r1; ++r) {
     const long tok0 = (long)r * N;
+    const bf16* Qg = a.qkvg + tok0 * a.ld + h * D;
+    const bf16* Og = b.dO + tok0 * a.ldo + h * D;
     __syncthreads();  // previous row's LDS readers are done
-    stage_rows2<D, NQB * 32>(Qs, a.qkvg + tok0 * a.ld + h * D, a.ld, Os,
-                             b.dO + tok0 * a.ldo + h * D, a.ldo, tid);
+    stage_rows2<D, CN>(Qs, Qg, a.ld, Os, Og, a.ldo, tid);
     int on = 0;
     for (int qq = tid; qq < N; qq += 256) {
       Ls[qq] = -a.lse[((long)r * H + h) * N + qq];
@@ -490,62 +538,84 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
     vf.load(a.qkvg + (tok0 + k) * a.ld + 2 * HD + h * D, g);
     const bool mk = a.mask[r * a.mask_sr + k * a.mask_sk] != 0.f;
     const bool live = __syncthreads_or(on);  // the row has an unmasked key
-    f32x4 accK[DT], accV[DT];
-#pragma unroll
-    for (int i = 0; i < DT; ++i) { accK[i] = z4; accV[i] = z4; }
     // exponent of a masked key: -inf (weight 0) in a live row, -log2 N
     // (weight 1/N) in a fully masked one; either way its dS is 0
     const float xm = live ? -INFINITY : -__log2f((float)N);
+    f32x4 accK[DT], accV[DT];
 #pragma unroll
-    for (int ib = 0; ib < NB; ++ib) {
-      const int blk = ib * 2 + half;
-      if (blk < NQB) {
-        const int qb = blk * 32;
-        bf16x8 pf, dsf;
+    for (int i = 0; i < DT; ++i) { accK[i] = z4; accV[i] = z4; }
 #pragma unroll
-        for (int qh = 0; qh < 2; ++qh) {
-          const int qrow = qb + qh * 16;
-          HFrag<D> qa, da;
-          qa.load(&Qs[(qrow + lk) * LD], g);
-          da.load(&Os[(qrow + lk) * LD], g);
-          const float4 lv = *reinterpret_cast<const float4*>(Ls + qrow + 4 * g);
-          const float4 dv = *reinterpret_cast<const float4*>(Ds + qrow + 4 * g);
-          f32x4 cs, cd;
-          cs[0] = bsl[ib][qh * 4 + 0] + lv.x;
-          cs[1] = bsl[ib][qh * 4 + 1] + lv.y;
-          cs[2] = bsl[ib][qh * 4 + 2] + lv.z;
-          cs[3] = bsl[ib][qh * 4 + 3] + lv.w;
-          cd[0] = dv.x; cd[1] = dv.y; cd[2] = dv.z; cd[3] = dv.w;
-          const f32x4 s = HFrag<D>::mma(qa, kf, cs);   // S + bias - lse
-          const f32x4 dp = HFrag<D>::mma(da, vf, cd);  // dP - Dsum
+    for (int c = 0; c < NCH; ++c) {
+      if (c > 0) {
+        __syncthreads();  // every wave is done with the previous chunk
+        stage_rows2<D, CN>(Qs, Qg + (long)c * CN * a.ld, a.ld, Os, Og + (long)c * CN * a.ldo,
+                           a.ldo, tid, min(CN, N - c * CN));
+        __syncthreads();
+      }
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float p = fast_exp2(mk ? s[i] : xm);
-            const float ds = mk ? p * dp[i] : 0.f;
-            pf[qh * 4 + i] = (bf16)p;
-            dsf[qh * 4 + i] = (bf16)ds;
-            dbias[ib][qh * 4 + i] += ds;
+      for (int ib = 0; ib < NB; ++ib) {
+        if (NCH > 1 && ib * QS / CQB != c) continue;  // block of another chunk
+        const int blk = ib * QS + qs;
+        if (blk < NQB) {
+          const int qb = blk * 32;         // query index
+          const int ql = qb - c * CN;      // row in the staged chunk
+          bf16x8 pf, dsf;
+#pragma unroll
+          for (int qh = 0; qh < 2; ++qh) {
+            HFrag<D> qa, da;
+            qa.load(&Qs[(ql + qh * 16 + lk) * LD], g);
+            da.load(&Os[(ql + qh * 16 + lk) * LD], g);
+            const float4 lv = *reinterpret_cast<const float4*>(Ls + qb + qh * 16 + 4 * g);
+            const float4 dv = *reinterpret_cast<const float4*>(Ds + qb + qh * 16 + 4 * g);
+            f32x4 cs, cd;
+            cs[0] = bsl[ib][qh * 4 + 0] + lv.x;
+            cs[1] = bsl[ib][qh * 4 + 1] + lv.y;
+            cs[2] = bsl[ib][qh * 4 + 2] + lv.z;
+            cs[3] = bsl[ib][qh * 4 + 3] + lv.w;
+            cd[0] = dv.x; cd[1] = dv.y; cd[2] = dv.z; cd[3] = dv.w;
+            const f32x4 s = HFrag<D>::mma(qa, kf, cs);   // S + bias - lse
+            const f32x4 dp = HFrag<D>::mma(da, vf, cd);  // dP - Dsum
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float p = fast_exp2(mk ? s[i] : xm);
+              const float ds = mk ? p * dp[i] : 0.f;
+              pf[qh * 4 + i] = (bf16)p;
+              dsf[qh * 4 + i] = (bf16)ds;
+              dbias[ib][qh * 4 + i] += ds;
+            }
           }
-        }
 #pragma unroll
-        for (int dh = 0; dh < DT; ++dh) {
-          accV[dh] = mfma16x16x32(ld_tr8(Os, LD, qb, dh * 16, lane), pf, accV[dh]);
-          accK[dh] = mfma16x16x32(ld_tr8(Qs, LD, qb, dh * 16, lane), dsf, accK[dh]);
+          for (int dh = 0; dh < DT; ++dh) {
+            accV[dh] = mfma16x16x32(ld_tr8(Os, LD, ql, dh * 16, lane), pf, accV[dh]);
+            accK[dh] = mfma16x16x32(ld_tr8(Qs, LD, ql, dh * 16, lane), dsf, accK[dh]);
+          }
         }
       }
     }
-    // combine the two query halves: half 1 parks its partials in LDS
-    if (half == 1) {
+    // add the query groups' partials: groups 1..QS-1 park theirs in LDS
+    if (qs > 0) {
+      float* x = Xs + ((qs - 1) * KT + kt_) * 2 * DT * 4 * 64;
 #pragma unroll
       for (int dh = 0; dh < DT; ++dh)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          xk[(dh * 4 + i) * 64 + lane] = accK[dh][i];
-          xv[(dh * 4 + i) * 64 + lane] = accV[dh][i];
+          x[(dh * 4 + i) * 64 + lane] = accK[dh][i];
+          x[(DT * 4 + dh * 4 + i) * 64 + lane] = accV[dh][i];
         }
     }
     __syncthreads();
-    if (half == 0) {
+    if (qs == 0) {
+#pragma unroll
+      for (int j = 1; j < QS; ++j) {
+        const float* x = Xs + ((j - 1) * KT + kt_) * 2 * DT * 4 * 64;
+#pragma unroll
+        for (int dh = 0; dh < DT; ++dh)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            accK[dh][i] += x[(dh * 4 + i) * 64 + lane];
+            accV[dh][i] += x[(DT * 4 + dh * 4 + i) * 64 + lane];
+          }
+      }
       // dK (w.r.t. the unscaled k) = sum_q dS * q_scaled / log2(e)
       bf16* dk = b.dqkvg + (tok0 + k) * a.ld + HD + h * D;
       bf16* dvp = b.dqkvg + (tok0 + k) * a.ld + 2 * HD + h * D;
@@ -554,8 +624,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
         bf16x4 kv, vv;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          kv[i] = (bf16)((accK[dh][i] + xk[(dh * 4 + i) * 64 + lane]) * (1.f / LOG2E));
-          vv[i] = (bf16)(accV[dh][i] + xv[(dh * 4 + i) * 64 + lane]);
+          kv[i] = (bf16)(accK[dh][i] * (1.f / LOG2E));
+          vv[i] = (bf16)accV[dh][i];
         }
         *reinterpret_cast<bf16x4*>(dk + dh * 16 + 4 * g) = kv;
         *reinterpret_cast<bf16x4*>(dvp + dh * 16 + 4 * g) = vv;
@@ -566,7 +636,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
   float* part = b.dbias_part + (((long)ch * H + h) * N) * N;
 #pragma unroll
   for (int ib = 0; ib < NB; ++ib) {
-    const int blk = ib * 2 + half;
+    const int blk = ib * QS + qs;
     if (blk >= NQB) break;
     const int qb = blk * 32;
 #pragma unroll
@@ -592,27 +662,31 @@ int attn_bwd_nchunk(int R, int rows_per_chunk) {
   return (R + rows_per_chunk - 1) / rows_per_chunk;
 }
 
-// Calls f(std::integral_constant<int, nb>) for nb = N/32 in 1..8: every
+// Rows per bias-gradient chunk: the partials are [nchunk][H][N][N] f32, so
+// longer rows take longer chunks (N = 512: 32 chunks, 134 MB at H = 4).
+int attn_rows_per_chunk(int N) { return N <= 256 ? 8 : 16; }
+
+// Calls f(std::integral_constant<int, nb>) for nb = N/32 in 1..16: every
 // kernel is instantiated for its exact number of 32-blocks.
 template <class F>
 static void with_blocks(int nb, F&& f) {
   switch (nb) {
-    case 1: f(std::integral_constant<int, 1>()); break;
-    case 2: f(std::integral_constant<int, 2>()); break;
-    case 3: f(std::integral_constant<int, 3>()); break;
-    case 4: f(std::integral_constant<int, 4>()); break;
-    case 5: f(std::integral_constant<int, 5>()); break;
-    case 6: f(std::integral_constant<int, 6>()); break;
-    case 7: f(std::integral_constant<int, 7>()); break;
-    case 8: f(std::integral_constant<int, 8>()); break;
+#define BC2N_NB(v) case v: f(std::integral_constant<int, v>()); break;
+    BC2N_NB(1) BC2N_NB(2) BC2N_NB(3) BC2N_NB(4) BC2N_NB(5) BC2N_NB(6) BC2N_NB(7) BC2N_NB(8)
+    BC2N_NB(9) BC2N_NB(10) BC2N_NB(11) BC2N_NB(12) BC2N_NB(13) BC2N_NB(14) BC2N_NB(15)
+    BC2N_NB(16)
+#undef BC2N_NB
     default: throw std::runtime_error("attention: N/32 out of range");
   }
 }
 
+// keys per LDS chunk of the forward / dQ kernels, rows per chunk of dK/dV
+static int attn_chunk(int N) { return N < 256 ? N : 256; }
+
 static void attn_check(const AttnArgs& a) {
   if (a.D != 32 && a.D != 16) throw std::runtime_error("attention: head width must be 16 or 32");
   if (a.N <= 0 || a.N % 32 != 0) throw std::runtime_error("attention: N must be a positive multiple of 32");
-  if (a.N > 256) throw std::runtime_error("attention: N > 256 not supported yet");
+  if (a.N > 512) throw std::runtime_error("attention: N > 512 not supported");
   if (a.ld % 8 != 0 || a.ldo % 8 != 0) throw std::runtime_error("attention: row strides must be multiples of 8");
   if (!a.qkvg || !a.mask || !a.lse || !a.o) throw std::runtime_error("attention: missing operand");
 }
@@ -620,7 +694,7 @@ static void attn_check(const AttnArgs& a) {
 template <int D>
 static void attn_fwd_t(hipStream_t st, const AttnArgs& a) {
   const int nqb = (a.N + 63) / 64;
-  const size_t lds = (size_t)a.N * (D + 8) * 2 * 2 + (size_t)a.N * 8;
+  const size_t lds = (size_t)attn_chunk(a.N) * (D + 8) * 2 * 2 + (size_t)a.N * 8;
   KTimed kt("attn_fwd", st);
   const dim3 grid(xcd_grid((long)a.R * a.H * nqb));
   with_blocks(a.N / 32, [&](auto nb) {
@@ -646,7 +720,7 @@ static void attn_bwd_t(hipStream_t st, const AttnBwdArgs& b) {
                        dim3(256), 0, st, b);
   }
   const int nqb = (a.N + 63) / 64;
-  const size_t lds_q = (size_t)a.N * (D + 8) * 2 * 2 + (size_t)a.N * 4;
+  const size_t lds_q = (size_t)attn_chunk(a.N) * (D + 8) * 2 * 2 + (size_t)a.N * 4;
   {
     KTimed kt("attn_bwd_dq", st);
     const dim3 grid(xcd_grid((long)a.R * a.H * nqb));
@@ -655,12 +729,14 @@ static void attn_bwd_t(hipStream_t st, const AttnBwdArgs& b) {
     });
   }
   const int nch = attn_bwd_nchunk(a.R, b.rows_per_chunk);
-  const int nkb = (a.N + 31) / 32;
-  const size_t lds_k = (size_t)a.N * (D + 8) * 2 * 2 + (size_t)a.N * 4 * 2 +
-                       (size_t)2 * 2 * (D / 16) * 4 * 64 * 4;
+  // query groups QS and key tiles KT per workgroup, as in the kernel
+  const int QS = a.N > 256 ? 4 : 2, KT = 4 / QS;
+  const int nkw = a.N / (16 * KT);
+  const size_t lds_k = (size_t)attn_chunk(a.N) * (D + 8) * 2 * 2 + (size_t)a.N * 4 * 2 +
+                       (size_t)(QS - 1) * KT * 2 * (D / 16) * 4 * 64 * 4;
   {
     KTimed kt("attn_bwd_dkv", st);
-    const dim3 grid(xcd_grid((long)nch * a.H * nkb));
+    const dim3 grid(xcd_grid((long)nch * a.H * nkw));
     with_blocks(a.N / 32, [&](auto nb) {
       hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, decltype(nb)::value>), grid, dim3(256), lds_k, st, b);
     });

@@ -56,6 +56,7 @@ struct AttnBwdArgs {
 };
 void attn_bwd(hipStream_t st, const AttnBwdArgs& a);
 int attn_bwd_nchunk(int R, int rows_per_chunk);
+int attn_rows_per_chunk(int N);
 
 // ---------------------------------------------------------------- dropout
 // Shared-dropout keep/scale table for one module: tbl[b*C+c] = keep/keep_rate

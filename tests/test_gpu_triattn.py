@@ -43,6 +43,9 @@ def _oracle(prm, per_column, pair, mask, tbl, dout):
     (32, False, False, 0.0), (32, True, False, 0.0),
     (64, False, True, 0.1), (64, True, True, 0.1),
     (96, True, True, 0.25),
+    # the benchmark length, and lengths past one 256-key chunk (chunked
+    # keys with an online rescale; four query groups in dK/dV)
+    (224, False, True, 0.1), (288, True, True, 0.1), (320, False, True, 0.25),
 ])
 def test_triattn_fwd_bwd_parity(cuda, n, per_column, drop, mask_frac):
     print(f"triattn n={n} per_column={per_column} drop={drop} mask={mask_frac}", flush=True)
@@ -64,9 +67,10 @@ def test_triattn_fwd_bwd_parity(cuda, n, per_column, drop, mask_frac):
     assert mg["rel_l2"] < 5e-2
 
 
-def test_triattn_fully_masked_rows(cuda):
+@pytest.mark.parametrize("n", [64, 288])
+def test_triattn_fully_masked_rows(cuda, n):
     """Padding residues: rows with every key masked attend uniformly."""
-    n = 64
+    print(f"triattn fully masked rows n={n}", flush=True)
     prm, wdir, pair, _, dout, _ = _case(n, False, 3, False, 0.0)
     m = np.ones(n, np.float32)
     m[-7:] = 0.0
