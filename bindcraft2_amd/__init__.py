@@ -63,12 +63,18 @@ def _declare(L):
         "bc2n_tplstack_save_bytes": (sz, [cs, i, c.c_int64]),
         "bc2n_tplstack_fwd": (i, [vp, vp, vp, vp, i, i, c.c_int64, c.c_int64, cs, vp, vp]),
         "bc2n_tplstack_bwd": (i, [vp, vp, vp, vp, vp, i, i, c.c_int64, c.c_int64, cs, vp]),
+        "bc2n_fold_save_bytes": (sz, [cs, i, c.c_int64]),
+        "bc2n_fold_fwd": (i, [vp, vp, vp, vp, vp, i, i, c.c_int64, c.c_int64, cs, vp, vp, vp]),
+        "bc2n_fold_bwd": (i, [vp, vp, vp, vp, vp, vp, vp, i, c.c_int64, c.c_int64, cs, vp, vp]),
         "bc2n_dropout_table": (i, [vp, vp, i, i, u32, u32, f]),
         "bc2n_bernoulli_bits": (i, [vp, vp, c.c_long, u32, u32, f]),
         "bc2n_stack_keys": (i, [vp, vp, i, vp]),
         "bc2n_prof_enable": (i, [i]),
         "bc2n_prof_read": (i, [vp, i, vp, vp, i]),
         "bc2n_probe_gemm": (i, [vp, i, i, i, vp, vp, vp]),
+        "bc2n_probe_gemm_f32": (i, [vp, i, i, i, i, vp, c.c_long, c.c_long, c.c_long, vp,
+                                    c.c_long, c.c_long, c.c_long, vp, c.c_long, c.c_long,
+                                    c.c_long]),
         "bc2n_probe_layernorm": (i, [vp, c.c_long, i, vp, vp, vp, i, vp, vp, vp]),
     }
     for name, (res, args) in sigs.items():

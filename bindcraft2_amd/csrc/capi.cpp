@@ -2,6 +2,7 @@
 #include "../../include/bc2n.h"
 #include "evoformer.h"
 #include "gemm.h"
+#include "gemm_f32.h"
 #include "modules.h"
 
 #include <map>
@@ -375,6 +376,63 @@ int bc2n_tplstack_bwd(void* stream, const float* ct, const float* pair_mask, con
   });
 }
 
+// ------------------------------------------------ structure module folding
+
+namespace {
+std::map<std::string, FoldW> g_fold;
+const FoldW& fold_w(const char* dir) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto it = g_fold.find(dir);
+  if (it != g_fold.end()) return it->second;
+  FoldW w = fold_weights(weights(dir));
+  return g_fold.emplace(dir, w).first->second;
+}
+}  // namespace
+
+size_t bc2n_fold_save_bytes(const char* weights_dir, int N, int64_t depth) {
+  size_t n = 0;
+  if (guarded([&] {
+        need(weights_dir != nullptr, "weights_dir required");
+        need(N > 0 && N <= 512 && depth > 0, "fold: bad shape");
+        (void)fold_w(weights_dir);
+        n = fold_save_bytes(N, (int)depth) + 256;
+      }) != 0)
+    return 0;
+  return n;
+}
+
+int bc2n_fold_fwd(void* stream, const float* single, const float* pair, const float* seq_mask,
+                  const uint32_t* seed, int seed_len, int N, int64_t depth, int64_t dropout,
+                  const char* weights_dir, float* act, float* traj, void* save) {
+  return guarded([&] {
+    hipStream_t st = as_stream(stream);
+    need(weights_dir && single && pair && seq_mask && act && traj && save, "null operand");
+    need(N > 0 && N <= 512 && depth > 0, "fold: bad shape");
+    need(seed_len == 2 || seed_len == 3, "fold: seed must be u32[2] or u32[3]");
+    need(!dropout || seed, "fold: dropout needs the seed operand");
+    const FoldW& w = fold_w(weights_dir);
+    const size_t bytes = fold_save_bytes(N, (int)depth) + 256;
+    uint32_t* keyslot = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(save) + bytes - 256);
+    const uint32_t* key = dropout ? stack_key(st, seed, seed_len, keyslot) : nullptr;
+    const uint32_t* enabled = dropout ? seed + (seed_len - 1) : nullptr;
+    fold_fwd(st, w, N, (int)depth, single, pair, seq_mask, key, enabled, dropout != 0, act, traj,
+             save);
+  });
+}
+
+int bc2n_fold_bwd(void* stream, const float* d_act, const float* d_traj, const float* single,
+                  const float* pair, const float* seq_mask, const void* save, int N,
+                  int64_t depth, int64_t dropout, const char* weights_dir, float* dsingle,
+                  float* dpair) {
+  return guarded([&] {
+    need(weights_dir && single && pair && seq_mask && save && dsingle && dpair, "null operand");
+    need(N > 0 && N <= 512 && depth > 0, "fold: bad shape");
+    const FoldW& w = fold_w(weights_dir);
+    fold_bwd(as_stream(stream), w, N, (int)depth, single, pair, seq_mask, dropout != 0, save,
+             d_act, d_traj, dsingle, dpair);
+  });
+}
+
 int bc2n_dropout_table(void* stream, float* tbl, int B, int C, uint32_t k0, uint32_t k1,
                        float rate) {
   return guarded([&] {
@@ -420,6 +478,19 @@ int bc2n_probe_gemm(void* stream, int M, int N, int K, const uint16_t* A, const 
     g.A = reinterpret_cast<const bf16*>(A); g.a_sm = K; g.a_sk = 1;
     g.B = reinterpret_cast<const bf16*>(B); g.b_sn = K; g.b_sk = 1;
     gemm<128, 128>(as_stream(stream), g, EpiStore<float>{C, N, 0, nullptr, N});
+  });
+}
+
+int bc2n_probe_gemm_f32(void* stream, int M, int N, int K, int batch, const float* A,
+                        long a_sm, long a_sk, long a_sb, const float* B, long b_sk, long b_sn,
+                        long b_sb, float* C, long c_sm, long c_sn, long c_sb) {
+  return guarded([&] {
+    GemmF32 g;
+    g.M = M; g.N = N; g.K = K; g.batch = batch;
+    g.A = A; g.a_sm = a_sm; g.a_sk = a_sk; g.a_sb = a_sb;
+    g.B = B; g.b_sk = b_sk; g.b_sn = b_sn; g.b_sb = b_sb;
+    g.C = C; g.c_sm = c_sm; g.c_sn = c_sn; g.c_sb = c_sb;
+    gemm_f32(as_stream(stream), g, "probe.gemm_f32");
   });
 }
 

@@ -1,0 +1,144 @@
+// Batched, strided f32 GEMM on gfx950 MFMA (v_mfma_f32_16x16x4_f32), for the
+// structure module, which AF2 runs in float32 throughout (the point and
+// rigid projections ask for Precision.HIGHEST; a frame is a rotation whose
+// orthogonality bf16 would not keep).  Shapes there are N-sized (N <= 512
+// residues, K <= 2112), so the kernel favours generality: any strides for
+// A, B and C, any M/N/K, and a fused epilogue
+//
+//   C = ((alpha * A B + bias[n]) -> relu? ) * gate? + add? (+ beta * C)
+//
+// where `gate` is an elementwise multiplier in C's layout (a dropout table or
+// a relu-derivative mask: gate > 0 keeps, as `gate_is_mask`), `add` an
+// elementwise addend in C's layout (a residual).
+//
+// Tile 64x64 per workgroup of 256 threads (4 waves, 32x32 each = 2x2 MFMA
+// tiles), K in steps of 16 staged through LDS as [k][m] / [k][n] so a lane's
+// MFMA operand read (row l%16 at k l/16) is one conflict-free LDS word.
+#pragma once
+#include <stdexcept>
+
+#include "common.h"
+#include "runtime.h"
+
+namespace bc2n {
+
+struct GemmF32 {
+  int M = 0, N = 0, K = 0, batch = 1;
+  const float* A = nullptr; long a_sm = 0, a_sk = 0, a_sb = 0;
+  const float* B = nullptr; long b_sk = 0, b_sn = 0, b_sb = 0;
+  float* C = nullptr; long c_sm = 0, c_sn = 0, c_sb = 0;
+  const float* bias = nullptr;  // [N]
+  const float* gate = nullptr;  // C layout
+  const float* add = nullptr;   // C layout
+  float alpha = 1.f, beta = 0.f;
+  bool relu = false, gate_is_mask = false;
+};
+
+namespace gf32 {
+constexpr int BM = 64, BN = 64, BK = 16, LDS_LD = BM + 4;
+}
+
+// internal linkage: the header is included by several translation units
+static __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmF32 g) {
+  using namespace gf32;
+  __shared__ float As[BK][LDS_LD];
+  __shared__ float Bs[BK][LDS_LD];
+  const int tiles_n = (g.N + BN - 1) / BN;
+  const int tiles = ((g.M + BM - 1) / BM) * tiles_n;
+  const long bid = xcd_block((long)tiles * g.batch);
+  if (bid >= (long)tiles * g.batch) return;
+  const int b = (int)(bid / tiles), t = (int)(bid % tiles);
+  const int m0 = (t / tiles_n) * BM, n0 = (t % tiles_n) * BN;
+  const float* A = g.A + (long)b * g.a_sb;
+  const float* B = g.B + (long)b * g.b_sb;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  // load mapping: the unit-stride index runs fastest across threads
+  const bool a_kfast = (g.a_sk == 1), b_nfast = (g.b_sn == 1) || (g.b_sk != 1);
+  f32x4 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int k0 = 0; k0 < g.K; k0 += BK) {
+#pragma unroll
+    for (int i = 0; i < (BM * BK) / 256; ++i) {
+      const int e = tid + 256 * i;
+      int m, k;
+      if (a_kfast) { k = e % BK; m = e / BK; } else { m = e % BM; k = e / BM; }
+      const int gm = m0 + m, gk = k0 + k;
+      As[k][m] = (gm < g.M && gk < g.K) ? A[gm * g.a_sm + gk * g.a_sk] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < (BN * BK) / 256; ++i) {
+      const int e = tid + 256 * i;
+      int n, k;
+      if (b_nfast) { n = e % BN; k = e / BN; } else { k = e % BK; n = e / BK; }
+      const int gn = n0 + n, gk = k0 + k;
+      Bs[k][n] = (gn < g.N && gk < g.K) ? B[gk * g.b_sk + gn * g.b_sn] : 0.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 4) {
+      const int kr = kk + (lane >> 4);
+      float av[2], bv[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) av[i] = As[kr][wm * 32 + i * 16 + (lane & 15)];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bv[j] = Bs[kr][wn * 32 + j * 16 + (lane & 15)];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], bv[j], acc[i][j], 0, 0, 0);
+    }
+    __syncthreads();
+  }
+
+  float* C = g.C + (long)b * g.c_sb;
+  const float* gate = g.gate ? g.gate + (long)b * g.c_sb : nullptr;
+  const float* add = g.add ? g.add + (long)b * g.c_sb : nullptr;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int n = n0 + wn * 32 + j * 16 + (lane & 15);
+      if (n >= g.N) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + r;
+        if (m >= g.M) continue;
+        const long o = (long)m * g.c_sm + (long)n * g.c_sn;
+        float v = g.alpha * acc[i][j][r];
+        if (g.bias) v += g.bias[n];
+        if (g.relu) v = fmaxf(v, 0.f);
+        if (gate) v = g.gate_is_mask ? (gate[o] > 0.f ? v : 0.f) : v * gate[o];
+        if (add) v += add[o];
+        if (g.beta != 0.f) v += g.beta * C[o];
+        C[o] = v;
+      }
+    }
+}
+
+inline void gemm_f32(hipStream_t st, const GemmF32& g, const char* name = "gemm_f32") {
+  if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.batch <= 0) throw std::runtime_error("gemm_f32: empty shape");
+  if (!g.A || !g.B || !g.C) throw std::runtime_error("gemm_f32: missing operand");
+  const long tiles = (long)((g.M + gf32::BM - 1) / gf32::BM) * ((g.N + gf32::BN - 1) / gf32::BN);
+  KTimed kt(name, st);
+  hipLaunchKernelGGL(gemm_f32_kernel, dim3(xcd_grid(tiles * g.batch)), dim3(256), 0, st, g);
+}
+
+// Row-major helpers: C[M,N] = A[M,K] . B[K,N] (or B^T given as [N,K]).
+inline GemmF32 gemm_rows(int M, int N, int K, const float* A, const float* B, float* C,
+                         bool b_transposed = false) {
+  GemmF32 g;
+  g.M = M; g.N = N; g.K = K;
+  g.A = A; g.a_sm = K; g.a_sk = 1;
+  g.B = B;
+  if (b_transposed) { g.b_sk = 1; g.b_sn = K; } else { g.b_sk = N; g.b_sn = 1; }
+  g.C = C; g.c_sm = N; g.c_sn = 1;
+  return g;
+}
+
+}  // namespace bc2n

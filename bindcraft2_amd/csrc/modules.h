@@ -113,4 +113,27 @@ void opm_bwd(hipStream_t st, const OpmW& w, int S, int N, const float* msa, cons
              const float* tbl, const void* save, const float* dpair, const float* dmsa_out,
              float* dmsa_in);
 
+// ------------------------------------------- structure module fold iterations
+// Weights of generate_monomer_rigids + FoldIteration (without the sidechain),
+// all f32 (folding_multimer.py:188-548); the iterations share one set.
+struct FoldW {
+  const float *ln_s_g = nullptr, *ln_s_b = nullptr, *wi = nullptr, *bi = nullptr;
+  const float *ln_z_g = nullptr, *ln_z_b = nullptr;
+  const float *wcat = nullptr, *bcat = nullptr;  // six projections [384][1152]
+  const float *w2d = nullptr, *b2d = nullptr, *wo = nullptr, *bo = nullptr, *pw = nullptr;
+  const float *ln1_g = nullptr, *ln1_b = nullptr, *ln2_g = nullptr, *ln2_b = nullptr;
+  const float *wt[3] = {nullptr, nullptr, nullptr}, *bt[3] = {nullptr, nullptr, nullptr};
+  const float *wq = nullptr, *bq = nullptr;
+};
+FoldW fold_weights(WeightStore& ws);
+size_t fold_save_bytes(int N, int depth);
+// act_out [N][384]; traj [depth][N][3][4] = [R | 20 t] after each iteration
+void fold_fwd(hipStream_t st, const FoldW& w, int N, int depth, const float* single,
+              const float* pair, const float* mask, const uint32_t* key, const uint32_t* enabled,
+              bool dropout, float* act_out, float* traj, void* save);
+// d_act / d_traj may be null (zero cotangent)
+void fold_bwd(hipStream_t st, const FoldW& w, int N, int depth, const float* single,
+              const float* pair, const float* mask, bool dropout, const void* save,
+              const float* d_act, const float* d_traj, float* dsingle, float* dpair);
+
 }  // namespace bc2n

@@ -289,6 +289,44 @@ class TemplatePairStack:
         return dpair
 
 
+class Fold:
+    """The structure module's fold iterations (IPA + transition + rigid
+    update, the part of StructureHeadsFwd/Bwd before the sidechain,
+    native/ffi.cu:1009-1044), f32."""
+
+    def __init__(self, weights_dir, depth=8):
+        self.dir, self.depth = weights_dir.encode(), depth
+
+    def save_bytes(self, n):
+        b = lib().bc2n_fold_save_bytes(self.dir, n, self.depth)
+        if b == 0:
+            check(1)
+        return b
+
+    def forward(self, single, pair, seq_mask, seed=None, dropout=True, save=None):
+        """-> (act [N,384], traj [depth,N,3,4], save)"""
+        n = single.shape[0]
+        act = torch.empty_like(single)
+        traj = torch.empty(self.depth, n, 3, 4, dtype=torch.float32, device=single.device)
+        if save is None:
+            save = torch.empty(self.save_bytes(n), dtype=torch.uint8, device=single.device)
+        seed_len = 3 if seed is None else seed.numel()
+        check(lib().bc2n_fold_fwd(_stream(), _ptr(single), _ptr(pair), _ptr(seq_mask), _ptr(seed),
+                                  seed_len, n, self.depth, int(dropout), self.dir, _ptr(act),
+                                  _ptr(traj), _ptr(save)))
+        return act, traj, save
+
+    def backward(self, d_act, d_traj, single, pair, seq_mask, save, dropout=True):
+        """-> (dsingle, dpair); d_act / d_traj may be None."""
+        n = single.shape[0]
+        dsingle = torch.empty_like(single)
+        dpair = torch.empty_like(pair)
+        check(lib().bc2n_fold_bwd(_stream(), _ptr(d_act), _ptr(d_traj), _ptr(single), _ptr(pair),
+                                  _ptr(seq_mask), _ptr(save), n, self.depth, int(dropout),
+                                  self.dir, _ptr(dsingle), _ptr(dpair)))
+        return dsingle, dpair
+
+
 def dropout_table(rows, channels, key, rate, device="cuda"):
     """[rows, channels] keep/keep_rate table from a JAX key (k0, k1)."""
     tbl = torch.empty(rows, channels, dtype=torch.float32, device=device)
@@ -330,3 +368,10 @@ def probe_layernorm(x, gamma, beta, fast=False):
     check(lib().bc2n_probe_layernorm(_stream(), m, c, _ptr(x), _ptr(gamma), _ptr(beta),
                                      int(fast), _ptr(y), _ptr(mean), _ptr(rstd)))
     return y, mean, rstd
+
+
+def probe_gemm_f32(A, B, C, M, N, K, batch, a_strides, b_strides, c_strides):
+    """C[b,m,n] = sum_k A[.] B[.] with element strides (test hook)."""
+    check(lib().bc2n_probe_gemm_f32(_stream(), M, N, K, batch, _ptr(A), *a_strides, _ptr(B),
+                                    *b_strides, _ptr(C), *c_strides))
+    return C

@@ -136,6 +136,75 @@ def init_block_params(block, rng, modules=None, gates="zero", ln="identity", **s
     return out
 
 
+# AF2 multimer structure module (folding_multimer.py, config.py:578-600):
+# single width 384, 12 heads, 16 scalar / 4 point qk, 16 scalar / 8 point v.
+C_S, IPA_H = 384, 12
+
+
+def fold_shapes(c_s=C_S, c_z=C_Z, h=IPA_H, sqk=16, pqk=4, sv=16, pv=8):
+    """{param: shape} of the post-trunk weights the fold iterations use, in
+    the naming of bindcraft/af/native.py:339-444 (post_weights_from_params):
+    no block index -- the iterations share one set."""
+    ipa = "fold_iteration/invariant_point_attention/"
+    sh = {
+        "single_layer_norm/scale": (c_s,), "single_layer_norm/offset": (c_s,),
+        "initial_projection/weights": (c_s, c_s), "initial_projection/bias": (c_s,),
+        "pair_layer_norm/scale": (c_z,), "pair_layer_norm/offset": (c_z,),
+        ipa + "trainable_point_weights": (h,),
+        ipa + "q_scalar_projection/weights": (c_s, h, sqk), ipa + "q_scalar_projection/bias": (h * sqk,),
+        ipa + "k_scalar_projection/weights": (c_s, h, sqk), ipa + "k_scalar_projection/bias": (h * sqk,),
+        ipa + "v_scalar_projection/weights": (c_s, h, sv), ipa + "v_scalar_projection/bias": (h * sv,),
+        ipa + "q_point_projection/point_projection/weights": (c_s, h, 3 * pqk),
+        ipa + "q_point_projection/point_projection/bias": (h, 3 * pqk),
+        ipa + "k_point_projection/point_projection/weights": (c_s, h, 3 * pqk),
+        ipa + "k_point_projection/point_projection/bias": (h, 3 * pqk),
+        ipa + "v_point_projection/point_projection/weights": (c_s, h, 3 * pv),
+        ipa + "v_point_projection/point_projection/bias": (h, 3 * pv),
+        ipa + "attention_2d/weights": (c_z, h), ipa + "attention_2d/bias": (h,),
+        ipa + "output_projection/weights": (h * sv + 4 * h * pv + h * c_z, c_s),
+        ipa + "output_projection/bias": (c_s,),
+        "fold_iteration/attention_layer_norm/scale": (c_s,),
+        "fold_iteration/attention_layer_norm/offset": (c_s,),
+        "fold_iteration/transition_layer_norm/scale": (c_s,),
+        "fold_iteration/transition_layer_norm/offset": (c_s,),
+        "fold_iteration/quat_rigid/rigid/weights": (c_s, 6),
+        "fold_iteration/quat_rigid/rigid/bias": (6,),
+    }
+    for t in ("transition", "transition_1", "transition_2"):
+        sh[f"fold_iteration/{t}/weights"] = (c_s, c_s)
+        sh[f"fold_iteration/{t}/bias"] = (c_s,)
+    return sh
+
+
+def init_fold_params(rng, final="random", ln="identity"):
+    """Flat {manifest name: array} of the fold iterations.  final='zero' is
+    AF2's zero init of the last layers (output projection, last transition,
+    quat_rigid); 'random' draws them (small) so every path carries signal in
+    tests.  trainable_point_weights start at softplus^-1(1) = log(e - 1)."""
+    out = {}
+    zero_last = ("output_projection", "transition_2/", "quat_rigid")
+    for pname, shape in fold_shapes().items():
+        leaf = pname.split("/")[-1]
+        if leaf == "trainable_point_weights":
+            v = np.full(shape, np.log(np.e - 1.0)) + (0.1 * rng.standard_normal(shape)
+                                                       if final == "random" else 0.0)
+        elif leaf == "scale":
+            v = np.ones(shape) if ln == "identity" else 1.0 + 0.1 * rng.standard_normal(shape)
+        elif leaf == "offset":
+            v = np.zeros(shape) if ln == "identity" else 0.1 * rng.standard_normal(shape)
+        elif leaf == "bias":
+            v = np.zeros(shape) if final == "zero" else 0.1 * rng.standard_normal(shape)
+        else:
+            last = any(z in pname for z in zero_last)
+            if last and final == "zero":
+                v = np.zeros(shape)
+            else:
+                scale = 0.1 if (last and "quat_rigid" in pname) else 1.0
+                v = scale * rng.standard_normal(shape) / np.sqrt(shape[0])
+        out[f"param/{pname}"] = np.asarray(v, np.float32)
+    return out
+
+
 def write_manifest(out_dir, params):
     """Write {name: array} as a weights directory (manifest.txt + .f32)."""
     os.makedirs(out_dir, exist_ok=True)

@@ -188,6 +188,33 @@ int bc2n_tplstack_bwd(void* stream, const float* ct, const float* pair_mask,
                       float* dpair);
 
 /* ------------------------------------------------------------------------
+ * Structure module fold iterations (the IPA step of the post-trunk
+ * StructureHeadsFwd/Bwd handlers, native/ffi.cu:1009-1044, up to and
+ * excluding the sidechain; native/foldit.cuh:141-440, ipa.cuh:507-842,
+ * quatrigid.cuh:172-250).  Replaces:
+ *   fwd(single f32[N,384], pair f32[N,N,128], seq_mask f32[N], seed; depth,
+ *       dropout, weights_dir) -> (act f32[N,384], traj f32[depth,N,3,4], save)
+ *   bwd(d_act, d_traj, single, pair, seq_mask, save; ...) -> (dsingle, dpair)
+ * following folding_multimer.py:476-548 (generate_monomer_rigids without
+ * initial_atom_pos): act = initial_projection(LN(single)), identity frames,
+ * act_2d = LN(pair), then `depth` FoldIterations (:374-474) sharing one set
+ * of weights, iteration i keyed by split(key, depth)[i] (dropout 0.1 with
+ * keys split(k_i, 3)[1], [2]).  traj[i] = [R | 20 t] after iteration i
+ * (StructureModule 'traj', position_scale 20).  All f32.  Weights in the
+ * post-trunk manifest naming of bindcraft/af/native.py:339-444.  N <= 512.
+ * d_act / d_traj may be NULL (zero cotangent).  seed as for the stacks.
+ * ---------------------------------------------------------------------- */
+size_t bc2n_fold_save_bytes(const char* weights_dir, int N, int64_t depth);
+int bc2n_fold_fwd(void* stream, const float* single, const float* pair,
+                  const float* seq_mask, const uint32_t* seed, int seed_len, int N,
+                  int64_t depth, int64_t dropout, const char* weights_dir,
+                  float* act, float* traj, void* save);
+int bc2n_fold_bwd(void* stream, const float* d_act, const float* d_traj,
+                  const float* single, const float* pair, const float* seq_mask,
+                  const void* save, int N, int64_t depth, int64_t dropout,
+                  const char* weights_dir, float* dsingle, float* dpair);
+
+/* ------------------------------------------------------------------------
  * Dropout with JAX's own bits.  tbl[b*C+c] = keep/keep_rate where
  * keep = jax.random.bernoulli(key, keep_rate, (B, C)), keep_rate =
  * float32(1) - float32(rate); key = (k0, k1) = jax.random.key_data(key).
@@ -221,6 +248,11 @@ int bc2n_prof_read(char* names, int name_len, double* ms, int* counts, int cap);
 /* C[M,N] = A[M,K] . B[N,K]^T, bf16 (uint16 bits) in, f32 out. */
 int bc2n_probe_gemm(void* stream, int M, int N, int K, const uint16_t* A,
                     const uint16_t* B, float* C);
+/* Batched f32 GEMM with element strides (the structure module's GEMM):
+ * C[b][m][n] = sum_k A[b*a_sb + m*a_sm + k*a_sk] * B[b*b_sb + k*b_sk + n*b_sn]. */
+int bc2n_probe_gemm_f32(void* stream, int M, int N, int K, int batch, const float* A,
+                        long a_sm, long a_sk, long a_sb, const float* B, long b_sk,
+                        long b_sn, long b_sb, float* C, long c_sm, long c_sn, long c_sb);
 /* y = LN(x) over C channels, bf16 out + mean/rstd. fast = E[x^2]-E[x]^2. */
 int bc2n_probe_layernorm(void* stream, long M, int C, const float* x,
                          const float* gamma, const float* beta, int fast,

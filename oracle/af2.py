@@ -317,3 +317,117 @@ def template_stack(act, pair_mask, params, depth, stack_key, use_dropout, dtype=
             sub = None
         act = template_iteration(act, pair_mask, params, f"param/block{b}/", sub, use_dropout, dtype)
     return act
+
+
+# ------------------------------------------------------------ structure module
+# folding_multimer.py (AF2 multimer structure module), config.py:578-600.
+IPA_HEADS, IPA_SCALAR_QK, IPA_POINT_QK, IPA_SCALAR_V, IPA_POINT_V = 12, 16, 4, 16, 8
+FOLD_DROPOUT = 0.1         # config.py:578
+POSITION_SCALE = 20.0      # config.py:595
+
+
+def _linear_nd(x, p, bias=True):
+    """common_modules.Linear with a multi-dimensional output: weights
+    [C, *out] flattened to [C, prod(out)], output reshaped back."""
+    w = p("weights")
+    out_shape = tuple(w.shape[1:])
+    y = torch.einsum("...c,cd->...d", x, w.reshape(w.shape[0], -1))
+    if bias and (p.prefix + "bias") in p.params:
+        y = y + p("bias").reshape(-1)
+    return y.reshape(*x.shape[:-1], *out_shape)
+
+
+def quat_to_rot(w, x, y, z, eps=1e-6):
+    """geometry/rotation_matrix.py:117-140 (from_quaternion, normalize=True):
+    rows [[xx, xy, xz], [yx, yy, yz], [zx, zy, zz]]."""
+    inv = torch.rsqrt(torch.clamp(w * w + x * x + y * y + z * z, min=eps))
+    w, x, y, z = w * inv, x * inv, y * inv, z * inv
+    r0 = torch.stack([1 - 2 * (y * y + z * z), 2 * (x * y - w * z), 2 * (x * z + w * y)], -1)
+    r1 = torch.stack([2 * (x * y + w * z), 1 - 2 * (x * x + z * z), 2 * (y * z - w * x)], -1)
+    r2 = torch.stack([2 * (x * z - w * y), 2 * (y * z + w * x), 1 - 2 * (x * x + y * y)], -1)
+    return torch.stack([r0, r1, r2], -2)
+
+
+def point_projection(act, p, R, t, num_points):
+    """folding_multimer.py:148-185: Linear(C -> H x 3P) split as
+    [x(P) | y(P) | z(P)] per head, then to the global frame R p + t."""
+    local = _linear_nd(act, p)                              # [N, H, 3P]
+    P_ = num_points
+    loc = torch.stack([local[..., :P_], local[..., P_:2 * P_], local[..., 2 * P_:]], -1)
+    return torch.einsum("nij,nhpj->nhpi", R, loc) + t[:, None, None, :]
+
+
+def invariant_point_attention(act, act_2d, mask, R, t, p, dist_eps=1e-8):
+    """folding_multimer.py:188-371 (InvariantPointAttention)."""
+    n = act.shape[0]
+    raw = p("trainable_point_weights")
+    point_w = math.sqrt(1.0 / (max(IPA_POINT_QK, 1) * 9.0 / 2)) * torch.logaddexp(
+        raw, torch.zeros_like(raw))
+    q_pt = point_projection(act, p.sub("q_point_projection/point_projection/"), R, t, IPA_POINT_QK)
+    k_pt = point_projection(act, p.sub("k_point_projection/point_projection/"), R, t, IPA_POINT_QK)
+    dist2 = ((q_pt[:, None] - k_pt[None]) ** 2).sum(-1)          # [q, k, H, P]
+    logits = -0.5 * (point_w[:, None] * dist2).sum(-1)             # [q, k, H]
+    q_s = _linear_nd(act, p.sub("q_scalar_projection/")) * math.sqrt(1.0 / IPA_SCALAR_QK)
+    k_s = _linear_nd(act, p.sub("k_scalar_projection/"))
+    logits = logits + torch.einsum("qhc,khc->qkh", q_s, k_s)
+    logits = logits + linear(act_2d, p.sub("attention_2d/"))
+    mask_2d = mask[:, None] * mask[None, :]
+    logits = logits - 1e5 * (1.0 - mask_2d[..., None])
+    logits = logits * math.sqrt(1.0 / 3)
+    attn = torch.softmax(logits, dim=-2)
+    v_s = _linear_nd(act, p.sub("v_scalar_projection/"))
+    res_s = torch.einsum("qkh,khc->qhc", attn, v_s)
+    v_pt = point_projection(act, p.sub("v_point_projection/point_projection/"), R, t, IPA_POINT_V)
+    res_g = torch.einsum("qkh,khpi->qhpi", attn, v_pt)
+    res_l = torch.einsum("nji,nhpj->nhpi", R, res_g - t[:, None, None, :])  # R^T (g - t)
+    norms = torch.sqrt(torch.clamp((res_l ** 2).sum(-1), min=dist_eps ** 2))
+    res_2d = torch.einsum("ijh,ijc->ihc", attn, act_2d)
+    final = torch.cat([res_s.reshape(n, -1), res_l[..., 0].reshape(n, -1),
+                       res_l[..., 1].reshape(n, -1), res_l[..., 2].reshape(n, -1),
+                       norms.reshape(n, -1), res_2d.reshape(n, -1)], -1)
+    return linear(final, p.sub("output_projection/"))
+
+
+def fold_iteration(act, R, t, act_2d, mask, p, key, use_dropout):
+    """folding_multimer.py:374-474 (FoldIteration, update_rigid=True) up to
+    the rigid update; the sidechain (MultiRigidSidechain) is not part of it.
+    The rotation carries gradient (the reference's stop_gradient is
+    commented out, :467)."""
+    act = act + invariant_point_attention(act, act_2d, mask, R, t,
+                                          p.sub("invariant_point_attention/"))
+    k1, k2 = jax_prng.split(key, 3)[1:3] if key is not None else (None, None)
+    rate = FOLD_DROPOUT if use_dropout else 0.0
+    act = apply_dropout(act, k1, rate, None)
+    act = layer_norm(act, p("attention_layer_norm/scale"), p("attention_layer_norm/offset"))
+    inp = act
+    act = torch.relu(linear(act, p.sub("transition/")))
+    act = torch.relu(linear(act, p.sub("transition_1/")))
+    act = linear(act, p.sub("transition_2/")) + inp
+    act = apply_dropout(act, k2, rate, None)
+    act = layer_norm(act, p("transition_layer_norm/scale"), p("transition_layer_norm/offset"))
+    flat = linear(act, p.sub("quat_rigid/rigid/"))                 # [N, 6]
+    Ru = quat_to_rot(torch.ones_like(flat[:, 0]), flat[:, 0], flat[:, 1], flat[:, 2])
+    t_new = torch.einsum("nij,nj->ni", R, flat[:, 3:6]) + t
+    return act, R @ Ru, t_new
+
+
+def fold(single, pair, mask, params, depth, key, use_dropout, dtype=torch.float64):
+    """folding_multimer.py:476-548 (generate_monomer_rigids, no initial atom
+    positions): LN + initial projection, identity frames, LN(pair), then
+    `depth` FoldIterations sharing one set of weights with per-layer keys
+    split(key, depth).  Returns the final act and the trajectory
+    [depth, N, 3, 4] = [R | POSITION_SCALE * t] (StructureModule 'traj')."""
+    P = Params(params, "param/", dtype)
+    act = layer_norm(single, P("single_layer_norm/scale"), P("single_layer_norm/offset"))
+    act = linear(act, P.sub("initial_projection/"))
+    act_2d = layer_norm(pair, P("pair_layer_norm/scale"), P("pair_layer_norm/offset"))
+    n = single.shape[0]
+    R = torch.eye(3, dtype=single.dtype).expand(n, 3, 3)
+    t = torch.zeros(n, 3, dtype=single.dtype)
+    keys = jax_prng.split(key, depth) if key is not None else [None] * depth
+    traj = []
+    fp = P.sub("fold_iteration/")
+    for i in range(depth):
+        act, R, t = fold_iteration(act, R, t, act_2d, mask, fp, keys[i], use_dropout)
+        traj.append(torch.cat([R, (POSITION_SCALE * t)[..., None]], -1))
+    return act, torch.stack(traj)

@@ -209,3 +209,76 @@ def test_evoformer_block_runs_and_is_identity_for_zero_outputs():
                                      prm, "param/block0/", None, False)
     torch.testing.assert_close(m2, msa)
     torch.testing.assert_close(p2, pair)
+
+
+# ------------------------------------------------------- structure module oracle
+def _fold_params(seed=0):
+    return bparams.init_fold_params(np.random.default_rng(seed), final="random", ln="random")
+
+
+def test_quat_to_rot_is_a_rotation_and_matches_scipy():
+    """rotation_matrix.py:117-140 against scipy's quaternion convention
+    (scalar last) and orthonormality / det +1."""
+    from scipy.spatial.transform import Rotation
+    rng = np.random.default_rng(3)
+    q = rng.standard_normal((20, 4))
+    R = af2.quat_to_rot(*[torch.tensor(q[:, i]) for i in range(4)]).numpy()
+    ref = Rotation.from_quat(q[:, [1, 2, 3, 0]]).as_matrix()
+    assert np.abs(R - ref).max() < 1e-12
+    assert np.abs(R @ R.transpose(0, 2, 1) - np.eye(3)).max() < 1e-12
+    assert np.abs(np.linalg.det(R) - 1).max() < 1e-12
+
+
+def test_ipa_invariant_under_global_rigid_motion():
+    """IPA's defining property: moving every frame by one global rigid
+    transform (R -> G R, t -> G t + g) leaves the output unchanged.  A
+    transposed rotation in the point projection or the local readout breaks
+    it."""
+    prm = _fold_params(1)
+    p = af2.Params(prm, "param/fold_iteration/invariant_point_attention/")
+    rng = np.random.default_rng(4)
+    n = 12
+    act = torch.tensor(rng.standard_normal((n, 384)))
+    a2d = torch.tensor(rng.standard_normal((n, n, 128)))
+    mask = torch.ones(n, dtype=torch.float64)
+    mask[3] = 0
+    q = torch.tensor(rng.standard_normal((n, 4)))
+    R = af2.quat_to_rot(q[:, 0], q[:, 1], q[:, 2], q[:, 3])
+    t = torch.tensor(rng.standard_normal((n, 3)))
+    o1 = af2.invariant_point_attention(act, a2d, mask, R, t, p)
+    G = af2.quat_to_rot(*torch.tensor(rng.standard_normal(4)))
+    g = torch.tensor(rng.standard_normal(3))
+    o2 = af2.invariant_point_attention(act, a2d, mask, G @ R, t @ G.T + g, p)
+    assert (o1 - o2).abs().max() < 1e-10 * o1.abs().max()
+    # and it is not trivially constant in the frames: move one residue
+    t3 = t.clone()
+    t3[0] += 1.0
+    o3 = af2.invariant_point_attention(act, a2d, mask, R, t3, p)
+    assert (o1 - o3).abs().max() > 1e-3
+
+
+def test_fold_grad_finite_differences():
+    """fp64 autograd of the fold (frames carried across 2 iterations, no
+    stop_gradient) against central differences on single and pair."""
+    prm = _fold_params(2)
+    rng = np.random.default_rng(5)
+    n = 4
+    s = torch.tensor(rng.standard_normal((n, 384)), requires_grad=True)
+    z = torch.tensor(rng.standard_normal((n, n, 128)), requires_grad=True)
+    m = torch.ones(n, dtype=torch.float64)
+    w_act = torch.tensor(rng.standard_normal((n, 384)))
+    w_traj = torch.tensor(rng.standard_normal((2, n, 3, 4)))
+
+    def f(s_, z_):
+        act, traj = af2.fold(s_, z_, m, prm, 2, None, False)
+        return (act * w_act).sum() + (traj * w_traj).sum()
+
+    gs, gz = torch.autograd.grad(f(s, z), (s, z))
+    eps = 1e-6
+    for (x, gx, idx) in ((s, gs, (1, 7)), (s, gs, (3, 300)), (z, gz, (0, 2, 5)), (z, gz, (3, 1, 100))):
+        xp = x.detach().clone(); xp[idx] += eps
+        xm = x.detach().clone(); xm[idx] -= eps
+        fp = f(xp, z.detach()) if x is s else f(s.detach(), xp)
+        fm = f(xm, z.detach()) if x is s else f(s.detach(), xm)
+        fd = ((fp - fm) / (2 * eps)).item()
+        assert abs(fd - gx[idx].item()) <= 1e-5 * max(1.0, abs(fd)), (idx, fd, gx[idx].item())
