@@ -55,6 +55,9 @@ def _declare(L):
         "bc2n_msacol_save_bytes": (sz, [i, i, i, i]),
         "bc2n_msacol_fwd": (i, [vp, cs, cs, i, i, vp, vp, vp, vp, vp]),
         "bc2n_msacol_bwd": (i, [vp, cs, cs, i, i, vp, vp, vp, vp, vp, vp]),
+        "bc2n_msaglobal_save_bytes": (sz, [cs, cs, i, i]),
+        "bc2n_msaglobal_fwd": (i, [vp, cs, cs, i, i, vp, vp, vp, vp, vp]),
+        "bc2n_msaglobal_bwd": (i, [vp, cs, cs, i, i, vp, vp, vp, vp, vp, vp]),
         "bc2n_evoformer_save_bytes": (sz, [cs, i, i, c.c_int64, c.c_int64]),
         "bc2n_evoformer_fwd": (i, [vp, vp, vp, vp, vp, vp, i, i, i, i, c.c_int64, c.c_int64,
                                    c.c_int64, c.c_int64, c.c_int64, c.c_int64, cs, vp, vp, vp, vp]),

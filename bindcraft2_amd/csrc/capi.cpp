@@ -248,6 +248,40 @@ int bc2n_msacol_fwd(void* stream, const char* weights_dir, const char* prefix, i
   });
 }
 
+std::map<std::pair<std::string, std::string>, MsaGlobW> g_glob;
+
+size_t bc2n_msaglobal_save_bytes(const char* weights_dir, const char* prefix, int S, int N) {
+  size_t n = 0;
+  if (guarded([&] {
+        need(weights_dir && prefix && S > 0 && N > 0, "bad arguments");
+        const MsaGlobW& w = cached(g_glob, weights_dir, prefix, msaglobal_weights);
+        n = msaglobal_save_bytes(w, S, N);
+      }) != 0)
+    return 0;
+  return n;
+}
+
+int bc2n_msaglobal_fwd(void* stream, const char* weights_dir, const char* prefix, int S, int N,
+                       const float* msa, const float* msa_mask, const float* drop_tbl,
+                       float* msa_out, void* save) {
+  return guarded([&] {
+    need(weights_dir && prefix && msa && msa_mask && msa_out && save, "null operand");
+    need(msa_out != msa, "msaglobal: msa_out must not alias msa");
+    const MsaGlobW& w = cached(g_glob, weights_dir, prefix, msaglobal_weights);
+    msaglobal_fwd(as_stream(stream), w, S, N, msa, msa_mask, drop_tbl, msa_out, save);
+  });
+}
+
+int bc2n_msaglobal_bwd(void* stream, const char* weights_dir, const char* prefix, int S, int N,
+                       const float* msa, const float* msa_mask, const float* drop_tbl,
+                       const void* save, const float* dmsa_out, float* dmsa_in) {
+  return guarded([&] {
+    need(weights_dir && prefix && msa && msa_mask && save && dmsa_out && dmsa_in, "null operand");
+    const MsaGlobW& w = cached(g_glob, weights_dir, prefix, msaglobal_weights);
+    msaglobal_bwd(as_stream(stream), w, S, N, msa, msa_mask, drop_tbl, save, dmsa_out, dmsa_in);
+  });
+}
+
 int bc2n_msacol_bwd(void* stream, const char* weights_dir, const char* prefix, int S, int N,
                     const float* msa, const float* msa_mask, const float* drop_tbl,
                     const void* save, const float* dmsa_out, float* dmsa_in) {

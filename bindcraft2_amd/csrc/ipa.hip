@@ -51,62 +51,6 @@ constexpr int MAXN = 512;
 
 static_assert(PROJ == 1152 && FIN == 2112, "IPA widths");
 
-// -------------------------------------------------------------- LayerNorm
-// f32 in, f32 out, one wave per row (two-pass variance).
-__global__ void ln_rows_fwd_kernel(const float* __restrict__ x, long M, int C,
-                                   const float* __restrict__ g, const float* __restrict__ b,
-                                   float* __restrict__ y, float* __restrict__ mean,
-                                   float* __restrict__ rstd) {
-  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (row >= M) return;
-  const float* xr = x + row * C;
-  float s = 0.f;
-  for (int c = lane; c < C; c += 64) s += xr[c];
-  s = group_sum<64>(s);
-  const float mu = s / C;
-  float v = 0.f;
-  for (int c = lane; c < C; c += 64) { const float d = xr[c] - mu; v += d * d; }
-  v = group_sum<64>(v);
-  const float r = rsqrtf(v / C + LN_EPS);
-  for (int c = lane; c < C; c += 64) y[row * C + c] = (xr[c] - mu) * r * g[c] + b[c];
-  if (lane == 0) { mean[row] = mu; rstd[row] = r; }
-}
-
-// dx = r * (g*dy - mean(g*dy) - xhat * mean(g*dy*xhat)); dx may alias dy.
-__global__ void ln_rows_bwd_kernel(const float* dy, const float* __restrict__ x,
-                                   long M, int C, const float* __restrict__ g,
-                                   const float* __restrict__ mean, const float* __restrict__ rstd,
-                                   float* dx) {
-  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (row >= M) return;
-  const float mu = mean[row], r = rstd[row];
-  float s1 = 0.f, s2 = 0.f;
-  for (int c = lane; c < C; c += 64) {
-    const float gd = g[c] * dy[row * C + c];
-    s1 += gd;
-    s2 += gd * (x[row * C + c] - mu) * r;
-  }
-  s1 = group_sum<64>(s1) / C;
-  s2 = group_sum<64>(s2) / C;
-  for (int c = lane; c < C; c += 64) {
-    const float xh = (x[row * C + c] - mu) * r;
-    dx[row * C + c] = r * (g[c] * dy[row * C + c] - s1 - xh * s2);
-  }
-}
-
-void ln_rows_fwd(hipStream_t st, const float* x, long M, int C, const float* g, const float* b,
-                 float* y, float* mean, float* rstd) {
-  hipLaunchKernelGGL(ln_rows_fwd_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, st, x, M, C,
-                     g, b, y, mean, rstd);
-}
-void ln_rows_bwd(hipStream_t st, const float* dy, const float* x, long M, int C, const float* g,
-                 const float* mean, const float* rstd, float* dx) {
-  hipLaunchKernelGGL(ln_rows_bwd_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, st, dy, x, M,
-                     C, g, mean, rstd, dx);
-}
-
 // ---------------------------------------------------------- small helpers
 __device__ __forceinline__ void rot_apply(const float* R, const float* p, float* o) {
 #pragma unroll
@@ -780,11 +724,11 @@ void fold_fwd(hipStream_t st, const FoldW& w, int N, int depth, const float* sin
   }
   {
     KTimed kt("fold.prologue", st);
-    ln_rows_fwd(st, single, N, CS, w.ln_s_g, w.ln_s_b, a0, sv.sm, sv.sr);
+    ln_f32_rows_fwd(st, single, N, CS, w.ln_s_g, w.ln_s_b, a0, sv.sm, sv.sr);
     GemmF32 g = gemm_rows(N, CS, CS, a0, w.wi, act);
     g.bias = w.bi;
     gemm_f32(st, g, "fold.gemm_init");
-    ln_rows_fwd(st, pair, M2, CZ, w.ln_z_g, w.ln_z_b, sv.act2d, sv.zm, sv.zr);
+    ln_f32_rows_fwd(st, pair, M2, CZ, w.ln_z_g, w.ln_z_b, sv.act2d, sv.zm, sv.zr);
     // b2d[h][m] = act2d[m] . w2d[:, h] + b[h]
     GemmF32 b = gemm_rows((int)M2, H, CZ, sv.act2d, w.w2d, sv.b2d);
     b.c_sm = 1; b.c_sn = M2;
@@ -828,7 +772,7 @@ void fold_fwd(hipStream_t st, const FoldW& w, int N, int depth, const float* sin
     {
       KTimed kt("fold.transition", st);
       add_scale(st, act, ipo, tb1, (long)N * CS, s.x1);
-      ln_rows_fwd(st, s.x1, N, CS, w.ln1_g, w.ln1_b, a2, s.m1, s.r1);
+      ln_f32_rows_fwd(st, s.x1, N, CS, w.ln1_g, w.ln1_b, a2, s.m1, s.r1);
       GemmF32 g1 = gemm_rows(N, CS, CS, a2, w.wt[0], s.t1);
       g1.bias = w.bt[0]; g1.relu = true;
       gemm_f32(st, g1, "fold.gemm_t1");
@@ -840,7 +784,7 @@ void fold_fwd(hipStream_t st, const FoldW& w, int N, int depth, const float* sin
       g3.bias = w.bt[2]; g3.add = a2;
       gemm_f32(st, g3, "fold.gemm_t3");
       scale(st, s.x3, tb2, (long)N * CS, s.x3);
-      ln_rows_fwd(st, s.x3, N, CS, w.ln2_g, w.ln2_b, a4, s.m3, s.r3);
+      ln_f32_rows_fwd(st, s.x3, N, CS, w.ln2_g, w.ln2_b, a4, s.m3, s.r3);
       GemmF32 gq = gemm_rows(N, 6, CS, a4, w.wq, s.flat);
       gq.bias = w.bq;
       gemm_f32(st, gq, "fold.gemm_quat");
@@ -916,7 +860,7 @@ void fold_bwd(hipStream_t st, const FoldW& w, int N, int depth, const float* sin
       GemmF32 gq = gemm_rows(N, CS, 6, dflat, w.wq, da, true);
       gq.beta = 1.f;
       gemm_f32(st, gq, "fold.gemm_quat_dx");
-      ln_rows_bwd(st, da, s.x3, N, CS, w.ln2_g, s.m3, s.r3, dx);  // dx3
+      ln_f32_rows_bwd(st, da, s.x3, N, CS, w.ln2_g, s.m3, s.r3, dx);  // dx3
       scale(st, dx, tb2, (long)N * CS, dx);                       // da3
       // dt2 = (da3 W3^T) * [t2 > 0]
       GemmF32 g3 = gemm_rows(N, CS, CS, dx, w.wt[2], dt2, true);
@@ -929,7 +873,7 @@ void fold_bwd(hipStream_t st, const FoldW& w, int N, int depth, const float* sin
       GemmF32 g1 = gemm_rows(N, CS, CS, dt1, w.wt[0], da2, true);
       g1.add = dx;
       gemm_f32(st, g1, "fold.gemm_t1_dx");
-      ln_rows_bwd(st, da2, s.x1, N, CS, w.ln1_g, s.m1, s.r1, dx);  // dx1
+      ln_f32_rows_bwd(st, da2, s.x1, N, CS, w.ln1_g, s.m1, s.r1, dx);  // dx1
       scale(st, dx, tb1, (long)N * CS, dx);                       // da1 = d act_in (residual) = d ipa
     }
     {
@@ -972,10 +916,10 @@ void fold_bwd(hipStream_t st, const FoldW& w, int N, int depth, const float* sin
     // act = Linear(LN(single)):  d LN(single) = da Wi^T
     GemmF32 g = gemm_rows(N, CS, CS, da, w.wi, dx, true);
     gemm_f32(st, g, "fold.gemm_init_dx");
-    ln_rows_bwd(st, dx, single, N, CS, w.ln_s_g, sv.sm, sv.sr, dsingle);
+    ln_f32_rows_bwd(st, dx, single, N, CS, w.ln_s_g, sv.sm, sv.sr, dsingle);
     hipLaunchKernelGGL(b2d_bwd_kernel, dim3((unsigned)((M2 * CZ + 255) / 256)), dim3(256), 0, st,
                        db2d, w.w2d, M2, dpair);
-    ln_rows_bwd(st, dpair, pair, M2, CZ, w.ln_z_g, sv.zm, sv.zr, dpair);
+    ln_f32_rows_bwd(st, dpair, pair, M2, CZ, w.ln_z_g, sv.zm, sv.zr, dpair);
   }
 }
 

@@ -58,6 +58,12 @@ void attn_bwd(hipStream_t st, const AttnBwdArgs& a);
 int attn_bwd_nchunk(int R, int rows_per_chunk);
 int attn_rows_per_chunk(int N);
 
+// f32 LayerNorm over rows of any width (one wave per row); dx may alias dy.
+void ln_f32_rows_fwd(hipStream_t st, const float* x, long M, int C, const float* g,
+                     const float* b, float* y, float* mean, float* rstd);
+void ln_f32_rows_bwd(hipStream_t st, const float* dy, const float* x, long M, int C,
+                     const float* g, const float* mean, const float* rstd, float* dx);
+
 // ---------------------------------------------------------------- dropout
 // Shared-dropout keep/scale table for one module: tbl[b*C+c] = keep/keep_rate
 // (0 where dropped), with keep = jax.random.uniform(key,(B,C)) < keep_rate.

@@ -435,4 +435,61 @@ void ln_bwd_cm(hipStream_t st, const float* dy, const float* x, long M, int C,
   else throw std::runtime_error("ln_bwd_cm: unsupported channel count");
 }
 
+// ------------------------------------------------- f32 rows, any width
+// f32 in, f32 out, one wave per row (two-pass variance): the structure
+// module and the small MSA modules, where rows are few or short.
+__global__ void ln_f32_rows_fwd_kernel(const float* __restrict__ x, long M, int C,
+                                   const float* __restrict__ g, const float* __restrict__ b,
+                                   float* __restrict__ y, float* __restrict__ mean,
+                                   float* __restrict__ rstd) {
+  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= M) return;
+  const float* xr = x + row * C;
+  float s = 0.f;
+  for (int c = lane; c < C; c += 64) s += xr[c];
+  s = group_sum<64>(s);
+  const float mu = s / C;
+  float v = 0.f;
+  for (int c = lane; c < C; c += 64) { const float d = xr[c] - mu; v += d * d; }
+  v = group_sum<64>(v);
+  const float r = rsqrtf(v / C + LN_EPS);
+  for (int c = lane; c < C; c += 64) y[row * C + c] = (xr[c] - mu) * r * g[c] + b[c];
+  if (lane == 0) { mean[row] = mu; rstd[row] = r; }
+}
+
+// dx = r * (g*dy - mean(g*dy) - xhat * mean(g*dy*xhat)); dx may alias dy.
+__global__ void ln_f32_rows_bwd_kernel(const float* dy, const float* __restrict__ x,
+                                   long M, int C, const float* __restrict__ g,
+                                   const float* __restrict__ mean, const float* __restrict__ rstd,
+                                   float* dx) {
+  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= M) return;
+  const float mu = mean[row], r = rstd[row];
+  float s1 = 0.f, s2 = 0.f;
+  for (int c = lane; c < C; c += 64) {
+    const float gd = g[c] * dy[row * C + c];
+    s1 += gd;
+    s2 += gd * (x[row * C + c] - mu) * r;
+  }
+  s1 = group_sum<64>(s1) / C;
+  s2 = group_sum<64>(s2) / C;
+  for (int c = lane; c < C; c += 64) {
+    const float xh = (x[row * C + c] - mu) * r;
+    dx[row * C + c] = r * (g[c] * dy[row * C + c] - s1 - xh * s2);
+  }
+}
+
+void ln_f32_rows_fwd(hipStream_t st, const float* x, long M, int C, const float* g, const float* b,
+                 float* y, float* mean, float* rstd) {
+  hipLaunchKernelGGL(ln_f32_rows_fwd_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, st, x, M, C,
+                     g, b, y, mean, rstd);
+}
+void ln_f32_rows_bwd(hipStream_t st, const float* dy, const float* x, long M, int C, const float* g,
+                 const float* mean, const float* rstd, float* dx) {
+  hipLaunchKernelGGL(ln_f32_rows_bwd_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, st, dy, x, M,
+                     C, g, mean, rstd, dx);
+}
+
 }  // namespace bc2n

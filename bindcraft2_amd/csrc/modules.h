@@ -98,6 +98,20 @@ void msacol_bwd(hipStream_t st, const MsaColW& w, int S, int N, const float* msa
                 const float* msa_mask, const float* tbl, const void* save,
                 const float* dmsa_out, float* dmsa_in);
 
+// ---------------------------------------------- MSA column global attention
+struct MsaGlobW {
+  int C = 0, H = 0, DK = 0, DV = 0;
+  const float *ln_g = nullptr, *ln_b = nullptr, *wq = nullptr, *wcat = nullptr, *bcat = nullptr;
+  const float *wo = nullptr, *bo = nullptr;
+};
+MsaGlobW msaglobal_weights(WeightStore& ws, const std::string& prefix);
+size_t msaglobal_save_bytes(const MsaGlobW& w, int S, int N);
+void msaglobal_fwd(hipStream_t st, const MsaGlobW& w, int S, int N, const float* msa_in,
+                   const float* msa_mask, const float* tbl, float* msa_out, void* save);
+void msaglobal_bwd(hipStream_t st, const MsaGlobW& w, int S, int N, const float* msa_in,
+                   const float* msa_mask, const float* tbl, const void* save,
+                   const float* dmsa_out, float* dmsa_in);
+
 // --------------------------------------------------------- outer product mean
 struct OpmW {
   int Cm = 0, O = 0, C = 0;

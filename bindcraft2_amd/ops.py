@@ -181,6 +181,32 @@ class MSARowAttentionWithPairBias:
         return din, dpair
 
 
+class MSAColumnGlobalAttention:
+    """The extra-MSA stack's column module (modules.py:619-672), f32."""
+
+    def __init__(self, weights_dir, prefix):
+        self.dir, self.prefix = weights_dir.encode(), prefix.encode()
+
+    def forward(self, msa, msa_mask, drop_tbl=None):
+        s, n, _ = msa.shape
+        out = torch.empty_like(msa)
+        nb = lib().bc2n_msaglobal_save_bytes(self.dir, self.prefix, s, n)
+        if nb == 0:
+            check(1)
+        save = torch.empty(nb, dtype=torch.uint8, device=msa.device)
+        check(lib().bc2n_msaglobal_fwd(_stream(), self.dir, self.prefix, s, n, _ptr(msa),
+                                       _ptr(msa_mask), _ptr(drop_tbl), _ptr(out), _ptr(save)))
+        return out, save
+
+    def backward(self, msa, msa_mask, drop_tbl, save, dout):
+        s, n, _ = msa.shape
+        din = torch.empty_like(dout)
+        check(lib().bc2n_msaglobal_bwd(_stream(), self.dir, self.prefix, s, n, _ptr(msa),
+                                       _ptr(msa_mask), _ptr(drop_tbl), _ptr(save), _ptr(dout),
+                                       _ptr(din)))
+        return din
+
+
 class MSAColumnAttention:
     def __init__(self, weights_dir, prefix, c_m=256, heads=8):
         self.dir, self.prefix, self.cm, self.h = weights_dir.encode(), prefix.encode(), c_m, heads

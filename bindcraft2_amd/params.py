@@ -124,6 +124,17 @@ def init_template_block_params(block, rng, gates="zero", ln="identity"):
     return out
 
 
+def global_attention_shapes(c=C_E, heads=8):
+    """MSAColumnGlobalAttention of the extra-MSA stack (modules.py:403-497,
+    619-672; config.py extra_msa: 8 heads, key/value dim c)."""
+    d = c // heads
+    return {"query_norm/scale": (c,), "query_norm/offset": (c,),
+            "attention/query_w": (c, heads, d), "attention/key_w": (c, d),
+            "attention/value_w": (c, d), "attention/gating_w": (c, heads, d),
+            "attention/gating_b": (heads, d), "attention/output_w": (heads, d, c),
+            "attention/output_b": (c,)}
+
+
 def init_block_params(block, rng, modules=None, gates="zero", ln="identity", **shape_kw):
     """Flat {manifest name: array} for one Evoformer block."""
     sh = module_shapes(**shape_kw)

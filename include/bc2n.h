@@ -127,6 +127,21 @@ int bc2n_msacol_bwd(void* stream, const char* weights_dir, const char* prefix,
                     const float* drop_tbl, const void* save,
                     const float* dmsa_out, float* dmsa_in);
 
+/* MSA column global attention, f32 (the extra-MSA stack's column module;
+ * modules.py:619-672 over GlobalAttention :403-497).  The reference runs it
+ * in JAX only: its native extra stack is the pair-only specialisation
+ * (native/block.cuh:79-91), so this has no native counterpart.  Widths from
+ * the weights (attention/query_w [C, H, DK], value_w [C, DV]).  The save-set
+ * size depends on the weights, hence weights_dir / prefix. */
+size_t bc2n_msaglobal_save_bytes(const char* weights_dir, const char* prefix, int S, int N);
+int bc2n_msaglobal_fwd(void* stream, const char* weights_dir, const char* prefix,
+                       int S, int N, const float* msa, const float* msa_mask,
+                       const float* drop_tbl, float* msa_out, void* save);
+int bc2n_msaglobal_bwd(void* stream, const char* weights_dir, const char* prefix,
+                       int S, int N, const float* msa, const float* msa_mask,
+                       const float* drop_tbl, const void* save,
+                       const float* dmsa_out, float* dmsa_in);
+
 /* ------------------------------------------------------------------------
  * The Evoformer stack: the drop-in for the reference's XLA FFI pair
  * NativeEvoformerFwd / NativeEvoformerBwd (native/ffi.cu:942-982, impl

@@ -112,3 +112,31 @@ def test_msa_column_attention(cuda, s, n):
     (g,) = torch.autograd.grad(ref, x, torch.as_tensor(dout, dtype=D))
     print(assert_act((out - tm).cpu().double(), ref.detach(), what="delta"),
           assert_grad((din - td).cpu().double(), g, what="dmsa"))
+
+
+@pytest.mark.parametrize("s,n,mfrac", [(1, 32, 0.0), (5, 64, 0.2), (40, 32, 0.3)])
+def test_msa_column_global_attention(cuda, s, n, mfrac):
+    """The extra-MSA column module (modules.py:619-672), f32 end to end,
+    with some fully masked columns."""
+    print(f"msa global s={s} n={n} mask={mfrac}", flush=True)
+    rng = np.random.default_rng(s * 31 + n)
+    name = "msa_column_global_attention"
+    prm = {f"param/block0/{name}/{k}": v for k, v in
+           bparams.init_module(bparams.global_attention_shapes(), rng, gates="random",
+                               ln="random").items()}
+    wdir = weights_dir(prm, f"glob_{s}_{n}")
+    msa = rng.standard_normal((s, n, 64)).astype(np.float32)
+    mask = (rng.random((s, n)) > mfrac).astype(np.float32)
+    mask[:, 3] = 0.0  # a fully masked column attends uniformly
+    dout = rng.standard_normal((s, n, 64)).astype(np.float32)
+    mod = ops.MSAColumnGlobalAttention(wdir, f"param/block0/{name}/")
+    tm, tk, td = _t(msa, cuda), _t(mask, cuda), _t(dout, cuda)
+    out, save = mod.forward(tm, tk)
+    din = mod.backward(tm, tk, None, save, td)
+    P = af2.Params(prm, f"param/block0/{name}/")
+    x = torch.tensor(msa, dtype=D, requires_grad=True)
+    ref = af2.msa_column_global_attention(x, torch.as_tensor(mask, dtype=D), P)
+    (g,) = torch.autograd.grad(ref, x, torch.as_tensor(dout, dtype=D))
+    ma = assert_act((out - tm).cpu().double(), ref.detach(), tol=1e-4, what="delta")
+    mg = assert_grad((din - td).cpu().double(), g, cos=0.99999, what="dmsa")
+    print(ma, mg)
