@@ -174,15 +174,92 @@ def cpu_triattn_baseline(n, seconds=12.0):
 
 
 # ------------------------------------------------------------------- roofline
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "traffic_trunk_L224.json")
+
+
+def traffic_of(kernel, n):
+    """HBM bytes per launch of `kernel` (per-launch kernel name as the event
+    timer records it) from the committed counter summary of the trunk step
+    (rocprofv3 FETCH_SIZE / WRITE_SIZE, scaled by a plain copy's reading);
+    None if there is no summary for this length."""
+    if not os.path.exists(TRAFFIC_SUMMARY):
+        return None
+    with open(TRAFFIC_SUMMARY) as fh:
+        summ = json.load(fh)
+    if summ.get("L") != n:
+        return None
+    # the triangle-attention launches are the head-width-32 instantiation
+    k = summ["kernels"].get(f"{kernel}<32, {n // 32}>") or summ["kernels"].get(kernel)
+    return None if k is None else int(k["fetch_bytes"] + k["write_bytes"])
+
+
 def roofline_from(prof, n):
     cand = {k: v for k, v in prof.items() if kernel_work(k, n) is not None}
+    if not cand:
+        return None
     dom = max(cand, key=lambda k: cand[k][0])
     tot, cnt = cand[dom]
     achieved = kernel_work(dom, n) / (tot / cnt * 1e-3) / 1e12
     return {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2),
             "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic_of(dom, n),
             "launch_us": round(tot / cnt * 1e3, 2)}
+
+
+def _short_kernel_name(sym):
+    """'void bc2n::attn_bwd_dkv_kernel<32, 7>(bc2n::AttnBwdArgs)' ->
+    'attn_bwd_dkv<32, 7>' (the event timer's name plus the template
+    arguments, which tell head widths and lengths apart)."""
+    s = sym.replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
+    base, _, targs = s.partition("<")
+    base = base.split("::")[-1]
+    base = base[:-len("_kernel")] if base.endswith("_kernel") else base
+    if targs and len(targs) < 24:
+        return f"{base}<{targs}"
+    return base
+
+
+def pmc_summarize(fetch_csv, write_csv, copy_fetch_csv, copy_write_csv, n, out):
+    """Per-kernel HBM bytes per launch from two rocprofv3 --pmc runs of the
+    trunk step (FETCH_SIZE, WRITE_SIZE in KiB per dispatch) and the same two
+    counters over a device copy of a known size (bench.py --workload copy),
+    whose reading fixes each counter's scale."""
+    import csv
+    import collections
+
+    def per_kernel(path):
+        # one entry per kernel name: its largest launch shape (grid size),
+        # e.g. the triangle-attention launches of a kernel MSA attention
+        # also uses with a smaller grid
+        d = collections.defaultdict(lambda: collections.defaultdict(lambda: [0.0, 0, 0]))
+        for r in csv.DictReader(open(path)):
+            k = _short_kernel_name(r["Kernel_Name"])
+            e = d[k][int(r["Grid_Size"])]
+            e[0] += float(r["Counter_Value"]) * 1024.0
+            e[1] += 1
+            e[2] += int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+        return {k: v[max(v)] + [max(v)] for k, v in d.items()}
+
+    def copy_scale(path):
+        big = [float(r["Counter_Value"]) * 1024.0 for r in csv.DictReader(open(path))
+               if "copyBuffer" in r["Kernel_Name"]]
+        return (256 << 20) / max(big)  # the copy moves 256 MiB each way
+
+    fs, ws = copy_scale(copy_fetch_csv), copy_scale(copy_write_csv)
+    f, w = per_kernel(fetch_csv), per_kernel(write_csv)
+    kern = {}
+    for k in f:
+        if k not in w:
+            continue
+        calls = f[k][1]
+        kern[k] = {"calls": calls, "grid": f[k][3], "fetch_bytes": round(f[k][0] / calls * fs),
+                   "write_bytes": round(w[k][0] / w[k][1] * ws),
+                   "us_under_counters": round((f[k][2] + w[k][2]) / (calls + w[k][1]) / 1e3, 2)}
+    summ = {"L": n, "copy_scale": {"FETCH_SIZE": round(fs, 4), "WRITE_SIZE": round(ws, 4)},
+            "kernels": dict(sorted(kern.items(), key=lambda kv: -kv[1]["fetch_bytes"]))}
+    with open(out, "w") as fh:
+        json.dump(summ, fh, indent=1)
+    return summ
 
 
 def kernel_table(prof):
@@ -190,16 +267,44 @@ def kernel_table(prof):
             for k, (t, c) in sorted(prof.items(), key=lambda kv: -kv[1][0])}
 
 
+PROGRESS = False  # --progress: a line on stderr per finished step
+
+
+def _progress(what):
+    if PROGRESS:
+        import torch
+        torch.cuda.synchronize()
+        print(f"bench: {what} done", file=sys.stderr, flush=True)
+
+
+def profiled(step, steps, skip):
+    """A second pass of `steps` steps with the per-kernel event timer on:
+    {name: (total ms, launches)}; {} when skipped (--no-kprof)."""
+    if skip:
+        return {}
+    import bindcraft2_amd as b
+    b.prof_enable(True)
+    for i in range(steps):
+        step()
+        _progress(f"profiled step {i}")
+    prof = b.prof_read()
+    b.prof_enable(False)
+    return prof
+
+
 def timed(step, steps, warmup):
     import torch
-    for _ in range(warmup):
+    for i in range(warmup):
         step()
+        _progress(f"warmup step {i}")
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
         step()
     torch.cuda.synchronize()
-    return (time.perf_counter() - t0) / steps * 1e3
+    ms = (time.perf_counter() - t0) / steps * 1e3
+    _progress(f"{steps} timed steps")
+    return ms
 
 
 def main():
@@ -208,9 +313,22 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--n", type=int, default=224)
-    ap.add_argument("--workload", choices=["trunk", "triattn", "copy"], default="trunk")
+    ap.add_argument("--workload", choices=["trunk", "triattn", "fold", "copy"], default="trunk")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--pmc-summarize", nargs=5, metavar=("FETCH_CSV", "WRITE_CSV", "COPY_FETCH_CSV",
+                                                         "COPY_WRITE_CSV", "OUT_JSON"),
+                    help="write the per-kernel HBM traffic summary from rocprofv3 --pmc runs")
+    ap.add_argument("--no-kprof", action="store_true",
+                    help="skip the per-kernel event-timer pass (roofline / kernel table)")
+    ap.add_argument("--progress", action="store_true",
+                    help="print a line on stderr after every step (long profiler runs)")
     args = ap.parse_args()
+    global PROGRESS
+    PROGRESS = args.progress
+    if args.pmc_summarize:
+        summ = pmc_summarize(*args.pmc_summarize[:4], args.n, args.pmc_summarize[4])
+        print(json.dumps({"kernels": len(summ["kernels"]), "copy_scale": summ["copy_scale"]}))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the trunk runs on one MI355X; "
               "multi-GPU sharding is a design note, not built)", file=sys.stderr)
@@ -243,6 +361,36 @@ def main():
                "higher_is_better": True, "config": {"workload": "copy", "bytes": nbytes}}
         print(json.dumps(out))
         return
+    if args.workload == "fold":
+        # BASELINE configs[4]'s structure-module part: 8 fold iterations (IPA,
+        # transition, rigid update) forward+backward, f32, dropout on
+        depth = 8
+        prm = bparams.init_fold_params(rng, final="random")
+        wdir = bparams.write_manifest(tempfile.mkdtemp(prefix="bc2n_bench_fold_"), prm)
+        fold = ops.Fold(wdir, depth)
+        single = torch.randn(n, 384, device=dev)
+        pair = torch.randn(n, n, 128, device=dev)
+        seqm = torch.as_tensor(m1, device=dev)
+        seed = ops.seed_tensor((0, 7), True, dev)
+        d_act = torch.randn(n, 384, device=dev)
+        d_traj = torch.randn(depth, n, 3, 4, device=dev)
+        save = torch.empty(fold.save_bytes(n), dtype=torch.uint8, device=dev)
+
+        def step():
+            fold.forward(single, pair, seqm, seed, save=save)
+            fold.backward(d_act, d_traj, single, pair, seqm, save)
+
+        ms = timed(step, args.steps, args.warmup)
+        prof = profiled(step, args.steps, args.no_kprof)
+        out = {"metric": "ms per structure-module fold (8 IPA iterations) fwd+bwd", "value": round(ms, 3),
+               "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+               "ms_per_step": round(ms, 3), "higher_is_better": False, "scaling": "weak",
+               "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+               "config": {"workload": "fold iterations of BASELINE configs[4] (c_s=384, 12 heads, "
+                                      "4/8 points, dropout 0.1)", "L": n, "depth": depth},
+               "kernels": kernel_table(prof)}
+        print(json.dumps(out))
+        return
     if args.workload == "triattn":
         mods = ["triangle_attention_starting_node", "triangle_attention_ending_node"]
         prm = bparams.init_block_params(0, rng, modules=mods, gates="zero")
@@ -262,11 +410,7 @@ def main():
 
         ms = timed(step, args.steps, args.warmup)
         flops = 2 * triattn_flops(n)
-        b.prof_enable(True)
-        for _ in range(args.steps):
-            step()
-        prof = b.prof_read()
-        b.prof_enable(False)
+        prof = profiled(step, args.steps, args.no_kprof)
         line = {"metric": METRIC, "value": round(flops / (ms * 1e-3) / 1e12, 3),
                 "unit": "TFLOP/s", "higher_is_better": True,
                 "config": {"workload": "triangle attention fwd+bwd, starting+ending node "
@@ -323,11 +467,7 @@ def main():
             tpl_stack.backward(ct_tpl, pmask, s_tpl, keys[0])
 
         ms = timed(step, args.steps, args.warmup)
-        b.prof_enable(True)
-        for _ in range(args.steps):
-            step()
-        prof = b.prof_read()
-        b.prof_enable(False)
+        prof = profiled(step, args.steps, args.no_kprof)
         tri = sum(v[0] for k, v in prof.items() if k.startswith("attn_") or k.startswith("triattn."))
         tm = sum(v[0] for k, v in prof.items() if k.startswith("trimul."))
         n_tri = 2 * (48 + 4) * args.steps
@@ -337,8 +477,8 @@ def main():
                                        "(BASELINE configs[3])",
                            "L": n, "n_seq": 1, "c_m": 256, "c_z": 128, "c_t": 64,
                            "dropout": [0.15, 0.25], "masked_residues": 0.1},
-                "triattn_tflops": round(n_tri * triattn_flops(n) / (tri * 1e-3) / 1e12, 2),
-                "trimul_tflops": round(n_tri * trimul_flops(n) / (tm * 1e-3) / 1e12, 2),
+                "triattn_tflops": round(n_tri * triattn_flops(n) / (tri * 1e-3) / 1e12, 2) if tri else None,
+                "trimul_tflops": round(n_tri * trimul_flops(n) / (tm * 1e-3) / 1e12, 2) if tm else None,
                 "save_set_gb": round((s_main.numel() + s_extra.numel() + s_tpl.numel()) / 1e9, 2)}
         cpu = None if args.no_cpu_baseline else cpu_trunk_baseline(n)
 

@@ -680,6 +680,17 @@ static void with_blocks(int nb, F&& f) {
   }
 }
 
+// Timer names per launch site: [kernel][0 triangle D=32, 1 MSA row, 2 D=16]
+static const char* const kTimerNames[5][3] = {
+    {"attn_fwd", "msarow.attn_fwd", "tpl.attn_fwd"},
+    {"attn_gate_bwd", "msarow.attn_gate_bwd", "tpl.attn_gate_bwd"},
+    {"attn_bwd_dq", "msarow.attn_bwd_dq", "tpl.attn_bwd_dq"},
+    {"attn_bwd_dkv", "msarow.attn_bwd_dkv", "tpl.attn_bwd_dkv"},
+    {"attn_dbias_reduce", "msarow.attn_dbias_reduce", "tpl.attn_dbias_reduce"}};
+static const char* timer_name(int kernel, const AttnArgs& a) {
+  return kTimerNames[kernel][a.site == 1 ? 1 : (a.D == 16 ? 2 : 0)];
+}
+
 // keys per LDS chunk of the forward / dQ kernels, rows per chunk of dK/dV
 static int attn_chunk(int N) { return N < 256 ? N : 256; }
 
@@ -695,7 +706,7 @@ template <int D>
 static void attn_fwd_t(hipStream_t st, const AttnArgs& a) {
   const int nqb = (a.N + 63) / 64;
   const size_t lds = (size_t)attn_chunk(a.N) * (D + 8) * 2 * 2 + (size_t)a.N * 8;
-  KTimed kt("attn_fwd", st);
+  KTimed kt(timer_name(0, a), st);
   const dim3 grid(xcd_grid((long)a.R * a.H * nqb));
   with_blocks(a.N / 32, [&](auto nb) {
     hipLaunchKernelGGL((attn_fwd_kernel<D, decltype(nb)::value>), grid, dim3(256), lds, st, a);
@@ -714,7 +725,7 @@ static void attn_bwd_t(hipStream_t st, const AttnBwdArgs& b) {
   const AttnArgs& a = b.f;
   const long tot = (long)a.R * a.N * a.H;
   {
-    KTimed kt("attn_gate_bwd", st);
+    KTimed kt(timer_name(1, a), st);
     const long per = 256 / (D / 8);
     hipLaunchKernelGGL((attn_gate_bwd_kernel<D>), dim3((unsigned)((tot + per - 1) / per)),
                        dim3(256), 0, st, b);
@@ -722,7 +733,7 @@ static void attn_bwd_t(hipStream_t st, const AttnBwdArgs& b) {
   const int nqb = (a.N + 63) / 64;
   const size_t lds_q = (size_t)attn_chunk(a.N) * (D + 8) * 2 * 2 + (size_t)a.N * 4;
   {
-    KTimed kt("attn_bwd_dq", st);
+    KTimed kt(timer_name(2, a), st);
     const dim3 grid(xcd_grid((long)a.R * a.H * nqb));
     with_blocks(a.N / 32, [&](auto nb) {
       hipLaunchKernelGGL((attn_bwd_dq_kernel<D, decltype(nb)::value>), grid, dim3(256), lds_q, st, b);
@@ -735,7 +746,7 @@ static void attn_bwd_t(hipStream_t st, const AttnBwdArgs& b) {
   const size_t lds_k = (size_t)attn_chunk(a.N) * (D + 8) * 2 * 2 + (size_t)a.N * 4 * 2 +
                        (size_t)(QS - 1) * KT * 2 * (D / 16) * 4 * 64 * 4;
   {
-    KTimed kt("attn_bwd_dkv", st);
+    KTimed kt(timer_name(3, a), st);
     const dim3 grid(xcd_grid((long)nch * a.H * nkw));
     with_blocks(a.N / 32, [&](auto nb) {
       hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, decltype(nb)::value>), grid, dim3(256), lds_k, st, b);
@@ -744,7 +755,7 @@ static void attn_bwd_t(hipStream_t st, const AttnBwdArgs& b) {
   if (b.dbias && a.bias) {
     if (!b.dbias_part) throw std::runtime_error("attention bwd: missing dbias scratch");
     const long n = (long)a.H * a.N * a.N;
-    KTimed kt("attn_dbias_reduce", st);
+    KTimed kt(timer_name(4, a), st);
     hipLaunchKernelGGL(attn_dbias_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
                        b.dbias_part, nch, n, b.dbias);
   }

@@ -40,6 +40,9 @@ struct AttnArgs {
   bf16* og = nullptr;           // sigmoid(g) * o   [R*N][H*D]
   long ldo = 0;
   float* lse = nullptr;         // [R][H][N], log2 domain
+  // launch-site tag for the per-kernel timer: 0 triangle attention, 1 MSA
+  // row attention (the template stack's D=16 launches are told apart by D)
+  int site = 0;
 };
 void attn_fwd(hipStream_t st, const AttnArgs& a);
 

@@ -337,6 +337,7 @@ void msarow_fwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa
   at.bias = sv.bias;
   at.o = sv.o; at.og = og; at.ldo = HD;
   at.lse = sv.lse;
+  at.site = 1;
   attn_fwd(st, at);
   out_gemm(st, a, R, og, msa_in, msa_out, tbl, N, "msarow.gemm_out");
 }
@@ -387,6 +388,7 @@ void msarow_bwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa
   at.bias = sv.bias;
   at.o = sv.o; at.og = nullptr; at.ldo = HD;
   at.lse = sv.lse;
+  at.site = 1;
   b.dog = dog;
   b.scale = 1.f / std::sqrt((float)a.D);
   attn_bwd(st, b);
