@@ -37,6 +37,7 @@
 // The bias gradient (a sum over rows) is accumulated in registers over a
 // chunk of rows and written once per chunk; a second pass adds the chunks in
 // a fixed order, so the result is deterministic (no float atomics anywhere).
+#include <algorithm>
 #include <type_traits>
 
 #include "kernels.h"
@@ -78,31 +79,45 @@ __device__ __forceinline__ bf16x8 ld_tr8(const bf16* T, int ld, int r0, int c0, 
 // Row-major copies of the first `rows` (<= N) rows of two head slices (row
 // strides lda, ldb) into LDS tiles [N][D + 8], by 256 threads: every 16-byte
 // load is issued before the first store, so one memory latency covers the
-// whole tile.
+// whole tile.  The loads and the LDS stores are separate steps, so a kernel
+// walking several rows can hold the next row's tiles in registers while it
+// computes.
+template <int D, int N>
+struct RowPair {
+  static constexpr int CPR = D / 8;  // 16-byte chunks per row
+  static constexpr int IT = (N * CPR + 255) / 256;
+  bf16x8 va[IT], vb[IT];
+  __device__ __forceinline__ void load(const bf16* sA, long lda, const bf16* sB, long ldb, int tid,
+                                       int rows) {
+    const int items = rows * CPR;
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      const int c = tid + 256 * i;
+      if (c < items) {
+        va[i] = ld8(sA + (long)(c / CPR) * lda + (c % CPR) * 8);
+        vb[i] = ld8(sB + (long)(c / CPR) * ldb + (c % CPR) * 8);
+      }
+    }
+  }
+  __device__ __forceinline__ void store(bf16* dA, bf16* dB, int tid, int rows) const {
+    const int items = rows * CPR;
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      const int c = tid + 256 * i;
+      if (c < items) {
+        st8(&dA[(c / CPR) * (D + 8) + (c % CPR) * 8], va[i]);
+        st8(&dB[(c / CPR) * (D + 8) + (c % CPR) * 8], vb[i]);
+      }
+    }
+  }
+};
+
 template <int D, int N>
 __device__ __forceinline__ void stage_rows2(bf16* dA, const bf16* sA, long lda, bf16* dB,
                                             const bf16* sB, long ldb, int tid, int rows = N) {
-  constexpr int CPR = D / 8;  // 16-byte chunks per row
-  constexpr int ITEMS = N * CPR;
-  constexpr int IT = (ITEMS + 255) / 256;
-  const int items = rows * CPR;
-  bf16x8 va[IT], vb[IT];
-#pragma unroll
-  for (int i = 0; i < IT; ++i) {
-    const int c = tid + 256 * i;
-    if (c < items) {
-      va[i] = ld8(sA + (long)(c / CPR) * lda + (c % CPR) * 8);
-      vb[i] = ld8(sB + (long)(c / CPR) * ldb + (c % CPR) * 8);
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < IT; ++i) {
-    const int c = tid + 256 * i;
-    if (c < items) {
-      st8(&dA[(c / CPR) * (D + 8) + (c % CPR) * 8], va[i]);
-      st8(&dB[(c / CPR) * (D + 8) + (c % CPR) * 8], vb[i]);
-    }
-  }
+  RowPair<D, N> p;
+  p.load(sA, lda, sB, ldb, tid, rows);
+  p.store(dA, dB, tid, rows);
 }
 
 // Operand fragment of the head-width contraction for lane group g.
@@ -484,6 +499,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
   float* Ls = reinterpret_cast<float*>(Os + CN * LD);   // [N] -lse
   float* Ds = Ls + N;                                   // [N] -Dsum
   float* Xs = Ds + N;                                   // [QS-1][KT][K,V][DT*4][64]
+  float* Ms = Xs + (QS - 1) * KT * 2 * DT * 4 * 64;     // [N] key mask of the row
+  bf16* KVs = reinterpret_cast<bf16*>(Ms + N);          // [K,V][16*KT][LD] own keys
 
   constexpr int NKW = N / (16 * KT);  // key groups per (chunk, head)
   const long G = (long)((a.R + b.rows_per_chunk - 1) / b.rows_per_chunk) * H * NKW;
@@ -521,78 +538,129 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
   }
   const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
 
-  for (int r = r0; r < r1; ++r) {
-    const long tok0 = (long)r * N;
-    const bf16* Qg = a.qkvg + tok0 * a.ld + h * D;
-    const bf16* Og = b.dO + tok0 * a.ldo + h * D;
-    __syncthreads();  // previous row's LDS readers are done
-    stage_rows2<D, CN>(Qs, Qg, a.ld, Os, Og, a.ldo, tid);
-    int on = 0;
-    for (int qq = tid; qq < N; qq += 256) {
-      Ls[qq] = -a.lse[((long)r * H + h) * N + qq];
-      Ds[qq] = -b.Dsum[((long)r * H + h) * N + qq];
-      on |= a.mask[r * a.mask_sr + qq * a.mask_sk] != 0.f;
-    }
-    HFrag<D> kf, vf;
-    kf.load(a.qkvg + (tok0 + k) * a.ld + HD + h * D, g);
-    vf.load(a.qkvg + (tok0 + k) * a.ld + 2 * HD + h * D, g);
-    const bool mk = a.mask[r * a.mask_sr + k * a.mask_sk] != 0.f;
-    const bool live = __syncthreads_or(on);  // the row has an unmasked key
-    // exponent of a masked key: -inf (weight 0) in a live row, -log2 N
-    // (weight 1/N) in a fully masked one; either way its dS is 0
-    const float xm = live ? -INFINITY : -__log2f((float)N);
-    f32x4 accK[DT], accV[DT];
+  // Stage s = (row r0 + s / NCH, chunk s % NCH).  While a stage computes, the
+  // next stage's Q/dO tile -- and, at a row's first chunk, the row's -lse,
+  // -Dsum, mask and this lane's key/value fragments -- are loaded into
+  // registers, so the row loop does not wait on memory at every row.
+  constexpr int NPT = (N + 255) / 256;  // row statistics per thread
+  const int nst = (r1 - r0) * NCH;
+  // Loaded values are only consumed at the next stage (vmcnt retires loads
+  // in order, so any use now would wait for the whole prefetch).
+  // The workgroup's own 16*KT keys and values of the row go through LDS too,
+  // so no register filled by the prefetch is read before the next stage.
+  RowPair<D, CN> nxt;
+  float nls[NPT], nds[NPT], nmask[NPT];
+  constexpr int KCH = 16 * KT * 2 * (D / 8);  // 16-byte chunks of own K and V
+  static_assert(KCH <= 256, "own keys: one chunk per thread");
+  bf16x8 nkv;
+  const int kvi = tid % (KCH / 2), kvs = tid / (KCH / 2);  // chunk, 0 = K / 1 = V
+  const int kvrow = kvi / (D / 8), kvc = (kvi % (D / 8)) * 8;
+  auto prefetch = [&](int s) {
+    const int r = r0 + s / NCH, c = s % NCH;
+    const long tok = (long)r * N + c * CN;
+    nxt.load(a.qkvg + tok * a.ld + h * D, a.ld, b.dO + tok * a.ldo + h * D, a.ldo, tid,
+             min(CN, N - c * CN));
+    if (c == 0) {
 #pragma unroll
-    for (int i = 0; i < DT; ++i) { accK[i] = z4; accV[i] = z4; }
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      if (c > 0) {
-        __syncthreads();  // every wave is done with the previous chunk
-        stage_rows2<D, CN>(Qs, Qg + (long)c * CN * a.ld, a.ld, Os, Og + (long)c * CN * a.ldo,
-                           a.ldo, tid, min(CN, N - c * CN));
-        __syncthreads();
+      for (int i = 0; i < NPT; ++i) {
+        const int qq = tid + 256 * i;
+        nls[i] = 0.f;
+        nds[i] = 0.f;
+        nmask[i] = 0.f;
+        if (qq < N) {
+          nls[i] = a.lse[((long)r * H + h) * N + qq];
+          nds[i] = b.Dsum[((long)r * H + h) * N + qq];
+          nmask[i] = a.mask[r * a.mask_sr + qq * a.mask_sk];
+        }
       }
+      if (tid < KCH) {
+        const long kt = (long)r * N + kw * 16 * KT + kvrow;
+        nkv = ld8(a.qkvg + kt * a.ld + (1 + kvs) * HD + h * D + kvc);
+      }
+    }
+  };
+
+  prefetch(0);
+  HFrag<D> kf, vf;
+  bool mk = false;
+  const int klocal = kt_ * 16 + lk;  // this lane's key among the workgroup's
+  float xm = 0.f;
+  f32x4 accK[DT], accV[DT];
+  for (int s = 0; s < nst; ++s) {
+    const int r = r0 + s / NCH, c = s % NCH;
+    const long tok0 = (long)r * N;
+    __syncthreads();  // the previous stage's LDS readers are done
+    nxt.store(Qs, Os, tid, min(CN, N - c * CN));
+    if (c == 0) {
+      int non = 0;
 #pragma unroll
-      for (int ib = 0; ib < NB; ++ib) {
-        if (NCH > 1 && ib * QS / CQB != c) continue;  // block of another chunk
-        const int blk = ib * QS + qs;
-        if (blk < NQB) {
-          const int qb = blk * 32;         // query index
-          const int ql = qb - c * CN;      // row in the staged chunk
-          bf16x8 pf, dsf;
+      for (int i = 0; i < NPT; ++i) {
+        const int qq = tid + 256 * i;
+        if (qq < N) {
+          Ls[qq] = -nls[i];
+          Ds[qq] = -nds[i];
+          Ms[qq] = nmask[i];
+        }
+        non |= nmask[i] != 0.f;
+      }
+      if (tid < KCH) st8(&KVs[(kvs * 16 * KT + kvrow) * LD + kvc], nkv);
+      const bool live = __syncthreads_or(non);  // the row has an unmasked key
+      kf.load(&KVs[klocal * LD], g);
+      vf.load(&KVs[(16 * KT + klocal) * LD], g);
+      mk = Ms[k] != 0.f;
+      // exponent of a masked key: -inf (weight 0) in a live row, -log2 N
+      // (weight 1/N) in a fully masked one; either way its dS is 0
+      xm = live ? -INFINITY : -__log2f((float)N);
 #pragma unroll
-          for (int qh = 0; qh < 2; ++qh) {
-            HFrag<D> qa, da;
-            qa.load(&Qs[(ql + qh * 16 + lk) * LD], g);
-            da.load(&Os[(ql + qh * 16 + lk) * LD], g);
-            const float4 lv = *reinterpret_cast<const float4*>(Ls + qb + qh * 16 + 4 * g);
-            const float4 dv = *reinterpret_cast<const float4*>(Ds + qb + qh * 16 + 4 * g);
-            f32x4 cs, cd;
-            cs[0] = bsl[ib][qh * 4 + 0] + lv.x;
-            cs[1] = bsl[ib][qh * 4 + 1] + lv.y;
-            cs[2] = bsl[ib][qh * 4 + 2] + lv.z;
-            cs[3] = bsl[ib][qh * 4 + 3] + lv.w;
-            cd[0] = dv.x; cd[1] = dv.y; cd[2] = dv.z; cd[3] = dv.w;
-            const f32x4 s = HFrag<D>::mma(qa, kf, cs);   // S + bias - lse
-            const f32x4 dp = HFrag<D>::mma(da, vf, cd);  // dP - Dsum
+      for (int i = 0; i < DT; ++i) { accK[i] = z4; accV[i] = z4; }
+    } else {
+      __syncthreads();
+    }
+    if (s + 1 < nst) prefetch(s + 1);
+
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const float p = fast_exp2(mk ? s[i] : xm);
-              const float ds = mk ? p * dp[i] : 0.f;
-              pf[qh * 4 + i] = (bf16)p;
-              dsf[qh * 4 + i] = (bf16)ds;
-              dbias[ib][qh * 4 + i] += ds;
-            }
+    for (int ib = 0; ib < NB; ++ib) {
+      if (NCH > 1 && ib * QS / CQB != c) continue;  // block of another chunk
+      const int blk = ib * QS + qs;
+      if (blk < NQB) {
+        const int qb = blk * 32;         // query index
+        const int ql = qb - c * CN;      // row in the staged chunk
+        bf16x8 pf, dsf;
+#pragma unroll
+        for (int qh = 0; qh < 2; ++qh) {
+          HFrag<D> qa, da;
+          qa.load(&Qs[(ql + qh * 16 + lk) * LD], g);
+          da.load(&Os[(ql + qh * 16 + lk) * LD], g);
+          const float4 lv = *reinterpret_cast<const float4*>(Ls + qb + qh * 16 + 4 * g);
+          const float4 dv = *reinterpret_cast<const float4*>(Ds + qb + qh * 16 + 4 * g);
+          f32x4 cs, cd;
+          cs[0] = bsl[ib][qh * 4 + 0] + lv.x;
+          cs[1] = bsl[ib][qh * 4 + 1] + lv.y;
+          cs[2] = bsl[ib][qh * 4 + 2] + lv.z;
+          cs[3] = bsl[ib][qh * 4 + 3] + lv.w;
+          cd[0] = dv.x; cd[1] = dv.y; cd[2] = dv.z; cd[3] = dv.w;
+          const f32x4 s4 = HFrag<D>::mma(qa, kf, cs);  // S + bias - lse
+          const f32x4 dp = HFrag<D>::mma(da, vf, cd);  // dP - Dsum
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float p = fast_exp2(mk ? s4[i] : xm);
+            const float ds = mk ? p * dp[i] : 0.f;
+            pf[qh * 4 + i] = (bf16)p;
+            dsf[qh * 4 + i] = (bf16)ds;
+            dbias[ib][qh * 4 + i] += ds;
           }
+        }
 #pragma unroll
-          for (int dh = 0; dh < DT; ++dh) {
-            accV[dh] = mfma16x16x32(ld_tr8(Os, LD, ql, dh * 16, lane), pf, accV[dh]);
-            accK[dh] = mfma16x16x32(ld_tr8(Qs, LD, ql, dh * 16, lane), dsf, accK[dh]);
-          }
+        for (int dh = 0; dh < DT; ++dh) {
+          accV[dh] = mfma16x16x32(ld_tr8(Os, LD, ql, dh * 16, lane), pf, accV[dh]);
+          accK[dh] = mfma16x16x32(ld_tr8(Qs, LD, ql, dh * 16, lane), dsf, accK[dh]);
         }
       }
     }
-    // add the query groups' partials: groups 1..QS-1 park theirs in LDS
+    if (c != NCH - 1) continue;
+
+    // row done: add the query groups' partials (groups 1..QS-1 park theirs
+    // in LDS) and write dK, dV
     if (qs > 0) {
       float* x = Xs + ((qs - 1) * KT + kt_) * 2 * DT * 4 * 64;
 #pragma unroll
@@ -662,9 +730,28 @@ int attn_bwd_nchunk(int R, int rows_per_chunk) {
   return (R + rows_per_chunk - 1) / rows_per_chunk;
 }
 
-// Rows per bias-gradient chunk: the partials are [nchunk][H][N][N] f32, so
-// longer rows take longer chunks (N = 512: 32 chunks, 134 MB at H = 4).
-int attn_rows_per_chunk(int N) { return N <= 256 ? 8 : 16; }
+// Rows per bias-gradient chunk.  A chunk is H * N / (16 KT) workgroups of
+// the dK/dV kernel, which is register bound at two workgroups per CU; the
+// chunk count is the largest that fits one round of 2 x CUs workgroups, so
+// no second, partly empty round follows (N = 224, H = 4 on 256 CUs: 18
+// chunks of 13 rows).  Fewer chunks also mean fewer [nchunk][H][N][N]
+// partials to write and add.
+int attn_rows_per_chunk(int R, int N, int H) {
+  static int cus[64] = {};
+  int dev = 0;
+  hip_check(hipGetDevice(&dev), "hipGetDevice");
+  if (dev < 0 || dev >= 64) dev = 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    hip_check(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev),
+              "hipDeviceGetAttribute");
+    cus[dev] = n > 0 ? n : 1;
+  }
+  const int KT = N > 256 ? 1 : 2;
+  const long per_chunk = (long)H * (N / (16 * KT));
+  const long nch = std::max(1L, 2L * cus[dev] / per_chunk);
+  return (int)std::max(1L, ((long)R + nch - 1) / nch);
+}
 
 // Calls f(std::integral_constant<int, nb>) for nb = N/32 in 1..16: every
 // kernel is instantiated for its exact number of 32-blocks.
@@ -743,8 +830,9 @@ static void attn_bwd_t(hipStream_t st, const AttnBwdArgs& b) {
   // query groups QS and key tiles KT per workgroup, as in the kernel
   const int QS = a.N > 256 ? 4 : 2, KT = 4 / QS;
   const int nkw = a.N / (16 * KT);
-  const size_t lds_k = (size_t)attn_chunk(a.N) * (D + 8) * 2 * 2 + (size_t)a.N * 4 * 2 +
-                       (size_t)(QS - 1) * KT * 2 * (D / 16) * 4 * 64 * 4;
+  const size_t lds_k = (size_t)attn_chunk(a.N) * (D + 8) * 2 * 2 + (size_t)a.N * 4 * 3 +
+                       (size_t)(QS - 1) * KT * 2 * (D / 16) * 4 * 64 * 4 +
+                       (size_t)2 * 16 * KT * (D + 8) * 2;
   {
     KTimed kt(timer_name(3, a), st);
     const dim3 grid(xcd_grid((long)nch * a.H * nkw));

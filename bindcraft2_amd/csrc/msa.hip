@@ -354,7 +354,7 @@ void msarow_bwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa
   Carver cv(const_cast<void*>(save));
   MsaRowSave<Carver> sv(cv, S, N, Cm, H);
   AttnBwdArgs b;
-  b.rows_per_chunk = attn_rows_per_chunk(N);
+  b.rows_per_chunk = attn_rows_per_chunk(S, N, H);
   const int nch = attn_bwd_nchunk(S, b.rows_per_chunk);
   Arena& ar = arena();
   std::lock_guard<std::recursive_mutex> lk(ar.lock());
