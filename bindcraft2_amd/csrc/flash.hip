@@ -301,6 +301,180 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   if (g == 0) a.lse[((long)r * H + h) * N + q] = mx + __log2f(lsum);
 }
 
+// Forward over a chunk of rows, N <= 256 (one key chunk).  Workgroup = (row
+// chunk, head h, 64 queries), 4 waves x 16 queries, as attn_fwd_kernel, but
+// it walks `rpc` rows: the pair bias of its queries is row-independent, so it
+// is read once into registers and enters every row's score MFMA as the
+// accumulator (no add per score); the next row's K, V, q, gate and key mask
+// are loaded into registers while the current row computes, and only stored
+// to LDS at the next row, so no compute waits on them.
+template <int D, int NKB>
+__global__ __launch_bounds__(256) void attn_fwd_rows_kernel(AttnArgs a, int rpc) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
+  constexpr int DT = D / 16;
+  constexpr int LD = D + 8;
+  constexpr int N = 32 * NKB;  // == a.N (dispatch)
+  static_assert(NKB <= 8, "one key chunk");
+  constexpr int QR = 64;       // query rows of the workgroup
+  const int H = a.H;
+  bf16* Ks = reinterpret_cast<bf16*>(smem_raw);          // [N][LD]
+  bf16* Vs = Ks + N * LD;                                // [N][LD]
+  bf16* Qs = Vs + N * LD;                                // [QR][LD]
+  bf16* Gs = Qs + QR * LD;                               // [QR][LD]
+  float* Mm = reinterpret_cast<float*>(Gs + QR * LD);    // [N] 1 / 0 per key
+  float* Ma = Mm + N;                                    // [N] 0 / NEG_LOGIT
+
+  const int nqb = (N + QR - 1) / QR;
+  const int nch = (a.R + rpc - 1) / rpc;
+  const long G = (long)nch * H * nqb;
+  const int bid = (int)xcd_block(G);  // (chunk, h, qb): the qb blocks of (chunk, h) share K, V
+  if (bid >= G) return;
+  const int qb = bid % nqb;
+  const int h = (bid / nqb) % H;
+  const int ch = bid / (nqb * H);
+  const int r0 = ch * rpc, r1 = min(a.R, r0 + rpc);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+  const int q0 = qb * QR + wave * 16;
+  const bool active = q0 < N;  // idle waves keep to the barriers only
+  const int lq = lane & 15, g = lane >> 4;
+  const int q = min(q0, N - 16) + lq;
+  const long HD = (long)H * D;
+
+  // pair bias of this lane's query, all N keys, in score-fragment order
+  float bsv[NKB][8];
+  {
+    const float* brow = a.bias + ((long)h * N + q) * N;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh) {
+        const float4 bb = *reinterpret_cast<const float4*>(brow + kb * 32 + kh * 16 + 4 * g);
+        bsv[kb][kh * 4 + 0] = bb.x;
+        bsv[kb][kh * 4 + 1] = bb.y;
+        bsv[kb][kh * 4 + 2] = bb.z;
+        bsv[kb][kh * 4 + 3] = bb.w;
+      }
+    // Make the bias resident here: the row loop then never waits on these
+    // loads (the wait counter retires in order, so a first use inside the
+    // loop would also wait for the prefetch issued before it).
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) asm volatile("" ::"v"(bsv[kb][e]));
+  }
+
+  // next-row registers: K/V rows, one q or gate chunk, one key's mask
+  constexpr int QCH = QR * (D / 8);  // 16-byte chunks of the q (or gate) tile
+  static_assert(2 * QCH <= 512, "q and gate: at most two chunks per thread");
+  RowPair<D, N> nkv;
+  bf16x8 nq, ng;
+  float nm = 0.f;
+  const int qrow = tid / (D / 8), qc = (tid % (D / 8)) * 8;  // tid < QCH
+  const int qtok = min(qb * QR + qrow, N - 1);               // rows past N: any in-bounds row
+  auto prefetch = [&](int r) {
+    const long tok0 = (long)r * N;
+    nkv.load(a.qkvg + tok0 * a.ld + HD + h * D, a.ld, a.qkvg + tok0 * a.ld + 2 * HD + h * D, a.ld,
+             tid, N);
+    if (tid < QCH) {
+      const bf16* row = a.qkvg + (tok0 + qtok) * a.ld + h * D + qc;
+      nq = ld8(row);
+      ng = ld8(row + 3 * HD);
+    }
+    if (tid < N) nm = a.mask[r * a.mask_sr + tid * a.mask_sk];
+  };
+
+  prefetch(r0);
+  const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+  for (int r = r0; r < r1; ++r) {
+    __syncthreads();  // the previous row's LDS readers are done
+    nkv.store(Ks, Vs, tid, N);
+    if (tid < QCH) {
+      st8(&Qs[qrow * LD + qc], nq);
+      st8(&Gs[qrow * LD + qc], ng);
+    }
+    if (tid < N) {
+      const bool on = nm != 0.f;
+      Mm[tid] = on ? 1.f : 0.f;
+      Ma[tid] = on ? 0.f : NEG_LOGIT;
+    }
+    __syncthreads();
+    if (r + 1 < r1) prefetch(r + 1);
+    __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
+    if (!active) continue;
+
+    HFrag<D> qf;
+    qf.load(&Qs[(wave * 16 + lq) * LD], g);
+    float sv[NKB][8];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh) {
+        HFrag<D> kf;
+        kf.load(&Ks[(kb * 32 + kh * 16 + lq) * LD], g);
+        f32x4 cb;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) cb[i] = bsv[kb][kh * 4 + i];
+        const f32x4 s = HFrag<D>::mma(kf, qf, cb);  // score + bias
+        const int kk = kb * 32 + kh * 16 + 4 * g;
+        const float4 mm = *reinterpret_cast<const float4*>(Mm + kk);
+        const float4 ma = *reinterpret_cast<const float4*>(Ma + kk);
+        const float mv[4] = {mm.x, mm.y, mm.z, mm.w};
+        const float av[4] = {ma.x, ma.y, ma.z, ma.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          // unmasked: s + bias; masked: exactly NEG_LOGIT
+          const float x = __builtin_fmaf(s[i], mv[i], av[i]);
+          sv[kb][kh * 4 + i] = x;
+          mx = fmaxf(mx, x);
+        }
+      }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    float lsum = 0.f;
+    f32x4 acc[DT];
+#pragma unroll
+    for (int i = 0; i < DT; ++i) acc[i] = z4;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      bf16x8 pf;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float p = fast_exp2(sv[kb][e] - mx);
+        lsum += p;
+        pf[e] = (bf16)p;
+      }
+#pragma unroll
+      for (int dh = 0; dh < DT; ++dh)
+        acc[dh] = mfma16x16x32(ld_tr8(Vs, LD, kb * 32, dh * 16, lane), pf, acc[dh]);
+    }
+    lsum += __shfl_xor(lsum, 16, 64);
+    lsum += __shfl_xor(lsum, 32, 64);
+    const float inv = __builtin_amdgcn_rcpf(lsum);
+    const long tok0 = (long)r * N;
+    const long orow = (tok0 + q) * a.ldo + h * D;
+    if (q0 + 16 <= N || lq < N - q0) {
+#pragma unroll
+      for (int dh = 0; dh < DT; ++dh) {
+        const int d0 = dh * 16 + 4 * g;
+        const bf16x4 gv = *reinterpret_cast<const bf16x4*>(&Gs[(wave * 16 + lq) * LD + d0]);
+        bf16x4 ov, gov;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float o = acc[dh][i] * inv;
+          ov[i] = (bf16)o;
+          gov[i] = (bf16)(o * sigmoidf_((float)gv[i]));
+        }
+        *reinterpret_cast<bf16x4*>(a.o + orow + d0) = ov;
+        *reinterpret_cast<bf16x4*>(a.og + orow + d0) = gov;
+      }
+      if (g == 0) a.lse[((long)r * H + h) * N + q] = mx + __log2f(lsum);
+    }
+  }
+}
+
 // ------------------------------------------------------- backward: gate + D
 // dO = dog * sigmoid(g); dG = dog * o * s(1-s); Dsum = sum_d dO * o.
 // D/8 lanes per (token, head), 8 channels each.
@@ -461,6 +635,152 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs b) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] = (bf16)(acc[dh][i] * b.scale);
     *reinterpret_cast<bf16x4*>(out + dh * 16 + 4 * g) = v;
+  }
+}
+
+// dQ over a chunk of rows, N <= 256: the forward's row-chunk structure
+// (bias of the workgroup's queries resident in registers across rows, next
+// row's K, V, q, dO, lse, Dsum and key mask prefetched into registers while
+// the current row computes).
+template <int D, int NKB>
+__global__ __launch_bounds__(256) void attn_bwd_dq_rows_kernel(AttnBwdArgs b, int rpc) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
+  constexpr int DT = D / 16;
+  constexpr int LD = D + 8;
+  const AttnArgs& a = b.f;
+  constexpr int N = 32 * NKB;  // == a.N (dispatch)
+  static_assert(NKB <= 8, "one key chunk");
+  constexpr int QR = 64;
+  const int H = a.H;
+  bf16* Ks = reinterpret_cast<bf16*>(smem_raw);         // [N][LD]
+  bf16* Vs = Ks + N * LD;                               // [N][LD]
+  bf16* Qs = Vs + N * LD;                               // [QR][LD]
+  bf16* Os = Qs + QR * LD;                              // [QR][LD] dO
+  float* Ms = reinterpret_cast<float*>(Os + QR * LD);   // [N] 0 / -inf per key
+  float* Ls = Ms + N;                                   // [QR] lse
+  float* Dl = Ls + QR;                                  // [QR] Dsum
+
+  const int nqb = (N + QR - 1) / QR;
+  const int nch = (a.R + rpc - 1) / rpc;
+  const long G = (long)nch * H * nqb;
+  const int bid = (int)xcd_block(G);
+  if (bid >= G) return;
+  const int qb = bid % nqb;
+  const int h = (bid / nqb) % H;
+  const int ch = bid / (nqb * H);
+  const int r0 = ch * rpc, r1 = min(a.R, r0 + rpc);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q0 = qb * QR + wave * 16;
+  const bool active = q0 < N;
+  const int lq = lane & 15, g = lane >> 4;
+  const int q = min(q0, N - 16) + lq;
+  const int ql = wave * 16 + lq;  // query row in the staged tiles
+  const long HD = (long)H * D;
+
+  float bsv[NKB][8];
+  {
+    const float* brow = a.bias + ((long)h * N + q) * N;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh) {
+        const float4 bb = *reinterpret_cast<const float4*>(brow + kb * 32 + kh * 16 + 4 * g);
+        bsv[kb][kh * 4 + 0] = bb.x;
+        bsv[kb][kh * 4 + 1] = bb.y;
+        bsv[kb][kh * 4 + 2] = bb.z;
+        bsv[kb][kh * 4 + 3] = bb.w;
+      }
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) asm volatile("" ::"v"(bsv[kb][e]));
+  }
+
+  constexpr int QCH = QR * (D / 8);
+  RowPair<D, N> nkv;
+  bf16x8 nq, no;
+  float nm = 0.f, nl = 0.f, nd = 0.f;
+  const int qrow = tid / (D / 8), qc = (tid % (D / 8)) * 8;  // tid < QCH
+  const int qtok = min(qb * QR + qrow, N - 1);
+  const int stok = min(qb * QR + tid, N - 1);                // tid < QR: statistics row
+  auto prefetch = [&](int r) {
+    const long tok0 = (long)r * N;
+    nkv.load(a.qkvg + tok0 * a.ld + HD + h * D, a.ld, a.qkvg + tok0 * a.ld + 2 * HD + h * D, a.ld,
+             tid, N);
+    if (tid < QCH) {
+      nq = ld8(a.qkvg + (tok0 + qtok) * a.ld + h * D + qc);
+      no = ld8(b.dO + (tok0 + qtok) * a.ldo + h * D + qc);
+    }
+    if (tid < N) nm = a.mask[r * a.mask_sr + tid * a.mask_sk];
+    if (tid < QR) {
+      nl = a.lse[((long)r * H + h) * N + stok];
+      nd = b.Dsum[((long)r * H + h) * N + stok];
+    }
+  };
+
+  prefetch(r0);
+  const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+  for (int r = r0; r < r1; ++r) {
+    __syncthreads();
+    nkv.store(Ks, Vs, tid, N);
+    if (tid < QCH) {
+      st8(&Qs[qrow * LD + qc], nq);
+      st8(&Os[qrow * LD + qc], no);
+    }
+    // a masked key's exponent becomes -inf, so p = dS = 0
+    if (tid < N) Ms[tid] = nm != 0.f ? 0.f : -INFINITY;
+    if (tid < QR) {
+      Ls[tid] = nl;
+      Dl[tid] = nd;
+    }
+    __syncthreads();
+    if (r + 1 < r1) prefetch(r + 1);
+    __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
+    if (!active) continue;
+
+    HFrag<D> qf, dof;
+    qf.load(&Qs[ql * LD], g);
+    dof.load(&Os[ql * LD], g);
+    const float lse = Ls[ql], Dq = Dl[ql];
+    const f32x4 nD = {-Dq, -Dq, -Dq, -Dq};
+    f32x4 acc[DT];
+#pragma unroll
+    for (int i = 0; i < DT; ++i) acc[i] = z4;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      bf16x8 dsf;
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh) {
+        const int krow = (kb * 32 + kh * 16 + lq) * LD;
+        HFrag<D> kf, vf;
+        kf.load(&Ks[krow], g);
+        vf.load(&Vs[krow], g);
+        const float4 mm = *reinterpret_cast<const float4*>(Ms + kb * 32 + kh * 16 + 4 * g);
+        f32x4 cs;
+        cs[0] = bsv[kb][kh * 4 + 0] + (mm.x - lse);
+        cs[1] = bsv[kb][kh * 4 + 1] + (mm.y - lse);
+        cs[2] = bsv[kb][kh * 4 + 2] + (mm.z - lse);
+        cs[3] = bsv[kb][kh * 4 + 3] + (mm.w - lse);
+        const f32x4 s = HFrag<D>::mma(kf, qf, cs);    // S + bias - lse
+        const f32x4 dp = HFrag<D>::mma(vf, dof, nD);  // dP - Dsum
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dsf[kh * 4 + i] = (bf16)(fast_exp2(s[i]) * dp[i]);
+      }
+#pragma unroll
+      for (int dh = 0; dh < DT; ++dh)
+        acc[dh] = mfma16x16x32(ld_tr8(Ks, LD, kb * 32, dh * 16, lane), dsf, acc[dh]);
+    }
+    if (q0 + 16 <= N || lq < N - q0) {
+      bf16* out = b.dqkvg + ((long)r * N + q) * a.ld + h * D;
+#pragma unroll
+      for (int dh = 0; dh < DT; ++dh) {
+        bf16x4 v;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = (bf16)(acc[dh][i] * b.scale);
+        *reinterpret_cast<bf16x4*>(out + dh * 16 + 4 * g) = v;
+      }
+    }
   }
 }
 
@@ -736,7 +1056,7 @@ int attn_bwd_nchunk(int R, int rows_per_chunk) {
 // no second, partly empty round follows (N = 224, H = 4 on 256 CUs: 18
 // chunks of 13 rows).  Fewer chunks also mean fewer [nchunk][H][N][N]
 // partials to write and add.
-int attn_rows_per_chunk(int R, int N, int H) {
+static int device_cus() {
   static int cus[64] = {};
   int dev = 0;
   hip_check(hipGetDevice(&dev), "hipGetDevice");
@@ -747,9 +1067,21 @@ int attn_rows_per_chunk(int R, int N, int H) {
               "hipDeviceGetAttribute");
     cus[dev] = n > 0 ? n : 1;
   }
+  return cus[dev];
+}
+
+// Rows per workgroup of the row-chunk forward: (chunk, head, 64 queries)
+// workgroups at two per CU (register bound), one round of 2 x CUs.
+int attn_fwd_rows_per_chunk(int R, int N, int H) {
+  const long per_chunk = (long)H * ((N + 63) / 64);
+  const long nch = std::max(1L, 2L * device_cus() / per_chunk);
+  return (int)std::max(1L, ((long)R + nch - 1) / nch);
+}
+
+int attn_rows_per_chunk(int R, int N, int H) {
   const int KT = N > 256 ? 1 : 2;
   const long per_chunk = (long)H * (N / (16 * KT));
-  const long nch = std::max(1L, 2L * cus[dev] / per_chunk);
+  const long nch = std::max(1L, 2L * device_cus() / per_chunk);
   return (int)std::max(1L, ((long)R + nch - 1) / nch);
 }
 
@@ -792,8 +1124,21 @@ static void attn_check(const AttnArgs& a) {
 template <int D>
 static void attn_fwd_t(hipStream_t st, const AttnArgs& a) {
   const int nqb = (a.N + 63) / 64;
-  const size_t lds = (size_t)attn_chunk(a.N) * (D + 8) * 2 * 2 + (size_t)a.N * 8;
   KTimed kt(timer_name(0, a), st);
+  if (a.N <= 256) {
+    if (!a.bias) throw std::runtime_error("attention: the row-chunk forward needs the pair bias");
+    const int rpc = attn_fwd_rows_per_chunk(a.R, a.N, a.H);
+    const long nch = (a.R + rpc - 1) / rpc;
+    const size_t lds = (size_t)(2 * a.N + 2 * 64) * (D + 8) * 2 + (size_t)a.N * 8;
+    const dim3 grid(xcd_grid(nch * a.H * nqb));
+    with_blocks(a.N / 32, [&](auto nb) {
+      if constexpr (decltype(nb)::value <= 8)
+        hipLaunchKernelGGL((attn_fwd_rows_kernel<D, decltype(nb)::value>), grid, dim3(256), lds, st,
+                           a, rpc);
+    });
+    return;
+  }
+  const size_t lds = (size_t)attn_chunk(a.N) * (D + 8) * 2 * 2 + (size_t)a.N * 8;
   const dim3 grid(xcd_grid((long)a.R * a.H * nqb));
   with_blocks(a.N / 32, [&](auto nb) {
     hipLaunchKernelGGL((attn_fwd_kernel<D, decltype(nb)::value>), grid, dim3(256), lds, st, a);
@@ -818,8 +1163,20 @@ static void attn_bwd_t(hipStream_t st, const AttnBwdArgs& b) {
                        dim3(256), 0, st, b);
   }
   const int nqb = (a.N + 63) / 64;
-  const size_t lds_q = (size_t)attn_chunk(a.N) * (D + 8) * 2 * 2 + (size_t)a.N * 4;
-  {
+  if (a.N <= 256) {
+    if (!a.bias) throw std::runtime_error("attention: the row-chunk dQ needs the pair bias");
+    const int rpc = attn_fwd_rows_per_chunk(a.R, a.N, a.H);
+    const long nch = (a.R + rpc - 1) / rpc;
+    const size_t lds = (size_t)(2 * a.N + 2 * 64) * (D + 8) * 2 + (size_t)(a.N + 2 * 64) * 4;
+    KTimed kt(timer_name(2, a), st);
+    const dim3 grid(xcd_grid(nch * a.H * nqb));
+    with_blocks(a.N / 32, [&](auto nb) {
+      if constexpr (decltype(nb)::value <= 8)
+        hipLaunchKernelGGL((attn_bwd_dq_rows_kernel<D, decltype(nb)::value>), grid, dim3(256), lds,
+                           st, b, rpc);
+    });
+  } else {
+    const size_t lds_q = (size_t)attn_chunk(a.N) * (D + 8) * 2 * 2 + (size_t)a.N * 4;
     KTimed kt(timer_name(2, a), st);
     const dim3 grid(xcd_grid((long)a.R * a.H * nqb));
     with_blocks(a.N / 32, [&](auto nb) {
