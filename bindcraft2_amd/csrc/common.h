@@ -56,18 +56,41 @@ __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-// Wave-level butterfly reductions over groups of lanes.
-template <int W>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+// DPP lane moves (gfx9 encodings): a VALU operand read from another lane of
+// the same 16-lane row, no LDS round trip.
+constexpr int DPP_QUAD_1032 = 0xB1;     // quad_perm [1,0,3,2]
+constexpr int DPP_QUAD_2301 = 0x4E;     // quad_perm [2,3,0,1]
+constexpr int DPP_ROW_HALF_MIRROR = 0x141;
+constexpr int DPP_ROW_MIRROR = 0x140;
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Reductions over aligned groups of W lanes (every lane of the group gets the
+// result).  Within a 16-lane row they are DPP steps: pairs, quads, the
+// half-row mirror (lane i <-> 7-i) and the row mirror (i <-> 15-i), each of
+// which pairs a partial with the complementary one; beyond 16 lanes, xor
+// shuffles.  Groups must be wholly active or wholly inactive.
+template <int W, class Op>
+__device__ __forceinline__ float group_reduce(float v, Op op) {
+  static_assert(W >= 1 && W <= 64 && (W & (W - 1)) == 0, "W: power of two <= 64");
+  if constexpr (W >= 2) v = op(v, dpp_mov<DPP_QUAD_1032>(v));
+  if constexpr (W >= 4) v = op(v, dpp_mov<DPP_QUAD_2301>(v));
+  if constexpr (W >= 8) v = op(v, dpp_mov<DPP_ROW_HALF_MIRROR>(v));
+  if constexpr (W >= 16) v = op(v, dpp_mov<DPP_ROW_MIRROR>(v));
+  if constexpr (W >= 32) v = op(v, __shfl_xor(v, 16, 64));
+  if constexpr (W >= 64) v = op(v, __shfl_xor(v, 32, 64));
   return v;
 }
 template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+  return group_reduce<W>(v, [](float a, float b) { return a + b; });
+}
+template <int W>
 __device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-  for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  return group_reduce<W>(v, [](float a, float b) { return fmaxf(a, b); });
 }
 
 // 16-byte vector load/store of 8 bf16 values.

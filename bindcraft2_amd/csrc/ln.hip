@@ -44,33 +44,6 @@ __device__ __forceinline__ long ln_src_row(long m, int nt) {
   return q * nt + p;
 }
 
-// Sum each of the H values v[0..H) over the TPR-lane group by halving
-// exchanges (reduce-scatter, H/2 + H/4 + ... shuffles instead of H full
-// butterflies); on return v[0] holds the group total of head `h`, the same in
-// every lane whose bits below the last exchanged bit differ.
-template <int TPR, int H>
-__device__ __forceinline__ float reduce_scatter(float (&v)[H], int lane, int& h) {
-  static_assert(H >= 1 && (H & (H - 1)) == 0 && H <= TPR, "H: power of two <= TPR");
-  int base = 0;
-  int bit = TPR / 2;
-#pragma unroll
-  for (int width = H; width > 1; width /= 2) {
-    const bool upper = (lane & bit) != 0;
-#pragma unroll
-    for (int j = 0; j < width / 2; ++j) {
-      const float send = upper ? v[j] : v[j + width / 2];
-      const float keep = upper ? v[j + width / 2] : v[j];
-      v[j] = keep + __shfl_xor(send, bit, 64);
-    }
-    base += upper ? width / 2 : 0;
-    bit /= 2;
-  }
-#pragma unroll
-  for (int b = bit; b >= 1; b /= 2) v[0] += __shfl_xor(v[0], b, 64);
-  h = base;
-  return v[0];
-}
-
 template <int H>
 __device__ __forceinline__ void load_w(const float* __restrict__ wb, int c0, float (&w)[8][H]) {
   const float4* p = reinterpret_cast<const float4*>(wb + c0 * H);
@@ -85,7 +58,10 @@ __device__ __forceinline__ void load_w(const float* __restrict__ wb, int c0, flo
 
 // H = 0: plain LayerNorm.  H in {4, 8}: also the pair-bias projection
 // bias_out[h][m] = bias_scale * sum_c y[m][c] W[c][h], from the f32 row.
-template <int C, bool FAST, class InT, int H>
+// A lane group handles U rows (RPB apart): all U rows are loaded before the
+// first is reduced, and gamma, beta and the projection slice are read once
+// per U rows.
+template <int C, bool FAST, class InT, int H, int U>
 __global__ __launch_bounds__(256) void ln_fwd_kernel(
     const InT* __restrict__ x, long M, int nt, const float* __restrict__ gamma,
     const float* __restrict__ beta, bf16* __restrict__ y,
@@ -93,62 +69,72 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(
     const float* __restrict__ wb, float* __restrict__ bias_out, float bias_scale) {
   using G = LnGeom<C>;
   const int t = threadIdx.x;
-  const long m = (long)blockIdx.x * G::RPB + t / G::TPR;
+  const long mb = (long)blockIdx.x * (U * G::RPB) + t / G::TPR;
   const int gl = t % G::TPR;
   const int c0 = gl * 8;
-  if (m >= M) return;  // whole lane groups exit together
-  float v[8], gm[8], bt[8];
-  load8f<InT>(x + ln_src_row(m, nt) * C + c0, v);
+  if (mb >= M) return;  // whole lane groups exit together
+  float v[U][8];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const long m = mb + (long)u * G::RPB;
+    if (m < M) load8f<InT>(x + ln_src_row(m, nt) * C + c0, v[u]);
+  }
+  float gm[8], bt[8];
   load8f<float>(gamma + c0, gm);
   load8f<float>(beta + c0, bt);
-  float s = 0.f, s2 = 0.f;
+  float w[8][H > 0 ? H : 1];
+  if constexpr (H > 0) load_w<H>(wb, c0, w);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) { s += v[e]; s2 += v[e] * v[e]; }
-  s = group_sum<G::TPR>(s);
-  const float mu = s / C;
-  float var;
-  if (FAST) {
-    s2 = group_sum<G::TPR>(s2);
-    var = s2 / C - mu * mu;
-  } else {
-    float d2 = 0.f;
+  for (int u = 0; u < U; ++u) {
+    const long m = mb + (long)u * G::RPB;
+    if (m >= M) break;  // uniform over the lane group
+    float s = 0.f, s2 = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) { const float d = v[e] - mu; d2 += d * d; }
-    var = group_sum<G::TPR>(d2) / C;
-  }
-  const float r = rsqrtf(var + LN_EPS);
-  float o[8];
-  bf16x8 ob;
+    for (int e = 0; e < 8; ++e) { s += v[u][e]; s2 += v[u][e] * v[u][e]; }
+    s = group_sum<G::TPR>(s);
+    const float mu = s / C;
+    float var;
+    if (FAST) {
+      s2 = group_sum<G::TPR>(s2);
+      var = s2 / C - mu * mu;
+    } else {
+      float d2 = 0.f;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    o[e] = (v[e] - mu) * r * gm[e] + bt[e];
-    ob[e] = (bf16)o[e];
-  }
-  if (y) st8(y + m * C + c0, ob);
-  if (gl == 0) {
-    if (mean_out) mean_out[m] = mu;
-    if (rstd_out) rstd_out[m] = r;
-  }
-  if constexpr (H > 0) {
-    float w[8][H], p[H];
-    load_w<H>(wb, c0, w);
-#pragma unroll
-    for (int h = 0; h < H; ++h) {
-      p[h] = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) p[h] += o[e] * w[e][h];
+      for (int e = 0; e < 8; ++e) { const float d = v[u][e] - mu; d2 += d * d; }
+      var = group_sum<G::TPR>(d2) / C;
     }
-    int h;
-    const float tot = reduce_scatter<G::TPR, H>(p, gl, h);
-    // the lanes that ended with the same head hold the same value; the one
-    // with the lowest index among them writes
-    constexpr int SPAN = G::TPR / H;  // lanes per head after the exchange
-    if ((gl % SPAN) == 0) bias_out[(long)h * M + m] = tot * bias_scale;
+    const float r = rsqrtf(var + LN_EPS);
+    float o[8];
+    bf16x8 ob;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      o[e] = (v[u][e] - mu) * r * gm[e] + bt[e];
+      ob[e] = (bf16)o[e];
+    }
+    if (y) st8(y + m * C + c0, ob);
+    if (gl == 0) {
+      if (mean_out) mean_out[m] = mu;
+      if (rstd_out) rstd_out[m] = r;
+    }
+    if constexpr (H > 0) {
+      static_assert(H <= G::TPR, "one lane per head writes");
+      float mine = 0.f;
+#pragma unroll
+      for (int h = 0; h < H; ++h) {
+        float p = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) p += o[e] * w[e][h];
+        p = group_sum<G::TPR>(p);
+        if (gl == h) mine = p;
+      }
+      if (gl < H) bias_out[(long)gl * M + m] = mine * bias_scale;
+    }
   }
 }
 
-// dx[src(m)] (+)= LN'(dy[m] + sum_h dbias[h][m] W[c][h])   (dy may be null)
-template <int C, class InT, bool ACC, int H>
+// dx[src(m)] (+)= LN'(dy[m] + sum_h dbias[h][m] W[c][h])   (dy may be null);
+// U rows per lane group, as the forward.
+template <int C, class InT, bool ACC, int H, int U>
 __global__ __launch_bounds__(256) void ln_bwd_kernel(
     const float* __restrict__ dy, const InT* __restrict__ x, long M, int nt,
     const float* __restrict__ gamma, const float* __restrict__ mean,
@@ -156,56 +142,65 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(
     const float* __restrict__ dbias, const float* __restrict__ wb) {
   using G = LnGeom<C>;
   const int t = threadIdx.x;
-  const long m = (long)blockIdx.x * G::RPB + t / G::TPR;
+  const long mb = (long)blockIdx.x * (U * G::RPB) + t / G::TPR;
   const int c0 = (t % G::TPR) * 8;
-  if (m >= M) return;
-  const long src = ln_src_row(m, nt);
-  float xv[8], g[8], gm[8];
-  load8f<InT>(x + src * C + c0, xv);
-  load8f<float>(gamma + c0, gm);
-  if (dy) {
-    load8f<float>(dy + m * C + c0, g);
-  } else {
+  if (mb >= M) return;
+  float xv[U][8], g[U][8], ov[U][8], mu[U], r[U];
+  float db[U][H > 0 ? H : 1];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) g[e] = 0.f;
-  }
-  if constexpr (H > 0) {
-    float w[8][H];
-    load_w<H>(wb, c0, w);
+  for (int u = 0; u < U; ++u) {
+    const long m = mb + (long)u * G::RPB;
+    if (m >= M) continue;
+    const long src = ln_src_row(m, nt);
+    load8f<InT>(x + src * C + c0, xv[u]);
+    if (dy) {
+      load8f<float>(dy + m * C + c0, g[u]);
+    } else {
 #pragma unroll
-    for (int h = 0; h < H; ++h) {
-      const float db = dbias[(long)h * M + m];
+      for (int e = 0; e < 8; ++e) g[u][e] = 0.f;
+    }
+    if (ACC) load8f<float>(dx + src * C + c0, ov[u]);
+    mu[u] = mean[m];
+    r[u] = rstd[m];
+    if constexpr (H > 0) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) g[e] += db * w[e][h];
+      for (int h = 0; h < H; ++h) db[u][h] = dbias[(long)h * M + m];
     }
   }
-  const float mu = mean[m], r = rstd[m];
-  float sg = 0.f, sgx = 0.f;
+  float gm[8];
+  load8f<float>(gamma + c0, gm);
+  float w[8][H > 0 ? H : 1];
+  if constexpr (H > 0) load_w<H>(wb, c0, w);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    xv[e] = (xv[e] - mu) * r;
-    g[e] *= gm[e];
-    sg += g[e];
-    sgx += g[e] * xv[e];
-  }
-  sg = group_sum<G::TPR>(sg) / C;
-  sgx = group_sum<G::TPR>(sgx) / C;
-  float* out = dx + src * C + c0;
-  float4 a, b;
-  float res[8];
+  for (int u = 0; u < U; ++u) {
+    const long m = mb + (long)u * G::RPB;
+    if (m >= M) break;
+    if constexpr (H > 0) {
 #pragma unroll
-  for (int e = 0; e < 8; ++e) res[e] = r * (g[e] - sg - xv[e] * sgx);
-  if (ACC) {
-    a = reinterpret_cast<float4*>(out)[0];
-    b = reinterpret_cast<float4*>(out)[1];
-    a.x += res[0]; a.y += res[1]; a.z += res[2]; a.w += res[3];
-    b.x += res[4]; b.y += res[5]; b.z += res[6]; b.w += res[7];
-  } else {
-    a = make_float4(res[0], res[1], res[2], res[3]);
-    b = make_float4(res[4], res[5], res[6], res[7]);
+      for (int h = 0; h < H; ++h)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) g[u][e] += db[u][h] * w[e][h];
+    }
+    float sg = 0.f, sgx = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      xv[u][e] = (xv[u][e] - mu[u]) * r[u];
+      g[u][e] *= gm[e];
+      sg += g[u][e];
+      sgx += g[u][e] * xv[u][e];
+    }
+    sg = group_sum<G::TPR>(sg) / C;
+    sgx = group_sum<G::TPR>(sgx) / C;
+    float* out = dx + ln_src_row(m, nt) * C + c0;
+    float res[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      res[e] = r[u] * (g[u][e] - sg - xv[u][e] * sgx);
+      if (ACC) res[e] += ov[u][e];
+    }
+    reinterpret_cast<float4*>(out)[0] = make_float4(res[0], res[1], res[2], res[3]);
+    reinterpret_cast<float4*>(out)[1] = make_float4(res[4], res[5], res[6], res[7]);
   }
-  reinterpret_cast<float4*>(out)[0] = a;
-  reinterpret_cast<float4*>(out)[1] = b;
 }
 
 // Channel-major input: x is [C][M] (one plane per channel).  A block of 64
@@ -338,17 +333,24 @@ __global__ __launch_bounds__(256) void ln_bwd_cm_kernel(
 
 // ------------------------------------------------------------------ launchers
 
+// Rows per lane group of the row-major kernels: several only where a bias
+// projection (weights in registers, H sums per row) is amortised over them;
+// a plain row keeps the register count, and so the occupancy, low.
+template <int H>
+constexpr int ln_rows() { return H > 0 ? 4 : 1; }
+
 template <int C, int H>
 static void ln_fwd_launch(hipStream_t st, const float* x, long M, int nt, const float* gamma,
                           const float* beta, bf16* y, float* mean, float* rstd, bool fast,
                           const float* wb, float* bias_out, float bs) {
-  const int grid = (int)((M + LnGeom<C>::RPB - 1) / LnGeom<C>::RPB);
+  constexpr int U = ln_rows<H>();
+  const int grid = (int)((M + U * LnGeom<C>::RPB - 1) / (U * LnGeom<C>::RPB));
   if (fast)
-    hipLaunchKernelGGL((ln_fwd_kernel<C, true, float, H>), dim3(grid), dim3(256), 0, st, x, M, nt,
-                       gamma, beta, y, mean, rstd, wb, bias_out, bs);
+    hipLaunchKernelGGL((ln_fwd_kernel<C, true, float, H, U>), dim3(grid), dim3(256), 0, st, x, M,
+                       nt, gamma, beta, y, mean, rstd, wb, bias_out, bs);
   else
-    hipLaunchKernelGGL((ln_fwd_kernel<C, false, float, H>), dim3(grid), dim3(256), 0, st, x, M, nt,
-                       gamma, beta, y, mean, rstd, wb, bias_out, bs);
+    hipLaunchKernelGGL((ln_fwd_kernel<C, false, float, H, U>), dim3(grid), dim3(256), 0, st, x, M,
+                       nt, gamma, beta, y, mean, rstd, wb, bias_out, bs);
 }
 
 template <int C>
@@ -379,13 +381,14 @@ template <int C, int H>
 static void ln_bwd_launch(hipStream_t st, const float* dy, const float* x, long M, int nt,
                           const float* gamma, const float* mean, const float* rstd, float* dx,
                           bool acc, const float* dbias, const float* wb) {
-  const int grid = (int)((M + LnGeom<C>::RPB - 1) / LnGeom<C>::RPB);
+  constexpr int U = ln_rows<H>();
+  const int grid = (int)((M + U * LnGeom<C>::RPB - 1) / (U * LnGeom<C>::RPB));
   if (acc)
-    hipLaunchKernelGGL((ln_bwd_kernel<C, float, true, H>), dim3(grid), dim3(256), 0, st, dy, x, M,
-                       nt, gamma, mean, rstd, dx, dbias, wb);
+    hipLaunchKernelGGL((ln_bwd_kernel<C, float, true, H, U>), dim3(grid), dim3(256), 0, st, dy, x,
+                       M, nt, gamma, mean, rstd, dx, dbias, wb);
   else
-    hipLaunchKernelGGL((ln_bwd_kernel<C, float, false, H>), dim3(grid), dim3(256), 0, st, dy, x, M,
-                       nt, gamma, mean, rstd, dx, dbias, wb);
+    hipLaunchKernelGGL((ln_bwd_kernel<C, float, false, H, U>), dim3(grid), dim3(256), 0, st, dy, x,
+                       M, nt, gamma, mean, rstd, dx, dbias, wb);
 }
 
 template <int C>
