@@ -107,38 +107,4 @@ void stack_keys(hipStream_t st, const uint32_t* seed, int depth, uint32_t* out, 
   hipLaunchKernelGGL(stack_keys_kernel, dim3(1), dim3(64), 0, st, seed, depth, n_used, out);
 }
 
-// -------------------------------------------------------------- residual glue
-// dd[m][c] = bf16(dy[src(m)][c] * tbl[(m % nt)*C + c])   (tbl may be null)
-__global__ void scale_rows_bf16_kernel(const float* __restrict__ dy, long M, int C,
-                                       int nt, bool transpose,
-                                       const float* __restrict__ tbl,
-                                       bf16* __restrict__ out) {
-  const long i8 = ((long)blockIdx.x * blockDim.x + threadIdx.x) * 8;
-  if (i8 >= M * C) return;
-  const long m = i8 / C;
-  const int c0 = (int)(i8 % C);
-  long src = m;
-  if (transpose) src = (m % nt) * nt + m / nt;
-  const float4 a = *reinterpret_cast<const float4*>(dy + src * C + c0);
-  const float4 b = *reinterpret_cast<const float4*>(dy + src * C + c0 + 4);
-  float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-  bf16x8 o;
-  if (tbl) {
-    const float* t = tbl + (m % nt) * C + c0;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = (bf16)(v[e] * t[e]);
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = (bf16)v[e];
-  }
-  st8(out + m * C + c0, o);
-}
-
-void scale_rows_bf16(hipStream_t st, const float* dy, long M, int C, int nt,
-                     bool transpose, const float* tbl, bf16* out) {
-  const long n8 = M * C / 8;
-  hipLaunchKernelGGL(scale_rows_bf16_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, st,
-                     dy, M, C, nt, transpose, tbl, out);
-}
-
 }  // namespace bc2n

@@ -1156,7 +1156,7 @@ template <int D>
 static void attn_bwd_t(hipStream_t st, const AttnBwdArgs& b) {
   const AttnArgs& a = b.f;
   const long tot = (long)a.R * a.N * a.H;
-  {
+  if (!b.gate_done) {
     KTimed kt(timer_name(1, a), st);
     const long per = 256 / (D / 8);
     hipLaunchKernelGGL((attn_gate_bwd_kernel<D>), dim3((unsigned)((tot + per - 1) / per)),
@@ -1208,7 +1208,8 @@ static void attn_bwd_t(hipStream_t st, const AttnBwdArgs& b) {
 
 void attn_bwd(hipStream_t st, const AttnBwdArgs& b) {
   attn_check(b.f);
-  if (!b.dog || !b.dO || !b.Dsum || !b.dqkvg) throw std::runtime_error("attention bwd: missing operand");
+  if ((!b.dog && !b.gate_done) || !b.dO || !b.Dsum || !b.dqkvg)
+    throw std::runtime_error("attention bwd: missing operand");
   if (b.f.D == 32) attn_bwd_t<32>(st, b);
   else attn_bwd_t<16>(st, b);
 }

@@ -74,6 +74,44 @@ struct EpiRows {
   __device__ __forceinline__ void col(int, int, int, const float (&)[8], const float*, int) const {}
 };
 
+// A-operand loaders.  The default reads bf16 A as the strides say; the
+// others build the K-contiguous A tile from f32 rows on the fly, so the
+// elementwise pass that would have written A to memory disappears.  A loader
+// with a side output (kSide) writes it as it loads, which is exact only when
+// every A element is loaded once: a single tile column (N <= BN), checked on
+// the host.
+struct ALoadDirect {
+  static constexpr bool kDirect = true;
+  static constexpr bool kSide = false;
+  __device__ __forceinline__ bf16x8 operator()(int, int, int) const { return bf16x8{}; }
+};
+
+// A[m][k] = bf16(src[src(m)][k] * tbl[(m % nt) * C + k]); src(m) transposes
+// the nt x nt grid when `transpose`; tbl may be null (no dropout).
+struct ALoadScaledRows {
+  static constexpr bool kDirect = false;
+  static constexpr bool kSide = false;
+  const float* src;
+  const float* tbl;
+  int nt, C;
+  bool transpose;
+  __device__ __forceinline__ bf16x8 operator()(int, int m, int k) const {
+    const long s = transpose ? (long)(m % nt) * nt + m / nt : m;
+    float v[8];
+    ld_f8(src + s * C + k, v);
+    if (tbl) {
+      float t[8];
+      ld_f8(tbl + (long)(m % nt) * C + k, t);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] *= t[e];
+    }
+    bf16x8 r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = (bf16)v[e];
+    return r;
+  }
+};
+
 template <int BM, int BN, int BK>
 struct GemmSmem {
   static constexpr int LDK = BK + 8;
@@ -83,8 +121,8 @@ struct GemmSmem {
   static constexpr int BYTES = AB > T ? AB : T;
 };
 
-template <int BM, int BN, int BK, bool AK, bool BKC, class Epi>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi) {
+template <int BM, int BN, int BK, bool AK, bool BKC, class Epi, class AL = ALoadDirect>
+__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi, AL al = AL{}) {
   using SM = GemmSmem<BM, BN, BK>;
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int TM = WM / 16, TN = WN / 16;
@@ -121,7 +159,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi) {
       if constexpr (AK) {
         const int row = c / (BK / 8), kc = (c % (BK / 8)) * 8;
         const int m = m0 + row;
-        ra[p] = (m < M) ? ld8(A + (long)m * g.a_sm + k0 + kc) : zero8;
+        if constexpr (AL::kDirect) ra[p] = (m < M) ? ld8(A + (long)m * g.a_sm + k0 + kc) : zero8;
+        else ra[p] = (m < M) ? al(b, m, k0 + kc) : zero8;
       } else {
         const int k = c / (BM / 8), mc = (c % (BM / 8)) * 8;
         const int m = m0 + mc;
@@ -252,9 +291,14 @@ inline void gemm_check(bool ok, const char* what) {
 }
 
 // Launch with tile BM x BN; picks the loader form from the strides and BK
-// from K.  Shapes are validated here, on the host, before any launch.
-template <int BM, int BN, class Epi>
-void gemm(hipStream_t st, const GemmArgs& g, const Epi& epi, const char* name = "gemm") {
+// from K.  Shapes are validated here, on the host, before any launch.  With a
+// loader other than ALoadDirect, A is K-contiguous by construction (g.A is
+// not read; a_sk must be 1).
+template <int BM, int BN, class Epi, class AL = ALoadDirect>
+void gemm(hipStream_t st, const GemmArgs& g, const Epi& epi, const char* name = "gemm",
+          const AL& al = AL{}) {
+  if constexpr (!AL::kDirect) gemm_check(g.a_sk == 1, "A loader: K-contiguous A");
+  if constexpr (AL::kSide) gemm_check(g.N <= BN && g.batch == 1, "A loader side output: one tile column");
   gemm_check(g.M > 0 && g.N > 0 && g.K > 0 && g.batch > 0, "empty shape");
   gemm_check(g.K % 32 == 0, "K must be a multiple of 32");
   gemm_check(g.N % 8 == 0, "N must be a multiple of 8 (vector epilogue)");
@@ -263,7 +307,7 @@ void gemm(hipStream_t st, const GemmArgs& g, const Epi& epi, const char* name = 
   gemm_check(ak || g.a_sm == 1, "A needs a unit stride");
   gemm_check(bk || g.b_sn == 1, "B needs a unit stride");
   auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
-  gemm_check(al16(g.A) && al16(g.B), "operands must be 16-byte aligned");
+  gemm_check((!AL::kDirect || al16(g.A)) && al16(g.B), "operands must be 16-byte aligned");
   if (ak) gemm_check(g.a_sm % 8 == 0, "A row stride must be a multiple of 8");
   else gemm_check(g.a_sk % 8 == 0, "A(T) stride must be a multiple of 8");
   if (bk) gemm_check(g.b_sn % 8 == 0, "B row stride must be a multiple of 8");
@@ -274,7 +318,7 @@ void gemm(hipStream_t st, const GemmArgs& g, const Epi& epi, const char* name = 
   const bool k64 = (g.K % 64 == 0);
   KTimed kt(name, st);
 #define BC2N_GEMM_LAUNCH(BKV, AKV, BKCV) \
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, BKV, AKV, BKCV, Epi>), grid, block, 0, st, g, epi)
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, BKV, AKV, BKCV, Epi, AL>), grid, block, 0, st, g, epi, al)
   if (k64) {
     if (ak && bk) BC2N_GEMM_LAUNCH(64, true, true);
     else if (ak) BC2N_GEMM_LAUNCH(64, true, false);
@@ -372,6 +416,45 @@ struct EpiResidualRows : EpiRows {
 #pragma unroll
     for (int e = 0; e < 8; ++e) r[e] += x[e];
     st_f8(out + src * C + n, r);
+  }
+};
+
+// Backward through attention's output gate, fused into the GEMM that makes
+// d(og) = acc (og = o * sigmoid(g)):  dO = d(og) s,  dG = d(og) o s (1 - s),
+// s = sigmoid(g), and Dsum[r][h][q] = sum over head h's D columns of dO * o
+// for token m = r * Ntok + q.  The D/8 row-mode calls of one head come from
+// consecutive lanes (8 columns each), which add their partials by DPP.
+struct EpiGateBwd : EpiRows {
+  const bf16* qkvg;  // gate pre-activation at column 3*HD + n of row m
+  long ld;
+  const bf16* o;     // ungated attention output [M][HD]
+  bf16* dO;          // [M][HD]
+  bf16* dqkvg;       // dG at column 3*HD + n
+  float* Dsum;       // [R][H][Ntok]
+  int HD, H, D, Ntok;
+  template <int W>
+  __device__ __forceinline__ float head_sum(float s) const { return group_sum<W>(s); }
+  __device__ __forceinline__ void row(int, int m, int n, const float (&v)[8]) const {
+    const bf16x8 gv = ld8(qkvg + (long)m * ld + 3 * HD + n);
+    const bf16x8 ov = ld8(o + (long)m * HD + n);
+    bf16x8 dov, dgv;
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float sg = sigmoidf_((float)gv[e]);
+      const float oo = (float)ov[e];
+      const float d = v[e] * sg;
+      dov[e] = (bf16)d;
+      dgv[e] = (bf16)(v[e] * oo * sg * (1.f - sg));
+      s += d * oo;
+    }
+    st8(dO + (long)m * HD + n, dov);
+    st8(dqkvg + (long)m * ld + 3 * HD + n, dgv);
+    s = D == 32 ? head_sum<4>(s) : head_sum<2>(s);
+    if (n % D == 0) {
+      const int r = m / Ntok, q = m % Ntok;
+      Dsum[((long)r * H + n / D) * Ntok + q] = s;
+    }
   }
 };
 

@@ -56,6 +56,9 @@ struct AttnBwdArgs {
   float* dbias = nullptr;      // out: [H][N][N] (natural units), or null
   float scale = 1.f;           // D^-1/2 (q scaling applied in the forward)
   int rows_per_chunk = 8;
+  // dO, Dsum and the gate gradient already written by the caller (the
+  // d(og) GEMM's EpiGateBwd epilogue); dog is then not read
+  bool gate_done = false;
 };
 void attn_bwd(hipStream_t st, const AttnBwdArgs& a);
 int attn_bwd_nchunk(int R, int rows_per_chunk);
@@ -86,11 +89,5 @@ void stack_keys(hipStream_t st, const uint32_t* seed, int depth, uint32_t* out,
                 int n_used = 9);
 // out[0..1] = (0, seed[0]): PRNGKey of a 32-bit seed word, on the device.
 void key_from_bits(hipStream_t st, const uint32_t* seed, uint32_t* out);
-
-// ---------------------------------------------------------------- glue
-// out[m][c] = bf16(dy[src(m)][c] * tbl[(m % nt)*C + c]); src transposes the
-// N x N grid when `transpose`; tbl may be null (no dropout).
-void scale_rows_bf16(hipStream_t st, const float* dy, long M, int C, int nt,
-                     bool transpose, const float* tbl, bf16* out);
 
 }  // namespace bc2n

@@ -251,15 +251,17 @@ void out_gemm(hipStream_t st, const AttnW& w, long rows, const bf16* og, const f
   gemm<128, 128>(st, g, EpiResidualRows(in, out, w.bo, tbl, nt, w.Cout, false), name);
 }
 
-// d(og) = dd . Wo^T and, after the attention backward, d(xn) = dqkvg . Wcat^T
-void dout_gemm(hipStream_t st, const AttnW& w, long rows, const bf16* dd, bf16* dog,
-               const char* name) {
+// d(og) = (tbl * dout) . Wo^T, the dropout scale applied as A is loaded,
+// with epilogue `epi`; after the attention backward, d(xn) = dqkvg . Wcat^T
+template <class Epi>
+void dout_gemm(hipStream_t st, const AttnW& w, long rows, const float* dout, const float* tbl,
+               int nt, const Epi& epi, const char* name) {
   const int HD = w.H * w.D;
   GemmArgs g;
   g.M = (int)rows; g.N = HD; g.K = w.Cout;
-  g.A = dd; g.a_sm = w.Cout; g.a_sk = 1;
+  g.a_sm = w.Cout; g.a_sk = 1;
   g.B = w.wo; g.b_sn = w.Cout; g.b_sk = 1;
-  gemm<128, 128>(st, g, EpiStore<bf16>{dog, HD, 0, nullptr, HD}, name);
+  gemm<128, 128>(st, g, epi, name, ALoadScaledRows{dout, tbl, nt, w.Cout, false});
 }
 
 void dx_gemm(hipStream_t st, const AttnW& w, long rows, const bf16* dqkvg, float* dxn,
@@ -359,8 +361,6 @@ void msarow_bwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa
   Arena& ar = arena();
   std::lock_guard<std::recursive_mutex> lk(ar.lock());
   Sizer need;
-  need.take<bf16>((size_t)R * Cm);
-  need.take<bf16>((size_t)R * HD);
   need.take<bf16>((size_t)R * HD);
   need.take<float>((size_t)S * H * N);
   need.take<bf16>((size_t)R * 4 * HD);
@@ -368,19 +368,17 @@ void msarow_bwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa
   need.take<float>((size_t)H * M);
   need.take<float>((size_t)R * Cm);
   ar.reset(st, need.off);
-  bf16* dd = ar.take_n<bf16>((size_t)R * Cm);
-  bf16* dog = ar.take_n<bf16>((size_t)R * HD);
   b.dO = ar.take_n<bf16>((size_t)R * HD);
   b.Dsum = ar.take_n<float>((size_t)S * H * N);
   b.dqkvg = ar.take_n<bf16>((size_t)R * 4 * HD);
   b.dbias_part = ar.take_n<float>((size_t)nch * H * M);
   b.dbias = ar.take_n<float>((size_t)H * M);
   float* dxn = ar.take_n<float>((size_t)R * Cm);
-  {
-    KTimed kt("msarow.dropout_bwd", st);
-    scale_rows_bf16(st, dmsa_out, R, Cm, N, false, tbl, dd);
-  }
-  dout_gemm(st, a, R, dd, dog, "msarow.gemm_dout");
+  EpiGateBwd eg;
+  eg.qkvg = sv.qkvg; eg.ld = 4L * HD; eg.o = sv.o; eg.dO = b.dO; eg.dqkvg = b.dqkvg;
+  eg.Dsum = b.Dsum; eg.HD = HD; eg.H = H; eg.D = a.D; eg.Ntok = N;
+  dout_gemm(st, a, R, dmsa_out, tbl, N, eg, "msarow.gemm_dout");
+  b.gate_done = true;
   AttnArgs& at = b.f;
   at.R = S; at.H = H; at.N = N; at.D = a.D;
   at.qkvg = sv.qkvg; at.ld = 4L * HD;
@@ -389,7 +387,6 @@ void msarow_bwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa
   at.o = sv.o; at.og = nullptr; at.ldo = HD;
   at.lse = sv.lse;
   at.site = 1;
-  b.dog = dog;
   b.scale = 1.f / std::sqrt((float)a.D);
   attn_bwd(st, b);
   dx_gemm(st, a, R, b.dqkvg, dxn, "msarow.gemm_dx");
@@ -445,20 +442,14 @@ void msacol_bwd(hipStream_t st, const MsaColW& w, int S, int N, const float* msa
   Arena& ar = arena();
   std::lock_guard<std::recursive_mutex> lk(ar.lock());
   Sizer need;
-  need.take<bf16>((size_t)R * Cm);
   need.take<bf16>((size_t)R * HD);
   need.take<bf16>((size_t)R * 4 * HD);
   need.take<float>((size_t)R * Cm);
   ar.reset(st, need.off);
-  bf16* dd = ar.take_n<bf16>((size_t)R * Cm);
   bf16* dog = ar.take_n<bf16>((size_t)R * HD);
   bf16* dqkvg = ar.take_n<bf16>((size_t)R * 4 * HD);
   float* dxn = ar.take_n<float>((size_t)R * Cm);
-  {
-    KTimed kt("msacol.dropout_bwd", st);
-    scale_rows_bf16(st, dmsa_out, R, Cm, N, false, tbl, dd);
-  }
-  dout_gemm(st, a, R, dd, dog, "msacol.gemm_dout");
+  dout_gemm(st, a, R, dmsa_out, tbl, N, EpiStore<bf16>{dog, HD, 0, nullptr, HD}, "msacol.gemm_dout");
   {
     KTimed kt("msacol.attn_bwd", st);
     hipLaunchKernelGGL(small_attn_bwd_kernel, dim3(N * H), dim3(64), 0, st, sv.qkvg, 4L * HD, S, N,

@@ -1,8 +1,8 @@
 // Transition (pair and MSA), forward and backward.
 //   LN -> GEMM (C -> F*C) + bias + relu (hidden kept, bf16)
 //      -> GEMM (F*C -> C) + bias, fused residual (+ shared dropout table)
-// Backward: dd = tbl*dout; dh = (dd . W2^T) * (h > 0); dxn = dh . W1^T;
-// LN backward accumulated into din.
+// Backward: dh = ((tbl*dout) . W2^T) * (h > 0), the dropout scale applied as
+// the GEMM loads A; dxn = dh . W1^T; LN backward accumulated into din.
 // Reference: modules.py:252-305 (Transition); native/transition.cuh:313-675.
 #include "gemm.h"
 #include "modules.h"
@@ -86,22 +86,18 @@ void transition_bwd(hipStream_t st, const TransW& w, long rows, int nt, const fl
   Arena& ar = arena();
   std::lock_guard<std::recursive_mutex> lk(ar.lock());
   Sizer need;
-  need.take<bf16>((size_t)rows * C);
   need.take<bf16>((size_t)rows * H);
   need.take<float>((size_t)rows * C);
   ar.reset(st, need.off);
-  bf16* dd = ar.take_n<bf16>((size_t)rows * C);
   bf16* dh = ar.take_n<bf16>((size_t)rows * H);
   float* dxn = ar.take_n<float>((size_t)rows * C);
-  {
-    KTimed kt("trans.dropout_bwd", st);
-    scale_rows_bf16(st, dout, rows, C, nt, false, tbl, dd);
-  }
+  // dH = ((tbl * dout) . W2^T) * (H > 0), the dropout scale applied as A is loaded
   GemmArgs g1;
   g1.M = (int)rows; g1.N = H; g1.K = C;
-  g1.A = dd; g1.a_sm = C; g1.a_sk = 1;
+  g1.a_sm = C; g1.a_sk = 1;
   g1.B = w.w2; g1.b_sn = C; g1.b_sk = 1;
-  gemm<128, 128>(st, g1, EpiReluMask(dh, sv.h, H), "trans.gemm_dh");
+  gemm<128, 128>(st, g1, EpiReluMask(dh, sv.h, H), "trans.gemm_dh",
+                 ALoadScaledRows{dout, tbl, nt, C, false});
   GemmArgs g2;
   g2.M = (int)rows; g2.N = C; g2.K = H;
   g2.A = dh; g2.a_sm = H; g2.a_sk = 1;

@@ -6,9 +6,9 @@
 //   flash attention (mask per row/key, bias per head)               -> o, og, lse
 //   GEMM og . Wo + bo, fused residual + shared dropout (+ transposed write)
 // Backward replays nothing: the save-set holds LN stats, bias, qkvg, o, lse.
-//   dd = tbl * dout                       (transposed read for ending node)
-//   GEMM dd . Wo^T                        -> d(og)
-//   attention backward                    -> dq|dk|dv|dg, d(bias)
+//   GEMM (tbl * dout) . Wo^T, the scale applied as A is loaded (transposed
+//        read for the ending node), epilogue through the gate -> dO, dG, Dsum
+//   attention backward                    -> dq|dk|dv, d(bias)
 //   GEMM dqkvg . [Wq|Wk|Wv|Wg]^T          -> d(xn)
 //   LN backward (+ d(bias) . W2d^T) accumulated into din
 // Reference: modules.py:675-734 (TriangleAttention), :313-400 (Attention),
@@ -155,8 +155,6 @@ void triattn_bwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
   Arena& ar = arena();
   std::lock_guard<std::recursive_mutex> lk(ar.lock());
   Sizer need;
-  need.take<bf16>((size_t)M * C);            // dd
-  need.take<bf16>((size_t)M * HD);           // dog
   need.take<bf16>((size_t)M * HD);           // dO
   need.take<float>((size_t)H * M);           // Dsum
   need.take<bf16>((size_t)M * 4 * HD);       // dqkvg
@@ -164,8 +162,6 @@ void triattn_bwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
   need.take<float>((size_t)H * M);           // dbias
   need.take<float>((size_t)M * C);           // dxn
   ar.reset(st, need.off);
-  bf16* dd = ar.take_n<bf16>((size_t)M * C);
-  bf16* dog = ar.take_n<bf16>((size_t)M * HD);
   b.dO = ar.take_n<bf16>((size_t)M * HD);
   b.Dsum = ar.take_n<float>((size_t)H * M);
   b.dqkvg = ar.take_n<bf16>((size_t)M * 4 * HD);
@@ -173,15 +169,17 @@ void triattn_bwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
   b.dbias = ar.take_n<float>((size_t)H * M);
   float* dxn = ar.take_n<float>((size_t)M * C);
 
-  {
-    KTimed kt("triattn.dropout_bwd", st);
-    scale_rows_bf16(st, dout, M, C, N, per_column, tbl, dd);
-  }
+  // d(og) = (tbl * dout) . Wo^T, the dropout scale applied as A is loaded;
+  // the epilogue continues through the gate (dO, dG, Dsum)
   GemmArgs g1;
   g1.M = (int)M; g1.N = HD; g1.K = C;
-  g1.A = dd; g1.a_sm = C; g1.a_sk = 1;
+  g1.a_sm = C; g1.a_sk = 1;
   g1.B = w.wo; g1.b_sn = C; g1.b_sk = 1;
-  gemm<128, 128>(st, g1, EpiStore<bf16>{dog, HD, 0, nullptr, HD}, "triattn.gemm_dout");
+  EpiGateBwd eg;
+  eg.qkvg = sv.qkvg; eg.ld = 4L * HD; eg.o = sv.o; eg.dO = b.dO; eg.dqkvg = b.dqkvg;
+  eg.Dsum = b.Dsum; eg.HD = HD; eg.H = H; eg.D = w.D; eg.Ntok = N;
+  gemm<128, 128>(st, g1, eg, "triattn.gemm_dout", ALoadScaledRows{dout, tbl, N, C, per_column});
+  b.gate_done = true;
 
   AttnArgs& a = b.f;
   a.R = N; a.H = H; a.N = N; a.D = w.D;
@@ -192,7 +190,6 @@ void triattn_bwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
   a.bias = sv.bias;
   a.o = sv.o; a.og = nullptr; a.ldo = HD;
   a.lse = sv.lse;
-  b.dog = dog;
   b.scale = 1.f / std::sqrt((float)w.D);
   attn_bwd(st, b);
 

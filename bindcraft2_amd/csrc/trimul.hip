@@ -125,22 +125,40 @@ struct TriMulSave {
   }
 };
 
-// dd = tbl*dout; do = dd*g_out (bf16, GEMM operand);
-// dcat[m][4I + c] = dd * o * g(1-g)   (gating_linear pre-activation grad)
-__global__ void trimul_out_bwd_kernel(const float* __restrict__ dout, const float* __restrict__ tbl,
-                                      const bf16* __restrict__ gout, const bf16* __restrict__ osave,
-                                      bf16* __restrict__ dob, bf16* __restrict__ dcat, long M,
-                                      int C, int ldcat, int off, int nt) {
-  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= M * C) return;
-  const long m = i / C;
-  const int c = (int)(i % C);
-  float d = dout[i];
-  if (tbl) d *= tbl[(m % nt) * C + c];
-  const float g = (float)gout[i], o = (float)osave[i];
-  dob[i] = (bf16)(d * g);
-  dcat[m * ldcat + off + c] = (bf16)(d * o * g * (1.f - g));
-}
+// A loader of the output-projection backward GEMM: d = tbl*dout;
+// A = d*g_out (the GEMM operand) and, as a side output,
+// dcat[m][off + c] = d * o * g(1-g)   (gating_linear pre-activation grad).
+struct ALoadTrimulOut {
+  static constexpr bool kDirect = false;
+  static constexpr bool kSide = true;
+  const float* dout;
+  const float* tbl;
+  const bf16* gout;
+  const bf16* osave;
+  bf16* dcat;
+  int C, ldcat, off, nt;
+  __device__ __forceinline__ bf16x8 operator()(int, int m, int k) const {
+    const long i = (long)m * C + k;
+    float d[8], gv[8], ov[8];
+    ld_f8(dout + i, d);
+    if (tbl) {
+      float t[8];
+      ld_f8(tbl + (long)(m % nt) * C + k, t);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) d[e] *= t[e];
+    }
+    ld_b8f(gout + i, gv);
+    ld_b8f(osave + i, ov);
+    bf16x8 a, dc;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      a[e] = (bf16)(d[e] * gv[e]);
+      dc[e] = (bf16)(d[e] * ov[e] * gv[e] * (1.f - gv[e]));
+    }
+    st8(dcat + (long)m * ldcat + off + k, dc);
+    return a;
+  }
+};
 
 // From channel-major dleft/dright and the kept pre-activations, write the
 // row-major [M][4I+C] gradient of the projection GEMM's output columns:
@@ -315,7 +333,6 @@ void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
   Arena& ar = arena();
   std::lock_guard<std::recursive_mutex> lk(ar.lock());
   Sizer need;
-  need.take<bf16>((size_t)M * C);   // do
   need.take<bf16>((size_t)M * NC);  // dcat
   need.take<float>((size_t)M * I);  // dTn
   need.take<bf16>((size_t)M * I);   // dT
@@ -323,7 +340,6 @@ void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
   need.take<bf16>((size_t)M * I);   // dR
   need.take<float>((size_t)M * C);  // dxn
   ar.reset(st, need.off);
-  bf16* dob = ar.take_n<bf16>((size_t)M * C);
   bf16* dcat = ar.take_n<bf16>((size_t)M * NC);
   float* dtn = ar.take_n<float>((size_t)M * I);
   bf16* dT = ar.take_n<bf16>((size_t)M * I);
@@ -331,17 +347,14 @@ void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
   bf16* dR = ar.take_n<bf16>((size_t)M * I);
   float* dxn = ar.take_n<float>((size_t)M * C);
 
-  {
-    KTimed kt("trimul.out_bwd", st);
-    const long n = M * C;
-    hipLaunchKernelGGL(trimul_out_bwd_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                       dout, tbl, sv.gout, sv.osave, dob, dcat, M, C, NC, 4 * I, N);
-  }
+  // d(tn) = (tbl*dout*g_out) . Wo^T, the operand built as the GEMM loads it;
+  // the loader also writes the gating_linear columns of dcat
   GemmArgs g1;
   g1.M = (int)M; g1.N = I; g1.K = C;
-  g1.A = dob; g1.a_sm = C; g1.a_sk = 1;
+  g1.a_sm = C; g1.a_sk = 1;
   g1.B = w.wo; g1.b_sn = C; g1.b_sk = 1;
-  gemm<128, 128>(st, g1, EpiStore<float>{dtn, I, 0, nullptr, I}, "trimul.gemm_dout");
+  gemm<128, 128>(st, g1, EpiStore<float>{dtn, I, 0, nullptr, I}, "trimul.gemm_dout",
+                 ALoadTrimulOut{dout, tbl, sv.gout, sv.osave, dcat, C, NC, 4 * I, N});
   {
     KTimed kt("trimul.ln_center_bwd", st);
     ln_bwd_cm(st, dtn, sv.T, M, I, w.cn_g, sv.cmean, sv.crstd, dT);
