@@ -21,6 +21,7 @@
 #include "runtime.h"
 #include <stdexcept>
 #include <string>
+#include <type_traits>
 
 namespace bc2n {
 
@@ -66,6 +67,14 @@ template <>
 __device__ __forceinline__ void ld_any8<float>(const float* p, float (&v)[8]) { ld_f8(p, v); }
 template <>
 __device__ __forceinline__ void ld_any8<bf16>(const bf16* p, float (&v)[8]) { ld_b8f(p, v); }
+
+// An epilogue with kTwoPhase = true runs both modes on a column-mode tile:
+// first `col` (which may rewrite the staged tile through its pointer), then,
+// after a barrier, `row` over the rewritten tile.
+template <class E, class = void>
+struct epi_two_phase : std::false_type {};
+template <class E>
+struct epi_two_phase<E, std::void_t<decltype(E::kTwoPhase)>> : std::bool_constant<E::kTwoPhase> {};
 
 // Base of every epilogue: row mode only.
 struct EpiRows {
@@ -262,18 +271,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi, AL al = 
     }
     __syncthreads();
     const int mb = m0 + pass * WM;
-    if (colm) {
-      for (int it = tid; it < BN * (WM / 8); it += 256) {
-        const int c = it % BN, rg = it / BN;
-        const int m = mb + rg * 8, n = n0 + c;
-        if (m >= M || n >= N) continue;
-        const float* tp = T + (rg * 8) * LDT + c;
-        float v[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = tp[e * LDT];
-        epi.col(b, m, n, v, tp, LDT);
-      }
-    } else {
+    auto rows = [&]() {
       for (int it = tid; it < WM * (BN / 8); it += 256) {
         const int r = it / (BN / 8), c8 = (it % (BN / 8)) * 8;
         const int m = mb + r, n = n0 + c8;
@@ -282,6 +280,24 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi, AL al = 
         ld_f8(T + r * LDT + c8, v);
         epi.row(b, m, n, v);
       }
+    };
+    if (colm) {
+      for (int it = tid; it < BN * (WM / 8); it += 256) {
+        const int c = it % BN, rg = it / BN;
+        const int m = mb + rg * 8, n = n0 + c;
+        if (m >= M || n >= N) continue;
+        float* tp = T + (rg * 8) * LDT + c;
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = tp[e * LDT];
+        epi.col(b, m, n, v, tp, LDT);
+      }
+      if constexpr (epi_two_phase<Epi>::value) {
+        __syncthreads();  // the column pass has rewritten the tile
+        rows();
+      }
+    } else {
+      rows();
     }
   }
 }

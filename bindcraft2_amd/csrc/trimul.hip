@@ -6,12 +6,15 @@
 //   GEMM xn . Wcat  (Wcat = [proj|gate] channel pairs interleaved in 16-wide
 //        blocks, then gating_linear), fused epilogue:
 //          a = mask * proj * sigmoid(gate)   -> left/right planes [I][N*N] bf16
-//          proj, gate pre-activations kept (channel-major) for the backward
 //          g_out = sigmoid(gating_linear)  -> [M][C] bf16
+//        (xn is kept; the backward recomputes the proj/gate pre-activations)
 //   batched MFMA GEMM over the I channels (plane layouts pick out/in)  -> T f32
 //   centre LN (fast variance) reading the channel-major T            -> Tn bf16
 //   GEMM Tn . Wo + bo, fused: o kept, out = in + tbl * (o * g_out)
-// Backward: the exact reverse with the contraction's two transposed GEMMs.
+// Backward: the exact reverse with the contraction's two transposed GEMMs; the
+// projection's gradient comes from a GEMM that recomputes the pre-activations
+// from xn and turns them, with d(left|right), into the [proj|gate] columns of
+// d(cat) in its epilogue.
 // Reference: modules.py:1044-1088 (_fused_triangle_multiplication), :909-919
 // (fast-variance LN); native/trimul_body.cuh:1183-1796 (TriMul).
 #include "gemm.h"
@@ -28,13 +31,11 @@ __host__ __device__ inline int col_gate(int ch) { return (ch / 16) * 32 + 16 + c
 // Projection epilogue.  Tiles of the [proj|gate] columns (n0 < 4I) run in
 // column mode: the thread of a proj column reads its gate column (16 to the
 // right, same tile) from LDS and writes 8 consecutive m of the channel-major
-// planes: a = mask * proj * sigmoid(gate) into left/right, proj and gate
-// pre-activations into psave/gsave.  Tiles of gating_linear columns run in
-// row mode: g_out[m][c] = sigmoid(acc + b).
+// planes: a = mask * proj * sigmoid(gate) into left/right.  Tiles of
+// gating_linear columns run in row mode: g_out[m][c] = sigmoid(acc + b).
 struct EpiTrimulProj {
   static constexpr bool kHasCol = true;
   bf16 *left, *right;   // [I][M]
-  bf16 *psave, *gsave;  // [2I][M] pre-activations
   bf16* gout;           // [M][C]
   const float *bp, *bg, *bgl, *mask;
   long M;
@@ -54,8 +55,6 @@ struct EpiTrimulProj {
       gv[e] = tp[e * ldt + 16] + bgv;
       av[e] = mk[e] * pv[e] * sigmoidf_(gv[e]);
     }
-    st_b8f(psave + (long)ch * M + m, pv);
-    st_b8f(gsave + (long)ch * M + m, gv);
     if (ch < I) st_b8f(left + (long)ch * M + m, av);
     else st_b8f(right + (long)(ch - I) * M + m, av);
   }
@@ -108,7 +107,7 @@ struct EpiTrimulOut : EpiRows {
 template <class A>
 struct TriMulSave {
   float *mean, *rstd, *cmean, *crstd, *T;
-  bf16 *left, *right, *psave, *gsave, *gout, *osave;
+  bf16 *xn, *left, *right, *gout, *osave;
   TriMulSave(A& a, int N, int C, int I) {
     const size_t M = (size_t)N * N;
     mean = a.template take<float>(M);
@@ -116,12 +115,49 @@ struct TriMulSave {
     cmean = a.template take<float>(M);
     crstd = a.template take<float>(M);
     T = a.template take<float>(M * I);
+    xn = a.template take<bf16>(M * C);
     left = a.template take<bf16>(M * I);
     right = a.template take<bf16>(M * I);
-    psave = a.template take<bf16>(M * 2 * I);
-    gsave = a.template take<bf16>(M * 2 * I);
     gout = a.template take<bf16>(M * C);
     osave = a.template take<bf16>(M * C);
+  }
+};
+
+// Backward of the projection, as the epilogue of the GEMM xn . Wcat[:, :4I]
+// that recomputes the [proj|gate] pre-activations.  Column pass: the thread of
+// a proj column takes its gate column (16 to the right) from the staged tile
+// and d(left|right) for 8 consecutive m (channel-major), and rewrites both
+// columns of the tile with
+//   dproj = da * mask * s,  dgate = da * mask * p * s(1-s),  s = sigmoid(gate);
+// row pass: the rewritten tile goes to the row-major d(cat) columns.
+struct EpiTrimulProjBwd {
+  static constexpr bool kHasCol = true;
+  static constexpr bool kTwoPhase = true;
+  const bf16 *dl, *dr;  // [I][M]
+  const float *bp, *bg, *mask;
+  bf16* dcat;           // [M][ldcat]
+  long M;
+  int I, ldcat;
+  __device__ __forceinline__ bool col_mode(int) const { return true; }
+  __device__ __forceinline__ void col(int, int m, int n, const float (&v)[8], float* tp,
+                                      int ldt) const {
+    if ((n & 31) >= 16) return;  // gate column: done by its projection column
+    const int ch = (n >> 5) * 16 + (n & 15);
+    const float bpv = bp[ch], bgv = bg[ch];
+    float mk[8], da[8];
+    ld_f8(mask + m, mk);
+    ld_b8f((ch < I ? dl + (long)ch * M : dr + (long)(ch - I) * M) + m, da);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float pv = v[e] + bpv;
+      const float sg = sigmoidf_(tp[e * ldt + 16] + bgv);
+      const float a = da[e] * mk[e];
+      tp[e * ldt] = a * sg;
+      tp[e * ldt + 16] = a * pv * sg * (1.f - sg);
+    }
+  }
+  __device__ __forceinline__ void row(int, int m, int n, const float (&v)[8]) const {
+    st_b8f(dcat + (long)m * ldcat + n, v);
   }
 };
 
@@ -159,56 +195,6 @@ struct ALoadTrimulOut {
     return a;
   }
 };
-
-// From channel-major dleft/dright and the kept pre-activations, write the
-// row-major [M][4I+C] gradient of the projection GEMM's output columns:
-//   dproj = da * mask * s,  dgate = da * mask * p * s(1-s),  s = sigmoid(gate)
-// A block handles 32 rows: each thread reads 8 consecutive rows of one channel
-// (16-byte loads), the transposed writes go through LDS.  Requires M % 8 == 0.
-__global__ __launch_bounds__(256) void trimul_proj_bwd_kernel(
-    const bf16* __restrict__ dl, const bf16* __restrict__ dr, const bf16* __restrict__ psave,
-    const bf16* __restrict__ gsave, const float* __restrict__ mask, bf16* __restrict__ dcat,
-    long M, int I, int ldcat) {
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
-  constexpr int R = 32;
-  const int W = 4 * I;                 // columns of the tile
-  const int LD = W + 8;
-  bf16* tile = reinterpret_cast<bf16*>(smem_raw);  // [R][LD]
-  const long m0 = (long)blockIdx.x * R;
-  const int t = threadIdx.x;
-  for (int idx = t; idx < 2 * I * (R / 8); idx += 256) {
-    const int ch = idx / (R / 8), r0 = (idx % (R / 8)) * 8;
-    const long m = m0 + r0;
-    bf16x8 dp8 = {}, dg8 = {};
-    if (m < M) {
-      const bf16x8 da = ld8((ch < I ? dl + (long)ch * M : dr + (long)(ch - I) * M) + m);
-      const bf16x8 gv = ld8(gsave + (long)ch * M + m);
-      const bf16x8 pv = ld8(psave + (long)ch * M + m);
-      const float4 mk0 = *reinterpret_cast<const float4*>(mask + m);
-      const float4 mk1 = *reinterpret_cast<const float4*>(mask + m + 4);
-      const float mk[8] = {mk0.x, mk0.y, mk0.z, mk0.w, mk1.x, mk1.y, mk1.z, mk1.w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float s = sigmoidf_((float)gv[e]);
-        const float a = (float)da[e] * mk[e];
-        dp8[e] = (bf16)(a * s);
-        dg8[e] = (bf16)(a * (float)pv[e] * s * (1.f - s));
-      }
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      tile[(r0 + e) * LD + col_proj(ch)] = dp8[e];
-      tile[(r0 + e) * LD + col_gate(ch)] = dg8[e];
-    }
-  }
-  __syncthreads();
-  const int chunks = W / 8;
-  for (int idx = t; idx < R * chunks; idx += 256) {
-    const int r = idx / chunks, c8 = (idx % chunks) * 8;
-    const long m = m0 + r;
-    if (m < M) st8(dcat + m * ldcat + c8, ld8(&tile[r * LD + c8]));
-  }
-}
 
 }  // namespace
 
@@ -291,8 +277,8 @@ void trimul_fwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
   TriMulSave<Carver> sv(cv, N, C, I);
   Arena& ar = arena();
   std::lock_guard<std::recursive_mutex> lk(ar.lock());
-  ar.reset(st, (size_t)M * C * 2 + (size_t)M * I * 2 + 1024);
-  bf16* xn = ar.take_n<bf16>((size_t)M * C);
+  ar.reset(st, (size_t)M * I * 2 + 1024);
+  bf16* xn = sv.xn;
   bf16* tn = ar.take_n<bf16>((size_t)M * I);
   {
     KTimed kt("trimul.ln_fwd", st);
@@ -304,8 +290,7 @@ void trimul_fwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
   g1.A = xn; g1.a_sm = C; g1.a_sk = 1;
   g1.B = w.wcat_t; g1.b_sn = C; g1.b_sk = 1;
   gemm<128, 128>(st, g1,
-                 EpiTrimulProj{sv.left, sv.right, sv.psave, sv.gsave, sv.gout, w.bp, w.bg, w.bgl,
-                               mask, M, I, C},
+                 EpiTrimulProj{sv.left, sv.right, sv.gout, w.bp, w.bg, w.bgl, mask, M, I, C},
                  "trimul.gemm_proj");
   contraction_fwd(st, outgoing, N, I, sv.left, sv.right, sv.T);
   {
@@ -382,10 +367,12 @@ void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
     gemm<64, 64>(st, b, EpiStore<bf16>{dR, N, M, nullptr, N}, "trimul.contract_bwd");
   }
   {
-    KTimed kt("trimul.proj_bwd", st);
-    const size_t lds = (size_t)32 * (4 * I + 8) * 2;
-    hipLaunchKernelGGL(trimul_proj_bwd_kernel, dim3((unsigned)((M + 31) / 32)), dim3(256), lds, st,
-                       dL, dR, sv.psave, sv.gsave, mask, dcat, M, I, NC);
+    GemmArgs g;
+    g.M = (int)M; g.N = 4 * I; g.K = C;
+    g.A = sv.xn; g.a_sm = C; g.a_sk = 1;
+    g.B = w.wcat_t; g.b_sn = C; g.b_sk = 1;
+    gemm<128, 128>(st, g, EpiTrimulProjBwd{dL, dR, w.bp, w.bg, mask, dcat, M, I, NC},
+                   "trimul.proj_bwd");
   }
   GemmArgs g2;
   g2.M = (int)M; g2.N = C; g2.K = NC;
