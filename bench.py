@@ -55,25 +55,55 @@ def trimul_flops(n, c=128, i=128):
     return fwd + bwd
 
 
-# executed MFMA work per launch of the kernels the roofline may name
-def kernel_work(name, n):
+# Per-launch algorithmic model of the hot kernels at length n (C = c_z = 128,
+# H = 4 heads of 32, I = 128, M = n^2 tokens): (MFMA FLOPs, HBM bytes).
+# Bytes count each operand read and each result written once (bf16 = 2 B,
+# f32 = 4 B); FLOPs are the products the kernel executes (the attention
+# backward's recomputed scores included).  A kernel whose FLOP/byte is below
+# the machine balance (RIDGE) is HBM-bound on the roofline, above it MFMA-bound.
+RIDGE = PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)  # 312.5 FLOP/B
+
+
+def kernel_model(name, n):
     c = 128
-    flops = {
-        "attn_fwd": 4 * n ** 3 * c,
-        "attn_bwd_dq": 6 * n ** 3 * c,
-        "attn_bwd_dkv": 8 * n ** 3 * c,
-        "triattn.gemm_qkvg": 2 * n * n * c * 4 * c,
-        "triattn.gemm_dx": 2 * n * n * 4 * c * c,
-        "trimul.gemm_proj": 2 * n * n * c * (4 * c + c),
-        "trimul.gemm_dx": 2 * n * n * (4 * c + c) * c,
-        "trimul.contract_fwd": 2 * c * n ** 3,
-        "trimul.contract_bwd": 2 * c * n ** 3,
-        "trans.gemm1": 2 * n * n * c * 4 * c,
-        "trans.gemm2": 2 * n * n * 4 * c * c,
-        "trans.gemm_dh": 2 * n * n * c * 4 * c,
-        "trans.gemm_dx": 2 * n * n * 4 * c * c,
+    m = n * n
+    gemm = lambda k, cols: 2 * m * k * cols
+    model = {
+        # q|k|v|g read, o and og written, bias/lse/mask
+        "attn_fwd": (4 * n ** 3 * c, m * (1024 + 512 + 16 + 16 + 4)),
+        # q,k,v,dO read, dq written, bias/lse/Dsum/mask
+        "attn_bwd_dq": (6 * n ** 3 * c, m * (768 + 256 + 256 + 16 + 32 + 4)),
+        # q,dO,k,v read, dk,dv written, bias/lse/Dsum/mask, d(bias) once
+        "attn_bwd_dkv": (8 * n ** 3 * c, m * (1024 + 512 + 16 + 32 + 4 + 16)),
+        "trimul.contract_fwd": (2 * c * n ** 3, m * (512 + 512)),
+        "trimul.contract_bwd": (2 * c * n ** 3, m * (256 + 256 + 256)),
+        "triattn.gemm_qkvg": (gemm(c, 4 * c), m * (256 + 1024)),
+        "triattn.gemm_out": (gemm(c, c), m * (256 + 512 + 512)),
+        "triattn.gemm_dout": (gemm(c, c), m * (512 + 256 * 4 + 16)),
+        "triattn.gemm_dx": (gemm(4 * c, c), m * (1024 + 512)),
+        "trimul.gemm_proj": (gemm(c, 5 * c), m * (256 + 512 + 256 + 4)),
+        "trimul.proj_bwd": (gemm(c, 4 * c), m * (256 + 512 + 4 + 1024)),
+        "trimul.gemm_out": (gemm(c, c), m * (256 + 256 + 512 + 256 + 512)),
+        "trimul.gemm_dout": (gemm(c, c), m * (512 + 256 + 256 + 512 + 256)),
+        "trimul.gemm_dx": (gemm(5 * c, c), m * (1280 + 512)),
+        "trans.gemm1": (gemm(c, 4 * c), m * (256 + 1024)),
+        "trans.gemm2": (gemm(4 * c, c), m * (1024 + 512 + 512)),
+        "trans.gemm_dh": (gemm(c, 4 * c), m * (512 + 1024 + 1024)),
+        "trans.gemm_dx": (gemm(4 * c, c), m * (1024 + 512)),
+        "triattn.ln_fwd": (0, m * (512 + 256 + 16 + 8)),
+        "triattn.ln_bwd": (0, m * (512 * 4 + 16 + 8)),
+        "trimul.ln_fwd": (0, m * (512 + 256 + 8)),
+        "trimul.ln_bwd": (0, m * (512 * 4 + 8)),
+        "trimul.ln_center": (0, m * (512 + 256 + 8)),
+        "trimul.ln_center_bwd": (0, m * (512 + 512 + 256 + 8)),
     }
-    return flops.get(name)
+    return model.get(name)
+
+
+def kernel_work(name, n):
+    """Executed MFMA FLOPs per launch (None for kernels outside the model)."""
+    km = kernel_model(name, n)
+    return None if km is None else km[0]
 
 
 # --------------------------------------------------------------- CPU baseline
@@ -188,22 +218,61 @@ def traffic_of(kernel, n):
         summ = json.load(fh)
     if summ.get("L") != n:
         return None
-    # the triangle-attention launches are the head-width-32 instantiation
-    k = summ["kernels"].get(f"{kernel}<32, {n // 32}>") or summ["kernels"].get(kernel)
-    return None if k is None else int(k["fetch_bytes"] + k["write_bytes"])
+    # the triangle-attention launches are the head-width-32 instantiation (the
+    # row-chunk forms for N <= 256); other timer names map to no one symbol
+    nb = n // 32
+    syms = {"attn_fwd": [f"attn_fwd_rows<32, {nb}>", f"attn_fwd<32, {nb}>"],
+            "attn_bwd_dq": [f"attn_bwd_dq_rows<32, {nb}>", f"attn_bwd_dq<32, {nb}>"],
+            "attn_bwd_dkv": [f"attn_bwd_dkv<32, {nb}>"]}.get(kernel, [kernel])
+    for sym in syms:
+        k = summ["kernels"].get(sym)
+        if k is not None:
+            return int(k["fetch_bytes"] + k["write_bytes"])
+    return None
+
+
+def _rate(name, n, tot_ms, cnt):
+    flops, nbytes = kernel_model(name, n)
+    us = tot_ms / cnt * 1e3
+    tf = flops / (us * 1e-6) / 1e12
+    gbs = nbytes / (us * 1e-6) / 1e9
+    bound = "mfma" if flops / nbytes >= RIDGE else "hbm"
+    return us, tf, gbs, bound
 
 
 def roofline_from(prof, n):
-    cand = {k: v for k, v in prof.items() if kernel_work(k, n) is not None}
+    """The dominant modelled kernel (largest total time): its achieved rate in
+    the unit of the bound its arithmetic intensity puts it under."""
+    cand = {k: v for k, v in prof.items() if kernel_model(k, n) is not None}
     if not cand:
         return None
     dom = max(cand, key=lambda k: cand[k][0])
     tot, cnt = cand[dom]
-    achieved = kernel_work(dom, n) / (tot / cnt * 1e-3) / 1e12
-    return {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2),
-            "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic_of(dom, n),
-            "launch_us": round(tot / cnt * 1e3, 2)}
+    us, tf, gbs, bound = _rate(dom, n, tot, cnt)
+    flops, nbytes = kernel_model(dom, n)
+    if bound == "mfma":
+        ach, peak, unit = tf, PEAK_BF16_TFLOPS, "TFLOP/s"
+    else:
+        ach, peak, unit = gbs, PEAK_HBM_GBS, "GB/s"
+    return {"kernel": dom, "bound": bound, "achieved": round(ach, 2), "peak": peak, "unit": unit,
+            "frac": round(ach / peak, 4), "traffic": traffic_of(dom, n), "launch_us": round(us, 2),
+            "algorithmic_bytes": nbytes, "algorithmic_flops": flops,
+            "flop_per_byte": round(flops / nbytes, 1), "ridge": round(RIDGE, 1),
+            "mfma_tflops": round(tf, 2), "mfma_frac": round(tf / PEAK_BF16_TFLOPS, 4)}
+
+
+def kernel_rooflines(prof, n):
+    """Every modelled kernel: MFMA TFLOP/s and HBM GB/s, each as a fraction of
+    its peak, and which one bounds it (by arithmetic intensity)."""
+    rows = []
+    for k, (tot, cnt) in sorted(prof.items(), key=lambda kv: -kv[1][0]):
+        if kernel_model(k, n) is None:
+            continue
+        us, tf, gbs, bound = _rate(k, n, tot, cnt)
+        rows.append({"kernel": k, "us": round(us, 2), "bound": bound, "tflops": round(tf, 1),
+                     "mfma_frac": round(tf / PEAK_BF16_TFLOPS, 4), "gbs": round(gbs, 0),
+                     "hbm_frac": round(gbs / PEAK_HBM_GBS, 4)})
+    return rows
 
 
 def _short_kernel_name(sym):
@@ -489,6 +558,8 @@ def main():
            "config": line.pop("config"), "roofline": roofline_from(prof, n),
            "cpu_baseline": cpu}
     out.update(line)
+    if prof and args.workload in ("trunk", "triattn"):
+        out["kernel_rooflines"] = kernel_rooflines(prof, n)
     out["kernels"] = kernel_table(prof)
     print(json.dumps(out))
 

@@ -70,6 +70,15 @@ void ln_f32_rows_fwd(hipStream_t st, const float* x, long M, int C, const float*
 void ln_f32_rows_bwd(hipStream_t st, const float* dy, const float* x, long M, int C,
                      const float* g, const float* mean, const float* rstd, float* dx);
 
+// ------------------------------------------------- triangle multiplication
+// C_c[m][n] = sum_k A_c[m][k] B_c[n][k] for c < channels, N x N planes at
+// stride N*N; an operand plane is K-contiguous ((r, k) at r*N + k) or k-major
+// ((r, k) at k*N + r).  Writes Cf (f32) if non-null, else Cb (bf16).  Returns
+// false (and launches nothing) when N is outside the kernel's range
+// (N % 32 != 0 or N > 256).
+bool trimul_contract(hipStream_t st, int N, int channels, const bf16* A, bool a_kcontig,
+                     const bf16* B, bool b_kcontig, float* Cf, bf16* Cb);
+
 // ---------------------------------------------------------------- dropout
 // Shared-dropout keep/scale table for one module: tbl[b*C+c] = keep/keep_rate
 // (0 where dropped), with keep = jax.random.uniform(key,(B,C)) < keep_rate.

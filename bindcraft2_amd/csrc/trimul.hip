@@ -249,6 +249,21 @@ static void trimul_check(int N) {
   if (N <= 0 || N % 32 != 0) throw std::runtime_error("trimul: N must be a positive multiple of 32");
 }
 
+// One batched contraction (operands described by `g`, one channel plane per
+// batch entry): the dedicated kernel for N <= 256, the tiled GEMM beyond.
+template <class OutT>
+static void contract(hipStream_t st, const GemmArgs& g, OutT* C, const char* name) {
+  {
+    KTimed kt(name, st);
+    float* cf = nullptr;
+    bf16* cb = nullptr;
+    if constexpr (sizeof(OutT) == 4) cf = C;
+    else cb = C;
+    if (trimul_contract(st, g.M, g.batch, g.A, g.a_sk == 1, g.B, g.b_sk == 1, cf, cb)) return;
+  }
+  gemm<64, 64>(st, g, EpiStore<OutT>{C, g.N, (long)g.M * g.N, nullptr, g.N}, name);
+}
+
 // Contraction operand layouts for one channel plane (row-major N x N).
 static void contraction_fwd(hipStream_t st, bool outgoing, int N, int I, const bf16* L,
                             const bf16* R, float* T) {
@@ -263,7 +278,7 @@ static void contraction_fwd(hipStream_t st, bool outgoing, int N, int I, const b
     g.B = L; g.b_sn = 1; g.b_sk = N;
   }
   g.a_sb = M; g.b_sb = M;
-  gemm<64, 64>(st, g, EpiStore<float>{T, N, M, nullptr, N}, "trimul.contract_fwd");
+  contract<float>(st, g, T, "trimul.contract_fwd");
 }
 
 void trimul_fwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const float* pair_in,
@@ -363,8 +378,8 @@ void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
       b.A = sv.left; b.a_sm = N; b.a_sk = 1;
       b.B = dT; b.b_sn = N; b.b_sk = 1;
     }
-    gemm<64, 64>(st, a, EpiStore<bf16>{dL, N, M, nullptr, N}, "trimul.contract_bwd");
-    gemm<64, 64>(st, b, EpiStore<bf16>{dR, N, M, nullptr, N}, "trimul.contract_bwd");
+    contract<bf16>(st, a, dL, "trimul.contract_bwd");
+    contract<bf16>(st, b, dR, "trimul.contract_bwd");
   }
   {
     GemmArgs g;

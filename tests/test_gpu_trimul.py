@@ -27,6 +27,7 @@ def _oracle(prm, outgoing, pair, mask, tbl, dout):
 @pytest.mark.parametrize("n,outgoing,drop,mask_frac", [
     (32, True, False, 0.0), (32, False, False, 0.0),
     (64, True, True, 0.1), (64, False, True, 0.1), (96, False, True, 0.2),
+    (224, True, True, 0.1), (224, False, True, 0.1), (288, True, True, 0.1),
 ])
 def test_trimul_fwd_bwd_parity(cuda, n, outgoing, drop, mask_frac):
     print(f"trimul n={n} outgoing={outgoing} drop={drop} mask={mask_frac}", flush=True)
