@@ -228,7 +228,21 @@ def traffic_of(kernel, n):
         k = summ["kernels"].get(sym)
         if k is not None:
             return int(k["fetch_bytes"] + k["write_bytes"])
-    return None
+    # GEMM-based timers: the kernel symbol names the epilogue (demangled or
+    # mangled); the contraction's output type tells forward from backward
+    pat = {"trimul.proj_bwd": r"EpiTrimulProjBwd",
+           "trimul.gemm_proj": r"EpiTrimulProj(?!Bwd)",
+           "trimul.gemm_out": r"EpiTrimulOut",
+           "trimul.contract_fwd": rf"contract(_kernel)?(<{nb}, .*float>|ILi{nb}E.*fEE)",
+           "trimul.contract_bwd": rf"contract(_kernel)?(<{nb}, .*bf16>|ILi{nb}E.*DF16bEE)"}.get(kernel)
+    if pat is None:
+        return None
+    import re
+    hits = [v for k, v in summ["kernels"].items() if re.search(pat, k)]
+    if not hits:
+        return None
+    k = max(hits, key=lambda v: v["calls"])
+    return int(k["fetch_bytes"] + k["write_bytes"])
 
 
 def _rate(name, n, tot_ms, cnt):
@@ -279,13 +293,14 @@ def _short_kernel_name(sym):
     """'void bc2n::attn_bwd_dkv_kernel<32, 7>(bc2n::AttnBwdArgs)' ->
     'attn_bwd_dkv<32, 7>' (the event timer's name plus the template
     arguments, which tell head widths and lengths apart)."""
-    s = sym.replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
+    s = sym.replace("(anonymous namespace)::", "").replace("void ", "").replace("bc2n::", "")
+    s = s.split("(")[0] if not s.startswith("_Z") else s
     base, _, targs = s.partition("<")
     base = base.split("::")[-1]
     base = base[:-len("_kernel")] if base.endswith("_kernel") else base
-    if targs and len(targs) < 24:
-        return f"{base}<{targs}"
-    return base
+    # template arguments kept whole: they tell lengths, head widths and the
+    # GEMM epilogues apart
+    return f"{base}<{targs}" if targs else base
 
 
 def pmc_summarize(fetch_csv, write_csv, copy_fetch_csv, copy_write_csv, n, out):
