@@ -66,6 +66,9 @@ def _declare(L):
         "bc2n_tplstack_save_bytes": (sz, [cs, i, c.c_int64]),
         "bc2n_tplstack_fwd": (i, [vp, vp, vp, vp, i, i, c.c_int64, c.c_int64, cs, vp, vp]),
         "bc2n_tplstack_bwd": (i, [vp, vp, vp, vp, vp, i, i, c.c_int64, c.c_int64, cs, vp]),
+        "bc2n_tplembed_save_bytes": (sz, [cs, i, c.c_int64]),
+        "bc2n_tplembed_fwd": (i, [vp, vp, vp, vp, vp, i, i, c.c_int64, c.c_int64, cs, vp, vp]),
+        "bc2n_tplembed_bwd": (i, [vp, vp, vp, vp, vp, vp, vp, i, i, c.c_int64, c.c_int64, cs, vp]),
         "bc2n_fold_save_bytes": (sz, [cs, i, c.c_int64]),
         "bc2n_fold_fwd": (i, [vp, vp, vp, vp, vp, i, i, c.c_int64, c.c_int64, cs, vp, vp, vp]),
         "bc2n_fold_bwd": (i, [vp, vp, vp, vp, vp, vp, vp, i, c.c_int64, c.c_int64, cs, vp, vp]),

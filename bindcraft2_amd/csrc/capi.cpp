@@ -4,6 +4,7 @@
 #include "gemm.h"
 #include "gemm_f32.h"
 #include "modules.h"
+#include "tplembed.h"
 
 #include <map>
 #include <tuple>
@@ -407,6 +408,59 @@ int bc2n_tplstack_bwd(void* stream, const float* ct, const float* pair_mask, con
     const StackW& w = stack_w(weights_dir, (int)depth, StackKind::TEMPLATE);
     stack_bwd(as_stream(stream), w, N, 1, (int)depth, pair_mask, nullptr, dropout != 0, save, ct,
               nullptr, dpair, nullptr);
+  });
+}
+
+// --------------------------------------------------------- template embedding
+
+namespace {
+std::map<std::pair<std::string, std::string>, TplEmbedW> g_te;
+const TplEmbedW& te_w(const char* dir, int depth) {
+  return cached(g_te, dir, std::to_string(depth).c_str(), [&](WeightStore& ws, const std::string&) {
+    return tplembed_weights(ws, depth);
+  });
+}
+}  // namespace
+
+size_t bc2n_tplembed_save_bytes(const char* weights_dir, int N, int64_t depth) {
+  size_t n = 0;
+  if (guarded([&] {
+        need(weights_dir != nullptr, "weights_dir required");
+        n = tplembed_save_bytes(te_w(weights_dir, (int)depth), N) + 256;
+      }) != 0)
+    return 0;
+  return n;
+}
+
+int bc2n_tplembed_fwd(void* stream, const float* query, const float* act_const,
+                      const float* pair_mask, const uint32_t* seed, int seed_len, int N,
+                      int64_t depth, int64_t dropout, const char* weights_dir, float* out,
+                      void* save) {
+  return guarded([&] {
+    hipStream_t st = as_stream(stream);
+    need(weights_dir && query && act_const && pair_mask && out && save, "null operand");
+    need(seed_len == 2 || seed_len == 3, "tplembed: seed must be u32[2] or u32[3]");
+    need(!dropout || seed, "tplembed: dropout needs the seed operand");
+    const TplEmbedW& w = te_w(weights_dir, (int)depth);
+    const size_t bytes = tplembed_save_bytes(w, N) + 256;
+    uint32_t* keyslot = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(save) + bytes - 256);
+    const uint32_t* key = dropout ? stack_key(st, seed, seed_len, keyslot) : nullptr;
+    const uint32_t* enabled = dropout ? seed + (seed_len - 1) : nullptr;
+    tplembed_fwd(st, w, N, query, act_const, pair_mask, key, enabled, dropout != 0, out, save);
+  });
+}
+
+int bc2n_tplembed_bwd(void* stream, const float* ct, const float* query, const float* act_const,
+                      const float* pair_mask, const void* save, const uint32_t* seed, int seed_len,
+                      int N, int64_t depth, int64_t dropout, const char* weights_dir,
+                      float* dquery) {
+  (void)act_const;
+  (void)seed;
+  (void)seed_len;
+  return guarded([&] {
+    need(weights_dir && ct && query && pair_mask && save && dquery, "null operand");
+    const TplEmbedW& w = te_w(weights_dir, (int)depth);
+    tplembed_bwd(as_stream(stream), w, N, query, pair_mask, dropout != 0, save, ct, dquery);
   });
 }
 

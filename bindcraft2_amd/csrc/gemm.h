@@ -474,19 +474,34 @@ struct EpiGateBwd : EpiRows {
   }
 };
 
-// dH = acc * (H > 0): backward through a ReLU whose output H is kept (bf16).
+// dH = acc * (H > 0): backward through a ReLU of the kept (bf16) tensor H.
+template <class OutT = bf16>
 struct EpiReluMask : EpiRows {
-  bf16* C;
+  OutT* C;
   const bf16* H;
   long ldc;
-  EpiReluMask(bf16* c, const bf16* h, long l) : C(c), H(h), ldc(l) {}
+  EpiReluMask(OutT* c, const bf16* h, long l) : C(c), H(h), ldc(l) {}
   __device__ __forceinline__ void row(int, int m, int n, const float (&v)[8]) const {
     const long o = (long)m * ldc + n;
     const bf16x8 h = ld8(H + o);
     float x[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) x[e] = (float)h[e] > 0.f ? v[e] : 0.f;
-    st_b8f(C + o, x);
+    st_any8<OutT>(C + o, x);
+  }
+};
+
+// A[m][k] = relu(src[m][k]) of a kept bf16 tensor (row stride C).
+struct ALoadReluBf16 {
+  static constexpr bool kDirect = false;
+  static constexpr bool kSide = false;
+  const bf16* src;
+  int C;
+  __device__ __forceinline__ bf16x8 operator()(int, int m, int k) const {
+    bf16x8 v = ld8(src + (long)m * C + k);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (float)v[e] > 0.f ? v[e] : (bf16)0.f;
+    return v;
   }
 };
 

@@ -96,7 +96,7 @@ void transition_bwd(hipStream_t st, const TransW& w, long rows, int nt, const fl
   g1.M = (int)rows; g1.N = H; g1.K = C;
   g1.a_sm = C; g1.a_sk = 1;
   g1.B = w.w2; g1.b_sn = C; g1.b_sk = 1;
-  gemm<128, 128>(st, g1, EpiReluMask(dh, sv.h, H), "trans.gemm_dh",
+  gemm<128, 128>(st, g1, EpiReluMask<bf16>(dh, sv.h, H), "trans.gemm_dh",
                  ALoadScaledRows{dout, tbl, nt, C, false});
   GemmArgs g2;
   g2.M = (int)rows; g2.N = C; g2.K = H;

@@ -315,6 +315,42 @@ class TemplatePairStack:
         return dpair
 
 
+class TemplateEmbedding:
+    """The drop-in for TemplateEmbeddingFwd/Bwd (native/ffi.cu:1072-1098): one
+    template, the eight constant feature projections summed into act_const;
+    query [N,N,128] -> out [N,N,128] through the template pair stack."""
+
+    def __init__(self, weights_dir, depth):
+        self.dir, self.depth = weights_dir.encode(), depth
+
+    def save_bytes(self, n):
+        b = lib().bc2n_tplembed_save_bytes(self.dir, n, self.depth)
+        if b == 0:
+            check(1)
+        return b
+
+    def forward(self, query, act_const, pair_mask, seed=None, dropout=True, out=None, save=None):
+        n = query.shape[0]
+        if out is None:
+            out = torch.empty_like(query)
+        if save is None:
+            save = torch.empty(self.save_bytes(n), dtype=torch.uint8, device=query.device)
+        seed_len = 3 if seed is None else seed.numel()
+        check(lib().bc2n_tplembed_fwd(_stream(), _ptr(query), _ptr(act_const), _ptr(pair_mask),
+                                      _ptr(seed), seed_len, n, self.depth, int(dropout), self.dir,
+                                      _ptr(out), _ptr(save)))
+        return out, save
+
+    def backward(self, ct, query, act_const, pair_mask, save, seed=None, dropout=True):
+        n = ct.shape[0]
+        dquery = torch.empty_like(ct)
+        seed_len = 3 if seed is None else seed.numel()
+        check(lib().bc2n_tplembed_bwd(_stream(), _ptr(ct), _ptr(query), _ptr(act_const),
+                                      _ptr(pair_mask), _ptr(save), _ptr(seed), seed_len, n,
+                                      self.depth, int(dropout), self.dir, _ptr(dquery)))
+        return dquery
+
+
 class Fold:
     """The structure module's fold iterations (IPA + transition + rigid
     update, the part of StructureHeadsFwd/Bwd before the sidechain,

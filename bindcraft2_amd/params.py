@@ -124,6 +124,27 @@ def init_template_block_params(block, rng, gates="zero", ln="identity"):
     return out
 
 
+def template_embedding_shapes(c_z=C_Z, c_t=C_T):
+    """The template embedding's own weights around the stack
+    (modules_multimer.py:704-1005; names as under param/ in the reference's
+    template-embedding weights directory)."""
+    return {"query_embedding_norm/scale": (c_z,), "query_embedding_norm/offset": (c_z,),
+            "template_pair_embedding_8/weights": (c_z, c_t), "template_pair_embedding_8/bias": (c_t,),
+            "output_layer_norm/scale": (c_t,), "output_layer_norm/offset": (c_t,),
+            "output_linear/weights": (c_t, c_z), "output_linear/bias": (c_z,)}
+
+
+def init_template_embedding_params(depth, rng, gates="zero", ln="identity"):
+    """Weights directory contents of a template embedding with `depth` stack
+    blocks."""
+    out = {}
+    for b in range(depth):
+        out.update(init_template_block_params(b, rng, gates, ln))
+    for pname, arr in init_module(template_embedding_shapes(), rng, gates, ln).items():
+        out[f"param/{pname}"] = arr
+    return out
+
+
 def global_attention_shapes(c=C_E, heads=8):
     """MSAColumnGlobalAttention of the extra-MSA stack (modules.py:403-497,
     619-672; config.py extra_msa: 8 heads, key/value dim c)."""

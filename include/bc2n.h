@@ -203,6 +203,37 @@ int bc2n_tplstack_bwd(void* stream, const float* ct, const float* pair_mask,
                       float* dpair);
 
 /* ------------------------------------------------------------------------
+ * Template embedding, one template (the reference's TemplateEmbeddingFwd /
+ * TemplateEmbeddingBwd custom calls, native/ffi.cu:1072-1098 (handlers
+ * TeFwdImpl / TeBwdImpl :766-803), called from bindcraft/af/native.py:
+ * 1049-1128 for modules_multimer.py:704-1005).  Replaces:
+ *   fwd(query f32[N,N,128], act_const f32[N,N,64], pair_mask f32[N,N],
+ *       seed; depth, dropout, weights_dir) -> (out f32[N,N,128], save)
+ *   bwd(ct f32[N,N,128], query, act_const, pair_mask, save, seed; ...)
+ *       -> dquery f32[N,N,128]
+ * act_const is the caller's sum of the eight constant template-feature
+ * projections; out = output_linear(relu(output_layer_norm(stack(act_const +
+ * template_pair_embedding_8(query_embedding_norm(query)))))).  The weights
+ * directory holds param/query_embedding_norm, template_pair_embedding_8,
+ * output_layer_norm, output_linear and the stack's param/block{b}/...
+ * save holds bc2n_tplembed_save_bytes() bytes (the backward replays no
+ * forward); seed as for the stacks.  act_const gets no gradient and is
+ * accepted by the backward for the reference's operand list only.  out
+ * (dquery) must not alias an input: it is used as staging before it is
+ * written.
+ * ---------------------------------------------------------------------- */
+size_t bc2n_tplembed_save_bytes(const char* weights_dir, int N, int64_t depth);
+int bc2n_tplembed_fwd(void* stream, const float* query, const float* act_const,
+                      const float* pair_mask, const uint32_t* seed, int seed_len,
+                      int N, int64_t depth, int64_t dropout,
+                      const char* weights_dir, float* out, void* save);
+int bc2n_tplembed_bwd(void* stream, const float* ct, const float* query,
+                      const float* act_const, const float* pair_mask,
+                      const void* save, const uint32_t* seed, int seed_len, int N,
+                      int64_t depth, int64_t dropout, const char* weights_dir,
+                      float* dquery);
+
+/* ------------------------------------------------------------------------
  * Structure module fold iterations (the IPA step of the post-trunk
  * StructureHeadsFwd/Bwd handlers, native/ffi.cu:1009-1044, up to and
  * excluding the sidechain; native/foldit.cuh:141-440, ipa.cuh:507-842,

@@ -319,6 +319,23 @@ def template_stack(act, pair_mask, params, depth, stack_key, use_dropout, dtype=
     return act
 
 
+def template_embedding(query, act_const, pair_mask, params, depth, stack_key, use_dropout,
+                       dtype=torch.float64):
+    """modules_multimer.py:704-1005 (TemplateEmbedding) for one template with the
+    eight constant feature projections already summed into `act_const`
+    (:940-951, query_projection :922-940): the ninth feature is
+    Linear(LN(query)) (query_embedding_norm, template_pair_embedding_8); the
+    stack (:956-991) gets `stack_key`; then output_layer_norm (:1000-1005),
+    the mean over num_templates = 1 and relu (:802-803), output_linear
+    (:804-808)."""
+    P = Params(params, "param/", dtype)
+    q = layer_norm(query, P("query_embedding_norm/scale"), P("query_embedding_norm/offset"))
+    act = act_const + linear(q, P.sub("template_pair_embedding_8/"))
+    act = template_stack(act, pair_mask, params, depth, stack_key, use_dropout, dtype)
+    act = layer_norm(act, P("output_layer_norm/scale"), P("output_layer_norm/offset"))
+    return linear(torch.relu(act), P.sub("output_linear/"))
+
+
 # ------------------------------------------------------------ structure module
 # folding_multimer.py (AF2 multimer structure module), config.py:578-600.
 IPA_HEADS, IPA_SCALAR_QK, IPA_POINT_QK, IPA_SCALAR_V, IPA_POINT_V = 12, 16, 4, 16, 8
