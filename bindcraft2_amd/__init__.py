@@ -69,6 +69,8 @@ def _declare(L):
         "bc2n_tplembed_save_bytes": (sz, [cs, i, c.c_int64]),
         "bc2n_tplembed_fwd": (i, [vp, vp, vp, vp, vp, i, i, c.c_int64, c.c_int64, cs, vp, vp]),
         "bc2n_tplembed_bwd": (i, [vp, vp, vp, vp, vp, vp, vp, i, i, c.c_int64, c.c_int64, cs, vp]),
+        "bc2n_embedder_fwd": (i, [vp, vp, vp, vp, vp, vp, vp, vp, i, i, cs, vp, vp]),
+        "bc2n_embedder_bwd": (i, [vp, vp, vp, vp, i, i, cs, vp, vp]),
         "bc2n_fold_save_bytes": (sz, [cs, i, c.c_int64]),
         "bc2n_fold_fwd": (i, [vp, vp, vp, vp, vp, i, i, c.c_int64, c.c_int64, cs, vp, vp, vp]),
         "bc2n_fold_bwd": (i, [vp, vp, vp, vp, vp, vp, vp, i, c.c_int64, c.c_int64, cs, vp, vp]),

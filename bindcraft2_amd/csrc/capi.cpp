@@ -5,6 +5,7 @@
 #include "gemm_f32.h"
 #include "modules.h"
 #include "tplembed.h"
+#include "embed.h"
 
 #include <map>
 #include <tuple>
@@ -461,6 +462,35 @@ int bc2n_tplembed_bwd(void* stream, const float* ct, const float* query, const f
     need(weights_dir && ct && query && pair_mask && save && dquery, "null operand");
     const TplEmbedW& w = te_w(weights_dir, (int)depth);
     tplembed_bwd(as_stream(stream), w, N, query, pair_mask, dropout != 0, save, ct, dquery);
+  });
+}
+
+// ------------------------------------------------------------------ embedder
+
+namespace {
+std::map<std::pair<std::string, std::string>, EmbedW> g_emb;
+const EmbedW& emb_w(const char* dir) {
+  return cached(g_emb, dir, "", [&](WeightStore& ws, const std::string&) { return embed_weights(ws); });
+}
+}  // namespace
+
+int bc2n_embedder_fwd(void* stream, const float* target_feat, const float* msa_feat,
+                      const float* residue_index, const float* asym_id, const float* entity_id,
+                      const float* sym_id, const int32_t* offset, int N, int S,
+                      const char* weights_dir, float* msa, float* pair) {
+  return guarded([&] {
+    need(weights_dir != nullptr, "weights_dir required");
+    embed_fwd(as_stream(stream), emb_w(weights_dir), N, S, target_feat, msa_feat, residue_index,
+              asym_id, entity_id, sym_id, offset, msa, pair);
+  });
+}
+
+int bc2n_embedder_bwd(void* stream, const float* dmsa, const float* dpair, const float* target_feat,
+                      int N, int S, const char* weights_dir, float* dtarget_feat, float* dmsa_feat) {
+  return guarded([&] {
+    need(weights_dir != nullptr, "weights_dir required");
+    embed_bwd(as_stream(stream), emb_w(weights_dir), N, S, dmsa, dpair, target_feat, dtarget_feat,
+              dmsa_feat);
   });
 }
 

@@ -1050,26 +1050,6 @@ int attn_bwd_nchunk(int R, int rows_per_chunk) {
   return (R + rows_per_chunk - 1) / rows_per_chunk;
 }
 
-// Rows per bias-gradient chunk.  A chunk is H * N / (16 KT) workgroups of
-// the dK/dV kernel, which is register bound at two workgroups per CU; the
-// chunk count is the largest that fits one round of 2 x CUs workgroups, so
-// no second, partly empty round follows (N = 224, H = 4 on 256 CUs: 18
-// chunks of 13 rows).  Fewer chunks also mean fewer [nchunk][H][N][N]
-// partials to write and add.
-static int device_cus() {
-  static int cus[64] = {};
-  int dev = 0;
-  hip_check(hipGetDevice(&dev), "hipGetDevice");
-  if (dev < 0 || dev >= 64) dev = 0;
-  if (cus[dev] == 0) {
-    int n = 0;
-    hip_check(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev),
-              "hipDeviceGetAttribute");
-    cus[dev] = n > 0 ? n : 1;
-  }
-  return cus[dev];
-}
-
 // Rows per workgroup of the row-chunk forward: (chunk, head, 64 queries)
 // workgroups at two per CU (register bound), one round of 2 x CUs.
 int attn_fwd_rows_per_chunk(int R, int N, int H) {
@@ -1078,6 +1058,12 @@ int attn_fwd_rows_per_chunk(int R, int N, int H) {
   return (int)std::max(1L, ((long)R + nch - 1) / nch);
 }
 
+// Rows per bias-gradient chunk.  A chunk is H * N / (16 KT) workgroups of
+// the dK/dV kernel, which is register bound at two workgroups per CU; the
+// chunk count is the largest that fits one round of 2 x CUs workgroups, so
+// no second, partly empty round follows (N = 224, H = 4 on 256 CUs: 18
+// chunks of 13 rows).  Fewer chunks also mean fewer [nchunk][H][N][N]
+// partials to write and add.
 int attn_rows_per_chunk(int R, int N, int H) {
   const int KT = N > 256 ? 1 : 2;
   const long per_chunk = (long)H * (N / (16 * KT));

@@ -107,6 +107,20 @@ Arena& arena() {
   return a;
 }
 
+int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  hip_check(hipGetDevice(&dev), "hipGetDevice");
+  if (dev < 0 || dev >= 64) dev = 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    hip_check(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev),
+              "hipDeviceGetAttribute");
+    cus[dev] = n > 0 ? n : 1;
+  }
+  return cus[dev];
+}
+
 namespace {
 struct KProf {
   bool on = false;

@@ -83,6 +83,9 @@ class Arena {
 };
 Arena& arena();
 
+// Compute units of the current device (cached per device).
+int device_cus();
+
 // Per-kernel device timing: when enabled, every launch site wrapped in
 // KTimed records a HIP event pair on its own stream; kprof_read() syncs the
 // events and returns per-name totals.  Off by default (no events recorded).

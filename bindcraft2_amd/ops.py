@@ -351,6 +351,38 @@ class TemplateEmbedding:
         return dquery
 
 
+class Embedder:
+    """The drop-in for EmbedderFwd/Bwd (native/ffi.cu:1046-1071): target_feat
+    [N,21] (padded), msa_feat [S,N,49] and the four id features [N] ->
+    msa [S,N,256], pair [N,N,128]; backward (dmsa, dpair, target_feat) ->
+    (dtarget_feat [N,21], dmsa_feat [S,N,49]).  All f32, no save-set."""
+
+    def __init__(self, weights_dir):
+        self.dir = weights_dir.encode()
+
+    def forward(self, target_feat, msa_feat, residue_index, asym_id, entity_id, sym_id,
+                offset=None, msa=None, pair=None):
+        n, s = target_feat.shape[0], msa_feat.shape[0]
+        dev = target_feat.device
+        if msa is None:
+            msa = torch.empty(s, n, 256, dtype=torch.float32, device=dev)
+        if pair is None:
+            pair = torch.empty(n, n, 128, dtype=torch.float32, device=dev)
+        check(lib().bc2n_embedder_fwd(_stream(), _ptr(target_feat), _ptr(msa_feat),
+                                      _ptr(residue_index), _ptr(asym_id), _ptr(entity_id),
+                                      _ptr(sym_id), _ptr(offset), n, s, self.dir, _ptr(msa),
+                                      _ptr(pair)))
+        return msa, pair
+
+    def backward(self, dmsa, dpair, target_feat):
+        s, n = dmsa.shape[0], dmsa.shape[1]
+        dtf = torch.empty(n, 21, dtype=torch.float32, device=dmsa.device)
+        dmf = torch.empty(s, n, 49, dtype=torch.float32, device=dmsa.device)
+        check(lib().bc2n_embedder_bwd(_stream(), _ptr(dmsa), _ptr(dpair), _ptr(target_feat), n, s,
+                                      self.dir, _ptr(dtf), _ptr(dmf)))
+        return dtf, dmf
+
+
 class Fold:
     """The structure module's fold iterations (IPA + transition + rigid
     update, the part of StructureHeadsFwd/Bwd before the sidechain,

@@ -8,6 +8,7 @@ The manifest format is kept identical on purpose so a directory written by
 the reference's ``weights_from_params`` loads here unchanged: one line
 ``name file ndim d0 d1 ...`` per tensor, raw little-endian float32 files.
 """
+import math
 import os
 
 import numpy as np
@@ -142,6 +143,34 @@ def init_template_embedding_params(depth, rng, gates="zero", ln="identity"):
         out.update(init_template_block_params(b, rng, gates, ln))
     for pname, arr in init_module(template_embedding_shapes(), rng, gates, ln).items():
         out[f"param/{pname}"] = arr
+    return out
+
+
+def embedder_shapes(c_m=C_M, c_z=C_Z):
+    """The multimer embedder's input Linears (modules_multimer.py:441-483;
+    names as under param/ in the reference's embedder weights directory,
+    bindcraft/af/native.py:529-570): target_feat 21 wide, msa_feat 49,
+    73 relative-position features."""
+    return {"preprocess_1d/weights": (21, c_m), "preprocess_1d/bias": (c_m,),
+            "preprocess_msa/weights": (49, c_m), "preprocess_msa/bias": (c_m,),
+            "left_single/weights": (21, c_z), "left_single/bias": (c_z,),
+            "right_single/weights": (21, c_z), "right_single/bias": (c_z,),
+            "position_activations/weights": (73, c_z), "position_activations/bias": (c_z,)}
+
+
+def init_embedder_params(rng, scoped=False):
+    """Weights directory contents of the embedder; `scoped` puts
+    position_activations under evoformer/~_relative_encoding/ as haiku's
+    method scope (and the checkpoint) does."""
+    out = {}
+    for name, shape in embedder_shapes().items():
+        fan_in = shape[0] if len(shape) == 2 else 1
+        arr = rng.standard_normal(shape) / math.sqrt(fan_in)
+        if len(shape) == 1:
+            arr = 0.1 * rng.standard_normal(shape)
+        if scoped and name.startswith("position_activations/"):
+            name = "evoformer/~_relative_encoding/" + name
+        out[f"param/{name}"] = arr.astype(np.float32)
     return out
 
 

@@ -234,6 +234,37 @@ int bc2n_tplembed_bwd(void* stream, const float* ct, const float* query,
                       float* dquery);
 
 /* ------------------------------------------------------------------------
+ * Input embedder, multimer (the reference's EmbedderFwd / EmbedderBwd custom
+ * calls, native/ffi.cu:1046-1071 (handlers EmbFwdImpl / EmbBwdImpl :682-729)
+ * over native/embed.cuh:54-372, called from bindcraft/af/native.py:573-622
+ * for modules_multimer.py:358-483).  Replaces:
+ *   fwd(target_feat f32[N,21], msa_feat f32[S,N,49], residue_index f32[N],
+ *       asym_id f32[N], entity_id f32[N], sym_id f32[N]; weights_dir)
+ *       -> (msa f32[S,N,256], pair f32[N,N,128])
+ *   bwd(dmsa f32[S,N,256], dpair f32[N,N,128], target_feat; weights_dir)
+ *       -> (dtarget_feat f32[N,21], dmsa_feat f32[S,N,49])
+ * target_feat is already padded to 21 columns.  msa = preprocess_1d(tf)
+ * (zeroed on rows whose target_feat sums to zero) + preprocess_msa(msa_feat);
+ * pair = left_single(tf)[:,None] + right_single(tf)[None] + the relative
+ * encoding (max_relative_idx 32, max_relative_chain 2, chain-relative).
+ * offset, i32[N,N] or NULL, is the optional batch['offset'] feature
+ * (modules_multimer.py:384-388) that replaces residue_index[i] -
+ * residue_index[j] when present.  No save-set; the id features get no
+ * gradient.  Weights under param/{preprocess_1d, preprocess_msa,
+ * left_single, right_single}/ and position_activations under param/ or
+ * param/evoformer/~_relative_encoding/ (native.py:529-570).
+ * ---------------------------------------------------------------------- */
+int bc2n_embedder_fwd(void* stream, const float* target_feat, const float* msa_feat,
+                      const float* residue_index, const float* asym_id,
+                      const float* entity_id, const float* sym_id,
+                      const int32_t* offset, int N, int S, const char* weights_dir,
+                      float* msa, float* pair);
+int bc2n_embedder_bwd(void* stream, const float* dmsa, const float* dpair,
+                      const float* target_feat, int N, int S,
+                      const char* weights_dir, float* dtarget_feat,
+                      float* dmsa_feat);
+
+/* ------------------------------------------------------------------------
  * Structure module fold iterations (the IPA step of the post-trunk
  * StructureHeadsFwd/Bwd handlers, native/ffi.cu:1009-1044, up to and
  * excluding the sidechain; native/foldit.cuh:141-440, ipa.cuh:507-842,

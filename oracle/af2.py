@@ -336,6 +336,64 @@ def template_embedding(query, act_const, pair_mask, params, depth, stack_key, us
     return linear(torch.relu(act), P.sub("output_linear/"))
 
 
+# -------------------------------------------------------------------- embedder
+# modules_multimer.py:358-483 (multimer embedder; config.py:465-467:
+# use_chain_relative, max_relative_chain 2, max_relative_idx 32).
+MAX_RELATIVE_IDX = 32
+MAX_RELATIVE_CHAIN = 2
+
+
+def relative_encoding(residue_index, asym_id, entity_id, sym_id, p, offset=None,
+                      dtype=torch.float64):
+    """modules_multimer.py:358-435 (_relative_encoding, use_chain_relative):
+    the concatenation of a 66-wide one-hot of the clipped offset (bin 65 =
+    different chain), the same-entity flag and a 6-wide one-hot of the
+    clipped sym_id difference (bin 5 = different entity), [N,N,73], through
+    position_activations.  `offset` replaces residue_index[i] -
+    residue_index[j] when given (:384-388).  Ids are integer-valued."""
+    k, c = MAX_RELATIVE_IDX, MAX_RELATIVE_CHAIN
+    ri, ai = torch.as_tensor(residue_index).long(), torch.as_tensor(asym_id).long()
+    ei, si = torch.as_tensor(entity_id).long(), torch.as_tensor(sym_id).long()
+    asym_same = ai[:, None] == ai[None, :]
+    off = ri[:, None] - ri[None, :] if offset is None else torch.as_tensor(offset).long()
+    clipped = torch.clamp(off + k, 0, 2 * k)
+    final = torch.where(asym_same, clipped, torch.full_like(clipped, 2 * k + 1))
+    rel_pos = torch.nn.functional.one_hot(final, 2 * k + 2).to(dtype)
+    ent_same = ei[:, None] == ei[None, :]
+    rel_sym = si[:, None] - si[None, :]
+    clipped_chain = torch.clamp(rel_sym + c, 0, 2 * c)
+    final_chain = torch.where(ent_same, clipped_chain, torch.full_like(clipped_chain, 2 * c + 1))
+    rel_chain = torch.nn.functional.one_hot(final_chain, 2 * c + 2).to(dtype)
+    feat = torch.cat([rel_pos, ent_same.to(dtype)[..., None], rel_chain], -1)
+    return linear(feat, p)
+
+
+def embedder(target_feat, msa_feat, residue_index, asym_id, entity_id, sym_id, params,
+             offset=None, feature_mask=True, dtype=torch.float64):
+    """modules_multimer.py:441-483 + :510-511 (the four input Linears and the
+    relative encoding) on target_feat ALREADY padded to 21 columns (:450):
+    msa = preprocess_1d(tf)[None] + preprocess_msa(msa_feat), pair =
+    left_single(tf)[:, None] + right_single(tf)[None] + relative encoding.
+    feature_mask zeroes preprocess_1d on rows whose target_feat sums to zero,
+    as the reference's native embedder does (native/embed.cuh:22-25, 187-195,
+    310); the JAX path (:476-478) has no such mask, and the two agree wherever
+    no row sums to zero.  position_activations may sit under
+    param/evoformer/~_relative_encoding/ (haiku's method scope) or param/."""
+    P = Params(params, "param/", dtype)
+    pre1d = linear(target_feat, P.sub("preprocess_1d/"))
+    if feature_mask:
+        pre1d = pre1d * (target_feat.sum(-1) != 0).to(dtype)[:, None]
+    msa = pre1d[None] + linear(msa_feat, P.sub("preprocess_msa/"))
+    left = linear(target_feat, P.sub("left_single/"))
+    right = linear(target_feat, P.sub("right_single/"))
+    scoped = "param/evoformer/~_relative_encoding/position_activations/"
+    pos = Params(params, scoped if scoped + "weights" in params else "param/position_activations/",
+                 dtype)
+    pair = left[:, None] + right[None] + relative_encoding(residue_index, asym_id, entity_id,
+                                                           sym_id, pos, offset, dtype)
+    return msa, pair
+
+
 # ------------------------------------------------------------ structure module
 # folding_multimer.py (AF2 multimer structure module), config.py:578-600.
 IPA_HEADS, IPA_SCALAR_QK, IPA_POINT_QK, IPA_SCALAR_V, IPA_POINT_V = 12, 16, 4, 16, 8

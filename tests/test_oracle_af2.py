@@ -282,3 +282,83 @@ def test_fold_grad_finite_differences():
         fm = f(xm, z.detach()) if x is s else f(s.detach(), xm)
         fd = ((fp - fm) / (2 * eps)).item()
         assert abs(fd - gx[idx].item()) <= 1e-5 * max(1.0, abs(fd)), (idx, fd, gx[idx].item())
+
+
+def _two_chain_ids(n1, n2, same_entity):
+    ri = np.concatenate([np.arange(n1), np.arange(n2) + 3]).astype(np.float32)
+    ai = np.concatenate([np.full(n1, 1), np.full(n2, 2)]).astype(np.float32)
+    ei = np.concatenate([np.full(n1, 1), np.full(n2, 1 if same_entity else 2)]).astype(np.float32)
+    si = np.concatenate([np.full(n1, 1), np.full(n2, 2 if same_entity else 1)]).astype(np.float32)
+    return ri, ai, ei, si
+
+
+@pytest.mark.parametrize("same_entity,use_offset", [(True, False), (False, False), (True, True)])
+def test_relative_encoding_is_the_row_gather(same_entity, use_offset):
+    """The one-hot concatenation times position_activations equals, per (i,j),
+    W[rel] + [same entity] W[66] + W[67 + chain] + b with the bins written out
+    by hand (the gather form of native/embed.cuh:58-103)."""
+    rng = np.random.default_rng(11)
+    prm = bparams.init_embedder_params(rng)
+    W = prm["param/position_activations/weights"].astype(np.float64)
+    b = prm["param/position_activations/bias"].astype(np.float64)
+    ri, ai, ei, si = _two_chain_ids(40, 9, same_entity)
+    ri[20:] += 50  # offsets beyond +-32 inside chain 1
+    n = ri.shape[0]
+    off = rng.integers(-40, 41, (n, n)).astype(np.int32) if use_offset else None
+    got = af2.relative_encoding(ri, ai, ei, si, af2.Params(prm, "param/position_activations/"),
+                                off).numpy()
+    for i in range(n):
+        for j in range(n):
+            o = int(off[i, j]) if use_offset else int(ri[i]) - int(ri[j])
+            rel = min(max(o + 32, 0), 64) if ai[i] == ai[j] else 65
+            chain = min(max(int(si[i]) - int(si[j]) + 2, 0), 4) if ei[i] == ei[j] else 5
+            want = W[rel] + (W[66] if ei[i] == ei[j] else 0) + W[67 + chain] + b
+            np.testing.assert_allclose(got[i, j], want, rtol=0, atol=1e-12)
+    # the bins the cases above must visit
+    if not use_offset:
+        assert (np.abs(ri[:20, None] - ri[None, 20:40]) > 32).all()
+
+
+def test_embedder_structure_and_feature_mask():
+    """msa[s,n] - preprocess_msa(mf)[s,n] is the same for every s and zero on
+    a padded (all-zero) target_feat row; pair - relpos splits into a row term
+    plus a column term; the gradients are the row/column sums and the S-sum
+    (finite differences on a tiny case pin the autograd)."""
+    rng = np.random.default_rng(12)
+    prm = bparams.init_embedder_params(rng, scoped=True)
+    n, s = 6, 3
+    tf = np.zeros((n, 21))
+    tf[:, :20] = rng.dirichlet(np.ones(20), n)
+    tf[4] = 0.0  # padded residue
+    mf = rng.standard_normal((s, n, 49))
+    ri, ai, ei, si = _two_chain_ids(4, 2, False)
+    T = lambda a: torch.tensor(a, dtype=torch.float64, requires_grad=True)
+    tft, mft = T(tf), T(mf)
+    msa, pair = af2.embedder(tft, mft, ri, ai, ei, si, prm)
+    P = af2.Params(prm, "param/")
+    premsa = af2.linear(torch.as_tensor(mf), P.sub("preprocess_msa/"))
+    d = (msa - premsa).detach()
+    assert torch.allclose(d, d[:1].expand_as(d), atol=1e-12)
+    assert torch.count_nonzero(d[:, 4]) == 0 and torch.count_nonzero(d[:, 3]) > 0
+    rel = af2.relative_encoding(ri, ai, ei, si, af2.Params(
+        prm, "param/evoformer/~_relative_encoding/position_activations/"))
+    q = (pair - rel).detach()
+    assert torch.allclose(q, q[:, :1] + q[:1, :] - q[:1, :1], atol=1e-12)
+    # gradient against central differences
+    dm, dp = rng.standard_normal((s, n, 256)), rng.standard_normal((n, n, 128))
+    loss = (msa * torch.as_tensor(dm)).sum() + (pair * torch.as_tensor(dp)).sum()
+    gtf, gmf = torch.autograd.grad(loss, (tft, mft))
+
+    def f(tf_, mf_):
+        a, p = af2.embedder(torch.as_tensor(tf_), torch.as_tensor(mf_), ri, ai, ei, si, prm)
+        return float((a * torch.as_tensor(dm)).sum() + (p * torch.as_tensor(dp)).sum())
+
+    h = 1e-6
+    for (i, k) in [(0, 3), (3, 20), (5, 7)]:
+        e = np.zeros_like(tf); e[i, k] = h
+        fd = (f(tf + e, mf) - f(tf - e, mf)) / (2 * h)
+        assert abs(fd - gtf[i, k].item()) <= 1e-5 * max(1.0, abs(fd))
+    for (t, i, k) in [(0, 0, 0), (2, 5, 48)]:
+        e = np.zeros_like(mf); e[t, i, k] = h
+        fd = (f(tf, mf + e) - f(tf, mf - e)) / (2 * h)
+        assert abs(fd - gmf[t, i, k].item()) <= 1e-5 * max(1.0, abs(fd))
