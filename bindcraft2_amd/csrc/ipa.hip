@@ -582,6 +582,7 @@ FoldW fold_weights(WeightStore& ws) {
       const std::string bn = I + names[m] + "/bias";  // the scalar biases may be absent (zero)
       if (ws.has(bn)) {
         const HostTensor& t = ws.host(bn);
+        if (t.data.size() != (size_t)width[m]) throw std::runtime_error("fold: " + bn + " has the wrong size");
         for (int j = 0; j < width[m]; ++j) c[off + j] = t.data[j];
       }
       off += width[m];
