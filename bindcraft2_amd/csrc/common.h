@@ -93,6 +93,14 @@ __device__ __forceinline__ float group_max(float v) {
   return group_reduce<W>(v, [](float a, float b) { return fmaxf(a, b); });
 }
 
+// Row of an N x N grid read in transposed order: row m of the transposed
+// view is row (m % nt) * nt + m / nt of the stored one (nt <= 0: identity).
+__device__ __forceinline__ long ln_src_row(long m, int nt) {
+  if (nt <= 0) return m;
+  const long p = m / nt, q = m % nt;
+  return q * nt + p;
+}
+
 // 16-byte vector load/store of 8 bf16 values.
 __device__ __forceinline__ bf16x8 ld8(const bf16* p) {
   return *reinterpret_cast<const bf16x8*>(p);

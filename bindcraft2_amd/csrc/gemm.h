@@ -76,6 +76,15 @@ struct epi_two_phase : std::false_type {};
 template <class E>
 struct epi_two_phase<E, std::void_t<decltype(E::kTwoPhase)>> : std::bool_constant<E::kTwoPhase> {};
 
+// An epilogue with kRowBlock = true takes each staged half tile whole: all
+// 256 threads call block<WM>(b, mb, T, ldt, tid) over its WM rows x BN
+// columns (rows mb.., row stride ldt in LDS), for row-wise reductions.  It
+// needs every column of a row in one tile (N == BN, checked on the host).
+template <class E, class = void>
+struct epi_row_block : std::false_type {};
+template <class E>
+struct epi_row_block<E, std::void_t<decltype(E::kRowBlock)>> : std::bool_constant<E::kRowBlock> {};
+
 // Base of every epilogue: row mode only.
 struct EpiRows {
   static constexpr bool kHasCol = false;
@@ -281,7 +290,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi, AL al = 
         epi.row(b, m, n, v);
       }
     };
-    if (colm) {
+    if constexpr (epi_row_block<Epi>::value) {
+      epi.template block<WM>(b, mb, T, LDT, tid);
+    } else if (colm) {
       for (int it = tid; it < BN * (WM / 8); it += 256) {
         const int c = it % BN, rg = it / BN;
         const int m = mb + rg * 8, n = n0 + c;
@@ -319,6 +330,8 @@ void gemm(hipStream_t st, const GemmArgs& g, const Epi& epi, const char* name = 
   gemm_check(g.K % 32 == 0, "K must be a multiple of 32");
   gemm_check(g.N % 8 == 0, "N must be a multiple of 8 (vector epilogue)");
   gemm_check(!Epi::kHasCol || g.M % 8 == 0, "M must be a multiple of 8 (column epilogue)");
+  gemm_check(!epi_row_block<Epi>::value || (g.N == BN && g.batch == 1),
+             "row-block epilogue: one tile column (N == BN)");
   const bool ak = (g.a_sk == 1), bk = (g.b_sk == 1);
   gemm_check(ak || g.a_sm == 1, "A needs a unit stride");
   gemm_check(bk || g.b_sn == 1, "B needs a unit stride");
@@ -502,6 +515,78 @@ struct ALoadReluBf16 {
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = (float)v[e] > 0.f ? v[e] : (bf16)0.f;
     return v;
+  }
+};
+
+
+// LayerNorm backward fused into the GEMM that produces its cotangent dy (the
+// d(LN output) of a module's input projections), C = BN = 128 channels, with
+// the residual cotangent added:
+//   out[src] = dres[src] + rstd * (g - mean(g) - xhat * mean(g * xhat)),
+//   g = gamma * (dy + sum_h dbias[h][m] wb[c][h]),  xhat = (x[src] - mean) * rstd,
+// src = ln_src_row(m, nt) (the transposed orientation when nt > 0).  dres
+// may alias out.  16 lanes per row (a DPP row), 8 channels each.
+template <int H>
+struct EpiLnBwd : EpiRows {
+  static constexpr bool kRowBlock = true;
+  static constexpr int C = 128;
+  const float *x, *gamma, *mean, *rstd, *dres, *dbias, *wb;
+  float* out;
+  long M;
+  int nt;
+  EpiLnBwd(const float* x_, const float* g_, const float* mu_, const float* rs_, const float* dres_,
+           float* out_, long M_, int nt_, const float* dbias_ = nullptr, const float* wb_ = nullptr)
+      : x(x_), gamma(g_), mean(mu_), rstd(rs_), dres(dres_), dbias(dbias_), wb(wb_), out(out_),
+        M(M_), nt(nt_) {}
+  __device__ __forceinline__ void row(int, int, int, const float (&)[8]) const {}
+  template <int WM>
+  __device__ __forceinline__ void block(int, long mb, const float* T, int ldt, int tid) const {
+    const int lr = tid >> 4, c0 = (tid & 15) * 8;
+    float gm[8];
+    ld_f8(gamma + c0, gm);
+    float w[8][H > 0 ? H : 1];
+    if constexpr (H > 0) {
+      const float4* p = reinterpret_cast<const float4*>(wb + c0 * H);
+#pragma unroll
+      for (int i = 0; i < 2 * H; ++i) {
+        const float4 q = p[i];
+        const float f[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) w[(4 * i + k) / H][(4 * i + k) % H] = f[k];
+      }
+    }
+#pragma unroll 1
+    for (int r0 = 0; r0 < WM; r0 += 16) {
+      const long m = mb + r0 + lr;
+      if (m >= M) continue;  // the row's 16 lanes leave together
+      float g[8], xv[8], dr[8];
+      ld_f8(T + (r0 + lr) * ldt + c0, g);
+      const long src = ln_src_row(m, nt);
+      ld_f8(x + src * C + c0, xv);
+      ld_f8(dres + src * C + c0, dr);
+      if constexpr (H > 0) {
+#pragma unroll
+        for (int h = 0; h < H; ++h) {
+          const float db = dbias[(long)h * M + m];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) g[e] += db * w[e][h];
+        }
+      }
+      const float mu = mean[m], rs = rstd[m];
+      float sg = 0.f, sgx = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        xv[e] = (xv[e] - mu) * rs;
+        g[e] *= gm[e];
+        sg += g[e];
+        sgx += g[e] * xv[e];
+      }
+      sg = group_sum<16>(sg) * (1.f / C);
+      sgx = group_sum<16>(sgx) * (1.f / C);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dr[e] += rs * (g[e] - sg - xv[e] * sgx);
+      st_f8(out + src * C + c0, dr);
+    }
   }
 };
 

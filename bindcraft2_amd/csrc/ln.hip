@@ -38,11 +38,6 @@ __device__ __forceinline__ void load8f<bf16>(const bf16* p, float (&v)[8]) {
   for (int e = 0; e < 8; ++e) v[e] = (float)a[e];
 }
 
-__device__ __forceinline__ long ln_src_row(long m, int nt) {
-  if (nt <= 0) return m;
-  const long p = m / nt, q = m % nt;
-  return q * nt + p;
-}
 
 template <int H>
 __device__ __forceinline__ void load_w(const float* __restrict__ wb, int c0, float (&w)[8][H]) {

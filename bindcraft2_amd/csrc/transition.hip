@@ -102,6 +102,12 @@ void transition_bwd(hipStream_t st, const TransW& w, long rows, int nt, const fl
   g2.M = (int)rows; g2.N = C; g2.K = H;
   g2.A = dh; g2.a_sm = H; g2.a_sk = 1;
   g2.B = w.w1; g2.b_sn = H; g2.b_sk = 1;
+  if (C == 128) {
+    // the input LayerNorm's backward and the residual add in the epilogue
+    gemm<128, 128>(st, g2, EpiLnBwd<0>(act_in, w.ln_g, sv.mean, sv.rstd, dout, din, rows, 0),
+                   "trans.gemm_dx_ln");
+    return;
+  }
   gemm<128, 128>(st, g2, EpiStore<float>{dxn, C, 0, nullptr, C}, "trans.gemm_dx");
   if (din != dout)
     BC2N_HIP(hipMemcpyAsync(din, dout, (size_t)rows * C * 4, hipMemcpyDeviceToDevice, st));

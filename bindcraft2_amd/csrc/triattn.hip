@@ -197,6 +197,15 @@ void triattn_bwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
   g2.M = (int)M; g2.N = C; g2.K = 4 * HD;
   g2.A = b.dqkvg; g2.a_sm = 4L * HD; g2.a_sk = 1;
   g2.B = w.wqkvg; g2.b_sn = 4L * HD; g2.b_sk = 1;
+  if (C == 128 && H == 4) {
+    // the input LayerNorm's backward (with the pair-bias projection's term)
+    // and the residual add in the epilogue
+    gemm<128, 128>(st, g2,
+                   EpiLnBwd<4>(pair_in, w.ln_g, sv.mean, sv.rstd, dout, din, M, per_column ? N : 0,
+                               b.dbias, w.w2d),
+                   "triattn.gemm_dx_ln");
+    return;
+  }
   gemm<128, 128>(st, g2, EpiStore<float>{dxn, C, 0, nullptr, C}, "triattn.gemm_dx");
 
   if (din != dout)

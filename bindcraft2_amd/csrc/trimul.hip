@@ -338,14 +338,14 @@ void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
   need.take<bf16>((size_t)M * I);   // dT
   need.take<bf16>((size_t)M * I);   // dL
   need.take<bf16>((size_t)M * I);   // dR
-  need.take<float>((size_t)M * C);  // dxn
+  if (C != 128) need.take<float>((size_t)M * C);  // dxn (C = 128: fused LayerNorm backward)
   ar.reset(st, need.off);
   bf16* dcat = ar.take_n<bf16>((size_t)M * NC);
   float* dtn = ar.take_n<float>((size_t)M * I);
   bf16* dT = ar.take_n<bf16>((size_t)M * I);
   bf16* dL = ar.take_n<bf16>((size_t)M * I);
   bf16* dR = ar.take_n<bf16>((size_t)M * I);
-  float* dxn = ar.take_n<float>((size_t)M * C);
+  float* dxn = C != 128 ? ar.take_n<float>((size_t)M * C) : nullptr;
 
   // d(tn) = (tbl*dout*g_out) . Wo^T, the operand built as the GEMM loads it;
   // the loader also writes the gating_linear columns of dcat
@@ -393,6 +393,12 @@ void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
   g2.M = (int)M; g2.N = C; g2.K = NC;
   g2.A = dcat; g2.a_sm = NC; g2.a_sk = 1;
   g2.B = w.wcat; g2.b_sn = NC; g2.b_sk = 1;
+  if (C == 128) {
+    // the input LayerNorm's backward and the residual add in the epilogue
+    gemm<128, 128>(st, g2, EpiLnBwd<0>(pair_in, w.ln_g, sv.mean, sv.rstd, dout, din, M, 0),
+                   "trimul.gemm_dx_ln");
+    return;
+  }
   gemm<128, 128>(st, g2, EpiStore<float>{dxn, C, 0, nullptr, C}, "trimul.gemm_dx");
   if (din != dout)
     BC2N_HIP(hipMemcpyAsync(din, dout, (size_t)M * C * 4, hipMemcpyDeviceToDevice, st));
