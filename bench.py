@@ -86,6 +86,13 @@ def kernel_model(name, n):
         "trimul.gemm_out": (gemm(c, c), m * (256 + 256 + 512 + 256 + 512)),
         "trimul.gemm_dout": (gemm(c, c), m * (512 + 256 + 256 + 512 + 256)),
         "trimul.gemm_dx": (gemm(5 * c, c), m * (1280 + 512)),
+        # recompute GEMM + d(cat) + dX GEMM + LayerNorm backward: xn, d(left|right),
+        # d(cat)'s gating columns, mask, x, dout read; din written
+        "trimul.tail_bwd": (gemm(c, 4 * c) + gemm(5 * c, c),
+                            m * (256 + 512 + 256 + 4 + 512 + 512 + 512 + 8)),
+        "trimul.gemm_dx_ln": (gemm(5 * c, c), m * (1280 + 512 * 3 + 8)),
+        "triattn.gemm_dx_ln": (gemm(4 * c, c), m * (1024 + 512 * 3 + 16 + 8)),
+        "trans.gemm_dx_ln": (gemm(4 * c, c), m * (1024 + 512 * 3 + 8)),
         "trans.gemm1": (gemm(c, 4 * c), m * (256 + 1024)),
         "trans.gemm2": (gemm(4 * c, c), m * (1024 + 512 + 512)),
         "trans.gemm_dh": (gemm(c, 4 * c), m * (512 + 1024 + 1024)),
@@ -397,7 +404,8 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--n", type=int, default=224)
-    ap.add_argument("--workload", choices=["trunk", "triattn", "fold", "copy"], default="trunk")
+    ap.add_argument("--workload", choices=["trunk", "triattn", "trimul", "fold", "copy"],
+                    default="trunk")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--pmc-summarize", nargs=5, metavar=("FETCH_CSV", "WRITE_CSV", "COPY_FETCH_CSV",
                                                          "COPY_WRITE_CSV", "OUT_JSON"),
@@ -501,6 +509,34 @@ def main():
                                        "(BASELINE configs[1])", "L": n, "c_z": 128, "heads": 4,
                            "head_dim": 32, "masked_residues": 0.1, "flops_per_step": flops}}
         cpu = None if args.no_cpu_baseline else cpu_triattn_baseline(n)
+    elif args.workload == "trimul":
+        mods = ["triangle_multiplication_outgoing", "triangle_multiplication_incoming"]
+        prm = bparams.init_block_params(0, rng, modules=mods, gates="zero")
+        wdir = bparams.write_manifest(tempfile.mkdtemp(prefix="bc2n_bench_"), prm)
+        pair = torch.randn(n, n, 128, device=dev)
+        dout = torch.randn(n, n, 128, device=dev)
+        ones = torch.ones(n, n, device=dev)  # configs[2]: all-ones mask
+        layers = [ops.TriangleMultiplication(wdir, f"param/block0/{mods[i]}/", outgoing=(i == 0))
+                  for i in range(2)]
+        outs = [torch.empty_like(pair) for _ in layers]
+        dins = [torch.empty_like(pair) for _ in layers]
+        saves = [torch.empty(l.save_bytes(n), dtype=torch.uint8, device=dev) for l in layers]
+
+        def step():
+            for l, o, s, d in zip(layers, outs, saves, dins):
+                l.forward(pair, ones, None, out=o, save=s)
+                l.backward(pair, ones, None, s, dout, din=d)
+
+        ms = timed(step, args.steps, args.warmup)
+        flops = 2 * trimul_flops(n)
+        prof = profiled(step, args.steps, args.no_kprof)
+        line = {"metric": "triangle multiplication fwd+bwd, outgoing + incoming (TFLOP/s)",
+                "value": round(flops / (ms * 1e-3) / 1e12, 3),
+                "unit": "TFLOP/s", "higher_is_better": True,
+                "config": {"workload": "triangle multiplication fwd+bwd, outgoing+incoming "
+                                       "(BASELINE configs[2])", "L": n, "c_z": 128, "hidden": 128,
+                           "mask": "all ones", "flops_per_step": flops}}
+        cpu = None
     else:
         # weights: 48 Evoformer blocks, 4 pair-only extra blocks, 2 template blocks
         evo = {}
@@ -573,7 +609,7 @@ def main():
            "config": line.pop("config"), "roofline": roofline_from(prof, n),
            "cpu_baseline": cpu}
     out.update(line)
-    if prof and args.workload in ("trunk", "triattn"):
+    if prof and args.workload in ("trunk", "triattn", "trimul"):
         out["kernel_rooflines"] = kernel_rooflines(prof, n)
     out["kernels"] = kernel_table(prof)
     print(json.dumps(out))

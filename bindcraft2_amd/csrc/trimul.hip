@@ -196,6 +196,259 @@ struct ALoadTrimulOut {
   }
 };
 
+// ---------------------------------------------------------------------------
+// The backward's tail in one kernel (C = I = 128):
+//
+//   P   = xn . Wcat[:, :4I]                    (recompute, K = C)
+//   d(cat)[:, :4I] from P, d(left|right), mask (the EpiTrimulProjBwd formulas)
+//   dy  = d(cat) . Wcat^T                      (K = 4I + C; the last C columns
+//                                               of d(cat) come from memory)
+//   din = dout + LN'(dy)                       (the input LayerNorm's backward)
+//
+// d(cat)'s [proj|gate] columns never leave registers: GEMM1 runs transposed
+// (the weights as the first MFMA operand), so a lane ends with row m = l%16 and
+// 4 consecutive columns 4g..4g+3 of a 16-column block.  The proj block and its
+// gate block (16 columns to the right) land in the same lane positions, so the
+// epilogue pairs them in registers, and the 8 values {proj 4g..4g+3, gate
+// 4g..4g+3} of a 32-column block are exactly one k-slot set of a 32-deep MFMA
+// step of GEMM2 -- the same slot order that its weights are read in.  GEMM2
+// also runs transposed, so each lane holds 32 channels (16j + 4g + r) of its
+// row for the LayerNorm's row sums (completed across the 4 lanes of the row).
+//
+// Workgroup: 128 rows, 4 waves of 32 rows (two 16-row tiles).  The weights
+// stream through LDS in 10 chunks (8 of 64 GEMM1 columns, with the matching
+// 64 rows of GEMM2's K, and 2 chunks of the gating_linear K), double-buffered
+// with a register prefetch of the next chunk.
+namespace tail {
+constexpr int C = 128, I = 128, NC = 4 * I + C;
+constexpr int BM = 128;
+constexpr int CH = 64;                    // GEMM1 columns (= GEMM2 k) per chunk
+constexpr int NPG = 4 * I / CH;           // [proj|gate] chunks
+constexpr int NCHUNK = NPG + C / CH;      // + gating_linear chunks
+constexpr int LD1 = C + 8;                // B1 chunk: [CH][C] (n rows, k contiguous)
+constexpr int LD2 = CH + 8;               // B2 chunk: [C][CH] (c rows, k contiguous)
+constexpr int B1E = CH * LD1, B2E = C * LD2;
+}  // namespace tail
+
+// 8 bf16 of row `row` at k = k0 + {4g..4g+3, 16+4g..16+4g+3} of a
+// K-contiguous tile (row stride ld), global or LDS.
+__device__ __forceinline__ bf16x8 kslots(const bf16* T, long ld, long row, int k0, int g) {
+  const bf16* p = T + row * ld + k0 + 4 * g;
+  const bf16x4 a = *reinterpret_cast<const bf16x4*>(p);
+  const bf16x4 b = *reinterpret_cast<const bf16x4*>(p + 16);
+  bf16x8 r;
+  r[0] = a[0]; r[1] = a[1]; r[2] = a[2]; r[3] = a[3];
+  r[4] = b[0]; r[5] = b[1]; r[6] = b[2]; r[7] = b[3];
+  return r;
+}
+
+struct TailArgs {
+  const bf16* xn;      // [M][C]
+  const bf16* wcat_t;  // [NC][C]
+  const bf16* wcat;    // [C][NC]
+  const bf16 *dl, *dr; // [I][M]
+  const bf16* dcg;     // [M][C]: d(cat)'s gating_linear columns
+  const float *bp, *bg, *mask;
+  const float *x, *ln_g, *mean, *rstd, *dres;
+  float* out;
+  long M;
+};
+
+__global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
+  using namespace tail;
+  __shared__ __attribute__((aligned(16))) bf16 B1s[2 * B1E];
+  __shared__ __attribute__((aligned(16))) bf16 B2s[2 * B2E];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, l16 = lane & 15;
+  const long m0 = (long)blockIdx.x * BM + wave * 32;
+  const long M = a.M;
+
+  // ---- chunk staging: 16 KB of B1 and 16 KB of B2 per chunk, 4 + 4 16-byte pieces a thread
+  // Chunk s's operands are fetched during chunk s - 1: its weights into
+  // p1/p2 (stored to LDS at the end of chunk s - 1), and the lane's own
+  // operands into registers -- d(left|right) at its rows and channels (da) for
+  // a [proj|gate] chunk, its d(cat) gating fragments (in p1) for the others.
+  // The weights are issued first, so waiting for them leaves the rest in flight.
+  bf16x8 p1[4], p2[4];
+  bf16 da[2][2][4];
+  auto prefetch = [&](int s) {
+    if (s < NPG) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int c = tid + 256 * q, r = c / (C / 8), k8 = (c % (C / 8)) * 8;
+        p1[q] = ld8(a.wcat_t + (long)(s * CH + r) * C + k8);
+      }
+    }
+    const int kb = s < NPG ? s * CH : 4 * I + (s - NPG) * CH;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int c = tid + 256 * q, r = c / (CH / 8), k8 = (c % (CH / 8)) * 8;
+      p2[q] = ld8(a.wcat + (long)r * NC + kb + k8);
+    }
+    if (s < NPG) {
+      const bf16* dsrc = s < NPG / 2 ? a.dl : a.dr;
+      const int chb = (s % (NPG / 2)) * 32;  // channel within left or right
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            da[i][q][r] = dsrc[(long)(chb + q * 16 + 4 * g + r) * M + m0 + i * 16 + l16];
+    } else {
+      const int kc = (s - NPG) * CH;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int q = 0; q < 2; ++q) p1[2 * i + q] = kslots(a.dcg, C, m0 + i * 16 + l16, kc + q * 32, g);
+    }
+  };
+  auto stash = [&](int s, int buf) {
+    if (s < NPG) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int c = tid + 256 * q, r = c / (C / 8), k8 = (c % (C / 8)) * 8;
+        st8(B1s + buf * B1E + r * LD1 + k8, p1[q]);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int c = tid + 256 * q, r = c / (CH / 8), k8 = (c % (CH / 8)) * 8;
+      st8(B2s + buf * B2E + r * LD2 + k8, p2[q]);
+    }
+  };
+
+  prefetch(0);
+  // xn fragments of the wave's two row tiles, all of K, in GEMM1's slot order
+  bf16x8 xf[2][C / 32];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int ks = 0; ks < C / 32; ++ks) xf[i][ks] = kslots(a.xn, C, m0 + i * 16 + l16, ks * 32, g);
+  float mk[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) mk[i] = a.mask[m0 + i * 16 + l16];
+  stash(0, 0);
+  __syncthreads();
+
+  f32x4 acc2[2][C / 16];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < C / 16; ++j) acc2[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll 1
+  for (int s = 0; s < NCHUNK; ++s) {
+    const int buf = s & 1;
+    const bf16* b1 = B1s + buf * B1E;
+    const bf16* b2 = B2s + buf * B2E;
+    bf16x8 af[2][2];  // GEMM2 A fragments: [row tile][k-step of this chunk]
+    if (s < NPG) {
+      // GEMM1: P for 4 column blocks (proj, gate, proj, gate)
+      f32x4 acc1[2][4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc1[i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < C / 32; ++ks) {
+        bf16x8 bfr[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) bfr[t] = kslots(b1, LD1, t * 16 + l16, ks * 32, g);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            acc1[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr[t], xf[i][ks], acc1[i][t], 0, 0, 0);
+      }
+      // epilogue: d(proj) = a * sigmoid(gate), d(gate) = a * proj * s (1 - s), a = d(act) * mask
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int ch = s * 32 + q * 16 + 4 * g;  // channel of slot r = ch + r (0..2I)
+        float bpv[4], bgv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) { bpv[r] = a.bp[ch + r]; bgv[r] = a.bg[ch + r]; }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          bf16x8 f;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float pv = acc1[i][2 * q][r] + bpv[r];
+            const float sg = sigmoidf_(acc1[i][2 * q + 1][r] + bgv[r]);
+            const float ad = (float)da[i][q][r] * mk[i];
+            f[r] = (bf16)(ad * sg);
+            f[4 + r] = (bf16)(ad * pv * sg * (1.f - sg));
+          }
+          af[i][q] = f;
+        }
+      }
+    } else {
+      // gating_linear columns of d(cat), fetched during the previous chunk
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int q = 0; q < 2; ++q) af[i][q] = p1[2 * i + q];
+    }
+    // the next chunk's operands load behind GEMM2 (the weights are
+    // L2-resident: every workgroup reads the same 288 KB)
+    if (s + 1 < NCHUNK) prefetch(s + 1);
+    // GEMM2: dy[m][c] += d(cat)[m][k] Wcat[c][k] over the chunk's 64 k
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+#pragma unroll
+      for (int j = 0; j < C / 16; ++j) {
+        const bf16x8 bfr = kslots(b2, LD2, j * 16 + l16, q * 32, g);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+          acc2[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr, af[i][q], acc2[i][j], 0, 0, 0);
+      }
+    }
+    if (s + 1 < NCHUNK) stash(s + 1, buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- LayerNorm backward + residual: lane has channels 16j + 4g + r of row m
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const long m = m0 + i * 16 + l16;
+    const float mu = a.mean[m], rs = a.rstd[m];
+    float xh[C / 16][4], gg[C / 16][4];
+    float sg = 0.f, sgx = 0.f;
+#pragma unroll
+    for (int j = 0; j < C / 16; ++j) {
+      const int c = 16 * j + 4 * g;
+      const float4 xv = *reinterpret_cast<const float4*>(a.x + m * C + c);
+      const float4 gm = *reinterpret_cast<const float4*>(a.ln_g + c);
+      const float xa[4] = {xv.x, xv.y, xv.z, xv.w}, ga[4] = {gm.x, gm.y, gm.z, gm.w};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        xh[j][r] = (xa[r] - mu) * rs;
+        gg[j][r] = acc2[i][j][r] * ga[r];
+        sg += gg[j][r];
+        sgx += gg[j][r] * xh[j][r];
+      }
+    }
+    sg += __shfl_xor(sg, 16, 64);
+    sg += __shfl_xor(sg, 32, 64);
+    sgx += __shfl_xor(sgx, 16, 64);
+    sgx += __shfl_xor(sgx, 32, 64);
+    sg *= 1.f / C;
+    sgx *= 1.f / C;
+#pragma unroll
+    for (int j = 0; j < C / 16; ++j) {
+      const int c = 16 * j + 4 * g;
+      const float4 d = *reinterpret_cast<const float4*>(a.dres + m * C + c);
+      float4 o;
+      o.x = d.x + rs * (gg[j][0] - sg - xh[j][0] * sgx);
+      o.y = d.y + rs * (gg[j][1] - sg - xh[j][1] * sgx);
+      o.z = d.z + rs * (gg[j][2] - sg - xh[j][2] * sgx);
+      o.w = d.w + rs * (gg[j][3] - sg - xh[j][3] * sgx);
+      *reinterpret_cast<float4*>(a.out + m * C + c) = o;
+    }
+  }
+}
+
 }  // namespace
 
 TriMulW trimul_weights(WeightStore& ws, const std::string& P) {
@@ -332,20 +585,24 @@ void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
   TriMulSave<Carver> sv(cv, N, C, I);
   Arena& ar = arena();
   std::lock_guard<std::recursive_mutex> lk(ar.lock());
+  // C = I = 128: the tail kernel keeps d(cat)'s [proj|gate] columns in
+  // registers; only its gating_linear columns ([M][C]) go through memory
+  const bool fused = (C == tail::C && I == tail::I && M % tail::BM == 0);
+  const int ldcat = fused ? C : NC, off = fused ? 0 : 4 * I;
   Sizer need;
-  need.take<bf16>((size_t)M * NC);  // dcat
+  need.take<bf16>((size_t)M * ldcat);  // dcat
   need.take<float>((size_t)M * I);  // dTn
   need.take<bf16>((size_t)M * I);   // dT
   need.take<bf16>((size_t)M * I);   // dL
   need.take<bf16>((size_t)M * I);   // dR
-  if (C != 128) need.take<float>((size_t)M * C);  // dxn (C = 128: fused LayerNorm backward)
+  if (!fused) need.take<float>((size_t)M * C);  // dxn
   ar.reset(st, need.off);
-  bf16* dcat = ar.take_n<bf16>((size_t)M * NC);
+  bf16* dcat = ar.take_n<bf16>((size_t)M * ldcat);
   float* dtn = ar.take_n<float>((size_t)M * I);
   bf16* dT = ar.take_n<bf16>((size_t)M * I);
   bf16* dL = ar.take_n<bf16>((size_t)M * I);
   bf16* dR = ar.take_n<bf16>((size_t)M * I);
-  float* dxn = C != 128 ? ar.take_n<float>((size_t)M * C) : nullptr;
+  float* dxn = fused ? nullptr : ar.take_n<float>((size_t)M * C);
 
   // d(tn) = (tbl*dout*g_out) . Wo^T, the operand built as the GEMM loads it;
   // the loader also writes the gating_linear columns of dcat
@@ -354,7 +611,7 @@ void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
   g1.a_sm = C; g1.a_sk = 1;
   g1.B = w.wo; g1.b_sn = C; g1.b_sk = 1;
   gemm<128, 128>(st, g1, EpiStore<float>{dtn, I, 0, nullptr, I}, "trimul.gemm_dout",
-                 ALoadTrimulOut{dout, tbl, sv.gout, sv.osave, dcat, C, NC, 4 * I, N});
+                 ALoadTrimulOut{dout, tbl, sv.gout, sv.osave, dcat, C, ldcat, off, N});
   {
     KTimed kt("trimul.ln_center_bwd", st);
     ln_bwd_cm(st, dtn, sv.T, M, I, w.cn_g, sv.cmean, sv.crstd, dT);
@@ -380,6 +637,17 @@ void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
     }
     contract<bf16>(st, a, dL, "trimul.contract_bwd");
     contract<bf16>(st, b, dR, "trimul.contract_bwd");
+  }
+  if (fused) {
+    TailArgs t;
+    t.xn = sv.xn; t.wcat_t = w.wcat_t; t.wcat = w.wcat;
+    t.dl = dL; t.dr = dR; t.dcg = dcat;
+    t.bp = w.bp; t.bg = w.bg; t.mask = mask;
+    t.x = pair_in; t.ln_g = w.ln_g; t.mean = sv.mean; t.rstd = sv.rstd; t.dres = dout;
+    t.out = din; t.M = M;
+    KTimed kt("trimul.tail_bwd", st);
+    hipLaunchKernelGGL(trimul_tail_kernel, dim3((unsigned)(M / tail::BM)), dim3(256), 0, st, t);
+    return;
   }
   {
     GemmArgs g;
