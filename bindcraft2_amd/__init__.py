@@ -74,6 +74,11 @@ def _declare(L):
         "bc2n_fold_save_bytes": (sz, [cs, i, c.c_int64]),
         "bc2n_fold_fwd": (i, [vp, vp, vp, vp, vp, i, i, c.c_int64, c.c_int64, cs, vp, vp, vp]),
         "bc2n_fold_bwd": (i, [vp, vp, vp, vp, vp, vp, vp, i, c.c_int64, c.c_int64, cs, vp, vp]),
+        "bc2n_structure_heads_save_bytes": (sz, [cs, i, c.c_int64]),
+        "bc2n_structure_heads_fwd": (i, [vp, vp, vp, vp, vp, vp, i, i, c.c_int64, c.c_int64, cs,
+                                         vp, vp, vp, vp, vp, vp]),
+        "bc2n_structure_heads_bwd": (i, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i, c.c_int64,
+                                         c.c_int64, cs, vp, vp]),
         "bc2n_dropout_table": (i, [vp, vp, i, i, u32, u32, f]),
         "bc2n_bernoulli_bits": (i, [vp, vp, c.c_long, u32, u32, f]),
         "bc2n_stack_keys": (i, [vp, vp, i, vp]),

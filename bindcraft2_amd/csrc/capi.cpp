@@ -6,6 +6,7 @@
 #include "modules.h"
 #include "tplembed.h"
 #include "embed.h"
+#include "heads.h"
 
 #include <map>
 #include <tuple>
@@ -548,6 +549,66 @@ int bc2n_fold_bwd(void* stream, const float* d_act, const float* d_traj, const f
     const FoldW& w = fold_w(weights_dir);
     fold_bwd(as_stream(stream), w, N, (int)depth, single, pair, seq_mask, dropout != 0, save,
              d_act, d_traj, dsingle, dpair);
+  });
+}
+
+// ------------------------------------------------ structure module + heads
+
+namespace {
+std::map<std::pair<std::string, std::string>, StructHeadsW> g_sh;
+const StructHeadsW& sh_w(const char* dir) {
+  return cached(g_sh, dir, "", [&](WeightStore& ws, const std::string&) { return structheads_weights(ws); });
+}
+}  // namespace
+
+size_t bc2n_structure_heads_save_bytes(const char* weights_dir, int N, int64_t depth) {
+  size_t n = 0;
+  if (guarded([&] {
+        need(weights_dir != nullptr, "weights_dir required");
+        need(N > 0 && N <= 512 && depth > 0, "structure heads: bad shape");
+        (void)sh_w(weights_dir);
+        n = structheads_save_bytes(N, (int)depth) + 256;
+      }) != 0)
+    return 0;
+  return n;
+}
+
+int bc2n_structure_heads_fwd(void* stream, const float* single, const float* pair,
+                             const float* seq_mask, const float* aatype, const uint32_t* seed,
+                             int seed_len, int N, int64_t depth, int64_t dropout,
+                             const char* weights_dir, float* atom14, float* distogram, float* pae,
+                             float* plddt, float* expres, void* save) {
+  return guarded([&] {
+    hipStream_t st = as_stream(stream);
+    need(weights_dir && single && pair && seq_mask && aatype && save, "null operand");
+    need(atom14 && distogram && pae && plddt && expres, "null output");
+    need(N > 0 && N <= 512 && depth > 0, "structure heads: bad shape");
+    need(seed_len == 2 || seed_len == 3, "structure heads: seed must be u32[2] or u32[3]");
+    need(!dropout || seed, "structure heads: dropout needs the seed operand");
+    const StructHeadsW& w = sh_w(weights_dir);
+    const size_t bytes = structheads_save_bytes(N, (int)depth) + 256;
+    uint32_t* keyslot = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(save) + bytes - 256);
+    const uint32_t* key = dropout ? stack_key(st, seed, seed_len, keyslot) : nullptr;
+    const uint32_t* enabled = dropout ? seed + (seed_len - 1) : nullptr;
+    structheads_fwd(st, w, N, (int)depth, single, pair, seq_mask, aatype, key, enabled,
+                    dropout != 0, atom14, distogram, pae, plddt, expres, save);
+  });
+}
+
+int bc2n_structure_heads_bwd(void* stream, const float* single, const float* pair,
+                             const float* seq_mask, const float* aatype, const float* d_atom14,
+                             const float* d_distogram, const float* d_pae, const float* d_plddt,
+                             const float* d_expres, void* save, int N, int64_t depth,
+                             int64_t dropout, const char* weights_dir, float* dsingle,
+                             float* dpair) {
+  return guarded([&] {
+    need(weights_dir && single && pair && seq_mask && aatype && save && dsingle && dpair,
+         "null operand");
+    need(N > 0 && N <= 512 && depth > 0, "structure heads: bad shape");
+    const StructHeadsW& w = sh_w(weights_dir);
+    structheads_bwd(as_stream(stream), w, N, (int)depth, single, pair, seq_mask, aatype,
+                    dropout != 0, save, d_atom14, d_distogram, d_pae, d_plddt, d_expres, dsingle,
+                    dpair);
   });
 }
 

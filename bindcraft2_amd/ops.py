@@ -421,6 +421,46 @@ class Fold:
         return dsingle, dpair
 
 
+class StructureHeads:
+    """The drop-in for StructureHeadsFwd/Bwd (native/ffi.cu:1009-1044): fold
+    iterations, the last iteration's sidechain (atom14) and the distogram,
+    PAE, pLDDT and experimentally-resolved heads, f32."""
+
+    def __init__(self, weights_dir, depth=8):
+        self.dir, self.depth = weights_dir.encode(), depth
+
+    def save_bytes(self, n):
+        b = lib().bc2n_structure_heads_save_bytes(self.dir, n, self.depth)
+        if b == 0:
+            check(1)
+        return b
+
+    def forward(self, single, pair, seq_mask, aatype, seed=None, dropout=True, save=None):
+        """-> ((atom14 [N,14,3], distogram [N,N,64], pae [N,N,64], plddt [N,50],
+        expres [N,37]), save)"""
+        n, dev = single.shape[0], single.device
+        outs = tuple(torch.empty(*sh, dtype=torch.float32, device=dev)
+                     for sh in ((n, 14, 3), (n, n, 64), (n, n, 64), (n, 50), (n, 37)))
+        if save is None:
+            save = torch.empty(self.save_bytes(n), dtype=torch.uint8, device=dev)
+        seed_len = 3 if seed is None else seed.numel()
+        check(lib().bc2n_structure_heads_fwd(_stream(), _ptr(single), _ptr(pair), _ptr(seq_mask),
+                                             _ptr(aatype), _ptr(seed), seed_len, n, self.depth,
+                                             int(dropout), self.dir, *map(_ptr, outs), _ptr(save)))
+        return outs, save
+
+    def backward(self, cts, single, pair, seq_mask, aatype, save, dropout=True):
+        """cts = (d_atom14, d_distogram, d_pae, d_plddt, d_expres), each may
+        be None -> (dsingle, dpair)"""
+        n = single.shape[0]
+        dsingle, dpair = torch.empty_like(single), torch.empty_like(pair)
+        check(lib().bc2n_structure_heads_bwd(_stream(), _ptr(single), _ptr(pair), _ptr(seq_mask),
+                                             _ptr(aatype), *map(_ptr, cts), _ptr(save), n,
+                                             self.depth, int(dropout), self.dir, _ptr(dsingle),
+                                             _ptr(dpair)))
+        return dsingle, dpair
+
+
 def dropout_table(rows, channels, key, rate, device="cuda"):
     """[rows, channels] keep/keep_rate table from a JAX key (k0, k1)."""
     tbl = torch.empty(rows, channels, dtype=torch.float32, device=device)

@@ -266,6 +266,91 @@ def init_fold_params(rng, final="random", ln="identity"):
     return out
 
 
+def sidechain_shapes(c_s=C_S, c=128):
+    """MultiRigidSidechain of the fold iteration (folding_multimer.py:950-1040,
+    config.py sidechain: num_channel 128, 2 residual blocks), under
+    fold_iteration/rigid_sidechain/."""
+    sh = {"input_projection/weights": (c_s, c), "input_projection/bias": (c,),
+          "input_projection_1/weights": (c_s, c), "input_projection_1/bias": (c,),
+          "unnormalized_angles/weights": (c, 14), "unnormalized_angles/bias": (14,)}
+    for sfx in ("", "_1"):
+        for r in ("resblock1", "resblock2"):
+            sh[f"{r}{sfx}/weights"] = (c, c)
+            sh[f"{r}{sfx}/bias"] = (c,)
+    return {f"fold_iteration/rigid_sidechain/{k}": v for k, v in sh.items()}
+
+
+def heads_shapes(c_s=C_S, c_z=C_Z):
+    """The four heads (modules.py:777-1120; config.py heads: 64 distogram
+    bins, 64 aligned-error bins, pLDDT 128 channels x 50 bins, 37
+    experimentally-resolved logits)."""
+    return {"distogram_head/half_logits/weights": (c_z, 64),
+            "distogram_head/half_logits/bias": (64,),
+            "predicted_aligned_error_head/logits/weights": (c_z, 64),
+            "predicted_aligned_error_head/logits/bias": (64,),
+            "predicted_lddt_head/input_layer_norm/scale": (c_s,),
+            "predicted_lddt_head/input_layer_norm/offset": (c_s,),
+            "predicted_lddt_head/act_0/weights": (c_s, 128),
+            "predicted_lddt_head/act_0/bias": (128,),
+            "predicted_lddt_head/act_1/weights": (128, 128),
+            "predicted_lddt_head/act_1/bias": (128,),
+            "predicted_lddt_head/logits/weights": (128, 50),
+            "predicted_lddt_head/logits/bias": (50,),
+            "experimentally_resolved_head/logits/weights": (c_s, 37),
+            "experimentally_resolved_head/logits/bias": (37,)}
+
+
+def init_structure_heads_params(rng, final="random", ln="identity"):
+    """The post-trunk weights directory: fold iterations, sidechain, heads
+    (LeCun-normal weights, small random biases unless final == 'zero')."""
+    out = init_fold_params(rng, final=final, ln=ln)
+    for name, shape in {**sidechain_shapes(), **heads_shapes()}.items():
+        leaf = name.split("/")[-1]
+        if leaf == "scale":
+            v = np.ones(shape) if ln == "identity" else 1.0 + 0.1 * rng.standard_normal(shape)
+        elif leaf == "offset":
+            v = np.zeros(shape) if ln == "identity" else 0.1 * rng.standard_normal(shape)
+        elif leaf == "bias":
+            v = np.zeros(shape) if final == "zero" else 0.1 * rng.standard_normal(shape)
+        else:
+            v = rng.standard_normal(shape) / np.sqrt(shape[0])
+        out[f"param/{name}"] = np.asarray(v, np.float32)
+    return out
+
+
+def init_residue_tables(rng):
+    """Random residue tables of the shapes the structure module reads
+    (const/default_frame [21,8,4,4] rigid 4x4 frames, const/atom14_to_group
+    [21,14], const/atom14_lit_pos [21,14,3], const/atom14_mask [21,14]).  The
+    sidechain is table-driven, so random tables exercise every path; the real
+    ones come from the model's residue_constants."""
+    q = rng.standard_normal((21, 8, 4))
+    q /= np.linalg.norm(q, axis=-1, keepdims=True)
+    w, x, y, z = q[..., 0], q[..., 1], q[..., 2], q[..., 3]
+    R = np.stack([1 - 2 * (y * y + z * z), 2 * (x * y - w * z), 2 * (x * z + w * y),
+                  2 * (x * y + w * z), 1 - 2 * (x * x + z * z), 2 * (y * z - w * x),
+                  2 * (x * z - w * y), 2 * (y * z + w * x), 1 - 2 * (x * x + y * y)],
+                 -1).reshape(21, 8, 3, 3)
+    fr = np.zeros((21, 8, 4, 4))
+    fr[..., :3, :3] = R
+    fr[..., :3, 3] = 1.5 * rng.standard_normal((21, 8, 3))
+    fr[..., 3, 3] = 1.0
+    fr[:, 0] = np.eye(4)  # the backbone group is the backbone frame
+    return {"default_frame": fr.astype(np.float32),
+            "atom14_to_group": rng.integers(0, 8, (21, 14)).astype(np.float32),
+            "atom14_lit_pos": (1.5 * rng.standard_normal((21, 14, 3))).astype(np.float32),
+            "atom14_mask": (rng.random((21, 14)) < 0.8).astype(np.float32)}
+
+
+def residue_tables_from(rc):
+    """The four tables from a residue_constants module (alphafold.common),
+    in the layout the weights directory stores (const/...)."""
+    return {"default_frame": np.asarray(rc.restype_rigid_group_default_frame, np.float32),
+            "atom14_to_group": np.asarray(rc.restype_atom14_to_rigid_group, np.float32),
+            "atom14_lit_pos": np.asarray(rc.restype_atom14_rigid_group_positions, np.float32),
+            "atom14_mask": np.asarray(rc.restype_atom14_mask, np.float32)}
+
+
 def write_manifest(out_dir, params):
     """Write {name: array} as a weights directory (manifest.txt + .f32)."""
     os.makedirs(out_dir, exist_ok=True)

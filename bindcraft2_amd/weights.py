@@ -262,8 +262,16 @@ def post_flat(tree):
     return flat
 
 
-def post_weights_from_params(tree, out_dir=None):
-    return write_dir(post_flat(tree), out_dir, "bc2n_post")
+def post_weights_from_params(tree, out_dir=None, tables=None):
+    """The post-trunk directory; `tables` (params.residue_tables_from(the
+    model's residue_constants), or any dict of the four arrays) adds the
+    residue tables the sidechain reads (const/default_frame,
+    const/atom14_to_group, const/atom14_lit_pos, const/atom14_mask)."""
+    flat = post_flat(tree)
+    if tables is not None:
+        for k in ("default_frame", "atom14_to_group", "atom14_lit_pos", "atom14_mask"):
+            flat[f"const/{k}"] = np.asarray(tables[k], np.float32)
+    return write_dir(flat, out_dir, "bc2n_post")
 
 
 # ------------------------------------------------------------- random trees

@@ -292,6 +292,44 @@ int bc2n_fold_bwd(void* stream, const float* d_act, const float* d_traj,
                   const char* weights_dir, float* dsingle, float* dpair);
 
 /* ------------------------------------------------------------------------
+ * Structure module and heads (the reference's StructureHeadsFwd /
+ * StructureHeadsBwd custom calls, native/ffi.cu:1009-1044 (handlers
+ * SmFwdImpl / SmBwdImpl :530-639) over native/structmod.cuh,
+ * sidechain.cuh, atom14.cuh, heads.cuh; runner bindcraft/af/native.py
+ * _make_post_runner).  Replaces:
+ *   fwd(single f32[N,384], pair f32[N,N,128], seq_mask f32[N], aatype f32[N],
+ *       seed; depth, weights_dir)
+ *       -> (atom14 f32[N,14,3], distogram f32[N,N,64], pae f32[N,N,64],
+ *           plddt f32[N,50], expres f32[N,37])
+ *   bwd(single, pair, seq_mask, aatype, d_atom14, d_distogram, d_pae,
+ *       d_plddt, d_expres, seed; ...) -> (dsingle, dpair)
+ * = the fold iterations (as bc2n_fold_*), the last iteration's sidechain
+ * (folding_multimer.py:950-1040: torsions, rigid-group frames, atom14
+ * positions from the residue tables const/default_frame, atom14_to_group,
+ * atom14_lit_pos, atom14_mask of the weights directory) and the distogram
+ * (symmetrised), predicted-aligned-error, pLDDT and experimentally-resolved
+ * heads (modules.py:777-1120).  All f32.  aatype holds residue types 0..20
+ * (clamped).  save holds bc2n_structure_heads_save_bytes() bytes; unlike the
+ * reference's, the backward replays nothing, and it uses the save buffer's
+ * tail as scratch (so save is writable in both calls).  Cotangents may be
+ * NULL (zero).  seed as for the stacks.  N <= 512.
+ * ---------------------------------------------------------------------- */
+size_t bc2n_structure_heads_save_bytes(const char* weights_dir, int N, int64_t depth);
+int bc2n_structure_heads_fwd(void* stream, const float* single, const float* pair,
+                             const float* seq_mask, const float* aatype,
+                             const uint32_t* seed, int seed_len, int N, int64_t depth,
+                             int64_t dropout, const char* weights_dir, float* atom14,
+                             float* distogram, float* pae, float* plddt, float* expres,
+                             void* save);
+int bc2n_structure_heads_bwd(void* stream, const float* single, const float* pair,
+                             const float* seq_mask, const float* aatype,
+                             const float* d_atom14, const float* d_distogram,
+                             const float* d_pae, const float* d_plddt,
+                             const float* d_expres, void* save, int N, int64_t depth,
+                             int64_t dropout, const char* weights_dir, float* dsingle,
+                             float* dpair);
+
+/* ------------------------------------------------------------------------
  * Dropout with JAX's own bits.  tbl[b*C+c] = keep/keep_rate where
  * keep = jax.random.bernoulli(key, keep_rate, (B, C)), keep_rate =
  * float32(1) - float32(rate); key = (k0, k1) = jax.random.key_data(key).

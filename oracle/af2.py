@@ -506,3 +506,108 @@ def fold(single, pair, mask, params, depth, key, use_dropout, dtype=torch.float6
         act, R, t = fold_iteration(act, R, t, act_2d, mask, fp, keys[i], use_dropout)
         traj.append(torch.cat([R, (POSITION_SCALE * t)[..., None]], -1))
     return act, torch.stack(traj)
+
+
+# ------------------------------------------------ sidechain, atom14 and heads
+# folding_multimer.py:950-1040 (MultiRigidSidechain), all_atom_multimer.py:
+# 370-468 (torsion_angles_to_frames, frames_and_literature_positions_to_
+# atom14_pos), modules.py:777-1120 (the four heads).  The residue tables are
+# inputs (`tables`: default_frame [21,8,4,4], atom14_to_group [21,14],
+# atom14_lit_pos [21,14,3], atom14_mask [21,14]), as the reference's native
+# structure module reads them from its weights directory (const/...).
+
+def _compose(Ra, ta, Rb, tb):
+    """Rigid composition (Ra, ta) @ (Rb, tb) = (Ra Rb, Ra tb + ta)."""
+    return Ra @ Rb, (Ra @ tb[..., None])[..., 0] + ta
+
+
+def torsion_angles_to_frames(aatype, R, t, sin_cos, tables):
+    """all_atom_multimer.py:370-435: default frames of the residue type
+    composed with a rotation about x by each torsion (backbone group: none),
+    chi2..chi4 chained onto the previous chi frame, all mapped by the backbone
+    frame (R, t).  Returns the 8 global frames (R [N,8,3,3], t [N,8,3])."""
+    dt_ = sin_cos.dtype
+    m = torch.as_tensor(np.asarray(tables["default_frame"]), dtype=dt_)[aatype]
+    dR, dtr = m[..., :3, :3], m[..., :3, 3]
+    n = aatype.shape[0]
+    s = torch.cat([torch.zeros(n, 1, dtype=dt_), sin_cos[..., 0]], -1)
+    c = torch.cat([torch.ones(n, 1, dtype=dt_), sin_cos[..., 1]], -1)
+    z, o = torch.zeros_like(s), torch.ones_like(s)
+    rot = torch.stack([o, z, z, z, c, -s, z, s, c], -1).reshape(n, 8, 3, 3)
+    fR, ft = dR @ rot, dtr
+    cR, ct = [fR[:, g] for g in range(8)], [ft[:, g] for g in range(8)]
+    for g in (5, 6, 7):  # chi2..chi4 frames map to the previous chi frame
+        cR[g], ct[g] = _compose(cR[g - 1], ct[g - 1], fR[:, g], ft[:, g])
+    BR, Bt = torch.stack(cR, 1), torch.stack(ct, 1)
+    return _compose(R[:, None], t[:, None], BR, Bt)
+
+
+def frames_to_atom14(aatype, GR, Gt, tables):
+    """all_atom_multimer.py:438-468: each atom's literature position mapped by
+    its rigid group's global frame, masked to the atoms the type has."""
+    dt_ = GR.dtype
+    grp = torch.as_tensor(np.asarray(tables["atom14_to_group"])).long()[aatype]
+    oh = torch.nn.functional.one_hot(grp, 8).to(dt_)
+    Ra = torch.einsum("nag,ngij->naij", oh, GR)
+    ta = torch.einsum("nag,ngi->nai", oh, Gt)
+    lit = torch.as_tensor(np.asarray(tables["atom14_lit_pos"]), dtype=dt_)[aatype]
+    mask = torch.as_tensor(np.asarray(tables["atom14_mask"]), dtype=dt_)[aatype]
+    return ((Ra @ lit[..., None])[..., 0] + ta) * mask[..., None]
+
+
+def multi_rigid_sidechain(R, t, act, initial_act, aatype, p, tables):
+    """folding_multimer.py:950-1040 (num_channel 128, 2 residual blocks):
+    input projections of relu(act) and relu(initial_act) (haiku names
+    input_projection, input_projection_1), residual blocks (resblock1/2,
+    then resblock1_1/2_1), 7 torsions as l2-normalised (sin, cos) pairs
+    (eps 1e-12, :927-932), frames, atom14 positions.  (R, t) is the
+    backbone frame with its translation in angstroms."""
+    relu = torch.relu
+    a = linear(relu(act), p.sub("input_projection/")) + \
+        linear(relu(initial_act), p.sub("input_projection_1/"))
+    for b in range(2):
+        sfx = "" if b == 0 else "_1"
+        old = a
+        a = linear(relu(a), p.sub(f"resblock1{sfx}/"))
+        a = linear(relu(a), p.sub(f"resblock2{sfx}/"))
+        a = a + old
+    un = linear(relu(a), p.sub("unnormalized_angles/")).reshape(-1, 7, 2)
+    ang = un / torch.sqrt(torch.clamp((un * un).sum(-1, keepdim=True), min=1e-12))
+    GR, Gt = torsion_angles_to_frames(aatype, R, t, ang, tables)
+    return frames_to_atom14(aatype, GR, Gt, tables)
+
+
+def heads(pair, act, single, params, dtype=torch.float64):
+    """modules.py:1091-1120 (distogram: half_logits + its transpose over the
+    residue axes), :835-873 (predicted aligned error, not symmetrised),
+    :777-833 (pLDDT on the structure module's act: LayerNorm, act_0 relu,
+    act_1 relu, logits), :875-900 (experimentally resolved on the trunk
+    single, 37 logits)."""
+    P = Params(params, "param/", dtype)
+    h = linear(pair, P.sub("distogram_head/half_logits/"))
+    dgram = h + h.transpose(0, 1)
+    pae = linear(pair, P.sub("predicted_aligned_error_head/logits/"))
+    L = P.sub("predicted_lddt_head/")
+    x = layer_norm(act, L("input_layer_norm/scale"), L("input_layer_norm/offset"))
+    x = torch.relu(linear(x, L.sub("act_0/")))
+    x = torch.relu(linear(x, L.sub("act_1/")))
+    plddt = linear(x, L.sub("logits/"))
+    expres = linear(single, P.sub("experimentally_resolved_head/logits/"))
+    return dgram, pae, plddt, expres
+
+
+def structure_heads(single, pair, mask, aatype, params, depth, key, use_dropout, tables,
+                    dtype=torch.float64):
+    """The post-trunk step of the reference's StructureHeadsFwd
+    (native/ffi.cu:530-575): the fold iterations (folding_multimer.py:
+    476-548), the last iteration's sidechain on [act, initial_act] with the
+    backbone frame scaled to angstroms (:465-466; final_atom14_positions,
+    :604-606), and the heads.  Returns (atom14 [N,14,3], distogram [N,N,64],
+    pae [N,N,64], plddt [N,50], experimentally resolved [N,37])."""
+    act, traj = fold(single, pair, mask, params, depth, key, use_dropout, dtype)
+    P = Params(params, "param/", dtype)
+    init = layer_norm(single, P("single_layer_norm/scale"), P("single_layer_norm/offset"))
+    aat = torch.as_tensor(aatype).long().clamp(0, 20)
+    atom14 = multi_rigid_sidechain(traj[-1][..., :3], traj[-1][..., 3], act, init, aat,
+                                   P.sub("fold_iteration/rigid_sidechain/"), tables)
+    return (atom14,) + heads(pair, act, single, params, dtype)

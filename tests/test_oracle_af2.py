@@ -362,3 +362,119 @@ def test_embedder_structure_and_feature_mask():
         e = np.zeros_like(mf); e[t, i, k] = h
         fd = (f(tf, mf + e) - f(tf, mf - e)) / (2 * h)
         assert abs(fd - gmf[t, i, k].item()) <= 1e-5 * max(1.0, abs(fd))
+
+
+def _h4(R, t):
+    m = np.eye(4)
+    m[:3, :3], m[:3, 3] = R, t
+    return m
+
+
+def _xrot4(s, c):
+    m = np.eye(4)
+    m[1, 1], m[1, 2], m[2, 1], m[2, 2] = c, -s, s, c
+    return m
+
+
+def test_torsion_frames_and_atom14_against_homogeneous_products():
+    """The 8 global frames equal products of 4x4 homogeneous matrices
+    T_bb D_g X_g (chi2..4 chained: T_bb D4 X4 D5 X5 ...), and every atom is
+    its group's frame applied to its literature position, masked."""
+    rng = np.random.default_rng(31)
+    tables = bparams.init_residue_tables(rng)
+    n = 5
+    aat = torch.as_tensor(rng.integers(0, 21, n))
+    q, _ = np.linalg.qr(rng.standard_normal((n, 3, 3)))
+    R = torch.as_tensor(q * np.sign(np.linalg.det(q))[:, None, None])
+    t = torch.as_tensor(rng.standard_normal((n, 3)))
+    ang = rng.standard_normal((n, 7, 2))
+    ang /= np.linalg.norm(ang, axis=-1, keepdims=True)
+    GR, Gt = af2.torsion_angles_to_frames(aat, R, t, torch.as_tensor(ang), tables)
+    pos = af2.frames_to_atom14(aat, GR, Gt, tables).numpy()
+    for i in range(n):
+        a = int(aat[i])
+        D = tables["default_frame"][a].astype(np.float64)
+        X = [np.eye(4)] + [_xrot4(ang[i, g, 0], ang[i, g, 1]) for g in range(7)]
+        T = _h4(R[i].numpy(), t[i].numpy())
+        want = [T @ D[g] @ X[g] for g in range(5)]
+        chain = D[4] @ X[4]
+        for g in (5, 6, 7):
+            chain = chain @ D[g] @ X[g]
+            want.append(T @ chain)
+        for g in range(8):
+            np.testing.assert_allclose(GR[i, g].numpy(), want[g][:3, :3], atol=1e-12)
+            np.testing.assert_allclose(Gt[i, g].numpy(), want[g][:3, 3], atol=1e-12)
+        for k in range(14):
+            g = int(tables["atom14_to_group"][a, k])
+            lit = np.append(tables["atom14_lit_pos"][a, k].astype(np.float64), 1.0)
+            p = (want[g] @ lit)[:3] * tables["atom14_mask"][a, k]
+            np.testing.assert_allclose(pos[i, k], p, atol=1e-12)
+
+
+def test_sidechain_rigid_equivariance_and_angle_scale():
+    """A global rigid motion of the backbone frames moves every atom with it
+    (a transposed rotation anywhere breaks this), and scaling the
+    unnormalised angles changes nothing (they are l2-normalised)."""
+    rng = np.random.default_rng(32)
+    tables = bparams.init_residue_tables(rng)
+    prm = bparams.init_structure_heads_params(rng)
+    n = 6
+    aat = torch.as_tensor(rng.integers(0, 21, n))
+    q, _ = np.linalg.qr(rng.standard_normal((n, 3, 3)))
+    R = torch.as_tensor(q * np.sign(np.linalg.det(q))[:, None, None])
+    t = torch.as_tensor(rng.standard_normal((n, 3)))
+    act = torch.as_tensor(rng.standard_normal((n, 384)))
+    init = torch.as_tensor(rng.standard_normal((n, 384)))
+    p = af2.Params(prm, "param/fold_iteration/rigid_sidechain/")
+    pos = af2.multi_rigid_sidechain(R, t, act, init, aat, p, tables)
+    Q, _ = np.linalg.qr(rng.standard_normal((3, 3)))
+    Q = torch.as_tensor(Q * np.sign(np.linalg.det(Q)))
+    u = torch.as_tensor(rng.standard_normal(3))
+    pos2 = af2.multi_rigid_sidechain(Q @ R, (Q @ t[..., None])[..., 0] + u, act, init, aat, p, tables)
+    mask = torch.as_tensor(tables["atom14_mask"], dtype=torch.float64)[aat][..., None]
+    moved = ((Q @ pos[..., None])[..., 0] + u) * mask
+    assert torch.allclose(pos2, moved, atol=1e-10)
+    prm3 = dict(prm)
+    for k in ("weights", "bias"):
+        nm = f"param/fold_iteration/rigid_sidechain/unnormalized_angles/{k}"
+        prm3[nm] = 3.0 * prm[nm]
+    pos3 = af2.multi_rigid_sidechain(R, t, act, init, aat,
+                                     af2.Params(prm3, "param/fold_iteration/rigid_sidechain/"), tables)
+    assert torch.allclose(pos3, pos, atol=1e-10)
+
+
+def test_structure_heads_symmetry_and_finite_differences():
+    rng = np.random.default_rng(33)
+    tables = bparams.init_residue_tables(rng)
+    prm = bparams.init_structure_heads_params(rng, ln="random")
+    n, depth = 5, 2
+    single = rng.standard_normal((n, 384))
+    pair = rng.standard_normal((n, n, 128))
+    mask = np.ones(n)
+    aat = rng.integers(0, 21, n).astype(np.float32)
+    outs = af2.structure_heads(torch.as_tensor(single), torch.as_tensor(pair), torch.as_tensor(mask),
+                               aat, prm, depth, None, False, tables)
+    dgram, pae = outs[1], outs[2]
+    assert torch.allclose(dgram, dgram.transpose(0, 1))
+    assert not torch.allclose(pae, pae.transpose(0, 1))
+    cts = [rng.standard_normal(tuple(o.shape)) for o in outs]
+
+    def f(s_, z_):
+        o = af2.structure_heads(torch.as_tensor(s_), torch.as_tensor(z_), torch.as_tensor(mask), aat,
+                                prm, depth, None, False, tables)
+        return sum(float((a * torch.as_tensor(c)).sum()) for a, c in zip(o, cts))
+
+    s_t = torch.tensor(single, requires_grad=True)
+    z_t = torch.tensor(pair, requires_grad=True)
+    o = af2.structure_heads(s_t, z_t, torch.as_tensor(mask), aat, prm, depth, None, False, tables)
+    loss = sum((a * torch.as_tensor(c)).sum() for a, c in zip(o, cts))
+    gs, gz = torch.autograd.grad(loss, (s_t, z_t))
+    h = 1e-6
+    for (i, k) in [(0, 0), (3, 200)]:
+        e = np.zeros_like(single); e[i, k] = h
+        fd = (f(single + e, pair) - f(single - e, pair)) / (2 * h)
+        assert abs(fd - gs[i, k].item()) <= 1e-5 * max(1.0, abs(fd))
+    for (i, j, k) in [(0, 1, 5), (4, 2, 127)]:
+        e = np.zeros_like(pair); e[i, j, k] = h
+        fd = (f(single, pair + e) - f(single, pair - e)) / (2 * h)
+        assert abs(fd - gz[i, j, k].item()) <= 1e-5 * max(1.0, abs(fd))
