@@ -295,7 +295,8 @@ def init_af2_params(rng, num_blocks=48, extra_blocks=4, template_blocks=2, gates
     """A random haiku tree of the AF2 multimer architecture (config.py:386-600)
     for every part the library runs: the main stack, the extra-MSA stack
     (c_e = 64, global column attention), the template embedding with its
-    stack, the embedder and the structure module.  Weights are LeCun normal;
+    stack, the embedder, the structure module with its sidechain, and the
+    four heads.  Weights are LeCun normal;
     gates/ln as for params.init_module."""
     tree = {}
 
@@ -341,8 +342,9 @@ def init_af2_params(rng, num_blocks=48, extra_blocks=4, template_blocks=2, gates
         path, _, leaf = name[len("param/"):].rpartition("/")
         tree.setdefault(f"{EVO}/{path}", {})[leaf] = arr
 
-    for name, arr in P.init_fold_params(rng, final="zero" if gates == "zero" else "random",
-                                        ln=ln).items():
+    for name, arr in P.init_structure_heads_params(
+            rng, final="zero" if gates == "zero" else "random", ln=ln).items():
         path, _, leaf = name[len("param/"):].rpartition("/")
-        tree.setdefault(f"{STRUCTURE}/{path}", {})[leaf] = arr
+        root = IT if path.split("/")[0] in HEADS else STRUCTURE
+        tree.setdefault(f"{root}/{path}", {})[leaf] = arr
     return tree

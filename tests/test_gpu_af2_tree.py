@@ -71,7 +71,8 @@ def test_tree_embedder_and_fold(cuda, tree, tmp_path):
     print("embedder msa", assert_act(msa.cpu().double(), rmsa, 1e-5, "msa"))
     print("embedder pair", assert_act(pair.cpu().double(), rpair, 1e-5, "pair"))
 
-    post = W.post_weights_from_params(tree, str(tmp_path / "post"))
+    tables = P.init_residue_tables(rng)
+    post = W.post_weights_from_params(tree, str(tmp_path / "post"), tables=tables)
     prm = P.read_manifest(post)
     single = rng.standard_normal((n, 384)).astype(np.float32)
     z = rng.standard_normal((n, n, 128)).astype(np.float32)
@@ -82,3 +83,11 @@ def test_tree_embedder_and_fold(cuda, tree, tmp_path):
                            torch.as_tensor(mask, dtype=D), prm, 2, None, False)
     print("fold act", assert_act(act.cpu().double(), ract, 1e-3, "act"))
     print("fold traj", assert_act(traj.cpu().double(), rtraj, 1e-3, "traj"))
+    aat = rng.integers(0, 21, n).astype(np.float32)
+    outs, _ = ops.StructureHeads(post, 2).forward(T(single), T(z), T(mask), T(aat), None,
+                                                  dropout=False)
+    torch.cuda.synchronize()
+    ref = af2.structure_heads(torch.as_tensor(single, dtype=D), torch.as_tensor(z, dtype=D),
+                              torch.as_tensor(mask, dtype=D), aat, prm, 2, None, False, tables)
+    for name, o, r in zip(("atom14", "distogram", "pae", "plddt", "expres"), outs, ref):
+        print("structure heads", name, assert_act(o.cpu().double(), r, 1e-3, name))

@@ -60,7 +60,8 @@ def test_template_embedding_embedder_post(tree):
     em = W.embed_flat(tree)
     assert _names_shapes(em) == {f"param/{k}": v for k, v in P.embedder_shapes().items()}
     po = W.post_flat(tree)
-    assert _names_shapes(po) == {f"param/{k}": v for k, v in P.fold_shapes().items()}
+    want = {**P.fold_shapes(), **P.sidechain_shapes(), **P.heads_shapes()}
+    assert _names_shapes(po) == {f"param/{k}": v for k, v in want.items()}
 
 
 def test_post_zero_scalar_biases(tree):
