@@ -344,7 +344,10 @@ void gemm(hipStream_t st, const GemmArgs& g, const Epi& epi, const char* name = 
   gemm_check(g.batch == 1 || (g.a_sb % 8 == 0 && g.b_sb % 8 == 0), "batch strides");
   const int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
   dim3 grid(xcd_grid((long)tiles * g.batch)), block(256);
-  const bool k64 = (g.K % 64 == 0);
+  // K <= 128 (two 64-deep steps at most): 32-deep steps halve the operand
+  // buffers (40 KB), so four workgroups share a CU and hide each other's
+  // load latency; longer K keeps 64-deep steps (fewer barriers)
+  const bool k64 = (g.K % 64 == 0) && g.K > 128;
   KTimed kt(name, st);
 #define BC2N_GEMM_LAUNCH(BKV, AKV, BKCV) \
   hipLaunchKernelGGL((gemm_kernel<BM, BN, BKV, AKV, BKCV, Epi, AL>), grid, block, 0, st, g, epi, al)
