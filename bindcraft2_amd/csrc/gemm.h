@@ -7,8 +7,10 @@
 // form on its way into LDS, so the MFMA fragments are always read the same
 // way.  A 256-thread workgroup (4 waves, 2x2) owns a BM x BN tile; each wave
 // owns (BM/2) x (BN/2) as a grid of 16x16 MFMA tiles fed by
-// v_mfma_f32_16x16x32_bf16.  K is walked in BK steps with two LDS buffers and
-// a register prefetch of the next step's tile.
+// v_mfma_f32_16x16x32_bf16.  K is walked in BK steps with a register prefetch
+// of the next step's tile: 32-deep steps (K <= 128) into a second LDS buffer,
+// 64-deep steps into the one buffer after a barrier, so that either way the
+// operand buffers take at most 40 KB and four workgroups share a CU.
 //
 // Epilogue: the f32 accumulator tile is staged through LDS (reusing the
 // operand buffers, half a tile per pass) and handed to the epilogue as
@@ -133,7 +135,10 @@ struct ALoadScaledRows {
 template <int BM, int BN, int BK>
 struct GemmSmem {
   static constexpr int LDK = BK + 8;
-  static constexpr int AB = 2 * (BM + BN) * LDK * 2;   // bytes of the operand buffers
+  // 64-deep steps (long K) keep one operand buffer and pay a second barrier
+  // per step, so four workgroups still fit a CU; 32-deep steps double-buffer
+  static constexpr int NBUF = BK == 64 ? 1 : 2;
+  static constexpr int AB = NBUF * (BM + BN) * LDK * 2;  // bytes of the operand buffers
   static constexpr int LDT = BN + 4;
   static constexpr int T = (BM / 2) * LDT * 4;          // bytes of one epilogue pass
   static constexpr int BYTES = AB > T ? AB : T;
@@ -150,7 +155,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi, AL al = 
   static_assert(A_CH >= 1 && B_CH >= 1, "tile too small for 256 threads");
   __shared__ __attribute__((aligned(16))) unsigned char smem[SM::BYTES];
   bf16* As = reinterpret_cast<bf16*>(smem);            // [2][BM * LDK]
-  bf16* Bs = As + 2 * BM * LDK;                        // [2][BN * LDK]
+  bf16* Bs = As + SM::NBUF * BM * LDK;                 // [NBUF][BN * LDK]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -240,7 +245,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi, AL al = 
   __syncthreads();
   const int fr = lane & 15, fk = (lane >> 4) * 8;
   for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
+    const int buf = SM::NBUF == 2 ? (kt & 1) : 0;
     const bf16* as = As + buf * BM * LDK;
     const bf16* bs = Bs + buf * BN * LDK;
     if (kt + 1 < nk) gload((kt + 1) * BK);
@@ -258,7 +263,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi, AL al = 
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = mfma16x16x32(af[i], bfr[j], acc[i][j]);
     }
-    if (kt + 1 < nk) sstore(buf ^ 1);
+    if constexpr (SM::NBUF == 2) {
+      if (kt + 1 < nk) sstore(buf ^ 1);
+    } else if (kt + 1 < nk) {
+      __syncthreads();  // every wave is done with the buffer
+      sstore(0);
+    }
     __syncthreads();
   }
 
