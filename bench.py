@@ -230,7 +230,8 @@ def traffic_of(kernel, n):
     nb = n // 32
     syms = {"attn_fwd": [f"attn_fwd_rows<32, {nb}>", f"attn_fwd<32, {nb}>"],
             "attn_bwd_dq": [f"attn_bwd_dq_rows<32, {nb}>", f"attn_bwd_dq<32, {nb}>"],
-            "attn_bwd_dkv": [f"attn_bwd_dkv<32, {nb}>"]}.get(kernel, [kernel])
+            "attn_bwd_dkv": [f"attn_bwd_dkv<32, {nb}>"],
+            "trimul.tail_bwd": ["trimul_tail", "_ZN4bc2n12_GLOBAL__N_118trimul_tail_kernelENS0_8TailArgsE"]}.get(kernel, [kernel])
     for sym in syms:
         k = summ["kernels"].get(sym)
         if k is not None:
@@ -240,6 +241,7 @@ def traffic_of(kernel, n):
     pat = {"trimul.proj_bwd": r"EpiTrimulProjBwd",
            "trimul.gemm_proj": r"EpiTrimulProj(?!Bwd)",
            "trimul.gemm_out": r"EpiTrimulOut",
+           "triattn.gemm_dx_ln": r"EpiLnBwd<4>|EpiLnBwdILi4E",
            "trimul.contract_fwd": rf"contract(_kernel)?(<{nb}, .*float>|ILi{nb}E.*fEE)",
            "trimul.contract_bwd": rf"contract(_kernel)?(<{nb}, .*bf16>|ILi{nb}E.*DF16bEE)"}.get(kernel)
     if pat is None:

@@ -13,9 +13,11 @@ void ln_fwd_f32(hipStream_t st, const float* x, long M, int C, int nt,
                 float* rstd, bool fast, int H, const float* wb, float* bias_out,
                 float bias_scale = 1.f);
 // dx[src(m)] (+)= LN-backward(dy[m] + sum_h dbias[h*M+m] * wb[c*H+h]).
+// acc: dx = res + LN'(...) with res = dres, or dx itself when dres is null.
 void ln_bwd_f32(hipStream_t st, const float* dy, const float* x, long M, int C,
                 int nt, const float* gamma, const float* mean, const float* rstd,
-                float* dx, bool acc, int H, const float* dbias, const float* wb);
+                float* dx, bool acc, int H, const float* dbias, const float* wb,
+                const float* dres = nullptr);
 // Channel-major ([C][M]) input forms used by the triangle multiplication.
 void ln_fwd_cm(hipStream_t st, const float* x, long M, int C, const float* gamma,
                const float* beta, bf16* y, float* mean, float* rstd, bool fast);

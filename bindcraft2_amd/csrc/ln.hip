@@ -127,17 +127,19 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(
   }
 }
 
-// dx[src(m)] (+)= LN'(dy[m] + sum_h dbias[h][m] W[c][h])   (dy may be null);
-// U rows per lane group, as the forward.
+// dx[src(m)] = (ACC ? res[src(m)] : 0) + LN'(dy[m] + sum_h dbias[h][m] W[c][h])
+// (dy may be null; res = dres, or dx itself when dres is null); U rows per
+// lane group, as the forward.
 template <int C, class InT, bool ACC, int H, int U>
 __global__ __launch_bounds__(256) void ln_bwd_kernel(
     const float* __restrict__ dy, const InT* __restrict__ x, long M, int nt,
     const float* __restrict__ gamma, const float* __restrict__ mean,
     const float* __restrict__ rstd, float* __restrict__ dx,
-    const float* __restrict__ dbias, const float* __restrict__ wb) {
+    const float* __restrict__ dbias, const float* __restrict__ wb, const float* dres) {
   using G = LnGeom<C>;
   const int t = threadIdx.x;
   const long mb = (long)blockIdx.x * (U * G::RPB) + t / G::TPR;
+  const float* res = dres ? dres : dx;  // the residual cotangent ACC adds
   const int c0 = (t % G::TPR) * 8;
   if (mb >= M) return;
   float xv[U][8], g[U][8], ov[U][8], mu[U], r[U];
@@ -154,7 +156,7 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(
 #pragma unroll
       for (int e = 0; e < 8; ++e) g[u][e] = 0.f;
     }
-    if (ACC) load8f<float>(dx + src * C + c0, ov[u]);
+    if (ACC) load8f<float>(res + src * C + c0, ov[u]);
     mu[u] = mean[m];
     r[u] = rstd[m];
     if constexpr (H > 0) {
@@ -375,36 +377,37 @@ void ln_fwd_f32(hipStream_t st, const float* x, long M, int C, int nt,
 template <int C, int H>
 static void ln_bwd_launch(hipStream_t st, const float* dy, const float* x, long M, int nt,
                           const float* gamma, const float* mean, const float* rstd, float* dx,
-                          bool acc, const float* dbias, const float* wb) {
+                          bool acc, const float* dbias, const float* wb, const float* dres) {
   constexpr int U = ln_rows<H>();
   const int grid = (int)((M + U * LnGeom<C>::RPB - 1) / (U * LnGeom<C>::RPB));
   if (acc)
     hipLaunchKernelGGL((ln_bwd_kernel<C, float, true, H, U>), dim3(grid), dim3(256), 0, st, dy, x,
-                       M, nt, gamma, mean, rstd, dx, dbias, wb);
+                       M, nt, gamma, mean, rstd, dx, dbias, wb, dres);
   else
     hipLaunchKernelGGL((ln_bwd_kernel<C, float, false, H, U>), dim3(grid), dim3(256), 0, st, dy, x,
-                       M, nt, gamma, mean, rstd, dx, dbias, wb);
+                       M, nt, gamma, mean, rstd, dx, dbias, wb, dres);
 }
 
 template <int C>
 static void ln_bwd_dispatch(hipStream_t st, const float* dy, const float* x, long M, int nt,
                             const float* gamma, const float* mean, const float* rstd, float* dx,
-                            bool acc, int H, const float* dbias, const float* wb) {
+                            bool acc, int H, const float* dbias, const float* wb, const float* dres) {
   switch (H) {
-    case 0: ln_bwd_launch<C, 0>(st, dy, x, M, nt, gamma, mean, rstd, dx, acc, dbias, wb); break;
-    case 4: ln_bwd_launch<C, 4>(st, dy, x, M, nt, gamma, mean, rstd, dx, acc, dbias, wb); break;
-    case 8: ln_bwd_launch<C, 8>(st, dy, x, M, nt, gamma, mean, rstd, dx, acc, dbias, wb); break;
+    case 0: ln_bwd_launch<C, 0>(st, dy, x, M, nt, gamma, mean, rstd, dx, acc, dbias, wb, dres); break;
+    case 4: ln_bwd_launch<C, 4>(st, dy, x, M, nt, gamma, mean, rstd, dx, acc, dbias, wb, dres); break;
+    case 8: ln_bwd_launch<C, 8>(st, dy, x, M, nt, gamma, mean, rstd, dx, acc, dbias, wb, dres); break;
     default: throw std::runtime_error("ln_bwd: bias heads must be 0, 4 or 8");
   }
 }
 
 void ln_bwd_f32(hipStream_t st, const float* dy, const float* x, long M, int C,
                 int nt, const float* gamma, const float* mean, const float* rstd,
-                float* dx, bool acc, int H, const float* dbias, const float* wb) {
+                float* dx, bool acc, int H, const float* dbias, const float* wb,
+                const float* dres) {
   switch (C) {
-    case 64: ln_bwd_dispatch<64>(st, dy, x, M, nt, gamma, mean, rstd, dx, acc, H, dbias, wb); break;
-    case 128: ln_bwd_dispatch<128>(st, dy, x, M, nt, gamma, mean, rstd, dx, acc, H, dbias, wb); break;
-    case 256: ln_bwd_dispatch<256>(st, dy, x, M, nt, gamma, mean, rstd, dx, acc, H, dbias, wb); break;
+    case 64: ln_bwd_dispatch<64>(st, dy, x, M, nt, gamma, mean, rstd, dx, acc, H, dbias, wb, dres); break;
+    case 128: ln_bwd_dispatch<128>(st, dy, x, M, nt, gamma, mean, rstd, dx, acc, H, dbias, wb, dres); break;
+    case 256: ln_bwd_dispatch<256>(st, dy, x, M, nt, gamma, mean, rstd, dx, acc, H, dbias, wb, dres); break;
     default: throw std::runtime_error("ln_bwd: unsupported channel count");
   }
 }

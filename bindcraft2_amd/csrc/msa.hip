@@ -390,11 +390,9 @@ void msarow_bwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa
   b.scale = 1.f / std::sqrt((float)a.D);
   attn_bwd(st, b);
   dx_gemm(st, a, R, b.dqkvg, dxn, "msarow.gemm_dx");
-  if (dmsa_in != dmsa_out)
-    BC2N_HIP(hipMemcpyAsync(dmsa_in, dmsa_out, (size_t)R * Cm * 4, hipMemcpyDeviceToDevice, st));
   KTimed kt("msarow.ln_bwd", st);
   ln_bwd_f32(st, dxn, msa_in, R, Cm, 0, a.ln_g, sv.mean, sv.rstd, dmsa_in, true, 0, nullptr,
-             nullptr);
+             nullptr, dmsa_out);
   // pair gradient: only through the bias projection
   ln_bwd_f32(st, nullptr, pair, M, w.Cz, 0, w.pn_g, sv.pmean, sv.prstd, dpair, true, H, b.dbias,
              w.w2d);
@@ -456,11 +454,9 @@ void msacol_bwd(hipStream_t st, const MsaColW& w, int S, int N, const float* msa
                        H, msa_mask, sv.o, dog, (long)HD, 1.f / std::sqrt((float)a.D), dqkvg);
   }
   dx_gemm(st, a, R, dqkvg, dxn, "msacol.gemm_dx");
-  if (dmsa_in != dmsa_out)
-    BC2N_HIP(hipMemcpyAsync(dmsa_in, dmsa_out, (size_t)R * Cm * 4, hipMemcpyDeviceToDevice, st));
   KTimed kt("msacol.ln_bwd", st);
   ln_bwd_f32(st, dxn, msa_in, R, Cm, 0, a.ln_g, sv.mean, sv.rstd, dmsa_in, true, 0, nullptr,
-             nullptr);
+             nullptr, dmsa_out);
 }
 
 }  // namespace bc2n

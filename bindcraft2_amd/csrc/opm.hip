@@ -314,10 +314,9 @@ void opm_bwd(hipStream_t st, const OpmW& w, int S, int N, const float* msa, cons
   g5.A = dlr; g5.a_sm = 2 * O; g5.a_sk = 1;
   g5.B = w.wlr; g5.b_sn = 2 * O; g5.b_sk = 1;
   gemm<128, 128>(st, g5, EpiStore<float>{dxn, Cm, 0, nullptr, Cm}, "opm.gemm_dx");
-  if (dmsa_in != dmsa_out)
-    BC2N_HIP(hipMemcpyAsync(dmsa_in, dmsa_out, (size_t)R * Cm * 4, hipMemcpyDeviceToDevice, st));
   KTimed kt("opm.ln_bwd", st);
-  ln_bwd_f32(st, dxn, msa, R, Cm, 0, w.ln_g, sv.mean, sv.rstd, dmsa_in, true, 0, nullptr, nullptr);
+  ln_bwd_f32(st, dxn, msa, R, Cm, 0, w.ln_g, sv.mean, sv.rstd, dmsa_in, true, 0, nullptr, nullptr,
+             dmsa_out);
 }
 
 }  // namespace bc2n

@@ -109,10 +109,9 @@ void transition_bwd(hipStream_t st, const TransW& w, long rows, int nt, const fl
     return;
   }
   gemm<128, 128>(st, g2, EpiStore<float>{dxn, C, 0, nullptr, C}, "trans.gemm_dx");
-  if (din != dout)
-    BC2N_HIP(hipMemcpyAsync(din, dout, (size_t)rows * C * 4, hipMemcpyDeviceToDevice, st));
   KTimed kt("trans.ln_bwd", st);
-  ln_bwd_f32(st, dxn, act_in, rows, C, 0, w.ln_g, sv.mean, sv.rstd, din, true, 0, nullptr, nullptr);
+  ln_bwd_f32(st, dxn, act_in, rows, C, 0, w.ln_g, sv.mean, sv.rstd, din, true, 0, nullptr, nullptr,
+             dout);
 }
 
 }  // namespace bc2n

@@ -208,11 +208,9 @@ void triattn_bwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
   }
   gemm<128, 128>(st, g2, EpiStore<float>{dxn, C, 0, nullptr, C}, "triattn.gemm_dx");
 
-  if (din != dout)
-    BC2N_HIP(hipMemcpyAsync(din, dout, (size_t)M * C * 4, hipMemcpyDeviceToDevice, st));
   KTimed kt("triattn.ln_bwd", st);
   ln_bwd_f32(st, dxn, pair_in, M, C, per_column ? N : 0, w.ln_g, sv.mean, sv.rstd, din, true,
-             H, b.dbias, w.w2d);
+             H, b.dbias, w.w2d, dout);
 }
 
 }  // namespace bc2n

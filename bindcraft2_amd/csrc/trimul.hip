@@ -668,10 +668,9 @@ void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
     return;
   }
   gemm<128, 128>(st, g2, EpiStore<float>{dxn, C, 0, nullptr, C}, "trimul.gemm_dx");
-  if (din != dout)
-    BC2N_HIP(hipMemcpyAsync(din, dout, (size_t)M * C * 4, hipMemcpyDeviceToDevice, st));
   KTimed kt("trimul.ln_bwd", st);
-  ln_bwd_f32(st, dxn, pair_in, M, C, 0, w.ln_g, sv.mean, sv.rstd, din, true, 0, nullptr, nullptr);
+  ln_bwd_f32(st, dxn, pair_in, M, C, 0, w.ln_g, sv.mean, sv.rstd, din, true, 0, nullptr, nullptr,
+             dout);
 }
 
 }  // namespace bc2n
