@@ -74,6 +74,12 @@ def _declare(L):
         "bc2n_fold_save_bytes": (sz, [cs, i, c.c_int64]),
         "bc2n_fold_fwd": (i, [vp, vp, vp, vp, vp, i, i, c.c_int64, c.c_int64, cs, vp, vp, vp]),
         "bc2n_fold_bwd": (i, [vp, vp, vp, vp, vp, vp, vp, i, c.c_int64, c.c_int64, cs, vp, vp]),
+        "bc2n_design_step_save_bytes": (sz, [cs, cs, cs, cs, cs, i, i, c.c_int64, c.c_int64,
+                                             c.c_int64, c.c_int64]),
+        "bc2n_design_step_fwd": (i, [vp] * 11 + [vp, i, i] + [c.c_int64] * 5 + [cs] * 5
+                                 + [vp] * 6),
+        "bc2n_design_step_bwd": (i, [vp, vp, vp, vp, c.c_int64] + [vp] * 6 + [i, i]
+                                 + [c.c_int64] * 5 + [cs] * 5 + [vp, vp]),
         "bc2n_structure_heads_save_bytes": (sz, [cs, i, c.c_int64]),
         "bc2n_structure_heads_fwd": (i, [vp, vp, vp, vp, vp, vp, i, i, c.c_int64, c.c_int64, cs,
                                          vp, vp, vp, vp, vp, vp]),
@@ -109,6 +115,8 @@ def exported_symbols():
     hdr = os.path.join(os.path.dirname(_HERE), "include", "bc2n.h")
     with open(hdr) as fh:
         txt = fh.read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)  # declarations only, not comments
+    txt = re.sub(r"//[^\n]*", "", txt)
     return sorted(set(re.findall(r"\b(bc2n_[a-z0-9_]+)\s*\(", txt)))
 
 

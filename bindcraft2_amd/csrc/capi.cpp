@@ -7,6 +7,7 @@
 #include "tplembed.h"
 #include "embed.h"
 #include "heads.h"
+#include "designstep.h"
 
 #include <map>
 #include <tuple>
@@ -609,6 +610,93 @@ int bc2n_structure_heads_bwd(void* stream, const float* single, const float* pai
     structheads_bwd(as_stream(stream), w, N, (int)depth, single, pair, seq_mask, aatype,
                     dropout != 0, save, d_atom14, d_distogram, d_pae, d_plddt, d_expres, dsingle,
                     dpair);
+  });
+}
+
+// ------------------------------------------------------- one-call design step
+
+namespace {
+std::map<std::string, DesignStepW> g_ds;
+const DesignStepW& ds_w(const char* emb, const char* tpl, const char* extra, const char* main,
+                        const char* post, int64_t dt, int64_t de, int64_t dm, int64_t df) {
+  need(emb && tpl && extra && main && post, "design step: five weights directories required");
+  const std::string key = std::string(emb) + "|" + tpl + "|" + extra + "|" + main + "|" + post +
+                          "|" + std::to_string(dt) + "," + std::to_string(de) + "," +
+                          std::to_string(dm) + "," + std::to_string(df);
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_ds.find(key);
+    if (it != g_ds.end()) return it->second;
+  }
+  DesignStepW w;
+  w.d_tpl = (int)dt; w.d_extra = (int)de; w.d_main = (int)dm; w.d_fold = (int)df;
+  w.emb = emb_w(emb);
+  WeightStore& ews = weights(emb);
+  w.wsa = ews.f32("param/single_activations/weights");
+  w.bsa = ews.f32("param/single_activations/bias");
+  if (ews.host("param/single_activations/weights").data.size() != 256u * 384u)
+    throw std::runtime_error("design step: single_activations must be [256,384]");
+  w.tpl = te_w(tpl, (int)dt);
+  w.extra = stack_w(extra, (int)de, StackKind::PAIR_ONLY);
+  w.main = stack_w(main, (int)dm, StackKind::EVO);
+  w.sh = sh_w(post);
+  std::lock_guard<std::mutex> lk(g_mu);
+  return g_ds.emplace(key, w).first->second;
+}
+}  // namespace
+
+size_t bc2n_design_step_save_bytes(const char* emb_dir, const char* tpl_dir,
+                                   const char* extra_dir, const char* main_dir,
+                                   const char* post_dir, int N, int S, int64_t d_tpl,
+                                   int64_t d_extra, int64_t d_main, int64_t d_fold) {
+  size_t n = 0;
+  if (guarded([&] {
+        const DesignStepW& w =
+            ds_w(emb_dir, tpl_dir, extra_dir, main_dir, post_dir, d_tpl, d_extra, d_main, d_fold);
+        need(N > 0 && S > 0, "design step: bad shape");
+        n = design_step_save_bytes(w, N, S);
+      }) != 0)
+    return 0;
+  return n;
+}
+
+int bc2n_design_step_fwd(void* stream, const float* target_feat, const float* msa_feat,
+                         const float* residue_index, const float* asym_id,
+                         const float* entity_id, const float* sym_id, const int32_t* offset,
+                         const float* seq_mask, const float* act_const, const float* aatype,
+                         const uint32_t* seeds, int N, int S, int64_t d_tpl, int64_t d_extra,
+                         int64_t d_main, int64_t d_fold, int64_t dropout, const char* emb_dir,
+                         const char* tpl_dir, const char* extra_dir, const char* main_dir,
+                         const char* post_dir, float* atom14, float* distogram, float* pae,
+                         float* plddt, float* expres, void* save) {
+  return guarded([&] {
+    need(target_feat && msa_feat && residue_index && asym_id && entity_id && sym_id && seq_mask &&
+             aatype && save, "null operand");
+    need(atom14 && distogram && pae && plddt && expres, "null output");
+    need(!dropout || seeds, "design step: dropout needs the seeds operand");
+    const DesignStepW& w =
+        ds_w(emb_dir, tpl_dir, extra_dir, main_dir, post_dir, d_tpl, d_extra, d_main, d_fold);
+    design_step_fwd(as_stream(stream), w, N, S, target_feat, msa_feat, residue_index, asym_id,
+                    entity_id, sym_id, offset, seq_mask, act_const, aatype, seeds, dropout != 0,
+                    atom14, distogram, pae, plddt, expres, save);
+  });
+}
+
+int bc2n_design_step_bwd(void* stream, const float* target_feat, const float* seq_mask,
+                         const float* aatype, int64_t with_template, const float* d_atom14,
+                         const float* d_distogram, const float* d_pae, const float* d_plddt,
+                         const float* d_expres, void* save, int N, int S, int64_t d_tpl,
+                         int64_t d_extra, int64_t d_main, int64_t d_fold, int64_t dropout,
+                         const char* emb_dir, const char* tpl_dir, const char* extra_dir,
+                         const char* main_dir, const char* post_dir, float* d_target_feat,
+                         float* d_msa_feat) {
+  return guarded([&] {
+    need(target_feat && seq_mask && aatype && save && d_target_feat && d_msa_feat, "null operand");
+    const DesignStepW& w =
+        ds_w(emb_dir, tpl_dir, extra_dir, main_dir, post_dir, d_tpl, d_extra, d_main, d_fold);
+    design_step_bwd(as_stream(stream), w, N, S, target_feat, seq_mask, with_template != 0, aatype,
+                    dropout != 0, save, d_atom14, d_distogram, d_pae, d_plddt, d_expres,
+                    d_target_feat, d_msa_feat);
   });
 }
 

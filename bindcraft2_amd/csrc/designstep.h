@@ -1,0 +1,36 @@
+// The trunk of one design step in one call: embedder, template embedding,
+// extra-MSA stack (pair only), main stack, single projection, structure
+// module and heads, forward and backward to the input features.
+#pragma once
+#include "embed.h"
+#include "heads.h"
+#include "tplembed.h"
+
+namespace bc2n {
+
+struct DesignStepW {
+  EmbedW emb;
+  const float *wsa = nullptr, *bsa = nullptr;  // single_activations [256][384], [384]
+  TplEmbedW tpl;
+  StackW extra, main;
+  StructHeadsW sh;
+  int d_tpl = 0, d_extra = 0, d_main = 0, d_fold = 0;
+};
+
+// Seeds: u32[4][3] on the device, one (k0, k1, enabled) JAX key per stack in
+// the order template, extra, main, structure module.
+size_t design_step_save_bytes(const DesignStepW& w, int N, int S);
+void design_step_fwd(hipStream_t st, const DesignStepW& w, int N, int S, const float* tf,
+                     const float* mf, const float* ri, const float* ai, const float* ei,
+                     const float* si, const int32_t* offset, const float* seq_mask,
+                     const float* act_const, const float* aatype, const uint32_t* seeds,
+                     bool dropout, float* atom14, float* dgram, float* pae, float* plddt,
+                     float* expres, void* save);
+// Cotangents may be null (zero) -> d target_feat [N][21], d msa_feat [S][N][49].
+void design_step_bwd(hipStream_t st, const DesignStepW& w, int N, int S, const float* tf,
+                     const float* seq_mask, bool with_template, const float* aatype,
+                     bool dropout, void* save, const float* datom, const float* ddgram,
+                     const float* dpae, const float* dplddt, const float* dexpres, float* dtf,
+                     float* dmf);
+
+}  // namespace bc2n

@@ -1,0 +1,157 @@
+// The trunk of one design step in one call, forward and backward (the
+// reference's fused NativeDesignStep, native/ffi.cu:1691-2178 over
+// native/design_step.cuh, restricted to the differentiable trunk: features
+// in, structure-module outputs out, no recycling, losses and confidence
+// metrics left to the caller):
+//
+//   msa0, pair0 = embedder(target_feat, msa_feat, ids)         (embed.hip)
+//   pair1 = pair0 + template_embedding(pair0, act_const)        (tplembed.hip; skipped without act_const)
+//   pair2 = extra-MSA stack, pair only (its MSA mask is zero)   (evoformer.hip)
+//   msa3, pair3 = main stack (msa0, pair2)
+//   single = msa3[0] . W + b                                    single_activations, f32
+//   outputs = structure module + heads (single, pair3)          (heads.hip)
+//
+// (modules_multimer.py:441-700 and the structure module / heads of
+// AlphaFoldIteration.)  The backward runs the chain in reverse to
+// d(target_feat) and d(msa_feat).  Every intermediate lives in the caller's
+// save buffer, so the two calls share nothing else.
+#include "designstep.h"
+
+#include "gemm_f32.h"
+
+namespace bc2n {
+
+namespace {
+
+constexpr int CM = 256, CZ = 128, CS = 384;
+
+template <class A>
+struct DsSave {
+  void *tpl, *extra, *main, *sh;
+  float *pmask, *mmask, *msa0, *pair0, *tplo, *pair1, *pair2, *msa3, *pair3, *single;
+  float *dpair, *dq, *dmsa, *dsingle;
+  DsSave(A& c, const DesignStepW& w, int N, int S) {
+    const size_t M = (size_t)N * N;
+    tpl = c.template take<char>(tplembed_save_bytes(w.tpl, N));
+    extra = c.template take<char>(stack_save_bytes(w.extra, N, 1, w.d_extra));
+    main = c.template take<char>(stack_save_bytes(w.main, N, S, w.d_main));
+    sh = c.template take<char>(structheads_save_bytes(N, w.d_fold));
+    pmask = c.template take<float>(M);
+    mmask = c.template take<float>((size_t)S * N);
+    msa0 = c.template take<float>((size_t)S * N * CM);
+    pair0 = c.template take<float>(M * CZ);
+    tplo = c.template take<float>(M * CZ);
+    pair1 = c.template take<float>(M * CZ);
+    pair2 = c.template take<float>(M * CZ);
+    msa3 = c.template take<float>((size_t)S * N * CM);
+    pair3 = c.template take<float>(M * CZ);
+    single = c.template take<float>((size_t)N * CS);
+    dpair = c.template take<float>(M * CZ);
+    dq = c.template take<float>(M * CZ);
+    dmsa = c.template take<float>((size_t)S * N * CM);
+    dsingle = c.template take<float>((size_t)N * CS);
+  }
+};
+
+// pmask[i][j] = m[i] m[j]; mmask[s][n] = m[n]
+__global__ void masks_kernel(const float* __restrict__ m, int N, int S, float* __restrict__ pm,
+                             float* __restrict__ mm) {
+  const long e = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e < (long)N * N) pm[e] = m[e / N] * m[e % N];
+  if (e < (long)S * N) mm[e] = m[e % N];
+}
+
+// y = a + b elementwise (y may alias a or b)
+__global__ void add2_kernel(const float* a, const float* b, long n, float* y) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = a[i] + b[i];
+}
+void add2(hipStream_t st, const float* a, const float* b, long n, float* y) {
+  hipLaunchKernelGGL(add2_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a, b, n, y);
+}
+
+void ds_check(const DesignStepW& w, int N, int S) {
+  if (N <= 0 || N % 32 != 0 || N > 512)
+    throw std::runtime_error("design step: N must be a positive multiple of 32, at most 512");
+  if (S <= 0) throw std::runtime_error("design step: S must be positive");
+  if (w.d_tpl <= 0 || w.d_extra <= 0 || w.d_main <= 0 || w.d_fold <= 0)
+    throw std::runtime_error("design step: depths must be positive");
+}
+
+}  // namespace
+
+size_t design_step_save_bytes(const DesignStepW& w, int N, int S) {
+  Sizer s;
+  DsSave<Sizer> plan(s, w, N, S);
+  (void)plan;
+  return s.off;
+}
+
+void design_step_fwd(hipStream_t st, const DesignStepW& w, int N, int S, const float* tf,
+                     const float* mf, const float* ri, const float* ai, const float* ei,
+                     const float* si, const int32_t* offset, const float* seq_mask,
+                     const float* act_const, const float* aatype, const uint32_t* seeds,
+                     bool dropout, float* atom14, float* dgram, float* pae, float* plddt,
+                     float* expres, void* save) {
+  ds_check(w, N, S);
+  nonnull(seq_mask, "design step seq_mask"); nonnull(save, "design step save");
+  if (dropout) nonnull(seeds, "design step seeds");
+  Carver cv(save);
+  DsSave<Carver> sv(cv, w, N, S);
+  const long M = (long)N * N;
+  {
+    const long n = std::max(M, (long)S * N);
+    hipLaunchKernelGGL(masks_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, seq_mask,
+                       N, S, sv.pmask, sv.mmask);
+  }
+  auto key = [&](int i) { return dropout ? seeds + 3 * i : nullptr; };
+  auto enabled = [&](int i) { return dropout ? seeds + 3 * i + 2 : nullptr; };
+  embed_fwd(st, w.emb, N, S, tf, mf, ri, ai, ei, si, offset, sv.msa0, sv.pair0);
+  const float* pair = sv.pair0;
+  if (act_const) {
+    tplembed_fwd(st, w.tpl, N, sv.pair0, act_const, sv.pmask, key(0), enabled(0), dropout, sv.tplo,
+                 sv.tpl);
+    add2(st, sv.pair0, sv.tplo, M * CZ, sv.pair1);
+    pair = sv.pair1;
+  }
+  stack_fwd(st, w.extra, N, 1, w.d_extra, pair, nullptr, sv.pmask, nullptr, key(1), enabled(1),
+            dropout, sv.pair2, nullptr, sv.extra);
+  stack_fwd(st, w.main, N, S, w.d_main, sv.pair2, sv.msa0, sv.pmask, sv.mmask, key(2), enabled(2),
+            dropout, sv.pair3, sv.msa3, sv.main);
+  GemmF32 g = gemm_rows(N, CS, CM, sv.msa3, w.wsa, sv.single);
+  g.bias = w.bsa;
+  gemm_f32(st, g, "design.gemm_single");
+  structheads_fwd(st, w.sh, N, w.d_fold, sv.single, sv.pair3, seq_mask, aatype, key(3), enabled(3),
+                  dropout, atom14, dgram, pae, plddt, expres, sv.sh);
+}
+
+void design_step_bwd(hipStream_t st, const DesignStepW& w, int N, int S, const float* tf,
+                     const float* seq_mask, bool with_template, const float* aatype,
+                     bool dropout, void* save, const float* datom, const float* ddgram,
+                     const float* dpae, const float* dplddt, const float* dexpres, float* dtf,
+                     float* dmf) {
+  ds_check(w, N, S);
+  nonnull(seq_mask, "design step seq_mask"); nonnull(save, "design step save");
+  Carver cv(save);
+  DsSave<Carver> sv(cv, w, N, S);
+  const long M = (long)N * N;
+  structheads_bwd(st, w.sh, N, w.d_fold, sv.single, sv.pair3, seq_mask, aatype, dropout, sv.sh,
+                  datom, ddgram, dpae, dplddt, dexpres, sv.dsingle, sv.dpair);
+  // d msa3: row 0 from the single projection, the other rows zero
+  BC2N_HIP(hipMemsetAsync(sv.dmsa, 0, (size_t)S * N * CM * 4, st));
+  GemmF32 g = gemm_rows(N, CM, CS, sv.dsingle, w.wsa, sv.dmsa, true);
+  gemm_f32(st, g, "design.gemm_single_dx");
+  // the stacks accumulate in place: d pair3 -> d pair2 -> d pair1, d msa3 -> d msa0
+  stack_bwd(st, w.main, N, S, w.d_main, sv.pmask, sv.mmask, dropout, sv.main, sv.dpair, sv.dmsa,
+            sv.dpair, sv.dmsa);
+  stack_bwd(st, w.extra, N, 1, w.d_extra, sv.pmask, nullptr, dropout, sv.extra, sv.dpair, nullptr,
+            sv.dpair, nullptr);
+  if (with_template) {
+    // pair1 = pair0 + template(pair0): d pair0 = d pair1 + d query
+    tplembed_bwd(st, w.tpl, N, sv.pair0, sv.pmask, dropout, sv.tpl, sv.dpair, sv.dq);
+    add2(st, sv.dpair, sv.dq, M * CZ, sv.dpair);
+  }
+  embed_bwd(st, w.emb, N, S, sv.dmsa, sv.dpair, tf, dtf, dmf);
+}
+
+}  // namespace bc2n

@@ -461,6 +461,50 @@ class StructureHeads:
         return dsingle, dpair
 
 
+class DesignStep:
+    """The trunk of one design step in one call (bc2n_design_step_*):
+    embedder, template embedding (when act_const is given), extra-MSA stack
+    (pair only), main stack, single projection, structure module and heads;
+    backward to d(target_feat), d(msa_feat)."""
+
+    def __init__(self, emb_dir, tpl_dir, extra_dir, main_dir, post_dir, depths=(2, 4, 48, 8)):
+        self.dirs = [d.encode() for d in (emb_dir, tpl_dir, extra_dir, main_dir, post_dir)]
+        self.depths = tuple(int(d) for d in depths)  # template, extra, main, fold
+
+    def save_bytes(self, n, s):
+        b = lib().bc2n_design_step_save_bytes(*self.dirs, n, s, *self.depths)
+        if b == 0:
+            check(1)
+        return b
+
+    def forward(self, target_feat, msa_feat, ids, seq_mask, aatype, act_const=None, offset=None,
+                seeds=None, dropout=True, save=None):
+        """ids = (residue_index, asym_id, entity_id, sym_id); seeds u32[4][3]
+        -> ((atom14, distogram, pae, plddt, expres), save)"""
+        n, s, dev = target_feat.shape[0], msa_feat.shape[0], target_feat.device
+        outs = tuple(torch.empty(*sh, dtype=torch.float32, device=dev)
+                     for sh in ((n, 14, 3), (n, n, 64), (n, n, 64), (n, 50), (n, 37)))
+        if save is None:
+            save = torch.empty(self.save_bytes(n, s), dtype=torch.uint8, device=dev)
+        check(lib().bc2n_design_step_fwd(_stream(), _ptr(target_feat), _ptr(msa_feat),
+                                         *map(_ptr, ids), _ptr(offset), _ptr(seq_mask),
+                                         _ptr(act_const), _ptr(aatype), _ptr(seeds), n, s,
+                                         *self.depths, int(dropout), *self.dirs,
+                                         *map(_ptr, outs), _ptr(save)))
+        return outs, save
+
+    def backward(self, cts, target_feat, seq_mask, aatype, save, with_template=True,
+                 dropout=True, msa_rows=1):
+        n = target_feat.shape[0]
+        dtf = torch.empty_like(target_feat)
+        dmf = torch.empty(msa_rows, n, 49, dtype=torch.float32, device=target_feat.device)
+        check(lib().bc2n_design_step_bwd(_stream(), _ptr(target_feat), _ptr(seq_mask),
+                                         _ptr(aatype), int(with_template), *map(_ptr, cts),
+                                         _ptr(save), n, msa_rows, *self.depths, int(dropout),
+                                         *self.dirs, _ptr(dtf), _ptr(dmf)))
+        return dtf, dmf
+
+
 def dropout_table(rows, channels, key, rate, device="cuda"):
     """[rows, channels] keep/keep_rate table from a JAX key (k0, k1)."""
     tbl = torch.empty(rows, channels, dtype=torch.float32, device=device)

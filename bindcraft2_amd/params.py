@@ -158,12 +158,20 @@ def embedder_shapes(c_m=C_M, c_z=C_Z):
             "position_activations/weights": (73, c_z), "position_activations/bias": (c_z,)}
 
 
+def single_activations_shapes(c_m=C_M, c_s=384):
+    """single_activations (modules_multimer.py EmbeddingsAndEvoformer: the
+    single representation from the main stack's msa[0]); it ships in the
+    embedder's weights directory (bindcraft/af/native.py:515-527)."""
+    return {"single_activations/weights": (c_m, c_s), "single_activations/bias": (c_s,)}
+
+
 def init_embedder_params(rng, scoped=False):
-    """Weights directory contents of the embedder; `scoped` puts
+    """Weights directory contents of the embedder (with single_activations);
+    `scoped` puts
     position_activations under evoformer/~_relative_encoding/ as haiku's
     method scope (and the checkpoint) does."""
     out = {}
-    for name, shape in embedder_shapes().items():
+    for name, shape in {**embedder_shapes(), **single_activations_shapes()}.items():
         fan_in = shape[0] if len(shape) == 2 else 1
         arr = rng.standard_normal(shape) / math.sqrt(fan_in)
         if len(shape) == 1:

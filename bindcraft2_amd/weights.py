@@ -37,6 +37,7 @@ HEADS = ("distogram_head", "predicted_aligned_error_head", "predicted_lddt_head"
          "experimentally_resolved_head")
 EMBED_LEAVES = ("preprocess_1d", "preprocess_msa", "left_single", "right_single",
                 "position_activations")
+EMBED_OPTIONAL = ("single_activations",)  # the one-call design step reads it
 IPA_HEADS = 12
 
 
@@ -180,7 +181,7 @@ def embed_flat(tree):
         if not mod.startswith(EVO + "/"):
             continue
         leaf = mod.rpartition("/")[2]
-        if leaf not in EMBED_LEAVES:
+        if leaf not in EMBED_LEAVES + EMBED_OPTIONAL:
             continue
         for pname, v in d.items():
             flat[f"param/{leaf}/{pname}"] = np.asarray(v, np.float32)

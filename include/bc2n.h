@@ -330,6 +330,50 @@ int bc2n_structure_heads_bwd(void* stream, const float* single, const float* pai
                              float* dpair);
 
 /* ------------------------------------------------------------------------
+ * The trunk of one design step in one call (a reduced form of the
+ * reference's NativeDesignStep custom call, native/ffi.cu:1691-2178, runner
+ * bindcraft/af/native_step.py: features in, structure-module outputs out;
+ * the sequence parametrisation, recycling, confidence metrics and losses
+ * stay with the caller).  fwd:
+ *   (target_feat f32[N,21], msa_feat f32[S,N,49], residue_index, asym_id,
+ *    entity_id, sym_id f32[N], offset i32[N,N] or NULL, seq_mask f32[N],
+ *    act_const f32[N,N,64] or NULL (no template), aatype f32[N],
+ *    seeds u32[4][3] = (k0, k1, enabled) keys of the template, extra, main
+ *    and structure-module stacks; depths, dropout, five weights directories)
+ *   -> (atom14 f32[N,14,3], distogram, pae f32[N,N,64], plddt f32[N,50],
+ *       expres f32[N,37]) and save
+ * = bc2n_embedder, + bc2n_tplembed on the embedded pair, bc2n_evoformer
+ * pair-only (extra MSA mask zero), bc2n_evoformer (main), single =
+ * msa[0] . single_activations (from the embedder's directory),
+ * bc2n_structure_heads (modules_multimer.py:441-700).  bwd: the five
+ * cotangents (any may be NULL) -> d_target_feat f32[N,21], d_msa_feat
+ * f32[S,N,49].  N is a runtime value (a multiple of 32, at most 512): one
+ * set of weights serves every length.  save holds
+ * bc2n_design_step_save_bytes() bytes and is written by both calls.
+ * ---------------------------------------------------------------------- */
+size_t bc2n_design_step_save_bytes(const char* emb_dir, const char* tpl_dir,
+                                   const char* extra_dir, const char* main_dir,
+                                   const char* post_dir, int N, int S, int64_t d_tpl,
+                                   int64_t d_extra, int64_t d_main, int64_t d_fold);
+int bc2n_design_step_fwd(void* stream, const float* target_feat, const float* msa_feat,
+                         const float* residue_index, const float* asym_id,
+                         const float* entity_id, const float* sym_id, const int32_t* offset,
+                         const float* seq_mask, const float* act_const, const float* aatype,
+                         const uint32_t* seeds, int N, int S, int64_t d_tpl, int64_t d_extra,
+                         int64_t d_main, int64_t d_fold, int64_t dropout, const char* emb_dir,
+                         const char* tpl_dir, const char* extra_dir, const char* main_dir,
+                         const char* post_dir, float* atom14, float* distogram, float* pae,
+                         float* plddt, float* expres, void* save);
+int bc2n_design_step_bwd(void* stream, const float* target_feat, const float* seq_mask,
+                         const float* aatype, int64_t with_template, const float* d_atom14,
+                         const float* d_distogram, const float* d_pae, const float* d_plddt,
+                         const float* d_expres, void* save, int N, int S, int64_t d_tpl,
+                         int64_t d_extra, int64_t d_main, int64_t d_fold, int64_t dropout,
+                         const char* emb_dir, const char* tpl_dir, const char* extra_dir,
+                         const char* main_dir, const char* post_dir, float* d_target_feat,
+                         float* d_msa_feat);
+
+/* ------------------------------------------------------------------------
  * Dropout with JAX's own bits.  tbl[b*C+c] = keep/keep_rate where
  * keep = jax.random.bernoulli(key, keep_rate, (B, C)), keep_rate =
  * float32(1) - float32(rate); key = (k0, k1) = jax.random.key_data(key).

@@ -611,3 +611,37 @@ def structure_heads(single, pair, mask, aatype, params, depth, key, use_dropout,
     atom14 = multi_rigid_sidechain(traj[-1][..., :3], traj[-1][..., 3], act, init, aat,
                                    P.sub("fold_iteration/rigid_sidechain/"), tables)
     return (atom14,) + heads(pair, act, single, params, dtype)
+
+
+def design_step(target_feat, msa_feat, ids, offset, seq_mask, act_const, aatype, emsa, prm,
+                depths, keys, use_dropout, tables, dtype=torch.float64, round_trunk=False):
+    """The trunk of one design step, input features to the structure-module
+    outputs (modules_multimer.py:441-700, EmbeddingsAndEvoformer, then
+    AlphaFoldIteration's structure module and heads): the embedder; the
+    template embedding added to the pair (:530-551, act_const = its eight
+    constant projections, None = no template); the extra-MSA stack with its
+    mask at zero (the design step's extra MSA; `emsa` is any [S_e, N, 64]);
+    the main stack; single = single_activations(msa[0]); structure_heads.
+    `prm` maps 'emb', 'tpl', 'extra', 'main', 'post' to flat parameter
+    dicts; `depths` and `keys` ('tpl', 'extra', 'main', 'fold') give each
+    stack its depth and its JAX key.  round_trunk rounds the trunk's
+    outputs (single, pair) to bfloat16 before the structure module, keeping
+    their gradient (straight through): a probe of how much the structure
+    module amplifies bf16-sized differences in its inputs."""
+    msa, pair = embedder(target_feat, msa_feat, *ids, prm["emb"], offset=offset, dtype=dtype)
+    pmask = seq_mask[:, None] * seq_mask[None, :]
+    mmask = seq_mask[None].expand(msa.shape[0], -1)
+    if act_const is not None:
+        pair = pair + template_embedding(pair, act_const, pmask, prm["tpl"], depths["tpl"],
+                                         keys["tpl"], use_dropout, dtype)
+    emask = torch.zeros(emsa.shape[:2], dtype=dtype)
+    _, pair = evoformer_stack(emsa, pair, emask, pmask, prm["extra"], depths["extra"], keys["extra"],
+                              use_dropout, is_extra_msa=True, dtype=dtype)
+    msa, pair = evoformer_stack(msa, pair, mmask, pmask, prm["main"], depths["main"], keys["main"],
+                                use_dropout, dtype=dtype)
+    single = linear(msa[0], Params(prm["emb"], "param/single_activations/", dtype))
+    if round_trunk:
+        bf = lambda x: x + (x.to(torch.bfloat16).to(dtype) - x).detach()
+        single, pair = bf(single), bf(pair)
+    return structure_heads(single, pair, seq_mask, aatype, prm["post"], depths["fold"], keys["fold"],
+                           use_dropout, tables, dtype)
