@@ -21,7 +21,11 @@ void ln_bwd_f32(hipStream_t st, const float* dy, const float* x, long M, int C,
 // Channel-major ([C][M]) input forms used by the triangle multiplication.
 void ln_fwd_cm(hipStream_t st, const float* x, long M, int C, const float* gamma,
                const float* beta, bf16* y, float* mean, float* rstd, bool fast);
+void ln_fwd_cm(hipStream_t st, const bf16* x, long M, int C, const float* gamma,
+               const float* beta, bf16* y, float* mean, float* rstd, bool fast);
 void ln_bwd_cm(hipStream_t st, const float* dy, const float* x, long M, int C,
+               const float* gamma, const float* mean, const float* rstd, bf16* dx);
+void ln_bwd_cm(hipStream_t st, const float* dy, const bf16* x, long M, int C,
                const float* gamma, const float* mean, const float* rstd, bf16* dx);
 
 // ---------------------------------------------------------------- attention

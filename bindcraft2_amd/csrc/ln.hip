@@ -204,9 +204,18 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(
 // rows stages the [C][64] tile through LDS (float4 loads along m) and then
 // normalises it 4 lanes per row; the output is row-major [M][C] bf16.
 // Requires M % 4 == 0.
-template <int C, bool FAST>
+// 4 consecutive m of channel plane c (x is [C][M], float or bf16)
+__device__ __forceinline__ float4 cm_load4(const float* x, long idx) {
+  return *reinterpret_cast<const float4*>(x + idx);
+}
+__device__ __forceinline__ float4 cm_load4(const bf16* x, long idx) {
+  const bf16x4 v = *reinterpret_cast<const bf16x4*>(x + idx);
+  return make_float4((float)v[0], (float)v[1], (float)v[2], (float)v[3]);
+}
+
+template <int C, bool FAST, class InT>
 __global__ __launch_bounds__(256) void ln_fwd_cm_kernel(
-    const float* __restrict__ x, long M, const float* __restrict__ gamma,
+    const InT* __restrict__ x, long M, const float* __restrict__ gamma,
     const float* __restrict__ beta, bf16* __restrict__ y,
     float* __restrict__ mean_out, float* __restrict__ rstd_out) {
   constexpr int R = 64;
@@ -217,7 +226,7 @@ __global__ __launch_bounds__(256) void ln_fwd_cm_kernel(
     const int c = i / (R / 4), q = (i % (R / 4)) * 4;
     const long m = m0 + q;
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (m < M) v = *reinterpret_cast<const float4*>(x + (long)c * M + m);
+    if (m < M) v = cm_load4(x, (long)c * M + m);
     tile[q + 0][c] = v.x;
     tile[q + 1][c] = v.y;
     tile[q + 2][c] = v.z;
@@ -264,9 +273,9 @@ __global__ __launch_bounds__(256) void ln_fwd_cm_kernel(
 
 // Backward of the channel-major norm: dy row-major [M][C] f32, x channel-major
 // [C][M] f32; writes dx channel-major [C][M] as bf16 (a GEMM operand).
-template <int C>
+template <int C, class InT>
 __global__ __launch_bounds__(256) void ln_bwd_cm_kernel(
-    const float* __restrict__ dy, const float* __restrict__ x, long M,
+    const float* __restrict__ dy, const InT* __restrict__ x, long M,
     const float* __restrict__ gamma, const float* __restrict__ mean,
     const float* __restrict__ rstd, bf16* __restrict__ dx) {
   constexpr int R = 64;
@@ -277,7 +286,7 @@ __global__ __launch_bounds__(256) void ln_bwd_cm_kernel(
     const int c = i / (R / 4), q = (i % (R / 4)) * 4;
     const long m = m0 + q;
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (m < M) v = *reinterpret_cast<const float4*>(x + (long)c * M + m);
+    if (m < M) v = cm_load4(x, (long)c * M + m);
     tile[q + 0][c] = v.x;
     tile[q + 1][c] = v.y;
     tile[q + 2][c] = v.z;
@@ -412,28 +421,47 @@ void ln_bwd_f32(hipStream_t st, const float* dy, const float* x, long M, int C,
   }
 }
 
-void ln_fwd_cm(hipStream_t st, const float* x, long M, int C, const float* gamma,
-               const float* beta, bf16* y, float* mean, float* rstd, bool fast) {
+template <class InT>
+static void ln_fwd_cm_t(hipStream_t st, const InT* x, long M, int C, const float* gamma,
+                        const float* beta, bf16* y, float* mean, float* rstd, bool fast) {
   if (M % 4 != 0) throw std::runtime_error("ln_fwd_cm: M must be a multiple of 4");
   const int grid = (int)((M + 63) / 64);
+#define BC2N_LNCM(CV, FV) \
+  hipLaunchKernelGGL((ln_fwd_cm_kernel<CV, FV, InT>), dim3(grid), dim3(256), 0, st, x, M, gamma, beta, y, mean, rstd)
   if (C == 128) {
-    if (fast) hipLaunchKernelGGL((ln_fwd_cm_kernel<128, true>), dim3(grid), dim3(256), 0, st, x, M, gamma, beta, y, mean, rstd);
-    else hipLaunchKernelGGL((ln_fwd_cm_kernel<128, false>), dim3(grid), dim3(256), 0, st, x, M, gamma, beta, y, mean, rstd);
+    if (fast) BC2N_LNCM(128, true); else BC2N_LNCM(128, false);
   } else if (C == 64) {
-    if (fast) hipLaunchKernelGGL((ln_fwd_cm_kernel<64, true>), dim3(grid), dim3(256), 0, st, x, M, gamma, beta, y, mean, rstd);
-    else hipLaunchKernelGGL((ln_fwd_cm_kernel<64, false>), dim3(grid), dim3(256), 0, st, x, M, gamma, beta, y, mean, rstd);
+    if (fast) BC2N_LNCM(64, true); else BC2N_LNCM(64, false);
   } else {
     throw std::runtime_error("ln_fwd_cm: unsupported channel count");
   }
+#undef BC2N_LNCM
+}
+void ln_fwd_cm(hipStream_t st, const float* x, long M, int C, const float* gamma,
+               const float* beta, bf16* y, float* mean, float* rstd, bool fast) {
+  ln_fwd_cm_t(st, x, M, C, gamma, beta, y, mean, rstd, fast);
+}
+void ln_fwd_cm(hipStream_t st, const bf16* x, long M, int C, const float* gamma,
+               const float* beta, bf16* y, float* mean, float* rstd, bool fast) {
+  ln_fwd_cm_t(st, x, M, C, gamma, beta, y, mean, rstd, fast);
 }
 
-void ln_bwd_cm(hipStream_t st, const float* dy, const float* x, long M, int C,
-               const float* gamma, const float* mean, const float* rstd, bf16* dx) {
+template <class InT>
+static void ln_bwd_cm_t(hipStream_t st, const float* dy, const InT* x, long M, int C,
+                        const float* gamma, const float* mean, const float* rstd, bf16* dx) {
   if (M % 4 != 0) throw std::runtime_error("ln_bwd_cm: M must be a multiple of 4");
   const int grid = (int)((M + 63) / 64);
-  if (C == 128) hipLaunchKernelGGL((ln_bwd_cm_kernel<128>), dim3(grid), dim3(256), 0, st, dy, x, M, gamma, mean, rstd, dx);
-  else if (C == 64) hipLaunchKernelGGL((ln_bwd_cm_kernel<64>), dim3(grid), dim3(256), 0, st, dy, x, M, gamma, mean, rstd, dx);
+  if (C == 128) hipLaunchKernelGGL((ln_bwd_cm_kernel<128, InT>), dim3(grid), dim3(256), 0, st, dy, x, M, gamma, mean, rstd, dx);
+  else if (C == 64) hipLaunchKernelGGL((ln_bwd_cm_kernel<64, InT>), dim3(grid), dim3(256), 0, st, dy, x, M, gamma, mean, rstd, dx);
   else throw std::runtime_error("ln_bwd_cm: unsupported channel count");
+}
+void ln_bwd_cm(hipStream_t st, const float* dy, const float* x, long M, int C,
+               const float* gamma, const float* mean, const float* rstd, bf16* dx) {
+  ln_bwd_cm_t(st, dy, x, M, C, gamma, mean, rstd, dx);
+}
+void ln_bwd_cm(hipStream_t st, const float* dy, const bf16* x, long M, int C,
+               const float* gamma, const float* mean, const float* rstd, bf16* dx) {
+  ln_bwd_cm_t(st, dy, x, M, C, gamma, mean, rstd, dx);
 }
 
 // ------------------------------------------------- f32 rows, any width

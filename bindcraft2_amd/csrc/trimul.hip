@@ -106,15 +106,15 @@ struct EpiTrimulOut : EpiRows {
 
 template <class A>
 struct TriMulSave {
-  float *mean, *rstd, *cmean, *crstd, *T;
-  bf16 *xn, *left, *right, *gout, *osave;
+  float *mean, *rstd, *cmean, *crstd;
+  bf16 *T, *xn, *left, *right, *gout, *osave;
   TriMulSave(A& a, int N, int C, int I) {
     const size_t M = (size_t)N * N;
     mean = a.template take<float>(M);
     rstd = a.template take<float>(M);
     cmean = a.template take<float>(M);
     crstd = a.template take<float>(M);
-    T = a.template take<float>(M * I);
+    T = a.template take<bf16>(M * I);
     xn = a.template take<bf16>(M * C);
     left = a.template take<bf16>(M * I);
     right = a.template take<bf16>(M * I);
@@ -519,7 +519,7 @@ static void contract(hipStream_t st, const GemmArgs& g, OutT* C, const char* nam
 
 // Contraction operand layouts for one channel plane (row-major N x N).
 static void contraction_fwd(hipStream_t st, bool outgoing, int N, int I, const bf16* L,
-                            const bf16* R, float* T) {
+                            const bf16* R, bf16* T) {
   const long M = (long)N * N;
   GemmArgs g;
   g.M = N; g.N = N; g.K = N; g.batch = I;
@@ -531,7 +531,7 @@ static void contraction_fwd(hipStream_t st, bool outgoing, int N, int I, const b
     g.B = L; g.b_sn = 1; g.b_sk = N;
   }
   g.a_sb = M; g.b_sb = M;
-  contract<float>(st, g, T, "trimul.contract_fwd");
+  contract<bf16>(st, g, T, "trimul.contract_fwd");
 }
 
 void trimul_fwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const float* pair_in,
