@@ -15,6 +15,8 @@
 // tiles), K in steps of 16 staged through LDS as [k][m] / [k][n] so a lane's
 // MFMA operand read (row l%16 at k l/16) is one conflict-free LDS word.
 #pragma once
+#include <algorithm>
+#include <mutex>
 #include <stdexcept>
 
 #include "common.h"
@@ -32,6 +34,11 @@ struct GemmF32 {
   const float* add = nullptr;   // C layout
   float alpha = 1.f, beta = 0.f;
   bool relu = false, gate_is_mask = false;
+  // split-K (set by gemm_f32): ksplit > 1 workgroups per tile each sum one
+  // K range into part[s][b][m][n]; a second kernel adds them and applies the
+  // epilogue
+  int ksplit = 1, kchunk = 0;
+  float* part = nullptr;
 };
 
 namespace gf32 {
@@ -45,8 +52,12 @@ static __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmF32 g) {
   __shared__ float Bs[BK][LDS_LD];
   const int tiles_n = (g.N + BN - 1) / BN;
   const int tiles = ((g.M + BM - 1) / BM) * tiles_n;
-  const long bid = xcd_block((long)tiles * g.batch);
-  if (bid >= (long)tiles * g.batch) return;
+  const long G = (long)tiles * g.batch * g.ksplit;
+  const long bid0 = xcd_block(G);
+  if (bid0 >= G) return;
+  const int ks = (int)(bid0 % g.ksplit);
+  const long bid = bid0 / g.ksplit;
+  const int kbeg = ks * g.kchunk, kend = g.ksplit > 1 ? min(g.K, kbeg + g.kchunk) : g.K;
   const int b = (int)(bid / tiles), t = (int)(bid % tiles);
   const int m0 = (t / tiles_n) * BM, n0 = (t % tiles_n) * BN;
   const float* A = g.A + (long)b * g.a_sb;
@@ -61,14 +72,14 @@ static __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmF32 g) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int k0 = 0; k0 < g.K; k0 += BK) {
+  for (int k0 = kbeg; k0 < kend; k0 += BK) {
 #pragma unroll
     for (int i = 0; i < (BM * BK) / 256; ++i) {
       const int e = tid + 256 * i;
       int m, k;
       if (a_kfast) { k = e % BK; m = e / BK; } else { m = e % BM; k = e / BM; }
       const int gm = m0 + m, gk = k0 + k;
-      As[k][m] = (gm < g.M && gk < g.K) ? A[gm * g.a_sm + gk * g.a_sk] : 0.f;
+      As[k][m] = (gm < g.M && gk < kend) ? A[gm * g.a_sm + gk * g.a_sk] : 0.f;
     }
 #pragma unroll
     for (int i = 0; i < (BN * BK) / 256; ++i) {
@@ -76,7 +87,7 @@ static __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmF32 g) {
       int n, k;
       if (b_nfast) { n = e % BN; k = e / BN; } else { k = e % BK; n = e / BK; }
       const int gn = n0 + n, gk = k0 + k;
-      Bs[k][n] = (gn < g.N && gk < g.K) ? B[gk * g.b_sk + gn * g.b_sn] : 0.f;
+      Bs[k][n] = (gn < g.N && gk < kend) ? B[gk * g.b_sk + gn * g.b_sn] : 0.f;
     }
     __syncthreads();
 #pragma unroll
@@ -96,6 +107,22 @@ static __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmF32 g) {
     __syncthreads();
   }
 
+  if (g.ksplit > 1) {
+    float* P = g.part + ((long)ks * g.batch + b) * g.M * g.N;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int n = n0 + wn * 32 + j * 16 + (lane & 15);
+        if (n >= g.N) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + r;
+          if (m < g.M) P[(long)m * g.N + n] = acc[i][j][r];
+        }
+      }
+    return;
+  }
   float* C = g.C + (long)b * g.c_sb;
   const float* gate = g.gate ? g.gate + (long)b * g.c_sb : nullptr;
   const float* add = g.add ? g.add + (long)b * g.c_sb : nullptr;
@@ -121,12 +148,63 @@ static __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmF32 g) {
     }
 }
 
-inline void gemm_f32(hipStream_t st, const GemmF32& g, const char* name = "gemm_f32") {
+// Sum of the split-K partials, then the epilogue of gemm_f32_kernel.
+static __global__ __launch_bounds__(256) void gemm_f32_splitk_reduce(GemmF32 g) {
+  const long e = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long MN = (long)g.M * g.N;
+  if (e >= MN * g.batch) return;
+  const int b = (int)(e / MN);
+  const int m = (int)((e % MN) / g.N), n = (int)(e % g.N);
+  float v = 0.f;
+  for (int s = 0; s < g.ksplit; ++s) v += g.part[((long)s * g.batch + b) * MN + (long)m * g.N + n];
+  const long o = (long)b * g.c_sb + (long)m * g.c_sm + (long)n * g.c_sn;
+  v *= g.alpha;
+  if (g.bias) v += g.bias[n];
+  if (g.relu) v = fmaxf(v, 0.f);
+  if (g.gate) v = g.gate_is_mask ? (g.gate[o] > 0.f ? v : 0.f) : v * g.gate[o];
+  if (g.add) v += g.add[o];
+  if (g.beta != 0.f) v += g.beta * g.C[o];
+  g.C[o] = v;
+}
+
+// Split-K partial buffer, grow-only, one per process (the arena is in use by
+// the callers while they launch these GEMMs).
+inline Arena& gemm_f32_scratch() {
+  static Arena a;
+  return a;
+}
+
+inline void gemm_f32(hipStream_t st, const GemmF32& g_in, const char* name = "gemm_f32") {
+  GemmF32 g = g_in;
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.batch <= 0) throw std::runtime_error("gemm_f32: empty shape");
   if (!g.A || !g.B || !g.C) throw std::runtime_error("gemm_f32: missing operand");
   const long tiles = (long)((g.M + gf32::BM - 1) / gf32::BM) * ((g.N + gf32::BN - 1) / gf32::BN);
   KTimed kt(name, st);
-  hipLaunchKernelGGL(gemm_f32_kernel, dim3(xcd_grid(tiles * g.batch)), dim3(256), 0, st, g);
+  // Few tiles and a long K (the structure module's N-row products, e.g. the
+  // IPA output projection, 224 x 384 over K = 2112, is 24 tiles): split K so
+  // that about one workgroup per CU works, each over >= 128 of K.
+  const long want = device_cus();
+  int split = 1;
+  if (tiles * g.batch < want / 2 && g.K >= 256) {
+    split = (int)std::min<long>((want + tiles * g.batch - 1) / (tiles * g.batch), g.K / 128);
+    split = std::max(split, 1);
+  }
+  if (split == 1) {
+    g.ksplit = 1; g.kchunk = g.K;
+    hipLaunchKernelGGL(gemm_f32_kernel, dim3(xcd_grid(tiles * g.batch)), dim3(256), 0, st, g);
+    return;
+  }
+  const int chunk = ((g.K + split - 1) / split + gf32::BK - 1) / gf32::BK * gf32::BK;
+  split = (g.K + chunk - 1) / chunk;
+  Arena& ar = gemm_f32_scratch();
+  std::lock_guard<std::recursive_mutex> lk(ar.lock());
+  const size_t elems = (size_t)split * g.batch * g.M * g.N;
+  ar.reset(st, elems * 4 + 256);
+  g.part = ar.take_n<float>(elems);
+  g.ksplit = split; g.kchunk = chunk;
+  hipLaunchKernelGGL(gemm_f32_kernel, dim3(xcd_grid(tiles * g.batch * split)), dim3(256), 0, st, g);
+  const long n = (long)g.M * g.N * g.batch;
+  hipLaunchKernelGGL(gemm_f32_splitk_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, g);
 }
 
 // Row-major helpers: C[M,N] = A[M,K] . B[K,N] (or B^T given as [N,K]).

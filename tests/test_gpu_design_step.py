@@ -75,6 +75,29 @@ def test_design_step_parity(cuda, n, with_template, dropout):
     shapes = ((n, 14, 3), (n, n, 64), (n, n, 64), (n, 50), (n, 37))
     cts = [rng.standard_normal(sh).astype(np.float32) for sh in shapes]
 
+    def oracle(round_trunk, grads=True):
+        tft = torch.tensor(tf, dtype=D, requires_grad=True)
+        mft = torch.tensor(mf, dtype=D, requires_grad=True)
+        ref = af2.design_step(tft, mft, ids, None, torch.as_tensor(seq_mask, dtype=D),
+                              None if act_const is None else torch.as_tensor(act_const, dtype=D),
+                              aatype, torch.as_tensor(emsa, dtype=D), prm, depths,
+                              keys if dropout else {k: None for k in keys}, dropout, tables,
+                              round_trunk=round_trunk)
+        if not grads:
+            return [r.detach() for r in ref]
+        loss = sum((r * torch.as_tensor(c, dtype=D)).sum() for r, c in zip(ref, cts))
+        return [r.detach() for r in ref] + list(torch.autograd.grad(loss, (tft, mft)))
+
+    # Residues whose atoms move far more than the rest when the trunk's
+    # outputs are merely rounded to bf16 (a near-zero torsion pair, a
+    # sensitive frame) are ill-conditioned in the oracle itself: their atom14
+    # cotangent would dominate every gradient, so it is dropped (both sides).
+    a0, a1 = oracle(False, False)[0], oracle(True, False)[0]
+    dev_res = (a1 - a0).abs().amax((1, 2))
+    bad = (dev_res > 20 * dev_res.median().clamp_min(1e-12)).numpy()
+    print("  ill-conditioned residues", np.where(bad)[0])
+    cts[0][bad] = 0.0
+
     T = lambda a: None if a is None else torch.as_tensor(a, device=cuda)
     step = ops.DesignStep(*dirs, depths=(depths["tpl"], depths["extra"], depths["main"],
                                          depths["fold"]))
@@ -84,17 +107,6 @@ def test_design_step_parity(cuda, n, with_template, dropout):
     dtf, dmf = step.backward([T(c) for c in cts], T(tf), T(seq_mask), T(aatype), save,
                              with_template=with_template, dropout=dropout)
     torch.cuda.synchronize()
-
-    def oracle(round_trunk):
-        tft = torch.tensor(tf, dtype=D, requires_grad=True)
-        mft = torch.tensor(mf, dtype=D, requires_grad=True)
-        ref = af2.design_step(tft, mft, ids, None, torch.as_tensor(seq_mask, dtype=D),
-                              None if act_const is None else torch.as_tensor(act_const, dtype=D),
-                              aatype, torch.as_tensor(emsa, dtype=D), prm, depths,
-                              keys if dropout else {k: None for k in keys}, dropout, tables,
-                              round_trunk=round_trunk)
-        loss = sum((r * torch.as_tensor(c, dtype=D)).sum() for r, c in zip(ref, cts))
-        return [r.detach() for r in ref] + list(torch.autograd.grad(loss, (tft, mft)))
 
     ref, probe = oracle(False), oracle(True)
     names = ("atom14", "distogram", "pae", "plddt", "expres", "d target_feat", "d msa_feat")
