@@ -137,7 +137,7 @@ struct GemmSmem {
   static constexpr int LDK = BK + 8;
   // 64-deep steps (long K) keep one operand buffer and pay a second barrier
   // per step, so four workgroups still fit a CU; 32-deep steps double-buffer
-  static constexpr int NBUF = BK == 64 ? 1 : 2;
+  static constexpr int NBUF = BK >= 64 ? 1 : 2;
   static constexpr int AB = NBUF * (BM + BN) * LDK * 2;  // bytes of the operand buffers
   static constexpr int LDT = BN + 4;
   static constexpr int T = (BM / 2) * LDT * 4;          // bytes of one epilogue pass

@@ -9,9 +9,11 @@ The stacks are bf16, so the bar is the north star's (outputs relL2 and
 normwise max error <= 2e-2, gradients cosine >= 0.999; 0.998 through the
 template embedding's relu hinge, as its own test documents), loosened per
 tensor to 4x (gradients: 6x) the difference that rounding the trunk's
-outputs to bf16 makes in the oracle itself (the structure module amplifies input differences at
-ill-conditioned residues: a random-weight fold can turn a bf16 rounding of
-its inputs into a 0.7 A move of one residue's atoms)."""
+outputs to bf16 makes in the oracle itself.  A random-weight fold amplifies
+input differences at ill-conditioned residues (a bf16 rounding of the trunk's
+outputs can move one residue's atoms by 0.7 A while the rest move by a few
+hundredths); the same rounding probe finds such residues and their atom14
+cotangent is dropped on both sides, so they do not dominate the gradients."""
 import numpy as np
 import pytest
 import torch
