@@ -258,6 +258,9 @@ __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
   using namespace tail;
   __shared__ __attribute__((aligned(16))) bf16 B1s[2 * B1E];
   __shared__ __attribute__((aligned(16))) bf16 B2s[2 * B2E];
+  // the projection biases, read in the d(cat) formulas from LDS: a global
+  // load there would wait (in-order vmcnt) for the next chunk's prefetch
+  __shared__ __attribute__((aligned(16))) float Bps[2 * I], Bgs[2 * I];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, l16 = lane & 15;
@@ -329,6 +332,10 @@ __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
   float mk[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) mk[i] = a.mask[m0 + i * 16 + l16];
+  if (tid < 2 * I) {
+    Bps[tid] = a.bp[tid];
+    Bgs[tid] = a.bg[tid];
+  }
   stash(0, 0);
   __syncthreads();
 
@@ -338,7 +345,9 @@ __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
 #pragma unroll
     for (int j = 0; j < C / 16; ++j) acc2[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-#pragma unroll 1
+  // fully unrolled: every chunk's registers are fixed at compile time, so the
+  // prefetched operands stay in flight until their use (no loop-carried copies)
+#pragma unroll
   for (int s = 0; s < NCHUNK; ++s) {
     const int buf = s & 1;
     const bf16* b1 = B1s + buf * B1E;
@@ -368,7 +377,7 @@ __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
         const int ch = s * 32 + q * 16 + 4 * g;  // channel of slot r = ch + r (0..2I)
         float bpv[4], bgv[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) { bpv[r] = a.bp[ch + r]; bgv[r] = a.bg[ch + r]; }
+        for (int r = 0; r < 4; ++r) { bpv[r] = Bps[ch + r]; bgv[r] = Bgs[ch + r]; }
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
           bf16x8 f;
