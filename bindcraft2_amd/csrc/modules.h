@@ -41,6 +41,10 @@ struct TriMulW {
   const float *bp = nullptr, *bg = nullptr, *bgl = nullptr, *bo = nullptr;
   const bf16* wcat = nullptr;    // [C][4I+C]  (GEMM column order)
   const bf16* wcat_t = nullptr;  // [4I+C][C]
+  // the same two matrices with k permuted within each 32-block (tail_kperm):
+  // the backward tail reads a lane's 8 MFMA k-slots as one 16-byte LDS read
+  const bf16* wcat_k = nullptr;
+  const bf16* wcat_tk = nullptr;
   const bf16* wo = nullptr;      // [I][C]
   const bf16* wo_t = nullptr;    // [C][I]
 };

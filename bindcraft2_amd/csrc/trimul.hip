@@ -225,8 +225,10 @@ constexpr int BM = 128;
 constexpr int CH = 64;                    // GEMM1 columns (= GEMM2 k) per chunk
 constexpr int NPG = 4 * I / CH;           // [proj|gate] chunks
 constexpr int NCHUNK = NPG + C / CH;      // + gating_linear chunks
-constexpr int LD1 = C + 8;                // B1 chunk: [CH][C] (n rows, k contiguous)
-constexpr int LD2 = CH + 8;               // B2 chunk: [C][CH] (c rows, k contiguous)
+// row strides = 8 (mod 64) dwords: the 16-byte fragment reads of 16 rows are
+// bank-conflict free
+constexpr int LD1 = C + 16;               // B1 chunk: [CH][C] (n rows, k contiguous)
+constexpr int LD2 = CH + 16;              // B2 chunk: [C][CH] (c rows, k contiguous)
 constexpr int B1E = CH * LD1, B2E = C * LD2;
 }  // namespace tail
 
@@ -242,10 +244,18 @@ __device__ __forceinline__ bf16x8 kslots(const bf16* T, long ld, long row, int k
   return r;
 }
 
+// The weights' k order in the tail kernel's copies: within each 32-block,
+// physical position 8g + e holds logical k = 4g + e (e < 4) and 8g + 4 + e
+// holds 16 + 4g + e, so kslots' 8 values are 16 contiguous bytes.
+inline int tail_kperm(int p) {
+  const int b = p & ~31, g = (p & 31) >> 3, e = p & 7;
+  return b + (e < 4 ? 4 * g + e : 16 + 4 * g + e - 4);
+}
+
 struct TailArgs {
   const bf16* xn;      // [M][C]
-  const bf16* wcat_t;  // [NC][C]
-  const bf16* wcat;    // [C][NC]
+  const bf16* wcat_t;  // [NC][C], k permuted (tail_kperm)
+  const bf16* wcat;    // [C][NC], k permuted (tail_kperm)
   const bf16 *dl, *dr; // [I][M]
   const bf16* dcg;     // [M][C]: d(cat)'s gating_linear columns
   const float *bp, *bg, *mask;
@@ -364,7 +374,7 @@ __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
       for (int ks = 0; ks < C / 32; ++ks) {
         bf16x8 bfr[4];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) bfr[t] = kslots(b1, LD1, t * 16 + l16, ks * 32, g);
+        for (int t = 0; t < 4; ++t) bfr[t] = ld8(b1 + (t * 16 + l16) * LD1 + ks * 32 + 8 * g);
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -407,7 +417,7 @@ __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
     for (int q = 0; q < 2; ++q) {
 #pragma unroll
       for (int j = 0; j < C / 16; ++j) {
-        const bf16x8 bfr = kslots(b2, LD2, j * 16 + l16, q * 32, g);
+        const bf16x8 bfr = ld8(b2 + (j * 16 + l16) * LD2 + q * 32 + 8 * g);
 #pragma unroll
         for (int i = 0; i < 2; ++i)
           acc2[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr, af[i][q], acc2[i][j], 0, 0, 0);
@@ -493,6 +503,17 @@ TriMulW trimul_weights(WeightStore& ws, const std::string& P) {
   w.wcat_t = ws.derived<bf16>("trimul.wcat_t:" + P, [&] {
     std::vector<float> c = cat();
     return transpose_bf16(c.data(), C, NC);
+  });
+  auto kperm_cols = [](std::vector<bf16> m, int rows, int cols) {
+    std::vector<bf16> o(m.size());
+    for (int r = 0; r < rows; ++r)
+      for (int p = 0; p < cols; ++p) o[(size_t)r * cols + p] = m[(size_t)r * cols + tail_kperm(p)];
+    return o;
+  };
+  w.wcat_k = ws.derived<bf16>("trimul.wcat_k:" + P, [&] { return kperm_cols(to_bf16(cat()), C, NC); });
+  w.wcat_tk = ws.derived<bf16>("trimul.wcat_tk:" + P, [&] {
+    std::vector<float> c = cat();
+    return kperm_cols(transpose_bf16(c.data(), C, NC), NC, C);
   });
   const HostTensor& ow = ws.host(P + "output_projection/weights");  // [I, C]
   w.wo = ws.derived<bf16>("trimul.wo:" + P, [&] { return to_bf16(ow.data); });
@@ -649,7 +670,7 @@ void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
   }
   if (fused) {
     TailArgs t;
-    t.xn = sv.xn; t.wcat_t = w.wcat_t; t.wcat = w.wcat;
+    t.xn = sv.xn; t.wcat_t = w.wcat_tk; t.wcat = w.wcat_k;
     t.dl = dL; t.dr = dR; t.dcg = dcat;
     t.bp = w.bp; t.bg = w.bg; t.mask = mask;
     t.x = pair_in; t.ln_g = w.ln_g; t.mean = sv.mean; t.rstd = sv.rstd; t.dres = dout;
