@@ -80,6 +80,16 @@ def _declare(L):
                                  + [vp] * 6),
         "bc2n_design_step_bwd": (i, [vp, vp, vp, vp, c.c_int64] + [vp] * 6 + [i, i]
                                  + [c.c_int64] * 5 + [cs] * 5 + [vp, vp]),
+        "bc2n_seqfeat_fwd": (i, [vp, vp, vp, vp, f, f, f, f, f, vp, i, vp, vp]),
+        "bc2n_seqfeat_bwd": (i, [vp, vp, vp, vp, vp, vp, f, f, f, f, f, vp, i, vp]),
+        "bc2n_design_inputs_fwd": (i, [vp, vp, vp, i, vp, vp, vp]),
+        "bc2n_design_inputs_bwd": (i, [vp, vp, vp, i, vp, vp]),
+        "bc2n_design_step_seq_save_bytes": (sz, [cs, cs, cs, cs, cs, i, c.c_int64, c.c_int64,
+                                                 c.c_int64, c.c_int64]),
+        "bc2n_design_step_seq_fwd": (i, [vp, vp, vp, vp, vp, f] + [vp] * 8 + [i]
+                                     + [c.c_int64] * 5 + [cs] * 5 + [vp] * 6),
+        "bc2n_design_step_seq_bwd": (i, [vp, vp, vp, vp, vp, f, vp, c.c_int64] + [vp] * 6 + [i]
+                                     + [c.c_int64] * 5 + [cs] * 5 + [vp]),
         "bc2n_structure_heads_save_bytes": (sz, [cs, i, c.c_int64]),
         "bc2n_structure_heads_fwd": (i, [vp, vp, vp, vp, vp, vp, i, i, c.c_int64, c.c_int64, cs,
                                          vp, vp, vp, vp, vp, vp]),

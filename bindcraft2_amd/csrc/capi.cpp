@@ -700,6 +700,109 @@ int bc2n_design_step_bwd(void* stream, const float* target_feat, const float* se
   });
 }
 
+int bc2n_seqfeat_fwd(void* stream, const float* logits, const uint8_t* flags, const float* aa_bias,
+                     float softmax_weight, float one_hot_weight, float temperature,
+                     float logit_scale, float omitted_half, const float* scalars, int N,
+                     float* feat, float* prof) {
+  return guarded([&] {
+    need(logits && flags && feat && prof, "null operand");
+    need(N > 0, "seqfeat: N must be positive");
+    need(scalars || temperature != 0.f, "seqfeat: temperature must be non-zero");
+    seqfeat_fwd(as_stream(stream), logits, flags, aa_bias,
+                SeqScalars{softmax_weight, one_hot_weight, temperature, logit_scale}, scalars,
+                omitted_half, N, feat, prof);
+  });
+}
+
+int bc2n_seqfeat_bwd(void* stream, const float* logits, const uint8_t* flags, const float* aa_bias,
+                     const float* d_feat, const float* d_prof, float softmax_weight,
+                     float one_hot_weight, float temperature, float logit_scale,
+                     float omitted_half, const float* scalars, int N, float* d_logits) {
+  return guarded([&] {
+    need(logits && flags && d_feat && d_prof && d_logits, "null operand");
+    need(N > 0, "seqfeat: N must be positive");
+    need(scalars || temperature != 0.f, "seqfeat: temperature must be non-zero");
+    seqfeat_bwd(as_stream(stream), logits, flags, aa_bias,
+                SeqScalars{softmax_weight, one_hot_weight, temperature, logit_scale}, scalars,
+                omitted_half, N, d_feat, d_prof, d_logits);
+  });
+}
+
+int bc2n_design_inputs_fwd(void* stream, const float* feat, const float* prof, int N,
+                           float* target_feat, float* msa_feat, float* aatype) {
+  return guarded([&] {
+    need(feat && prof && target_feat && msa_feat && aatype, "null operand");
+    need(N > 0, "design inputs: N must be positive");
+    design_inputs_fwd(as_stream(stream), feat, prof, N, target_feat, msa_feat, aatype);
+  });
+}
+
+int bc2n_design_inputs_bwd(void* stream, const float* d_target_feat, const float* d_msa_feat,
+                           int N, float* d_feat, float* d_prof) {
+  return guarded([&] {
+    need(d_target_feat && d_msa_feat && d_feat && d_prof, "null operand");
+    need(N > 0, "design inputs: N must be positive");
+    design_inputs_bwd(as_stream(stream), d_target_feat, d_msa_feat, N, d_feat, d_prof);
+  });
+}
+
+size_t bc2n_design_step_seq_save_bytes(const char* emb_dir, const char* tpl_dir,
+                                       const char* extra_dir, const char* main_dir,
+                                       const char* post_dir, int N, int64_t d_tpl,
+                                       int64_t d_extra, int64_t d_main, int64_t d_fold) {
+  size_t n = 0;
+  if (guarded([&] {
+        const DesignStepW& w =
+            ds_w(emb_dir, tpl_dir, extra_dir, main_dir, post_dir, d_tpl, d_extra, d_main, d_fold);
+        need(N > 0, "design step: bad shape");
+        n = design_step_seq_save_bytes(w, N);
+      }) != 0)
+    return 0;
+  return n;
+}
+
+int bc2n_design_step_seq_fwd(void* stream, const float* logits, const uint8_t* flags,
+                             const float* aa_bias, const float* scalars, float omitted_half,
+                             const float* residue_index, const float* asym_id,
+                             const float* entity_id, const float* sym_id, const int32_t* offset,
+                             const float* seq_mask, const float* act_const,
+                             const uint32_t* seeds, int N, int64_t d_tpl, int64_t d_extra,
+                             int64_t d_main, int64_t d_fold, int64_t dropout, const char* emb_dir,
+                             const char* tpl_dir, const char* extra_dir, const char* main_dir,
+                             const char* post_dir, float* atom14, float* distogram, float* pae,
+                             float* plddt, float* expres, void* save) {
+  return guarded([&] {
+    need(logits && flags && scalars && residue_index && asym_id && entity_id && sym_id &&
+             seq_mask && save, "null operand");
+    need(atom14 && distogram && pae && plddt && expres, "null output");
+    need(!dropout || seeds, "design step: dropout needs the seeds operand");
+    const DesignStepW& w =
+        ds_w(emb_dir, tpl_dir, extra_dir, main_dir, post_dir, d_tpl, d_extra, d_main, d_fold);
+    design_step_seq_fwd(as_stream(stream), w, N, logits, flags, aa_bias, scalars, omitted_half,
+                        residue_index, asym_id, entity_id, sym_id, offset, seq_mask, act_const,
+                        seeds, dropout != 0, atom14, distogram, pae, plddt, expres, save);
+  });
+}
+
+int bc2n_design_step_seq_bwd(void* stream, const float* logits, const uint8_t* flags,
+                             const float* aa_bias, const float* scalars, float omitted_half,
+                             const float* seq_mask, int64_t with_template,
+                             const float* d_atom14, const float* d_distogram, const float* d_pae,
+                             const float* d_plddt, const float* d_expres, void* save, int N,
+                             int64_t d_tpl, int64_t d_extra, int64_t d_main, int64_t d_fold,
+                             int64_t dropout, const char* emb_dir, const char* tpl_dir,
+                             const char* extra_dir, const char* main_dir, const char* post_dir,
+                             float* d_logits) {
+  return guarded([&] {
+    need(logits && flags && scalars && seq_mask && save && d_logits, "null operand");
+    const DesignStepW& w =
+        ds_w(emb_dir, tpl_dir, extra_dir, main_dir, post_dir, d_tpl, d_extra, d_main, d_fold);
+    design_step_seq_bwd(as_stream(stream), w, N, logits, flags, aa_bias, scalars, omitted_half,
+                        seq_mask, with_template != 0, dropout != 0, save, d_atom14, d_distogram,
+                        d_pae, d_plddt, d_expres, d_logits);
+  });
+}
+
 int bc2n_dropout_table(void* stream, float* tbl, int B, int C, uint32_t k0, uint32_t k1,
                        float rate) {
   return guarded([&] {

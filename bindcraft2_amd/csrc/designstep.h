@@ -4,6 +4,7 @@
 #pragma once
 #include "embed.h"
 #include "heads.h"
+#include "seqfeat.h"
 #include "tplembed.h"
 
 namespace bc2n {
@@ -32,5 +33,25 @@ void design_step_bwd(hipStream_t st, const DesignStepW& w, int N, int S, const f
                      bool dropout, void* save, const float* datom, const float* ddgram,
                      const float* dpae, const float* dplddt, const float* dexpres, float* dtf,
                      float* dmf);
+
+// The same step from the designed sequence logits [N][20] (one MSA row):
+// sequence features and profile (seqfeat.h) -> target_feat, msa_feat and
+// aatype -> the step above; the backward returns d logits.  `sc4` is the
+// device buffer of the four design scalars (softmax_weight, one_hot_weight,
+// temperature, logit_scale); `bias` [20] may be null.
+size_t design_step_seq_save_bytes(const DesignStepW& w, int N);
+void design_step_seq_fwd(hipStream_t st, const DesignStepW& w, int N, const float* logits,
+                         const uint8_t* flags, const float* bias, const float* sc4,
+                         float omitted_half, const float* ri, const float* ai, const float* ei,
+                         const float* si, const int32_t* offset, const float* seq_mask,
+                         const float* act_const, const uint32_t* seeds, bool dropout,
+                         float* atom14, float* dgram, float* pae, float* plddt, float* expres,
+                         void* save);
+void design_step_seq_bwd(hipStream_t st, const DesignStepW& w, int N, const float* logits,
+                         const uint8_t* flags, const float* bias, const float* sc4,
+                         float omitted_half, const float* seq_mask, bool with_template,
+                         bool dropout, void* save, const float* datom, const float* ddgram,
+                         const float* dpae, const float* dplddt, const float* dexpres,
+                         float* d_logits);
 
 }  // namespace bc2n

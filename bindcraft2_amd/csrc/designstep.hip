@@ -154,4 +154,69 @@ void design_step_bwd(hipStream_t st, const DesignStepW& w, int N, int S, const f
   embed_bwd(st, w.emb, N, S, sv.dmsa, sv.dpair, tf, dtf, dmf);
 }
 
+namespace {
+
+// The sequence front's buffers, carved ahead of the step's own save-set.
+template <class A>
+struct SeqExtra {
+  float *feat, *prof, *tf, *mf, *aatype, *dtf, *dmf, *dfeat, *dprof;
+  SeqExtra(A& c, int N) {
+    feat = c.template take<float>((size_t)N * SEQ_A);
+    prof = c.template take<float>((size_t)N * SEQ_A);
+    tf = c.template take<float>((size_t)N * (SEQ_A + 1));
+    mf = c.template take<float>((size_t)N * 49);
+    aatype = c.template take<float>(N);
+    dtf = c.template take<float>((size_t)N * (SEQ_A + 1));
+    dmf = c.template take<float>((size_t)N * 49);
+    dfeat = c.template take<float>((size_t)N * SEQ_A);
+    dprof = c.template take<float>((size_t)N * SEQ_A);
+  }
+};
+
+}  // namespace
+
+size_t design_step_seq_save_bytes(const DesignStepW& w, int N) {
+  Sizer s;
+  SeqExtra<Sizer> x(s, N);
+  (void)x;
+  return s.off + design_step_save_bytes(w, N, 1);
+}
+
+void design_step_seq_fwd(hipStream_t st, const DesignStepW& w, int N, const float* logits,
+                         const uint8_t* flags, const float* bias, const float* sc4,
+                         float omitted_half, const float* ri, const float* ai, const float* ei,
+                         const float* si, const int32_t* offset, const float* seq_mask,
+                         const float* act_const, const uint32_t* seeds, bool dropout,
+                         float* atom14, float* dgram, float* pae, float* plddt, float* expres,
+                         void* save) {
+  ds_check(w, N, 1);
+  nonnull(logits, "design step logits"); nonnull(flags, "design step flags");
+  nonnull(sc4, "design step scalars"); nonnull(save, "design step save");
+  Carver cv(save);
+  SeqExtra<Carver> x(cv, N);
+  seqfeat_fwd(st, logits, flags, bias, SeqScalars{}, sc4, omitted_half, N, x.feat, x.prof);
+  design_inputs_fwd(st, x.feat, x.prof, N, x.tf, x.mf, x.aatype);
+  design_step_fwd(st, w, N, 1, x.tf, x.mf, ri, ai, ei, si, offset, seq_mask, act_const, x.aatype,
+                  seeds, dropout, atom14, dgram, pae, plddt, expres, cv.p + cv.off);
+}
+
+void design_step_seq_bwd(hipStream_t st, const DesignStepW& w, int N, const float* logits,
+                         const uint8_t* flags, const float* bias, const float* sc4,
+                         float omitted_half, const float* seq_mask, bool with_template,
+                         bool dropout, void* save, const float* datom, const float* ddgram,
+                         const float* dpae, const float* dplddt, const float* dexpres,
+                         float* d_logits) {
+  ds_check(w, N, 1);
+  nonnull(logits, "design step logits"); nonnull(flags, "design step flags");
+  nonnull(sc4, "design step scalars"); nonnull(save, "design step save");
+  nonnull(d_logits, "design step d_logits");
+  Carver cv(save);
+  SeqExtra<Carver> x(cv, N);
+  design_step_bwd(st, w, N, 1, x.tf, seq_mask, with_template, x.aatype, dropout, cv.p + cv.off,
+                  datom, ddgram, dpae, dplddt, dexpres, x.dtf, x.dmf);
+  design_inputs_bwd(st, x.dtf, x.dmf, N, x.dfeat, x.dprof);
+  seqfeat_bwd(st, logits, flags, bias, SeqScalars{}, sc4, omitted_half, N, x.dfeat, x.dprof,
+              d_logits);
+}
+
 }  // namespace bc2n

@@ -505,6 +505,95 @@ class DesignStep:
         return dtf, dmf
 
 
+OMITTED_HALF = -5000.0  # half of BindCraft's omitted-acid logit (-1e4)
+
+
+class SeqFeat:
+    """Design sequence features (bc2n_seqfeat_*, the reference's GlueSeqFeat /
+    GlueSeqFeatBwd): logits [N, 20], flags u8 [N] (bit 0 = designed), bias [20]
+    or None; scalars = (softmax_weight, one_hot_weight, temperature,
+    logit_scale) as floats, or a device tensor [4] that overrides them."""
+
+    def __init__(self, scalars, aa_bias=None, omitted_half=OMITTED_HALF):
+        self.dev_scalars = scalars if torch.is_tensor(scalars) else None
+        self.vals = (1.0, 0.0, 1.0, 1.0) if self.dev_scalars is not None else \
+            tuple(float(x) for x in scalars)
+        self.bias, self.omitted = aa_bias, float(omitted_half)
+
+    def forward(self, logits, flags):
+        n = logits.shape[0]
+        feat, prof = torch.empty_like(logits), torch.empty_like(logits)
+        check(lib().bc2n_seqfeat_fwd(_stream(), _ptr(logits), _ptr(flags), _ptr(self.bias),
+                                     *self.vals, self.omitted, _ptr(self.dev_scalars), n,
+                                     _ptr(feat), _ptr(prof)))
+        return feat, prof
+
+    def backward(self, logits, flags, d_feat, d_prof):
+        n = logits.shape[0]
+        d = torch.empty_like(logits)
+        check(lib().bc2n_seqfeat_bwd(_stream(), _ptr(logits), _ptr(flags), _ptr(self.bias),
+                                     _ptr(d_feat), _ptr(d_prof), *self.vals, self.omitted,
+                                     _ptr(self.dev_scalars), n, _ptr(d)))
+        return d
+
+
+def design_inputs(feat, prof):
+    """(feat, prof) [N, 20] -> target_feat [N, 21], msa_feat [1, N, 49], aatype [N] (float)."""
+    n, dev = feat.shape[0], feat.device
+    tf = torch.empty(n, 21, dtype=torch.float32, device=dev)
+    mf = torch.empty(1, n, 49, dtype=torch.float32, device=dev)
+    aat = torch.empty(n, dtype=torch.float32, device=dev)
+    check(lib().bc2n_design_inputs_fwd(_stream(), _ptr(feat), _ptr(prof), n, _ptr(tf), _ptr(mf),
+                                       _ptr(aat)))
+    return tf, mf, aat
+
+
+def design_inputs_backward(d_target_feat, d_msa_feat):
+    n, dev = d_target_feat.shape[0], d_target_feat.device
+    d_feat = torch.empty(n, 20, dtype=torch.float32, device=dev)
+    d_prof = torch.empty(n, 20, dtype=torch.float32, device=dev)
+    check(lib().bc2n_design_inputs_bwd(_stream(), _ptr(d_target_feat), _ptr(d_msa_feat), n,
+                                       _ptr(d_feat), _ptr(d_prof)))
+    return d_feat, d_prof
+
+
+class DesignStepSeq(DesignStep):
+    """The one-call design step from the designed logits
+    (bc2n_design_step_seq_*): sequence features -> trunk inputs -> the step;
+    backward to d(logits).  scalars: device tensor [4] (softmax_weight,
+    one_hot_weight, temperature, logit_scale)."""
+
+    def save_bytes(self, n, s=1):
+        b = lib().bc2n_design_step_seq_save_bytes(*self.dirs, n, *self.depths)
+        if b == 0:
+            check(1)
+        return b
+
+    def forward(self, logits, flags, scalars, ids, seq_mask, aa_bias=None, act_const=None,
+                offset=None, seeds=None, dropout=True, save=None, omitted_half=OMITTED_HALF):
+        n, dev = logits.shape[0], logits.device
+        outs = tuple(torch.empty(*sh, dtype=torch.float32, device=dev)
+                     for sh in ((n, 14, 3), (n, n, 64), (n, n, 64), (n, 50), (n, 37)))
+        if save is None:
+            save = torch.empty(self.save_bytes(n), dtype=torch.uint8, device=dev)
+        check(lib().bc2n_design_step_seq_fwd(_stream(), _ptr(logits), _ptr(flags), _ptr(aa_bias),
+                                             _ptr(scalars), float(omitted_half), *map(_ptr, ids),
+                                             _ptr(offset), _ptr(seq_mask), _ptr(act_const),
+                                             _ptr(seeds), n, *self.depths, int(dropout),
+                                             *self.dirs, *map(_ptr, outs), _ptr(save)))
+        return outs, save
+
+    def backward(self, cts, logits, flags, scalars, seq_mask, save, aa_bias=None,
+                 with_template=True, dropout=True, omitted_half=OMITTED_HALF):
+        n = logits.shape[0]
+        d = torch.empty_like(logits)
+        check(lib().bc2n_design_step_seq_bwd(_stream(), _ptr(logits), _ptr(flags), _ptr(aa_bias),
+                                             _ptr(scalars), float(omitted_half), _ptr(seq_mask),
+                                             int(with_template), *map(_ptr, cts), _ptr(save), n,
+                                             *self.depths, int(dropout), *self.dirs, _ptr(d)))
+        return d
+
+
 def dropout_table(rows, channels, key, rate, device="cuda"):
     """[rows, channels] keep/keep_rate table from a JAX key (k0, k1)."""
     tbl = torch.empty(rows, channels, dtype=torch.float32, device=device)

@@ -374,6 +374,76 @@ int bc2n_design_step_bwd(void* stream, const float* target_feat, const float* se
                          float* d_msa_feat);
 
 /* ------------------------------------------------------------------------
+ * Design sequence features: replaces GlueSeqFeat / GlueSeqFeatBwd
+ * (native/ffi.cu:1105-1118 SeqFeatImpl, :1213-1227 GlueBwdImpl over
+ * native/seqfeat.cuh).  logits f32[N,20], flags u8[N] (bit 0 = designed),
+ * aa_bias f32[20] or NULL, the four design scalars (softmax_weight,
+ * one_hot_weight, temperature, logit_scale) as values or, when `scalars` is
+ * non-NULL, from that device buffer f32[4] in the same order; omitted_half =
+ * the logit at or below which an acid counts as omitted (-5000 in BindCraft)
+ *   -> feat, prof f32[N,20] (bindcraft/af2.py:99-104 over
+ *      bindcraft/sequence_optimization.py:33-52; the one-hot is
+ *      straight-through).
+ * bwd: d_feat, d_prof f32[N,20] -> d_logits f32[N,20].
+ * ---------------------------------------------------------------------- */
+int bc2n_seqfeat_fwd(void* stream, const float* logits, const uint8_t* flags, const float* aa_bias,
+                     float softmax_weight, float one_hot_weight, float temperature,
+                     float logit_scale, float omitted_half, const float* scalars, int N,
+                     float* feat, float* prof);
+int bc2n_seqfeat_bwd(void* stream, const float* logits, const uint8_t* flags, const float* aa_bias,
+                     const float* d_feat, const float* d_prof, float softmax_weight,
+                     float one_hot_weight, float temperature, float logit_scale,
+                     float omitted_half, const float* scalars, int N, float* d_logits);
+
+/* ------------------------------------------------------------------------
+ * The trunk inputs of the sequence features: the target_feat, msa_feat and
+ * aatype entries of alphafold_input_features (bindcraft/af2.py:187-192;
+ * native/inputfeat.cuh).  feat, prof f32[N,20] -> target_feat f32[N,21]
+ * (feat and a zero column), msa_feat f32[1,N,49] (feat in channels 0..19,
+ * prof in 25..44), aatype f32[N] = argmax(feat).  bwd: d_target_feat,
+ * d_msa_feat -> d_feat, d_prof.
+ * ---------------------------------------------------------------------- */
+int bc2n_design_inputs_fwd(void* stream, const float* feat, const float* prof, int N,
+                           float* target_feat, float* msa_feat, float* aatype);
+int bc2n_design_inputs_bwd(void* stream, const float* d_target_feat, const float* d_msa_feat,
+                           int N, float* d_feat, float* d_prof);
+
+/* ------------------------------------------------------------------------
+ * The one-call design step from the designed logits: the front of the
+ * reference's NativeDesignStep (native/design_step.cuh seqfeat -> inputfeat
+ * -> embed ..., native/ffi.cu:1691-2178) ahead of bc2n_design_step_fwd with
+ * one MSA row.  logits f32[N,20], flags u8[N], aa_bias f32[20] or NULL,
+ * scalars f32[4] on the device (softmax_weight, one_hot_weight, temperature,
+ * logit_scale), omitted_half; the rest as bc2n_design_step_fwd without
+ * target_feat, msa_feat, aatype (derived) and S (1).  bwd: the five
+ * cotangents -> d_logits f32[N,20].  save holds
+ * bc2n_design_step_seq_save_bytes() bytes.
+ * ---------------------------------------------------------------------- */
+size_t bc2n_design_step_seq_save_bytes(const char* emb_dir, const char* tpl_dir,
+                                       const char* extra_dir, const char* main_dir,
+                                       const char* post_dir, int N, int64_t d_tpl,
+                                       int64_t d_extra, int64_t d_main, int64_t d_fold);
+int bc2n_design_step_seq_fwd(void* stream, const float* logits, const uint8_t* flags,
+                             const float* aa_bias, const float* scalars, float omitted_half,
+                             const float* residue_index, const float* asym_id,
+                             const float* entity_id, const float* sym_id, const int32_t* offset,
+                             const float* seq_mask, const float* act_const,
+                             const uint32_t* seeds, int N, int64_t d_tpl, int64_t d_extra,
+                             int64_t d_main, int64_t d_fold, int64_t dropout, const char* emb_dir,
+                             const char* tpl_dir, const char* extra_dir, const char* main_dir,
+                             const char* post_dir, float* atom14, float* distogram, float* pae,
+                             float* plddt, float* expres, void* save);
+int bc2n_design_step_seq_bwd(void* stream, const float* logits, const uint8_t* flags,
+                             const float* aa_bias, const float* scalars, float omitted_half,
+                             const float* seq_mask, int64_t with_template,
+                             const float* d_atom14, const float* d_distogram, const float* d_pae,
+                             const float* d_plddt, const float* d_expres, void* save, int N,
+                             int64_t d_tpl, int64_t d_extra, int64_t d_main, int64_t d_fold,
+                             int64_t dropout, const char* emb_dir, const char* tpl_dir,
+                             const char* extra_dir, const char* main_dir, const char* post_dir,
+                             float* d_logits);
+
+/* ------------------------------------------------------------------------
  * Dropout with JAX's own bits.  tbl[b*C+c] = keep/keep_rate where
  * keep = jax.random.bernoulli(key, keep_rate, (B, C)), keep_rate =
  * float32(1) - float32(rate); key = (k0, k1) = jax.random.key_data(key).

@@ -645,3 +645,56 @@ def design_step(target_feat, msa_feat, ids, offset, seq_mask, act_const, aatype,
         single, pair = bf(single), bf(pair)
     return structure_heads(single, pair, seq_mask, aatype, prm["post"], depths["fold"], keys["fold"],
                            use_dropout, tables, dtype)
+
+
+# ---------------------------------------------------------------------------
+# The design sequence's features and the trunk inputs built from them.
+
+OMITTED_AMINO_ACID_LOGIT = -10000.0  # bindcraft/sequence_optimization.py:33
+
+
+def sequence_features(logits, flags, softmax_weight, one_hot_weight, temperature, logit_scale,
+                      bias=None):
+    """(features, profile) of the designed logits [N, 20]
+    (bindcraft/af2.py:99-104 prepare_design_sequence_features over
+    bindcraft/sequence_optimization.py:35-52): p = softmax(logits *
+    logit_scale / temperature + bias); f = sw p + (1 - sw) (logits, zero
+    where omitted); out = ohw onehot(argmax p) + (1 - ohw) f with the one-hot
+    straight-through (stop_gradient(onehot - p) + p); the profile is the same
+    with one_hot_weight = 1.  Residues without the DESIGN flag (bit 0) keep
+    their logits in both."""
+    def feats(ohw):
+        scaled = logits * logit_scale / temperature
+        p = torch.softmax(scaled if bias is None else scaled + bias, -1)
+        blended = torch.where(logits <= OMITTED_AMINO_ACID_LOGIT / 2, torch.zeros_like(logits),
+                              logits)
+        f = softmax_weight * p + (1 - softmax_weight) * blended
+        oh = torch.nn.functional.one_hot(p.argmax(-1), p.shape[-1]).to(p.dtype)
+        return ohw * ((oh - p).detach() + p) + (1 - ohw) * f
+
+    designed = torch.as_tensor((np.asarray(flags) & 1) != 0)[:, None]
+    return (torch.where(designed, feats(one_hot_weight), logits),
+            torch.where(designed, feats(1.0), logits))
+
+
+def design_inputs(feat, prof):
+    """target_feat [N, 21], msa_feat [1, N, 49] and aatype of the sequence
+    features (bindcraft/af2.py:187-192: target_feat = the features, msa_feat
+    channels 0..19 = features and 25..44 = profile, aatype = argmax; the
+    multimer embedder pads target_feat with one zero column,
+    modules_multimer.py:450)."""
+    n = feat.shape[0]
+    tf = torch.cat([feat, torch.zeros(n, 1, dtype=feat.dtype)], -1)
+    z = lambda k: torch.zeros(n, k, dtype=feat.dtype)
+    mf = torch.cat([feat, z(5), prof, z(4)], -1)[None]
+    return tf, mf, feat.detach().argmax(-1).numpy().astype(np.float32)
+
+
+def design_step_seq(logits, flags, scalars, ids, offset, seq_mask, act_const, emsa, prm, depths,
+                    keys, use_dropout, tables, bias=None, dtype=torch.float64, round_trunk=False):
+    """design_step from the designed logits: sequence_features ->
+    design_inputs -> design_step (one MSA row)."""
+    feat, prof = sequence_features(logits, flags, *scalars, bias=bias)
+    tf, mf, aatype = design_inputs(feat, prof)
+    return design_step(tf, mf, ids, offset, seq_mask, act_const, aatype, emsa, prm, depths, keys,
+                       use_dropout, tables, dtype=dtype, round_trunk=round_trunk)
