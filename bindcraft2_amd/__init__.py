@@ -90,6 +90,9 @@ def _declare(L):
                                      + [c.c_int64] * 5 + [cs] * 5 + [vp] * 6),
         "bc2n_design_step_seq_bwd": (i, [vp, vp, vp, vp, vp, f, vp, c.c_int64] + [vp] * 6 + [i]
                                      + [c.c_int64] * 5 + [cs] * 5 + [vp]),
+        "bc2n_confidence_save_bytes": (sz, [i]),
+        "bc2n_confidence_fwd": (i, [vp] * 6 + [i] + [vp] * 7),
+        "bc2n_confidence_bwd": (i, [vp] * 13 + [i, vp, vp, vp]),
         "bc2n_structure_heads_save_bytes": (sz, [cs, i, c.c_int64]),
         "bc2n_structure_heads_fwd": (i, [vp, vp, vp, vp, vp, vp, i, i, c.c_int64, c.c_int64, cs,
                                          vp, vp, vp, vp, vp, vp]),

@@ -8,6 +8,7 @@
 #include "embed.h"
 #include "heads.h"
 #include "designstep.h"
+#include "confidence.h"
 
 #include <map>
 #include <tuple>
@@ -800,6 +801,38 @@ int bc2n_design_step_seq_bwd(void* stream, const float* logits, const uint8_t* f
     design_step_seq_bwd(as_stream(stream), w, N, logits, flags, aa_bias, scalars, omitted_half,
                         seq_mask, with_template != 0, dropout != 0, save, d_atom14, d_distogram,
                         d_pae, d_plddt, d_expres, d_logits);
+  });
+}
+
+size_t bc2n_confidence_save_bytes(int N) { return N > 0 ? confidence_save_bytes(N) : 0; }
+
+int bc2n_confidence_fwd(void* stream, const float* plddt_logits, const float* pae_logits,
+                        const float* expres_logits, const float* seq_mask,
+                        const int32_t* interface_asym, int N, float* plddt, float* pae,
+                        float* ptm, float* iptm, float* iptm_per_residue, float* expres_ca,
+                        void* save) {
+  return guarded([&] {
+    need(plddt_logits && pae_logits && expres_logits && seq_mask && interface_asym && save,
+         "null operand");
+    need(plddt && pae && ptm && iptm && iptm_per_residue && expres_ca, "null output");
+    confidence_fwd(as_stream(stream), plddt_logits, pae_logits, expres_logits, seq_mask,
+                   interface_asym, N, plddt, pae, ptm, iptm, iptm_per_residue, expres_ca, save);
+  });
+}
+
+int bc2n_confidence_bwd(void* stream, const float* plddt_logits, const float* pae_logits,
+                        const float* expres_logits, const float* seq_mask,
+                        const int32_t* interface_asym, const void* save, const float* d_plddt,
+                        const float* d_pae, const float* d_ptm, const float* d_iptm,
+                        const float* d_iptm_per_residue, const float* d_expres_ca, int N,
+                        float* d_plddt_logits, float* d_pae_logits, float* d_expres_logits) {
+  return guarded([&] {
+    need(plddt_logits && pae_logits && expres_logits && seq_mask && interface_asym && save,
+         "null operand");
+    need(d_plddt_logits && d_pae_logits && d_expres_logits, "null output");
+    confidence_bwd(as_stream(stream), plddt_logits, pae_logits, expres_logits, seq_mask,
+                   interface_asym, N, save, d_plddt, d_pae, d_ptm, d_iptm, d_iptm_per_residue,
+                   d_expres_ca, d_plddt_logits, d_pae_logits, d_expres_logits);
   });
 }
 

@@ -594,6 +594,33 @@ class DesignStepSeq(DesignStep):
         return d
 
 
+class Confidence:
+    """pLDDT, symmetrised PAE, pTM, ipTM (+ per residue) and the CA
+    experimentally-resolved probability from the head logits
+    (bc2n_confidence_*)."""
+
+    def forward(self, plddt_logits, pae_logits, expres_logits, seq_mask, interface_asym):
+        n, dev = plddt_logits.shape[0], plddt_logits.device
+        e = lambda *sh: torch.empty(*sh, dtype=torch.float32, device=dev)
+        outs = (e(n), e(n, n), e(1), e(1), e(n), e(n))
+        save = torch.empty(lib().bc2n_confidence_save_bytes(n), dtype=torch.uint8, device=dev)
+        check(lib().bc2n_confidence_fwd(_stream(), _ptr(plddt_logits), _ptr(pae_logits),
+                                        _ptr(expres_logits), _ptr(seq_mask), _ptr(interface_asym),
+                                        n, *map(_ptr, outs), _ptr(save)))
+        return outs, save
+
+    def backward(self, cts, plddt_logits, pae_logits, expres_logits, seq_mask, interface_asym,
+                 save):
+        """cts = (d_plddt, d_pae, d_ptm, d_iptm, d_iptm_per_residue, d_expres_ca), any None"""
+        n = plddt_logits.shape[0]
+        d = (torch.empty_like(plddt_logits), torch.empty_like(pae_logits),
+             torch.empty_like(expres_logits))
+        check(lib().bc2n_confidence_bwd(_stream(), _ptr(plddt_logits), _ptr(pae_logits),
+                                        _ptr(expres_logits), _ptr(seq_mask), _ptr(interface_asym),
+                                        _ptr(save), *map(_ptr, cts), n, *map(_ptr, d)))
+        return d
+
+
 def dropout_table(rows, channels, key, rate, device="cuda"):
     """[rows, channels] keep/keep_rate table from a JAX key (k0, k1)."""
     tbl = torch.empty(rows, channels, dtype=torch.float32, device=device)

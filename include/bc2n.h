@@ -444,6 +444,33 @@ int bc2n_design_step_seq_bwd(void* stream, const float* logits, const uint8_t* f
                              float* d_logits);
 
 /* ------------------------------------------------------------------------
+ * Confidence metrics: replaces Confidence / ConfidenceBwd (native/ffi.cu:
+ * 1120-1159 ConfidenceImpl, :1227-1252 ConfBwdImpl over native/confidence.cuh).
+ * plddt_logits f32[N,50], pae_logits f32[N,N,64] (16-byte aligned),
+ * expres_logits f32[N,37] (the structure heads' outputs), seq_mask f32[N],
+ * interface_asym i32[N] -> plddt f32[N], pae f32[N,N] (symmetrised), ptm
+ * f32[1], iptm f32[1], iptm_per_residue f32[N], expres_ca f32[N]
+ * (bindcraft/af2.py:197-219 with AF2's predicted_tm_score; the bin tables,
+ * including d0 of the runtime residue weights, are built on the device).
+ * save holds bc2n_confidence_save_bytes(N) bytes, written by fwd, read by bwd.
+ * bwd: cotangents of the six outputs (any may be NULL; d_ptm and d_iptm are
+ * device scalars; pTM/ipTM route through their max to one row, as the
+ * reference's tmBwdK does) -> d_plddt_logits, d_pae_logits, d_expres_logits.
+ * ---------------------------------------------------------------------- */
+size_t bc2n_confidence_save_bytes(int N);
+int bc2n_confidence_fwd(void* stream, const float* plddt_logits, const float* pae_logits,
+                        const float* expres_logits, const float* seq_mask,
+                        const int32_t* interface_asym, int N, float* plddt, float* pae,
+                        float* ptm, float* iptm, float* iptm_per_residue, float* expres_ca,
+                        void* save);
+int bc2n_confidence_bwd(void* stream, const float* plddt_logits, const float* pae_logits,
+                        const float* expres_logits, const float* seq_mask,
+                        const int32_t* interface_asym, const void* save, const float* d_plddt,
+                        const float* d_pae, const float* d_ptm, const float* d_iptm,
+                        const float* d_iptm_per_residue, const float* d_expres_ca, int N,
+                        float* d_plddt_logits, float* d_pae_logits, float* d_expres_logits);
+
+/* ------------------------------------------------------------------------
  * Dropout with JAX's own bits.  tbl[b*C+c] = keep/keep_rate where
  * keep = jax.random.bernoulli(key, keep_rate, (B, C)), keep_rate =
  * float32(1) - float32(rate); key = (k0, k1) = jax.random.key_data(key).

@@ -698,3 +698,46 @@ def design_step_seq(logits, flags, scalars, ids, offset, seq_mask, act_const, em
     tf, mf, aatype = design_inputs(feat, prof)
     return design_step(tf, mf, ids, offset, seq_mask, act_const, aatype, emsa, prm, depths, keys,
                        use_dropout, tables, dtype=dtype, round_trunk=round_trunk)
+
+
+# ---------------------------------------------------------------------------
+# Confidence metrics of the head logits.
+
+def _tm_score(pae_logits, breaks, residue_weights, asym=None):
+    """AF2's predicted_tm_score with its per-alignment vector
+    (bindcraft/af/alphafold/common/confidence.py:113-176): d0 from the
+    clipped residue-weight sum, T = E_softmax[1 / (1 + c^2 / d0^2)], per
+    alignment the pair-weight-normalised sum, the score the weighted max."""
+    step = breaks[1] - breaks[0]
+    centres = torch.cat([breaks + step / 2, (breaks[-1:] + 1.5 * step)])
+    d0 = 1.24 * (torch.clamp(residue_weights.sum(), min=19) - 15) ** (1.0 / 3) - 1.8
+    probs = torch.softmax(pae_logits, -1)
+    term = (probs * (1.0 / (1 + centres ** 2 / d0 ** 2))).sum(-1)
+    n = residue_weights.shape[0]
+    mask = (torch.ones(n, n, dtype=torch.bool) if asym is None
+            else torch.as_tensor(asym)[:, None] != torch.as_tensor(asym)[None, :])
+    term = term * mask
+    w = mask * (residue_weights[None, :] * residue_weights[:, None])
+    per = (term * (w / (1e-8 + w.sum(-1, keepdim=True)))).sum(-1)
+    return (per * residue_weights).max(), per
+
+
+def confidence(plddt_logits, pae_logits, expres_logits, seq_mask, interface_asym):
+    """alphafold_prediction_metrics (bindcraft/af2.py:197-219): pLDDT from the
+    50 lddt bins, the PAE expectation symmetrised, pTM, ipTM and its
+    per-residue vector (residue_weights = seq_mask), sigmoid of the CA
+    experimentally-resolved logit.  The PAE head's breaks are
+    linspace(0, 31, 63)."""
+    dt = pae_logits.dtype
+    nb = plddt_logits.shape[-1]
+    bw = 1.0 / nb
+    centres_l = torch.arange(0.5 * bw, 1.0, bw, dtype=dt)[:nb]
+    plddt = (torch.softmax(plddt_logits, -1) * centres_l).sum(-1)
+    breaks = torch.linspace(0, 31, pae_logits.shape[-1] - 1, dtype=dt)
+    step = breaks[1] - breaks[0]
+    centres = torch.cat([breaks + step / 2, breaks[-1:] + 1.5 * step])
+    pae = (torch.softmax(pae_logits, -1) * centres).sum(-1)
+    pae = (pae + pae.T) / 2
+    ptm, _ = _tm_score(pae_logits, breaks, seq_mask)
+    iptm, iptm_pr = _tm_score(pae_logits, breaks, seq_mask, interface_asym)
+    return plddt, pae, ptm.reshape(1), iptm.reshape(1), iptm_pr, torch.sigmoid(expres_logits[:, 1])
