@@ -771,17 +771,24 @@ int bc2n_design_step_seq_fwd(void* stream, const float* logits, const uint8_t* f
                              int64_t d_main, int64_t d_fold, int64_t dropout, const char* emb_dir,
                              const char* tpl_dir, const char* extra_dir, const char* main_dir,
                              const char* post_dir, float* atom14, float* distogram, float* pae,
-                             float* plddt, float* expres, void* save) {
+                             float* plddt, float* expres, const int32_t* interface_asym,
+                             float* conf_plddt, float* conf_pae, float* ptm, float* iptm,
+                             float* iptm_per_residue, float* expres_ca, void* save) {
   return guarded([&] {
     need(logits && flags && scalars && residue_index && asym_id && entity_id && sym_id &&
              seq_mask && save, "null operand");
     need(atom14 && distogram && pae && plddt && expres, "null output");
     need(!dropout || seeds, "design step: dropout needs the seeds operand");
+    need(!conf_plddt || (interface_asym && conf_pae && ptm && iptm && iptm_per_residue && expres_ca),
+         "design step: the confidence outputs come together, with interface_asym");
     const DesignStepW& w =
         ds_w(emb_dir, tpl_dir, extra_dir, main_dir, post_dir, d_tpl, d_extra, d_main, d_fold);
     design_step_seq_fwd(as_stream(stream), w, N, logits, flags, aa_bias, scalars, omitted_half,
                         residue_index, asym_id, entity_id, sym_id, offset, seq_mask, act_const,
-                        seeds, dropout != 0, atom14, distogram, pae, plddt, expres, save);
+                        seeds, dropout != 0, atom14, distogram, pae, plddt, expres,
+                        ConfOut{interface_asym, conf_plddt, conf_pae, ptm, iptm, iptm_per_residue,
+                                expres_ca},
+                        save);
   });
 }
 
@@ -789,7 +796,11 @@ int bc2n_design_step_seq_bwd(void* stream, const float* logits, const uint8_t* f
                              const float* aa_bias, const float* scalars, float omitted_half,
                              const float* seq_mask, int64_t with_template,
                              const float* d_atom14, const float* d_distogram, const float* d_pae,
-                             const float* d_plddt, const float* d_expres, void* save, int N,
+                             const float* d_plddt, const float* d_expres,
+                             const int32_t* interface_asym, const float* d_conf_plddt,
+                             const float* d_conf_pae, const float* d_ptm, const float* d_iptm,
+                             const float* d_iptm_per_residue, const float* d_expres_ca, void* save,
+                             int N,
                              int64_t d_tpl, int64_t d_extra, int64_t d_main, int64_t d_fold,
                              int64_t dropout, const char* emb_dir, const char* tpl_dir,
                              const char* extra_dir, const char* main_dir, const char* post_dir,
@@ -800,7 +811,10 @@ int bc2n_design_step_seq_bwd(void* stream, const float* logits, const uint8_t* f
         ds_w(emb_dir, tpl_dir, extra_dir, main_dir, post_dir, d_tpl, d_extra, d_main, d_fold);
     design_step_seq_bwd(as_stream(stream), w, N, logits, flags, aa_bias, scalars, omitted_half,
                         seq_mask, with_template != 0, dropout != 0, save, d_atom14, d_distogram,
-                        d_pae, d_plddt, d_expres, d_logits);
+                        d_pae, d_plddt, d_expres,
+                        ConfCt{interface_asym, d_conf_plddt, d_conf_pae, d_ptm, d_iptm,
+                               d_iptm_per_residue, d_expres_ca},
+                        d_logits);
   });
 }
 

@@ -4,6 +4,7 @@
 #pragma once
 #include "embed.h"
 #include "heads.h"
+#include "confidence.h"
 #include "seqfeat.h"
 #include "tplembed.h"
 
@@ -39,6 +40,19 @@ void design_step_bwd(hipStream_t st, const DesignStepW& w, int N, int S, const f
 // aatype -> the step above; the backward returns d logits.  `sc4` is the
 // device buffer of the four design scalars (softmax_weight, one_hot_weight,
 // temperature, logit_scale); `bias` [20] may be null.
+// The confidence metrics of the step's head logits (confidence.h), computed
+// when `plddt` is set; their cotangents join the logits' in the backward.
+struct ConfOut {
+  const int32_t* asym = nullptr;  // interface chain ids [N]
+  float *plddt = nullptr, *pae = nullptr, *ptm = nullptr, *iptm = nullptr, *iptm_pr = nullptr,
+        *expres_ca = nullptr;
+};
+struct ConfCt {
+  const int32_t* asym = nullptr;
+  const float *plddt = nullptr, *pae = nullptr, *ptm = nullptr, *iptm = nullptr,
+              *iptm_pr = nullptr, *expres_ca = nullptr;
+  bool any() const { return plddt || pae || ptm || iptm || iptm_pr || expres_ca; }
+};
 size_t design_step_seq_save_bytes(const DesignStepW& w, int N);
 void design_step_seq_fwd(hipStream_t st, const DesignStepW& w, int N, const float* logits,
                          const uint8_t* flags, const float* bias, const float* sc4,
@@ -46,12 +60,12 @@ void design_step_seq_fwd(hipStream_t st, const DesignStepW& w, int N, const floa
                          const float* si, const int32_t* offset, const float* seq_mask,
                          const float* act_const, const uint32_t* seeds, bool dropout,
                          float* atom14, float* dgram, float* pae, float* plddt, float* expres,
-                         void* save);
+                         const ConfOut& conf, void* save);
 void design_step_seq_bwd(hipStream_t st, const DesignStepW& w, int N, const float* logits,
                          const uint8_t* flags, const float* bias, const float* sc4,
                          float omitted_half, const float* seq_mask, bool with_template,
                          bool dropout, void* save, const float* datom, const float* ddgram,
                          const float* dpae, const float* dplddt, const float* dexpres,
-                         float* d_logits);
+                         const ConfCt& conf, float* d_logits);
 
 }  // namespace bc2n

@@ -170,8 +170,27 @@ struct SeqExtra {
     dmf = c.template take<float>((size_t)N * 49);
     dfeat = c.template take<float>((size_t)N * SEQ_A);
     dprof = c.template take<float>((size_t)N * SEQ_A);
+    conf = c.template take<char>(confidence_save_bytes(N));
+    dl = c.template take<float>((size_t)N * CONF_LBINS);
+    dp = c.template take<float>((size_t)N * N * CONF_PBINS);
+    de = c.template take<float>((size_t)N * CONF_EXPRES);
+    ll = c.template take<float>((size_t)N * CONF_LBINS);
+    pl = c.template take<float>((size_t)N * N * CONF_PBINS);
+    el = c.template take<float>((size_t)N * CONF_EXPRES);
   }
+  char* conf;
+  float *dl, *dp, *de;  // head-logit cotangents with the confidence terms added
+  float *ll, *pl, *el;  // the head logits the confidence metrics were computed from
 };
+
+// y += a + b, either may be null (zero)
+__global__ void add_opt_kernel(const float* a, const float* b, long n, float* y) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] += (a ? a[i] : 0.f) + (b ? b[i] : 0.f);  // y already holds one term
+}
+void add_into(hipStream_t st, const float* a, const float* b, long n, float* y) {
+  hipLaunchKernelGGL(add_opt_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a, b, n, y);
+}
 
 }  // namespace
 
@@ -188,7 +207,7 @@ void design_step_seq_fwd(hipStream_t st, const DesignStepW& w, int N, const floa
                          const float* si, const int32_t* offset, const float* seq_mask,
                          const float* act_const, const uint32_t* seeds, bool dropout,
                          float* atom14, float* dgram, float* pae, float* plddt, float* expres,
-                         void* save) {
+                         const ConfOut& conf, void* save) {
   ds_check(w, N, 1);
   nonnull(logits, "design step logits"); nonnull(flags, "design step flags");
   nonnull(sc4, "design step scalars"); nonnull(save, "design step save");
@@ -198,6 +217,15 @@ void design_step_seq_fwd(hipStream_t st, const DesignStepW& w, int N, const floa
   design_inputs_fwd(st, x.feat, x.prof, N, x.tf, x.mf, x.aatype);
   design_step_fwd(st, w, N, 1, x.tf, x.mf, ri, ai, ei, si, offset, seq_mask, act_const, x.aatype,
                   seeds, dropout, atom14, dgram, pae, plddt, expres, cv.p + cv.off);
+  if (conf.plddt) {
+    nonnull(conf.asym, "design step interface asym");
+    confidence_fwd(st, plddt, pae, expres, seq_mask, conf.asym, N, conf.plddt, conf.pae, conf.ptm,
+                   conf.iptm, conf.iptm_pr, conf.expres_ca, x.conf);
+    // the backward reads the logits from the save buffer, not the caller's outputs
+    BC2N_HIP(hipMemcpyAsync(x.ll, plddt, (size_t)N * CONF_LBINS * 4, hipMemcpyDeviceToDevice, st));
+    BC2N_HIP(hipMemcpyAsync(x.pl, pae, (size_t)N * N * CONF_PBINS * 4, hipMemcpyDeviceToDevice, st));
+    BC2N_HIP(hipMemcpyAsync(x.el, expres, (size_t)N * CONF_EXPRES * 4, hipMemcpyDeviceToDevice, st));
+  }
 }
 
 void design_step_seq_bwd(hipStream_t st, const DesignStepW& w, int N, const float* logits,
@@ -205,13 +233,25 @@ void design_step_seq_bwd(hipStream_t st, const DesignStepW& w, int N, const floa
                          float omitted_half, const float* seq_mask, bool with_template,
                          bool dropout, void* save, const float* datom, const float* ddgram,
                          const float* dpae, const float* dplddt, const float* dexpres,
-                         float* d_logits) {
+                         const ConfCt& conf, float* d_logits) {
   ds_check(w, N, 1);
   nonnull(logits, "design step logits"); nonnull(flags, "design step flags");
   nonnull(sc4, "design step scalars"); nonnull(save, "design step save");
   nonnull(d_logits, "design step d_logits");
   Carver cv(save);
   SeqExtra<Carver> x(cv, N);
+  if (conf.any()) {
+    // the confidence metrics' backward over the logits the forward kept (confidence requested there)
+    nonnull(conf.asym, "design step interface asym");
+    confidence_bwd(st, x.ll, x.pl, x.el, seq_mask, conf.asym, N, x.conf, conf.plddt,
+                   conf.pae, conf.ptm, conf.iptm, conf.iptm_pr, conf.expres_ca, x.dl, x.dp, x.de);
+    add_into(st, dplddt, nullptr, (long)N * CONF_LBINS, x.dl);
+    add_into(st, dpae, nullptr, (long)N * N * CONF_PBINS, x.dp);
+    add_into(st, dexpres, nullptr, (long)N * CONF_EXPRES, x.de);
+    dplddt = x.dl;
+    dpae = x.dp;
+    dexpres = x.de;
+  }
   design_step_bwd(st, w, N, 1, x.tf, seq_mask, with_template, x.aatype, dropout, cv.p + cv.off,
                   datom, ddgram, dpae, dplddt, dexpres, x.dtf, x.dmf);
   design_inputs_bwd(st, x.dtf, x.dmf, N, x.dfeat, x.dprof);

@@ -570,27 +570,38 @@ class DesignStepSeq(DesignStep):
         return b
 
     def forward(self, logits, flags, scalars, ids, seq_mask, aa_bias=None, act_const=None,
-                offset=None, seeds=None, dropout=True, save=None, omitted_half=OMITTED_HALF):
+                offset=None, seeds=None, dropout=True, save=None, omitted_half=OMITTED_HALF,
+                interface_asym=None):
+        """-> ((atom14, distogram, pae, plddt, expres), save), plus the confidence
+        metrics (plddt, pae, ptm, iptm, iptm_per_residue, expres_ca) as a third
+        element when interface_asym (i32 [N]) is given."""
         n, dev = logits.shape[0], logits.device
-        outs = tuple(torch.empty(*sh, dtype=torch.float32, device=dev)
-                     for sh in ((n, 14, 3), (n, n, 64), (n, n, 64), (n, 50), (n, 37)))
+        e = lambda *sh: torch.empty(*sh, dtype=torch.float32, device=dev)
+        outs = (e(n, 14, 3), e(n, n, 64), e(n, n, 64), e(n, 50), e(n, 37))
+        conf = (e(n), e(n, n), e(1), e(1), e(n), e(n)) if interface_asym is not None else (None,) * 6
         if save is None:
             save = torch.empty(self.save_bytes(n), dtype=torch.uint8, device=dev)
         check(lib().bc2n_design_step_seq_fwd(_stream(), _ptr(logits), _ptr(flags), _ptr(aa_bias),
                                              _ptr(scalars), float(omitted_half), *map(_ptr, ids),
                                              _ptr(offset), _ptr(seq_mask), _ptr(act_const),
                                              _ptr(seeds), n, *self.depths, int(dropout),
-                                             *self.dirs, *map(_ptr, outs), _ptr(save)))
-        return outs, save
+                                             *self.dirs, *map(_ptr, outs), _ptr(interface_asym),
+                                             *map(_ptr, conf), _ptr(save)))
+        if interface_asym is None:
+            return outs, save
+        return outs, save, conf
 
     def backward(self, cts, logits, flags, scalars, seq_mask, save, aa_bias=None,
-                 with_template=True, dropout=True, omitted_half=OMITTED_HALF):
+                 with_template=True, dropout=True, omitted_half=OMITTED_HALF,
+                 interface_asym=None, conf_cts=(None,) * 6):
         n = logits.shape[0]
         d = torch.empty_like(logits)
         check(lib().bc2n_design_step_seq_bwd(_stream(), _ptr(logits), _ptr(flags), _ptr(aa_bias),
                                              _ptr(scalars), float(omitted_half), _ptr(seq_mask),
-                                             int(with_template), *map(_ptr, cts), _ptr(save), n,
-                                             *self.depths, int(dropout), *self.dirs, _ptr(d)))
+                                             int(with_template), *map(_ptr, cts),
+                                             _ptr(interface_asym), *map(_ptr, conf_cts),
+                                             _ptr(save), n, *self.depths, int(dropout),
+                                             *self.dirs, _ptr(d)))
         return d
 
 

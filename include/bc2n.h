@@ -415,9 +415,13 @@ int bc2n_design_inputs_bwd(void* stream, const float* d_target_feat, const float
  * one MSA row.  logits f32[N,20], flags u8[N], aa_bias f32[20] or NULL,
  * scalars f32[4] on the device (softmax_weight, one_hot_weight, temperature,
  * logit_scale), omitted_half; the rest as bc2n_design_step_fwd without
- * target_feat, msa_feat, aatype (derived) and S (1).  bwd: the five
- * cotangents -> d_logits f32[N,20].  save holds
- * bc2n_design_step_seq_save_bytes() bytes.
+ * target_feat, msa_feat, aatype (derived) and S (1).  When conf_plddt is
+ * non-NULL the step also returns the confidence metrics of its head logits
+ * (as bc2n_confidence_fwd: plddt, pae f32[N,N], ptm, iptm, iptm_per_residue,
+ * expres_ca; interface_asym i32[N]), the reference step's Outputs.  bwd: the
+ * five head cotangents and those of the confidence metrics (any may be NULL;
+ * the latter need a forward that computed them) -> d_logits f32[N,20].  save
+ * holds bc2n_design_step_seq_save_bytes() bytes.
  * ---------------------------------------------------------------------- */
 size_t bc2n_design_step_seq_save_bytes(const char* emb_dir, const char* tpl_dir,
                                        const char* extra_dir, const char* main_dir,
@@ -432,12 +436,18 @@ int bc2n_design_step_seq_fwd(void* stream, const float* logits, const uint8_t* f
                              int64_t d_main, int64_t d_fold, int64_t dropout, const char* emb_dir,
                              const char* tpl_dir, const char* extra_dir, const char* main_dir,
                              const char* post_dir, float* atom14, float* distogram, float* pae,
-                             float* plddt, float* expres, void* save);
+                             float* plddt, float* expres, const int32_t* interface_asym,
+                             float* conf_plddt, float* conf_pae, float* ptm, float* iptm,
+                             float* iptm_per_residue, float* expres_ca, void* save);
 int bc2n_design_step_seq_bwd(void* stream, const float* logits, const uint8_t* flags,
                              const float* aa_bias, const float* scalars, float omitted_half,
                              const float* seq_mask, int64_t with_template,
                              const float* d_atom14, const float* d_distogram, const float* d_pae,
-                             const float* d_plddt, const float* d_expres, void* save, int N,
+                             const float* d_plddt, const float* d_expres,
+                             const int32_t* interface_asym, const float* d_conf_plddt,
+                             const float* d_conf_pae, const float* d_ptm, const float* d_iptm,
+                             const float* d_iptm_per_residue, const float* d_expres_ca, void* save,
+                             int N,
                              int64_t d_tpl, int64_t d_extra, int64_t d_main, int64_t d_fold,
                              int64_t dropout, const char* emb_dir, const char* tpl_dir,
                              const char* extra_dir, const char* main_dir, const char* post_dir,

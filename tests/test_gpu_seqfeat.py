@@ -114,8 +114,10 @@ def test_design_step_seq_parity(cuda, with_template, dropout):
     keys = {k: J.prng_key(400 + i) for i, k in enumerate(("tpl", "extra", "main", "fold"))}
     seeds = torch.tensor([[int(keys[k][0]), int(keys[k][1]), 1]
                           for k in ("tpl", "extra", "main", "fold")], dtype=torch.int64)
-    shapes = ((n, 14, 3), (n, n, 64), (n, n, 64), (n, 50), (n, 37))
+    shapes = ((n, 14, 3), (n, n, 64), (n, n, 64), (n, 50), (n, 37),
+              (n,), (n, n), (1,), (1,), (n,), (n,))  # + the confidence metrics
     cts = [rng.standard_normal(sh).astype(np.float32) for sh in shapes]
+    iasym = ids[1].astype(np.int32)
 
     def oracle(round_trunk, grads=True):
         t = torch.tensor(x, dtype=D, requires_grad=True)
@@ -124,6 +126,8 @@ def test_design_step_seq_parity(cuda, with_template, dropout):
                                   torch.as_tensor(emsa, dtype=D), prm, depths,
                                   keys if dropout else {k: None for k in keys}, dropout, tables,
                                   bias=torch.tensor(bias, dtype=D), round_trunk=round_trunk)
+        ref = list(ref) + list(af2.confidence(ref[3], ref[2], ref[4],
+                                              torch.as_tensor(seq_mask, dtype=D), iasym))
         if not grads:
             return [r.detach() for r in ref]
         loss = sum((r * torch.as_tensor(c, dtype=D)).sum() for r, c in zip(ref, cts))
@@ -139,22 +143,28 @@ def test_design_step_seq_parity(cuda, with_template, dropout):
     step = ops.DesignStepSeq(*dirs, depths=(depths["tpl"], depths["extra"], depths["main"],
                                             depths["fold"]))
     sc = torch.tensor(scalars, dtype=torch.float32, device=cuda)
-    outs, save = step.forward(T(x), T(flags), sc, [T(v) for v in ids], T(seq_mask),
-                              aa_bias=T(bias), act_const=T(act_const),
-                              seeds=seeds.to(torch.uint32).to(cuda), dropout=dropout)
-    dlog = step.backward([T(c) for c in cts], T(x), T(flags), sc, T(seq_mask), save,
-                         aa_bias=T(bias), with_template=with_template, dropout=dropout)
+    outs, save, conf = step.forward(T(x), T(flags), sc, [T(v) for v in ids], T(seq_mask),
+                                    aa_bias=T(bias), act_const=T(act_const),
+                                    seeds=seeds.to(torch.uint32).to(cuda), dropout=dropout,
+                                    interface_asym=T(iasym))
+    dlog = step.backward([T(c) for c in cts[:5]], T(x), T(flags), sc, T(seq_mask), save,
+                         aa_bias=T(bias), with_template=with_template, dropout=dropout,
+                         interface_asym=T(iasym), conf_cts=[T(c) for c in cts[5:]])
     torch.cuda.synchronize()
 
     ref, probe = oracle(False), oracle(True)
-    names = ("atom14", "distogram", "pae", "plddt", "expres", "d logits")
-    for i, (name, g, r, p) in enumerate(zip(names, list(outs) + [dlog], ref, probe)):
+    names = ("atom14", "distogram", "pae", "plddt", "expres", "conf plddt", "conf pae", "ptm",
+             "iptm", "iptm_per_residue", "expres_ca", "d logits")
+    last = len(names) - 1
+    for i, (name, g, r, p) in enumerate(zip(names, list(outs) + list(conf) + [dlog], ref, probe)):
         m, c = metrics(g.cpu().double(), r), metrics(p, r)
         tol = max(2e-2, 4 * c["rel_l2"], 4 * c["max_rel"])
-        base = (0.998 if with_template else 0.999) if i == 5 else 0.9999
-        cos = min(base, 1 - (6 if i == 5 else 4) * (1 - c["cos"]))
+        base = (0.998 if with_template else 0.999) if i == last else 0.9999
+        cos = min(base, 1 - (6 if i == last else 4) * (1 - c["cos"]))
         print(f"  {name}", m, "| probe", {k: round(v, 6) for k, v in c.items()})
-        if i < 5:
+        if i in (7, 8):  # scalars: relative error only
+            assert m["rel_l2"] <= tol, name
+        elif i < last:
             assert m["rel_l2"] <= tol and m["max_rel"] <= tol and m["cos"] >= cos, name
         else:
             assert m["cos"] >= cos, name
