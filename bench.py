@@ -512,9 +512,10 @@ def main():
                            "head_dim": 32, "masked_residues": 0.1, "flops_per_step": flops}}
         cpu = None if args.no_cpu_baseline else cpu_triattn_baseline(n)
     elif args.workload == "design":
-        # the one-call design step: embedder, template embedding (2 blocks),
-        # extra stack (4, pair only), main stack (48), structure module (8
-        # iterations) and heads, forward + backward to the input features
+        # the one-call design step from the designed logits: sequence features,
+        # embedder, template embedding (2 blocks), extra stack (4, pair only),
+        # main stack (48), structure module (8 iterations), heads and the
+        # confidence metrics, forward + backward to the logits
         from bindcraft2_amd import weights as W
         tree = W.init_af2_params(rng, num_blocks=48, extra_blocks=4, template_blocks=2)
         root = tempfile.mkdtemp(prefix="bc2n_bench_ds_")
@@ -524,33 +525,41 @@ def main():
                 W.stack_weights_from_params(tree, os.path.join(root, "extra"), prefix=W.EXTRA),
                 W.stack_weights_from_params(tree, os.path.join(root, "main"), prefix=W.MAIN),
                 W.post_weights_from_params(tree, os.path.join(root, "post"), tables=tables)]
-        step_mod = ops.DesignStep(*dirs, depths=(2, 4, 48, 8))
-        tf = torch.zeros(n, 21, device=dev)
-        tf[:, :20] = torch.softmax(torch.randn(n, 20, device=dev), -1)
-        mf = torch.randn(1, n, 49, device=dev)
+        step_mod = ops.DesignStepSeq(*dirs, depths=(2, 4, 48, 8))
+        logits = 0.5 * torch.randn(n, 20, device=dev)
+        flags = torch.zeros(n, dtype=torch.uint8, device=dev)
+        flags[160:] = 1  # the 64-residue binder is designed; the target passes through
+        logits[:160] = torch.nn.functional.one_hot(torch.randint(0, 20, (160,), device=dev),
+                                                   20).float()
+        scalars = torch.tensor([1.0, 0.0, 1.0, 1.0], device=dev)  # the soft stage
         ids = [torch.arange(n, dtype=torch.float32, device=dev),
                (torch.arange(n, device=dev) >= 160).float() + 1,
                (torch.arange(n, device=dev) >= 160).float() + 1, torch.ones(n, device=dev)]
+        iasym = (torch.arange(n, device=dev) >= 160).int()
         seqm = torch.as_tensor(m1, device=dev)
         act_const = 0.1 * torch.randn(n, n, 64, device=dev)
-        aat = torch.randint(0, 20, (n,), device=dev).float()
         seeds = torch.tensor([[0, 11 + i, 1] for i in range(4)], dtype=torch.int64).to(
             torch.uint32).to(dev)
-        save = torch.empty(step_mod.save_bytes(n, 1), dtype=torch.uint8, device=dev)
+        save = torch.empty(step_mod.save_bytes(n), dtype=torch.uint8, device=dev)
         cts = [torch.randn(*sh, device=dev) for sh in ((n, 14, 3), (n, n, 64), (n, n, 64),
                                                       (n, 50), (n, 37))]
+        conf_cts = [torch.randn(*sh, device=dev) for sh in ((n,), (n, n), (1,), (1,), (n,), (n,))]
 
         def step():
-            step_mod.forward(tf, mf, ids, seqm, aat, act_const=act_const, seeds=seeds, save=save)
-            step_mod.backward(cts, tf, seqm, aat, save)
+            step_mod.forward(logits, flags, scalars, ids, seqm, act_const=act_const, seeds=seeds,
+                             save=save, interface_asym=iasym)
+            step_mod.backward(cts, logits, flags, scalars, seqm, save, interface_asym=iasym,
+                              conf_cts=conf_cts)
 
         ms = timed(step, args.steps, args.warmup)
         prof = profiled(step, args.steps, args.no_kprof)
-        line = {"metric": "ms per one-call design step (embedder + template + 4 extra + 48 "
-                          "Evoformer + 8-iteration structure module + heads, fwd+bwd)",
+        line = {"metric": "ms per one-call design step (sequence features + embedder + template "
+                          "+ 4 extra + 48 Evoformer + 8-iteration structure module + heads + "
+                          "confidence, fwd+bwd)",
                 "value": round(ms, 2), "unit": "ms", "higher_is_better": False,
-                "config": {"workload": "one-call design step at L=224 (160 + 64), features in, "
-                                       "structure-module outputs out, dropout on",
+                "config": {"workload": "one-call design step at L=224 (160 target + 64 designed), "
+                                       "logits in, structure and confidence outputs out, d logits "
+                                       "back, dropout on",
                            "L": n, "n_seq": 1, "depths": [2, 4, 48, 8]},
                 "save_set_gb": round(save.numel() / 1e9, 2)}
         cpu = None
