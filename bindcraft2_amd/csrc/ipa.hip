@@ -690,6 +690,15 @@ static void launch_logits(hipStream_t st, const float* qpk, const float* kpk, co
 }
 
 // ------------------------------------------------------------------ forward
+
+// rigid frames [N][12] (rotation row-major, then translation) set to the identity
+__global__ void ident_frames_kernel(float* __restrict__ r, int N) {
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= N * 12) return;
+  const int k = e % 12;
+  r[e] = (k == 0 || k == 4 || k == 8) ? 1.f : 0.f;
+}
+
 void fold_fwd(hipStream_t st, const FoldW& w, int N, int depth, const float* single,
               const float* pair, const float* mask, const uint32_t* key, const uint32_t* enabled,
               bool dropout, float* act_out, float* traj, void* save) {
@@ -735,11 +744,8 @@ void fold_fwd(hipStream_t st, const FoldW& w, int N, int depth, const float* sin
     b.c_sm = 1; b.c_sn = M2;
     b.bias = w.b2d;
     gemm_f32(st, b, "fold.gemm_b2d");
-    // identity frames
-    std::vector<float> ident((size_t)N * 12, 0.f);
-    for (int n = 0; n < N; ++n) ident[n * 12] = ident[n * 12 + 4] = ident[n * 12 + 8] = 1.f;
-    BC2N_HIP(hipMemcpyAsync(rigA, ident.data(), ident.size() * 4, hipMemcpyHostToDevice, st));
-    BC2N_HIP(hipStreamSynchronize(st));  // `ident` is pageable host memory
+    // identity frames, written on the device (no host copy, no stream sync)
+    hipLaunchKernelGGL(ident_frames_kernel, dim3((N * 12 + 255) / 256), dim3(256), 0, st, rigA, N);
   }
   const int NJ = (N + 63) / 64;
   for (int it = 0; it < depth; ++it) {
