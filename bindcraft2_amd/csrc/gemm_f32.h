@@ -42,7 +42,7 @@ struct GemmF32 {
 };
 
 namespace gf32 {
-constexpr int BM = 64, BN = 64, BK = 16, LDS_LD = BM + 4;
+constexpr int BM = 64, BN = 64, BK = 32, LDS_LD = BM + 4;
 }
 
 // internal linkage: the header is included by several translation units
@@ -72,24 +72,49 @@ static __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmF32 g) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int k0 = kbeg; k0 < kend; k0 += BK) {
+  // The next K step's elements are loaded into registers while the current
+  // step multiplies out of LDS, so a step waits for memory only once.
+  constexpr int NA = (BM * BK) / 256, NB = (BN * BK) / 256;
+  float ra[NA], rb[NB];
+  auto gload = [&](int k0) {
 #pragma unroll
-    for (int i = 0; i < (BM * BK) / 256; ++i) {
+    for (int i = 0; i < NA; ++i) {
       const int e = tid + 256 * i;
       int m, k;
       if (a_kfast) { k = e % BK; m = e / BK; } else { m = e % BM; k = e / BM; }
       const int gm = m0 + m, gk = k0 + k;
-      As[k][m] = (gm < g.M && gk < kend) ? A[gm * g.a_sm + gk * g.a_sk] : 0.f;
+      ra[i] = (gm < g.M && gk < kend) ? A[gm * g.a_sm + gk * g.a_sk] : 0.f;
     }
 #pragma unroll
-    for (int i = 0; i < (BN * BK) / 256; ++i) {
+    for (int i = 0; i < NB; ++i) {
       const int e = tid + 256 * i;
       int n, k;
       if (b_nfast) { n = e % BN; k = e / BN; } else { k = e % BK; n = e / BK; }
       const int gn = n0 + n, gk = k0 + k;
-      Bs[k][n] = (gn < g.N && gk < kend) ? B[gk * g.b_sk + gn * g.b_sn] : 0.f;
+      rb[i] = (gn < g.N && gk < kend) ? B[gk * g.b_sk + gn * g.b_sn] : 0.f;
     }
+  };
+  auto sstore = [&]() {
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const int e = tid + 256 * i;
+      int m, k;
+      if (a_kfast) { k = e % BK; m = e / BK; } else { m = e % BM; k = e / BM; }
+      As[k][m] = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int e = tid + 256 * i;
+      int n, k;
+      if (b_nfast) { n = e % BN; k = e / BN; } else { k = e % BK; n = e / BK; }
+      Bs[k][n] = rb[i];
+    }
+  };
+  if (kbeg < kend) gload(kbeg);
+  for (int k0 = kbeg; k0 < kend; k0 += BK) {
+    sstore();
     __syncthreads();
+    if (k0 + BK < kend) gload(k0 + BK);
 #pragma unroll
     for (int kk = 0; kk < BK; kk += 4) {
       const int kr = kk + (lane >> 4);
