@@ -252,14 +252,9 @@ void stack_fwd(hipStream_t st, const StackW& w, int N, int S, int depth, const f
     const int pm_evo[4] = {K_TMO, K_TMI, K_TAS, K_TAE};
     const int pm_tpl[4] = {T_TMO, T_TMI, T_TAS, T_TAE};
     const int* pm = L.tpl ? pm_tpl : pm_evo;
-    for (int b = 0; b < depth; ++b) {
-      float* tb = tbl + b * L.tbl_per_block;
-      if (!L.pair_only)
-        dropout_table_dev(st, tb, N, L.Cm, keys + (b * nk + K_ROW) * 2, enabled, 1.0f - 0.15f);
-      for (int k = 0; k < 4; ++k)
-        dropout_table_dev(st, tb + (size_t)N * L.Cm + (size_t)k * N * L.Cz, N, L.Cz,
-                          keys + (b * nk + pm[k]) * 2, enabled, 1.0f - 0.25f);
-    }
+    const int pk[4] = {pm[0], pm[1], pm[2], pm[3]};
+    stack_dropout_tables(st, tbl, (long)L.tbl_per_block, N, L.Cm, L.Cz, depth, nk, !L.pair_only,
+                         K_ROW, pk, keys, enabled);
     t.base = tbl;
   }
   if (!L.pair_only)

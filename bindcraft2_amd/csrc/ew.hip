@@ -26,6 +26,52 @@ void dropout_table_dev(hipStream_t st, float* tbl, int B, int C,
                      tbl, B, C, key, enabled, keep_rate);
 }
 
+// Every dropout table of a stack in one launch: per block, the MSA row
+// attention's [N][Cm] table (when msa_row) and the four pair modules' [N][Cz]
+// tables, at the same offsets and from the same keys as one
+// dropout_table_dev call each.
+__global__ void stack_dropout_tables_kernel(float* __restrict__ tbl, long per_block, int N, int Cm,
+                                            int Cz, int depth, int nk, int msa_row, int row_key,
+                                            int4 pair_keys, const uint32_t* __restrict__ keys,
+                                            const uint32_t* __restrict__ enabled) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long row_n = msa_row ? (long)N * Cm : 0, pn = (long)N * Cz;
+  const long per = row_n + 4 * pn;
+  if (i >= per * depth) return;
+  const int b = (int)(i / per);
+  long r = i % per, off, e;
+  int kidx;
+  float keep;
+  if (r < row_n) {
+    kidx = row_key;
+    e = off = r;
+    keep = 1.0f - 0.15f;
+  } else {
+    r -= row_n;
+    const int k = (int)(r / pn);
+    e = r % pn;
+    kidx = k == 0 ? pair_keys.x : k == 1 ? pair_keys.y : k == 2 ? pair_keys.z : pair_keys.w;
+    off = (long)N * Cm + k * pn + e;
+    keep = 1.0f - 0.25f;
+  }
+  float* dst = tbl + b * per_block + off;
+  const bool on = enabled == nullptr || enabled[0] != 0u;
+  if (!on) { *dst = 1.f; return; }
+  const uint32_t* key = keys + ((long)b * nk + kidx) * 2;
+  const float u = jax_uniform01(key[0], key[1], (uint64_t)e);
+  *dst = (u < keep) ? 1.f / keep : 0.f;
+}
+
+void stack_dropout_tables(hipStream_t st, float* tbl, long per_block, int N, int Cm, int Cz,
+                          int depth, int nk, bool msa_row, int row_key, const int (&pair_keys)[4],
+                          const uint32_t* keys, const uint32_t* enabled) {
+  const long n = ((msa_row ? (long)N * Cm : 0) + 4L * N * Cz) * depth;
+  hipLaunchKernelGGL(stack_dropout_tables_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     st, tbl, per_block, N, Cm, Cz, depth, nk, msa_row ? 1 : 0, row_key,
+                     make_int4(pair_keys[0], pair_keys[1], pair_keys[2], pair_keys[3]), keys,
+                     enabled);
+}
+
 __global__ void dropout_table_host_key_kernel(float* __restrict__ tbl, int B, int C,
                                               uint32_t k0, uint32_t k1, float keep_rate) {
   const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;

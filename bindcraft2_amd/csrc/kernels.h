@@ -94,6 +94,10 @@ void dropout_table(hipStream_t st, float* tbl, int B, int C, uint32_t k0,
 // memory; a disabled flag gives an all-ones table (rate 0).
 void dropout_table_dev(hipStream_t st, float* tbl, int B, int C,
                        const uint32_t* key, const uint32_t* enabled, float keep_rate);
+// All of a stack's dropout tables in one launch (see ew.hip).
+void stack_dropout_tables(hipStream_t st, float* tbl, long per_block, int N, int Cm, int Cz,
+                          int depth, int nk, bool msa_row, int row_key, const int (&pair_keys)[4],
+                          const uint32_t* keys, const uint32_t* enabled);
 // out[i] = jax.random.bernoulli(key, keep_rate, (n,))[i].
 void bernoulli_bits(hipStream_t st, uint8_t* out, long n, uint32_t k0, uint32_t k1,
                     float keep_rate);
