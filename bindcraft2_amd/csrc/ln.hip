@@ -200,9 +200,10 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(
   }
 }
 
-// Channel-major input: x is [C][M] (one plane per channel).  A block of 64
-// rows stages the [C][64] tile through LDS (float4 loads along m) and then
-// normalises it 4 lanes per row; the output is row-major [M][C] bf16.
+// Channel-major input: x is [C][M] (one plane per channel).  A block of
+// LNCM_R rows stages the [C][LNCM_R] tile through LDS (4-wide loads along m)
+// and then normalises it 256/LNCM_R lanes per row; the output is row-major
+// [M][C] bf16.
 // Requires M % 4 == 0.
 // 4 consecutive m of channel plane c (x is [C][M], float or bf16)
 __device__ __forceinline__ float4 cm_load4(const float* x, long idx) {
@@ -213,12 +214,15 @@ __device__ __forceinline__ float4 cm_load4(const bf16* x, long idx) {
   return make_float4((float)v[0], (float)v[1], (float)v[2], (float)v[3]);
 }
 
+// Rows per workgroup of the channel-major kernels (256 threads, 256/R lanes a row).
+constexpr int LNCM_R = 32;
+
 template <int C, bool FAST, class InT>
 __global__ __launch_bounds__(256) void ln_fwd_cm_kernel(
     const InT* __restrict__ x, long M, const float* __restrict__ gamma,
     const float* __restrict__ beta, bf16* __restrict__ y,
     float* __restrict__ mean_out, float* __restrict__ rstd_out) {
-  constexpr int R = 64;
+  constexpr int R = LNCM_R;
   __shared__ float tile[R][C + 1];
   const int t = threadIdx.x;
   const long m0 = (long)blockIdx.x * R;
@@ -233,8 +237,8 @@ __global__ __launch_bounds__(256) void ln_fwd_cm_kernel(
     tile[q + 3][c] = v.w;
   }
   __syncthreads();
-  constexpr int CPL = C / 4;
-  const int r = t / 4, part = t % 4;
+  constexpr int P = 256 / R, CPL = C / P;  // lanes and channels per row
+  const int r = t / P, part = t % P;
   const long m = m0 + r;
   float v[CPL];
   float s = 0.f, s2 = 0.f;
@@ -244,16 +248,16 @@ __global__ __launch_bounds__(256) void ln_fwd_cm_kernel(
     s += v[e];
     s2 += v[e] * v[e];
   }
-  s = group_sum<4>(s);
+  s = group_sum<P>(s);
   const float mu = s / C;
   float var;
   if (FAST) {
-    var = group_sum<4>(s2) / C - mu * mu;
+    var = group_sum<P>(s2) / C - mu * mu;
   } else {
     float d2 = 0.f;
 #pragma unroll
     for (int e = 0; e < CPL; ++e) { const float d = v[e] - mu; d2 += d * d; }
-    var = group_sum<4>(d2) / C;
+    var = group_sum<P>(d2) / C;
   }
   const float rs = rsqrtf(var + LN_EPS);
   if (m < M) {
@@ -278,7 +282,7 @@ __global__ __launch_bounds__(256) void ln_bwd_cm_kernel(
     const float* __restrict__ dy, const InT* __restrict__ x, long M,
     const float* __restrict__ gamma, const float* __restrict__ mean,
     const float* __restrict__ rstd, bf16* __restrict__ dx) {
-  constexpr int R = 64;
+  constexpr int R = LNCM_R;
   __shared__ float tile[R][C + 1];
   const int t = threadIdx.x;
   const long m0 = (long)blockIdx.x * R;
@@ -293,8 +297,8 @@ __global__ __launch_bounds__(256) void ln_bwd_cm_kernel(
     tile[q + 3][c] = v.w;
   }
   __syncthreads();
-  constexpr int CPL = C / 4;
-  const int r = t / 4, part = t % 4;
+  constexpr int P = 256 / R, CPL = C / P;  // lanes and channels per row
+  const int r = t / P, part = t % P;
   const long m = m0 + r;
   const bool live = m < M;
   const float mu = live ? mean[m] : 0.f, rs = live ? rstd[m] : 0.f;
@@ -314,8 +318,8 @@ __global__ __launch_bounds__(256) void ln_bwd_cm_kernel(
       sgx += g[e] * xh[e];
     }
   }
-  sg = group_sum<4>(sg) / C;
-  sgx = group_sum<4>(sgx) / C;
+  sg = group_sum<P>(sg) / C;
+  sgx = group_sum<P>(sgx) / C;
   __syncthreads();
 #pragma unroll
   for (int e = 0; e < CPL; ++e) {
@@ -425,7 +429,7 @@ template <class InT>
 static void ln_fwd_cm_t(hipStream_t st, const InT* x, long M, int C, const float* gamma,
                         const float* beta, bf16* y, float* mean, float* rstd, bool fast) {
   if (M % 4 != 0) throw std::runtime_error("ln_fwd_cm: M must be a multiple of 4");
-  const int grid = (int)((M + 63) / 64);
+  const int grid = (int)((M + LNCM_R - 1) / LNCM_R);
 #define BC2N_LNCM(CV, FV) \
   hipLaunchKernelGGL((ln_fwd_cm_kernel<CV, FV, InT>), dim3(grid), dim3(256), 0, st, x, M, gamma, beta, y, mean, rstd)
   if (C == 128) {
@@ -450,7 +454,7 @@ template <class InT>
 static void ln_bwd_cm_t(hipStream_t st, const float* dy, const InT* x, long M, int C,
                         const float* gamma, const float* mean, const float* rstd, bf16* dx) {
   if (M % 4 != 0) throw std::runtime_error("ln_bwd_cm: M must be a multiple of 4");
-  const int grid = (int)((M + 63) / 64);
+  const int grid = (int)((M + LNCM_R - 1) / LNCM_R);
   if (C == 128) hipLaunchKernelGGL((ln_bwd_cm_kernel<128, InT>), dim3(grid), dim3(256), 0, st, dy, x, M, gamma, mean, rstd, dx);
   else if (C == 64) hipLaunchKernelGGL((ln_bwd_cm_kernel<64, InT>), dim3(grid), dim3(256), 0, st, dy, x, M, gamma, mean, rstd, dx);
   else throw std::runtime_error("ln_bwd_cm: unsupported channel count");
