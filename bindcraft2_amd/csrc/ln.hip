@@ -216,6 +216,7 @@ __device__ __forceinline__ float4 cm_load4(const bf16* x, long idx) {
 
 // Rows per workgroup of the channel-major kernels (256 threads, 256/R lanes a row).
 constexpr int LNCM_R = 32;
+static_assert(64 / (256 / LNCM_R) >= 8, "the 64-channel kernels store 8 channels a lane");
 
 template <int C, bool FAST, class InT>
 __global__ __launch_bounds__(256) void ln_fwd_cm_kernel(
