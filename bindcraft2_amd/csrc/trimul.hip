@@ -349,6 +349,7 @@ __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
   stash(0, 0);
   __syncthreads();
 
+  float4 xpre[2][C / 16];
   f32x4 acc2[2][C / 16];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -412,6 +413,15 @@ __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
     // the next chunk's operands load behind GEMM2 (the weights are
     // L2-resident: every workgroup reads the same 288 KB)
     if (s + 1 < NCHUNK) prefetch(s + 1);
+    if (s == NPG) {
+      // the LayerNorm tail's x rows, loaded behind the last two chunks (GEMM1
+      // is done, so its operand registers are free)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < C / 16; ++j)
+          xpre[i][j] = *reinterpret_cast<const float4*>(a.x + (m0 + i * 16 + l16) * C + 16 * j + 4 * g);
+    }
     // GEMM2: dy[m][c] += d(cat)[m][k] Wcat[c][k] over the chunk's 64 k
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
@@ -437,7 +447,7 @@ __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
 #pragma unroll
     for (int j = 0; j < C / 16; ++j) {
       const int c = 16 * j + 4 * g;
-      const float4 xv = *reinterpret_cast<const float4*>(a.x + m * C + c);
+      const float4 xv = xpre[i][j];
       const float4 gm = *reinterpret_cast<const float4*>(a.ln_g + c);
       const float xa[4] = {xv.x, xv.y, xv.z, xv.w}, ga[4] = {gm.x, gm.y, gm.z, gm.w};
 #pragma unroll
