@@ -1039,8 +1039,17 @@ __global__ void attn_dbias_reduce_kernel(const float* __restrict__ part, int nch
                                          long n, float* __restrict__ out) {
   const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
+  // eight partials loaded at a time (in flight together), added in chunk order
   float s = 0.f;
-  for (int c = 0; c < nch; ++c) s += part[(long)c * n + i];
+  int c = 0;
+  for (; c + 8 <= nch; c += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = part[(long)(c + u) * n + i];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s += v[u];
+  }
+  for (; c < nch; ++c) s += part[(long)c * n + i];
   out[i] = s;
 }
 
