@@ -120,8 +120,17 @@ __global__ void opm_reduce_kernel(const float* __restrict__ part, int nch, long 
                                   int O, bool left, bf16* __restrict__ dlr) {
   const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (long)rows * cols) return;
+  // eight partials loaded at a time (in flight together), added in chunk order
   float s = 0.f;
-  for (int c = 0; c < nch; ++c) s += part[(long)c * chunk_stride + idx];
+  int ch = 0;
+  for (; ch + 8 <= nch; ch += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = part[(long)(ch + u) * chunk_stride + idx];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s += v[u];
+  }
+  for (; ch < nch; ++ch) s += part[(long)ch * chunk_stride + idx];
   const int row = (int)(idx / cols), col = (int)(idx % cols);
   int sr, r, c;
   if (left) { r = row; sr = col / O; c = col % O; }
