@@ -358,10 +358,19 @@ void gemm(hipStream_t st, const GemmArgs& g, const Epi& epi, const char* name = 
   // buffers (40 KB), so four workgroups share a CU and hide each other's
   // load latency; longer K keeps 64-deep steps (fewer barriers)
   const bool k64 = (g.K % 64 == 0) && g.K > 128;
+  // A grid of a few tiles (the MSA's S x N-row products) runs one chain of
+  // K steps per workgroup, each waiting for its loads: 128-deep steps halve
+  // the chain (the operand tiles fit one buffer of 68 KB).
+  const bool k128 = (g.K % 128 == 0) && g.K >= 256 && (long)tiles * g.batch * 8 <= device_cus();
   KTimed kt(name, st);
 #define BC2N_GEMM_LAUNCH(BKV, AKV, BKCV) \
   hipLaunchKernelGGL((gemm_kernel<BM, BN, BKV, AKV, BKCV, Epi, AL>), grid, block, 0, st, g, epi, al)
-  if (k64) {
+  if (k128) {
+    if (ak && bk) BC2N_GEMM_LAUNCH(128, true, true);
+    else if (ak) BC2N_GEMM_LAUNCH(128, true, false);
+    else if (bk) BC2N_GEMM_LAUNCH(128, false, true);
+    else BC2N_GEMM_LAUNCH(128, false, false);
+  } else if (k64) {
     if (ak && bk) BC2N_GEMM_LAUNCH(64, true, true);
     else if (ak) BC2N_GEMM_LAUNCH(64, true, false);
     else if (bk) BC2N_GEMM_LAUNCH(64, false, true);
