@@ -592,20 +592,9 @@ def main():
                            "mask": "all ones", "flops_per_step": flops}}
         cpu = None
     else:
-        # weights: 48 Evoformer blocks, 4 pair-only extra blocks, 2 template blocks
-        evo = {}
-        for blk in range(48):
-            evo.update(bparams.init_block_params(blk, rng, gates="zero"))
-        extra = {}
-        for blk in range(4):
-            extra.update(bparams.init_block_params(
-                blk, rng, gates="zero",
-                modules=["outer_product_mean", "triangle_multiplication_outgoing",
-                         "triangle_multiplication_incoming", "triangle_attention_starting_node",
-                         "triangle_attention_ending_node", "pair_transition"]))
-        tpl = {}
-        for blk in range(2):
-            tpl.update(bparams.init_template_block_params(blk, rng, gates="zero"))
+        # weights: 48 Evoformer blocks, 4 pair-only extra blocks, 2 template
+        # blocks (the same draws tests/test_gpu_trunk_full.py checks)
+        evo, extra, tpl = bparams.init_trunk_params(rng)
         root = tempfile.mkdtemp(prefix="bc2n_bench_")
         d_evo = bparams.write_manifest(os.path.join(root, "evo"), evo)
         d_extra = bparams.write_manifest(os.path.join(root, "extra"), extra)

@@ -13,6 +13,8 @@ namespace bc2n {
 typedef __bf16 bf16;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16;
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -54,6 +56,13 @@ __device__ __forceinline__ long xcd_block(long G) {
 // is applied identically to both operands yields the exact product.
 __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+// The same product, same lane layout and rate, with IEEE binary16 operands:
+// the 16-bit words of a and b hold halfs (11-bit significands, against
+// bf16's 8), for products whose operands have a bounded range.
+__device__ __forceinline__ f32x4 mfma16x16x32_f16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
 // DPP lane moves (gfx9 encodings): a VALU operand read from another lane of

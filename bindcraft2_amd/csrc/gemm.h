@@ -12,6 +12,11 @@
 // 64-deep steps into the one buffer after a barrier, so that either way the
 // operand buffers take at most 40 KB and four workgroups share a CU.
 //
+// With F16 the operand words are IEEE binary16 instead (the 16-bit words of
+// A and B hold halfs; v_mfma_f32_16x16x32_f16, same rate): for products of
+// bounded operands (LayerNorm outputs and weights) that need the 3 extra
+// significand bits.
+//
 // Epilogue: the f32 accumulator tile is staged through LDS (reusing the
 // operand buffers, half a tile per pass) and handed to the epilogue as
 // vectors of 8, either 8 consecutive columns of one row (`row`, the default)
@@ -29,6 +34,7 @@ namespace bc2n {
 
 struct GemmArgs {
   int M = 0, N = 0, K = 0, batch = 1;
+  // 16-bit operand words: bf16, or binary16 when the launch says F16
   const bf16* A = nullptr;
   long a_sm = 0, a_sk = 0, a_sb = 0;  // element strides; a_sm==1 or a_sk==1
   const bf16* B = nullptr;
@@ -57,18 +63,33 @@ __device__ __forceinline__ void st_b8f(bf16* p, const float (&v)[8]) {
   for (int e = 0; e < 8; ++e) a[e] = (bf16)v[e];
   st8(p, a);
 }
+__device__ __forceinline__ void ld_h8f(const f16* p, float (&v)[8]) {
+  const f16x8 a = __builtin_bit_cast(f16x8, ld8(reinterpret_cast<const bf16*>(p)));
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = (float)a[e];
+}
+__device__ __forceinline__ void st_h8f(f16* p, const float (&v)[8]) {
+  f16x8 a;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) a[e] = (f16)v[e];
+  st8(reinterpret_cast<bf16*>(p), __builtin_bit_cast(bf16x8, a));
+}
 template <class T>
 __device__ __forceinline__ void st_any8(T* p, const float (&v)[8]);
 template <>
 __device__ __forceinline__ void st_any8<float>(float* p, const float (&v)[8]) { st_f8(p, v); }
 template <>
 __device__ __forceinline__ void st_any8<bf16>(bf16* p, const float (&v)[8]) { st_b8f(p, v); }
+template <>
+__device__ __forceinline__ void st_any8<f16>(f16* p, const float (&v)[8]) { st_h8f(p, v); }
 template <class T>
 __device__ __forceinline__ void ld_any8(const T* p, float (&v)[8]);
 template <>
 __device__ __forceinline__ void ld_any8<float>(const float* p, float (&v)[8]) { ld_f8(p, v); }
 template <>
 __device__ __forceinline__ void ld_any8<bf16>(const bf16* p, float (&v)[8]) { ld_b8f(p, v); }
+template <>
+__device__ __forceinline__ void ld_any8<f16>(const f16* p, float (&v)[8]) { ld_h8f(p, v); }
 
 // An epilogue with kTwoPhase = true runs both modes on a column-mode tile:
 // first `col` (which may rewrite the staged tile through its pointer), then,
@@ -144,7 +165,8 @@ struct GemmSmem {
   static constexpr int BYTES = AB > T ? AB : T;
 };
 
-template <int BM, int BN, int BK, bool AK, bool BKC, class Epi, class AL = ALoadDirect>
+template <int BM, int BN, int BK, bool AK, bool BKC, class Epi, class AL = ALoadDirect,
+          bool F16 = false>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi, AL al = AL{}) {
   using SM = GemmSmem<BM, BN, BK>;
   constexpr int WM = BM / 2, WN = BN / 2;
@@ -261,7 +283,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi, AL al = 
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma16x16x32(af[i], bfr[j], acc[i][j]);
+        for (int j = 0; j < TN; ++j) {
+          if constexpr (F16) acc[i][j] = mfma16x16x32_f16(af[i], bfr[j], acc[i][j]);
+          else acc[i][j] = mfma16x16x32(af[i], bfr[j], acc[i][j]);
+        }
     }
     if constexpr (SM::NBUF == 2) {
       if (kt + 1 < nk) sstore(buf ^ 1);
@@ -330,8 +355,9 @@ inline void gemm_check(bool ok, const char* what) {
 // Launch with tile BM x BN; picks the loader form from the strides and BK
 // from K.  Shapes are validated here, on the host, before any launch.  With a
 // loader other than ALoadDirect, A is K-contiguous by construction (g.A is
-// not read; a_sk must be 1).
-template <int BM, int BN, class Epi, class AL = ALoadDirect>
+// not read; a_sk must be 1).  F16: the operand words are binary16 (the A
+// loader, if any, must produce binary16 words too).
+template <int BM, int BN, bool F16 = false, class Epi, class AL = ALoadDirect>
 void gemm(hipStream_t st, const GemmArgs& g, const Epi& epi, const char* name = "gemm",
           const AL& al = AL{}) {
   if constexpr (!AL::kDirect) gemm_check(g.a_sk == 1, "A loader: K-contiguous A");
@@ -364,7 +390,7 @@ void gemm(hipStream_t st, const GemmArgs& g, const Epi& epi, const char* name = 
   const bool k128 = (g.K % 128 == 0) && g.K >= 256 && (long)tiles * g.batch * 8 <= device_cus();
   KTimed kt(name, st);
 #define BC2N_GEMM_LAUNCH(BKV, AKV, BKCV) \
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, BKV, AKV, BKCV, Epi, AL>), grid, block, 0, st, g, epi, al)
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, BKV, AKV, BKCV, Epi, AL, F16>), grid, block, 0, st, g, epi, al)
   if (k128) {
     if (ak && bk) BC2N_GEMM_LAUNCH(128, true, true);
     else if (ak) BC2N_GEMM_LAUNCH(128, true, false);
@@ -509,19 +535,21 @@ struct EpiGateBwd : EpiRows {
   }
 };
 
-// dH = acc * (H > 0): backward through a ReLU of the kept (bf16) tensor H.
-template <class OutT = bf16>
+// dH = acc * (H > 0): backward through a ReLU of the kept tensor H (bf16
+// or binary16).
+template <class OutT = bf16, class HT = bf16>
 struct EpiReluMask : EpiRows {
   OutT* C;
-  const bf16* H;
+  const HT* H;
   long ldc;
-  EpiReluMask(OutT* c, const bf16* h, long l) : C(c), H(h), ldc(l) {}
+  EpiReluMask(OutT* c, const HT* h, long l) : C(c), H(h), ldc(l) {}
   __device__ __forceinline__ void row(int, int m, int n, const float (&v)[8]) const {
     const long o = (long)m * ldc + n;
-    const bf16x8 h = ld8(H + o);
+    float h[8];
+    ld_any8<HT>(H + o, h);
     float x[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = (float)h[e] > 0.f ? v[e] : 0.f;
+    for (int e = 0; e < 8; ++e) x[e] = h[e] > 0.f ? v[e] : 0.f;
     st_any8<OutT>(C + o, x);
   }
 };

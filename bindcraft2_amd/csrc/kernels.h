@@ -8,10 +8,11 @@ namespace bc2n {
 // ---------------------------------------------------------------- LayerNorm
 // y[m] = LN(x[src(m)]) with src(m) = m, or (q*nt+p) for m = p*nt+q when nt>0.
 // When H>0, bias_out[h*M+m] = bias_scale * sum_c LN(x)[m][c] * wb[c*H+h].
+// y_f16: y holds binary16 words instead of bf16 (H = 0, two-pass only).
 void ln_fwd_f32(hipStream_t st, const float* x, long M, int C, int nt,
                 const float* gamma, const float* beta, bf16* y, float* mean,
                 float* rstd, bool fast, int H, const float* wb, float* bias_out,
-                float bias_scale = 1.f);
+                float bias_scale = 1.f, bool y_f16 = false);
 // dx[src(m)] (+)= LN-backward(dy[m] + sum_h dbias[h*M+m] * wb[c*H+h]).
 // acc: dx = res + LN'(...) with res = dres, or dx itself when dres is null.
 void ln_bwd_f32(hipStream_t st, const float* dy, const float* x, long M, int C,

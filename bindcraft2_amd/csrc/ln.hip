@@ -56,7 +56,8 @@ __device__ __forceinline__ void load_w(const float* __restrict__ wb, int c0, flo
 // A lane group handles U rows (RPB apart): all U rows are loaded before the
 // first is reduced, and gamma, beta and the projection slice are read once
 // per U rows.
-template <int C, bool FAST, class InT, int H, int U>
+// YF16: y holds binary16 words instead of bf16.
+template <int C, bool FAST, class InT, int H, int U, bool YF16 = false>
 __global__ __launch_bounds__(256) void ln_fwd_kernel(
     const InT* __restrict__ x, long M, int nt, const float* __restrict__ gamma,
     const float* __restrict__ beta, bf16* __restrict__ y,
@@ -101,11 +102,14 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(
     const float r = rsqrtf(var + LN_EPS);
     float o[8];
     bf16x8 ob;
+    f16x8 oh;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       o[e] = (v[u][e] - mu) * r * gm[e] + bt[e];
-      ob[e] = (bf16)o[e];
+      if constexpr (YF16) oh[e] = (f16)o[e];
+      else ob[e] = (bf16)o[e];
     }
+    if constexpr (YF16) ob = __builtin_bit_cast(bf16x8, oh);
     if (y) st8(y + m * C + c0, ob);
     if (gl == 0) {
       if (mean_out) mean_out[m] = mu;
@@ -353,9 +357,19 @@ constexpr int ln_rows() { return H > 0 ? 4 : 1; }
 template <int C, int H>
 static void ln_fwd_launch(hipStream_t st, const float* x, long M, int nt, const float* gamma,
                           const float* beta, bf16* y, float* mean, float* rstd, bool fast,
-                          const float* wb, float* bias_out, float bs) {
+                          const float* wb, float* bias_out, float bs, bool yf16) {
   constexpr int U = ln_rows<H>();
   const int grid = (int)((M + U * LnGeom<C>::RPB - 1) / (U * LnGeom<C>::RPB));
+  if (yf16) {
+    if constexpr (H == 0) {
+      if (fast) throw std::runtime_error("ln_fwd: binary16 output is two-pass only");
+      hipLaunchKernelGGL((ln_fwd_kernel<C, false, float, 0, U, true>), dim3(grid), dim3(256), 0,
+                         st, x, M, nt, gamma, beta, y, mean, rstd, wb, bias_out, bs);
+      return;
+    } else {
+      throw std::runtime_error("ln_fwd: binary16 output has no bias projection");
+    }
+  }
   if (fast)
     hipLaunchKernelGGL((ln_fwd_kernel<C, true, float, H, U>), dim3(grid), dim3(256), 0, st, x, M,
                        nt, gamma, beta, y, mean, rstd, wb, bias_out, bs);
@@ -367,11 +381,11 @@ static void ln_fwd_launch(hipStream_t st, const float* x, long M, int nt, const 
 template <int C>
 static void ln_fwd_dispatch(hipStream_t st, const float* x, long M, int nt, const float* gamma,
                             const float* beta, bf16* y, float* mean, float* rstd, bool fast, int H,
-                            const float* wb, float* bias_out, float bs) {
+                            const float* wb, float* bias_out, float bs, bool yf16) {
   switch (H) {
-    case 0: ln_fwd_launch<C, 0>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, wb, bias_out, bs); break;
-    case 4: ln_fwd_launch<C, 4>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, wb, bias_out, bs); break;
-    case 8: ln_fwd_launch<C, 8>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, wb, bias_out, bs); break;
+    case 0: ln_fwd_launch<C, 0>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, wb, bias_out, bs, yf16); break;
+    case 4: ln_fwd_launch<C, 4>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, wb, bias_out, bs, yf16); break;
+    case 8: ln_fwd_launch<C, 8>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, wb, bias_out, bs, yf16); break;
     default: throw std::runtime_error("ln_fwd: bias heads must be 0, 4 or 8");
   }
 }
@@ -379,11 +393,11 @@ static void ln_fwd_dispatch(hipStream_t st, const float* x, long M, int nt, cons
 void ln_fwd_f32(hipStream_t st, const float* x, long M, int C, int nt,
                 const float* gamma, const float* beta, bf16* y, float* mean,
                 float* rstd, bool fast, int H, const float* wb, float* bias_out,
-                float bs) {
+                float bs, bool y_f16) {
   switch (C) {
-    case 64: ln_fwd_dispatch<64>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, H, wb, bias_out, bs); break;
-    case 128: ln_fwd_dispatch<128>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, H, wb, bias_out, bs); break;
-    case 256: ln_fwd_dispatch<256>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, H, wb, bias_out, bs); break;
+    case 64: ln_fwd_dispatch<64>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, H, wb, bias_out, bs, y_f16); break;
+    case 128: ln_fwd_dispatch<128>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, H, wb, bias_out, bs, y_f16); break;
+    case 256: ln_fwd_dispatch<256>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, H, wb, bias_out, bs, y_f16); break;
     default: throw std::runtime_error("ln_fwd: unsupported channel count");
   }
 }

@@ -62,7 +62,8 @@ void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
 struct TransW {
   int C = 0, F = 0;
   const float *ln_g = nullptr, *ln_b = nullptr, *b1 = nullptr, *b2 = nullptr;
-  const bf16 *w1 = nullptr, *w1_t = nullptr, *w2 = nullptr, *w2_t = nullptr;
+  const bf16 *w1 = nullptr, *w2 = nullptr;      // backward operands (bf16)
+  const f16 *w1_t = nullptr, *w2_t = nullptr;   // forward operands (binary16)
 };
 TransW transition_weights(WeightStore& ws, const std::string& prefix);
 size_t transition_save_bytes(long rows, int C, int F);

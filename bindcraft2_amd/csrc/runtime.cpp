@@ -102,6 +102,13 @@ void* Arena::take(size_t bytes) {
   return r;
 }
 
+std::vector<f16> transpose_f16(const float* src, int rows, int cols) {
+  std::vector<f16> o((size_t)rows * cols);
+  for (int r = 0; r < rows; ++r)
+    for (int c = 0; c < cols; ++c) o[(size_t)c * rows + r] = (f16)src[(size_t)r * cols + c];
+  return o;
+}
+
 Arena& arena() {
   static Arena a;
   return a;

@@ -65,6 +65,8 @@ WeightStore& weights(const std::string& dir);
 std::vector<bf16> to_bf16(const std::vector<float>& v);
 // [rows][cols] f32 -> [cols][rows] bf16
 std::vector<bf16> transpose_bf16(const float* src, int rows, int cols);
+// The same transpose to binary16 (operands of the GEMMs launched with F16).
+std::vector<f16> transpose_f16(const float* src, int rows, int cols);
 
 // Grow-only device scratch arena, carved by bump allocation per call.  One
 // arena per device; callers hold `lock()` for the duration of a call.

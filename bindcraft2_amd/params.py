@@ -205,6 +205,32 @@ def init_block_params(block, rng, modules=None, gates="zero", ln="identity", **s
     return out
 
 
+# The pair-track modules of an extra-MSA block in its pair-only form (the
+# outer product mean kept for its output_b, which the fully masked extra MSA
+# turns into a constant pair update).
+PAIR_ONLY_MODULES = ("outer_product_mean", "triangle_multiplication_outgoing",
+                     "triangle_multiplication_incoming", "triangle_attention_starting_node",
+                     "triangle_attention_ending_node", "pair_transition")
+
+
+def init_trunk_params(rng, depth=48, extra_depth=4, tpl_depth=2, gates="zero", ln="identity"):
+    """The design-step trunk of BASELINE configs[3]/[4] with random weights:
+    `depth` Evoformer blocks (c_m=256, c_z=128), `extra_depth` pair-only
+    extra-MSA blocks and `tpl_depth` template pair blocks (c_t=64), LeCun-normal
+    weights with AF2's gate init.  Returns three flat manifest dicts (main,
+    extra, template), drawn in that order from `rng`."""
+    evo = {}
+    for blk in range(depth):
+        evo.update(init_block_params(blk, rng, gates=gates, ln=ln))
+    extra = {}
+    for blk in range(extra_depth):
+        extra.update(init_block_params(blk, rng, gates=gates, ln=ln, modules=PAIR_ONLY_MODULES))
+    tpl = {}
+    for blk in range(tpl_depth):
+        tpl.update(init_template_block_params(blk, rng, gates=gates, ln=ln))
+    return evo, extra, tpl
+
+
 # AF2 multimer structure module (folding_multimer.py, config.py:578-600):
 # single width 384, 12 heads, 16 scalar / 4 point qk, 16 scalar / 8 point v.
 C_S, IPA_H = 384, 12

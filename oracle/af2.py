@@ -263,6 +263,47 @@ def evoformer_iteration(msa, pair, msa_mask, pair_mask, params, prefix, key,
     return msa, pair
 
 
+def pair_only_iteration(pair, pair_mask, params, prefix, key, use_dropout, dtype=torch.float64):
+    """The pair track of an extra-MSA EvoformerIteration (modules.py:1278-1391)
+    whose extra-MSA mask is all zero, as the design step runs it
+    (bindcraft/af2.py:193; the reference's native pair-only stack,
+    bindcraft/af/native.py:1131-1193): the outer product mean of a fully
+    masked MSA is output_b / 1e-3 (left = right = 0, norm = 0) at dropout
+    rate 0, the MSA modules never reach the pair again, and the five pair
+    modules take keys 5..9 of the block key's split into 10."""
+    P = Params(params, prefix, dtype)
+    sub = jax_prng.split(key, 10)[1:] if key is not None else [None] * 9
+    cfg = {n: (r, o) for n, r, o in EVO_MODULES}
+    pair = pair + P("outer_product_mean/output_b") / 1e-3
+    for i, name in enumerate(("triangle_multiplication_outgoing", "triangle_multiplication_incoming",
+                              "triangle_attention_starting_node", "triangle_attention_ending_node",
+                              "pair_transition")):
+        p = P.sub(name + "/")
+        if name.startswith("triangle_multiplication"):
+            res = triangle_multiplication(pair, pair_mask, p, name.endswith("outgoing"))
+        elif name.startswith("triangle_attention"):
+            res = triangle_attention(pair, pair_mask, p, name.endswith("ending_node"))
+        else:
+            res = transition(pair, pair_mask, p)
+        r, o = cfg[name]
+        pair = dropout_wrapper(res, pair, sub[4 + i], r, o, use_dropout)
+    return pair
+
+
+def stack_block_keys(stack_key, depth):
+    """The key each layer of a layer_stack scan hands its block
+    (modules_multimer.py:622-641, :957-975): per layer (carry, sub) =
+    split(carry); None entries when there is no key."""
+    out, carry = [], stack_key
+    for _ in range(depth):
+        if carry is None:
+            out.append(None)
+            continue
+        carry, sub = jax_prng.split(carry, 2)
+        out.append(sub)
+    return out
+
+
 def evoformer_stack(msa, pair, msa_mask, pair_mask, params, depth, stack_key,
                     use_dropout, is_extra_msa=False, dtype=torch.float64):
     """modules_multimer.py:610-641 (layer_stack scan of evoformer_fn): per

@@ -28,15 +28,17 @@ def _case(n, per_column, seed, drop, mask_frac):
 
 
 def _oracle(prm, per_column, pair, mask, tbl, dout):
-    P = af2.Params(prm, f"param/block0/{NAMES[per_column]}/")
-    x = torch.tensor(pair, dtype=torch.float64, requires_grad=True)
-    m = torch.as_tensor(mask, dtype=torch.float64)
+    # fp64, or fp32 from L=512 (the [L,H,L,L] logits then take 4 GB per copy)
+    dt = torch.float64 if pair.shape[0] < 512 else torch.float32
+    P = af2.Params(prm, f"param/block0/{NAMES[per_column]}/", dt)
+    x = torch.tensor(pair, dtype=dt, requires_grad=True)
+    m = torch.as_tensor(mask, dtype=dt)
     delta = af2.triangle_attention(x, m, P, per_column)
     if tbl is not None:
-        t = torch.as_tensor(tbl, dtype=torch.float64)
+        t = torch.as_tensor(tbl, dtype=dt)
         delta = delta * (t[None] if not per_column else t[:, None])
-    (g,) = torch.autograd.grad(delta, x, torch.as_tensor(dout, dtype=torch.float64))
-    return delta.detach(), g
+    (g,) = torch.autograd.grad(delta, x, torch.as_tensor(dout, dtype=dt))
+    return delta.detach().double(), g.double()
 
 
 @pytest.mark.parametrize("n,per_column,drop,mask_frac", [
@@ -45,7 +47,10 @@ def _oracle(prm, per_column, pair, mask, tbl, dout):
     (96, True, True, 0.25),
     # the benchmark length, and lengths past one 256-key chunk (chunked
     # keys with an online rescale; four query groups in dK/dV)
-    (224, False, True, 0.1), (288, True, True, 0.1), (320, False, True, 0.25),
+    (224, False, True, 0.1), (224, True, True, 0.1), (288, True, True, 0.1),
+    (320, False, True, 0.25),
+    # the large complex of BASELINE configs[4]
+    (512, False, True, 0.1), (512, True, True, 0.1),
 ])
 def test_triattn_fwd_bwd_parity(cuda, n, per_column, drop, mask_frac):
     print(f"triattn n={n} per_column={per_column} drop={drop} mask={mask_frac}", flush=True)

@@ -15,19 +15,22 @@ NAMES = {True: "triangle_multiplication_outgoing", False: "triangle_multiplicati
 
 
 def _oracle(prm, outgoing, pair, mask, tbl, dout):
-    P = af2.Params(prm, f"param/block0/{NAMES[outgoing]}/")
-    x = torch.tensor(pair, dtype=torch.float64, requires_grad=True)
-    delta = af2.triangle_multiplication(x, torch.as_tensor(mask, dtype=torch.float64), P, outgoing)
+    dt = torch.float64 if pair.shape[0] < 512 else torch.float32
+    P = af2.Params(prm, f"param/block0/{NAMES[outgoing]}/", dt)
+    x = torch.tensor(pair, dtype=dt, requires_grad=True)
+    delta = af2.triangle_multiplication(x, torch.as_tensor(mask, dtype=dt), P, outgoing)
     if tbl is not None:
-        delta = delta * torch.as_tensor(tbl, dtype=torch.float64)[None]
-    (g,) = torch.autograd.grad(delta, x, torch.as_tensor(dout, dtype=torch.float64))
-    return delta.detach(), g
+        delta = delta * torch.as_tensor(tbl, dtype=dt)[None]
+    (g,) = torch.autograd.grad(delta, x, torch.as_tensor(dout, dtype=dt))
+    return delta.detach().double(), g.double()
 
 
 @pytest.mark.parametrize("n,outgoing,drop,mask_frac", [
     (32, True, False, 0.0), (32, False, False, 0.0),
     (64, True, True, 0.1), (64, False, True, 0.1), (96, False, True, 0.2),
     (224, True, True, 0.1), (224, False, True, 0.1), (288, True, True, 0.1),
+    # the large complex of BASELINE configs[4]
+    (512, True, True, 0.1), (512, False, True, 0.1),
 ])
 def test_trimul_fwd_bwd_parity(cuda, n, outgoing, drop, mask_frac):
     print(f"trimul n={n} outgoing={outgoing} drop={drop} mask={mask_frac}", flush=True)

@@ -478,3 +478,118 @@ def test_structure_heads_symmetry_and_finite_differences():
         e = np.zeros_like(pair); e[i, j, k] = h
         fd = (f(single, pair + e) - f(single, pair - e)) / (2 * h)
         assert abs(fd - gz[i, j, k].item()) <= 1e-5 * max(1.0, abs(fd))
+
+
+# ------------------------------------------------------------- global attention
+def _global_params(rng, c=8, heads=2):
+    shapes = bparams.global_attention_shapes(c, heads)
+    return {f"x/{k}": v for k, v in bparams.init_module(shapes, rng, "random", "random").items()}
+
+
+def _loop_global_attention(x, mask, P):
+    """modules.py:403-497 written out as loops over (column, head, key): the
+    masked-mean query (utils.py:61-86 with a [.., 1] mask: broadcast factor 1),
+    one query per head, shared single-head keys and values, softmax over the
+    sequences, then per query row the head-wise sigmoid gate and the output
+    projection."""
+    qw, kw, vw = P("attention/query_w"), P("attention/key_w"), P("attention/value_w")
+    gw, gb = P("attention/gating_w"), P("attention/gating_b")
+    ow, ob = P("attention/output_w"), P("attention/output_b")
+    B, K, A = x.shape
+    H, D = qw.shape[1], qw.shape[2]
+    out = torch.zeros(B, K, ow.shape[-1], dtype=DT)
+    for b in range(B):
+        msum = sum(float(mask[b, k]) for k in range(K))
+        qa = [sum(float(mask[b, k]) * float(x[b, k, a]) for k in range(K)) / (msum + 1e-10)
+              for a in range(A)]
+        keys = [[sum(float(x[b, k, a]) * float(kw[a, c]) for a in range(A)) for c in range(D)]
+                for k in range(K)]
+        vals = [[sum(float(x[b, k, a]) * float(vw[a, c]) for a in range(A)) for c in range(D)]
+                for k in range(K)]
+        wa = []
+        for h in range(H):
+            q = [sum(qa[a] * float(qw[a, h, c]) for a in range(A)) / D ** 0.5 for c in range(D)]
+            lg = [sum(q[c] * keys[k][c] for c in range(D)) + 1e9 * (float(mask[b, k]) - 1.0)
+                  for k in range(K)]
+            m = max(lg)
+            w = [np.exp(v - m) for v in lg]
+            s = sum(w)
+            wa.append([sum(w[k] / s * vals[k][c] for k in range(K)) for c in range(D)])
+        for i in range(K):
+            for o in range(ow.shape[-1]):
+                acc = float(ob[o])
+                for h in range(H):
+                    for c in range(D):
+                        g = sum(float(x[b, i, a]) * float(gw[a, h, c]) for a in range(A)) + float(gb[h, c])
+                        acc += wa[h][c] / (1.0 + np.exp(-g)) * float(ow[h, c, o])
+                out[b, i, o] = acc
+    return out
+
+
+def test_global_attention_matches_loops():
+    rng = np.random.default_rng(21)
+    P = af2.Params(_global_params(rng), "x/")
+    x = torch.as_tensor(rng.standard_normal((3, 5, 8)), dtype=DT)
+    mask = torch.ones(3, 5, dtype=DT)
+    mask[0, 1] = mask[2, 0] = mask[2, 4] = 0
+    got = af2.global_attention(x, x, mask[..., None], P)
+    torch.testing.assert_close(got, _loop_global_attention(x, mask, P), rtol=1e-10, atol=1e-10)
+
+
+def _gated_output(x, v, P):
+    """sum_h (v . sigmoid(gate_h(x))) W_o[h] + b_o for one value vector per head."""
+    g = torch.sigmoid(torch.einsum("bqc,chv->bqhv", x, P("attention/gating_w")) + P("attention/gating_b"))
+    return torch.einsum("bqhc,hco->bqo", v * g, P("attention/output_w")) + P("attention/output_b")
+
+
+@pytest.mark.parametrize("masked", [False, True])
+def test_global_attention_single_sequence_closed_form(masked):
+    """One sequence: the softmax over one key is 1 whatever its mask, so every
+    head reads the one value row."""
+    rng = np.random.default_rng(22)
+    P = af2.Params(_global_params(rng), "x/")
+    x = torch.as_tensor(rng.standard_normal((4, 1, 8)), dtype=DT)
+    mask = torch.full((4, 1), 0.0 if masked else 1.0, dtype=DT)
+    v = torch.einsum("bka,ac->bkc", x, P("attention/value_w"))[:, :, None]  # [B,1,1,D]
+    torch.testing.assert_close(af2.global_attention(x, x, mask[..., None], P), _gated_output(x, v, P),
+                               rtol=1e-12, atol=1e-12)
+
+
+def test_global_attention_fully_masked_column_is_uniform():
+    """All sequences masked: the masked-mean query is 0, so every logit is the
+    same -1e9 and the weights are uniform: each head reads the mean value."""
+    rng = np.random.default_rng(23)
+    P = af2.Params(_global_params(rng), "x/")
+    x = torch.as_tensor(rng.standard_normal((2, 6, 8)), dtype=DT)
+    mask = torch.zeros(2, 6, dtype=DT)
+    v = torch.einsum("bka,ac->bkc", x, P("attention/value_w")).mean(1)[:, None, None]
+    torch.testing.assert_close(af2.global_attention(x, x, mask[..., None], P), _gated_output(x, v, P),
+                               rtol=1e-12, atol=1e-12)
+
+
+def test_pair_only_iteration_is_the_extra_block_at_zero_mask():
+    """The pair-only block equals the full extra-MSA EvoformerIteration (MSA
+    row attention, global column attention, MSA transition, outer product
+    mean on a c_e MSA) on an all-zero extra-MSA mask, dropout on."""
+    from oracle import jax_prng as J
+    rng = np.random.default_rng(24)
+    kw = dict(c_z=16, c_m=8, tri_heads=2, trimul_hidden=8, opm_c=4, row_heads=2, col_heads=2)
+    sh = bparams.module_shapes(**kw)
+    sh.pop("msa_column_attention")
+    sh["msa_column_global_attention"] = bparams.global_attention_shapes(8, 2)
+    prm = {}
+    for mod, shapes in sh.items():
+        for pname, arr in bparams.init_module(shapes, rng, "random", "random").items():
+            prm[f"param/block0/{mod}/{pname}"] = arr
+    prm["param/block0/outer_product_mean/output_b"] *= 1e-3
+    pair = torch.as_tensor(rng.standard_normal((7, 7, 16)), dtype=DT)
+    msa = torch.as_tensor(rng.standard_normal((3, 7, 8)), dtype=DT)
+    pmask = torch.as_tensor((rng.random((7, 7)) > 0.2).astype(np.float64))
+    key = J.prng_key(5)
+    _, full = af2.evoformer_iteration(msa, pair, torch.zeros(3, 7, dtype=DT), pmask, prm,
+                                      "param/block0/", key, True, is_extra_msa=True)
+    got = af2.pair_only_iteration(pair, pmask, prm, "param/block0/", key, True)
+    torch.testing.assert_close(got, full, rtol=1e-12, atol=1e-12)
+    # and the dropout is live: a different key changes the result
+    other = af2.pair_only_iteration(pair, pmask, prm, "param/block0/", J.prng_key(6), True)
+    assert not torch.allclose(other, full)
