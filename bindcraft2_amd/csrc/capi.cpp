@@ -892,8 +892,8 @@ int bc2n_probe_gemm(void* stream, int M, int N, int K, const uint16_t* A, const 
     need(A && B && C, "null operand");
     GemmArgs g;
     g.M = M; g.N = N; g.K = K;
-    g.A = reinterpret_cast<const bf16*>(A); g.a_sm = K; g.a_sk = 1;
-    g.B = reinterpret_cast<const bf16*>(B); g.b_sn = K; g.b_sk = 1;
+    g.A = reinterpret_cast<const h16*>(A); g.a_sm = K; g.a_sk = 1;
+    g.B = reinterpret_cast<const h16*>(B); g.b_sn = K; g.b_sk = 1;
     gemm<128, 128>(as_stream(stream), g, EpiStore<float>{C, N, 0, nullptr, N});
   });
 }
@@ -915,7 +915,7 @@ int bc2n_probe_layernorm(void* stream, long M, int C, const float* x, const floa
                          const float* beta, int fast, uint16_t* y, float* mean, float* rstd) {
   return guarded([&] {
     need(x && gamma && beta && y && mean && rstd, "null operand");
-    ln_fwd_f32(as_stream(stream), x, M, C, 0, gamma, beta, reinterpret_cast<bf16*>(y), mean,
+    ln_fwd_f32(as_stream(stream), x, M, C, 0, gamma, beta, reinterpret_cast<h16*>(y), mean,
                rstd, fast != 0, 0, nullptr, nullptr);
   });
 }

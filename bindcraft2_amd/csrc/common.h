@@ -1,8 +1,20 @@
 // Shared device/host helpers for the gfx950 (CDNA4) trunk kernels.
 //
 // Everything here is written for wave64 and the gfx950 MFMA set; there is no
-// other target.  bf16 is the storage type of GEMM operands, f32 the type of
-// every accumulation, residual carry and softmax statistic.
+// other target.  IEEE binary16 (h16) is the storage type of every MFMA
+// operand, f32 the type of every accumulation, residual carry, softmax
+// statistic and of the one product without a range bound (the triangle
+// multiplication's contraction output).
+//
+// Why binary16 and not bf16: the trunk's MFMA operands are either bounded by
+// construction (LayerNorm outputs, projections of them, softmax
+// probabilities, sigmoid gates, weights) or backward cotangents, which every
+// module multiplies by a power-of-two scale s (s * max|cotangent| in (8, 16],
+// ct_scale in kernels.h) before they are rounded and divides out in the f32
+// epilogue that ends the module.  So the 5 exponent bits suffice, and the 3
+// extra significand bits make each rounding 8x finer at the same MFMA rate
+// and conversion cost (v_cvt_pk_f16_f32).  Over a 48-block stack the bf16
+// roundings compound to a few percent of the input gradient in L2.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -10,11 +22,9 @@
 
 namespace bc2n {
 
-typedef __bf16 bf16;
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-typedef _Float16 f16;
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h16;
+typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -25,11 +35,18 @@ constexpr float LN2 = 0.6931471805599453f;
 constexpr float LOGIT_CLIP = 1e8f;
 constexpr float MASK_BIAS = 1e9f;
 
-__device__ __forceinline__ float bf2f(bf16 v) { return (float)v; }
-__device__ __forceinline__ bf16 f2bf(float v) { return (bf16)v; }
+__device__ __forceinline__ float h2f(h16 v) { return (float)v; }
+__device__ __forceinline__ h16 f2h(float v) { return (h16)v; }
+// Round to binary16, saturating at the largest finite value instead of going
+// to infinity: for backward tensors, where an exact-model value that is huge
+// but finite (the LayerNorm backward of an all-zero masked row) is later
+// multiplied by a zero mask; inf * 0 would be NaN, 65504 * 0 is 0.
+__device__ __forceinline__ h16 f2h_sat(float v) {
+  return (h16)__builtin_amdgcn_fmed3f(v, -65504.f, 65504.f);
+}
 
 // 1/(1+e^-x) with the hardware reciprocal (v_rcp_f32, 1 ulp) instead of an
-// IEEE division: the results feed bf16 operands or f32 sums far coarser than
+// IEEE division: the results feed binary16 operands or f32 sums far coarser than
 // that.  exp(-x) = 2^(-x log2 e).
 __device__ __forceinline__ float sigmoidf_(float x) {
   return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
@@ -49,20 +66,13 @@ __device__ __forceinline__ long xcd_block(long G) {
   return (b % NUM_XCD) * xcd_per(G) + b / NUM_XCD;
 }
 
-// D += A(16x32) * B(32x16), bf16 operands, f32 accumulation.
+// D += A(16x32) * B(32x16), binary16 operands, f32 accumulation.
 // Lane l: A row l%16, B column l%16, 8 K-slots per lane; D lane l holds
 // column l%16, rows 4*(l/16)+r.  The K-slot -> k mapping is the same for A
 // and B, so any bijection of the 32 k values over (lane group, element) that
 // is applied identically to both operands yields the exact product.
-__device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-// The same product, same lane layout and rate, with IEEE binary16 operands:
-// the 16-bit words of a and b hold halfs (11-bit significands, against
-// bf16's 8), for products whose operands have a bounded range.
-__device__ __forceinline__ f32x4 mfma16x16x32_f16(bf16x8 a, bf16x8 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
-                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+__device__ __forceinline__ f32x4 mfma16x16x32(h16x8 a, h16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
 // DPP lane moves (gfx9 encodings): a VALU operand read from another lane of
@@ -110,12 +120,12 @@ __device__ __forceinline__ long ln_src_row(long m, int nt) {
   return q * nt + p;
 }
 
-// 16-byte vector load/store of 8 bf16 values.
-__device__ __forceinline__ bf16x8 ld8(const bf16* p) {
-  return *reinterpret_cast<const bf16x8*>(p);
+// 16-byte vector load/store of 8 binary16 values.
+__device__ __forceinline__ h16x8 ld8(const h16* p) {
+  return *reinterpret_cast<const h16x8*>(p);
 }
-__device__ __forceinline__ void st8(bf16* p, bf16x8 v) {
-  *reinterpret_cast<bf16x8*>(p) = v;
+__device__ __forceinline__ void st8(h16* p, h16x8 v) {
+  *reinterpret_cast<h16x8*>(p) = v;
 }
 
 // ---------------------------------------------------------------------------

@@ -8,10 +8,10 @@
 //
 // A workgroup is NB waves on one channel; wave w owns the 32 columns
 // n = 32w .. 32w+31 and keeps their B fragments for the whole K in registers
-// (NB k-steps x 2 n-tiles x 8 bf16).  The workgroup walks strips of 16 rows of
+// (NB k-steps x 2 n-tiles x 8 h16).  The workgroup walks strips of 16 rows of
 // A (the strips s = g, g+G, ... of its channel, G workgroups per channel):
 // each strip is staged in LDS, double-buffered with a register prefetch of the
-// next one, and feeds v_mfma_f32_16x16x32_bf16 with B as the first operand, so
+// next one, and feeds v_mfma_f32_16x16x32_f16 with B as the first operand, so
 // a lane ends with 4 consecutive columns of one output row (a vector store).
 //
 // K-slot order: both operands present the 32 k of a step to lane group g as
@@ -31,14 +31,14 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 // T[r0 + 4g + j][c0 + l%16], j = 0..3, of a row-major LDS tile (ld % 4 == 0)
-__device__ __forceinline__ bf16x4 tr4(const bf16* T, int ld, int r0, int c0, int lane) {
+__device__ __forceinline__ h16x4 tr4(const h16* T, int ld, int r0, int c0, int lane) {
   const int g = lane >> 4, m = lane & 15;
-  const bf16* p = T + (r0 + 4 * g + (m >> 2)) * ld + c0 + 4 * (m & 3);
-  return __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p));
+  const h16* p = T + (r0 + 4 * g + (m >> 2)) * ld + c0 + 4 * (m & 3);
+  return __builtin_bit_cast(h16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p));
 }
 
-__device__ __forceinline__ bf16x8 cat8(bf16x4 a, bf16x4 b) {
-  bf16x8 r;
+__device__ __forceinline__ h16x8 cat8(h16x4 a, h16x4 b) {
+  h16x8 r;
   r[0] = a[0]; r[1] = a[1]; r[2] = a[2]; r[3] = a[3];
   r[4] = b[0]; r[5] = b[1]; r[6] = b[2]; r[7] = b[3];
   return r;
@@ -46,12 +46,12 @@ __device__ __forceinline__ bf16x8 cat8(bf16x4 a, bf16x4 b) {
 
 // Fragment of row `row` (the lane's m or n) for k-step ks from a K-contiguous
 // tile T[row][k] (row stride ld) ...
-__device__ __forceinline__ bf16x8 frag_rows(const bf16* T, int ld, int row, int ks, int g) {
-  const bf16* p = T + row * ld + ks * 32 + 4 * g;
-  return cat8(*reinterpret_cast<const bf16x4*>(p), *reinterpret_cast<const bf16x4*>(p + 16));
+__device__ __forceinline__ h16x8 frag_rows(const h16* T, int ld, int row, int ks, int g) {
+  const h16* p = T + row * ld + ks * 32 + 4 * g;
+  return cat8(*reinterpret_cast<const h16x4*>(p), *reinterpret_cast<const h16x4*>(p + 16));
 }
 // ... and from a k-major tile T[k][col] (column c0 + l%16).
-__device__ __forceinline__ bf16x8 frag_cols(const bf16* T, int ld, int c0, int ks, int lane) {
+__device__ __forceinline__ h16x8 frag_cols(const h16* T, int ld, int c0, int ks, int lane) {
   return cat8(tr4(T, ld, ks * 32, c0, lane), tr4(T, ld, ks * 32 + 16, c0, lane));
 }
 
@@ -62,17 +62,17 @@ __device__ __forceinline__ void store4<float>(float* p, f32x4 v) {
   *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
 }
 template <>
-__device__ __forceinline__ void store4<bf16>(bf16* p, f32x4 v) {
-  bf16x4 o;
-  o[0] = (bf16)v[0]; o[1] = (bf16)v[1]; o[2] = (bf16)v[2]; o[3] = (bf16)v[3];
-  *reinterpret_cast<bf16x4*>(p) = o;
+__device__ __forceinline__ void store4<h16>(h16* p, f32x4 v) {
+  h16x4 o;
+  o[0] = f2h_sat(v[0]); o[1] = f2h_sat(v[1]); o[2] = f2h_sat(v[2]); o[3] = f2h_sat(v[3]);
+  *reinterpret_cast<h16x4*>(p) = o;
 }
 
 constexpr int SR = 16;  // rows of A per strip
 
 template <int NB, bool AK, bool BK, class OutT>
-__global__ __launch_bounds__(64 * NB) void contract_kernel(const bf16* __restrict__ A,
-                                                           const bf16* __restrict__ B,
+__global__ __launch_bounds__(64 * NB) void contract_kernel(const h16* __restrict__ A,
+                                                           const h16* __restrict__ B,
                                                            OutT* __restrict__ C, long P,
                                                            int channels, int groups) {
   constexpr int N = 32 * NB;
@@ -84,16 +84,16 @@ __global__ __launch_bounds__(64 * NB) void contract_kernel(const bf16* __restric
   constexpr int LDA = AK ? N + 8 : SR + 8;   // A strip: [16][N] (K-contig) or [N][16] (k-major)
   constexpr int AROWS = AK ? SR : N;
   constexpr int ABUF = AROWS * LDA;
-  __shared__ __attribute__((aligned(16))) bf16 As[2 * ABUF];
-  __shared__ __attribute__((aligned(16))) bf16 Bs[BROWS * LDB];
+  __shared__ __attribute__((aligned(16))) h16 As[2 * ABUF];
+  __shared__ __attribute__((aligned(16))) h16 Bs[BROWS * LDB];
   static_assert(SR * N / 8 == NT, "one 16-byte chunk of a strip per thread");
 
   const long G = (long)channels * groups;
   const long bid = xcd_block(G);  // (channel, group): a channel's groups share its B plane in L2
   if (bid >= G) return;
   const int ch = (int)(bid / groups), grp = (int)(bid % groups);
-  const bf16* Ap = A + (long)ch * P;
-  const bf16* Bp = B + (long)ch * P;
+  const h16* Ap = A + (long)ch * P;
+  const h16* Bp = B + (long)ch * P;
   OutT* Cp = C + (long)ch * P;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -101,11 +101,11 @@ __global__ __launch_bounds__(64 * NB) void contract_kernel(const bf16* __restric
   const int n0 = wave * 32;
 
   // ---- B fragments of this wave's 32 columns, all k, via LDS chunks of 32 k
-  bf16x8 bf[NB][2];
+  h16x8 bf[NB][2];
 #pragma unroll
   for (int kc = 0; kc < NB; ++kc) {
     constexpr int CH = BROWS * (BK ? 4 : N / 8);  // 16-byte chunks per staging chunk
-    bf16x8 v[(CH + NT - 1) / NT];
+    h16x8 v[(CH + NT - 1) / NT];
 #pragma unroll
     for (int i = 0; i < (CH + NT - 1) / NT; ++i) {
       const int c = tid + NT * i;
@@ -137,7 +137,7 @@ __global__ __launch_bounds__(64 * NB) void contract_kernel(const bf16* __restric
   }
 
   // ---- A strips
-  auto load_strip = [&](int s) -> bf16x8 {
+  auto load_strip = [&](int s) -> h16x8 {
     if constexpr (AK) {
       const int r = tid / (N / 8), q = (tid % (N / 8)) * 8;
       return ld8(Ap + (long)(s * SR + r) * N + q);
@@ -146,8 +146,8 @@ __global__ __launch_bounds__(64 * NB) void contract_kernel(const bf16* __restric
       return ld8(Ap + (long)k * N + s * SR + q);
     }
   };
-  auto stash = [&](int buf, bf16x8 v) {
-    bf16* as = As + buf * ABUF;
+  auto stash = [&](int buf, h16x8 v) {
+    h16* as = As + buf * ABUF;
     if constexpr (AK) st8(&as[(tid / (N / 8)) * LDA + (tid % (N / 8)) * 8], v);
     else st8(&as[(tid / 2) * LDA + (tid % 2) * 8], v);
   };
@@ -159,18 +159,18 @@ __global__ __launch_bounds__(64 * NB) void contract_kernel(const bf16* __restric
   int buf = 0;
   for (; s < NS; s += groups) {
     const bool more = s + groups < NS;
-    bf16x8 nxt;
+    h16x8 nxt;
     if (more) nxt = load_strip(s + groups);
-    const bf16* as = As + buf * ABUF;
+    const h16* as = As + buf * ABUF;
     f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
     for (int ks = 0; ks < NB; ++ks) {
-      bf16x8 af;
+      h16x8 af;
       if constexpr (AK) af = frag_rows(as, LDA, l16, ks, g);
       else af = frag_cols(as, LDA, 0, ks, lane);
 #pragma unroll
       for (int j = 0; j < 2; ++j)
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[ks][j], af, acc[j], 0, 0, 0);
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[ks][j], af, acc[j], 0, 0, 0);
     }
     // lane: row m = strip row l16, columns n0 + 16j + 4g .. +3
     const int m = s * SR + l16;
@@ -183,7 +183,7 @@ __global__ __launch_bounds__(64 * NB) void contract_kernel(const bf16* __restric
 }
 
 template <int NB, class OutT>
-void launch(hipStream_t st, bool ak, bool bk, const bf16* A, const bf16* B, OutT* C, long P,
+void launch(hipStream_t st, bool ak, bool bk, const h16* A, const h16* B, OutT* C, long P,
             int channels, int groups) {
   const dim3 grid(xcd_grid((long)channels * groups)), block(64 * NB);
 #define BC2N_CT(AKV, BKV) \
@@ -196,7 +196,7 @@ void launch(hipStream_t st, bool ak, bool bk, const bf16* A, const bf16* B, OutT
 }
 
 template <class OutT>
-bool contract_t(hipStream_t st, int N, int channels, const bf16* A, bool ak, const bf16* B,
+bool contract_t(hipStream_t st, int N, int channels, const h16* A, bool ak, const h16* B,
                 bool bk, OutT* C, int groups) {
   const long P = (long)N * N;
   switch (N / 32) {
@@ -209,8 +209,8 @@ bool contract_t(hipStream_t st, int N, int channels, const bf16* A, bool ak, con
 
 }  // namespace
 
-bool trimul_contract(hipStream_t st, int N, int channels, const bf16* A, bool a_kcontig,
-                     const bf16* B, bool b_kcontig, float* Cf, bf16* Cb) {
+bool trimul_contract(hipStream_t st, int N, int channels, const h16* A, bool a_kcontig,
+                     const h16* B, bool b_kcontig, float* Cf, h16* Cb) {
   if (N <= 0 || N % 32 != 0 || N > 256) return false;
   if (((uintptr_t)A & 15) || ((uintptr_t)B & 15) || ((uintptr_t)Cf & 15) || ((uintptr_t)Cb & 7))
     throw std::runtime_error("contract: operands must be 16-byte aligned");
@@ -222,7 +222,7 @@ bool trimul_contract(hipStream_t st, int N, int channels, const bf16* A, bool a_
   const int ns = N / SR;
   const int groups = std::max(1, std::min(ns, (2 * cus + channels - 1) / channels));
   if (Cf) return contract_t<float>(st, N, channels, A, a_kcontig, B, b_kcontig, Cf, groups);
-  return contract_t<bf16>(st, N, channels, A, a_kcontig, B, b_kcontig, Cb, groups);
+  return contract_t<h16>(st, N, channels, A, a_kcontig, B, b_kcontig, Cb, groups);
 }
 
 }  // namespace bc2n

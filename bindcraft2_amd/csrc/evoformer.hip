@@ -180,16 +180,30 @@ void block_bwd(hipStream_t st, const BlockW& B, const Layout& L, int b, const Ta
   BlockPtrs p = carve(L, save);
   const int N = L.N, S = L.S;
   const long M = (long)N * N;
-  transition_bwd(st, B.ptr, M, N, p.p5, nullptr, p.ptr, dpair, dpair);
-  triattn_bwd(st, B.tae, true, N, p.p4, pmask, t.pair(b, 3), p.tae, dpair, dpair);
-  triattn_bwd(st, B.tas, false, N, p.p3, pmask, t.pair(b, 2), p.tas, dpair, dpair);
-  trimul_bwd(st, B.tmi, false, N, p.p2, pmask, t.pair(b, 1), p.tmi, dpair, dpair);
-  trimul_bwd(st, B.tmo, true, N, L.tpl ? f.pin : p.p1, pmask, t.pair(b, 0), p.tmo, dpair, dpair);
+  // one cotangent scale per carry and block (the modules' own would cost a
+  // max-reduction each); within a block the pair cotangent grows by a few
+  // tens of percent, far inside binary16's headroom over the scaled maximum
+  float* sp = ct_scale_slot(1);
+  {
+    KTimed kt("block.ct_scale", st);
+    ct_scale(st, dpair, M * L.Cz, sp);
+  }
+  transition_bwd(st, B.ptr, M, N, p.p5, nullptr, p.ptr, dpair, dpair, sp);
+  triattn_bwd(st, B.tae, true, N, p.p4, pmask, t.pair(b, 3), p.tae, dpair, dpair, sp);
+  triattn_bwd(st, B.tas, false, N, p.p3, pmask, t.pair(b, 2), p.tas, dpair, dpair, sp);
+  trimul_bwd(st, B.tmi, false, N, p.p2, pmask, t.pair(b, 1), p.tmi, dpair, dpair, sp);
+  trimul_bwd(st, B.tmo, true, N, L.tpl ? f.pin : p.p1, pmask, t.pair(b, 0), p.tmo, dpair, dpair,
+             sp);
   if (!L.pair_only) {
-    transition_bwd(st, B.mtr, (long)S * N, N, p.m2, nullptr, p.mtr, dmsa, dmsa);
-    msacol_bwd(st, B.col, S, N, p.m1, mmask, nullptr, p.col, dmsa, dmsa);
-    msarow_bwd(st, B.row, S, N, f.min, mmask, p.p1, t.row(b), p.row, dmsa, dmsa, dpair);
-    opm_bwd(st, B.opm, S, N, f.min, mmask, nullptr, p.opm, dpair, dmsa, dmsa);
+    float* sm = ct_scale_slot(2);
+    {
+      KTimed kt("block.ct_scale", st);
+      ct_scale(st, dmsa, (long)S * N * L.Cm, sm);
+    }
+    transition_bwd(st, B.mtr, (long)S * N, N, p.m2, nullptr, p.mtr, dmsa, dmsa, sm);
+    msacol_bwd(st, B.col, S, N, p.m1, mmask, nullptr, p.col, dmsa, dmsa, sm);
+    msarow_bwd(st, B.row, S, N, f.min, mmask, p.p1, t.row(b), p.row, dmsa, dmsa, dpair, sm);
+    opm_bwd(st, B.opm, S, N, f.min, mmask, nullptr, p.opm, dpair, dmsa, dmsa, sp);
   }
 }
 

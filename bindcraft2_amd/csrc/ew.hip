@@ -1,8 +1,99 @@
 // Small elementwise kernels: dropout tables from JAX keys, the JAX key chain of
-// the Evoformer stack, residual/dropout glue of the backward passes.
+// the Evoformer stack, residual/dropout glue of the backward passes, and the
+// backward's cotangent scales.
 #include "kernels.h"
+#include "runtime.h"
+
+#include <algorithm>
+#include <mutex>
 
 namespace bc2n {
+
+// -------------------------------------------------------- cotangent scales
+// {s, 1/s} slots and the partial maxima of ct_scale live in file-scope device
+// arrays (one copy per GPU, resolved per device by hipGetSymbolAddress), so
+// computing a scale allocates nothing.  Calls on one device share them: the
+// backward runs on one stream at a time (the library's single-stream
+// contract).
+namespace {
+constexpr int CT_SLOTS = 8;
+constexpr int CT_PART = 512;  // partial-maximum blocks (grid of the first pass)
+__device__ __align__(256) float g_ct_slots[CT_SLOTS * 2];
+__device__ __align__(256) float g_ct_part[CT_PART];
+
+struct CtPtrs {
+  float* slots = nullptr;
+  float* part = nullptr;
+};
+CtPtrs ct_ptrs() {
+  static std::mutex mu;
+  static CtPtrs per_dev[64];
+  int dev = 0;
+  hip_check(hipGetDevice(&dev), "hipGetDevice");
+  if (dev < 0 || dev >= 64) throw std::runtime_error("ct_scale: device index out of range");
+  std::lock_guard<std::mutex> lk(mu);
+  CtPtrs& p = per_dev[dev];
+  if (!p.slots) {
+    void *a = nullptr, *b = nullptr;
+    hip_check(hipGetSymbolAddress(&a, HIP_SYMBOL(g_ct_slots)), "hipGetSymbolAddress(slots)");
+    hip_check(hipGetSymbolAddress(&b, HIP_SYMBOL(g_ct_part)), "hipGetSymbolAddress(part)");
+    p.slots = static_cast<float*>(a);
+    p.part = static_cast<float*>(b);
+  }
+  return p;
+}
+}  // namespace
+
+// part[block] = max |x| over a grid-stride range (4 floats a load); x and n
+// are 16-byte aligned / a multiple of 4 (checked on the host).
+__global__ __launch_bounds__(256) void amax_part_kernel(const float* __restrict__ x, long n4,
+                                                        float* __restrict__ part) {
+  __shared__ float red[4];
+  float m = 0.f;
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n4; i += (long)gridDim.x * 256) {
+    const float4 v = x4[i];
+    m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+  }
+  m = group_max<64>(m);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) part[blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// sc = {s, 1/s}: s = 2^(4 - e) for max|x| in (2^(e-1), 2^e], so s*max|x| is
+// in (8, 16]; s = 1 when x is all zero or its maximum is not finite.
+__global__ __launch_bounds__(64) void amax_final_kernel(const float* __restrict__ part, int np,
+                                                        float* __restrict__ sc) {
+  float m = 0.f;
+  for (int i = threadIdx.x; i < np; i += 64) m = fmaxf(m, part[i]);
+  m = group_max<64>(m);
+  if (threadIdx.x == 0) {
+    float s = 1.f;
+    if (m > 0.f && m <= 3.0e38f) {
+      int e = 0;
+      (void)frexpf(m, &e);
+      s = ldexpf(1.f, max(-100, min(100, 4 - e)));
+    }
+    sc[0] = s;
+    sc[1] = 1.f / s;
+  }
+}
+
+float* ct_scale_slot(int k) {
+  if (k < 0 || k >= CT_SLOTS) throw std::runtime_error("ct_scale: slot out of range");
+  return ct_ptrs().slots + 2 * k;
+}
+
+void ct_scale(hipStream_t st, const float* x, long n, float* sc) {
+  if (x == nullptr || n <= 0 || n % 4 != 0 || ((uintptr_t)x & 15))
+    throw std::runtime_error("ct_scale: x must be 16-byte aligned with n a positive multiple of 4");
+  const CtPtrs p = ct_ptrs();
+  const long n4 = n / 4;
+  const int blocks = (int)std::min<long>(CT_PART, (n4 + 255) / 256);
+  hipLaunchKernelGGL(amax_part_kernel, dim3(blocks), dim3(256), 0, st, x, n4, p.part);
+  hipLaunchKernelGGL(amax_final_kernel, dim3(1), dim3(64), 0, st, p.part, blocks, sc);
+}
 
 // -------------------------------------------------------------- dropout
 // tbl[b*C+c] = keep ? 1/keep_rate : 0 where keep = uniform(key, (B,C)) < keep_rate

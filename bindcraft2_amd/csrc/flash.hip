@@ -12,8 +12,8 @@
 //   dK/dV:         S = Q K^T         -> lane l owns key l%16, 8 queries
 //                  dV^T += dO^T P,   dK^T += Q^T dS
 //
-// The contraction over the head width uses v_mfma_f32_16x16x32_bf16 (D=32)
-// or v_mfma_f32_16x16x16_bf16 (D=16); the contraction over 32 keys (or 32
+// The contraction over the head width uses v_mfma_f32_16x16x32_f16 (D=32)
+// or v_mfma_f32_16x16x16_f16 (D=16); the contraction over 32 keys (or 32
 // queries) always uses the x32 form.  For that second product the 8 K-slots
 // of lane group g=l/16 are mapped to positions {4g..4g+3, 16+4g..16+4g+3}
 // of the 32-block, for both operands; the first product's result already
@@ -32,7 +32,7 @@
 // matter, 2^13 log2-units (5678 natural units) is far beyond any unmasked
 // logit, and at that magnitude f32 still resolves the row's log-sum-exp
 // (lse = -2^13 + log2 N) to ~1e-3, so the backward's exp2(s - lse) = 1/N on a
-// fully masked row is exact to bf16 precision.
+// fully masked row is exact to h16 precision.
 //
 // The bias gradient (a sum over rows) is accumulated in registers over a
 // chunk of rows and written once per chunk; a second pass adds the chunks in
@@ -52,25 +52,25 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
-// Column read of a row-major bf16 LDS tile T[row][ld] (ld % 4 == 0):
+// Column read of a row-major h16 LDS tile T[row][ld] (ld % 4 == 0):
 // returns, for lane l (column c = l%16, group g = l/16), the four values
 // T[r0 + 4g + j][c0 + c], j = 0..3.  One ds_read_b64_tr_b16: within each
 // 16-lane group, lane m addresses the 8-byte chunk T[r0 + 4g + m/4][c0 + 4(m%4)
 // .. +3] and the instruction returns to lane 4a + c element c of the chunks
 // of lanes a, a+4, a+8, a+12.
-__device__ __forceinline__ bf16x4 ld_tr4(const bf16* T, int ld, int r0, int c0, int lane) {
+__device__ __forceinline__ h16x4 ld_tr4(const h16* T, int ld, int r0, int c0, int lane) {
   const int g = lane >> 4, m = lane & 15;
-  const bf16* p = T + (r0 + 4 * g + (m >> 2)) * ld + c0 + 4 * (m & 3);
+  const h16* p = T + (r0 + 4 * g + (m >> 2)) * ld + c0 + 4 * (m & 3);
   const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p);
-  return __builtin_bit_cast(bf16x4, v);
+  return __builtin_bit_cast(h16x4, v);
 }
 
 // x32 operand over a 32-block at row r0 (slots {4g..4g+3, 16+4g..16+4g+3}),
 // column c0 + l%16 of a row-major LDS tile.
-__device__ __forceinline__ bf16x8 ld_tr8(const bf16* T, int ld, int r0, int c0, int lane) {
-  const bf16x4 a = ld_tr4(T, ld, r0, c0, lane);
-  const bf16x4 b = ld_tr4(T, ld, r0 + 16, c0, lane);
-  bf16x8 r;
+__device__ __forceinline__ h16x8 ld_tr8(const h16* T, int ld, int r0, int c0, int lane) {
+  const h16x4 a = ld_tr4(T, ld, r0, c0, lane);
+  const h16x4 b = ld_tr4(T, ld, r0 + 16, c0, lane);
+  h16x8 r;
   r[0] = a[0]; r[1] = a[1]; r[2] = a[2]; r[3] = a[3];
   r[4] = b[0]; r[5] = b[1]; r[6] = b[2]; r[7] = b[3];
   return r;
@@ -86,8 +86,8 @@ template <int D, int N>
 struct RowPair {
   static constexpr int CPR = D / 8;  // 16-byte chunks per row
   static constexpr int IT = (N * CPR + 255) / 256;
-  bf16x8 va[IT], vb[IT];
-  __device__ __forceinline__ void load(const bf16* sA, long lda, const bf16* sB, long ldb, int tid,
+  h16x8 va[IT], vb[IT];
+  __device__ __forceinline__ void load(const h16* sA, long lda, const h16* sB, long ldb, int tid,
                                        int rows) {
     const int items = rows * CPR;
 #pragma unroll
@@ -99,7 +99,7 @@ struct RowPair {
       }
     }
   }
-  __device__ __forceinline__ void store(bf16* dA, bf16* dB, int tid, int rows) const {
+  __device__ __forceinline__ void store(h16* dA, h16* dB, int tid, int rows) const {
     const int items = rows * CPR;
 #pragma unroll
     for (int i = 0; i < IT; ++i) {
@@ -113,8 +113,8 @@ struct RowPair {
 };
 
 template <int D, int N>
-__device__ __forceinline__ void stage_rows2(bf16* dA, const bf16* sA, long lda, bf16* dB,
-                                            const bf16* sB, long ldb, int tid, int rows = N) {
+__device__ __forceinline__ void stage_rows2(h16* dA, const h16* sA, long lda, h16* dB,
+                                            const h16* sB, long ldb, int tid, int rows = N) {
   RowPair<D, N> p;
   p.load(sA, lda, sB, ldb, tid, rows);
   p.store(dA, dB, tid, rows);
@@ -125,20 +125,20 @@ template <int D>
 struct HFrag;
 template <>
 struct HFrag<32> {
-  bf16x8 v;
-  __device__ __forceinline__ void load(const bf16* row, int g) { v = ld8(row + 8 * g); }
+  h16x8 v;
+  __device__ __forceinline__ void load(const h16* row, int g) { v = ld8(row + 8 * g); }
   __device__ __forceinline__ static f32x4 mma(const HFrag& a, const HFrag& b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a.v, b.v, c, 0, 0, 0);
   }
 };
 template <>
 struct HFrag<16> {
-  bf16x4 v;
-  __device__ __forceinline__ void load(const bf16* row, int g) {
-    v = *reinterpret_cast<const bf16x4*>(row + 4 * g);
+  h16x4 v;
+  __device__ __forceinline__ void load(const h16* row, int g) {
+    v = *reinterpret_cast<const h16x4*>(row + 4 * g);
   }
   __device__ __forceinline__ static f32x4 mma(const HFrag& a, const HFrag& b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a.v, b.v, c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a.v, b.v, c, 0, 0, 0);
   }
 };
 
@@ -162,8 +162,8 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   constexpr int NCH = (NKB + CB - 1) / CB;
   constexpr int CN = 32 * CB;            // keys per chunk
   const int H = a.H;
-  bf16* Ks = reinterpret_cast<bf16*>(smem_raw);          // [CN][LD]
-  bf16* Vs = Ks + CN * LD;                               // [CN][LD]
+  h16* Ks = reinterpret_cast<h16*>(smem_raw);          // [CN][LD]
+  h16* Vs = Ks + CN * LD;                               // [CN][LD]
   float* Mm = reinterpret_cast<float*>(Vs + CN * LD);    // [N] 1 / 0 per key
   float* Ma = Mm + N;                                    // [N] 0 / NEG_LOGIT
 
@@ -177,8 +177,8 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const long tok0 = (long)r * N;
-  const bf16* Kg = a.qkvg + tok0 * a.ld + H * D + h * D;
-  const bf16* Vg = a.qkvg + tok0 * a.ld + 2 * H * D + h * D;
+  const h16* Kg = a.qkvg + tok0 * a.ld + H * D + h * D;
+  const h16* Vg = a.qkvg + tok0 * a.ld + 2 * H * D + h * D;
   stage_rows2<D, CN>(Ks, Kg, a.ld, Vs, Vg, a.ld, tid);
   for (int k = tid; k < N; k += 256) {
     const bool on = a.mask[r * a.mask_sr + k * a.mask_sk] != 0.f;
@@ -191,10 +191,10 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   const int q = min(q0, N - 16) + lq;  // idle waves read in bounds, store nothing
   HFrag<D> qf;
   qf.load(a.qkvg + (tok0 + q) * a.ld + h * D, g);
-  const bf16* grow = a.qkvg + (tok0 + q) * a.ld + 3 * H * D + h * D;
-  bf16x4 gv[DT];
+  const h16* grow = a.qkvg + (tok0 + q) * a.ld + 3 * H * D + h * D;
+  h16x4 gv[DT];
 #pragma unroll
-  for (int dh = 0; dh < DT; ++dh) gv[dh] = *reinterpret_cast<const bf16x4*>(grow + dh * 16 + 4 * g);
+  for (int dh = 0; dh < DT; ++dh) gv[dh] = *reinterpret_cast<const h16x4*>(grow + dh * 16 + 4 * g);
   const float* brow = a.bias ? a.bias + ((long)h * N + q) * N : nullptr;
   const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
   float mx = -INFINITY, lsum = 0.f;
@@ -267,12 +267,12 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
     for (int kb = 0; kb < CB; ++kb) {
       if (c * CB + kb < NKB) {
-        bf16x8 pf;
+        h16x8 pf;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const float p = fast_exp2(sv[kb][e] - mx);
           lsum += p;
-          pf[e] = (bf16)p;
+          pf[e] = (h16)p;
         }
 #pragma unroll
         for (int dh = 0; dh < DT; ++dh)
@@ -288,15 +288,15 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
   for (int dh = 0; dh < DT; ++dh) {
     const int d0 = dh * 16 + 4 * g;
-    bf16x4 ov, gov;
+    h16x4 ov, gov;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float o = acc[dh][i] * inv;
-      ov[i] = (bf16)o;
-      gov[i] = (bf16)(o * sigmoidf_((float)gv[dh][i]));
+      ov[i] = (h16)o;
+      gov[i] = (h16)(o * sigmoidf_((float)gv[dh][i]));
     }
-    *reinterpret_cast<bf16x4*>(a.o + orow + d0) = ov;
-    *reinterpret_cast<bf16x4*>(a.og + orow + d0) = gov;
+    *reinterpret_cast<h16x4*>(a.o + orow + d0) = ov;
+    *reinterpret_cast<h16x4*>(a.og + orow + d0) = gov;
   }
   if (g == 0) a.lse[((long)r * H + h) * N + q] = mx + __log2f(lsum);
 }
@@ -317,10 +317,10 @@ __global__ __launch_bounds__(256) void attn_fwd_rows_kernel(AttnArgs a, int rpc)
   static_assert(NKB <= 8, "one key chunk");
   constexpr int QR = 64;       // query rows of the workgroup
   const int H = a.H;
-  bf16* Ks = reinterpret_cast<bf16*>(smem_raw);          // [N][LD]
-  bf16* Vs = Ks + N * LD;                                // [N][LD]
-  bf16* Qs = Vs + N * LD;                                // [QR][LD]
-  bf16* Gs = Qs + QR * LD;                               // [QR][LD]
+  h16* Ks = reinterpret_cast<h16*>(smem_raw);          // [N][LD]
+  h16* Vs = Ks + N * LD;                                // [N][LD]
+  h16* Qs = Vs + N * LD;                                // [QR][LD]
+  h16* Gs = Qs + QR * LD;                               // [QR][LD]
   float* Mm = reinterpret_cast<float*>(Gs + QR * LD);    // [N] 1 / 0 per key
   float* Ma = Mm + N;                                    // [N] 0 / NEG_LOGIT
 
@@ -368,7 +368,7 @@ __global__ __launch_bounds__(256) void attn_fwd_rows_kernel(AttnArgs a, int rpc)
   constexpr int QCH = QR * (D / 8);  // 16-byte chunks of the q (or gate) tile
   static_assert(2 * QCH <= 512, "q and gate: at most two chunks per thread");
   RowPair<D, N> nkv;
-  bf16x8 nq, ng;
+  h16x8 nq, ng;
   float nm = 0.f;
   const int qrow = tid / (D / 8), qc = (tid % (D / 8)) * 8;  // tid < QCH
   const int qtok = min(qb * QR + qrow, N - 1);               // rows past N: any in-bounds row
@@ -377,7 +377,7 @@ __global__ __launch_bounds__(256) void attn_fwd_rows_kernel(AttnArgs a, int rpc)
     nkv.load(a.qkvg + tok0 * a.ld + HD + h * D, a.ld, a.qkvg + tok0 * a.ld + 2 * HD + h * D, a.ld,
              tid, N);
     if (tid < QCH) {
-      const bf16* row = a.qkvg + (tok0 + qtok) * a.ld + h * D + qc;
+      const h16* row = a.qkvg + (tok0 + qtok) * a.ld + h * D + qc;
       nq = ld8(row);
       ng = ld8(row + 3 * HD);
     }
@@ -439,12 +439,12 @@ __global__ __launch_bounds__(256) void attn_fwd_rows_kernel(AttnArgs a, int rpc)
     for (int i = 0; i < DT; ++i) acc[i] = z4;
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
-      bf16x8 pf;
+      h16x8 pf;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float p = fast_exp2(sv[kb][e] - mx);
         lsum += p;
-        pf[e] = (bf16)p;
+        pf[e] = (h16)p;
       }
 #pragma unroll
       for (int dh = 0; dh < DT; ++dh)
@@ -459,16 +459,16 @@ __global__ __launch_bounds__(256) void attn_fwd_rows_kernel(AttnArgs a, int rpc)
 #pragma unroll
       for (int dh = 0; dh < DT; ++dh) {
         const int d0 = dh * 16 + 4 * g;
-        const bf16x4 gv = *reinterpret_cast<const bf16x4*>(&Gs[(wave * 16 + lq) * LD + d0]);
-        bf16x4 ov, gov;
+        const h16x4 gv = *reinterpret_cast<const h16x4*>(&Gs[(wave * 16 + lq) * LD + d0]);
+        h16x4 ov, gov;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float o = acc[dh][i] * inv;
-          ov[i] = (bf16)o;
-          gov[i] = (bf16)(o * sigmoidf_((float)gv[i]));
+          ov[i] = (h16)o;
+          gov[i] = (h16)(o * sigmoidf_((float)gv[i]));
         }
-        *reinterpret_cast<bf16x4*>(a.o + orow + d0) = ov;
-        *reinterpret_cast<bf16x4*>(a.og + orow + d0) = gov;
+        *reinterpret_cast<h16x4*>(a.o + orow + d0) = ov;
+        *reinterpret_cast<h16x4*>(a.og + orow + d0) = gov;
       }
       if (g == 0) a.lse[((long)r * H + h) * N + q] = mx + __log2f(lsum);
     }
@@ -490,18 +490,18 @@ __global__ __launch_bounds__(256) void attn_gate_bwd_kernel(AttnBwdArgs b) {
   const long tok = idx / a.H;
   const int HD = a.H * D;
   const int c0 = h * D + part * 8;
-  const bf16x8 gv = ld8(a.qkvg + tok * a.ld + 3 * HD + c0);
-  const bf16x8 ov = ld8(a.o + tok * a.ldo + c0);
-  const bf16x8 dv = ld8(b.dog + tok * a.ldo + c0);
-  bf16x8 dov, dgv;
+  const h16x8 gv = ld8(a.qkvg + tok * a.ld + 3 * HD + c0);
+  const h16x8 ov = ld8(a.o + tok * a.ldo + c0);
+  const h16x8 dv = ld8(b.dog + tok * a.ldo + c0);
+  h16x8 dov, dgv;
   float s = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const float sg = sigmoidf_((float)gv[e]);
     const float o = (float)ov[e], d = (float)dv[e];
     const float dO = d * sg;
-    dov[e] = (bf16)dO;
-    dgv[e] = (bf16)(d * o * sg * (1.f - sg));
+    dov[e] = (h16)dO;
+    dgv[e] = (h16)(d * o * sg * (1.f - sg));
     s += dO * o;
   }
   st8(b.dO + tok * a.ldo + c0, dov);
@@ -529,8 +529,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs b) {
   constexpr int NCH = (NKB + CB - 1) / CB;
   constexpr int CN = 32 * CB;
   const int H = a.H;
-  bf16* Ks = reinterpret_cast<bf16*>(smem_raw);   // [CN][LD]
-  bf16* Vs = Ks + CN * LD;                        // [CN][LD]
+  h16* Ks = reinterpret_cast<h16*>(smem_raw);   // [CN][LD]
+  h16* Vs = Ks + CN * LD;                        // [CN][LD]
   float* Ms = reinterpret_cast<float*>(Vs + CN * LD);  // [N]
 
   const int nqb = (N + 63) / 64;
@@ -543,8 +543,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs b) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const long tok0 = (long)r * N;
-  const bf16* Kg = a.qkvg + tok0 * a.ld + H * D + h * D;
-  const bf16* Vg = a.qkvg + tok0 * a.ld + 2 * H * D + h * D;
+  const h16* Kg = a.qkvg + tok0 * a.ld + H * D + h * D;
+  const h16* Vg = a.qkvg + tok0 * a.ld + 2 * H * D + h * D;
   stage_rows2<D, CN>(Ks, Kg, a.ld, Vs, Vg, a.ld, tid);
   // additive key mask: a masked key's exponent becomes -inf, so p = dS = 0
   for (int k = tid; k < N; k += 256)
@@ -606,7 +606,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs b) {
 #pragma unroll
     for (int kb = 0; kb < CB; ++kb) {
       if (c * CB + kb < NKB) {
-        bf16x8 dsf;
+        h16x8 dsf;
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh) {
           const int krow = (kb * 32 + kh * 16 + lq) * LD;
@@ -619,7 +619,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs b) {
           const f32x4 s = HFrag<D>::mma(kf, qf, cs);    // S + bias - lse
           const f32x4 dp = HFrag<D>::mma(vf, dof, nD);  // dP - Dsum
 #pragma unroll
-          for (int i = 0; i < 4; ++i) dsf[kh * 4 + i] = (bf16)(fast_exp2(s[i]) * dp[i]);
+          for (int i = 0; i < 4; ++i) dsf[kh * 4 + i] = (h16)(fast_exp2(s[i]) * dp[i]);
         }
 #pragma unroll
         for (int dh = 0; dh < DT; ++dh)
@@ -628,13 +628,13 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs b) {
     }
   }
   if (q0 >= N) return;
-  bf16* out = b.dqkvg + (tok0 + q) * a.ld + h * D;
+  h16* out = b.dqkvg + (tok0 + q) * a.ld + h * D;
 #pragma unroll
   for (int dh = 0; dh < DT; ++dh) {
-    bf16x4 v;
+    h16x4 v;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = (bf16)(acc[dh][i] * b.scale);
-    *reinterpret_cast<bf16x4*>(out + dh * 16 + 4 * g) = v;
+    for (int i = 0; i < 4; ++i) v[i] = (h16)(acc[dh][i] * b.scale);
+    *reinterpret_cast<h16x4*>(out + dh * 16 + 4 * g) = v;
   }
 }
 
@@ -652,10 +652,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_rows_kernel(AttnBwdArgs b, in
   static_assert(NKB <= 8, "one key chunk");
   constexpr int QR = 64;
   const int H = a.H;
-  bf16* Ks = reinterpret_cast<bf16*>(smem_raw);         // [N][LD]
-  bf16* Vs = Ks + N * LD;                               // [N][LD]
-  bf16* Qs = Vs + N * LD;                               // [QR][LD]
-  bf16* Os = Qs + QR * LD;                              // [QR][LD] dO
+  h16* Ks = reinterpret_cast<h16*>(smem_raw);         // [N][LD]
+  h16* Vs = Ks + N * LD;                               // [N][LD]
+  h16* Qs = Vs + N * LD;                               // [QR][LD]
+  h16* Os = Qs + QR * LD;                              // [QR][LD] dO
   float* Ms = reinterpret_cast<float*>(Os + QR * LD);   // [N] 0 / -inf per key
   float* Ls = Ms + N;                                   // [QR] lse
   float* Dl = Ls + QR;                                  // [QR] Dsum
@@ -699,7 +699,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_rows_kernel(AttnBwdArgs b, in
 
   constexpr int QCH = QR * (D / 8);
   RowPair<D, N> nkv;
-  bf16x8 nq, no;
+  h16x8 nq, no;
   float nm = 0.f, nl = 0.f, nd = 0.f;
   const int qrow = tid / (D / 8), qc = (tid % (D / 8)) * 8;  // tid < QCH
   const int qtok = min(qb * QR + qrow, N - 1);
@@ -749,7 +749,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_rows_kernel(AttnBwdArgs b, in
     for (int i = 0; i < DT; ++i) acc[i] = z4;
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
-      bf16x8 dsf;
+      h16x8 dsf;
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh) {
         const int krow = (kb * 32 + kh * 16 + lq) * LD;
@@ -765,20 +765,20 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_rows_kernel(AttnBwdArgs b, in
         const f32x4 s = HFrag<D>::mma(kf, qf, cs);    // S + bias - lse
         const f32x4 dp = HFrag<D>::mma(vf, dof, nD);  // dP - Dsum
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dsf[kh * 4 + i] = (bf16)(fast_exp2(s[i]) * dp[i]);
+        for (int i = 0; i < 4; ++i) dsf[kh * 4 + i] = (h16)(fast_exp2(s[i]) * dp[i]);
       }
 #pragma unroll
       for (int dh = 0; dh < DT; ++dh)
         acc[dh] = mfma16x16x32(ld_tr8(Ks, LD, kb * 32, dh * 16, lane), dsf, acc[dh]);
     }
     if (q0 + 16 <= N || lq < N - q0) {
-      bf16* out = b.dqkvg + ((long)r * N + q) * a.ld + h * D;
+      h16* out = b.dqkvg + ((long)r * N + q) * a.ld + h * D;
 #pragma unroll
       for (int dh = 0; dh < DT; ++dh) {
-        bf16x4 v;
+        h16x4 v;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = (bf16)(acc[dh][i] * b.scale);
-        *reinterpret_cast<bf16x4*>(out + dh * 16 + 4 * g) = v;
+        for (int i = 0; i < 4; ++i) v[i] = (h16)(acc[dh][i] * b.scale);
+        *reinterpret_cast<h16x4*>(out + dh * 16 + 4 * g) = v;
       }
     }
   }
@@ -814,13 +814,13 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
   static_assert(NCH == 1 || CQB % QS == 0, "chunk must hold whole rounds of query groups");
   const AttnArgs& a = b.f;
   const int H = a.H;
-  bf16* Qs = reinterpret_cast<bf16*>(smem_raw);         // [CN][LD]
-  bf16* Os = Qs + CN * LD;                              // [CN][LD] dO
+  h16* Qs = reinterpret_cast<h16*>(smem_raw);         // [CN][LD]
+  h16* Os = Qs + CN * LD;                              // [CN][LD] dO
   float* Ls = reinterpret_cast<float*>(Os + CN * LD);   // [N] -lse
   float* Ds = Ls + N;                                   // [N] -Dsum
   float* Xs = Ds + N;                                   // [QS-1][KT][K,V][DT*4][64]
   float* Ms = Xs + (QS - 1) * KT * 2 * DT * 4 * 64;     // [N] key mask of the row
-  bf16* KVs = reinterpret_cast<bf16*>(Ms + N);          // [K,V][16*KT][LD] own keys
+  h16* KVs = reinterpret_cast<h16*>(Ms + N);          // [K,V][16*KT][LD] own keys
 
   constexpr int NKW = N / (16 * KT);  // key groups per (chunk, head)
   const long G = (long)((a.R + b.rows_per_chunk - 1) / b.rows_per_chunk) * H * NKW;
@@ -872,7 +872,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
   float nls[NPT], nds[NPT], nmask[NPT];
   constexpr int KCH = 16 * KT * 2 * (D / 8);  // 16-byte chunks of own K and V
   static_assert(KCH <= 256, "own keys: one chunk per thread");
-  bf16x8 nkv;
+  h16x8 nkv;
   const int kvi = tid % (KCH / 2), kvs = tid / (KCH / 2);  // chunk, 0 = K / 1 = V
   const int kvrow = kvi / (D / 8), kvc = (kvi % (D / 8)) * 8;
   auto prefetch = [&](int s) {
@@ -945,7 +945,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
       if (blk < NQB) {
         const int qb = blk * 32;         // query index
         const int ql = qb - c * CN;      // row in the staged chunk
-        bf16x8 pf, dsf;
+        h16x8 pf, dsf;
 #pragma unroll
         for (int qh = 0; qh < 2; ++qh) {
           HFrag<D> qa, da;
@@ -965,8 +965,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
           for (int i = 0; i < 4; ++i) {
             const float p = fast_exp2(mk ? s4[i] : xm);
             const float ds = mk ? p * dp[i] : 0.f;
-            pf[qh * 4 + i] = (bf16)p;
-            dsf[qh * 4 + i] = (bf16)ds;
+            pf[qh * 4 + i] = (h16)p;
+            dsf[qh * 4 + i] = (h16)ds;
             dbias[ib][qh * 4 + i] += ds;
           }
         }
@@ -1005,18 +1005,18 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
           }
       }
       // dK (w.r.t. the unscaled k) = sum_q dS * q_scaled / log2(e)
-      bf16* dk = b.dqkvg + (tok0 + k) * a.ld + HD + h * D;
-      bf16* dvp = b.dqkvg + (tok0 + k) * a.ld + 2 * HD + h * D;
+      h16* dk = b.dqkvg + (tok0 + k) * a.ld + HD + h * D;
+      h16* dvp = b.dqkvg + (tok0 + k) * a.ld + 2 * HD + h * D;
 #pragma unroll
       for (int dh = 0; dh < DT; ++dh) {
-        bf16x4 kv, vv;
+        h16x4 kv, vv;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          kv[i] = (bf16)(accK[dh][i] * (1.f / LOG2E));
-          vv[i] = (bf16)accV[dh][i];
+          kv[i] = (h16)(accK[dh][i] * (1.f / LOG2E));
+          vv[i] = (h16)accV[dh][i];
         }
-        *reinterpret_cast<bf16x4*>(dk + dh * 16 + 4 * g) = kv;
-        *reinterpret_cast<bf16x4*>(dvp + dh * 16 + 4 * g) = vv;
+        *reinterpret_cast<h16x4*>(dk + dh * 16 + 4 * g) = kv;
+        *reinterpret_cast<h16x4*>(dvp + dh * 16 + 4 * g) = vv;
       }
     }
   }

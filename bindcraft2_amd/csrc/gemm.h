@@ -1,4 +1,4 @@
-// LDS-tiled bf16 MFMA GEMM for gfx950 with fused, caller-supplied epilogues.
+// LDS-tiled binary16 MFMA GEMM for gfx950 with fused, caller-supplied epilogues.
 //
 //   C_b[m, n] = sum_k A_b[m, k] * B_b[n, k]        (f32 accumulation)
 //
@@ -7,15 +7,10 @@
 // form on its way into LDS, so the MFMA fragments are always read the same
 // way.  A 256-thread workgroup (4 waves, 2x2) owns a BM x BN tile; each wave
 // owns (BM/2) x (BN/2) as a grid of 16x16 MFMA tiles fed by
-// v_mfma_f32_16x16x32_bf16.  K is walked in BK steps with a register prefetch
+// v_mfma_f32_16x16x32_f16.  K is walked in BK steps with a register prefetch
 // of the next step's tile: 32-deep steps (K <= 128) into a second LDS buffer,
 // 64-deep steps into the one buffer after a barrier, so that either way the
 // operand buffers take at most 40 KB and four workgroups share a CU.
-//
-// With F16 the operand words are IEEE binary16 instead (the 16-bit words of
-// A and B hold halfs; v_mfma_f32_16x16x32_f16, same rate): for products of
-// bounded operands (LayerNorm outputs and weights) that need the 3 extra
-// significand bits.
 //
 // Epilogue: the f32 accumulator tile is staged through LDS (reusing the
 // operand buffers, half a tile per pass) and handed to the epilogue as
@@ -34,10 +29,9 @@ namespace bc2n {
 
 struct GemmArgs {
   int M = 0, N = 0, K = 0, batch = 1;
-  // 16-bit operand words: bf16, or binary16 when the launch says F16
-  const bf16* A = nullptr;
+  const h16* A = nullptr;
   long a_sm = 0, a_sk = 0, a_sb = 0;  // element strides; a_sm==1 or a_sk==1
-  const bf16* B = nullptr;
+  const h16* B = nullptr;
   long b_sn = 0, b_sk = 0, b_sb = 0;  // element strides; b_sn==1 or b_sk==1
 };
 
@@ -52,44 +46,32 @@ __device__ __forceinline__ void st_f8(float* p, const float (&v)[8]) {
   reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
   reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
 }
-__device__ __forceinline__ void ld_b8f(const bf16* p, float (&v)[8]) {
-  const bf16x8 a = ld8(p);
+__device__ __forceinline__ void ld_h8f(const h16* p, float (&v)[8]) {
+  const h16x8 a = ld8(p);
 #pragma unroll
   for (int e = 0; e < 8; ++e) v[e] = (float)a[e];
 }
-__device__ __forceinline__ void st_b8f(bf16* p, const float (&v)[8]) {
-  bf16x8 a;
+// Epilogue stores round with saturation (f2h_sat): the backward's tensors
+// are scaled cotangents, and a masked row may hold a huge finite value that
+// a zero mask removes later.
+__device__ __forceinline__ void st_h8f(h16* p, const float (&v)[8]) {
+  h16x8 a;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) a[e] = (bf16)v[e];
+  for (int e = 0; e < 8; ++e) a[e] = f2h_sat(v[e]);
   st8(p, a);
-}
-__device__ __forceinline__ void ld_h8f(const f16* p, float (&v)[8]) {
-  const f16x8 a = __builtin_bit_cast(f16x8, ld8(reinterpret_cast<const bf16*>(p)));
-#pragma unroll
-  for (int e = 0; e < 8; ++e) v[e] = (float)a[e];
-}
-__device__ __forceinline__ void st_h8f(f16* p, const float (&v)[8]) {
-  f16x8 a;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) a[e] = (f16)v[e];
-  st8(reinterpret_cast<bf16*>(p), __builtin_bit_cast(bf16x8, a));
 }
 template <class T>
 __device__ __forceinline__ void st_any8(T* p, const float (&v)[8]);
 template <>
 __device__ __forceinline__ void st_any8<float>(float* p, const float (&v)[8]) { st_f8(p, v); }
 template <>
-__device__ __forceinline__ void st_any8<bf16>(bf16* p, const float (&v)[8]) { st_b8f(p, v); }
-template <>
-__device__ __forceinline__ void st_any8<f16>(f16* p, const float (&v)[8]) { st_h8f(p, v); }
+__device__ __forceinline__ void st_any8<h16>(h16* p, const float (&v)[8]) { st_h8f(p, v); }
 template <class T>
 __device__ __forceinline__ void ld_any8(const T* p, float (&v)[8]);
 template <>
 __device__ __forceinline__ void ld_any8<float>(const float* p, float (&v)[8]) { ld_f8(p, v); }
 template <>
-__device__ __forceinline__ void ld_any8<bf16>(const bf16* p, float (&v)[8]) { ld_b8f(p, v); }
-template <>
-__device__ __forceinline__ void ld_any8<f16>(const f16* p, float (&v)[8]) { ld_h8f(p, v); }
+__device__ __forceinline__ void ld_any8<h16>(const h16* p, float (&v)[8]) { ld_h8f(p, v); }
 
 // An epilogue with kTwoPhase = true runs both modes on a column-mode tile:
 // first `col` (which may rewrite the staged tile through its pointer), then,
@@ -115,7 +97,7 @@ struct EpiRows {
   __device__ __forceinline__ void col(int, int, int, const float (&)[8], const float*, int) const {}
 };
 
-// A-operand loaders.  The default reads bf16 A as the strides say; the
+// A-operand loaders.  The default reads h16 A as the strides say; the
 // others build the K-contiguous A tile from f32 rows on the fly, so the
 // elementwise pass that would have written A to memory disappears.  A loader
 // with a side output (kSide) writes it as it loads, which is exact only when
@@ -124,11 +106,12 @@ struct EpiRows {
 struct ALoadDirect {
   static constexpr bool kDirect = true;
   static constexpr bool kSide = false;
-  __device__ __forceinline__ bf16x8 operator()(int, int, int) const { return bf16x8{}; }
+  __device__ __forceinline__ h16x8 operator()(int, int, int) const { return h16x8{}; }
 };
 
-// A[m][k] = bf16(src[src(m)][k] * tbl[(m % nt) * C + k]); src(m) transposes
-// the nt x nt grid when `transpose`; tbl may be null (no dropout).
+// A[m][k] = h16(s * src[src(m)][k] * tbl[(m % nt) * C + k]); src(m)
+// transposes the nt x nt grid when `transpose`; tbl may be null (no dropout);
+// s = *mul, the backward's cotangent scale (1 when mul is null).
 struct ALoadScaledRows {
   static constexpr bool kDirect = false;
   static constexpr bool kSide = false;
@@ -136,19 +119,24 @@ struct ALoadScaledRows {
   const float* tbl;
   int nt, C;
   bool transpose;
-  __device__ __forceinline__ bf16x8 operator()(int, int m, int k) const {
+  const float* mul = nullptr;
+  __device__ __forceinline__ h16x8 operator()(int, int m, int k) const {
     const long s = transpose ? (long)(m % nt) * nt + m / nt : m;
     float v[8];
     ld_f8(src + s * C + k, v);
+    const float sm = mul ? *mul : 1.f;
     if (tbl) {
       float t[8];
       ld_f8(tbl + (long)(m % nt) * C + k, t);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] *= t[e];
-    }
-    bf16x8 r;
+      for (int e = 0; e < 8; ++e) v[e] *= t[e] * sm;
+    } else {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) r[e] = (bf16)v[e];
+      for (int e = 0; e < 8; ++e) v[e] *= sm;
+    }
+    h16x8 r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = f2h_sat(v[e]);
     return r;
   }
 };
@@ -165,8 +153,7 @@ struct GemmSmem {
   static constexpr int BYTES = AB > T ? AB : T;
 };
 
-template <int BM, int BN, int BK, bool AK, bool BKC, class Epi, class AL = ALoadDirect,
-          bool F16 = false>
+template <int BM, int BN, int BK, bool AK, bool BKC, class Epi, class AL = ALoadDirect>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi, AL al = AL{}) {
   using SM = GemmSmem<BM, BN, BK>;
   constexpr int WM = BM / 2, WN = BN / 2;
@@ -176,8 +163,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi, AL al = 
   constexpr int B_CH = BN * BK / 8 / 256;
   static_assert(A_CH >= 1 && B_CH >= 1, "tile too small for 256 threads");
   __shared__ __attribute__((aligned(16))) unsigned char smem[SM::BYTES];
-  bf16* As = reinterpret_cast<bf16*>(smem);            // [2][BM * LDK]
-  bf16* Bs = As + SM::NBUF * BM * LDK;                 // [NBUF][BN * LDK]
+  h16* As = reinterpret_cast<h16*>(smem);            // [2][BM * LDK]
+  h16* Bs = As + SM::NBUF * BM * LDK;                 // [NBUF][BN * LDK]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -190,12 +177,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi, AL al = 
   const int b = (int)(bid / tiles), t = (int)(bid % tiles);
   const int m0 = (t / tiles_n) * BM;
   const int n0 = (t % tiles_n) * BN;
-  const bf16* __restrict__ A = g.A + (long)b * g.a_sb;
-  const bf16* __restrict__ B = g.B + (long)b * g.b_sb;
+  const h16* __restrict__ A = g.A + (long)b * g.a_sb;
+  const h16* __restrict__ B = g.B + (long)b * g.b_sb;
   const int M = g.M, N = g.N;
 
-  bf16x8 ra[A_CH], rb[B_CH];
-  const bf16x8 zero8 = {};
+  h16x8 ra[A_CH], rb[B_CH];
+  const h16x8 zero8 = {};
 
   auto gload = [&](int k0) {
 #pragma unroll
@@ -227,8 +214,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi, AL al = 
     }
   };
   auto sstore = [&](int buf) {
-    bf16* as = As + buf * BM * LDK;
-    bf16* bs = Bs + buf * BN * LDK;
+    h16* as = As + buf * BM * LDK;
+    h16* bs = Bs + buf * BN * LDK;
 #pragma unroll
     for (int p = 0; p < A_CH; ++p) {
       const int c = tid + 256 * p;
@@ -268,12 +255,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi, AL al = 
   const int fr = lane & 15, fk = (lane >> 4) * 8;
   for (int kt = 0; kt < nk; ++kt) {
     const int buf = SM::NBUF == 2 ? (kt & 1) : 0;
-    const bf16* as = As + buf * BM * LDK;
-    const bf16* bs = Bs + buf * BN * LDK;
+    const h16* as = As + buf * BM * LDK;
+    const h16* bs = Bs + buf * BN * LDK;
     if (kt + 1 < nk) gload((kt + 1) * BK);
 #pragma unroll
     for (int kk = 0; kk < BK / 32; ++kk) {
-      bf16x8 af[TM], bfr[TN];
+      h16x8 af[TM], bfr[TN];
 #pragma unroll
       for (int i = 0; i < TM; ++i)
         af[i] = ld8(&as[(wm * WM + i * 16 + fr) * LDK + kk * 32 + fk]);
@@ -283,10 +270,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi, AL al = 
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          if constexpr (F16) acc[i][j] = mfma16x16x32_f16(af[i], bfr[j], acc[i][j]);
-          else acc[i][j] = mfma16x16x32(af[i], bfr[j], acc[i][j]);
-        }
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma16x16x32(af[i], bfr[j], acc[i][j]);
     }
     if constexpr (SM::NBUF == 2) {
       if (kt + 1 < nk) sstore(buf ^ 1);
@@ -355,9 +339,8 @@ inline void gemm_check(bool ok, const char* what) {
 // Launch with tile BM x BN; picks the loader form from the strides and BK
 // from K.  Shapes are validated here, on the host, before any launch.  With a
 // loader other than ALoadDirect, A is K-contiguous by construction (g.A is
-// not read; a_sk must be 1).  F16: the operand words are binary16 (the A
-// loader, if any, must produce binary16 words too).
-template <int BM, int BN, bool F16 = false, class Epi, class AL = ALoadDirect>
+// not read; a_sk must be 1).
+template <int BM, int BN, class Epi, class AL = ALoadDirect>
 void gemm(hipStream_t st, const GemmArgs& g, const Epi& epi, const char* name = "gemm",
           const AL& al = AL{}) {
   if constexpr (!AL::kDirect) gemm_check(g.a_sk == 1, "A loader: K-contiguous A");
@@ -390,7 +373,7 @@ void gemm(hipStream_t st, const GemmArgs& g, const Epi& epi, const char* name = 
   const bool k128 = (g.K % 128 == 0) && g.K >= 256 && (long)tiles * g.batch * 8 <= device_cus();
   KTimed kt(name, st);
 #define BC2N_GEMM_LAUNCH(BKV, AKV, BKCV) \
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, BKV, AKV, BKCV, Epi, AL, F16>), grid, block, 0, st, g, epi, al)
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, BKV, AKV, BKCV, Epi, AL>), grid, block, 0, st, g, epi, al)
   if (k128) {
     if (ak && bk) BC2N_GEMM_LAUNCH(128, true, true);
     else if (ak) BC2N_GEMM_LAUNCH(128, true, false);
@@ -412,7 +395,7 @@ void gemm(hipStream_t st, const GemmArgs& g, const Epi& epi, const char* name = 
 
 // ---------------------------------------------------------------- epilogues
 
-// C[b][m][n] = act(acc + bias[n]) (+= existing when ACC), OutT in {float, bf16}.
+// C[b][m][n] = act(acc + bias[n]) (+= existing when ACC), OutT in {float, h16}.
 template <class OutT, bool RELU = false, bool ACC = false>
 struct EpiStore : EpiRows {
   OutT* C;
@@ -446,15 +429,15 @@ struct EpiStore : EpiRows {
   }
 };
 
-// bf16 store of acc + bias[n], columns n < qcols additionally scaled by
+// h16 store of acc + bias[n], columns n < qcols additionally scaled by
 // qscale (attention projections: q carries D^-1/2 log2 e).
 struct EpiScaledCols : EpiRows {
-  bf16* C;
+  h16* C;
   long ldc;
   const float* bias;
   float qscale;
   int qcols;
-  EpiScaledCols(bf16* c, long l, const float* b, float q, int qc)
+  EpiScaledCols(h16* c, long l, const float* b, float q, int qc)
       : C(c), ldc(l), bias(b), qscale(q), qcols(qc) {}
   __device__ __forceinline__ void row(int, int m, int n, const float (&v)[8]) const {
     float bb[8], x[8];
@@ -462,7 +445,7 @@ struct EpiScaledCols : EpiRows {
     const float s = n < qcols ? qscale : 1.f;  // qcols is a multiple of 8
 #pragma unroll
     for (int e = 0; e < 8; ++e) x[e] = (v[e] + bb[e]) * s;
-    st_b8f(C + (long)m * ldc + n, x);
+    st_h8f(C + (long)m * ldc + n, x);
   }
 };
 
@@ -502,27 +485,27 @@ struct EpiResidualRows : EpiRows {
 // for token m = r * Ntok + q.  The D/8 row-mode calls of one head come from
 // consecutive lanes (8 columns each), which add their partials by DPP.
 struct EpiGateBwd : EpiRows {
-  const bf16* qkvg;  // gate pre-activation at column 3*HD + n of row m
+  const h16* qkvg;  // gate pre-activation at column 3*HD + n of row m
   long ld;
-  const bf16* o;     // ungated attention output [M][HD]
-  bf16* dO;          // [M][HD]
-  bf16* dqkvg;       // dG at column 3*HD + n
+  const h16* o;     // ungated attention output [M][HD]
+  h16* dO;          // [M][HD]
+  h16* dqkvg;       // dG at column 3*HD + n
   float* Dsum;       // [R][H][Ntok]
   int HD, H, D, Ntok;
   template <int W>
   __device__ __forceinline__ float head_sum(float s) const { return group_sum<W>(s); }
   __device__ __forceinline__ void row(int, int m, int n, const float (&v)[8]) const {
-    const bf16x8 gv = ld8(qkvg + (long)m * ld + 3 * HD + n);
-    const bf16x8 ov = ld8(o + (long)m * HD + n);
-    bf16x8 dov, dgv;
+    const h16x8 gv = ld8(qkvg + (long)m * ld + 3 * HD + n);
+    const h16x8 ov = ld8(o + (long)m * HD + n);
+    h16x8 dov, dgv;
     float s = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float sg = sigmoidf_((float)gv[e]);
       const float oo = (float)ov[e];
       const float d = v[e] * sg;
-      dov[e] = (bf16)d;
-      dgv[e] = (bf16)(v[e] * oo * sg * (1.f - sg));
+      dov[e] = f2h_sat(d);
+      dgv[e] = f2h_sat(v[e] * oo * sg * (1.f - sg));
       s += d * oo;
     }
     st8(dO + (long)m * HD + n, dov);
@@ -535,9 +518,9 @@ struct EpiGateBwd : EpiRows {
   }
 };
 
-// dH = acc * (H > 0): backward through a ReLU of the kept tensor H (bf16
+// dH = acc * (H > 0): backward through a ReLU of the kept tensor H (h16
 // or binary16).
-template <class OutT = bf16, class HT = bf16>
+template <class OutT = h16, class HT = h16>
 struct EpiReluMask : EpiRows {
   OutT* C;
   const HT* H;
@@ -554,16 +537,16 @@ struct EpiReluMask : EpiRows {
   }
 };
 
-// A[m][k] = relu(src[m][k]) of a kept bf16 tensor (row stride C).
-struct ALoadReluBf16 {
+// A[m][k] = relu(src[m][k]) of a kept h16 tensor (row stride C).
+struct ALoadRelu16 {
   static constexpr bool kDirect = false;
   static constexpr bool kSide = false;
-  const bf16* src;
+  const h16* src;
   int C;
-  __device__ __forceinline__ bf16x8 operator()(int, int m, int k) const {
-    bf16x8 v = ld8(src + (long)m * C + k);
+  __device__ __forceinline__ h16x8 operator()(int, int m, int k) const {
+    h16x8 v = ld8(src + (long)m * C + k);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = (float)v[e] > 0.f ? v[e] : (bf16)0.f;
+    for (int e = 0; e < 8; ++e) v[e] = (float)v[e] > 0.f ? v[e] : (h16)0.f;
     return v;
   }
 };
@@ -573,27 +556,34 @@ struct ALoadReluBf16 {
 // d(LN output) of a module's input projections), C = BN = 128 channels, with
 // the residual cotangent added:
 //   out[src] = dres[src] + rstd * (g - mean(g) - xhat * mean(g * xhat)),
-//   g = gamma * (dy + sum_h dbias[h][m] wb[c][h]),  xhat = (x[src] - mean) * rstd,
-// src = ln_src_row(m, nt) (the transposed orientation when nt > 0).  dres
-// may alias out.  16 lanes per row (a DPP row), 8 channels each.
+//   g = gs * gamma * (dy + sum_h dbias[h][m] wb[c][h]),  xhat = (x[src] - mean) * rstd,
+// src = ln_src_row(m, nt) (the transposed orientation when nt > 0), gs =
+// *gmul (the module's inverse cotangent scale; 1 when null).  dres may alias
+// out.  16 lanes per row (a DPP row), 8 channels each.
 template <int H>
 struct EpiLnBwd : EpiRows {
   static constexpr bool kRowBlock = true;
   static constexpr int C = 128;
-  const float *x, *gamma, *mean, *rstd, *dres, *dbias, *wb;
+  const float *x, *gamma, *mean, *rstd, *dres, *dbias, *wb, *gmul;
   float* out;
   long M;
   int nt;
   EpiLnBwd(const float* x_, const float* g_, const float* mu_, const float* rs_, const float* dres_,
-           float* out_, long M_, int nt_, const float* dbias_ = nullptr, const float* wb_ = nullptr)
-      : x(x_), gamma(g_), mean(mu_), rstd(rs_), dres(dres_), dbias(dbias_), wb(wb_), out(out_),
-        M(M_), nt(nt_) {}
+           float* out_, long M_, int nt_, const float* dbias_ = nullptr, const float* wb_ = nullptr,
+           const float* gmul_ = nullptr)
+      : x(x_), gamma(g_), mean(mu_), rstd(rs_), dres(dres_), dbias(dbias_), wb(wb_), gmul(gmul_),
+        out(out_), M(M_), nt(nt_) {}
   __device__ __forceinline__ void row(int, int, int, const float (&)[8]) const {}
   template <int WM>
   __device__ __forceinline__ void block(int, long mb, const float* T, int ldt, int tid) const {
     const int lr = tid >> 4, c0 = (tid & 15) * 8;
     float gm[8];
     ld_f8(gamma + c0, gm);
+    if (gmul) {
+      const float gs = *gmul;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) gm[e] *= gs;
+    }
     float w[8][H > 0 ? H : 1];
     if constexpr (H > 0) {
       const float4* p = reinterpret_cast<const float4*>(wb + c0 * H);

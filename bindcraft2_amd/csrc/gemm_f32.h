@@ -1,7 +1,7 @@
 // Batched, strided f32 GEMM on gfx950 MFMA (v_mfma_f32_16x16x4_f32), for the
 // structure module, which AF2 runs in float32 throughout (the point and
 // rigid projections ask for Precision.HIGHEST; a frame is a rotation whose
-// orthogonality bf16 would not keep).  Shapes there are N-sized (N <= 512
+// orthogonality h16 would not keep).  Shapes there are N-sized (N <= 512
 // residues, K <= 2112), so the kernel favours generality: any strides for
 // A, B and C, any M/N/K, and a fused epilogue
 //

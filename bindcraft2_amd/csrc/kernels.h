@@ -8,26 +8,26 @@ namespace bc2n {
 // ---------------------------------------------------------------- LayerNorm
 // y[m] = LN(x[src(m)]) with src(m) = m, or (q*nt+p) for m = p*nt+q when nt>0.
 // When H>0, bias_out[h*M+m] = bias_scale * sum_c LN(x)[m][c] * wb[c*H+h].
-// y_f16: y holds binary16 words instead of bf16 (H = 0, two-pass only).
 void ln_fwd_f32(hipStream_t st, const float* x, long M, int C, int nt,
-                const float* gamma, const float* beta, bf16* y, float* mean,
+                const float* gamma, const float* beta, h16* y, float* mean,
                 float* rstd, bool fast, int H, const float* wb, float* bias_out,
-                float bias_scale = 1.f, bool y_f16 = false);
-// dx[src(m)] (+)= LN-backward(dy[m] + sum_h dbias[h*M+m] * wb[c*H+h]).
+                float bias_scale = 1.f);
+// dx[src(m)] (+)= LN-backward(gs * (dy[m] + sum_h dbias[h*M+m] * wb[c*H+h])).
 // acc: dx = res + LN'(...) with res = dres, or dx itself when dres is null.
+// gs = *gmul (device scalar: a module's inverse cotangent scale), 1 if null.
 void ln_bwd_f32(hipStream_t st, const float* dy, const float* x, long M, int C,
                 int nt, const float* gamma, const float* mean, const float* rstd,
                 float* dx, bool acc, int H, const float* dbias, const float* wb,
-                const float* dres = nullptr);
+                const float* dres = nullptr, const float* gmul = nullptr);
 // Channel-major ([C][M]) input forms used by the triangle multiplication.
 void ln_fwd_cm(hipStream_t st, const float* x, long M, int C, const float* gamma,
-               const float* beta, bf16* y, float* mean, float* rstd, bool fast);
-void ln_fwd_cm(hipStream_t st, const bf16* x, long M, int C, const float* gamma,
-               const float* beta, bf16* y, float* mean, float* rstd, bool fast);
+               const float* beta, h16* y, float* mean, float* rstd, bool fast);
+void ln_fwd_cm(hipStream_t st, const h16* x, long M, int C, const float* gamma,
+               const float* beta, h16* y, float* mean, float* rstd, bool fast);
 void ln_bwd_cm(hipStream_t st, const float* dy, const float* x, long M, int C,
-               const float* gamma, const float* mean, const float* rstd, bf16* dx);
-void ln_bwd_cm(hipStream_t st, const float* dy, const bf16* x, long M, int C,
-               const float* gamma, const float* mean, const float* rstd, bf16* dx);
+               const float* gamma, const float* mean, const float* rstd, h16* dx);
+void ln_bwd_cm(hipStream_t st, const float* dy, const h16* x, long M, int C,
+               const float* gamma, const float* mean, const float* rstd, h16* dx);
 
 // ---------------------------------------------------------------- attention
 // Gated multi-head attention over R independent rows of N tokens, H heads of
@@ -38,13 +38,13 @@ struct AttnArgs {
   // q|k|v|g for token t = r*N+i live in row t of `qkvg` (row stride ld):
   // q at column h*D (pre-scaled by D^-1/2 * log2 e), k at H*D+h*D,
   // v at 2*H*D+h*D, gate pre-activation at 3*H*D+h*D.
-  const bf16* qkvg = nullptr;
+  const h16* qkvg = nullptr;
   long ld = 0;
   const float* mask = nullptr;  // mask[r*mask_sr + k*mask_sk], binary 0/1
   long mask_sr = 0, mask_sk = 0;
   const float* bias = nullptr;  // [H][N][N], log2 domain, or null
-  bf16* o = nullptr;            // ungated output [R*N][H*D]
-  bf16* og = nullptr;           // sigmoid(g) * o   [R*N][H*D]
+  h16* o = nullptr;            // ungated output [R*N][H*D]
+  h16* og = nullptr;           // sigmoid(g) * o   [R*N][H*D]
   long ldo = 0;
   float* lse = nullptr;         // [R][H][N], log2 domain
   // launch-site tag for the per-kernel timer: 0 triangle attention, 1 MSA
@@ -55,10 +55,10 @@ void attn_fwd(hipStream_t st, const AttnArgs& a);
 
 struct AttnBwdArgs {
   AttnArgs f;                  // forward operands (o, lse read back)
-  const bf16* dog = nullptr;   // upstream gradient of og [R*N][H*D]
-  bf16* dO = nullptr;          // scratch: dL/do [R*N][H*D]
+  const h16* dog = nullptr;   // upstream gradient of og [R*N][H*D]
+  h16* dO = nullptr;          // scratch: dL/do [R*N][H*D]
   float* Dsum = nullptr;       // scratch: [R][H][N] rowsum(dO*o)
-  bf16* dqkvg = nullptr;       // out: dq|dk|dv|dg with the layout of qkvg
+  h16* dqkvg = nullptr;       // out: dq|dk|dv|dg with the layout of qkvg
   float* dbias_part = nullptr; // scratch: [nchunk][H][N][N]
   float* dbias = nullptr;      // out: [H][N][N] (natural units), or null
   float scale = 1.f;           // D^-1/2 (q scaling applied in the forward)
@@ -80,11 +80,24 @@ void ln_f32_rows_bwd(hipStream_t st, const float* dy, const float* x, long M, in
 // ------------------------------------------------- triangle multiplication
 // C_c[m][n] = sum_k A_c[m][k] B_c[n][k] for c < channels, N x N planes at
 // stride N*N; an operand plane is K-contiguous ((r, k) at r*N + k) or k-major
-// ((r, k) at k*N + r).  Writes Cf (f32) if non-null, else Cb (bf16).  Returns
+// ((r, k) at k*N + r).  Writes Cf (f32) if non-null, else Cb (h16).  Returns
 // false (and launches nothing) when N is outside the kernel's range
 // (N % 32 != 0 or N > 256).
-bool trimul_contract(hipStream_t st, int N, int channels, const bf16* A, bool a_kcontig,
-                     const bf16* B, bool b_kcontig, float* Cf, bf16* Cb);
+bool trimul_contract(hipStream_t st, int N, int channels, const h16* A, bool a_kcontig,
+                     const h16* B, bool b_kcontig, float* Cf, h16* Cb);
+
+// ------------------------------------------------------- cotangent scales
+// The backward rounds cotangents to binary16 after multiplying them by a
+// power-of-two scale s and divides s out in the f32 epilogue that ends the
+// module (the backward is linear in the cotangent, so this is exact up to the
+// rounding it is for).  ct_scale writes sc[0] = s, sc[1] = 1/s with
+// s * max|x| in (8, 16] (s = 1 for an all-zero x); x: n floats, 16-byte
+// aligned, n % 4 == 0.  sc must be device memory; ct_scale_slot(k) is one of
+// the library's 8 two-float slots on the current device (0: a module's own
+// scale; 1, 2: the stack's per-block pair and MSA scales; 3: the template
+// embedding).  No allocation.
+void ct_scale(hipStream_t st, const float* x, long n, float* sc);
+float* ct_scale_slot(int k);
 
 // ---------------------------------------------------------------- dropout
 // Shared-dropout keep/scale table for one module: tbl[b*C+c] = keep/keep_rate

@@ -32,8 +32,8 @@ __device__ __forceinline__ void load8f<float>(const float* p, float (&v)[8]) {
   v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 template <>
-__device__ __forceinline__ void load8f<bf16>(const bf16* p, float (&v)[8]) {
-  const bf16x8 a = ld8(p);
+__device__ __forceinline__ void load8f<h16>(const h16* p, float (&v)[8]) {
+  const h16x8 a = ld8(p);
 #pragma unroll
   for (int e = 0; e < 8; ++e) v[e] = (float)a[e];
 }
@@ -56,11 +56,10 @@ __device__ __forceinline__ void load_w(const float* __restrict__ wb, int c0, flo
 // A lane group handles U rows (RPB apart): all U rows are loaded before the
 // first is reduced, and gamma, beta and the projection slice are read once
 // per U rows.
-// YF16: y holds binary16 words instead of bf16.
-template <int C, bool FAST, class InT, int H, int U, bool YF16 = false>
+template <int C, bool FAST, class InT, int H, int U>
 __global__ __launch_bounds__(256) void ln_fwd_kernel(
     const InT* __restrict__ x, long M, int nt, const float* __restrict__ gamma,
-    const float* __restrict__ beta, bf16* __restrict__ y,
+    const float* __restrict__ beta, h16* __restrict__ y,
     float* __restrict__ mean_out, float* __restrict__ rstd_out,
     const float* __restrict__ wb, float* __restrict__ bias_out, float bias_scale) {
   using G = LnGeom<C>;
@@ -101,15 +100,12 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(
     }
     const float r = rsqrtf(var + LN_EPS);
     float o[8];
-    bf16x8 ob;
-    f16x8 oh;
+    h16x8 ob;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       o[e] = (v[u][e] - mu) * r * gm[e] + bt[e];
-      if constexpr (YF16) oh[e] = (f16)o[e];
-      else ob[e] = (bf16)o[e];
+      ob[e] = (h16)o[e];
     }
-    if constexpr (YF16) ob = __builtin_bit_cast(bf16x8, oh);
     if (y) st8(y + m * C + c0, ob);
     if (gl == 0) {
       if (mean_out) mean_out[m] = mu;
@@ -131,15 +127,17 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(
   }
 }
 
-// dx[src(m)] = (ACC ? res[src(m)] : 0) + LN'(dy[m] + sum_h dbias[h][m] W[c][h])
-// (dy may be null; res = dres, or dx itself when dres is null); U rows per
-// lane group, as the forward.
+// dx[src(m)] = (ACC ? res[src(m)] : 0) + LN'(gs * (dy[m] + sum_h dbias[h][m] W[c][h]))
+// (dy may be null; res = dres, or dx itself when dres is null; gs = *gmul,
+// the inverse cotangent scale of the module, or 1 when gmul is null); U rows
+// per lane group, as the forward.
 template <int C, class InT, bool ACC, int H, int U>
 __global__ __launch_bounds__(256) void ln_bwd_kernel(
     const float* __restrict__ dy, const InT* __restrict__ x, long M, int nt,
     const float* __restrict__ gamma, const float* __restrict__ mean,
     const float* __restrict__ rstd, float* __restrict__ dx,
-    const float* __restrict__ dbias, const float* __restrict__ wb, const float* dres) {
+    const float* __restrict__ dbias, const float* __restrict__ wb, const float* dres,
+    const float* __restrict__ gmul) {
   using G = LnGeom<C>;
   const int t = threadIdx.x;
   const long mb = (long)blockIdx.x * (U * G::RPB) + t / G::TPR;
@@ -170,6 +168,11 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(
   }
   float gm[8];
   load8f<float>(gamma + c0, gm);
+  if (gmul) {
+    const float gs = *gmul;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) gm[e] *= gs;
+  }
   float w[8][H > 0 ? H : 1];
   if constexpr (H > 0) load_w<H>(wb, c0, w);
 #pragma unroll
@@ -207,14 +210,14 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(
 // Channel-major input: x is [C][M] (one plane per channel).  A block of
 // LNCM_R rows stages the [C][LNCM_R] tile through LDS (4-wide loads along m)
 // and then normalises it 256/LNCM_R lanes per row; the output is row-major
-// [M][C] bf16.
+// [M][C] h16.
 // Requires M % 4 == 0.
-// 4 consecutive m of channel plane c (x is [C][M], float or bf16)
+// 4 consecutive m of channel plane c (x is [C][M], float or h16)
 __device__ __forceinline__ float4 cm_load4(const float* x, long idx) {
   return *reinterpret_cast<const float4*>(x + idx);
 }
-__device__ __forceinline__ float4 cm_load4(const bf16* x, long idx) {
-  const bf16x4 v = *reinterpret_cast<const bf16x4*>(x + idx);
+__device__ __forceinline__ float4 cm_load4(const h16* x, long idx) {
+  const h16x4 v = *reinterpret_cast<const h16x4*>(x + idx);
   return make_float4((float)v[0], (float)v[1], (float)v[2], (float)v[3]);
 }
 
@@ -225,7 +228,7 @@ static_assert(64 / (256 / LNCM_R) >= 8, "the 64-channel kernels store 8 channels
 template <int C, bool FAST, class InT>
 __global__ __launch_bounds__(256) void ln_fwd_cm_kernel(
     const InT* __restrict__ x, long M, const float* __restrict__ gamma,
-    const float* __restrict__ beta, bf16* __restrict__ y,
+    const float* __restrict__ beta, h16* __restrict__ y,
     float* __restrict__ mean_out, float* __restrict__ rstd_out) {
   constexpr int R = LNCM_R;
   __shared__ float tile[R][C + 1];
@@ -268,11 +271,11 @@ __global__ __launch_bounds__(256) void ln_fwd_cm_kernel(
   if (m < M) {
 #pragma unroll
     for (int e0 = 0; e0 < CPL; e0 += 8) {
-      bf16x8 ob;
+      h16x8 ob;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int c = part * CPL + e0 + e;
-        ob[e] = (bf16)((v[e0 + e] - mu) * rs * gamma[c] + beta[c]);
+        ob[e] = (h16)((v[e0 + e] - mu) * rs * gamma[c] + beta[c]);
       }
       st8(y + m * C + part * CPL + e0, ob);
     }
@@ -281,12 +284,12 @@ __global__ __launch_bounds__(256) void ln_fwd_cm_kernel(
 }
 
 // Backward of the channel-major norm: dy row-major [M][C] f32, x channel-major
-// [C][M] f32; writes dx channel-major [C][M] as bf16 (a GEMM operand).
+// [C][M] f32; writes dx channel-major [C][M] as h16 (a GEMM operand).
 template <int C, class InT>
 __global__ __launch_bounds__(256) void ln_bwd_cm_kernel(
     const float* __restrict__ dy, const InT* __restrict__ x, long M,
     const float* __restrict__ gamma, const float* __restrict__ mean,
-    const float* __restrict__ rstd, bf16* __restrict__ dx) {
+    const float* __restrict__ rstd, h16* __restrict__ dx) {
   constexpr int R = LNCM_R;
   __shared__ float tile[R][C + 1];
   const int t = threadIdx.x;
@@ -336,12 +339,12 @@ __global__ __launch_bounds__(256) void ln_bwd_cm_kernel(
     const int c = i / (R / 4), q = (i % (R / 4)) * 4;
     const long mm = m0 + q;
     if (mm < M) {
-      bf16x4 o;
-      o[0] = (bf16)tile[q + 0][c];
-      o[1] = (bf16)tile[q + 1][c];
-      o[2] = (bf16)tile[q + 2][c];
-      o[3] = (bf16)tile[q + 3][c];
-      *reinterpret_cast<bf16x4*>(dx + (long)c * M + mm) = o;
+      h16x4 o;
+      o[0] = f2h_sat(tile[q + 0][c]);
+      o[1] = f2h_sat(tile[q + 1][c]);
+      o[2] = f2h_sat(tile[q + 2][c]);
+      o[3] = f2h_sat(tile[q + 3][c]);
+      *reinterpret_cast<h16x4*>(dx + (long)c * M + mm) = o;
     }
   }
 }
@@ -356,20 +359,10 @@ constexpr int ln_rows() { return H > 0 ? 4 : 1; }
 
 template <int C, int H>
 static void ln_fwd_launch(hipStream_t st, const float* x, long M, int nt, const float* gamma,
-                          const float* beta, bf16* y, float* mean, float* rstd, bool fast,
-                          const float* wb, float* bias_out, float bs, bool yf16) {
+                          const float* beta, h16* y, float* mean, float* rstd, bool fast,
+                          const float* wb, float* bias_out, float bs) {
   constexpr int U = ln_rows<H>();
   const int grid = (int)((M + U * LnGeom<C>::RPB - 1) / (U * LnGeom<C>::RPB));
-  if (yf16) {
-    if constexpr (H == 0) {
-      if (fast) throw std::runtime_error("ln_fwd: binary16 output is two-pass only");
-      hipLaunchKernelGGL((ln_fwd_kernel<C, false, float, 0, U, true>), dim3(grid), dim3(256), 0,
-                         st, x, M, nt, gamma, beta, y, mean, rstd, wb, bias_out, bs);
-      return;
-    } else {
-      throw std::runtime_error("ln_fwd: binary16 output has no bias projection");
-    }
-  }
   if (fast)
     hipLaunchKernelGGL((ln_fwd_kernel<C, true, float, H, U>), dim3(grid), dim3(256), 0, st, x, M,
                        nt, gamma, beta, y, mean, rstd, wb, bias_out, bs);
@@ -380,24 +373,24 @@ static void ln_fwd_launch(hipStream_t st, const float* x, long M, int nt, const 
 
 template <int C>
 static void ln_fwd_dispatch(hipStream_t st, const float* x, long M, int nt, const float* gamma,
-                            const float* beta, bf16* y, float* mean, float* rstd, bool fast, int H,
-                            const float* wb, float* bias_out, float bs, bool yf16) {
+                            const float* beta, h16* y, float* mean, float* rstd, bool fast, int H,
+                            const float* wb, float* bias_out, float bs) {
   switch (H) {
-    case 0: ln_fwd_launch<C, 0>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, wb, bias_out, bs, yf16); break;
-    case 4: ln_fwd_launch<C, 4>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, wb, bias_out, bs, yf16); break;
-    case 8: ln_fwd_launch<C, 8>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, wb, bias_out, bs, yf16); break;
+    case 0: ln_fwd_launch<C, 0>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, wb, bias_out, bs); break;
+    case 4: ln_fwd_launch<C, 4>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, wb, bias_out, bs); break;
+    case 8: ln_fwd_launch<C, 8>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, wb, bias_out, bs); break;
     default: throw std::runtime_error("ln_fwd: bias heads must be 0, 4 or 8");
   }
 }
 
 void ln_fwd_f32(hipStream_t st, const float* x, long M, int C, int nt,
-                const float* gamma, const float* beta, bf16* y, float* mean,
+                const float* gamma, const float* beta, h16* y, float* mean,
                 float* rstd, bool fast, int H, const float* wb, float* bias_out,
-                float bs, bool y_f16) {
+                float bs) {
   switch (C) {
-    case 64: ln_fwd_dispatch<64>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, H, wb, bias_out, bs, y_f16); break;
-    case 128: ln_fwd_dispatch<128>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, H, wb, bias_out, bs, y_f16); break;
-    case 256: ln_fwd_dispatch<256>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, H, wb, bias_out, bs, y_f16); break;
+    case 64: ln_fwd_dispatch<64>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, H, wb, bias_out, bs); break;
+    case 128: ln_fwd_dispatch<128>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, H, wb, bias_out, bs); break;
+    case 256: ln_fwd_dispatch<256>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, H, wb, bias_out, bs); break;
     default: throw std::runtime_error("ln_fwd: unsupported channel count");
   }
 }
@@ -405,25 +398,27 @@ void ln_fwd_f32(hipStream_t st, const float* x, long M, int C, int nt,
 template <int C, int H>
 static void ln_bwd_launch(hipStream_t st, const float* dy, const float* x, long M, int nt,
                           const float* gamma, const float* mean, const float* rstd, float* dx,
-                          bool acc, const float* dbias, const float* wb, const float* dres) {
+                          bool acc, const float* dbias, const float* wb, const float* dres,
+                          const float* gmul) {
   constexpr int U = ln_rows<H>();
   const int grid = (int)((M + U * LnGeom<C>::RPB - 1) / (U * LnGeom<C>::RPB));
   if (acc)
     hipLaunchKernelGGL((ln_bwd_kernel<C, float, true, H, U>), dim3(grid), dim3(256), 0, st, dy, x,
-                       M, nt, gamma, mean, rstd, dx, dbias, wb, dres);
+                       M, nt, gamma, mean, rstd, dx, dbias, wb, dres, gmul);
   else
     hipLaunchKernelGGL((ln_bwd_kernel<C, float, false, H, U>), dim3(grid), dim3(256), 0, st, dy, x,
-                       M, nt, gamma, mean, rstd, dx, dbias, wb, dres);
+                       M, nt, gamma, mean, rstd, dx, dbias, wb, dres, gmul);
 }
 
 template <int C>
 static void ln_bwd_dispatch(hipStream_t st, const float* dy, const float* x, long M, int nt,
                             const float* gamma, const float* mean, const float* rstd, float* dx,
-                            bool acc, int H, const float* dbias, const float* wb, const float* dres) {
+                            bool acc, int H, const float* dbias, const float* wb, const float* dres,
+                            const float* gmul) {
   switch (H) {
-    case 0: ln_bwd_launch<C, 0>(st, dy, x, M, nt, gamma, mean, rstd, dx, acc, dbias, wb, dres); break;
-    case 4: ln_bwd_launch<C, 4>(st, dy, x, M, nt, gamma, mean, rstd, dx, acc, dbias, wb, dres); break;
-    case 8: ln_bwd_launch<C, 8>(st, dy, x, M, nt, gamma, mean, rstd, dx, acc, dbias, wb, dres); break;
+    case 0: ln_bwd_launch<C, 0>(st, dy, x, M, nt, gamma, mean, rstd, dx, acc, dbias, wb, dres, gmul); break;
+    case 4: ln_bwd_launch<C, 4>(st, dy, x, M, nt, gamma, mean, rstd, dx, acc, dbias, wb, dres, gmul); break;
+    case 8: ln_bwd_launch<C, 8>(st, dy, x, M, nt, gamma, mean, rstd, dx, acc, dbias, wb, dres, gmul); break;
     default: throw std::runtime_error("ln_bwd: bias heads must be 0, 4 or 8");
   }
 }
@@ -431,18 +426,18 @@ static void ln_bwd_dispatch(hipStream_t st, const float* dy, const float* x, lon
 void ln_bwd_f32(hipStream_t st, const float* dy, const float* x, long M, int C,
                 int nt, const float* gamma, const float* mean, const float* rstd,
                 float* dx, bool acc, int H, const float* dbias, const float* wb,
-                const float* dres) {
+                const float* dres, const float* gmul) {
   switch (C) {
-    case 64: ln_bwd_dispatch<64>(st, dy, x, M, nt, gamma, mean, rstd, dx, acc, H, dbias, wb, dres); break;
-    case 128: ln_bwd_dispatch<128>(st, dy, x, M, nt, gamma, mean, rstd, dx, acc, H, dbias, wb, dres); break;
-    case 256: ln_bwd_dispatch<256>(st, dy, x, M, nt, gamma, mean, rstd, dx, acc, H, dbias, wb, dres); break;
+    case 64: ln_bwd_dispatch<64>(st, dy, x, M, nt, gamma, mean, rstd, dx, acc, H, dbias, wb, dres, gmul); break;
+    case 128: ln_bwd_dispatch<128>(st, dy, x, M, nt, gamma, mean, rstd, dx, acc, H, dbias, wb, dres, gmul); break;
+    case 256: ln_bwd_dispatch<256>(st, dy, x, M, nt, gamma, mean, rstd, dx, acc, H, dbias, wb, dres, gmul); break;
     default: throw std::runtime_error("ln_bwd: unsupported channel count");
   }
 }
 
 template <class InT>
 static void ln_fwd_cm_t(hipStream_t st, const InT* x, long M, int C, const float* gamma,
-                        const float* beta, bf16* y, float* mean, float* rstd, bool fast) {
+                        const float* beta, h16* y, float* mean, float* rstd, bool fast) {
   if (M % 4 != 0) throw std::runtime_error("ln_fwd_cm: M must be a multiple of 4");
   const int grid = (int)((M + LNCM_R - 1) / LNCM_R);
 #define BC2N_LNCM(CV, FV) \
@@ -457,17 +452,17 @@ static void ln_fwd_cm_t(hipStream_t st, const InT* x, long M, int C, const float
 #undef BC2N_LNCM
 }
 void ln_fwd_cm(hipStream_t st, const float* x, long M, int C, const float* gamma,
-               const float* beta, bf16* y, float* mean, float* rstd, bool fast) {
+               const float* beta, h16* y, float* mean, float* rstd, bool fast) {
   ln_fwd_cm_t(st, x, M, C, gamma, beta, y, mean, rstd, fast);
 }
-void ln_fwd_cm(hipStream_t st, const bf16* x, long M, int C, const float* gamma,
-               const float* beta, bf16* y, float* mean, float* rstd, bool fast) {
+void ln_fwd_cm(hipStream_t st, const h16* x, long M, int C, const float* gamma,
+               const float* beta, h16* y, float* mean, float* rstd, bool fast) {
   ln_fwd_cm_t(st, x, M, C, gamma, beta, y, mean, rstd, fast);
 }
 
 template <class InT>
 static void ln_bwd_cm_t(hipStream_t st, const float* dy, const InT* x, long M, int C,
-                        const float* gamma, const float* mean, const float* rstd, bf16* dx) {
+                        const float* gamma, const float* mean, const float* rstd, h16* dx) {
   if (M % 4 != 0) throw std::runtime_error("ln_bwd_cm: M must be a multiple of 4");
   const int grid = (int)((M + LNCM_R - 1) / LNCM_R);
   if (C == 128) hipLaunchKernelGGL((ln_bwd_cm_kernel<128, InT>), dim3(grid), dim3(256), 0, st, dy, x, M, gamma, mean, rstd, dx);
@@ -475,11 +470,11 @@ static void ln_bwd_cm_t(hipStream_t st, const float* dy, const InT* x, long M, i
   else throw std::runtime_error("ln_bwd_cm: unsupported channel count");
 }
 void ln_bwd_cm(hipStream_t st, const float* dy, const float* x, long M, int C,
-               const float* gamma, const float* mean, const float* rstd, bf16* dx) {
+               const float* gamma, const float* mean, const float* rstd, h16* dx) {
   ln_bwd_cm_t(st, dy, x, M, C, gamma, mean, rstd, dx);
 }
-void ln_bwd_cm(hipStream_t st, const float* dy, const bf16* x, long M, int C,
-               const float* gamma, const float* mean, const float* rstd, bf16* dx) {
+void ln_bwd_cm(hipStream_t st, const float* dy, const h16* x, long M, int C,
+               const float* gamma, const float* mean, const float* rstd, h16* dx) {
   ln_bwd_cm_t(st, dy, x, M, C, gamma, mean, rstd, dx);
 }
 

@@ -4,11 +4,27 @@
 // and adds the module's input cotangent to the residual cotangent.  Scratch
 // comes from the process arena; nothing is allocated inside a call once the
 // arena has grown to the call's plan.
+//
+// Every backward takes `sc`, the device pair {s, 1/s} of its cotangent scale
+// (ct_scale in kernels.h): its incoming cotangent is multiplied by s where it
+// is first rounded to binary16, and 1/s is applied in the f32 epilogue that
+// writes the module's input cotangent.  A caller running many modules on one
+// cotangent (the stack, per block) computes it once; sc = nullptr makes the
+// module compute its own from its incoming cotangent.
 #pragma once
 #include "runtime.h"
 #include "kernels.h"
 
 namespace bc2n {
+
+// The scale a backward uses: the caller's, or one computed now from the n
+// floats of the module's incoming cotangent into the module slot.
+inline const float* module_scale(hipStream_t st, const float* sc, const float* dout, long n) {
+  if (sc) return sc;
+  float* s = ct_scale_slot(0);
+  ct_scale(st, dout, n, s);
+  return s;
+}
 
 // ---------------------------------------------------------- triangle attention
 // modules.py TriangleAttention (+ Attention with pair bias and gating).
@@ -16,10 +32,10 @@ struct TriAttnW {
   int C = 0, H = 0, D = 0;
   const float *ln_g = nullptr, *ln_b = nullptr, *w2d = nullptr;  // w2d [C][H]
   const float* bqkvg = nullptr;  // [4HD]: zeros for q,k,v; gating_b for g
-  const bf16* wqkvg_t = nullptr; // [4HD][C]
-  const bf16* wqkvg = nullptr;   // [C][4HD]
-  const bf16* wo_t = nullptr;    // [C][HD]
-  const bf16* wo = nullptr;      // [HD][C]
+  const h16* wqkvg_t = nullptr; // [4HD][C]
+  const h16* wqkvg = nullptr;   // [C][4HD]
+  const h16* wo_t = nullptr;    // [C][HD]
+  const h16* wo = nullptr;      // [HD][C]
   const float* bo = nullptr;     // [C]
 };
 TriAttnW triattn_weights(WeightStore& ws, const std::string& prefix);
@@ -31,7 +47,7 @@ void triattn_fwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
                  float* pair_out, void* save);
 void triattn_bwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
                  const float* pair_in, const float* mask, const float* tbl,
-                 const void* save, const float* dout, float* din);
+                 const void* save, const float* dout, float* din, const float* sc = nullptr);
 
 // ------------------------------------------------------ triangle multiplication
 // modules.py:1044-1088 (fused projection weights).
@@ -39,14 +55,14 @@ struct TriMulW {
   int C = 0, I = 0;
   const float *ln_g = nullptr, *ln_b = nullptr, *cn_g = nullptr, *cn_b = nullptr;
   const float *bp = nullptr, *bg = nullptr, *bgl = nullptr, *bo = nullptr;
-  const bf16* wcat = nullptr;    // [C][4I+C]  (GEMM column order)
-  const bf16* wcat_t = nullptr;  // [4I+C][C]
+  const h16* wcat = nullptr;    // [C][4I+C]  (GEMM column order)
+  const h16* wcat_t = nullptr;  // [4I+C][C]
   // the same two matrices with k permuted within each 32-block (tail_kperm):
   // the backward tail reads a lane's 8 MFMA k-slots as one 16-byte LDS read
-  const bf16* wcat_k = nullptr;
-  const bf16* wcat_tk = nullptr;
-  const bf16* wo = nullptr;      // [I][C]
-  const bf16* wo_t = nullptr;    // [C][I]
+  const h16* wcat_k = nullptr;
+  const h16* wcat_tk = nullptr;
+  const h16* wo = nullptr;      // [I][C]
+  const h16* wo_t = nullptr;    // [C][I]
 };
 TriMulW trimul_weights(WeightStore& ws, const std::string& prefix);
 size_t trimul_save_bytes(int N, int C, int I);
@@ -54,7 +70,7 @@ void trimul_fwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
                 const float* mask, const float* tbl, float* pair_out, void* save);
 void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const float* pair_in,
                 const float* mask, const float* tbl, const void* save, const float* dout,
-                float* din);
+                float* din, const float* sc = nullptr);
 
 // ----------------------------------------------------------------- transition
 // modules.py:252-305; pair (rows = N*N) and MSA (rows = S*N) alike.  `nt` is
@@ -62,21 +78,21 @@ void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
 struct TransW {
   int C = 0, F = 0;
   const float *ln_g = nullptr, *ln_b = nullptr, *b1 = nullptr, *b2 = nullptr;
-  const bf16 *w1 = nullptr, *w2 = nullptr;      // backward operands (bf16)
-  const f16 *w1_t = nullptr, *w2_t = nullptr;   // forward operands (binary16)
+  const h16 *w1 = nullptr, *w1_t = nullptr, *w2 = nullptr, *w2_t = nullptr;
 };
 TransW transition_weights(WeightStore& ws, const std::string& prefix);
 size_t transition_save_bytes(long rows, int C, int F);
 void transition_fwd(hipStream_t st, const TransW& w, long rows, int nt, const float* act_in,
                     const float* tbl, float* act_out, void* save);
 void transition_bwd(hipStream_t st, const TransW& w, long rows, int nt, const float* act_in,
-                    const float* tbl, const void* save, const float* dout, float* din);
+                    const float* tbl, const void* save, const float* dout, float* din,
+                    const float* sc = nullptr);
 
 // ------------------------------------------------------------- MSA attention
 struct AttnW {
   int Cin = 0, Cout = 0, H = 0, D = 0;
   const float *ln_g = nullptr, *ln_b = nullptr, *bqkvg = nullptr, *bo = nullptr;
-  const bf16 *wqkvg = nullptr, *wqkvg_t = nullptr, *wo = nullptr, *wo_t = nullptr;
+  const h16 *wqkvg = nullptr, *wqkvg_t = nullptr, *wo = nullptr, *wo_t = nullptr;
 };
 struct MsaRowW {
   AttnW a;
@@ -96,12 +112,12 @@ void msarow_fwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa
 // dpair is accumulated (+=), dmsa_in = dmsa_out + J^T(...)
 void msarow_bwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa_in,
                 const float* msa_mask, const float* pair, const float* tbl, const void* save,
-                const float* dmsa_out, float* dmsa_in, float* dpair);
+                const float* dmsa_out, float* dmsa_in, float* dpair, const float* sc = nullptr);
 void msacol_fwd(hipStream_t st, const MsaColW& w, int S, int N, const float* msa_in,
                 const float* msa_mask, const float* tbl, float* msa_out, void* save);
 void msacol_bwd(hipStream_t st, const MsaColW& w, int S, int N, const float* msa_in,
                 const float* msa_mask, const float* tbl, const void* save,
-                const float* dmsa_out, float* dmsa_in);
+                const float* dmsa_out, float* dmsa_in, const float* sc = nullptr);
 
 // ---------------------------------------------- MSA column global attention
 struct MsaGlobW {
@@ -121,7 +137,7 @@ void msaglobal_bwd(hipStream_t st, const MsaGlobW& w, int S, int N, const float*
 struct OpmW {
   int Cm = 0, O = 0, C = 0;
   const float *ln_g = nullptr, *ln_b = nullptr, *blr = nullptr, *bo = nullptr;
-  const bf16 *wlr = nullptr, *wlr_t = nullptr, *wt = nullptr, *wt2 = nullptr;
+  const h16 *wlr = nullptr, *wlr_t = nullptr, *wt = nullptr, *wt2 = nullptr;
 };
 OpmW opm_weights(WeightStore& ws, const std::string& prefix);
 size_t opm_save_bytes(int S, int N, int O, int C);
@@ -130,7 +146,7 @@ void opm_fwd(hipStream_t st, const OpmW& w, int S, int N, const float* msa, cons
 // dmsa_in = dmsa_out + J^T(tbl * dpair)
 void opm_bwd(hipStream_t st, const OpmW& w, int S, int N, const float* msa, const float* msa_mask,
              const float* tbl, const void* save, const float* dpair, const float* dmsa_out,
-             float* dmsa_in);
+             float* dmsa_in, const float* sc = nullptr);
 
 // ------------------------------------------- structure module fold iterations
 // Weights of generate_monomer_rigids + FoldIteration (without the sidechain),

@@ -39,10 +39,10 @@ void attn_weights(WeightStore& ws, const std::string& P, AttnW& w) {
     }
     return c;
   };
-  w.wqkvg = ws.derived<bf16>("attn.wqkvg:" + P, [&] { return to_bf16(cat()); });
-  w.wqkvg_t = ws.derived<bf16>("attn.wqkvg_t:" + P, [&] {
+  w.wqkvg = ws.derived<h16>("attn.wqkvg:" + P, [&] { return to_h16(cat()); });
+  w.wqkvg_t = ws.derived<h16>("attn.wqkvg_t:" + P, [&] {
     std::vector<float> c = cat();
-    return transpose_bf16(c.data(), C, 4 * HD);
+    return transpose_h16(c.data(), C, 4 * HD);
   });
   w.bqkvg = ws.derived<float>("attn.bqkvg:" + P, [&] {
     std::vector<float> b((size_t)4 * HD, 0.f);
@@ -50,8 +50,8 @@ void attn_weights(WeightStore& ws, const std::string& P, AttnW& w) {
     for (int j = 0; j < HD; ++j) b[3 * HD + j] = gb.data[j];
     return b;
   });
-  w.wo = ws.derived<bf16>("attn.wo:" + P, [&] { return to_bf16(ow.data); });
-  w.wo_t = ws.derived<bf16>("attn.wo_t:" + P, [&] { return transpose_bf16(ow.data.data(), HD, w.Cout); });
+  w.wo = ws.derived<h16>("attn.wo:" + P, [&] { return to_h16(ow.data); });
+  w.wo_t = ws.derived<h16>("attn.wo_t:" + P, [&] { return transpose_h16(ow.data.data(), HD, w.Cout); });
   w.bo = ws.f32(P + "attention/output_b");
   w.ln_g = ws.f32(P + "query_norm/scale");
   w.ln_b = ws.f32(P + "query_norm/offset");
@@ -65,8 +65,8 @@ void attn_weights(WeightStore& ws, const std::string& P, AttnW& w) {
 constexpr int SA_D = 32;
 
 __global__ __launch_bounds__(64) void small_attn_fwd_kernel(
-    const bf16* __restrict__ qkvg, long ld, int S, int N, int H,
-    const float* __restrict__ mask, bf16* __restrict__ o, bf16* __restrict__ og, long ldo,
+    const h16* __restrict__ qkvg, long ld, int S, int N, int H,
+    const float* __restrict__ mask, h16* __restrict__ o, h16* __restrict__ og, long ldo,
     float* __restrict__ lse) {
   const int j = blockIdx.x / H, h = blockIdx.x % H;
   const int lane = threadIdx.x;
@@ -74,14 +74,14 @@ __global__ __launch_bounds__(64) void small_attn_fwd_kernel(
   // every lane handles one query row (lane < S) over all keys
   if (lane >= S) return;
   const int sq = lane;
-  const bf16* q = qkvg + ((long)sq * N + j) * ld + h * SA_D;
+  const h16* q = qkvg + ((long)sq * N + j) * ld + h * SA_D;
   float qv[SA_D];
 #pragma unroll
   for (int d = 0; d < SA_D; ++d) qv[d] = (float)q[d];
   float mx = -INFINITY;
   float sc[32];
   for (int sk = 0; sk < S; ++sk) {
-    const bf16* k = qkvg + ((long)sk * N + j) * ld + HD + h * SA_D;
+    const h16* k = qkvg + ((long)sk * N + j) * ld + HD + h * SA_D;
     float s = 0.f;
 #pragma unroll
     for (int d = 0; d < SA_D; ++d) s += qv[d] * (float)k[d];
@@ -100,17 +100,17 @@ __global__ __launch_bounds__(64) void small_attn_fwd_kernel(
 #pragma unroll
   for (int d = 0; d < SA_D; ++d) acc[d] = 0.f;
   for (int sk = 0; sk < S; ++sk) {
-    const bf16* v = qkvg + ((long)sk * N + j) * ld + 2 * HD + h * SA_D;
+    const h16* v = qkvg + ((long)sk * N + j) * ld + 2 * HD + h * SA_D;
     const float p = sc[sk] * inv;
 #pragma unroll
     for (int d = 0; d < SA_D; ++d) acc[d] += p * (float)v[d];
   }
   const long row = (long)sq * N + j;
-  const bf16* g = qkvg + row * ld + 3 * HD + h * SA_D;
+  const h16* g = qkvg + row * ld + 3 * HD + h * SA_D;
 #pragma unroll
   for (int d = 0; d < SA_D; ++d) {
-    o[row * ldo + h * SA_D + d] = (bf16)acc[d];
-    og[row * ldo + h * SA_D + d] = (bf16)(acc[d] * sigmoidf_((float)g[d]));
+    o[row * ldo + h * SA_D + d] = (h16)acc[d];
+    og[row * ldo + h * SA_D + d] = (h16)(acc[d] * sigmoidf_((float)g[d]));
   }
   lse[((long)j * H + h) * S + sq] = mx + __logf(sum);
 }
@@ -118,9 +118,9 @@ __global__ __launch_bounds__(64) void small_attn_fwd_kernel(
 // Backward, same decomposition; lane = query row.  dK/dV sums over queries
 // go through LDS atomics of the one wave that owns the (j,h) pair.
 __global__ __launch_bounds__(64) void small_attn_bwd_kernel(
-    const bf16* __restrict__ qkvg, long ld, int S, int N, int H,
-    const float* __restrict__ mask, const bf16* __restrict__ o, const bf16* __restrict__ dog,
-    long ldo, float qscale, bf16* __restrict__ dqkvg) {
+    const h16* __restrict__ qkvg, long ld, int S, int N, int H,
+    const float* __restrict__ mask, const h16* __restrict__ o, const h16* __restrict__ dog,
+    long ldo, float qscale, h16* __restrict__ dqkvg) {
   __shared__ float dk_s[32][SA_D + 1];
   __shared__ float dv_s[32][SA_D + 1];
   const int j = blockIdx.x / H, h = blockIdx.x % H;
@@ -134,8 +134,8 @@ __global__ __launch_bounds__(64) void small_attn_bwd_kernel(
   if (lane < S) {
     const int sq = lane;
     const long row = (long)sq * N + j;
-    const bf16* q = qkvg + row * ld + h * SA_D;
-    const bf16* g = qkvg + row * ld + 3 * HD + h * SA_D;
+    const h16* q = qkvg + row * ld + h * SA_D;
+    const h16* g = qkvg + row * ld + 3 * HD + h * SA_D;
     float qv[SA_D], dO[SA_D];
     float Dsum = 0.f;
 #pragma unroll
@@ -146,14 +146,14 @@ __global__ __launch_bounds__(64) void small_attn_bwd_kernel(
       const float ov = (float)o[row * ldo + h * SA_D + d];
       dO[d] = dgo * sg;
       Dsum += dO[d] * ov;
-      dqkvg[row * ld + 3 * HD + h * SA_D + d] = (bf16)(dgo * ov * sg * (1.f - sg));
+      dqkvg[row * ld + 3 * HD + h * SA_D + d] = f2h_sat(dgo * ov * sg * (1.f - sg));
     }
     // softmax recomputed in full (S is small): exact even for a fully masked
     // column, where every clipped logit is -1e8 and f32 cannot carry an lse
     float sc[32], mx = -INFINITY;
     bool live[32];
     for (int sk = 0; sk < S; ++sk) {
-      const bf16* k = qkvg + ((long)sk * N + j) * ld + HD + h * SA_D;
+      const h16* k = qkvg + ((long)sk * N + j) * ld + HD + h * SA_D;
       float s = 0.f;
 #pragma unroll
       for (int d = 0; d < SA_D; ++d) s += qv[d] * (float)k[d];
@@ -173,8 +173,8 @@ __global__ __launch_bounds__(64) void small_attn_bwd_kernel(
     for (int d = 0; d < SA_D; ++d) dq[d] = 0.f;
     for (int sk = 0; sk < S; ++sk) {
       const long krow = (long)sk * N + j;
-      const bf16* k = qkvg + krow * ld + HD + h * SA_D;
-      const bf16* v = qkvg + krow * ld + 2 * HD + h * SA_D;
+      const h16* k = qkvg + krow * ld + HD + h * SA_D;
+      const h16* v = qkvg + krow * ld + 2 * HD + h * SA_D;
       float dp = 0.f;
 #pragma unroll
       for (int d = 0; d < SA_D; ++d) dp += dO[d] * (float)v[d];
@@ -188,22 +188,22 @@ __global__ __launch_bounds__(64) void small_attn_bwd_kernel(
       }
     }
 #pragma unroll
-    for (int d = 0; d < SA_D; ++d) dqkvg[row * ld + h * SA_D + d] = (bf16)(dq[d] * qscale);
+    for (int d = 0; d < SA_D; ++d) dqkvg[row * ld + h * SA_D + d] = f2h_sat(dq[d] * qscale);
   }
   __syncthreads();
   for (int i = lane; i < S * SA_D; i += 64) {
     const int sk = i / SA_D, d = i % SA_D;
     const long krow = (long)sk * N + j;
     // q was scaled by qscale: dK (unscaled k) = sum ds * q_scaled
-    dqkvg[krow * ld + HD + h * SA_D + d] = (bf16)dk_s[sk][d];
-    dqkvg[krow * ld + 2 * HD + h * SA_D + d] = (bf16)dv_s[sk][d];
+    dqkvg[krow * ld + HD + h * SA_D + d] = f2h_sat(dk_s[sk][d]);
+    dqkvg[krow * ld + 2 * HD + h * SA_D + d] = f2h_sat(dv_s[sk][d]);
   }
 }
 
 template <class A>
 struct MsaRowSave {
   float *mean, *rstd, *pmean, *prstd, *bias, *lse;
-  bf16 *qkvg, *o;
+  h16 *qkvg, *o;
   MsaRowSave(A& a, int S, int N, int Cm, int H) {
     const size_t R = (size_t)S * N, M = (size_t)N * N;
     mean = a.template take<float>(R);
@@ -212,26 +212,26 @@ struct MsaRowSave {
     prstd = a.template take<float>(M);
     bias = a.template take<float>((size_t)H * M);
     lse = a.template take<float>((size_t)S * H * N);
-    qkvg = a.template take<bf16>(R * 4 * Cm);
-    o = a.template take<bf16>(R * Cm);
+    qkvg = a.template take<h16>(R * 4 * Cm);
+    o = a.template take<h16>(R * Cm);
   }
 };
 
 template <class A>
 struct MsaColSave {
   float *mean, *rstd, *lse;
-  bf16 *qkvg, *o;
+  h16 *qkvg, *o;
   MsaColSave(A& a, int S, int N, int Cm, int H) {
     const size_t R = (size_t)S * N;
     mean = a.template take<float>(R);
     rstd = a.template take<float>(R);
     lse = a.template take<float>((size_t)N * H * S);
-    qkvg = a.template take<bf16>(R * 4 * Cm);
-    o = a.template take<bf16>(R * Cm);
+    qkvg = a.template take<h16>(R * 4 * Cm);
+    o = a.template take<h16>(R * Cm);
   }
 };
 
-void qkvg_gemm(hipStream_t st, const AttnW& w, long rows, const bf16* xn, bf16* qkvg, float qscale,
+void qkvg_gemm(hipStream_t st, const AttnW& w, long rows, const h16* xn, h16* qkvg, float qscale,
                const char* name) {
   const int HD = w.H * w.D;
   GemmArgs g;
@@ -241,7 +241,7 @@ void qkvg_gemm(hipStream_t st, const AttnW& w, long rows, const bf16* xn, bf16* 
   gemm<128, 128>(st, g, EpiScaledCols(qkvg, 4L * HD, w.bqkvg, qscale, HD), name);
 }
 
-void out_gemm(hipStream_t st, const AttnW& w, long rows, const bf16* og, const float* in,
+void out_gemm(hipStream_t st, const AttnW& w, long rows, const h16* og, const float* in,
               float* out, const float* tbl, int nt, const char* name) {
   const int HD = w.H * w.D;
   GemmArgs g;
@@ -251,20 +251,21 @@ void out_gemm(hipStream_t st, const AttnW& w, long rows, const bf16* og, const f
   gemm<128, 128>(st, g, EpiResidualRows(in, out, w.bo, tbl, nt, w.Cout, false), name);
 }
 
-// d(og) = (tbl * dout) . Wo^T, the dropout scale applied as A is loaded,
-// with epilogue `epi`; after the attention backward, d(xn) = dqkvg . Wcat^T
+// d(og) = (s * tbl * dout) . Wo^T, the dropout table and the cotangent scale
+// s = *sc applied as A is loaded, with epilogue `epi`; after the attention
+// backward, d(xn) = dqkvg . Wcat^T
 template <class Epi>
 void dout_gemm(hipStream_t st, const AttnW& w, long rows, const float* dout, const float* tbl,
-               int nt, const Epi& epi, const char* name) {
+               int nt, const Epi& epi, const char* name, const float* sc) {
   const int HD = w.H * w.D;
   GemmArgs g;
   g.M = (int)rows; g.N = HD; g.K = w.Cout;
   g.a_sm = w.Cout; g.a_sk = 1;
   g.B = w.wo; g.b_sn = w.Cout; g.b_sk = 1;
-  gemm<128, 128>(st, g, epi, name, ALoadScaledRows{dout, tbl, nt, w.Cout, false});
+  gemm<128, 128>(st, g, epi, name, ALoadScaledRows{dout, tbl, nt, w.Cout, false, sc});
 }
 
-void dx_gemm(hipStream_t st, const AttnW& w, long rows, const bf16* dqkvg, float* dxn,
+void dx_gemm(hipStream_t st, const AttnW& w, long rows, const h16* dqkvg, float* dxn,
              const char* name) {
   const int HD = w.H * w.D;
   GemmArgs g;
@@ -322,8 +323,8 @@ void msarow_fwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa
   Arena& ar = arena();
   std::lock_guard<std::recursive_mutex> lk(ar.lock());
   ar.reset(st, (size_t)R * Cm * 2 + (size_t)R * HD * 2 + 1024);
-  bf16* xn = ar.take_n<bf16>((size_t)R * Cm);
-  bf16* og = ar.take_n<bf16>((size_t)R * HD);
+  h16* xn = ar.take_n<h16>((size_t)R * Cm);
+  h16* og = ar.take_n<h16>((size_t)R * HD);
   {
     KTimed kt("msarow.ln", st);
     ln_fwd_f32(st, msa_in, R, Cm, 0, a.ln_g, a.ln_b, xn, sv.mean, sv.rstd, false, 0, nullptr,
@@ -346,7 +347,7 @@ void msarow_fwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa
 
 void msarow_bwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa_in,
                 const float* msa_mask, const float* pair, const float* tbl, const void* save,
-                const float* dmsa_out, float* dmsa_in, float* dpair) {
+                const float* dmsa_out, float* dmsa_in, float* dpair, const float* sc) {
   nonnull(msa_in, "msarow msa"); nonnull(msa_mask, "msarow mask"); nonnull(pair, "msarow pair");
   nonnull(save, "msarow save"); nonnull(dmsa_out, "msarow dout"); nonnull(dmsa_in, "msarow din");
   nonnull(dpair, "msarow dpair");
@@ -360,24 +361,25 @@ void msarow_bwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa
   const int nch = attn_bwd_nchunk(S, b.rows_per_chunk);
   Arena& ar = arena();
   std::lock_guard<std::recursive_mutex> lk(ar.lock());
+  sc = module_scale(st, sc, dmsa_out, R * Cm);
   Sizer need;
-  need.take<bf16>((size_t)R * HD);
+  need.take<h16>((size_t)R * HD);
   need.take<float>((size_t)S * H * N);
-  need.take<bf16>((size_t)R * 4 * HD);
+  need.take<h16>((size_t)R * 4 * HD);
   need.take<float>((size_t)nch * H * M);
   need.take<float>((size_t)H * M);
   need.take<float>((size_t)R * Cm);
   ar.reset(st, need.off);
-  b.dO = ar.take_n<bf16>((size_t)R * HD);
+  b.dO = ar.take_n<h16>((size_t)R * HD);
   b.Dsum = ar.take_n<float>((size_t)S * H * N);
-  b.dqkvg = ar.take_n<bf16>((size_t)R * 4 * HD);
+  b.dqkvg = ar.take_n<h16>((size_t)R * 4 * HD);
   b.dbias_part = ar.take_n<float>((size_t)nch * H * M);
   b.dbias = ar.take_n<float>((size_t)H * M);
   float* dxn = ar.take_n<float>((size_t)R * Cm);
   EpiGateBwd eg;
   eg.qkvg = sv.qkvg; eg.ld = 4L * HD; eg.o = sv.o; eg.dO = b.dO; eg.dqkvg = b.dqkvg;
   eg.Dsum = b.Dsum; eg.HD = HD; eg.H = H; eg.D = a.D; eg.Ntok = N;
-  dout_gemm(st, a, R, dmsa_out, tbl, N, eg, "msarow.gemm_dout");
+  dout_gemm(st, a, R, dmsa_out, tbl, N, eg, "msarow.gemm_dout", sc);
   b.gate_done = true;
   AttnArgs& at = b.f;
   at.R = S; at.H = H; at.N = N; at.D = a.D;
@@ -392,10 +394,10 @@ void msarow_bwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa
   dx_gemm(st, a, R, b.dqkvg, dxn, "msarow.gemm_dx");
   KTimed kt("msarow.ln_bwd", st);
   ln_bwd_f32(st, dxn, msa_in, R, Cm, 0, a.ln_g, sv.mean, sv.rstd, dmsa_in, true, 0, nullptr,
-             nullptr, dmsa_out);
+             nullptr, dmsa_out, sc + 1);
   // pair gradient: only through the bias projection
   ln_bwd_f32(st, nullptr, pair, M, w.Cz, 0, w.pn_g, sv.pmean, sv.prstd, dpair, true, H, b.dbias,
-             w.w2d);
+             w.w2d, nullptr, sc + 1);
 }
 
 void msacol_fwd(hipStream_t st, const MsaColW& w, int S, int N, const float* msa_in,
@@ -411,8 +413,8 @@ void msacol_fwd(hipStream_t st, const MsaColW& w, int S, int N, const float* msa
   Arena& ar = arena();
   std::lock_guard<std::recursive_mutex> lk(ar.lock());
   ar.reset(st, (size_t)R * Cm * 2 + (size_t)R * HD * 2 + 1024);
-  bf16* xn = ar.take_n<bf16>((size_t)R * Cm);
-  bf16* og = ar.take_n<bf16>((size_t)R * HD);
+  h16* xn = ar.take_n<h16>((size_t)R * Cm);
+  h16* og = ar.take_n<h16>((size_t)R * HD);
   {
     KTimed kt("msacol.ln", st);
     ln_fwd_f32(st, msa_in, R, Cm, 0, a.ln_g, a.ln_b, xn, sv.mean, sv.rstd, false, 0, nullptr,
@@ -429,7 +431,7 @@ void msacol_fwd(hipStream_t st, const MsaColW& w, int S, int N, const float* msa
 
 void msacol_bwd(hipStream_t st, const MsaColW& w, int S, int N, const float* msa_in,
                 const float* msa_mask, const float* tbl, const void* save,
-                const float* dmsa_out, float* dmsa_in) {
+                const float* dmsa_out, float* dmsa_in, const float* sc) {
   nonnull(msa_in, "msacol msa"); nonnull(msa_mask, "msacol mask"); nonnull(save, "msacol save");
   nonnull(dmsa_out, "msacol dout"); nonnull(dmsa_in, "msacol din");
   const AttnW& a = w.a;
@@ -439,15 +441,17 @@ void msacol_bwd(hipStream_t st, const MsaColW& w, int S, int N, const float* msa
   MsaColSave<Carver> sv(cv, S, N, Cm, H);
   Arena& ar = arena();
   std::lock_guard<std::recursive_mutex> lk(ar.lock());
+  sc = module_scale(st, sc, dmsa_out, R * Cm);
   Sizer need;
-  need.take<bf16>((size_t)R * HD);
-  need.take<bf16>((size_t)R * 4 * HD);
+  need.take<h16>((size_t)R * HD);
+  need.take<h16>((size_t)R * 4 * HD);
   need.take<float>((size_t)R * Cm);
   ar.reset(st, need.off);
-  bf16* dog = ar.take_n<bf16>((size_t)R * HD);
-  bf16* dqkvg = ar.take_n<bf16>((size_t)R * 4 * HD);
+  h16* dog = ar.take_n<h16>((size_t)R * HD);
+  h16* dqkvg = ar.take_n<h16>((size_t)R * 4 * HD);
   float* dxn = ar.take_n<float>((size_t)R * Cm);
-  dout_gemm(st, a, R, dmsa_out, tbl, N, EpiStore<bf16>{dog, HD, 0, nullptr, HD}, "msacol.gemm_dout");
+  dout_gemm(st, a, R, dmsa_out, tbl, N, EpiStore<h16>{dog, HD, 0, nullptr, HD}, "msacol.gemm_dout",
+            sc);
   {
     KTimed kt("msacol.attn_bwd", st);
     hipLaunchKernelGGL(small_attn_bwd_kernel, dim3(N * H), dim3(64), 0, st, sv.qkvg, 4L * HD, S, N,
@@ -456,7 +460,7 @@ void msacol_bwd(hipStream_t st, const MsaColW& w, int S, int N, const float* msa
   dx_gemm(st, a, R, dqkvg, dxn, "msacol.gemm_dx");
   KTimed kt("msacol.ln_bwd", st);
   ln_bwd_f32(st, dxn, msa_in, R, Cm, 0, a.ln_g, sv.mean, sv.rstd, dmsa_in, true, 0, nullptr,
-             nullptr, dmsa_out);
+             nullptr, dmsa_out, sc + 1);
 }
 
 }  // namespace bc2n

@@ -17,12 +17,12 @@ namespace bc2n {
 
 namespace {
 
-// lr = (acc + b) * mask -> left_t [N][S][O] and right [S*N][O] (bf16)
+// lr = (acc + b) * mask -> left_t [N][S][O] and right [S*N][O] (h16)
 struct EpiOpmLR : EpiRows {
-  bf16 *left_t, *right;
+  h16 *left_t, *right;
   const float *b, *mask;
   int S, N, O;
-  EpiOpmLR(bf16* l, bf16* r, const float* bb, const float* mk, int s, int n, int o)
+  EpiOpmLR(h16* l, h16* r, const float* bb, const float* mk, int s, int n, int o)
       : left_t(l), right(r), b(bb), mask(mk), S(s), N(n), O(o) {}
   __device__ __forceinline__ void row(int, int m, int n, const float (&v)[8]) const {
     const int s = m / N, r = m % N;
@@ -31,21 +31,21 @@ struct EpiOpmLR : EpiRows {
     ld_f8(b + n, bb);
 #pragma unroll
     for (int e = 0; e < 8; ++e) x[e] = (v[e] + bb[e]) * mk;
-    if (n < O) st_b8f(left_t + ((long)r * S + s) * O + n, x);
-    else st_b8f(right + (long)m * O + (n - O), x);
+    if (n < O) st_h8f(left_t + ((long)r * S + s) * O + n, x);
+    else st_h8f(right + (long)m * O + (n - O), x);
   }
 };
 
 // R'[(s,j)][(c,f)] -> Rp[(j,f)][(s,c)]  (the main GEMM's K-contiguous B)
 struct EpiOpmR : EpiRows {
-  bf16* rp;
+  h16* rp;
   int S, N, O, C;
-  EpiOpmR(bf16* r, int s, int n, int o, int c) : rp(r), S(s), N(n), O(o), C(c) {}
+  EpiOpmR(h16* r, int s, int n, int o, int c) : rp(r), S(s), N(n), O(o), C(c) {}
   __device__ __forceinline__ void row(int, int m, int n, const float (&v)[8]) const {
     const int s = m / N, jj = m % N;
     const int c = n / C, f0 = n % C;  // 8 columns share c (C % 8 == 0)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) rp[(((long)jj * C + f0 + e) * S + s) * O + c] = (bf16)v[e];
+    for (int e = 0; e < 8; ++e) rp[(((long)jj * C + f0 + e) * S + s) * O + c] = (h16)v[e];
   }
 };
 
@@ -78,15 +78,15 @@ struct EpiOpmOut : EpiRows {
   }
 };
 
-// dR'[(s,c)][(j,f)] -> dRp2[(s,j)][(c,f)] (bf16)
+// dR'[(s,c)][(j,f)] -> dRp2[(s,j)][(c,f)] (h16)
 struct EpiOpmDR : EpiRows {
-  bf16* d;
+  h16* d;
   int S, N, O, C;
-  EpiOpmDR(bf16* dd, int s, int n, int o, int c) : d(dd), S(s), N(n), O(o), C(c) {}
+  EpiOpmDR(h16* dd, int s, int n, int o, int c) : d(dd), S(s), N(n), O(o), C(c) {}
   __device__ __forceinline__ void row(int, int m, int n, const float (&v)[8]) const {
     const int s = m / O, c = m % O;
     const int jj = n / C, f0 = n % C;
-    st_b8f(d + ((long)s * N + jj) * O * C + (long)c * C + f0, v);
+    st_h8f(d + ((long)s * N + jj) * O * C + (long)c * C + f0, v);
   }
 };
 
@@ -100,24 +100,25 @@ __global__ void opm_norm_kernel(const float* __restrict__ mask, int S, int N,
   normf[idx] = 1.f / (1e-3f + s);
 }
 
-// d_act[i][(j,f)] = bf16(dout * tbl[j][f] * normf[i][j])
+// d_act[i][(j,f)] = h16(s * dout * tbl[j][f] * normf[i][j]), s = sc[0] (the
+// cotangent scale)
 __global__ void opm_dact_kernel(const float* __restrict__ dout, const float* __restrict__ tbl,
                                 const float* __restrict__ normf, int N, int C,
-                                bf16* __restrict__ dact) {
+                                const float* __restrict__ sc, h16* __restrict__ dact) {
   const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (long)N * N * C) return;
   const long ij = idx / C;
   const int f = (int)(idx % C);
-  float x = dout[idx] * normf[ij];
+  float x = dout[idx] * normf[ij] * sc[0];
   if (tbl) x *= tbl[(ij % N) * C + f];
-  dact[idx] = (bf16)x;
+  dact[idx] = f2h_sat(x);
 }
 
 // dlr[(s,r)][col0 + c] = mask[s][r] * sum_chunk part[chunk][row(r,s)][c]
 // left:  part rows are residues r, columns (s,c);   right: rows (s,r), cols c
 __global__ void opm_reduce_kernel(const float* __restrict__ part, int nch, long chunk_stride,
                                   int rows, int cols, const float* __restrict__ mask, int S, int N,
-                                  int O, bool left, bf16* __restrict__ dlr) {
+                                  int O, bool left, h16* __restrict__ dlr) {
   const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (long)rows * cols) return;
   // eight partials loaded at a time (in flight together), added in chunk order
@@ -136,19 +137,19 @@ __global__ void opm_reduce_kernel(const float* __restrict__ part, int nch, long 
   if (left) { r = row; sr = col / O; c = col % O; }
   else { sr = row / N; r = row % N; c = col; }
   const long m = (long)sr * N + r;
-  dlr[m * 2 * O + (left ? 0 : O) + c] = (bf16)(s * mask[m]);
+  dlr[m * 2 * O + (left ? 0 : O) + c] = f2h_sat(s * mask[m]);
 }
 
 template <class A>
 struct OpmSave {
   float *mean, *rstd, *normf;
-  bf16 *left_t, *rp;
+  h16 *left_t, *rp;
   OpmSave(A& a, int S, int N, int O, int C) {
     mean = a.template take<float>((size_t)S * N);
     rstd = a.template take<float>((size_t)S * N);
     normf = a.template take<float>((size_t)N * N);
-    left_t = a.template take<bf16>((size_t)N * S * O);
-    rp = a.template take<bf16>((size_t)N * C * S * O);
+    left_t = a.template take<h16>((size_t)N * S * O);
+    rp = a.template take<h16>((size_t)N * C * S * O);
   }
 };
 
@@ -182,26 +183,26 @@ OpmW opm_weights(WeightStore& ws, const std::string& P) {
       }
     return c;
   };
-  w.wlr = ws.derived<bf16>("opm.wlr:" + P, [&] { return to_bf16(wlr()); });
-  w.wlr_t = ws.derived<bf16>("opm.wlr_t:" + P, [&] {
+  w.wlr = ws.derived<h16>("opm.wlr:" + P, [&] { return to_h16(wlr()); });
+  w.wlr_t = ws.derived<h16>("opm.wlr_t:" + P, [&] {
     std::vector<float> c = wlr();
-    return transpose_bf16(c.data(), Cm, 2 * O);
+    return transpose_h16(c.data(), Cm, 2 * O);
   });
   // wt[(c,f)][e] = W[c,e,f]; wt2[e][(c,f)] = W[c,e,f]
-  w.wt = ws.derived<bf16>("opm.wt:" + P, [&] {
-    std::vector<bf16> t((size_t)O * C * O);
+  w.wt = ws.derived<h16>("opm.wt:" + P, [&] {
+    std::vector<h16> t((size_t)O * C * O);
     for (int c = 0; c < O; ++c)
       for (int e = 0; e < O; ++e)
         for (int f = 0; f < C; ++f)
-          t[((size_t)c * C + f) * O + e] = (bf16)ow.data[((size_t)c * O + e) * C + f];
+          t[((size_t)c * C + f) * O + e] = (h16)ow.data[((size_t)c * O + e) * C + f];
     return t;
   });
-  w.wt2 = ws.derived<bf16>("opm.wt2:" + P, [&] {
-    std::vector<bf16> t((size_t)O * O * C);
+  w.wt2 = ws.derived<h16>("opm.wt2:" + P, [&] {
+    std::vector<h16> t((size_t)O * O * C);
     for (int c = 0; c < O; ++c)
       for (int e = 0; e < O; ++e)
         for (int f = 0; f < C; ++f)
-          t[(size_t)e * O * C + (size_t)c * C + f] = (bf16)ow.data[((size_t)c * O + e) * C + f];
+          t[(size_t)e * O * C + (size_t)c * C + f] = (h16)ow.data[((size_t)c * O + e) * C + f];
     return t;
   });
   return w;
@@ -226,8 +227,8 @@ void opm_fwd(hipStream_t st, const OpmW& w, int S, int N, const float* msa, cons
   Arena& ar = arena();
   std::lock_guard<std::recursive_mutex> lk(ar.lock());
   ar.reset(st, (size_t)R * Cm * 2 + (size_t)R * O * 2 + 1024);
-  bf16* xn = ar.take_n<bf16>((size_t)R * Cm);
-  bf16* right = ar.take_n<bf16>((size_t)R * O);
+  h16* xn = ar.take_n<h16>((size_t)R * Cm);
+  h16* right = ar.take_n<h16>((size_t)R * O);
   {
     KTimed kt("opm.ln", st);
     ln_fwd_f32(st, msa, R, Cm, 0, w.ln_g, w.ln_b, xn, sv.mean, sv.rstd, false, 0, nullptr, nullptr);
@@ -254,7 +255,7 @@ void opm_fwd(hipStream_t st, const OpmW& w, int S, int N, const float* msa, cons
 
 void opm_bwd(hipStream_t st, const OpmW& w, int S, int N, const float* msa, const float* msa_mask,
              const float* tbl, const void* save, const float* dpair, const float* dmsa_out,
-             float* dmsa_in) {
+             float* dmsa_in, const float* sc) {
   nonnull(msa, "opm msa"); nonnull(msa_mask, "opm mask"); nonnull(save, "opm save");
   nonnull(dpair, "opm dpair"); nonnull(dmsa_out, "opm dout"); nonnull(dmsa_in, "opm din");
   const int Cm = w.Cm, O = w.O, C = w.C;
@@ -268,25 +269,26 @@ void opm_bwd(hipStream_t st, const OpmW& w, int S, int N, const float* msa, cons
   if (NC % kc1 != 0 || (O * C) % kc2 != 0) throw std::runtime_error("opm: unsupported split");
   Arena& ar = arena();
   std::lock_guard<std::recursive_mutex> lk(ar.lock());
+  sc = module_scale(st, sc, dpair, (long)N * NC);
   Sizer need;
-  need.take<bf16>((size_t)N * NC);
+  need.take<h16>((size_t)N * NC);
   need.take<float>((size_t)nch1 * N * S * O);
-  need.take<bf16>((size_t)R * O * C);
+  need.take<h16>((size_t)R * O * C);
   need.take<float>((size_t)nch2 * R * O);
-  need.take<bf16>((size_t)R * 2 * O);
+  need.take<h16>((size_t)R * 2 * O);
   need.take<float>((size_t)R * Cm);
   ar.reset(st, need.off);
-  bf16* dact = ar.take_n<bf16>((size_t)N * NC);
+  h16* dact = ar.take_n<h16>((size_t)N * NC);
   float* p1 = ar.take_n<float>((size_t)nch1 * N * S * O);
-  bf16* drp = ar.take_n<bf16>((size_t)R * O * C);
+  h16* drp = ar.take_n<h16>((size_t)R * O * C);
   float* p2 = ar.take_n<float>((size_t)nch2 * R * O);
-  bf16* dlr = ar.take_n<bf16>((size_t)R * 2 * O);
+  h16* dlr = ar.take_n<h16>((size_t)R * 2 * O);
   float* dxn = ar.take_n<float>((size_t)R * Cm);
   {
     KTimed kt("opm.dact", st);
     const long n = (long)N * NC;
     hipLaunchKernelGGL(opm_dact_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, dpair,
-                       tbl, sv.normf, N, C, dact);
+                       tbl, sv.normf, N, C, sc, dact);
   }
   {  // dleft partials: [chunk][i][(s,c)]
     GemmArgs g;
@@ -325,7 +327,7 @@ void opm_bwd(hipStream_t st, const OpmW& w, int S, int N, const float* msa, cons
   gemm<128, 128>(st, g5, EpiStore<float>{dxn, Cm, 0, nullptr, Cm}, "opm.gemm_dx");
   KTimed kt("opm.ln_bwd", st);
   ln_bwd_f32(st, dxn, msa, R, Cm, 0, w.ln_g, sv.mean, sv.rstd, dmsa_in, true, 0, nullptr, nullptr,
-             dmsa_out);
+             dmsa_out, sc + 1);
 }
 
 }  // namespace bc2n

@@ -67,16 +67,16 @@ WeightStore& weights(const std::string& dir) {
   return *p;
 }
 
-std::vector<bf16> to_bf16(const std::vector<float>& v) {
-  std::vector<bf16> o(v.size());
-  for (size_t i = 0; i < v.size(); ++i) o[i] = (bf16)v[i];
+std::vector<h16> to_h16(const std::vector<float>& v) {
+  std::vector<h16> o(v.size());
+  for (size_t i = 0; i < v.size(); ++i) o[i] = (h16)v[i];
   return o;
 }
 
-std::vector<bf16> transpose_bf16(const float* src, int rows, int cols) {
-  std::vector<bf16> o((size_t)rows * cols);
+std::vector<h16> transpose_h16(const float* src, int rows, int cols) {
+  std::vector<h16> o((size_t)rows * cols);
   for (int r = 0; r < rows; ++r)
-    for (int c = 0; c < cols; ++c) o[(size_t)c * rows + r] = (bf16)src[(size_t)r * cols + c];
+    for (int c = 0; c < cols; ++c) o[(size_t)c * rows + r] = (h16)src[(size_t)r * cols + c];
   return o;
 }
 
@@ -100,13 +100,6 @@ void* Arena::take(size_t bytes) {
   void* r = base_ + off_;
   off_ += b;
   return r;
-}
-
-std::vector<f16> transpose_f16(const float* src, int rows, int cols) {
-  std::vector<f16> o((size_t)rows * cols);
-  for (int r = 0; r < rows; ++r)
-    for (int c = 0; c < cols; ++c) o[(size_t)c * rows + r] = (f16)src[(size_t)r * cols + c];
-  return o;
 }
 
 Arena& arena() {

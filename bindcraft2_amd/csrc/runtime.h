@@ -28,7 +28,7 @@ struct HostTensor {
 // A weights directory as written by the reference's manifest writer
 // (bindcraft/af/native.py weights_from_params): manifest.txt plus one .f32
 // file per parameter, names param/block{b}/<module path>/<param>.  Device
-// forms (f32 copies, transposed bf16 GEMM operands) are built on first use
+// forms (f32 copies, transposed h16 GEMM operands) are built on first use
 // and kept for the life of the process.
 class WeightStore {
  public:
@@ -62,11 +62,9 @@ class WeightStore {
 WeightStore& weights(const std::string& dir);
 
 // Host-side conversions used to build GEMM operands.
-std::vector<bf16> to_bf16(const std::vector<float>& v);
-// [rows][cols] f32 -> [cols][rows] bf16
-std::vector<bf16> transpose_bf16(const float* src, int rows, int cols);
-// The same transpose to binary16 (operands of the GEMMs launched with F16).
-std::vector<f16> transpose_f16(const float* src, int rows, int cols);
+std::vector<h16> to_h16(const std::vector<float>& v);
+// [rows][cols] f32 -> [cols][rows] h16
+std::vector<h16> transpose_h16(const float* src, int rows, int cols);
 
 // Grow-only device scratch arena, carved by bump allocation per call.  One
 // arena per device; callers hold `lock()` for the duration of a call.

@@ -10,8 +10,8 @@ struct TplEmbedW {
   const float *b8 = nullptr;                     // template_pair_embedding_8 bias
   const float *on_g = nullptr, *on_b = nullptr;  // output_layer_norm
   const float *bo = nullptr;                     // output_linear bias
-  const bf16 *w8 = nullptr, *w8_t = nullptr;     // [128][64] and its transpose
-  const bf16 *wo = nullptr, *wo_t = nullptr;     // [64][128] and its transpose
+  const h16 *w8 = nullptr, *w8_t = nullptr;     // [128][64] and its transpose
+  const h16 *wo = nullptr, *wo_t = nullptr;     // [64][128] and its transpose
   StackW stack;
   int depth = 0;
 };

@@ -26,7 +26,7 @@ constexpr int CT = 64;   // template stack channels
 template <class A>
 struct TplEmbedSave {
   float *qmean, *qrstd, *omean, *orstd, *act2;
-  bf16* y;
+  h16* y;
   void* stack;
   TplEmbedSave(A& a, int N, size_t stack_bytes) {
     const size_t M = (size_t)N * N;
@@ -35,7 +35,7 @@ struct TplEmbedSave {
     omean = a.template take<float>(M);
     orstd = a.template take<float>(M);
     act2 = a.template take<float>(M * CT);
-    y = a.template take<bf16>(M * CT);
+    y = a.template take<h16>(M * CT);
     stack = a.template take<char>(stack_bytes);
   }
 };
@@ -56,10 +56,10 @@ TplEmbedW tplembed_weights(WeightStore& ws, int depth) {
   w.on_g = ws.f32(P + "output_layer_norm/scale");
   w.on_b = ws.f32(P + "output_layer_norm/offset");
   w.bo = ws.f32(P + "output_linear/bias");
-  w.w8 = ws.derived<bf16>("tplembed.w8", [&] { return to_bf16(w8.data); });
-  w.w8_t = ws.derived<bf16>("tplembed.w8_t", [&] { return transpose_bf16(w8.data.data(), CQ, CT); });
-  w.wo = ws.derived<bf16>("tplembed.wo", [&] { return to_bf16(wo.data); });
-  w.wo_t = ws.derived<bf16>("tplembed.wo_t", [&] { return transpose_bf16(wo.data.data(), CT, CQ); });
+  w.w8 = ws.derived<h16>("tplembed.w8", [&] { return to_h16(w8.data); });
+  w.w8_t = ws.derived<h16>("tplembed.w8_t", [&] { return transpose_h16(w8.data.data(), CQ, CT); });
+  w.wo = ws.derived<h16>("tplembed.wo", [&] { return to_h16(wo.data); });
+  w.wo_t = ws.derived<h16>("tplembed.wo_t", [&] { return transpose_h16(wo.data.data(), CT, CQ); });
   w.stack = stack_weights(ws, depth, StackKind::TEMPLATE);
   w.depth = depth;
   return w;
@@ -94,7 +94,7 @@ void tplembed_fwd(hipStream_t st, const TplEmbedW& w, int N, const float* query,
     Arena& ar = arena();
     std::lock_guard<std::recursive_mutex> lk(ar.lock());
     ar.reset(st, (size_t)M * CQ * 2 + 1024);
-    bf16* qn = ar.take_n<bf16>((size_t)M * CQ);
+    h16* qn = ar.take_n<h16>((size_t)M * CQ);
     {
       KTimed kt("tplembed.ln_query", st);
       ln_fwd_f32(st, query, M, CQ, 0, w.qn_g, w.qn_b, qn, sv.qmean, sv.qrstd, false, 0, nullptr,
@@ -121,7 +121,7 @@ void tplembed_fwd(hipStream_t st, const TplEmbedW& w, int N, const float* query,
   g.a_sm = CT; g.a_sk = 1;
   g.B = w.wo_t; g.b_sn = CT; g.b_sk = 1;
   gemm<128, 128>(st, g, EpiStore<float>{out, CQ, 0, w.bo, CQ}, "tplembed.gemm_out",
-                 ALoadReluBf16{sv.y, CT});
+                 ALoadRelu16{sv.y, CT});
 }
 
 void tplembed_bwd(hipStream_t st, const TplEmbedW& w, int N, const float* query,
@@ -143,16 +143,18 @@ void tplembed_bwd(hipStream_t st, const TplEmbedW& w, int N, const float* query,
     std::lock_guard<std::recursive_mutex> lk(ar.lock());
     ar.reset(st, (size_t)M * CT * 4 + 1024);
     float* dy = ar.take_n<float>((size_t)M * CT);
-    // d(y) = (dout . Wo^T) * (y > 0)
+    // d(y) = (s dout . Wo^T) * (y > 0), s the cotangent scale of dout
+    float* sc = ct_scale_slot(3);
+    ct_scale(st, dout, M * CQ, sc);
     GemmArgs g;
     g.M = (int)M; g.N = CT; g.K = CQ;
     g.a_sm = CQ; g.a_sk = 1;
     g.B = w.wo; g.b_sn = CQ; g.b_sk = 1;
     gemm<128, 128>(st, g, EpiReluMask<float>(dy, sv.y, CT), "tplembed.gemm_dout",
-                   ALoadScaledRows{dout, nullptr, N, CQ, false});
+                   ALoadScaledRows{dout, nullptr, N, CQ, false, sc});
     KTimed kt("tplembed.ln_out_bwd", st);
     ln_bwd_f32(st, dy, sv.act2, M, CT, 0, w.on_g, sv.omean, sv.orstd, dact, false, 0, nullptr,
-               nullptr);
+               nullptr, nullptr, sc + 1);
   }
   stack_bwd(st, w.stack, N, 1, w.depth, pmask, nullptr, dropout, sv.stack, dact, nullptr, dact,
             nullptr);
@@ -160,16 +162,19 @@ void tplembed_bwd(hipStream_t st, const TplEmbedW& w, int N, const float* query,
   std::lock_guard<std::recursive_mutex> lk(ar.lock());
   ar.reset(st, (size_t)M * CQ * 4 + 1024);
   float* dq = ar.take_n<float>((size_t)M * CQ);
-  // d(q) = d(act) . W8^T, then the query LayerNorm's backward
+  // d(q) = d(act) . W8^T (scaled by the cotangent scale of d(act)), then the
+  // query LayerNorm's backward, which divides it out
+  float* sc = ct_scale_slot(3);
+  ct_scale(st, dact, M * CT, sc);
   GemmArgs g;
   g.M = (int)M; g.N = CQ; g.K = CT;
   g.a_sm = CT; g.a_sk = 1;
   g.B = w.w8; g.b_sn = CT; g.b_sk = 1;
   gemm<128, 128>(st, g, EpiStore<float>{dq, CQ, 0, nullptr, CQ}, "tplembed.gemm_dq",
-                 ALoadScaledRows{dact, nullptr, N, CT, false});
+                 ALoadScaledRows{dact, nullptr, N, CT, false, sc});
   KTimed kt("tplembed.ln_query_bwd", st);
   ln_bwd_f32(st, dq, query, M, CQ, 0, w.qn_g, sv.qmean, sv.qrstd, dquery, false, 0, nullptr,
-             nullptr);
+             nullptr, nullptr, sc + 1);
 }
 
 }  // namespace bc2n

@@ -4,14 +4,10 @@
 // Backward: dh = ((tbl*dout) . W2^T) * (h > 0), the dropout scale applied as
 // the GEMM loads A; dxn = dh . W1^T; LN backward accumulated into din.
 //
-// The forward's operands (LN output, hidden layer, weights) are binary16,
-// not bf16: the backward's ReLU mask is h > 0, and every pre-activation the
-// rounding moves across zero flips a mask entry against the exact model.
-// bf16 operands flip about 0.1% of them, which is 4-5% of d(hidden) in L2;
-// binary16's 3 extra significand bits cut that 8-fold at the same MFMA rate.
-// Both operands are bounded (LayerNorm outputs, ReLU outputs of O(1)
-// pre-activations, weights), far inside binary16's range.  The backward
-// stays bf16 (cotangents have no such bound).
+// The backward's ReLU mask is h > 0, and every pre-activation that rounding
+// moves across zero flips a mask entry against the exact model: with bf16
+// operands about 0.1% of them flip, 4-5% of d(hidden) in L2; the binary16
+// operands flip 8x fewer.
 // Reference: modules.py:252-305 (Transition); native/transition.cuh:313-675.
 #include "gemm.h"
 #include "modules.h"
@@ -23,11 +19,11 @@ namespace {
 template <class A>
 struct TransSave {
   float *mean, *rstd;
-  f16* h;  // relu(xn . W1 + b1), binary16
+  h16* h;  // relu(xn . W1 + b1)
   TransSave(A& a, long rows, int C, int F) {
     mean = a.template take<float>(rows);
     rstd = a.template take<float>(rows);
-    h = a.template take<f16>((size_t)rows * C * F);
+    h = a.template take<h16>((size_t)rows * C * F);
   }
 };
 
@@ -44,10 +40,10 @@ TransW transition_weights(WeightStore& ws, const std::string& P) {
   w.b1 = ws.f32(P + "transition1/bias");
   w.b2 = ws.f32(P + "transition2/bias");
   const HostTensor& w2 = ws.host(P + "transition2/weights");  // [F*C, C]
-  w.w1 = ws.derived<bf16>("trans.w1:" + P, [&] { return to_bf16(w1.data); });
-  w.w1_t = ws.derived<f16>("trans.w1_t16:" + P, [&] { return transpose_f16(w1.data.data(), C, H); });
-  w.w2 = ws.derived<bf16>("trans.w2:" + P, [&] { return to_bf16(w2.data); });
-  w.w2_t = ws.derived<f16>("trans.w2_t16:" + P, [&] { return transpose_f16(w2.data.data(), H, C); });
+  w.w1 = ws.derived<h16>("trans.w1:" + P, [&] { return to_h16(w1.data); });
+  w.w1_t = ws.derived<h16>("trans.w1_t:" + P, [&] { return transpose_h16(w1.data.data(), C, H); });
+  w.w2 = ws.derived<h16>("trans.w2:" + P, [&] { return to_h16(w2.data); });
+  w.w2_t = ws.derived<h16>("trans.w2_t:" + P, [&] { return transpose_h16(w2.data.data(), H, C); });
   return w;
 }
 
@@ -67,29 +63,27 @@ void transition_fwd(hipStream_t st, const TransW& w, long rows, int nt, const fl
   Arena& ar = arena();
   std::lock_guard<std::recursive_mutex> lk(ar.lock());
   ar.reset(st, (size_t)rows * C * 2 + 256);
-  f16* xn = ar.take_n<f16>((size_t)rows * C);
+  h16* xn = ar.take_n<h16>((size_t)rows * C);
   {
     KTimed kt("trans.ln_fwd", st);
-    ln_fwd_f32(st, act_in, rows, C, 0, w.ln_g, w.ln_b, reinterpret_cast<bf16*>(xn), sv.mean,
-               sv.rstd, false, 0, nullptr, nullptr, 1.f, /*y_f16=*/true);
+    ln_fwd_f32(st, act_in, rows, C, 0, w.ln_g, w.ln_b, xn, sv.mean, sv.rstd, false, 0, nullptr,
+               nullptr);
   }
-  // binary16 operand words in the GEMMs' 16-bit operand slots
-  auto w16 = [](const f16* p) { return reinterpret_cast<const bf16*>(p); };
   GemmArgs g1;
   g1.M = (int)rows; g1.N = H; g1.K = C;
-  g1.A = w16(xn); g1.a_sm = C; g1.a_sk = 1;
-  g1.B = w16(w.w1_t); g1.b_sn = C; g1.b_sk = 1;
-  gemm<128, 128, true>(st, g1, EpiStore<f16, true>{sv.h, H, 0, w.b1, H}, "trans.gemm1");
+  g1.A = xn; g1.a_sm = C; g1.a_sk = 1;
+  g1.B = w.w1_t; g1.b_sn = C; g1.b_sk = 1;
+  gemm<128, 128>(st, g1, EpiStore<h16, true>{sv.h, H, 0, w.b1, H}, "trans.gemm1");
   GemmArgs g2;
   g2.M = (int)rows; g2.N = C; g2.K = H;
-  g2.A = w16(sv.h); g2.a_sm = H; g2.a_sk = 1;
-  g2.B = w16(w.w2_t); g2.b_sn = H; g2.b_sk = 1;
-  gemm<128, 128, true>(st, g2, EpiResidualRows(act_in, act_out, w.b2, tbl, nt, C, false),
-                       "trans.gemm2");
+  g2.A = sv.h; g2.a_sm = H; g2.a_sk = 1;
+  g2.B = w.w2_t; g2.b_sn = H; g2.b_sk = 1;
+  gemm<128, 128>(st, g2, EpiResidualRows(act_in, act_out, w.b2, tbl, nt, C, false), "trans.gemm2");
 }
 
 void transition_bwd(hipStream_t st, const TransW& w, long rows, int nt, const float* act_in,
-                    const float* tbl, const void* save, const float* dout, float* din) {
+                    const float* tbl, const void* save, const float* dout, float* din,
+                    const float* sc) {
   nonnull(act_in, "transition act"); nonnull(save, "transition save");
   nonnull(dout, "transition dout"); nonnull(din, "transition din");
   const int C = w.C, H = w.C * w.F;
@@ -97,33 +91,36 @@ void transition_bwd(hipStream_t st, const TransW& w, long rows, int nt, const fl
   TransSave<Carver> sv(cv, rows, C, w.F);
   Arena& ar = arena();
   std::lock_guard<std::recursive_mutex> lk(ar.lock());
+  sc = module_scale(st, sc, dout, rows * C);
   Sizer need;
-  need.take<bf16>((size_t)rows * H);
+  need.take<h16>((size_t)rows * H);
   need.take<float>((size_t)rows * C);
   ar.reset(st, need.off);
-  bf16* dh = ar.take_n<bf16>((size_t)rows * H);
+  h16* dh = ar.take_n<h16>((size_t)rows * H);
   float* dxn = ar.take_n<float>((size_t)rows * C);
   // dH = ((tbl * dout) . W2^T) * (H > 0), the dropout scale applied as A is loaded
   GemmArgs g1;
   g1.M = (int)rows; g1.N = H; g1.K = C;
   g1.a_sm = C; g1.a_sk = 1;
   g1.B = w.w2; g1.b_sn = C; g1.b_sk = 1;
-  gemm<128, 128>(st, g1, EpiReluMask<bf16, f16>(dh, sv.h, H), "trans.gemm_dh",
-                 ALoadScaledRows{dout, tbl, nt, C, false});
+  gemm<128, 128>(st, g1, EpiReluMask<h16>(dh, sv.h, H), "trans.gemm_dh",
+                 ALoadScaledRows{dout, tbl, nt, C, false, sc});
   GemmArgs g2;
   g2.M = (int)rows; g2.N = C; g2.K = H;
   g2.A = dh; g2.a_sm = H; g2.a_sk = 1;
   g2.B = w.w1; g2.b_sn = H; g2.b_sk = 1;
   if (C == 128) {
     // the input LayerNorm's backward and the residual add in the epilogue
-    gemm<128, 128>(st, g2, EpiLnBwd<0>(act_in, w.ln_g, sv.mean, sv.rstd, dout, din, rows, 0),
+    gemm<128, 128>(st, g2,
+                   EpiLnBwd<0>(act_in, w.ln_g, sv.mean, sv.rstd, dout, din, rows, 0, nullptr,
+                               nullptr, sc + 1),
                    "trans.gemm_dx_ln");
     return;
   }
   gemm<128, 128>(st, g2, EpiStore<float>{dxn, C, 0, nullptr, C}, "trans.gemm_dx");
   KTimed kt("trans.ln_bwd", st);
   ln_bwd_f32(st, dxn, act_in, rows, C, 0, w.ln_g, sv.mean, sv.rstd, din, true, 0, nullptr, nullptr,
-             dout);
+             dout, sc + 1);
 }
 
 }  // namespace bc2n

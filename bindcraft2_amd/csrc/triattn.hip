@@ -1,11 +1,13 @@
 // Triangle attention (starting / ending node), forward and backward.
 //
 // Forward, in the module's frame (the transposed pair for the ending node):
-//   LN (two-pass) + fused pair-bias projection  -> xn bf16, bias[H][M] (log2 e)
+//   LN (two-pass) + fused pair-bias projection  -> xn h16, bias[H][M] (log2 e)
 //   GEMM xn . [Wq|Wk|Wv|Wg]  (q scaled by D^-1/2 log2 e, +gating_b)  -> qkvg
 //   flash attention (mask per row/key, bias per head)               -> o, og, lse
 //   GEMM og . Wo + bo, fused residual + shared dropout (+ transposed write)
 // Backward replays nothing: the save-set holds LN stats, bias, qkvg, o, lse.
+// It runs on the cotangent times the module's scale s (ct_scale): loaded so
+// by the first GEMM, divided out by the LayerNorm backward that ends it.
 //   GEMM (tbl * dout) . Wo^T, the scale applied as A is loaded (transposed
 //        read for the ending node), epilogue through the gate -> dO, dG, Dsum
 //   attention backward                    -> dq|dk|dv, d(bias)
@@ -24,15 +26,15 @@ namespace {
 template <class A>
 struct TriAttnSave {
   float *mean, *rstd, *bias, *lse;
-  bf16 *qkvg, *o;
+  h16 *qkvg, *o;
   TriAttnSave(A& a, int N, int C, int H) {
     const size_t M = (size_t)N * N;
     mean = a.template take<float>(M);
     rstd = a.template take<float>(M);
     bias = a.template take<float>((size_t)H * M);
     lse = a.template take<float>((size_t)H * M);
-    qkvg = a.template take<bf16>(M * 4 * C);
-    o = a.template take<bf16>(M * C);
+    qkvg = a.template take<h16>(M * 4 * C);
+    o = a.template take<h16>(M * C);
   }
 };
 
@@ -61,10 +63,10 @@ TriAttnW triattn_weights(WeightStore& ws, const std::string& P) {
     }
     return c;
   };
-  w.wqkvg = ws.derived<bf16>("triattn.wqkvg:" + P, [&] { return to_bf16(cat()); });
-  w.wqkvg_t = ws.derived<bf16>("triattn.wqkvg_t:" + P, [&] {
+  w.wqkvg = ws.derived<h16>("triattn.wqkvg:" + P, [&] { return to_h16(cat()); });
+  w.wqkvg_t = ws.derived<h16>("triattn.wqkvg_t:" + P, [&] {
     std::vector<float> c = cat();
-    return transpose_bf16(c.data(), C, 4 * HD);
+    return transpose_h16(c.data(), C, 4 * HD);
   });
   w.bqkvg = ws.derived<float>("triattn.bqkvg:" + P, [&] {
     std::vector<float> b((size_t)4 * HD, 0.f);
@@ -73,8 +75,8 @@ TriAttnW triattn_weights(WeightStore& ws, const std::string& P) {
     return b;
   });
   const HostTensor& ow = ws.host(P + "attention/output_w");  // [H,D,C]
-  w.wo = ws.derived<bf16>("triattn.wo:" + P, [&] { return to_bf16(ow.data); });
-  w.wo_t = ws.derived<bf16>("triattn.wo_t:" + P, [&] { return transpose_bf16(ow.data.data(), HD, C); });
+  w.wo = ws.derived<h16>("triattn.wo:" + P, [&] { return to_h16(ow.data); });
+  w.wo_t = ws.derived<h16>("triattn.wo_t:" + P, [&] { return transpose_h16(ow.data.data(), HD, C); });
   w.bo = ws.f32(P + "attention/output_b");
   return w;
 }
@@ -104,8 +106,8 @@ void triattn_fwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
   Arena& ar = arena();
   std::lock_guard<std::recursive_mutex> lk(ar.lock());
   ar.reset(st, (size_t)M * C * 2 + (size_t)M * HD * 2 + 1024);
-  bf16* xn = ar.take_n<bf16>((size_t)M * C);
-  bf16* og = ar.take_n<bf16>((size_t)M * HD);
+  h16* xn = ar.take_n<h16>((size_t)M * C);
+  h16* og = ar.take_n<h16>((size_t)M * HD);
 
   {
     KTimed kt("triattn.ln_fwd", st);
@@ -141,7 +143,7 @@ void triattn_fwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
 
 void triattn_bwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
                  const float* pair_in, const float* mask, const float* tbl,
-                 const void* save, const float* dout, float* din) {
+                 const void* save, const float* dout, float* din, const float* sc) {
   triattn_check(w, N);
   nonnull(pair_in, "triattn pair_in"); nonnull(mask, "triattn mask"); nonnull(save, "triattn save");
   nonnull(dout, "triattn dout"); nonnull(din, "triattn din");
@@ -154,17 +156,18 @@ void triattn_bwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
   const int nch = attn_bwd_nchunk(N, b.rows_per_chunk);
   Arena& ar = arena();
   std::lock_guard<std::recursive_mutex> lk(ar.lock());
+  sc = module_scale(st, sc, dout, M * C);
   Sizer need;
-  need.take<bf16>((size_t)M * HD);           // dO
+  need.take<h16>((size_t)M * HD);           // dO
   need.take<float>((size_t)H * M);           // Dsum
-  need.take<bf16>((size_t)M * 4 * HD);       // dqkvg
+  need.take<h16>((size_t)M * 4 * HD);       // dqkvg
   need.take<float>((size_t)nch * H * M);     // dbias partials
   need.take<float>((size_t)H * M);           // dbias
   need.take<float>((size_t)M * C);           // dxn
   ar.reset(st, need.off);
-  b.dO = ar.take_n<bf16>((size_t)M * HD);
+  b.dO = ar.take_n<h16>((size_t)M * HD);
   b.Dsum = ar.take_n<float>((size_t)H * M);
-  b.dqkvg = ar.take_n<bf16>((size_t)M * 4 * HD);
+  b.dqkvg = ar.take_n<h16>((size_t)M * 4 * HD);
   b.dbias_part = ar.take_n<float>((size_t)nch * H * M);
   b.dbias = ar.take_n<float>((size_t)H * M);
   float* dxn = ar.take_n<float>((size_t)M * C);
@@ -178,7 +181,7 @@ void triattn_bwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
   EpiGateBwd eg;
   eg.qkvg = sv.qkvg; eg.ld = 4L * HD; eg.o = sv.o; eg.dO = b.dO; eg.dqkvg = b.dqkvg;
   eg.Dsum = b.Dsum; eg.HD = HD; eg.H = H; eg.D = w.D; eg.Ntok = N;
-  gemm<128, 128>(st, g1, eg, "triattn.gemm_dout", ALoadScaledRows{dout, tbl, N, C, per_column});
+  gemm<128, 128>(st, g1, eg, "triattn.gemm_dout", ALoadScaledRows{dout, tbl, N, C, per_column, sc});
   b.gate_done = true;
 
   AttnArgs& a = b.f;
@@ -202,7 +205,7 @@ void triattn_bwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
     // and the residual add in the epilogue
     gemm<128, 128>(st, g2,
                    EpiLnBwd<4>(pair_in, w.ln_g, sv.mean, sv.rstd, dout, din, M, per_column ? N : 0,
-                               b.dbias, w.w2d),
+                               b.dbias, w.w2d, sc + 1),
                    "triattn.gemm_dx_ln");
     return;
   }
@@ -210,7 +213,7 @@ void triattn_bwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
 
   KTimed kt("triattn.ln_bwd", st);
   ln_bwd_f32(st, dxn, pair_in, M, C, per_column ? N : 0, w.ln_g, sv.mean, sv.rstd, din, true,
-             H, b.dbias, w.w2d, dout);
+             H, b.dbias, w.w2d, dout, sc + 1);
 }
 
 }  // namespace bc2n

@@ -2,19 +2,22 @@
 // AF2's fused-projection form, forward and backward.
 //
 // Forward:
-//   LN (fast variance) -> xn bf16
+//   LN (fast variance) -> xn h16
 //   GEMM xn . Wcat  (Wcat = [proj|gate] channel pairs interleaved in 16-wide
 //        blocks, then gating_linear), fused epilogue:
-//          a = mask * proj * sigmoid(gate)   -> left/right planes [I][N*N] bf16
-//          g_out = sigmoid(gating_linear)  -> [M][C] bf16
+//          a = mask * proj * sigmoid(gate)   -> left/right planes [I][N*N] h16
+//          g_out = sigmoid(gating_linear)  -> [M][C] h16
 //        (xn is kept; the backward recomputes the proj/gate pre-activations)
 //   batched MFMA GEMM over the I channels (plane layouts pick out/in)  -> T f32
-//   centre LN (fast variance) reading the channel-major T            -> Tn bf16
+//     (kept in f32: a sum of N products has no range bound binary16 holds)
+//   centre LN (fast variance) reading the channel-major T            -> Tn h16
 //   GEMM Tn . Wo + bo, fused: o kept, out = in + tbl * (o * g_out)
 // Backward: the exact reverse with the contraction's two transposed GEMMs; the
 // projection's gradient comes from a GEMM that recomputes the pre-activations
 // from xn and turns them, with d(left|right), into the [proj|gate] columns of
-// d(cat) in its epilogue.
+// d(cat) in its epilogue.  The backward runs on the cotangent times the
+// module's scale s (ct_scale), applied as the output projection's backward
+// loads it and divided out by the input LayerNorm's backward at the end.
 // Reference: modules.py:1044-1088 (_fused_triangle_multiplication), :909-919
 // (fast-variance LN); native/trimul_body.cuh:1183-1796 (TriMul).
 #include "gemm.h"
@@ -35,8 +38,8 @@ __host__ __device__ inline int col_gate(int ch) { return (ch / 16) * 32 + 16 + c
 // gating_linear columns run in row mode: g_out[m][c] = sigmoid(acc + b).
 struct EpiTrimulProj {
   static constexpr bool kHasCol = true;
-  bf16 *left, *right;   // [I][M]
-  bf16* gout;           // [M][C]
+  h16 *left, *right;   // [I][M]
+  h16* gout;           // [M][C]
   const float *bp, *bg, *bgl, *mask;
   long M;
   int I, C;
@@ -55,8 +58,8 @@ struct EpiTrimulProj {
       gv[e] = tp[e * ldt + 16] + bgv;
       av[e] = mk[e] * pv[e] * sigmoidf_(gv[e]);
     }
-    if (ch < I) st_b8f(left + (long)ch * M + m, av);
-    else st_b8f(right + (long)(ch - I) * M + m, av);
+    if (ch < I) st_h8f(left + (long)ch * M + m, av);
+    else st_h8f(right + (long)(ch - I) * M + m, av);
   }
   __device__ __forceinline__ void row(int, int m, int n, const float (&v)[8]) const {
     const int c = n - 4 * I;
@@ -65,20 +68,20 @@ struct EpiTrimulProj {
     ld_f8(bgl + c, bb);
 #pragma unroll
     for (int e = 0; e < 8; ++e) x[e] = sigmoidf_(v[e] + bb[e]);
-    st_b8f(gout + (long)m * C + c, x);
+    st_h8f(gout + (long)m * C + c, x);
   }
 };
 
-// o = acc + bo (kept, bf16); out[m] = in[m] + tbl[(m%nt)*C+c] * o * g_out
+// o = acc + bo (kept, h16); out[m] = in[m] + tbl[(m%nt)*C+c] * o * g_out
 struct EpiTrimulOut : EpiRows {
   const float* in;
   float* out;
   const float* bo;
-  const bf16* gout;
-  bf16* osave;
+  const h16* gout;
+  h16* osave;
   const float* tbl;
   int nt, C;
-  EpiTrimulOut(const float* i, float* o, const float* b, const bf16* g, bf16* os, const float* t,
+  EpiTrimulOut(const float* i, float* o, const float* b, const h16* g, h16* os, const float* t,
                int n, int c)
       : in(i), out(o), bo(b), gout(g), osave(os), tbl(t), nt(n), C(c) {}
   __device__ __forceinline__ void row(int, int m, int n, const float (&v)[8]) const {
@@ -87,8 +90,8 @@ struct EpiTrimulOut : EpiRows {
     ld_f8(bo + n, bb);
 #pragma unroll
     for (int e = 0; e < 8; ++e) ov[e] = v[e] + bb[e];
-    st_b8f(osave + o, ov);
-    ld_b8f(gout + o, gv);
+    st_h8f(osave + o, ov);
+    ld_h8f(gout + o, gv);
 #pragma unroll
     for (int e = 0; e < 8; ++e) gv[e] *= ov[e];
     if (tbl) {
@@ -106,20 +109,20 @@ struct EpiTrimulOut : EpiRows {
 
 template <class A>
 struct TriMulSave {
-  float *mean, *rstd, *cmean, *crstd;
-  bf16 *T, *xn, *left, *right, *gout, *osave;
+  float *mean, *rstd, *cmean, *crstd, *T;
+  h16 *xn, *left, *right, *gout, *osave;
   TriMulSave(A& a, int N, int C, int I) {
     const size_t M = (size_t)N * N;
     mean = a.template take<float>(M);
     rstd = a.template take<float>(M);
     cmean = a.template take<float>(M);
     crstd = a.template take<float>(M);
-    T = a.template take<bf16>(M * I);
-    xn = a.template take<bf16>(M * C);
-    left = a.template take<bf16>(M * I);
-    right = a.template take<bf16>(M * I);
-    gout = a.template take<bf16>(M * C);
-    osave = a.template take<bf16>(M * C);
+    T = a.template take<float>(M * I);
+    xn = a.template take<h16>(M * C);
+    left = a.template take<h16>(M * I);
+    right = a.template take<h16>(M * I);
+    gout = a.template take<h16>(M * C);
+    osave = a.template take<h16>(M * C);
   }
 };
 
@@ -133,9 +136,9 @@ struct TriMulSave {
 struct EpiTrimulProjBwd {
   static constexpr bool kHasCol = true;
   static constexpr bool kTwoPhase = true;
-  const bf16 *dl, *dr;  // [I][M]
+  const h16 *dl, *dr;  // [I][M]
   const float *bp, *bg, *mask;
-  bf16* dcat;           // [M][ldcat]
+  h16* dcat;           // [M][ldcat]
   long M;
   int I, ldcat;
   __device__ __forceinline__ bool col_mode(int) const { return true; }
@@ -146,7 +149,7 @@ struct EpiTrimulProjBwd {
     const float bpv = bp[ch], bgv = bg[ch];
     float mk[8], da[8];
     ld_f8(mask + m, mk);
-    ld_b8f((ch < I ? dl + (long)ch * M : dr + (long)(ch - I) * M) + m, da);
+    ld_h8f((ch < I ? dl + (long)ch * M : dr + (long)(ch - I) * M) + m, da);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float pv = v[e] + bpv;
@@ -157,39 +160,44 @@ struct EpiTrimulProjBwd {
     }
   }
   __device__ __forceinline__ void row(int, int m, int n, const float (&v)[8]) const {
-    st_b8f(dcat + (long)m * ldcat + n, v);
+    st_h8f(dcat + (long)m * ldcat + n, v);
   }
 };
 
-// A loader of the output-projection backward GEMM: d = tbl*dout;
-// A = d*g_out (the GEMM operand) and, as a side output,
+// A loader of the output-projection backward GEMM: d = s*tbl*dout (s = *mul,
+// the cotangent scale); A = d*g_out (the GEMM operand) and, as a side output,
 // dcat[m][off + c] = d * o * g(1-g)   (gating_linear pre-activation grad).
 struct ALoadTrimulOut {
   static constexpr bool kDirect = false;
   static constexpr bool kSide = true;
   const float* dout;
   const float* tbl;
-  const bf16* gout;
-  const bf16* osave;
-  bf16* dcat;
+  const h16* gout;
+  const h16* osave;
+  h16* dcat;
   int C, ldcat, off, nt;
-  __device__ __forceinline__ bf16x8 operator()(int, int m, int k) const {
+  const float* mul;
+  __device__ __forceinline__ h16x8 operator()(int, int m, int k) const {
     const long i = (long)m * C + k;
     float d[8], gv[8], ov[8];
     ld_f8(dout + i, d);
+    const float sm = *mul;
     if (tbl) {
       float t[8];
       ld_f8(tbl + (long)(m % nt) * C + k, t);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) d[e] *= t[e];
+      for (int e = 0; e < 8; ++e) d[e] *= t[e] * sm;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) d[e] *= sm;
     }
-    ld_b8f(gout + i, gv);
-    ld_b8f(osave + i, ov);
-    bf16x8 a, dc;
+    ld_h8f(gout + i, gv);
+    ld_h8f(osave + i, ov);
+    h16x8 a, dc;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      a[e] = (bf16)(d[e] * gv[e]);
-      dc[e] = (bf16)(d[e] * ov[e] * gv[e] * (1.f - gv[e]));
+      a[e] = f2h_sat(d[e] * gv[e]);
+      dc[e] = f2h_sat(d[e] * ov[e] * gv[e] * (1.f - gv[e]));
     }
     st8(dcat + (long)m * ldcat + off + k, dc);
     return a;
@@ -232,13 +240,13 @@ constexpr int LD2 = CH + 16;              // B2 chunk: [C][CH] (c rows, k contig
 constexpr int B1E = CH * LD1, B2E = C * LD2;
 }  // namespace tail
 
-// 8 bf16 of row `row` at k = k0 + {4g..4g+3, 16+4g..16+4g+3} of a
+// 8 h16 of row `row` at k = k0 + {4g..4g+3, 16+4g..16+4g+3} of a
 // K-contiguous tile (row stride ld), global or LDS.
-__device__ __forceinline__ bf16x8 kslots(const bf16* T, long ld, long row, int k0, int g) {
-  const bf16* p = T + row * ld + k0 + 4 * g;
-  const bf16x4 a = *reinterpret_cast<const bf16x4*>(p);
-  const bf16x4 b = *reinterpret_cast<const bf16x4*>(p + 16);
-  bf16x8 r;
+__device__ __forceinline__ h16x8 kslots(const h16* T, long ld, long row, int k0, int g) {
+  const h16* p = T + row * ld + k0 + 4 * g;
+  const h16x4 a = *reinterpret_cast<const h16x4*>(p);
+  const h16x4 b = *reinterpret_cast<const h16x4*>(p + 16);
+  h16x8 r;
   r[0] = a[0]; r[1] = a[1]; r[2] = a[2]; r[3] = a[3];
   r[4] = b[0]; r[5] = b[1]; r[6] = b[2]; r[7] = b[3];
   return r;
@@ -253,21 +261,22 @@ inline int tail_kperm(int p) {
 }
 
 struct TailArgs {
-  const bf16* xn;      // [M][C]
-  const bf16* wcat_t;  // [NC][C], k permuted (tail_kperm)
-  const bf16* wcat;    // [C][NC], k permuted (tail_kperm)
-  const bf16 *dl, *dr; // [I][M]
-  const bf16* dcg;     // [M][C]: d(cat)'s gating_linear columns
+  const h16* xn;      // [M][C]
+  const h16* wcat_t;  // [NC][C], k permuted (tail_kperm)
+  const h16* wcat;    // [C][NC], k permuted (tail_kperm)
+  const h16 *dl, *dr; // [I][M]
+  const h16* dcg;     // [M][C]: d(cat)'s gating_linear columns
   const float *bp, *bg, *mask;
   const float *x, *ln_g, *mean, *rstd, *dres;
+  const float* gmul;  // inverse cotangent scale (device scalar)
   float* out;
   long M;
 };
 
 __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
   using namespace tail;
-  __shared__ __attribute__((aligned(16))) bf16 B1s[2 * B1E];
-  __shared__ __attribute__((aligned(16))) bf16 B2s[2 * B2E];
+  __shared__ __attribute__((aligned(16))) h16 B1s[2 * B1E];
+  __shared__ __attribute__((aligned(16))) h16 B2s[2 * B2E];
   // the projection biases, read in the d(cat) formulas from LDS: a global
   // load there would wait (in-order vmcnt) for the next chunk's prefetch
   __shared__ __attribute__((aligned(16))) float Bps[2 * I], Bgs[2 * I];
@@ -283,8 +292,8 @@ __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
   // operands into registers -- d(left|right) at its rows and channels (da) for
   // a [proj|gate] chunk, its d(cat) gating fragments (in p1) for the others.
   // The weights are issued first, so waiting for them leaves the rest in flight.
-  bf16x8 p1[4], p2[4];
-  bf16 da[2][2][4];
+  h16x8 p1[4], p2[4];
+  h16 da[2][2][4];
   auto prefetch = [&](int s) {
     if (s < NPG) {
 #pragma unroll
@@ -300,7 +309,7 @@ __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
       p2[q] = ld8(a.wcat + (long)r * NC + kb + k8);
     }
     if (s < NPG) {
-      const bf16* dsrc = s < NPG / 2 ? a.dl : a.dr;
+      const h16* dsrc = s < NPG / 2 ? a.dl : a.dr;
       const int chb = (s % (NPG / 2)) * 32;  // channel within left or right
 #pragma unroll
       for (int i = 0; i < 2; ++i)
@@ -334,7 +343,7 @@ __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
 
   prefetch(0);
   // xn fragments of the wave's two row tiles, all of K, in GEMM1's slot order
-  bf16x8 xf[2][C / 32];
+  h16x8 xf[2][C / 32];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -361,9 +370,9 @@ __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
 #pragma unroll
   for (int s = 0; s < NCHUNK; ++s) {
     const int buf = s & 1;
-    const bf16* b1 = B1s + buf * B1E;
-    const bf16* b2 = B2s + buf * B2E;
-    bf16x8 af[2][2];  // GEMM2 A fragments: [row tile][k-step of this chunk]
+    const h16* b1 = B1s + buf * B1E;
+    const h16* b2 = B2s + buf * B2E;
+    h16x8 af[2][2];  // GEMM2 A fragments: [row tile][k-step of this chunk]
     if (s < NPG) {
       // GEMM1: P for 4 column blocks (proj, gate, proj, gate)
       f32x4 acc1[2][4];
@@ -373,14 +382,14 @@ __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
         for (int t = 0; t < 4; ++t) acc1[i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < C / 32; ++ks) {
-        bf16x8 bfr[4];
+        h16x8 bfr[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) bfr[t] = ld8(b1 + (t * 16 + l16) * LD1 + ks * 32 + 8 * g);
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
           for (int t = 0; t < 4; ++t)
-            acc1[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr[t], xf[i][ks], acc1[i][t], 0, 0, 0);
+            acc1[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bfr[t], xf[i][ks], acc1[i][t], 0, 0, 0);
       }
       // epilogue: d(proj) = a * sigmoid(gate), d(gate) = a * proj * s (1 - s), a = d(act) * mask
 #pragma unroll
@@ -391,14 +400,14 @@ __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
         for (int r = 0; r < 4; ++r) { bpv[r] = Bps[ch + r]; bgv[r] = Bgs[ch + r]; }
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-          bf16x8 f;
+          h16x8 f;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const float pv = acc1[i][2 * q][r] + bpv[r];
             const float sg = sigmoidf_(acc1[i][2 * q + 1][r] + bgv[r]);
             const float ad = (float)da[i][q][r] * mk[i];
-            f[r] = (bf16)(ad * sg);
-            f[4 + r] = (bf16)(ad * pv * sg * (1.f - sg));
+            f[r] = f2h_sat(ad * sg);
+            f[4 + r] = f2h_sat(ad * pv * sg * (1.f - sg));
           }
           af[i][q] = f;
         }
@@ -427,10 +436,10 @@ __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
     for (int q = 0; q < 2; ++q) {
 #pragma unroll
       for (int j = 0; j < C / 16; ++j) {
-        const bf16x8 bfr = ld8(b2 + (j * 16 + l16) * LD2 + q * 32 + 8 * g);
+        const h16x8 bfr = ld8(b2 + (j * 16 + l16) * LD2 + q * 32 + 8 * g);
 #pragma unroll
         for (int i = 0; i < 2; ++i)
-          acc2[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr, af[i][q], acc2[i][j], 0, 0, 0);
+          acc2[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bfr, af[i][q], acc2[i][j], 0, 0, 0);
       }
     }
     if (s + 1 < NCHUNK) stash(s + 1, buf ^ 1);
@@ -438,6 +447,7 @@ __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
   }
 
   // ---- LayerNorm backward + residual: lane has channels 16j + 4g + r of row m
+  const float gs = *a.gmul;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const long m = m0 + i * 16 + l16;
@@ -453,7 +463,7 @@ __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         xh[j][r] = (xa[r] - mu) * rs;
-        gg[j][r] = acc2[i][j][r] * ga[r];
+        gg[j][r] = acc2[i][j][r] * (ga[r] * gs);
         sg += gg[j][r];
         sgx += gg[j][r] * xh[j][r];
       }
@@ -509,25 +519,25 @@ TriMulW trimul_weights(WeightStore& ws, const std::string& P) {
     }
     return c;
   };
-  w.wcat = ws.derived<bf16>("trimul.wcat:" + P, [&] { return to_bf16(cat()); });
-  w.wcat_t = ws.derived<bf16>("trimul.wcat_t:" + P, [&] {
+  w.wcat = ws.derived<h16>("trimul.wcat:" + P, [&] { return to_h16(cat()); });
+  w.wcat_t = ws.derived<h16>("trimul.wcat_t:" + P, [&] {
     std::vector<float> c = cat();
-    return transpose_bf16(c.data(), C, NC);
+    return transpose_h16(c.data(), C, NC);
   });
-  auto kperm_cols = [](std::vector<bf16> m, int rows, int cols) {
-    std::vector<bf16> o(m.size());
+  auto kperm_cols = [](std::vector<h16> m, int rows, int cols) {
+    std::vector<h16> o(m.size());
     for (int r = 0; r < rows; ++r)
       for (int p = 0; p < cols; ++p) o[(size_t)r * cols + p] = m[(size_t)r * cols + tail_kperm(p)];
     return o;
   };
-  w.wcat_k = ws.derived<bf16>("trimul.wcat_k:" + P, [&] { return kperm_cols(to_bf16(cat()), C, NC); });
-  w.wcat_tk = ws.derived<bf16>("trimul.wcat_tk:" + P, [&] {
+  w.wcat_k = ws.derived<h16>("trimul.wcat_k:" + P, [&] { return kperm_cols(to_h16(cat()), C, NC); });
+  w.wcat_tk = ws.derived<h16>("trimul.wcat_tk:" + P, [&] {
     std::vector<float> c = cat();
-    return kperm_cols(transpose_bf16(c.data(), C, NC), NC, C);
+    return kperm_cols(transpose_h16(c.data(), C, NC), NC, C);
   });
   const HostTensor& ow = ws.host(P + "output_projection/weights");  // [I, C]
-  w.wo = ws.derived<bf16>("trimul.wo:" + P, [&] { return to_bf16(ow.data); });
-  w.wo_t = ws.derived<bf16>("trimul.wo_t:" + P, [&] { return transpose_bf16(ow.data.data(), I, C); });
+  w.wo = ws.derived<h16>("trimul.wo:" + P, [&] { return to_h16(ow.data); });
+  w.wo_t = ws.derived<h16>("trimul.wo_t:" + P, [&] { return transpose_h16(ow.data.data(), I, C); });
   return w;
 }
 
@@ -549,7 +559,7 @@ static void contract(hipStream_t st, const GemmArgs& g, OutT* C, const char* nam
   {
     KTimed kt(name, st);
     float* cf = nullptr;
-    bf16* cb = nullptr;
+    h16* cb = nullptr;
     if constexpr (sizeof(OutT) == 4) cf = C;
     else cb = C;
     if (trimul_contract(st, g.M, g.batch, g.A, g.a_sk == 1, g.B, g.b_sk == 1, cf, cb)) return;
@@ -558,8 +568,8 @@ static void contract(hipStream_t st, const GemmArgs& g, OutT* C, const char* nam
 }
 
 // Contraction operand layouts for one channel plane (row-major N x N).
-static void contraction_fwd(hipStream_t st, bool outgoing, int N, int I, const bf16* L,
-                            const bf16* R, bf16* T) {
+static void contraction_fwd(hipStream_t st, bool outgoing, int N, int I, const h16* L,
+                            const h16* R, float* T) {
   const long M = (long)N * N;
   GemmArgs g;
   g.M = N; g.N = N; g.K = N; g.batch = I;
@@ -571,7 +581,7 @@ static void contraction_fwd(hipStream_t st, bool outgoing, int N, int I, const b
     g.B = L; g.b_sn = 1; g.b_sk = N;
   }
   g.a_sb = M; g.b_sb = M;
-  contract<bf16>(st, g, T, "trimul.contract_fwd");
+  contract<float>(st, g, T, "trimul.contract_fwd");
 }
 
 void trimul_fwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const float* pair_in,
@@ -586,8 +596,8 @@ void trimul_fwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
   Arena& ar = arena();
   std::lock_guard<std::recursive_mutex> lk(ar.lock());
   ar.reset(st, (size_t)M * I * 2 + 1024);
-  bf16* xn = sv.xn;
-  bf16* tn = ar.take_n<bf16>((size_t)M * I);
+  h16* xn = sv.xn;
+  h16* tn = ar.take_n<h16>((size_t)M * I);
   {
     KTimed kt("trimul.ln_fwd", st);
     ln_fwd_f32(st, pair_in, M, C, 0, w.ln_g, w.ln_b, xn, sv.mean, sv.rstd, true, 0, nullptr,
@@ -615,7 +625,7 @@ void trimul_fwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
 
 void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const float* pair_in,
                 const float* mask, const float* tbl, const void* save, const float* dout,
-                float* din) {
+                float* din, const float* sc) {
   trimul_check(N);
   nonnull(pair_in, "trimul pair_in"); nonnull(mask, "trimul mask"); nonnull(save, "trimul save");
   nonnull(dout, "trimul dout"); nonnull(din, "trimul din");
@@ -625,23 +635,24 @@ void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
   TriMulSave<Carver> sv(cv, N, C, I);
   Arena& ar = arena();
   std::lock_guard<std::recursive_mutex> lk(ar.lock());
+  sc = module_scale(st, sc, dout, M * C);
   // C = I = 128: the tail kernel keeps d(cat)'s [proj|gate] columns in
   // registers; only its gating_linear columns ([M][C]) go through memory
   const bool fused = (C == tail::C && I == tail::I && M % tail::BM == 0);
   const int ldcat = fused ? C : NC, off = fused ? 0 : 4 * I;
   Sizer need;
-  need.take<bf16>((size_t)M * ldcat);  // dcat
+  need.take<h16>((size_t)M * ldcat);  // dcat
   need.take<float>((size_t)M * I);  // dTn
-  need.take<bf16>((size_t)M * I);   // dT
-  need.take<bf16>((size_t)M * I);   // dL
-  need.take<bf16>((size_t)M * I);   // dR
+  need.take<h16>((size_t)M * I);   // dT
+  need.take<h16>((size_t)M * I);   // dL
+  need.take<h16>((size_t)M * I);   // dR
   if (!fused) need.take<float>((size_t)M * C);  // dxn
   ar.reset(st, need.off);
-  bf16* dcat = ar.take_n<bf16>((size_t)M * ldcat);
+  h16* dcat = ar.take_n<h16>((size_t)M * ldcat);
   float* dtn = ar.take_n<float>((size_t)M * I);
-  bf16* dT = ar.take_n<bf16>((size_t)M * I);
-  bf16* dL = ar.take_n<bf16>((size_t)M * I);
-  bf16* dR = ar.take_n<bf16>((size_t)M * I);
+  h16* dT = ar.take_n<h16>((size_t)M * I);
+  h16* dL = ar.take_n<h16>((size_t)M * I);
+  h16* dR = ar.take_n<h16>((size_t)M * I);
   float* dxn = fused ? nullptr : ar.take_n<float>((size_t)M * C);
 
   // d(tn) = (tbl*dout*g_out) . Wo^T, the operand built as the GEMM loads it;
@@ -651,7 +662,7 @@ void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
   g1.a_sm = C; g1.a_sk = 1;
   g1.B = w.wo; g1.b_sn = C; g1.b_sk = 1;
   gemm<128, 128>(st, g1, EpiStore<float>{dtn, I, 0, nullptr, I}, "trimul.gemm_dout",
-                 ALoadTrimulOut{dout, tbl, sv.gout, sv.osave, dcat, C, ldcat, off, N});
+                 ALoadTrimulOut{dout, tbl, sv.gout, sv.osave, dcat, C, ldcat, off, N, sc});
   {
     KTimed kt("trimul.ln_center_bwd", st);
     ln_bwd_cm(st, dtn, sv.T, M, I, w.cn_g, sv.cmean, sv.crstd, dT);
@@ -675,8 +686,8 @@ void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
       b.A = sv.left; b.a_sm = N; b.a_sk = 1;
       b.B = dT; b.b_sn = N; b.b_sk = 1;
     }
-    contract<bf16>(st, a, dL, "trimul.contract_bwd");
-    contract<bf16>(st, b, dR, "trimul.contract_bwd");
+    contract<h16>(st, a, dL, "trimul.contract_bwd");
+    contract<h16>(st, b, dR, "trimul.contract_bwd");
   }
   if (fused) {
     TailArgs t;
@@ -684,6 +695,7 @@ void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
     t.dl = dL; t.dr = dR; t.dcg = dcat;
     t.bp = w.bp; t.bg = w.bg; t.mask = mask;
     t.x = pair_in; t.ln_g = w.ln_g; t.mean = sv.mean; t.rstd = sv.rstd; t.dres = dout;
+    t.gmul = sc + 1;
     t.out = din; t.M = M;
     KTimed kt("trimul.tail_bwd", st);
     hipLaunchKernelGGL(trimul_tail_kernel, dim3((unsigned)(M / tail::BM)), dim3(256), 0, st, t);
@@ -703,14 +715,16 @@ void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
   g2.B = w.wcat; g2.b_sn = NC; g2.b_sk = 1;
   if (C == 128) {
     // the input LayerNorm's backward and the residual add in the epilogue
-    gemm<128, 128>(st, g2, EpiLnBwd<0>(pair_in, w.ln_g, sv.mean, sv.rstd, dout, din, M, 0),
+    gemm<128, 128>(st, g2,
+                   EpiLnBwd<0>(pair_in, w.ln_g, sv.mean, sv.rstd, dout, din, M, 0, nullptr,
+                               nullptr, sc + 1),
                    "trimul.gemm_dx_ln");
     return;
   }
   gemm<128, 128>(st, g2, EpiStore<float>{dxn, C, 0, nullptr, C}, "trimul.gemm_dx");
   KTimed kt("trimul.ln_bwd", st);
   ln_bwd_f32(st, dxn, pair_in, M, C, 0, w.ln_g, sv.mean, sv.rstd, din, true, 0, nullptr, nullptr,
-             dout);
+             dout, sc + 1);
 }
 
 }  // namespace bc2n

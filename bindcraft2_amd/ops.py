@@ -656,18 +656,20 @@ def stack_keys(seed, depth, device="cuda"):
     return out.view(depth, 9, 2)
 
 
-def probe_gemm(a_bf16, b_bf16):
-    """C = A . B^T (bf16 in, f32 out) through the library's MFMA GEMM."""
-    m, k = a_bf16.shape
-    n = b_bf16.shape[0]
-    c = torch.empty(m, n, dtype=torch.float32, device=a_bf16.device)
-    check(lib().bc2n_probe_gemm(_stream(), m, n, k, _ptr(a_bf16), _ptr(b_bf16), _ptr(c)))
+def probe_gemm(a_f16, b_f16):
+    """C = A . B^T (binary16 in, f32 out) through the library's MFMA GEMM."""
+    if a_f16.dtype != torch.float16 or b_f16.dtype != torch.float16:
+        raise TypeError("probe_gemm: operands must be float16 (the GEMM's operand format)")
+    m, k = a_f16.shape
+    n = b_f16.shape[0]
+    c = torch.empty(m, n, dtype=torch.float32, device=a_f16.device)
+    check(lib().bc2n_probe_gemm(_stream(), m, n, k, _ptr(a_f16), _ptr(b_f16), _ptr(c)))
     return c
 
 
 def probe_layernorm(x, gamma, beta, fast=False):
     m, c = x.shape
-    y = torch.empty(m, c, dtype=torch.bfloat16, device=x.device)
+    y = torch.empty(m, c, dtype=torch.float16, device=x.device)
     mean = torch.empty(m, dtype=torch.float32, device=x.device)
     rstd = torch.empty(m, dtype=torch.float32, device=x.device)
     check(lib().bc2n_probe_layernorm(_stream(), m, c, _ptr(x), _ptr(gamma), _ptr(beta),

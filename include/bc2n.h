@@ -511,7 +511,7 @@ int bc2n_prof_read(char* names, int name_len, double* ms, int* counts, int cap);
  * Kernel probes (test hooks; no reference counterpart beyond the module
  * gates of native/*.cu).
  * ---------------------------------------------------------------------- */
-/* C[M,N] = A[M,K] . B[N,K]^T, bf16 (uint16 bits) in, f32 out. */
+/* C[M,N] = A[M,K] . B[N,K]^T, IEEE binary16 (uint16 bits) in, f32 out. */
 int bc2n_probe_gemm(void* stream, int M, int N, int K, const uint16_t* A,
                     const uint16_t* B, float* C);
 /* Batched f32 GEMM with element strides (the structure module's GEMM):
@@ -519,7 +519,7 @@ int bc2n_probe_gemm(void* stream, int M, int N, int K, const uint16_t* A,
 int bc2n_probe_gemm_f32(void* stream, int M, int N, int K, int batch, const float* A,
                         long a_sm, long a_sk, long a_sb, const float* B, long b_sk,
                         long b_sn, long b_sb, float* C, long c_sm, long c_sn, long c_sb);
-/* y = LN(x) over C channels, bf16 out + mean/rstd. fast = E[x^2]-E[x]^2. */
+/* y = LN(x) over C channels, binary16 out + mean/rstd. fast = E[x^2]-E[x]^2. */
 int bc2n_probe_layernorm(void* stream, long M, int C, const float* x,
                          const float* gamma, const float* beta, int fast,
                          uint16_t* y, float* mean, float* rstd);

@@ -15,7 +15,10 @@ closed forms and torch.nn.functional at fp64; attention against a pure-Python
 loop on tiny inputs; triangle attention ending == starting on the transposed
 pair; incoming == outgoing with swapped operands; OPM against its direct
 4-index sum and the mask==0 constant; S=1 column attention against its
-softmax==1 closed form; gradients against central finite differences.
+softmax==1 closed form; global attention against a pure-Python loop, its
+S=1 closed form and its fully-masked-column closed form; the pair-only extra
+block against the full extra-MSA iteration on a zero mask; gradients against
+central finite differences.
 """
 import math
 
@@ -655,7 +658,7 @@ def structure_heads(single, pair, mask, aatype, params, depth, key, use_dropout,
 
 
 def design_step(target_feat, msa_feat, ids, offset, seq_mask, act_const, aatype, emsa, prm,
-                depths, keys, use_dropout, tables, dtype=torch.float64, round_trunk=False):
+                depths, keys, use_dropout, tables, dtype=torch.float64):
     """The trunk of one design step, input features to the structure-module
     outputs (modules_multimer.py:441-700, EmbeddingsAndEvoformer, then
     AlphaFoldIteration's structure module and heads): the embedder; the
@@ -665,10 +668,7 @@ def design_step(target_feat, msa_feat, ids, offset, seq_mask, act_const, aatype,
     the main stack; single = single_activations(msa[0]); structure_heads.
     `prm` maps 'emb', 'tpl', 'extra', 'main', 'post' to flat parameter
     dicts; `depths` and `keys` ('tpl', 'extra', 'main', 'fold') give each
-    stack its depth and its JAX key.  round_trunk rounds the trunk's
-    outputs (single, pair) to bfloat16 before the structure module, keeping
-    their gradient (straight through): a probe of how much the structure
-    module amplifies bf16-sized differences in its inputs."""
+    stack its depth and its JAX key."""
     msa, pair = embedder(target_feat, msa_feat, *ids, prm["emb"], offset=offset, dtype=dtype)
     pmask = seq_mask[:, None] * seq_mask[None, :]
     mmask = seq_mask[None].expand(msa.shape[0], -1)
@@ -681,9 +681,6 @@ def design_step(target_feat, msa_feat, ids, offset, seq_mask, act_const, aatype,
     msa, pair = evoformer_stack(msa, pair, mmask, pmask, prm["main"], depths["main"], keys["main"],
                                 use_dropout, dtype=dtype)
     single = linear(msa[0], Params(prm["emb"], "param/single_activations/", dtype))
-    if round_trunk:
-        bf = lambda x: x + (x.to(torch.bfloat16).to(dtype) - x).detach()
-        single, pair = bf(single), bf(pair)
     return structure_heads(single, pair, seq_mask, aatype, prm["post"], depths["fold"], keys["fold"],
                            use_dropout, tables, dtype)
 
@@ -732,13 +729,13 @@ def design_inputs(feat, prof):
 
 
 def design_step_seq(logits, flags, scalars, ids, offset, seq_mask, act_const, emsa, prm, depths,
-                    keys, use_dropout, tables, bias=None, dtype=torch.float64, round_trunk=False):
+                    keys, use_dropout, tables, bias=None, dtype=torch.float64):
     """design_step from the designed logits: sequence_features ->
     design_inputs -> design_step (one MSA row)."""
     feat, prof = sequence_features(logits, flags, *scalars, bias=bias)
     tf, mf, aatype = design_inputs(feat, prof)
     return design_step(tf, mf, ids, offset, seq_mask, act_const, aatype, emsa, prm, depths, keys,
-                       use_dropout, tables, dtype=dtype, round_trunk=round_trunk)
+                       use_dropout, tables, dtype=dtype)
 
 
 # ---------------------------------------------------------------------------

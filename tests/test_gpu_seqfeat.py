@@ -4,12 +4,10 @@ design_inputs and design_step_seq (bindcraft/af2.py:99-104, :187-192 over
 bindcraft/sequence_optimization.py:33-52).
 
 The features are f32 arithmetic on 20 values per residue: forward and
-gradient within 1e-5 relative of the fp64 oracle.  The one-call step runs
-the bf16 stacks, so it takes the design-step bars (tests/test_gpu_design_step.py):
-outputs relL2 and normwise max error <= 2e-2, d(logits) cosine >= 0.999
-(0.998 through the template embedding), each loosened to what rounding the
-trunk's outputs to bf16 does to the oracle, with residues that this probe
-shows ill-conditioned left out of the atom14 cotangent."""
+gradient within 1e-5 relative of the fp64 oracle.  The one-call step takes
+the design-step bars (tests/test_gpu_design_step.py), absolute: outputs
+relL2 and normwise max error <= 2e-2 and cosine >= 0.9999 (pTM/ipTM:
+relative error), d(logits) cosine >= 0.999 and relL2 <= 5e-2."""
 import numpy as np
 import pytest
 import torch
@@ -119,25 +117,16 @@ def test_design_step_seq_parity(cuda, with_template, dropout):
     cts = [rng.standard_normal(sh).astype(np.float32) for sh in shapes]
     iasym = ids[1].astype(np.int32)
 
-    def oracle(round_trunk, grads=True):
-        t = torch.tensor(x, dtype=D, requires_grad=True)
-        ref = af2.design_step_seq(t, flags, scalars, ids, None, torch.as_tensor(seq_mask, dtype=D),
-                                  None if act_const is None else torch.as_tensor(act_const, dtype=D),
-                                  torch.as_tensor(emsa, dtype=D), prm, depths,
-                                  keys if dropout else {k: None for k in keys}, dropout, tables,
-                                  bias=torch.tensor(bias, dtype=D), round_trunk=round_trunk)
-        ref = list(ref) + list(af2.confidence(ref[3], ref[2], ref[4],
-                                              torch.as_tensor(seq_mask, dtype=D), iasym))
-        if not grads:
-            return [r.detach() for r in ref]
-        loss = sum((r * torch.as_tensor(c, dtype=D)).sum() for r, c in zip(ref, cts))
-        return [r.detach() for r in ref] + list(torch.autograd.grad(loss, (t,)))
-
-    a0, a1 = oracle(False, False)[0], oracle(True, False)[0]
-    dev_res = (a1 - a0).abs().amax((1, 2))
-    bad = (dev_res > 20 * dev_res.median().clamp_min(1e-12)).numpy()
-    print("  ill-conditioned residues", np.where(bad)[0])
-    cts[0][bad] = 0.0
+    t = torch.tensor(x, dtype=D, requires_grad=True)
+    ref = af2.design_step_seq(t, flags, scalars, ids, None, torch.as_tensor(seq_mask, dtype=D),
+                              None if act_const is None else torch.as_tensor(act_const, dtype=D),
+                              torch.as_tensor(emsa, dtype=D), prm, depths,
+                              keys if dropout else {k: None for k in keys}, dropout, tables,
+                              bias=torch.tensor(bias, dtype=D))
+    ref = list(ref) + list(af2.confidence(ref[3], ref[2], ref[4],
+                                          torch.as_tensor(seq_mask, dtype=D), iasym))
+    loss = sum((r * torch.as_tensor(c, dtype=D)).sum() for r, c in zip(ref, cts))
+    ref = [r.detach() for r in ref] + list(torch.autograd.grad(loss, (t,)))
 
     T = lambda a: None if a is None else torch.as_tensor(a, device=cuda)
     step = ops.DesignStepSeq(*dirs, depths=(depths["tpl"], depths["extra"], depths["main"],
@@ -152,19 +141,15 @@ def test_design_step_seq_parity(cuda, with_template, dropout):
                          interface_asym=T(iasym), conf_cts=[T(c) for c in cts[5:]])
     torch.cuda.synchronize()
 
-    ref, probe = oracle(False), oracle(True)
     names = ("atom14", "distogram", "pae", "plddt", "expres", "conf plddt", "conf pae", "ptm",
              "iptm", "iptm_per_residue", "expres_ca", "d logits")
     last = len(names) - 1
-    for i, (name, g, r, p) in enumerate(zip(names, list(outs) + list(conf) + [dlog], ref, probe)):
-        m, c = metrics(g.cpu().double(), r), metrics(p, r)
-        tol = max(2e-2, 4 * c["rel_l2"], 4 * c["max_rel"])
-        base = (0.998 if with_template else 0.999) if i == last else 0.9999
-        cos = min(base, 1 - (6 if i == last else 4) * (1 - c["cos"]))
-        print(f"  {name}", m, "| probe", {k: round(v, 6) for k, v in c.items()})
+    for i, (name, g, r) in enumerate(zip(names, list(outs) + list(conf) + [dlog], ref)):
+        m = metrics(g.cpu().double(), r)
+        print(f"  {name}", m)
         if i in (7, 8):  # scalars: relative error only
-            assert m["rel_l2"] <= tol, name
+            assert m["rel_l2"] <= 2e-2, name
         elif i < last:
-            assert m["rel_l2"] <= tol and m["max_rel"] <= tol and m["cos"] >= cos, name
+            assert m["rel_l2"] <= 2e-2 and m["max_rel"] <= 2e-2 and m["cos"] >= 0.9999, name
         else:
-            assert m["cos"] >= cos, name
+            assert m["cos"] >= 0.999 and m["rel_l2"] <= 5e-2, name

@@ -15,14 +15,13 @@ pytestmark = pytest.mark.gpu
 D = torch.float64
 
 
-# The relu acts on LN(stack output).  The stack's bf16 kernels leave that
-# input ~5e-3 (relative) from the fp64 oracle, so the elements within that
-# distance of 0 (about 0.4% of N(0,1) values) can take the other side of the
-# hinge; each such flip moves its whole gradient term, which gives a d(query)
-# relL2 of about sqrt(0.004) = 6% (cosine ~0.998) however exact the rest is.
-# `hinge=False` shifts output_layer_norm's offset by +5 so that no element
-# lies near the hinge: the full composite gradient is then held to the strict
-# cosine bar.  `hinge=True` keeps the hinge live with the bound above.
+# The relu acts on LN(stack output), so every element the kernels' rounding
+# moves across zero flips its whole gradient term.  `hinge=False` shifts
+# output_layer_norm's offset by +5 so that no element lies near the hinge
+# (the composite gradient alone); `hinge=True` keeps the hinge live.  With
+# binary16 operands the stack's output is ~5e-4 (relative) from the fp64
+# oracle and both cases are held to the north star's cosine bar (measured:
+# 0.99995+ strict, 0.99965 live).
 @pytest.mark.parametrize("depth,n,dropout,hinge", [(1, 32, False, False), (2, 64, True, False),
                                                    (2, 96, True, False), (2, 64, True, True)])
 def test_template_embedding_parity(cuda, depth, n, dropout, hinge):
@@ -51,5 +50,4 @@ def test_template_embedding_parity(cuda, depth, n, dropout, hinge):
                                  prm, depth, key if dropout else None, dropout)
     (g,) = torch.autograd.grad(ref, x, torch.as_tensor(ct, dtype=D))
     print(" out", assert_act(out.cpu().double(), ref.detach(), what="out"))
-    print(" dquery", assert_grad(dq.cpu().double(), g, cos=0.999 if not hinge else 0.995,
-                                 what="dquery"))
+    print(" dquery", assert_grad(dq.cpu().double(), g, what="dquery"))
