@@ -40,6 +40,7 @@ def _declare(L):
         "bc2n_triattn_save_bytes": (sz, [i, i, i]),
         "bc2n_triattn_fwd": (i, [vp, cs, cs, i, i, vp, vp, vp, vp, vp]),
         "bc2n_triattn_bwd": (i, [vp, cs, cs, i, i, vp, vp, vp, vp, vp, vp]),
+        "bc2n_triattn_fwd_noalloc": (i, [vp, cs, cs, i, i, vp, vp, vp, vp, vp]),
         "bc2n_trimul_save_bytes": (sz, [i, i, i]),
         "bc2n_trimul_fwd": (i, [vp, cs, cs, i, i, vp, vp, vp, vp, vp]),
         "bc2n_trimul_bwd": (i, [vp, cs, cs, i, i, vp, vp, vp, vp, vp, vp]),

@@ -126,6 +126,28 @@ int bc2n_triattn_fwd(void* stream, const char* weights_dir, const char* prefix, 
   });
 }
 
+int bc2n_triattn_fwd_noalloc(void* stream, const char* weights_dir, const char* prefix,
+                             int per_column, int N, const float* pair, const float* pair_mask,
+                             const float* drop_tbl, float* pair_out, void* save) {
+  return guarded([&] {
+    need(weights_dir && prefix, "weights_dir/prefix required");
+    need(pair && pair_mask && pair_out && save, "null operand");
+    need(pair_out != pair, "triattn: pair_out must not alias pair");
+    const TriAttnW* w = nullptr;
+    {
+      // only weights already on the device: loading would allocate
+      std::lock_guard<std::mutex> lk(g_mu);
+      auto it = g_triattn.find(std::make_pair(std::string(weights_dir), std::string(prefix)));
+      if (it != g_triattn.end()) w = &it->second;
+    }
+    need(w != nullptr,
+         "triattn_fwd_noalloc: weights not resident; call bc2n_triattn_fwd once with this "
+         "weights_dir and prefix first");
+    triattn_fwd_noalloc(as_stream(stream), *w, per_column != 0, N, pair, pair_mask, drop_tbl,
+                        pair_out, save);
+  });
+}
+
 int bc2n_triattn_bwd(void* stream, const char* weights_dir, const char* prefix, int per_column,
                      int N, const float* pair, const float* pair_mask, const float* drop_tbl,
                      const void* save, const float* dpair_out, float* dpair_in) {

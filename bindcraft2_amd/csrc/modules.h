@@ -45,6 +45,13 @@ size_t triattn_save_bytes(int N, int C, int H);
 void triattn_fwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
                  const float* pair_in, const float* mask, const float* tbl,
                  float* pair_out, void* save);
+// triattn_fwd without any allocation: its scratch is a static device array
+// of TRIATTN_NOALLOC_SCRATCH_BYTES (N <= 256 at C = 128); larger N throw
+// std::invalid_argument before any launch.  Calls overlapping on one GPU race.
+constexpr size_t TRIATTN_NOALLOC_SCRATCH_BYTES = 2ull * 256 * 256 * 128 * 2;
+void triattn_fwd_noalloc(hipStream_t st, const TriAttnW& w, bool per_column, int N,
+                         const float* pair_in, const float* mask, const float* tbl,
+                         float* pair_out, void* save);
 void triattn_bwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
                  const float* pair_in, const float* mask, const float* tbl,
                  const void* save, const float* dout, float* din, const float* sc = nullptr);

@@ -18,6 +18,8 @@
 #include "gemm.h"
 #include "modules.h"
 #include <cmath>
+#include <mutex>
+#include <string>
 
 namespace bc2n {
 
@@ -93,22 +95,14 @@ static void triattn_check(const TriAttnW& w, int N) {
   if (w.D != 32 && w.D != 16) throw std::runtime_error("triattn: head width 16 or 32 only");
 }
 
-void triattn_fwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
-                 const float* pair_in, const float* mask, const float* tbl,
-                 float* pair_out, void* save) {
-  triattn_check(w, N);
-  nonnull(pair_in, "triattn pair_in"); nonnull(mask, "triattn mask");
-  nonnull(pair_out, "triattn pair_out"); nonnull(save, "triattn save");
+// The forward with its scratch (xn [M][C], og [M][HD], binary16) supplied.
+static void triattn_fwd_with(hipStream_t st, const TriAttnW& w, bool per_column, int N,
+                             const float* pair_in, const float* mask, const float* tbl,
+                             float* pair_out, void* save, h16* xn, h16* og) {
   const int C = w.C, H = w.H, HD = w.H * w.D;
   const long M = (long)N * N;
   Carver cv(save);
   TriAttnSave<Carver> sv(cv, N, C, H);
-  Arena& ar = arena();
-  std::lock_guard<std::recursive_mutex> lk(ar.lock());
-  ar.reset(st, (size_t)M * C * 2 + (size_t)M * HD * 2 + 1024);
-  h16* xn = ar.take_n<h16>((size_t)M * C);
-  h16* og = ar.take_n<h16>((size_t)M * HD);
-
   {
     KTimed kt("triattn.ln_fwd", st);
     ln_fwd_f32(st, pair_in, M, C, per_column ? N : 0, w.ln_g, w.ln_b, xn, sv.mean, sv.rstd,
@@ -139,6 +133,66 @@ void triattn_fwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
   g2.B = w.wo_t; g2.b_sn = HD; g2.b_sk = 1;
   gemm<128, 128>(st, g2, EpiResidualRows(pair_in, pair_out, w.bo, tbl, N, C, per_column),
                  "triattn.gemm_out");
+}
+
+void triattn_fwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
+                 const float* pair_in, const float* mask, const float* tbl,
+                 float* pair_out, void* save) {
+  triattn_check(w, N);
+  nonnull(pair_in, "triattn pair_in"); nonnull(mask, "triattn mask");
+  nonnull(pair_out, "triattn pair_out"); nonnull(save, "triattn save");
+  const int C = w.C, HD = w.H * w.D;
+  const long M = (long)N * N;
+  Arena& ar = arena();
+  std::lock_guard<std::recursive_mutex> lk(ar.lock());
+  ar.reset(st, (size_t)M * C * 2 + (size_t)M * HD * 2 + 1024);
+  h16* xn = ar.take_n<h16>((size_t)M * C);
+  h16* og = ar.take_n<h16>((size_t)M * HD);
+  triattn_fwd_with(st, w, per_column, N, pair_in, mask, tbl, pair_out, save, xn, og);
+}
+
+// ------------------------------------------------- the allocation-free variant
+// Its scratch (xn and og of triattn_fwd_with) is this file-scope device
+// array: one copy per GPU, allocated with the code object, held until the
+// process ends.  Host code never passes `scratch` itself (its host-side name
+// is a stand-in, not a device address): the first call on each device looks
+// up the device address with hipGetSymbolAddress and keeps it per device.
+// Calls on one GPU share the array, so calls that overlap on one GPU race.
+static __device__ __align__(256) unsigned char scratch[TRIATTN_NOALLOC_SCRATCH_BYTES];
+
+static void* scratch_ptr() {
+  static std::mutex mu;
+  static void* per_dev[64] = {};
+  int dev = 0;
+  hip_check(hipGetDevice(&dev), "hipGetDevice");
+  if (dev < 0 || dev >= 64) throw std::runtime_error("triattn noalloc: device index out of range");
+  std::lock_guard<std::mutex> lk(mu);
+  if (!per_dev[dev]) {
+    void* p = nullptr;
+    hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    per_dev[dev] = p;
+  }
+  return per_dev[dev];
+}
+
+void triattn_fwd_noalloc(hipStream_t st, const TriAttnW& w, bool per_column, int N,
+                         const float* pair_in, const float* mask, const float* tbl,
+                         float* pair_out, void* save) {
+  triattn_check(w, N);
+  nonnull(pair_in, "triattn pair_in"); nonnull(mask, "triattn mask");
+  nonnull(pair_out, "triattn pair_out"); nonnull(save, "triattn save");
+  const int C = w.C, HD = w.H * w.D;
+  const size_t M = (size_t)N * N;
+  const size_t xn_bytes = (M * C * sizeof(h16) + 255) & ~size_t(255);
+  if (xn_bytes + M * HD * sizeof(h16) > TRIATTN_NOALLOC_SCRATCH_BYTES)
+    throw std::invalid_argument(
+        "triattn_fwd_noalloc: N = " + std::to_string(N) + " needs " +
+        std::to_string(xn_bytes + M * HD * sizeof(h16)) + " bytes of scratch; the static scratch holds " +
+        std::to_string(TRIATTN_NOALLOC_SCRATCH_BYTES) + " (N <= 256 at C = 128)");
+  char* base = static_cast<char*>(scratch_ptr());
+  h16* xn = reinterpret_cast<h16*>(base);
+  h16* og = reinterpret_cast<h16*>(base + xn_bytes);
+  triattn_fwd_with(st, w, per_column, N, pair_in, mask, tbl, pair_out, save, xn, og);
 }
 
 void triattn_bwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,

@@ -60,6 +60,19 @@ int bc2n_triattn_bwd(void* stream, const char* weights_dir, const char* prefix,
                      int per_column, int N, const float* pair,
                      const float* pair_mask, const float* drop_tbl,
                      const void* save, const float* dpair_out, float* dpair_in);
+/* bc2n_triattn_fwd that allocates nothing.  No counterpart in the reference:
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * operands and results as bc2n_triattn_fwd (bit for bit); its scratch is a
+ * static 32 MiB device array per GPU, so N <= 256 at C = 128 (a larger N
+ * returns an error before any launch).  The weights must already be
+ * resident: call bc2n_triattn_fwd once with the same weights_dir/prefix
+ * first, else an error is returned.  Calls that overlap on one GPU share
+ * the array and race; serialise them (one stream). */
+int bc2n_triattn_fwd_noalloc(void* stream, const char* weights_dir, const char* prefix,
+                             int per_column, int N, const float* pair,
+                             const float* pair_mask, const float* drop_tbl,
+                             float* pair_out, void* save);
 
 /* Triangle multiplication, outgoing (outgoing=1, 'ikc,jkc->ijc') or incoming
  * (outgoing=0, 'kjc,kic->ijc'), AF2's fused-projection form with

@@ -34,3 +34,11 @@ def test_bad_arguments_return_status_not_exit():
     st = L.bc2n_triattn_fwd(None, None, None, 0, 32, None, None, None, None, None)
     assert st != 0
     assert b"weights_dir" in L.bc2n_last_error()
+
+
+def test_noalloc_refuses_weights_not_resident():
+    # host-side refusal: the weights cache is consulted before any GPU call
+    L = b.lib()
+    st = L.bc2n_triattn_fwd_noalloc(None, b"/nonexistent", b"p/", 0, 32, 1, 1, None, 2, 3)
+    assert st != 0
+    assert b"not resident" in L.bc2n_last_error()
