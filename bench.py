@@ -9,19 +9,25 @@ trunk of one design gradient step at L=224 -- forward AND backward of
     (native_evoformer_fwd/bwd),
 with dropout on (JAX-exact masks from a stack key), random-init weights
 (LeCun normal, AF2 gate init) and N(0,1) synthetic activations resident in
-HBM, 10% of residues masked.  The embedder, template-feature embedding,
-structure module and losses around the trunk are not part of the timed
-step (they are ~1% of the reference's step and not built yet).
+HBM, 10% of residues masked.  The same line also carries `design_step_ms`:
+the one-call design step from the designed logits (sequence features,
+embedder, template embedding, the three stacks, the 8-iteration structure
+module, heads and confidence metrics, forward and backward to d(logits)).
 
-`--workload triattn` times BASELINE configs[1] instead (flash triangle
-attention fwd+bwd, both orientations, L=224).
+`--workload triattn` / `trimul` time BASELINE configs[1] / configs[2]
+(one module fwd+bwd, both orientations / directions); `--workload design`
+the one-call design step alone; `--workload fold` the structure module's 8
+fold iterations; `--n 512` any of them at the large complex's length.
 
-Prints ONE JSON line.  `roofline` is the dominant kernel's achieved rate
-(its algorithmic work per launch / its mean launch time, HIP events on its
-own stream, recorded in a second pass of the same K steps) against the
-MI355X dense bf16 MFMA peak or the HBM peak; `cpu_baseline` times the
-oracle (fp32 torch-CPU restatement of the reference's JAX modules) on this
-host on a bounded sample and extrapolates to one step.
+Prints ONE JSON line.  `roofline` is the dominant kernel's achieved rate:
+its algorithmic work per launch (kernel_model) over its mean launch time,
+HIP events recorded on its own stream around its launches alone in a second
+pass of the same K steps (events around every launch slow the step by ~10%),
+against the MI355X dense MFMA peak or the HBM peak, whichever its arithmetic
+intensity puts it under.  `cpu_baseline` times the oracle (fp32 torch-CPU
+restatement of the reference's JAX modules) on this host: one Evoformer block
+forward at L=64 and, extrapolated from one block of
+each kind, the trunk step.
 """
 import argparse
 import json
@@ -34,7 +40,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "ms per design grad step (48-block trunk fwd+bwd) at L=224; triattn/trimul TFLOP/s"
-PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_MFMA_TFLOPS = 2500.0   # MI355X dense fp16/bf16 MFMA
 PEAK_HBM_GBS = 8000.0
 
 
@@ -55,54 +61,64 @@ def trimul_flops(n, c=128, i=128):
     return fwd + bwd
 
 
-# Per-launch algorithmic model of the hot kernels at length n (C = c_z = 128,
-# H = 4 heads of 32, I = 128, M = n^2 tokens): (MFMA FLOPs, HBM bytes).
-# Bytes count each operand read and each result written once (bf16 = 2 B,
-# f32 = 4 B); FLOPs are the products the kernel executes (the attention
-# backward's recomputed scores included).  A kernel whose FLOP/byte is below
-# the machine balance (RIDGE) is HBM-bound on the roofline, above it MFMA-bound.
-RIDGE = PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)  # 312.5 FLOP/B
+# Per-launch algorithmic model of the hot kernels at length n (M = n^2
+# tokens): (MFMA FLOPs, HBM bytes).  Timer names without a prefix are the
+# pair track's launches (C = c_z = 128, H = 4 heads, I = 128, transition
+# factor 4); "tpl."-prefixed ones are the template stack's (C = I = 64,
+# H = 4 heads of 16, factor 2).  Bytes count each operand read and each
+# result written once (binary16 = 2 B, f32 = 4 B); FLOPs are the products the
+# kernel executes (the attention backward's recomputed scores included).  A
+# kernel whose FLOP/byte is below the machine balance (RIDGE) is HBM-bound on
+# the roofline, above it MFMA-bound.  Names of other widths ("msa.") and
+# kernels outside the model give None.
+RIDGE = PEAK_MFMA_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)  # 312.5 FLOP/B
 
 
 def kernel_model(name, n):
-    c = 128
+    c, h, f = 128, 4, 4
+    if name.startswith("tpl."):
+        c, h, f, name = 64, 4, 2, name[4:]
+    elif name.startswith("msa."):
+        return None
     m = n * n
     gemm = lambda k, cols: 2 * m * k * cols
     model = {
-        # q|k|v|g read, o and og written, bias/lse/mask
-        "attn_fwd": (4 * n ** 3 * c, m * (1024 + 512 + 16 + 16 + 4)),
-        # q,k,v,dO read, dq written, bias/lse/Dsum/mask
-        "attn_bwd_dq": (6 * n ** 3 * c, m * (768 + 256 + 256 + 16 + 32 + 4)),
-        # q,dO,k,v read, dk,dv written, bias/lse/Dsum/mask, d(bias) once
-        "attn_bwd_dkv": (8 * n ** 3 * c, m * (1024 + 512 + 16 + 32 + 4 + 16)),
-        "trimul.contract_fwd": (2 * c * n ** 3, m * (512 + 512)),
-        "trimul.contract_bwd": (2 * c * n ** 3, m * (256 + 256 + 256)),
-        "triattn.gemm_qkvg": (gemm(c, 4 * c), m * (256 + 1024)),
-        "triattn.gemm_out": (gemm(c, c), m * (256 + 512 + 512)),
-        "triattn.gemm_dout": (gemm(c, c), m * (512 + 256 * 4 + 16)),
-        "triattn.gemm_dx": (gemm(4 * c, c), m * (1024 + 512)),
-        "trimul.gemm_proj": (gemm(c, 5 * c), m * (256 + 512 + 256 + 4)),
-        "trimul.proj_bwd": (gemm(c, 4 * c), m * (256 + 512 + 4 + 1024)),
-        "trimul.gemm_out": (gemm(c, c), m * (256 + 256 + 512 + 256 + 512)),
-        "trimul.gemm_dout": (gemm(c, c), m * (512 + 256 + 256 + 512 + 256)),
-        "trimul.gemm_dx": (gemm(5 * c, c), m * (1280 + 512)),
+        # q|k|v|g read, o and og written, bias, lse, mask
+        "attn_fwd": (4 * n ** 3 * c, m * (8 * c + 4 * c + 4 * h + 4 * h + 4)),
+        # q,k,v,dO read, dq written, bias, lse + Dsum, mask
+        "attn_bwd_dq": (6 * n ** 3 * c, m * (6 * c + 2 * c + 2 * c + 4 * h + 8 * h + 4)),
+        # q,dO,k,v read, dk,dv written, bias, lse + Dsum, mask, d(bias) once
+        "attn_bwd_dkv": (8 * n ** 3 * c, m * (8 * c + 4 * c + 4 * h + 8 * h + 4 + 4 * h)),
+        # left, right read (binary16); T written (f32)
+        "trimul.contract_fwd": (2 * c * n ** 3, m * (4 * c + 4 * c)),
+        # dT and one operand read, dL or dR written (binary16)
+        "trimul.contract_bwd": (2 * c * n ** 3, m * 6 * c),
+        "triattn.gemm_qkvg": (gemm(c, 4 * c), m * (2 * c + 8 * c)),
+        "triattn.gemm_out": (gemm(c, c), m * (2 * c + 4 * c + 4 * c)),
+        "triattn.gemm_dout": (gemm(c, c), m * (4 * c + 8 * c + 4 * h)),
+        "triattn.gemm_dx": (gemm(4 * c, c), m * (8 * c + 4 * c)),
+        "trimul.gemm_proj": (gemm(c, 5 * c), m * (2 * c + 4 * c + 2 * c + 4)),
+        "trimul.proj_bwd": (gemm(c, 4 * c), m * (2 * c + 4 * c + 4 + 8 * c)),
+        "trimul.gemm_out": (gemm(c, c), m * (2 * c + 2 * c + 4 * c + 2 * c + 4 * c)),
+        "trimul.gemm_dout": (gemm(c, c), m * (4 * c + 2 * c + 2 * c + 4 * c + 2 * c)),
+        "trimul.gemm_dx": (gemm(5 * c, c), m * (10 * c + 4 * c)),
         # recompute GEMM + d(cat) + dX GEMM + LayerNorm backward: xn, d(left|right),
-        # d(cat)'s gating columns, mask, x, dout read; din written
+        # d(cat)'s gating columns, mask, x, dout read, din written, LN stats
         "trimul.tail_bwd": (gemm(c, 4 * c) + gemm(5 * c, c),
-                            m * (256 + 512 + 256 + 4 + 512 + 512 + 512 + 8)),
-        "trimul.gemm_dx_ln": (gemm(5 * c, c), m * (1280 + 512 * 3 + 8)),
-        "triattn.gemm_dx_ln": (gemm(4 * c, c), m * (1024 + 512 * 3 + 16 + 8)),
-        "trans.gemm_dx_ln": (gemm(4 * c, c), m * (1024 + 512 * 3 + 8)),
-        "trans.gemm1": (gemm(c, 4 * c), m * (256 + 1024)),
-        "trans.gemm2": (gemm(4 * c, c), m * (1024 + 512 + 512)),
-        "trans.gemm_dh": (gemm(c, 4 * c), m * (512 + 1024 + 1024)),
-        "trans.gemm_dx": (gemm(4 * c, c), m * (1024 + 512)),
-        "triattn.ln_fwd": (0, m * (512 + 256 + 16 + 8)),
-        "triattn.ln_bwd": (0, m * (512 * 4 + 16 + 8)),
-        "trimul.ln_fwd": (0, m * (512 + 256 + 8)),
-        "trimul.ln_bwd": (0, m * (512 * 4 + 8)),
-        "trimul.ln_center": (0, m * (512 + 256 + 8)),
-        "trimul.ln_center_bwd": (0, m * (512 + 512 + 256 + 8)),
+                            m * (2 * c + 4 * c + 2 * c + 4 + 4 * c + 4 * c + 4 * c + 8)),
+        "trimul.gemm_dx_ln": (gemm(5 * c, c), m * (10 * c + 12 * c + 8)),
+        "triattn.gemm_dx_ln": (gemm(4 * c, c), m * (8 * c + 12 * c + 4 * h + 8)),
+        "trans.gemm_dx_ln": (gemm(f * c, c), m * (2 * f * c + 12 * c + 8)),
+        "trans.gemm1": (gemm(c, f * c), m * (2 * c + 2 * f * c)),
+        "trans.gemm2": (gemm(f * c, c), m * (2 * f * c + 4 * c + 4 * c)),
+        "trans.gemm_dh": (gemm(c, f * c), m * (4 * c + 4 * f * c)),
+        "trans.gemm_dx": (gemm(f * c, c), m * (2 * f * c + 4 * c)),
+        "triattn.ln_fwd": (0, m * (6 * c + 4 * h + 8)),
+        "triattn.ln_bwd": (0, m * (16 * c + 4 * h + 8)),
+        "trimul.ln_fwd": (0, m * (6 * c + 8)),
+        "trimul.ln_bwd": (0, m * (16 * c + 8)),
+        "trimul.ln_center": (0, m * (6 * c + 8)),
+        "trimul.ln_center_bwd": (0, m * (10 * c + 8)),
     }
     return model.get(name)
 
@@ -159,6 +175,22 @@ def cpu_trunk_baseline(n, budget_s=20.0):
         out = af2.template_iteration(pair, pmask, tprm, "param/block0/", key, True, dtype=f32)
         torch.autograd.grad(out, pair, torch.randn_like(out))
 
+    def config1_block():
+        # one Evoformer block forward at L=64, S=1, fp32,
+        # N(0,1) activations, all-ones masks, AF2 gate init, no dropout
+        n1 = 64
+        with torch.no_grad():
+            af2.evoformer_iteration(torch.randn(1, n1, 256), torch.randn(n1, n1, 128),
+                                    torch.ones(1, n1), torch.ones(n1, n1), prm, "param/block0/",
+                                    None, False, dtype=f32)
+
+    config1_block()  # first-call setup out of the timing
+    reps, t0 = 0, time.perf_counter()
+    while reps < 50 and time.perf_counter() - t0 < 3.0:
+        config1_block()
+        reps += 1
+    config1_ms = (time.perf_counter() - t0) / reps * 1e3
+
     times = {}
     spent = 0.0
     for name, fn in (("evo", evo_block), ("pair_only", pair_only_block), ("tpl", tpl_block)):
@@ -173,10 +205,26 @@ def cpu_trunk_baseline(n, budget_s=20.0):
         spent += el
     step_ms = (48 * times["evo"] + 4 * times["pair_only"] + 2 * times["tpl"]) * 1e3
     return {"value": round(step_ms, 1), "unit": "ms", "cores": threads, "kind": "port",
+            "cpu": cpu_model(), "config1_block_fwd_ms": round(config1_ms, 2),
             "sample": (f"oracle fp32 torch-CPU, one block each fwd+bwd at L={n}: Evoformer "
                        f"{times['evo']:.2f} s, pair-only {times['pair_only']:.2f} s, template "
                        f"{times['tpl']:.2f} s ({spent:.1f} s of CPU work on {threads} threads); "
-                       f"step = 48 x Evoformer + 4 x pair-only + 2 x template (extrapolated)")}
+                       f"step = 48 x Evoformer + 4 x pair-only + 2 x template (extrapolated); "
+                       f"config1_block_fwd_ms = one Evoformer block forward at L=64 "
+                       f"(BASELINE configs[0]), {reps} reps")}
+
+
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), or the platform string."""
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or platform.machine()
 
 
 def cpu_triattn_baseline(n, seconds=12.0):
@@ -205,7 +253,7 @@ def cpu_triattn_baseline(n, seconds=12.0):
         if el >= seconds or reps >= 50:
             break
     return {"value": round(triattn_flops(n) * reps / el / 1e12, 4), "unit": "TFLOP/s",
-            "cores": threads, "kind": "port",
+            "cores": threads, "kind": "port", "cpu": cpu_model(),
             "sample": f"oracle fp32 torch-CPU triangle attention (starting node) fwd+bwd at "
                       f"L={n}, {reps} reps in {el:.1f} s on {threads} host threads"}
 
@@ -243,7 +291,7 @@ def traffic_of(kernel, n):
            "trimul.gemm_out": r"EpiTrimulOut",
            "triattn.gemm_dx_ln": r"EpiLnBwd<4>|EpiLnBwdILi4E",
            "trimul.contract_fwd": rf"contract(_kernel)?(<{nb}, .*float>|ILi{nb}E.*fEE)",
-           "trimul.contract_bwd": rf"contract(_kernel)?(<{nb}, .*bf16>|ILi{nb}E.*DF16bEE)"}.get(kernel)
+           "trimul.contract_bwd": rf"contract(_kernel)?(<{nb}, .*_Float16>|ILi{nb}E.*DF16_EE)"}.get(kernel)
     if pat is None:
         return None
     import re
@@ -254,34 +302,58 @@ def traffic_of(kernel, n):
     return int(k["fetch_bytes"] + k["write_bytes"])
 
 
+def event_overhead_us(reps=200):
+    """Median elapsed time of an empty event pair (two events recorded back
+    to back on the idle stream): what bracketing a launch with events adds to
+    its measured duration."""
+    import torch
+    torch.cuda.synchronize()
+    pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+             for _ in range(reps)]
+    for a, b in pairs:
+        a.record()
+        b.record()
+    torch.cuda.synchronize()
+    v = sorted(a.elapsed_time(b) for a, b in pairs)
+    return v[len(v) // 2] * 1e3
+
+
+EVENT_OVERHEAD_US = 0.0  # set by main() once the GPU is up
+
+
 def _rate(name, n, tot_ms, cnt):
     flops, nbytes = kernel_model(name, n)
-    us = tot_ms / cnt * 1e3
+    us = max(tot_ms / cnt * 1e3 - EVENT_OVERHEAD_US, 1e-3)
     tf = flops / (us * 1e-6) / 1e12
     gbs = nbytes / (us * 1e-6) / 1e9
     bound = "mfma" if flops / nbytes >= RIDGE else "hbm"
     return us, tf, gbs, bound
 
 
-def roofline_from(prof, n):
-    """The dominant modelled kernel (largest total time): its achieved rate in
-    the unit of the bound its arithmetic intensity puts it under."""
-    cand = {k: v for k, v in prof.items() if kernel_model(k, n) is not None}
-    if not cand:
+def roofline_from(prof, n, dom_prof=None):
+    """The dominant modelled kernel (largest total time in `prof`): its
+    achieved rate in the unit of the bound its arithmetic intensity puts it
+    under, timed from `dom_prof` (a pass timing that kernel alone) when
+    given."""
+    dom = dominant(prof, n)
+    if dom is None:
         return None
-    dom = max(cand, key=lambda k: cand[k][0])
-    tot, cnt = cand[dom]
+    tot, cnt = (dom_prof or prof)[dom]
     us, tf, gbs, bound = _rate(dom, n, tot, cnt)
     flops, nbytes = kernel_model(dom, n)
     if bound == "mfma":
-        ach, peak, unit = tf, PEAK_BF16_TFLOPS, "TFLOP/s"
+        ach, peak, unit = tf, PEAK_MFMA_TFLOPS, "TFLOP/s"
     else:
         ach, peak, unit = gbs, PEAK_HBM_GBS, "GB/s"
     return {"kernel": dom, "bound": bound, "achieved": round(ach, 2), "peak": peak, "unit": unit,
             "frac": round(ach / peak, 4), "traffic": traffic_of(dom, n), "launch_us": round(us, 2),
             "algorithmic_bytes": nbytes, "algorithmic_flops": flops,
             "flop_per_byte": round(flops / nbytes, 1), "ridge": round(RIDGE, 1),
-            "mfma_tflops": round(tf, 2), "mfma_frac": round(tf / PEAK_BF16_TFLOPS, 4)}
+            "mfma_tflops": round(tf, 2), "mfma_frac": round(tf / PEAK_MFMA_TFLOPS, 4),
+            "timing": ("events around this kernel's launches alone" if dom_prof else
+                       "events around every launch") +
+                      f", less the {EVENT_OVERHEAD_US:.2f} us an empty event pair measures",
+            "launch_us_events": round(tot / cnt * 1e3, 2)}
 
 
 def kernel_rooflines(prof, n):
@@ -292,9 +364,14 @@ def kernel_rooflines(prof, n):
         if kernel_model(k, n) is None:
             continue
         us, tf, gbs, bound = _rate(k, n, tot, cnt)
-        rows.append({"kernel": k, "us": round(us, 2), "bound": bound, "tflops": round(tf, 1),
-                     "mfma_frac": round(tf / PEAK_BF16_TFLOPS, 4), "gbs": round(gbs, 0),
-                     "hbm_frac": round(gbs / PEAK_HBM_GBS, 4)})
+        row = {"kernel": k, "us": round(us, 2), "bound": bound, "tflops": round(tf, 1),
+               "mfma_frac": round(tf / PEAK_MFMA_TFLOPS, 4), "gbs": round(gbs, 0),
+               "hbm_frac": round(gbs / PEAK_HBM_GBS, 4)}
+        if row["mfma_frac"] > 1.0 or row["hbm_frac"] > 1.0:
+            # a rate above peak is a byte/FLOP model error, never a result
+            row["model_error"] = True
+            print(f"bench.py: kernel_model overstates {k} ({row})", file=sys.stderr)
+        rows.append(row)
     return rows
 
 
@@ -370,19 +447,26 @@ def _progress(what):
         print(f"bench: {what} done", file=sys.stderr, flush=True)
 
 
-def profiled(step, steps, skip):
-    """A second pass of `steps` steps with the per-kernel event timer on:
-    {name: (total ms, launches)}; {} when skipped (--no-kprof)."""
+def profiled(step, steps, skip, only=None):
+    """A pass of `steps` steps with the per-kernel event timer on (around the
+    launches named `only` alone, if given): {name: (total ms, launches)}; {}
+    when skipped (--no-kprof)."""
     if skip:
         return {}
     import bindcraft2_amd as b
-    b.prof_enable(True)
+    b.prof_enable(True, only=only)
     for i in range(steps):
         step()
-        _progress(f"profiled step {i}")
+        _progress(f"profiled step {i}" + (f" ({only})" if only else ""))
     prof = b.prof_read()
     b.prof_enable(False)
     return prof
+
+
+def dominant(prof, n):
+    """The modelled kernel with the largest total time in `prof`."""
+    cand = {k: v for k, v in prof.items() if kernel_model(k, n) is not None}
+    return max(cand, key=lambda k: cand[k][0]) if cand else None
 
 
 def timed(step, steps, warmup):
@@ -400,6 +484,51 @@ def timed(step, steps, warmup):
     return ms
 
 
+def design_step_setup(n, rng, dev, m1):
+    """The one-call design step from the designed logits (sequence features,
+    embedder, template embedding (2 blocks), extra stack (4, pair only), main
+    stack (48), structure module (8 iterations), heads and the confidence
+    metrics), forward + backward to the logits, on random weights and inputs:
+    returns (step closure, save-set bytes)."""
+    import torch
+    from bindcraft2_amd import ops, params as bparams, weights as W
+    tree = W.init_af2_params(rng, num_blocks=48, extra_blocks=4, template_blocks=2)
+    root = tempfile.mkdtemp(prefix="bc2n_bench_ds_")
+    tables = bparams.init_residue_tables(rng)
+    dirs = [W.embed_weights_from_params(tree, os.path.join(root, "emb")),
+            W.tplembed_weights_from_params(tree, os.path.join(root, "tpl")),
+            W.stack_weights_from_params(tree, os.path.join(root, "extra"), prefix=W.EXTRA),
+            W.stack_weights_from_params(tree, os.path.join(root, "main"), prefix=W.MAIN),
+            W.post_weights_from_params(tree, os.path.join(root, "post"), tables=tables)]
+    step_mod = ops.DesignStepSeq(*dirs, depths=(2, 4, 48, 8))
+    nt = n - 64  # the target; the last 64 residues are designed
+    logits = 0.5 * torch.randn(n, 20, device=dev)
+    flags = torch.zeros(n, dtype=torch.uint8, device=dev)
+    flags[nt:] = 1  # the binder is designed; the target passes through
+    logits[:nt] = torch.nn.functional.one_hot(torch.randint(0, 20, (nt,), device=dev), 20).float()
+    scalars = torch.tensor([1.0, 0.0, 1.0, 1.0], device=dev)  # the soft stage
+    ids = [torch.arange(n, dtype=torch.float32, device=dev),
+           (torch.arange(n, device=dev) >= nt).float() + 1,
+           (torch.arange(n, device=dev) >= nt).float() + 1, torch.ones(n, device=dev)]
+    iasym = (torch.arange(n, device=dev) >= nt).int()
+    seqm = torch.as_tensor(m1, device=dev)
+    act_const = 0.1 * torch.randn(n, n, 64, device=dev)
+    seeds = torch.tensor([[0, 11 + i, 1] for i in range(4)], dtype=torch.int64).to(
+        torch.uint32).to(dev)
+    save = torch.empty(step_mod.save_bytes(n), dtype=torch.uint8, device=dev)
+    cts = [torch.randn(*sh, device=dev) for sh in ((n, 14, 3), (n, n, 64), (n, n, 64),
+                                                  (n, 50), (n, 37))]
+    conf_cts = [torch.randn(*sh, device=dev) for sh in ((n,), (n, n), (1,), (1,), (n,), (n,))]
+
+    def step():
+        step_mod.forward(logits, flags, scalars, ids, seqm, act_const=act_const, seeds=seeds,
+                         save=save, interface_asym=iasym)
+        step_mod.backward(cts, logits, flags, scalars, seqm, save, interface_asym=iasym,
+                          conf_cts=conf_cts)
+
+    return step, save.numel()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -414,6 +543,8 @@ def main():
                     help="write the per-kernel HBM traffic summary from rocprofv3 --pmc runs")
     ap.add_argument("--no-kprof", action="store_true",
                     help="skip the per-kernel event-timer pass (roofline / kernel table)")
+    ap.add_argument("--no-design", action="store_true",
+                    help="trunk workload: skip the secondary one-call design-step timing")
     ap.add_argument("--progress", action="store_true",
                     help="print a line on stderr after every step (long profiler runs)")
     args = ap.parse_args()
@@ -455,6 +586,9 @@ def main():
                "higher_is_better": True, "config": {"workload": "copy", "bytes": nbytes}}
         print(json.dumps(out))
         return
+    global EVENT_OVERHEAD_US
+    EVENT_OVERHEAD_US = event_overhead_us()
+    dom_prof = None  # the roofline kernel's own timing pass
     if args.workload == "fold":
         # BASELINE configs[4]'s structure-module part: 8 fold iterations (IPA,
         # transition, rigid update) forward+backward, f32, dropout on
@@ -512,56 +646,18 @@ def main():
                            "head_dim": 32, "masked_residues": 0.1, "flops_per_step": flops}}
         cpu = None if args.no_cpu_baseline else cpu_triattn_baseline(n)
     elif args.workload == "design":
-        # the one-call design step from the designed logits: sequence features,
-        # embedder, template embedding (2 blocks), extra stack (4, pair only),
-        # main stack (48), structure module (8 iterations), heads and the
-        # confidence metrics, forward + backward to the logits
-        from bindcraft2_amd import weights as W
-        tree = W.init_af2_params(rng, num_blocks=48, extra_blocks=4, template_blocks=2)
-        root = tempfile.mkdtemp(prefix="bc2n_bench_ds_")
-        tables = bparams.init_residue_tables(rng)
-        dirs = [W.embed_weights_from_params(tree, os.path.join(root, "emb")),
-                W.tplembed_weights_from_params(tree, os.path.join(root, "tpl")),
-                W.stack_weights_from_params(tree, os.path.join(root, "extra"), prefix=W.EXTRA),
-                W.stack_weights_from_params(tree, os.path.join(root, "main"), prefix=W.MAIN),
-                W.post_weights_from_params(tree, os.path.join(root, "post"), tables=tables)]
-        step_mod = ops.DesignStepSeq(*dirs, depths=(2, 4, 48, 8))
-        logits = 0.5 * torch.randn(n, 20, device=dev)
-        flags = torch.zeros(n, dtype=torch.uint8, device=dev)
-        flags[160:] = 1  # the 64-residue binder is designed; the target passes through
-        logits[:160] = torch.nn.functional.one_hot(torch.randint(0, 20, (160,), device=dev),
-                                                   20).float()
-        scalars = torch.tensor([1.0, 0.0, 1.0, 1.0], device=dev)  # the soft stage
-        ids = [torch.arange(n, dtype=torch.float32, device=dev),
-               (torch.arange(n, device=dev) >= 160).float() + 1,
-               (torch.arange(n, device=dev) >= 160).float() + 1, torch.ones(n, device=dev)]
-        iasym = (torch.arange(n, device=dev) >= 160).int()
-        seqm = torch.as_tensor(m1, device=dev)
-        act_const = 0.1 * torch.randn(n, n, 64, device=dev)
-        seeds = torch.tensor([[0, 11 + i, 1] for i in range(4)], dtype=torch.int64).to(
-            torch.uint32).to(dev)
-        save = torch.empty(step_mod.save_bytes(n), dtype=torch.uint8, device=dev)
-        cts = [torch.randn(*sh, device=dev) for sh in ((n, 14, 3), (n, n, 64), (n, n, 64),
-                                                      (n, 50), (n, 37))]
-        conf_cts = [torch.randn(*sh, device=dev) for sh in ((n,), (n, n), (1,), (1,), (n,), (n,))]
-
-        def step():
-            step_mod.forward(logits, flags, scalars, ids, seqm, act_const=act_const, seeds=seeds,
-                             save=save, interface_asym=iasym)
-            step_mod.backward(cts, logits, flags, scalars, seqm, save, interface_asym=iasym,
-                              conf_cts=conf_cts)
-
+        step, save_bytes = design_step_setup(n, rng, dev, m1)
         ms = timed(step, args.steps, args.warmup)
         prof = profiled(step, args.steps, args.no_kprof)
         line = {"metric": "ms per one-call design step (sequence features + embedder + template "
                           "+ 4 extra + 48 Evoformer + 8-iteration structure module + heads + "
                           "confidence, fwd+bwd)",
                 "value": round(ms, 2), "unit": "ms", "higher_is_better": False,
-                "config": {"workload": "one-call design step at L=224 (160 target + 64 designed), "
-                                       "logits in, structure and confidence outputs out, d logits "
-                                       "back, dropout on",
+                "config": {"workload": f"one-call design step at L={n} ({n - 64} target + 64 "
+                                       "designed), logits in, structure and confidence outputs "
+                                       "out, d logits back, dropout on",
                            "L": n, "n_seq": 1, "depths": [2, 4, 48, 8]},
-                "save_set_gb": round(save.numel() / 1e9, 2)}
+                "save_set_gb": round(save_bytes / 1e9, 2)}
         cpu = None
     elif args.workload == "trimul":
         mods = ["triangle_multiplication_outgoing", "triangle_multiplication_incoming"]
@@ -631,25 +727,38 @@ def main():
 
         ms = timed(step, args.steps, args.warmup)
         prof = profiled(step, args.steps, args.no_kprof)
+        dom = dominant(prof, n)
+        dom_prof = profiled(step, args.steps, args.no_kprof or dom is None, only=dom)
         tri = sum(v[0] for k, v in prof.items() if k.startswith("attn_") or k.startswith("triattn."))
         tm = sum(v[0] for k, v in prof.items() if k.startswith("trimul."))
         n_tri = 2 * (48 + 4) * args.steps
+        cfg = "BASELINE configs[3]" if n == 224 else "BASELINE configs[4]'s trunk" if n == 512 else "custom length"
         line = {"metric": METRIC, "value": round(ms, 2), "unit": "ms", "higher_is_better": False,
-                "config": {"workload": "design-step trunk fwd+bwd at L=224: 48 Evoformer + 4 "
-                                       "extra-MSA (pair-only) + 2 template blocks "
-                                       "(BASELINE configs[3])",
+                "config": {"workload": f"design-step trunk fwd+bwd at L={n}: 48 Evoformer + 4 "
+                                       f"extra-MSA (pair-only) + 2 template blocks ({cfg})",
                            "L": n, "n_seq": 1, "c_m": 256, "c_z": 128, "c_t": 64,
                            "dropout": [0.15, 0.25], "masked_residues": 0.1},
                 "triattn_tflops": round(n_tri * triattn_flops(n) / (tri * 1e-3) / 1e12, 2) if tri else None,
                 "trimul_tflops": round(n_tri * trimul_flops(n) / (tm * 1e-3) / 1e12, 2) if tm else None,
                 "save_set_gb": round((s_main.numel() + s_extra.numel() + s_tpl.numel()) / 1e9, 2)}
+        if not args.no_design:
+            # the whole one-call design step around this trunk (logits to
+            # d(logits)), timed the same way: a secondary key of the line
+            del s_main, s_extra, s_tpl
+            torch.cuda.empty_cache()
+            dstep, _ = design_step_setup(n, np.random.default_rng(1), dev, m1)
+            line["design_step_ms"] = round(timed(dstep, args.steps, args.warmup), 2)
         cpu = None if args.no_cpu_baseline else cpu_trunk_baseline(n)
 
+    if dom_prof is None and prof:
+        dom = dominant(prof, n)
+        if dom is not None:
+            dom_prof = profiled(step, args.steps, args.no_kprof, only=dom)
     out = {"metric": line.pop("metric"), "value": line.pop("value"), "unit": line.pop("unit"),
            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
            "ms_per_step": round(ms, 3), "higher_is_better": line.pop("higher_is_better"),
-           "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
-           "config": line.pop("config"), "roofline": roofline_from(prof, n),
+           "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic",
+           "config": line.pop("config"), "roofline": roofline_from(prof, n, dom_prof),
            "cpu_baseline": cpu}
     out.update(line)
     if prof and args.workload in ("trunk", "triattn", "trimul"):

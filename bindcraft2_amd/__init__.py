@@ -103,6 +103,7 @@ def _declare(L):
         "bc2n_bernoulli_bits": (i, [vp, vp, c.c_long, u32, u32, f]),
         "bc2n_stack_keys": (i, [vp, vp, i, vp]),
         "bc2n_prof_enable": (i, [i]),
+        "bc2n_prof_filter": (i, [cs]),
         "bc2n_prof_read": (i, [vp, i, vp, vp, i]),
         "bc2n_probe_gemm": (i, [vp, i, i, i, vp, vp, vp]),
         "bc2n_probe_gemm_f32": (i, [vp, i, i, i, i, vp, c.c_long, c.c_long, c.c_long, vp,
@@ -134,7 +135,10 @@ def exported_symbols():
     return sorted(set(re.findall(r"\b(bc2n_[a-z0-9_]+)\s*\(", txt)))
 
 
-def prof_enable(on=True):
+def prof_enable(on=True, only=None):
+    """Per-kernel event timing on/off; `only`: time just the launches of that
+    timer name."""
+    check(lib().bc2n_prof_filter(None if only is None else only.encode()))
     check(lib().bc2n_prof_enable(int(on)))
 
 

@@ -902,6 +902,10 @@ int bc2n_prof_enable(int on) {
   return guarded([&] { kprof_enable(on != 0); });
 }
 
+int bc2n_prof_filter(const char* name) {
+  return guarded([&] { kprof_filter(name); });
+}
+
 int bc2n_prof_read(char* names, int name_len, double* ms, int* counts, int cap) {
   int n = -1;
   if (guarded([&] { n = kprof_read(names, name_len, ms, counts, cap); }) != 0) return -1;

@@ -124,6 +124,7 @@ int device_cus() {
 namespace {
 struct KProf {
   bool on = false;
+  std::string filter;  // empty: every launch
   std::mutex mu;
   std::vector<hipEvent_t> pool;
   size_t next = 0;
@@ -137,6 +138,16 @@ KProf& kp() {
 
 void kprof_enable(bool on) { kp().on = on; }
 bool kprof_on() { return kp().on; }
+void kprof_filter(const char* name) {
+  KProf& k = kp();
+  std::lock_guard<std::mutex> lk(k.mu);
+  k.filter = name ? name : "";
+}
+bool kprof_wants(const char* name) {
+  KProf& k = kp();
+  std::lock_guard<std::mutex> lk(k.mu);
+  return k.filter.empty() || k.filter == name;
+}
 
 hipEvent_t kprof_event() {
   KProf& k = kp();

@@ -91,18 +91,28 @@ int device_cus();
 // events and returns per-name totals.  Off by default (no events recorded).
 void kprof_enable(bool on);
 bool kprof_on();
+// Restrict the timer to launches named `name` (null: every launch): events
+// around one kernel's launches only perturb the rest of the step least.
+void kprof_filter(const char* name);
+bool kprof_wants(const char* name);
 void kprof_record(const char* name, hipEvent_t a, hipEvent_t b);
 hipEvent_t kprof_event();
 // Fills names/ms/counts (up to cap entries), returns the number of entries,
 // and clears the records.
 int kprof_read(char* names, int name_len, double* ms, int* counts, int cap);
 
+// Timer name of a module launch by its channel width C: the pair track's
+// names at C = 128, "tpl."-prefixed ones at C = 64 (the template stack),
+// "msa."-prefixed ones otherwise (the MSA transition's C = 256), so a
+// per-kernel table never mixes launches of different widths under one name.
+#define BC2N_TN(C, name) ((C) == 128 ? name : (C) == 64 ? "tpl." name : "msa." name)
+
 struct KTimed {
   const char* name;
   hipStream_t st;
   hipEvent_t a = nullptr;
   KTimed(const char* n, hipStream_t s) : name(n), st(s) {
-    if (kprof_on()) {
+    if (kprof_on() && kprof_wants(n)) {
       a = kprof_event();
       hip_check(hipEventRecord(a, st), "hipEventRecord");
     }

@@ -65,7 +65,7 @@ void transition_fwd(hipStream_t st, const TransW& w, long rows, int nt, const fl
   ar.reset(st, (size_t)rows * C * 2 + 256);
   h16* xn = ar.take_n<h16>((size_t)rows * C);
   {
-    KTimed kt("trans.ln_fwd", st);
+    KTimed kt(BC2N_TN(C, "trans.ln_fwd"), st);
     ln_fwd_f32(st, act_in, rows, C, 0, w.ln_g, w.ln_b, xn, sv.mean, sv.rstd, false, 0, nullptr,
                nullptr);
   }
@@ -73,12 +73,12 @@ void transition_fwd(hipStream_t st, const TransW& w, long rows, int nt, const fl
   g1.M = (int)rows; g1.N = H; g1.K = C;
   g1.A = xn; g1.a_sm = C; g1.a_sk = 1;
   g1.B = w.w1_t; g1.b_sn = C; g1.b_sk = 1;
-  gemm<128, 128>(st, g1, EpiStore<h16, true>{sv.h, H, 0, w.b1, H}, "trans.gemm1");
+  gemm<128, 128>(st, g1, EpiStore<h16, true>{sv.h, H, 0, w.b1, H}, BC2N_TN(C, "trans.gemm1"));
   GemmArgs g2;
   g2.M = (int)rows; g2.N = C; g2.K = H;
   g2.A = sv.h; g2.a_sm = H; g2.a_sk = 1;
   g2.B = w.w2_t; g2.b_sn = H; g2.b_sk = 1;
-  gemm<128, 128>(st, g2, EpiResidualRows(act_in, act_out, w.b2, tbl, nt, C, false), "trans.gemm2");
+  gemm<128, 128>(st, g2, EpiResidualRows(act_in, act_out, w.b2, tbl, nt, C, false), BC2N_TN(C, "trans.gemm2"));
 }
 
 void transition_bwd(hipStream_t st, const TransW& w, long rows, int nt, const float* act_in,
@@ -103,7 +103,7 @@ void transition_bwd(hipStream_t st, const TransW& w, long rows, int nt, const fl
   g1.M = (int)rows; g1.N = H; g1.K = C;
   g1.a_sm = C; g1.a_sk = 1;
   g1.B = w.w2; g1.b_sn = C; g1.b_sk = 1;
-  gemm<128, 128>(st, g1, EpiReluMask<h16>(dh, sv.h, H), "trans.gemm_dh",
+  gemm<128, 128>(st, g1, EpiReluMask<h16>(dh, sv.h, H), BC2N_TN(C, "trans.gemm_dh"),
                  ALoadScaledRows{dout, tbl, nt, C, false, sc});
   GemmArgs g2;
   g2.M = (int)rows; g2.N = C; g2.K = H;
@@ -114,11 +114,11 @@ void transition_bwd(hipStream_t st, const TransW& w, long rows, int nt, const fl
     gemm<128, 128>(st, g2,
                    EpiLnBwd<0>(act_in, w.ln_g, sv.mean, sv.rstd, dout, din, rows, 0, nullptr,
                                nullptr, sc + 1),
-                   "trans.gemm_dx_ln");
+                   BC2N_TN(C, "trans.gemm_dx_ln"));
     return;
   }
-  gemm<128, 128>(st, g2, EpiStore<float>{dxn, C, 0, nullptr, C}, "trans.gemm_dx");
-  KTimed kt("trans.ln_bwd", st);
+  gemm<128, 128>(st, g2, EpiStore<float>{dxn, C, 0, nullptr, C}, BC2N_TN(C, "trans.gemm_dx"));
+  KTimed kt(BC2N_TN(C, "trans.ln_bwd"), st);
   ln_bwd_f32(st, dxn, act_in, rows, C, 0, w.ln_g, sv.mean, sv.rstd, din, true, 0, nullptr, nullptr,
              dout, sc + 1);
 }

@@ -104,7 +104,7 @@ static void triattn_fwd_with(hipStream_t st, const TriAttnW& w, bool per_column,
   Carver cv(save);
   TriAttnSave<Carver> sv(cv, N, C, H);
   {
-    KTimed kt("triattn.ln_fwd", st);
+    KTimed kt(BC2N_TN(C, "triattn.ln_fwd"), st);
     ln_fwd_f32(st, pair_in, M, C, per_column ? N : 0, w.ln_g, w.ln_b, xn, sv.mean, sv.rstd,
                false, H, w.w2d, sv.bias, LOG2E);
   }
@@ -114,7 +114,7 @@ static void triattn_fwd_with(hipStream_t st, const TriAttnW& w, bool per_column,
   g1.B = w.wqkvg_t; g1.b_sn = C; g1.b_sk = 1;
   const float qscale = LOG2E / std::sqrt((float)w.D);
   gemm<128, 128>(st, g1, EpiScaledCols(sv.qkvg, 4L * HD, w.bqkvg, qscale, HD),
-                 "triattn.gemm_qkvg");
+                 BC2N_TN(C, "triattn.gemm_qkvg"));
 
   AttnArgs a;
   a.R = N; a.H = H; a.N = N; a.D = w.D;
@@ -132,7 +132,7 @@ static void triattn_fwd_with(hipStream_t st, const TriAttnW& w, bool per_column,
   g2.A = og; g2.a_sm = HD; g2.a_sk = 1;
   g2.B = w.wo_t; g2.b_sn = HD; g2.b_sk = 1;
   gemm<128, 128>(st, g2, EpiResidualRows(pair_in, pair_out, w.bo, tbl, N, C, per_column),
-                 "triattn.gemm_out");
+                 BC2N_TN(C, "triattn.gemm_out"));
 }
 
 void triattn_fwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
@@ -235,7 +235,7 @@ void triattn_bwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
   EpiGateBwd eg;
   eg.qkvg = sv.qkvg; eg.ld = 4L * HD; eg.o = sv.o; eg.dO = b.dO; eg.dqkvg = b.dqkvg;
   eg.Dsum = b.Dsum; eg.HD = HD; eg.H = H; eg.D = w.D; eg.Ntok = N;
-  gemm<128, 128>(st, g1, eg, "triattn.gemm_dout", ALoadScaledRows{dout, tbl, N, C, per_column, sc});
+  gemm<128, 128>(st, g1, eg, BC2N_TN(C, "triattn.gemm_dout"), ALoadScaledRows{dout, tbl, N, C, per_column, sc});
   b.gate_done = true;
 
   AttnArgs& a = b.f;
@@ -260,12 +260,12 @@ void triattn_bwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
     gemm<128, 128>(st, g2,
                    EpiLnBwd<4>(pair_in, w.ln_g, sv.mean, sv.rstd, dout, din, M, per_column ? N : 0,
                                b.dbias, w.w2d, sc + 1),
-                   "triattn.gemm_dx_ln");
+                   BC2N_TN(C, "triattn.gemm_dx_ln"));
     return;
   }
-  gemm<128, 128>(st, g2, EpiStore<float>{dxn, C, 0, nullptr, C}, "triattn.gemm_dx");
+  gemm<128, 128>(st, g2, EpiStore<float>{dxn, C, 0, nullptr, C}, BC2N_TN(C, "triattn.gemm_dx"));
 
-  KTimed kt("triattn.ln_bwd", st);
+  KTimed kt(BC2N_TN(C, "triattn.ln_bwd"), st);
   ln_bwd_f32(st, dxn, pair_in, M, C, per_column ? N : 0, w.ln_g, sv.mean, sv.rstd, din, true,
              H, b.dbias, w.w2d, dout, sc + 1);
 }

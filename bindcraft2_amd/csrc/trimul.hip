@@ -581,7 +581,7 @@ static void contraction_fwd(hipStream_t st, bool outgoing, int N, int I, const h
     g.B = L; g.b_sn = 1; g.b_sk = N;
   }
   g.a_sb = M; g.b_sb = M;
-  contract<float>(st, g, T, "trimul.contract_fwd");
+  contract<float>(st, g, T, BC2N_TN(I, "trimul.contract_fwd"));
 }
 
 void trimul_fwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const float* pair_in,
@@ -599,7 +599,7 @@ void trimul_fwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
   h16* xn = sv.xn;
   h16* tn = ar.take_n<h16>((size_t)M * I);
   {
-    KTimed kt("trimul.ln_fwd", st);
+    KTimed kt(BC2N_TN(C, "trimul.ln_fwd"), st);
     ln_fwd_f32(st, pair_in, M, C, 0, w.ln_g, w.ln_b, xn, sv.mean, sv.rstd, true, 0, nullptr,
                nullptr);
   }
@@ -609,10 +609,10 @@ void trimul_fwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
   g1.B = w.wcat_t; g1.b_sn = C; g1.b_sk = 1;
   gemm<128, 128>(st, g1,
                  EpiTrimulProj{sv.left, sv.right, sv.gout, w.bp, w.bg, w.bgl, mask, M, I, C},
-                 "trimul.gemm_proj");
+                 BC2N_TN(C, "trimul.gemm_proj"));
   contraction_fwd(st, outgoing, N, I, sv.left, sv.right, sv.T);
   {
-    KTimed kt("trimul.ln_center", st);
+    KTimed kt(BC2N_TN(C, "trimul.ln_center"), st);
     ln_fwd_cm(st, sv.T, M, I, w.cn_g, w.cn_b, tn, sv.cmean, sv.crstd, true);
   }
   GemmArgs g2;
@@ -620,7 +620,7 @@ void trimul_fwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
   g2.A = tn; g2.a_sm = I; g2.a_sk = 1;
   g2.B = w.wo_t; g2.b_sn = I; g2.b_sk = 1;
   gemm<128, 128>(st, g2, EpiTrimulOut(pair_in, pair_out, w.bo, sv.gout, sv.osave, tbl, N, C),
-                 "trimul.gemm_out");
+                 BC2N_TN(C, "trimul.gemm_out"));
 }
 
 void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const float* pair_in,
@@ -661,10 +661,10 @@ void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
   g1.M = (int)M; g1.N = I; g1.K = C;
   g1.a_sm = C; g1.a_sk = 1;
   g1.B = w.wo; g1.b_sn = C; g1.b_sk = 1;
-  gemm<128, 128>(st, g1, EpiStore<float>{dtn, I, 0, nullptr, I}, "trimul.gemm_dout",
+  gemm<128, 128>(st, g1, EpiStore<float>{dtn, I, 0, nullptr, I}, BC2N_TN(C, "trimul.gemm_dout"),
                  ALoadTrimulOut{dout, tbl, sv.gout, sv.osave, dcat, C, ldcat, off, N, sc});
   {
-    KTimed kt("trimul.ln_center_bwd", st);
+    KTimed kt(BC2N_TN(C, "trimul.ln_center_bwd"), st);
     ln_bwd_cm(st, dtn, sv.T, M, I, w.cn_g, sv.cmean, sv.crstd, dT);
   }
   {
@@ -686,8 +686,8 @@ void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
       b.A = sv.left; b.a_sm = N; b.a_sk = 1;
       b.B = dT; b.b_sn = N; b.b_sk = 1;
     }
-    contract<h16>(st, a, dL, "trimul.contract_bwd");
-    contract<h16>(st, b, dR, "trimul.contract_bwd");
+    contract<h16>(st, a, dL, BC2N_TN(C, "trimul.contract_bwd"));
+    contract<h16>(st, b, dR, BC2N_TN(C, "trimul.contract_bwd"));
   }
   if (fused) {
     TailArgs t;
@@ -697,7 +697,7 @@ void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
     t.x = pair_in; t.ln_g = w.ln_g; t.mean = sv.mean; t.rstd = sv.rstd; t.dres = dout;
     t.gmul = sc + 1;
     t.out = din; t.M = M;
-    KTimed kt("trimul.tail_bwd", st);
+    KTimed kt(BC2N_TN(C, "trimul.tail_bwd"), st);
     hipLaunchKernelGGL(trimul_tail_kernel, dim3((unsigned)(M / tail::BM)), dim3(256), 0, st, t);
     return;
   }
@@ -707,7 +707,7 @@ void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
     g.A = sv.xn; g.a_sm = C; g.a_sk = 1;
     g.B = w.wcat_t; g.b_sn = C; g.b_sk = 1;
     gemm<128, 128>(st, g, EpiTrimulProjBwd{dL, dR, w.bp, w.bg, mask, dcat, M, I, NC},
-                   "trimul.proj_bwd");
+                   BC2N_TN(C, "trimul.proj_bwd"));
   }
   GemmArgs g2;
   g2.M = (int)M; g2.N = C; g2.K = NC;
@@ -718,11 +718,11 @@ void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
     gemm<128, 128>(st, g2,
                    EpiLnBwd<0>(pair_in, w.ln_g, sv.mean, sv.rstd, dout, din, M, 0, nullptr,
                                nullptr, sc + 1),
-                   "trimul.gemm_dx_ln");
+                   BC2N_TN(C, "trimul.gemm_dx_ln"));
     return;
   }
-  gemm<128, 128>(st, g2, EpiStore<float>{dxn, C, 0, nullptr, C}, "trimul.gemm_dx");
-  KTimed kt("trimul.ln_bwd", st);
+  gemm<128, 128>(st, g2, EpiStore<float>{dxn, C, 0, nullptr, C}, BC2N_TN(C, "trimul.gemm_dx"));
+  KTimed kt(BC2N_TN(C, "trimul.ln_bwd"), st);
   ln_bwd_f32(st, dxn, pair_in, M, C, 0, w.ln_g, sv.mean, sv.rstd, din, true, 0, nullptr, nullptr,
              dout, sc + 1);
 }

@@ -518,6 +518,8 @@ int bc2n_stack_keys(void* stream, const uint32_t* seed, int depth, uint32_t* out
  * returns the entry count (-1 on error).
  * ---------------------------------------------------------------------- */
 int bc2n_prof_enable(int on);
+/* Time only the launches named `name` (NULL: every launch). */
+int bc2n_prof_filter(const char* name);
 int bc2n_prof_read(char* names, int name_len, double* ms, int* counts, int cap);
 
 /* ------------------------------------------------------------------------
