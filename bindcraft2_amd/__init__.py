@@ -60,6 +60,12 @@ def _declare(L):
         "bc2n_msaglobal_fwd": (i, [vp, cs, cs, i, i, vp, vp, vp, vp, vp]),
         "bc2n_msaglobal_bwd": (i, [vp, cs, cs, i, i, vp, vp, vp, vp, vp, vp]),
         "bc2n_evoformer_save_bytes": (sz, [cs, i, i, c.c_int64, c.c_int64]),
+        "bc2n_evoformer_detached_bytes": (sz, [cs, i, i, c.c_int64, c.c_int64]),
+        "bc2n_save_slots_probe": (i, [cs, i, i, i, i]),
+        "bc2n_stack_prealloc": (i, [i, i, i, cs, i, i, i]),
+        "bc2n_tplstack_prealloc": (i, [i, i, cs]),
+        "bc2n_sm_prealloc": (i, [i, i, cs]),
+        "bc2n_tplembed_prealloc": (i, [i, i, cs]),
         "bc2n_evoformer_fwd": (i, [vp, vp, vp, vp, vp, vp, i, i, i, i, c.c_int64, c.c_int64,
                                    c.c_int64, c.c_int64, c.c_int64, c.c_int64, cs, vp, vp, vp, vp]),
         "bc2n_evoformer_bwd": (i, [vp, vp, vp, vp, vp, vp, vp, vp, i, i, i, i, c.c_int64,

@@ -10,6 +10,7 @@
 #include "designstep.h"
 #include "confidence.h"
 
+#include <cstdio>
 #include <map>
 #include <tuple>
 
@@ -99,6 +100,8 @@ struct OwnSave {
   }
 };
 OwnSave g_own;
+// Scratch of detached forwards (save = 0): one block's worth, reused.
+OwnSave g_det;
 
 void need(bool ok, const char* msg) {
   if (!ok) throw std::invalid_argument(msg);
@@ -333,6 +336,18 @@ size_t bc2n_evoformer_save_bytes(const char* weights_dir, int N, int S, int64_t 
   return n;
 }
 
+size_t bc2n_evoformer_detached_bytes(const char* weights_dir, int N, int S, int64_t depth,
+                                     int64_t pair_only) {
+  size_t n = 0;
+  if (guarded([&] {
+        need(weights_dir != nullptr, "weights_dir required");
+        const StackW& w = stack_w(weights_dir, (int)depth, evo_kind(pair_only));
+        n = stack_detached_bytes(w, N, S, (int)depth) + 256;
+      }) != 0)
+    return 0;
+  return n;
+}
+
 static const uint32_t* stack_key(hipStream_t st, const uint32_t* seed, int seed_len,
                                  uint32_t* scratch) {
   if (seed_len == 3) return seed;  // [k0, k1, enabled]: jax.random.key_data
@@ -356,13 +371,17 @@ int bc2n_evoformer_fwd(void* stream, const float* pair, const float* msa, const 
     need(pair_out != pair && (pair_only || msa_out != msa), "evoformer: outputs must not alias inputs");
     const StackW& w = stack_w(weights_dir, (int)depth, evo_kind(pair_only));
     if (!pair_only) need(Cm == w.blocks[0].row.a.Cin, "evoformer: msa channel width mismatch");
-    const size_t bytes = stack_save_bytes(w, N, S, (int)depth) + 256;
-    void* sv = (save == 0 || own_save != 0 || psave == nullptr) ? g_own.get(st, bytes) : psave;
+    // save = 0: a detached forward (no backward follows), one block's scratch
+    const bool detached = (save == 0);
+    const size_t bytes = (detached ? stack_detached_bytes(w, N, S, (int)depth)
+                                   : stack_save_bytes(w, N, S, (int)depth)) + 256;
+    void* sv = detached ? g_det.get(st, bytes)
+               : (own_save != 0 || psave == nullptr) ? g_own.get(st, bytes) : psave;
     uint32_t* keyslot = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(sv) + bytes - 256);
     const uint32_t* key = dropout ? stack_key(st, seed, seed_len, keyslot) : nullptr;
     const uint32_t* enabled = dropout ? seed + (seed_len - 1) : nullptr;
     stack_fwd(st, w, N, S, (int)depth, pair, msa, pair_mask, msa_mask, key, enabled, dropout != 0,
-              pair_out, msa_out, sv);
+              pair_out, msa_out, sv, detached);
     if (pair_only && msa && msa_out && msa_out != msa && Cm > 0)
       BC2N_HIP(hipMemcpyAsync(msa_out, msa, (size_t)S * N * Cm * 4, hipMemcpyDeviceToDevice, st));
   });
@@ -390,6 +409,102 @@ int bc2n_evoformer_bwd(void* stream, const float* ct_pair, const float* ct_msa,
     if (pair_only && dmsa && ct_msa && dmsa != ct_msa && Cm > 0)
       BC2N_HIP(hipMemcpyAsync(dmsa, ct_msa, (size_t)S * N * Cm * 4, hipMemcpyDeviceToDevice, st));
   });
+}
+
+// ------------------------------------------------------------ preallocation
+// Called before the first real call (the reference calls its counterparts at
+// trace time, before XLA has allocated): upload the component's weights and
+// grow every scratch arena to what its calls at these shapes need, so that
+// no call allocates afterwards.  The arenas' needs depend on the shapes, not
+// on the depth, so one forward and backward of the first block on zero
+// inputs (on the null stream, synchronised) grows them exactly; detached
+// forwards' scratch is grown to its size as well.  Prints what it took.
+
+namespace {
+
+struct DevBuf {
+  void* p = nullptr;
+  explicit DevBuf(size_t n) {
+    BC2N_HIP(hipMalloc(&p, n < 256 ? 256 : n));
+    BC2N_HIP(hipMemset(p, 0, n < 256 ? 256 : n));
+  }
+  ~DevBuf() { if (p) (void)hipFree(p); }
+  float* f() const { return static_cast<float*>(p); }
+};
+
+size_t free_bytes(size_t* total = nullptr) {
+  size_t f = 0, t = 0;
+  BC2N_HIP(hipMemGetInfo(&f, &t));
+  if (total) *total = t;
+  return f;
+}
+
+void report(const char* what, const std::string& shape, size_t f0) {
+  size_t t = 0;
+  const size_t f1 = free_bytes(&t);
+  fprintf(stderr, "bc2n: prealloc %s %s took %.2f GB (%.2f of %.2f GB free after)\n", what,
+          shape.c_str(), (double)((f0 > f1) ? f0 - f1 : 0) / 1e9, (double)f1 / 1e9,
+          (double)t / 1e9);
+}
+
+void stack_dry_run(const StackW& w, int N, int S) {
+  const long M = (long)N * N;
+  const int Cz = w.blocks[0].tmo.C, Cm = w.pair_only ? 64 : w.blocks[0].row.a.Cin;
+  const size_t sb = stack_save_bytes(w, N, S, 1);
+  DevBuf pair(M * Cz * 4), pair_out(M * Cz * 4), dpair(M * Cz * 4), pmask(M * 4);
+  DevBuf msa((size_t)S * N * Cm * 4), msa_out((size_t)S * N * Cm * 4),
+      dmsa((size_t)S * N * Cm * 4), mmask((size_t)S * N * 4), save(sb);
+  hipStream_t st = nullptr;
+  stack_fwd(st, w, N, S, 1, pair.f(), w.pair_only ? nullptr : msa.f(),
+            pmask.f(), mmask.f(), nullptr, nullptr, false, pair_out.f(),
+            w.pair_only ? nullptr : msa_out.f(), save.p);
+  stack_bwd(st, w, N, S, 1, pmask.f(), mmask.f(), false, save.p,
+            pair_out.f(), w.pair_only ? nullptr : msa_out.f(), dpair.f(),
+            w.pair_only ? nullptr : dmsa.f());
+  BC2N_HIP(hipDeviceSynchronize());
+}
+
+}  // namespace
+
+int bc2n_stack_prealloc(int N, int S, int depth, const char* weights_dir, int pair_only,
+                        int opm_first, int dropout) {
+  (void)dropout;
+  return guarded([&] {
+    need(weights_dir != nullptr, "weights_dir required");
+    need(opm_first == 1, "evoformer: only outer_product_mean.first=True (AF2-multimer) is built");
+    const size_t f0 = free_bytes();
+    const StackW& w = stack_w(weights_dir, depth, evo_kind(pair_only));
+    stack_dry_run(w, N, S);
+    (void)g_det.get(nullptr, stack_detached_bytes(w, N, S, depth) + 256);
+    BC2N_HIP(hipDeviceSynchronize());
+    report("stack", "N=" + std::to_string(N) + " S=" + std::to_string(S) + " depth=" +
+           std::to_string(depth) + " pair_only=" + std::to_string(pair_only), f0);
+  });
+}
+
+int bc2n_tplstack_prealloc(int N, int depth, const char* weights_dir) {
+  return guarded([&] {
+    need(weights_dir != nullptr, "weights_dir required");
+    const size_t f0 = free_bytes();
+    stack_dry_run(stack_w(weights_dir, depth, StackKind::TEMPLATE), N, 1);
+    report("tplstack", "N=" + std::to_string(N) + " depth=" + std::to_string(depth), f0);
+  });
+}
+
+// (the structure-module and template-embedding counterparts follow their
+// weight caches below)
+
+int bc2n_save_slots_probe(const char* weights_dir, int depth, int N, int S, int pair_only) {
+  int slots = -1;
+  if (guarded([&] {
+        need(weights_dir != nullptr, "weights_dir required");
+        const StackW& w = stack_w(weights_dir, depth, evo_kind(pair_only));
+        const size_t bytes = stack_save_bytes(w, N, S, depth) + 256;
+        const size_t slot = (size_t)N * N * 128 * 2;  // one bf16 [N,N,128] slot
+        slots = (int)((bytes + slot - 1) / slot);
+      }) != 0)
+    return -1;
+  return slots;
 }
 
 // ------------------------------------------------------ template pair stack
@@ -447,6 +562,23 @@ const TplEmbedW& te_w(const char* dir, int depth) {
   });
 }
 }  // namespace
+
+int bc2n_tplembed_prealloc(int N, int depth, const char* weights_dir) {
+  return guarded([&] {
+    need(weights_dir != nullptr, "weights_dir required");
+    const size_t f0 = free_bytes();
+    const TplEmbedW& w = te_w(weights_dir, depth);
+    const long M = (long)N * N;
+    DevBuf query(M * 128 * 4), act_const(M * 64 * 4), pmask(M * 4), out(M * 128 * 4),
+        dq(M * 128 * 4), save(tplembed_save_bytes(w, N) + 256);
+    tplembed_fwd(nullptr, w, N, query.f(), act_const.f(), pmask.f(),
+                 nullptr, nullptr, false, out.f(), save.p);
+    tplembed_bwd(nullptr, w, N, query.f(), pmask.f(), false, save.p,
+                 out.f(), dq.f());
+    BC2N_HIP(hipDeviceSynchronize());
+    report("tplembed", "N=" + std::to_string(N) + " depth=" + std::to_string(depth), f0);
+  });
+}
 
 size_t bc2n_tplembed_save_bytes(const char* weights_dir, int N, int64_t depth) {
   size_t n = 0;
@@ -584,6 +716,31 @@ const StructHeadsW& sh_w(const char* dir) {
   return cached(g_sh, dir, "", [&](WeightStore& ws, const std::string&) { return structheads_weights(ws); });
 }
 }  // namespace
+
+int bc2n_sm_prealloc(int N, int depth, const char* weights_dir) {
+  return guarded([&] {
+    need(weights_dir != nullptr, "weights_dir required");
+    need(N > 0 && N <= 512 && depth > 0, "structure heads: bad shape");
+    const size_t f0 = free_bytes();
+    const StructHeadsW& w = sh_w(weights_dir);
+    const long M = (long)N * N;
+    DevBuf single((size_t)N * 384 * 4), pair(M * 128 * 4), seq_mask((size_t)N * 4),
+        aatype((size_t)N * 4), atom14((size_t)N * 14 * 3 * 4), dgram(M * 64 * 4),
+        pae(M * 64 * 4), plddt((size_t)N * 50 * 4), expres((size_t)N * 37 * 4),
+        dsingle((size_t)N * 384 * 4), dpair(M * 128 * 4),
+        save(structheads_save_bytes(N, 1) + 256);
+    structheads_fwd(nullptr, w, N, 1, single.f(), pair.f(), seq_mask.f(),
+                    aatype.f(), nullptr, nullptr, false, atom14.f(),
+                    dgram.f(), pae.f(), plddt.f(), expres.f(),
+                    save.p);
+    structheads_bwd(nullptr, w, N, 1, single.f(), pair.f(), seq_mask.f(),
+                    aatype.f(), false, save.p, atom14.f(), dgram.f(),
+                    pae.f(), plddt.f(), expres.f(), dsingle.f(),
+                    dpair.f());
+    BC2N_HIP(hipDeviceSynchronize());
+    report("structure module", "N=" + std::to_string(N) + " depth=" + std::to_string(depth), f0);
+  });
+}
 
 size_t bc2n_structure_heads_save_bytes(const char* weights_dir, int N, int64_t depth) {
   size_t n = 0;

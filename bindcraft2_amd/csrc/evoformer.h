@@ -36,12 +36,18 @@ StackW stack_weights(WeightStore& ws, int depth, StackKind kind,
 // reads (every block's carries and module save-sets, the dropout tables).
 size_t stack_save_bytes(const StackW& w, int N, int S, int depth);
 
+// Bytes of a detached forward's scratch (detached = true below): one
+// block's module save-sets, two carries of each track, the dropout tables.
+size_t stack_detached_bytes(const StackW& w, int N, int S, int depth);
+
 // Forward of `depth` blocks.  key = stack key (2 x u32, device), enabled =
 // device u32 flag (may be null = on); dropout=false skips every mask.
+// detached: no backward will follow (a recycling or inference pass); `save`
+// is then stack_detached_bytes of scratch, reused block after block.
 void stack_fwd(hipStream_t st, const StackW& w, int N, int S, int depth, const float* pair,
                const float* msa, const float* pmask, const float* mmask, const uint32_t* key,
                const uint32_t* enabled, bool dropout, float* pair_out, float* msa_out,
-               void* save);
+               void* save, bool detached = false);
 // Backward: cotangents of the stack outputs in, of the stack inputs out.
 // Everything else it needs (inputs, carries, dropout tables) is in `save`.
 void stack_bwd(hipStream_t st, const StackW& w, int N, int S, int depth, const float* pmask,

@@ -31,6 +31,9 @@ size_t al256(size_t n) { return (n + 255) & ~size_t(255); }
 struct Layout {
   int N = 0, S = 0, Cz = 0, Cm = 0, depth = 0;
   bool pair_only = false, tpl = false;
+  // a detached forward (no backward follows): one block region reused by
+  // every block and two carry slots used in turn, instead of the save-set
+  bool detached = false;
   size_t opm = 0, row = 0, col = 0, mtr = 0, tmo = 0, tmi = 0, tas = 0, tae = 0, ptr = 0;
   size_t pair_bytes = 0, msa_bytes = 0, block_bytes = 0;
   size_t tbl_per_block = 0;  // floats
@@ -39,9 +42,9 @@ struct Layout {
          off_keys = 0, total = 0;
 };
 
-Layout layout(const StackW& w, int N, int S, int depth) {
+Layout layout(const StackW& w, int N, int S, int depth, bool detached = false) {
   Layout L;
-  L.N = N; L.S = S; L.depth = depth; L.pair_only = w.pair_only;
+  L.N = N; L.S = S; L.depth = depth; L.pair_only = w.pair_only; L.detached = detached;
   L.tpl = (w.kind == StackKind::TEMPLATE);
   const BlockW& b = w.blocks[0];
   L.Cz = b.tmo.C;
@@ -65,14 +68,15 @@ Layout layout(const StackW& w, int N, int S, int depth) {
   L.block_bytes = L.opm + L.row + L.col + L.mtr + L.tmo + L.tmi + L.tas + L.tae + L.ptr +
                   5 * L.pair_bytes + 2 * L.msa_bytes;
   L.tbl_per_block = (size_t)N * L.Cm + 4 * (size_t)N * L.Cz;
-  L.off_carry_p = (size_t)depth * L.block_bytes;
-  L.off_carry_m = L.off_carry_p + (size_t)(depth - 1) * L.pair_bytes;
+  const size_t regions = detached ? 1 : (size_t)depth, carries = detached ? 2 : (size_t)depth - 1;
+  L.off_carry_p = regions * L.block_bytes;
+  L.off_carry_m = L.off_carry_p + carries * L.pair_bytes;
   // the stack's msa input, kept for the backward of block 0
-  L.off_msa_in = L.off_carry_m + (size_t)(depth - 1) * L.msa_bytes;
+  L.off_msa_in = L.off_carry_m + carries * L.msa_bytes;
   // the template iteration's first module reads the block input itself: the
   // stack's pair input is kept for block 0's backward
-  L.off_pair_in = L.off_msa_in + L.msa_bytes;
-  L.off_tbl = L.off_pair_in + (L.tpl ? L.pair_bytes : 0);
+  L.off_pair_in = L.off_msa_in + (detached ? 0 : L.msa_bytes);
+  L.off_tbl = L.off_pair_in + (L.tpl && !detached ? L.pair_bytes : 0);
   L.off_keys = L.off_tbl + al256((size_t)depth * L.tbl_per_block * 4);
   L.total = L.off_keys + al256((size_t)depth * 9 * 2 * 4);
   (void)K_OPM; (void)K_COL; (void)K_MTR; (void)K_PTR; (void)T_PTR;
@@ -130,8 +134,10 @@ struct Frame {
 Frame frame(const Layout& L, char* save, int b, const float* pair, const float* msa,
             float* pair_out, float* msa_out) {
   Frame f;
-  auto cp = [&](int k) { return reinterpret_cast<float*>(save + L.off_carry_p + (size_t)k * L.pair_bytes); };
-  auto cm = [&](int k) { return reinterpret_cast<float*>(save + L.off_carry_m + (size_t)k * L.msa_bytes); };
+  // carry k = output of block k; a detached forward alternates two slots
+  auto slot = [&](int k) { return (size_t)(L.detached ? k % 2 : k); };
+  auto cp = [&](int k) { return reinterpret_cast<float*>(save + L.off_carry_p + slot(k) * L.pair_bytes); };
+  auto cm = [&](int k) { return reinterpret_cast<float*>(save + L.off_carry_m + slot(k) * L.msa_bytes); };
   // pair == nullptr: the backward, which reads block 0's input from the save-set
   f.pin = b == 0 ? (pair ? pair : (L.tpl ? reinterpret_cast<float*>(save + L.off_pair_in) : nullptr))
                  : cp(b - 1);
@@ -247,12 +253,17 @@ size_t stack_save_bytes(const StackW& w, int N, int S, int depth) {
   return layout(w, N, S, depth).total;
 }
 
+size_t stack_detached_bytes(const StackW& w, int N, int S, int depth) {
+  stack_check(w, N, S, depth);
+  return layout(w, N, S, depth, true).total;
+}
+
 void stack_fwd(hipStream_t st, const StackW& w, int N, int S, int depth, const float* pair,
                const float* msa, const float* pmask, const float* mmask, const uint32_t* key,
                const uint32_t* enabled, bool dropout, float* pair_out, float* msa_out,
-               void* save) {
+               void* save, bool detached) {
   stack_check(w, N, S, depth);
-  const Layout L = layout(w, N, S, depth);
+  const Layout L = layout(w, N, S, depth, detached);
   char* sv = reinterpret_cast<char*>(save);
   Tables t;
   t.L = &L;
@@ -271,15 +282,15 @@ void stack_fwd(hipStream_t st, const StackW& w, int N, int S, int depth, const f
                          K_ROW, pk, keys, enabled);
     t.base = tbl;
   }
-  if (!L.pair_only)
+  if (!L.pair_only && !detached)
     BC2N_HIP(hipMemcpyAsync(sv + L.off_msa_in, msa, (size_t)S * N * L.Cm * 4,
                             hipMemcpyDeviceToDevice, st));
-  if (L.tpl)
+  if (L.tpl && !detached)
     BC2N_HIP(hipMemcpyAsync(sv + L.off_pair_in, pair, (size_t)N * N * L.Cz * 4,
                             hipMemcpyDeviceToDevice, st));
   for (int b = 0; b < depth; ++b)
     block_fwd(st, w.blocks[b], L, b, t, frame(L, sv, b, pair, msa, pair_out, msa_out), pmask,
-              mmask, sv + (size_t)b * L.block_bytes);
+              mmask, sv + (detached ? 0 : (size_t)b * L.block_bytes));
 }
 
 void stack_bwd(hipStream_t st, const StackW& w, int N, int S, int depth, const float* pmask,

@@ -250,22 +250,37 @@ class EvoformerStack:
             check(1)
         return b
 
+    def detached_bytes(self, n, s):
+        b = lib().bc2n_evoformer_detached_bytes(self.dir, n, s, self.depth, int(self.pair_only))
+        if b == 0:
+            check(1)
+        return b
+
+    def prealloc(self, n, s, dropout=True):
+        """Upload the weights and grow every scratch buffer the calls at
+        these shapes use (native_stack_prealloc's counterpart)."""
+        check(lib().bc2n_stack_prealloc(n, s, self.depth, self.dir, int(self.pair_only), 1,
+                                        int(dropout)))
+
     def forward(self, pair, msa, pair_mask, msa_mask, seed=None, dropout=True, save=None,
-                pair_out=None, msa_out=None):
+                pair_out=None, msa_out=None, detached=False):
+        """detached=True: the save=0 forward (no backward follows); no
+        save-set is written and None is returned for it."""
         n = pair.shape[0]
         s, _, cm = msa.shape
         if pair_out is None:
             pair_out = torch.empty_like(pair)
         if msa_out is None:
             msa_out = torch.empty_like(msa)
-        if save is None:
+        if save is None and not detached:
             save = torch.empty(self.save_bytes(n, s), dtype=torch.uint8, device=pair.device)
         seed_len = 0 if seed is None else seed.numel()
         check(lib().bc2n_evoformer_fwd(_stream(), _ptr(pair), _ptr(msa), _ptr(pair_mask),
                                        _ptr(msa_mask), _ptr(seed), max(seed_len, 3), n, s, cm,
-                                       self.depth, 1, int(self.pair_only), 0, 1, int(dropout),
-                                       self.dir, _ptr(pair_out), _ptr(msa_out), _ptr(save), None))
-        return pair_out, msa_out, save
+                                       self.depth, 0 if detached else 1, int(self.pair_only), 0,
+                                       1, int(dropout), self.dir, _ptr(pair_out), _ptr(msa_out),
+                                       None if detached else _ptr(save), None))
+        return pair_out, msa_out, (None if detached else save)
 
     def backward(self, ct_pair, ct_msa, pair_mask, msa_mask, save, seed=None, dropout=True):
         n = ct_pair.shape[0]

@@ -168,7 +168,10 @@ int bc2n_msaglobal_bwd(void* stream, const char* weights_dir, const char* prefix
  * Shapes cross as N, S, Cm.  psave is one opaque byte buffer of
  * bc2n_evoformer_save_bytes() (every block's carries and module save-sets:
  * the backward replays nothing); msave is accepted and unused (may be NULL).
- * save=0 or own_save=1 use a library-owned save-set instead.
+ * save=0 is a detached forward (no backward follows: a recycling or
+ * inference pass): psave is not written (may be NULL) and the library uses
+ * bc2n_evoformer_detached_bytes() of its own scratch, one block's worth
+ * reused block after block.  own_save=1 uses a library-owned save-set.
  * seed: seed_len=3 -> [k0, k1, enabled] with (k0,k1) = key_data of the
  * stack's JAX key: dropout masks are bit-identical to jax.random.bernoulli
  * through AF2's key chain.  seed_len=2 -> the reference's [bits, enabled]
@@ -179,6 +182,31 @@ int bc2n_msaglobal_bwd(void* stream, const char* weights_dir, const char* prefix
  * ---------------------------------------------------------------------- */
 size_t bc2n_evoformer_save_bytes(const char* weights_dir, int N, int S,
                                  int64_t depth, int64_t pair_only);
+/* Scratch bytes of a detached (save=0) forward: one block's module
+ * save-sets, two carries of each track and the dropout tables. */
+size_t bc2n_evoformer_detached_bytes(const char* weights_dir, int N, int S,
+                                     int64_t depth, int64_t pair_only);
+/* The number of bf16 [N,N,128] slots that hold the save-set, for a caller
+ * that declares psave in the reference's shape bf16[slots,N,N,128]
+ * (replaces native_save_slots_probe(depth, n), native/ffi.cu:1684-1689,
+ * whose Python twin is _save_slots, bindcraft/af/native.py:1250-1272; the
+ * save-set here also depends on the widths in weights_dir, S and pair_only).
+ * -1 on error. */
+int bc2n_save_slots_probe(const char* weights_dir, int depth, int N, int S,
+                          int pair_only);
+/* Preallocation before the first call (the reference calls these at trace
+ * time, before XLA allocates): upload the weights and grow every scratch
+ * buffer the component's calls at these shapes use (and, for the stack, its
+ * detached-forward scratch), so that no later call at these shapes
+ * allocates.  0 on success; prints what it took to stderr.  Replace
+ * native_stack_prealloc, native_tplstack_prealloc, native_sm_prealloc and
+ * native_tplembed_prealloc (native/ffi.cu:835-937; callers
+ * bindcraft/af/native.py:1279-1407), same signatures. */
+int bc2n_stack_prealloc(int N, int S, int depth, const char* weights_dir, int pair_only,
+                        int opm_first, int dropout);
+int bc2n_tplstack_prealloc(int N, int depth, const char* weights_dir);
+int bc2n_sm_prealloc(int N, int depth, const char* weights_dir);
+int bc2n_tplembed_prealloc(int N, int depth, const char* weights_dir);
 int bc2n_evoformer_fwd(void* stream, const float* pair, const float* msa,
                        const float* pair_mask, const float* msa_mask,
                        const uint32_t* seed, int seed_len, int N, int S, int Cm,
