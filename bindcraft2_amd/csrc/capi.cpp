@@ -18,21 +18,74 @@ using namespace bc2n;
 
 namespace {
 
-template <class F>
-int guarded(F f) {
-  try {
-    f();
-    return 0;
-  } catch (const std::exception& e) {
-    set_error(e.what());
-    return 1;
-  } catch (...) {
-    set_error("unknown error");
-    return 1;
+// The library's scratch (arenas, detached and own save-sets, cotangent
+// scales) is shared by every call on a GPU, so calls on different streams
+// are ordered: each call records an event on its stream after its last
+// launch, and a call arriving on another stream first waits for the
+// previous call's event.  Calls on one stream pay one event record.  Under
+// graph capture nothing is recorded or waited for (a captured graph runs on
+// the capturing stream's order only).
+struct StreamOrder {
+  hipStream_t last = nullptr;
+  hipEvent_t ev = nullptr;
+  bool recorded = false;
+};
+std::mutex g_order_mu;
+std::map<int, StreamOrder> g_order;
+thread_local bool t_call_has_stream = false;
+thread_local hipStream_t t_call_stream = nullptr;
+thread_local int t_call_device = 0;
+
+bool capturing(hipStream_t st) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+
+hipStream_t as_stream(void* s) {
+  hipStream_t st = reinterpret_cast<hipStream_t>(s);
+  if (capturing(st)) return st;
+  int dev = 0;
+  BC2N_HIP(hipGetDevice(&dev));
+  {
+    std::lock_guard<std::mutex> lk(g_order_mu);
+    StreamOrder& o = g_order[dev];
+    if (o.recorded && o.last != st) BC2N_HIP(hipStreamWaitEvent(st, o.ev, 0));
+  }
+  t_call_has_stream = true;
+  t_call_stream = st;
+  t_call_device = dev;
+  return st;
+}
+
+// after a call: mark the end of its work on its stream
+void end_call() {
+  if (!t_call_has_stream) return;
+  t_call_has_stream = false;
+  std::lock_guard<std::mutex> lk(g_order_mu);
+  StreamOrder& o = g_order[t_call_device];
+  if (!o.ev && hipEventCreateWithFlags(&o.ev, hipEventDisableTiming) != hipSuccess) return;
+  if (hipEventRecord(o.ev, t_call_stream) == hipSuccess) {
+    o.last = t_call_stream;
+    o.recorded = true;
   }
 }
 
-hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+template <class F>
+int guarded(F f) {
+  t_call_has_stream = false;
+  int rc = 0;
+  try {
+    f();
+  } catch (const std::exception& e) {
+    set_error(e.what());
+    rc = 1;
+  } catch (...) {
+    set_error("unknown error");
+    rc = 1;
+  }
+  end_call();
+  return rc;
+}
 
 std::mutex g_mu;
 std::map<std::pair<std::string, std::string>, TriAttnW> g_triattn;

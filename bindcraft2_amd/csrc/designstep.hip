@@ -25,13 +25,56 @@ namespace {
 
 constexpr int CM = 256, CZ = 128, CS = 384;
 
+// Every save buffer opens with a 256-byte header that the forward writes:
+// hdr[0] a magic word naming the layout, hdr[1] the optional parts it
+// computed.  The backward refuses a buffer whose parts differ from the ones
+// it is asked to differentiate, instead of reading memory never written.
+constexpr uint32_t DS_MAGIC = 0xBC2D0001u, SEQ_MAGIC = 0xBC2D0002u;
+constexpr uint32_t HAS_TEMPLATE = 1u, HAS_CONFIDENCE = 2u;
+
+__global__ void hdr_set_kernel(uint32_t* h, uint32_t magic, uint32_t flags) {
+  if (threadIdx.x == 0) {
+    h[0] = magic;
+    h[1] = flags;
+  }
+}
+
+void hdr_set(hipStream_t st, uint32_t* h, uint32_t magic, uint32_t flags) {
+  hipLaunchKernelGGL(hdr_set_kernel, dim3(1), dim3(64), 0, st, h, magic, flags);
+}
+
+// The header's flags, after the forward that wrote them has finished (this
+// waits for the stream).  Under graph capture nothing can be read back, so
+// the check is skipped there and -1 returned.
+long hdr_flags(hipStream_t st, const uint32_t* h, uint32_t magic, const char* what) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  BC2N_HIP(hipStreamIsCapturing(st, &cs));
+  if (cs != hipStreamCaptureStatusNone) return -1;
+  uint32_t v[2] = {0, 0};
+  BC2N_HIP(hipMemcpyAsync(v, h, sizeof v, hipMemcpyDeviceToHost, st));
+  BC2N_HIP(hipStreamSynchronize(st));
+  if (v[0] != magic)
+    throw std::invalid_argument(std::string(what) +
+                                ": the save buffer was not written by this step's forward");
+  return v[1];
+}
+
+void hdr_require(long flags, uint32_t bit, bool want, const char* what) {
+  if (flags < 0 || ((flags & bit) != 0) == want) return;
+  throw std::invalid_argument(std::string(what) + (want ? ": the backward asks for " : ": the backward omits ") +
+                              (bit == HAS_TEMPLATE ? "the template embedding" : "the confidence metrics") +
+                              (want ? ", which the forward did not compute" : ", which the forward computed"));
+}
+
 template <class A>
 struct DsSave {
+  uint32_t* hdr;
   void *tpl, *extra, *main, *sh;
   float *pmask, *mmask, *msa0, *pair0, *tplo, *pair1, *pair2, *msa3, *pair3, *single;
   float *dpair, *dq, *dmsa, *dsingle;
   DsSave(A& c, const DesignStepW& w, int N, int S) {
     const size_t M = (size_t)N * N;
+    hdr = c.template take<uint32_t>(64);
     tpl = c.template take<char>(tplembed_save_bytes(w.tpl, N));
     extra = c.template take<char>(stack_save_bytes(w.extra, N, 1, w.d_extra));
     main = c.template take<char>(stack_save_bytes(w.main, N, S, w.d_main));
@@ -99,6 +142,7 @@ void design_step_fwd(hipStream_t st, const DesignStepW& w, int N, int S, const f
   Carver cv(save);
   DsSave<Carver> sv(cv, w, N, S);
   const long M = (long)N * N;
+  hdr_set(st, sv.hdr, DS_MAGIC, act_const ? HAS_TEMPLATE : 0u);
   {
     const long n = std::max(M, (long)S * N);
     hipLaunchKernelGGL(masks_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, seq_mask,
@@ -135,10 +179,12 @@ void design_step_bwd(hipStream_t st, const DesignStepW& w, int N, int S, const f
   Carver cv(save);
   DsSave<Carver> sv(cv, w, N, S);
   const long M = (long)N * N;
+  hdr_require(hdr_flags(st, sv.hdr, DS_MAGIC, "design step"), HAS_TEMPLATE, with_template,
+              "design step");
   structheads_bwd(st, w.sh, N, w.d_fold, sv.single, sv.pair3, seq_mask, aatype, dropout, sv.sh,
                   datom, ddgram, dpae, dplddt, dexpres, sv.dsingle, sv.dpair);
   // d msa3: row 0 from the single projection, the other rows zero
-  BC2N_HIP(hipMemsetAsync(sv.dmsa, 0, (size_t)S * N * CM * 4, st));
+  zero_f32(st, sv.dmsa, (long)S * N * CM);
   GemmF32 g = gemm_rows(N, CM, CS, sv.dsingle, w.wsa, sv.dmsa, true);
   gemm_f32(st, g, "design.gemm_single_dx");
   // the stacks accumulate in place: d pair3 -> d pair2 -> d pair1, d msa3 -> d msa0
@@ -159,8 +205,10 @@ namespace {
 // The sequence front's buffers, carved ahead of the step's own save-set.
 template <class A>
 struct SeqExtra {
+  uint32_t* hdr;
   float *feat, *prof, *tf, *mf, *aatype, *dtf, *dmf, *dfeat, *dprof;
   SeqExtra(A& c, int N) {
+    hdr = c.template take<uint32_t>(64);
     feat = c.template take<float>((size_t)N * SEQ_A);
     prof = c.template take<float>((size_t)N * SEQ_A);
     tf = c.template take<float>((size_t)N * (SEQ_A + 1));
@@ -213,6 +261,7 @@ void design_step_seq_fwd(hipStream_t st, const DesignStepW& w, int N, const floa
   nonnull(sc4, "design step scalars"); nonnull(save, "design step save");
   Carver cv(save);
   SeqExtra<Carver> x(cv, N);
+  hdr_set(st, x.hdr, SEQ_MAGIC, conf.plddt ? HAS_CONFIDENCE : 0u);
   seqfeat_fwd(st, logits, flags, bias, SeqScalars{}, sc4, omitted_half, N, x.feat, x.prof);
   design_inputs_fwd(st, x.feat, x.prof, N, x.tf, x.mf, x.aatype);
   design_step_fwd(st, w, N, 1, x.tf, x.mf, ri, ai, ei, si, offset, seq_mask, act_const, x.aatype,
@@ -240,6 +289,9 @@ void design_step_seq_bwd(hipStream_t st, const DesignStepW& w, int N, const floa
   nonnull(d_logits, "design step d_logits");
   Carver cv(save);
   SeqExtra<Carver> x(cv, N);
+  // confidence cotangents need the forward's metrics; leaving them out is allowed
+  const long seq_flags = hdr_flags(st, x.hdr, SEQ_MAGIC, "design step");
+  if (conf.any()) hdr_require(seq_flags, HAS_CONFIDENCE, true, "design step");
   if (conf.any()) {
     // the confidence metrics' backward over the logits the forward kept (confidence requested there)
     nonnull(conf.asym, "design step interface asym");

@@ -95,6 +95,20 @@ void ct_scale(hipStream_t st, const float* x, long n, float* sc) {
   hipLaunchKernelGGL(amax_final_kernel, dim3(1), dim3(64), 0, st, p.part, blocks, sc);
 }
 
+// ----------------------------------------------------------------- zero fill
+// A kernel, not hipMemsetAsync: memset nodes in a captured HIP graph have
+// given wrong results on replays after the first.
+__global__ void zero_f32_kernel(float* __restrict__ p, long n) {
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x)
+    p[i] = 0.f;
+}
+
+void zero_f32(hipStream_t st, float* p, long n) {
+  if (n <= 0) return;
+  const long blocks = std::min<long>((n + 255) / 256, 4096);
+  hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)blocks), dim3(256), 0, st, p, n);
+}
+
 // -------------------------------------------------------------- dropout
 // tbl[b*C+c] = keep ? 1/keep_rate : 0 where keep = uniform(key, (B,C)) < keep_rate
 // and the key (k0,k1) / enable flag are read on the device.

@@ -413,12 +413,12 @@ void structheads_bwd(hipStream_t st, const StructHeadsW& w, int N, int depth, co
       gemm_f32(st, g0, "heads.gemm_plddt0_dx");
       ln_f32_rows_bwd(st, dy, sv.act, N, CS, w.hd.ln_g, sv.lmean, sv.lrstd, sv.d_act);
     } else {
-      BC2N_HIP(hipMemsetAsync(sv.d_act, 0, (size_t)N * CS * 4, st));
+      zero_f32(st, sv.d_act, (long)N * CS);
     }
     // sidechain -> d act, d initial act, d traj[-1]
     if (datom) {
       KTimed kt("sidechain.bwd", st);
-      BC2N_HIP(hipMemsetAsync(sv.d_traj, 0, (size_t)(depth - 1) * N * 12 * 4, st));
+      zero_f32(st, sv.d_traj, (long)(depth - 1) * N * 12);
       const float* trj = sv.traj + (size_t)(depth - 1) * N * 12;
       hipLaunchKernelGGL(side_atoms_bwd_kernel, dim3((N + 63) / 64), dim3(64), 0, st, sv.un, trj,
                          aatype, w.tab, N, datom, dun, sv.d_traj + (size_t)(depth - 1) * N * 12);

@@ -848,11 +848,11 @@ void fold_bwd(hipStream_t st, const FoldW& w, int N, int depth, const float* sin
   float* drB = ar.take_n<float>((size_t)N * 12);
   float* dflat = ar.take_n<float>((size_t)N * 6);
   // d LN(pair) accumulates in dpair, then the LN backward runs in place
-  BC2N_HIP(hipMemsetAsync(dpair, 0, (size_t)M2 * CZ * 4, st));
-  BC2N_HIP(hipMemsetAsync(db2d, 0, (size_t)H * M2 * 4, st));
+  zero_f32(st, dpair, (long)M2 * CZ);
+  zero_f32(st, db2d, (long)H * M2);
   if (d_act) BC2N_HIP(hipMemcpyAsync(da, d_act, (size_t)N * CS * 4, hipMemcpyDeviceToDevice, st));
-  else BC2N_HIP(hipMemsetAsync(da, 0, (size_t)N * CS * 4, st));
-  BC2N_HIP(hipMemsetAsync(drA, 0, (size_t)N * 12 * 4, st));  // d rigid' of the last iteration
+  else zero_f32(st, da, (long)N * CS);
+  zero_f32(st, drA, (long)N * 12);  // d rigid' of the last iteration
 
   for (int it = depth - 1; it >= 0; --it) {
     FoldIterSave<Carver> s = iter_save(const_cast<void*>(save), N, depth, it);

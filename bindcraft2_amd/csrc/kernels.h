@@ -86,6 +86,9 @@ void ln_f32_rows_bwd(hipStream_t st, const float* dy, const float* x, long M, in
 bool trimul_contract(hipStream_t st, int N, int channels, const h16* A, bool a_kcontig,
                      const h16* B, bool b_kcontig, float* Cf, h16* Cb);
 
+// p[0..n) = 0 by a kernel (graph-capture safe, unlike hipMemsetAsync).
+void zero_f32(hipStream_t st, float* p, long n);
+
 // ------------------------------------------------------- cotangent scales
 // The backward rounds cotangents to binary16 after multiplying them by a
 // power-of-two scale s and divides s out in the f32 epilogue that ends the

@@ -153,3 +153,58 @@ def test_design_step_seq_parity(cuda, with_template, dropout):
             assert m["rel_l2"] <= 2e-2 and m["max_rel"] <= 2e-2 and m["cos"] >= 0.9999, name
         else:
             assert m["cos"] >= 0.999 and m["rel_l2"] <= 5e-2, name
+
+
+def test_design_step_save_flags(cuda):
+    """The backward refuses a save buffer whose optional parts (template
+    embedding, confidence metrics) differ from the ones it is asked to
+    differentiate, and one no forward wrote."""
+    from bindcraft2_amd import NativeError
+    n = 32
+    print(f"design step save-buffer flags n={n}", flush=True)
+    depths = {"tpl": 1, "extra": 1, "main": 1, "fold": 1}
+    rng = np.random.default_rng(9200)
+    prm = {"emb": bparams.init_embedder_params(rng),
+           "tpl": bparams.init_template_embedding_params(depths["tpl"], rng),
+           "extra": _extra_params(depths["extra"], rng),
+           "main": bparams.init_block_params(0, rng),
+           "post": bparams.init_structure_heads_params(rng)}
+    prm["post"].update({f"const/{k}": v for k, v in bparams.init_residue_tables(rng).items()})
+    dirs = [weights_dir(prm[k], f"dsf_{k}") for k in ("emb", "tpl", "extra", "main", "post")]
+    T = lambda a: None if a is None else torch.as_tensor(a, device=cuda)
+    x, flags, _ = _inputs(n, rng, False)
+    ids = [np.arange(n, dtype=np.float32), np.repeat([1, 2], n // 2).astype(np.float32),
+           np.repeat([1, 2], n // 2).astype(np.float32), np.ones(n, np.float32)]
+    seq_mask = np.ones(n, np.float32)
+    sc = torch.tensor((1.0, 0.0, 1.0, 1.0), dtype=torch.float32, device=cuda)
+    step = ops.DesignStepSeq(*dirs, depths=tuple(depths[k] for k in ("tpl", "extra", "main", "fold")))
+    shapes = ((n, 14, 3), (n, n, 64), (n, n, 64), (n, 50), (n, 37))
+    cts = [T(rng.standard_normal(sh).astype(np.float32)) for sh in shapes]
+    conf_cts = [T(np.ones(n, np.float32))] + [None] * 5
+    iasym = T(ids[1].astype(np.int32))
+    args = (T(x), T(flags), sc, T(seq_mask))
+
+    # forward with neither template nor confidence
+    _, save = step.forward(T(x), T(flags), sc, [T(v) for v in ids], T(seq_mask), dropout=False)
+    with pytest.raises(NativeError, match="template embedding, which the forward did not"):
+        step.backward(cts, *args, save, with_template=True, dropout=False)
+    with pytest.raises(NativeError, match="confidence metrics, which the forward did not"):
+        step.backward(cts, *args, save, with_template=False, dropout=False,
+                      interface_asym=iasym, conf_cts=conf_cts)
+    d_ok = step.backward(cts, *args, save, with_template=False, dropout=False)
+
+    # forward with both: leaving the template out of the backward is refused,
+    # leaving the confidence cotangents out is allowed
+    act_const = T((0.5 * rng.standard_normal((n, n, 64))).astype(np.float32))
+    _, save2, _ = step.forward(T(x), T(flags), sc, [T(v) for v in ids], T(seq_mask),
+                               act_const=act_const, dropout=False, interface_asym=iasym)
+    with pytest.raises(NativeError, match="omits the template embedding"):
+        step.backward(cts, *args, save2, with_template=False, dropout=False)
+    d2 = step.backward(cts, *args, save2, with_template=True, dropout=False)
+
+    # a buffer no forward wrote
+    blank = torch.zeros_like(save)
+    with pytest.raises(NativeError, match="not written by this step's forward"):
+        step.backward(cts, *args, blank, with_template=False, dropout=False)
+    torch.cuda.synchronize()
+    assert torch.isfinite(d_ok).all() and torch.isfinite(d2).all()
