@@ -47,6 +47,14 @@ namespace bc2n {
 
 constexpr float NEG_LOGIT = -8192.0f;
 
+// Row stride (in h16) of the LDS token x head-width tiles.  gfx950's LDS
+// serves a wave's 8-byte transposed read in two 32-lane halves of 256 bytes
+// and a 16-byte row read in four; with D = 32 a 96-byte stride puts every
+// half-wave's rows on distinct banks for both patterns (80 bytes costs two
+// cycles of conflicts per read, measured with SQ_LDS_BANK_CONFLICT).
+template <int D>
+__host__ __device__ constexpr int lds_ld() { return D == 32 ? 48 : D + 8; }
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -77,7 +85,7 @@ __device__ __forceinline__ h16x8 ld_tr8(const h16* T, int ld, int r0, int c0, in
 }
 
 // Row-major copies of the first `rows` (<= N) rows of two head slices (row
-// strides lda, ldb) into LDS tiles [N][D + 8], by 256 threads: every 16-byte
+// strides lda, ldb) into LDS tiles [N][lds_ld<D>()], by 256 threads: every 16-byte
 // load is issued before the first store, so one memory latency covers the
 // whole tile.  The loads and the LDS stores are separate steps, so a kernel
 // walking several rows can hold the next row's tiles in registers while it
@@ -105,8 +113,8 @@ struct RowPair {
     for (int i = 0; i < IT; ++i) {
       const int c = tid + 256 * i;
       if (c < items) {
-        st8(&dA[(c / CPR) * (D + 8) + (c % CPR) * 8], va[i]);
-        st8(&dB[(c / CPR) * (D + 8) + (c % CPR) * 8], vb[i]);
+        st8(&dA[(c / CPR) * lds_ld<D>() + (c % CPR) * 8], va[i]);
+        st8(&dB[(c / CPR) * lds_ld<D>() + (c % CPR) * 8], vb[i]);
       }
     }
   }
@@ -156,7 +164,7 @@ template <int D, int NKB>
 __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   constexpr int DT = D / 16;
-  constexpr int LD = D + 8;
+  constexpr int LD = lds_ld<D>();
   constexpr int N = 32 * NKB;  // == a.N (dispatch)
   constexpr int CB = NKB < 8 ? NKB : 8;  // key blocks per chunk
   constexpr int NCH = (NKB + CB - 1) / CB;
@@ -312,7 +320,7 @@ template <int D, int NKB>
 __global__ __launch_bounds__(256) void attn_fwd_rows_kernel(AttnArgs a, int rpc) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   constexpr int DT = D / 16;
-  constexpr int LD = D + 8;
+  constexpr int LD = lds_ld<D>();
   constexpr int N = 32 * NKB;  // == a.N (dispatch)
   static_assert(NKB <= 8, "one key chunk");
   constexpr int QR = 64;       // query rows of the workgroup
@@ -476,7 +484,7 @@ __global__ __launch_bounds__(256) void attn_fwd_rows_kernel(AttnArgs a, int rpc)
 }
 
 // ------------------------------------------------------- backward: gate + D
-// dO = dog * sigmoid(g); dG = dog * o * s(1-s); Dsum = sum_d dO * o.
+// dO = dog * sigmoid(g); dG = dog * o * s(1-s); nDsum = -sum_d dO * o.
 // D/8 lanes per (token, head), 8 channels each.
 template <int D>
 __global__ __launch_bounds__(256) void attn_gate_bwd_kernel(AttnBwdArgs b) {
@@ -509,7 +517,7 @@ __global__ __launch_bounds__(256) void attn_gate_bwd_kernel(AttnBwdArgs b) {
   s = group_sum<LPH>(s);
   if (part == 0) {
     const long r = tok / a.N, q = tok % a.N;
-    b.Dsum[(r * a.H + h) * a.N + q] = s;
+    b.nDsum[(r * a.H + h) * a.N + q] = -s;
   }
 }
 
@@ -522,7 +530,7 @@ template <int D, int NKB>
 __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs b) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   constexpr int DT = D / 16;
-  constexpr int LD = D + 8;
+  constexpr int LD = lds_ld<D>();
   const AttnArgs& a = b.f;
   constexpr int N = 32 * NKB;  // == a.N (dispatch)
   constexpr int CB = NKB < 8 ? NKB : 8;  // key blocks per chunk
@@ -557,10 +565,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs b) {
   qf.load(a.qkvg + (tok0 + q) * a.ld + h * D, g);
   dof.load(b.dO + (tok0 + q) * a.ldo + h * D, g);
   const float lse = a.lse[((long)r * H + h) * N + q];
-  const float Dq = b.Dsum[((long)r * H + h) * N + q];
+  const float nDq = b.nDsum[((long)r * H + h) * N + q];
   const float* brow = a.bias ? a.bias + ((long)h * N + q) * N : nullptr;
   const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
-  const f32x4 nD = {-Dq, -Dq, -Dq, -Dq};
+  const f32x4 nD = {nDq, nDq, nDq, nDq};
   f32x4 acc[DT];
 #pragma unroll
   for (int i = 0; i < DT; ++i) acc[i] = z4;
@@ -646,7 +654,7 @@ template <int D, int NKB>
 __global__ __launch_bounds__(256) void attn_bwd_dq_rows_kernel(AttnBwdArgs b, int rpc) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   constexpr int DT = D / 16;
-  constexpr int LD = D + 8;
+  constexpr int LD = lds_ld<D>();
   const AttnArgs& a = b.f;
   constexpr int N = 32 * NKB;  // == a.N (dispatch)
   static_assert(NKB <= 8, "one key chunk");
@@ -658,7 +666,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_rows_kernel(AttnBwdArgs b, in
   h16* Os = Qs + QR * LD;                              // [QR][LD] dO
   float* Ms = reinterpret_cast<float*>(Os + QR * LD);   // [N] 0 / -inf per key
   float* Ls = Ms + N;                                   // [QR] lse
-  float* Dl = Ls + QR;                                  // [QR] Dsum
+  float* Dl = Ls + QR;                                  // [QR] -Dsum
 
   const int nqb = (N + QR - 1) / QR;
   const int nch = (a.R + rpc - 1) / rpc;
@@ -715,7 +723,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_rows_kernel(AttnBwdArgs b, in
     if (tid < N) nm = a.mask[r * a.mask_sr + tid * a.mask_sk];
     if (tid < QR) {
       nl = a.lse[((long)r * H + h) * N + stok];
-      nd = b.Dsum[((long)r * H + h) * N + stok];
+      nd = b.nDsum[((long)r * H + h) * N + stok];
     }
   };
 
@@ -742,8 +750,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_rows_kernel(AttnBwdArgs b, in
     HFrag<D> qf, dof;
     qf.load(&Qs[ql * LD], g);
     dof.load(&Os[ql * LD], g);
-    const float lse = Ls[ql], Dq = Dl[ql];
-    const f32x4 nD = {-Dq, -Dq, -Dq, -Dq};
+    const float lse = Ls[ql], nDq = Dl[ql];
+    const f32x4 nD = {nDq, nDq, nDq, nDq};
     f32x4 acc[DT];
 #pragma unroll
     for (int i = 0; i < DT; ++i) acc[i] = z4;
@@ -803,7 +811,7 @@ template <int D, int NQB>
 __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   constexpr int DT = D / 16;
-  constexpr int LD = D + 8;
+  constexpr int LD = lds_ld<D>();
   constexpr int N = 32 * NQB;            // == a.N (dispatch)
   constexpr int QS = NQB > 8 ? 4 : 2;    // query groups per key tile
   constexpr int KT = 4 / QS;             // 16-key tiles per workgroup
@@ -889,7 +897,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
         nmask[i] = 0.f;
         if (qq < N) {
           nls[i] = a.lse[((long)r * H + h) * N + qq];
-          nds[i] = b.Dsum[((long)r * H + h) * N + qq];
+          nds[i] = b.nDsum[((long)r * H + h) * N + qq];
           nmask[i] = a.mask[r * a.mask_sr + qq * a.mask_sk];
         }
       }
@@ -918,7 +926,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
         const int qq = tid + 256 * i;
         if (qq < N) {
           Ls[qq] = -nls[i];
-          Ds[qq] = -nds[i];
+          Ds[qq] = nds[i];
           Ms[qq] = nmask[i];
         }
         non |= nmask[i] != 0.f;
@@ -1035,6 +1043,349 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
   }
 }
 
+// Direct global -> LDS copies (gfx950 global_load_lds_dword / _dwordx4): lane
+// i writes its 4 (16) bytes at LDS byte m0 + 4 i (16 i).  Issued as inline
+// asm, so the compiler neither counts them nor makes every later LDS read
+// wait for them; the kernels that use them retire them with explicit
+// vmcnt waits before the barrier that publishes the data.
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+  return (unsigned)(size_t)((const __attribute__((address_space(3))) unsigned char*)p);
+}
+__device__ __forceinline__ void dma16(const void* src, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void* src, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds)
+               : "memory", "m0");
+}
+// The same with a uniform 64-bit base (SGPRs) and a per-lane 32-bit byte
+// offset: the per-row address update is scalar.
+__device__ __forceinline__ void dma16s(unsigned voff, const void* sbase, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma4s(unsigned voff, const void* sbase, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
+               : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 16, "vmcnt");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+}
+
+// dK/dV/dBias for D = 32 and N <= 256, the same work split and arithmetic
+// as attn_bwd_dkv_kernel, with the row staging rebuilt around the direct
+// copies:
+//
+//  * LDS holds two row buffers.  Each is Q, dO (the row's N tokens) and K, V
+//    (the workgroup's 32 keys) as h16 tiles of 64-byte rows, the 16-byte
+//    chunk c of tile row t stored at chunk c ^ ((t >> 1) & 3) -- conflict-free
+//    for both the row reads (b128) and the transposed reads
+//    (ds_read_b64_tr_b16) -- then the row's lse, -Dsum and key mask.  While
+//    row s computes from one buffer, the copies of row s+1 fill the other;
+//    their addresses are a per-lane offset fixed for the kernel plus a
+//    scalar row base.
+//  * Nothing else in the row loop reads global memory, and each wave issues
+//    the same copies and stores every row (the last row's prefetch re-reads
+//    that row), so the wait that opens a row retires exactly its copies and
+//    leaves the previous row's dK/dV stores in flight.
+//  * The two query groups split the 32-query blocks evenly: with an odd
+//    count, each takes one 16-query half of the last block.
+//  * Two barriers per row: one after the copies land, one to add the query
+//    groups' dK/dV partials.
+template <int NQB>
+__global__ __launch_bounds__(256, 2) void attn_bwd_dkv_lds_kernel(AttnBwdArgs b) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
+  constexpr int D = 32, DT = 2;
+  constexpr int N = 32 * NQB;            // == a.N (dispatch)
+  static_assert(NQB <= 8, "one query chunk");
+  constexpr int QS = 2, KT = 2;          // query groups x 16-key tiles per workgroup
+  constexpr int FULL = NQB / QS;         // whole blocks per query group
+  constexpr bool HALF = NQB % QS != 0;   // plus half of the last block
+  constexpr int NB = FULL + (HALF ? 1 : 0);
+  constexpr int TILE = N * 64;           // bytes of one [N][32] h16 tile
+  constexpr int KVT = 16 * KT * 64;      // bytes of the K (or V) tile
+  constexpr int SOFF = 2 * TILE + 2 * KVT;
+  constexpr int BUF = SOFF + 3 * N * 4;
+  constexpr int JT = N / 16;             // 1 KB copies per Q (dO) tile
+  constexpr int NCP = NQB + 1;           // tile copies per wave: (2 JT + 2 KT) / 4
+  constexpr int JS = (N + 63) / 64;      // 256-byte copies per statistic
+  constexpr int NSC = (3 * JS + 3) / 4;  // statistic copies per wave (at most)
+  const AttnArgs& a = b.f;
+  const int H = a.H;
+  float* Xs = reinterpret_cast<float*>(smem_raw + 2 * BUF);  // [KT][K,V][DT*4][64], query group 1
+
+  constexpr int NKW = N / (16 * KT);
+  const long G = (long)((a.R + b.rows_per_chunk - 1) / b.rows_per_chunk) * H * NKW;
+  const int bid = (int)xcd_block(G);
+  if (bid >= G) return;
+  const int kw = bid % NKW;
+  const int h = (bid / NKW) % H;
+  const int ch = bid / (NKW * H);
+  const int r0 = ch * b.rows_per_chunk;
+  const int r1 = min(a.R, r0 + b.rows_per_chunk);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kt_ = wave % KT, qs = wave / KT;
+  const int lk = lane & 15, g = lane >> 4;
+  const int klocal = kt_ * 16 + lk;
+  const int k = kw * 16 * KT + klocal;
+  const long HD = (long)H * D;
+  const unsigned lds0 = lds_addr(smem_raw);
+
+  // blocks of this wave: 32-query block ib * QS + qs for ib < FULL, and
+  // queries [16 qs, 16 qs + 16) of block NQB - 1 when HALF
+  auto blk_q0 = [&](int ib) { return ib < FULL ? (ib * QS + qs) * 32 : (NQB - 1) * 32; };
+  float bsl[NB][8], dbias[NB][8];
+  const float* bcol = a.bias + (long)h * N * N + k;
+#pragma unroll
+  for (int ib = 0; ib < NB; ++ib) {
+    const int qb = blk_q0(ib);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      bsl[ib][e] = bcol[(long)(qb + (e / 4) * 16 + 4 * g + (e % 4)) * N];
+      dbias[ib][e] = 0.f;
+    }
+  }
+
+  // Tile copy j (1 KB) fills rows 16 j'..16 j'+15 of one tile: lane i writes
+  // physical chunk i & 3 of row 16 j' + i / 4, read from the logical chunk
+  // the swizzle puts there.  Wave w issues tile copies w + 4 i (Q: j < JT,
+  // dO: j < 2 JT, then K, V) and statistic copies w + 4 i (lse, -Dsum, mask).
+  unsigned voff[NCP], sdst[NCP];
+  long soff[NCP];
+  bool sdo[NCP];
+#pragma unroll
+  for (int i = 0; i < NCP; ++i) {
+    const int j = wave + 4 * i;
+    const int tile = j < 2 * JT ? j / JT : 2 + (j - 2 * JT) / KT;  // Q, dO, K, V
+    const int jr = j < 2 * JT ? j % JT : (j - 2 * JT) % KT;
+    const int row = jr * 16 + (lane >> 2);
+    const int c = (lane & 3) ^ ((row >> 1) & 3);
+    sdo[i] = tile == 1;
+    const long ld = tile == 1 ? a.ldo : a.ld;
+    voff[i] = (unsigned)((row * ld + c * 8) * 2);
+    soff[i] = tile == 0 || tile == 1 ? (long)h * D * 2
+                                     : ((long)kw * 16 * KT * a.ld + (tile - 1) * HD + h * D) * 2;
+    sdst[i] = (tile < 2 ? tile * TILE : 2 * TILE + (tile - 2) * KVT) + jr * 1024;
+  }
+  unsigned svoff[NSC], ssdst[NSC];
+  int swhich[NSC];
+  bool son[NSC], slive[NSC];
+#pragma unroll
+  for (int i = 0; i < NSC; ++i) {
+    const int j = wave + 4 * i;
+    son[i] = j < 3 * JS;
+    const int which = son[i] ? j / JS : 0, js = son[i] ? j % JS : 0;
+    const int q = js * 64 + lane;
+    swhich[i] = which;
+    slive[i] = q < N;
+    svoff[i] = which == 2 ? (unsigned)(q * a.mask_sk * 4) : (unsigned)(q * 4);
+    ssdst[i] = SOFF + which * N * 4 + js * 256;
+  }
+  auto copy_row = [&](int r, int u) __attribute__((always_inline)) {
+    const unsigned base = lds0 + u * BUF;
+    const char* qrow = reinterpret_cast<const char*>(a.qkvg + (long)r * N * a.ld);
+    const char* orow = reinterpret_cast<const char*>(b.dO + (long)r * N * a.ldo);
+#pragma unroll
+    for (int i = 0; i < NCP; ++i) dma16s(voff[i], (sdo[i] ? orow : qrow) + soff[i], base + sdst[i]);
+    const long srow = ((long)r * H + h) * N;
+#pragma unroll
+    for (int i = 0; i < NSC; ++i) {
+      if (son[i]) {
+        const float* sb = swhich[i] == 0 ? a.lse + srow
+                        : swhich[i] == 1 ? b.nDsum + srow
+                                         : a.mask + (long)r * a.mask_sr;
+        if (slive[i]) dma4s(svoff[i], sb, base + ssdst[i]);
+      }
+    }
+  };
+
+  // lane-constant swizzled offsets (h16 units): row reads at rows ≡ lk
+  // (mod 16), transposed reads at rows 4g + lk/4 (mod 16)
+  const int rsw = ((g ^ ((lk >> 1) & 3)) << 3);
+  const int trow = 4 * g + (lk >> 2);
+  const int tsw0 = (((lk & 3) >> 1) ^ ((trow >> 1) & 3)) * 8 + 4 * (lk & 1);       // columns 0..15
+  const int tsw1 = ((2 + ((lk & 3) >> 1)) ^ ((trow >> 1) & 3)) * 8 + 4 * (lk & 1);  // columns 16..31
+  auto tr4 = [&](const h16* T, int r0_, int dh) __attribute__((always_inline)) -> h16x4 {
+    const h16* p = T + (r0_ + trow) * 32 + (dh ? tsw1 : tsw0);
+    return __builtin_bit_cast(h16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p));
+  };
+  auto tr8 = [&](const h16* T, int r0_, int dh) __attribute__((always_inline)) -> h16x8 {
+    const h16x4 x = tr4(T, r0_, dh), y = tr4(T, r0_ + 16, dh);
+    h16x8 v;
+    v[0] = x[0]; v[1] = x[1]; v[2] = x[2]; v[3] = x[3];
+    v[4] = y[0]; v[5] = y[1]; v[6] = y[2]; v[7] = y[3];
+    return v;
+  };
+
+  const int nst = r1 - r0;
+  copy_row(r0, 0);
+  wait_vm<0>();  // the bias tile and row r0's copies
+  const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < nst; ++s) {
+    const int r = r0 + s, u = s & 1;
+    // this row's copies are in; query group 0's four dK/dV stores of the
+    // previous row may still be in flight
+    if (qs == 0) wait_vm<4>();
+    else wait_vm<0>();
+    __syncthreads();
+    copy_row(min(r + 1, r1 - 1), u ^ 1);  // the last row reloads itself: same count every row
+    const unsigned char* cur = smem_raw + u * BUF;
+    const h16* Qs = reinterpret_cast<const h16*>(cur);
+    const h16* Os = reinterpret_cast<const h16*>(cur + TILE);
+    const h16* Ks = reinterpret_cast<const h16*>(cur + 2 * TILE);
+    const h16* Vs = reinterpret_cast<const h16*>(cur + 2 * TILE + KVT);
+    const float* Ls = reinterpret_cast<const float*>(cur + SOFF);  // lse
+    const float* Ds = Ls + N;                                      // -Dsum
+    const float* Ms = Ds + N;                                      // key mask
+    HFrag<D> kf, vf;
+    kf.v = ld8(Ks + klocal * 32 + rsw);
+    vf.v = ld8(Vs + klocal * 32 + rsw);
+    const bool mk = Ms[k] != 0.f;
+    bool any = false;
+#pragma unroll
+    for (int i = 0; i < JS; ++i)
+      if (i * 64 + lane < N) any |= Ms[i * 64 + lane] != 0.f;
+    // the row has an unmasked key; every key of this wave is unmasked
+    const bool live = __builtin_amdgcn_ballot_w64(any) != 0;
+    const bool allk = __builtin_amdgcn_ballot_w64(!mk) == 0;
+    f32x4 accK[DT], accV[DT];
+#pragma unroll
+    for (int i = 0; i < DT; ++i) { accK[i] = z4; accV[i] = z4; }
+
+    // One unit = this wave's 16 keys against 32 queries (block ib, or the
+    // 16-query half qs of the last block).  Its LDS operands are read in one
+    // batch, and the next unit's batch is issued right after this unit's
+    // S / dP products, so the reads are in flight during the exponentials.
+    struct Ops {
+      h16x8 q[2], o[2];
+      float4 l[2], d[2];
+    };
+    auto load_ops = [&](int ib, Ops& x) __attribute__((always_inline)) {
+      const int qb = blk_q0(ib);
+#pragma unroll
+      for (int qh = 0; qh < 2; ++qh) {
+        x.q[qh] = ld8(Qs + (qb + qh * 16 + lk) * 32 + rsw);
+        x.o[qh] = ld8(Os + (qb + qh * 16 + lk) * 32 + rsw);
+        x.l[qh] = *reinterpret_cast<const float4*>(Ls + qb + qh * 16 + 4 * g);
+        x.d[qh] = *reinterpret_cast<const float4*>(Ds + qb + qh * 16 + 4 * g);
+      }
+    };
+    // MODE 0: every key of the wave unmasked (no selects); 1: a masked key
+    // gets exponent -inf; 2: fully masked row (p = 1/N, dS = 0)
+    auto row_units = [&](auto mode_c) __attribute__((always_inline)) {
+      constexpr int MODE = decltype(mode_c)::value;
+      Ops cur, nxt;
+      load_ops(0, cur);
+#pragma unroll
+      for (int ib = 0; ib < NB; ++ib) {
+        const bool half = HALF && ib == FULL;
+        const int qb = blk_q0(ib);
+        f32x4 s4[2], dp[2];
+#pragma unroll
+        for (int qh = 0; qh < 2; ++qh) {
+          f32x4 cs, cd;
+          cs[0] = bsl[ib][qh * 4 + 0] - cur.l[qh].x;
+          cs[1] = bsl[ib][qh * 4 + 1] - cur.l[qh].y;
+          cs[2] = bsl[ib][qh * 4 + 2] - cur.l[qh].z;
+          cs[3] = bsl[ib][qh * 4 + 3] - cur.l[qh].w;
+          cd[0] = cur.d[qh].x; cd[1] = cur.d[qh].y; cd[2] = cur.d[qh].z; cd[3] = cur.d[qh].w;
+          HFrag<D> qa, da;
+          qa.v = cur.q[qh];
+          da.v = cur.o[qh];
+          if constexpr (MODE != 2) {
+            s4[qh] = HFrag<D>::mma(qa, kf, cs);  // S + bias - lse
+            dp[qh] = HFrag<D>::mma(da, vf, cd);  // dP - Dsum
+          }
+        }
+        if (ib + 1 < NB) load_ops(ib + 1, nxt);
+        h16x8 pf, dsf;
+#pragma unroll
+        for (int qh = 0; qh < 2; ++qh) {
+          const bool on = !half || qh == qs;  // this wave's half of a split block
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float p, ds;
+            if constexpr (MODE == 0) {
+              p = fast_exp2(s4[qh][i]);
+              ds = p * dp[qh][i];
+            } else if constexpr (MODE == 1) {
+              p = fast_exp2(mk ? s4[qh][i] : -INFINITY);
+              ds = p * dp[qh][i];
+            } else {
+              p = 1.f / N;
+              ds = 0.f;
+            }
+            if (!on) {
+              p = 0.f;
+              ds = 0.f;
+            }
+            pf[qh * 4 + i] = (h16)p;
+            dsf[qh * 4 + i] = (h16)ds;
+            if constexpr (MODE != 2) dbias[ib][qh * 4 + i] += ds;
+          }
+        }
+#pragma unroll
+        for (int dh = 0; dh < DT; ++dh) {
+          accV[dh] = mfma16x16x32(tr8(Os, qb, dh), pf, accV[dh]);
+          if constexpr (MODE != 2) accK[dh] = mfma16x16x32(tr8(Qs, qb, dh), dsf, accK[dh]);
+        }
+        if (ib + 1 < NB) cur = nxt;
+      }
+    };
+    if (live && allk) row_units(std::integral_constant<int, 0>{});
+    else if (live) row_units(std::integral_constant<int, 1>{});
+    else row_units(std::integral_constant<int, 2>{});
+
+    // row done: query group 1 parks its partials, query group 0 adds them
+    // and writes dK, dV of its key tile
+    if (qs == 1) {
+      float* x = Xs + kt_ * (2 * DT * 4 * 64);
+#pragma unroll
+      for (int dh = 0; dh < DT; ++dh)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          x[(dh * 4 + i) * 64 + lane] = accK[dh][i];
+          x[(DT * 4 + dh * 4 + i) * 64 + lane] = accV[dh][i];
+        }
+    }
+    __syncthreads();
+    if (qs == 0) {
+      const float* x = Xs + kt_ * (2 * DT * 4 * 64);
+      h16* dk = b.dqkvg + ((long)r * N + k) * a.ld + HD + h * D;
+      h16* dvp = dk + HD;
+      // lane (lk, g) holds channels [4g, 4g+4) and [16+4g, 16+4g+4) of key k;
+      // dK is w.r.t. the unscaled k: sum_q dS * q_scaled / log2(e)
+#pragma unroll
+      for (int dh = 0; dh < DT; ++dh) {
+        h16x4 kv, vv;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          kv[i] = (h16)((accK[dh][i] + x[(dh * 4 + i) * 64 + lane]) * (1.f / LOG2E));
+          vv[i] = (h16)(accV[dh][i] + x[(DT * 4 + dh * 4 + i) * 64 + lane]);
+        }
+        *reinterpret_cast<h16x4*>(dk + dh * 16 + 4 * g) = kv;
+        *reinterpret_cast<h16x4*>(dvp + dh * 16 + 4 * g) = vv;
+      }
+    }
+  }
+  if (b.dbias_part == nullptr) return;
+  float* part = b.dbias_part + (((long)ch * H + h) * N) * N;
+#pragma unroll
+  for (int ib = 0; ib < NB; ++ib) {
+    const int qb = blk_q0(ib);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (ib == FULL && e / 4 != qs) continue;  // the other group's half
+      const int qi = qb + (e / 4) * 16 + 4 * g + (e % 4);
+      part[(long)qi * N + k] = dbias[ib][e];
+    }
+  }
+}
+
 __global__ void attn_dbias_reduce_kernel(const float* __restrict__ part, int nch,
                                          long n, float* __restrict__ out) {
   const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -1124,7 +1475,7 @@ static void attn_fwd_t(hipStream_t st, const AttnArgs& a) {
     if (!a.bias) throw std::runtime_error("attention: the row-chunk forward needs the pair bias");
     const int rpc = attn_fwd_rows_per_chunk(a.R, a.N, a.H);
     const long nch = (a.R + rpc - 1) / rpc;
-    const size_t lds = (size_t)(2 * a.N + 2 * 64) * (D + 8) * 2 + (size_t)a.N * 8;
+    const size_t lds = (size_t)(2 * a.N + 2 * 64) * lds_ld<D>() * 2 + (size_t)a.N * 8;
     const dim3 grid(xcd_grid(nch * a.H * nqb));
     with_blocks(a.N / 32, [&](auto nb) {
       if constexpr (decltype(nb)::value <= 8)
@@ -1133,7 +1484,7 @@ static void attn_fwd_t(hipStream_t st, const AttnArgs& a) {
     });
     return;
   }
-  const size_t lds = (size_t)attn_chunk(a.N) * (D + 8) * 2 * 2 + (size_t)a.N * 8;
+  const size_t lds = (size_t)attn_chunk(a.N) * lds_ld<D>() * 2 * 2 + (size_t)a.N * 8;
   const dim3 grid(xcd_grid((long)a.R * a.H * nqb));
   with_blocks(a.N / 32, [&](auto nb) {
     hipLaunchKernelGGL((attn_fwd_kernel<D, decltype(nb)::value>), grid, dim3(256), lds, st, a);
@@ -1162,7 +1513,7 @@ static void attn_bwd_t(hipStream_t st, const AttnBwdArgs& b) {
     if (!a.bias) throw std::runtime_error("attention: the row-chunk dQ needs the pair bias");
     const int rpc = attn_fwd_rows_per_chunk(a.R, a.N, a.H);
     const long nch = (a.R + rpc - 1) / rpc;
-    const size_t lds = (size_t)(2 * a.N + 2 * 64) * (D + 8) * 2 + (size_t)(a.N + 2 * 64) * 4;
+    const size_t lds = (size_t)(2 * a.N + 2 * 64) * lds_ld<D>() * 2 + (size_t)(a.N + 2 * 64) * 4;
     KTimed kt(timer_name(2, a), st);
     const dim3 grid(xcd_grid(nch * a.H * nqb));
     with_blocks(a.N / 32, [&](auto nb) {
@@ -1171,7 +1522,7 @@ static void attn_bwd_t(hipStream_t st, const AttnBwdArgs& b) {
                            st, b, rpc);
     });
   } else {
-    const size_t lds_q = (size_t)attn_chunk(a.N) * (D + 8) * 2 * 2 + (size_t)a.N * 4;
+    const size_t lds_q = (size_t)attn_chunk(a.N) * lds_ld<D>() * 2 * 2 + (size_t)a.N * 4;
     KTimed kt(timer_name(2, a), st);
     const dim3 grid(xcd_grid((long)a.R * a.H * nqb));
     with_blocks(a.N / 32, [&](auto nb) {
@@ -1182,16 +1533,29 @@ static void attn_bwd_t(hipStream_t st, const AttnBwdArgs& b) {
   // query groups QS and key tiles KT per workgroup, as in the kernel
   const int QS = a.N > 256 ? 4 : 2, KT = 4 / QS;
   const int nkw = a.N / (16 * KT);
-  const size_t lds_k = (size_t)attn_chunk(a.N) * (D + 8) * 2 * 2 + (size_t)a.N * 4 * 3 +
+  const size_t lds_k = (size_t)attn_chunk(a.N) * lds_ld<D>() * 2 * 2 + (size_t)a.N * 4 * 3 +
                        (size_t)(QS - 1) * KT * 2 * (D / 16) * 4 * 64 * 4 +
-                       (size_t)2 * 16 * KT * (D + 8) * 2;
+                       (size_t)2 * 16 * KT * lds_ld<D>() * 2;
   {
     KTimed kt(timer_name(3, a), st);
     const dim3 grid(xcd_grid((long)nch * a.H * nkw));
+    if constexpr (D == 32) {
+      if (a.N <= 256 && a.bias) {
+        // two row buffers (Q, dO tiles + lse, -Dsum, mask) + 4 waves' partials
+        const size_t lds = (size_t)2 * (2 * a.N * 64 + 3 * a.N * 4) + (size_t)4 * 2 * 2 * 4 * 64 * 4;
+        with_blocks(a.N / 32, [&](auto nb) {
+          if constexpr (decltype(nb)::value <= 8)
+            hipLaunchKernelGGL((attn_bwd_dkv_lds_kernel<decltype(nb)::value>), grid, dim3(256), lds,
+                               st, b);
+        });
+        goto dkv_done;
+      }
+    }
     with_blocks(a.N / 32, [&](auto nb) {
       hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, decltype(nb)::value>), grid, dim3(256), lds_k, st, b);
     });
   }
+dkv_done:
   if (b.dbias && a.bias) {
     if (!b.dbias_part) throw std::runtime_error("attention bwd: missing dbias scratch");
     const long n = (long)a.H * a.N * a.N;
@@ -1203,7 +1567,7 @@ static void attn_bwd_t(hipStream_t st, const AttnBwdArgs& b) {
 
 void attn_bwd(hipStream_t st, const AttnBwdArgs& b) {
   attn_check(b.f);
-  if ((!b.dog && !b.gate_done) || !b.dO || !b.Dsum || !b.dqkvg)
+  if ((!b.dog && !b.gate_done) || !b.dO || !b.nDsum || !b.dqkvg)
     throw std::runtime_error("attention bwd: missing operand");
   if (b.f.D == 32) attn_bwd_t<32>(st, b);
   else attn_bwd_t<16>(st, b);

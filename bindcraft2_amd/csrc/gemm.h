@@ -481,7 +481,7 @@ struct EpiResidualRows : EpiRows {
 
 // Backward through attention's output gate, fused into the GEMM that makes
 // d(og) = acc (og = o * sigmoid(g)):  dO = d(og) s,  dG = d(og) o s (1 - s),
-// s = sigmoid(g), and Dsum[r][h][q] = sum over head h's D columns of dO * o
+// s = sigmoid(g), and nDsum[r][h][q] = -(sum over head h's D columns of dO * o)
 // for token m = r * Ntok + q.  The D/8 row-mode calls of one head come from
 // consecutive lanes (8 columns each), which add their partials by DPP.
 struct EpiGateBwd : EpiRows {
@@ -490,7 +490,7 @@ struct EpiGateBwd : EpiRows {
   const h16* o;     // ungated attention output [M][HD]
   h16* dO;          // [M][HD]
   h16* dqkvg;       // dG at column 3*HD + n
-  float* Dsum;       // [R][H][Ntok]
+  float* nDsum;      // [R][H][Ntok]
   int HD, H, D, Ntok;
   template <int W>
   __device__ __forceinline__ float head_sum(float s) const { return group_sum<W>(s); }
@@ -513,7 +513,7 @@ struct EpiGateBwd : EpiRows {
     s = D == 32 ? head_sum<4>(s) : head_sum<2>(s);
     if (n % D == 0) {
       const int r = m / Ntok, q = m % Ntok;
-      Dsum[((long)r * H + n / D) * Ntok + q] = s;
+      nDsum[((long)r * H + n / D) * Ntok + q] = -s;
     }
   }
 };

@@ -57,13 +57,14 @@ struct AttnBwdArgs {
   AttnArgs f;                  // forward operands (o, lse read back)
   const h16* dog = nullptr;   // upstream gradient of og [R*N][H*D]
   h16* dO = nullptr;          // scratch: dL/do [R*N][H*D]
-  float* Dsum = nullptr;       // scratch: [R][H][N] rowsum(dO*o)
+  float* nDsum = nullptr;      // scratch: [R][H][N] -rowsum(dO*o) (negated: the
+                               // dP - Dsum accumulators start from it as stored)
   h16* dqkvg = nullptr;       // out: dq|dk|dv|dg with the layout of qkvg
   float* dbias_part = nullptr; // scratch: [nchunk][H][N][N]
   float* dbias = nullptr;      // out: [H][N][N] (natural units), or null
   float scale = 1.f;           // D^-1/2 (q scaling applied in the forward)
   int rows_per_chunk = 8;
-  // dO, Dsum and the gate gradient already written by the caller (the
+  // dO, nDsum and the gate gradient already written by the caller (the
   // d(og) GEMM's EpiGateBwd epilogue); dog is then not read
   bool gate_done = false;
 };

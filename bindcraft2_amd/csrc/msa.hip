@@ -371,14 +371,14 @@ void msarow_bwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa
   need.take<float>((size_t)R * Cm);
   ar.reset(st, need.off);
   b.dO = ar.take_n<h16>((size_t)R * HD);
-  b.Dsum = ar.take_n<float>((size_t)S * H * N);
+  b.nDsum = ar.take_n<float>((size_t)S * H * N);
   b.dqkvg = ar.take_n<h16>((size_t)R * 4 * HD);
   b.dbias_part = ar.take_n<float>((size_t)nch * H * M);
   b.dbias = ar.take_n<float>((size_t)H * M);
   float* dxn = ar.take_n<float>((size_t)R * Cm);
   EpiGateBwd eg;
   eg.qkvg = sv.qkvg; eg.ld = 4L * HD; eg.o = sv.o; eg.dO = b.dO; eg.dqkvg = b.dqkvg;
-  eg.Dsum = b.Dsum; eg.HD = HD; eg.H = H; eg.D = a.D; eg.Ntok = N;
+  eg.nDsum = b.nDsum; eg.HD = HD; eg.H = H; eg.D = a.D; eg.Ntok = N;
   dout_gemm(st, a, R, dmsa_out, tbl, N, eg, "msarow.gemm_dout", sc);
   b.gate_done = true;
   AttnArgs& at = b.f;

@@ -220,7 +220,7 @@ void triattn_bwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
   need.take<float>((size_t)M * C);           // dxn
   ar.reset(st, need.off);
   b.dO = ar.take_n<h16>((size_t)M * HD);
-  b.Dsum = ar.take_n<float>((size_t)H * M);
+  b.nDsum = ar.take_n<float>((size_t)H * M);
   b.dqkvg = ar.take_n<h16>((size_t)M * 4 * HD);
   b.dbias_part = ar.take_n<float>((size_t)nch * H * M);
   b.dbias = ar.take_n<float>((size_t)H * M);
@@ -234,7 +234,7 @@ void triattn_bwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
   g1.B = w.wo; g1.b_sn = C; g1.b_sk = 1;
   EpiGateBwd eg;
   eg.qkvg = sv.qkvg; eg.ld = 4L * HD; eg.o = sv.o; eg.dO = b.dO; eg.dqkvg = b.dqkvg;
-  eg.Dsum = b.Dsum; eg.HD = HD; eg.H = H; eg.D = w.D; eg.Ntok = N;
+  eg.nDsum = b.nDsum; eg.HD = HD; eg.H = H; eg.D = w.D; eg.Ntok = N;
   gemm<128, 128>(st, g1, eg, BC2N_TN(C, "triattn.gemm_dout"), ALoadScaledRows{dout, tbl, N, C, per_column, sc});
   b.gate_done = true;
 
