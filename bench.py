@@ -11,8 +11,10 @@ with dropout on (JAX-exact masks from a stack key), random-init weights
 (LeCun normal, AF2 gate init) and N(0,1) synthetic activations resident in
 HBM, 10% of residues masked.  The same line also carries `design_step_ms`:
 the one-call design step from the designed logits (sequence features,
-embedder, template embedding, the three stacks, the 8-iteration structure
-module, heads and confidence metrics, forward and backward to d(logits)).
+embedder with its recycle terms, template embedding, the three stacks, the
+8-iteration structure module, heads and confidence metrics) at the
+reference's design default of one recycle: a forward-only pass, then the
+differentiated pass forward and backward to d(logits) (`design_recycles`).
 
 `--workload triattn` / `trimul` time BASELINE configs[1] / configs[2]
 (one module fwd+bwd, both orientations / directions); `--workload design`
@@ -484,6 +486,9 @@ def timed(step, steps, warmup):
     return ms
 
 
+DESIGN_RECYCLES = 1
+
+
 def design_step_setup(n, rng, dev, m1):
     """The one-call design step from the designed logits (sequence features,
     embedder, template embedding (2 blocks), extra stack (4, pair only), main
@@ -513,8 +518,11 @@ def design_step_setup(n, rng, dev, m1):
     iasym = (torch.arange(n, device=dev) >= nt).int()
     seqm = torch.as_tensor(m1, device=dev)
     act_const = 0.1 * torch.randn(n, n, 64, device=dev)
-    seeds = torch.tensor([[0, 11 + i, 1] for i in range(4)], dtype=torch.int64).to(
-        torch.uint32).to(dev)
+    # the reference's design default: one forward-only recycle pass ahead of
+    # the differentiated one (settings/core/default.json:38), each pass
+    # with its own four stack keys
+    seeds = torch.tensor([[0, 11 + i, 1] for i in range(4 * (DESIGN_RECYCLES + 1))],
+                         dtype=torch.int64).to(torch.uint32).to(dev)
     save = torch.empty(step_mod.save_bytes(n), dtype=torch.uint8, device=dev)
     cts = [torch.randn(*sh, device=dev) for sh in ((n, 14, 3), (n, n, 64), (n, n, 64),
                                                   (n, 50), (n, 37))]
@@ -522,7 +530,7 @@ def design_step_setup(n, rng, dev, m1):
 
     def step():
         step_mod.forward(logits, flags, scalars, ids, seqm, act_const=act_const, seeds=seeds,
-                         save=save, interface_asym=iasym)
+                         save=save, interface_asym=iasym, recycles=DESIGN_RECYCLES)
         step_mod.backward(cts, logits, flags, scalars, seqm, save, interface_asym=iasym,
                           conf_cts=conf_cts)
 
@@ -748,6 +756,7 @@ def main():
             torch.cuda.empty_cache()
             dstep, _ = design_step_setup(n, np.random.default_rng(1), dev, m1)
             line["design_step_ms"] = round(timed(dstep, args.steps, args.warmup), 2)
+            line["design_recycles"] = DESIGN_RECYCLES
         cpu = None if args.no_cpu_baseline else cpu_trunk_baseline(n)
 
     if dom_prof is None and prof:

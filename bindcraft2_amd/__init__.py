@@ -83,7 +83,7 @@ def _declare(L):
         "bc2n_fold_bwd": (i, [vp, vp, vp, vp, vp, vp, vp, i, c.c_int64, c.c_int64, cs, vp, vp]),
         "bc2n_design_step_save_bytes": (sz, [cs, cs, cs, cs, cs, i, i, c.c_int64, c.c_int64,
                                              c.c_int64, c.c_int64]),
-        "bc2n_design_step_fwd": (i, [vp] * 11 + [vp, i, i] + [c.c_int64] * 5 + [cs] * 5
+        "bc2n_design_step_fwd": (i, [vp] * 11 + [vp, i, i] + [c.c_int64] * 6 + [cs] * 5
                                  + [vp] * 6),
         "bc2n_design_step_bwd": (i, [vp, vp, vp, vp, c.c_int64] + [vp] * 6 + [i, i]
                                  + [c.c_int64] * 5 + [cs] * 5 + [vp, vp]),
@@ -94,7 +94,7 @@ def _declare(L):
         "bc2n_design_step_seq_save_bytes": (sz, [cs, cs, cs, cs, cs, i, c.c_int64, c.c_int64,
                                                  c.c_int64, c.c_int64]),
         "bc2n_design_step_seq_fwd": (i, [vp, vp, vp, vp, vp, f] + [vp] * 8 + [i]
-                                     + [c.c_int64] * 5 + [cs] * 5 + [vp] * 13),
+                                     + [c.c_int64] * 6 + [cs] * 5 + [vp] * 13),
         "bc2n_design_step_seq_bwd": (i, [vp, vp, vp, vp, vp, f, vp, c.c_int64] + [vp] * 13 + [i]
                                      + [c.c_int64] * 5 + [cs] * 5 + [vp]),
         "bc2n_confidence_save_bytes": (sz, [i]),
@@ -116,6 +116,7 @@ def _declare(L):
                                     c.c_long, c.c_long, c.c_long, vp, c.c_long, c.c_long,
                                     c.c_long]),
         "bc2n_probe_layernorm": (i, [vp, c.c_long, i, vp, vp, vp, i, vp, vp, vp]),
+        "bc2n_probe_recycle": (i, [vp, i, cs, vp, vp, vp, vp, vp, vp]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)

@@ -165,7 +165,7 @@ void need(bool ok, const char* msg) {
 extern "C" {
 
 const char* bc2n_last_error(void) { return last_error(); }
-int bc2n_abi_version(void) { return 1; }
+int bc2n_abi_version(void) { return 2; }
 
 size_t bc2n_triattn_save_bytes(int N, int C, int H) { return triattn_save_bytes(N, C, H); }
 
@@ -850,6 +850,25 @@ int bc2n_structure_heads_bwd(void* stream, const float* single, const float* pai
 
 namespace {
 std::map<std::string, DesignStepW> g_ds;
+// The recycle terms' weights live in the embedder's directory
+// (native/design_step.cuh:884, bindcraft/af/native.py:515-527).
+RecycleW recycle_w(WeightStore& ews) {
+  auto rec = [&](const char* name, size_t n) {
+    const std::string k = std::string("param/") + name;
+    if (ews.host(k).data.size() != n)
+      throw std::runtime_error(std::string("recycle terms: ") + k + " has the wrong size");
+    return ews.f32(k);
+  };
+  RecycleW r;
+  r.wpp = rec("prev_pos_linear/weights", 15 * 128);
+  r.bpp = rec("prev_pos_linear/bias", 128);
+  r.s_msa = rec("prev_msa_first_row_norm/scale", 256);
+  r.o_msa = rec("prev_msa_first_row_norm/offset", 256);
+  r.s_pair = rec("prev_pair_norm/scale", 128);
+  r.o_pair = rec("prev_pair_norm/offset", 128);
+  return r;
+}
+
 const DesignStepW& ds_w(const char* emb, const char* tpl, const char* extra, const char* main,
                         const char* post, int64_t dt, int64_t de, int64_t dm, int64_t df) {
   need(emb && tpl && extra && main && post, "design step: five weights directories required");
@@ -869,6 +888,7 @@ const DesignStepW& ds_w(const char* emb, const char* tpl, const char* extra, con
   w.bsa = ews.f32("param/single_activations/bias");
   if (ews.host("param/single_activations/weights").data.size() != 256u * 384u)
     throw std::runtime_error("design step: single_activations must be [256,384]");
+  w.rec = recycle_w(ews);
   w.tpl = te_w(tpl, (int)dt);
   w.extra = stack_w(extra, (int)de, StackKind::PAIR_ONLY);
   w.main = stack_w(main, (int)dm, StackKind::EVO);
@@ -898,10 +918,10 @@ int bc2n_design_step_fwd(void* stream, const float* target_feat, const float* ms
                          const float* entity_id, const float* sym_id, const int32_t* offset,
                          const float* seq_mask, const float* act_const, const float* aatype,
                          const uint32_t* seeds, int N, int S, int64_t d_tpl, int64_t d_extra,
-                         int64_t d_main, int64_t d_fold, int64_t dropout, const char* emb_dir,
-                         const char* tpl_dir, const char* extra_dir, const char* main_dir,
-                         const char* post_dir, float* atom14, float* distogram, float* pae,
-                         float* plddt, float* expres, void* save) {
+                         int64_t d_main, int64_t d_fold, int64_t dropout, int64_t recycles,
+                         const char* emb_dir, const char* tpl_dir, const char* extra_dir,
+                         const char* main_dir, const char* post_dir, float* atom14,
+                         float* distogram, float* pae, float* plddt, float* expres, void* save) {
   return guarded([&] {
     need(target_feat && msa_feat && residue_index && asym_id && entity_id && sym_id && seq_mask &&
              aatype && save, "null operand");
@@ -911,7 +931,7 @@ int bc2n_design_step_fwd(void* stream, const float* target_feat, const float* ms
         ds_w(emb_dir, tpl_dir, extra_dir, main_dir, post_dir, d_tpl, d_extra, d_main, d_fold);
     design_step_fwd(as_stream(stream), w, N, S, target_feat, msa_feat, residue_index, asym_id,
                     entity_id, sym_id, offset, seq_mask, act_const, aatype, seeds, dropout != 0,
-                    atom14, distogram, pae, plddt, expres, save);
+                    (int)recycles, atom14, distogram, pae, plddt, expres, save);
   });
 }
 
@@ -1000,12 +1020,13 @@ int bc2n_design_step_seq_fwd(void* stream, const float* logits, const uint8_t* f
                              const float* entity_id, const float* sym_id, const int32_t* offset,
                              const float* seq_mask, const float* act_const,
                              const uint32_t* seeds, int N, int64_t d_tpl, int64_t d_extra,
-                             int64_t d_main, int64_t d_fold, int64_t dropout, const char* emb_dir,
-                             const char* tpl_dir, const char* extra_dir, const char* main_dir,
-                             const char* post_dir, float* atom14, float* distogram, float* pae,
-                             float* plddt, float* expres, const int32_t* interface_asym,
-                             float* conf_plddt, float* conf_pae, float* ptm, float* iptm,
-                             float* iptm_per_residue, float* expres_ca, void* save) {
+                             int64_t d_main, int64_t d_fold, int64_t dropout, int64_t recycles,
+                             const char* emb_dir, const char* tpl_dir, const char* extra_dir,
+                             const char* main_dir, const char* post_dir, float* atom14,
+                             float* distogram, float* pae, float* plddt, float* expres,
+                             const int32_t* interface_asym, float* conf_plddt, float* conf_pae,
+                             float* ptm, float* iptm, float* iptm_per_residue, float* expres_ca,
+                             void* save) {
   return guarded([&] {
     need(logits && flags && scalars && residue_index && asym_id && entity_id && sym_id &&
              seq_mask && save, "null operand");
@@ -1017,7 +1038,7 @@ int bc2n_design_step_seq_fwd(void* stream, const float* logits, const uint8_t* f
         ds_w(emb_dir, tpl_dir, extra_dir, main_dir, post_dir, d_tpl, d_extra, d_main, d_fold);
     design_step_seq_fwd(as_stream(stream), w, N, logits, flags, aa_bias, scalars, omitted_half,
                         residue_index, asym_id, entity_id, sym_id, offset, seq_mask, act_const,
-                        seeds, dropout != 0, atom14, distogram, pae, plddt, expres,
+                        seeds, dropout != 0, (int)recycles, atom14, distogram, pae, plddt, expres,
                         ConfOut{interface_asym, conf_plddt, conf_pae, ptm, iptm, iptm_per_residue,
                                 expres_ca},
                         save);
@@ -1144,6 +1165,16 @@ int bc2n_probe_gemm_f32(void* stream, int M, int N, int K, int batch, const floa
     g.B = B; g.b_sk = b_sk; g.b_sn = b_sn; g.b_sb = b_sb;
     g.C = C; g.c_sm = c_sm; g.c_sn = c_sn; g.c_sb = c_sb;
     gemm_f32(as_stream(stream), g, "probe.gemm_f32");
+  });
+}
+
+int bc2n_probe_recycle(void* stream, int N, const char* emb_dir, const float* aatype,
+                       const float* prev_atom14, const float* prev_pair, const float* prev_msa0,
+                       float* pair, float* msa0) {
+  return guarded([&] {
+    need(emb_dir && pair && msa0, "null operand");
+    RecycleW r = recycle_w(weights(emb_dir));
+    recycle_terms(as_stream(stream), r, N, aatype, prev_atom14, prev_pair, prev_msa0, pair, msa0);
   });
 }
 

@@ -10,8 +10,16 @@
 
 namespace bc2n {
 
+// The embedder's three recycle terms (modules_multimer.py:487-507).
+struct RecycleW {
+  const float *wpp = nullptr, *bpp = nullptr;      // prev_pos_linear [15][128], [128]
+  const float *s_msa = nullptr, *o_msa = nullptr;  // prev_msa_first_row_norm [256]
+  const float *s_pair = nullptr, *o_pair = nullptr;  // prev_pair_norm [128]
+};
+
 struct DesignStepW {
   EmbedW emb;
+  RecycleW rec;
   const float *wsa = nullptr, *bsa = nullptr;  // single_activations [256][384], [384]
   TplEmbedW tpl;
   StackW extra, main;
@@ -19,15 +27,26 @@ struct DesignStepW {
   int d_tpl = 0, d_extra = 0, d_main = 0, d_fold = 0;
 };
 
-// Seeds: u32[4][3] on the device, one (k0, k1, enabled) JAX key per stack in
-// the order template, extra, main, structure module.
+// pair [N][N][128] += the pair recycle term, msa0 [N][256] += the msa[0] term,
+// of the previous pass's atoms (atom14 [N][14][3], pseudo-beta by aatype),
+// pair and msa[0]; prev_atom14 null = the first pass (a zero state).
+void recycle_terms(hipStream_t st, const RecycleW& r, int N, const float* aatype,
+                   const float* prev_atom14, const float* prev_pair, const float* prev_msa0,
+                   float* pair, float* msa0);
+
+// Every pass adds the embedder's recycle terms of the previous pass's atoms,
+// pair and msa[0] (all zero before the first).  `recycles` forward-only
+// passes run before the differentiated one (bindcraft/af2.py:195-202); the
+// outputs are the last pass's.  Seeds: u32[recycles + 1][4][3] on the
+// device, per pass one (k0, k1, enabled) JAX key per stack in the order
+// template, extra, main, structure module.
 size_t design_step_save_bytes(const DesignStepW& w, int N, int S);
 void design_step_fwd(hipStream_t st, const DesignStepW& w, int N, int S, const float* tf,
                      const float* mf, const float* ri, const float* ai, const float* ei,
                      const float* si, const int32_t* offset, const float* seq_mask,
                      const float* act_const, const float* aatype, const uint32_t* seeds,
-                     bool dropout, float* atom14, float* dgram, float* pae, float* plddt,
-                     float* expres, void* save);
+                     bool dropout, int recycles, float* atom14, float* dgram, float* pae,
+                     float* plddt, float* expres, void* save);
 // Cotangents may be null (zero) -> d target_feat [N][21], d msa_feat [S][N][49].
 void design_step_bwd(hipStream_t st, const DesignStepW& w, int N, int S, const float* tf,
                      const float* seq_mask, bool with_template, const float* aatype,
@@ -59,8 +78,8 @@ void design_step_seq_fwd(hipStream_t st, const DesignStepW& w, int N, const floa
                          float omitted_half, const float* ri, const float* ai, const float* ei,
                          const float* si, const int32_t* offset, const float* seq_mask,
                          const float* act_const, const uint32_t* seeds, bool dropout,
-                         float* atom14, float* dgram, float* pae, float* plddt, float* expres,
-                         const ConfOut& conf, void* save);
+                         int recycles, float* atom14, float* dgram, float* pae, float* plddt,
+                         float* expres, const ConfOut& conf, void* save);
 void design_step_seq_bwd(hipStream_t st, const DesignStepW& w, int N, const float* logits,
                          const uint8_t* flags, const float* bias, const float* sc4,
                          float omitted_half, const float* seq_mask, bool with_template,

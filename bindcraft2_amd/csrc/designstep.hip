@@ -1,10 +1,11 @@
 // The trunk of one design step in one call, forward and backward (the
 // reference's fused NativeDesignStep, native/ffi.cu:1691-2178 over
 // native/design_step.cuh, restricted to the differentiable trunk: features
-// in, structure-module outputs out, no recycling, losses and confidence
-// metrics left to the caller):
+// in, structure-module outputs out, losses left to the caller; `recycles`
+// forward-only passes ahead of the differentiated one):
 //
 //   msa0, pair0 = embedder(target_feat, msa_feat, ids)         (embed.hip)
+//   pair0 += recycle terms, msa0[0] += recycle term            (previous pass, or constants)
 //   pair1 = pair0 + template_embedding(pair0, act_const)        (tplembed.hip; skipped without act_const)
 //   pair2 = extra-MSA stack, pair only (its MSA mask is zero)   (evoformer.hip)
 //   msa3, pair3 = main stack (msa0, pair2)
@@ -93,7 +94,11 @@ struct DsSave {
     dq = c.template take<float>(M * CZ);
     dmsa = c.template take<float>((size_t)S * N * CM);
     dsingle = c.template take<float>((size_t)N * CS);
+    rpb = c.template take<float>((size_t)N * 4);
+    rpair = c.template take<float>(M * CZ);
+    rmsa0 = c.template take<float>((size_t)N * CM);
   }
+  float *rpb, *rpair, *rmsa0;  // the previous pass's pseudo-beta [N][3(+1)], pair, msa[0]
 };
 
 // pmask[i][j] = m[i] m[j]; mmask[s][n] = m[n]
@@ -113,6 +118,119 @@ void add2(hipStream_t st, const float* a, const float* b, long n, float* y) {
   hipLaunchKernelGGL(add2_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a, b, n, y);
 }
 
+// ------------------------------------------------------------- recycling
+// The embedder's three recycle terms (modules_multimer.py:487-507):
+//   pair  += prev_pos_linear(dgram(pseudo_beta(prev atoms))) + LN_pair(prev pair)
+//   msa[0] += LN_msa(prev msa[0])
+// The distogram (modules.py:1215-1238) is one-hot in 15 bins between the
+// squared lower breaks 3.25 + 1.25 b (b = 0..14; exact in f32), strict on
+// both sides, the last bin open to 1e8: at most one bin is set, so the
+// Linear is the bias plus one weight row.  LayerNorms: eps 1e-5, two-pass.
+constexpr int RBINS = 15;
+
+// First pass: the previous state is zero, so the terms are constants -- the
+// Linear's bias (a zero distance lies in no bin) and the two norms' offsets
+// (a LayerNorm of a zero vector is its offset).
+__global__ void recycle_first_kernel(float* __restrict__ pair, float* __restrict__ msa0, long M,
+                                     int N, const float* __restrict__ bpp,
+                                     const float* __restrict__ o_pair,
+                                     const float* __restrict__ o_msa) {
+  const long e = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e < M * CZ) {
+    const int c = (int)(e % CZ);
+    pair[e] += bpp[c] + o_pair[c];
+  } else if (e < M * CZ + (long)N * CM) {
+    const long f = e - M * CZ;
+    msa0[f] += o_msa[f % CM];
+  }
+}
+
+// One wave per pair row (i, j): 2 channels per lane.
+__global__ __launch_bounds__(256) void recycle_pair_kernel(
+    float* __restrict__ pair, const float* __restrict__ prev_pair, const float* __restrict__ pb,
+    int N, const float* __restrict__ wpp, const float* __restrict__ bpp,
+    const float* __restrict__ s_pair, const float* __restrict__ o_pair) {
+  const long m = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (m >= (long)N * N) return;
+  const int i = (int)(m / N), j = (int)(m % N);
+  float d2 = 0.f;
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    const float d = pb[i * 4 + c] - pb[j * 4 + c];
+    d2 += d * d;
+  }
+  int bin = -1;
+#pragma unroll
+  for (int b = 0; b < RBINS; ++b) {
+    const float lo = 3.25f + 1.25f * (float)b;
+    const float hi = 3.25f + 1.25f * (float)(b + 1);
+    if (d2 > lo * lo && (b == RBINS - 1 ? d2 < 1e8f : d2 < hi * hi)) bin = b;
+  }
+  const float* x = prev_pair + m * CZ;
+  const float x0 = x[lane], x1 = x[lane + 64];
+  float sum = x0 + x1;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+  const float mean = sum * (1.f / CZ);
+  float var = (x0 - mean) * (x0 - mean) + (x1 - mean) * (x1 - mean);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) var += __shfl_xor(var, o, 64);
+  const float rstd = rsqrtf(var * (1.f / CZ) + 1e-5f);
+  float* y = pair + m * CZ;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int c = lane + 64 * h;
+    const float xv = h ? x1 : x0;
+    const float lin = bpp[c] + (bin >= 0 ? wpp[bin * CZ + c] : 0.f);
+    y[c] += lin + (xv - mean) * rstd * s_pair[c] + o_pair[c];
+  }
+}
+
+// One wave per residue: msa[0][i] += LN_msa(prev msa[0][i]), 4 channels per lane.
+__global__ __launch_bounds__(256) void recycle_msa_kernel(float* __restrict__ msa0,
+                                                          const float* __restrict__ prev, int N,
+                                                          const float* __restrict__ s_msa,
+                                                          const float* __restrict__ o_msa) {
+  const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (i >= N) return;
+  const float* x = prev + (long)i * CM;
+  float v[4], sum = 0.f;
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    v[h] = x[lane + 64 * h];
+    sum += v[h];
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+  const float mean = sum * (1.f / CM);
+  float var = 0.f;
+#pragma unroll
+  for (int h = 0; h < 4; ++h) var += (v[h] - mean) * (v[h] - mean);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) var += __shfl_xor(var, o, 64);
+  const float rstd = rsqrtf(var * (1.f / CM) + 1e-5f);
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    const int c = lane + 64 * h;
+    msa0[(long)i * CM + c] += (v[h] - mean) * rstd * s_msa[c] + o_msa[c];
+  }
+}
+
+// pseudo_beta_fn (modules.py:1249-1264): CB, or CA for glycine (aatype 7),
+// read from atom14 (CA slot 1, CB slot 4); stored with stride 4.
+__global__ void pseudo_beta_kernel(const float* __restrict__ aatype,
+                                   const float* __restrict__ atom14, int N,
+                                   float* __restrict__ pb) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= N) return;
+  const int slot = (int)aatype[i] == 7 ? 1 : 4;
+#pragma unroll
+  for (int c = 0; c < 3; ++c) pb[i * 4 + c] = atom14[((long)i * 14 + slot) * 3 + c];
+  pb[i * 4 + 3] = 0.f;
+}
+
 void ds_check(const DesignStepW& w, int N, int S) {
   if (N <= 0 || N % 32 != 0 || N > 512)
     throw std::runtime_error("design step: N must be a positive multiple of 32, at most 512");
@@ -122,6 +240,32 @@ void ds_check(const DesignStepW& w, int N, int S) {
 }
 
 }  // namespace
+
+void recycle_terms(hipStream_t st, const RecycleW& r, int N, const float* aatype,
+                   const float* prev_atom14, const float* prev_pair, const float* prev_msa0,
+                   float* pair, float* msa0) {
+  if (N <= 0) throw std::invalid_argument("recycle terms: N must be positive");
+  nonnull(pair, "recycle terms pair"); nonnull(msa0, "recycle terms msa0");
+  const long M = (long)N * N;
+  if (!prev_atom14) {
+    const long n = M * CZ + (long)N * CM;
+    hipLaunchKernelGGL(recycle_first_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                       pair, msa0, M, N, r.bpp, r.o_pair, r.o_msa);
+    return;
+  }
+  nonnull(aatype, "recycle terms aatype"); nonnull(prev_pair, "recycle terms prev_pair");
+  nonnull(prev_msa0, "recycle terms prev_msa0");
+  Arena& ar = arena();
+  std::lock_guard<std::recursive_mutex> lk(ar.lock());
+  ar.reset(st, (size_t)N * 16 + 256);
+  float* pb = ar.take_n<float>((size_t)N * 4);
+  hipLaunchKernelGGL(pseudo_beta_kernel, dim3((unsigned)((N + 127) / 128)), dim3(128), 0, st,
+                     aatype, prev_atom14, N, pb);
+  hipLaunchKernelGGL(recycle_pair_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, st, pair,
+                     prev_pair, pb, N, r.wpp, r.bpp, r.s_pair, r.o_pair);
+  hipLaunchKernelGGL(recycle_msa_kernel, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, st, msa0,
+                     prev_msa0, N, r.s_msa, r.o_msa);
+}
 
 size_t design_step_save_bytes(const DesignStepW& w, int N, int S) {
   Sizer s;
@@ -134,11 +278,13 @@ void design_step_fwd(hipStream_t st, const DesignStepW& w, int N, int S, const f
                      const float* mf, const float* ri, const float* ai, const float* ei,
                      const float* si, const int32_t* offset, const float* seq_mask,
                      const float* act_const, const float* aatype, const uint32_t* seeds,
-                     bool dropout, float* atom14, float* dgram, float* pae, float* plddt,
-                     float* expres, void* save) {
+                     bool dropout, int recycles, float* atom14, float* dgram, float* pae,
+                     float* plddt, float* expres, void* save) {
   ds_check(w, N, S);
   nonnull(seq_mask, "design step seq_mask"); nonnull(save, "design step save");
+  nonnull(aatype, "design step aatype");
   if (dropout) nonnull(seeds, "design step seeds");
+  if (recycles < 0 || recycles > 64) throw std::invalid_argument("design step: recycles must be in [0, 64]");
   Carver cv(save);
   DsSave<Carver> sv(cv, w, N, S);
   const long M = (long)N * N;
@@ -148,25 +294,51 @@ void design_step_fwd(hipStream_t st, const DesignStepW& w, int N, int S, const f
     hipLaunchKernelGGL(masks_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, seq_mask,
                        N, S, sv.pmask, sv.mmask);
   }
-  auto key = [&](int i) { return dropout ? seeds + 3 * i : nullptr; };
-  auto enabled = [&](int i) { return dropout ? seeds + 3 * i + 2 : nullptr; };
-  embed_fwd(st, w.emb, N, S, tf, mf, ri, ai, ei, si, offset, sv.msa0, sv.pair0);
-  const float* pair = sv.pair0;
-  if (act_const) {
-    tplembed_fwd(st, w.tpl, N, sv.pair0, act_const, sv.pmask, key(0), enabled(0), dropout, sv.tplo,
-                 sv.tpl);
-    add2(st, sv.pair0, sv.tplo, M * CZ, sv.pair1);
-    pair = sv.pair1;
+  for (int pass = 0; pass <= recycles; ++pass) {
+    // forward-only passes keep no save-sets: their stacks run detached
+    const bool last = pass == recycles;
+    const uint32_t* sp = dropout ? seeds + 12 * pass : nullptr;
+    auto key = [&](int i) { return sp ? sp + 3 * i : nullptr; };
+    auto enabled = [&](int i) { return sp ? sp + 3 * i + 2 : nullptr; };
+    embed_fwd(st, w.emb, N, S, tf, mf, ri, ai, ei, si, offset, sv.msa0, sv.pair0);
+    {
+      KTimed kt("design.recycle_terms", st);
+      if (pass == 0) {
+        const long n = M * CZ + (long)N * CM;
+        hipLaunchKernelGGL(recycle_first_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                           st, sv.pair0, sv.msa0, M, N, w.rec.bpp, w.rec.o_pair, w.rec.o_msa);
+      } else {
+        hipLaunchKernelGGL(recycle_pair_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, st,
+                           sv.pair0, sv.rpair, sv.rpb, N, w.rec.wpp, w.rec.bpp, w.rec.s_pair,
+                           w.rec.o_pair);
+        hipLaunchKernelGGL(recycle_msa_kernel, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, st,
+                           sv.msa0, sv.rmsa0, N, w.rec.s_msa, w.rec.o_msa);
+      }
+    }
+    const float* pair = sv.pair0;
+    if (act_const) {
+      tplembed_fwd(st, w.tpl, N, sv.pair0, act_const, sv.pmask, key(0), enabled(0), dropout,
+                   sv.tplo, sv.tpl);
+      add2(st, sv.pair0, sv.tplo, M * CZ, sv.pair1);
+      pair = sv.pair1;
+    }
+    stack_fwd(st, w.extra, N, 1, w.d_extra, pair, nullptr, sv.pmask, nullptr, key(1), enabled(1),
+              dropout, sv.pair2, nullptr, sv.extra, !last);
+    stack_fwd(st, w.main, N, S, w.d_main, sv.pair2, sv.msa0, sv.pmask, sv.mmask, key(2),
+              enabled(2), dropout, sv.pair3, sv.msa3, sv.main, !last);
+    GemmF32 g = gemm_rows(N, CS, CM, sv.msa3, w.wsa, sv.single);
+    g.bias = w.bsa;
+    gemm_f32(st, g, "design.gemm_single");
+    structheads_fwd(st, w.sh, N, w.d_fold, sv.single, sv.pair3, seq_mask, aatype, key(3),
+                    enabled(3), dropout, atom14, dgram, pae, plddt, expres, sv.sh);
+    if (!last) {
+      // what the next pass's recycle terms read (under stop_gradient)
+      hipLaunchKernelGGL(pseudo_beta_kernel, dim3((unsigned)((N + 127) / 128)), dim3(128), 0, st,
+                         aatype, atom14, N, sv.rpb);
+      BC2N_HIP(hipMemcpyAsync(sv.rpair, sv.pair3, (size_t)M * CZ * 4, hipMemcpyDeviceToDevice, st));
+      BC2N_HIP(hipMemcpyAsync(sv.rmsa0, sv.msa3, (size_t)N * CM * 4, hipMemcpyDeviceToDevice, st));
+    }
   }
-  stack_fwd(st, w.extra, N, 1, w.d_extra, pair, nullptr, sv.pmask, nullptr, key(1), enabled(1),
-            dropout, sv.pair2, nullptr, sv.extra);
-  stack_fwd(st, w.main, N, S, w.d_main, sv.pair2, sv.msa0, sv.pmask, sv.mmask, key(2), enabled(2),
-            dropout, sv.pair3, sv.msa3, sv.main);
-  GemmF32 g = gemm_rows(N, CS, CM, sv.msa3, w.wsa, sv.single);
-  g.bias = w.bsa;
-  gemm_f32(st, g, "design.gemm_single");
-  structheads_fwd(st, w.sh, N, w.d_fold, sv.single, sv.pair3, seq_mask, aatype, key(3), enabled(3),
-                  dropout, atom14, dgram, pae, plddt, expres, sv.sh);
 }
 
 void design_step_bwd(hipStream_t st, const DesignStepW& w, int N, int S, const float* tf,
@@ -254,8 +426,8 @@ void design_step_seq_fwd(hipStream_t st, const DesignStepW& w, int N, const floa
                          float omitted_half, const float* ri, const float* ai, const float* ei,
                          const float* si, const int32_t* offset, const float* seq_mask,
                          const float* act_const, const uint32_t* seeds, bool dropout,
-                         float* atom14, float* dgram, float* pae, float* plddt, float* expres,
-                         const ConfOut& conf, void* save) {
+                         int recycles, float* atom14, float* dgram, float* pae, float* plddt,
+                         float* expres, const ConfOut& conf, void* save) {
   ds_check(w, N, 1);
   nonnull(logits, "design step logits"); nonnull(flags, "design step flags");
   nonnull(sc4, "design step scalars"); nonnull(save, "design step save");
@@ -265,7 +437,7 @@ void design_step_seq_fwd(hipStream_t st, const DesignStepW& w, int N, const floa
   seqfeat_fwd(st, logits, flags, bias, SeqScalars{}, sc4, omitted_half, N, x.feat, x.prof);
   design_inputs_fwd(st, x.feat, x.prof, N, x.tf, x.mf, x.aatype);
   design_step_fwd(st, w, N, 1, x.tf, x.mf, ri, ai, ei, si, offset, seq_mask, act_const, x.aatype,
-                  seeds, dropout, atom14, dgram, pae, plddt, expres, cv.p + cv.off);
+                  seeds, dropout, recycles, atom14, dgram, pae, plddt, expres, cv.p + cv.off);
   if (conf.plddt) {
     nonnull(conf.asym, "design step interface asym");
     confidence_fwd(st, plddt, pae, expres, seq_mask, conf.asym, N, conf.plddt, conf.pae, conf.ptm,

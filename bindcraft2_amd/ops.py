@@ -493,10 +493,13 @@ class DesignStep:
         return b
 
     def forward(self, target_feat, msa_feat, ids, seq_mask, aatype, act_const=None, offset=None,
-                seeds=None, dropout=True, save=None):
-        """ids = (residue_index, asym_id, entity_id, sym_id); seeds u32[4][3]
-        -> ((atom14, distogram, pae, plddt, expres), save)"""
+                seeds=None, dropout=True, save=None, recycles=0):
+        """ids = (residue_index, asym_id, entity_id, sym_id); seeds
+        u32[recycles + 1][4][3] (per pass the keys of the template, extra,
+        main and structure-module stacks) -> ((atom14, distogram, pae, plddt,
+        expres), save) of the last of recycles + 1 passes"""
         n, s, dev = target_feat.shape[0], msa_feat.shape[0], target_feat.device
+        _check_seeds(seeds, dropout, recycles)
         outs = tuple(torch.empty(*sh, dtype=torch.float32, device=dev)
                      for sh in ((n, 14, 3), (n, n, 64), (n, n, 64), (n, 50), (n, 37)))
         if save is None:
@@ -504,7 +507,7 @@ class DesignStep:
         check(lib().bc2n_design_step_fwd(_stream(), _ptr(target_feat), _ptr(msa_feat),
                                          *map(_ptr, ids), _ptr(offset), _ptr(seq_mask),
                                          _ptr(act_const), _ptr(aatype), _ptr(seeds), n, s,
-                                         *self.depths, int(dropout), *self.dirs,
+                                         *self.depths, int(dropout), int(recycles), *self.dirs,
                                          *map(_ptr, outs), _ptr(save)))
         return outs, save
 
@@ -518,6 +521,14 @@ class DesignStep:
                                          _ptr(save), n, msa_rows, *self.depths, int(dropout),
                                          *self.dirs, _ptr(dtf), _ptr(dmf)))
         return dtf, dmf
+
+
+def _check_seeds(seeds, dropout, recycles):
+    """A design step's seeds hold (recycles + 1) x 4 keys of 3 words."""
+    if recycles < 0:
+        raise ValueError("recycles must be >= 0")
+    if dropout and (seeds is None or seeds.numel() != (recycles + 1) * 12):
+        raise ValueError(f"dropout needs seeds u32[{recycles + 1}][4][3]")
 
 
 OMITTED_HALF = -5000.0  # half of BindCraft's omitted-acid logit (-1e4)
@@ -586,11 +597,12 @@ class DesignStepSeq(DesignStep):
 
     def forward(self, logits, flags, scalars, ids, seq_mask, aa_bias=None, act_const=None,
                 offset=None, seeds=None, dropout=True, save=None, omitted_half=OMITTED_HALF,
-                interface_asym=None):
+                interface_asym=None, recycles=0):
         """-> ((atom14, distogram, pae, plddt, expres), save), plus the confidence
         metrics (plddt, pae, ptm, iptm, iptm_per_residue, expres_ca) as a third
         element when interface_asym (i32 [N]) is given."""
         n, dev = logits.shape[0], logits.device
+        _check_seeds(seeds, dropout, recycles)
         e = lambda *sh: torch.empty(*sh, dtype=torch.float32, device=dev)
         outs = (e(n, 14, 3), e(n, n, 64), e(n, n, 64), e(n, 50), e(n, 37))
         conf = (e(n), e(n, n), e(1), e(1), e(n), e(n)) if interface_asym is not None else (None,) * 6
@@ -600,7 +612,8 @@ class DesignStepSeq(DesignStep):
                                              _ptr(scalars), float(omitted_half), *map(_ptr, ids),
                                              _ptr(offset), _ptr(seq_mask), _ptr(act_const),
                                              _ptr(seeds), n, *self.depths, int(dropout),
-                                             *self.dirs, *map(_ptr, outs), _ptr(interface_asym),
+                                             int(recycles), *self.dirs, *map(_ptr, outs),
+                                             _ptr(interface_asym),
                                              *map(_ptr, conf), _ptr(save)))
         if interface_asym is None:
             return outs, save
@@ -697,3 +710,15 @@ def probe_gemm_f32(A, B, C, M, N, K, batch, a_strides, b_strides, c_strides):
     check(lib().bc2n_probe_gemm_f32(_stream(), M, N, K, batch, _ptr(A), *a_strides, _ptr(B),
                                     *b_strides, _ptr(C), *c_strides))
     return C
+
+
+def probe_recycle(emb_dir, pair, msa0, aatype=None, prev_atom14=None, prev_pair=None,
+                  prev_msa0=None):
+    """pair [N,N,128] and msa0 [N,256] (f32, in place) += the design step's
+    recycle terms of the previous state (bc2n_probe_recycle); no previous
+    state = the first pass."""
+    n = pair.shape[0]
+    check(lib().bc2n_probe_recycle(_stream(), n, emb_dir.encode(), _ptr(aatype), _ptr(prev_atom14),
+                                   _ptr(prev_pair), _ptr(prev_msa0), _ptr(pair), _ptr(msa0)))
+    return pair, msa0
+

@@ -158,6 +158,16 @@ def embedder_shapes(c_m=C_M, c_z=C_Z):
             "position_activations/weights": (73, c_z), "position_activations/bias": (c_z,)}
 
 
+def recycle_shapes(c_m=C_M, c_z=C_Z, bins=15):
+    """The embedder's three recycle terms (modules_multimer.py:487-507; in
+    the embedder's weights directory, bindcraft/af/native.py:515-527):
+    prev_pos_linear over the 15-bin distogram of the previous pseudo-beta
+    positions, and the LayerNorms of the previous msa[0] and pair."""
+    return {"prev_pos_linear/weights": (bins, c_z), "prev_pos_linear/bias": (c_z,),
+            "prev_msa_first_row_norm/scale": (c_m,), "prev_msa_first_row_norm/offset": (c_m,),
+            "prev_pair_norm/scale": (c_z,), "prev_pair_norm/offset": (c_z,)}
+
+
 def single_activations_shapes(c_m=C_M, c_s=384):
     """single_activations (modules_multimer.py EmbeddingsAndEvoformer: the
     single representation from the main stack's msa[0]); it ships in the
@@ -171,7 +181,8 @@ def init_embedder_params(rng, scoped=False):
     position_activations under evoformer/~_relative_encoding/ as haiku's
     method scope (and the checkpoint) does."""
     out = {}
-    for name, shape in {**embedder_shapes(), **single_activations_shapes()}.items():
+    for name, shape in {**embedder_shapes(), **single_activations_shapes(),
+                        **recycle_shapes()}.items():
         fan_in = shape[0] if len(shape) == 2 else 1
         arr = rng.standard_normal(shape) / math.sqrt(fan_in)
         if len(shape) == 1:

@@ -374,19 +374,27 @@ int bc2n_structure_heads_bwd(void* stream, const float* single, const float* pai
  * The trunk of one design step in one call (a reduced form of the
  * reference's NativeDesignStep custom call, native/ffi.cu:1691-2178, runner
  * bindcraft/af/native_step.py: features in, structure-module outputs out;
- * the sequence parametrisation, recycling, confidence metrics and losses
- * stay with the caller).  fwd:
+ * the sequence parametrisation, confidence metrics and losses stay with the
+ * caller).  fwd:
  *   (target_feat f32[N,21], msa_feat f32[S,N,49], residue_index, asym_id,
  *    entity_id, sym_id f32[N], offset i32[N,N] or NULL, seq_mask f32[N],
  *    act_const f32[N,N,64] or NULL (no template), aatype f32[N],
- *    seeds u32[4][3] = (k0, k1, enabled) keys of the template, extra, main
- *    and structure-module stacks; depths, dropout, five weights directories)
+ *    seeds u32[recycles+1][4][3] = per pass the (k0, k1, enabled) keys of the
+ *    template, extra, main and structure-module stacks; depths, dropout,
+ *    recycles, five weights directories)
  *   -> (atom14 f32[N,14,3], distogram, pae f32[N,N,64], plddt f32[N,50],
  *       expres f32[N,37]) and save
- * = bc2n_embedder, + bc2n_tplembed on the embedded pair, bc2n_evoformer
- * pair-only (extra MSA mask zero), bc2n_evoformer (main), single =
- * msa[0] . single_activations (from the embedder's directory),
- * bc2n_structure_heads (modules_multimer.py:441-700).  bwd: the five
+ * = bc2n_embedder plus the three recycle terms (modules_multimer.py:
+ * 487-507; their weights prev_pos_linear, prev_msa_first_row_norm and
+ * prev_pair_norm in the embedder's directory), + bc2n_tplembed on that
+ * pair, bc2n_evoformer pair-only (extra MSA mask zero), bc2n_evoformer
+ * (main), single = msa[0] . single_activations (from the embedder's
+ * directory), bc2n_structure_heads (modules_multimer.py:441-700).
+ * `recycles` forward-only passes run first (bindcraft/af2.py:195-202; the
+ * reference's design default is 1, settings/core/default.json:38), each
+ * feeding its atoms' pseudo-beta, pair and msa[0] to the next pass's recycle
+ * terms; the first pass's terms are the constants of a zero state.  The
+ * outputs and the save-set are the last pass's.  bwd: the five
  * cotangents (any may be NULL) -> d_target_feat f32[N,21], d_msa_feat
  * f32[S,N,49].  N is a runtime value (a multiple of 32, at most 512): one
  * set of weights serves every length.  save holds
@@ -401,10 +409,10 @@ int bc2n_design_step_fwd(void* stream, const float* target_feat, const float* ms
                          const float* entity_id, const float* sym_id, const int32_t* offset,
                          const float* seq_mask, const float* act_const, const float* aatype,
                          const uint32_t* seeds, int N, int S, int64_t d_tpl, int64_t d_extra,
-                         int64_t d_main, int64_t d_fold, int64_t dropout, const char* emb_dir,
-                         const char* tpl_dir, const char* extra_dir, const char* main_dir,
-                         const char* post_dir, float* atom14, float* distogram, float* pae,
-                         float* plddt, float* expres, void* save);
+                         int64_t d_main, int64_t d_fold, int64_t dropout, int64_t recycles,
+                         const char* emb_dir, const char* tpl_dir, const char* extra_dir,
+                         const char* main_dir, const char* post_dir, float* atom14,
+                         float* distogram, float* pae, float* plddt, float* expres, void* save);
 int bc2n_design_step_bwd(void* stream, const float* target_feat, const float* seq_mask,
                          const float* aatype, int64_t with_template, const float* d_atom14,
                          const float* d_distogram, const float* d_pae, const float* d_plddt,
@@ -474,12 +482,13 @@ int bc2n_design_step_seq_fwd(void* stream, const float* logits, const uint8_t* f
                              const float* entity_id, const float* sym_id, const int32_t* offset,
                              const float* seq_mask, const float* act_const,
                              const uint32_t* seeds, int N, int64_t d_tpl, int64_t d_extra,
-                             int64_t d_main, int64_t d_fold, int64_t dropout, const char* emb_dir,
-                             const char* tpl_dir, const char* extra_dir, const char* main_dir,
-                             const char* post_dir, float* atom14, float* distogram, float* pae,
-                             float* plddt, float* expres, const int32_t* interface_asym,
-                             float* conf_plddt, float* conf_pae, float* ptm, float* iptm,
-                             float* iptm_per_residue, float* expres_ca, void* save);
+                             int64_t d_main, int64_t d_fold, int64_t dropout, int64_t recycles,
+                             const char* emb_dir, const char* tpl_dir, const char* extra_dir,
+                             const char* main_dir, const char* post_dir, float* atom14,
+                             float* distogram, float* pae, float* plddt, float* expres,
+                             const int32_t* interface_asym, float* conf_plddt, float* conf_pae,
+                             float* ptm, float* iptm, float* iptm_per_residue, float* expres_ca,
+                             void* save);
 int bc2n_design_step_seq_bwd(void* stream, const float* logits, const uint8_t* flags,
                              const float* aa_bias, const float* scalars, float omitted_half,
                              const float* seq_mask, int64_t with_template,
@@ -562,6 +571,14 @@ int bc2n_probe_gemm(void* stream, int M, int N, int K, const uint16_t* A,
 int bc2n_probe_gemm_f32(void* stream, int M, int N, int K, int batch, const float* A,
                         long a_sm, long a_sk, long a_sb, const float* B, long b_sk,
                         long b_sn, long b_sb, float* C, long c_sm, long c_sn, long c_sb);
+/* The design step's recycle terms, in place (modules_multimer.py:487-507):
+ * pair f32[N,N,128] += prev_pos_linear(dgram(pseudo_beta(prev_atom14, aatype)))
+ * + prev_pair_norm(prev_pair), msa0 f32[N,256] +=
+ * prev_msa_first_row_norm(prev_msa0); weights from emb_dir.  prev_atom14
+ * NULL = the first pass (bias and offsets only). */
+int bc2n_probe_recycle(void* stream, int N, const char* emb_dir, const float* aatype,
+                       const float* prev_atom14, const float* prev_pair, const float* prev_msa0,
+                       float* pair, float* msa0);
 /* y = LN(x) over C channels, binary16 out + mean/rstd. fast = E[x^2]-E[x]^2. */
 int bc2n_probe_layernorm(void* stream, long M, int C, const float* x,
                          const float* gamma, const float* beta, int fast,

@@ -17,8 +17,10 @@ pair; incoming == outgoing with swapped operands; OPM against its direct
 4-index sum and the mask==0 constant; S=1 column attention against its
 softmax==1 closed form; global attention against a pure-Python loop, its
 S=1 closed form and its fully-masked-column closed form; the pair-only extra
-block against the full extra-MSA iteration on a zero mask; gradients against
-central finite differences.
+block against the full extra-MSA iteration on a zero mask; the recycle
+terms' distogram against a loop over the squared breaks, and the first-pass
+terms against their closed form (bias + offsets); gradients against central
+finite differences.
 """
 import math
 
@@ -657,32 +659,96 @@ def structure_heads(single, pair, mask, aatype, params, depth, key, use_dropout,
     return (atom14,) + heads(pair, act, single, params, dtype)
 
 
+# ------------------------------------------------------------------ recycling
+# modules_multimer.py:487-507 (the three prev_* terms of the embedder) and
+# bindcraft/af2.py:195-202 (recycled_alphafold_outputs).
+PREV_POS_BINS, PREV_POS_MIN, PREV_POS_MAX = 15, 3.25, 20.75  # config.py prev_pos
+GLY = 7  # residue_constants.restype_order['G']
+
+
+def pseudo_beta_atom14(aatype, atom14):
+    """pseudo_beta_fn (modules.py:1249-1264, no mask): CB, or CA for glycine,
+    read from atom14 positions (CA is slot 1, CB slot 4 of every residue
+    type's atom14 list, the same atoms atom37 slots 1 and 3 hold)."""
+    gly = torch.as_tensor(np.asarray(aatype)).long() == GLY
+    return torch.where(gly[:, None], atom14[:, 1], atom14[:, 4])
+
+
+def dgram_from_positions(pos, num_bins=PREV_POS_BINS, min_bin=PREV_POS_MIN, max_bin=PREV_POS_MAX):
+    """modules.py:1215-1238: one-hot of the squared distance between the
+    squared lower breaks linspace(min, max, bins)^2 (strict on both sides;
+    the last bin is open to 1e8).  Breaks in float32, as the JAX computes
+    them; a zero distance lies in no bin."""
+    lower = torch.linspace(min_bin, max_bin, num_bins, dtype=torch.float32).to(pos.dtype) ** 2
+    upper = torch.cat([lower[1:], torch.tensor([1e8], dtype=pos.dtype)])
+    d2 = ((pos[:, None, :] - pos[None, :, :]) ** 2).sum(-1, keepdim=True)
+    return ((d2 > lower) & (d2 < upper)).to(pos.dtype)
+
+
+def recycle_terms(aatype, prev_atom14, prev_pair, prev_msa0, p_emb, dtype=torch.float64):
+    """The embedder's three recycle terms (modules_multimer.py:487-507):
+    pair += prev_pos_linear(dgram(pseudo_beta(prev_pos))) +
+    prev_pair_norm(prev_pair); msa[0] += prev_msa_first_row_norm(prev_msa0).
+    With the previous state all zero (the first pass) they are the Linear's
+    bias plus the pair norm's offset, and the msa norm's offset: a
+    LayerNorm of a zero vector is its offset, and a zero distance lies in
+    no bin.  Returns (pair term [N,N,128], msa row-0 term [N,256])."""
+    P = Params(p_emb, "param/", dtype)
+    dg = dgram_from_positions(pseudo_beta_atom14(aatype, prev_atom14))
+    pair_t = linear(dg, P.sub("prev_pos_linear/")) + layer_norm(
+        prev_pair, P("prev_pair_norm/scale"), P("prev_pair_norm/offset"))
+    msa_t = layer_norm(prev_msa0, P("prev_msa_first_row_norm/scale"),
+                       P("prev_msa_first_row_norm/offset"))
+    return pair_t, msa_t
+
+
 def design_step(target_feat, msa_feat, ids, offset, seq_mask, act_const, aatype, emsa, prm,
-                depths, keys, use_dropout, tables, dtype=torch.float64):
+                depths, keys, use_dropout, tables, recycles=0, dtype=torch.float64):
     """The trunk of one design step, input features to the structure-module
     outputs (modules_multimer.py:441-700, EmbeddingsAndEvoformer, then
-    AlphaFoldIteration's structure module and heads): the embedder; the
-    template embedding added to the pair (:530-551, act_const = its eight
-    constant projections, None = no template); the extra-MSA stack with its
-    mask at zero (the design step's extra MSA; `emsa` is any [S_e, N, 64]);
-    the main stack; single = single_activations(msa[0]); structure_heads.
-    `prm` maps 'emb', 'tpl', 'extra', 'main', 'post' to flat parameter
-    dicts; `depths` and `keys` ('tpl', 'extra', 'main', 'fold') give each
-    stack its depth and its JAX key."""
-    msa, pair = embedder(target_feat, msa_feat, *ids, prm["emb"], offset=offset, dtype=dtype)
+    AlphaFoldIteration's structure module and heads): the embedder plus the
+    three recycle terms; the template embedding added to the pair (:530-551,
+    act_const = its eight constant projections, None = no template); the
+    extra-MSA stack with its mask at zero (the design step's extra MSA;
+    `emsa` is any [S_e, N, 64]); the main stack; single =
+    single_activations(msa[0]); structure_heads.  `prm` maps 'emb', 'tpl',
+    'extra', 'main', 'post' to flat parameter dicts; `depths` and `keys`
+    ('tpl', 'extra', 'main', 'fold') give each stack its depth and its JAX
+    key.  With `recycles` > 0 the step runs that many forward-only passes
+    first (bindcraft/af2.py:195-202), each feeding its atoms, pair and
+    msa[0] to the next pass's recycle terms under stop_gradient; `keys` is
+    then a list of recycles + 1 such dicts, one per pass."""
+    keys = keys if isinstance(keys, (list, tuple)) else [keys]
+    if len(keys) != recycles + 1:
+        raise ValueError("design_step: one key dict per pass")
+    n = target_feat.shape[0]
+    prev = (torch.zeros(n, 14, 3, dtype=dtype), torch.zeros(n, n, 128, dtype=dtype),
+            torch.zeros(n, 256, dtype=dtype))
     pmask = seq_mask[:, None] * seq_mask[None, :]
-    mmask = seq_mask[None].expand(msa.shape[0], -1)
-    if act_const is not None:
-        pair = pair + template_embedding(pair, act_const, pmask, prm["tpl"], depths["tpl"],
-                                         keys["tpl"], use_dropout, dtype)
-    emask = torch.zeros(emsa.shape[:2], dtype=dtype)
-    _, pair = evoformer_stack(emsa, pair, emask, pmask, prm["extra"], depths["extra"], keys["extra"],
-                              use_dropout, is_extra_msa=True, dtype=dtype)
-    msa, pair = evoformer_stack(msa, pair, mmask, pmask, prm["main"], depths["main"], keys["main"],
-                                use_dropout, dtype=dtype)
-    single = linear(msa[0], Params(prm["emb"], "param/single_activations/", dtype))
-    return structure_heads(single, pair, seq_mask, aatype, prm["post"], depths["fold"], keys["fold"],
-                           use_dropout, tables, dtype)
+    for p in range(recycles + 1):
+        final = p == recycles
+        with (torch.enable_grad() if final else torch.no_grad()):
+            msa, pair = embedder(target_feat, msa_feat, *ids, prm["emb"], offset=offset,
+                                 dtype=dtype)
+            pair_t, msa_t = recycle_terms(aatype, *prev, prm["emb"], dtype)
+            pair = pair + pair_t
+            msa = torch.cat([msa[:1] + msa_t[None], msa[1:]], 0)
+            mmask = seq_mask[None].expand(msa.shape[0], -1)
+            k = keys[p]
+            if act_const is not None:
+                pair = pair + template_embedding(pair, act_const, pmask, prm["tpl"], depths["tpl"],
+                                                 k["tpl"], use_dropout, dtype)
+            emask = torch.zeros(emsa.shape[:2], dtype=dtype)
+            _, pair = evoformer_stack(emsa, pair, emask, pmask, prm["extra"], depths["extra"],
+                                      k["extra"], use_dropout, is_extra_msa=True, dtype=dtype)
+            msa, pair = evoformer_stack(msa, pair, mmask, pmask, prm["main"], depths["main"],
+                                        k["main"], use_dropout, dtype=dtype)
+            single = linear(msa[0], Params(prm["emb"], "param/single_activations/", dtype))
+            out = structure_heads(single, pair, seq_mask, aatype, prm["post"], depths["fold"],
+                                  k["fold"], use_dropout, tables, dtype)
+        if not final:
+            prev = (out[0].detach(), pair.detach(), msa[0].detach())
+    return out
 
 
 # ---------------------------------------------------------------------------
@@ -729,13 +795,13 @@ def design_inputs(feat, prof):
 
 
 def design_step_seq(logits, flags, scalars, ids, offset, seq_mask, act_const, emsa, prm, depths,
-                    keys, use_dropout, tables, bias=None, dtype=torch.float64):
+                    keys, use_dropout, tables, bias=None, recycles=0, dtype=torch.float64):
     """design_step from the designed logits: sequence_features ->
     design_inputs -> design_step (one MSA row)."""
     feat, prof = sequence_features(logits, flags, *scalars, bias=bias)
     tf, mf, aatype = design_inputs(feat, prof)
     return design_step(tf, mf, ids, offset, seq_mask, act_const, aatype, emsa, prm, depths, keys,
-                       use_dropout, tables, dtype=dtype)
+                       use_dropout, tables, recycles=recycles, dtype=dtype)
 
 
 # ---------------------------------------------------------------------------

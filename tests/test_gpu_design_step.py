@@ -35,12 +35,15 @@ def _extra_params(depth, rng):
     return prm
 
 
-@pytest.mark.parametrize("n,with_template,dropout", [(32, False, False), (64, False, True),
-                                                     (32, True, False), (32, True, True)])
-def test_design_step_parity(cuda, n, with_template, dropout):
-    print(f"design step n={n} template={with_template} dropout={dropout}", flush=True)
+@pytest.mark.parametrize("n,with_template,dropout,recycles", [
+    (32, False, False, 0), (64, False, True, 0), (32, True, False, 0), (32, True, True, 0),
+    # forward-only passes first, each with its own dropout keys
+    (32, True, True, 1), (32, False, False, 2)])
+def test_design_step_parity(cuda, n, with_template, dropout, recycles):
+    print(f"design step n={n} template={with_template} dropout={dropout} recycles={recycles}",
+          flush=True)
     depths = {"tpl": 1, "extra": 1, "main": 1, "fold": 2}
-    rng = np.random.default_rng(9000 + n + int(with_template) + 2 * int(dropout))
+    rng = np.random.default_rng(9000 + n + int(with_template) + 2 * int(dropout) + 4 * recycles)
     prm = {"emb": bparams.init_embedder_params(rng),
            "tpl": bparams.init_template_embedding_params(depths["tpl"], rng, gates="random",
                                                          ln="random"),
@@ -49,7 +52,14 @@ def test_design_step_parity(cuda, n, with_template, dropout):
            "post": bparams.init_structure_heads_params(rng, final="random", ln="random")}
     tables = bparams.init_residue_tables(rng)
     prm["post"].update({f"const/{k}": v for k, v in tables.items()})
-    tag = f"{n}_{int(with_template)}_{int(dropout)}"  # one directory set per case
+    if recycles:
+        # The distogram term is a step function of the previous pass's atoms:
+        # a pair whose GPU and oracle positions straddle a bin break picks a
+        # different weight row.  Scaling prev_pos_linear's rows bounds each
+        # such flip; the bins themselves are pinned exactly by
+        # tests/test_gpu_recycle.py on shared positions.
+        prm["emb"]["param/prev_pos_linear/weights"] *= 1e-3
+    tag = f"{n}_{int(with_template)}_{int(dropout)}_{recycles}"  # one directory set per case
     dirs = [weights_dir(prm[k], f"ds_{k}_{tag}") for k in ("emb", "tpl", "extra", "main", "post")]
 
     s = 1
@@ -65,9 +75,11 @@ def test_design_step_parity(cuda, n, with_template, dropout):
     act_const = (0.5 * rng.standard_normal((n, n, 64))).astype(np.float32) if with_template else None
     aatype = rng.integers(0, 21, n).astype(np.float32)
     emsa = rng.standard_normal((1, n, C_E))
-    keys = {k: J.prng_key(300 + i) for i, k in enumerate(("tpl", "extra", "main", "fold"))}
-    seeds = torch.tensor([[int(keys[k][0]), int(keys[k][1]), 1]
-                          for k in ("tpl", "extra", "main", "fold")], dtype=torch.int64)
+    stacks = ("tpl", "extra", "main", "fold")
+    keys = [{k: J.prng_key(300 + 10 * p + i) for i, k in enumerate(stacks)}
+            for p in range(recycles + 1)]
+    seeds = torch.tensor([[int(kp[k][0]), int(kp[k][1]), 1] for kp in keys for k in stacks],
+                         dtype=torch.int64)
     shapes = ((n, 14, 3), (n, n, 64), (n, n, 64), (n, 50), (n, 37))
     cts = [rng.standard_normal(sh).astype(np.float32) for sh in shapes]
 
@@ -76,7 +88,8 @@ def test_design_step_parity(cuda, n, with_template, dropout):
     ref = af2.design_step(tft, mft, ids, None, torch.as_tensor(seq_mask, dtype=D),
                           None if act_const is None else torch.as_tensor(act_const, dtype=D),
                           aatype, torch.as_tensor(emsa, dtype=D), prm, depths,
-                          keys if dropout else {k: None for k in keys}, dropout, tables)
+                          keys if dropout else [{k: None for k in stacks}] * (recycles + 1),
+                          dropout, tables, recycles=recycles)
     loss = sum((r * torch.as_tensor(c, dtype=D)).sum() for r, c in zip(ref, cts))
     ref = [r.detach() for r in ref] + list(torch.autograd.grad(loss, (tft, mft)))
 
@@ -85,7 +98,7 @@ def test_design_step_parity(cuda, n, with_template, dropout):
                                          depths["fold"]))
     outs, save = step.forward(T(tf), T(mf), [T(x) for x in ids], T(seq_mask), T(aatype),
                               act_const=T(act_const), seeds=seeds.to(torch.uint32).to(cuda),
-                              dropout=dropout)
+                              dropout=dropout, recycles=recycles)
     dtf, dmf = step.backward([T(c) for c in cts], T(tf), T(seq_mask), T(aatype), save,
                              with_template=with_template, dropout=dropout)
     torch.cuda.synchronize()
