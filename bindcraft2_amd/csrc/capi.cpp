@@ -893,6 +893,14 @@ const DesignStepW& ds_w(const char* emb, const char* tpl, const char* extra, con
   w.extra = stack_w(extra, (int)de, StackKind::PAIR_ONLY);
   w.main = stack_w(main, (int)dm, StackKind::EVO);
   w.sh = sh_w(post);
+  WeightStore& pws = weights(post);
+  if (pws.has("const/atom37_to_atom14") && pws.has("const/atom37_mask")) {
+    if (pws.host("const/atom37_to_atom14").data.size() != 21u * 37u ||
+        pws.host("const/atom37_mask").data.size() != 21u * 37u)
+      throw std::runtime_error("design step: the atom37 tables must be [21,37]");
+    w.a37_14 = pws.f32("const/atom37_to_atom14");
+    w.a37_mask = pws.f32("const/atom37_mask");
+  }
   std::lock_guard<std::mutex> lk(g_mu);
   return g_ds.emplace(key, w).first->second;
 }
@@ -1024,9 +1032,10 @@ int bc2n_design_step_seq_fwd(void* stream, const float* logits, const uint8_t* f
                              const char* emb_dir, const char* tpl_dir, const char* extra_dir,
                              const char* main_dir, const char* post_dir, float* atom14,
                              float* distogram, float* pae, float* plddt, float* expres,
-                             const int32_t* interface_asym, float* conf_plddt, float* conf_pae,
-                             float* ptm, float* iptm, float* iptm_per_residue, float* expres_ca,
-                             void* save) {
+                             const float* tpl_atoms37, const float* tpl_mask37, float* atom37,
+                             float* atom37_mask, const int32_t* interface_asym,
+                             float* conf_plddt, float* conf_pae, float* ptm, float* iptm,
+                             float* iptm_per_residue, float* expres_ca, void* save) {
   return guarded([&] {
     need(logits && flags && scalars && residue_index && asym_id && entity_id && sym_id &&
              seq_mask && save, "null operand");
@@ -1039,6 +1048,7 @@ int bc2n_design_step_seq_fwd(void* stream, const float* logits, const uint8_t* f
     design_step_seq_fwd(as_stream(stream), w, N, logits, flags, aa_bias, scalars, omitted_half,
                         residue_index, asym_id, entity_id, sym_id, offset, seq_mask, act_const,
                         seeds, dropout != 0, (int)recycles, atom14, distogram, pae, plddt, expres,
+                        AtomsOut{tpl_atoms37, tpl_mask37, atom37, atom37_mask},
                         ConfOut{interface_asym, conf_plddt, conf_pae, ptm, iptm, iptm_per_residue,
                                 expres_ca},
                         save);
@@ -1049,7 +1059,7 @@ int bc2n_design_step_seq_bwd(void* stream, const float* logits, const uint8_t* f
                              const float* aa_bias, const float* scalars, float omitted_half,
                              const float* seq_mask, int64_t with_template,
                              const float* d_atom14, const float* d_distogram, const float* d_pae,
-                             const float* d_plddt, const float* d_expres,
+                             const float* d_plddt, const float* d_expres, const float* d_atom37,
                              const int32_t* interface_asym, const float* d_conf_plddt,
                              const float* d_conf_pae, const float* d_ptm, const float* d_iptm,
                              const float* d_iptm_per_residue, const float* d_expres_ca, void* save,
@@ -1064,7 +1074,7 @@ int bc2n_design_step_seq_bwd(void* stream, const float* logits, const uint8_t* f
         ds_w(emb_dir, tpl_dir, extra_dir, main_dir, post_dir, d_tpl, d_extra, d_main, d_fold);
     design_step_seq_bwd(as_stream(stream), w, N, logits, flags, aa_bias, scalars, omitted_half,
                         seq_mask, with_template != 0, dropout != 0, save, d_atom14, d_distogram,
-                        d_pae, d_plddt, d_expres,
+                        d_pae, d_plddt, d_expres, d_atom37,
                         ConfCt{interface_asym, d_conf_plddt, d_conf_pae, d_ptm, d_iptm,
                                d_iptm_per_residue, d_expres_ca},
                         d_logits);

@@ -24,6 +24,9 @@ struct DesignStepW {
   TplEmbedW tpl;
   StackW extra, main;
   StructHeadsW sh;
+  // the atom37 gather (residx_atom37_to_atom14, atom37_mask [21][37]); null
+  // when the structure module's directory holds no such tables
+  const float *a37_14 = nullptr, *a37_mask = nullptr;
   int d_tpl = 0, d_extra = 0, d_main = 0, d_fold = 0;
 };
 
@@ -72,6 +75,18 @@ struct ConfCt {
               *iptm_pr = nullptr, *expres_ca = nullptr;
   bool any() const { return plddt || pae || ptm || iptm || iptm_pr || expres_ca; }
 };
+// The reference step's atoms (native/design_step.cuh:77-80, 1162-1168): the
+// atom14 prediction gathered to atom37 (times restype_atom37_mask[aatype] *
+// seq_mask) and, given the template's atoms, superposed on them by a Kabsch
+// of the CA atoms of the TEMPLATE-and-not-DESIGN residues (flags bits 1, 0;
+// bindcraft/af2.py:89-97, bindcraft/protein.py:75-83).  Its cotangent joins
+// the atom14 one in the backward (the rotation is under stop_gradient).
+struct AtomsOut {
+  const float* tpl37 = nullptr;   // template atoms [N][37][3], or null (no alignment)
+  const float* tplm37 = nullptr;  // their mask [N][37]
+  float* atom37 = nullptr;        // [N][37][3], or null (no atom37 output)
+  float* mask37 = nullptr;        // [N][37]
+};
 size_t design_step_seq_save_bytes(const DesignStepW& w, int N);
 void design_step_seq_fwd(hipStream_t st, const DesignStepW& w, int N, const float* logits,
                          const uint8_t* flags, const float* bias, const float* sc4,
@@ -79,12 +94,12 @@ void design_step_seq_fwd(hipStream_t st, const DesignStepW& w, int N, const floa
                          const float* si, const int32_t* offset, const float* seq_mask,
                          const float* act_const, const uint32_t* seeds, bool dropout,
                          int recycles, float* atom14, float* dgram, float* pae, float* plddt,
-                         float* expres, const ConfOut& conf, void* save);
+                         float* expres, const AtomsOut& atoms, const ConfOut& conf, void* save);
 void design_step_seq_bwd(hipStream_t st, const DesignStepW& w, int N, const float* logits,
                          const uint8_t* flags, const float* bias, const float* sc4,
                          float omitted_half, const float* seq_mask, bool with_template,
                          bool dropout, void* save, const float* datom, const float* ddgram,
                          const float* dpae, const float* dplddt, const float* dexpres,
-                         const ConfCt& conf, float* d_logits);
+                         const float* datom37, const ConfCt& conf, float* d_logits);
 
 }  // namespace bc2n

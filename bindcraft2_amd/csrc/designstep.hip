@@ -31,7 +31,7 @@ constexpr int CM = 256, CZ = 128, CS = 384;
 // computed.  The backward refuses a buffer whose parts differ from the ones
 // it is asked to differentiate, instead of reading memory never written.
 constexpr uint32_t DS_MAGIC = 0xBC2D0001u, SEQ_MAGIC = 0xBC2D0002u;
-constexpr uint32_t HAS_TEMPLATE = 1u, HAS_CONFIDENCE = 2u;
+constexpr uint32_t HAS_TEMPLATE = 1u, HAS_CONFIDENCE = 2u, HAS_ATOM37 = 4u;
 
 __global__ void hdr_set_kernel(uint32_t* h, uint32_t magic, uint32_t flags) {
   if (threadIdx.x == 0) {
@@ -63,7 +63,9 @@ long hdr_flags(hipStream_t st, const uint32_t* h, uint32_t magic, const char* wh
 void hdr_require(long flags, uint32_t bit, bool want, const char* what) {
   if (flags < 0 || ((flags & bit) != 0) == want) return;
   throw std::invalid_argument(std::string(what) + (want ? ": the backward asks for " : ": the backward omits ") +
-                              (bit == HAS_TEMPLATE ? "the template embedding" : "the confidence metrics") +
+                              (bit == HAS_TEMPLATE    ? "the template embedding"
+                               : bit == HAS_ATOM37 ? "the atom37 positions"
+                                                   : "the confidence metrics") +
                               (want ? ", which the forward did not compute" : ", which the forward computed"));
 }
 
@@ -397,7 +399,11 @@ struct SeqExtra {
     ll = c.template take<float>((size_t)N * CONF_LBINS);
     pl = c.template take<float>((size_t)N * N * CONF_PBINS);
     el = c.template take<float>((size_t)N * CONF_EXPRES);
+    kab = c.template take<float>(64);
+    d14 = c.template take<float>((size_t)N * 14 * 3);
   }
+  float* kab;  // the superposition: R [3][3], centres of the prediction and template
+  float* d14;  // the atom14 cotangent with the atom37 one folded in
   char* conf;
   float *dl, *dp, *de;  // head-logit cotangents with the confidence terms added
   float *ll, *pl, *el;  // the head logits the confidence metrics were computed from
@@ -414,6 +420,223 @@ void add_into(hipStream_t st, const float* a, const float* b, long n, float* y) 
 
 }  // namespace
 
+// ------------------------------------------------------ atom37 + alignment
+constexpr int A37 = 37, CA37 = 1;
+constexpr uint8_t F_DESIGN = 1u, F_TEMPLATE = 2u;  // bindcraft/protein.py:42-51
+
+// atom37[i][a] = atom14[i][a37_14[aat][a]] * ex, ex = a37_mask[aat][a] * seq_mask[i]
+__global__ void atom37_kernel(const float* __restrict__ atom14, const float* __restrict__ aatype,
+                              const float* __restrict__ seq_mask,
+                              const float* __restrict__ a37_14,
+                              const float* __restrict__ a37_mask, int N,
+                              float* __restrict__ atom37, float* __restrict__ mask37) {
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= N * A37) return;
+  const int i = e / A37, a = e % A37;
+  const int aat = min(max((int)aatype[i], 0), 20);
+  const float ex = a37_mask[aat * A37 + a] * (seq_mask[i] != 0.f ? 1.f : 0.f);
+  const int j = (int)a37_14[aat * A37 + a];
+#pragma unroll
+  for (int c = 0; c < 3; ++c) atom37[(long)e * 3 + c] = atom14[((long)i * 14 + j) * 3 + c] * ex;
+  mask37[e] = ex;
+}
+
+// The 3x3 SVD by one-sided Jacobi (Hestenes; Golub & Van Loan 8.6.3): rotate
+// column pairs of A until orthogonal, accumulating the rotations in V; the
+// column norms are the singular values and the normalised columns U.
+__device__ void svd3(const double (&H)[3][3], double (&U)[3][3], double (&S)[3], double (&V)[3][3]) {
+  double A[3][3];
+  for (int i = 0; i < 3; ++i)
+    for (int j = 0; j < 3; ++j) {
+      A[i][j] = H[i][j];
+      V[i][j] = i == j ? 1.0 : 0.0;
+    }
+  for (int sweep = 0; sweep < 30; ++sweep) {
+    double off = 0.0;
+    for (int p = 0; p < 2; ++p)
+      for (int q = p + 1; q < 3; ++q) {
+        double al = 0, be = 0, ga = 0;
+        for (int i = 0; i < 3; ++i) {
+          al += A[i][p] * A[i][p];
+          be += A[i][q] * A[i][q];
+          ga += A[i][p] * A[i][q];
+        }
+        if (ga == 0.0 || fabs(ga) <= 1e-15 * sqrt(al * be)) continue;
+        off = fmax(off, fabs(ga) / sqrt(al * be));
+        const double z = (be - al) / (2.0 * ga);
+        const double t = (z >= 0 ? 1.0 : -1.0) / (fabs(z) + sqrt(1.0 + z * z));
+        const double c = 1.0 / sqrt(1.0 + t * t), s = c * t;
+        for (int i = 0; i < 3; ++i) {
+          const double ap = A[i][p], aq = A[i][q];
+          A[i][p] = c * ap - s * aq;
+          A[i][q] = s * ap + c * aq;
+          const double vp = V[i][p], vq = V[i][q];
+          V[i][p] = c * vp - s * vq;
+          V[i][q] = s * vp + c * vq;
+        }
+      }
+    if (off < 1e-15) break;
+  }
+  for (int j = 0; j < 3; ++j) {
+    double n = 0;
+    for (int i = 0; i < 3; ++i) n += A[i][j] * A[i][j];
+    S[j] = sqrt(n);
+  }
+  // descending singular values (the determinant fix acts on the smallest)
+  for (int a = 0; a < 2; ++a)
+    for (int b = a + 1; b < 3; ++b)
+      if (S[b] > S[a]) {
+        double t = S[a]; S[a] = S[b]; S[b] = t;
+        for (int i = 0; i < 3; ++i) {
+          t = A[i][a]; A[i][a] = A[i][b]; A[i][b] = t;
+          t = V[i][a]; V[i][a] = V[i][b]; V[i][b] = t;
+        }
+      }
+  for (int j = 0; j < 3; ++j)
+    for (int i = 0; i < 3; ++i) U[i][j] = S[j] > 0 ? A[i][j] / S[j] : 0.0;
+  // a vanishing smallest singular value leaves its left vector free: complete
+  // U to an orthonormal basis (its sign is absorbed by the determinant fix)
+  if (!(S[2] > 1e-12 * fmax(S[0], 1e-300))) {
+    U[0][2] = U[1][0] * U[2][1] - U[2][0] * U[1][1];
+    U[1][2] = U[2][0] * U[0][1] - U[0][0] * U[2][1];
+    U[2][2] = U[0][0] * U[1][1] - U[1][0] * U[0][1];
+  }
+}
+
+// One workgroup: weighted centres and covariance of the CA atoms (f64), the
+// SVD and the rotation R = V diag(1, 1, sign det(V U^T)) U^T; kab = R, xc, yc.
+__global__ __launch_bounds__(256) void kabsch_kernel(const float* __restrict__ atom37,
+                                                     const float* __restrict__ tpl37,
+                                                     const float* __restrict__ tplm37,
+                                                     const uint8_t* __restrict__ flags, int N,
+                                                     float* __restrict__ kab) {
+  __shared__ double red[256][10];
+  const int tid = threadIdx.x;
+  auto weight = [&](int i) -> double {
+    const bool t = (flags[i] & F_TEMPLATE) && !(flags[i] & F_DESIGN);
+    return t && tplm37[(long)i * A37 + CA37] > 0.f ? 1.0 : 0.0;
+  };
+  double acc[10] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  for (int i = tid; i < N; i += 256) {
+    const double w = weight(i);
+    acc[0] += w;
+    for (int c = 0; c < 3; ++c) {
+      acc[1 + c] += w * atom37[((long)i * A37 + CA37) * 3 + c];
+      acc[4 + c] += w * tpl37[((long)i * A37 + CA37) * 3 + c];
+    }
+  }
+  auto reduce = [&](int n) {
+    for (int k = 0; k < n; ++k) red[tid][k] = acc[k];
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+      if (tid < o)
+        for (int k = 0; k < n; ++k) red[tid][k] += red[tid + o][k];
+      __syncthreads();
+    }
+    for (int k = 0; k < n; ++k) acc[k] = red[0][k];
+    __syncthreads();
+  };
+  reduce(7);
+  const double ws = acc[0], inv = 1.0 / (ws + 1e-8);
+  double xc[3], yc[3];
+  for (int c = 0; c < 3; ++c) {
+    xc[c] = acc[1 + c] * inv;
+    yc[c] = acc[4 + c] * inv;
+  }
+  for (int k = 0; k < 9; ++k) acc[k] = 0;
+  for (int i = tid; i < N; i += 256) {
+    const double w = weight(i);
+    if (w == 0.0) continue;
+    double p[3], q[3];
+    for (int c = 0; c < 3; ++c) {
+      p[c] = atom37[((long)i * A37 + CA37) * 3 + c] - xc[c];
+      q[c] = tpl37[((long)i * A37 + CA37) * 3 + c] - yc[c];
+    }
+    for (int a = 0; a < 3; ++a)
+      for (int b = 0; b < 3; ++b) acc[a * 3 + b] += w * p[a] * q[b];
+  }
+  reduce(9);
+  if (tid != 0) return;
+  double H[3][3], U[3][3], S[3], V[3][3];
+  for (int a = 0; a < 3; ++a)
+    for (int b = 0; b < 3; ++b) H[a][b] = ws > 0 ? acc[a * 3 + b] : (a == b ? 1.0 : 0.0);
+  svd3(H, U, S, V);
+  double M[3][3];  // V U^T
+  for (int i = 0; i < 3; ++i)
+    for (int j = 0; j < 3; ++j) M[i][j] = V[i][0] * U[j][0] + V[i][1] * U[j][1] + V[i][2] * U[j][2];
+  const double det = M[0][0] * (M[1][1] * M[2][2] - M[1][2] * M[2][1]) -
+                     M[0][1] * (M[1][0] * M[2][2] - M[1][2] * M[2][0]) +
+                     M[0][2] * (M[1][0] * M[2][1] - M[1][1] * M[2][0]);
+  const double d = det >= 0 ? 1.0 : -1.0;
+  for (int i = 0; i < 3; ++i)
+    for (int j = 0; j < 3; ++j)
+      kab[i * 3 + j] = (float)(V[i][0] * U[j][0] + V[i][1] * U[j][1] + d * V[i][2] * U[j][2]);
+  for (int c = 0; c < 3; ++c) {
+    kab[9 + c] = (float)xc[c];
+    kab[12 + c] = (float)yc[c];
+  }
+}
+
+// kab = the identity and zero centres (no alignment)
+__global__ void kabsch_identity_kernel(float* kab) {
+  const int t = threadIdx.x;
+  if (t < 15) kab[t] = t < 9 ? (t % 4 == 0 ? 1.f : 0.f) : 0.f;
+}
+
+// atom37 = ((atom37 - xc) R^T + yc) * ex, in place (the xc, R of the CA atoms)
+__global__ void align_apply_kernel(float* __restrict__ atom37, const float* __restrict__ mask37,
+                                   const float* __restrict__ kab, int N) {
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= N * A37) return;
+  float x[3];
+#pragma unroll
+  for (int c = 0; c < 3; ++c) x[c] = atom37[(long)e * 3 + c] - kab[9 + c];
+  const float ex = mask37[e];
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    const float y = kab[c * 3 + 0] * x[0] + kab[c * 3 + 1] * x[1] + kab[c * 3 + 2] * x[2] + kab[12 + c];
+    atom37[(long)e * 3 + c] = y * ex;
+  }
+}
+
+// d14 = d_atom14 (or 0) + the gather's transpose of (ex * d37 . R), one
+// residue per thread (a fixed order over its 37 slots)
+__global__ void atom37_bwd_kernel(const float* __restrict__ datom14, const float* __restrict__ d37,
+                                  const float* __restrict__ aatype, const float* __restrict__ seq_mask,
+                                  const float* __restrict__ a37_14,
+                                  const float* __restrict__ a37_mask,
+                                  const float* __restrict__ kab, int N, float* __restrict__ d14) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= N) return;
+  float g[14][3];
+#pragma unroll
+  for (int j = 0; j < 14; ++j)
+#pragma unroll
+    for (int c = 0; c < 3; ++c) g[j][c] = datom14 ? datom14[((long)i * 14 + j) * 3 + c] : 0.f;
+  const int aat = min(max((int)aatype[i], 0), 20);
+  const bool on = seq_mask[i] != 0.f;
+  for (int a = 0; a < A37; ++a) {
+    const float ex = on ? a37_mask[aat * A37 + a] : 0.f;
+    if (ex == 0.f) continue;
+    const int j = (int)a37_14[aat * A37 + a];
+    const float* d = d37 + ((long)i * A37 + a) * 3;
+    // both masks (the gather's and the alignment's) scale the cotangent
+    float r[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+      r[k] = (d[0] * kab[0 * 3 + k] + d[1] * kab[1 * 3 + k] + d[2] * kab[2 * 3 + k]) * ex * ex;
+#pragma unroll
+    for (int jj = 0; jj < 14; ++jj)
+      if (jj == j)
+#pragma unroll
+        for (int k = 0; k < 3; ++k) g[jj][k] += r[k];
+  }
+#pragma unroll
+  for (int j = 0; j < 14; ++j)
+#pragma unroll
+    for (int c = 0; c < 3; ++c) d14[((long)i * 14 + j) * 3 + c] = g[j][c];
+}
+
 size_t design_step_seq_save_bytes(const DesignStepW& w, int N) {
   Sizer s;
   SeqExtra<Sizer> x(s, N);
@@ -427,17 +650,41 @@ void design_step_seq_fwd(hipStream_t st, const DesignStepW& w, int N, const floa
                          const float* si, const int32_t* offset, const float* seq_mask,
                          const float* act_const, const uint32_t* seeds, bool dropout,
                          int recycles, float* atom14, float* dgram, float* pae, float* plddt,
-                         float* expres, const ConfOut& conf, void* save) {
+                         float* expres, const AtomsOut& atoms, const ConfOut& conf, void* save) {
   ds_check(w, N, 1);
   nonnull(logits, "design step logits"); nonnull(flags, "design step flags");
   nonnull(sc4, "design step scalars"); nonnull(save, "design step save");
   Carver cv(save);
   SeqExtra<Carver> x(cv, N);
-  hdr_set(st, x.hdr, SEQ_MAGIC, conf.plddt ? HAS_CONFIDENCE : 0u);
+  if (atoms.atom37) {
+    if (!w.a37_14 || !w.a37_mask)
+      throw std::invalid_argument("design step: atom37 outputs need const/atom37_to_atom14 and "
+                                  "const/atom37_mask in the structure module's directory");
+    nonnull(atoms.mask37, "design step atom37 mask");
+    if (atoms.tpl37) nonnull(atoms.tplm37, "design step template atom mask");
+  } else if (atoms.tpl37) {
+    throw std::invalid_argument("design step: the alignment needs the atom37 output");
+  }
+  hdr_set(st, x.hdr, SEQ_MAGIC,
+          (conf.plddt ? HAS_CONFIDENCE : 0u) | (atoms.atom37 ? HAS_ATOM37 : 0u));
   seqfeat_fwd(st, logits, flags, bias, SeqScalars{}, sc4, omitted_half, N, x.feat, x.prof);
   design_inputs_fwd(st, x.feat, x.prof, N, x.tf, x.mf, x.aatype);
   design_step_fwd(st, w, N, 1, x.tf, x.mf, ri, ai, ei, si, offset, seq_mask, act_const, x.aatype,
                   seeds, dropout, recycles, atom14, dgram, pae, plddt, expres, cv.p + cv.off);
+  if (atoms.atom37) {
+    KTimed kt("design.atom37", st);
+    hipLaunchKernelGGL(atom37_kernel, dim3((unsigned)((N * A37 + 255) / 256)), dim3(256), 0, st,
+                       atom14, x.aatype, seq_mask, w.a37_14, w.a37_mask, N, atoms.atom37,
+                       atoms.mask37);
+    if (atoms.tpl37) {
+      hipLaunchKernelGGL(kabsch_kernel, dim3(1), dim3(256), 0, st, atoms.atom37, atoms.tpl37,
+                         atoms.tplm37, flags, N, x.kab);
+      hipLaunchKernelGGL(align_apply_kernel, dim3((unsigned)((N * A37 + 255) / 256)), dim3(256), 0,
+                         st, atoms.atom37, atoms.mask37, x.kab, N);
+    } else {
+      hipLaunchKernelGGL(kabsch_identity_kernel, dim3(1), dim3(64), 0, st, x.kab);
+    }
+  }
   if (conf.plddt) {
     nonnull(conf.asym, "design step interface asym");
     confidence_fwd(st, plddt, pae, expres, seq_mask, conf.asym, N, conf.plddt, conf.pae, conf.ptm,
@@ -454,7 +701,7 @@ void design_step_seq_bwd(hipStream_t st, const DesignStepW& w, int N, const floa
                          float omitted_half, const float* seq_mask, bool with_template,
                          bool dropout, void* save, const float* datom, const float* ddgram,
                          const float* dpae, const float* dplddt, const float* dexpres,
-                         const ConfCt& conf, float* d_logits) {
+                         const float* datom37, const ConfCt& conf, float* d_logits) {
   ds_check(w, N, 1);
   nonnull(logits, "design step logits"); nonnull(flags, "design step flags");
   nonnull(sc4, "design step scalars"); nonnull(save, "design step save");
@@ -464,6 +711,13 @@ void design_step_seq_bwd(hipStream_t st, const DesignStepW& w, int N, const floa
   // confidence cotangents need the forward's metrics; leaving them out is allowed
   const long seq_flags = hdr_flags(st, x.hdr, SEQ_MAGIC, "design step");
   if (conf.any()) hdr_require(seq_flags, HAS_CONFIDENCE, true, "design step");
+  if (datom37) {
+    hdr_require(seq_flags, HAS_ATOM37, true, "design step");
+    KTimed kt("design.atom37_bwd", st);
+    hipLaunchKernelGGL(atom37_bwd_kernel, dim3((unsigned)((N + 63) / 64)), dim3(64), 0, st, datom,
+                       datom37, x.aatype, seq_mask, w.a37_14, w.a37_mask, x.kab, N, x.d14);
+    datom = x.d14;
+  }
   if (conf.any()) {
     // the confidence metrics' backward over the logits the forward kept (confidence requested there)
     nonnull(conf.asym, "design step interface asym");

@@ -597,15 +597,21 @@ class DesignStepSeq(DesignStep):
 
     def forward(self, logits, flags, scalars, ids, seq_mask, aa_bias=None, act_const=None,
                 offset=None, seeds=None, dropout=True, save=None, omitted_half=OMITTED_HALF,
-                interface_asym=None, recycles=0):
+                interface_asym=None, recycles=0, atom37=False, tpl_atoms37=None,
+                tpl_mask37=None):
         """-> ((atom14, distogram, pae, plddt, expres), save), plus the confidence
         metrics (plddt, pae, ptm, iptm, iptm_per_residue, expres_ca) as a third
-        element when interface_asym (i32 [N]) is given."""
+        element when interface_asym (i32 [N]) is given.  With atom37=True (or
+        template atoms tpl_atoms37 [N,37,3] / tpl_mask37 [N,37], which align
+        them) a fourth element (atom37 [N,37,3], exists mask [N,37]) follows
+        the third (None without interface_asym)."""
         n, dev = logits.shape[0], logits.device
         _check_seeds(seeds, dropout, recycles)
         e = lambda *sh: torch.empty(*sh, dtype=torch.float32, device=dev)
         outs = (e(n, 14, 3), e(n, n, 64), e(n, n, 64), e(n, 50), e(n, 37))
         conf = (e(n), e(n, n), e(1), e(1), e(n), e(n)) if interface_asym is not None else (None,) * 6
+        want37 = atom37 or tpl_atoms37 is not None
+        a37 = (e(n, 37, 3), e(n, 37)) if want37 else (None, None)
         if save is None:
             save = torch.empty(self.save_bytes(n), dtype=torch.uint8, device=dev)
         check(lib().bc2n_design_step_seq_fwd(_stream(), _ptr(logits), _ptr(flags), _ptr(aa_bias),
@@ -613,21 +619,25 @@ class DesignStepSeq(DesignStep):
                                              _ptr(offset), _ptr(seq_mask), _ptr(act_const),
                                              _ptr(seeds), n, *self.depths, int(dropout),
                                              int(recycles), *self.dirs, *map(_ptr, outs),
-                                             _ptr(interface_asym),
+                                             _ptr(tpl_atoms37), _ptr(tpl_mask37),
+                                             *map(_ptr, a37), _ptr(interface_asym),
                                              *map(_ptr, conf), _ptr(save)))
+        if want37:
+            return outs, save, (conf if interface_asym is not None else None), a37
         if interface_asym is None:
             return outs, save
         return outs, save, conf
 
     def backward(self, cts, logits, flags, scalars, seq_mask, save, aa_bias=None,
                  with_template=True, dropout=True, omitted_half=OMITTED_HALF,
-                 interface_asym=None, conf_cts=(None,) * 6):
+                 interface_asym=None, conf_cts=(None,) * 6, d_atom37=None):
         n = logits.shape[0]
         d = torch.empty_like(logits)
         check(lib().bc2n_design_step_seq_bwd(_stream(), _ptr(logits), _ptr(flags), _ptr(aa_bias),
                                              _ptr(scalars), float(omitted_half), _ptr(seq_mask),
                                              int(with_template), *map(_ptr, cts),
-                                             _ptr(interface_asym), *map(_ptr, conf_cts),
+                                             _ptr(d_atom37), _ptr(interface_asym),
+                                             *map(_ptr, conf_cts),
                                              _ptr(save), n, *self.depths, int(dropout),
                                              *self.dirs, _ptr(d)))
         return d

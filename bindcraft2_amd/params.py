@@ -366,9 +366,11 @@ def init_structure_heads_params(rng, final="random", ln="identity"):
 def init_residue_tables(rng):
     """Random residue tables of the shapes the structure module reads
     (const/default_frame [21,8,4,4] rigid 4x4 frames, const/atom14_to_group
-    [21,14], const/atom14_lit_pos [21,14,3], const/atom14_mask [21,14]).  The
-    sidechain is table-driven, so random tables exercise every path; the real
-    ones come from the model's residue_constants."""
+    [21,14], const/atom14_lit_pos [21,14,3], const/atom14_mask [21,14]) and
+    the design step's atom37 gather (const/atom37_to_atom14 [21,37],
+    const/atom37_mask [21,37]).  Both are table-driven, so random tables
+    exercise every path; the real ones come from the model's
+    residue_constants."""
     q = rng.standard_normal((21, 8, 4))
     q /= np.linalg.norm(q, axis=-1, keepdims=True)
     w, x, y, z = q[..., 0], q[..., 1], q[..., 2], q[..., 3]
@@ -381,19 +383,38 @@ def init_residue_tables(rng):
     fr[..., :3, 3] = 1.5 * rng.standard_normal((21, 8, 3))
     fr[..., 3, 3] = 1.0
     fr[:, 0] = np.eye(4)  # the backbone group is the backbone frame
-    return {"default_frame": fr.astype(np.float32),
-            "atom14_to_group": rng.integers(0, 8, (21, 14)).astype(np.float32),
-            "atom14_lit_pos": (1.5 * rng.standard_normal((21, 14, 3))).astype(np.float32),
-            "atom14_mask": (rng.random((21, 14)) < 0.8).astype(np.float32)}
+    out = {"default_frame": fr.astype(np.float32),
+           "atom14_to_group": rng.integers(0, 8, (21, 14)).astype(np.float32),
+           "atom14_lit_pos": (1.5 * rng.standard_normal((21, 14, 3))).astype(np.float32),
+           "atom14_mask": (rng.random((21, 14)) < 0.8).astype(np.float32)}
+    # the atom37 gather of the design step's outputs: every atom37 slot reads
+    # one atom14 slot (CA always slot 1, as in residue_constants)
+    a37 = rng.integers(0, 14, (21, 37))
+    a37[:, 1] = 1
+    m37 = (rng.random((21, 37)) < 0.5).astype(np.float32)
+    m37[:, 1] = 1.0
+    out["atom37_to_atom14"] = a37.astype(np.float32)
+    out["atom37_mask"] = m37
+    return out
 
 
 def residue_tables_from(rc):
-    """The four tables from a residue_constants module (alphafold.common),
-    in the layout the weights directory stores (const/...)."""
+    """The residue tables from a residue_constants module (alphafold.common),
+    in the layout the weights directory stores (const/...): the structure
+    module's four and the atom37 gather's two."""
+    # residx_atom37_to_atom14 per restype (the make_atom14_masks tables):
+    # restypes order, UNK all zeros
+    a37 = np.zeros((21, 37), np.float32)
+    for r, rt in enumerate(rc.restypes):
+        for j, name in enumerate(rc.restype_name_to_atom14_names[rc.restype_1to3[rt]]):
+            if name:
+                a37[r, rc.atom_order[name]] = j
     return {"default_frame": np.asarray(rc.restype_rigid_group_default_frame, np.float32),
             "atom14_to_group": np.asarray(rc.restype_atom14_to_rigid_group, np.float32),
             "atom14_lit_pos": np.asarray(rc.restype_atom14_rigid_group_positions, np.float32),
-            "atom14_mask": np.asarray(rc.restype_atom14_mask, np.float32)}
+            "atom14_mask": np.asarray(rc.restype_atom14_mask, np.float32),
+            "atom37_to_atom14": a37,
+            "atom37_mask": np.asarray(rc.restype_atom37_mask, np.float32)}
 
 
 def write_manifest(out_dir, params):

@@ -467,10 +467,20 @@ int bc2n_design_inputs_bwd(void* stream, const float* d_target_feat, const float
  * target_feat, msa_feat, aatype (derived) and S (1).  When conf_plddt is
  * non-NULL the step also returns the confidence metrics of its head logits
  * (as bc2n_confidence_fwd: plddt, pae f32[N,N], ptm, iptm, iptm_per_residue,
- * expres_ca; interface_asym i32[N]), the reference step's Outputs.  bwd: the
- * five head cotangents and those of the confidence metrics (any may be NULL;
- * the latter need a forward that computed them) -> d_logits f32[N,20].  save
- * holds bc2n_design_step_seq_save_bytes() bytes.
+ * expres_ca; interface_asym i32[N]), the reference step's Outputs.  When
+ * atom37 is non-NULL the step also returns the prediction's atom37 positions
+ * f32[N,37,3] and their exists mask f32[N,37] (the atom14 positions gathered
+ * by residx_atom37_to_atom14 times restype_atom37_mask[aatype] * seq_mask,
+ * tables const/atom37_to_atom14 and const/atom37_mask in post_dir); given
+ * the template's atoms tpl_atoms37 f32[N,37,3] and mask f32[N,37] they are
+ * superposed on them, as the reference step's atoms are
+ * (native/design_step.cuh:1162-1168): a Kabsch of the CA atoms of the
+ * residues flagged TEMPLATE and not DESIGN (flags bits 1, 0;
+ * bindcraft/af2.py:89-97, bindcraft/protein.py:75-83), its rotation under
+ * stop_gradient.  bwd: the five head cotangents, the atom37 one and those of
+ * the confidence metrics (any may be NULL; the atom37 and confidence ones
+ * need a forward that computed them) -> d_logits f32[N,20].  save holds
+ * bc2n_design_step_seq_save_bytes() bytes.
  * ---------------------------------------------------------------------- */
 size_t bc2n_design_step_seq_save_bytes(const char* emb_dir, const char* tpl_dir,
                                        const char* extra_dir, const char* main_dir,
@@ -486,14 +496,15 @@ int bc2n_design_step_seq_fwd(void* stream, const float* logits, const uint8_t* f
                              const char* emb_dir, const char* tpl_dir, const char* extra_dir,
                              const char* main_dir, const char* post_dir, float* atom14,
                              float* distogram, float* pae, float* plddt, float* expres,
-                             const int32_t* interface_asym, float* conf_plddt, float* conf_pae,
-                             float* ptm, float* iptm, float* iptm_per_residue, float* expres_ca,
-                             void* save);
+                             const float* tpl_atoms37, const float* tpl_mask37, float* atom37,
+                             float* atom37_mask, const int32_t* interface_asym,
+                             float* conf_plddt, float* conf_pae, float* ptm, float* iptm,
+                             float* iptm_per_residue, float* expres_ca, void* save);
 int bc2n_design_step_seq_bwd(void* stream, const float* logits, const uint8_t* flags,
                              const float* aa_bias, const float* scalars, float omitted_half,
                              const float* seq_mask, int64_t with_template,
                              const float* d_atom14, const float* d_distogram, const float* d_pae,
-                             const float* d_plddt, const float* d_expres,
+                             const float* d_plddt, const float* d_expres, const float* d_atom37,
                              const int32_t* interface_asym, const float* d_conf_plddt,
                              const float* d_conf_pae, const float* d_ptm, const float* d_iptm,
                              const float* d_iptm_per_residue, const float* d_expres_ca, void* save,

@@ -19,8 +19,11 @@ softmax==1 closed form; global attention against a pure-Python loop, its
 S=1 closed form and its fully-masked-column closed form; the pair-only extra
 block against the full extra-MSA iteration on a zero mask; the recycle
 terms' distogram against a loop over the squared breaks, and the first-pass
-terms against their closed form (bias + offsets); gradients against central
-finite differences.
+terms against their closed form (bias + offsets); Kabsch against scipy's
+weighted Rotation.align_vectors, an exact rigid motion (recovered exactly), a
+mirror image (a proper rotation still) and no weights (the identity); the
+atom37 gather against a loop; gradients against central finite
+differences.
 """
 import math
 
@@ -794,14 +797,71 @@ def design_inputs(feat, prof):
     return tf, mf, feat.detach().argmax(-1).numpy().astype(np.float32)
 
 
+def atom14_to_atom37(atom14, aatype, seq_mask, tables):
+    """all_atom.atom14_to_atom37 as the design step uses it: a gather by
+    residx_atom37_to_atom14 times atom37_atom_exists =
+    restype_atom37_mask[aatype] * seq_mask (bindcraft/af2.py:187-192 builds
+    both from aatype).  tables['atom37_to_atom14'], ['atom37_mask'] [21, 37].
+    Returns (atom37 [N, 37, 3], exists [N, 37])."""
+    aat = torch.as_tensor(np.asarray(aatype)).long().clamp(0, 20)
+    idx = torch.as_tensor(tables["atom37_to_atom14"]).long()[aat]            # [N, 37]
+    ex = torch.as_tensor(tables["atom37_mask"], dtype=atom14.dtype)[aat] * seq_mask[:, None]
+    a37 = torch.gather(atom14, 1, idx[..., None].expand(-1, -1, 3)) * ex[..., None]
+    return a37, ex
+
+
+def kabsch(coords, ref, weights):
+    """bindcraft/protein.py:75-83: weighted centroids, covariance
+    ((x - xc) w)^T (y - yc) (the identity when no weight is set), SVD, and the
+    rotation R = V diag(1, 1, sign det(V U^T)) U^T that maps centred coords
+    onto centred ref.  Returns (R, coords centre, ref centre)."""
+    w = weights.to(coords.dtype)
+    ws = w.sum() + 1e-8
+    xc = (coords * w[:, None]).sum(0) / ws
+    yc = (ref * w[:, None]).sum(0) / ws
+    cov = ((coords - xc) * w[:, None]).T @ (ref - yc)
+    if float(w.sum()) <= 0:
+        cov = torch.eye(3, dtype=coords.dtype)
+    u, _, vt = torch.linalg.svd(cov)
+    d = torch.sign(torch.linalg.det(vt.T @ u.T))
+    R = (vt.T * torch.tensor([1.0, 1.0, float(d)], dtype=coords.dtype)) @ u.T
+    return R, xc, yc
+
+
+DESIGN, TEMPLATE = 1, 2  # bindcraft/protein.py:42-51 ResidueFlags
+CA37 = 1                 # residue_constants.atom_order['CA']
+
+
+def align_to_template(atom37, exists, tpl_atoms37, tpl_mask37, flags):
+    """bindcraft/af2.py:89-97 align_prediction_to_target_template: Kabsch of
+    the predicted CA (under stop_gradient) onto the template's CA over the
+    TEMPLATE-and-not-DESIGN residues whose template CA exists, then every
+    predicted atom moved by it; atoms that do not exist are zero."""
+    f = np.asarray(flags).astype(np.int64)
+    sel = torch.as_tensor(((f & TEMPLATE) != 0) & ((f & DESIGN) == 0))
+    w = (sel & (torch.as_tensor(tpl_mask37)[:, CA37] > 0)).to(atom37.dtype)
+    R, xc, yc = kabsch(atom37[:, CA37].detach(), torch.as_tensor(tpl_atoms37)[:, CA37].to(
+        atom37.dtype), w)
+    out = (atom37 - xc) @ R.T + yc
+    return out * exists[..., None]
+
+
 def design_step_seq(logits, flags, scalars, ids, offset, seq_mask, act_const, emsa, prm, depths,
-                    keys, use_dropout, tables, bias=None, recycles=0, dtype=torch.float64):
+                    keys, use_dropout, tables, bias=None, recycles=0, tpl_atoms37=None,
+                    tpl_mask37=None, dtype=torch.float64):
     """design_step from the designed logits: sequence_features ->
-    design_inputs -> design_step (one MSA row)."""
+    design_inputs -> design_step (one MSA row).  With template atoms
+    (tpl_atoms37 [N,37,3], tpl_mask37 [N,37]) the outputs gain the predicted
+    atom37 positions aligned onto the template, and their exists mask (the
+    reference step's first two outputs, native/design_step.cuh:77-80)."""
     feat, prof = sequence_features(logits, flags, *scalars, bias=bias)
     tf, mf, aatype = design_inputs(feat, prof)
-    return design_step(tf, mf, ids, offset, seq_mask, act_const, aatype, emsa, prm, depths, keys,
-                       use_dropout, tables, recycles=recycles, dtype=dtype)
+    out = design_step(tf, mf, ids, offset, seq_mask, act_const, aatype, emsa, prm, depths, keys,
+                      use_dropout, tables, recycles=recycles, dtype=dtype)
+    if tpl_atoms37 is None:
+        return out
+    a37, ex = atom14_to_atom37(out[0], aatype, seq_mask, tables)
+    return tuple(out) + (align_to_template(a37, ex, tpl_atoms37, tpl_mask37, flags), ex)
 
 
 # ---------------------------------------------------------------------------

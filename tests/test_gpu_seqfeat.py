@@ -191,6 +191,9 @@ def test_design_step_save_flags(cuda):
     with pytest.raises(NativeError, match="confidence metrics, which the forward did not"):
         step.backward(cts, *args, save, with_template=False, dropout=False,
                       interface_asym=iasym, conf_cts=conf_cts)
+    with pytest.raises(NativeError, match="atom37 positions, which the forward did not"):
+        step.backward(cts, *args, save, with_template=False, dropout=False,
+                      d_atom37=T(np.ones((n, 37, 3), np.float32)))
     d_ok = step.backward(cts, *args, save, with_template=False, dropout=False)
 
     # forward with both: leaving the template out of the backward is refused,
@@ -208,3 +211,76 @@ def test_design_step_save_flags(cuda):
         step.backward(cts, *args, blank, with_template=False, dropout=False)
     torch.cuda.synchronize()
     assert torch.isfinite(d_ok).all() and torch.isfinite(d2).all()
+
+
+@pytest.mark.parametrize("align", [False, True])
+def test_design_step_seq_atom37(cuda, align):
+    """The step's atom37 output (gathered, masked) and its superposition on
+    the template's CA atoms (bindcraft/af2.py:89-97), with an atom37
+    cotangent in the loss, one recycle pass first.  Bars as the step's
+    (outputs relL2/max <= 2e-2, cos >= 0.9999; d(logits) cos >= 0.999,
+    relL2 <= 5e-2); the exists mask exactly."""
+    n, recycles = 32, 1
+    print(f"design step atom37 n={n} align={align} recycles={recycles}", flush=True)
+    depths = {"tpl": 1, "extra": 1, "main": 1, "fold": 2}
+    rng = np.random.default_rng(9300 + int(align))
+    prm = {"emb": bparams.init_embedder_params(rng),
+           "tpl": bparams.init_template_embedding_params(depths["tpl"], rng, gates="random",
+                                                         ln="random"),
+           "extra": _extra_params(depths["extra"], rng),
+           "main": bparams.init_block_params(0, rng, gates="random", ln="random"),
+           "post": bparams.init_structure_heads_params(rng, final="random", ln="random")}
+    prm["emb"]["param/prev_pos_linear/weights"] *= 1e-3  # see test_gpu_design_step.py
+    tables = bparams.init_residue_tables(rng)
+    prm["post"].update({f"const/{k}": v for k, v in tables.items()})
+    dirs = [weights_dir(prm[k], f"dsa_{k}_{int(align)}") for k in ("emb", "tpl", "extra", "main",
+                                                                    "post")]
+    x, flags, bias = _inputs(n, rng, False)
+    flags[n // 2:] |= 2  # the target chain is the template
+    scalars = (0.9, 0.1, 1.0, 1.0)
+    ids = [np.arange(n, dtype=np.float32), np.repeat([1, 2], n // 2).astype(np.float32),
+           np.repeat([1, 2], n // 2).astype(np.float32), np.ones(n, np.float32)]
+    seq_mask = np.ones(n, np.float32)
+    seq_mask[3] = 0.0
+    emsa = rng.standard_normal((1, n, 64))
+    stacks = ("tpl", "extra", "main", "fold")
+    keys = [{k: None for k in stacks}] * (recycles + 1)
+    tpl37 = (8 * rng.standard_normal((n, 37, 3))).astype(np.float32)
+    tplm37 = (rng.random((n, 37)) < 0.8).astype(np.float32)
+    tplm37[n // 2 + 1, 1] = 0.0  # a template residue without its CA is not aligned on
+    shapes = ((n, 14, 3), (n, n, 64), (n, n, 64), (n, 50), (n, 37))
+    cts = [rng.standard_normal(sh).astype(np.float32) for sh in shapes]
+    ct37 = rng.standard_normal((n, 37, 3)).astype(np.float32)
+
+    t = torch.tensor(x, dtype=D, requires_grad=True)
+    ref = af2.design_step_seq(t, flags, scalars, ids, None, torch.as_tensor(seq_mask, dtype=D),
+                              None, torch.as_tensor(emsa, dtype=D), prm, depths, keys, False,
+                              tables, recycles=recycles,
+                              tpl_atoms37=tpl37 if align else None,
+                              tpl_mask37=tplm37 if align else None)
+    if not align:  # the gather alone: the oracle's atom37 of its atom14
+        a37, ex = af2.atom14_to_atom37(ref[0], af2.design_inputs(*af2.sequence_features(
+            t, flags, *scalars))[2], torch.as_tensor(seq_mask, dtype=D), tables)
+        ref = tuple(ref) + (a37, ex)
+    loss = sum((r * torch.as_tensor(c, dtype=D)).sum() for r, c in zip(ref[:5], cts))
+    loss = loss + (ref[5] * torch.as_tensor(ct37, dtype=D)).sum()
+    (dref,) = torch.autograd.grad(loss, (t,))
+
+    T = lambda a: None if a is None else torch.as_tensor(a, device=cuda)
+    step = ops.DesignStepSeq(*dirs, depths=tuple(depths[k] for k in stacks))
+    sc = torch.tensor(scalars, dtype=torch.float32, device=cuda)
+    outs, save, _, (g37, gm37) = step.forward(
+        T(x), T(flags), sc, [T(v) for v in ids], T(seq_mask), dropout=False, recycles=recycles,
+        atom37=True, tpl_atoms37=T(tpl37) if align else None,
+        tpl_mask37=T(tplm37) if align else None)
+    dlog = step.backward([T(c) for c in cts], T(x), T(flags), sc, T(seq_mask), save,
+                         with_template=False, dropout=False, d_atom37=T(ct37))
+    torch.cuda.synchronize()
+    assert torch.equal(gm37.cpu().double(), ref[6].detach()), "atom37 exists mask"
+    for name, g, r in (("atom14", outs[0], ref[0]), ("atom37", g37, ref[5])):
+        m = metrics(g.cpu().double(), r.detach())
+        print(f"  {name}", m)
+        assert m["rel_l2"] <= 2e-2 and m["max_rel"] <= 2e-2 and m["cos"] >= 0.9999, name
+    m = metrics(dlog.cpu().double(), dref)
+    print("  d logits", m)
+    assert m["cos"] >= 0.999 and m["rel_l2"] <= 5e-2
