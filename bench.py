@@ -11,10 +11,12 @@ with dropout on (JAX-exact masks from a stack key), random-init weights
 (LeCun normal, AF2 gate init) and N(0,1) synthetic activations resident in
 HBM, 10% of residues masked.  The same line also carries `design_step_ms`:
 the one-call design step from the designed logits (sequence features,
-embedder with its recycle terms, template embedding, the three stacks, the
-8-iteration structure module, heads and confidence metrics) at the
-reference's design default of one recycle: a forward-only pass, then the
-differentiated pass forward and backward to d(logits) (`design_recycles`).
+embedder with its recycle terms, template embedding, the template's MSA row
+(S = 2 in the main stack, the reference's design shape), the three stacks,
+the 8-iteration structure module, heads, confidence metrics, and the atom37
+positions superposed on the template) at the reference's design default of
+one recycle: a forward-only pass, then the differentiated pass forward and
+backward to d(logits) (`design_recycles`).
 
 `--workload triattn` / `trimul` time BASELINE configs[1] / configs[2]
 (one module fwd+bwd, both orientations / directions); `--workload design`
@@ -510,6 +512,7 @@ def design_step_setup(n, rng, dev, m1):
     logits = 0.5 * torch.randn(n, 20, device=dev)
     flags = torch.zeros(n, dtype=torch.uint8, device=dev)
     flags[nt:] = 1  # the binder is designed; the target passes through
+    flags[:nt] = 2  # the target is the template: its MSA row joins the stack (S = 2)
     logits[:nt] = torch.nn.functional.one_hot(torch.randint(0, 20, (nt,), device=dev), 20).float()
     scalars = torch.tensor([1.0, 0.0, 1.0, 1.0], device=dev)  # the soft stage
     ids = [torch.arange(n, dtype=torch.float32, device=dev),
@@ -518,6 +521,8 @@ def design_step_setup(n, rng, dev, m1):
     iasym = (torch.arange(n, device=dev) >= nt).int()
     seqm = torch.as_tensor(m1, device=dev)
     act_const = 0.1 * torch.randn(n, n, 64, device=dev)
+    tpl37 = 8.0 * torch.randn(n, 37, 3, device=dev)  # the template's (the input) atoms
+    tplm37 = torch.ones(n, 37, device=dev)
     # the reference's design default: one forward-only recycle pass ahead of
     # the differentiated one (settings/core/default.json:38), each pass
     # with its own four stack keys
@@ -527,12 +532,14 @@ def design_step_setup(n, rng, dev, m1):
     cts = [torch.randn(*sh, device=dev) for sh in ((n, 14, 3), (n, n, 64), (n, n, 64),
                                                   (n, 50), (n, 37))]
     conf_cts = [torch.randn(*sh, device=dev) for sh in ((n,), (n, n), (1,), (1,), (n,), (n,))]
+    ct37 = torch.randn(n, 37, 3, device=dev)
 
     def step():
         step_mod.forward(logits, flags, scalars, ids, seqm, act_const=act_const, seeds=seeds,
-                         save=save, interface_asym=iasym, recycles=DESIGN_RECYCLES)
+                         save=save, interface_asym=iasym, recycles=DESIGN_RECYCLES, atom37=True,
+                         tpl_atoms37=tpl37, tpl_mask37=tplm37)
         step_mod.backward(cts, logits, flags, scalars, seqm, save, interface_asym=iasym,
-                          conf_cts=conf_cts)
+                          conf_cts=conf_cts, d_atom37=ct37)
 
     return step, save.numel()
 

@@ -894,6 +894,20 @@ const DesignStepW& ds_w(const char* emb, const char* tpl, const char* extra, con
   w.main = stack_w(main, (int)dm, StackKind::EVO);
   w.sh = sh_w(post);
   WeightStore& pws = weights(post);
+  // the template's MSA row: Linears in the embedder's directory, chi tables
+  // in the structure module's (both optional; the row needs all six)
+  auto opt = [](WeightStore& ws, const char* name, size_t n) -> const float* {
+    if (!ws.has(name)) return nullptr;
+    if (ws.host(name).data.size() != n)
+      throw std::runtime_error(std::string("design step: ") + name + " has the wrong size");
+    return ws.f32(name);
+  };
+  w.trow.w1 = opt(ews, "param/template_single_embedding/weights", 34 * 256);
+  w.trow.b1 = opt(ews, "param/template_single_embedding/bias", 256);
+  w.trow.w2 = opt(ews, "param/template_projection/weights", 256 * 256);
+  w.trow.b2 = opt(ews, "param/template_projection/bias", 256);
+  w.trow.chi_idx = opt(pws, "const/chi_atom_indices", 21 * 16);
+  w.trow.chi_mask = opt(pws, "const/chi_angles_mask", 21 * 4);
   if (pws.has("const/atom37_to_atom14") && pws.has("const/atom37_mask")) {
     if (pws.host("const/atom37_to_atom14").data.size() != 21u * 37u ||
         pws.host("const/atom37_mask").data.size() != 21u * 37u)

@@ -17,9 +17,20 @@ struct RecycleW {
   const float *s_pair = nullptr, *o_pair = nullptr;  // prev_pair_norm [128]
 };
 
+// The template's MSA row (modules_multimer.py:1080-1137): Linears from the
+// embedder's directory, chi tables (const/chi_atom_indices [21][4][4],
+// const/chi_angles_mask [21][4]) from the structure module's; null if absent.
+struct TplRowW {
+  const float *w1 = nullptr, *b1 = nullptr;  // template_single_embedding [34][256], [256]
+  const float *w2 = nullptr, *b2 = nullptr;  // template_projection [256][256], [256]
+  const float *chi_idx = nullptr, *chi_mask = nullptr;
+  bool ok() const { return w1 && b1 && w2 && b2 && chi_idx && chi_mask; }
+};
+
 struct DesignStepW {
   EmbedW emb;
   RecycleW rec;
+  TplRowW trow;
   const float *wsa = nullptr, *bsa = nullptr;  // single_activations [256][384], [384]
   TplEmbedW tpl;
   StackW extra, main;
@@ -49,13 +60,18 @@ void design_step_fwd(hipStream_t st, const DesignStepW& w, int N, int S, const f
                      const float* si, const int32_t* offset, const float* seq_mask,
                      const float* act_const, const float* aatype, const uint32_t* seeds,
                      bool dropout, int recycles, float* atom14, float* dgram, float* pae,
-                     float* plddt, float* expres, void* save);
-// Cotangents may be null (zero) -> d target_feat [N][21], d msa_feat [S][N][49].
+                     float* plddt, float* expres, void* save, const float* row = nullptr,
+                     const float* row_mask = nullptr);
+// row [N][256] / row_mask [N]: a constant MSA row appended after the
+// embedder's S rows (the template's, modules_multimer.py:608-617); the main
+// stack then runs S + 1 rows and `save` must hold design_step_save_bytes(S + 1).
+// Cotangents may be null (zero) -> d target_feat [N][21], d msa_feat [S][N][49];
+// `row` says whether the forward appended one.
 void design_step_bwd(hipStream_t st, const DesignStepW& w, int N, int S, const float* tf,
                      const float* seq_mask, bool with_template, const float* aatype,
                      bool dropout, void* save, const float* datom, const float* ddgram,
                      const float* dpae, const float* dplddt, const float* dexpres, float* dtf,
-                     float* dmf);
+                     float* dmf, bool row = false);
 
 // The same step from the designed sequence logits [N][20] (one MSA row):
 // sequence features and profile (seqfeat.h) -> target_feat, msa_feat and

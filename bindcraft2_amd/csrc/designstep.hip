@@ -31,7 +31,7 @@ constexpr int CM = 256, CZ = 128, CS = 384;
 // computed.  The backward refuses a buffer whose parts differ from the ones
 // it is asked to differentiate, instead of reading memory never written.
 constexpr uint32_t DS_MAGIC = 0xBC2D0001u, SEQ_MAGIC = 0xBC2D0002u;
-constexpr uint32_t HAS_TEMPLATE = 1u, HAS_CONFIDENCE = 2u, HAS_ATOM37 = 4u;
+constexpr uint32_t HAS_TEMPLATE = 1u, HAS_CONFIDENCE = 2u, HAS_ATOM37 = 4u, HAS_ROW = 8u;
 
 __global__ void hdr_set_kernel(uint32_t* h, uint32_t magic, uint32_t flags) {
   if (threadIdx.x == 0) {
@@ -65,6 +65,7 @@ void hdr_require(long flags, uint32_t bit, bool want, const char* what) {
   throw std::invalid_argument(std::string(what) + (want ? ": the backward asks for " : ": the backward omits ") +
                               (bit == HAS_TEMPLATE    ? "the template embedding"
                                : bit == HAS_ATOM37 ? "the atom37 positions"
+                               : bit == HAS_ROW    ? "the template's MSA row"
                                                    : "the confidence metrics") +
                               (want ? ", which the forward did not compute" : ", which the forward computed"));
 }
@@ -281,20 +282,30 @@ void design_step_fwd(hipStream_t st, const DesignStepW& w, int N, int S, const f
                      const float* si, const int32_t* offset, const float* seq_mask,
                      const float* act_const, const float* aatype, const uint32_t* seeds,
                      bool dropout, int recycles, float* atom14, float* dgram, float* pae,
-                     float* plddt, float* expres, void* save) {
-  ds_check(w, N, S);
+                     float* plddt, float* expres, void* save, const float* row,
+                     const float* row_mask) {
+  const int SM = S + (row ? 1 : 0);  // the main stack's msa rows
+  ds_check(w, N, SM);
   nonnull(seq_mask, "design step seq_mask"); nonnull(save, "design step save");
   nonnull(aatype, "design step aatype");
+  if (row) nonnull(row_mask, "design step row mask");
   if (dropout) nonnull(seeds, "design step seeds");
   if (recycles < 0 || recycles > 64) throw std::invalid_argument("design step: recycles must be in [0, 64]");
   Carver cv(save);
-  DsSave<Carver> sv(cv, w, N, S);
+  DsSave<Carver> sv(cv, w, N, SM);
   const long M = (long)N * N;
-  hdr_set(st, sv.hdr, DS_MAGIC, act_const ? HAS_TEMPLATE : 0u);
+  hdr_set(st, sv.hdr, DS_MAGIC, (act_const ? HAS_TEMPLATE : 0u) | (row ? HAS_ROW : 0u));
   {
-    const long n = std::max(M, (long)S * N);
+    const long n = std::max(M, (long)SM * N);
     hipLaunchKernelGGL(masks_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, seq_mask,
-                       N, S, sv.pmask, sv.mmask);
+                       N, SM, sv.pmask, sv.mmask);
+  }
+  if (row) {
+    // the constant row after the embedder's S rows (embed_fwd writes those only)
+    BC2N_HIP(hipMemcpyAsync(sv.msa0 + (size_t)S * N * CM, row, (size_t)N * CM * 4,
+                            hipMemcpyDeviceToDevice, st));
+    BC2N_HIP(hipMemcpyAsync(sv.mmask + (size_t)S * N, row_mask, (size_t)N * 4,
+                            hipMemcpyDeviceToDevice, st));
   }
   for (int pass = 0; pass <= recycles; ++pass) {
     // forward-only passes keep no save-sets: their stacks run detached
@@ -326,7 +337,7 @@ void design_step_fwd(hipStream_t st, const DesignStepW& w, int N, int S, const f
     }
     stack_fwd(st, w.extra, N, 1, w.d_extra, pair, nullptr, sv.pmask, nullptr, key(1), enabled(1),
               dropout, sv.pair2, nullptr, sv.extra, !last);
-    stack_fwd(st, w.main, N, S, w.d_main, sv.pair2, sv.msa0, sv.pmask, sv.mmask, key(2),
+    stack_fwd(st, w.main, N, SM, w.d_main, sv.pair2, sv.msa0, sv.pmask, sv.mmask, key(2),
               enabled(2), dropout, sv.pair3, sv.msa3, sv.main, !last);
     GemmF32 g = gemm_rows(N, CS, CM, sv.msa3, w.wsa, sv.single);
     g.bias = w.bsa;
@@ -347,22 +358,24 @@ void design_step_bwd(hipStream_t st, const DesignStepW& w, int N, int S, const f
                      const float* seq_mask, bool with_template, const float* aatype,
                      bool dropout, void* save, const float* datom, const float* ddgram,
                      const float* dpae, const float* dplddt, const float* dexpres, float* dtf,
-                     float* dmf) {
-  ds_check(w, N, S);
+                     float* dmf, bool row) {
+  const int SM = S + (row ? 1 : 0);
+  ds_check(w, N, SM);
   nonnull(seq_mask, "design step seq_mask"); nonnull(save, "design step save");
   Carver cv(save);
-  DsSave<Carver> sv(cv, w, N, S);
+  DsSave<Carver> sv(cv, w, N, SM);
   const long M = (long)N * N;
-  hdr_require(hdr_flags(st, sv.hdr, DS_MAGIC, "design step"), HAS_TEMPLATE, with_template,
-              "design step");
+  const long ds_flags = hdr_flags(st, sv.hdr, DS_MAGIC, "design step");
+  hdr_require(ds_flags, HAS_TEMPLATE, with_template, "design step");
+  hdr_require(ds_flags, HAS_ROW, row, "design step");
   structheads_bwd(st, w.sh, N, w.d_fold, sv.single, sv.pair3, seq_mask, aatype, dropout, sv.sh,
                   datom, ddgram, dpae, dplddt, dexpres, sv.dsingle, sv.dpair);
   // d msa3: row 0 from the single projection, the other rows zero
-  zero_f32(st, sv.dmsa, (long)S * N * CM);
+  zero_f32(st, sv.dmsa, (long)SM * N * CM);
   GemmF32 g = gemm_rows(N, CM, CS, sv.dsingle, w.wsa, sv.dmsa, true);
   gemm_f32(st, g, "design.gemm_single_dx");
   // the stacks accumulate in place: d pair3 -> d pair2 -> d pair1, d msa3 -> d msa0
-  stack_bwd(st, w.main, N, S, w.d_main, sv.pmask, sv.mmask, dropout, sv.main, sv.dpair, sv.dmsa,
+  stack_bwd(st, w.main, N, SM, w.d_main, sv.pmask, sv.mmask, dropout, sv.main, sv.dpair, sv.dmsa,
             sv.dpair, sv.dmsa);
   stack_bwd(st, w.extra, N, 1, w.d_extra, sv.pmask, nullptr, dropout, sv.extra, sv.dpair, nullptr,
             sv.dpair, nullptr);
@@ -401,7 +414,10 @@ struct SeqExtra {
     el = c.template take<float>((size_t)N * CONF_EXPRES);
     kab = c.template take<float>(64);
     d14 = c.template take<float>((size_t)N * 14 * 3);
+    row = c.template take<float>((size_t)N * CM);
+    rmask = c.template take<float>(N);
   }
+  float *row, *rmask;  // the template's MSA row [N][256] and its mask
   float* kab;  // the superposition: R [3][3], centres of the prediction and template
   float* d14;  // the atom14 cotangent with the atom37 one folded in
   char* conf;
@@ -637,11 +653,73 @@ __global__ void atom37_bwd_kernel(const float* __restrict__ datom14, const float
     for (int c = 0; c < 3; ++c) d14[((long)i * 14 + j) * 3 + c] = g[j][c];
 }
 
+// The template's MSA row, one workgroup per residue (modules_multimer.py:
+// 1080-1137; the template arrays as bindcraft/af2.py:153-160 builds them
+// from the input atoms): features one_hot(t, 22) with t = aatype on TEMPLATE
+// residues, else 21 (the gap), then for the 4 chi angles sin m, cos m, m
+// (atoms chi_idx[t], m = chi_mask[t] times all four present; t = 21 reads
+// the unknown type's row 20), then relu(f . W1 + b1) . W2 + b2; the row's
+// mask is m of chi 1.  Dihedral as geometry/vector.py:187-212.
+__global__ __launch_bounds__(256) void template_row_kernel(
+    const float* __restrict__ aatype, const uint8_t* __restrict__ flags,
+    const float* __restrict__ tpl37, const float* __restrict__ tplm37,
+    const float* __restrict__ chi_idx, const float* __restrict__ chi_mask,
+    const float* __restrict__ w1, const float* __restrict__ b1, const float* __restrict__ w2,
+    const float* __restrict__ b2, float* __restrict__ row, float* __restrict__ rmask) {
+  __shared__ float f[34];
+  __shared__ float hid[CM];
+  const int i = blockIdx.x, t = threadIdx.x;
+  const bool tres = (flags[i] & F_TEMPLATE) != 0;
+  const int aat = tres ? min(max((int)aatype[i], 0), 20) : 21;
+  const int g = min(aat, 20);
+  if (t < 22) f[t] = t == aat ? 1.f : 0.f;
+  if (t < 4) {
+    float p[4][3], m = chi_mask[g * 4 + t];
+    for (int k = 0; k < 4; ++k) {
+      const int a = (int)chi_idx[(g * 4 + t) * 4 + k];
+      const long o = (long)i * A37 + a;
+      m *= tres ? tplm37[o] : 0.f;
+      for (int c = 0; c < 3; ++c) p[k][c] = tres ? tpl37[o * 3 + c] : 0.f;
+    }
+    float v1[3], v2[3], v3[3];
+    for (int c = 0; c < 3; ++c) {
+      v1[c] = p[0][c] - p[1][c];
+      v2[c] = p[1][c] - p[2][c];
+      v3[c] = p[3][c] - p[2][c];
+    }
+    auto cross = [](const float* x, const float* y, float* o) {
+      o[0] = x[1] * y[2] - x[2] * y[1];
+      o[1] = x[2] * y[0] - x[0] * y[2];
+      o[2] = x[0] * y[1] - x[1] * y[0];
+    };
+    float c1[3], c2[3], c3[3];
+    cross(v1, v2, c1);
+    cross(v3, v2, c2);
+    cross(c2, c1, c3);
+    const float v2n = sqrtf(fmaxf(v2[0] * v2[0] + v2[1] * v2[1] + v2[2] * v2[2], 1e-12f));
+    const float ang = atan2f(c3[0] * v2[0] + c3[1] * v2[1] + c3[2] * v2[2],
+                             v2n * (c1[0] * c2[0] + c1[1] * c2[1] + c1[2] * c2[2]));
+    f[22 + t] = sinf(ang) * m;
+    f[26 + t] = cosf(ang) * m;
+    f[30 + t] = m;
+  }
+  __syncthreads();
+  float h = b1[t];
+  for (int k = 0; k < 34; ++k) h += f[k] * w1[k * CM + t];
+  hid[t] = fmaxf(h, 0.f);
+  __syncthreads();
+  float o = b2[t];
+  for (int j = 0; j < CM; ++j) o += hid[j] * w2[j * CM + t];
+  row[(long)i * CM + t] = o;
+  if (t == 0) rmask[i] = f[30];
+}
+
 size_t design_step_seq_save_bytes(const DesignStepW& w, int N) {
   Sizer s;
   SeqExtra<Sizer> x(s, N);
   (void)x;
-  return s.off + design_step_save_bytes(w, N, 1);
+  // room for the template's MSA row: the main stack runs two rows then
+  return s.off + design_step_save_bytes(w, N, 2);
 }
 
 void design_step_seq_fwd(hipStream_t st, const DesignStepW& w, int N, const float* logits,
@@ -661,16 +739,29 @@ void design_step_seq_fwd(hipStream_t st, const DesignStepW& w, int N, const floa
       throw std::invalid_argument("design step: atom37 outputs need const/atom37_to_atom14 and "
                                   "const/atom37_mask in the structure module's directory");
     nonnull(atoms.mask37, "design step atom37 mask");
-    if (atoms.tpl37) nonnull(atoms.tplm37, "design step template atom mask");
-  } else if (atoms.tpl37) {
-    throw std::invalid_argument("design step: the alignment needs the atom37 output");
   }
+  if (atoms.tpl37) nonnull(atoms.tplm37, "design step template atom mask");
+  // A template embedding adds the template's MSA row whenever its weights
+  // are there (modules_multimer.py:608-617 adds it with every template), so
+  // the backward knows the row from with_template alone.
+  const bool row = act_const && w.trow.ok();
+  if (row && !atoms.tpl37)
+    throw std::invalid_argument("design step: the template's MSA row needs the template's atoms "
+                                "(tpl_atoms37, tpl_mask37)");
   hdr_set(st, x.hdr, SEQ_MAGIC,
-          (conf.plddt ? HAS_CONFIDENCE : 0u) | (atoms.atom37 ? HAS_ATOM37 : 0u));
+          (conf.plddt ? HAS_CONFIDENCE : 0u) | (atoms.atom37 ? HAS_ATOM37 : 0u) |
+              (row ? HAS_ROW : 0u));
   seqfeat_fwd(st, logits, flags, bias, SeqScalars{}, sc4, omitted_half, N, x.feat, x.prof);
   design_inputs_fwd(st, x.feat, x.prof, N, x.tf, x.mf, x.aatype);
+  if (row) {
+    KTimed kt("design.template_row", st);
+    hipLaunchKernelGGL(template_row_kernel, dim3((unsigned)N), dim3(CM), 0, st, x.aatype, flags,
+                       atoms.tpl37, atoms.tplm37, w.trow.chi_idx, w.trow.chi_mask, w.trow.w1,
+                       w.trow.b1, w.trow.w2, w.trow.b2, x.row, x.rmask);
+  }
   design_step_fwd(st, w, N, 1, x.tf, x.mf, ri, ai, ei, si, offset, seq_mask, act_const, x.aatype,
-                  seeds, dropout, recycles, atom14, dgram, pae, plddt, expres, cv.p + cv.off);
+                  seeds, dropout, recycles, atom14, dgram, pae, plddt, expres, cv.p + cv.off,
+                  row ? x.row : nullptr, row ? x.rmask : nullptr);
   if (atoms.atom37) {
     KTimed kt("design.atom37", st);
     hipLaunchKernelGGL(atom37_kernel, dim3((unsigned)((N * A37 + 255) / 256)), dim3(256), 0, st,
@@ -730,8 +821,10 @@ void design_step_seq_bwd(hipStream_t st, const DesignStepW& w, int N, const floa
     dpae = x.dp;
     dexpres = x.de;
   }
+  // the inner step's header checks the template embedding, then the row
+  const bool row = with_template && w.trow.ok();
   design_step_bwd(st, w, N, 1, x.tf, seq_mask, with_template, x.aatype, dropout, cv.p + cv.off,
-                  datom, ddgram, dpae, dplddt, dexpres, x.dtf, x.dmf);
+                  datom, ddgram, dpae, dplddt, dexpres, x.dtf, x.dmf, row);
   design_inputs_bwd(st, x.dtf, x.dmf, N, x.dfeat, x.dprof);
   seqfeat_bwd(st, logits, flags, bias, SeqScalars{}, sc4, omitted_half, N, x.dfeat, x.dprof,
               d_logits);

@@ -168,6 +168,16 @@ def recycle_shapes(c_m=C_M, c_z=C_Z, bins=15):
             "prev_pair_norm/scale": (c_z,), "prev_pair_norm/offset": (c_z,)}
 
 
+def template_row_shapes(c_m=C_M, nfeat=34):
+    """template_embedding_1d's two Linears (modules_multimer.py:1080-1137):
+    the template's MSA row from 34 features (one-hot template aatype 22,
+    sin/cos/mask of 4 chi angles); in the embedder's weights directory
+    (bindcraft/af/native.py:521-524)."""
+    return {"template_single_embedding/weights": (nfeat, c_m),
+            "template_single_embedding/bias": (c_m,),
+            "template_projection/weights": (c_m, c_m), "template_projection/bias": (c_m,)}
+
+
 def single_activations_shapes(c_m=C_M, c_s=384):
     """single_activations (modules_multimer.py EmbeddingsAndEvoformer: the
     single representation from the main stack's msa[0]); it ships in the
@@ -182,7 +192,7 @@ def init_embedder_params(rng, scoped=False):
     method scope (and the checkpoint) does."""
     out = {}
     for name, shape in {**embedder_shapes(), **single_activations_shapes(),
-                        **recycle_shapes()}.items():
+                        **recycle_shapes(), **template_row_shapes()}.items():
         fan_in = shape[0] if len(shape) == 2 else 1
         arr = rng.standard_normal(shape) / math.sqrt(fan_in)
         if len(shape) == 1:
@@ -395,6 +405,13 @@ def init_residue_tables(rng):
     m37[:, 1] = 1.0
     out["atom37_to_atom14"] = a37.astype(np.float32)
     out["atom37_mask"] = m37
+    # the template row's chi angles: four distinct atom37 slots per chi (as
+    # the real table has; a repeated atom makes the dihedral 0/0), and which
+    # chis each residue type has (the unknown type, row 20, has none)
+    out["chi_atom_indices"] = rng.random((21, 4, 37)).argsort(-1)[..., :4].astype(np.float32)
+    cm = (rng.random((21, 4)) < 0.7).astype(np.float32)
+    cm[20] = 0.0
+    out["chi_angles_mask"] = cm
     return out
 
 
@@ -409,12 +426,19 @@ def residue_tables_from(rc):
         for j, name in enumerate(rc.restype_name_to_atom14_names[rc.restype_1to3[rt]]):
             if name:
                 a37[r, rc.atom_order[name]] = j
+    # all_atom_multimer.get_chi_atom_indices: restypes order, UNK all zeros
+    chi = np.zeros((21, 4, 4), np.float32)
+    for r, rt in enumerate(rc.restypes):
+        for c, atoms in enumerate(rc.chi_angles_atoms[rc.restype_1to3[rt]]):
+            chi[r, c] = [rc.atom_order[a] for a in atoms]
     return {"default_frame": np.asarray(rc.restype_rigid_group_default_frame, np.float32),
             "atom14_to_group": np.asarray(rc.restype_atom14_to_rigid_group, np.float32),
             "atom14_lit_pos": np.asarray(rc.restype_atom14_rigid_group_positions, np.float32),
             "atom14_mask": np.asarray(rc.restype_atom14_mask, np.float32),
             "atom37_to_atom14": a37,
-            "atom37_mask": np.asarray(rc.restype_atom37_mask, np.float32)}
+            "atom37_mask": np.asarray(rc.restype_atom37_mask, np.float32),
+            "chi_atom_indices": chi,
+            "chi_angles_mask": np.asarray(list(rc.chi_angles_mask) + [[0.0] * 4], np.float32)}
 
 
 def write_manifest(out_dir, params):

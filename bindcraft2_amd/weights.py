@@ -37,10 +37,11 @@ HEADS = ("distogram_head", "predicted_aligned_error_head", "predicted_lddt_head"
          "experimentally_resolved_head")
 EMBED_LEAVES = ("preprocess_1d", "preprocess_msa", "left_single", "right_single",
                 "position_activations")
-# the one-call design step reads these: the single projection and the three
-# recycle terms (bindcraft/af/native.py:525 lists them with the embedder's)
+# the one-call design step reads these: the single projection, the template
+# row's two Linears and the three recycle terms (bindcraft/af/native.py:521-524
+# lists them with the embedder's)
 EMBED_OPTIONAL = ("single_activations", "prev_pos_linear", "prev_msa_first_row_norm",
-                  "prev_pair_norm")
+                  "prev_pair_norm", "template_single_embedding", "template_projection")
 IPA_HEADS = 12
 
 

@@ -477,7 +477,15 @@ int bc2n_design_inputs_bwd(void* stream, const float* d_target_feat, const float
  * (native/design_step.cuh:1162-1168): a Kabsch of the CA atoms of the
  * residues flagged TEMPLATE and not DESIGN (flags bits 1, 0;
  * bindcraft/af2.py:89-97, bindcraft/protein.py:75-83), its rotation under
- * stop_gradient.  bwd: the five head cotangents, the atom37 one and those of
+ * stop_gradient.  With a template embedding (act_const) and the template
+ * row's weights present (template_single_embedding, template_projection in
+ * emb_dir; const/chi_atom_indices, const/chi_angles_mask in post_dir) the
+ * template's MSA row joins the main stack, as modules_multimer.py:608-617
+ * adds it (the reference's S = 2): its features are the one-hot of aatype
+ * on TEMPLATE residues (21 elsewhere) and the template's chi angles from
+ * tpl_atoms37 / tpl_mask37, which are then required (template_embedding_1d,
+ * modules_multimer.py:1080-1137; bindcraft/af2.py:153-160).
+ * bwd: the five head cotangents, the atom37 one and those of
  * the confidence metrics (any may be NULL; the atom37 and confidence ones
  * need a forward that computed them) -> d_logits f32[N,20].  save holds
  * bc2n_design_step_seq_save_bytes() bytes.

@@ -22,8 +22,9 @@ terms' distogram against a loop over the squared breaks, and the first-pass
 terms against their closed form (bias + offsets); Kabsch against scipy's
 weighted Rotation.align_vectors, an exact rigid motion (recovered exactly), a
 mirror image (a proper rotation still) and no weights (the identity); the
-atom37 gather against a loop; gradients against central finite
-differences.
+atom37 gather against a loop; the dihedral against constructed quadruples of
+known torsion and the chi mask against a loop; gradients against central
+finite differences.
 """
 import math
 
@@ -705,8 +706,50 @@ def recycle_terms(aatype, prev_atom14, prev_pair, prev_msa0, p_emb, dtype=torch.
     return pair_t, msa_t
 
 
+# ------------------------------------------------------------ template row
+# modules_multimer.py:1080-1137 template_embedding_1d with
+# all_atom_multimer.py:854-941 (get_chi_atom_indices, compute_chi_angles) and
+# geometry/vector.py:187-212 (dihedral_angle); bindcraft/af2.py:153-160 builds
+# the template arrays from the input atoms.
+
+def dihedral_angle(a, b, c, d):
+    """geometry/vector.py:187-212: v1 = a - b, v2 = b - c, v3 = d - c,
+    c1 = v1 x v2, c2 = v3 x v2, c3 = c2 x c1, atan2(c3 . v2,
+    |v2| (c1 . c2)) with |v2| clipped at 1e-6."""
+    v1, v2, v3 = a - b, b - c, d - c
+    c1, c2 = torch.linalg.cross(v1, v2), torch.linalg.cross(v3, v2)
+    c3 = torch.linalg.cross(c2, c1)
+    v2n = torch.sqrt(torch.clamp((v2 * v2).sum(-1), min=1e-12))
+    return torch.atan2((c3 * v2).sum(-1), v2n * (c1 * c2).sum(-1))
+
+
+def template_row(template_aatype, atoms37, mask37, p_emb, tables, dtype=torch.float64):
+    """The template's MSA row and its mask: features one_hot(aatype, 22),
+    sin(chi) m, cos(chi) m, m for the 4 chi angles (chi atoms by
+    tables['chi_atom_indices'][aatype], m = tables['chi_angles_mask'][aatype]
+    times all four atoms present; aatype 21 (gap) reads the unknown type's
+    row 20, as XLA's clamped gather does), then template_single_embedding,
+    relu, template_projection; mask = m of chi 1."""
+    aat = torch.as_tensor(np.asarray(template_aatype)).long()
+    g = aat.clamp(0, 20)
+    idx = torch.as_tensor(tables["chi_atom_indices"]).long()[g]            # [N, 4, 4]
+    pos = torch.as_tensor(atoms37, dtype=dtype)
+    msk = torch.as_tensor(mask37, dtype=dtype)
+    n = pos.shape[0]
+    ar = torch.arange(n)[:, None, None]
+    pts = pos[ar, idx]                                                      # [N, 4, 4, 3]
+    chi = dihedral_angle(pts[..., 0, :], pts[..., 1, :], pts[..., 2, :], pts[..., 3, :])
+    m = torch.as_tensor(tables["chi_angles_mask"], dtype=dtype)[g] * msk[ar, idx].prod(-1)
+    feat = torch.cat([torch.nn.functional.one_hot(aat, 22).to(dtype), torch.sin(chi) * m,
+                      torch.cos(chi) * m, m], -1)
+    P = Params(p_emb, "param/", dtype)
+    h = torch.relu(linear(feat, P.sub("template_single_embedding/")))
+    return linear(h, P.sub("template_projection/")), m[:, 0]
+
+
 def design_step(target_feat, msa_feat, ids, offset, seq_mask, act_const, aatype, emsa, prm,
-                depths, keys, use_dropout, tables, recycles=0, dtype=torch.float64):
+                depths, keys, use_dropout, tables, recycles=0, tpl_row=None,
+                dtype=torch.float64):
     """The trunk of one design step, input features to the structure-module
     outputs (modules_multimer.py:441-700, EmbeddingsAndEvoformer, then
     AlphaFoldIteration's structure module and heads): the embedder plus the
@@ -720,7 +763,9 @@ def design_step(target_feat, msa_feat, ids, offset, seq_mask, act_const, aatype,
     key.  With `recycles` > 0 the step runs that many forward-only passes
     first (bindcraft/af2.py:195-202), each feeding its atoms, pair and
     msa[0] to the next pass's recycle terms under stop_gradient; `keys` is
-    then a list of recycles + 1 such dicts, one per pass."""
+    then a list of recycles + 1 such dicts, one per pass.  tpl_row = (row
+    [N, 256], mask [N]) is the template's MSA row, appended to the main
+    stack's msa and msa mask (modules_multimer.py:608-617)."""
     keys = keys if isinstance(keys, (list, tuple)) else [keys]
     if len(keys) != recycles + 1:
         raise ValueError("design_step: one key dict per pass")
@@ -737,6 +782,9 @@ def design_step(target_feat, msa_feat, ids, offset, seq_mask, act_const, aatype,
             pair = pair + pair_t
             msa = torch.cat([msa[:1] + msa_t[None], msa[1:]], 0)
             mmask = seq_mask[None].expand(msa.shape[0], -1)
+            if tpl_row is not None:
+                msa = torch.cat([msa, tpl_row[0][None].to(dtype)], 0)
+                mmask = torch.cat([mmask, tpl_row[1][None].to(dtype)], 0)
             k = keys[p]
             if act_const is not None:
                 pair = pair + template_embedding(pair, act_const, pmask, prm["tpl"], depths["tpl"],
@@ -853,11 +901,21 @@ def design_step_seq(logits, flags, scalars, ids, offset, seq_mask, act_const, em
     design_inputs -> design_step (one MSA row).  With template atoms
     (tpl_atoms37 [N,37,3], tpl_mask37 [N,37]) the outputs gain the predicted
     atom37 positions aligned onto the template, and their exists mask (the
-    reference step's first two outputs, native/design_step.cuh:77-80)."""
+    reference step's first two outputs, native/design_step.cuh:77-80); with
+    a template embedding (act_const) as well, the template's MSA row joins
+    the main stack (modules_multimer.py:608-617, the reference's S = 2)."""
     feat, prof = sequence_features(logits, flags, *scalars, bias=bias)
     tf, mf, aatype = design_inputs(feat, prof)
+    row = None
+    if act_const is not None and tpl_atoms37 is not None:
+        # bindcraft/af2.py:153-160: the template covers the TEMPLATE residues
+        tres = (np.asarray(flags).astype(np.int64) & TEMPLATE) != 0
+        t_aat = np.where(tres, aatype, 21)
+        t_pos = np.where(tres[:, None, None], np.asarray(tpl_atoms37), 0.0)
+        t_msk = np.asarray(tpl_mask37) * tres[:, None]
+        row = template_row(t_aat, t_pos, t_msk, prm["emb"], tables, dtype)
     out = design_step(tf, mf, ids, offset, seq_mask, act_const, aatype, emsa, prm, depths, keys,
-                      use_dropout, tables, recycles=recycles, dtype=dtype)
+                      use_dropout, tables, recycles=recycles, tpl_row=row, dtype=dtype)
     if tpl_atoms37 is None:
         return out
     a37, ex = atom14_to_atom37(out[0], aatype, seq_mask, tables)

@@ -100,6 +100,9 @@ def test_design_step_seq_parity(cuda, with_template, dropout):
     dirs = [weights_dir(prm[k], f"dss_{k}_{tag}") for k in ("emb", "tpl", "extra", "main", "post")]
 
     x, flags, bias = _inputs(n, rng, True)
+    flags[n // 2:] |= 2  # the target chain is the template (its MSA row's chi angles)
+    tpl37 = (3 * rng.standard_normal((n, 37, 3))).astype(np.float32)
+    tplm37 = (rng.random((n, 37)) < 0.9).astype(np.float32)
     scalars = (0.8, 0.25, 1.2, 1.5)
     cut = n // 2 + 3
     ids = [np.concatenate([np.arange(cut), np.arange(n - cut)]).astype(np.float32),
@@ -122,9 +125,11 @@ def test_design_step_seq_parity(cuda, with_template, dropout):
                               None if act_const is None else torch.as_tensor(act_const, dtype=D),
                               torch.as_tensor(emsa, dtype=D), prm, depths,
                               keys if dropout else {k: None for k in keys}, dropout, tables,
-                              bias=torch.tensor(bias, dtype=D))
-    ref = list(ref) + list(af2.confidence(ref[3], ref[2], ref[4],
-                                          torch.as_tensor(seq_mask, dtype=D), iasym))
+                              bias=torch.tensor(bias, dtype=D),
+                              tpl_atoms37=tpl37 if with_template else None,
+                              tpl_mask37=tplm37 if with_template else None)
+    ref = list(ref[:5]) + list(af2.confidence(ref[3], ref[2], ref[4],
+                                              torch.as_tensor(seq_mask, dtype=D), iasym))
     loss = sum((r * torch.as_tensor(c, dtype=D)).sum() for r, c in zip(ref, cts))
     ref = [r.detach() for r in ref] + list(torch.autograd.grad(loss, (t,)))
 
@@ -135,7 +140,9 @@ def test_design_step_seq_parity(cuda, with_template, dropout):
     outs, save, conf = step.forward(T(x), T(flags), sc, [T(v) for v in ids], T(seq_mask),
                                     aa_bias=T(bias), act_const=T(act_const),
                                     seeds=seeds.to(torch.uint32).to(cuda), dropout=dropout,
-                                    interface_asym=T(iasym))
+                                    interface_asym=T(iasym),
+                                    tpl_atoms37=T(tpl37) if with_template else None,
+                                    tpl_mask37=T(tplm37) if with_template else None)[:3]
     dlog = step.backward([T(c) for c in cts[:5]], T(x), T(flags), sc, T(seq_mask), save,
                          aa_bias=T(bias), with_template=with_template, dropout=dropout,
                          interface_asym=T(iasym), conf_cts=[T(c) for c in cts[5:]])
@@ -199,9 +206,11 @@ def test_design_step_save_flags(cuda):
     # forward with both: leaving the template out of the backward is refused,
     # leaving the confidence cotangents out is allowed
     act_const = T((0.5 * rng.standard_normal((n, n, 64))).astype(np.float32))
-    _, save2, _ = step.forward(T(x), T(flags), sc, [T(v) for v in ids], T(seq_mask),
-                               act_const=act_const, dropout=False, interface_asym=iasym)
-    with pytest.raises(NativeError, match="omits the template embedding"):
+    tpl37 = T((3 * rng.standard_normal((n, 37, 3))).astype(np.float32))
+    _, save2, _, _ = step.forward(T(x), T(flags), sc, [T(v) for v in ids], T(seq_mask),
+                                  act_const=act_const, dropout=False, interface_asym=iasym,
+                                  tpl_atoms37=tpl37, tpl_mask37=torch.ones(n, 37, device=cuda))
+    with pytest.raises(NativeError, match="omits the template"):
         step.backward(cts, *args, save2, with_template=False, dropout=False)
     d2 = step.backward(cts, *args, save2, with_template=True, dropout=False)
 
@@ -253,8 +262,11 @@ def test_design_step_seq_atom37(cuda, align):
     ct37 = rng.standard_normal((n, 37, 3)).astype(np.float32)
 
     t = torch.tensor(x, dtype=D, requires_grad=True)
+    # with the alignment, a template embedding too: its MSA row joins the stack
+    act_const = (0.5 * rng.standard_normal((n, n, 64))).astype(np.float32) if align else None
     ref = af2.design_step_seq(t, flags, scalars, ids, None, torch.as_tensor(seq_mask, dtype=D),
-                              None, torch.as_tensor(emsa, dtype=D), prm, depths, keys, False,
+                              None if act_const is None else torch.as_tensor(act_const, dtype=D),
+                              torch.as_tensor(emsa, dtype=D), prm, depths, keys, False,
                               tables, recycles=recycles,
                               tpl_atoms37=tpl37 if align else None,
                               tpl_mask37=tplm37 if align else None)
@@ -270,11 +282,11 @@ def test_design_step_seq_atom37(cuda, align):
     step = ops.DesignStepSeq(*dirs, depths=tuple(depths[k] for k in stacks))
     sc = torch.tensor(scalars, dtype=torch.float32, device=cuda)
     outs, save, _, (g37, gm37) = step.forward(
-        T(x), T(flags), sc, [T(v) for v in ids], T(seq_mask), dropout=False, recycles=recycles,
-        atom37=True, tpl_atoms37=T(tpl37) if align else None,
+        T(x), T(flags), sc, [T(v) for v in ids], T(seq_mask), act_const=T(act_const),
+        dropout=False, recycles=recycles, atom37=True, tpl_atoms37=T(tpl37) if align else None,
         tpl_mask37=T(tplm37) if align else None)
     dlog = step.backward([T(c) for c in cts], T(x), T(flags), sc, T(seq_mask), save,
-                         with_template=False, dropout=False, d_atom37=T(ct37))
+                         with_template=align, dropout=False, d_atom37=T(ct37))
     torch.cuda.synchronize()
     assert torch.equal(gm37.cpu().double(), ref[6].detach()), "atom37 exists mask"
     for name, g, r in (("atom14", outs[0], ref[0]), ("atom37", g37, ref[5])):

@@ -58,7 +58,8 @@ def test_template_embedding_embedder_post(tree):
     assert te["param/template_pair_embedding_1/weights"].shape == (64,)
     assert "param/block1/pair_transition/transition1/weights" in te
     em = W.embed_flat(tree)
-    want = {**P.embedder_shapes(), **P.single_activations_shapes(), **P.recycle_shapes()}
+    want = {**P.embedder_shapes(), **P.single_activations_shapes(), **P.recycle_shapes(),
+            **P.template_row_shapes()}
     assert _names_shapes(em) == {f"param/{k}": v for k, v in want.items()}
     po = W.post_flat(tree)
     want = {**P.fold_shapes(), **P.sidechain_shapes(), **P.heads_shapes()}
