@@ -263,7 +263,9 @@ def cpu_triattn_baseline(n, seconds=12.0):
 
 
 # ------------------------------------------------------------------- roofline
-TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "traffic_trunk_L224.json")
+def traffic_summary(n):
+    """The committed counter summary of the trunk step at length n."""
+    return os.path.join(ROOT, "profiles", f"traffic_trunk_L{n}.json")
 
 
 def traffic_of(kernel, n):
@@ -271,9 +273,9 @@ def traffic_of(kernel, n):
     timer records it) from the committed counter summary of the trunk step
     (rocprofv3 FETCH_SIZE / WRITE_SIZE, scaled by a plain copy's reading);
     None if there is no summary for this length."""
-    if not os.path.exists(TRAFFIC_SUMMARY):
+    if not os.path.exists(traffic_summary(n)):
         return None
-    with open(TRAFFIC_SUMMARY) as fh:
+    with open(traffic_summary(n)) as fh:
         summ = json.load(fh)
     if summ.get("L") != n:
         return None

@@ -269,13 +269,18 @@ def post_flat(tree):
 
 def post_weights_from_params(tree, out_dir=None, tables=None):
     """The post-trunk directory; `tables` (params.residue_tables_from(the
-    model's residue_constants), or any dict of the four arrays) adds the
-    residue tables the sidechain reads (const/default_frame,
-    const/atom14_to_group, const/atom14_lit_pos, const/atom14_mask)."""
+    model's residue_constants), or any dict of the arrays) adds the residue
+    tables the sidechain reads (const/default_frame, const/atom14_to_group,
+    const/atom14_lit_pos, const/atom14_mask) and, where the dict has them,
+    the design step's atom37 (const/atom37_to_atom14, const/atom37_mask) and
+    template-row chi tables (const/chi_atom_indices, const/chi_angles_mask)."""
     flat = post_flat(tree)
     if tables is not None:
         for k in ("default_frame", "atom14_to_group", "atom14_lit_pos", "atom14_mask"):
             flat[f"const/{k}"] = np.asarray(tables[k], np.float32)
+        for k in ("atom37_to_atom14", "atom37_mask", "chi_atom_indices", "chi_angles_mask"):
+            if k in tables:
+                flat[f"const/{k}"] = np.asarray(tables[k], np.float32)
     return write_dir(flat, out_dir, "bc2n_post")
 
 
