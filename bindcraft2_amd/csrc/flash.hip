@@ -150,6 +150,36 @@ struct HFrag<16> {
   }
 };
 
+// Logical (row, head, query block) of workgroup `bid` of the per-row
+// forward and dQ kernels (N > 256), ordered head, tile of 8 rows, query
+// block, row in the tile.  The 8 x nqb neighbours one XCD runs together then
+// share 8 rows' K and V and the head's whole pair bias in that XCD's L2; in
+// (row, head, query block) order no two workgroups in flight shared a bias
+// tile (64 queries x N keys of f32), and every row re-read all of it.
+struct RowHeadQb {
+  int r, h, qb;
+};
+__device__ __forceinline__ RowHeadQb row_tile_order(int bid, int R, int nqb) {
+  constexpr int T = 8;
+  const int per_head = R * nqb;
+  const int h = bid / per_head;
+  int j = bid - h * per_head;
+  const int full = (R / T) * T;  // rows in whole tiles
+  RowHeadQb o;
+  o.h = h;
+  if (j < full * nqb) {
+    const int t = j / (T * nqb), w = j - t * (T * nqb);
+    o.qb = w / T;
+    o.r = t * T + w % T;
+  } else {  // the last R % T rows
+    j -= full * nqb;
+    const int rem = R - full;
+    o.qb = j / rem;
+    o.r = full + j % rem;
+  }
+  return o;
+}
+
 // ------------------------------------------------------------------ forward
 // Workgroup = (row r, head h, 64 queries); 4 waves x 16 queries.  N = 32*NKB
 // exactly (one instantiation per block count, so every loop over key blocks
@@ -177,11 +207,10 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
 
   const int nqb = (N + 63) / 64;
   const long G = (long)a.R * H * nqb;
-  const int bid = (int)xcd_block(G);  // (r, h, qb): the qb blocks of (r, h) share K, V
+  const int bid = (int)xcd_block(G);
   if (bid >= G) return;
-  const int qb = bid % nqb;
-  const int h = (bid / nqb) % H;
-  const int r = bid / (nqb * H);
+  const RowHeadQb ord = row_tile_order(bid, a.R, nqb);
+  const int qb = ord.qb, h = ord.h, r = ord.r;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const long tok0 = (long)r * N;
@@ -543,11 +572,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs b) {
 
   const int nqb = (N + 63) / 64;
   const long G = (long)a.R * H * nqb;
-  const int bid = (int)xcd_block(G);  // (r, h, qb): the qb blocks of (r, h) share K, V
+  const int bid = (int)xcd_block(G);
   if (bid >= G) return;
-  const int qb = bid % nqb;
-  const int h = (bid / nqb) % H;
-  const int r = bid / (nqb * H);
+  const RowHeadQb ord = row_tile_order(bid, a.R, nqb);
+  const int qb = ord.qb, h = ord.h, r = ord.r;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const long tok0 = (long)r * N;
