@@ -165,7 +165,7 @@ void need(bool ok, const char* msg) {
 extern "C" {
 
 const char* bc2n_last_error(void) { return last_error(); }
-int bc2n_abi_version(void) { return 2; }
+int bc2n_abi_version(void) { return 3; }
 
 size_t bc2n_triattn_save_bytes(int N, int C, int H) { return triattn_save_bytes(N, C, H); }
 
@@ -1041,12 +1041,13 @@ int bc2n_design_step_seq_fwd(void* stream, const float* logits, const uint8_t* f
                              const float* residue_index, const float* asym_id,
                              const float* entity_id, const float* sym_id, const int32_t* offset,
                              const float* seq_mask, const float* act_const,
-                             const uint32_t* seeds, int N, int64_t d_tpl, int64_t d_extra,
-                             int64_t d_main, int64_t d_fold, int64_t dropout, int64_t recycles,
-                             const char* emb_dir, const char* tpl_dir, const char* extra_dir,
-                             const char* main_dir, const char* post_dir, float* atom14,
-                             float* distogram, float* pae, float* plddt, float* expres,
-                             const float* tpl_atoms37, const float* tpl_mask37, float* atom37,
+                             const uint32_t* seeds, int N, const int32_t* n, int64_t d_tpl,
+                             int64_t d_extra, int64_t d_main, int64_t d_fold, int64_t dropout,
+                             int64_t recycles, const char* emb_dir, const char* tpl_dir,
+                             const char* extra_dir, const char* main_dir, const char* post_dir,
+                             float* atom14, float* distogram, float* pae, float* plddt,
+                             float* expres, const float* tpl_atoms37, const float* tpl_mask37,
+                             float* atom37,
                              float* atom37_mask, const int32_t* interface_asym,
                              float* conf_plddt, float* conf_pae, float* ptm, float* iptm,
                              float* iptm_per_residue, float* expres_ca, void* save) {
@@ -1059,7 +1060,7 @@ int bc2n_design_step_seq_fwd(void* stream, const float* logits, const uint8_t* f
          "design step: the confidence outputs come together, with interface_asym");
     const DesignStepW& w =
         ds_w(emb_dir, tpl_dir, extra_dir, main_dir, post_dir, d_tpl, d_extra, d_main, d_fold);
-    design_step_seq_fwd(as_stream(stream), w, N, logits, flags, aa_bias, scalars, omitted_half,
+    design_step_seq_fwd(as_stream(stream), w, N, n, logits, flags, aa_bias, scalars, omitted_half,
                         residue_index, asym_id, entity_id, sym_id, offset, seq_mask, act_const,
                         seeds, dropout != 0, (int)recycles, atom14, distogram, pae, plddt, expres,
                         AtomsOut{tpl_atoms37, tpl_mask37, atom37, atom37_mask},
@@ -1077,8 +1078,7 @@ int bc2n_design_step_seq_bwd(void* stream, const float* logits, const uint8_t* f
                              const int32_t* interface_asym, const float* d_conf_plddt,
                              const float* d_conf_pae, const float* d_ptm, const float* d_iptm,
                              const float* d_iptm_per_residue, const float* d_expres_ca, void* save,
-                             int N,
-                             int64_t d_tpl, int64_t d_extra, int64_t d_main, int64_t d_fold,
+                             int N, const int32_t* n, int64_t d_tpl, int64_t d_extra, int64_t d_main, int64_t d_fold,
                              int64_t dropout, const char* emb_dir, const char* tpl_dir,
                              const char* extra_dir, const char* main_dir, const char* post_dir,
                              float* d_logits) {
@@ -1086,7 +1086,7 @@ int bc2n_design_step_seq_bwd(void* stream, const float* logits, const uint8_t* f
     need(logits && flags && scalars && seq_mask && save && d_logits, "null operand");
     const DesignStepW& w =
         ds_w(emb_dir, tpl_dir, extra_dir, main_dir, post_dir, d_tpl, d_extra, d_main, d_fold);
-    design_step_seq_bwd(as_stream(stream), w, N, logits, flags, aa_bias, scalars, omitted_half,
+    design_step_seq_bwd(as_stream(stream), w, N, n, logits, flags, aa_bias, scalars, omitted_half,
                         seq_mask, with_template != 0, dropout != 0, save, d_atom14, d_distogram,
                         d_pae, d_plddt, d_expres, d_atom37,
                         ConfCt{interface_asym, d_conf_plddt, d_conf_pae, d_ptm, d_iptm,

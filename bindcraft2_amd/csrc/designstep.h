@@ -104,15 +104,17 @@ struct AtomsOut {
   float* mask37 = nullptr;        // [N][37]
 };
 size_t design_step_seq_save_bytes(const DesignStepW& w, int N);
-void design_step_seq_fwd(hipStream_t st, const DesignStepW& w, int N, const float* logits,
-                         const uint8_t* flags, const float* bias, const float* sc4,
+// nlen: the runtime length on the device (rows >= *nlen are padding), or
+// null for all N rows.
+void design_step_seq_fwd(hipStream_t st, const DesignStepW& w, int N, const int32_t* nlen,
+                         const float* logits, const uint8_t* flags, const float* bias, const float* sc4,
                          float omitted_half, const float* ri, const float* ai, const float* ei,
                          const float* si, const int32_t* offset, const float* seq_mask,
                          const float* act_const, const uint32_t* seeds, bool dropout,
                          int recycles, float* atom14, float* dgram, float* pae, float* plddt,
                          float* expres, const AtomsOut& atoms, const ConfOut& conf, void* save);
-void design_step_seq_bwd(hipStream_t st, const DesignStepW& w, int N, const float* logits,
-                         const uint8_t* flags, const float* bias, const float* sc4,
+void design_step_seq_bwd(hipStream_t st, const DesignStepW& w, int N, const int32_t* nlen,
+                         const float* logits, const uint8_t* flags, const float* bias, const float* sc4,
                          float omitted_half, const float* seq_mask, bool with_template,
                          bool dropout, void* save, const float* datom, const float* ddgram,
                          const float* dpae, const float* dplddt, const float* dexpres,

@@ -416,8 +416,17 @@ struct SeqExtra {
     d14 = c.template take<float>((size_t)N * 14 * 3);
     row = c.template take<float>((size_t)N * CM);
     rmask = c.template take<float>(N);
+    smask = c.template take<float>(N);
+    fl = c.template take<uint8_t>(N);
+    dd = c.template take<float>((size_t)N * N * CONF_PBINS);
+    cc = c.template take<float>((size_t)3 * N + (size_t)N * N);
   }
   float *row, *rmask;  // the template's MSA row [N][256] and its mask
+  // with a runtime length: seq_mask and flags with the padding rows zeroed,
+  // and the padding-masked distogram and confidence cotangents
+  float* smask;
+  uint8_t* fl;
+  float *dd, *cc;
   float* kab;  // the superposition: R [3][3], centres of the prediction and template
   float* d14;  // the atom14 cotangent with the atom37 one folded in
   char* conf;
@@ -714,6 +723,46 @@ __global__ __launch_bounds__(256) void template_row_kernel(
   if (t == 0) rmask[i] = f[30];
 }
 
+namespace {
+
+// The runtime length: rows i >= *n of the caller's [N]-row buffers are
+// padding.  smask = seq_mask and fl = flags on real rows, 0 on padding, so
+// every mask the step derives (pair and MSA masks, the template row, the
+// Kabsch selection, the confidence residue weights) leaves the padding out.
+__global__ void pad_rows_kernel(const float* __restrict__ seq_mask,
+                                const uint8_t* __restrict__ flags, const int32_t* __restrict__ n,
+                                int N, float* __restrict__ smask, uint8_t* __restrict__ fl) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= N) return;
+  const bool real = i < *n;
+  smask[i] = real ? seq_mask[i] : 0.f;
+  fl[i] = real ? flags[i] : (uint8_t)0;
+}
+
+// y = a where the entry's row (and, for a pair array, its column) is real,
+// 0 on padding; with acc, y += that instead.  [N][K] (pair false) or
+// [N][N][K] arrays; a == nullptr reads as zeros; a == y masks in place.
+__global__ void pad_mask_kernel(const float* a, long total, int N, int K, bool pair,
+                                const int32_t* __restrict__ n, bool acc, float* y) {
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int nn = *n;
+  const long row = idx / K;  // i (row arrays) or i * N + j (pair arrays)
+  const bool real = pair ? (row / N < nn && row % N < nn) : row < nn;
+  const float v = (real && a) ? a[idx] : 0.f;
+  y[idx] = acc ? y[idx] + v : v;
+}
+
+void pad_mask(hipStream_t st, const float* a, int N, int K, bool pair, const int32_t* n, bool acc,
+              float* y) {
+  if (!y) return;
+  const long total = (long)N * (pair ? N : 1) * K;
+  hipLaunchKernelGGL(pad_mask_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, a,
+                     total, N, K, pair, n, acc, y);
+}
+
+}  // namespace
+
 size_t design_step_seq_save_bytes(const DesignStepW& w, int N) {
   Sizer s;
   SeqExtra<Sizer> x(s, N);
@@ -722,18 +771,30 @@ size_t design_step_seq_save_bytes(const DesignStepW& w, int N) {
   return s.off + design_step_save_bytes(w, N, 2);
 }
 
-void design_step_seq_fwd(hipStream_t st, const DesignStepW& w, int N, const float* logits,
-                         const uint8_t* flags, const float* bias, const float* sc4,
-                         float omitted_half, const float* ri, const float* ai, const float* ei,
-                         const float* si, const int32_t* offset, const float* seq_mask,
-                         const float* act_const, const uint32_t* seeds, bool dropout,
-                         int recycles, float* atom14, float* dgram, float* pae, float* plddt,
-                         float* expres, const AtomsOut& atoms, const ConfOut& conf, void* save) {
+void design_step_seq_fwd(hipStream_t st, const DesignStepW& w, int N, const int32_t* nlen,
+                         const float* logits, const uint8_t* flags_in, const float* bias,
+                         const float* sc4, float omitted_half, const float* ri, const float* ai,
+                         const float* ei, const float* si, const int32_t* offset,
+                         const float* seq_mask_in, const float* act_const, const uint32_t* seeds,
+                         bool dropout, int recycles, float* atom14, float* dgram, float* pae,
+                         float* plddt, float* expres, const AtomsOut& atoms, const ConfOut& conf,
+                         void* save) {
   ds_check(w, N, 1);
-  nonnull(logits, "design step logits"); nonnull(flags, "design step flags");
+  nonnull(logits, "design step logits"); nonnull(flags_in, "design step flags");
   nonnull(sc4, "design step scalars"); nonnull(save, "design step save");
+  nonnull(seq_mask_in, "design step seq_mask");
   Carver cv(save);
   SeqExtra<Carver> x(cv, N);
+  // a runtime length masks the padding rows out of seq_mask and flags; every
+  // mask downstream derives from these two
+  const float* seq_mask = seq_mask_in;
+  const uint8_t* flags = flags_in;
+  if (nlen) {
+    hipLaunchKernelGGL(pad_rows_kernel, dim3((unsigned)((N + 127) / 128)), dim3(128), 0, st,
+                       seq_mask_in, flags_in, nlen, N, x.smask, x.fl);
+    seq_mask = x.smask;
+    flags = x.fl;
+  }
   if (atoms.atom37) {
     if (!w.a37_14 || !w.a37_mask)
       throw std::invalid_argument("design step: atom37 outputs need const/atom37_to_atom14 and "
@@ -785,28 +846,72 @@ void design_step_seq_fwd(hipStream_t st, const DesignStepW& w, int N, const floa
     BC2N_HIP(hipMemcpyAsync(x.pl, pae, (size_t)N * N * CONF_PBINS * 4, hipMemcpyDeviceToDevice, st));
     BC2N_HIP(hipMemcpyAsync(x.el, expres, (size_t)N * CONF_EXPRES * 4, hipMemcpyDeviceToDevice, st));
   }
+  if (nlen) {
+    // the padding's outputs are zero (the metrics' backward keeps its own copies)
+    KTimed kt("design.pad_outputs", st);
+    pad_mask(st, atom14, N, 14 * 3, false, nlen, false, atom14);
+    pad_mask(st, dgram, N, CONF_PBINS, true, nlen, false, dgram);
+    pad_mask(st, pae, N, CONF_PBINS, true, nlen, false, pae);
+    pad_mask(st, plddt, N, CONF_LBINS, false, nlen, false, plddt);
+    pad_mask(st, expres, N, CONF_EXPRES, false, nlen, false, expres);
+    pad_mask(st, atoms.atom37, N, A37 * 3, false, nlen, false, atoms.atom37);
+    pad_mask(st, atoms.mask37, N, A37, false, nlen, false, atoms.mask37);
+    pad_mask(st, conf.plddt, N, 1, false, nlen, false, conf.plddt);
+    pad_mask(st, conf.pae, N, 1, true, nlen, false, conf.pae);
+    pad_mask(st, conf.iptm_pr, N, 1, false, nlen, false, conf.iptm_pr);
+    pad_mask(st, conf.expres_ca, N, 1, false, nlen, false, conf.expres_ca);
+  }
 }
 
-void design_step_seq_bwd(hipStream_t st, const DesignStepW& w, int N, const float* logits,
-                         const uint8_t* flags, const float* bias, const float* sc4,
-                         float omitted_half, const float* seq_mask, bool with_template,
-                         bool dropout, void* save, const float* datom, const float* ddgram,
-                         const float* dpae, const float* dplddt, const float* dexpres,
-                         const float* datom37, const ConfCt& conf, float* d_logits) {
+void design_step_seq_bwd(hipStream_t st, const DesignStepW& w, int N, const int32_t* nlen,
+                         const float* logits, const uint8_t* flags_in, const float* bias,
+                         const float* sc4, float omitted_half, const float* seq_mask_in,
+                         bool with_template, bool dropout, void* save, const float* datom,
+                         const float* ddgram, const float* dpae, const float* dplddt,
+                         const float* dexpres, const float* datom37, const ConfCt& conf_in,
+                         float* d_logits) {
   ds_check(w, N, 1);
-  nonnull(logits, "design step logits"); nonnull(flags, "design step flags");
+  nonnull(logits, "design step logits"); nonnull(flags_in, "design step flags");
   nonnull(sc4, "design step scalars"); nonnull(save, "design step save");
-  nonnull(d_logits, "design step d_logits");
+  nonnull(d_logits, "design step d_logits"); nonnull(seq_mask_in, "design step seq_mask");
   Carver cv(save);
   SeqExtra<Carver> x(cv, N);
   // confidence cotangents need the forward's metrics; leaving them out is allowed
   const long seq_flags = hdr_flags(st, x.hdr, SEQ_MAGIC, "design step");
-  if (conf.any()) hdr_require(seq_flags, HAS_CONFIDENCE, true, "design step");
+  if (conf_in.any()) hdr_require(seq_flags, HAS_CONFIDENCE, true, "design step");
+  if (datom37) hdr_require(seq_flags, HAS_ATOM37, true, "design step");
+  const float* seq_mask = seq_mask_in;
+  const uint8_t* flags = flags_in;
+  ConfCt conf = conf_in;
+  if (nlen) {
+    // the forward's masks again, and every cotangent with its padding zeroed:
+    // a query at a padding position still attends to real keys, so a nonzero
+    // cotangent there would reach the real rows
+    KTimed kt("design.pad_cotangents", st);
+    hipLaunchKernelGGL(pad_rows_kernel, dim3((unsigned)((N + 127) / 128)), dim3(128), 0, st,
+                       seq_mask_in, flags_in, nlen, N, x.smask, x.fl);
+    seq_mask = x.smask;
+    flags = x.fl;
+    float* c0 = x.cc;  // [N] plddt, [N][N] pae, [N] per-residue ipTM, [N] expres-CA
+    float* c1 = c0 + N;
+    float* c2 = c1 + (size_t)N * N;
+    float* c3 = c2 + N;
+    if (conf.plddt) pad_mask(st, conf.plddt, N, 1, false, nlen, false, c0), conf.plddt = c0;
+    if (conf.pae) pad_mask(st, conf.pae, N, 1, true, nlen, false, c1), conf.pae = c1;
+    if (conf.iptm_pr) pad_mask(st, conf.iptm_pr, N, 1, false, nlen, false, c2), conf.iptm_pr = c2;
+    if (conf.expres_ca)
+      pad_mask(st, conf.expres_ca, N, 1, false, nlen, false, c3), conf.expres_ca = c3;
+    if (ddgram) pad_mask(st, ddgram, N, CONF_PBINS, true, nlen, false, x.dd), ddgram = x.dd;
+  }
   if (datom37) {
-    hdr_require(seq_flags, HAS_ATOM37, true, "design step");
     KTimed kt("design.atom37_bwd", st);
     hipLaunchKernelGGL(atom37_bwd_kernel, dim3((unsigned)((N + 63) / 64)), dim3(64), 0, st, datom,
                        datom37, x.aatype, seq_mask, w.a37_14, w.a37_mask, x.kab, N, x.d14);
+    datom = x.d14;
+  }
+  if (nlen && datom) {
+    // per residue, so masking the sum masks both terms
+    pad_mask(st, datom, N, 14 * 3, false, nlen, false, x.d14);
     datom = x.d14;
   }
   if (conf.any()) {
@@ -814,12 +919,22 @@ void design_step_seq_bwd(hipStream_t st, const DesignStepW& w, int N, const floa
     nonnull(conf.asym, "design step interface asym");
     confidence_bwd(st, x.ll, x.pl, x.el, seq_mask, conf.asym, N, x.conf, conf.plddt,
                    conf.pae, conf.ptm, conf.iptm, conf.iptm_pr, conf.expres_ca, x.dl, x.dp, x.de);
-    add_into(st, dplddt, nullptr, (long)N * CONF_LBINS, x.dl);
-    add_into(st, dpae, nullptr, (long)N * N * CONF_PBINS, x.dp);
-    add_into(st, dexpres, nullptr, (long)N * CONF_EXPRES, x.de);
+    if (nlen) {
+      pad_mask(st, dplddt, N, CONF_LBINS, false, nlen, true, x.dl);
+      pad_mask(st, dpae, N, CONF_PBINS, true, nlen, true, x.dp);
+      pad_mask(st, dexpres, N, CONF_EXPRES, false, nlen, true, x.de);
+    } else {
+      add_into(st, dplddt, nullptr, (long)N * CONF_LBINS, x.dl);
+      add_into(st, dpae, nullptr, (long)N * N * CONF_PBINS, x.dp);
+      add_into(st, dexpres, nullptr, (long)N * CONF_EXPRES, x.de);
+    }
     dplddt = x.dl;
     dpae = x.dp;
     dexpres = x.de;
+  } else if (nlen) {
+    if (dplddt) pad_mask(st, dplddt, N, CONF_LBINS, false, nlen, false, x.dl), dplddt = x.dl;
+    if (dpae) pad_mask(st, dpae, N, CONF_PBINS, true, nlen, false, x.dp), dpae = x.dp;
+    if (dexpres) pad_mask(st, dexpres, N, CONF_EXPRES, false, nlen, false, x.de), dexpres = x.de;
   }
   // the inner step's header checks the template embedding, then the row
   const bool row = with_template && w.trow.ok();
@@ -828,6 +943,7 @@ void design_step_seq_bwd(hipStream_t st, const DesignStepW& w, int N, const floa
   design_inputs_bwd(st, x.dtf, x.dmf, N, x.dfeat, x.dprof);
   seqfeat_bwd(st, logits, flags, bias, SeqScalars{}, sc4, omitted_half, N, x.dfeat, x.dprof,
               d_logits);
+  if (nlen) pad_mask(st, d_logits, N, 20, false, nlen, false, d_logits);
 }
 
 }  // namespace bc2n

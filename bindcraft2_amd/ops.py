@@ -583,6 +583,16 @@ def design_inputs_backward(d_target_feat, d_msa_feat):
     return d_feat, d_prof
 
 
+def _length(t):
+    """A runtime length operand: None, or an i32 tensor of one element on the
+    device (never read on the host)."""
+    if t is None:
+        return None
+    if t.dtype != torch.int32 or t.numel() != 1 or not t.is_cuda:
+        raise ValueError("length must be a one-element int32 tensor on the device")
+    return t
+
+
 class DesignStepSeq(DesignStep):
     """The one-call design step from the designed logits
     (bc2n_design_step_seq_*): sequence features -> trunk inputs -> the step;
@@ -598,13 +608,15 @@ class DesignStepSeq(DesignStep):
     def forward(self, logits, flags, scalars, ids, seq_mask, aa_bias=None, act_const=None,
                 offset=None, seeds=None, dropout=True, save=None, omitted_half=OMITTED_HALF,
                 interface_asym=None, recycles=0, atom37=False, tpl_atoms37=None,
-                tpl_mask37=None):
+                tpl_mask37=None, length=None):
         """-> ((atom14, distogram, pae, plddt, expres), save), plus the confidence
         metrics (plddt, pae, ptm, iptm, iptm_per_residue, expres_ca) as a third
         element when interface_asym (i32 [N]) is given.  With atom37=True (or
         template atoms tpl_atoms37 [N,37,3] / tpl_mask37 [N,37], which align
         them) a fourth element (atom37 [N,37,3], exists mask [N,37]) follows
-        the third (None without interface_asym)."""
+        the third (None without interface_asym).  length: an i32 device tensor
+        [1] holding the runtime length (rows at or past it are padding), or
+        None for all N rows."""
         n, dev = logits.shape[0], logits.device
         _check_seeds(seeds, dropout, recycles)
         e = lambda *sh: torch.empty(*sh, dtype=torch.float32, device=dev)
@@ -617,7 +629,8 @@ class DesignStepSeq(DesignStep):
         check(lib().bc2n_design_step_seq_fwd(_stream(), _ptr(logits), _ptr(flags), _ptr(aa_bias),
                                              _ptr(scalars), float(omitted_half), *map(_ptr, ids),
                                              _ptr(offset), _ptr(seq_mask), _ptr(act_const),
-                                             _ptr(seeds), n, *self.depths, int(dropout),
+                                             _ptr(seeds), n, _ptr(_length(length)),
+                                             *self.depths, int(dropout),
                                              int(recycles), *self.dirs, *map(_ptr, outs),
                                              _ptr(tpl_atoms37), _ptr(tpl_mask37),
                                              *map(_ptr, a37), _ptr(interface_asym),
@@ -630,7 +643,7 @@ class DesignStepSeq(DesignStep):
 
     def backward(self, cts, logits, flags, scalars, seq_mask, save, aa_bias=None,
                  with_template=True, dropout=True, omitted_half=OMITTED_HALF,
-                 interface_asym=None, conf_cts=(None,) * 6, d_atom37=None):
+                 interface_asym=None, conf_cts=(None,) * 6, d_atom37=None, length=None):
         n = logits.shape[0]
         d = torch.empty_like(logits)
         check(lib().bc2n_design_step_seq_bwd(_stream(), _ptr(logits), _ptr(flags), _ptr(aa_bias),
@@ -638,8 +651,8 @@ class DesignStepSeq(DesignStep):
                                              int(with_template), *map(_ptr, cts),
                                              _ptr(d_atom37), _ptr(interface_asym),
                                              *map(_ptr, conf_cts),
-                                             _ptr(save), n, *self.depths, int(dropout),
-                                             *self.dirs, _ptr(d)))
+                                             _ptr(save), n, _ptr(_length(length)),
+                                             *self.depths, int(dropout), *self.dirs, _ptr(d)))
         return d
 
 

@@ -489,6 +489,15 @@ int bc2n_design_inputs_bwd(void* stream, const float* d_target_feat, const float
  * the confidence metrics (any may be NULL; the atom37 and confidence ones
  * need a forward that computed them) -> d_logits f32[N,20].  save holds
  * bc2n_design_step_seq_save_bytes() bytes.
+ * RUNTIME LENGTH (the reference's `n`, native/design_step.cuh:10-19,
+ * :42-58): n is NULL (all N rows real) or an i32 scalar in device memory,
+ * 1 <= *n <= N, read by the kernels and never by the host, so one set of
+ * buffers sized N (the bucket) serves every length up to it.  Rows i >= *n
+ * of every input are padding (any finite values): seq_mask and flags are
+ * zeroed there before any mask is derived, the padding's outputs are
+ * written as zeros, and in the backward the padding's cotangents are
+ * zeroed before use and its d_logits rows are zero.  Pass the same n to
+ * both calls.
  * ---------------------------------------------------------------------- */
 size_t bc2n_design_step_seq_save_bytes(const char* emb_dir, const char* tpl_dir,
                                        const char* extra_dir, const char* main_dir,
@@ -499,12 +508,13 @@ int bc2n_design_step_seq_fwd(void* stream, const float* logits, const uint8_t* f
                              const float* residue_index, const float* asym_id,
                              const float* entity_id, const float* sym_id, const int32_t* offset,
                              const float* seq_mask, const float* act_const,
-                             const uint32_t* seeds, int N, int64_t d_tpl, int64_t d_extra,
-                             int64_t d_main, int64_t d_fold, int64_t dropout, int64_t recycles,
-                             const char* emb_dir, const char* tpl_dir, const char* extra_dir,
-                             const char* main_dir, const char* post_dir, float* atom14,
-                             float* distogram, float* pae, float* plddt, float* expres,
-                             const float* tpl_atoms37, const float* tpl_mask37, float* atom37,
+                             const uint32_t* seeds, int N, const int32_t* n, int64_t d_tpl,
+                             int64_t d_extra, int64_t d_main, int64_t d_fold, int64_t dropout,
+                             int64_t recycles, const char* emb_dir, const char* tpl_dir,
+                             const char* extra_dir, const char* main_dir, const char* post_dir,
+                             float* atom14, float* distogram, float* pae, float* plddt,
+                             float* expres, const float* tpl_atoms37, const float* tpl_mask37,
+                             float* atom37,
                              float* atom37_mask, const int32_t* interface_asym,
                              float* conf_plddt, float* conf_pae, float* ptm, float* iptm,
                              float* iptm_per_residue, float* expres_ca, void* save);
@@ -516,8 +526,7 @@ int bc2n_design_step_seq_bwd(void* stream, const float* logits, const uint8_t* f
                              const int32_t* interface_asym, const float* d_conf_plddt,
                              const float* d_conf_pae, const float* d_ptm, const float* d_iptm,
                              const float* d_iptm_per_residue, const float* d_expres_ca, void* save,
-                             int N,
-                             int64_t d_tpl, int64_t d_extra, int64_t d_main, int64_t d_fold,
+                             int N, const int32_t* n, int64_t d_tpl, int64_t d_extra, int64_t d_main, int64_t d_fold,
                              int64_t dropout, const char* emb_dir, const char* tpl_dir,
                              const char* extra_dir, const char* main_dir, const char* post_dir,
                              float* d_logits);

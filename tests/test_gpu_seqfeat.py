@@ -296,3 +296,126 @@ def test_design_step_seq_atom37(cuda, align):
     m = metrics(dlog.cpu().double(), dref)
     print("  d logits", m)
     assert m["cos"] >= 0.999 and m["rel_l2"] <= 5e-2
+
+
+def test_design_step_seq_runtime_length(cuda):
+    """The runtime length (the reference's `n`, native/design_step.cuh:10-19):
+    buffers sized for a bucket of 64 rows, the length 45 in device memory.
+    The 19 padding rows hold junk -- random logits, DESIGN and TEMPLATE
+    flags, seq_mask 1, template atoms, and random cotangents on every
+    padding row and column -- which must not reach the 45 real rows.  The
+    real rows are held to the step's bars against the oracle run on the 45
+    residues alone (template row, dropout with JAX keys, one recycle,
+    confidence metrics, atom37 aligned); every padding output and padding
+    d(logits) row is exactly zero.  The length equal to the bucket gives the
+    same bits as no length at all."""
+    nb, n, recycles = 64, 45, 1
+    print(f"design step runtime length bucket={nb} n={n} recycles={recycles}", flush=True)
+    depths = {"tpl": 1, "extra": 1, "main": 1, "fold": 2}
+    rng = np.random.default_rng(9400)
+    prm = {"emb": bparams.init_embedder_params(rng),
+           "tpl": bparams.init_template_embedding_params(depths["tpl"], rng, gates="random",
+                                                         ln="random"),
+           "extra": _extra_params(depths["extra"], rng),
+           "main": bparams.init_block_params(0, rng, gates="random", ln="random"),
+           "post": bparams.init_structure_heads_params(rng, final="random", ln="random")}
+    prm["emb"]["param/prev_pos_linear/weights"] *= 1e-3  # see test_gpu_design_step.py
+    tables = bparams.init_residue_tables(rng)
+    prm["post"].update({f"const/{k}": v for k, v in tables.items()})
+    dirs = [weights_dir(prm[k], f"dsl_{k}") for k in ("emb", "tpl", "extra", "main", "post")]
+    stacks = ("tpl", "extra", "main", "fold")
+
+    # the bucket's inputs: real rows first, junk after
+    x, flags, bias = _inputs(nb, rng, True)
+    flags[n // 2:n] |= 2  # the real target chain is the template
+    flags[n:] = rng.integers(0, 4, nb - n).astype(np.uint8)
+    x[n:] = 3 * rng.standard_normal((nb - n, 20)).astype(np.float32)
+    cut = 20
+    ids = [np.concatenate([np.arange(cut), np.arange(n - cut), 100 + np.arange(nb - n)]),
+           np.concatenate([np.repeat([1, 2], [cut, n - cut]), np.full(nb - n, 3)]),
+           np.concatenate([np.repeat([1, 2], [cut, n - cut]), np.full(nb - n, 3)]),
+           np.ones(nb)]
+    ids = [v.astype(np.float32) for v in ids]
+    # every real row unmasked: a masked real residue's attention rows are
+    # fully masked, which the f32 model (and the GPU) turns uniform while the
+    # fp64 oracle keeps the logit differences (1e9 absorbs them only in f32)
+    seq_mask = np.ones(nb, np.float32)
+    iasym = ids[1].astype(np.int32)
+    tpl37 = (8 * rng.standard_normal((nb, 37, 3))).astype(np.float32)
+    tplm37 = (rng.random((nb, 37)) < 0.8).astype(np.float32)
+    act_const = (0.5 * rng.standard_normal((nb, nb, 64))).astype(np.float32)
+    scalars = (0.8, 0.25, 1.2, 1.5)
+    keys = [{k: J.prng_key(700 + 10 * p + i) for i, k in enumerate(stacks)}
+            for p in range(recycles + 1)]
+    seeds = torch.tensor([[int(kp[k][0]), int(kp[k][1]), 1] for kp in keys for k in stacks],
+                         dtype=torch.int64)
+    shapes = ((nb, 14, 3), (nb, nb, 64), (nb, nb, 64), (nb, 50), (nb, 37))
+    cts = [rng.standard_normal(sh).astype(np.float32) for sh in shapes]
+    ct37 = rng.standard_normal((nb, 37, 3)).astype(np.float32)
+    conf_cts = [rng.standard_normal(sh).astype(np.float32) for sh in ((nb,), (nb, nb), (1,), (1,),
+                                                                      (nb,), (nb,))]
+
+    # the oracle on the 45 real residues
+    r1, r2 = slice(0, n), (slice(0, n), slice(0, n))
+    t = torch.tensor(x[:n], dtype=D, requires_grad=True)
+    sm = torch.as_tensor(seq_mask[:n], dtype=D)
+    ref = af2.design_step_seq(t, flags[:n], scalars, [v[:n] for v in ids], None, sm,
+                              torch.as_tensor(act_const[r2], dtype=D),
+                              torch.as_tensor(rng.standard_normal((1, n, 64)), dtype=D), prm,
+                              depths, keys, True, tables, bias=torch.tensor(bias, dtype=D),
+                              recycles=recycles, tpl_atoms37=tpl37[:n], tpl_mask37=tplm37[:n])
+    conf = af2.confidence(ref[3], ref[2], ref[4], sm, iasym[:n])
+    real = [(ref[0], cts[0][r1]), (ref[1], cts[1][r2]), (ref[2], cts[2][r2]),
+            (ref[3], cts[3][r1]), (ref[4], cts[4][r1]), (ref[5], ct37[r1])]
+    real += [(c, ct[r2] if c.dim() == 2 else ct[r1] if c.numel() == n else ct)
+             for c, ct in zip(conf, conf_cts)]
+    loss = sum((r * torch.as_tensor(c, dtype=D)).sum() for r, c in real)
+    (dref,) = torch.autograd.grad(loss, (t,))
+
+    T = lambda a: None if a is None else torch.as_tensor(a, device=cuda)
+    step = ops.DesignStepSeq(*dirs, depths=tuple(depths[k] for k in stacks))
+    sc = torch.tensor(scalars, dtype=torch.float32, device=cuda)
+    length = torch.tensor([n], dtype=torch.int32, device=cuda)
+    common = dict(aa_bias=T(bias), act_const=T(act_const), seeds=seeds.to(torch.uint32).to(cuda),
+                  dropout=True, interface_asym=T(iasym), recycles=recycles,
+                  tpl_atoms37=T(tpl37), tpl_mask37=T(tplm37))
+    outs, save, gconf, (g37, gm37) = step.forward(T(x), T(flags), sc, [T(v) for v in ids],
+                                                  T(seq_mask), length=length, **common)
+    dlog = step.backward([T(c) for c in cts], T(x), T(flags), sc, T(seq_mask), save,
+                         aa_bias=T(bias), with_template=True, dropout=True,
+                         interface_asym=T(iasym), conf_cts=[T(c) for c in conf_cts],
+                         d_atom37=T(ct37), length=length)
+    torch.cuda.synchronize()
+
+    names = ("atom14", "distogram", "pae", "plddt", "expres", "atom37", "conf plddt", "conf pae",
+             "ptm", "iptm", "iptm_per_residue", "expres_ca")
+    gots = list(outs) + [g37] + list(gconf)
+    refs = list(ref[:6]) + list(conf)
+    for name, g, r in zip(names, gots, refs):
+        g = g.cpu().double()
+        pair = g.dim() >= 2 and g.shape[0] == nb and g.shape[1] == nb
+        gr = g[r2] if pair else g[r1] if g.shape[0] == nb else g
+        m = metrics(gr, r.detach())
+        print(f"  {name}", m)
+        if name in ("ptm", "iptm"):
+            assert m["rel_l2"] <= 2e-2, name
+        else:
+            assert m["rel_l2"] <= 2e-2 and m["max_rel"] <= 2e-2 and m["cos"] >= 0.9999, name
+        if g.shape[0] == nb:  # the padding is written as zeros
+            assert not g[n:].any(), name
+            if pair:
+                assert not g[:, n:].any(), name
+    assert not gm37.cpu()[n:].any()
+    m = metrics(dlog.cpu().double()[:n], dref)
+    print("  d logits", m)
+    assert m["cos"] >= 0.999 and m["rel_l2"] <= 5e-2
+    assert not dlog.cpu()[n:].any(), "padding d(logits)"
+
+    # the bucket's own length gives the bits of no length at all
+    full = torch.tensor([nb], dtype=torch.int32, device=cuda)
+    a = step.forward(T(x), T(flags), sc, [T(v) for v in ids], T(seq_mask), length=full,
+                     **common)[0]
+    b = step.forward(T(x), T(flags), sc, [T(v) for v in ids], T(seq_mask), **common)[0]
+    torch.cuda.synchronize()
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
