@@ -94,7 +94,7 @@ def _declare(L):
         "bc2n_design_step_seq_save_bytes": (sz, [cs, cs, cs, cs, cs, i, c.c_int64, c.c_int64,
                                                  c.c_int64, c.c_int64]),
         "bc2n_design_step_seq_fwd": (i, [vp, vp, vp, vp, vp, f] + [vp] * 8 + [i, vp]
-                                     + [c.c_int64] * 6 + [cs] * 5 + [vp] * 17),
+                                     + [c.c_int64] * 7 + [f] + [cs] * 5 + [vp] * 17),
         "bc2n_design_step_seq_bwd": (i, [vp, vp, vp, vp, vp, f, vp, c.c_int64] + [vp] * 14
                                      + [i, vp] + [c.c_int64] * 5 + [cs] * 5 + [vp]),
         "bc2n_confidence_save_bytes": (sz, [i]),

@@ -165,7 +165,7 @@ void need(bool ok, const char* msg) {
 extern "C" {
 
 const char* bc2n_last_error(void) { return last_error(); }
-int bc2n_abi_version(void) { return 3; }
+int bc2n_abi_version(void) { return 4; }
 
 size_t bc2n_triattn_save_bytes(int N, int C, int H) { return triattn_save_bytes(N, C, H); }
 
@@ -1043,7 +1043,8 @@ int bc2n_design_step_seq_fwd(void* stream, const float* logits, const uint8_t* f
                              const float* seq_mask, const float* act_const,
                              const uint32_t* seeds, int N, const int32_t* n, int64_t d_tpl,
                              int64_t d_extra, int64_t d_main, int64_t d_fold, int64_t dropout,
-                             int64_t recycles, const char* emb_dir, const char* tpl_dir,
+                             int64_t recycles, int64_t cyclic_mode, float flexibility,
+                             const char* emb_dir, const char* tpl_dir,
                              const char* extra_dir, const char* main_dir, const char* post_dir,
                              float* atom14, float* distogram, float* pae, float* plddt,
                              float* expres, const float* tpl_atoms37, const float* tpl_mask37,
@@ -1062,7 +1063,8 @@ int bc2n_design_step_seq_fwd(void* stream, const float* logits, const uint8_t* f
         ds_w(emb_dir, tpl_dir, extra_dir, main_dir, post_dir, d_tpl, d_extra, d_main, d_fold);
     design_step_seq_fwd(as_stream(stream), w, N, n, logits, flags, aa_bias, scalars, omitted_half,
                         residue_index, asym_id, entity_id, sym_id, offset, seq_mask, act_const,
-                        seeds, dropout != 0, (int)recycles, atom14, distogram, pae, plddt, expres,
+                        seeds, dropout != 0, (int)recycles, (int)cyclic_mode, flexibility,
+                        atom14, distogram, pae, plddt, expres,
                         AtomsOut{tpl_atoms37, tpl_mask37, atom37, atom37_mask},
                         ConfOut{interface_asym, conf_plddt, conf_pae, ptm, iptm, iptm_per_residue,
                                 expres_ca},

@@ -111,7 +111,7 @@ void design_step_seq_fwd(hipStream_t st, const DesignStepW& w, int N, const int3
                          float omitted_half, const float* ri, const float* ai, const float* ei,
                          const float* si, const int32_t* offset, const float* seq_mask,
                          const float* act_const, const uint32_t* seeds, bool dropout,
-                         int recycles, float* atom14, float* dgram, float* pae, float* plddt,
+                         int recycles, int cyclic_mode, float flexibility, float* atom14, float* dgram, float* pae, float* plddt,
                          float* expres, const AtomsOut& atoms, const ConfOut& conf, void* save);
 void design_step_seq_bwd(hipStream_t st, const DesignStepW& w, int N, const int32_t* nlen,
                          const float* logits, const uint8_t* flags, const float* bias, const float* sc4,

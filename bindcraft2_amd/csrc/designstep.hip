@@ -420,7 +420,9 @@ struct SeqExtra {
     fl = c.template take<uint8_t>(N);
     dd = c.template take<float>((size_t)N * N * CONF_PBINS);
     cc = c.template take<float>((size_t)3 * N + (size_t)N * N);
+    off = c.template take<int32_t>((size_t)N * N);
   }
+  int32_t* off;  // the cyclic sequence offsets [N][N]
   float *row, *rmask;  // the template's MSA row [N][256] and its mask
   // with a runtime length: seq_mask and flags with the padding rows zeroed,
   // and the padding-masked distogram and confidence cotangents
@@ -447,7 +449,7 @@ void add_into(hipStream_t st, const float* a, const float* b, long n, float* y) 
 
 // ------------------------------------------------------ atom37 + alignment
 constexpr int A37 = 37, CA37 = 1;
-constexpr uint8_t F_DESIGN = 1u, F_TEMPLATE = 2u;  // bindcraft/protein.py:42-51
+constexpr uint8_t F_DESIGN = 1u, F_TEMPLATE = 2u, F_CYCLIC = 64u;  // bindcraft/protein.py:42-51
 
 // atom37[i][a] = atom14[i][a37_14[aat][a]] * ex, ex = a37_mask[aat][a] * seq_mask[i]
 __global__ void atom37_kernel(const float* __restrict__ atom14, const float* __restrict__ aatype,
@@ -671,15 +673,21 @@ __global__ void atom37_bwd_kernel(const float* __restrict__ datom14, const float
 // mask is m of chi 1.  Dihedral as geometry/vector.py:187-212.
 __global__ __launch_bounds__(256) void template_row_kernel(
     const float* __restrict__ aatype, const uint8_t* __restrict__ flags,
-    const float* __restrict__ tpl37, const float* __restrict__ tplm37,
-    const float* __restrict__ chi_idx, const float* __restrict__ chi_mask,
-    const float* __restrict__ w1, const float* __restrict__ b1, const float* __restrict__ w2,
-    const float* __restrict__ b2, float* __restrict__ row, float* __restrict__ rmask) {
+    const float* __restrict__ ridx, float flex, const float* __restrict__ tpl37,
+    const float* __restrict__ tplm37, const float* __restrict__ chi_idx,
+    const float* __restrict__ chi_mask, const float* __restrict__ w1, const float* __restrict__ b1,
+    const float* __restrict__ w2, const float* __restrict__ b2, float* __restrict__ row,
+    float* __restrict__ rmask) {
   __shared__ float f[34];
   __shared__ float hid[CM];
   const int i = blockIdx.x, t = threadIdx.x;
   const bool tres = (flags[i] & F_TEMPLATE) != 0;
-  const int aat = tres ? min(max((int)aatype[i], 0), 20) : 21;
+  // target flexibility (bindcraft/af2.py:150-157): a template residue, not
+  // designed, whose index i has floor((i + 1) f) > floor(i f) (f32, as JAX)
+  // is a gap; its chi features vanish with the gap's all-zero chi mask
+  const bool flexible = tres && flex > 0.f && !(flags[i] & F_DESIGN) &&
+                        floorf((ridx[i] + 1.f) * flex) > floorf(ridx[i] * flex);
+  const int aat = (tres && !flexible) ? min(max((int)aatype[i], 0), 20) : 21;
   const int g = min(aat, 20);
   if (t < 22) f[t] = t == aat ? 1.f : 0.f;
   if (t < 4) {
@@ -724,6 +732,37 @@ __global__ __launch_bounds__(256) void template_row_kernel(
 }
 
 namespace {
+
+// Cyclic sequence offsets (bindcraft/af2.py:174-185): off[i][j] = r_i - r_j,
+// except between two unmasked CYCLIC residues of one chain, whose offset is
+// the ring distance min(|d|, L - |d|) with d's sign (L = the chain's unmasked
+// residue count); mode 1 ('direction') and 2 ('neighbours') negate it where
+// the short way round is the other way, mode 2 then saturates beyond 2 at
+// +-32.  One wave per row i: it first counts its chain's length.
+__global__ __launch_bounds__(64) void cyclic_offsets_kernel(
+    const float* __restrict__ ridx, const float* __restrict__ asym,
+    const uint8_t* __restrict__ flags, const float* __restrict__ smask, int N, int mode,
+    int32_t* __restrict__ off) {
+  const int i = blockIdx.x, lane = threadIdx.x;
+  const float ai = asym[i];
+  float len = 0.f;
+  for (int j = lane; j < N; j += 64) len += asym[j] == ai ? smask[j] : 0.f;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) len += __shfl_xor(len, o, 64);
+  const bool ci = (flags[i] & F_CYCLIC) && smask[i] != 0.f;
+  for (int j = lane; j < N; j += 64) {
+    const int d = (int)ridx[i] - (int)ridx[j];
+    int v = d;
+    if (ci && asym[j] == ai && (flags[j] & F_CYCLIC) && smask[j] != 0.f) {
+      const float ad = (float)abs(d);
+      float cd = fminf(ad, len - ad);
+      if (mode >= 1 && cd < ad) cd = -cd;
+      if (mode == 2 && fabsf(cd) > 2.f) cd = cd > 0.f ? 32.f : -32.f;
+      v = (int)(cd * (float)((d > 0) - (d < 0)));
+    }
+    off[(long)i * N + j] = v;
+  }
+}
 
 // The runtime length: rows i >= *n of the caller's [N]-row buffers are
 // padding.  smask = seq_mask and fl = flags on real rows, 0 on padding, so
@@ -776,10 +815,13 @@ void design_step_seq_fwd(hipStream_t st, const DesignStepW& w, int N, const int3
                          const float* sc4, float omitted_half, const float* ri, const float* ai,
                          const float* ei, const float* si, const int32_t* offset,
                          const float* seq_mask_in, const float* act_const, const uint32_t* seeds,
-                         bool dropout, int recycles, float* atom14, float* dgram, float* pae,
-                         float* plddt, float* expres, const AtomsOut& atoms, const ConfOut& conf,
-                         void* save) {
+                         bool dropout, int recycles, int cyclic_mode, float flexibility,
+                         float* atom14, float* dgram, float* pae, float* plddt, float* expres,
+                         const AtomsOut& atoms, const ConfOut& conf, void* save) {
   ds_check(w, N, 1);
+  if (cyclic_mode < -1 || cyclic_mode > 2)
+    throw std::invalid_argument("design step: cyclic_mode must be -1 (offset as given), 0, 1 or 2");
+  if (!(flexibility >= 0.f)) throw std::invalid_argument("design step: flexibility must be >= 0");
   nonnull(logits, "design step logits"); nonnull(flags_in, "design step flags");
   nonnull(sc4, "design step scalars"); nonnull(save, "design step save");
   nonnull(seq_mask_in, "design step seq_mask");
@@ -817,8 +859,15 @@ void design_step_seq_fwd(hipStream_t st, const DesignStepW& w, int N, const int3
   if (row) {
     KTimed kt("design.template_row", st);
     hipLaunchKernelGGL(template_row_kernel, dim3((unsigned)N), dim3(CM), 0, st, x.aatype, flags,
-                       atoms.tpl37, atoms.tplm37, w.trow.chi_idx, w.trow.chi_mask, w.trow.w1,
-                       w.trow.b1, w.trow.w2, w.trow.b2, x.row, x.rmask);
+                       ri, flexibility, atoms.tpl37, atoms.tplm37, w.trow.chi_idx,
+                       w.trow.chi_mask, w.trow.w1, w.trow.b1, w.trow.w2, w.trow.b2, x.row,
+                       x.rmask);
+  }
+  if (cyclic_mode >= 0) {
+    // the offset feature the embedder reads, built here (bindcraft/af2.py:193)
+    hipLaunchKernelGGL(cyclic_offsets_kernel, dim3((unsigned)N), dim3(64), 0, st, ri, ai, flags,
+                       seq_mask, N, cyclic_mode, x.off);
+    offset = x.off;
   }
   design_step_fwd(st, w, N, 1, x.tf, x.mf, ri, ai, ei, si, offset, seq_mask, act_const, x.aatype,
                   seeds, dropout, recycles, atom14, dgram, pae, plddt, expres, cv.p + cv.off,

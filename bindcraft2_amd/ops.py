@@ -608,7 +608,7 @@ class DesignStepSeq(DesignStep):
     def forward(self, logits, flags, scalars, ids, seq_mask, aa_bias=None, act_const=None,
                 offset=None, seeds=None, dropout=True, save=None, omitted_half=OMITTED_HALF,
                 interface_asym=None, recycles=0, atom37=False, tpl_atoms37=None,
-                tpl_mask37=None, length=None):
+                tpl_mask37=None, length=None, cyclic_mode=None, flexibility=0.0):
         """-> ((atom14, distogram, pae, plddt, expres), save), plus the confidence
         metrics (plddt, pae, ptm, iptm, iptm_per_residue, expres_ca) as a third
         element when interface_asym (i32 [N]) is given.  With atom37=True (or
@@ -616,7 +616,12 @@ class DesignStepSeq(DesignStep):
         them) a fourth element (atom37 [N,37,3], exists mask [N,37]) follows
         the third (None without interface_asym).  length: an i32 device tensor
         [1] holding the runtime length (rows at or past it are padding), or
-        None for all N rows."""
+        None for all N rows.  cyclic_mode ('distance', 'direction',
+        'neighbours' or None = `offset` as given) builds the offset feature
+        from the ids and the CYCLIC flag (bit 6); flexibility is the target
+        flexibility of the template row."""
+        modes = ("distance", "direction", "neighbours")
+        cmode = -1 if cyclic_mode is None else modes.index(cyclic_mode)
         n, dev = logits.shape[0], logits.device
         _check_seeds(seeds, dropout, recycles)
         e = lambda *sh: torch.empty(*sh, dtype=torch.float32, device=dev)
@@ -631,7 +636,8 @@ class DesignStepSeq(DesignStep):
                                              _ptr(offset), _ptr(seq_mask), _ptr(act_const),
                                              _ptr(seeds), n, _ptr(_length(length)),
                                              *self.depths, int(dropout),
-                                             int(recycles), *self.dirs, *map(_ptr, outs),
+                                             int(recycles), cmode, float(flexibility),
+                                             *self.dirs, *map(_ptr, outs),
                                              _ptr(tpl_atoms37), _ptr(tpl_mask37),
                                              *map(_ptr, a37), _ptr(interface_asym),
                                              *map(_ptr, conf), _ptr(save)))

@@ -489,6 +489,16 @@ int bc2n_design_inputs_bwd(void* stream, const float* d_target_feat, const float
  * the confidence metrics (any may be NULL; the atom37 and confidence ones
  * need a forward that computed them) -> d_logits f32[N,20].  save holds
  * bc2n_design_step_seq_save_bytes() bytes.
+ * cyclic_mode: -1 takes `offset` as given (NULL: residue_index
+ * differences); 0 'distance', 1 'direction', 2 'neighbours' build the
+ * offset feature on the device from residue_index, asym_id, flags (bit 6 =
+ * CYCLIC) and seq_mask as bc2's cyclic_sequence_offsets does
+ * (bindcraft/af2.py:174-185, :193; the reference's cyclic_mode attribute,
+ * native/inputfeat.cuh offsetK), ignoring `offset`.  flexibility: the
+ * reference's target flexibility f (>= 0; 0 = off): a TEMPLATE residue not
+ * designed whose residue_index i has floor((i + 1) f) > floor(i f) is a gap
+ * of the template row (bindcraft/af2.py:150-157).  The initial-atom-position
+ * bit of the reference's cyclic_mode (4) is not built.
  * RUNTIME LENGTH (the reference's `n`, native/design_step.cuh:10-19,
  * :42-58): n is NULL (all N rows real) or an i32 scalar in device memory,
  * 1 <= *n <= N, read by the kernels and never by the host, so one set of
@@ -510,7 +520,8 @@ int bc2n_design_step_seq_fwd(void* stream, const float* logits, const uint8_t* f
                              const float* seq_mask, const float* act_const,
                              const uint32_t* seeds, int N, const int32_t* n, int64_t d_tpl,
                              int64_t d_extra, int64_t d_main, int64_t d_fold, int64_t dropout,
-                             int64_t recycles, const char* emb_dir, const char* tpl_dir,
+                             int64_t recycles, int64_t cyclic_mode, float flexibility,
+                             const char* emb_dir, const char* tpl_dir,
                              const char* extra_dir, const char* main_dir, const char* post_dir,
                              float* atom14, float* distogram, float* pae, float* plddt,
                              float* expres, const float* tpl_atoms37, const float* tpl_mask37,

@@ -876,8 +876,39 @@ def kabsch(coords, ref, weights):
     return R, xc, yc
 
 
-DESIGN, TEMPLATE = 1, 2  # bindcraft/protein.py:42-51 ResidueFlags
+DESIGN, TEMPLATE, CYCLIC = 1, 2, 64  # bindcraft/protein.py:42-51 ResidueFlags
 CA37 = 1                 # residue_constants.atom_order['CA']
+CYCLIC_MODES = ("distance", "direction", "neighbours")  # bindcraft/settings.py:87
+
+
+def cyclic_sequence_offsets(residue_index, asym_id, flags, seq_mask, mode):
+    """bindcraft/af2.py:174-185: residue_index differences, except between
+    two unmasked CYCLIC residues of one chain, where the ring distance
+    min(|d|, L - |d|) (L = the chain's unmasked residue count) takes d's
+    sign; 'direction' and 'neighbours' negate it where the short way round
+    is the other way, 'neighbours' then saturates beyond 2 at +-32."""
+    ri = np.asarray(residue_index, np.int64)
+    asym = np.asarray(asym_id)
+    sm = np.asarray(seq_mask, np.float64)
+    off = ri[:, None] - ri[None, :]
+    same = asym[:, None] == asym[None, :]
+    clen = (same * sm[None, :]).sum(-1)
+    cyc = ((np.asarray(flags).astype(np.int64) & CYCLIC) != 0) * sm
+    pairs = same * cyc[:, None] * cyc[None, :]
+    dist = np.minimum(np.abs(off), clen[:, None] - np.abs(off))
+    if mode in ("direction", "neighbours"):
+        dist = np.where(dist < np.abs(off), -dist, dist)
+    if mode == "neighbours":
+        dist = np.where(np.abs(dist) > 2, 32 * np.sign(dist), dist)
+    return np.where(pairs != 0, dist * np.sign(off), off).astype(np.int32)
+
+
+def flexible_target_residues(residue_index, template_mask, flexibility):
+    """bindcraft/af2.py:150-151: every template residue (not designed) whose
+    index i has floor((i + 1) f) > floor(i f), in float32 as JAX computes it."""
+    i = np.asarray(residue_index, np.float32)
+    f = np.float32(flexibility)
+    return np.asarray(template_mask, bool) & (np.floor((i + 1) * f) > np.floor(i * f))
 
 
 def align_to_template(atom37, exists, tpl_atoms37, tpl_mask37, flags):
@@ -896,23 +927,34 @@ def align_to_template(atom37, exists, tpl_atoms37, tpl_mask37, flags):
 
 def design_step_seq(logits, flags, scalars, ids, offset, seq_mask, act_const, emsa, prm, depths,
                     keys, use_dropout, tables, bias=None, recycles=0, tpl_atoms37=None,
-                    tpl_mask37=None, dtype=torch.float64):
+                    tpl_mask37=None, cyclic_mode=None, flexibility=0.0, dtype=torch.float64):
     """design_step from the designed logits: sequence_features ->
     design_inputs -> design_step (one MSA row).  With template atoms
     (tpl_atoms37 [N,37,3], tpl_mask37 [N,37]) the outputs gain the predicted
     atom37 positions aligned onto the template, and their exists mask (the
     reference step's first two outputs, native/design_step.cuh:77-80); with
     a template embedding (act_const) as well, the template's MSA row joins
-    the main stack (modules_multimer.py:608-617, the reference's S = 2)."""
+    the main stack (modules_multimer.py:608-617, the reference's S = 2).
+    cyclic_mode (one of CYCLIC_MODES) replaces `offset` by the cyclic
+    sequence offsets (bindcraft/af2.py:193); flexibility > 0 turns the
+    flexible target residues into gaps of the template (af2.py:153-157)."""
     feat, prof = sequence_features(logits, flags, *scalars, bias=bias)
     tf, mf, aatype = design_inputs(feat, prof)
+    if cyclic_mode is not None:
+        offset = torch.as_tensor(cyclic_sequence_offsets(ids[0], ids[1], flags, seq_mask,
+                                                         cyclic_mode))
     row = None
     if act_const is not None and tpl_atoms37 is not None:
-        # bindcraft/af2.py:153-160: the template covers the TEMPLATE residues
-        tres = (np.asarray(flags).astype(np.int64) & TEMPLATE) != 0
-        t_aat = np.where(tres, aatype, 21)
+        # bindcraft/af2.py:153-160: the template covers the TEMPLATE residues,
+        # minus the flexible ones (a gap, their side chains unmasked out)
+        fl = np.asarray(flags).astype(np.int64)
+        tres = (fl & TEMPLATE) != 0
+        flex = (flexible_target_residues(ids[0], tres & ((fl & DESIGN) == 0), flexibility)
+                if flexibility else np.zeros_like(tres))
+        t_aat = np.where(tres & ~flex, np.asarray(aatype), 21)
         t_pos = np.where(tres[:, None, None], np.asarray(tpl_atoms37), 0.0)
-        t_msk = np.asarray(tpl_mask37) * tres[:, None]
+        side = np.arange(37) > 4  # everything past N, CA, C, CB, O
+        t_msk = np.asarray(tpl_mask37) * tres[:, None] * ~(flex[:, None] & side[None])
         row = template_row(t_aat, t_pos, t_msk, prm["emb"], tables, dtype)
     out = design_step(tf, mf, ids, offset, seq_mask, act_const, aatype, emsa, prm, depths, keys,
                       use_dropout, tables, recycles=recycles, tpl_row=row, dtype=dtype)

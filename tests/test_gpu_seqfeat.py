@@ -419,3 +419,82 @@ def test_design_step_seq_runtime_length(cuda):
     torch.cuda.synchronize()
     for u, v in zip(a, b):
         assert torch.equal(u, v)
+
+
+@pytest.mark.parametrize("mode,flex", [("direction", 0.5), ("neighbours", 0.25),
+                                       ("distance", 0.0)])
+def test_design_step_seq_cyclic_flexible(cuda, mode, flex):
+    """Cyclic offsets built on the device (bindcraft/af2.py:174-185, the
+    reference's cyclic_mode) for a cyclic designed chain, and the target
+    flexibility's gaps in the template row (af2.py:150-157), against the
+    oracle at the step's bars; the oracle without the two features is far
+    from the GPU result, so both are exercised."""
+    n, nb = 64, 24  # a 24-residue cyclic binder, a 40-residue template target
+    print(f"design step cyclic mode={mode} flexibility={flex} n={n}", flush=True)
+    depths = {"tpl": 1, "extra": 1, "main": 1, "fold": 2}
+    rng = np.random.default_rng(9500 + int(100 * flex))
+    prm = {"emb": bparams.init_embedder_params(rng),
+           "tpl": bparams.init_template_embedding_params(depths["tpl"], rng, gates="random",
+                                                         ln="random"),
+           "extra": _extra_params(depths["extra"], rng),
+           "main": bparams.init_block_params(0, rng, gates="random", ln="random"),
+           "post": bparams.init_structure_heads_params(rng, final="random", ln="random")}
+    tables = bparams.init_residue_tables(rng)
+    prm["post"].update({f"const/{k}": v for k, v in tables.items()})
+    dirs = [weights_dir(prm[k], f"dsc_{k}_{mode}") for k in ("emb", "tpl", "extra", "main", "post")]
+    stacks = ("tpl", "extra", "main", "fold")
+    x = rng.standard_normal((n, 20)).astype(np.float32)
+    x[nb:] = np.eye(20, dtype=np.float32)[rng.integers(0, 20, n - nb)]
+    flags = np.zeros(n, np.uint8)
+    flags[:nb] = 1 | af2.CYCLIC
+    flags[nb:] = 2
+    ids = [np.concatenate([np.arange(nb), 100 + np.arange(n - nb)]),
+           np.repeat([1, 2], [nb, n - nb]), np.repeat([1, 2], [nb, n - nb]), np.ones(n)]
+    ids = [v.astype(np.float32) for v in ids]
+    seq_mask = np.ones(n, np.float32)
+    iasym = ids[1].astype(np.int32)
+    tpl37 = (8 * rng.standard_normal((n, 37, 3))).astype(np.float32)
+    tplm37 = (rng.random((n, 37)) < 0.9).astype(np.float32)
+    act_const = (0.5 * rng.standard_normal((n, n, 64))).astype(np.float32)
+    scalars = (0.8, 0.25, 1.2, 1.5)
+    keys = {k: J.prng_key(800 + i) for i, k in enumerate(stacks)}
+    seeds = torch.tensor([[int(keys[k][0]), int(keys[k][1]), 1] for k in stacks],
+                         dtype=torch.int64)
+    shapes = ((n, 14, 3), (n, n, 64), (n, n, 64), (n, 50), (n, 37))
+    cts = [rng.standard_normal(sh).astype(np.float32) for sh in shapes]
+    emsa = torch.as_tensor(rng.standard_normal((1, n, 64)), dtype=D)
+
+    def oracle(cyclic, fl, grad):
+        t = torch.tensor(x, dtype=D, requires_grad=grad)
+        r = af2.design_step_seq(t, flags, scalars, ids, None, torch.as_tensor(seq_mask, dtype=D),
+                                torch.as_tensor(act_const, dtype=D), emsa, prm, depths, keys,
+                                True, tables, tpl_atoms37=tpl37, tpl_mask37=tplm37,
+                                cyclic_mode=cyclic, flexibility=fl)
+        if not grad:
+            return r, None
+        loss = sum((a * torch.as_tensor(c, dtype=D)).sum() for a, c in zip(r[:5], cts))
+        return r, torch.autograd.grad(loss, (t,))[0]
+
+    ref, dref = oracle(mode, flex, True)
+    plain, _ = oracle(None, 0.0, False)
+
+    T = lambda a: None if a is None else torch.as_tensor(a, device=cuda)
+    step = ops.DesignStepSeq(*dirs, depths=tuple(depths[k] for k in stacks))
+    sc = torch.tensor(scalars, dtype=torch.float32, device=cuda)
+    outs, save, _, _ = step.forward(T(x), T(flags), sc, [T(v) for v in ids], T(seq_mask),
+                                    act_const=T(act_const), seeds=seeds.to(torch.uint32).to(cuda),
+                                    dropout=True, interface_asym=T(iasym), tpl_atoms37=T(tpl37),
+                                    tpl_mask37=T(tplm37), cyclic_mode=mode, flexibility=flex)
+    dlog = step.backward([T(c) for c in cts], T(x), T(flags), sc, T(seq_mask), save,
+                         with_template=True, dropout=True)
+    torch.cuda.synchronize()
+    for name, g, r, p in zip(("atom14", "distogram", "pae", "plddt", "expres"), outs, ref, plain):
+        m = metrics(g.cpu().double(), r.detach())
+        away = metrics(g.cpu().double(), p.detach())
+        print(f"  {name}", m, "| without the features: rel", away["rel_l2"])
+        assert m["rel_l2"] <= 2e-2 and m["max_rel"] <= 2e-2 and m["cos"] >= 0.9999, name
+        if name == "distogram":  # the offsets change the pair, the row the msa
+            assert away["rel_l2"] > 10 * m["rel_l2"], "the features were not exercised"
+    m = metrics(dlog.cpu().double(), dref)
+    print("  d logits", m)
+    assert m["cos"] >= 0.999 and m["rel_l2"] <= 5e-2
