@@ -61,7 +61,11 @@ void design_step_fwd(hipStream_t st, const DesignStepW& w, int N, int S, const f
                      const float* act_const, const float* aatype, const uint32_t* seeds,
                      bool dropout, int recycles, float* atom14, float* dgram, float* pae,
                      float* plddt, float* expres, void* save, const float* row = nullptr,
-                     const float* row_mask = nullptr);
+                     const float* row_mask = nullptr, const float* init_pos37 = nullptr);
+// init_pos37 (atom37 [N][37][3]) or null: the structure module of the first
+// pass starts from these atoms' frames (the model's initial_atom_pos), each
+// later pass from the previous pass's atom37 positions (needs the atom37
+// tables).
 // row [N][256] / row_mask [N]: a constant MSA row appended after the
 // embedder's S rows (the template's, modules_multimer.py:608-617); the main
 // stack then runs S + 1 rows and `save` must hold design_step_save_bytes(S + 1).

@@ -100,8 +100,11 @@ struct DsSave {
     rpb = c.template take<float>((size_t)N * 4);
     rpair = c.template take<float>(M * CZ);
     rmsa0 = c.template take<float>((size_t)N * CM);
+    rpos = c.template take<float>((size_t)N * 37 * 3);
+    rposm = c.template take<float>((size_t)N * 37);
   }
   float *rpb, *rpair, *rmsa0;  // the previous pass's pseudo-beta [N][3(+1)], pair, msa[0]
+  float *rpos, *rposm;         // and its atom37 positions (and their mask)
 };
 
 // pmask[i][j] = m[i] m[j]; mmask[s][n] = m[n]
@@ -277,13 +280,19 @@ size_t design_step_save_bytes(const DesignStepW& w, int N, int S) {
   return s.off;
 }
 
+__global__ void atom37_kernel(const float* __restrict__ atom14, const float* __restrict__ aatype,
+                              const float* __restrict__ seq_mask,
+                              const float* __restrict__ a37_14,
+                              const float* __restrict__ a37_mask, int N,
+                              float* __restrict__ atom37, float* __restrict__ mask37);
+
 void design_step_fwd(hipStream_t st, const DesignStepW& w, int N, int S, const float* tf,
                      const float* mf, const float* ri, const float* ai, const float* ei,
                      const float* si, const int32_t* offset, const float* seq_mask,
                      const float* act_const, const float* aatype, const uint32_t* seeds,
                      bool dropout, int recycles, float* atom14, float* dgram, float* pae,
                      float* plddt, float* expres, void* save, const float* row,
-                     const float* row_mask) {
+                     const float* row_mask, const float* init_pos37) {
   const int SM = S + (row ? 1 : 0);  // the main stack's msa rows
   ds_check(w, N, SM);
   nonnull(seq_mask, "design step seq_mask"); nonnull(save, "design step save");
@@ -291,6 +300,10 @@ void design_step_fwd(hipStream_t st, const DesignStepW& w, int N, int S, const f
   if (row) nonnull(row_mask, "design step row mask");
   if (dropout) nonnull(seeds, "design step seeds");
   if (recycles < 0 || recycles > 64) throw std::invalid_argument("design step: recycles must be in [0, 64]");
+  if (init_pos37 && recycles > 0 && (!w.a37_14 || !w.a37_mask))
+    throw std::invalid_argument("design step: initial atom positions with recycling need "
+                                "const/atom37_to_atom14 and const/atom37_mask in the structure "
+                                "module's directory");
   Carver cv(save);
   DsSave<Carver> sv(cv, w, N, SM);
   const long M = (long)N * N;
@@ -342,12 +355,18 @@ void design_step_fwd(hipStream_t st, const DesignStepW& w, int N, int S, const f
     GemmF32 g = gemm_rows(N, CS, CM, sv.msa3, w.wsa, sv.single);
     g.bias = w.bsa;
     gemm_f32(st, g, "design.gemm_single");
+    // the first pass starts from the given atoms, later ones from the
+    // previous pass's (native/design_step.cuh:1112-1114)
+    const float* init = init_pos37 ? (pass == 0 ? init_pos37 : sv.rpos) : nullptr;
     structheads_fwd(st, w.sh, N, w.d_fold, sv.single, sv.pair3, seq_mask, aatype, key(3),
-                    enabled(3), dropout, atom14, dgram, pae, plddt, expres, sv.sh);
+                    enabled(3), dropout, atom14, dgram, pae, plddt, expres, sv.sh, init);
     if (!last) {
       // what the next pass's recycle terms read (under stop_gradient)
       hipLaunchKernelGGL(pseudo_beta_kernel, dim3((unsigned)((N + 127) / 128)), dim3(128), 0, st,
                          aatype, atom14, N, sv.rpb);
+      if (init_pos37)
+        hipLaunchKernelGGL(atom37_kernel, dim3((unsigned)((N * 37 + 255) / 256)), dim3(256), 0, st,
+                           atom14, aatype, seq_mask, w.a37_14, w.a37_mask, N, sv.rpos, sv.rposm);
       BC2N_HIP(hipMemcpyAsync(sv.rpair, sv.pair3, (size_t)M * CZ * 4, hipMemcpyDeviceToDevice, st));
       BC2N_HIP(hipMemcpyAsync(sv.rmsa0, sv.msa3, (size_t)N * CM * 4, hipMemcpyDeviceToDevice, st));
     }
@@ -819,8 +838,15 @@ void design_step_seq_fwd(hipStream_t st, const DesignStepW& w, int N, const int3
                          float* atom14, float* dgram, float* pae, float* plddt, float* expres,
                          const AtomsOut& atoms, const ConfOut& conf, void* save) {
   ds_check(w, N, 1);
-  if (cyclic_mode < -1 || cyclic_mode > 2)
-    throw std::invalid_argument("design step: cyclic_mode must be -1 (offset as given), 0, 1 or 2");
+  // the reference's attribute: bits 0-1 the offset mode, bit 2 the initial
+  // atom positions; -1 here takes `offset` as given
+  if (cyclic_mode < -1 || cyclic_mode > 6 || (cyclic_mode >= 0 && (cyclic_mode & 3) == 3))
+    throw std::invalid_argument("design step: cyclic_mode must be -1 (offset as given) or an offset "
+                                "mode 0, 1, 2 plus 4 for the initial atom positions");
+  const bool init_pos = cyclic_mode >= 0 && (cyclic_mode & 4);
+  if (init_pos && !atoms.tpl37)
+    throw std::invalid_argument("design step: the initial atom positions are the atoms operand "
+                                "(tpl_atoms37), which is missing");
   if (!(flexibility >= 0.f)) throw std::invalid_argument("design step: flexibility must be >= 0");
   nonnull(logits, "design step logits"); nonnull(flags_in, "design step flags");
   nonnull(sc4, "design step scalars"); nonnull(save, "design step save");
@@ -866,12 +892,13 @@ void design_step_seq_fwd(hipStream_t st, const DesignStepW& w, int N, const int3
   if (cyclic_mode >= 0) {
     // the offset feature the embedder reads, built here (bindcraft/af2.py:193)
     hipLaunchKernelGGL(cyclic_offsets_kernel, dim3((unsigned)N), dim3(64), 0, st, ri, ai, flags,
-                       seq_mask, N, cyclic_mode, x.off);
+                       seq_mask, N, cyclic_mode & 3, x.off);
     offset = x.off;
   }
   design_step_fwd(st, w, N, 1, x.tf, x.mf, ri, ai, ei, si, offset, seq_mask, act_const, x.aatype,
                   seeds, dropout, recycles, atom14, dgram, pae, plddt, expres, cv.p + cv.off,
-                  row ? x.row : nullptr, row ? x.rmask : nullptr);
+                  row ? x.row : nullptr, row ? x.rmask : nullptr,
+                  init_pos ? atoms.tpl37 : nullptr);
   if (atoms.atom37) {
     KTimed kt("design.atom37", st);
     hipLaunchKernelGGL(atom37_kernel, dim3((unsigned)((N * A37 + 255) / 256)), dim3(256), 0, st,

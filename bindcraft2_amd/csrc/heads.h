@@ -43,7 +43,8 @@ size_t structheads_save_bytes(int N, int depth);
 void structheads_fwd(hipStream_t st, const StructHeadsW& w, int N, int depth, const float* single,
                      const float* pair, const float* mask, const float* aatype,
                      const uint32_t* key, const uint32_t* enabled, bool dropout, float* atom14,
-                     float* dgram, float* pae, float* plddt, float* expres, void* save);
+                     float* dgram, float* pae, float* plddt, float* expres, void* save,
+                     const float* init_pos37 = nullptr);
 // Cotangents may be null (zero) -> dsingle [N][384], dpair [N][N][128].
 void structheads_bwd(hipStream_t st, const StructHeadsW& w, int N, int depth, const float* single,
                      const float* pair, const float* mask, const float* aatype, bool dropout,

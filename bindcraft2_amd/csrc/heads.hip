@@ -302,7 +302,8 @@ size_t structheads_save_bytes(int N, int depth) {
 void structheads_fwd(hipStream_t st, const StructHeadsW& w, int N, int depth, const float* single,
                      const float* pair, const float* mask, const float* aatype,
                      const uint32_t* key, const uint32_t* enabled, bool dropout, float* atom14,
-                     float* dgram, float* pae, float* plddt, float* expres, void* save) {
+                     float* dgram, float* pae, float* plddt, float* expres, void* save,
+                     const float* init_pos37) {
   sh_check(N, depth);
   nonnull(single, "structure heads single"); nonnull(pair, "structure heads pair");
   nonnull(mask, "structure heads mask"); nonnull(aatype, "structure heads aatype");
@@ -314,7 +315,7 @@ void structheads_fwd(hipStream_t st, const StructHeadsW& w, int N, int depth, co
   ShSave<Carver> sv(cv, N, depth);
   const long M2 = (long)N * N;
   fold_fwd(st, w.fold, N, depth, single, pair, mask, key, enabled, dropout, sv.act, sv.traj,
-           sv.fold);
+           sv.fold, init_pos37);
   Arena& ar = arena();
   std::lock_guard<std::recursive_mutex> lk(ar.lock());
   ar.reset(st, (size_t)M2 * SH_DGRAM * 4 + (size_t)N * (3 * CS + 2 * SC) * 4 + 4096);

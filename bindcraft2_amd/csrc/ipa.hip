@@ -699,9 +699,46 @@ __global__ void ident_frames_kernel(float* __restrict__ r, int N) {
   r[e] = (k == 0 || k == 4 || k == 8) ? 1.f : 0.f;
 }
 
+// Initial frames from atom positions (folding_multimer.py:508-515 with
+// initial_atom_pos; all_atom_multimer.py:943-966 and
+// geometry/rotation_matrix.py:79-99): R's columns are e0 = unit(C - CA),
+// e1 = unit((N - CA) minus its e0 part), e2 = e0 x e1, each unit() clipping
+// the norm at 1e-6 (an all-zero row gives the zero matrix, as in the
+// multimer model); t = CA / position_scale.  pos: atom37 [N][37][3].
+__global__ void ref_frames_kernel(const float* __restrict__ pos, int N, float* __restrict__ r) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= N) return;
+  const float* p = pos + (long)i * 37 * 3;
+  float e0[3], e1[3];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    e0[k] = p[2 * 3 + k] - p[1 * 3 + k];
+    e1[k] = p[0 * 3 + k] - p[1 * 3 + k];
+  }
+  const float n0 = sqrtf(fmaxf(e0[0] * e0[0] + e0[1] * e0[1] + e0[2] * e0[2], 1e-12f));
+#pragma unroll
+  for (int k = 0; k < 3; ++k) e0[k] /= n0;
+  const float c = e1[0] * e0[0] + e1[1] * e0[1] + e1[2] * e0[2];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) e1[k] -= c * e0[k];
+  const float n1 = sqrtf(fmaxf(e1[0] * e1[0] + e1[1] * e1[1] + e1[2] * e1[2], 1e-12f));
+#pragma unroll
+  for (int k = 0; k < 3; ++k) e1[k] /= n1;
+  const float e2[3] = {e0[1] * e1[2] - e0[2] * e1[1], e0[2] * e1[0] - e0[0] * e1[2],
+                       e0[0] * e1[1] - e0[1] * e1[0]};
+  float* o = r + (long)i * 12;
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    o[k * 3 + 0] = e0[k];
+    o[k * 3 + 1] = e1[k];
+    o[k * 3 + 2] = e2[k];
+    o[9 + k] = p[1 * 3 + k] * (1.f / POSITION_SCALE);
+  }
+}
+
 void fold_fwd(hipStream_t st, const FoldW& w, int N, int depth, const float* single,
               const float* pair, const float* mask, const uint32_t* key, const uint32_t* enabled,
-              bool dropout, float* act_out, float* traj, void* save) {
+              bool dropout, float* act_out, float* traj, void* save, const float* init_pos37) {
   fold_check(N, depth);
   nonnull(single, "fold single"); nonnull(pair, "fold pair"); nonnull(mask, "fold mask");
   nonnull(act_out, "fold act_out"); nonnull(traj, "fold traj"); nonnull(save, "fold save");
@@ -744,8 +781,14 @@ void fold_fwd(hipStream_t st, const FoldW& w, int N, int depth, const float* sin
     b.c_sm = 1; b.c_sn = M2;
     b.bias = w.b2d;
     gemm_f32(st, b, "fold.gemm_b2d");
-    // identity frames, written on the device (no host copy, no stream sync)
-    hipLaunchKernelGGL(ident_frames_kernel, dim3((N * 12 + 255) / 256), dim3(256), 0, st, rigA, N);
+    // identity frames (or those of the given atoms), written on the device
+    // (no host copy, no stream sync)
+    if (init_pos37)
+      hipLaunchKernelGGL(ref_frames_kernel, dim3((N + 127) / 128), dim3(128), 0, st, init_pos37, N,
+                         rigA);
+    else
+      hipLaunchKernelGGL(ident_frames_kernel, dim3((N * 12 + 255) / 256), dim3(256), 0, st, rigA,
+                         N);
   }
   const int NJ = (N + 63) / 64;
   for (int it = 0; it < depth; ++it) {

@@ -169,10 +169,13 @@ struct FoldW {
 };
 FoldW fold_weights(WeightStore& ws);
 size_t fold_save_bytes(int N, int depth);
-// act_out [N][384]; traj [depth][N][3][4] = [R | 20 t] after each iteration
+// act_out [N][384]; traj [depth][N][3][4] = [R | 20 t] after each iteration.
+// init_pos37 (atom37 [N][37][3]) or null: the first frames are those of its
+// N, CA, C atoms instead of the identity (the model's initial_atom_pos).
 void fold_fwd(hipStream_t st, const FoldW& w, int N, int depth, const float* single,
               const float* pair, const float* mask, const uint32_t* key, const uint32_t* enabled,
-              bool dropout, float* act_out, float* traj, void* save);
+              bool dropout, float* act_out, float* traj, void* save,
+              const float* init_pos37 = nullptr);
 // d_act / d_traj may be null (zero cotangent)
 void fold_bwd(hipStream_t st, const FoldW& w, int N, int depth, const float* single,
               const float* pair, const float* mask, bool dropout, const void* save,

@@ -608,7 +608,8 @@ class DesignStepSeq(DesignStep):
     def forward(self, logits, flags, scalars, ids, seq_mask, aa_bias=None, act_const=None,
                 offset=None, seeds=None, dropout=True, save=None, omitted_half=OMITTED_HALF,
                 interface_asym=None, recycles=0, atom37=False, tpl_atoms37=None,
-                tpl_mask37=None, length=None, cyclic_mode=None, flexibility=0.0):
+                tpl_mask37=None, length=None, cyclic_mode=None, flexibility=0.0,
+                initial_atom_pos=False):
         """-> ((atom14, distogram, pae, plddt, expres), save), plus the confidence
         metrics (plddt, pae, ptm, iptm, iptm_per_residue, expres_ca) as a third
         element when interface_asym (i32 [N]) is given.  With atom37=True (or
@@ -619,9 +620,15 @@ class DesignStepSeq(DesignStep):
         None for all N rows.  cyclic_mode ('distance', 'direction',
         'neighbours' or None = `offset` as given) builds the offset feature
         from the ids and the CYCLIC flag (bit 6); flexibility is the target
-        flexibility of the template row."""
+        flexibility of the template row; initial_atom_pos starts the structure
+        module from tpl_atoms37 (needs a cyclic_mode, as the reference packs
+        it into that attribute)."""
         modes = ("distance", "direction", "neighbours")
         cmode = -1 if cyclic_mode is None else modes.index(cyclic_mode)
+        if initial_atom_pos:
+            if cyclic_mode is None:
+                raise ValueError("initial_atom_pos goes with a cyclic_mode")
+            cmode |= 4
         n, dev = logits.shape[0], logits.device
         _check_seeds(seeds, dropout, recycles)
         e = lambda *sh: torch.empty(*sh, dtype=torch.float32, device=dev)

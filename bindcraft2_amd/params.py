@@ -400,9 +400,9 @@ def init_residue_tables(rng):
     # the atom37 gather of the design step's outputs: every atom37 slot reads
     # one atom14 slot (CA always slot 1, as in residue_constants)
     a37 = rng.integers(0, 14, (21, 37))
-    a37[:, 1] = 1
+    a37[:, :3] = [0, 1, 2]  # N, CA, C: atom14 slots 0-2 and present, as in every real type
     m37 = (rng.random((21, 37)) < 0.5).astype(np.float32)
-    m37[:, 1] = 1.0
+    m37[:, :3] = 1.0
     out["atom37_to_atom14"] = a37.astype(np.float32)
     out["atom37_mask"] = m37
     # the template row's chi angles: four distinct atom37 slots per chi (as

@@ -497,8 +497,12 @@ int bc2n_design_inputs_bwd(void* stream, const float* d_target_feat, const float
  * native/inputfeat.cuh offsetK), ignoring `offset`.  flexibility: the
  * reference's target flexibility f (>= 0; 0 = off): a TEMPLATE residue not
  * designed whose residue_index i has floor((i + 1) f) > floor(i f) is a gap
- * of the template row (bindcraft/af2.py:150-157).  The initial-atom-position
- * bit of the reference's cyclic_mode (4) is not built.
+ * of the template row (bindcraft/af2.py:150-157).  cyclic_mode + 4 (the
+ * reference's bit 2, bc2's large_complex_initialization; needs an offset
+ * mode and tpl_atoms37): the first pass's structure module starts from the
+ * frames of tpl_atoms37's N, CA, C (an all-zero residue: the zero matrix, as
+ * the multimer model's), each recycle pass from the previous pass's atom37
+ * positions (folding_multimer.py:508-515, native/design_step.cuh:1112-1114).
  * RUNTIME LENGTH (the reference's `n`, native/design_step.cuh:10-19,
  * :42-58): n is NULL (all N rows real) or an i32 scalar in device memory,
  * 1 <= *n <= N, read by the kernels and never by the host, so one set of

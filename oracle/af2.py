@@ -536,10 +536,31 @@ def fold_iteration(act, R, t, act_2d, mask, p, key, use_dropout):
     return act, R @ Ru, t_new
 
 
-def fold(single, pair, mask, params, depth, key, use_dropout, dtype=torch.float64):
-    """folding_multimer.py:476-548 (generate_monomer_rigids, no initial atom
-    positions): LN + initial projection, identity frames, LN(pair), then
-    `depth` FoldIterations sharing one set of weights with per-layer keys
+def frames_from_atoms(pos37):
+    """folding_multimer.py:508-515 (initial_atom_pos) with
+    all_atom_multimer.py:943-966 and geometry/rotation_matrix.py:79-99:
+    R's columns e0 = unit(C - CA), e1 = unit((N - CA) - ((N - CA).e0) e0),
+    e2 = e0 x e1, unit() clipping the norm at 1e-6 (an all-zero residue
+    gives the zero matrix); t = CA / POSITION_SCALE."""
+    pos = torch.as_tensor(pos37)
+
+    def unit(v):
+        return v / torch.sqrt(torch.clamp((v * v).sum(-1, keepdim=True), min=1e-12))
+
+    n, ca, c = pos[:, 0], pos[:, 1], pos[:, 2]
+    e0 = unit(c - ca)
+    e1 = n - ca
+    e1 = unit(e1 - (e1 * e0).sum(-1, keepdim=True) * e0)
+    e2 = torch.linalg.cross(e0, e1)
+    return torch.stack([e0, e1, e2], -1), ca / POSITION_SCALE
+
+
+def fold(single, pair, mask, params, depth, key, use_dropout, dtype=torch.float64,
+         init_pos=None):
+    """folding_multimer.py:476-548 (generate_monomer_rigids): LN + initial
+    projection, identity frames (or, given initial atom positions init_pos
+    [N,37,3], frames_from_atoms of them), LN(pair), then `depth`
+    FoldIterations sharing one set of weights with per-layer keys
     split(key, depth).  Returns the final act and the trajectory
     [depth, N, 3, 4] = [R | POSITION_SCALE * t] (StructureModule 'traj')."""
     P = Params(params, "param/", dtype)
@@ -547,8 +568,11 @@ def fold(single, pair, mask, params, depth, key, use_dropout, dtype=torch.float6
     act = linear(act, P.sub("initial_projection/"))
     act_2d = layer_norm(pair, P("pair_layer_norm/scale"), P("pair_layer_norm/offset"))
     n = single.shape[0]
-    R = torch.eye(3, dtype=single.dtype).expand(n, 3, 3)
-    t = torch.zeros(n, 3, dtype=single.dtype)
+    if init_pos is None:
+        R = torch.eye(3, dtype=single.dtype).expand(n, 3, 3)
+        t = torch.zeros(n, 3, dtype=single.dtype)
+    else:
+        R, t = frames_from_atoms(torch.as_tensor(init_pos).to(single.dtype).detach())
     keys = jax_prng.split(key, depth) if key is not None else [None] * depth
     traj = []
     fp = P.sub("fold_iteration/")
@@ -647,14 +671,14 @@ def heads(pair, act, single, params, dtype=torch.float64):
 
 
 def structure_heads(single, pair, mask, aatype, params, depth, key, use_dropout, tables,
-                    dtype=torch.float64):
+                    dtype=torch.float64, init_pos=None):
     """The post-trunk step of the reference's StructureHeadsFwd
     (native/ffi.cu:530-575): the fold iterations (folding_multimer.py:
     476-548), the last iteration's sidechain on [act, initial_act] with the
     backbone frame scaled to angstroms (:465-466; final_atom14_positions,
     :604-606), and the heads.  Returns (atom14 [N,14,3], distogram [N,N,64],
     pae [N,N,64], plddt [N,50], experimentally resolved [N,37])."""
-    act, traj = fold(single, pair, mask, params, depth, key, use_dropout, dtype)
+    act, traj = fold(single, pair, mask, params, depth, key, use_dropout, dtype, init_pos)
     P = Params(params, "param/", dtype)
     init = layer_norm(single, P("single_layer_norm/scale"), P("single_layer_norm/offset"))
     aat = torch.as_tensor(aatype).long().clamp(0, 20)
@@ -749,7 +773,7 @@ def template_row(template_aatype, atoms37, mask37, p_emb, tables, dtype=torch.fl
 
 def design_step(target_feat, msa_feat, ids, offset, seq_mask, act_const, aatype, emsa, prm,
                 depths, keys, use_dropout, tables, recycles=0, tpl_row=None,
-                dtype=torch.float64):
+                dtype=torch.float64, init_pos=None):
     """The trunk of one design step, input features to the structure-module
     outputs (modules_multimer.py:441-700, EmbeddingsAndEvoformer, then
     AlphaFoldIteration's structure module and heads): the embedder plus the
@@ -765,7 +789,10 @@ def design_step(target_feat, msa_feat, ids, offset, seq_mask, act_const, aatype,
     msa[0] to the next pass's recycle terms under stop_gradient; `keys` is
     then a list of recycles + 1 such dicts, one per pass.  tpl_row = (row
     [N, 256], mask [N]) is the template's MSA row, appended to the main
-    stack's msa and msa mask (modules_multimer.py:608-617)."""
+    stack's msa and msa mask (modules_multimer.py:608-617).  init_pos
+    [N,37,3]: the first pass's structure module starts from these atoms'
+    frames, each later pass from the previous pass's atom37 positions
+    (native/design_step.cuh:1112-1114, the model's initial_atom_pos)."""
     keys = keys if isinstance(keys, (list, tuple)) else [keys]
     if len(keys) != recycles + 1:
         raise ValueError("design_step: one key dict per pass")
@@ -795,8 +822,12 @@ def design_step(target_feat, msa_feat, ids, offset, seq_mask, act_const, aatype,
             msa, pair = evoformer_stack(msa, pair, mmask, pmask, prm["main"], depths["main"],
                                         k["main"], use_dropout, dtype=dtype)
             single = linear(msa[0], Params(prm["emb"], "param/single_activations/", dtype))
+            start = None
+            if init_pos is not None:
+                start = (torch.as_tensor(init_pos) if p == 0 else
+                         atom14_to_atom37(prev[0], aatype, seq_mask, tables)[0])
             out = structure_heads(single, pair, seq_mask, aatype, prm["post"], depths["fold"],
-                                  k["fold"], use_dropout, tables, dtype)
+                                  k["fold"], use_dropout, tables, dtype, init_pos=start)
         if not final:
             prev = (out[0].detach(), pair.detach(), msa[0].detach())
     return out
@@ -927,7 +958,8 @@ def align_to_template(atom37, exists, tpl_atoms37, tpl_mask37, flags):
 
 def design_step_seq(logits, flags, scalars, ids, offset, seq_mask, act_const, emsa, prm, depths,
                     keys, use_dropout, tables, bias=None, recycles=0, tpl_atoms37=None,
-                    tpl_mask37=None, cyclic_mode=None, flexibility=0.0, dtype=torch.float64):
+                    tpl_mask37=None, cyclic_mode=None, flexibility=0.0,
+                    initial_atom_pos=False, dtype=torch.float64):
     """design_step from the designed logits: sequence_features ->
     design_inputs -> design_step (one MSA row).  With template atoms
     (tpl_atoms37 [N,37,3], tpl_mask37 [N,37]) the outputs gain the predicted
@@ -937,7 +969,9 @@ def design_step_seq(logits, flags, scalars, ids, offset, seq_mask, act_const, em
     the main stack (modules_multimer.py:608-617, the reference's S = 2).
     cyclic_mode (one of CYCLIC_MODES) replaces `offset` by the cyclic
     sequence offsets (bindcraft/af2.py:193); flexibility > 0 turns the
-    flexible target residues into gaps of the template (af2.py:153-157)."""
+    flexible target residues into gaps of the template (af2.py:153-157);
+    initial_atom_pos starts the structure module from tpl_atoms37 (af2.py:193,
+    large_complex_initialization)."""
     feat, prof = sequence_features(logits, flags, *scalars, bias=bias)
     tf, mf, aatype = design_inputs(feat, prof)
     if cyclic_mode is not None:
@@ -957,7 +991,9 @@ def design_step_seq(logits, flags, scalars, ids, offset, seq_mask, act_const, em
         t_msk = np.asarray(tpl_mask37) * tres[:, None] * ~(flex[:, None] & side[None])
         row = template_row(t_aat, t_pos, t_msk, prm["emb"], tables, dtype)
     out = design_step(tf, mf, ids, offset, seq_mask, act_const, aatype, emsa, prm, depths, keys,
-                      use_dropout, tables, recycles=recycles, tpl_row=row, dtype=dtype)
+                      use_dropout, tables, recycles=recycles, tpl_row=row, dtype=dtype,
+                      init_pos=(torch.as_tensor(np.asarray(tpl_atoms37), dtype=dtype)
+                                if initial_atom_pos else None))
     if tpl_atoms37 is None:
         return out
     a37, ex = atom14_to_atom37(out[0], aatype, seq_mask, tables)

@@ -498,3 +498,88 @@ def test_design_step_seq_cyclic_flexible(cuda, mode, flex):
     m = metrics(dlog.cpu().double(), dref)
     print("  d logits", m)
     assert m["cos"] >= 0.999 and m["rel_l2"] <= 5e-2
+
+
+@pytest.mark.parametrize("recycles", [0, 1])
+def test_design_step_seq_initial_atom_pos(cuda, recycles):
+    """The initial atom positions (bit 2 of the reference's cyclic_mode,
+    bc2's large_complex_initialization): the structure module's first frames
+    are those of the atoms operand's N, CA, C (all-zero binder rows: the zero
+    matrix, as the multimer model's), a recycle pass's those of the previous
+    pass's atom37 positions; against the oracle at the step's bars, and far
+    from the oracle that starts from the identity."""
+    n, nb = 64, 24
+    print(f"design step initial atom positions n={n} recycles={recycles}", flush=True)
+    depths = {"tpl": 1, "extra": 1, "main": 1, "fold": 2}
+    rng = np.random.default_rng(9600 + recycles)
+    prm = {"emb": bparams.init_embedder_params(rng),
+           "tpl": bparams.init_template_embedding_params(depths["tpl"], rng, gates="random",
+                                                         ln="random"),
+           "extra": _extra_params(depths["extra"], rng),
+           "main": bparams.init_block_params(0, rng, gates="random", ln="random"),
+           "post": bparams.init_structure_heads_params(rng, final="random", ln="random")}
+    prm["emb"]["param/prev_pos_linear/weights"] *= 1e-3  # see test_gpu_design_step.py
+    tables = bparams.init_residue_tables(rng)
+    prm["post"].update({f"const/{k}": v for k, v in tables.items()})
+    dirs = [weights_dir(prm[k], f"dsi_{k}_{recycles}") for k in ("emb", "tpl", "extra", "main",
+                                                                 "post")]
+    stacks = ("tpl", "extra", "main", "fold")
+    x = rng.standard_normal((n, 20)).astype(np.float32)
+    x[nb:] = np.eye(20, dtype=np.float32)[rng.integers(0, 20, n - nb)]
+    flags = np.zeros(n, np.uint8)
+    flags[:nb] = 1
+    flags[nb:] = 2
+    ids = [np.concatenate([np.arange(nb), np.arange(n - nb)]), np.repeat([1, 2], [nb, n - nb]),
+           np.repeat([1, 2], [nb, n - nb]), np.ones(n)]
+    ids = [v.astype(np.float32) for v in ids]
+    seq_mask = np.ones(n, np.float32)
+    tpl37 = (8 * rng.standard_normal((n, 37, 3))).astype(np.float32)
+    tpl37[:nb] = 0.0  # the binder has no atoms yet
+    tplm37 = (rng.random((n, 37)) < 0.9).astype(np.float32)
+    tplm37[:nb] = 0.0
+    act_const = (0.5 * rng.standard_normal((n, n, 64))).astype(np.float32)
+    scalars = (0.8, 0.25, 1.2, 1.5)
+    keys = [{k: J.prng_key(900 + 10 * p + i) for i, k in enumerate(stacks)}
+            for p in range(recycles + 1)]
+    seeds = torch.tensor([[int(kp[k][0]), int(kp[k][1]), 1] for kp in keys for k in stacks],
+                         dtype=torch.int64)
+    shapes = ((n, 14, 3), (n, n, 64), (n, n, 64), (n, 50), (n, 37))
+    cts = [rng.standard_normal(sh).astype(np.float32) for sh in shapes]
+    emsa = torch.as_tensor(rng.standard_normal((1, n, 64)), dtype=D)
+
+    def oracle(init, grad):
+        t = torch.tensor(x, dtype=D, requires_grad=grad)
+        r = af2.design_step_seq(t, flags, scalars, ids, None, torch.as_tensor(seq_mask, dtype=D),
+                                torch.as_tensor(act_const, dtype=D), emsa, prm, depths, keys,
+                                True, tables, recycles=recycles, tpl_atoms37=tpl37,
+                                tpl_mask37=tplm37, cyclic_mode="direction",
+                                initial_atom_pos=init)
+        if not grad:
+            return r, None
+        loss = sum((a * torch.as_tensor(c, dtype=D)).sum() for a, c in zip(r[:5], cts))
+        return r, torch.autograd.grad(loss, (t,))[0]
+
+    ref, dref = oracle(True, True)
+    plain, _ = oracle(False, False)
+
+    T = lambda a: None if a is None else torch.as_tensor(a, device=cuda)
+    step = ops.DesignStepSeq(*dirs, depths=tuple(depths[k] for k in stacks))
+    sc = torch.tensor(scalars, dtype=torch.float32, device=cuda)
+    outs, save, _ = step.forward(T(x), T(flags), sc, [T(v) for v in ids], T(seq_mask),
+                                 act_const=T(act_const), seeds=seeds.to(torch.uint32).to(cuda),
+                                 dropout=True, recycles=recycles, tpl_atoms37=T(tpl37),
+                                 tpl_mask37=T(tplm37), cyclic_mode="direction",
+                                 initial_atom_pos=True)[:3]
+    dlog = step.backward([T(c) for c in cts], T(x), T(flags), sc, T(seq_mask), save,
+                         with_template=True, dropout=True)
+    torch.cuda.synchronize()
+    for name, g, r, p in zip(("atom14", "distogram", "pae", "plddt", "expres"), outs, ref, plain):
+        m = metrics(g.cpu().double(), r.detach())
+        away = metrics(g.cpu().double(), p.detach())
+        print(f"  {name}", m, "| from the identity: rel", away["rel_l2"])
+        assert m["rel_l2"] <= 2e-2 and m["max_rel"] <= 2e-2 and m["cos"] >= 0.9999, name
+        if name == "atom14":
+            assert away["rel_l2"] > 10 * m["rel_l2"], "the initial positions were not exercised"
+    m = metrics(dlog.cpu().double(), dref)
+    print("  d logits", m)
+    assert m["cos"] >= 0.999 and m["rel_l2"] <= 5e-2

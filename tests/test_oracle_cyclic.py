@@ -75,3 +75,22 @@ def test_flexible_residue_is_a_template_gap():
     msk2[4, 5:] = 0
     row2, _ = af2.template_row(aat2, pos, msk2, prm, tables)
     torch.testing.assert_close(row2[4], row[2], rtol=0, atol=1e-12)
+
+
+def test_frames_from_atoms_recovers_the_rotation():
+    """A backbone triple in the canonical frame (C on +x, N in the xy plane
+    with y > 0, CA at 0) moved by a rotation Q and a shift s gives back
+    R = Q and t = s / position_scale; an all-zero residue (no atoms) gives
+    the zero matrix, as the multimer model's Gram-Schmidt does."""
+    from scipy.spatial.transform import Rotation
+    rng = np.random.default_rng(5)
+    can = np.array([[-0.52, 1.36, 0.0], [0.0, 0.0, 0.0], [1.52, 0.0, 0.0]])  # N, CA, C
+    Q = Rotation.random(4, random_state=7).as_matrix()
+    s = 10 * rng.standard_normal((4, 3))
+    pos = np.zeros((5, 37, 3))
+    for i in range(4):
+        pos[i, :3] = can @ Q[i].T + s[i]
+    R, t = af2.frames_from_atoms(torch.as_tensor(pos))
+    torch.testing.assert_close(R[:4], torch.as_tensor(Q), rtol=0, atol=1e-12)
+    torch.testing.assert_close(t[:4], torch.as_tensor(s) / af2.POSITION_SCALE, rtol=0, atol=1e-12)
+    assert torch.equal(R[4], torch.zeros(3, 3, dtype=R.dtype)) and not t[4].any()
