@@ -401,6 +401,20 @@ size_t bc2n_evoformer_detached_bytes(const char* weights_dir, int N, int S, int6
   return n;
 }
 
+int bc2n_set_save_policy(int policy) { return set_save_policy(policy); }
+
+int bc2n_evoformer_replays(const char* weights_dir, int N, int S, int64_t depth,
+                           int64_t pair_only) {
+  int r = -1;
+  if (guarded([&] {
+        need(weights_dir != nullptr, "weights_dir required");
+        const StackW& w = stack_w(weights_dir, (int)depth, evo_kind(pair_only));
+        r = stack_replays(w, N, S, (int)depth) ? 1 : 0;
+      }) != 0)
+    return -1;
+  return r;
+}
+
 static const uint32_t* stack_key(hipStream_t st, const uint32_t* seed, int seed_len,
                                  uint32_t* scratch) {
   if (seed_len == 3) return seed;  // [k0, k1, enabled]: jax.random.key_data
@@ -721,7 +735,7 @@ size_t bc2n_fold_save_bytes(const char* weights_dir, int N, int64_t depth) {
   size_t n = 0;
   if (guarded([&] {
         need(weights_dir != nullptr, "weights_dir required");
-        need(N > 0 && N <= 512 && depth > 0, "fold: bad shape");
+        need(N > 0 && N <= 1024 && depth > 0, "fold: bad shape");
         (void)fold_w(weights_dir);
         n = fold_save_bytes(N, (int)depth) + 256;
       }) != 0)
@@ -735,7 +749,7 @@ int bc2n_fold_fwd(void* stream, const float* single, const float* pair, const fl
   return guarded([&] {
     hipStream_t st = as_stream(stream);
     need(weights_dir && single && pair && seq_mask && act && traj && save, "null operand");
-    need(N > 0 && N <= 512 && depth > 0, "fold: bad shape");
+    need(N > 0 && N <= 1024 && depth > 0, "fold: bad shape");
     need(seed_len == 2 || seed_len == 3, "fold: seed must be u32[2] or u32[3]");
     need(!dropout || seed, "fold: dropout needs the seed operand");
     const FoldW& w = fold_w(weights_dir);
@@ -754,7 +768,7 @@ int bc2n_fold_bwd(void* stream, const float* d_act, const float* d_traj, const f
                   float* dpair) {
   return guarded([&] {
     need(weights_dir && single && pair && seq_mask && save && dsingle && dpair, "null operand");
-    need(N > 0 && N <= 512 && depth > 0, "fold: bad shape");
+    need(N > 0 && N <= 1024 && depth > 0, "fold: bad shape");
     const FoldW& w = fold_w(weights_dir);
     fold_bwd(as_stream(stream), w, N, (int)depth, single, pair, seq_mask, dropout != 0, save,
              d_act, d_traj, dsingle, dpair);
@@ -773,7 +787,7 @@ const StructHeadsW& sh_w(const char* dir) {
 int bc2n_sm_prealloc(int N, int depth, const char* weights_dir) {
   return guarded([&] {
     need(weights_dir != nullptr, "weights_dir required");
-    need(N > 0 && N <= 512 && depth > 0, "structure heads: bad shape");
+    need(N > 0 && N <= 1024 && depth > 0, "structure heads: bad shape");
     const size_t f0 = free_bytes();
     const StructHeadsW& w = sh_w(weights_dir);
     const long M = (long)N * N;
@@ -799,7 +813,7 @@ size_t bc2n_structure_heads_save_bytes(const char* weights_dir, int N, int64_t d
   size_t n = 0;
   if (guarded([&] {
         need(weights_dir != nullptr, "weights_dir required");
-        need(N > 0 && N <= 512 && depth > 0, "structure heads: bad shape");
+        need(N > 0 && N <= 1024 && depth > 0, "structure heads: bad shape");
         (void)sh_w(weights_dir);
         n = structheads_save_bytes(N, (int)depth) + 256;
       }) != 0)
@@ -816,7 +830,7 @@ int bc2n_structure_heads_fwd(void* stream, const float* single, const float* pai
     hipStream_t st = as_stream(stream);
     need(weights_dir && single && pair && seq_mask && aatype && save, "null operand");
     need(atom14 && distogram && pae && plddt && expres, "null output");
-    need(N > 0 && N <= 512 && depth > 0, "structure heads: bad shape");
+    need(N > 0 && N <= 1024 && depth > 0, "structure heads: bad shape");
     need(seed_len == 2 || seed_len == 3, "structure heads: seed must be u32[2] or u32[3]");
     need(!dropout || seed, "structure heads: dropout needs the seed operand");
     const StructHeadsW& w = sh_w(weights_dir);
@@ -838,7 +852,7 @@ int bc2n_structure_heads_bwd(void* stream, const float* single, const float* pai
   return guarded([&] {
     need(weights_dir && single && pair && seq_mask && aatype && save && dsingle && dpair,
          "null operand");
-    need(N > 0 && N <= 512 && depth > 0, "structure heads: bad shape");
+    need(N > 0 && N <= 1024 && depth > 0, "structure heads: bad shape");
     const StructHeadsW& w = sh_w(weights_dir);
     structheads_bwd(as_stream(stream), w, N, (int)depth, single, pair, seq_mask, aatype,
                     dropout != 0, save, d_atom14, d_distogram, d_pae, d_plddt, d_expres, dsingle,

@@ -33,8 +33,19 @@ StackW stack_weights(WeightStore& ws, int depth, StackKind kind,
                      const std::string& root = "param/");
 
 // Bytes of the save-set a forward with these shapes writes and the backward
-// reads (every block's carries and module save-sets, the dropout tables).
+// reads: every block's carries and module save-sets and the dropout tables,
+// or, in the replay tier, every block's input carries and one block's module
+// save-sets (the backward runs each block's forward again first).
 size_t stack_save_bytes(const StackW& w, int N, int S, int depth);
+
+// The save policy of every stack in the process: 0 = by size (the replay
+// tier when the full save-set would take more than 60% of the device's
+// memory), 1 = always full, 2 = always the replay tier.  Returns the
+// previous policy (-1 for a bad value).  A forward and its backward must run
+// under the same policy.
+int set_save_policy(int policy);
+// Whether a stack of these shapes keeps the replay tier under the policy.
+bool stack_replays(const StackW& w, int N, int S, int depth);
 
 // Bytes of a detached forward's scratch (detached = true below): one
 // block's module save-sets, two carries of each track, the dropout tables.

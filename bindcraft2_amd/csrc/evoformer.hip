@@ -34,13 +34,41 @@ struct Layout {
   // a detached forward (no backward follows): one block region reused by
   // every block and two carry slots used in turn, instead of the save-set
   bool detached = false;
+  // the replay tier: every block's input carries and one block region; the
+  // backward runs each block's forward again into that region first
+  bool replay = false;
   size_t opm = 0, row = 0, col = 0, mtr = 0, tmo = 0, tmi = 0, tas = 0, tae = 0, ptr = 0;
   size_t pair_bytes = 0, msa_bytes = 0, block_bytes = 0;
   size_t tbl_per_block = 0;  // floats
   // offsets of the save-set regions
-  size_t off_carry_p = 0, off_carry_m = 0, off_msa_in = 0, off_pair_in = 0, off_tbl = 0,
-         off_keys = 0, total = 0;
+  size_t off_carry_p = 0, off_carry_m = 0, off_msa_in = 0, off_pair_in = 0, off_scr = 0,
+         off_tbl = 0, off_keys = 0, total = 0;
 };
+
+// Which save-set a stack keeps: 0 = by size (the replay tier when the full
+// one would take more than 60% of the device's memory), 1 = always the full
+// one, 2 = always the replay tier.  Process-wide; the forward and its
+// backward must see the same policy (bc2n_set_save_policy).
+int g_save_policy = 0;
+
+size_t device_total_bytes() {
+  static size_t cache[64] = {};
+  int dev = 0;
+  BC2N_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) throw std::runtime_error("stack: device index out of range");
+  if (!cache[dev]) {
+    size_t fr = 0, tot = 0;
+    BC2N_HIP(hipMemGetInfo(&fr, &tot));
+    cache[dev] = tot;
+  }
+  return cache[dev];
+}
+
+bool use_replay(size_t full_bytes) {
+  if (g_save_policy == 1) return false;
+  if (g_save_policy == 2) return true;
+  return full_bytes > device_total_bytes() / 10 * 6;
+}
 
 Layout layout(const StackW& w, int N, int S, int depth, bool detached = false) {
   Layout L;
@@ -68,17 +96,25 @@ Layout layout(const StackW& w, int N, int S, int depth, bool detached = false) {
   L.block_bytes = L.opm + L.row + L.col + L.mtr + L.tmo + L.tmi + L.tas + L.tae + L.ptr +
                   5 * L.pair_bytes + 2 * L.msa_bytes;
   L.tbl_per_block = (size_t)N * L.Cm + 4 * (size_t)N * L.Cz;
-  const size_t regions = detached ? 1 : (size_t)depth, carries = detached ? 2 : (size_t)depth - 1;
-  L.off_carry_p = regions * L.block_bytes;
-  L.off_carry_m = L.off_carry_p + carries * L.pair_bytes;
-  // the stack's msa input, kept for the backward of block 0
-  L.off_msa_in = L.off_carry_m + carries * L.msa_bytes;
-  // the template iteration's first module reads the block input itself: the
-  // stack's pair input is kept for block 0's backward
-  L.off_pair_in = L.off_msa_in + (detached ? 0 : L.msa_bytes);
-  L.off_tbl = L.off_pair_in + (L.tpl && !detached ? L.pair_bytes : 0);
-  L.off_keys = L.off_tbl + al256((size_t)depth * L.tbl_per_block * 4);
-  L.total = L.off_keys + al256((size_t)depth * 9 * 2 * 4);
+  auto place = [&](bool replay) {
+    L.replay = replay;
+    const size_t regions = (detached || replay) ? 1 : (size_t)depth;
+    const size_t carries = detached ? 2 : (size_t)depth - 1;
+    L.off_carry_p = regions * L.block_bytes;
+    L.off_carry_m = L.off_carry_p + carries * L.pair_bytes;
+    // the stack's msa input, kept for the backward of block 0
+    L.off_msa_in = L.off_carry_m + carries * L.msa_bytes;
+    // the template iteration's first module reads the block input itself, and
+    // a replayed block 0 reads both inputs: the stack's pair input is kept
+    L.off_pair_in = L.off_msa_in + (detached ? 0 : L.msa_bytes);
+    L.off_scr = L.off_pair_in + ((L.tpl || replay) && !detached ? L.pair_bytes : 0);
+    // the replayed last block's outputs land here (the caller's are not given)
+    L.off_tbl = L.off_scr + (replay ? L.pair_bytes + L.msa_bytes : 0);
+    L.off_keys = L.off_tbl + al256((size_t)depth * L.tbl_per_block * 4);
+    L.total = L.off_keys + al256((size_t)depth * 9 * 2 * 4);
+  };
+  place(false);
+  if (!detached && use_replay(L.total)) place(true);
   (void)K_OPM; (void)K_COL; (void)K_MTR; (void)K_PTR; (void)T_PTR;
   return L;
 }
@@ -285,12 +321,13 @@ void stack_fwd(hipStream_t st, const StackW& w, int N, int S, int depth, const f
   if (!L.pair_only && !detached)
     BC2N_HIP(hipMemcpyAsync(sv + L.off_msa_in, msa, (size_t)S * N * L.Cm * 4,
                             hipMemcpyDeviceToDevice, st));
-  if (L.tpl && !detached)
+  if ((L.tpl || L.replay) && !detached)
     BC2N_HIP(hipMemcpyAsync(sv + L.off_pair_in, pair, (size_t)N * N * L.Cz * 4,
                             hipMemcpyDeviceToDevice, st));
+  const bool one_region = detached || L.replay;
   for (int b = 0; b < depth; ++b)
     block_fwd(st, w.blocks[b], L, b, t, frame(L, sv, b, pair, msa, pair_out, msa_out), pmask,
-              mmask, sv + (detached ? 0 : (size_t)b * L.block_bytes));
+              mmask, sv + (one_region ? 0 : (size_t)b * L.block_bytes));
 }
 
 void stack_bwd(hipStream_t st, const StackW& w, int N, int S, int depth, const float* pmask,
@@ -307,9 +344,40 @@ void stack_bwd(hipStream_t st, const StackW& w, int N, int S, int depth, const f
     BC2N_HIP(hipMemcpyAsync(dpair, ct_pair, (size_t)M * L.Cz * 4, hipMemcpyDeviceToDevice, st));
   if (!L.pair_only && dmsa != ct_msa)
     BC2N_HIP(hipMemcpyAsync(dmsa, ct_msa, (size_t)S * N * L.Cm * 4, hipMemcpyDeviceToDevice, st));
+  if (L.replay) {
+    // each block's forward again from its kept inputs, into the one region,
+    // then its backward (the recomputed carries are the same bits)
+    const float* pin0 = reinterpret_cast<const float*>(sv + L.off_pair_in);
+    const float* min0 = reinterpret_cast<const float*>(sv + L.off_msa_in);
+    float* scr_p = reinterpret_cast<float*>(sv + L.off_scr);
+    float* scr_m = L.pair_only ? nullptr : reinterpret_cast<float*>(sv + L.off_scr + L.pair_bytes);
+    for (int b = depth - 1; b >= 0; --b) {
+      {
+        KTimed kt("stack.replay", st);
+        block_fwd(st, w.blocks[b], L, b, t,
+                  frame(L, sv, b, b == 0 ? pin0 : nullptr, b == 0 ? min0 : nullptr, scr_p, scr_m),
+                  pmask, mmask, sv);
+      }
+      Frame f = frame(L, sv, b, b == 0 ? pin0 : nullptr, b == 0 ? min0 : nullptr, nullptr, nullptr);
+      block_bwd(st, w.blocks[b], L, b, t, f, pmask, mmask, sv, dpair, dmsa);
+    }
+    return;
+  }
   for (int b = depth - 1; b >= 0; --b)
     block_bwd(st, w.blocks[b], L, b, t, frame(L, sv, b, nullptr, nullptr, nullptr, nullptr),
               pmask, mmask, sv + (size_t)b * L.block_bytes, dpair, dmsa);
+}
+
+int set_save_policy(int p) {
+  if (p < 0 || p > 2) return -1;
+  const int old = g_save_policy;
+  g_save_policy = p;
+  return old;
+}
+
+bool stack_replays(const StackW& w, int N, int S, int depth) {
+  stack_check(w, N, S, depth);
+  return layout(w, N, S, depth).replay;
 }
 
 }  // namespace bc2n

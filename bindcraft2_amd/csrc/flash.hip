@@ -90,17 +90,17 @@ __device__ __forceinline__ h16x8 ld_tr8(const h16* T, int ld, int r0, int c0, in
 // whole tile.  The loads and the LDS stores are separate steps, so a kernel
 // walking several rows can hold the next row's tiles in registers while it
 // computes.
-template <int D, int N>
+template <int D, int N, int T = 256>
 struct RowPair {
   static constexpr int CPR = D / 8;  // 16-byte chunks per row
-  static constexpr int IT = (N * CPR + 255) / 256;
+  static constexpr int IT = (N * CPR + T - 1) / T;
   h16x8 va[IT], vb[IT];
   __device__ __forceinline__ void load(const h16* sA, long lda, const h16* sB, long ldb, int tid,
                                        int rows) {
     const int items = rows * CPR;
 #pragma unroll
     for (int i = 0; i < IT; ++i) {
-      const int c = tid + 256 * i;
+      const int c = tid + T * i;
       if (c < items) {
         va[i] = ld8(sA + (long)(c / CPR) * lda + (c % CPR) * 8);
         vb[i] = ld8(sB + (long)(c / CPR) * ldb + (c % CPR) * 8);
@@ -111,7 +111,7 @@ struct RowPair {
     const int items = rows * CPR;
 #pragma unroll
     for (int i = 0; i < IT; ++i) {
-      const int c = tid + 256 * i;
+      const int c = tid + T * i;
       if (c < items) {
         st8(&dA[(c / CPR) * lds_ld<D>() + (c % CPR) * 8], va[i]);
         st8(&dB[(c / CPR) * lds_ld<D>() + (c % CPR) * 8], vb[i]);
@@ -835,14 +835,19 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_rows_kernel(AttnBwdArgs b, in
 // exponent -inf (p = dS = 0) -- exact for a row with any unmasked key, where
 // AF2's masked weight exp(-1e8 - lse) underflows to 0.  A fully masked row is
 // the uniform distribution (p = 1/N, dS = 0).
-template <int D, int NQB>
-__global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
+//
+// W waves per workgroup: 4, or 8 beyond N = 512, where eight query groups
+// keep a wave's bias column and bias-gradient registers at the 4 query
+// blocks they hold at N = 512 (one workgroup per CU then).
+template <int D, int NQB, int W>
+__global__ __launch_bounds__(64 * W) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
+  constexpr int T = 64 * W;              // threads
   constexpr int DT = D / 16;
   constexpr int LD = lds_ld<D>();
   constexpr int N = 32 * NQB;            // == a.N (dispatch)
-  constexpr int QS = NQB > 8 ? 4 : 2;    // query groups per key tile
-  constexpr int KT = 4 / QS;             // 16-key tiles per workgroup
+  constexpr int QS = W == 8 ? 8 : NQB > 8 ? 4 : 2;  // query groups per key tile
+  constexpr int KT = W / QS;             // 16-key tiles per workgroup
   constexpr int NB = (NQB + QS - 1) / QS;  // query blocks per wave (at most)
   constexpr int CQB = NQB < 8 ? NQB : 8;   // query blocks per staged chunk
   constexpr int NCH = (NQB + CQB - 1) / CQB;
@@ -898,16 +903,16 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
   // next stage's Q/dO tile -- and, at a row's first chunk, the row's -lse,
   // -Dsum, mask and this lane's key/value fragments -- are loaded into
   // registers, so the row loop does not wait on memory at every row.
-  constexpr int NPT = (N + 255) / 256;  // row statistics per thread
+  constexpr int NPT = (N + T - 1) / T;  // row statistics per thread
   const int nst = (r1 - r0) * NCH;
   // Loaded values are only consumed at the next stage (vmcnt retires loads
   // in order, so any use now would wait for the whole prefetch).
   // The workgroup's own 16*KT keys and values of the row go through LDS too,
   // so no register filled by the prefetch is read before the next stage.
-  RowPair<D, CN> nxt;
+  RowPair<D, CN, T> nxt;
   float nls[NPT], nds[NPT], nmask[NPT];
   constexpr int KCH = 16 * KT * 2 * (D / 8);  // 16-byte chunks of own K and V
-  static_assert(KCH <= 256, "own keys: one chunk per thread");
+  static_assert(KCH <= T, "own keys: one chunk per thread");
   h16x8 nkv;
   const int kvi = tid % (KCH / 2), kvs = tid / (KCH / 2);  // chunk, 0 = K / 1 = V
   const int kvrow = kvi / (D / 8), kvc = (kvi % (D / 8)) * 8;
@@ -919,7 +924,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
     if (c == 0) {
 #pragma unroll
       for (int i = 0; i < NPT; ++i) {
-        const int qq = tid + 256 * i;
+        const int qq = tid + T * i;
         nls[i] = 0.f;
         nds[i] = 0.f;
         nmask[i] = 0.f;
@@ -951,7 +956,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
       int non = 0;
 #pragma unroll
       for (int i = 0; i < NPT; ++i) {
-        const int qq = tid + 256 * i;
+        const int qq = tid + T * i;
         if (qq < N) {
           Ls[qq] = -nls[i];
           Ds[qq] = nds[i];
@@ -1455,11 +1460,12 @@ int attn_fwd_rows_per_chunk(int R, int N, int H) {
 int attn_rows_per_chunk(int R, int N, int H) {
   const int KT = N > 256 ? 1 : 2;
   const long per_chunk = (long)H * (N / (16 * KT));
-  const long nch = std::max(1L, 2L * device_cus() / per_chunk);
+  const long per_cu = N > 512 ? 1 : 2;  // eight-wave workgroups beyond 512
+  const long nch = std::max(1L, per_cu * device_cus() / per_chunk);
   return (int)std::max(1L, ((long)R + nch - 1) / nch);
 }
 
-// Calls f(std::integral_constant<int, nb>) for nb = N/32 in 1..16: every
+// Calls f(std::integral_constant<int, nb>) for nb = N/32 in 1..32: every
 // kernel is instantiated for its exact number of 32-blocks.
 template <class F>
 static void with_blocks(int nb, F&& f) {
@@ -1467,7 +1473,9 @@ static void with_blocks(int nb, F&& f) {
 #define BC2N_NB(v) case v: f(std::integral_constant<int, v>()); break;
     BC2N_NB(1) BC2N_NB(2) BC2N_NB(3) BC2N_NB(4) BC2N_NB(5) BC2N_NB(6) BC2N_NB(7) BC2N_NB(8)
     BC2N_NB(9) BC2N_NB(10) BC2N_NB(11) BC2N_NB(12) BC2N_NB(13) BC2N_NB(14) BC2N_NB(15)
-    BC2N_NB(16)
+    BC2N_NB(16) BC2N_NB(17) BC2N_NB(18) BC2N_NB(19) BC2N_NB(20) BC2N_NB(21) BC2N_NB(22)
+    BC2N_NB(23) BC2N_NB(24) BC2N_NB(25) BC2N_NB(26) BC2N_NB(27) BC2N_NB(28) BC2N_NB(29)
+    BC2N_NB(30) BC2N_NB(31) BC2N_NB(32)
 #undef BC2N_NB
     default: throw std::runtime_error("attention: N/32 out of range");
   }
@@ -1490,7 +1498,7 @@ static int attn_chunk(int N) { return N < 256 ? N : 256; }
 static void attn_check(const AttnArgs& a) {
   if (a.D != 32 && a.D != 16) throw std::runtime_error("attention: head width must be 16 or 32");
   if (a.N <= 0 || a.N % 32 != 0) throw std::runtime_error("attention: N must be a positive multiple of 32");
-  if (a.N > 512) throw std::runtime_error("attention: N > 512 not supported");
+  if (a.N > 1024) throw std::runtime_error("attention: N > 1024 not supported");
   if (a.ld % 8 != 0 || a.ldo % 8 != 0) throw std::runtime_error("attention: row strides must be multiples of 8");
   if (!a.qkvg || !a.mask || !a.lse || !a.o) throw std::runtime_error("attention: missing operand");
 }
@@ -1558,8 +1566,9 @@ static void attn_bwd_t(hipStream_t st, const AttnBwdArgs& b) {
     });
   }
   const int nch = attn_bwd_nchunk(a.R, b.rows_per_chunk);
-  // query groups QS and key tiles KT per workgroup, as in the kernel
-  const int QS = a.N > 256 ? 4 : 2, KT = 4 / QS;
+  // waves W, query groups QS and key tiles KT per workgroup, as in the kernel
+  const int W = a.N > 512 ? 8 : 4;
+  const int QS = W == 8 ? 8 : a.N > 256 ? 4 : 2, KT = W / QS;
   const int nkw = a.N / (16 * KT);
   const size_t lds_k = (size_t)attn_chunk(a.N) * lds_ld<D>() * 2 * 2 + (size_t)a.N * 4 * 3 +
                        (size_t)(QS - 1) * KT * 2 * (D / 16) * 4 * 64 * 4 +
@@ -1580,7 +1589,9 @@ static void attn_bwd_t(hipStream_t st, const AttnBwdArgs& b) {
       }
     }
     with_blocks(a.N / 32, [&](auto nb) {
-      hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, decltype(nb)::value>), grid, dim3(256), lds_k, st, b);
+      constexpr int NB = decltype(nb)::value;
+      hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, NB, (NB > 16 ? 8 : 4)>), grid, dim3(64 * W),
+                         lds_k, st, b);
     });
   }
 dkv_done:

@@ -247,7 +247,7 @@ const float* need_f32(WeightStore& ws, const std::string& name, size_t count) {
 }
 
 void sh_check(int N, int depth) {
-  if (N <= 0 || N > 512) throw std::runtime_error("structure heads: N must be in 1..512");
+  if (N <= 0 || N > 1024) throw std::runtime_error("structure heads: N must be in 1..1024");
   if (depth <= 0) throw std::runtime_error("structure heads: depth must be positive");
 }
 

@@ -47,7 +47,7 @@ constexpr float SCALAR_W = 0.25f;                 // sqrt(1/16)
 constexpr float DIST_EPS2 = 1e-16f;               // (1e-8)^2, Vec3Array.norm clip
 constexpr float QUAT_EPS = 1e-6f;
 constexpr float POSITION_SCALE = 20.f;            // config.py:595 (multimer)
-constexpr int MAXN = 512;
+constexpr int MAXN = 1024;
 
 static_assert(PROJ == 1152 && FIN == 2112, "IPA widths");
 
@@ -183,11 +183,12 @@ __global__ __launch_bounds__(256) void ipa_logits_kernel(
 // One workgroup per query: scalar and point readouts (pairs (h, j<40)), the
 // pair readout (thread = channel x half of the heads), then the points to
 // the query's local frame and their norms.
+template <int MN>  // the attention row's capacity: 512, or 1024 for longer N
 __global__ __launch_bounds__(256) void ipa_readout_kernel(
     const float* __restrict__ attn, const float* __restrict__ vpk,
     const float* __restrict__ act2d, const float* __restrict__ rig, int N,
     float* __restrict__ fin) {
-  __shared__ float at[H][MAXN];
+  __shared__ float at[H][MN];
   __shared__ float r40[H][VW];
   const int q = blockIdx.x, t = threadIdx.x;
   for (int i = t; i < H * N; i += 256) at[i / N][i % N] = attn[((long)(i / N) * N + q) * N + i % N];
@@ -233,14 +234,15 @@ __global__ __launch_bounds__(256) void ipa_readout_kernel(
 // conversion (added to drig[q]), d attn, the softmax backward (dlogit,
 // scaled by sqrt(1/3), also accumulated into db2d_sum), and the pair
 // readout's contribution to d LN(pair)[q] (added to dact2d[q]).
+template <int MN>
 __global__ __launch_bounds__(256) void ipa_readout_bwd_kernel(
     const float* __restrict__ dfin, const float* __restrict__ fin,
     const float* __restrict__ attn, const float* __restrict__ vpk,
     const float* __restrict__ act2d, const float* __restrict__ rig, int N,
     float* __restrict__ dres, float* __restrict__ drig, float* __restrict__ dlogit,
     float* __restrict__ db2d_sum, float* __restrict__ dact2d) {
-  __shared__ float at[H][MAXN];
-  __shared__ float da[H][MAXN];
+  __shared__ float at[H][MN];
+  __shared__ float da[H][MN];
   __shared__ float d40[H][VW];
   __shared__ float dp[H][CZ];
   __shared__ float rg[H * PV][12];
@@ -669,7 +671,7 @@ size_t fold_save_bytes(int N, int depth) {
 }
 
 static void fold_check(int N, int depth) {
-  if (N <= 0 || N > MAXN) throw std::runtime_error("fold: N must be in 1..512");
+  if (N <= 0 || N > MAXN) throw std::runtime_error("fold: N must be in 1..1024");
   if (depth <= 0) throw std::runtime_error("fold: depth must be positive");
 }
 
@@ -811,10 +813,17 @@ void fold_fwd(hipStream_t st, const FoldW& w, int N, int depth, const float* sin
         case 5: launch_logits<5>(st, s.qpk, s.kpk, sv.b2d, mask, w.pw, N, s.attn); break;
         case 6: launch_logits<6>(st, s.qpk, s.kpk, sv.b2d, mask, w.pw, N, s.attn); break;
         case 7: launch_logits<7>(st, s.qpk, s.kpk, sv.b2d, mask, w.pw, N, s.attn); break;
-        default: launch_logits<8>(st, s.qpk, s.kpk, sv.b2d, mask, w.pw, N, s.attn); break;
+        case 8: launch_logits<8>(st, s.qpk, s.kpk, sv.b2d, mask, w.pw, N, s.attn); break;
+        case 9: case 10: launch_logits<10>(st, s.qpk, s.kpk, sv.b2d, mask, w.pw, N, s.attn); break;
+        case 11: case 12: launch_logits<12>(st, s.qpk, s.kpk, sv.b2d, mask, w.pw, N, s.attn); break;
+        default: launch_logits<16>(st, s.qpk, s.kpk, sv.b2d, mask, w.pw, N, s.attn); break;
       }
-      hipLaunchKernelGGL(ipa_readout_kernel, dim3(N), dim3(256), 0, st, s.attn, s.vpk, sv.act2d,
-                         s.rig, N, s.fin);
+      if (N <= 512)
+        hipLaunchKernelGGL(ipa_readout_kernel<512>, dim3(N), dim3(256), 0, st, s.attn, s.vpk,
+                           sv.act2d, s.rig, N, s.fin);
+      else
+        hipLaunchKernelGGL(ipa_readout_kernel<MAXN>, dim3(N), dim3(256), 0, st, s.attn, s.vpk,
+                           sv.act2d, s.rig, N, s.fin);
       GemmF32 o = gemm_rows(N, CS, FIN, s.fin, w.wo, ipo);
       o.bias = w.bo;
       gemm_f32(st, o, "fold.gemm_out");
@@ -930,8 +939,12 @@ void fold_bwd(hipStream_t st, const FoldW& w, int N, int depth, const float* sin
       KTimed kt("fold.ipa_bwd", st);
       GemmF32 go = gemm_rows(N, FIN, CS, dx, w.wo, dfin, true);
       gemm_f32(st, go, "fold.gemm_out_dx");
-      hipLaunchKernelGGL(ipa_readout_bwd_kernel, dim3(N), dim3(256), 0, st, dfin, s.fin, s.attn,
-                         s.vpk, sv.act2d, s.rig, N, dres, drB, dlog, db2d, dpair);
+      if (N <= 512)
+        hipLaunchKernelGGL(ipa_readout_bwd_kernel<512>, dim3(N), dim3(256), 0, st, dfin, s.fin,
+                           s.attn, s.vpk, sv.act2d, s.rig, N, dres, drB, dlog, db2d, dpair);
+      else
+        hipLaunchKernelGGL(ipa_readout_bwd_kernel<MAXN>, dim3(N), dim3(256), 0, st, dfin, s.fin,
+                           s.attn, s.vpk, sv.act2d, s.rig, N, dres, drB, dlog, db2d, dpair);
       // dvpk[k][h][j] = sum_q attn[h][q][k] dres[q][h][j]
       GemmF32 gv;
       gv.M = N; gv.N = VW; gv.K = N; gv.batch = H;

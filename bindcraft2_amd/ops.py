@@ -5,6 +5,7 @@ weights directory + name prefix, forward -> (output, save), backward from the
 save-set) so tests and benchmarks read like the reference's own module gates
 (native/triattn.cu:51-75).  All arithmetic happens in libbc2n.so.
 """
+import contextlib
 import ctypes
 
 import torch
@@ -294,6 +295,23 @@ class EvoformerStack:
                                        int(self.pair_only), 0, 1, int(dropout), self.dir,
                                        _ptr(dpair), _ptr(dmsa)))
         return dpair, dmsa
+
+
+SAVE_POLICIES = {"auto": 0, "full": 1, "replay": 2}
+
+
+@contextlib.contextmanager
+def save_policy(name):
+    """Run the enclosed stack calls under a save policy (bc2n_set_save_policy):
+    'auto' (the replay tier only where the full save-set would not fit),
+    'full' or 'replay'; the previous policy is restored on exit."""
+    old = lib().bc2n_set_save_policy(SAVE_POLICIES[name])
+    if old < 0:
+        check(1)
+    try:
+        yield
+    finally:
+        lib().bc2n_set_save_policy(old)
 
 
 class TemplatePairStack:

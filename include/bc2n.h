@@ -186,6 +186,23 @@ size_t bc2n_evoformer_save_bytes(const char* weights_dir, int N, int S,
  * save-sets, two carries of each track and the dropout tables. */
 size_t bc2n_evoformer_detached_bytes(const char* weights_dir, int N, int S,
                                      int64_t depth, int64_t pair_only);
+/* The save-set tier of every stack in the process (the evoformer and
+ * template stacks here, and those inside the template embedding and the
+ * design step): 0 = by size (the default: the full save-set, whose backward
+ * replays nothing, unless it would take more than 60% of the device's
+ * memory -- e.g. the 48-block stack beyond L ~ 600 on a 288 GB MI355X --
+ * then the replay tier), 1 = always full, 2 = always the replay tier: every
+ * block's input carries and one block's module save-sets, the backward
+ * running each block's forward again before its backward (the reference's
+ * replay/remat tiers, native/stack.cuh:775-798, priced the same way: about
+ * one more forward).  The *_save_bytes functions, forwards and backwards
+ * all follow it, so a forward and its backward must see the same policy.
+ * Returns the previous policy, or -1 for a bad value. */
+int bc2n_set_save_policy(int policy);
+/* 1 if a stack of these shapes keeps the replay tier under the policy, 0 if
+ * the full save-set, -1 on error. */
+int bc2n_evoformer_replays(const char* weights_dir, int N, int S, int64_t depth,
+                           int64_t pair_only);
 /* The number of bf16 [N,N,128] slots that hold the save-set, for a caller
  * that declares psave in the reference's shape bf16[slots,N,N,128]
  * (replaces native_save_slots_probe(depth, n), native/ffi.cu:1684-1689,
@@ -319,7 +336,7 @@ int bc2n_embedder_bwd(void* stream, const float* dmsa, const float* dpair,
  * of weights, iteration i keyed by split(key, depth)[i] (dropout 0.1 with
  * keys split(k_i, 3)[1], [2]).  traj[i] = [R | 20 t] after iteration i
  * (StructureModule 'traj', position_scale 20).  All f32.  Weights in the
- * post-trunk manifest naming of bindcraft/af/native.py:339-444.  N <= 512.
+ * post-trunk manifest naming of bindcraft/af/native.py:339-444.  N <= 1024.
  * d_act / d_traj may be NULL (zero cotangent).  seed as for the stacks.
  * ---------------------------------------------------------------------- */
 size_t bc2n_fold_save_bytes(const char* weights_dir, int N, int64_t depth);
@@ -353,7 +370,7 @@ int bc2n_fold_bwd(void* stream, const float* d_act, const float* d_traj,
  * (clamped).  save holds bc2n_structure_heads_save_bytes() bytes; unlike the
  * reference's, the backward replays nothing, and it uses the save buffer's
  * tail as scratch (so save is writable in both calls).  Cotangents may be
- * NULL (zero).  seed as for the stacks.  N <= 512.
+ * NULL (zero).  seed as for the stacks.  N <= 1024.
  * ---------------------------------------------------------------------- */
 size_t bc2n_structure_heads_save_bytes(const char* weights_dir, int N, int64_t depth);
 int bc2n_structure_heads_fwd(void* stream, const float* single, const float* pair,
@@ -396,7 +413,7 @@ int bc2n_structure_heads_bwd(void* stream, const float* single, const float* pai
  * terms; the first pass's terms are the constants of a zero state.  The
  * outputs and the save-set are the last pass's.  bwd: the five
  * cotangents (any may be NULL) -> d_target_feat f32[N,21], d_msa_feat
- * f32[S,N,49].  N is a runtime value (a multiple of 32, at most 512): one
+ * f32[S,N,49].  N is a runtime value (a multiple of 32, at most 1024): one
  * set of weights serves every length.  save holds
  * bc2n_design_step_save_bytes() bytes and is written by both calls.
  * ---------------------------------------------------------------------- */

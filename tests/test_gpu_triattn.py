@@ -51,6 +51,8 @@ def _oracle(prm, per_column, pair, mask, tbl, dout):
     (320, False, True, 0.25),
     # the large complex of BASELINE configs[4]
     (512, False, True, 0.1), (512, True, True, 0.1),
+    # past 512: 24 key blocks, eight-wave dK/dV (the long-length path)
+    (768, False, True, 0.1), (768, True, True, 0.1),
 ])
 def test_triattn_fwd_bwd_parity(cuda, n, per_column, drop, mask_frac):
     print(f"triattn n={n} per_column={per_column} drop={drop} mask={mask_frac}", flush=True)

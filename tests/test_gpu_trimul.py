@@ -31,6 +31,7 @@ def _oracle(prm, outgoing, pair, mask, tbl, dout):
     (224, True, True, 0.1), (224, False, True, 0.1), (288, True, True, 0.1),
     # the large complex of BASELINE configs[4]
     (512, True, True, 0.1), (512, False, True, 0.1),
+    (768, True, True, 0.1),
 ])
 def test_trimul_fwd_bwd_parity(cuda, n, outgoing, drop, mask_frac):
     print(f"trimul n={n} outgoing={outgoing} drop={drop} mask={mask_frac}", flush=True)
