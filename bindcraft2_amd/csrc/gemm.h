@@ -336,6 +336,93 @@ inline void gemm_check(bool ok, const char* what) {
   if (!ok) throw std::runtime_error(std::string("bc2n gemm: ") + what);
 }
 
+// The launch: loader form from the strides, BK from K (shapes checked).
+template <int BM, int BN, class Epi, class AL>
+void gemm_launch(hipStream_t st, const GemmArgs& g, const Epi& epi, const AL& al) {
+  const bool ak = (g.a_sk == 1), bk = (g.b_sk == 1);
+  const int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
+  dim3 grid(xcd_grid((long)tiles * g.batch)), block(256);
+  // K <= 128 (two 64-deep steps at most): 32-deep steps halve the operand
+  // buffers (40 KB), so four workgroups share a CU and hide each other's
+  // load latency; longer K keeps 64-deep steps (fewer barriers)
+  const bool k64 = (g.K % 64 == 0) && g.K > 128;
+  // A grid of a few tiles (the MSA's S x N-row products) runs one chain of
+  // K steps per workgroup, each waiting for its loads: 128-deep steps halve
+  // the chain (the operand tiles fit one buffer of 68 KB).
+  const bool k128 = (g.K % 128 == 0) && g.K >= 256 && (long)tiles * g.batch * 8 <= device_cus();
+#define BC2N_GEMM_LAUNCH(BKV, AKV, BKCV) \
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, BKV, AKV, BKCV, Epi, AL>), grid, block, 0, st, g, epi, al)
+  if (k128) {
+    if (ak && bk) BC2N_GEMM_LAUNCH(128, true, true);
+    else if (ak) BC2N_GEMM_LAUNCH(128, true, false);
+    else if (bk) BC2N_GEMM_LAUNCH(128, false, true);
+    else BC2N_GEMM_LAUNCH(128, false, false);
+  } else if (k64) {
+    if (ak && bk) BC2N_GEMM_LAUNCH(64, true, true);
+    else if (ak) BC2N_GEMM_LAUNCH(64, true, false);
+    else if (bk) BC2N_GEMM_LAUNCH(64, false, true);
+    else BC2N_GEMM_LAUNCH(64, false, false);
+  } else {
+    if (ak && bk) BC2N_GEMM_LAUNCH(32, true, true);
+    else if (ak) BC2N_GEMM_LAUNCH(32, true, false);
+    else if (bk) BC2N_GEMM_LAUNCH(32, false, true);
+    else BC2N_GEMM_LAUNCH(32, false, false);
+  }
+#undef BC2N_GEMM_LAUNCH
+}
+
+// Split K for a grid of a few tiles and a long K (the MSA track's S x N-row
+// products at S = 1: e.g. 224 x 256 over K = 1024 is 4 tiles of 128 x 128,
+// each a chain of 8 dependent K steps): the K slices run as the batch
+// entries of the same kernel (the batch strides step along K) and write f32
+// partial tiles; gemm_splitk_epi adds them in slice order (the result does
+// not depend on timing) and applies the epilogue's row() to each 8-column
+// vector with the kernel's own lane order (consecutive lanes, consecutive
+// column groups of one row).
+template <class AL>
+struct ALoadSliced {
+  static constexpr bool kDirect = false;
+  static constexpr bool kSide = false;
+  AL al;
+  int kslice;
+  __device__ __forceinline__ h16x8 operator()(int b, int m, int k) const {
+    return al(0, m, k + b * kslice);
+  }
+};
+
+// f32 partial tile of K slice b: part[b][m][n] (row stride ldc, slice stride sb).
+struct EpiPartial : EpiRows {
+  float* C;
+  long ldc, sb;
+  __device__ __forceinline__ void row(int b, int m, int n, const float (&v)[8]) const {
+    st_f8(C + (long)b * sb + (long)m * ldc + n, v);
+  }
+};
+
+inline Arena& gemm_splitk_scratch() {
+  static Arena a;
+  return a;
+}
+
+template <class Epi>
+__global__ __launch_bounds__(256) void gemm_splitk_epi(const float* __restrict__ part, int S,
+                                                      int M, int N, Epi epi) {
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int n8 = N / 8;
+  if (idx >= (long)M * n8) return;  // M * n8 is a multiple of 8: whole lane groups
+  const int m = (int)(idx / n8), n = (int)(idx % n8) * 8;
+  const long MN = (long)M * N;
+  float v[8];
+  ld_f8(part + (long)m * N + n, v);
+  for (int sl = 1; sl < S; ++sl) {
+    float w[8];
+    ld_f8(part + sl * MN + (long)m * N + n, w);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] += w[e];
+  }
+  epi.row(0, m, n, v);
+}
+
 // Launch with tile BM x BN; picks the loader form from the strides and BK
 // from K.  Shapes are validated here, on the host, before any launch.  With a
 // loader other than ALoadDirect, A is K-contiguous by construction (g.A is
@@ -361,36 +448,42 @@ void gemm(hipStream_t st, const GemmArgs& g, const Epi& epi, const char* name = 
   if (bk) gemm_check(g.b_sn % 8 == 0, "B row stride must be a multiple of 8");
   else gemm_check(g.b_sk % 8 == 0, "B(T) stride must be a multiple of 8");
   gemm_check(g.batch == 1 || (g.a_sb % 8 == 0 && g.b_sb % 8 == 0), "batch strides");
-  const int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
-  dim3 grid(xcd_grid((long)tiles * g.batch)), block(256);
-  // K <= 128 (two 64-deep steps at most): 32-deep steps halve the operand
-  // buffers (40 KB), so four workgroups share a CU and hide each other's
-  // load latency; longer K keeps 64-deep steps (fewer barriers)
-  const bool k64 = (g.K % 64 == 0) && g.K > 128;
-  // A grid of a few tiles (the MSA's S x N-row products) runs one chain of
-  // K steps per workgroup, each waiting for its loads: 128-deep steps halve
-  // the chain (the operand tiles fit one buffer of 68 KB).
-  const bool k128 = (g.K % 128 == 0) && g.K >= 256 && (long)tiles * g.batch * 8 <= device_cus();
+  const long tiles = (long)((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
   KTimed kt(name, st);
-#define BC2N_GEMM_LAUNCH(BKV, AKV, BKCV) \
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, BKV, AKV, BKCV, Epi, AL>), grid, block, 0, st, g, epi, al)
-  if (k128) {
-    if (ak && bk) BC2N_GEMM_LAUNCH(128, true, true);
-    else if (ak) BC2N_GEMM_LAUNCH(128, true, false);
-    else if (bk) BC2N_GEMM_LAUNCH(128, false, true);
-    else BC2N_GEMM_LAUNCH(128, false, false);
-  } else if (k64) {
-    if (ak && bk) BC2N_GEMM_LAUNCH(64, true, true);
-    else if (ak) BC2N_GEMM_LAUNCH(64, true, false);
-    else if (bk) BC2N_GEMM_LAUNCH(64, false, true);
-    else BC2N_GEMM_LAUNCH(64, false, false);
-  } else {
-    if (ak && bk) BC2N_GEMM_LAUNCH(32, true, true);
-    else if (ak) BC2N_GEMM_LAUNCH(32, true, false);
-    else if (bk) BC2N_GEMM_LAUNCH(32, false, true);
-    else BC2N_GEMM_LAUNCH(32, false, false);
+  constexpr bool kSplittable = !epi_row_block<Epi>::value && !Epi::kHasCol && !AL::kSide;
+  if constexpr (kSplittable) {
+    if (g.batch == 1 && tiles * 2 < device_cus() && g.K >= 256 && g.N % 64 == 0) {
+      // slices of at least 128 (a multiple of 32 that divides K), about one
+      // workgroup per CU in all
+      const int kb = g.K / 32;
+      int split = (int)std::min<long>((device_cus() + tiles - 1) / tiles, g.K / 128);
+      while (split > 1 && kb % split != 0) --split;
+      if (split > 1) {
+        const int kslice = g.K / split;
+        GemmArgs gs = g;
+        gs.K = kslice;
+        gs.batch = split;
+        gs.a_sb = (g.a_sk == 1) ? kslice : (long)kslice * g.a_sk;
+        gs.b_sb = (g.b_sk == 1) ? kslice : (long)kslice * g.b_sk;
+        Arena& ar = gemm_splitk_scratch();
+        std::lock_guard<std::recursive_mutex> lk(ar.lock());
+        const size_t elems = (size_t)split * g.M * g.N;
+        ar.reset(st, elems * 4 + 256);
+        float* part = ar.take_n<float>(elems);
+        EpiPartial pe;
+        pe.C = part;
+        pe.ldc = g.N;
+        pe.sb = (long)g.M * g.N;
+        if constexpr (AL::kDirect) gemm_launch<BM, BN>(st, gs, pe, al);
+        else gemm_launch<BM, BN>(st, gs, pe, ALoadSliced<AL>{al, kslice});
+        const long n = (long)g.M * (g.N / 8);
+        hipLaunchKernelGGL((gemm_splitk_epi<Epi>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                           st, part, split, g.M, g.N, epi);
+        return;
+      }
+    }
   }
-#undef BC2N_GEMM_LAUNCH
+  gemm_launch<BM, BN>(st, g, epi, al);
 }
 
 // ---------------------------------------------------------------- epilogues

@@ -156,8 +156,11 @@ __global__ __launch_bounds__(256) void ipa_logits_kernel(
       for (int c = 0; c < SQK; ++c) s += qr[c] * kv[c];
 #pragma unroll
       for (int c = SQK; c < 28; ++c) { const float d = qr[c] - kv[c]; d2 += d * d; }
+      // the mask term 1e5 (1 - m_q m_k): for a masked query it is the same
+      // on every key, which the softmax ignores, so it is left out there --
+      // in f32 it would round the row's logits to ~4e-3
       const float l = s - 0.5f * w * d2 + b2d[((long)h * N + q) * N + k] -
-                      1e5f * (1.f - mq * mask[k]);
+                      (mq != 0.f ? 1e5f * (1.f - mq * mask[k]) : 0.f);
       lg[j] = l * LOGIT_W;
       mx = fmaxf(mx, lg[j]);
     }

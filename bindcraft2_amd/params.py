@@ -367,6 +367,12 @@ def init_structure_heads_params(rng, final="random", ln="identity"):
             v = np.zeros(shape) if ln == "identity" else 0.1 * rng.standard_normal(shape)
         elif leaf == "bias":
             v = np.zeros(shape) if final == "zero" else 0.1 * rng.standard_normal(shape)
+            if final != "zero" and "unnormalized_angles" in name:
+                # cos components +2: every (sin, cos) torsion vector keeps a norm
+                # well away from 0, as trained weights give, so its normalisation
+                # does not amplify upstream rounding (a random head can put one
+                # near 0, where the angle's direction is ill-conditioned)
+                v[1::2] += 2.0
         else:
             v = rng.standard_normal(shape) / np.sqrt(shape[0])
         out[f"param/{name}"] = np.asarray(v, np.float32)

@@ -11,7 +11,10 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("m,n,k", [(128, 128, 64), (200, 96, 32), (50176 // 49, 512, 128),
-                                   (333, 640, 224), (64, 16, 1024)])
+                                   (333, 640, 224), (64, 16, 1024),
+                                   # few tiles and a long K: split over K, partials
+                                   # added in slice order by the epilogue pass
+                                   (224, 256, 1024), (96, 512, 512)])
 def test_gemm_matches_fp32(cuda, m, n, k):
     print(f"gemm m={m} n={n} k={k}", flush=True)
     g = torch.Generator().manual_seed(m * 7 + n)
