@@ -151,54 +151,65 @@ struct HFrag<16> {
 };
 
 // Logical (row, head, query block) of workgroup `bid` of the per-row
-// forward and dQ kernels (N > 256), ordered head, tile of 8 rows, query
-// block, row in the tile.  The 8 x nqb neighbours one XCD runs together then
-// share 8 rows' K and V and the head's whole pair bias in that XCD's L2; in
+// forward and dQ kernels (N > 256), ordered head pair, tile of 8 rows, query
+// block, head in the pair, row in the tile.  The neighbours one XCD runs
+// together then share 8 rows' K and V and the pair's pair bias in that XCD's
+// L2; the two heads of a pair share every 128-byte line of a token's q, k, v
+// and gate slices (64 bytes a head), so each line is fetched once.  (In
 // (row, head, query block) order no two workgroups in flight shared a bias
-// tile (64 queries x N keys of f32), and every row re-read all of it.
+// tile; in head-major order each line was fetched once per head, a head's
+// whole pass apart.)
 struct RowHeadQb {
   int r, h, qb;
 };
-__device__ __forceinline__ RowHeadQb row_tile_order(int bid, int R, int nqb) {
+__device__ __forceinline__ RowHeadQb row_tile_order(int bid, int R, int H, int nqb) {
   constexpr int T = 8;
   const int per_head = R * nqb;
-  const int h = bid / per_head;
-  int j = bid - h * per_head;
-  const int full = (R / T) * T;  // rows in whole tiles
+  const int h0 = 2 * (bid / (2 * per_head));  // first head of the pair
+  const int nh = min(2, H - h0);              // heads in the pair (1 for an odd last head)
+  int j = bid - h0 * per_head;                // index among the pair's nh * R * nqb
+  const int full = (R / T) * T;               // rows in whole tiles
   RowHeadQb o;
-  o.h = h;
-  if (j < full * nqb) {
-    const int t = j / (T * nqb), w = j - t * (T * nqb);
-    o.qb = w / T;
-    o.r = t * T + w % T;
+  if (j < full * nqb * nh) {
+    const int t = j / (T * nqb * nh), w = j - t * (T * nqb * nh);
+    o.qb = w / (T * nh);
+    const int u = w - o.qb * (T * nh);
+    o.h = h0 + u / T;
+    o.r = t * T + u % T;
   } else {  // the last R % T rows
-    j -= full * nqb;
+    j -= full * nqb * nh;
     const int rem = R - full;
-    o.qb = j / rem;
-    o.r = full + j % rem;
+    o.qb = j / (rem * nh);
+    const int u = j - o.qb * (rem * nh);
+    o.h = h0 + u / rem;
+    o.r = full + u % rem;
   }
   return o;
 }
 
 // ------------------------------------------------------------------ forward
-// Workgroup = (row r, head h, 64 queries); 4 waves x 16 queries.  N = 32*NKB
-// exactly (one instantiation per block count, so every loop over key blocks
-// unrolls without guards and the scheduler can overlap one block's MFMAs
-// with the previous block's softmax).  Keys are processed in chunks of up to
-// 256 (8 blocks) whose K and V are staged in LDS; within a chunk a lane
-// keeps its query's scores (8 keys of every block) in registers, so the
-// chunk's maximum is taken once and every score costs one exponent.  For
-// N <= 256 there is one chunk and no rescale at all; beyond that the output
-// accumulator is rescaled once per chunk (online softmax over chunks).
+// Workgroup = (row r, head h, 64 queries); 4 waves x 16 queries; N = 32*NKB
+// > 256.  Keys are processed in chunks of 128 (4 blocks of 32) staged in one
+// LDS buffer; the next chunk's K and V are loaded into registers while the
+// current one computes, so the buffer is small (five workgroups fit a CU)
+// and the register budget leaves four waves per SIMD.  A lane keeps its
+// query's 32 scores of the chunk (8 keys of every block) in registers.
+// Per score: the pair bias is the score MFMA's accumulator, then one fma
+// (the key mask), half a max, a subtract, the exponent and half a convert;
+// the row sum of the probabilities comes from the P V product itself (one
+// more MFMA per block with an all-ones operand), summed over the same h16
+// probabilities the numerator uses.  Online softmax across chunks: the
+// output accumulator and the row sum are rescaled once per chunk.
 template <int D, int NKB>
 __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   constexpr int DT = D / 16;
   constexpr int LD = lds_ld<D>();
   constexpr int N = 32 * NKB;  // == a.N (dispatch)
-  constexpr int CB = NKB < 8 ? NKB : 8;  // key blocks per chunk
-  constexpr int NCH = (NKB + CB - 1) / CB;
-  constexpr int CN = 32 * CB;            // keys per chunk
+  constexpr int CB = 4;        // key blocks per chunk
+  constexpr int CN = 32 * CB;  // keys per chunk
+  constexpr int NFULL = NKB / CB, TAIL = NKB % CB;
+  constexpr int NCH = NFULL + (TAIL ? 1 : 0);
   const int H = a.H;
   h16* Ks = reinterpret_cast<h16*>(smem_raw);          // [CN][LD]
   h16* Vs = Ks + CN * LD;                               // [CN][LD]
@@ -209,14 +220,15 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   const long G = (long)a.R * H * nqb;
   const int bid = (int)xcd_block(G);
   if (bid >= G) return;
-  const RowHeadQb ord = row_tile_order(bid, a.R, nqb);
+  const RowHeadQb ord = row_tile_order(bid, a.R, H, nqb);
   const int qb = ord.qb, h = ord.h, r = ord.r;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const long tok0 = (long)r * N;
   const h16* Kg = a.qkvg + tok0 * a.ld + H * D + h * D;
   const h16* Vg = a.qkvg + tok0 * a.ld + 2 * H * D + h * D;
-  stage_rows2<D, CN>(Ks, Kg, a.ld, Vs, Vg, a.ld, tid);
+  RowPair<D, CN> nkv;  // the next chunk's K and V rows
+  nkv.load(Kg, a.ld, Vg, a.ld, tid, min(CN, N));
   for (int k = tid; k < N; k += 256) {
     const bool on = a.mask[r * a.mask_sr + k * a.mask_sk] != 0.f;
     Mm[k] = on ? 1.f : 0.f;
@@ -224,6 +236,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   }
 
   const int q0 = qb * 64 + wave * 16;
+  const bool active = q0 < N;  // idle waves keep to the barriers only
   const int lq = lane & 15, g = lane >> 4;
   const int q = min(q0, N - 16) + lq;  // idle waves read in bounds, store nothing
   HFrag<D> qf;
@@ -232,49 +245,50 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   h16x4 gv[DT];
 #pragma unroll
   for (int dh = 0; dh < DT; ++dh) gv[dh] = *reinterpret_cast<const h16x4*>(grow + dh * 16 + 4 * g);
-  const float* brow = a.bias ? a.bias + ((long)h * N + q) * N : nullptr;
+  const int qt = q >> 4;  // the wave's 16-query tile (bias blocks; the launcher requires the bias)
   const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
-  float mx = -INFINITY, lsum = 0.f;
-  f32x4 acc[DT];
+  h16x8 ones;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ones[e] = (h16)1.f;
+  float mx = -INFINITY;  // running maximum (exp2(-inf - m) = 0 rescales nothing)
+  f32x4 acc[DT], lacc = z4;
 #pragma unroll
   for (int i = 0; i < DT; ++i) acc[i] = z4;
 
+  auto chunk = [&](int c, auto nbc) {
+    constexpr int NBC = decltype(nbc)::value;  // key blocks in this chunk
+    const int k0 = c * CN;
+    // the chunk's pair bias: the score MFMAs' accumulators
+    f32x4 sv[NBC][2];
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int k0c = c * CN;
-    float sv[CB][8];
+    for (int kb = 0; kb < NBC; ++kb)
 #pragma unroll
-    for (int kb = 0; kb < CB; ++kb) {
-      if (c * CB + kb < NKB) {
-#pragma unroll
-        for (int kh = 0; kh < 2; ++kh) {
-          const float4 bb = brow ? *reinterpret_cast<const float4*>(brow + k0c + kb * 32 + kh * 16 + 4 * g)
-                                 : make_float4(0.f, 0.f, 0.f, 0.f);
-          sv[kb][kh * 4 + 0] = bb.x;
-          sv[kb][kh * 4 + 1] = bb.y;
-          sv[kb][kh * 4 + 2] = bb.z;
-          sv[kb][kh * 4 + 3] = bb.w;
-        }
+      for (int kh = 0; kh < 2; ++kh) {
+        const float4 bb =
+            *reinterpret_cast<const float4*>(bias_frag_block(a.bias, h, qt, (k0 >> 5) + kb, N, lane) + kh * 4);
+        sv[kb][kh][0] = bb.x; sv[kb][kh][1] = bb.y; sv[kb][kh][2] = bb.z; sv[kb][kh][3] = bb.w;
       }
-    }
-    if (c > 0) {
-      __syncthreads();  // every wave is done with the previous chunk
-      stage_rows2<D, CN>(Ks, Kg + (long)k0c * a.ld, a.ld, Vs, Vg + (long)k0c * a.ld, a.ld, tid,
-                         min(CN, N - k0c));
-    }
+    __syncthreads();  // the previous chunk's LDS readers are done
+    nkv.store(Ks, Vs, tid, NBC * 32);
     __syncthreads();
-    if (NCH == 1 && q0 >= N) return;  // idle wave, no barrier follows
-
+    // the next chunk's K and V, issued after this chunk's scores (the wait
+    // counter retires loads in order: issued earlier, they would hold up
+    // the scores' wait for the bias)
+    auto prefetch = [&] {
+      if (c + 1 < NCH)
+        nkv.load(Kg + (long)(k0 + CN) * a.ld, a.ld, Vg + (long)(k0 + CN) * a.ld, a.ld, tid,
+                 min(CN, N - k0 - CN));
+    };
     float mc = -INFINITY;
+    if (active) {
 #pragma unroll
-    for (int kb = 0; kb < CB; ++kb) {
-      if (c * CB + kb < NKB) {
+      for (int kb = 0; kb < NBC; ++kb) {
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh) {
           HFrag<D> kf;
           kf.load(&Ks[(kb * 32 + kh * 16 + lq) * LD], g);
-          const f32x4 s = HFrag<D>::mma(kf, qf, z4);
-          const int kk = k0c + kb * 32 + kh * 16 + 4 * g;
+          sv[kb][kh] = HFrag<D>::mma(kf, qf, sv[kb][kh]);  // score + bias
+          const int kk = k0 + kb * 32 + kh * 16 + 4 * g;
           const float4 mm = *reinterpret_cast<const float4*>(Mm + kk);
           const float4 ma = *reinterpret_cast<const float4*>(Ma + kk);
           const float mv[4] = {mm.x, mm.y, mm.z, mm.w};
@@ -282,44 +296,43 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             // unmasked: s + bias; masked: exactly NEG_LOGIT
-            float& x = sv[kb][kh * 4 + i];
-            x = __builtin_fmaf(s[i] + x, mv[i], av[i]);
+            const float x = __builtin_fmaf(sv[kb][kh][i], mv[i], av[i]);
+            sv[kb][kh][i] = x;
             mc = fmaxf(mc, x);
           }
         }
       }
     }
+    prefetch();
+    if (!active) return;
     mc = fmaxf(mc, __shfl_xor(mc, 16, 64));
     mc = fmaxf(mc, __shfl_xor(mc, 32, 64));
-    if (c > 0) {
-      const float mn = fmaxf(mx, mc);
-      const float alpha = fast_exp2(mx - mn);
-      lsum *= alpha;
+    const float mn = fmaxf(mx, mc);
+    const float alpha = fast_exp2(mx - mn);
 #pragma unroll
-      for (int dh = 0; dh < DT; ++dh) acc[dh] *= alpha;
-      mx = mn;
-    } else {
-      mx = mc;
+    for (int dh = 0; dh < DT; ++dh) acc[dh] *= alpha;
+    lacc *= alpha;
+    mx = mn;
+#pragma unroll
+    for (int kb = 0; kb < NBC; ++kb) {
+      h16x8 pf;
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pf[kh * 4 + i] = (h16)fast_exp2(sv[kb][kh][i] - mx);
+#pragma unroll
+      for (int dh = 0; dh < DT; ++dh)
+        acc[dh] = mfma16x16x32(ld_tr8(Vs, LD, kb * 32, dh * 16, lane), pf, acc[dh]);
+      lacc = mfma16x16x32(ones, pf, lacc);  // row sum of the probabilities
     }
+  };
+  // unrolled, so the wait for each chunk's loads counts only what is in flight
 #pragma unroll
-    for (int kb = 0; kb < CB; ++kb) {
-      if (c * CB + kb < NKB) {
-        h16x8 pf;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float p = fast_exp2(sv[kb][e] - mx);
-          lsum += p;
-          pf[e] = (h16)p;
-        }
-#pragma unroll
-        for (int dh = 0; dh < DT; ++dh)
-          acc[dh] = mfma16x16x32(ld_tr8(Vs, LD, kb * 32, dh * 16, lane), pf, acc[dh]);
-      }
-    }
-  }
-  if (q0 >= N) return;
-  lsum += __shfl_xor(lsum, 16, 64);
-  lsum += __shfl_xor(lsum, 32, 64);
+  for (int c = 0; c < NFULL; ++c) chunk(c, std::integral_constant<int, CB>());
+  if constexpr (TAIL > 0) chunk(NFULL, std::integral_constant<int, TAIL>());
+
+  if (!active) return;
+  const float lsum = lacc[0];
   const float inv = __builtin_amdgcn_rcpf(lsum);
   const long orow = (tok0 + q) * a.ldo + h * D;
 #pragma unroll
@@ -381,12 +394,12 @@ __global__ __launch_bounds__(256) void attn_fwd_rows_kernel(AttnArgs a, int rpc)
   // pair bias of this lane's query, all N keys, in score-fragment order
   float bsv[NKB][8];
   {
-    const float* brow = a.bias + ((long)h * N + q) * N;
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh) {
-        const float4 bb = *reinterpret_cast<const float4*>(brow + kb * 32 + kh * 16 + 4 * g);
+        const float4 bb =
+            *reinterpret_cast<const float4*>(bias_frag_block(a.bias, h, q >> 4, kb, N, lane) + kh * 4);
         bsv[kb][kh * 4 + 0] = bb.x;
         bsv[kb][kh * 4 + 1] = bb.y;
         bsv[kb][kh * 4 + 2] = bb.z;
@@ -574,7 +587,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs b) {
   const long G = (long)a.R * H * nqb;
   const int bid = (int)xcd_block(G);
   if (bid >= G) return;
-  const RowHeadQb ord = row_tile_order(bid, a.R, nqb);
+  const RowHeadQb ord = row_tile_order(bid, a.R, H, nqb);
   const int qb = ord.qb, h = ord.h, r = ord.r;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
@@ -594,7 +607,6 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs b) {
   dof.load(b.dO + (tok0 + q) * a.ldo + h * D, g);
   const float lse = a.lse[((long)r * H + h) * N + q];
   const float nDq = b.nDsum[((long)r * H + h) * N + q];
-  const float* brow = a.bias ? a.bias + ((long)h * N + q) * N : nullptr;
   const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
   const f32x4 nD = {nDq, nDq, nDq, nDq};
   f32x4 acc[DT];
@@ -610,8 +622,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs b) {
       if (c * CB + kb < NKB) {
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh) {
-          const float4 bb = brow ? *reinterpret_cast<const float4*>(brow + k0c + kb * 32 + kh * 16 + 4 * g)
-                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+          const float4 bb = *reinterpret_cast<const float4*>(
+              bias_frag_block(a.bias, h, q >> 4, (k0c >> 5) + kb, N, lane) + kh * 4);
           bsv[kb][kh * 4 + 0] = bb.x - lse;
           bsv[kb][kh * 4 + 1] = bb.y - lse;
           bsv[kb][kh * 4 + 2] = bb.z - lse;
@@ -716,12 +728,12 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_rows_kernel(AttnBwdArgs b, in
 
   float bsv[NKB][8];
   {
-    const float* brow = a.bias + ((long)h * N + q) * N;
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh) {
-        const float4 bb = *reinterpret_cast<const float4*>(brow + kb * 32 + kh * 16 + 4 * g);
+        const float4 bb =
+            *reinterpret_cast<const float4*>(bias_frag_block(a.bias, h, q >> 4, kb, N, lane) + kh * 4);
         bsv[kb][kh * 4 + 0] = bb.x;
         bsv[kb][kh * 4 + 1] = bb.y;
         bsv[kb][kh * 4 + 2] = bb.z;
@@ -881,11 +893,11 @@ __global__ __launch_bounds__(64 * W) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
 
   // bias column k at this wave's queries; bias-gradient accumulators
   float bsl[NB][8], dbias[NB][8];
-  const float* bcol = a.bias ? a.bias + (long)h * N * N + k : nullptr;
+  const bool hasb = a.bias != nullptr;
 #pragma unroll
   for (int ib = 0; ib < NB; ++ib) {
     const int qb = (ib * QS + qs) * 32;
-    const bool have = bcol && qb < N;  // wave-uniform
+    const bool have = hasb && qb < N;  // wave-uniform
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       bsl[ib][e] = 0.f;
@@ -894,7 +906,7 @@ __global__ __launch_bounds__(64 * W) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
     if (have) {
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        bsl[ib][e] = bcol[(long)(qb + (e / 4) * 16 + 4 * g + (e % 4)) * N];
+        bsl[ib][e] = a.bias[bias_frag_index(h, qb + (e / 4) * 16 + 4 * g + (e % 4), k, N)];
     }
   }
   const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
@@ -1172,13 +1184,13 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkv_lds_kernel(AttnBwdArgs b)
   // queries [16 qs, 16 qs + 16) of block NQB - 1 when HALF
   auto blk_q0 = [&](int ib) { return ib < FULL ? (ib * QS + qs) * 32 : (NQB - 1) * 32; };
   float bsl[NB][8], dbias[NB][8];
-  const float* bcol = a.bias + (long)h * N * N + k;
+
 #pragma unroll
   for (int ib = 0; ib < NB; ++ib) {
     const int qb = blk_q0(ib);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      bsl[ib][e] = bcol[(long)(qb + (e / 4) * 16 + 4 * g + (e % 4)) * N];
+      bsl[ib][e] = a.bias[bias_frag_index(h, qb + (e / 4) * 16 + 4 * g + (e % 4), k, N)];
       dbias[ib][e] = 0.f;
     }
   }
@@ -1520,7 +1532,9 @@ static void attn_fwd_t(hipStream_t st, const AttnArgs& a) {
     });
     return;
   }
-  const size_t lds = (size_t)attn_chunk(a.N) * lds_ld<D>() * 2 * 2 + (size_t)a.N * 8;
+  if (!a.bias) throw std::runtime_error("attention: the chunked forward needs the pair bias");
+  // one 128-key K/V buffer + the row's key mask (two floats a key)
+  const size_t lds = (size_t)128 * lds_ld<D>() * 2 * 2 + (size_t)a.N * 8;
   const dim3 grid(xcd_grid((long)a.R * a.H * nqb));
   with_blocks(a.N / 32, [&](auto nb) {
     hipLaunchKernelGGL((attn_fwd_kernel<D, decltype(nb)::value>), grid, dim3(256), lds, st, a);
@@ -1558,6 +1572,7 @@ static void attn_bwd_t(hipStream_t st, const AttnBwdArgs& b) {
                            st, b, rpc);
     });
   } else {
+    if (!a.bias) throw std::runtime_error("attention: the chunked dQ needs the pair bias");
     const size_t lds_q = (size_t)attn_chunk(a.N) * lds_ld<D>() * 2 * 2 + (size_t)a.N * 4;
     KTimed kt(timer_name(2, a), st);
     const dim3 grid(xcd_grid((long)a.R * a.H * nqb));

@@ -6,8 +6,28 @@
 namespace bc2n {
 
 // ---------------------------------------------------------------- LayerNorm
+// Pair-bias layout shared by its producer (ln_fwd_f32 with H > 0) and the
+// attention kernels, "score-fragment order": bias (h, q, k) of an N x N grid
+// (N % 32 == 0) sits in the 2 KB block of (head h, 16-query tile q/16,
+// 32-key block k/32), at lane ((k%16)/4)*16 + q%16, element ((k%32)/16)*4 +
+// k%4 -- the 8 floats one lane of a score MFMA's accumulator takes for the
+// block, so a wave reads a block as two contiguous 1 KB vectors (in [h][q][k]
+// order every 16-byte lane read was a separate cache line).
+__host__ __device__ __forceinline__ long bias_frag_index(int h, int q, int k, int N) {
+  const int lane = ((k & 15) >> 2) * 16 + (q & 15);
+  const int e = ((k & 31) >> 4) * 4 + (k & 3);
+  return ((((long)h * (N >> 4) + (q >> 4)) * (N >> 5) + (k >> 5)) << 9) + lane * 8 + e;
+}
+// The 8 floats of lane `lane` for (head h, query tile qt, key block kb).
+__host__ __device__ __forceinline__ const float* bias_frag_block(const float* bias, int h, int qt,
+                                                                 int kb, int N, int lane) {
+  return bias + ((((long)h * (N >> 4) + qt) * (N >> 5) + kb) << 9) + lane * 8;
+}
+
 // y[m] = LN(x[src(m)]) with src(m) = m, or (q*nt+p) for m = p*nt+q when nt>0.
-// When H>0, bias_out[h*M+m] = bias_scale * sum_c LN(x)[m][c] * wb[c*H+h].
+// When H>0, M = N*N for an N x N grid (N % 32 == 0) and the pair bias
+// bias_scale * sum_c LN(x)[m][c] * wb[c*H+h] of m = q*N+k is written at
+// bias_out[bias_frag_index(h, q, k, N)].
 void ln_fwd_f32(hipStream_t st, const float* x, long M, int C, int nt,
                 const float* gamma, const float* beta, h16* y, float* mean,
                 float* rstd, bool fast, int H, const float* wb, float* bias_out,

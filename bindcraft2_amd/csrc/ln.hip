@@ -52,7 +52,8 @@ __device__ __forceinline__ void load_w(const float* __restrict__ wb, int c0, flo
 }
 
 // H = 0: plain LayerNorm.  H in {4, 8}: also the pair-bias projection
-// bias_out[h][m] = bias_scale * sum_c y[m][c] W[c][h], from the f32 row.
+// bias_scale * sum_c y[m][c] W[c][h], from the f32 row, written in the
+// attention kernels' score-fragment order (bias_frag_index, grid side bn).
 // A lane group handles U rows (RPB apart): all U rows are loaded before the
 // first is reduced, and gamma, beta and the projection slice are read once
 // per U rows.
@@ -61,7 +62,7 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(
     const InT* __restrict__ x, long M, int nt, const float* __restrict__ gamma,
     const float* __restrict__ beta, h16* __restrict__ y,
     float* __restrict__ mean_out, float* __restrict__ rstd_out,
-    const float* __restrict__ wb, float* __restrict__ bias_out, float bias_scale) {
+    const float* __restrict__ wb, float* __restrict__ bias_out, float bias_scale, int bn) {
   using G = LnGeom<C>;
   const int t = threadIdx.x;
   const long mb = (long)blockIdx.x * (U * G::RPB) + t / G::TPR;
@@ -122,7 +123,7 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(
         p = group_sum<G::TPR>(p);
         if (gl == h) mine = p;
       }
-      if (gl < H) bias_out[(long)gl * M + m] = mine * bias_scale;
+      if (gl < H) bias_out[bias_frag_index(gl, (int)(m / bn), (int)(m % bn), bn)] = mine * bias_scale;
     }
   }
 }
@@ -360,25 +361,25 @@ constexpr int ln_rows() { return H > 0 ? 4 : 1; }
 template <int C, int H>
 static void ln_fwd_launch(hipStream_t st, const float* x, long M, int nt, const float* gamma,
                           const float* beta, h16* y, float* mean, float* rstd, bool fast,
-                          const float* wb, float* bias_out, float bs) {
+                          const float* wb, float* bias_out, float bs, int bn) {
   constexpr int U = ln_rows<H>();
   const int grid = (int)((M + U * LnGeom<C>::RPB - 1) / (U * LnGeom<C>::RPB));
   if (fast)
     hipLaunchKernelGGL((ln_fwd_kernel<C, true, float, H, U>), dim3(grid), dim3(256), 0, st, x, M,
-                       nt, gamma, beta, y, mean, rstd, wb, bias_out, bs);
+                       nt, gamma, beta, y, mean, rstd, wb, bias_out, bs, bn);
   else
     hipLaunchKernelGGL((ln_fwd_kernel<C, false, float, H, U>), dim3(grid), dim3(256), 0, st, x, M,
-                       nt, gamma, beta, y, mean, rstd, wb, bias_out, bs);
+                       nt, gamma, beta, y, mean, rstd, wb, bias_out, bs, bn);
 }
 
 template <int C>
 static void ln_fwd_dispatch(hipStream_t st, const float* x, long M, int nt, const float* gamma,
                             const float* beta, h16* y, float* mean, float* rstd, bool fast, int H,
-                            const float* wb, float* bias_out, float bs) {
+                            const float* wb, float* bias_out, float bs, int bn) {
   switch (H) {
-    case 0: ln_fwd_launch<C, 0>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, wb, bias_out, bs); break;
-    case 4: ln_fwd_launch<C, 4>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, wb, bias_out, bs); break;
-    case 8: ln_fwd_launch<C, 8>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, wb, bias_out, bs); break;
+    case 0: ln_fwd_launch<C, 0>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, wb, bias_out, bs, bn); break;
+    case 4: ln_fwd_launch<C, 4>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, wb, bias_out, bs, bn); break;
+    case 8: ln_fwd_launch<C, 8>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, wb, bias_out, bs, bn); break;
     default: throw std::runtime_error("ln_fwd: bias heads must be 0, 4 or 8");
   }
 }
@@ -387,10 +388,16 @@ void ln_fwd_f32(hipStream_t st, const float* x, long M, int C, int nt,
                 const float* gamma, const float* beta, h16* y, float* mean,
                 float* rstd, bool fast, int H, const float* wb, float* bias_out,
                 float bs) {
+  int bn = 0;  // side of the N x N grid of the pair bias
+  if (H > 0) {
+    while ((long)(bn + 1) * (bn + 1) <= M) ++bn;
+    if ((long)bn * bn != M || bn % 32 != 0)
+      throw std::runtime_error("ln_fwd: the pair bias needs M = N*N with N % 32 == 0");
+  }
   switch (C) {
-    case 64: ln_fwd_dispatch<64>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, H, wb, bias_out, bs); break;
-    case 128: ln_fwd_dispatch<128>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, H, wb, bias_out, bs); break;
-    case 256: ln_fwd_dispatch<256>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, H, wb, bias_out, bs); break;
+    case 64: ln_fwd_dispatch<64>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, H, wb, bias_out, bs, bn); break;
+    case 128: ln_fwd_dispatch<128>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, H, wb, bias_out, bs, bn); break;
+    case 256: ln_fwd_dispatch<256>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, H, wb, bias_out, bs, bn); break;
     default: throw std::runtime_error("ln_fwd: unsupported channel count");
   }
 }
