@@ -848,17 +848,20 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_rows_kernel(AttnBwdArgs b, in
 // AF2's masked weight exp(-1e8 - lse) underflows to 0.  A fully masked row is
 // the uniform distribution (p = 1/N, dS = 0).
 //
-// W waves per workgroup: 4, or 8 beyond N = 512, where eight query groups
-// keep a wave's bias column and bias-gradient registers at the 4 query
-// blocks they hold at N = 512 (one workgroup per CU then).
-template <int D, int NQB, int W>
+// W waves per workgroup as QS query groups x KT key tiles: 4 = 2 x 2 up to
+// N = 256; 8 beyond, as 4 x 2 up to N = 512 and 8 x 1 past it, so a wave's
+// bias column and bias-gradient registers stay at the 4 query blocks they
+// hold at N = 512 (one workgroup per CU).  Every key group of a row re-stages
+// the row's Q and dO, so 32 keys a workgroup instead of 16 halve that
+// traffic at N = 512.
+template <int D, int NQB, int W, int QS>
 __global__ __launch_bounds__(64 * W) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   constexpr int T = 64 * W;              // threads
   constexpr int DT = D / 16;
   constexpr int LD = lds_ld<D>();
   constexpr int N = 32 * NQB;            // == a.N (dispatch)
-  constexpr int QS = W == 8 ? 8 : NQB > 8 ? 4 : 2;  // query groups per key tile
+  static_assert(W % QS == 0, "query groups x key tiles");
   constexpr int KT = W / QS;             // 16-key tiles per workgroup
   constexpr int NB = (NQB + QS - 1) / QS;  // query blocks per wave (at most)
   constexpr int CQB = NQB < 8 ? NQB : 8;   // query blocks per staged chunk
@@ -1470,9 +1473,9 @@ int attn_fwd_rows_per_chunk(int R, int N, int H) {
 // chunks of 13 rows).  Fewer chunks also mean fewer [nchunk][H][N][N]
 // partials to write and add.
 int attn_rows_per_chunk(int R, int N, int H) {
-  const int KT = N > 256 ? 1 : 2;
+  const int KT = N > 512 ? 1 : 2;
   const long per_chunk = (long)H * (N / (16 * KT));
-  const long per_cu = N > 512 ? 1 : 2;  // eight-wave workgroups beyond 512
+  const long per_cu = N > 256 ? 1 : 2;  // eight-wave workgroups beyond 256
   const long nch = std::max(1L, per_cu * device_cus() / per_chunk);
   return (int)std::max(1L, ((long)R + nch - 1) / nch);
 }
@@ -1582,8 +1585,8 @@ static void attn_bwd_t(hipStream_t st, const AttnBwdArgs& b) {
   }
   const int nch = attn_bwd_nchunk(a.R, b.rows_per_chunk);
   // waves W, query groups QS and key tiles KT per workgroup, as in the kernel
-  const int W = a.N > 512 ? 8 : 4;
-  const int QS = W == 8 ? 8 : a.N > 256 ? 4 : 2, KT = W / QS;
+  const int W = a.N > 256 ? 8 : 4;
+  const int QS = a.N > 512 ? 8 : a.N > 256 ? 4 : 2, KT = W / QS;
   const int nkw = a.N / (16 * KT);
   const size_t lds_k = (size_t)attn_chunk(a.N) * lds_ld<D>() * 2 * 2 + (size_t)a.N * 4 * 3 +
                        (size_t)(QS - 1) * KT * 2 * (D / 16) * 4 * 64 * 4 +
@@ -1605,8 +1608,8 @@ static void attn_bwd_t(hipStream_t st, const AttnBwdArgs& b) {
     }
     with_blocks(a.N / 32, [&](auto nb) {
       constexpr int NB = decltype(nb)::value;
-      hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, NB, (NB > 16 ? 8 : 4)>), grid, dim3(64 * W),
-                         lds_k, st, b);
+      hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, NB, (NB > 8 ? 8 : 4), (NB > 16 ? 8 : NB > 8 ? 4 : 2)>),
+                         grid, dim3(64 * W), lds_k, st, b);
     });
   }
 dkv_done:
