@@ -656,7 +656,8 @@ def main():
         ms = timed(step, args.steps, args.warmup)
         flops = 2 * triattn_flops(n)
         prof = profiled(step, args.steps, args.no_kprof)
-        line = {"metric": METRIC, "value": round(flops / (ms * 1e-3) / 1e12, 3),
+        line = {"metric": METRIC if n == 224 else METRIC.replace("at L=224", f"at L={n}"),
+                "value": round(flops / (ms * 1e-3) / 1e12, 3),
                 "unit": "TFLOP/s", "higher_is_better": True,
                 "config": {"workload": "triangle attention fwd+bwd, starting+ending node "
                                        "(BASELINE configs[1])", "L": n, "c_z": 128, "heads": 4,
@@ -750,7 +751,9 @@ def main():
         tm = sum(v[0] for k, v in prof.items() if k.startswith("trimul."))
         n_tri = 2 * (48 + 4) * args.steps
         cfg = "BASELINE configs[3]" if n == 224 else "BASELINE configs[4]'s trunk" if n == 512 else "custom length"
-        line = {"metric": METRIC, "value": round(ms, 2), "unit": "ms", "higher_is_better": False,
+        # BASELINE.json's metric names L = 224; a line at another length says its own
+        metric = METRIC if n == 224 else METRIC.replace("at L=224", f"at L={n}")
+        line = {"metric": metric, "value": round(ms, 2), "unit": "ms", "higher_is_better": False,
                 "config": {"workload": f"design-step trunk fwd+bwd at L={n}: 48 Evoformer + 4 "
                                        f"extra-MSA (pair-only) + 2 template blocks ({cfg})",
                            "L": n, "n_seq": 1, "c_m": 256, "c_z": 128, "c_t": 64,

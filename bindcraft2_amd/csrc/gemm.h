@@ -141,13 +141,40 @@ struct ALoadScaledRows {
   }
 };
 
+// x32 operand from a k-major LDS tile T[k][col] (row stride ld h16, ld % 4
+// == 0): lane l gets column c0 + l%16 at k = r0 + {4g..4g+3, 16+4g..16+4g+3}
+// (g = l/16), by two ds_read_b64_tr_b16 (each the column read of a 4 x 16
+// block: within a 16-lane group, lane m addresses the 8 bytes at row
+// r0 + 4g + m/4, columns c0 + 4(m%4) .. +3).
+typedef short gemm_s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) gemm_s16x4 gemm_lds_s16x4;
+__device__ __forceinline__ h16x4 gemm_tr4(const h16* T, int ld, int r0, int c0, int lane) {
+  const int g = lane >> 4, m = lane & 15;
+  const h16* p = T + (r0 + 4 * g + (m >> 2)) * ld + c0 + 4 * (m & 3);
+  return __builtin_bit_cast(h16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((gemm_lds_s16x4*)p));
+}
+__device__ __forceinline__ h16x8 gemm_tr8(const h16* T, int ld, int r0, int c0, int lane) {
+  const h16x4 a = gemm_tr4(T, ld, r0, c0, lane), b = gemm_tr4(T, ld, r0 + 16, c0, lane);
+  h16x8 r;
+  r[0] = a[0]; r[1] = a[1]; r[2] = a[2]; r[3] = a[3];
+  r[4] = b[0]; r[5] = b[1]; r[6] = b[2]; r[7] = b[3];
+  return r;
+}
+
 template <int BM, int BN, int BK>
 struct GemmSmem {
   static constexpr int LDK = BK + 8;
   // 64-deep steps (long K) keep one operand buffer and pay a second barrier
   // per step, so four workgroups still fit a CU; 32-deep steps double-buffer
   static constexpr int NBUF = BK >= 64 ? 1 : 2;
-  static constexpr int AB = NBUF * (BM + BN) * LDK * 2;  // bytes of the operand buffers
+  // A k-major operand tile is kept k-major, [BK][rows + 16]: a row stride of
+  // 16 (mod 32) h16 puts the 8 rows of a half-wave's transposed read on
+  // distinct banks
+  static constexpr int LDMA = BM + 16, LDMB = BN + 16;
+  static constexpr int cmax(int a, int b) { return a > b ? a : b; }
+  static constexpr int AE = cmax(BM * LDK, BK * LDMA);  // h16 of one A buffer
+  static constexpr int BE = cmax(BN * LDK, BK * LDMB);  // h16 of one B buffer
+  static constexpr int AB = NBUF * (AE + BE) * 2;  // bytes of the operand buffers
   static constexpr int LDT = BN + 4;
   static constexpr int T = (BM / 2) * LDT * 4;          // bytes of one epilogue pass
   static constexpr int BYTES = AB > T ? AB : T;
@@ -163,8 +190,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi, AL al = 
   constexpr int B_CH = BN * BK / 8 / 256;
   static_assert(A_CH >= 1 && B_CH >= 1, "tile too small for 256 threads");
   __shared__ __attribute__((aligned(16))) unsigned char smem[SM::BYTES];
-  h16* As = reinterpret_cast<h16*>(smem);            // [2][BM * LDK]
-  h16* Bs = As + SM::NBUF * BM * LDK;                 // [NBUF][BN * LDK]
+  h16* As = reinterpret_cast<h16*>(smem);            // [NBUF][AE]
+  h16* Bs = As + SM::NBUF * SM::AE;                   // [NBUF][BE]
+  // With a k-major operand both fragments take the K-slots {4g..4g+3,
+  // 16+4g..16+4g+3} of a 32-step (lane group g): the k-major tile gives them
+  // by two transposed reads, a K-contiguous tile by two 8-byte reads.  With
+  // both K-contiguous, slots 8g..8g+7 (one 16-byte read).
+  constexpr bool TR = !AK || !BKC;
+  constexpr int LDMA = SM::LDMA, LDMB = SM::LDMB;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -214,8 +247,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi, AL al = 
     }
   };
   auto sstore = [&](int buf) {
-    h16* as = As + buf * BM * LDK;
-    h16* bs = Bs + buf * BN * LDK;
+    h16* as = As + buf * SM::AE;
+    h16* bs = Bs + buf * SM::BE;
 #pragma unroll
     for (int p = 0; p < A_CH; ++p) {
       const int c = tid + 256 * p;
@@ -224,8 +257,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi, AL al = 
         st8(&as[row * LDK + kc], ra[p]);
       } else {
         const int k = c / (BM / 8), mc = (c % (BM / 8)) * 8;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) as[(mc + e) * LDK + k] = ra[p][e];
+        st8(&as[k * LDMA + mc], ra[p]);
       }
     }
 #pragma unroll
@@ -236,10 +268,21 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi, AL al = 
         st8(&bs[row * LDK + kc], rb[p]);
       } else {
         const int k = c / (BN / 8), nc = (c % (BN / 8)) * 8;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) bs[(nc + e) * LDK + k] = rb[p][e];
+        st8(&bs[k * LDMB + nc], rb[p]);
       }
     }
+  };
+  // fragments in the transposed-read slot order (TR)
+  auto frag_rows = [&](const h16* T, int row, int kk) __attribute__((always_inline)) -> h16x8 {
+    const h16* q = T + row * LDK + kk * 32 + 4 * (lane >> 4);
+    const h16x4 x = *reinterpret_cast<const h16x4*>(q), y = *reinterpret_cast<const h16x4*>(q + 16);
+    h16x8 v;
+    v[0] = x[0]; v[1] = x[1]; v[2] = x[2]; v[3] = x[3];
+    v[4] = y[0]; v[5] = y[1]; v[6] = y[2]; v[7] = y[3];
+    return v;
+  };
+  auto frag_cols = [&](const h16* T, int ld, int c0, int kk) __attribute__((always_inline)) -> h16x8 {
+    return gemm_tr8(T, ld, kk * 32, c0, lane);
   };
 
   f32x4 acc[TM][TN];
@@ -255,18 +298,24 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi, AL al = 
   const int fr = lane & 15, fk = (lane >> 4) * 8;
   for (int kt = 0; kt < nk; ++kt) {
     const int buf = SM::NBUF == 2 ? (kt & 1) : 0;
-    const h16* as = As + buf * BM * LDK;
-    const h16* bs = Bs + buf * BN * LDK;
+    const h16* as = As + buf * SM::AE;
+    const h16* bs = Bs + buf * SM::BE;
     if (kt + 1 < nk) gload((kt + 1) * BK);
 #pragma unroll
     for (int kk = 0; kk < BK / 32; ++kk) {
       h16x8 af[TM], bfr[TN];
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
-        af[i] = ld8(&as[(wm * WM + i * 16 + fr) * LDK + kk * 32 + fk]);
+      for (int i = 0; i < TM; ++i) {
+        if constexpr (!TR) af[i] = ld8(&as[(wm * WM + i * 16 + fr) * LDK + kk * 32 + fk]);
+        else if constexpr (AK) af[i] = frag_rows(as, wm * WM + i * 16 + fr, kk);
+        else af[i] = frag_cols(as, LDMA, wm * WM + i * 16, kk);
+      }
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
-        bfr[j] = ld8(&bs[(wn * WN + j * 16 + fr) * LDK + kk * 32 + fk]);
+      for (int j = 0; j < TN; ++j) {
+        if constexpr (!TR) bfr[j] = ld8(&bs[(wn * WN + j * 16 + fr) * LDK + kk * 32 + fk]);
+        else if constexpr (BKC) bfr[j] = frag_rows(bs, wn * WN + j * 16 + fr, kk);
+        else bfr[j] = frag_cols(bs, LDMB, wn * WN + j * 16, kk);
+      }
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll

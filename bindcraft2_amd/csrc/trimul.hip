@@ -553,7 +553,9 @@ static void trimul_check(int N) {
 }
 
 // One batched contraction (operands described by `g`, one channel plane per
-// batch entry): the dedicated kernel for N <= 256, the tiled GEMM beyond.
+// batch entry): the dedicated kernel for N <= 256, the tiled GEMM beyond, in
+// 128 x 128 tiles (64 x 64 tiles read every operand row of a plane from 8
+// tiles: 1 GB of L2 traffic per contraction at N = 512).
 template <class OutT>
 static void contract(hipStream_t st, const GemmArgs& g, OutT* C, const char* name) {
   {
@@ -564,7 +566,7 @@ static void contract(hipStream_t st, const GemmArgs& g, OutT* C, const char* nam
     else cb = C;
     if (trimul_contract(st, g.M, g.batch, g.A, g.a_sk == 1, g.B, g.b_sk == 1, cf, cb)) return;
   }
-  gemm<64, 64>(st, g, EpiStore<OutT>{C, g.N, (long)g.M * g.N, nullptr, g.N}, name);
+  gemm<128, 128>(st, g, EpiStore<OutT>{C, g.N, (long)g.M * g.N, nullptr, g.N}, name);
 }
 
 // Contraction operand layouts for one channel plane (row-major N x N).
