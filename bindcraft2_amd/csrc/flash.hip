@@ -849,11 +849,11 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_rows_kernel(AttnBwdArgs b, in
 // the uniform distribution (p = 1/N, dS = 0).
 //
 // W waves per workgroup as QS query groups x KT key tiles: 4 = 2 x 2 up to
-// N = 256; 8 beyond, as 4 x 2 up to N = 512 and 8 x 1 past it, so a wave's
-// bias column and bias-gradient registers stay at the 4 query blocks they
-// hold at N = 512 (one workgroup per CU).  Every key group of a row re-stages
-// the row's Q and dO, so 32 keys a workgroup instead of 16 halve that
-// traffic at N = 512.
+// N = 256; 8 beyond, as 4 x 2 up to N = 768 (6 query blocks a wave: 235
+// registers) and 8 x 1 past it, so a wave's bias column and bias-gradient
+// registers stay within two waves per SIMD (one workgroup per CU).  Every key
+// group of a row re-stages the row's Q and dO, so 32 keys a workgroup
+// instead of 16 halve that traffic.
 template <int D, int NQB, int W, int QS>
 __global__ __launch_bounds__(64 * W) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
@@ -1473,10 +1473,26 @@ int attn_fwd_rows_per_chunk(int R, int N, int H) {
 // chunks of 13 rows).  Fewer chunks also mean fewer [nchunk][H][N][N]
 // partials to write and add.
 int attn_rows_per_chunk(int R, int N, int H) {
-  const int KT = N > 512 ? 1 : 2;
+  const int KT = N > 768 ? 1 : 2;
   const long per_chunk = (long)H * (N / (16 * KT));
   const long per_cu = N > 256 ? 1 : 2;  // eight-wave workgroups beyond 256
-  const long nch = std::max(1L, per_cu * device_cus() / per_chunk);
+  const long slots = per_cu * device_cus();
+  long nch = std::max(1L, slots / per_chunk);
+  // a round that leaves many CUs idle (N = 768: 2 chunks of 96 workgroups
+  // fill 192 of 256 CUs) is worth more chunks: the smallest count, up to four
+  // rounds, whose rounds are at least 95% full
+  auto fill = [&](long c) {
+    const long w = c * per_chunk;
+    return (double)w / (double)(slots * ((w + slots - 1) / slots));
+  };
+  if (fill(nch) < 0.85) {
+    for (long c = nch + 1; c * per_chunk <= 4 * slots && c <= R; ++c)
+      if (fill(c) >= 0.95) {
+        nch = c;
+        break;
+      }
+  }
+  nch = std::min<long>(nch, R);
   return (int)std::max(1L, ((long)R + nch - 1) / nch);
 }
 
@@ -1586,7 +1602,7 @@ static void attn_bwd_t(hipStream_t st, const AttnBwdArgs& b) {
   const int nch = attn_bwd_nchunk(a.R, b.rows_per_chunk);
   // waves W, query groups QS and key tiles KT per workgroup, as in the kernel
   const int W = a.N > 256 ? 8 : 4;
-  const int QS = a.N > 512 ? 8 : a.N > 256 ? 4 : 2, KT = W / QS;
+  const int QS = a.N > 768 ? 8 : a.N > 256 ? 4 : 2, KT = W / QS;
   const int nkw = a.N / (16 * KT);
   const size_t lds_k = (size_t)attn_chunk(a.N) * lds_ld<D>() * 2 * 2 + (size_t)a.N * 4 * 3 +
                        (size_t)(QS - 1) * KT * 2 * (D / 16) * 4 * 64 * 4 +
@@ -1608,7 +1624,7 @@ static void attn_bwd_t(hipStream_t st, const AttnBwdArgs& b) {
     }
     with_blocks(a.N / 32, [&](auto nb) {
       constexpr int NB = decltype(nb)::value;
-      hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, NB, (NB > 8 ? 8 : 4), (NB > 16 ? 8 : NB > 8 ? 4 : 2)>),
+      hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, NB, (NB > 8 ? 8 : 4), (NB > 24 ? 8 : NB > 8 ? 4 : 2)>),
                          grid, dim3(64 * W), lds_k, st, b);
     });
   }
