@@ -502,10 +502,10 @@ void gemm(hipStream_t st, const GemmArgs& g, const Epi& epi, const char* name = 
   constexpr bool kSplittable = !epi_row_block<Epi>::value && !Epi::kHasCol && !AL::kSide;
   if constexpr (kSplittable) {
     if (g.batch == 1 && tiles * 2 < device_cus() && g.K >= 256 && g.N % 64 == 0) {
-      // slices of at least 128 (a multiple of 32 that divides K), about one
+      // slices of at least 64 (a multiple of 32 that divides K), about one
       // workgroup per CU in all
       const int kb = g.K / 32;
-      int split = (int)std::min<long>((device_cus() + tiles - 1) / tiles, g.K / 128);
+      int split = (int)std::min<long>((device_cus() + tiles - 1) / tiles, g.K / 64);
       while (split > 1 && kb % split != 0) --split;
       if (split > 1) {
         const int kslice = g.K / split;
