@@ -262,10 +262,12 @@ void opm_bwd(hipStream_t st, const OpmW& w, int S, int N, const float* msa, cons
   const long R = (long)S * N, NC = (long)N * C;
   Carver cv(const_cast<void*>(save));
   OpmSave<Carver> sv(cv, S, N, O, C);
-  // split-K plans: dleft over the N*C axis in chunks of 8 residues (1024), dright
-  // over the O*C axis in chunks of 1024
-  const int kc1 = 8 * C, nch1 = (int)((NC + kc1 - 1) / kc1);
-  const int kc2 = 1024, nch2 = (O * C + kc2 - 1) / kc2;
+  // split-K plans: dleft over the N*C axis in chunks of 2 residues (256),
+  // dright over the O*C axis in chunks of 256 -- chains of four 64-deep K
+  // steps, and enough workgroups (N/2 x 4 and 16 x 4 at N = 224) to cover the
+  // latency; the ordered reduce adds the chunks
+  const int kc1 = 2 * C, nch1 = (int)((NC + kc1 - 1) / kc1);
+  const int kc2 = 256, nch2 = (O * C + kc2 - 1) / kc2;
   if (NC % kc1 != 0 || (O * C) % kc2 != 0) throw std::runtime_error("opm: unsupported split");
   Arena& ar = arena();
   std::lock_guard<std::recursive_mutex> lk(ar.lock());

@@ -229,7 +229,8 @@ struct ALoadTrimulOut {
 // with a register prefetch of the next chunk.
 namespace tail {
 constexpr int C = 128, I = 128, NC = 4 * I + C;
-constexpr int BM = 128;
+constexpr int RT = 2;                     // 16-row tiles per wave
+constexpr int BM = 64 * RT;               // rows per workgroup (4 waves)
 constexpr int CH = 64;                    // GEMM1 columns (= GEMM2 k) per chunk
 constexpr int NPG = 4 * I / CH;           // [proj|gate] chunks
 constexpr int NCHUNK = NPG + C / CH;      // + gating_linear chunks
@@ -283,7 +284,7 @@ __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, l16 = lane & 15;
-  const long m0 = (long)blockIdx.x * BM + wave * 32;
+  const long m0 = (long)blockIdx.x * BM + wave * 16 * RT;
   const long M = a.M;
 
   // ---- chunk staging: 16 KB of B1 and 16 KB of B2 per chunk, 4 + 4 16-byte pieces a thread
@@ -293,7 +294,7 @@ __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
   // a [proj|gate] chunk, its d(cat) gating fragments (in p1) for the others.
   // The weights are issued first, so waiting for them leaves the rest in flight.
   h16x8 p1[4], p2[4];
-  h16 da[2][2][4];
+  h16 da[RT][2][4];
   auto prefetch = [&](int s) {
     if (s < NPG) {
 #pragma unroll
@@ -312,7 +313,7 @@ __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
       const h16* dsrc = s < NPG / 2 ? a.dl : a.dr;
       const int chb = (s % (NPG / 2)) * 32;  // channel within left or right
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < RT; ++i)
 #pragma unroll
         for (int q = 0; q < 2; ++q)
 #pragma unroll
@@ -321,7 +322,7 @@ __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
     } else {
       const int kc = (s - NPG) * CH;
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < RT; ++i)
 #pragma unroll
         for (int q = 0; q < 2; ++q) p1[2 * i + q] = kslots(a.dcg, C, m0 + i * 16 + l16, kc + q * 32, g);
     }
@@ -343,14 +344,14 @@ __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
 
   prefetch(0);
   // xn fragments of the wave's two row tiles, all of K, in GEMM1's slot order
-  h16x8 xf[2][C / 32];
+  h16x8 xf[RT][C / 32];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < RT; ++i)
 #pragma unroll
     for (int ks = 0; ks < C / 32; ++ks) xf[i][ks] = kslots(a.xn, C, m0 + i * 16 + l16, ks * 32, g);
-  float mk[2];
+  float mk[RT];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) mk[i] = a.mask[m0 + i * 16 + l16];
+  for (int i = 0; i < RT; ++i) mk[i] = a.mask[m0 + i * 16 + l16];
   if (tid < 2 * I) {
     Bps[tid] = a.bp[tid];
     Bgs[tid] = a.bg[tid];
@@ -358,10 +359,10 @@ __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
   stash(0, 0);
   __syncthreads();
 
-  float4 xpre[2][C / 16];
-  f32x4 acc2[2][C / 16];
+  float4 xpre[RT][C / 16];
+  f32x4 acc2[RT][C / 16];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < RT; ++i)
 #pragma unroll
     for (int j = 0; j < C / 16; ++j) acc2[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
@@ -372,12 +373,12 @@ __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
     const int buf = s & 1;
     const h16* b1 = B1s + buf * B1E;
     const h16* b2 = B2s + buf * B2E;
-    h16x8 af[2][2];  // GEMM2 A fragments: [row tile][k-step of this chunk]
+    h16x8 af[RT][2];  // GEMM2 A fragments: [row tile][k-step of this chunk]
     if (s < NPG) {
       // GEMM1: P for 4 column blocks (proj, gate, proj, gate)
-      f32x4 acc1[2][4];
+      f32x4 acc1[RT][4];
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < RT; ++i)
 #pragma unroll
         for (int t = 0; t < 4; ++t) acc1[i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -386,7 +387,7 @@ __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) bfr[t] = ld8(b1 + (t * 16 + l16) * LD1 + ks * 32 + 8 * g);
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < RT; ++i)
 #pragma unroll
           for (int t = 0; t < 4; ++t)
             acc1[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bfr[t], xf[i][ks], acc1[i][t], 0, 0, 0);
@@ -399,7 +400,7 @@ __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) { bpv[r] = Bps[ch + r]; bgv[r] = Bgs[ch + r]; }
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < RT; ++i) {
           h16x8 f;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
@@ -415,7 +416,7 @@ __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
     } else {
       // gating_linear columns of d(cat), fetched during the previous chunk
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < RT; ++i)
 #pragma unroll
         for (int q = 0; q < 2; ++q) af[i][q] = p1[2 * i + q];
     }
@@ -426,7 +427,7 @@ __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
       // the LayerNorm tail's x rows, loaded behind the last two chunks (GEMM1
       // is done, so its operand registers are free)
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < RT; ++i)
 #pragma unroll
         for (int j = 0; j < C / 16; ++j)
           xpre[i][j] = *reinterpret_cast<const float4*>(a.x + (m0 + i * 16 + l16) * C + 16 * j + 4 * g);
@@ -438,7 +439,7 @@ __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
       for (int j = 0; j < C / 16; ++j) {
         const h16x8 bfr = ld8(b2 + (j * 16 + l16) * LD2 + q * 32 + 8 * g);
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < RT; ++i)
           acc2[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bfr, af[i][q], acc2[i][j], 0, 0, 0);
       }
     }
@@ -449,7 +450,7 @@ __global__ __launch_bounds__(256, 2) void trimul_tail_kernel(TailArgs a) {
   // ---- LayerNorm backward + residual: lane has channels 16j + 4g + r of row m
   const float gs = *a.gmul;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < RT; ++i) {
     const long m = m0 + i * 16 + l16;
     const float mu = a.mean[m], rs = a.rstd[m];
     float xh[C / 16][4], gg[C / 16][4];
