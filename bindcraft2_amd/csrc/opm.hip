@@ -102,16 +102,30 @@ __global__ void opm_norm_kernel(const float* __restrict__ mask, int S, int N,
 
 // d_act[i][(j,f)] = h16(s * dout * tbl[j][f] * normf[i][j]), s = sc[0] (the
 // cotangent scale)
+// 8 consecutive channels a thread (C % 8 == 0): 16-byte store, 32-bit index
+// math (N * N * C < 2^31 for N <= 1024, C <= 128)
 __global__ void opm_dact_kernel(const float* __restrict__ dout, const float* __restrict__ tbl,
                                 const float* __restrict__ normf, int N, int C,
                                 const float* __restrict__ sc, h16* __restrict__ dact) {
-  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (long)N * N * C) return;
-  const long ij = idx / C;
-  const int f = (int)(idx % C);
-  float x = dout[idx] * normf[ij] * sc[0];
-  if (tbl) x *= tbl[(ij % N) * C + f];
-  dact[idx] = f2h_sat(x);
+  const int v = blockIdx.x * blockDim.x + threadIdx.x;  // 8-channel group
+  const int c8 = C / 8;
+  if (v >= N * N * c8) return;
+  const int ij = v / c8, f = (v - ij * c8) * 8;
+  const float s = normf[ij] * sc[0];
+  const float4* d4 = reinterpret_cast<const float4*>(dout + (long)ij * C + f);
+  const float4 a = d4[0], b = d4[1];
+  float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  if (tbl) {
+    const float4* t4 = reinterpret_cast<const float4*>(tbl + (long)(ij % N) * C + f);
+    const float4 ta = t4[0], tb = t4[1];
+    const float t[8] = {ta.x, ta.y, ta.z, ta.w, tb.x, tb.y, tb.z, tb.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] *= t[e];
+  }
+  h16x8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = f2h_sat(x[e] * s);
+  st8(dact + (long)ij * C + f, o);
 }
 
 // dlr[(s,r)][col0 + c] = mask[s][r] * sum_chunk part[chunk][row(r,s)][c]
@@ -288,7 +302,8 @@ void opm_bwd(hipStream_t st, const OpmW& w, int S, int N, const float* msa, cons
   float* dxn = ar.take_n<float>((size_t)R * Cm);
   {
     KTimed kt("opm.dact", st);
-    const long n = (long)N * NC;
+    if (C % 8 != 0) throw std::runtime_error("opm: C must be a multiple of 8");
+    const long n = (long)N * NC / 8;
     hipLaunchKernelGGL(opm_dact_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, dpair,
                        tbl, sv.normf, N, C, sc, dact);
   }
