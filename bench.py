@@ -284,7 +284,9 @@ def traffic_of(kernel, n):
     nb = n // 32
     syms = {"attn_fwd": [f"attn_fwd_rows<32, {nb}>", f"attn_fwd<32, {nb}>"],
             "attn_bwd_dq": [f"attn_bwd_dq_rows<32, {nb}>", f"attn_bwd_dq<32, {nb}>"],
-            "attn_bwd_dkv": [f"attn_bwd_dkv<32, {nb}>"],
+            "attn_bwd_dkv": [f"attn_bwd_dkv_lds<{nb}>",
+                             f"attn_bwd_dkv<32, {nb}, {8 if nb > 8 else 4}, "
+                             f"{8 if nb > 24 else 4 if nb > 8 else 2}>"],
             "trimul.tail_bwd": ["trimul_tail", "_ZN4bc2n12_GLOBAL__N_118trimul_tail_kernelENS0_8TailArgsE"]}.get(kernel, [kernel])
     for sym in syms:
         k = summ["kernels"].get(sym)
