@@ -115,6 +115,72 @@ __global__ __launch_bounds__(64) void small_attn_fwd_kernel(
   lse[((long)j * H + h) * S + sq] = mx + __logf(sum);
 }
 
+// S = 1 (one sequence: the design step's MSA).  The softmax over one key is
+// exactly 1 (exp(s - s) = 1), so o = v and the general kernels' arithmetic
+// reduces to the lines below, bit for bit; one thread per (residue, head)
+// instead of a 64-lane wave with one live lane.  The score is still formed
+// (same order of products) for the saved lse.
+__global__ __launch_bounds__(256) void small_attn1_fwd_kernel(
+    const h16* __restrict__ qkvg, long ld, int N, int H, const float* __restrict__ mask,
+    h16* __restrict__ o, h16* __restrict__ og, long ldo, float* __restrict__ lse) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= N * H) return;
+  const int j = t / H, h = t % H;
+  const int HD = H * SA_D;
+  const h16* q = qkvg + (long)j * ld + h * SA_D;
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < SA_D / 8; ++c) {
+    const h16x8 qa = ld8(q + 8 * c), ka = ld8(q + HD + 8 * c);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s += (float)qa[e] * (float)ka[e];
+  }
+  s = fminf(fmaxf(s + MASK_BIAS * (mask[j] - 1.f), -LOGIT_CLIP), LOGIT_CLIP);
+#pragma unroll
+  for (int c = 0; c < SA_D / 8; ++c) {
+    const h16x8 v = ld8(q + 2 * HD + 8 * c), g = ld8(q + 3 * HD + 8 * c);
+    h16x8 ov, gv;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float a = (float)v[e];
+      ov[e] = (h16)a;
+      gv[e] = (h16)(a * sigmoidf_((float)g[e]));
+    }
+    st8(o + (long)j * ldo + h * SA_D + 8 * c, ov);
+    st8(og + (long)j * ldo + h * SA_D + 8 * c, gv);
+  }
+  lse[t] = s + __logf(1.f);
+}
+
+// dS = p (dP - Dsum) is exactly 0 at S = 1 (o = v, so dP and Dsum are the same
+// products summed in the same order): dq = dk = 0, dv = dO.
+__global__ __launch_bounds__(256) void small_attn1_bwd_kernel(
+    const h16* __restrict__ qkvg, long ld, int N, int H, const h16* __restrict__ o,
+    const h16* __restrict__ dog, long ldo, h16* __restrict__ dqkvg) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= N * H * (SA_D / 8)) return;
+  const int c = t % (SA_D / 8), jh = t / (SA_D / 8);  // 8 channels of one (residue, head)
+  const int j = jh / H, h = jh % H;
+  const int HD = H * SA_D;
+  const long orow = (long)j * ldo + h * SA_D + 8 * c;
+  const h16x8 g = ld8(qkvg + (long)j * ld + 3 * HD + h * SA_D + 8 * c);
+  const h16x8 dg = ld8(dog + orow), ov = ld8(o + orow);
+  h16x8 dgate, dv;
+  const h16x8 zero = {};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float sg = sigmoidf_((float)g[e]);
+    const float dgo = (float)dg[e];
+    dgate[e] = f2h_sat(dgo * (float)ov[e] * sg * (1.f - sg));
+    dv[e] = f2h_sat(dgo * sg);
+  }
+  h16* dq = dqkvg + (long)j * ld + h * SA_D + 8 * c;
+  st8(dq, zero);
+  st8(dq + HD, zero);
+  st8(dq + 2 * HD, dv);
+  st8(dq + 3 * HD, dgate);
+}
+
 // Backward, same decomposition; lane = query row.  dK/dV sums over queries
 // go through LDS atomics of the one wave that owns the (j,h) pair.
 __global__ __launch_bounds__(64) void small_attn_bwd_kernel(
@@ -423,8 +489,12 @@ void msacol_fwd(hipStream_t st, const MsaColW& w, int S, int N, const float* msa
   qkvg_gemm(st, a, R, xn, sv.qkvg, 1.f / std::sqrt((float)a.D), "msacol.gemm_qkvg");
   {
     KTimed kt("msacol.attn", st);
-    hipLaunchKernelGGL(small_attn_fwd_kernel, dim3(N * H), dim3(64), 0, st, sv.qkvg, 4L * HD, S, N,
-                       H, msa_mask, sv.o, og, (long)HD, sv.lse);
+    if (S == 1)
+      hipLaunchKernelGGL(small_attn1_fwd_kernel, dim3((N * H + 255) / 256), dim3(256), 0, st,
+                         sv.qkvg, 4L * HD, N, H, msa_mask, sv.o, og, (long)HD, sv.lse);
+    else
+      hipLaunchKernelGGL(small_attn_fwd_kernel, dim3(N * H), dim3(64), 0, st, sv.qkvg, 4L * HD, S,
+                         N, H, msa_mask, sv.o, og, (long)HD, sv.lse);
   }
   out_gemm(st, a, R, og, msa_in, msa_out, tbl, N, "msacol.gemm_out");
 }
@@ -454,8 +524,12 @@ void msacol_bwd(hipStream_t st, const MsaColW& w, int S, int N, const float* msa
             sc);
   {
     KTimed kt("msacol.attn_bwd", st);
-    hipLaunchKernelGGL(small_attn_bwd_kernel, dim3(N * H), dim3(64), 0, st, sv.qkvg, 4L * HD, S, N,
-                       H, msa_mask, sv.o, dog, (long)HD, 1.f / std::sqrt((float)a.D), dqkvg);
+    if (S == 1)
+      hipLaunchKernelGGL(small_attn1_bwd_kernel, dim3((N * H * 4 + 255) / 256), dim3(256), 0, st,
+                         sv.qkvg, 4L * HD, N, H, sv.o, dog, (long)HD, dqkvg);
+    else
+      hipLaunchKernelGGL(small_attn_bwd_kernel, dim3(N * H), dim3(64), 0, st, sv.qkvg, 4L * HD, S,
+                         N, H, msa_mask, sv.o, dog, (long)HD, 1.f / std::sqrt((float)a.D), dqkvg);
   }
   dx_gemm(st, a, R, dqkvg, dxn, "msacol.gemm_dx");
   KTimed kt("msacol.ln_bwd", st);
