@@ -1568,7 +1568,12 @@ void attn_fwd(hipStream_t st, const AttnArgs& a) {
 }
 
 template <int D>
-static void attn_bwd_t(hipStream_t st, const AttnBwdArgs& b) {
+static void attn_bwd_t(hipStream_t st, const AttnBwdArgs& b0) {
+  // one chunk of rows (the MSA row attention of one sequence): the dK/dV
+  // kernel's partial is the whole bias gradient, written in place
+  AttnBwdArgs b = b0;
+  const bool one_chunk = attn_bwd_nchunk(b.f.R, b.rows_per_chunk) == 1;
+  if (one_chunk && b.dbias && b.f.bias) b.dbias_part = b.dbias;
   const AttnArgs& a = b.f;
   const long tot = (long)a.R * a.N * a.H;
   if (!b.gate_done) {
@@ -1629,7 +1634,7 @@ static void attn_bwd_t(hipStream_t st, const AttnBwdArgs& b) {
     });
   }
 dkv_done:
-  if (b.dbias && a.bias) {
+  if (b.dbias && a.bias && !one_chunk) {
     if (!b.dbias_part) throw std::runtime_error("attention bwd: missing dbias scratch");
     const long n = (long)a.H * a.N * a.N;
     KTimed kt(timer_name(4, a), st);
