@@ -113,9 +113,9 @@ def kernel_model(name, n):
         "trimul.gemm_dx_ln": (gemm(5 * c, c), m * (10 * c + 12 * c + 8)),
         "triattn.gemm_dx_ln": (gemm(4 * c, c), m * (8 * c + 12 * c + 4 * h + 8)),
         "trans.gemm_dx_ln": (gemm(f * c, c), m * (2 * f * c + 12 * c + 8)),
-        "trans.gemm1": (gemm(c, f * c), m * (2 * c + 2 * f * c)),
+        "trans.gemm1": (gemm(c, f * c), m * (2 * c + 2 * f * c + f * c // 8)),
         "trans.gemm2": (gemm(f * c, c), m * (2 * f * c + 4 * c + 4 * c)),
-        "trans.gemm_dh": (gemm(c, f * c), m * (4 * c + 4 * f * c)),
+        "trans.gemm_dh": (gemm(c, f * c), m * (4 * c + 2 * f * c + f * c // 8)),
         "trans.gemm_dx": (gemm(f * c, c), m * (2 * f * c + 4 * c)),
         "triattn.ln_fwd": (0, m * (6 * c + 4 * h + 8)),
         "triattn.ln_bwd": (0, m * (16 * c + 4 * h + 8)),

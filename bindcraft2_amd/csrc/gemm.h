@@ -679,6 +679,47 @@ struct EpiReluMask : EpiRows {
   }
 };
 
+// C[m][n] = h16(relu(acc + bias[n])) as EpiStore<h16, true> writes it, plus
+// bits[m * (ldc / 8) + n / 8] bit e = (C[m][n + e] > 0): the ReLU's mask
+// taken from the rounded value, so a backward that reads the bits masks
+// exactly as one that reads C.
+struct EpiReluBits : EpiRows {
+  h16* C;
+  uint8_t* bits;
+  long ldc;
+  const float* bias;
+  EpiReluBits(h16* c, uint8_t* b, long l, const float* bi) : C(c), bits(b), ldc(l), bias(bi) {}
+  __device__ __forceinline__ void row(int, int m, int n, const float (&v)[8]) const {
+    float bb[8], x[8];
+    ld_f8(bias + n, bb);
+    unsigned mk = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      x[e] = fmaxf(v[e] + bb[e], 0.f);
+      mk |= ((float)f2h_sat(x[e]) > 0.f ? 1u : 0u) << e;
+    }
+    st_any8<h16>(C + (long)m * ldc + n, x);
+    bits[(long)m * (ldc >> 3) + (n >> 3)] = (uint8_t)mk;
+  }
+};
+
+// dH = acc * mask, the ReLU mask as EpiReluBits writes it (row stride ldc
+// elements, ldc / 8 bytes).
+template <class OutT = h16>
+struct EpiReluMaskBits : EpiRows {
+  OutT* C;
+  const uint8_t* bits;
+  long ldc;
+  EpiReluMaskBits(OutT* c, const uint8_t* b, long l) : C(c), bits(b), ldc(l) {}
+  __device__ __forceinline__ void row(int, int m, int n, const float (&v)[8]) const {
+    const unsigned mk = bits[(long)m * (ldc >> 3) + (n >> 3)];
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = (mk >> e) & 1u ? v[e] : 0.f;
+    st_any8<OutT>(C + (long)m * ldc + n, x);
+  }
+};
+
 // A[m][k] = relu(src[m][k]) of a kept h16 tensor (row stride C).
 struct ALoadRelu16 {
   static constexpr bool kDirect = false;

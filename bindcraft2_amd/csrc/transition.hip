@@ -1,5 +1,6 @@
 // Transition (pair and MSA), forward and backward.
-//   LN -> GEMM (C -> F*C) + bias + relu (hidden kept)
+//   LN -> GEMM (C -> F*C) + bias + relu (the hidden's ReLU mask kept, a bit
+//      an element; the hidden itself is scratch)
 //      -> GEMM (F*C -> C) + bias, fused residual (+ shared dropout table)
 // Backward: dh = ((tbl*dout) . W2^T) * (h > 0), the dropout scale applied as
 // the GEMM loads A; dxn = dh . W1^T; LN backward accumulated into din.
@@ -19,11 +20,11 @@ namespace {
 template <class A>
 struct TransSave {
   float *mean, *rstd;
-  h16* h;  // relu(xn . W1 + b1)
+  uint8_t* hbits;  // bit n of row m: relu(xn . W1 + b1)[m][n] > 0
   TransSave(A& a, long rows, int C, int F) {
     mean = a.template take<float>(rows);
     rstd = a.template take<float>(rows);
-    h = a.template take<h16>((size_t)rows * C * F);
+    hbits = a.template take<uint8_t>((size_t)rows * C * F / 8);
   }
 };
 
@@ -62,8 +63,12 @@ void transition_fwd(hipStream_t st, const TransW& w, long rows, int nt, const fl
   TransSave<Carver> sv(cv, rows, C, w.F);
   Arena& ar = arena();
   std::lock_guard<std::recursive_mutex> lk(ar.lock());
-  ar.reset(st, (size_t)rows * C * 2 + 256);
+  Sizer need;
+  need.take<h16>((size_t)rows * C);
+  need.take<h16>((size_t)rows * H);
+  ar.reset(st, need.off);
   h16* xn = ar.take_n<h16>((size_t)rows * C);
+  h16* hid = ar.take_n<h16>((size_t)rows * H);
   {
     KTimed kt(BC2N_TN(C, "trans.ln_fwd"), st);
     ln_fwd_f32(st, act_in, rows, C, 0, w.ln_g, w.ln_b, xn, sv.mean, sv.rstd, false, 0, nullptr,
@@ -73,10 +78,10 @@ void transition_fwd(hipStream_t st, const TransW& w, long rows, int nt, const fl
   g1.M = (int)rows; g1.N = H; g1.K = C;
   g1.A = xn; g1.a_sm = C; g1.a_sk = 1;
   g1.B = w.w1_t; g1.b_sn = C; g1.b_sk = 1;
-  gemm<128, 128>(st, g1, EpiStore<h16, true>{sv.h, H, 0, w.b1, H}, BC2N_TN(C, "trans.gemm1"));
+  gemm<128, 128>(st, g1, EpiReluBits(hid, sv.hbits, H, w.b1), BC2N_TN(C, "trans.gemm1"));
   GemmArgs g2;
   g2.M = (int)rows; g2.N = C; g2.K = H;
-  g2.A = sv.h; g2.a_sm = H; g2.a_sk = 1;
+  g2.A = hid; g2.a_sm = H; g2.a_sk = 1;
   g2.B = w.w2_t; g2.b_sn = H; g2.b_sk = 1;
   gemm<128, 128>(st, g2, EpiResidualRows(act_in, act_out, w.b2, tbl, nt, C, false), BC2N_TN(C, "trans.gemm2"));
 }
@@ -103,7 +108,7 @@ void transition_bwd(hipStream_t st, const TransW& w, long rows, int nt, const fl
   g1.M = (int)rows; g1.N = H; g1.K = C;
   g1.a_sm = C; g1.a_sk = 1;
   g1.B = w.w2; g1.b_sn = C; g1.b_sk = 1;
-  gemm<128, 128>(st, g1, EpiReluMask<h16>(dh, sv.h, H), BC2N_TN(C, "trans.gemm_dh"),
+  gemm<128, 128>(st, g1, EpiReluMaskBits<h16>(dh, sv.hbits, H), BC2N_TN(C, "trans.gemm_dh"),
                  ALoadScaledRows{dout, tbl, nt, C, false, sc});
   GemmArgs g2;
   g2.M = (int)rows; g2.N = C; g2.K = H;
