@@ -113,6 +113,11 @@ def kernel_model(name, n):
         "trimul.gemm_dx_ln": (gemm(5 * c, c), m * (10 * c + 12 * c + 8)),
         "triattn.gemm_dx_ln": (gemm(4 * c, c), m * (8 * c + 12 * c + 4 * h + 8)),
         "trans.gemm_dx_ln": (gemm(f * c, c), m * (2 * f * c + 12 * c + 8)),
+        # the pair transition as one kernel a direction (C = 128): x read, out
+        # written, LN statistics, the hidden's mask bits; the hidden stays on chip
+        "trans.fused_fwd": (gemm(c, f * c) + gemm(f * c, c), m * (4 * c + 4 * c + 8 + f * c // 8)),
+        "trans.fused_bwd": (gemm(c, f * c) + gemm(f * c, c),
+                            m * (4 * c + 4 * c + 4 * c + 8 + f * c // 8)),
         "trans.gemm1": (gemm(c, f * c), m * (2 * c + 2 * f * c + f * c // 8)),
         "trans.gemm2": (gemm(f * c, c), m * (2 * f * c + 4 * c + 4 * c)),
         "trans.gemm_dh": (gemm(c, f * c), m * (4 * c + 2 * f * c + f * c // 8)),

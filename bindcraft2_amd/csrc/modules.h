@@ -86,6 +86,9 @@ struct TransW {
   int C = 0, F = 0;
   const float *ln_g = nullptr, *ln_b = nullptr, *b1 = nullptr, *b2 = nullptr;
   const h16 *w1 = nullptr, *w1_t = nullptr, *w2 = nullptr, *w2_t = nullptr;
+  // C = 128, F = 4: both products' B operands in MFMA fragment order, per
+  // direction (forward W1^T / W2^T, backward W2 / W1)
+  const h16 *frag1_f = nullptr, *frag2_f = nullptr, *frag1_b = nullptr, *frag2_b = nullptr;
 };
 TransW transition_weights(WeightStore& ws, const std::string& prefix);
 size_t transition_save_bytes(long rows, int C, int F);

@@ -38,6 +38,31 @@ def test_transition(cuda, kind, b, n):
           assert_grad((din - td).cpu().double(), g, what="dact"))
 
 
+@pytest.mark.parametrize("b,n", [(5, 20), (3, 50)])
+def test_pair_transition_ragged_rows_with_dropout_table(cuda, b, n):
+    """Row counts that are not a multiple of the fused kernel's 64-row tile,
+    and the shared dropout table (row m takes table row m % n) on both the
+    residual add and the cotangent."""
+    print(f"pair transition + dropout table b={b} n={n}", flush=True)
+    rng = np.random.default_rng(7 * b + n)
+    prm = bparams.init_block_params(0, rng, modules=["pair_transition"], gates="random",
+                                    ln="random")
+    wdir = weights_dir(prm, f"trd_{b}_{n}")
+    act = rng.standard_normal((b, n, 128)).astype(np.float32)
+    dout = rng.standard_normal((b, n, 128)).astype(np.float32)
+    tbl = ((rng.random((n, 128)) > 0.25) / 0.75).astype(np.float32)
+    mod = ops.Transition(wdir, "param/block0/pair_transition/", 128)
+    ta, td, tt = _t(act, cuda), _t(dout, cuda), _t(tbl, cuda)
+    out, save = mod.forward(ta, tt)
+    din = mod.backward(ta, tt, save, td)
+    P = af2.Params(prm, "param/block0/pair_transition/")
+    x = torch.tensor(act, dtype=D, requires_grad=True)
+    ref = torch.as_tensor(tbl, dtype=D)[None] * af2.transition(x, None, P)
+    (g,) = torch.autograd.grad(ref, x, torch.as_tensor(dout, dtype=D))
+    print(assert_act((out - ta).cpu().double(), ref.detach(), what="delta"),
+          assert_grad((din - td).cpu().double(), g, what="dact"))
+
+
 @pytest.mark.parametrize("s,n,mfrac", [(1, 32, 0.0), (1, 64, 0.1), (3, 32, 0.2)])
 def test_outer_product_mean(cuda, s, n, mfrac):
     print(f"opm s={s} n={n}", flush=True)
