@@ -142,14 +142,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
       ld_f8(a.ln_g + c0, gm);
       ld_f8(a.ln_b + c0, bt);
     }
-    // backward: the tile's mask bits, 16 bytes a thread (BM * H / 128 pieces)
-    static_assert(BM * (H / 128) % 256 == 0, "whole passes over the mask tile");
-    constexpr int NBP = BM * (H / 128) / 256;
+    // backward: the tile's mask bits, 16 bytes a thread (NP pieces; the
+    // threads past NP load a valid piece again and store nothing)
+    constexpr int NP = BM * (H / 128), NBP = (NP + 255) / 256;
     uint4 mb[BWD ? NBP : 1];
     if constexpr (BWD) {
 #pragma unroll
       for (int q = 0; q < NBP; ++q) {
-        const int it = tid + 256 * q, r = it / (H / 128), c = it % (H / 128);
+        const int it = min(tid + 256 * q, NP - 1), r = it / (H / 128), c = it % (H / 128);
         const long m = min(m0 + r, M - 1);
         mb[q] = *reinterpret_cast<const uint4*>(a.bits + m * (H / 8) + c * 16);
       }
@@ -160,8 +160,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 #pragma unroll
       for (int q = 0; q < NBP; ++q) {
         const int it = tid + 256 * q, r = it / (H / 128), c = it % (H / 128);
-        *reinterpret_cast<uint4*>(bw + r * (H / 32) + c * 4) =
-            m0 + r < M ? mb[q] : make_uint4(0u, 0u, 0u, 0u);
+        if (it < NP)
+          *reinterpret_cast<uint4*>(bw + r * (H / 32) + c * 4) =
+              m0 + r < M ? mb[q] : make_uint4(0u, 0u, 0u, 0u);
       }
     }
 #pragma unroll
@@ -211,7 +212,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) ao[i][jj] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-#pragma unroll 1
+#pragma unroll
   for (int j = 0; j < NCH; ++j) {
     const int jc = (j + rot) & (NCH - 1);
     // GEMM1: hidden columns jc*HC + 32w + 16jj + l16 of rows i*16 + 4g + r
@@ -325,7 +326,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   }
 }
 
-constexpr int kRT = 4;
+constexpr int kRT = 3;  // 48-row tiles (64 and 32 measured slower)
 
 // B operands in the kernel's fragment order.  Lane l = 16 g + c of fragment
 // (j, w, jj, ks) holds B[n][k0 + s(e)], e = 0..7, n = column j*HC + 32w +
