@@ -98,6 +98,9 @@ def kernel_model(name, n):
         # dT and one operand read, dL or dR written (binary16)
         "trimul.contract_bwd": (2 * c * n ** 3, m * 6 * c),
         "triattn.gemm_qkvg": (gemm(c, 4 * c), m * (2 * c + 8 * c)),
+        # input LayerNorm + bias heads + q|k|v|g projection in one kernel (C = 128):
+        # pair read, xn + statistics + bias + qkvg written
+        "triattn.ln_qkvg": (gemm(c, 4 * c), m * (4 * c + 2 * c + 8 + 4 * h + 8 * c)),
         "triattn.gemm_out": (gemm(c, c), m * (2 * c + 4 * c + 4 * c)),
         "triattn.gemm_dout": (gemm(c, c), m * (4 * c + 8 * c + 4 * h)),
         "triattn.gemm_dx": (gemm(4 * c, c), m * (8 * c + 4 * c)),

@@ -535,6 +535,29 @@ void gemm(hipStream_t st, const GemmArgs& g, const Epi& epi, const char* name = 
   gemm_launch<BM, BN>(st, g, epi, al);
 }
 
+// B operand of an N x 128 product (B(n, k), n < N, k < 128), N a multiple of
+// 128, rearranged for kernels that read B fragments straight from memory:
+// fragment ((j * 4 + w) * 2 + jj) * 4 + ks holds, at lane 16 g + c, the 8
+// values B(j*128 + 32w + 16jj + c, ks*32 + 8g + e), e = 0..7 -- the
+// v_mfma_f32_16x16x32_f16 B operand when A is K-contiguous -- so a wave
+// loads a fragment as one contiguous 1 KB.
+template <class B>
+std::vector<h16> b_frags_k128(int N, B b) {
+  std::vector<h16> f((size_t)N * 128);
+  for (int j = 0; j < N / 128; ++j)
+    for (int w = 0; w < 4; ++w)
+      for (int jj = 0; jj < 2; ++jj)
+        for (int ks = 0; ks < 4; ++ks)
+          for (int l = 0; l < 64; ++l)
+            for (int e = 0; e < 8; ++e)
+              f[((size_t)(((j * 4 + w) * 2 + jj) * 4 + ks) * 64 + l) * 8 + e] =
+                  (h16)b(j * 128 + 32 * w + 16 * jj + (l & 15), ks * 32 + 8 * (l >> 4) + e);
+  return f;
+}
+__device__ __forceinline__ h16x8 b_frag_k128(const h16* F, int j, int w, int jj, int ks, int lane) {
+  return ld8(F + ((long)(((j * 4 + w) * 2 + jj) * 4 + ks) * 64 + lane) * 8);
+}
+
 // ---------------------------------------------------------------- epilogues
 
 // C[b][m][n] = act(acc + bias[n]) (+= existing when ACC), OutT in {float, h16}.
