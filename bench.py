@@ -100,6 +100,8 @@ def kernel_model(name, n):
         "triattn.gemm_qkvg": (gemm(c, 4 * c), m * (2 * c + 8 * c)),
         # input LayerNorm + bias heads + q|k|v|g projection in one kernel (C = 128):
         # pair read, xn + statistics + bias + qkvg written
+        # input LayerNorm + the 4I + C projection columns in one kernel (C = 128)
+        "trimul.ln_proj": (gemm(c, 5 * c), m * (4 * c + 2 * c + 8 + 4 + 2 * 2 * c + 2 * c)),
         "triattn.ln_qkvg": (gemm(c, 4 * c), m * (4 * c + 2 * c + 8 + 4 * h + 8 * c)),
         "triattn.gemm_out": (gemm(c, c), m * (2 * c + 4 * c + 4 * c)),
         "triattn.gemm_dout": (gemm(c, c), m * (4 * c + 8 * c + 4 * h)),

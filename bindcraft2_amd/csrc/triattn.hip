@@ -16,6 +16,7 @@
 // Reference: modules.py:675-734 (TriangleAttention), :313-400 (Attention),
 // accel.py:13-24 (logit clip); native/triattn_body.cuh:647-1488 (TriAttn).
 #include "gemm.h"
+#include "lnproj.h"
 #include "modules.h"
 #include <cmath>
 #include <mutex>
@@ -101,155 +102,6 @@ static void triattn_check(const TriAttnW& w, int N) {
   if (w.D != 32 && w.D != 16) throw std::runtime_error("triattn: head width 16 or 32 only");
 }
 
-// The input LayerNorm, its pair-bias projection and the q|k|v|g projection
-// in one kernel (C = 128): a workgroup LayerNorms 48 rows (xn, mean, rstd
-// and the H bias heads written as the unfused LayerNorm writes them), keeps
-// the binary16 rows in LDS and multiplies them by the 4HD x 128 weights 128
-// output columns at a time (fragments read straight from memory in
-// b_frags_k128 order, prefetched a chunk ahead), each chunk's accumulators
-// staged through LDS for the row epilogue's 16-byte stores.  Saves xn's
-// write-then-read and the GEMM's per-tile operand staging.
-namespace lnproj {
-constexpr int C = 128, RT = 3, BM = 16 * RT, LDX = C + 8, LDT = 128 + 4;
-
-struct Args {
-  long M;
-  int nt, bn, nout;  // nt: transposed read (ending node) when > 0; bn = N; nout = 4HD
-  const float* x;
-  const float *g, *b, *wb;  // LayerNorm scale, offset; bias weights [C][H]
-  float bscale;
-  h16* xn;
-  float *mean, *rstd, *bias;
-  const h16* W;  // [nout][C] in b_frags_k128 order
-};
-
-template <int H, class Epi>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void kernel(Args a,
-                                                                                           Epi epi) {
-  __shared__ __align__(16) h16 xs[BM * LDX];
-  __shared__ __align__(16) float T[BM * LDT];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, l16 = lane & 15;
-  const long M = a.M, m0 = (long)blockIdx.x * BM;
-  const int nch = a.nout / 128;
-  h16x8 bf[4][2];
-  auto load_b = [&](int j) {
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj) bf[ks][jj] = b_frag_k128(a.W, j, w, jj, ks, lane);
-  };
-  {
-    const int lr = lane >> 4, c0 = l16 * 8;
-    float v[RT][8];
-#pragma unroll
-    for (int p = 0; p < RT; ++p) {
-      const long m = min(m0 + p * 16 + w * 4 + lr, M - 1);  // rows past M: in bounds, unused
-      ld_f8(a.x + ln_src_row(m, a.nt) * C + c0, v[p]);
-    }
-    float gm[8], bt[8], wv[8][H];
-    ld_f8(a.g + c0, gm);
-    ld_f8(a.b + c0, bt);
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-#pragma unroll
-      for (int h = 0; h < H; ++h) wv[e][h] = a.wb[(c0 + e) * H + h];
-    load_b(0);
-#pragma unroll
-    for (int p = 0; p < RT; ++p) {
-      const int r = p * 16 + w * 4 + lr;
-      const long m = m0 + r;
-      float s = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) s += v[p][e];
-      const float mu = group_sum<16>(s) / C;
-      float d2 = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float d = v[p][e] - mu;
-        d2 += d * d;
-      }
-      const float rs = rsqrtf(group_sum<16>(d2) / C + LN_EPS);
-      float o[8];
-      h16x8 ob;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        o[e] = (v[p][e] - mu) * rs * gm[e] + bt[e];
-        ob[e] = (h16)o[e];
-      }
-      float mine = 0.f;
-#pragma unroll
-      for (int h = 0; h < H; ++h) {
-        float q = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) q += o[e] * wv[e][h];
-        q = group_sum<16>(q);
-        if (l16 == h) mine = q;
-      }
-      if (m < M) {
-        st8(a.xn + m * C + c0, ob);
-        if (l16 == 0) {
-          a.mean[m] = mu;
-          a.rstd[m] = rs;
-        }
-        if (l16 < H)
-          a.bias[bias_frag_index(l16, (int)(m / a.bn), (int)(m % a.bn), a.bn)] = mine * a.bscale;
-      } else {
-        ob = h16x8{};
-      }
-      st8(xs + r * LDX + c0, ob);
-    }
-  }
-  __syncthreads();
-  const int g = lane >> 4;
-#pragma unroll 1
-  for (int j = 0; j < nch; ++j) {
-    f32x4 acc[RT][2];
-#pragma unroll
-    for (int i = 0; i < RT; ++i)
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj) acc[i][jj] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      h16x8 af[RT];
-#pragma unroll
-      for (int i = 0; i < RT; ++i) af[i] = ld8(xs + (i * 16 + l16) * LDX + ks * 32 + 8 * g);
-#pragma unroll
-      for (int i = 0; i < RT; ++i)
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj) acc[i][jj] = mfma16x16x32(af[i], bf[ks][jj], acc[i][jj]);
-    }
-    // unconditional (the last chunk reloads its own): a load under a branch
-    // leaves the in-order memory counter unknown at the join
-    load_b(min(j + 1, nch - 1));
-    __syncthreads();  // the previous chunk's epilogue is done with T
-#pragma unroll
-    for (int i = 0; i < RT; ++i)
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          T[(i * 16 + 4 * g + r) * LDT + 32 * w + 16 * jj + l16] = acc[i][jj][r];
-    __syncthreads();
-    for (int it = tid; it < BM * 16; it += 256) {
-      const int r = it >> 4, c8 = (it & 15) * 8;
-      const long m = m0 + r;
-      if (m >= M) continue;
-      float vv[8];
-      ld_f8(T + r * LDT + c8, vv);
-      epi.row(0, (int)m, j * 128 + c8, vv);
-    }
-  }
-}
-
-template <class Epi>
-void launch(hipStream_t st, int H, const Args& a, const Epi& epi) {
-  if (a.M <= 0 || a.nout % 128 != 0 || a.bn <= 0 || (long)a.bn * a.bn != a.M)
-    throw std::runtime_error("triattn: LayerNorm-projection shape");
-  const dim3 grid((unsigned)((a.M + BM - 1) / BM));
-  if (H != 4) throw std::runtime_error("triattn: the fused LayerNorm-projection takes 4 bias heads");
-  hipLaunchKernelGGL((kernel<4, Epi>), grid, dim3(256), 0, st, a, epi);
-}
-}  // namespace lnproj
 
 // The forward with its scratch (xn [M][C], og [M][HD], binary16) supplied.
 static void triattn_fwd_with(hipStream_t st, const TriAttnW& w, bool per_column, int N,
@@ -266,7 +118,8 @@ static void triattn_fwd_with(hipStream_t st, const TriAttnW& w, bool per_column,
     la.x = pair_in; la.g = w.ln_g; la.b = w.ln_b; la.wb = w.w2d; la.bscale = LOG2E;
     la.xn = xn; la.mean = sv.mean; la.rstd = sv.rstd; la.bias = sv.bias; la.W = w.wqkvg_frag;
     KTimed kt(BC2N_TN(C, "triattn.ln_qkvg"), st);
-    lnproj::launch(st, H, la, EpiScaledCols(sv.qkvg, 4L * HD, w.bqkvg, qscale, HD));
+    if (H != 4) throw std::runtime_error("triattn: the fused LayerNorm-projection takes 4 bias heads");
+    lnproj::launch<4, false>(st, la, EpiScaledCols(sv.qkvg, 4L * HD, w.bqkvg, qscale, HD));
   } else {
     {
       KTimed kt(BC2N_TN(C, "triattn.ln_fwd"), st);

@@ -21,6 +21,7 @@
 // Reference: modules.py:1044-1088 (_fused_triangle_multiplication), :909-919
 // (fast-variance LN); native/trimul_body.cuh:1183-1796 (TriMul).
 #include "gemm.h"
+#include "lnproj.h"
 #include "modules.h"
 
 namespace bc2n {
@@ -525,6 +526,12 @@ TriMulW trimul_weights(WeightStore& ws, const std::string& P) {
     std::vector<float> c = cat();
     return transpose_h16(c.data(), C, NC);
   });
+  if (C == 128 && NC % 128 == 0) {
+    w.wcat_frag = ws.derived<h16>("trimul.wcat_frag:" + P, [&] {
+      const std::vector<float> c = cat();  // [C][NC]
+      return b_frags_k128(NC, [&](int n, int k) { return c[(size_t)k * NC + n]; });
+    });
+  }
   auto kperm_cols = [](std::vector<h16> m, int rows, int cols) {
     std::vector<h16> o(m.size());
     for (int r = 0; r < rows; ++r)
@@ -601,18 +608,26 @@ void trimul_fwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
   ar.reset(st, (size_t)M * I * 2 + 1024);
   h16* xn = sv.xn;
   h16* tn = ar.take_n<h16>((size_t)M * I);
-  {
-    KTimed kt(BC2N_TN(C, "trimul.ln_fwd"), st);
-    ln_fwd_f32(st, pair_in, M, C, 0, w.ln_g, w.ln_b, xn, sv.mean, sv.rstd, true, 0, nullptr,
-               nullptr);
+  const EpiTrimulProj proj{sv.left, sv.right, sv.gout, w.bp, w.bg, w.bgl, mask, M, I, C};
+  if (w.wcat_frag) {
+    lnproj::Args la{};
+    la.M = M; la.nt = 0; la.bn = N; la.nout = NC;
+    la.x = pair_in; la.g = w.ln_g; la.b = w.ln_b;
+    la.xn = xn; la.mean = sv.mean; la.rstd = sv.rstd; la.W = w.wcat_frag;
+    KTimed kt(BC2N_TN(C, "trimul.ln_proj"), st);
+    lnproj::launch<0, true>(st, la, proj);
+  } else {
+    {
+      KTimed kt(BC2N_TN(C, "trimul.ln_fwd"), st);
+      ln_fwd_f32(st, pair_in, M, C, 0, w.ln_g, w.ln_b, xn, sv.mean, sv.rstd, true, 0, nullptr,
+                 nullptr);
+    }
+    GemmArgs g1;
+    g1.M = (int)M; g1.N = NC; g1.K = C;
+    g1.A = xn; g1.a_sm = C; g1.a_sk = 1;
+    g1.B = w.wcat_t; g1.b_sn = C; g1.b_sk = 1;
+    gemm<128, 128>(st, g1, proj, BC2N_TN(C, "trimul.gemm_proj"));
   }
-  GemmArgs g1;
-  g1.M = (int)M; g1.N = NC; g1.K = C;
-  g1.A = xn; g1.a_sm = C; g1.a_sk = 1;
-  g1.B = w.wcat_t; g1.b_sn = C; g1.b_sk = 1;
-  gemm<128, 128>(st, g1,
-                 EpiTrimulProj{sv.left, sv.right, sv.gout, w.bp, w.bg, w.bgl, mask, M, I, C},
-                 BC2N_TN(C, "trimul.gemm_proj"));
   contraction_fwd(st, outgoing, N, I, sv.left, sv.right, sv.T);
   {
     KTimed kt(BC2N_TN(C, "trimul.ln_center"), st);
