@@ -305,7 +305,11 @@ def traffic_of(kernel, n):
     # GEMM-based timers: the kernel symbol names the epilogue (demangled or
     # mangled); the contraction's output type tells forward from backward
     pat = {"trimul.proj_bwd": r"EpiTrimulProjBwd",
-           "trimul.gemm_proj": r"EpiTrimulProj(?!Bwd)",
+           "trimul.gemm_proj": r"gemm.*EpiTrimulProj(?!Bwd)",
+           "trimul.ln_proj": r"^kernel<0, true, EpiTrimulProj>|lnproj.*EpiTrimulProj",
+           "triattn.ln_qkvg": r"^kernel<4, false, EpiScaledCols>|lnproj.*EpiScaledCols",
+           "trans.fused_fwd": r"^fused<.*EpiResidualRows|fused_kernel.*EpiResidualRows",
+           "trans.fused_bwd": r"^fused<.*EpiLnBwd|fused_kernel.*EpiLnBwd",
            "trimul.gemm_out": r"EpiTrimulOut",
            "triattn.gemm_dx_ln": r"EpiLnBwd<4>|EpiLnBwdILi4E",
            "trimul.contract_fwd": rf"contract(_kernel)?(<{nb}, .*float>|ILi{nb}E.*fEE)",
