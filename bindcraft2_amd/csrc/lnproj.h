@@ -26,7 +26,8 @@ struct Args {
   const h16* W;  // [nout][C] in b_frags_k128 order
 };
 
-template <int H, bool FAST, class Epi>
+// LN = false: no LayerNorm; the binary16 rows are read from a.xn as they are.
+template <int H, bool FAST, class Epi, bool LN = true>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void kernel(Args a,
                                                                                            Epi epi) {
   __shared__ __align__(16) h16 xs[BM * LDX];
@@ -41,7 +42,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) bf[ks][jj] = b_frag_k128(a.W, j, w, jj, ks, lane);
   };
-  {
+  if constexpr (!LN) {
+    const int lr = lane >> 4, c0 = l16 * 8;
+    h16x8 ob[RT];
+#pragma unroll
+    for (int p = 0; p < RT; ++p) {
+      const long m = min(m0 + p * 16 + w * 4 + lr, M - 1);  // rows past M: in bounds, zeroed below
+      ob[p] = ld8(a.xn + m * C + c0);
+    }
+    load_b(0);
+#pragma unroll
+    for (int p = 0; p < RT; ++p) {
+      const int r = p * 16 + w * 4 + lr;
+      st8(xs + r * LDX + c0, m0 + r < M ? ob[p] : h16x8{});
+    }
+  } else {
     const int lr = lane >> 4, c0 = l16 * 8;
     float v[RT][8];
 #pragma unroll
@@ -178,6 +193,14 @@ void launch(hipStream_t st, const Args& a, const Epi& epi) {
     throw std::runtime_error("LayerNorm-projection: shape");
   const dim3 grid((unsigned)((a.M + BM - 1) / BM));
   hipLaunchKernelGGL((kernel<H, FAST, Epi>), grid, dim3(256), 0, st, a, epi);
+}
+// The same product without the LayerNorm: rows = a.xn (binary16 [M][128]).
+template <class Epi>
+void launch_rows(hipStream_t st, const Args& a, const Epi& epi) {
+  if (a.M <= 0 || a.M % 8 != 0 || a.nout % 128 != 0 || !a.xn || !a.W)
+    throw std::runtime_error("row projection: shape");
+  const dim3 grid((unsigned)((a.M + BM - 1) / BM));
+  hipLaunchKernelGGL((kernel<0, false, Epi, false>), grid, dim3(256), 0, st, a, epi);
 }
 }  // namespace lnproj
 }  // namespace bc2n

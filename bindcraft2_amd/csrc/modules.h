@@ -34,6 +34,7 @@ struct TriAttnW {
   const float* bqkvg = nullptr;  // [4HD]: zeros for q,k,v; gating_b for g
   const h16* wqkvg_t = nullptr; // [4HD][C]
   const h16* wqkvg_frag = nullptr;  // C = 128: wqkvg_t in b_frags_k128 order
+  const h16* wo_frag = nullptr;     // C = HD = 128: wo_t in b_frags_k128 order
   const h16* wqkvg = nullptr;   // [C][4HD]
   const h16* wo_t = nullptr;    // [C][HD]
   const h16* wo = nullptr;      // [HD][C]

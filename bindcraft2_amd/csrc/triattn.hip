@@ -87,6 +87,11 @@ TriAttnW triattn_weights(WeightStore& ws, const std::string& P) {
   w.wo = ws.derived<h16>("triattn.wo:" + P, [&] { return to_h16(ow.data); });
   w.wo_t = ws.derived<h16>("triattn.wo_t:" + P, [&] { return transpose_h16(ow.data.data(), HD, C); });
   w.bo = ws.f32(P + "attention/output_b");
+  if (C == 128 && HD == 128) {
+    w.wo_frag = ws.derived<h16>("triattn.wo_frag:" + P, [&] {
+      return b_frags_k128(C, [&](int n, int k) { return ow.data[(size_t)k * C + n]; });
+    });
+  }
   return w;
 }
 
@@ -145,12 +150,19 @@ static void triattn_fwd_with(hipStream_t st, const TriAttnW& w, bool per_column,
   a.lse = sv.lse;
   attn_fwd(st, a);
 
+  const EpiResidualRows res(pair_in, pair_out, w.bo, tbl, N, C, per_column);
+  if (w.wo_frag) {
+    lnproj::Args la{};
+    la.M = M; la.nout = C; la.xn = og; la.W = w.wo_frag;
+    KTimed kt(BC2N_TN(C, "triattn.gemm_out"), st);
+    lnproj::launch_rows(st, la, res);
+    return;
+  }
   GemmArgs g2;
   g2.M = (int)M; g2.N = C; g2.K = HD;
   g2.A = og; g2.a_sm = HD; g2.a_sk = 1;
   g2.B = w.wo_t; g2.b_sn = HD; g2.b_sk = 1;
-  gemm<128, 128>(st, g2, EpiResidualRows(pair_in, pair_out, w.bo, tbl, N, C, per_column),
-                 BC2N_TN(C, "triattn.gemm_out"));
+  gemm<128, 128>(st, g2, res, BC2N_TN(C, "triattn.gemm_out"));
 }
 
 void triattn_fwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
