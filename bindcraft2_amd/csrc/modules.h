@@ -67,6 +67,7 @@ struct TriMulW {
   const h16* wcat = nullptr;    // [C][4I+C]  (GEMM column order)
   const h16* wcat_t = nullptr;  // [4I+C][C]
   const h16* wcat_frag = nullptr;  // C = 128: wcat_t in b_frags_k128 order
+  const h16* wo_frag = nullptr;    // C = I = 128: wo_t in b_frags_k128 order
   // the same two matrices with k permuted within each 32-block (tail_kperm):
   // the backward tail reads a lane's 8 MFMA k-slots as one 16-byte LDS read
   const h16* wcat_k = nullptr;

@@ -546,6 +546,11 @@ TriMulW trimul_weights(WeightStore& ws, const std::string& P) {
   const HostTensor& ow = ws.host(P + "output_projection/weights");  // [I, C]
   w.wo = ws.derived<h16>("trimul.wo:" + P, [&] { return to_h16(ow.data); });
   w.wo_t = ws.derived<h16>("trimul.wo_t:" + P, [&] { return transpose_h16(ow.data.data(), I, C); });
+  if (C == 128 && I == 128) {
+    w.wo_frag = ws.derived<h16>("trimul.wo_frag:" + P, [&] {
+      return b_frags_k128(C, [&](int n, int k) { return ow.data[(size_t)k * C + n]; });
+    });
+  }
   return w;
 }
 
@@ -633,12 +638,19 @@ void trimul_fwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
     KTimed kt(BC2N_TN(C, "trimul.ln_center"), st);
     ln_fwd_cm(st, sv.T, M, I, w.cn_g, w.cn_b, tn, sv.cmean, sv.crstd, true);
   }
+  const EpiTrimulOut out(pair_in, pair_out, w.bo, sv.gout, sv.osave, tbl, N, C);
+  if (w.wo_frag) {
+    lnproj::Args la{};
+    la.M = M; la.nout = C; la.xn = tn; la.W = w.wo_frag;
+    KTimed kt(BC2N_TN(C, "trimul.gemm_out"), st);
+    lnproj::launch_rows(st, la, out);
+    return;
+  }
   GemmArgs g2;
   g2.M = (int)M; g2.N = C; g2.K = I;
   g2.A = tn; g2.a_sm = I; g2.a_sk = 1;
   g2.B = w.wo_t; g2.b_sn = I; g2.b_sk = 1;
-  gemm<128, 128>(st, g2, EpiTrimulOut(pair_in, pair_out, w.bo, sv.gout, sv.osave, tbl, N, C),
-                 BC2N_TN(C, "trimul.gemm_out"));
+  gemm<128, 128>(st, g2, out, BC2N_TN(C, "trimul.gemm_out"));
 }
 
 void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const float* pair_in,
