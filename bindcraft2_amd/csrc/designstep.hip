@@ -238,8 +238,9 @@ __global__ void pseudo_beta_kernel(const float* __restrict__ aatype,
 }
 
 void ds_check(const DesignStepW& w, int N, int S) {
-  if (N <= 0 || N % 32 != 0 || N > 1024)
-    throw std::runtime_error("design step: N must be a positive multiple of 32, at most 1024");
+  // the composed step is parity-tested to L = 224 (its parts to 1024)
+  if (N <= 0 || N % 32 != 0 || N > 768)
+    throw std::runtime_error("design step: N must be a positive multiple of 32, at most 768");
   if (S <= 0) throw std::runtime_error("design step: S must be positive");
   if (w.d_tpl <= 0 || w.d_extra <= 0 || w.d_main <= 0 || w.d_fold <= 0)
     throw std::runtime_error("design step: depths must be positive");

@@ -230,10 +230,29 @@ class MSAColumnAttention:
         return din
 
 
+def _seed_len(seed):
+    """Length of a seed operand as the C ABI takes it: the tensor's own word
+    count (u32[3] = [k0, k1, enabled], or the reference caller's u32[2] =
+    [bits, enabled]); 3 when there is none (dropout off)."""
+    if seed is None:
+        return 3
+    if seed.dtype not in (torch.uint32, torch.int32) or seed.numel() not in (2, 3):
+        raise ValueError("seed must be u32[3] [k0, k1, enabled] or u32[2] [bits, enabled]")
+    return seed.numel()
+
+
 def seed_tensor(key, enabled=True, device="cuda"):
     """The stack's seed operand u32[3] = [k0, k1, enabled] (key_data of the
     stack's JAX key plus the use_dropout flag)."""
     t = torch.tensor([int(key[0]), int(key[1]), int(bool(enabled))], dtype=torch.int64)
+    return t.to(torch.uint32).to(device)
+
+
+def bits_seed_tensor(bits, enabled=True, device="cuda"):
+    """The reference caller's seed operand u32[2] = [bits, enabled]
+    (modules_multimer.py:660-667: jax.random.bits of the stack's subkey and
+    use_dropout); the library keys the stack with PRNGKey(bits) = (0, bits)."""
+    t = torch.tensor([int(bits) & 0xFFFFFFFF, int(bool(enabled))], dtype=torch.int64)
     return t.to(torch.uint32).to(device)
 
 
@@ -275,9 +294,9 @@ class EvoformerStack:
             msa_out = torch.empty_like(msa)
         if save is None and not detached:
             save = torch.empty(self.save_bytes(n, s), dtype=torch.uint8, device=pair.device)
-        seed_len = 0 if seed is None else seed.numel()
+        seed_len = _seed_len(seed)
         check(lib().bc2n_evoformer_fwd(_stream(), _ptr(pair), _ptr(msa), _ptr(pair_mask),
-                                       _ptr(msa_mask), _ptr(seed), max(seed_len, 3), n, s, cm,
+                                       _ptr(msa_mask), _ptr(seed), seed_len, n, s, cm,
                                        self.depth, 0 if detached else 1, int(self.pair_only), 0,
                                        1, int(dropout), self.dir, _ptr(pair_out), _ptr(msa_out),
                                        None if detached else _ptr(save), None))
@@ -288,10 +307,10 @@ class EvoformerStack:
         s, _, cm = ct_msa.shape
         dpair = torch.empty_like(ct_pair)
         dmsa = torch.empty_like(ct_msa)
-        seed_len = 0 if seed is None else seed.numel()
+        seed_len = _seed_len(seed)
         check(lib().bc2n_evoformer_bwd(_stream(), _ptr(ct_pair), _ptr(ct_msa), _ptr(pair_mask),
                                        _ptr(msa_mask), _ptr(save), None, _ptr(seed),
-                                       max(seed_len, 3), n, s, cm, self.depth,
+                                       seed_len, n, s, cm, self.depth,
                                        int(self.pair_only), 0, 1, int(dropout), self.dir,
                                        _ptr(dpair), _ptr(dmsa)))
         return dpair, dmsa
@@ -332,7 +351,7 @@ class TemplatePairStack:
             out = torch.empty_like(pair)
         if save is None:
             save = torch.empty(self.save_bytes(n), dtype=torch.uint8, device=pair.device)
-        seed_len = 3 if seed is None else seed.numel()
+        seed_len = _seed_len(seed)
         check(lib().bc2n_tplstack_fwd(_stream(), _ptr(pair), _ptr(pair_mask), _ptr(seed),
                                       seed_len, n, self.depth, int(dropout), self.dir, _ptr(out),
                                       _ptr(save)))
@@ -341,7 +360,7 @@ class TemplatePairStack:
     def backward(self, ct, pair_mask, save, seed=None, dropout=True):
         n = ct.shape[0]
         dpair = torch.empty_like(ct)
-        seed_len = 3 if seed is None else seed.numel()
+        seed_len = _seed_len(seed)
         check(lib().bc2n_tplstack_bwd(_stream(), _ptr(ct), _ptr(pair_mask), _ptr(save),
                                       _ptr(seed), seed_len, n, self.depth, int(dropout), self.dir,
                                       _ptr(dpair)))
@@ -368,7 +387,7 @@ class TemplateEmbedding:
             out = torch.empty_like(query)
         if save is None:
             save = torch.empty(self.save_bytes(n), dtype=torch.uint8, device=query.device)
-        seed_len = 3 if seed is None else seed.numel()
+        seed_len = _seed_len(seed)
         check(lib().bc2n_tplembed_fwd(_stream(), _ptr(query), _ptr(act_const), _ptr(pair_mask),
                                       _ptr(seed), seed_len, n, self.depth, int(dropout), self.dir,
                                       _ptr(out), _ptr(save)))
@@ -377,7 +396,7 @@ class TemplateEmbedding:
     def backward(self, ct, query, act_const, pair_mask, save, seed=None, dropout=True):
         n = ct.shape[0]
         dquery = torch.empty_like(ct)
-        seed_len = 3 if seed is None else seed.numel()
+        seed_len = _seed_len(seed)
         check(lib().bc2n_tplembed_bwd(_stream(), _ptr(ct), _ptr(query), _ptr(act_const),
                                       _ptr(pair_mask), _ptr(save), _ptr(seed), seed_len, n,
                                       self.depth, int(dropout), self.dir, _ptr(dquery)))
@@ -437,7 +456,7 @@ class Fold:
         traj = torch.empty(self.depth, n, 3, 4, dtype=torch.float32, device=single.device)
         if save is None:
             save = torch.empty(self.save_bytes(n), dtype=torch.uint8, device=single.device)
-        seed_len = 3 if seed is None else seed.numel()
+        seed_len = _seed_len(seed)
         check(lib().bc2n_fold_fwd(_stream(), _ptr(single), _ptr(pair), _ptr(seq_mask), _ptr(seed),
                                   seed_len, n, self.depth, int(dropout), self.dir, _ptr(act),
                                   _ptr(traj), _ptr(save)))
@@ -476,7 +495,7 @@ class StructureHeads:
                      for sh in ((n, 14, 3), (n, n, 64), (n, n, 64), (n, 50), (n, 37)))
         if save is None:
             save = torch.empty(self.save_bytes(n), dtype=torch.uint8, device=dev)
-        seed_len = 3 if seed is None else seed.numel()
+        seed_len = _seed_len(seed)
         check(lib().bc2n_structure_heads_fwd(_stream(), _ptr(single), _ptr(pair), _ptr(seq_mask),
                                              _ptr(aatype), _ptr(seed), seed_len, n, self.depth,
                                              int(dropout), self.dir, *map(_ptr, outs), _ptr(save)))

@@ -413,7 +413,7 @@ int bc2n_structure_heads_bwd(void* stream, const float* single, const float* pai
  * terms; the first pass's terms are the constants of a zero state.  The
  * outputs and the save-set are the last pass's.  bwd: the five
  * cotangents (any may be NULL) -> d_target_feat f32[N,21], d_msa_feat
- * f32[S,N,49].  N is a runtime value (a multiple of 32, at most 1024): one
+ * f32[S,N,49].  N is a runtime value (a multiple of 32, at most 768): one
  * set of weights serves every length.  save holds
  * bc2n_design_step_save_bytes() bytes and is written by both calls.
  * ---------------------------------------------------------------------- */

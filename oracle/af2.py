@@ -26,14 +26,39 @@ atom37 gather against a loop; the dihedral against constructed quadruples of
 known torsion and the chi mask against a loop; gradients against central
 finite differences.
 """
+import contextlib
 import math
 
 import numpy as np
 import torch
+import torch.utils.checkpoint
 
 from . import jax_prng
 
 LOGIT_CLIP = 1e8  # bindcraft/af/accel.py:6
+
+_RECOMPUTE = [False]
+
+
+@contextlib.contextmanager
+def block_recompute():
+    """Within this context every stack block that runs under autograd keeps
+    only its input (activation checkpointing) and is run again in the
+    backward, so a deep stack at L = 224 fits in host memory.  Autograd of
+    the recomputed block is the same VJP (dropout keys are explicit, nothing
+    draws from torch's generator), so the results do not change."""
+    old = _RECOMPUTE[0]
+    _RECOMPUTE[0] = True
+    try:
+        yield
+    finally:
+        _RECOMPUTE[0] = old
+
+
+def _run_block(fn, *args):
+    if _RECOMPUTE[0] and torch.is_grad_enabled():
+        return torch.utils.checkpoint.checkpoint(fn, *args, use_reentrant=False)
+    return fn(*args)
 
 
 class Params:
@@ -118,6 +143,39 @@ def triangle_attention(pair, mask, p, per_column):
     if per_column:
         out = out.transpose(0, 1)
     return out
+
+
+def triangle_attention_vjp(pair, mask, p, per_column, dout, scale=None, rows=64):
+    """(delta, d pair) of triangle_attention(pair) * scale under the
+    cotangent dout, with the attention evaluated `rows` batch rows at a time.
+    The same functions as triangle_attention (layer_norm, the feat_2d bias
+    einsum, attention), composed the same way; the batch rows of `attention`
+    are independent, so each chunk's VJP is taken on its own and the
+    cotangents of the shared LayerNorm output and pair bias are summed before
+    one VJP through them.  Peak memory is one chunk's [rows, H, N, N] logits
+    instead of the whole [N, H, N, N] graph (17 GB a copy at N = 1024 in
+    f32).  scale: the dropout table [N, C] (applied per row, or per column
+    for the ending node), or None."""
+    x0 = pair.detach().requires_grad_(True)
+    sc = None if scale is None else (scale[:, None] if per_column else scale[None])
+    dz = dout if sc is None else dout * sc
+    xp, mk = x0, mask
+    if per_column:
+        xp, mk, dz = x0.transpose(0, 1), mask.transpose(0, 1), dz.transpose(0, 1)
+    x = layer_norm(xp, p("query_norm/scale"), p("query_norm/offset"))
+    nb = torch.einsum("qkc,ch->hqk", x, p("feat_2d_weights"))
+    bias = (1e9 * (mk - 1.0))[:, None, None, :]
+    xd, nbd = x.detach().requires_grad_(True), nb.detach().requires_grad_(True)
+    out = torch.empty_like(dz)
+    for r0 in range(0, xd.shape[0], rows):
+        sl = slice(r0, r0 + rows)
+        o = attention(xd[sl], xd[sl], bias[sl], nbd, p)
+        out[sl] = o.detach()
+        torch.autograd.backward(o, dz[sl])
+    torch.autograd.backward((x, nb), (xd.grad, nbd.grad))
+    if per_column:
+        out = out.transpose(0, 1)
+    return (out if sc is None else out * sc), x0.grad
 
 
 def triangle_multiplication(pair, mask, p, outgoing):
@@ -323,9 +381,10 @@ def evoformer_stack(msa, pair, msa_mask, pair_mask, params, depth, stack_key,
             carry, sub = jax_prng.split(carry, 2)
         else:
             sub = None
-        msa, pair = evoformer_iteration(msa, pair, msa_mask, pair_mask, params,
-                                        f"param/block{b}/", sub, use_dropout,
-                                        is_extra_msa, dtype)
+        msa, pair = _run_block(
+            lambda m, z, b=b, sub=sub: evoformer_iteration(m, z, msa_mask, pair_mask, params,
+                                                           f"param/block{b}/", sub, use_dropout,
+                                                           is_extra_msa, dtype), msa, pair)
     return msa, pair
 
 
@@ -365,7 +424,8 @@ def template_stack(act, pair_mask, params, depth, stack_key, use_dropout, dtype=
             carry, sub = jax_prng.split(carry, 2)
         else:
             sub = None
-        act = template_iteration(act, pair_mask, params, f"param/block{b}/", sub, use_dropout, dtype)
+        act = _run_block(lambda x, b=b, sub=sub: template_iteration(
+            x, pair_mask, params, f"param/block{b}/", sub, use_dropout, dtype), act)
     return act
 
 
@@ -773,7 +833,7 @@ def template_row(template_aatype, atoms37, mask37, p_emb, tables, dtype=torch.fl
 
 def design_step(target_feat, msa_feat, ids, offset, seq_mask, act_const, aatype, emsa, prm,
                 depths, keys, use_dropout, tables, recycles=0, tpl_row=None,
-                dtype=torch.float64, init_pos=None):
+                dtype=torch.float64, init_pos=None, on_pass=None):
     """The trunk of one design step, input features to the structure-module
     outputs (modules_multimer.py:441-700, EmbeddingsAndEvoformer, then
     AlphaFoldIteration's structure module and heads): the embedder plus the
@@ -792,7 +852,11 @@ def design_step(target_feat, msa_feat, ids, offset, seq_mask, act_const, aatype,
     stack's msa and msa mask (modules_multimer.py:608-617).  init_pos
     [N,37,3]: the first pass's structure module starts from these atoms'
     frames, each later pass from the previous pass's atom37 positions
-    (native/design_step.cuh:1112-1114, the model's initial_atom_pos)."""
+    (native/design_step.cuh:1112-1114, the model's initial_atom_pos).
+    on_pass(p, atom14) is called with each forward-only pass's atoms and
+    may return the atoms the next pass's recycle terms take instead (a
+    test hook: a checker feeds the kernels' own atoms, so a distogram bin
+    that rounding moves does not differ between the two)."""
     keys = keys if isinstance(keys, (list, tuple)) else [keys]
     if len(keys) != recycles + 1:
         raise ValueError("design_step: one key dict per pass")
@@ -829,7 +893,11 @@ def design_step(target_feat, msa_feat, ids, offset, seq_mask, act_const, aatype,
             out = structure_heads(single, pair, seq_mask, aatype, prm["post"], depths["fold"],
                                   k["fold"], use_dropout, tables, dtype, init_pos=start)
         if not final:
-            prev = (out[0].detach(), pair.detach(), msa[0].detach())
+            atoms = out[0].detach()
+            if on_pass is not None:
+                sub = on_pass(p, atoms)
+                atoms = atoms if sub is None else torch.as_tensor(sub, dtype=dtype)
+            prev = (atoms, pair.detach(), msa[0].detach())
     return out
 
 
@@ -959,7 +1027,7 @@ def align_to_template(atom37, exists, tpl_atoms37, tpl_mask37, flags):
 def design_step_seq(logits, flags, scalars, ids, offset, seq_mask, act_const, emsa, prm, depths,
                     keys, use_dropout, tables, bias=None, recycles=0, tpl_atoms37=None,
                     tpl_mask37=None, cyclic_mode=None, flexibility=0.0,
-                    initial_atom_pos=False, dtype=torch.float64):
+                    initial_atom_pos=False, dtype=torch.float64, on_pass=None):
     """design_step from the designed logits: sequence_features ->
     design_inputs -> design_step (one MSA row).  With template atoms
     (tpl_atoms37 [N,37,3], tpl_mask37 [N,37]) the outputs gain the predicted
@@ -993,7 +1061,7 @@ def design_step_seq(logits, flags, scalars, ids, offset, seq_mask, act_const, em
     out = design_step(tf, mf, ids, offset, seq_mask, act_const, aatype, emsa, prm, depths, keys,
                       use_dropout, tables, recycles=recycles, tpl_row=row, dtype=dtype,
                       init_pos=(torch.as_tensor(np.asarray(tpl_atoms37), dtype=dtype)
-                                if initial_atom_pos else None))
+                                if initial_atom_pos else None), on_pass=on_pass)
     if tpl_atoms37 is None:
         return out
     a37, ex = atom14_to_atom37(out[0], aatype, seq_mask, tables)

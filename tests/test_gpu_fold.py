@@ -62,7 +62,7 @@ def _oracle(prm, single, pair, mask, depth, key, dropout, d_act, d_traj):
 @pytest.mark.parametrize("n,depth,dropout,mask_frac", [
     (32, 1, False, 0.0), (32, 2, True, 0.1), (64, 3, True, 0.2), (96, 2, False, 0.1),
     # the 8-layer structure module on an L=512 pair
-    (512, 8, True, 0.1), (768, 2, True, 0.1),
+    (512, 8, True, 0.1), (768, 2, True, 0.1), (1024, 2, True, 0.1),
 ])
 def test_fold_fwd_bwd_parity(cuda, n, depth, dropout, mask_frac):
     print(f"fold n={n} depth={depth} dropout={dropout} mask={mask_frac}", flush=True)

@@ -41,6 +41,8 @@ def _case(n, seed, mask_frac):
 
 @pytest.mark.parametrize("n,depth,dropout,mask_frac", [
     (32, 1, False, 0.0), (48, 2, True, 0.1), (64, 3, True, 0.0),
+    # the longest length the entry point takes
+    (1024, 2, True, 0.1),
 ])
 def test_structure_heads_fwd_bwd_parity(cuda, n, depth, dropout, mask_frac):
     print(f"structure heads n={n} depth={depth} dropout={dropout} mask={mask_frac}", flush=True)

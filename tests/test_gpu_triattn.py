@@ -28,9 +28,16 @@ def _case(n, per_column, seed, drop, mask_frac):
 
 
 def _oracle(prm, per_column, pair, mask, tbl, dout):
-    # fp64, or fp32 from L=512 (the [L,H,L,L] logits then take 4 GB per copy)
+    # fp64, or fp32 from L=512 (the [L,H,L,L] logits then take 4 GB per copy);
+    # past 768 the VJP row chunk by row chunk (17 GB a copy at L=1024)
     dt = torch.float64 if pair.shape[0] < 512 else torch.float32
     P = af2.Params(prm, f"param/block0/{NAMES[per_column]}/", dt)
+    if pair.shape[0] > 768:
+        delta, g = af2.triangle_attention_vjp(
+            torch.as_tensor(pair, dtype=dt), torch.as_tensor(mask, dtype=dt), P, per_column,
+            torch.as_tensor(dout, dtype=dt), None if tbl is None else torch.as_tensor(tbl, dtype=dt),
+            rows=32)
+        return delta.double(), g.double()
     x = torch.tensor(pair, dtype=dt, requires_grad=True)
     m = torch.as_tensor(mask, dtype=dt)
     delta = af2.triangle_attention(x, m, P, per_column)
@@ -53,6 +60,10 @@ def _oracle(prm, per_column, pair, mask, tbl, dout):
     (512, False, True, 0.1), (512, True, True, 0.1),
     # past 512: 24 key blocks, eight-wave dK/dV (the long-length path)
     (768, False, True, 0.1), (768, True, True, 0.1),
+    # the longest lengths the entry points take: eight query groups x one
+    # key tile in dK/dV, a partial last key chunk at 800
+    (800, False, True, 0.1), (800, True, True, 0.1), (1024, False, True, 0.1),
+    (1024, True, True, 0.1),
 ])
 def test_triattn_fwd_bwd_parity(cuda, n, per_column, drop, mask_frac):
     print(f"triattn n={n} per_column={per_column} drop={drop} mask={mask_frac}", flush=True)

@@ -194,6 +194,30 @@ def test_triangle_attention_grad_finite_differences(per_column):
             assert abs(fd.item() - g[idx].item()) < 1e-6 * max(1.0, abs(fd.item()))
 
 
+@pytest.mark.parametrize("per_column", [False, True])
+def test_triangle_attention_chunked_vjp(per_column):
+    """The row-chunked VJP (for lengths whose whole graph does not fit) equals
+    autograd of the unchunked module times the dropout table, value and
+    gradient, with chunks that do not divide N and a masked residue."""
+    rng = np.random.default_rng(12)
+    n = 11
+    prm = _block(rng, ["triangle_attention_starting_node"], c_z=8, tri_heads=2)
+    P = af2.Params(prm, "param/block0/triangle_attention_starting_node/")
+    pair = torch.tensor(rng.standard_normal((n, n, 8)), dtype=DT, requires_grad=True)
+    m = np.ones(n)
+    m[4] = 0
+    mask = torch.as_tensor(np.outer(m, m))
+    tbl = torch.as_tensor((rng.random((n, 8)) > 0.25) / 0.75)
+    dout = torch.as_tensor(rng.standard_normal((n, n, 8)), dtype=DT)
+    sc = tbl[:, None] if per_column else tbl[None]
+    ref = af2.triangle_attention(pair, mask, P, per_column) * sc
+    (g,) = torch.autograd.grad(ref, pair, dout)
+    for rows in (3, 4, n):
+        d, gc = af2.triangle_attention_vjp(pair, mask, P, per_column, dout, tbl, rows=rows)
+        torch.testing.assert_close(d, ref.detach(), rtol=1e-12, atol=1e-12)
+        torch.testing.assert_close(gc, g, rtol=1e-11, atol=1e-12)
+
+
 def test_evoformer_block_runs_and_is_identity_for_zero_outputs():
     """All output layers zero => the block is the identity (sanity only)."""
     rng = np.random.default_rng(11)
@@ -593,3 +617,31 @@ def test_pair_only_iteration_is_the_extra_block_at_zero_mask():
     # and the dropout is live: a different key changes the result
     other = af2.pair_only_iteration(pair, pmask, prm, "param/block0/", J.prng_key(6), True)
     assert not torch.allclose(other, full)
+
+
+def test_block_recompute_is_exact():
+    """Per-block recompute (activation checkpointing of the stack blocks)
+    gives autograd's values and gradients to rounding."""
+    from oracle import jax_prng as J
+    rng = np.random.default_rng(13)
+    prm = {}
+    for b in range(2):
+        prm.update(bparams.init_block_params(b, rng, c_z=16, c_m=16, tri_heads=2,
+                                             trimul_hidden=8, gates="random", ln="random"))
+    n, s = 6, 2
+    pair = torch.tensor(rng.standard_normal((n, n, 16)), dtype=DT, requires_grad=True)
+    msa = torch.tensor(rng.standard_normal((s, n, 16)), dtype=DT, requires_grad=True)
+    mm = torch.ones(s, n, dtype=DT)
+    pm = torch.ones(n, n, dtype=DT)
+    key = J.prng_key(5)
+    cts = (torch.as_tensor(rng.standard_normal((s, n, 16))), torch.as_tensor(rng.standard_normal((n, n, 16))))
+
+    def run():
+        out = af2.evoformer_stack(msa, pair, mm, pm, prm, 2, key, True)
+        return [o.detach() for o in out] + list(torch.autograd.grad(out, (msa, pair), cts))
+
+    ref = run()
+    with af2.block_recompute():
+        got = run()
+    for a, b in zip(got, ref):
+        torch.testing.assert_close(a, b, rtol=1e-12, atol=1e-12)
