@@ -454,6 +454,72 @@ def pmc_summarize(fetch_csv, write_csv, copy_fetch_csv, copy_write_csv, n, out):
     return summ
 
 
+SQ_COUNTERS = ("SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_MFMA", "SQ_INSTS_LDS",
+               "SQ_LDS_BANK_CONFLICT", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_BUSY_CYCLES",
+               "GRBM_GUI_ACTIVE")
+
+
+def pmc_sq_summarize(trunk_csv, probe_csv, n, out_json, out_md, top=12):
+    """Per-kernel instruction mix and MFMA busy fraction from one rocprofv3
+    --pmc pass of SQ_COUNTERS over a trunk step, with the MFMA issue-rate
+    probe (bench.py --workload mfma) read by the same counters as the scale:
+    a kernel's MFMA busy fraction is its SQ_VALU_MFMA_BUSY_CYCLES per
+    GRBM_GUI_ACTIVE cycle divided by the probe's (whose matrix cores are busy
+    every cycle).  Counts are per launch, for each kernel's largest launch
+    shape."""
+    import csv
+    import collections
+
+    def per_dispatch(path):
+        d = collections.defaultdict(dict)
+        for r in csv.DictReader(open(path)):
+            key = (r.get("Dispatch_Id") or r.get("Correlation_Id") or r["Kernel_Name"] + r["Start_Timestamp"])
+            e = d[key]
+            e["name"] = _short_kernel_name(r["Kernel_Name"])
+            e["grid"] = int(r["Grid_Size"])
+            e["ns"] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+            e[r["Counter_Name"]] = e.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        return list(d.values())
+
+    probe = [e for e in per_dispatch(probe_csv) if e["name"].startswith("mfma_rate<0")]
+    if not probe:
+        raise SystemExit("pmc_sq_summarize: no mfma_rate<0> dispatch in the probe csv")
+    busy_scale = max(e["SQ_VALU_MFMA_BUSY_CYCLES"] / e["GRBM_GUI_ACTIVE"] for e in probe)
+    agg = collections.defaultdict(lambda: collections.defaultdict(list))
+    for e in per_dispatch(trunk_csv):
+        if all(c in e for c in SQ_COUNTERS):
+            agg[e["name"]][e["grid"]].append(e)
+    rows = {}
+    for name, shapes in agg.items():
+        grid = max(shapes)
+        es = shapes[grid]
+        mean = {c: sum(x[c] for x in es) / len(es) for c in SQ_COUNTERS}
+        us = sum(x["ns"] for x in es) / len(es) / 1e3
+        mf = max(mean["SQ_INSTS_MFMA"], 1.0)
+        rows[name] = {"grid": grid, "launches": len(es), "us": round(us, 2),
+                      **{c: round(mean[c]) for c in SQ_COUNTERS},
+                      "valu_per_mfma": round(mean["SQ_INSTS_VALU"] / mf, 2),
+                      "salu_per_mfma": round(mean["SQ_INSTS_SALU"] / mf, 2),
+                      "mfma_busy": round(mean["SQ_VALU_MFMA_BUSY_CYCLES"] / mean["GRBM_GUI_ACTIVE"]
+                                         / busy_scale, 4),
+                      "total_us": us * len(es)}
+    order = sorted(rows, key=lambda k: -rows[k]["total_us"])
+    summ = {"L": n, "counters": list(SQ_COUNTERS), "probe_busy_per_cycle": busy_scale,
+            "kernels": {k: rows[k] for k in order}}
+    with open(out_json, "w") as fh:
+        json.dump(summ, fh, indent=1)
+    with open(out_md, "w") as fh:
+        fh.write(f"| kernel (largest launch, L={n}) | us | VALU | SALU | MFMA | LDS | LDS bank "
+                 "conflict cycles | VALU/MFMA | SALU/MFMA | MFMA busy |\n|---|---|---|---|---|---|---|"
+                 "---|---|---|\n")
+        for k in order[:top]:
+            r = rows[k]
+            fh.write(f"| `{k}` | {r['us']} | {r['SQ_INSTS_VALU']} | {r['SQ_INSTS_SALU']} | "
+                     f"{r['SQ_INSTS_MFMA']} | {r['SQ_INSTS_LDS']} | {r['SQ_LDS_BANK_CONFLICT']} | "
+                     f"{r['valu_per_mfma']} | {r['salu_per_mfma']} | {r['mfma_busy']} |\n")
+    return summ
+
+
 def kernel_table(prof):
     return {k: {"ms_total": round(t, 3), "launches": c, "us_mean": round(t / c * 1e3, 2)}
             for k, (t, c) in sorted(prof.items(), key=lambda kv: -kv[1][0])}
@@ -568,12 +634,17 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--n", type=int, default=224)
-    ap.add_argument("--workload", choices=["trunk", "design", "triattn", "trimul", "fold", "copy"],
+    ap.add_argument("--workload", choices=["trunk", "design", "triattn", "trimul", "fold", "copy",
+                                           "mfma"],
                     default="trunk")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--pmc-summarize", nargs=5, metavar=("FETCH_CSV", "WRITE_CSV", "COPY_FETCH_CSV",
                                                          "COPY_WRITE_CSV", "OUT_JSON"),
                     help="write the per-kernel HBM traffic summary from rocprofv3 --pmc runs")
+    ap.add_argument("--pmc-sq-summarize", nargs=4, metavar=("TRUNK_CSV", "PROBE_CSV", "OUT_JSON",
+                                                           "OUT_MD"),
+                    help="write the per-kernel instruction mix / MFMA busy table from rocprofv3 "
+                         "--pmc runs of the SQ counters")
     ap.add_argument("--no-kprof", action="store_true",
                     help="skip the per-kernel event-timer pass (roofline / kernel table)")
     ap.add_argument("--no-design", action="store_true",
@@ -586,6 +657,11 @@ def main():
     if args.pmc_summarize:
         summ = pmc_summarize(*args.pmc_summarize[:4], args.n, args.pmc_summarize[4])
         print(json.dumps({"kernels": len(summ["kernels"]), "copy_scale": summ["copy_scale"]}))
+        return
+    if args.pmc_sq_summarize:
+        summ = pmc_sq_summarize(*args.pmc_sq_summarize[:2], args.n, *args.pmc_sq_summarize[2:])
+        print(json.dumps({"kernels": len(summ["kernels"]),
+                          "probe_busy_per_cycle": summ["probe_busy_per_cycle"]}))
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the trunk runs on one MI355X; "
@@ -617,6 +693,35 @@ def main():
                round(2 * nbytes / (ms * 1e-3) / 1e9, 1), "unit": "GB/s", "n_gpus": 1,
                "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
                "higher_is_better": True, "config": {"workload": "copy", "bytes": nbytes}}
+        print(json.dumps(out))
+        return
+    if args.workload == "mfma":
+        # the matrix-core ceiling: the MFMA forms the kernels use, issued from
+        # registers by 8 waves a CU (8 independent chains each), and the
+        # product's own GEMM kernel on a compute-bound shape
+        blocks, iters = 8 * torch.cuda.get_device_properties(dev).multi_processor_count, 256
+        rates = {}
+        for form, name in ((0, "v_mfma_f32_16x16x32_f16"), (1, "v_mfma_f32_16x16x16_f16")):
+            box = {}
+
+            def step(form=form):
+                box["flops"], _ = ops.probe_mfma(form, blocks, iters, dev)
+
+            ms = timed(step, args.steps, args.warmup)
+            rates[name] = round(box["flops"] / (ms * 1e-3) / 1e12, 1)
+        g = 8192
+        A = torch.randn(g, g, device=dev).half()
+        B = torch.randn(g, g, device=dev).half()
+        ms = timed(lambda: ops.probe_gemm(A, B), args.steps, args.warmup)
+        out = {"metric": "MFMA rate (dense f16, TFLOP/s)", "value": rates["v_mfma_f32_16x16x32_f16"],
+               "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+               "higher_is_better": True, "dtype": "f16", "data": "synthetic",
+               "config": {"workload": "mfma issue-rate probe (registers only) and gemm_kernel "
+                                      "at M=N=K=8192 (f16 in, f32 out)", "blocks": blocks,
+                          "iters": iters},
+               "mfma_forms": rates, "peak_published": 2500.0,
+               "gemm_8192_tflops": round(2 * g ** 3 / (ms * 1e-3) / 1e12, 1),
+               "gemm_8192_ms": round(ms, 3)}
         print(json.dumps(out))
         return
     global EVENT_OVERHEAD_US

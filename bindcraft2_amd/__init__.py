@@ -114,6 +114,7 @@ def _declare(L):
         "bc2n_prof_filter": (i, [cs]),
         "bc2n_prof_read": (i, [vp, i, vp, vp, i]),
         "bc2n_probe_gemm": (i, [vp, i, i, i, vp, vp, vp]),
+        "bc2n_probe_mfma": (c.c_double, [vp, i, i, i, vp]),
         "bc2n_probe_gemm_f32": (i, [vp, i, i, i, i, vp, c.c_long, c.c_long, c.c_long, vp,
                                     c.c_long, c.c_long, c.c_long, vp, c.c_long, c.c_long,
                                     c.c_long]),

@@ -15,7 +15,7 @@ LIB = os.path.join(HERE, "libbc2n.so")
 SOURCES = ["runtime.cpp", "ln.hip", "flash.hip", "ew.hip", "triattn.hip", "trimul.hip", "transition.hip",
            "msa.hip", "opm.hip", "evoformer.hip", "ipa.hip", "msaglobal.hip", "contract.hip", "tplembed.hip",
            "embed.hip", "heads.hip", "designstep.hip", "seqfeat.hip", "confidence.hip",
-           "capi.cpp"]
+           "probe.hip", "capi.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 FLAGS = [

@@ -1195,6 +1195,13 @@ int bc2n_probe_gemm(void* stream, int M, int N, int K, const uint16_t* A, const 
   });
 }
 
+double bc2n_probe_mfma(void* stream, int form, int blocks, int iters, float* out) {
+  double flops = -1.0;
+  if (guarded([&] { flops = probe_mfma_rate(as_stream(stream), form, blocks, iters, out); }) != 0)
+    return -1.0;
+  return flops;
+}
+
 int bc2n_probe_gemm_f32(void* stream, int M, int N, int K, int batch, const float* A,
                         long a_sm, long a_sk, long a_sb, const float* B, long b_sk, long b_sn,
                         long b_sb, float* C, long c_sm, long c_sn, long c_sb) {

@@ -147,4 +147,10 @@ void stack_keys(hipStream_t st, const uint32_t* seed, int depth, uint32_t* out,
 // out[0..1] = (0, seed[0]): PRNGKey of a 32-bit seed word, on the device.
 void key_from_bits(hipStream_t st, const uint32_t* seed, uint32_t* out);
 
+// MFMA issue-rate probe (probe.hip): `blocks` workgroups of 4 waves, each
+// wave 8 independent chains of `iters` MFMAs of one form (0: 16x16x32 f16,
+// 1: 16x16x16 f16) on register operands; out holds blocks*256 floats.
+// Returns the FLOPs the launch executes.
+double probe_mfma_rate(hipStream_t st, int form, int blocks, int iters, float* out);
+
 }  // namespace bc2n

@@ -626,6 +626,11 @@ int bc2n_prof_read(char* names, int name_len, double* ms, int* counts, int cap);
 /* C[M,N] = A[M,K] . B[N,K]^T, IEEE binary16 (uint16 bits) in, f32 out. */
 int bc2n_probe_gemm(void* stream, int M, int N, int K, const uint16_t* A,
                     const uint16_t* B, float* C);
+/* MFMA issue rate: `blocks` workgroups of 4 waves, each wave 8 independent
+ * accumulator chains of `iters` MFMAs from registers (form 0:
+ * v_mfma_f32_16x16x32_f16, 1: v_mfma_f32_16x16x16_f16); out f32[blocks*256].
+ * Returns the FLOPs launched, or -1 on a bad argument (bc2n_last_error()). */
+double bc2n_probe_mfma(void* stream, int form, int blocks, int iters, float* out);
 /* Batched f32 GEMM with element strides (the structure module's GEMM):
  * C[b][m][n] = sum_k A[b*a_sb + m*a_sm + k*a_sk] * B[b*b_sb + k*b_sk + n*b_sn]. */
 int bc2n_probe_gemm_f32(void* stream, int M, int N, int K, int batch, const float* A,
