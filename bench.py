@@ -495,13 +495,18 @@ def pmc_sq_summarize(trunk_csv, probe_csv, n, out_json, out_md, top=12):
         es = shapes[grid]
         mean = {c: sum(x[c] for x in es) / len(es) for c in SQ_COUNTERS}
         us = sum(x["ns"] for x in es) / len(es) / 1e3
-        mf = max(mean["SQ_INSTS_MFMA"], 1.0)
+        mf = mean["SQ_INSTS_MFMA"]
         rows[name] = {"grid": grid, "launches": len(es), "us": round(us, 2),
                       **{c: round(mean[c]) for c in SQ_COUNTERS},
-                      "valu_per_mfma": round(mean["SQ_INSTS_VALU"] / mf, 2),
-                      "salu_per_mfma": round(mean["SQ_INSTS_SALU"] / mf, 2),
+                      "valu_per_mfma": round(mean["SQ_INSTS_VALU"] / mf, 2) if mf else "-",
+                      "salu_per_mfma": round(mean["SQ_INSTS_SALU"] / mf, 2) if mf else "-",
                       "mfma_busy": round(mean["SQ_VALU_MFMA_BUSY_CYCLES"] / mean["GRBM_GUI_ACTIVE"]
                                          / busy_scale, 4),
+                      # SQ_INSTS_VALU counts the MFMAs too; a wave64 VALU
+                      # instruction holds its SIMD 4 cycles; GRBM_GUI_ACTIVE
+                      # sums the 8 XCDs' cycles; 1024 SIMDs
+                      "valu_busy": round((mean["SQ_INSTS_VALU"] - mean["SQ_INSTS_MFMA"]) * 4.0
+                                         / (1024.0 * mean["GRBM_GUI_ACTIVE"] / 8.0), 4),
                       "total_us": us * len(es)}
     order = sorted(rows, key=lambda k: -rows[k]["total_us"])
     summ = {"L": n, "counters": list(SQ_COUNTERS), "probe_busy_per_cycle": busy_scale,
@@ -510,13 +515,14 @@ def pmc_sq_summarize(trunk_csv, probe_csv, n, out_json, out_md, top=12):
         json.dump(summ, fh, indent=1)
     with open(out_md, "w") as fh:
         fh.write(f"| kernel (largest launch, L={n}) | us | VALU | SALU | MFMA | LDS | LDS bank "
-                 "conflict cycles | VALU/MFMA | SALU/MFMA | MFMA busy |\n|---|---|---|---|---|---|---|"
-                 "---|---|---|\n")
+                 "conflict cycles | VALU/MFMA | SALU/MFMA | MFMA busy | VALU busy |\n"
+                 "|---|---|---|---|---|---|---|---|---|---|---|\n")
         for k in order[:top]:
             r = rows[k]
             fh.write(f"| `{k}` | {r['us']} | {r['SQ_INSTS_VALU']} | {r['SQ_INSTS_SALU']} | "
                      f"{r['SQ_INSTS_MFMA']} | {r['SQ_INSTS_LDS']} | {r['SQ_LDS_BANK_CONFLICT']} | "
-                     f"{r['valu_per_mfma']} | {r['salu_per_mfma']} | {r['mfma_busy']} |\n")
+                     f"{r['valu_per_mfma']} | {r['salu_per_mfma']} | {r['mfma_busy']} | "
+                     f"{r['valu_busy']} |\n")
     return summ
 
 
@@ -701,7 +707,8 @@ def main():
         # product's own GEMM kernel on a compute-bound shape
         blocks, iters = 8 * torch.cuda.get_device_properties(dev).multi_processor_count, 256
         rates = {}
-        for form, name in ((0, "v_mfma_f32_16x16x32_f16"), (1, "v_mfma_f32_16x16x16_f16")):
+        for form, name in ((0, "v_mfma_f32_16x16x32_f16"), (1, "v_mfma_f32_16x16x16_f16"),
+                           (2, "v_mfma_f32_32x32x16_f16"), (3, "v_mfma_f32_16x16x32_bf16")):
             box = {}
 
             def step(form=form):

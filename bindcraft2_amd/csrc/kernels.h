@@ -149,7 +149,8 @@ void key_from_bits(hipStream_t st, const uint32_t* seed, uint32_t* out);
 
 // MFMA issue-rate probe (probe.hip): `blocks` workgroups of 4 waves, each
 // wave 8 independent chains of `iters` MFMAs of one form (0: 16x16x32 f16,
-// 1: 16x16x16 f16) on register operands; out holds blocks*256 floats.
+// 1: 16x16x16 f16, 2: 32x32x16 f16, 3: 16x16x32 bf16) on register operands;
+// out holds blocks*256 floats.
 // Returns the FLOPs the launch executes.
 double probe_mfma_rate(hipStream_t st, int form, int blocks, int iters, float* out);
 

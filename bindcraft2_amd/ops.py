@@ -770,7 +770,8 @@ def probe_gemm(a_f16, b_f16):
 
 def probe_mfma(form, blocks, iters, device="cuda"):
     """Launch the MFMA issue-rate probe (form 0: 16x16x32 f16, 1: 16x16x16
-    f16); returns (FLOPs launched, output tensor)."""
+    f16, 2: 32x32x16 f16, 3: 16x16x32 bf16); returns (FLOPs launched, output
+    tensor)."""
     out = torch.empty(blocks * 256, dtype=torch.float32, device=device)
     flops = lib().bc2n_probe_mfma(_stream(), int(form), int(blocks), int(iters), _ptr(out))
     if flops < 0:

@@ -628,7 +628,8 @@ int bc2n_probe_gemm(void* stream, int M, int N, int K, const uint16_t* A,
                     const uint16_t* B, float* C);
 /* MFMA issue rate: `blocks` workgroups of 4 waves, each wave 8 independent
  * accumulator chains of `iters` MFMAs from registers (form 0:
- * v_mfma_f32_16x16x32_f16, 1: v_mfma_f32_16x16x16_f16); out f32[blocks*256].
+ * v_mfma_f32_16x16x32_f16, 1: v_mfma_f32_16x16x16_f16, 2:
+ * v_mfma_f32_32x32x16_f16, 3: v_mfma_f32_16x16x32_bf16); out f32[blocks*256].
  * Returns the FLOPs launched, or -1 on a bad argument (bc2n_last_error()). */
 double bc2n_probe_mfma(void* stream, int form, int blocks, int iters, float* out);
 /* Batched f32 GEMM with element strides (the structure module's GEMM):
