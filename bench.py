@@ -655,6 +655,9 @@ def main():
                     help="skip the per-kernel event-timer pass (roofline / kernel table)")
     ap.add_argument("--no-design", action="store_true",
                     help="trunk workload: skip the secondary one-call design-step timing")
+    ap.add_argument("--no-msa-overlap", action="store_true",
+                    help="run the Evoformer blocks' MSA side on the caller's stream (A/B of the "
+                         "default two-stream order)")
     ap.add_argument("--progress", action="store_true",
                     help="print a line on stderr after every step (long profiler runs)")
     args = ap.parse_args()
@@ -680,6 +683,8 @@ def main():
     from bindcraft2_amd import ops, params as bparams
 
     dev = torch.device("cuda:0")
+    if args.no_msa_overlap:
+        b.lib().bc2n_set_msa_overlap(0)
     n = args.n
     rng = np.random.default_rng(0)
     m1 = np.ones(n, np.float32)

@@ -63,6 +63,7 @@ def _declare(L):
         "bc2n_evoformer_detached_bytes": (sz, [cs, i, i, c.c_int64, c.c_int64]),
         "bc2n_save_slots_probe": (i, [cs, i, i, i, i]),
         "bc2n_set_save_policy": (i, [i]),
+        "bc2n_set_msa_overlap": (i, [i]),
         "bc2n_evoformer_replays": (i, [cs, i, i, c.c_int64, c.c_int64]),
         "bc2n_stack_prealloc": (i, [i, i, i, cs, i, i, i]),
         "bc2n_tplstack_prealloc": (i, [i, i, cs]),

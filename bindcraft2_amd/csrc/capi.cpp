@@ -403,6 +403,8 @@ size_t bc2n_evoformer_detached_bytes(const char* weights_dir, int N, int S, int6
 
 int bc2n_set_save_policy(int policy) { return set_save_policy(policy); }
 
+int bc2n_set_msa_overlap(int on) { return set_msa_overlap(on != 0) ? 1 : 0; }
+
 int bc2n_evoformer_replays(const char* weights_dir, int N, int S, int64_t depth,
                            int64_t pair_only) {
   int r = -1;

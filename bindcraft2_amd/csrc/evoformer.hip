@@ -201,17 +201,31 @@ void block_fwd(hipStream_t st, const BlockW& B, const Layout& L, int b, const Ta
     KTimed kt("block.opm_const", st);
     hipLaunchKernelGGL(add_const_kernel, dim3((unsigned)((M * L.Cz + 255) / 256)), dim3(256), 0,
                        st, f.pin, p.p1, B.opm_b, M, L.Cz);
-  } else {
+  }
+  // The MSA side of the block (row attention -- which reads the pair after
+  // OPM, p1, and nothing the pair track writes --, column attention, MSA
+  // transition) runs on the side stream beside the pair track; the block's
+  // end joins the two, so the next block's OPM sees both carries.
+  const bool msa_side = !L.tpl && !L.pair_only;
+  const bool overlap = msa_side && msa_overlap();
+  hipStream_t ms = st;
+  if (msa_side) {
     opm_fwd(st, B.opm, S, N, f.min, mmask, f.pin, nullptr, p.p1, p.opm);
-    msarow_fwd(st, B.row, S, N, f.min, mmask, p.p1, t.row(b), p.m1, p.row);
-    msacol_fwd(st, B.col, S, N, p.m1, mmask, nullptr, p.m2, p.col);
-    transition_fwd(st, B.mtr, (long)S * N, N, p.m2, nullptr, f.mout, p.mtr);
+    if (overlap) {
+      ms = side_stream();
+      stream_wait(ms, st);
+    }
+    LaneGuard lg(overlap ? 1 : lane());
+    msarow_fwd(ms, B.row, S, N, f.min, mmask, p.p1, t.row(b), p.m1, p.row);
+    msacol_fwd(ms, B.col, S, N, p.m1, mmask, nullptr, p.m2, p.col);
+    transition_fwd(ms, B.mtr, (long)S * N, N, p.m2, nullptr, f.mout, p.mtr);
   }
   trimul_fwd(st, B.tmo, true, N, p1, pmask, t.pair(b, 0), p.p2, p.tmo);
   trimul_fwd(st, B.tmi, false, N, p.p2, pmask, t.pair(b, 1), p.p3, p.tmi);
   triattn_fwd(st, B.tas, false, N, p.p3, pmask, t.pair(b, 2), p.p4, p.tas);
   triattn_fwd(st, B.tae, true, N, p.p4, pmask, t.pair(b, 3), p.p5, p.tae);
   transition_fwd(st, B.ptr, M, N, p.p5, nullptr, f.pout, p.ptr);
+  if (overlap) stream_wait(st, ms);
 }
 
 // dpair / dmsa: cotangents of the block outputs on entry, of its inputs on
@@ -225,6 +239,27 @@ void block_bwd(hipStream_t st, const BlockW& B, const Layout& L, int b, const Ta
   // one cotangent scale per carry and block (the modules' own would cost a
   // max-reduction each); within a block the pair cotangent grows by a few
   // tens of percent, far inside binary16's headroom over the scaled maximum
+  // The MSA transition's and column attention's backward depend on the msa
+  // cotangent only: they run on the side stream beside the pair track's
+  // backward; the row attention's backward (which adds into the pair
+  // cotangent) and OPM's follow the join.
+  const bool msa_side = !L.tpl && !L.pair_only;
+  const bool overlap = msa_side && msa_overlap();
+  hipStream_t ms = st;
+  float* sm = msa_side ? ct_scale_slot(2) : nullptr;
+  if (msa_side) {
+    if (overlap) {
+      ms = side_stream();
+      stream_wait(ms, st);
+    }
+    LaneGuard lg(overlap ? 1 : lane());
+    {
+      KTimed kt("block.ct_scale", ms);
+      ct_scale(ms, dmsa, (long)S * N * L.Cm, sm);
+    }
+    transition_bwd(ms, B.mtr, (long)S * N, N, p.m2, nullptr, p.mtr, dmsa, dmsa, sm);
+    msacol_bwd(ms, B.col, S, N, p.m1, mmask, nullptr, p.col, dmsa, dmsa, sm);
+  }
   float* sp = ct_scale_slot(1);
   {
     KTimed kt("block.ct_scale", st);
@@ -236,14 +271,8 @@ void block_bwd(hipStream_t st, const BlockW& B, const Layout& L, int b, const Ta
   trimul_bwd(st, B.tmi, false, N, p.p2, pmask, t.pair(b, 1), p.tmi, dpair, dpair, sp);
   trimul_bwd(st, B.tmo, true, N, L.tpl ? f.pin : p.p1, pmask, t.pair(b, 0), p.tmo, dpair, dpair,
              sp);
-  if (!L.pair_only) {
-    float* sm = ct_scale_slot(2);
-    {
-      KTimed kt("block.ct_scale", st);
-      ct_scale(st, dmsa, (long)S * N * L.Cm, sm);
-    }
-    transition_bwd(st, B.mtr, (long)S * N, N, p.m2, nullptr, p.mtr, dmsa, dmsa, sm);
-    msacol_bwd(st, B.col, S, N, p.m1, mmask, nullptr, p.col, dmsa, dmsa, sm);
+  if (msa_side) {
+    if (overlap) stream_wait(st, ms);
     msarow_bwd(st, B.row, S, N, f.min, mmask, p.p1, t.row(b), p.row, dmsa, dmsa, dpair, sm);
     opm_bwd(st, B.opm, S, N, f.min, mmask, nullptr, p.opm, dpair, dmsa, dmsa, sp);
   }

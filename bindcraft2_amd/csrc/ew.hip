@@ -12,14 +12,14 @@ namespace bc2n {
 // -------------------------------------------------------- cotangent scales
 // {s, 1/s} slots and the partial maxima of ct_scale live in file-scope device
 // arrays (one copy per GPU, resolved per device by hipGetSymbolAddress), so
-// computing a scale allocates nothing.  Calls on one device share them: the
-// backward runs on one stream at a time (the library's single-stream
-// contract).
+// computing a scale allocates nothing.  Each work lane has its own partials
+// (the two lanes' scales are computed on two streams at once); the slots are
+// assigned per carry by the callers.
 namespace {
 constexpr int CT_SLOTS = 8;
 constexpr int CT_PART = 512;  // partial-maximum blocks (grid of the first pass)
 __device__ __align__(256) float g_ct_slots[CT_SLOTS * 2];
-__device__ __align__(256) float g_ct_part[CT_PART];
+__device__ __align__(256) float g_ct_part[NUM_LANES * CT_PART];
 
 struct CtPtrs {
   float* slots = nullptr;
@@ -91,8 +91,9 @@ void ct_scale(hipStream_t st, const float* x, long n, float* sc) {
   const CtPtrs p = ct_ptrs();
   const long n4 = n / 4;
   const int blocks = (int)std::min<long>(CT_PART, (n4 + 255) / 256);
-  hipLaunchKernelGGL(amax_part_kernel, dim3(blocks), dim3(256), 0, st, x, n4, p.part);
-  hipLaunchKernelGGL(amax_final_kernel, dim3(1), dim3(64), 0, st, p.part, blocks, sc);
+  float* part = p.part + (size_t)lane() * CT_PART;
+  hipLaunchKernelGGL(amax_part_kernel, dim3(blocks), dim3(256), 0, st, x, n4, part);
+  hipLaunchKernelGGL(amax_final_kernel, dim3(1), dim3(64), 0, st, part, blocks, sc);
 }
 
 // ----------------------------------------------------------------- zero fill

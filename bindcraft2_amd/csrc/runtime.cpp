@@ -102,9 +102,69 @@ void* Arena::take(size_t bytes) {
   return r;
 }
 
+namespace {
+thread_local int t_lane = 0;
+}  // namespace
+
+int lane() { return t_lane; }
+LaneGuard::LaneGuard(int l) : old(t_lane) {
+  if (l < 0 || l >= NUM_LANES) throw std::runtime_error("lane out of range");
+  t_lane = l;
+}
+LaneGuard::~LaneGuard() { t_lane = old; }
+
 Arena& arena() {
-  static Arena a;
-  return a;
+  static Arena a[NUM_LANES];
+  return a[t_lane];
+}
+
+namespace {
+struct SideStream {
+  std::mutex mu;
+  hipStream_t st = nullptr;
+  std::vector<hipEvent_t> ring;
+  size_t next = 0;
+  bool overlap = true;
+};
+SideStream& side() {
+  static SideStream s;
+  return s;
+}
+}  // namespace
+
+hipStream_t side_stream() {
+  SideStream& s = side();
+  std::lock_guard<std::mutex> lk(s.mu);
+  if (!s.st) hip_check(hipStreamCreateWithFlags(&s.st, hipStreamNonBlocking), "hipStreamCreate");
+  return s.st;
+}
+
+void stream_wait(hipStream_t to, hipStream_t from) {
+  SideStream& s = side();
+  hipEvent_t e;
+  {
+    std::lock_guard<std::mutex> lk(s.mu);
+    if (s.ring.size() < 16) {
+      hip_check(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate");
+      s.ring.push_back(e);
+    }
+    e = s.ring[s.next++ % s.ring.size()];
+  }
+  hip_check(hipEventRecord(e, from), "hipEventRecord");
+  hip_check(hipStreamWaitEvent(to, e, 0), "hipStreamWaitEvent");
+}
+
+bool set_msa_overlap(bool on) {
+  SideStream& s = side();
+  std::lock_guard<std::mutex> lk(s.mu);
+  const bool old = s.overlap;
+  s.overlap = on;
+  return old;
+}
+bool msa_overlap() {
+  SideStream& s = side();
+  std::lock_guard<std::mutex> lk(s.mu);
+  return s.overlap;
 }
 
 int device_cus() {

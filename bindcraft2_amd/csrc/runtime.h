@@ -67,7 +67,8 @@ std::vector<h16> to_h16(const std::vector<float>& v);
 std::vector<h16> transpose_h16(const float* src, int rows, int cols);
 
 // Grow-only device scratch arena, carved by bump allocation per call.  One
-// arena per device; callers hold `lock()` for the duration of a call.
+// arena per work lane (below); callers hold `lock()` for the duration of a
+// call.
 class Arena {
  public:
   void reset(hipStream_t st, size_t need);
@@ -81,7 +82,32 @@ class Arena {
   size_t cap_ = 0, off_ = 0;
   std::recursive_mutex mu_;
 };
+// The current work lane's arena.
 Arena& arena();
+
+// Work lanes.  The Evoformer stacks issue the MSA side of a block (row and
+// column attention and the MSA transition, forward; the transition and
+// column attention, backward) on a second stream beside the pair track.  A
+// module call takes its scratch from the arena of the lane the issuing thread
+// is in (lane 0 = the caller's stream, 1 = the side stream), so work of the
+// two lanes never shares scratch; the cotangent-scale partials are per lane
+// as well.  The library drives one device per process.
+constexpr int NUM_LANES = 2;
+int lane();
+struct LaneGuard {
+  int old;
+  explicit LaneGuard(int l);
+  ~LaneGuard();
+};
+// The side stream (created on first use, default priority, non-blocking).
+hipStream_t side_stream();
+// `to` waits for all work issued to `from` so far (an event recorded on
+// `from`; captured into a graph when `from` is being captured).
+void stream_wait(hipStream_t to, hipStream_t from);
+// Whether the stacks overlap the MSA side with the pair track (on by
+// default); returns the previous setting.  Off: everything on one stream.
+bool set_msa_overlap(bool on);
+bool msa_overlap();
 
 // Compute units of the current device (cached per device).
 int device_cus();

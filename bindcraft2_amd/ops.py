@@ -333,6 +333,18 @@ def save_policy(name):
         lib().bc2n_set_save_policy(old)
 
 
+@contextlib.contextmanager
+def msa_overlap(on):
+    """Run the enclosed stack calls with the MSA side of each Evoformer block
+    on the library's second stream (True, the default) or on the caller's
+    stream (False); the previous setting is restored on exit."""
+    old = lib().bc2n_set_msa_overlap(int(bool(on)))
+    try:
+        yield
+    finally:
+        lib().bc2n_set_msa_overlap(old)
+
+
 class TemplatePairStack:
     """The drop-in for TemplatePairStackFwd/Bwd (native/ffi.cu:983-1008)."""
 

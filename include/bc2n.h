@@ -11,8 +11,13 @@
  * directory (manifest.txt + raw little-endian f32 files, names
  * "param/block{b}/<module path>/<param>") loaded once per process.
  *
- * Calls are serialised by one process-wide lock and share one scratch arena,
- * so all calls of a process must use the same stream.
+ * Calls are serialised by one process-wide lock and share one scratch arena
+ * and one weight cache, so a process drives one GPU (the reference runs one
+ * design worker process per GPU).  Calls may use different streams: each
+ * call records an event on its stream after its last launch and a call on
+ * another stream first waits for it, so calls run one after another as on
+ * one stream (under graph capture only the capturing stream orders a call).
+ * Calls from several host threads must not overlap.
  *
  * Lengths: N (residues) must be a multiple of 32 -- the reference's caller
  * pads to 32 outside the custom VJP (bindcraft/af/native.py:950-972).
@@ -199,6 +204,14 @@ size_t bc2n_evoformer_detached_bytes(const char* weights_dir, int N, int S,
  * all follow it, so a forward and its backward must see the same policy.
  * Returns the previous policy, or -1 for a bad value. */
 int bc2n_set_save_policy(int policy);
+/* Process-wide: whether the Evoformer stacks run the MSA side of each block
+ * (row and column attention and the MSA transition forward; the transition
+ * and column attention backward) on a library-owned second stream beside
+ * the pair track, joined at the block's end (1, the default), or everything
+ * on the caller's stream (0).  Results are bit-identical either way.  No
+ * reference counterpart (the reference's trunk is single-stream).  Returns
+ * the previous setting. */
+int bc2n_set_msa_overlap(int on);
 /* 1 if a stack of these shapes keeps the replay tier under the policy, 0 if
  * the full save-set, -1 on error. */
 int bc2n_evoformer_replays(const char* weights_dir, int N, int S, int64_t depth,

@@ -74,3 +74,33 @@ def test_stack_dropout_is_keyed(cuda):
     assert not torch.equal(a, c)
     assert not torch.equal(a, d)
     assert torch.equal(d, e)
+
+
+@pytest.mark.parametrize("n,s,depth,policy", [(64, 2, 2, "full"), (224, 1, 3, "full"),
+                                              (96, 2, 2, "replay")])
+def test_stack_msa_overlap_bit_identical(cuda, n, s, depth, policy):
+    """The MSA side of each block on the library's second stream (the
+    default) gives exactly the bits of the single-stream order, forward and
+    backward, under both save tiers."""
+    print(f"stack msa overlap n={n} s={s} depth={depth} policy={policy}", flush=True)
+    rng = np.random.default_rng(8800 + n)
+    prm = _params(depth, rng)
+    st = ops.EvoformerStack(weights_dir(prm, f"overlap_{n}_{s}_{policy}"), depth)
+    T = lambda a: torch.as_tensor(a, device=cuda)
+    pmask, m1 = random_mask(n, 0.1, rng)
+    pmask, mmask = T(pmask), T(np.tile(m1, (s, 1)).astype(np.float32))
+    pair = T(rng.standard_normal((n, n, 128)).astype(np.float32))
+    msa = T(rng.standard_normal((s, n, 256)).astype(np.float32))
+    ct_p, ct_m = torch.randn_like(pair), torch.randn_like(msa)
+    seed = ops.seed_tensor(J.prng_key(31), True, cuda)
+    res = []
+    with ops.save_policy(policy):
+        for on in (False, True, True):
+            with ops.msa_overlap(on):
+                po, mo, sv = st.forward(pair, msa, pmask, mmask, seed)
+                dp, dm = st.backward(ct_p, ct_m, pmask, mmask, sv, seed)
+                res.append([t.clone() for t in (po, mo, dp, dm)])
+    torch.cuda.synchronize()
+    for r in res[1:]:
+        for a, b in zip(res[0], r):
+            assert torch.equal(a, b)
