@@ -189,92 +189,165 @@ Frame frame(const Layout& L, char* save, int b, const float* pair, const float* 
   return f;
 }
 
+// ------------------------------------------------------------ two streams
+// With the MSA overlap on (msa_overlap(), the default), a block's MSA side
+// runs on the side stream (lane 1, its own arena) beside the pair track:
+//
+//  forward   main: OPM's pair half, then the pair track
+//            side: row attention (reads p1 only), column attention, MSA
+//                  transition, then the NEXT block's OPM MSA half (LayerNorm
+//                  and projections of this block's msa output)
+//  backward  side: the later block's deferred OPM backward, then this
+//                  block's MSA transition and column attention backward and
+//                  the row attention's backward up to its pair-bias gradient
+//            main: the pair track's backward, then (join) the row attention's
+//                  pair term; this block's OPM backward is deferred to the
+//                  side stream, beside the earlier block's pair track
+//
+// The deferred OPM backward reads this block's pair cotangent while the
+// earlier block's pair track writes its own, so the stack alternates two pair
+// cotangent buffers; it finishes (on the side stream, in order) before the
+// earlier block's bias gradient, which main waits for before touching the
+// buffer again.  Every kernel computes what it computes on one stream, so
+// the results are bit-identical to the single-stream order.
+
+struct FwdPipe {
+  bool on = false;
+  hipStream_t ms = nullptr;
+  bool prepped = false;  // this block's OPM MSA half was issued by the block before
+  // the next block's OPM MSA half, issued by this block (null: none)
+  const OpmW* next_opm = nullptr;
+  char* next_opm_save = nullptr;
+};
+
+struct OpmPending {
+  bool on = false;
+  const OpmW* w = nullptr;
+  const float* min = nullptr;
+  const char* save = nullptr;
+  const float* dpair = nullptr;
+  const float* sp = nullptr;
+};
+
+struct BwdPipe {
+  bool on = false;
+  bool defer_opm = false;  // false: each block's OPM backward before the next block (replay tier)
+  hipStream_t ms = nullptr;
+  OpmPending opm;
+};
+
+namespace {
+void issue_opm_bwd(hipStream_t ms, const OpmPending& o, int S, int N, const float* mmask,
+                   float* dmsa) {
+  opm_bwd(ms, *o.w, S, N, o.min, mmask, nullptr, o.save, o.dpair, dmsa, dmsa, o.sp);
+}
+}  // namespace
+
 void block_fwd(hipStream_t st, const BlockW& B, const Layout& L, int b, const Tables& t,
-               const Frame& f, const float* pmask, const float* mmask, char* save) {
+               const Frame& f, const float* pmask, const float* mmask, char* save,
+               const FwdPipe* pipe = nullptr) {
   BlockPtrs p = carve(L, save);
   const int N = L.N, S = L.S;
   const long M = (long)N * N;
   // the template iteration starts at the triangle multiplications
   const float* p1 = L.tpl ? f.pin : p.p1;
+  const bool msa_side = !L.tpl && !L.pair_only;
+  const bool two = msa_side && pipe && pipe->on;
   if (L.tpl) {
   } else if (L.pair_only) {
     KTimed kt("block.opm_const", st);
     hipLaunchKernelGGL(add_const_kernel, dim3((unsigned)((M * L.Cz + 255) / 256)), dim3(256), 0,
                        st, f.pin, p.p1, B.opm_b, M, L.Cz);
-  }
-  // The MSA side of the block (row attention -- which reads the pair after
-  // OPM, p1, and nothing the pair track writes --, column attention, MSA
-  // transition) runs on the side stream beside the pair track; the block's
-  // end joins the two, so the next block's OPM sees both carries.
-  const bool msa_side = !L.tpl && !L.pair_only;
-  const bool overlap = msa_side && msa_overlap();
-  hipStream_t ms = st;
-  if (msa_side) {
+  } else if (!two) {
     opm_fwd(st, B.opm, S, N, f.min, mmask, f.pin, nullptr, p.p1, p.opm);
-    if (overlap) {
-      ms = side_stream();
-      stream_wait(ms, st);
-    }
-    LaneGuard lg(overlap ? 1 : lane());
+    msarow_fwd(st, B.row, S, N, f.min, mmask, p.p1, t.row(b), p.m1, p.row);
+    msacol_fwd(st, B.col, S, N, p.m1, mmask, nullptr, p.m2, p.col);
+    transition_fwd(st, B.mtr, (long)S * N, N, p.m2, nullptr, f.mout, p.mtr);
+  } else {
+    hipStream_t ms = pipe->ms;
+    if (pipe->prepped) stream_wait(st, ms);  // this block's OPM MSA half, the last MSA side
+    else opm_fwd_msa(st, B.opm, S, N, f.min, mmask, p.opm);
+    opm_fwd_pair(st, B.opm, S, N, f.pin, nullptr, p.p1, p.opm);
+    stream_wait(ms, st);
+    LaneGuard lg(1);
     msarow_fwd(ms, B.row, S, N, f.min, mmask, p.p1, t.row(b), p.m1, p.row);
     msacol_fwd(ms, B.col, S, N, p.m1, mmask, nullptr, p.m2, p.col);
     transition_fwd(ms, B.mtr, (long)S * N, N, p.m2, nullptr, f.mout, p.mtr);
+    if (pipe->next_opm) opm_fwd_msa(ms, *pipe->next_opm, S, N, f.mout, mmask, pipe->next_opm_save);
   }
   trimul_fwd(st, B.tmo, true, N, p1, pmask, t.pair(b, 0), p.p2, p.tmo);
   trimul_fwd(st, B.tmi, false, N, p.p2, pmask, t.pair(b, 1), p.p3, p.tmi);
   triattn_fwd(st, B.tas, false, N, p.p3, pmask, t.pair(b, 2), p.p4, p.tas);
   triattn_fwd(st, B.tae, true, N, p.p4, pmask, t.pair(b, 3), p.p5, p.tae);
   transition_fwd(st, B.ptr, M, N, p.p5, nullptr, f.pout, p.ptr);
-  if (overlap) stream_wait(st, ms);
 }
 
-// dpair / dmsa: cotangents of the block outputs on entry, of its inputs on
-// exit (updated in place).
+// dp_in: the cotangent of the block's pair output; dp_out (== dp_in on one
+// stream) receives that of its pair input.  dmsa: the msa cotangent, in place.
 void block_bwd(hipStream_t st, const BlockW& B, const Layout& L, int b, const Tables& t,
-               const Frame& f, const float* pmask, const float* mmask, char* save, float* dpair,
-               float* dmsa) {
+               const Frame& f, const float* pmask, const float* mmask, char* save,
+               const float* dp_in, float* dp_out, float* dmsa, BwdPipe* pipe = nullptr) {
   BlockPtrs p = carve(L, save);
   const int N = L.N, S = L.S;
   const long M = (long)N * N;
+  const bool msa_side = !L.tpl && !L.pair_only;
+  const bool two = msa_side && pipe && pipe->on;
   // one cotangent scale per carry and block (the modules' own would cost a
   // max-reduction each); within a block the pair cotangent grows by a few
   // tens of percent, far inside binary16's headroom over the scaled maximum
-  // The MSA transition's and column attention's backward depend on the msa
-  // cotangent only: they run on the side stream beside the pair track's
-  // backward; the row attention's backward (which adds into the pair
-  // cotangent) and OPM's follow the join.
-  const bool msa_side = !L.tpl && !L.pair_only;
-  const bool overlap = msa_side && msa_overlap();
-  hipStream_t ms = st;
   float* sm = msa_side ? ct_scale_slot(2) : nullptr;
-  if (msa_side) {
-    if (overlap) {
-      ms = side_stream();
-      stream_wait(ms, st);
+  const float* dbias = nullptr;
+  if (two) {
+    hipStream_t ms = pipe->ms;
+    stream_wait(ms, st);
+    LaneGuard lg(1);
+    if (pipe->opm.on) {
+      issue_opm_bwd(ms, pipe->opm, S, N, mmask, dmsa);
+      pipe->opm.on = false;
     }
-    LaneGuard lg(overlap ? 1 : lane());
     {
       KTimed kt("block.ct_scale", ms);
       ct_scale(ms, dmsa, (long)S * N * L.Cm, sm);
     }
     transition_bwd(ms, B.mtr, (long)S * N, N, p.m2, nullptr, p.mtr, dmsa, dmsa, sm);
     msacol_bwd(ms, B.col, S, N, p.m1, mmask, nullptr, p.col, dmsa, dmsa, sm);
+    dbias = msarow_bwd_msa(ms, B.row, S, N, f.min, mmask, t.row(b), p.row, dmsa, dmsa, sm);
   }
-  float* sp = ct_scale_slot(1);
+  // the pair scale alternates two slots a block when the OPM backward that
+  // reads it is deferred past the next block's ct_scale
+  float* sp = ct_scale_slot(two ? 4 + (b & 1) : 1);
   {
     KTimed kt("block.ct_scale", st);
-    ct_scale(st, dpair, M * L.Cz, sp);
+    ct_scale(st, dp_in, M * L.Cz, sp);
   }
-  transition_bwd(st, B.ptr, M, N, p.p5, nullptr, p.ptr, dpair, dpair, sp);
-  triattn_bwd(st, B.tae, true, N, p.p4, pmask, t.pair(b, 3), p.tae, dpair, dpair, sp);
-  triattn_bwd(st, B.tas, false, N, p.p3, pmask, t.pair(b, 2), p.tas, dpair, dpair, sp);
-  trimul_bwd(st, B.tmi, false, N, p.p2, pmask, t.pair(b, 1), p.tmi, dpair, dpair, sp);
-  trimul_bwd(st, B.tmo, true, N, L.tpl ? f.pin : p.p1, pmask, t.pair(b, 0), p.tmo, dpair, dpair,
+  transition_bwd(st, B.ptr, M, N, p.p5, nullptr, p.ptr, dp_in, dp_out, sp);
+  triattn_bwd(st, B.tae, true, N, p.p4, pmask, t.pair(b, 3), p.tae, dp_out, dp_out, sp);
+  triattn_bwd(st, B.tas, false, N, p.p3, pmask, t.pair(b, 2), p.tas, dp_out, dp_out, sp);
+  trimul_bwd(st, B.tmi, false, N, p.p2, pmask, t.pair(b, 1), p.tmi, dp_out, dp_out, sp);
+  trimul_bwd(st, B.tmo, true, N, L.tpl ? f.pin : p.p1, pmask, t.pair(b, 0), p.tmo, dp_out, dp_out,
              sp);
-  if (msa_side) {
-    if (overlap) stream_wait(st, ms);
-    msarow_bwd(st, B.row, S, N, f.min, mmask, p.p1, t.row(b), p.row, dmsa, dmsa, dpair, sm);
-    opm_bwd(st, B.opm, S, N, f.min, mmask, nullptr, p.opm, dpair, dmsa, dmsa, sp);
+  if (!msa_side) return;
+  if (!two) {
+    {
+      KTimed kt("block.ct_scale", st);
+      ct_scale(st, dmsa, (long)S * N * L.Cm, sm);
+    }
+    transition_bwd(st, B.mtr, (long)S * N, N, p.m2, nullptr, p.mtr, dmsa, dmsa, sm);
+    msacol_bwd(st, B.col, S, N, p.m1, mmask, nullptr, p.col, dmsa, dmsa, sm);
+    msarow_bwd(st, B.row, S, N, f.min, mmask, p.p1, t.row(b), p.row, dmsa, dmsa, dp_out, sm);
+    opm_bwd(st, B.opm, S, N, f.min, mmask, nullptr, p.opm, dp_out, dmsa, dmsa, sp);
+    return;
+  }
+  stream_wait(st, pipe->ms);  // the pair-bias gradient (and the MSA side so far)
+  msarow_bwd_pair(st, B.row, S, N, p.p1, p.row, dbias, dp_out, sm);
+  pipe->opm = OpmPending{true, &B.opm, f.min, p.opm, dp_out, sp};
+  if (!pipe->defer_opm) {
+    hipStream_t ms = pipe->ms;
+    stream_wait(ms, st);
+    LaneGuard lg(1);
+    issue_opm_bwd(ms, pipe->opm, S, N, mmask, dmsa);
+    pipe->opm.on = false;
+    stream_wait(st, ms);
   }
 }
 
@@ -354,9 +427,18 @@ void stack_fwd(hipStream_t st, const StackW& w, int N, int S, int depth, const f
     BC2N_HIP(hipMemcpyAsync(sv + L.off_pair_in, pair, (size_t)N * N * L.Cz * 4,
                             hipMemcpyDeviceToDevice, st));
   const bool one_region = detached || L.replay;
-  for (int b = 0; b < depth; ++b)
+  auto region = [&](int b) { return sv + (one_region ? 0 : (size_t)b * L.block_bytes); };
+  FwdPipe pipe;
+  pipe.on = !L.tpl && !L.pair_only && msa_overlap();
+  if (pipe.on) pipe.ms = side_stream();
+  for (int b = 0; b < depth; ++b) {
+    pipe.prepped = b > 0;
+    pipe.next_opm = b + 1 < depth ? &w.blocks[b + 1].opm : nullptr;
+    pipe.next_opm_save = b + 1 < depth ? carve(L, region(b + 1)).opm : nullptr;
     block_fwd(st, w.blocks[b], L, b, t, frame(L, sv, b, pair, msa, pair_out, msa_out), pmask,
-              mmask, sv + (one_region ? 0 : (size_t)b * L.block_bytes));
+              mmask, region(b), &pipe);
+  }
+  if (pipe.on) stream_wait(st, pipe.ms);  // the last block's MSA output
 }
 
 void stack_bwd(hipStream_t st, const StackW& w, int N, int S, int depth, const float* pmask,
@@ -369,10 +451,29 @@ void stack_bwd(hipStream_t st, const StackW& w, int N, int S, int depth, const f
   t.L = &L;
   if (dropout) t.base = reinterpret_cast<const float*>(sv + L.off_tbl);
   const long M = (long)N * N;
-  if (dpair != ct_pair)
-    BC2N_HIP(hipMemcpyAsync(dpair, ct_pair, (size_t)M * L.Cz * 4, hipMemcpyDeviceToDevice, st));
+  BwdPipe pipe;
+  pipe.on = !L.tpl && !L.pair_only && msa_overlap();
+  pipe.defer_opm = !L.replay;  // the replay tier's next forward reuses the block region
+  if (pipe.on) pipe.ms = side_stream();
+  // two streams: block b's pair cotangent input dp(b + 1), output dp(b), with
+  // dp(0) = dpair; one stream: dpair throughout
+  const size_t pb = (size_t)M * L.Cz * 4;
+  float* alt = pipe.on ? stack_pair_scratch(pb) : nullptr;
+  auto dp = [&](int k) { return (!pipe.on || k % 2 == 0) ? dpair : alt; };
+  if (dp(depth) != ct_pair)
+    BC2N_HIP(hipMemcpyAsync(dp(depth), ct_pair, pb, hipMemcpyDeviceToDevice, st));
   if (!L.pair_only && dmsa != ct_msa)
     BC2N_HIP(hipMemcpyAsync(dmsa, ct_msa, (size_t)S * N * L.Cm * 4, hipMemcpyDeviceToDevice, st));
+  auto finish = [&] {
+    if (!pipe.on) return;
+    if (pipe.opm.on) {
+      stream_wait(pipe.ms, st);
+      LaneGuard lg(1);
+      issue_opm_bwd(pipe.ms, pipe.opm, S, N, mmask, dmsa);
+      pipe.opm.on = false;
+    }
+    stream_wait(st, pipe.ms);
+  };
   if (L.replay) {
     // each block's forward again from its kept inputs, into the one region,
     // then its backward (the recomputed carries are the same bits)
@@ -388,13 +489,15 @@ void stack_bwd(hipStream_t st, const StackW& w, int N, int S, int depth, const f
                   pmask, mmask, sv);
       }
       Frame f = frame(L, sv, b, b == 0 ? pin0 : nullptr, b == 0 ? min0 : nullptr, nullptr, nullptr);
-      block_bwd(st, w.blocks[b], L, b, t, f, pmask, mmask, sv, dpair, dmsa);
+      block_bwd(st, w.blocks[b], L, b, t, f, pmask, mmask, sv, dp(b + 1), dp(b), dmsa, &pipe);
     }
+    finish();
     return;
   }
   for (int b = depth - 1; b >= 0; --b)
     block_bwd(st, w.blocks[b], L, b, t, frame(L, sv, b, nullptr, nullptr, nullptr, nullptr),
-              pmask, mmask, sv + (size_t)b * L.block_bytes, dpair, dmsa);
+              pmask, mmask, sv + (size_t)b * L.block_bytes, dp(b + 1), dp(b), dmsa, &pipe);
+  finish();
 }
 
 int set_save_policy(int p) {

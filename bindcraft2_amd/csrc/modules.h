@@ -127,6 +127,14 @@ void msarow_fwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa
 void msarow_bwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa_in,
                 const float* msa_mask, const float* pair, const float* tbl, const void* save,
                 const float* dmsa_out, float* dmsa_in, float* dpair, const float* sc = nullptr);
+// msarow_bwd in two halves: everything but the pair term (returns the pair
+// bias gradient [H][N][N], in the calling lane's arena until its next call;
+// sc required), then dpair += the pair LayerNorm's backward of it.
+const float* msarow_bwd_msa(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa_in,
+                            const float* msa_mask, const float* tbl, const void* save,
+                            const float* dmsa_out, float* dmsa_in, const float* sc);
+void msarow_bwd_pair(hipStream_t st, const MsaRowW& w, int S, int N, const float* pair,
+                     const void* save, const float* dbias, float* dpair, const float* sc);
 void msacol_fwd(hipStream_t st, const MsaColW& w, int S, int N, const float* msa_in,
                 const float* msa_mask, const float* tbl, float* msa_out, void* save);
 void msacol_bwd(hipStream_t st, const MsaColW& w, int S, int N, const float* msa_in,
@@ -157,6 +165,13 @@ OpmW opm_weights(WeightStore& ws, const std::string& prefix);
 size_t opm_save_bytes(int S, int N, int O, int C);
 void opm_fwd(hipStream_t st, const OpmW& w, int S, int N, const float* msa, const float* msa_mask,
              const float* pair_in, const float* tbl, float* pair_out, void* save);
+// opm_fwd in two halves: the MSA one (LayerNorm, mask norm, left / right
+// projections into the save-set; reads no pair) and the pair one (the outer
+// product of the saved projections added to the pair).
+void opm_fwd_msa(hipStream_t st, const OpmW& w, int S, int N, const float* msa,
+                 const float* msa_mask, void* save);
+void opm_fwd_pair(hipStream_t st, const OpmW& w, int S, int N, const float* pair_in,
+                  const float* tbl, float* pair_out, void* save);
 // dmsa_in = dmsa_out + J^T(tbl * dpair)
 void opm_bwd(hipStream_t st, const OpmW& w, int S, int N, const float* msa, const float* msa_mask,
              const float* tbl, const void* save, const float* dpair, const float* dmsa_out,

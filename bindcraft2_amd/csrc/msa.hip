@@ -411,12 +411,15 @@ void msarow_fwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa
   out_gemm(st, a, R, og, msa_in, msa_out, tbl, N, "msarow.gemm_out");
 }
 
-void msarow_bwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa_in,
-                const float* msa_mask, const float* pair, const float* tbl, const void* save,
-                const float* dmsa_out, float* dmsa_in, float* dpair, const float* sc) {
-  nonnull(msa_in, "msarow msa"); nonnull(msa_mask, "msarow mask"); nonnull(pair, "msarow pair");
+// Everything of the backward but the pair term: dmsa_in, and the gradient of
+// the pair bias [H][N][N] left in the calling lane's arena (the returned
+// pointer, valid until that arena's next call).  sc must be given.
+const float* msarow_bwd_msa(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa_in,
+                            const float* msa_mask, const float* tbl, const void* save,
+                            const float* dmsa_out, float* dmsa_in, const float* sc) {
+  nonnull(msa_in, "msarow msa"); nonnull(msa_mask, "msarow mask");
   nonnull(save, "msarow save"); nonnull(dmsa_out, "msarow dout"); nonnull(dmsa_in, "msarow din");
-  nonnull(dpair, "msarow dpair");
+  nonnull(sc, "msarow scale");
   const AttnW& a = w.a;
   const int Cm = a.Cin, H = a.H, HD = H * a.D;
   const long R = (long)S * N, M = (long)N * N;
@@ -461,9 +464,36 @@ void msarow_bwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa
   KTimed kt("msarow.ln_bwd", st);
   ln_bwd_f32(st, dxn, msa_in, R, Cm, 0, a.ln_g, sv.mean, sv.rstd, dmsa_in, true, 0, nullptr,
              nullptr, dmsa_out, sc + 1);
-  // pair gradient: only through the bias projection
-  ln_bwd_f32(st, nullptr, pair, M, w.Cz, 0, w.pn_g, sv.pmean, sv.prstd, dpair, true, H, b.dbias,
+  return b.dbias;
+}
+
+// The pair term: dpair += the pair LayerNorm's backward of the bias
+// projection's gradient (the only way the pair enters the row attention).
+void msarow_bwd_pair(hipStream_t st, const MsaRowW& w, int S, int N, const float* pair,
+                     const void* save, const float* dbias, float* dpair, const float* sc) {
+  nonnull(pair, "msarow pair"); nonnull(save, "msarow save"); nonnull(dbias, "msarow dbias");
+  nonnull(dpair, "msarow dpair");
+  const AttnW& a = w.a;
+  const int Cm = a.Cin, H = a.H;
+  const long M = (long)N * N;
+  Carver cv(const_cast<void*>(save));
+  MsaRowSave<Carver> sv(cv, S, N, Cm, H);
+  KTimed kt("msarow.ln_bwd_pair", st);
+  ln_bwd_f32(st, nullptr, pair, M, w.Cz, 0, w.pn_g, sv.pmean, sv.prstd, dpair, true, H, dbias,
              w.w2d, nullptr, sc + 1);
+}
+
+void msarow_bwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa_in,
+                const float* msa_mask, const float* pair, const float* tbl, const void* save,
+                const float* dmsa_out, float* dmsa_in, float* dpair, const float* sc) {
+  nonnull(pair, "msarow pair"); nonnull(dpair, "msarow dpair");
+  nonnull(dmsa_out, "msarow dout");
+  Arena& ar = arena();
+  std::lock_guard<std::recursive_mutex> lk(ar.lock());
+  sc = module_scale(st, sc, dmsa_out, (long)S * N * w.a.Cin);
+  const float* dbias = msarow_bwd_msa(st, w, S, N, msa_in, msa_mask, tbl, save, dmsa_out, dmsa_in,
+                                      sc);
+  msarow_bwd_pair(st, w, S, N, pair, save, dbias, dpair, sc);
 }
 
 void msacol_fwd(hipStream_t st, const MsaColW& w, int S, int N, const float* msa_in,

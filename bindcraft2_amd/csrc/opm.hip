@@ -229,10 +229,12 @@ size_t opm_save_bytes(int S, int N, int O, int C) {
   return s.off;
 }
 
-void opm_fwd(hipStream_t st, const OpmW& w, int S, int N, const float* msa, const float* msa_mask,
-             const float* pair_in, const float* tbl, float* pair_out, void* save) {
-  nonnull(msa, "opm msa"); nonnull(msa_mask, "opm mask"); nonnull(pair_in, "opm pair");
-  nonnull(pair_out, "opm out"); nonnull(save, "opm save");
+// The MSA half of the forward: LayerNorm, the mask norm and the left / right
+// projections, all into the save-set; nothing here reads the pair, so a
+// stack can issue it as soon as the MSA input exists.
+void opm_fwd_msa(hipStream_t st, const OpmW& w, int S, int N, const float* msa,
+                 const float* msa_mask, void* save) {
+  nonnull(msa, "opm msa"); nonnull(msa_mask, "opm mask"); nonnull(save, "opm save");
   const int Cm = w.Cm, O = w.O, C = w.C;
   if ((S * O) % 32 != 0 || N % 32 != 0) throw std::runtime_error("opm: S*O and N must be multiples of 32");
   const long R = (long)S * N;
@@ -260,11 +262,27 @@ void opm_fwd(hipStream_t st, const OpmW& w, int S, int N, const float* msa, cons
   g2.A = right; g2.a_sm = O; g2.a_sk = 1;
   g2.B = w.wt; g2.b_sn = O; g2.b_sk = 1;
   gemm<64, 64>(st, g2, EpiOpmR(sv.rp, S, N, O, C), "opm.gemm_r");
+}
+
+// The pair half: the outer product of the saved projections, normalised,
+// added to the pair.
+void opm_fwd_pair(hipStream_t st, const OpmW& w, int S, int N, const float* pair_in,
+                  const float* tbl, float* pair_out, void* save) {
+  nonnull(pair_in, "opm pair"); nonnull(pair_out, "opm out"); nonnull(save, "opm save");
+  const int O = w.O, C = w.C;
+  Carver cv(save);
+  OpmSave<Carver> sv(cv, S, N, O, C);
   GemmArgs g3;
   g3.M = N; g3.N = N * C; g3.K = S * O;
   g3.A = sv.left_t; g3.a_sm = (long)S * O; g3.a_sk = 1;
   g3.B = sv.rp; g3.b_sn = (long)S * O; g3.b_sk = 1;
   gemm<128, 128>(st, g3, EpiOpmOut(pair_in, pair_out, w.bo, sv.normf, tbl, N, C), "opm.gemm_out");
+}
+
+void opm_fwd(hipStream_t st, const OpmW& w, int S, int N, const float* msa, const float* msa_mask,
+             const float* pair_in, const float* tbl, float* pair_out, void* save) {
+  opm_fwd_msa(st, w, S, N, msa, msa_mask, save);
+  opm_fwd_pair(st, w, S, N, pair_in, tbl, pair_out, save);
 }
 
 void opm_bwd(hipStream_t st, const OpmW& w, int S, int N, const float* msa, const float* msa_mask,

@@ -83,9 +83,10 @@ std::vector<h16> transpose_h16(const float* src, int rows, int cols) {
 void Arena::reset(hipStream_t st, size_t need) {
   off_ = 0;
   if (need <= cap_) return;
+  (void)st;
   if (base_) {
-    // queued kernels may still read the old block
-    BC2N_HIP(hipStreamSynchronize(st));
+    // queued kernels may still read the old block, on either stream
+    BC2N_HIP(hipDeviceSynchronize());
     BC2N_HIP(hipFree(base_));
     base_ = nullptr;
   }
@@ -161,6 +162,24 @@ bool set_msa_overlap(bool on) {
   s.overlap = on;
   return old;
 }
+float* stack_pair_scratch(size_t bytes) {
+  static std::mutex mu;
+  static char* base = nullptr;
+  static size_t cap = 0;
+  std::lock_guard<std::mutex> lk(mu);
+  if (bytes > cap) {
+    if (base) {
+      BC2N_HIP(hipDeviceSynchronize());
+      BC2N_HIP(hipFree(base));
+      base = nullptr;
+      cap = 0;
+    }
+    BC2N_HIP(hipMalloc(reinterpret_cast<void**>(&base), bytes));
+    cap = bytes;
+  }
+  return reinterpret_cast<float*>(base);
+}
+
 bool msa_overlap() {
   SideStream& s = side();
   std::lock_guard<std::mutex> lk(s.mu);

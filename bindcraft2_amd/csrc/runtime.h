@@ -108,6 +108,10 @@ void stream_wait(hipStream_t to, hipStream_t from);
 // default); returns the previous setting.  Off: everything on one stream.
 bool set_msa_overlap(bool on);
 bool msa_overlap();
+// A grow-only device buffer of at least `bytes` (the stacks' second pair
+// cotangent when the two streams alternate them); growing waits for the
+// device first.  Grown by the preallocation calls' dry runs.
+float* stack_pair_scratch(size_t bytes);
 
 // Compute units of the current device (cached per device).
 int device_cus();
