@@ -544,16 +544,22 @@ def _progress(what):
 def profiled(step, steps, skip, only=None):
     """A pass of `steps` steps with the per-kernel event timer on (around the
     launches named `only` alone, if given): {name: (total ms, launches)}; {}
-    when skipped (--no-kprof)."""
+    when skipped (--no-kprof).  The pass runs the stacks on one stream (the
+    MSA overlap off), so every kernel's time is its own, not shared with a
+    kernel of the other stream; the timed steps keep the overlap."""
     if skip:
         return {}
     import bindcraft2_amd as b
+    old = b.lib().bc2n_set_msa_overlap(0)
     b.prof_enable(True, only=only)
-    for i in range(steps):
-        step()
-        _progress(f"profiled step {i}" + (f" ({only})" if only else ""))
-    prof = b.prof_read()
-    b.prof_enable(False)
+    try:
+        for i in range(steps):
+            step()
+            _progress(f"profiled step {i}" + (f" ({only})" if only else ""))
+        prof = b.prof_read()
+    finally:
+        b.prof_enable(False)
+        b.lib().bc2n_set_msa_overlap(old)
     return prof
 
 

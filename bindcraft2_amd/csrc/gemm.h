@@ -448,9 +448,11 @@ struct EpiPartial : EpiRows {
   }
 };
 
+// The split-K partials: one arena per work lane (two streams may each run a
+// split product at once).
 inline Arena& gemm_splitk_scratch() {
-  static Arena a;
-  return a;
+  static Arena a[NUM_LANES];
+  return a[lane()];
 }
 
 template <class Epi>
