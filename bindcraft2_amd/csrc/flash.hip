@@ -261,13 +261,13 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
     // the chunk's pair bias: the score MFMAs' accumulators
     f32x4 sv[NBC][2];
 #pragma unroll
-    for (int kb = 0; kb < NBC; ++kb)
+    for (int kb = 0; kb < NBC; ++kb) {
+      const h16x8 bb = ld8(bias_frag_block(a.bias, h, qt, (k0 >> 5) + kb, N, lane));
 #pragma unroll
-      for (int kh = 0; kh < 2; ++kh) {
-        const float4 bb =
-            *reinterpret_cast<const float4*>(bias_frag_block(a.bias, h, qt, (k0 >> 5) + kb, N, lane) + kh * 4);
-        sv[kb][kh][0] = bb.x; sv[kb][kh][1] = bb.y; sv[kb][kh][2] = bb.z; sv[kb][kh][3] = bb.w;
-      }
+      for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sv[kb][kh][i] = (float)bb[kh * 4 + i];
+    }
     __syncthreads();  // the previous chunk's LDS readers are done
     nkv.store(Ks, Vs, tid, NBC * 32);
     __syncthreads();
@@ -395,16 +395,11 @@ __global__ __launch_bounds__(256) void attn_fwd_rows_kernel(AttnArgs a, int rpc)
   float bsv[NKB][8];
   {
 #pragma unroll
-    for (int kb = 0; kb < NKB; ++kb)
+    for (int kb = 0; kb < NKB; ++kb) {
+      const h16x8 bb = ld8(bias_frag_block(a.bias, h, q >> 4, kb, N, lane));
 #pragma unroll
-      for (int kh = 0; kh < 2; ++kh) {
-        const float4 bb =
-            *reinterpret_cast<const float4*>(bias_frag_block(a.bias, h, q >> 4, kb, N, lane) + kh * 4);
-        bsv[kb][kh * 4 + 0] = bb.x;
-        bsv[kb][kh * 4 + 1] = bb.y;
-        bsv[kb][kh * 4 + 2] = bb.z;
-        bsv[kb][kh * 4 + 3] = bb.w;
-      }
+      for (int e = 0; e < 8; ++e) bsv[kb][e] = (float)bb[e];
+    }
     // Make the bias resident here: the row loop then never waits on these
     // loads (the wait counter retires in order, so a first use inside the
     // loop would also wait for the prefetch issued before it).
@@ -620,15 +615,9 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs b) {
 #pragma unroll
     for (int kb = 0; kb < CB; ++kb) {
       if (c * CB + kb < NKB) {
+        const h16x8 bb = ld8(bias_frag_block(a.bias, h, q >> 4, (k0c >> 5) + kb, N, lane));
 #pragma unroll
-        for (int kh = 0; kh < 2; ++kh) {
-          const float4 bb = *reinterpret_cast<const float4*>(
-              bias_frag_block(a.bias, h, q >> 4, (k0c >> 5) + kb, N, lane) + kh * 4);
-          bsv[kb][kh * 4 + 0] = bb.x - lse;
-          bsv[kb][kh * 4 + 1] = bb.y - lse;
-          bsv[kb][kh * 4 + 2] = bb.z - lse;
-          bsv[kb][kh * 4 + 3] = bb.w - lse;
-        }
+        for (int e = 0; e < 8; ++e) bsv[kb][e] = (float)bb[e] - lse;
       }
     }
     if (c > 0) {
@@ -729,16 +718,11 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_rows_kernel(AttnBwdArgs b, in
   float bsv[NKB][8];
   {
 #pragma unroll
-    for (int kb = 0; kb < NKB; ++kb)
+    for (int kb = 0; kb < NKB; ++kb) {
+      const h16x8 bb = ld8(bias_frag_block(a.bias, h, q >> 4, kb, N, lane));
 #pragma unroll
-      for (int kh = 0; kh < 2; ++kh) {
-        const float4 bb =
-            *reinterpret_cast<const float4*>(bias_frag_block(a.bias, h, q >> 4, kb, N, lane) + kh * 4);
-        bsv[kb][kh * 4 + 0] = bb.x;
-        bsv[kb][kh * 4 + 1] = bb.y;
-        bsv[kb][kh * 4 + 2] = bb.z;
-        bsv[kb][kh * 4 + 3] = bb.w;
-      }
+      for (int e = 0; e < 8; ++e) bsv[kb][e] = (float)bb[e];
+    }
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
@@ -909,7 +893,7 @@ __global__ __launch_bounds__(64 * W) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
     if (have) {
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        bsl[ib][e] = a.bias[bias_frag_index(h, qb + (e / 4) * 16 + 4 * g + (e % 4), k, N)];
+        bsl[ib][e] = (float)a.bias[bias_frag_index(h, qb + (e / 4) * 16 + 4 * g + (e % 4), k, N)];
     }
   }
   const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
@@ -1193,7 +1177,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkv_lds_kernel(AttnBwdArgs b)
     const int qb = blk_q0(ib);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      bsl[ib][e] = a.bias[bias_frag_index(h, qb + (e / 4) * 16 + 4 * g + (e % 4), k, N)];
+      bsl[ib][e] = (float)a.bias[bias_frag_index(h, qb + (e / 4) * 16 + 4 * g + (e % 4), k, N)];
       dbias[ib][e] = 0.f;
     }
   }

@@ -12,15 +12,17 @@ namespace bc2n {
 // 32-key block k/32), at lane ((k%16)/4)*16 + q%16, element ((k%32)/16)*4 +
 // k%4 -- the 8 floats one lane of a score MFMA's accumulator takes for the
 // block, so a wave reads a block as two contiguous 1 KB vectors (in [h][q][k]
-// order every 16-byte lane read was a separate cache line).
+// order every 16-byte lane read was a separate cache line).  Stored as
+// binary16 (the reference's flash kernels take an f16 bias as well): a lane
+// reads its 8 values of a block as one 16-byte vector.
 __host__ __device__ __forceinline__ long bias_frag_index(int h, int q, int k, int N) {
   const int lane = ((k & 15) >> 2) * 16 + (q & 15);
   const int e = ((k & 31) >> 4) * 4 + (k & 3);
   return ((((long)h * (N >> 4) + (q >> 4)) * (N >> 5) + (k >> 5)) << 9) + lane * 8 + e;
 }
-// The 8 floats of lane `lane` for (head h, query tile qt, key block kb).
-__host__ __device__ __forceinline__ const float* bias_frag_block(const float* bias, int h, int qt,
-                                                                 int kb, int N, int lane) {
+// The 8 values of lane `lane` for (head h, query tile qt, key block kb).
+__host__ __device__ __forceinline__ const h16* bias_frag_block(const h16* bias, int h, int qt,
+                                                               int kb, int N, int lane) {
   return bias + ((((long)h * (N >> 4) + qt) * (N >> 5) + kb) << 9) + lane * 8;
 }
 
@@ -30,7 +32,7 @@ __host__ __device__ __forceinline__ const float* bias_frag_block(const float* bi
 // bias_out[bias_frag_index(h, q, k, N)].
 void ln_fwd_f32(hipStream_t st, const float* x, long M, int C, int nt,
                 const float* gamma, const float* beta, h16* y, float* mean,
-                float* rstd, bool fast, int H, const float* wb, float* bias_out,
+                float* rstd, bool fast, int H, const float* wb, h16* bias_out,
                 float bias_scale = 1.f);
 // dx[src(m)] (+)= LN-backward(gs * (dy[m] + sum_h dbias[h*M+m] * wb[c*H+h])).
 // acc: dx = res + LN'(...) with res = dres, or dx itself when dres is null.
@@ -62,7 +64,7 @@ struct AttnArgs {
   long ld = 0;
   const float* mask = nullptr;  // mask[r*mask_sr + k*mask_sk], binary 0/1
   long mask_sr = 0, mask_sk = 0;
-  const float* bias = nullptr;  // [H][N][N], log2 domain, or null
+  const h16* bias = nullptr;  // [H][N][N] binary16, log2 domain, score-fragment order, or null
   h16* o = nullptr;            // ungated output [R*N][H*D]
   h16* og = nullptr;           // sigmoid(g) * o   [R*N][H*D]
   long ldo = 0;

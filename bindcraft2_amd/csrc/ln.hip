@@ -62,7 +62,7 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(
     const InT* __restrict__ x, long M, int nt, const float* __restrict__ gamma,
     const float* __restrict__ beta, h16* __restrict__ y,
     float* __restrict__ mean_out, float* __restrict__ rstd_out,
-    const float* __restrict__ wb, float* __restrict__ bias_out, float bias_scale, int bn) {
+    const float* __restrict__ wb, h16* __restrict__ bias_out, float bias_scale, int bn) {
   using G = LnGeom<C>;
   const int t = threadIdx.x;
   const long mb = (long)blockIdx.x * (U * G::RPB) + t / G::TPR;
@@ -123,7 +123,7 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(
         p = group_sum<G::TPR>(p);
         if (gl == h) mine = p;
       }
-      if (gl < H) bias_out[bias_frag_index(gl, (int)(m / bn), (int)(m % bn), bn)] = mine * bias_scale;
+      if (gl < H) bias_out[bias_frag_index(gl, (int)(m / bn), (int)(m % bn), bn)] = (h16)(mine * bias_scale);
     }
   }
 }
@@ -361,7 +361,7 @@ constexpr int ln_rows() { return H > 0 ? 4 : 1; }
 template <int C, int H>
 static void ln_fwd_launch(hipStream_t st, const float* x, long M, int nt, const float* gamma,
                           const float* beta, h16* y, float* mean, float* rstd, bool fast,
-                          const float* wb, float* bias_out, float bs, int bn) {
+                          const float* wb, h16* bias_out, float bs, int bn) {
   constexpr int U = ln_rows<H>();
   const int grid = (int)((M + U * LnGeom<C>::RPB - 1) / (U * LnGeom<C>::RPB));
   if (fast)
@@ -375,7 +375,7 @@ static void ln_fwd_launch(hipStream_t st, const float* x, long M, int nt, const 
 template <int C>
 static void ln_fwd_dispatch(hipStream_t st, const float* x, long M, int nt, const float* gamma,
                             const float* beta, h16* y, float* mean, float* rstd, bool fast, int H,
-                            const float* wb, float* bias_out, float bs, int bn) {
+                            const float* wb, h16* bias_out, float bs, int bn) {
   switch (H) {
     case 0: ln_fwd_launch<C, 0>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, wb, bias_out, bs, bn); break;
     case 4: ln_fwd_launch<C, 4>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, wb, bias_out, bs, bn); break;
@@ -386,7 +386,7 @@ static void ln_fwd_dispatch(hipStream_t st, const float* x, long M, int nt, cons
 
 void ln_fwd_f32(hipStream_t st, const float* x, long M, int C, int nt,
                 const float* gamma, const float* beta, h16* y, float* mean,
-                float* rstd, bool fast, int H, const float* wb, float* bias_out,
+                float* rstd, bool fast, int H, const float* wb, h16* bias_out,
                 float bs) {
   int bn = 0;  // side of the N x N grid of the pair bias
   if (H > 0) {

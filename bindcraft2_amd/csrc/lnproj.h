@@ -22,7 +22,8 @@ struct Args {
   const float *g, *b, *wb;  // LayerNorm scale, offset; bias weights [C][H]
   float bscale;
   h16* xn;
-  float *mean, *rstd, *bias;
+  float *mean, *rstd;
+  h16* bias;  // [H][M] binary16 in score-fragment order
   const h16* W;  // [nout][C] in b_frags_k128 order
 };
 
@@ -119,7 +120,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
           a.rstd[m] = rs;
         }
         if (H > 0 && l16 < H)
-          a.bias[bias_frag_index(l16, (int)(m / a.bn), (int)(m % a.bn), a.bn)] = mine * a.bscale;
+          a.bias[bias_frag_index(l16, (int)(m / a.bn), (int)(m % a.bn), a.bn)] = (h16)(mine * a.bscale);
       } else {
         ob = h16x8{};
       }

@@ -268,7 +268,8 @@ __global__ __launch_bounds__(64) void small_attn_bwd_kernel(
 
 template <class A>
 struct MsaRowSave {
-  float *mean, *rstd, *pmean, *prstd, *bias, *lse;
+  float *mean, *rstd, *pmean, *prstd, *lse;
+  h16* bias;
   h16 *qkvg, *o;
   MsaRowSave(A& a, int S, int N, int Cm, int H) {
     const size_t R = (size_t)S * N, M = (size_t)N * N;
@@ -276,7 +277,7 @@ struct MsaRowSave {
     rstd = a.template take<float>(R);
     pmean = a.template take<float>(M);
     prstd = a.template take<float>(M);
-    bias = a.template take<float>((size_t)H * M);
+    bias = a.template take<h16>((size_t)H * M);
     lse = a.template take<float>((size_t)S * H * N);
     qkvg = a.template take<h16>(R * 4 * Cm);
     o = a.template take<h16>(R * Cm);

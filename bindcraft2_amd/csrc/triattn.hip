@@ -28,13 +28,14 @@ namespace {
 
 template <class A>
 struct TriAttnSave {
-  float *mean, *rstd, *bias, *lse;
+  float *mean, *rstd, *lse;
+  h16* bias;
   h16 *qkvg, *o;
   TriAttnSave(A& a, int N, int C, int H) {
     const size_t M = (size_t)N * N;
     mean = a.template take<float>(M);
     rstd = a.template take<float>(M);
-    bias = a.template take<float>((size_t)H * M);
+    bias = a.template take<h16>((size_t)H * M);
     lse = a.template take<float>((size_t)H * M);
     qkvg = a.template take<h16>(M * 4 * C);
     o = a.template take<h16>(M * C);
