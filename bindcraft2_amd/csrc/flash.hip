@@ -120,10 +120,10 @@ struct RowPair {
   }
 };
 
-template <int D, int N>
+template <int D, int N, int T = 256>
 __device__ __forceinline__ void stage_rows2(h16* dA, const h16* sA, long lda, h16* dB,
                                             const h16* sB, long ldb, int tid, int rows = N) {
-  RowPair<D, N> p;
+  RowPair<D, N, T> p;
   p.load(sA, lda, sB, ldb, tid, rows);
   p.store(dA, dB, tid, rows);
 }
@@ -200,8 +200,8 @@ __device__ __forceinline__ RowHeadQb row_tile_order(int bid, int R, int H, int n
 // more MFMA per block with an all-ones operand), summed over the same h16
 // probabilities the numerator uses.  Online softmax across chunks: the
 // output accumulator and the row sum are rescaled once per chunk.
-template <int D, int NKB>
-__global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
+template <int D, int NKB, int QW>
+__global__ __launch_bounds__(64 * QW) void attn_fwd_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   constexpr int DT = D / 16;
   constexpr int LD = lds_ld<D>();
@@ -215,8 +215,9 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   h16* Vs = Ks + CN * LD;                               // [CN][LD]
   float* Mm = reinterpret_cast<float*>(Vs + CN * LD);    // [N] 1 / 0 per key
   float* Ma = Mm + N;                                    // [N] 0 / NEG_LOGIT
+  constexpr int T = 64 * QW;   // threads; QW waves of 16 queries
 
-  const int nqb = (N + 63) / 64;
+  const int nqb = (N + 16 * QW - 1) / (16 * QW);
   const long G = (long)a.R * H * nqb;
   const int bid = (int)xcd_block(G);
   if (bid >= G) return;
@@ -227,15 +228,15 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   const long tok0 = (long)r * N;
   const h16* Kg = a.qkvg + tok0 * a.ld + H * D + h * D;
   const h16* Vg = a.qkvg + tok0 * a.ld + 2 * H * D + h * D;
-  RowPair<D, CN> nkv;  // the next chunk's K and V rows
+  RowPair<D, CN, T> nkv;  // the next chunk's K and V rows
   nkv.load(Kg, a.ld, Vg, a.ld, tid, min(CN, N));
-  for (int k = tid; k < N; k += 256) {
+  for (int k = tid; k < N; k += T) {
     const bool on = a.mask[r * a.mask_sr + k * a.mask_sk] != 0.f;
     Mm[k] = on ? 1.f : 0.f;
     Ma[k] = on ? 0.f : NEG_LOGIT;
   }
 
-  const int q0 = qb * 64 + wave * 16;
+  const int q0 = qb * 16 * QW + wave * 16;
   const bool active = q0 < N;  // idle waves keep to the barriers only
   const int lq = lane & 15, g = lane >> 4;
   const int q = min(q0, N - 16) + lq;  // idle waves read in bounds, store nothing
@@ -563,8 +564,8 @@ __global__ __launch_bounds__(256) void attn_gate_bwd_kernel(AttnBwdArgs b) {
 // in chunks of up to 256 staged in LDS.  Per chunk the lane's pair-bias row
 // (minus lse, with -inf at masked keys so p = dS = 0 there) is fetched up
 // front, all loads in flight at once.
-template <int D, int NKB>
-__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs b) {
+template <int D, int NKB, int QW>
+__global__ __launch_bounds__(64 * QW) void attn_bwd_dq_kernel(AttnBwdArgs b) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   constexpr int DT = D / 16;
   constexpr int LD = lds_ld<D>();
@@ -577,8 +578,9 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs b) {
   h16* Ks = reinterpret_cast<h16*>(smem_raw);   // [CN][LD]
   h16* Vs = Ks + CN * LD;                        // [CN][LD]
   float* Ms = reinterpret_cast<float*>(Vs + CN * LD);  // [N]
+  constexpr int T = 64 * QW;   // threads; QW waves of 16 queries
 
-  const int nqb = (N + 63) / 64;
+  const int nqb = (N + 16 * QW - 1) / (16 * QW);
   const long G = (long)a.R * H * nqb;
   const int bid = (int)xcd_block(G);
   if (bid >= G) return;
@@ -589,12 +591,12 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs b) {
   const long tok0 = (long)r * N;
   const h16* Kg = a.qkvg + tok0 * a.ld + H * D + h * D;
   const h16* Vg = a.qkvg + tok0 * a.ld + 2 * H * D + h * D;
-  stage_rows2<D, CN>(Ks, Kg, a.ld, Vs, Vg, a.ld, tid);
+  stage_rows2<D, CN, T>(Ks, Kg, a.ld, Vs, Vg, a.ld, tid);
   // additive key mask: a masked key's exponent becomes -inf, so p = dS = 0
-  for (int k = tid; k < N; k += 256)
+  for (int k = tid; k < N; k += T)
     Ms[k] = a.mask[r * a.mask_sr + k * a.mask_sk] != 0.f ? 0.f : -INFINITY;
 
-  const int q0 = qb * 64 + wave * 16;
+  const int q0 = qb * 16 * QW + wave * 16;
   const int lq = lane & 15, g = lane >> 4;
   const int q = min(q0, N - 16) + lq;  // idle waves read in bounds, store nothing
   HFrag<D> qf, dof;
@@ -622,8 +624,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs b) {
     }
     if (c > 0) {
       __syncthreads();  // every wave is done with the previous chunk
-      stage_rows2<D, CN>(Ks, Kg + (long)k0c * a.ld, a.ld, Vs, Vg + (long)k0c * a.ld, a.ld, tid,
-                         min(CN, N - k0c));
+      stage_rows2<D, CN, T>(Ks, Kg + (long)k0c * a.ld, a.ld, Vs, Vg + (long)k0c * a.ld, a.ld, tid,
+                            min(CN, N - k0c));
     }
     __syncthreads();
     if (NCH == 1 && q0 >= N) return;  // idle wave, no barrier follows
@@ -1536,11 +1538,15 @@ static void attn_fwd_t(hipStream_t st, const AttnArgs& a) {
     return;
   }
   if (!a.bias) throw std::runtime_error("attention: the chunked forward needs the pair bias");
-  // one 128-key K/V buffer + the row's key mask (two floats a key)
+  // one 128-key K/V buffer + the row's key mask (two floats a key); eight
+  // waves (128 queries) a workgroup, so each row's K/V is read by N / 128
+  // workgroups
+  constexpr int QW = 8;
   const size_t lds = (size_t)128 * lds_ld<D>() * 2 * 2 + (size_t)a.N * 8;
-  const dim3 grid(xcd_grid((long)a.R * a.H * nqb));
+  const dim3 grid(xcd_grid((long)a.R * a.H * ((a.N + 16 * QW - 1) / (16 * QW))));
   with_blocks(a.N / 32, [&](auto nb) {
-    hipLaunchKernelGGL((attn_fwd_kernel<D, decltype(nb)::value>), grid, dim3(256), lds, st, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<D, decltype(nb)::value, QW>), grid, dim3(64 * QW), lds, st,
+                       a);
   });
 }
 
@@ -1583,9 +1589,11 @@ static void attn_bwd_t(hipStream_t st, const AttnBwdArgs& b0) {
     if (!a.bias) throw std::runtime_error("attention: the chunked dQ needs the pair bias");
     const size_t lds_q = (size_t)attn_chunk(a.N) * lds_ld<D>() * 2 * 2 + (size_t)a.N * 4;
     KTimed kt(timer_name(2, a), st);
-    const dim3 grid(xcd_grid((long)a.R * a.H * nqb));
+    constexpr int QW = 8;  // 128 queries a workgroup, as the forward
+    const dim3 grid(xcd_grid((long)a.R * a.H * ((a.N + 16 * QW - 1) / (16 * QW))));
     with_blocks(a.N / 32, [&](auto nb) {
-      hipLaunchKernelGGL((attn_bwd_dq_kernel<D, decltype(nb)::value>), grid, dim3(256), lds_q, st, b);
+      hipLaunchKernelGGL((attn_bwd_dq_kernel<D, decltype(nb)::value, QW>), grid, dim3(64 * QW),
+                         lds_q, st, b);
     });
   }
   const int nch = attn_bwd_nchunk(a.R, b.rows_per_chunk);
