@@ -205,12 +205,15 @@ size_t bc2n_evoformer_detached_bytes(const char* weights_dir, int N, int S,
  * Returns the previous policy, or -1 for a bad value. */
 int bc2n_set_save_policy(int policy);
 /* Process-wide: whether the Evoformer stacks run the MSA side of each block
- * (row and column attention and the MSA transition forward; the transition
- * and column attention backward) on a library-owned second stream beside
- * the pair track, joined at the block's end (1, the default), or everything
- * on the caller's stream (0).  Results are bit-identical either way.  No
- * reference counterpart (the reference's trunk is single-stream).  Returns
- * the previous setting. */
+ * (forward: row and column attention, the MSA transition and the next
+ * block's outer-product-mean MSA half; backward: the transition, column
+ * attention, row attention up to its bias gradient and the outer product
+ * mean) on a library-owned second stream (non-blocking, default priority)
+ * beside the pair track, ordered by events and joined back to the caller's
+ * stream before the call returns (1, the default), or everything on the
+ * caller's stream (0).  Results are bit-identical either way.  No reference
+ * counterpart (the reference's trunk is single-stream).  Returns the
+ * previous setting. */
 int bc2n_set_msa_overlap(int on);
 /* 1 if a stack of these shapes keeps the replay tier under the policy, 0 if
  * the full save-set, -1 on error. */
