@@ -980,43 +980,79 @@ __global__ __launch_bounds__(64 * W) void attn_bwd_dkv_kernel(AttnBwdArgs b) {
     }
     if (s + 1 < nst) prefetch(s + 1);
 
+    // One unit = this wave's 16 keys against one 32-query block.  Its LDS
+    // operands (row reads, -lse, -Dsum and the transposed reads) are read in
+    // one batch; with PF the next unit's batch of the same stage is issued
+    // right after this unit's S / dP products, so the reads are in flight
+    // during the exponentials and the dV / dK products.  Without PF each
+    // batch is read at its unit: five or six units a wave (N = 544..768),
+    // whose bias registers leave no room, and the four-wave D = 32 shapes
+    // (N <= 256 without a pair bias), whose next-row registers hold a whole
+    // row's Q and dO.
+    constexpr bool PF = NB <= 4 && (D == 16 || W == 8);
+    struct Ops {
+      HFrag<D> q[2], o[2];
+      h16x8 to[DT], tq[DT];
+      float4 l[2], d[2];
+    };
+    auto load_ops = [&](int ib, Ops& x) __attribute__((always_inline)) {
+      const int qb = (ib * QS + qs) * 32, ql = qb - c * CN;
+#pragma unroll
+      for (int qh = 0; qh < 2; ++qh) {
+        x.q[qh].load(&Qs[(ql + qh * 16 + lk) * LD], g);
+        x.o[qh].load(&Os[(ql + qh * 16 + lk) * LD], g);
+        x.l[qh] = *reinterpret_cast<const float4*>(Ls + qb + qh * 16 + 4 * g);
+        x.d[qh] = *reinterpret_cast<const float4*>(Ds + qb + qh * 16 + 4 * g);
+      }
+#pragma unroll
+      for (int dh = 0; dh < DT; ++dh) {
+        x.to[dh] = ld_tr8(Os, LD, ql, dh * 16, lane);
+        x.tq[dh] = ld_tr8(Qs, LD, ql, dh * 16, lane);
+      }
+    };
+    // this stage's units: ib = ib0 .. (blocks of chunk c; all blocks with one chunk)
+    const int ib0 = NCH > 1 ? c * (CQB / QS) : 0;
+    Ops cur, nxt;
+    if (PF && ib0 < NB && ib0 * QS + qs < NQB) load_ops(ib0, cur);
 #pragma unroll
     for (int ib = 0; ib < NB; ++ib) {
       if (NCH > 1 && ib * QS / CQB != c) continue;  // block of another chunk
       const int blk = ib * QS + qs;
       if (blk < NQB) {
-        const int qb = blk * 32;         // query index
-        const int ql = qb - c * CN;      // row in the staged chunk
+        if constexpr (!PF) load_ops(ib, cur);
         h16x8 pf, dsf;
+        f32x4 s4[2], dp[2];
 #pragma unroll
         for (int qh = 0; qh < 2; ++qh) {
-          HFrag<D> qa, da;
-          qa.load(&Qs[(ql + qh * 16 + lk) * LD], g);
-          da.load(&Os[(ql + qh * 16 + lk) * LD], g);
-          const float4 lv = *reinterpret_cast<const float4*>(Ls + qb + qh * 16 + 4 * g);
-          const float4 dv = *reinterpret_cast<const float4*>(Ds + qb + qh * 16 + 4 * g);
           f32x4 cs, cd;
-          cs[0] = bsl[ib][qh * 4 + 0] + lv.x;
-          cs[1] = bsl[ib][qh * 4 + 1] + lv.y;
-          cs[2] = bsl[ib][qh * 4 + 2] + lv.z;
-          cs[3] = bsl[ib][qh * 4 + 3] + lv.w;
-          cd[0] = dv.x; cd[1] = dv.y; cd[2] = dv.z; cd[3] = dv.w;
-          const f32x4 s4 = HFrag<D>::mma(qa, kf, cs);  // S + bias - lse
-          const f32x4 dp = HFrag<D>::mma(da, vf, cd);  // dP - Dsum
+          cs[0] = bsl[ib][qh * 4 + 0] + cur.l[qh].x;
+          cs[1] = bsl[ib][qh * 4 + 1] + cur.l[qh].y;
+          cs[2] = bsl[ib][qh * 4 + 2] + cur.l[qh].z;
+          cs[3] = bsl[ib][qh * 4 + 3] + cur.l[qh].w;
+          cd[0] = cur.d[qh].x; cd[1] = cur.d[qh].y; cd[2] = cur.d[qh].z; cd[3] = cur.d[qh].w;
+          s4[qh] = HFrag<D>::mma(cur.q[qh], kf, cs);  // S + bias - lse
+          dp[qh] = HFrag<D>::mma(cur.o[qh], vf, cd);  // dP - Dsum
+        }
+        // the next unit of this stage (wave-uniform)
+        const bool more = PF && ib + 1 < NB && (NCH == 1 || (ib + 1) * QS / CQB == c) &&
+                          (ib + 1) * QS + qs < NQB;
+        if (more) load_ops(ib + 1, nxt);
+#pragma unroll
+        for (int qh = 0; qh < 2; ++qh)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float p = fast_exp2(mk ? s4[i] : xm);
-            const float ds = mk ? p * dp[i] : 0.f;
+            const float p = fast_exp2(mk ? s4[qh][i] : xm);
+            const float ds = mk ? p * dp[qh][i] : 0.f;
             pf[qh * 4 + i] = (h16)p;
             dsf[qh * 4 + i] = (h16)ds;
             dbias[ib][qh * 4 + i] += ds;
           }
-        }
 #pragma unroll
         for (int dh = 0; dh < DT; ++dh) {
-          accV[dh] = mfma16x16x32(ld_tr8(Os, LD, ql, dh * 16, lane), pf, accV[dh]);
-          accK[dh] = mfma16x16x32(ld_tr8(Qs, LD, ql, dh * 16, lane), dsf, accK[dh]);
+          accV[dh] = mfma16x16x32(cur.to[dh], pf, accV[dh]);
+          accK[dh] = mfma16x16x32(cur.tq[dh], dsf, accK[dh]);
         }
+        if (more) cur = nxt;
       }
     }
     if (c != NCH - 1) continue;
