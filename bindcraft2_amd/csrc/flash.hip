@@ -1456,6 +1456,350 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkv_lds_kernel(AttnBwdArgs b)
   }
 }
 
+// dK/dV/dBias for D = 32 and 256 < N <= 512 with direct global -> LDS
+// copies, as attn_bwd_dkv_lds_kernel, reorganised around the copy volume:
+// every workgroup re-stages each row's Q and dO for its own keys, so at
+// L = 512 the staging moved 2.4 GB from L2 a launch and cost about as much
+// as the products (531 us with it, 363 us with it taken out).  Here a
+// workgroup owns 64 keys (eight waves: four 16-key tiles x two query
+// groups, one workgroup a CU), which halves that volume, and the pair bias
+// it keeps in registers for all its rows is binary16 as stored (the bias
+// gradient sums stay f32).
+//
+//  * A stage is one 256-query chunk of a row: the chunk's Q and dO tiles,
+//    the workgroup's K and V tiles, the chunk's lse and -Dsum and the row's
+//    key mask, copied into one of three LDS buffers two stages ahead of its
+//    use.  Tiles are 64-byte h16 rows with the 16-byte chunk c of row t
+//    stored at chunk c ^ ((t >> 1) & 3).
+//  * Every wave issues the same NCOPY copies every stage (spare statistic
+//    slots repeat the wave's own copy: the same bytes to the same place), and
+//    only query group 0 stores (four dK/dV stores at a row's end), so the
+//    wait that opens a stage retires exactly that stage's copies, leaving the
+//    next stage's copies and, in query group 0, the previous row's four
+//    stores in flight.
+//  * Queries and keys past N are read at clamped, in-bounds addresses (a key
+//    tile wholly past N computes nothing and writes nothing); what they
+//    stage is never read.
+template <int NQB>
+__global__ __launch_bounds__(512) void attn_bwd_dkv_lds8_kernel(AttnBwdArgs b) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
+  constexpr int D = 32, DT = 2;
+  constexpr int N = 32 * NQB;             // == a.N (dispatch)
+  static_assert(NQB > 8 && NQB <= 16, "256 < N <= 512");
+  constexpr int QS = 2, KT = 4, W = 8;    // query groups x 16-key tiles
+  constexpr int CQ = 256, NCH = 2;        // queries a stage, stages a row
+  constexpr int UPS = CQ / 32 / QS;       // units a wave a stage (4)
+  constexpr int NB = UPS * NCH;           // units a wave a row (8)
+  constexpr int TILE = CQ * 64;           // bytes of a [CQ][32] h16 tile
+  constexpr int KVT = 16 * KT * 64;       // bytes of the K (or V) tile
+  constexpr int JSM = (N + 63) / 64;      // 64-key groups of the mask
+  constexpr int SOFF = 2 * TILE + 2 * KVT;
+  constexpr int BUF = SOFF + 2 * CQ * 4 + JSM * 64 * 4;  // + lse, -Dsum, mask
+  constexpr int NT = 2 * (CQ / 16) + 2 * KT;  // 1 KB tile copies a stage
+  static_assert(NT % W == 0, "tile copies: the same count a wave");
+  constexpr int NCT = NT / W;                  // a wave's (5)
+  constexpr int TS = 2 * (CQ / 64) + JSM;      // 256-byte statistic copies a stage
+  static_assert(TS > W && TS <= 2 * W, "two statistic copies a wave");
+  constexpr int NCOPY = NCT + 2;
+  static_assert(NCOPY + 4 < 16, "vmcnt immediate");
+  const AttnArgs& a = b.f;
+  const int H = a.H;
+  float* Xs = reinterpret_cast<float*>(smem_raw + 3 * BUF);  // [KT][K,V][DT*4][64], query group 1
+
+  constexpr int NKW = (N + 16 * KT - 1) / (16 * KT);
+  const long G = (long)((a.R + b.rows_per_chunk - 1) / b.rows_per_chunk) * H * NKW;
+  const int bid = (int)xcd_block(G);
+  if (bid >= G) return;
+  const int kw = bid % NKW;
+  const int h = (bid / NKW) % H;
+  const int ch = bid / (NKW * H);
+  const int r0 = ch * b.rows_per_chunk;
+  const int r1 = min(a.R, r0 + b.rows_per_chunk);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kt_ = wave % KT, qs = wave / KT;
+  const int lk = lane & 15, g = lane >> 4;
+  const int klocal = kt_ * 16 + lk;
+  const bool kon = kw * 16 * KT + kt_ * 16 < N;  // the wave's key tile exists (wave-uniform)
+  const int k = min(kw * 16 * KT + klocal, N - 1);
+  const bool stores = qs == 0 && kon;  // writes dK, dV at each row's end
+  const long HD = (long)H * D;
+  const unsigned lds0 = lds_addr(smem_raw);
+
+  // unit ib = UPS c + i of this wave: 32-query block 8 c + qs + QS i (rows
+  // ql = 32 (qs + QS i) of chunk c's tiles); the bias column k at its
+  // queries (binary16), the bias-gradient sums (f32)
+  h16x8 bsh[NB];
+  float dbias[NB][8];
+#pragma unroll
+  for (int ib = 0; ib < NB; ++ib) {
+    const int blk = min(8 * (ib / UPS) + qs + QS * (ib % UPS), NQB - 1);  // past N: never used
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      bsh[ib][e] = a.bias[bias_frag_index(h, blk * 32 + (e / 4) * 16 + 4 * g + (e % 4), k, N)];
+      dbias[ib][e] = 0.f;
+    }
+  }
+  // all in flight together, then resident before the first copy is issued:
+  // a first use inside the row loop would wait for every copy in flight
+  // (vmcnt retires in order)
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int ib = 0; ib < NB; ++ib) asm volatile("" ::"v"(bsh[ib]));
+
+  // Tile copy j (1 KB): rows 16 jr .. 16 jr + 15 of tile Q (j < 16), dO
+  // (j < 32), K, V.  Lane i writes physical chunk i & 3 of row 16 jr + i / 4
+  // from the logical chunk the swizzle puts there.  Wave w issues copies
+  // w + 8 i.
+  // (the per-lane offsets are recomputed at each stage: kept, they would
+  // take registers the bias-gradient sums need)
+  auto tile_voff = [&](int i, int c, int lane) __attribute__((always_inline)) -> unsigned {
+    const int j = wave + W * i;
+    const int tile = j < CQ / 8 ? j / (CQ / 16) : 2 + (j - CQ / 8) / KT;  // Q, dO, K, V
+    const int jr = j < CQ / 8 ? j % (CQ / 16) : (j - CQ / 8) % KT;
+    const int row = jr * 16 + (lane >> 2);
+    const int c8 = ((lane & 3) ^ ((row >> 1) & 3)) * 8;
+    const int ld = tile == 1 ? a.ldo : a.ld;
+    // a query of chunk c, or a key of the workgroup's tile
+    const int tok = tile < 2 ? min(c * CQ + row, N - 1) : min(kw * 16 * KT + row, N - 1);
+    return (unsigned)((tok * ld + c8) * 2);
+  };
+  unsigned sdst[NCT];
+  long soff[NCT];
+  bool sdo[NCT];
+#pragma unroll
+  for (int i = 0; i < NCT; ++i) {
+    const int j = wave + W * i;
+    const int tile = j < CQ / 8 ? j / (CQ / 16) : 2 + (j - CQ / 8) / KT;
+    const int jr = j < CQ / 8 ? j % (CQ / 16) : (j - CQ / 8) % KT;
+    sdo[i] = tile == 1;
+    soff[i] = tile < 2 ? (long)h * D * 2 : ((tile - 1) * HD + h * D) * 2;
+    sdst[i] = (tile < 2 ? tile * TILE : 2 * TILE + (tile - 2) * KVT) + jr * 1024;
+  }
+  // Statistic copy j (256 bytes): lse (j < 4), -Dsum (j < 8) of the chunk's
+  // queries, then the row's key mask; waves w and w + 8 (a slot past TS
+  // repeats the wave's first).
+  auto stat_voff = [&](int i, int c, int lane) __attribute__((always_inline)) -> unsigned {
+    int j = wave + W * i;
+    if (j >= TS) j -= W;
+    const int which = j < CQ / 64 ? 0 : j < 2 * (CQ / 64) ? 1 : 2;
+    const int js = which < 2 ? j % (CQ / 64) : j - 2 * (CQ / 64);
+    const int q = which < 2 ? min(c * CQ + js * 64 + lane, N - 1) : min(js * 64 + lane, N - 1);
+    return which == 2 ? (unsigned)(q * a.mask_sk * 4) : (unsigned)(q * 4);
+  };
+  unsigned ssdst[2];
+  int swhich[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    int j = wave + W * i;
+    if (j >= TS) j -= W;
+    const int which = j < CQ / 64 ? 0 : j < 2 * (CQ / 64) ? 1 : 2;
+    const int js = which < 2 ? j % (CQ / 64) : j - 2 * (CQ / 64);
+    swhich[i] = which;
+    ssdst[i] = SOFF + (which < 2 ? which * CQ * 4 : 2 * CQ * 4) + js * 256;
+  }
+  // the copies of stage (row r, chunk C) into buffer u
+  auto copy_stage = [&](int r, auto c_, int u) __attribute__((always_inline)) {
+    constexpr int C = decltype(c_)::value;
+    const unsigned base = lds0 + u * BUF;
+    int ln = lane;  // opaque: the offsets are recomputed here, not hoisted into registers
+    asm volatile("" : "+v"(ln));
+    const char* qrow = reinterpret_cast<const char*>(a.qkvg + (long)r * N * a.ld);
+    const char* orow = reinterpret_cast<const char*>(b.dO + (long)r * N * a.ldo);
+#pragma unroll
+    for (int i = 0; i < NCT; ++i) dma16s(tile_voff(i, C, ln), (sdo[i] ? orow : qrow) + soff[i], base + sdst[i]);
+    const long srow = ((long)r * H + h) * N;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const float* sb = swhich[i] == 0 ? a.lse + srow
+                      : swhich[i] == 1 ? b.nDsum + srow
+                                       : a.mask + (long)r * a.mask_sr;
+      dma4s(stat_voff(i, C, ln), sb, base + ssdst[i]);
+    }
+  };
+
+  // lane-constant swizzled offsets (h16 units): row reads at rows = lk
+  // (mod 16), transposed reads at rows 4g + lk/4 (mod 16)
+  const int rsw = ((g ^ ((lk >> 1) & 3)) << 3);
+  const int trow = 4 * g + (lk >> 2);
+  const int tsw0 = (((lk & 3) >> 1) ^ ((trow >> 1) & 3)) * 8 + 4 * (lk & 1);       // columns 0..15
+  const int tsw1 = ((2 + ((lk & 3) >> 1)) ^ ((trow >> 1) & 3)) * 8 + 4 * (lk & 1);  // columns 16..31
+  auto tr8 = [&](const h16* T, int r0_, int dh) __attribute__((always_inline)) -> h16x8 {
+    const h16* p = T + (r0_ + trow) * 32 + (dh ? tsw1 : tsw0);
+    const h16x4 x = __builtin_bit_cast(h16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p));
+    const h16x4 y =
+        __builtin_bit_cast(h16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p + 16 * 32)));
+    h16x8 v;
+    v[0] = x[0]; v[1] = x[1]; v[2] = x[2]; v[3] = x[3];
+    v[4] = y[0]; v[5] = y[1]; v[6] = y[2]; v[7] = y[3];
+    return v;
+  };
+
+  const int nrow = r1 - r0;
+  copy_stage(r0, std::integral_constant<int, 0>{}, 0);
+  copy_stage(r0, std::integral_constant<int, 1>{}, 1);
+  const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+  f32x4 accK[DT], accV[DT];
+  int u = 0;  // buffer of the current stage
+  for (int rr = 0; rr < nrow; ++rr) {
+    const int r = r0 + rr;
+#pragma unroll
+    for (int i = 0; i < DT; ++i) { accK[i] = z4; accV[i] = z4; }
+    auto stage = [&](auto c_) __attribute__((always_inline)) {
+      constexpr int C = decltype(c_)::value;
+      // this stage's copies are in; the next stage's (and in a storing
+      // wave the previous row's four dK/dV stores) may still be in flight
+      if (stores && rr > 0) wait_vm<NCOPY + 4>();
+      else wait_vm<NCOPY>();
+      __syncthreads();
+      // two stages ahead: (row r + 1, chunk C) -- the last row reloads itself
+      copy_stage(min(r + 1, r1 - 1), c_, u >= 1 ? u - 1 : 2);
+      const unsigned char* cur = smem_raw + u * BUF;
+      u = u == 2 ? 0 : u + 1;
+      if (!kon) return;
+      const h16* Qs = reinterpret_cast<const h16*>(cur);
+      const h16* Os = reinterpret_cast<const h16*>(cur + TILE);
+      const h16* Ks = reinterpret_cast<const h16*>(cur + 2 * TILE);
+      const h16* Vs = reinterpret_cast<const h16*>(cur + 2 * TILE + KVT);
+      const float* Ls = reinterpret_cast<const float*>(cur + SOFF);  // lse of the chunk
+      const float* Ds = Ls + CQ;                                     // -Dsum of the chunk
+      const float* Ms = Ds + CQ;                                     // key mask of the row
+      HFrag<D> kf, vf;
+      kf.v = ld8(Ks + klocal * 32 + rsw);
+      vf.v = ld8(Vs + klocal * 32 + rsw);
+      const bool mk = Ms[k] != 0.f;
+      bool any = false;
+#pragma unroll
+      for (int i = 0; i < JSM; ++i)
+        if (i * 64 + lane < N) any |= Ms[i * 64 + lane] != 0.f;
+      const bool live = __builtin_amdgcn_ballot_w64(any) != 0;
+      const bool allk = __builtin_amdgcn_ballot_w64(!mk) == 0;
+
+      struct Ops {
+        h16x8 q[2], o[2];
+        float4 l[2], d[2];
+      };
+      auto load_ops = [&](int ql, Ops& x) __attribute__((always_inline)) {
+#pragma unroll
+        for (int qh = 0; qh < 2; ++qh) {
+          x.q[qh] = ld8(Qs + (ql + qh * 16 + lk) * 32 + rsw);
+          x.o[qh] = ld8(Os + (ql + qh * 16 + lk) * 32 + rsw);
+          x.l[qh] = *reinterpret_cast<const float4*>(Ls + ql + qh * 16 + 4 * g);
+          x.d[qh] = *reinterpret_cast<const float4*>(Ds + ql + qh * 16 + 4 * g);
+        }
+      };
+      // MODE 0: every key of the wave unmasked; 1: a masked key gets
+      // exponent -inf; 2: fully masked row (p = 1/N, dS = 0)
+      auto units = [&](auto mode_c) __attribute__((always_inline)) {
+        constexpr int MODE = decltype(mode_c)::value;
+#pragma unroll
+        for (int i = 0; i < UPS; ++i) {
+          if (8 * C + qs + QS * i >= NQB) continue;  // wave-uniform
+          const int ib = UPS * C + i;
+          const int ql = (qs + QS * i) * 32;
+          // the bias stays binary16 between uses: converted here, not
+          // hoisted out of the row loop as 64 f32 registers
+          asm volatile("" : "+v"(bsh[ib]));
+          Ops cur_;
+          load_ops(ql, cur_);
+          f32x4 s4[2], dp[2];
+#pragma unroll
+          for (int qh = 0; qh < 2; ++qh) {
+            f32x4 cs, cd;
+            cs[0] = (float)bsh[ib][qh * 4 + 0] - cur_.l[qh].x;
+            cs[1] = (float)bsh[ib][qh * 4 + 1] - cur_.l[qh].y;
+            cs[2] = (float)bsh[ib][qh * 4 + 2] - cur_.l[qh].z;
+            cs[3] = (float)bsh[ib][qh * 4 + 3] - cur_.l[qh].w;
+            cd[0] = cur_.d[qh].x; cd[1] = cur_.d[qh].y; cd[2] = cur_.d[qh].z; cd[3] = cur_.d[qh].w;
+            HFrag<D> qa, da;
+            qa.v = cur_.q[qh];
+            da.v = cur_.o[qh];
+            if constexpr (MODE != 2) {
+              s4[qh] = HFrag<D>::mma(qa, kf, cs);  // S + bias - lse
+              dp[qh] = HFrag<D>::mma(da, vf, cd);  // dP - Dsum
+            }
+          }
+          h16x8 pf, dsf;
+#pragma unroll
+          for (int qh = 0; qh < 2; ++qh)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              float p, ds;
+              if constexpr (MODE == 0) {
+                p = fast_exp2(s4[qh][e]);
+                ds = p * dp[qh][e];
+              } else if constexpr (MODE == 1) {
+                p = fast_exp2(mk ? s4[qh][e] : -INFINITY);
+                ds = p * dp[qh][e];
+              } else {
+                p = 1.f / N;
+                ds = 0.f;
+              }
+              pf[qh * 4 + e] = (h16)p;
+              dsf[qh * 4 + e] = (h16)ds;
+              if constexpr (MODE != 2) dbias[ib][qh * 4 + e] += ds;
+            }
+#pragma unroll
+          for (int dh = 0; dh < DT; ++dh) {
+            accV[dh] = mfma16x16x32(tr8(Os, ql, dh), pf, accV[dh]);
+            if constexpr (MODE != 2) accK[dh] = mfma16x16x32(tr8(Qs, ql, dh), dsf, accK[dh]);
+          }
+        }
+      };
+      if (live && allk) units(std::integral_constant<int, 0>{});
+      else if (live) units(std::integral_constant<int, 1>{});
+      else units(std::integral_constant<int, 2>{});
+    };
+    stage(std::integral_constant<int, 0>{});
+    stage(std::integral_constant<int, 1>{});
+
+    // row done: query group 1 parks its partials, query group 0 adds them
+    // and writes dK, dV of its key tile
+    if (qs == 1 && kon) {
+      float* x = Xs + kt_ * (2 * DT * 4 * 64);
+#pragma unroll
+      for (int dh = 0; dh < DT; ++dh)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          x[(dh * 4 + i) * 64 + lane] = accK[dh][i];
+          x[(DT * 4 + dh * 4 + i) * 64 + lane] = accV[dh][i];
+        }
+    }
+    __syncthreads();
+    if (stores) {
+      const float* x = Xs + kt_ * (2 * DT * 4 * 64);
+      h16* dk = b.dqkvg + ((long)r * N + k) * a.ld + HD + h * D;
+      h16* dvp = dk + HD;
+      // lane (lk, g) holds channels [4g, 4g+4) and [16+4g, 16+4g+4) of key k;
+      // dK is w.r.t. the unscaled k: sum_q dS * q_scaled / log2(e)
+#pragma unroll
+      for (int dh = 0; dh < DT; ++dh) {
+        h16x4 kv, vv;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          kv[i] = (h16)((accK[dh][i] + x[(dh * 4 + i) * 64 + lane]) * (1.f / LOG2E));
+          vv[i] = (h16)(accV[dh][i] + x[(DT * 4 + dh * 4 + i) * 64 + lane]);
+        }
+        *reinterpret_cast<h16x4*>(dk + dh * 16 + 4 * g) = kv;
+        *reinterpret_cast<h16x4*>(dvp + dh * 16 + 4 * g) = vv;
+      }
+    }
+  }
+  wait_vm<0>();  // the last stages' copies land before the workgroup's LDS is released
+  if (b.dbias_part == nullptr || !kon) return;
+  float* part = b.dbias_part + (((long)ch * H + h) * N) * N;
+#pragma unroll
+  for (int ib = 0; ib < NB; ++ib) {
+    const int blk = 8 * (ib / UPS) + qs + QS * (ib % UPS);
+    if (blk >= NQB) continue;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int qi = blk * 32 + (e / 4) * 16 + 4 * g + (e % 4);
+      part[(long)qi * N + k] = dbias[ib][e];
+    }
+  }
+}
+
 __global__ void attn_dbias_reduce_kernel(const float* __restrict__ part, int nch,
                                          long n, float* __restrict__ out) {
   const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -1488,15 +1832,17 @@ int attn_fwd_rows_per_chunk(int R, int N, int H) {
   return (int)std::max(1L, ((long)R + nch - 1) / nch);
 }
 
-// Rows per bias-gradient chunk.  A chunk is H * N / (16 KT) workgroups of
+// Rows per bias-gradient chunk.  A chunk is H * N / (keys a workgroup) workgroups of
 // the dK/dV kernel, which is register bound at two workgroups per CU; the
 // chunk count is the largest that fits one round of 2 x CUs workgroups, so
 // no second, partly empty round follows (N = 224, H = 4 on 256 CUs: 18
 // chunks of 13 rows).  Fewer chunks also mean fewer [nchunk][H][N][N]
 // partials to write and add.
-int attn_rows_per_chunk(int R, int N, int H) {
-  const int KT = N > 768 ? 1 : 2;
-  const long per_chunk = (long)H * (N / (16 * KT));
+int attn_rows_per_chunk(int R, int N, int H, int D) {
+  // keys a workgroup: 64 in the D = 32 kernel for 256 < N <= 512, 32 to
+  // N = 768, 16 beyond
+  const int kpw = D == 32 && N > 256 && N <= 512 ? 64 : N > 768 ? 16 : 32;
+  const long per_chunk = (long)H * ((N + kpw - 1) / kpw);
   const long per_cu = N > 256 ? 1 : 2;  // eight-wave workgroups beyond 256
   const long slots = per_cu * device_cus();
   long nch = std::max(1L, slots / per_chunk);
@@ -1650,6 +1996,19 @@ static void attn_bwd_t(hipStream_t st, const AttnBwdArgs& b0) {
         with_blocks(a.N / 32, [&](auto nb) {
           if constexpr (decltype(nb)::value <= 8)
             hipLaunchKernelGGL((attn_bwd_dkv_lds_kernel<decltype(nb)::value>), grid, dim3(256), lds,
+                               st, b);
+        });
+        goto dkv_done;
+      }
+      if (a.N > 256 && a.N <= 512 && a.bias) {
+        // three stage buffers (Q, dO chunk tiles, K, V tiles, lse, -Dsum,
+        // mask) + query group 1's partials
+        const size_t buf = (size_t)2 * 256 * 64 + 2 * 64 * 64 + 2 * 256 * 4 + (size_t)((a.N + 63) / 64) * 64 * 4;
+        const size_t lds = 3 * buf + (size_t)4 * 2 * 2 * 4 * 64 * 4;
+        const dim3 grid8(xcd_grid((long)nch * a.H * ((a.N + 63) / 64)));  // 64 keys a workgroup
+        with_blocks(a.N / 32, [&](auto nb) {
+          if constexpr (decltype(nb)::value > 8 && decltype(nb)::value <= 16)
+            hipLaunchKernelGGL((attn_bwd_dkv_lds8_kernel<decltype(nb)::value>), grid8, dim3(512), lds,
                                st, b);
         });
         goto dkv_done;

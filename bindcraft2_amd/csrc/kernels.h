@@ -92,7 +92,7 @@ struct AttnBwdArgs {
 };
 void attn_bwd(hipStream_t st, const AttnBwdArgs& a);
 int attn_bwd_nchunk(int R, int rows_per_chunk);
-int attn_rows_per_chunk(int R, int N, int H);
+int attn_rows_per_chunk(int R, int N, int H, int D);
 
 // f32 LayerNorm over rows of any width (one wave per row); dx may alias dy.
 void ln_f32_rows_fwd(hipStream_t st, const float* x, long M, int C, const float* g,

@@ -427,7 +427,7 @@ const float* msarow_bwd_msa(hipStream_t st, const MsaRowW& w, int S, int N, cons
   Carver cv(const_cast<void*>(save));
   MsaRowSave<Carver> sv(cv, S, N, Cm, H);
   AttnBwdArgs b;
-  b.rows_per_chunk = attn_rows_per_chunk(S, N, H);
+  b.rows_per_chunk = attn_rows_per_chunk(S, N, H, a.D);
   const int nch = attn_bwd_nchunk(S, b.rows_per_chunk);
   Arena& ar = arena();
   std::lock_guard<std::recursive_mutex> lk(ar.lock());

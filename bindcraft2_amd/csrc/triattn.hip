@@ -237,7 +237,7 @@ void triattn_bwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
   Carver cv(const_cast<void*>(save));
   TriAttnSave<Carver> sv(cv, N, C, H);
   AttnBwdArgs b;
-  b.rows_per_chunk = attn_rows_per_chunk(N, N, H);
+  b.rows_per_chunk = attn_rows_per_chunk(N, N, H, w.D);
   const int nch = attn_bwd_nchunk(N, b.rows_per_chunk);
   Arena& ar = arena();
   std::lock_guard<std::recursive_mutex> lk(ar.lock());
