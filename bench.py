@@ -292,9 +292,9 @@ def traffic_of(kernel, n):
     # the triangle-attention launches are the head-width-32 instantiation (the
     # row-chunk forms for N <= 256); other timer names map to no one symbol
     nb = n // 32
-    syms = {"attn_fwd": [f"attn_fwd_rows<32, {nb}>", f"attn_fwd<32, {nb}>"],
-            "attn_bwd_dq": [f"attn_bwd_dq_rows<32, {nb}>", f"attn_bwd_dq<32, {nb}>"],
-            "attn_bwd_dkv": [f"attn_bwd_dkv_lds<{nb}>",
+    syms = {"attn_fwd": [f"attn_fwd_rows<32, {nb}>", f"attn_fwd<32, {nb}, 8>"],
+            "attn_bwd_dq": [f"attn_bwd_dq_rows<32, {nb}>", f"attn_bwd_dq<32, {nb}, 8>"],
+            "attn_bwd_dkv": [f"attn_bwd_dkv_lds<{nb}>", f"attn_bwd_dkv_lds8<{nb}>",
                              f"attn_bwd_dkv<32, {nb}, {8 if nb > 8 else 4}, "
                              f"{8 if nb > 24 else 4 if nb > 8 else 2}>"],
             "trimul.tail_bwd": ["trimul_tail", "_ZN4bc2n12_GLOBAL__N_118trimul_tail_kernelENS0_8TailArgsE"]}.get(kernel, [kernel])
@@ -306,8 +306,8 @@ def traffic_of(kernel, n):
     # mangled); the contraction's output type tells forward from backward
     pat = {"trimul.proj_bwd": r"EpiTrimulProjBwd",
            "trimul.gemm_proj": r"gemm.*EpiTrimulProj(?!Bwd)",
-           "trimul.ln_proj": r"^kernel<0, true, EpiTrimulProj>|lnproj.*EpiTrimulProj",
-           "triattn.ln_qkvg": r"^kernel<4, false, EpiScaledCols>|lnproj.*EpiScaledCols",
+           "trimul.ln_proj": r"^kernel<0, true, EpiTrimulProj\b|lnproj.*EpiTrimulProj",
+           "triattn.ln_qkvg": r"^kernel<4, false, EpiScaledCols\b|lnproj.*EpiScaledCols",
            "trans.fused_fwd": r"^fused<.*EpiResidualRows|fused_kernel.*EpiResidualRows",
            "trans.fused_bwd": r"^fused<.*EpiLnBwd|fused_kernel.*EpiLnBwd",
            "trimul.gemm_out": r"EpiTrimulOut",
