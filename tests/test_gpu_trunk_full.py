@@ -11,9 +11,10 @@ pair, the template stack on its own activations; the backward runs main ->
 extra.  The oracle is the reference's JAX trunk restated in oracle/af2.py,
 run in fp32 with per-block recompute (tests/trunk_ref.py).
 
-a 2-block Evoformer stack at L=512 (the 8-iteration fold at
-L=512 is in test_gpu_fold.py, the single modules at L=512 in
-test_gpu_triattn.py and test_gpu_trimul.py).
+the same chain at L=512 with 8 main-stack blocks, and a 2-block
+Evoformer stack at L=512 on its own (the 8-iteration fold at L=512 is in
+test_gpu_fold.py, the single modules at L=512 in test_gpu_triattn.py and
+test_gpu_trimul.py).
 
 Bars (north star): activations relL2 and max|d|/max|ref| <= 2e-2; gradient
 cosine >= 0.999."""
@@ -40,15 +41,14 @@ def _t(a, dev):
     return torch.as_tensor(a, device=dev)
 
 
-@pytest.mark.timeout(1500)
-def test_trunk_full_depth_L224(cuda):
-    n, t0 = 224, time.time()
-    _say(f"trunk 48+4+2 blocks n={n} s=1 dropout=on mask=0.1")
+def _trunk_case(cuda, n, depth, seed):
+    t0 = time.time()
+    _say(f"trunk {depth}+4+2 blocks n={n} s=1 dropout=on mask=0.1")
     # the benchmark's draws: residue mask, then the three stacks' weights
-    rng = np.random.default_rng(0)
+    rng = np.random.default_rng(seed)
     m1 = np.ones(n, np.float32)
     m1[rng.choice(n, int(round(0.1 * n)), replace=False)] = 0
-    evo, extra, tpl = bparams.init_trunk_params(rng)
+    evo, extra, tpl = bparams.init_trunk_params(rng, depth=depth)
     pmask = np.outer(m1, m1).astype(np.float32)
     mmask = m1[None].copy()
     emask = np.zeros((1, n), np.float32)
@@ -62,9 +62,9 @@ def test_trunk_full_depth_L224(cuda):
     ct_tpl = g.standard_normal((n, n, 64)).astype(np.float32)
     keys = [J.prng_key(11 + i) for i in range(3)]  # template, extra, main
 
-    main = ops.EvoformerStack(weights_dir(evo, "full_main"), 48)
-    xst = ops.EvoformerStack(weights_dir(extra, "full_extra"), 4, pair_only=True, c_m=64)
-    tst = ops.TemplatePairStack(weights_dir(tpl, "full_tpl"), 2)
+    main = ops.EvoformerStack(weights_dir(evo, f"full_main_{n}_{depth}"), depth)
+    xst = ops.EvoformerStack(weights_dir(extra, f"full_extra_{n}"), 4, pair_only=True, c_m=64)
+    tst = ops.TemplatePairStack(weights_dir(tpl, f"full_tpl_{n}"), 2)
     T = lambda a: _t(a, cuda)
     seeds = [ops.seed_tensor(k, True, cuda) for k in keys]
     to, s_t = tst.forward(T(tpl0), T(pmask), seeds[0])
@@ -85,7 +85,7 @@ def test_trunk_full_depth_L224(cuda):
     bt = R.template_block(tpl, pm_t, True, F)
     be = R.pair_only_block(extra, pm_t, True, F)
     bm = R.evoformer_block(evo, pm_t, mm_t, True, F)
-    kt, ke, km = (af2.stack_block_keys(k, d) for k, d in zip(keys, (2, 4, 48)))
+    kt, ke, km = (af2.stack_block_keys(k, d) for k, d in zip(keys, (2, 4, depth)))
     xt = R.stack_forward(bt, (torch.as_tensor(tpl0),), kt)
     r_to = xt[-1][0]
     (r_dtpl,) = R.stack_backward(bt, xt, kt, (torch.as_tensor(ct_tpl),))
@@ -110,6 +110,19 @@ def test_trunk_full_depth_L224(cuda):
     _say("  d msa", assert_grad(got["dmsa"], d(r_dmsa), what="dmsa"))
     _say("  d template", assert_grad(got["dtpl"], d(r_dtpl), what="dtpl"))
     _say(f"  total {time.time() - t0:.0f}s")
+
+
+@pytest.mark.timeout(1500)
+def test_trunk_full_depth_L224(cuda):
+    _trunk_case(cuda, 224, 48, 0)
+
+
+@pytest.mark.timeout(1500)
+def test_trunk_L512_depth8(cuda):
+    """configs[4]'s trunk structure at L=512 (template 2, extra 4, main 8
+    blocks), chained as at L=224: the stacks' hand-offs and eight main
+    blocks of accumulated rounding at the large-complex length."""
+    _trunk_case(cuda, 512, 8, 5120)
 
 
 @pytest.mark.timeout(900)
