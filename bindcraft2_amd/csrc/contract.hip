@@ -69,6 +69,7 @@ __device__ __forceinline__ void store4<h16>(h16* p, f32x4 v) {
 }
 
 constexpr int SR = 16;  // rows of A per strip
+constexpr int MAXS = 4;  // A strips a workgroup (held in registers)
 
 template <int NB, bool AK, bool BK, class OutT>
 __global__ __launch_bounds__(64 * NB) void contract_kernel(const h16* __restrict__ A,
@@ -100,28 +101,55 @@ __global__ __launch_bounds__(64 * NB) void contract_kernel(const h16* __restrict
   const int g = lane >> 4, l16 = lane & 15;
   const int n0 = wave * 32;
 
+  // Every global load the workgroup needs is issued before its first wait:
+  // the staging chunks of B (32 k each) PD chunks ahead of their turn, and
+  // all of its A strips (at most MAXS, held in registers) behind the first PD
+  // chunks.  Staged one chunk and one strip at a time, each chunk and strip
+  // had cost a full memory round trip (7 + 3.5 of them a workgroup at N =
+  // 224, about 14 us a launch).
+  constexpr int CH = BROWS * (BK ? 4 : N / 8);  // 16-byte pieces per staging chunk
+  constexpr int CPT = (CH + NT - 1) / NT;        // a thread's pieces per chunk
+  constexpr int PD = NB < 2 ? NB : 2;            // chunks in flight
+  auto load_b = [&](int kc, h16x8 (&v)[CPT]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = min(tid + NT * i, CH - 1);  // a spare piece re-reads the last one
+      if constexpr (BK) {
+        const int r = c / 4, q = (c % 4) * 8;
+        v[i] = ld8(Bp + (long)r * N + kc * 32 + q);
+      } else {
+        const int r = c / (N / 8), q = (c % (N / 8)) * 8;
+        v[i] = ld8(Bp + (long)(kc * 32 + r) * N + q);
+      }
+    }
+  };
+  h16x8 vb[PD][CPT];
+#pragma unroll
+  for (int p = 0; p < PD; ++p) load_b(p, vb[p]);
+
+  // ---- A strips: s = grp + i * groups, i < nsw (the launcher keeps nsw <= MAXS)
+  auto load_strip = [&](int s) -> h16x8 {
+    if constexpr (AK) {
+      const int r = tid / (N / 8), q = (tid % (N / 8)) * 8;
+      return ld8(Ap + (long)(s * SR + r) * N + q);
+    } else {
+      const int k = tid / 2, q = (tid % 2) * 8;
+      return ld8(Ap + (long)k * N + s * SR + q);
+    }
+  };
+  const int nsw = grp < NS ? (NS - grp + groups - 1) / groups : 0;
+  h16x8 va[MAXS];
+#pragma unroll
+  for (int i = 0; i < MAXS; ++i) va[i] = load_strip(min(grp + i * groups, NS - 1));  // spares: in bounds
+
   // ---- B fragments of this wave's 32 columns, all k, via LDS chunks of 32 k
   h16x8 bf[NB][2];
 #pragma unroll
   for (int kc = 0; kc < NB; ++kc) {
-    constexpr int CH = BROWS * (BK ? 4 : N / 8);  // 16-byte chunks per staging chunk
-    h16x8 v[(CH + NT - 1) / NT];
-#pragma unroll
-    for (int i = 0; i < (CH + NT - 1) / NT; ++i) {
-      const int c = tid + NT * i;
-      if (c < CH) {
-        if constexpr (BK) {
-          const int r = c / 4, q = (c % 4) * 8;
-          v[i] = ld8(Bp + (long)r * N + kc * 32 + q);
-        } else {
-          const int r = c / (N / 8), q = (c % (N / 8)) * 8;
-          v[i] = ld8(Bp + (long)(kc * 32 + r) * N + q);
-        }
-      }
-    }
+    h16x8 (&v)[CPT] = vb[kc % PD];
     if (kc > 0) __syncthreads();  // the previous chunk's readers are done
 #pragma unroll
-    for (int i = 0; i < (CH + NT - 1) / NT; ++i) {
+    for (int i = 0; i < CPT; ++i) {
       const int c = tid + NT * i;
       if (c < CH) {
         if constexpr (BK) st8(&Bs[(c / 4) * LDB + (c % 4) * 8], v[i]);
@@ -134,33 +162,21 @@ __global__ __launch_bounds__(64 * NB) void contract_kernel(const h16* __restrict
       if constexpr (BK) bf[kc][j] = frag_rows(Bs, LDB, n0 + j * 16 + l16, 0, g);
       else bf[kc][j] = frag_cols(Bs, LDB, n0 + j * 16, 0, lane);
     }
+    if (kc + PD < NB) load_b(kc + PD, v);
   }
 
-  // ---- A strips
-  auto load_strip = [&](int s) -> h16x8 {
-    if constexpr (AK) {
-      const int r = tid / (N / 8), q = (tid % (N / 8)) * 8;
-      return ld8(Ap + (long)(s * SR + r) * N + q);
-    } else {
-      const int k = tid / 2, q = (tid % 2) * 8;
-      return ld8(Ap + (long)k * N + s * SR + q);
-    }
-  };
   auto stash = [&](int buf, h16x8 v) {
     h16* as = As + buf * ABUF;
     if constexpr (AK) st8(&as[(tid / (N / 8)) * LDA + (tid % (N / 8)) * 8], v);
     else st8(&as[(tid / 2) * LDA + (tid % 2) * 8], v);
   };
-
-  int s = grp;
-  if (s >= NS) return;  // no barrier follows for this (uniform) workgroup
-  stash(0, load_strip(s));
+  if (nsw == 0) return;  // (uniform) no barrier follows
+  stash(0, va[0]);
   __syncthreads();
-  int buf = 0;
-  for (; s < NS; s += groups) {
-    const bool more = s + groups < NS;
-    h16x8 nxt;
-    if (more) nxt = load_strip(s + groups);
+#pragma unroll
+  for (int i = 0; i < MAXS; ++i) {
+    if (i >= nsw) break;  // uniform
+    const int s = grp + i * groups, buf = i & 1;
     const h16* as = As + buf * ABUF;
     f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
@@ -176,9 +192,8 @@ __global__ __launch_bounds__(64 * NB) void contract_kernel(const h16* __restrict
     const int m = s * SR + l16;
 #pragma unroll
     for (int j = 0; j < 2; ++j) store4<OutT>(Cp + (long)m * N + n0 + j * 16 + 4 * g, acc[j]);
-    if (more) stash(buf ^ 1, nxt);
+    if (i + 1 < nsw) stash(buf ^ 1, va[i + 1 < MAXS ? i + 1 : i]);
     __syncthreads();
-    buf ^= 1;
   }
 }
 
@@ -220,7 +235,8 @@ bool trimul_contract(hipStream_t st, int N, int channels, const h16* A, bool a_k
             "hipDeviceGetAttribute");
   // about two workgroups per CU, a channel's strips spread over its groups
   const int ns = N / SR;
-  const int groups = std::max(1, std::min(ns, (2 * cus + channels - 1) / channels));
+  const int groups = std::max((ns + MAXS - 1) / MAXS,
+                              std::max(1, std::min(ns, (2 * cus + channels - 1) / channels)));
   if (Cf) return contract_t<float>(st, N, channels, A, a_kcontig, B, b_kcontig, Cf, groups);
   return contract_t<h16>(st, N, channels, A, a_kcontig, B, b_kcontig, Cb, groups);
 }
