@@ -86,7 +86,7 @@ __global__ __launch_bounds__(64 * NB) void contract_kernel(const h16* __restrict
   constexpr int AROWS = AK ? SR : N;
   constexpr int ABUF = AROWS * LDA;
   __shared__ __attribute__((aligned(16))) h16 As[2 * ABUF];
-  __shared__ __attribute__((aligned(16))) h16 Bs[BROWS * LDB];
+  __shared__ __attribute__((aligned(16))) h16 Bs[2 * BROWS * LDB];  // two staging chunks
   static_assert(SR * N / 8 == NT, "one 16-byte chunk of a strip per thread");
 
   const long G = (long)channels * groups;
@@ -144,23 +144,25 @@ __global__ __launch_bounds__(64 * NB) void contract_kernel(const h16* __restrict
 
   // ---- B fragments of this wave's 32 columns, all k, via LDS chunks of 32 k
   h16x8 bf[NB][2];
+  // (two LDS chunks: the barrier after a chunk's stores also orders the
+  // reads of the chunk before it, whose buffer the next stores reuse)
 #pragma unroll
   for (int kc = 0; kc < NB; ++kc) {
     h16x8 (&v)[CPT] = vb[kc % PD];
-    if (kc > 0) __syncthreads();  // the previous chunk's readers are done
+    h16* bs = Bs + (kc & 1) * BROWS * LDB;
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       const int c = tid + NT * i;
       if (c < CH) {
-        if constexpr (BK) st8(&Bs[(c / 4) * LDB + (c % 4) * 8], v[i]);
-        else st8(&Bs[(c / (N / 8)) * LDB + (c % (N / 8)) * 8], v[i]);
+        if constexpr (BK) st8(&bs[(c / 4) * LDB + (c % 4) * 8], v[i]);
+        else st8(&bs[(c / (N / 8)) * LDB + (c % (N / 8)) * 8], v[i]);
       }
     }
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      if constexpr (BK) bf[kc][j] = frag_rows(Bs, LDB, n0 + j * 16 + l16, 0, g);
-      else bf[kc][j] = frag_cols(Bs, LDB, n0 + j * 16, 0, lane);
+      if constexpr (BK) bf[kc][j] = frag_rows(bs, LDB, n0 + j * 16 + l16, 0, g);
+      else bf[kc][j] = frag_cols(bs, LDB, n0 + j * 16, 0, lane);
     }
     if (kc + PD < NB) load_b(kc + PD, v);
   }
