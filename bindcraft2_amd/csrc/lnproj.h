@@ -13,6 +13,14 @@
 
 namespace bc2n {
 namespace lnproj {
+// An epilogue whose column calls each handle a pair of columns (c and c + 16
+// of every 32-column block: a projection and its gate) says kColPairs; the
+// column loop then visits only the first of each pair, so no lane idles.
+template <class E, class = void>
+struct col_pairs : std::false_type {};
+template <class E>
+struct col_pairs<E, std::void_t<decltype(E::kColPairs)>> : std::bool_constant<E::kColPairs> {};
+
 constexpr int C = 128, RT = 3, BM = 16 * RT, LDX = C + 8, LDT = 128 + 4;
 
 struct Args {
@@ -163,8 +171,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     if (colm) {
       // 8 consecutive rows of one column a call (channel-major outputs),
       // columns fastest (M and BM are multiples of 8)
-      for (int it = tid; it < 128 * (BM / 8); it += 256) {
-        const int c = it & 127, rg = it >> 7;
+      constexpr int CV = col_pairs<Epi>::value ? 64 : 128;  // columns visited
+      for (int it = tid; it < CV * (BM / 8); it += 256) {
+        const int cv = it % CV, rg = it / CV;
+        const int c = col_pairs<Epi>::value ? (cv >> 4) * 32 + (cv & 15) : cv;
         const long m = m0 + rg * 8;
         if (m >= M) continue;
         const float* tp = T + (rg * 8) * LDT + c;

@@ -39,6 +39,7 @@ __host__ __device__ inline int col_gate(int ch) { return (ch / 16) * 32 + 16 + c
 // gating_linear columns run in row mode: g_out[m][c] = sigmoid(acc + b).
 struct EpiTrimulProj {
   static constexpr bool kHasCol = true;
+  static constexpr bool kColPairs = true;  // col() of column c also does its gate c + 16
   h16 *left, *right;   // [I][M]
   h16* gout;           // [M][C]
   const float *bp, *bg, *bgl, *mask;
