@@ -266,7 +266,10 @@ void triattn_bwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
   EpiGateBwd eg;
   eg.qkvg = sv.qkvg; eg.ld = 4L * HD; eg.o = sv.o; eg.dO = b.dO; eg.dqkvg = b.dqkvg;
   eg.nDsum = b.nDsum; eg.HD = HD; eg.H = H; eg.D = w.D; eg.Ntok = N;
-  gemm<128, 128>(st, g1, eg, BC2N_TN(C, "triattn.gemm_dout"), ALoadScaledRows{dout, tbl, N, C, per_column, sc});
+  // 64-row tiles: with N = K = 128 a 128-row grid leaves most workgroup
+  // slots empty (392 workgroups at 224 tokens); the 128 x 128 B operand is
+  // cheap to re-read
+  gemm<64, 128>(st, g1, eg, BC2N_TN(C, "triattn.gemm_dout"), ALoadScaledRows{dout, tbl, N, C, per_column, sc});
   b.gate_done = true;
 
   AttnArgs& a = b.f;

@@ -692,8 +692,11 @@ void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
   g1.M = (int)M; g1.N = I; g1.K = C;
   g1.a_sm = C; g1.a_sk = 1;
   g1.B = w.wo; g1.b_sn = C; g1.b_sk = 1;
-  gemm<128, 128>(st, g1, EpiStore<float>{dtn, I, 0, nullptr, I}, BC2N_TN(C, "trimul.gemm_dout"),
-                 ALoadTrimulOut{dout, tbl, sv.gout, sv.osave, dcat, C, ldcat, off, N, sc});
+  // 64-row tiles: with N = K = 128 a 128-row grid leaves most workgroup
+  // slots empty (392 workgroups at 224 tokens); the 128 x 128 B operand is
+  // cheap to re-read
+  gemm<64, 128>(st, g1, EpiStore<float>{dtn, I, 0, nullptr, I}, BC2N_TN(C, "trimul.gemm_dout"),
+                ALoadTrimulOut{dout, tbl, sv.gout, sv.osave, dcat, C, ldcat, off, N, sc});
   {
     KTimed kt(BC2N_TN(C, "trimul.ln_center_bwd"), st);
     ln_bwd_cm(st, dtn, sv.T, M, I, w.cn_g, sv.cmean, sv.crstd, dT);
