@@ -803,37 +803,55 @@ struct EpiLnBwd : EpiRows {
         for (int k = 0; k < 4; ++k) w[(4 * i + k) / H][(4 * i + k) % H] = f[k];
       }
     }
+    // G rows a lane group at a time, every global load of the group issued
+    // before its arithmetic: one memory round trip a group, not one a row
+    // (the GEMM's 64-row halves take 4 rows a lane group; the transition's
+    // 48-row tile keeps one, its register budget allows no more)
+    constexpr int G = WM % 64 == 0 ? 4 : 1;
+    static_assert(WM % (16 * G) == 0, "rows a pass");
 #pragma unroll 1
-    for (int r0 = 0; r0 < WM; r0 += 16) {
-      const long m = mb + r0 + lr;
-      if (m >= M) continue;  // the row's 16 lanes leave together
-      float g[8], xv[8], dr[8];
-      ld_f8(T + (r0 + lr) * ldt + c0, g);
-      const long src = ln_src_row(m, nt);
-      ld_f8(x + src * C + c0, xv);
-      ld_f8(dres + src * C + c0, dr);
-      if constexpr (H > 0) {
+    for (int r0 = 0; r0 < WM; r0 += 16 * G) {
+      float xv[G][8], dr[G][8], db[G][H > 0 ? H : 1], mu[G], rs[G];
+      long src[G];
 #pragma unroll
-        for (int h = 0; h < H; ++h) {
-          const float db = dbias[(long)h * M + m];
+      for (int q = 0; q < G; ++q) {
+        // rows past M read row M - 1 (in bounds) and store nothing
+        const long m = min(mb + r0 + 16 * q + lr, M - 1);
+        src[q] = ln_src_row(m, nt);
+        ld_f8(x + src[q] * C + c0, xv[q]);
+        ld_f8(dres + src[q] * C + c0, dr[q]);
+        if constexpr (H > 0) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) g[e] += db * w[e][h];
+          for (int h = 0; h < H; ++h) db[q][h] = dbias[(long)h * M + m];
         }
+        mu[q] = mean[m];
+        rs[q] = rstd[m];
       }
-      const float mu = mean[m], rs = rstd[m];
-      float sg = 0.f, sgx = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        xv[e] = (xv[e] - mu) * rs;
-        g[e] *= gm[e];
-        sg += g[e];
-        sgx += g[e] * xv[e];
+      for (int q = 0; q < G; ++q) {
+        if (mb + r0 + 16 * q + lr >= M) continue;  // the row's 16 lanes leave together
+        float g[8];
+        ld_f8(T + (r0 + 16 * q + lr) * ldt + c0, g);
+        if constexpr (H > 0) {
+#pragma unroll
+          for (int h = 0; h < H; ++h)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) g[e] += db[q][h] * w[e][h];
+        }
+        float sg = 0.f, sgx = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          xv[q][e] = (xv[q][e] - mu[q]) * rs[q];
+          g[e] *= gm[e];
+          sg += g[e];
+          sgx += g[e] * xv[q][e];
+        }
+        sg = group_sum<16>(sg) * (1.f / C);
+        sgx = group_sum<16>(sgx) * (1.f / C);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dr[q][e] += rs[q] * (g[e] - sg - xv[q][e] * sgx);
+        st_f8(out + src[q] * C + c0, dr[q]);
       }
-      sg = group_sum<16>(sg) * (1.f / C);
-      sgx = group_sum<16>(sgx) * (1.f / C);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) dr[e] += rs * (g[e] - sg - xv[e] * sgx);
-      st_f8(out + src * C + c0, dr);
     }
   }
 };
