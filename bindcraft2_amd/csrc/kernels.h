@@ -34,6 +34,20 @@ void ln_fwd_f32(hipStream_t st, const float* x, long M, int C, int nt,
                 const float* gamma, const float* beta, h16* y, float* mean,
                 float* rstd, bool fast, int H, const float* wb, h16* bias_out,
                 float bias_scale = 1.f);
+// The pair bias of ln_fwd_f32 (C = 128, no normalised output) with the
+// LayerNorm's scale and offset folded into the weights: wfrag =
+// ln_bias_frags(gamma, wb, H) (binary16 MFMA fragments of gamma_c wb[c][h]),
+// wconst = ln_bias_const(beta, wb, H) (sum_c beta_c wb[c][h], 16 floats).
+std::vector<h16> ln_bias_frags(const float* gamma, const float* wb, int H);
+std::vector<float> ln_bias_const(const float* beta, const float* wb, int H);
+void ln_pair_bias_f32(hipStream_t st, const float* x, long M, bool fast, float* mean, float* rstd,
+                      const h16* wfrag, const float* wconst, int H, h16* bias_out, float bias_scale);
+// Its backward, accumulated: dx[m] += LN'(gs * sum_h dbias[h*M+m] wb[c][h])
+// (gs = *gmul, 1 if null), afrag = ln_bias_bwd_frags(gamma, wb, H) (f32).
+std::vector<float> ln_bias_bwd_frags(const float* gamma, const float* wb, int H);
+void ln_pair_bias_bwd_f32(hipStream_t st, const float* x, long M, const float* mean,
+                          const float* rstd, const float* afrag, int H, const float* dbias,
+                          float* dx, const float* gmul);
 // dx[src(m)] (+)= LN-backward(gs * (dy[m] + sum_h dbias[h*M+m] * wb[c*H+h])).
 // acc: dx = res + LN'(...) with res = dres, or dx itself when dres is null.
 // gs = *gmul (device scalar: a module's inverse cotangent scale), 1 if null.

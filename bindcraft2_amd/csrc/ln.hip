@@ -128,6 +128,158 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(
   }
 }
 
+// The LayerNorm + pair-bias projection of C = 128 rows with no normalised
+// output (the MSA row attention's pair bias, 8 heads), in the MFMA operand
+// layout: a wave takes 16 rows, lane l row l & 15 and channels
+// 32 ks + 8 (l >> 4) + e (ks < 4, e < 8) -- its A fragments of the
+// 16 x 128 x 16 product with the weights (heads padded to 16 columns), so
+// the statistics need two xor exchanges and the H dot products are four
+// v_mfma_f32_16x16x32_f16 instead of H lane-group reductions.  The
+// LayerNorm's scale and offset are folded into the weights on the host
+// (ln_bias_frags): bias = sum_c xhat_c (gamma_c W_ch) + sum_c beta_c W_ch,
+// with xhat in binary16 (as every other projection of the trunk) and the
+// second sum a per-head constant, so a lane reads four 16-byte fragments
+// and one constant.  Result lane l holds head l & 15 of rows 4 (l >> 4) + r,
+// r < 4: four consecutive bias_frag_index slots, one 8-byte store.
+template <bool FAST>
+__global__ __launch_bounds__(256) void ln_bias16_kernel(
+    const float* __restrict__ x, long M, float* __restrict__ mean_out,
+    float* __restrict__ rstd_out, const h16* __restrict__ wfrag, const float* __restrict__ wconst,
+    int H, h16* __restrict__ bias_out, float bias_scale, int bn) {
+  constexpr int C = 128;
+  const int lane = threadIdx.x & 63;
+  const long m0 = ((long)blockIdx.x * 4 + (threadIdx.x >> 6)) * 16;
+  if (m0 >= M) return;  // M % 16 == 0: whole waves
+  const int r = lane & 15, kg = lane >> 4;
+  float v[4][8];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) load8f<float>(x + (m0 + r) * C + ks * 32 + kg * 8, v[ks]);
+  h16x8 bf[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) bf[ks] = ld8(wfrag + (ks * 64 + lane) * 8);
+  const float wc = wconst[r];
+  auto quad_sum = [](float a) {
+    a += __shfl_xor(a, 16, 64);
+    return a + __shfl_xor(a, 32, 64);
+  };
+  float s = 0.f, s2 = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      s += v[ks][e];
+      s2 += v[ks][e] * v[ks][e];
+    }
+  const float mu = quad_sum(s) / C;
+  float var;
+  if constexpr (FAST) {
+    var = quad_sum(s2) / C - mu * mu;
+  } else {
+    float d2 = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float d = v[ks][e] - mu;
+        d2 += d * d;
+      }
+    var = quad_sum(d2) / C;
+  }
+  const float rs = rsqrtf(var + LN_EPS);
+  if (kg == 0) {
+    if (mean_out) mean_out[m0 + r] = mu;
+    if (rstd_out) rstd_out[m0 + r] = rs;
+  }
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    h16x8 af;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) af[e] = (h16)((v[ks][e] - mu) * rs);
+    acc = mfma16x16x32(af, bf[ks], acc);
+  }
+  if (r < H) {
+    // rows m0 + 4 kg + i: query q, keys k0 + i (k0 % 4 == 0, one 16-key tile)
+    const long m = m0 + 4 * kg;
+    const int q = (int)(m / bn), k0 = (int)(m % bn);
+    h16x4 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = (h16)((acc[i] + wc) * bias_scale);
+    *reinterpret_cast<h16x4*>(bias_out + bias_frag_index(r, q, k0, bn)) = o;
+  }
+}
+
+// Its backward with the residual add, dx[m] += LN'(gs * sum_h dbias[h][m]
+// W[c][h]) (C = 128, H <= 16), the bias term as an f32 MFMA product in the
+// forward's row-per-lane layout: the transposed product
+// G^T[c][m] = sum_h (gamma_c W_ch) dbias[h][m], one 16-channel block at a
+// time (v_mfma_f32_16x16x4_f32, K = 4 heads a step, A fragments pre-arranged
+// on the host by ln_bias_bwd_frags), leaves lane l with row m0 + (l & 15) and
+// channels 16 cb + 4 (l >> 4) + i (cb < 8, i < 4): the row sums of the
+// LayerNorm backward are two xor exchanges, and x and dx move in 16-byte
+// pieces.  Exact f32 arithmetic throughout.
+__global__ __launch_bounds__(256) void ln_bias16_bwd_kernel(
+    const float* __restrict__ x, long M, const float* __restrict__ mean,
+    const float* __restrict__ rstd, const float* __restrict__ afrag, int H,
+    const float* __restrict__ dbias, float* __restrict__ dx, const float* __restrict__ gmul) {
+  constexpr int C = 128;
+  const int lane = threadIdx.x & 63;
+  const long m0 = ((long)blockIdx.x * 4 + (threadIdx.x >> 6)) * 16;
+  if (m0 >= M) return;  // M % 16 == 0: whole waves
+  const int r = lane & 15, kg = lane >> 4;
+  const long row = (m0 + r) * C + 4 * kg;
+  float4 xv[8], dr[8];
+#pragma unroll
+  for (int cb = 0; cb < 8; ++cb) {
+    xv[cb] = *reinterpret_cast<const float4*>(x + row + 16 * cb);
+    dr[cb] = *reinterpret_cast<const float4*>(dx + row + 16 * cb);
+  }
+  const float mu = mean[m0 + r], rs = rstd[m0 + r];
+  const float gs = gmul ? *gmul : 1.f;
+  const int T = (H + 3) / 4;
+  float bv[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int h = 4 * t + kg;
+    bv[t] = (t < T && h < H) ? dbias[(long)h * M + m0 + r] : 0.f;
+  }
+  f32x4 g[8];
+#pragma unroll
+  for (int cb = 0; cb < 8; ++cb) {
+    g[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      if (t < T)
+        g[cb] = __builtin_amdgcn_mfma_f32_16x16x4f32(afrag[(t * 8 + cb) * 64 + lane], bv[t], g[cb],
+                                                     0, 0, 0);
+  }
+  float sg = 0.f, sgx = 0.f;
+#pragma unroll
+  for (int cb = 0; cb < 8; ++cb) {
+    const float xs[4] = {xv[cb].x, xv[cb].y, xv[cb].z, xv[cb].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      g[cb][i] *= gs;
+      sg += g[cb][i];
+      sgx += g[cb][i] * ((xs[i] - mu) * rs);
+    }
+  }
+  auto quad_sum = [](float a) {
+    a += __shfl_xor(a, 16, 64);
+    return a + __shfl_xor(a, 32, 64);
+  };
+  sg = quad_sum(sg) * (1.f / C);
+  sgx = quad_sum(sgx) * (1.f / C);
+#pragma unroll
+  for (int cb = 0; cb < 8; ++cb) {
+    const float xs[4] = {xv[cb].x, xv[cb].y, xv[cb].z, xv[cb].w};
+    float o[4] = {dr[cb].x, dr[cb].y, dr[cb].z, dr[cb].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] += rs * (g[cb][i] - sg - ((xs[i] - mu) * rs) * sgx);
+    *reinterpret_cast<float4*>(dx + row + 16 * cb) = make_float4(o[0], o[1], o[2], o[3]);
+  }
+}
+
 // dx[src(m)] = (ACC ? res[src(m)] : 0) + LN'(gs * (dy[m] + sum_h dbias[h][m] W[c][h]))
 // (dy may be null; res = dres, or dx itself when dres is null; gs = *gmul,
 // the inverse cotangent scale of the module, or 1 when gmul is null); U rows
@@ -400,6 +552,66 @@ void ln_fwd_f32(hipStream_t st, const float* x, long M, int C, int nt,
     case 256: ln_fwd_dispatch<256>(st, x, M, nt, gamma, beta, y, mean, rstd, fast, H, wb, bias_out, bs, bn); break;
     default: throw std::runtime_error("ln_fwd: unsupported channel count");
   }
+}
+
+std::vector<h16> ln_bias_frags(const float* gamma, const float* wb, int H) {
+  if (H <= 0 || H > 16) throw std::runtime_error("ln_bias_frags: 1 to 16 heads");
+  std::vector<h16> f(4 * 64 * 8);
+  for (int ks = 0; ks < 4; ++ks)
+    for (int l = 0; l < 64; ++l)
+      for (int e = 0; e < 8; ++e) {
+        const int c = ks * 32 + 8 * (l >> 4) + e, h = l & 15;
+        f[(ks * 64 + l) * 8 + e] = h < H ? (h16)(gamma[c] * wb[c * H + h]) : (h16)0.f;
+      }
+  return f;
+}
+
+std::vector<float> ln_bias_const(const float* beta, const float* wb, int H) {
+  if (H <= 0 || H > 16) throw std::runtime_error("ln_bias_const: 1 to 16 heads");
+  std::vector<float> b(16, 0.f);
+  for (int h = 0; h < H; ++h) {
+    double t = 0.0;
+    for (int c = 0; c < 128; ++c) t += (double)beta[c] * wb[c * H + h];
+    b[h] = (float)t;
+  }
+  return b;
+}
+
+std::vector<float> ln_bias_bwd_frags(const float* gamma, const float* wb, int H) {
+  if (H <= 0 || H > 16) throw std::runtime_error("ln_bias_bwd_frags: 1 to 16 heads");
+  std::vector<float> f(4 * 8 * 64, 0.f);
+  for (int t = 0; t < 4; ++t)
+    for (int cb = 0; cb < 8; ++cb)
+      for (int l = 0; l < 64; ++l) {
+        const int c = 16 * cb + (l & 15), h = 4 * t + (l >> 4);
+        if (h < H) f[(t * 8 + cb) * 64 + l] = gamma[c] * wb[c * H + h];
+      }
+  return f;
+}
+
+void ln_pair_bias_bwd_f32(hipStream_t st, const float* x, long M, const float* mean,
+                          const float* rstd, const float* afrag, int H, const float* dbias,
+                          float* dx, const float* gmul) {
+  if (M <= 0 || M % 16 != 0 || H <= 0 || H > 16 || !x || !mean || !rstd || !afrag || !dbias || !dx)
+    throw std::runtime_error("ln_pair_bias_bwd: M % 16 == 0, 1 to 16 heads");
+  const unsigned grid = (unsigned)((M / 16 + 3) / 4);
+  hipLaunchKernelGGL(ln_bias16_bwd_kernel, dim3(grid), dim3(256), 0, st, x, M, mean, rstd, afrag, H,
+                     dbias, dx, gmul);
+}
+
+void ln_pair_bias_f32(hipStream_t st, const float* x, long M, bool fast, float* mean, float* rstd,
+                      const h16* wfrag, const float* wconst, int H, h16* bias_out, float bs) {
+  int bn = 0;
+  while ((long)(bn + 1) * (bn + 1) <= M) ++bn;
+  if ((long)bn * bn != M || bn % 32 != 0 || H <= 0 || H > 16 || !x || !wfrag || !wconst || !bias_out)
+    throw std::runtime_error("ln_pair_bias: M = N*N with N % 32 == 0, 1 to 16 heads");
+  const unsigned grid = (unsigned)((M / 16 + 3) / 4);
+  if (fast)
+    hipLaunchKernelGGL(ln_bias16_kernel<true>, dim3(grid), dim3(256), 0, st, x, M, mean, rstd,
+                       wfrag, wconst, H, bias_out, bs, bn);
+  else
+    hipLaunchKernelGGL(ln_bias16_kernel<false>, dim3(grid), dim3(256), 0, st, x, M, mean, rstd,
+                       wfrag, wconst, H, bias_out, bs, bn);
 }
 
 template <int C, int H>

@@ -112,6 +112,10 @@ struct MsaRowW {
   AttnW a;
   int Cz = 0;
   const float *pn_g = nullptr, *pn_b = nullptr, *w2d = nullptr;
+  // the bias projection with the pair LayerNorm folded in (Cz = 128)
+  const h16* pb_frag = nullptr;
+  const float* pb_const = nullptr;
+  const float* pb_bwd_frag = nullptr;
 };
 struct MsaColW {
   AttnW a;

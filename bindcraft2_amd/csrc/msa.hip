@@ -351,6 +351,18 @@ MsaRowW msarow_weights(WeightStore& ws, const std::string& P) {
   w.pn_b = ws.f32(P + "feat_2d_norm/offset");
   w.w2d = ws.f32(P + "feat_2d_weights");
   w.Cz = ws.host(P + "feat_2d_weights").shape[0];
+  const int H = w.a.H;
+  if (w.Cz == 128 && H > 0 && H <= 16) {
+    const HostTensor& g = ws.host(P + "feat_2d_norm/scale");
+    const HostTensor& b = ws.host(P + "feat_2d_norm/offset");
+    const HostTensor& wt = ws.host(P + "feat_2d_weights");  // [Cz][H]
+    w.pb_frag = ws.derived<h16>("msarow.pb_frag:" + P,
+                                [&] { return ln_bias_frags(g.data.data(), wt.data.data(), H); });
+    w.pb_const = ws.derived<float>("msarow.pb_const:" + P,
+                                   [&] { return ln_bias_const(b.data.data(), wt.data.data(), H); });
+    w.pb_bwd_frag = ws.derived<float>(
+        "msarow.pb_bwd_frag:" + P, [&] { return ln_bias_bwd_frags(g.data.data(), wt.data.data(), H); });
+  }
   return w;
 }
 
@@ -396,8 +408,12 @@ void msarow_fwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa
     KTimed kt("msarow.ln", st);
     ln_fwd_f32(st, msa_in, R, Cm, 0, a.ln_g, a.ln_b, xn, sv.mean, sv.rstd, false, 0, nullptr,
                nullptr);
-    ln_fwd_f32(st, pair, M, w.Cz, 0, w.pn_g, w.pn_b, nullptr, sv.pmean, sv.prstd, false, H, w.w2d,
-               sv.bias, LOG2E);
+    if (w.pb_frag)
+      ln_pair_bias_f32(st, pair, M, false, sv.pmean, sv.prstd, w.pb_frag, w.pb_const, H, sv.bias,
+                       LOG2E);
+    else
+      ln_fwd_f32(st, pair, M, w.Cz, 0, w.pn_g, w.pn_b, nullptr, sv.pmean, sv.prstd, false, H,
+                 w.w2d, sv.bias, LOG2E);
   }
   qkvg_gemm(st, a, R, xn, sv.qkvg, LOG2E / std::sqrt((float)a.D), "msarow.gemm_qkvg");
   AttnArgs at;
@@ -480,8 +496,11 @@ void msarow_bwd_pair(hipStream_t st, const MsaRowW& w, int S, int N, const float
   Carver cv(const_cast<void*>(save));
   MsaRowSave<Carver> sv(cv, S, N, Cm, H);
   KTimed kt("msarow.ln_bwd_pair", st);
-  ln_bwd_f32(st, nullptr, pair, M, w.Cz, 0, w.pn_g, sv.pmean, sv.prstd, dpair, true, H, dbias,
-             w.w2d, nullptr, sc + 1);
+  if (w.pb_bwd_frag)
+    ln_pair_bias_bwd_f32(st, pair, M, sv.pmean, sv.prstd, w.pb_bwd_frag, H, dbias, dpair, sc + 1);
+  else
+    ln_bwd_f32(st, nullptr, pair, M, w.Cz, 0, w.pn_g, sv.pmean, sv.prstd, dpair, true, H, dbias,
+               w.w2d, nullptr, sc + 1);
 }
 
 void msarow_bwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa_in,
