@@ -234,6 +234,10 @@ struct BwdPipe {
   bool defer_opm = false;  // false: each block's OPM backward before the next block (replay tier)
   hipStream_t ms = nullptr;
   OpmPending opm;
+  // partial maxima of the last block's pair cotangent output amax_of, left
+  // in the pair lane's ct_fused_parts() by its last writer (amax_np of them)
+  long amax_np = 0;
+  const float* amax_of = nullptr;
 };
 
 namespace {
@@ -318,7 +322,11 @@ void block_bwd(hipStream_t st, const BlockW& B, const Layout& L, int b, const Ta
   float* sp = ct_scale_slot(two ? 4 + (b & 1) : 1);
   {
     KTimed kt("block.ct_scale", st);
-    ct_scale(st, dp_in, M * L.Cz, sp);
+    if (pipe && pipe->amax_np > 0 && pipe->amax_of == dp_in)
+      ct_scale_parts(st, ct_fused_parts(), pipe->amax_np, sp);
+    else
+      ct_scale(st, dp_in, M * L.Cz, sp);
+    if (pipe) pipe->amax_np = 0;
   }
   transition_bwd(st, B.ptr, M, N, p.p5, nullptr, p.ptr, dp_in, dp_out, sp);
   triattn_bwd(st, B.tae, true, N, p.p4, pmask, t.pair(b, 3), p.tae, dp_out, dp_out, sp);
@@ -334,12 +342,21 @@ void block_bwd(hipStream_t st, const BlockW& B, const Layout& L, int b, const Ta
     }
     transition_bwd(st, B.mtr, (long)S * N, N, p.m2, nullptr, p.mtr, dmsa, dmsa, sm);
     msacol_bwd(st, B.col, S, N, p.m1, mmask, nullptr, p.col, dmsa, dmsa, sm);
-    msarow_bwd(st, B.row, S, N, f.min, mmask, p.p1, t.row(b), p.row, dmsa, dmsa, dp_out, sm);
+    // the row attention's pair term is the block's last write of dp_out: its
+    // partial maxima serve the next block's pair scale
+    const long np = msarow_bwd(st, B.row, S, N, f.min, mmask, p.p1, t.row(b), p.row, dmsa, dmsa,
+                               dp_out, sm, pipe ? ct_fused_parts() : nullptr);
+    if (pipe) {
+      pipe->amax_np = np;
+      pipe->amax_of = dp_out;
+    }
     opm_bwd(st, B.opm, S, N, f.min, mmask, nullptr, p.opm, dp_out, dmsa, dmsa, sp);
     return;
   }
   stream_wait(st, pipe->ms);  // the pair-bias gradient (and the MSA side so far)
-  msarow_bwd_pair(st, B.row, S, N, p.p1, p.row, dbias, dp_out, sm);
+  // the block's last write of dp_out (the OPM backward only reads it)
+  pipe->amax_np = msarow_bwd_pair(st, B.row, S, N, p.p1, p.row, dbias, dp_out, sm, ct_fused_parts());
+  pipe->amax_of = dp_out;
   pipe->opm = OpmPending{true, &B.opm, f.min, p.opm, dp_out, sp};
   if (!pipe->defer_opm) {
     hipStream_t ms = pipe->ms;

@@ -20,10 +20,12 @@ constexpr int CT_SLOTS = 8;
 constexpr int CT_PART = 512;  // partial-maximum blocks (grid of the first pass)
 __device__ __align__(256) float g_ct_slots[CT_SLOTS * 2];
 __device__ __align__(256) float g_ct_part[NUM_LANES * CT_PART];
+__device__ __align__(256) float g_ct_fused[NUM_LANES * CT_FUSED];
 
 struct CtPtrs {
   float* slots = nullptr;
   float* part = nullptr;
+  float* fused = nullptr;
 };
 CtPtrs ct_ptrs() {
   static std::mutex mu;
@@ -34,11 +36,13 @@ CtPtrs ct_ptrs() {
   std::lock_guard<std::mutex> lk(mu);
   CtPtrs& p = per_dev[dev];
   if (!p.slots) {
-    void *a = nullptr, *b = nullptr;
+    void *a = nullptr, *b = nullptr, *c = nullptr;
     hip_check(hipGetSymbolAddress(&a, HIP_SYMBOL(g_ct_slots)), "hipGetSymbolAddress(slots)");
     hip_check(hipGetSymbolAddress(&b, HIP_SYMBOL(g_ct_part)), "hipGetSymbolAddress(part)");
+    hip_check(hipGetSymbolAddress(&c, HIP_SYMBOL(g_ct_fused)), "hipGetSymbolAddress(fused)");
     p.slots = static_cast<float*>(a);
     p.part = static_cast<float*>(b);
+    p.fused = static_cast<float*>(c);
   }
   return p;
 }
@@ -63,11 +67,21 @@ __global__ __launch_bounds__(256) void amax_part_kernel(const float* __restrict_
 
 // sc = {s, 1/s}: s = 2^(4 - e) for max|x| in (2^(e-1), 2^e], so s*max|x| is
 // in (8, 16]; s = 1 when x is all zero or its maximum is not finite.
-__global__ __launch_bounds__(64) void amax_final_kernel(const float* __restrict__ part, int np,
-                                                        float* __restrict__ sc) {
-  float m = 0.f;
-  for (int i = threadIdx.x; i < np; i += 64) m = fmaxf(m, part[i]);
-  m = group_max<64>(m);
+// One workgroup of 256; four independent loads a thread in flight (up to
+// CT_FUSED partials).
+__global__ __launch_bounds__(256) void amax_final_kernel(const float* __restrict__ part, int np,
+                                                         float* __restrict__ sc) {
+  float m4[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int i = threadIdx.x; i < np; i += 1024) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (i + 256 * u < np) m4[u] = fmaxf(m4[u], part[i + 256 * u]);
+  }
+  float m = group_max<64>(fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3])));
+  __shared__ float red[4];
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   if (threadIdx.x == 0) {
     float s = 1.f;
     if (m > 0.f && m <= 3.0e38f) {
@@ -93,7 +107,15 @@ void ct_scale(hipStream_t st, const float* x, long n, float* sc) {
   const int blocks = (int)std::min<long>(CT_PART, (n4 + 255) / 256);
   float* part = p.part + (size_t)lane() * CT_PART;
   hipLaunchKernelGGL(amax_part_kernel, dim3(blocks), dim3(256), 0, st, x, n4, part);
-  hipLaunchKernelGGL(amax_final_kernel, dim3(1), dim3(64), 0, st, part, blocks, sc);
+  hipLaunchKernelGGL(amax_final_kernel, dim3(1), dim3(256), 0, st, part, blocks, sc);
+}
+
+float* ct_fused_parts() { return ct_ptrs().fused + (size_t)lane() * CT_FUSED; }
+
+void ct_scale_parts(hipStream_t st, const float* part, long np, float* sc) {
+  if (!part || !sc || np <= 0 || np > CT_FUSED)
+    throw std::runtime_error("ct_scale_parts: 1 to CT_FUSED partial maxima");
+  hipLaunchKernelGGL(amax_final_kernel, dim3(1), dim3(256), 0, st, part, (int)np, sc);
 }
 
 // ----------------------------------------------------------------- zero fill

@@ -43,11 +43,15 @@ std::vector<float> ln_bias_const(const float* beta, const float* wb, int H);
 void ln_pair_bias_f32(hipStream_t st, const float* x, long M, bool fast, float* mean, float* rstd,
                       const h16* wfrag, const float* wconst, int H, h16* bias_out, float bias_scale);
 // Its backward, accumulated: dx[m] += LN'(gs * sum_h dbias[h*M+m] wb[c][h])
-// (gs = *gmul, 1 if null), afrag = ln_bias_bwd_frags(gamma, wb, H) (f32).
+// (gs = *gmul, 1 if null), afrag = ln_bias_bwd_frags(gamma, wb, H) (f32),
+// M % 64 == 0.  With amax_part (room for amax_cap floats) the partial maxima
+// of |dx| for ct_scale_parts, one a 64 rows; returns their count (0: none
+// written, the grid exceeds amax_cap).
 std::vector<float> ln_bias_bwd_frags(const float* gamma, const float* wb, int H);
-void ln_pair_bias_bwd_f32(hipStream_t st, const float* x, long M, const float* mean,
+long ln_pair_bias_bwd_f32(hipStream_t st, const float* x, long M, const float* mean,
                           const float* rstd, const float* afrag, int H, const float* dbias,
-                          float* dx, const float* gmul);
+                          float* dx, const float* gmul, float* amax_part = nullptr,
+                          long amax_cap = 0);
 // dx[src(m)] (+)= LN-backward(gs * (dy[m] + sum_h dbias[h*M+m] * wb[c*H+h])).
 // acc: dx = res + LN'(...) with res = dres, or dx itself when dres is null.
 // gs = *gmul (device scalar: a module's inverse cotangent scale), 1 if null.
@@ -138,6 +142,12 @@ void zero_f32(hipStream_t st, float* p, long n);
 // embedding).  No allocation.
 void ct_scale(hipStream_t st, const float* x, long n, float* sc);
 float* ct_scale_slot(int k);
+// The same scale from partial maxima a producing kernel wrote (np of them at
+// ct_fused_parts()): the final reduction alone.  ct_fused_parts is the
+// calling lane's region of CT_FUSED floats (file-scope device memory).
+constexpr long CT_FUSED = 16384;
+float* ct_fused_parts();
+void ct_scale_parts(hipStream_t st, const float* part, long np, float* sc);
 
 // ---------------------------------------------------------------- dropout
 // Shared-dropout keep/scale table for one module: tbl[b*C+c] = keep/keep_rate

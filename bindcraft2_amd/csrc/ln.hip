@@ -217,15 +217,18 @@ __global__ __launch_bounds__(256) void ln_bias16_kernel(
 // on the host by ln_bias_bwd_frags), leaves lane l with row m0 + (l & 15) and
 // channels 16 cb + 4 (l >> 4) + i (cb < 8, i < 4): the row sums of the
 // LayerNorm backward are two xor exchanges, and x and dx move in 16-byte
-// pieces.  Exact f32 arithmetic throughout.
+// pieces.  Exact f32 arithmetic throughout.  With amax_part, the
+// workgroup's max |dx| of its 64 rows goes to amax_part[blockIdx.x] (the
+// partial maxima of the next cotangent scale, saving that pass its read).
 __global__ __launch_bounds__(256) void ln_bias16_bwd_kernel(
     const float* __restrict__ x, long M, const float* __restrict__ mean,
     const float* __restrict__ rstd, const float* __restrict__ afrag, int H,
-    const float* __restrict__ dbias, float* __restrict__ dx, const float* __restrict__ gmul) {
+    const float* __restrict__ dbias, float* __restrict__ dx, const float* __restrict__ gmul,
+    float* __restrict__ amax_part) {
   constexpr int C = 128;
   const int lane = threadIdx.x & 63;
+  // M % 64 == 0 and the grid is exact (host): every wave has its 16 rows
   const long m0 = ((long)blockIdx.x * 4 + (threadIdx.x >> 6)) * 16;
-  if (m0 >= M) return;  // M % 16 == 0: whole waves
   const int r = lane & 15, kg = lane >> 4;
   const long row = (m0 + r) * C + 4 * kg;
   float4 xv[8], dr[8];
@@ -270,13 +273,25 @@ __global__ __launch_bounds__(256) void ln_bias16_bwd_kernel(
   };
   sg = quad_sum(sg) * (1.f / C);
   sgx = quad_sum(sgx) * (1.f / C);
+  float am = 0.f;
 #pragma unroll
   for (int cb = 0; cb < 8; ++cb) {
     const float xs[4] = {xv[cb].x, xv[cb].y, xv[cb].z, xv[cb].w};
     float o[4] = {dr[cb].x, dr[cb].y, dr[cb].z, dr[cb].w};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] += rs * (g[cb][i] - sg - ((xs[i] - mu) * rs) * sgx);
+    for (int i = 0; i < 4; ++i) {
+      o[i] += rs * (g[cb][i] - sg - ((xs[i] - mu) * rs) * sgx);
+      am = fmaxf(am, fabsf(o[i]));
+    }
     *reinterpret_cast<float4*>(dx + row + 16 * cb) = make_float4(o[0], o[1], o[2], o[3]);
+  }
+  if (amax_part) {  // the same maximum as amax_part_kernel's (fmaxf of |dx|)
+    am = group_max<64>(am);
+    __shared__ float red[4];
+    if (lane == 0) red[threadIdx.x >> 6] = am;
+    __syncthreads();
+    if (threadIdx.x == 0)
+      amax_part[blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   }
 }
 
@@ -589,14 +604,16 @@ std::vector<float> ln_bias_bwd_frags(const float* gamma, const float* wb, int H)
   return f;
 }
 
-void ln_pair_bias_bwd_f32(hipStream_t st, const float* x, long M, const float* mean,
+long ln_pair_bias_bwd_f32(hipStream_t st, const float* x, long M, const float* mean,
                           const float* rstd, const float* afrag, int H, const float* dbias,
-                          float* dx, const float* gmul) {
-  if (M <= 0 || M % 16 != 0 || H <= 0 || H > 16 || !x || !mean || !rstd || !afrag || !dbias || !dx)
-    throw std::runtime_error("ln_pair_bias_bwd: M % 16 == 0, 1 to 16 heads");
-  const unsigned grid = (unsigned)((M / 16 + 3) / 4);
-  hipLaunchKernelGGL(ln_bias16_bwd_kernel, dim3(grid), dim3(256), 0, st, x, M, mean, rstd, afrag, H,
-                     dbias, dx, gmul);
+                          float* dx, const float* gmul, float* amax_part, long amax_cap) {
+  if (M <= 0 || M % 64 != 0 || H <= 0 || H > 16 || !x || !mean || !rstd || !afrag || !dbias || !dx)
+    throw std::runtime_error("ln_pair_bias_bwd: M % 64 == 0, 1 to 16 heads");
+  const long grid = M / 64;
+  if (grid > amax_cap) amax_part = nullptr;
+  hipLaunchKernelGGL(ln_bias16_bwd_kernel, dim3((unsigned)grid), dim3(256), 0, st, x, M, mean, rstd,
+                     afrag, H, dbias, dx, gmul, amax_part);
+  return amax_part ? grid : 0;
 }
 
 void ln_pair_bias_f32(hipStream_t st, const float* x, long M, bool fast, float* mean, float* rstd,

@@ -128,17 +128,22 @@ void msarow_fwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa
                 const float* msa_mask, const float* pair, const float* tbl, float* msa_out,
                 void* save);
 // dpair is accumulated (+=), dmsa_in = dmsa_out + J^T(...)
-void msarow_bwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa_in,
+// With amax_part (room for CT_FUSED floats, the calling lane's
+// ct_fused_parts()): also the partial maxima of the final dpair for
+// ct_scale_parts; returns their count (0: none written).
+long msarow_bwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa_in,
                 const float* msa_mask, const float* pair, const float* tbl, const void* save,
-                const float* dmsa_out, float* dmsa_in, float* dpair, const float* sc = nullptr);
+                const float* dmsa_out, float* dmsa_in, float* dpair, const float* sc = nullptr,
+                float* amax_part = nullptr);
 // msarow_bwd in two halves: everything but the pair term (returns the pair
 // bias gradient [H][N][N], in the calling lane's arena until its next call;
 // sc required), then dpair += the pair LayerNorm's backward of it.
 const float* msarow_bwd_msa(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa_in,
                             const float* msa_mask, const float* tbl, const void* save,
                             const float* dmsa_out, float* dmsa_in, const float* sc);
-void msarow_bwd_pair(hipStream_t st, const MsaRowW& w, int S, int N, const float* pair,
-                     const void* save, const float* dbias, float* dpair, const float* sc);
+long msarow_bwd_pair(hipStream_t st, const MsaRowW& w, int S, int N, const float* pair,
+                     const void* save, const float* dbias, float* dpair, const float* sc,
+                     float* amax_part = nullptr);
 void msacol_fwd(hipStream_t st, const MsaColW& w, int S, int N, const float* msa_in,
                 const float* msa_mask, const float* tbl, float* msa_out, void* save);
 void msacol_bwd(hipStream_t st, const MsaColW& w, int S, int N, const float* msa_in,

@@ -486,8 +486,9 @@ const float* msarow_bwd_msa(hipStream_t st, const MsaRowW& w, int S, int N, cons
 
 // The pair term: dpair += the pair LayerNorm's backward of the bias
 // projection's gradient (the only way the pair enters the row attention).
-void msarow_bwd_pair(hipStream_t st, const MsaRowW& w, int S, int N, const float* pair,
-                     const void* save, const float* dbias, float* dpair, const float* sc) {
+long msarow_bwd_pair(hipStream_t st, const MsaRowW& w, int S, int N, const float* pair,
+                     const void* save, const float* dbias, float* dpair, const float* sc,
+                     float* amax_part) {
   nonnull(pair, "msarow pair"); nonnull(save, "msarow save"); nonnull(dbias, "msarow dbias");
   nonnull(dpair, "msarow dpair");
   const AttnW& a = w.a;
@@ -497,15 +498,17 @@ void msarow_bwd_pair(hipStream_t st, const MsaRowW& w, int S, int N, const float
   MsaRowSave<Carver> sv(cv, S, N, Cm, H);
   KTimed kt("msarow.ln_bwd_pair", st);
   if (w.pb_bwd_frag)
-    ln_pair_bias_bwd_f32(st, pair, M, sv.pmean, sv.prstd, w.pb_bwd_frag, H, dbias, dpair, sc + 1);
-  else
-    ln_bwd_f32(st, nullptr, pair, M, w.Cz, 0, w.pn_g, sv.pmean, sv.prstd, dpair, true, H, dbias,
-               w.w2d, nullptr, sc + 1);
+    return ln_pair_bias_bwd_f32(st, pair, M, sv.pmean, sv.prstd, w.pb_bwd_frag, H, dbias, dpair,
+                                sc + 1, amax_part, amax_part ? CT_FUSED : 0);
+  ln_bwd_f32(st, nullptr, pair, M, w.Cz, 0, w.pn_g, sv.pmean, sv.prstd, dpair, true, H, dbias,
+             w.w2d, nullptr, sc + 1);
+  return 0;
 }
 
-void msarow_bwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa_in,
+long msarow_bwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa_in,
                 const float* msa_mask, const float* pair, const float* tbl, const void* save,
-                const float* dmsa_out, float* dmsa_in, float* dpair, const float* sc) {
+                const float* dmsa_out, float* dmsa_in, float* dpair, const float* sc,
+                float* amax_part) {
   nonnull(pair, "msarow pair"); nonnull(dpair, "msarow dpair");
   nonnull(dmsa_out, "msarow dout");
   Arena& ar = arena();
@@ -513,7 +516,7 @@ void msarow_bwd(hipStream_t st, const MsaRowW& w, int S, int N, const float* msa
   sc = module_scale(st, sc, dmsa_out, (long)S * N * w.a.Cin);
   const float* dbias = msarow_bwd_msa(st, w, S, N, msa_in, msa_mask, tbl, save, dmsa_out, dmsa_in,
                                       sc);
-  msarow_bwd_pair(st, w, S, N, pair, save, dbias, dpair, sc);
+  return msarow_bwd_pair(st, w, S, N, pair, save, dbias, dpair, sc, amax_part);
 }
 
 void msacol_fwd(hipStream_t st, const MsaColW& w, int S, int N, const float* msa_in,
