@@ -29,7 +29,7 @@ struct Args {
   const float* x;
   const float *g, *b, *wb;  // LayerNorm scale, offset; bias weights [C][H]
   float bscale;
-  h16* xn;
+  h16* xn;  // LayerNorm output (written when not null); the input rows when LN = false
   float *mean, *rstd;
   h16* bias;  // [H][M] binary16 in score-fragment order
   const h16* W;  // [nout][C] in b_frags_k128 order
@@ -122,7 +122,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         if (l16 == h) mine = q;
       }
       if (m < M) {
-        st8(a.xn + m * C + c0, ob);
+        if (a.xn) st8(a.xn + m * C + c0, ob);
         if (l16 == 0) {
           a.mean[m] = mu;
           a.rstd[m] = rs;

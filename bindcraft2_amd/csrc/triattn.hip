@@ -122,7 +122,8 @@ static void triattn_fwd_with(hipStream_t st, const TriAttnW& w, bool per_column,
     lnproj::Args la{};
     la.M = M; la.nt = per_column ? N : 0; la.bn = N; la.nout = 4 * HD;
     la.x = pair_in; la.g = w.ln_g; la.b = w.ln_b; la.wb = w.w2d; la.bscale = LOG2E;
-    la.xn = xn; la.mean = sv.mean; la.rstd = sv.rstd; la.bias = sv.bias; la.W = w.wqkvg_frag;
+    // xn stays on chip: the backward's LayerNorm term reads pair_in, mean and rstd
+    la.xn = nullptr; la.mean = sv.mean; la.rstd = sv.rstd; la.bias = sv.bias; la.W = w.wqkvg_frag;
     KTimed kt(BC2N_TN(C, "triattn.ln_qkvg"), st);
     if (H != 4) throw std::runtime_error("triattn: the fused LayerNorm-projection takes 4 bias heads");
     lnproj::launch<4, false>(st, la, EpiScaledCols(sv.qkvg, 4L * HD, w.bqkvg, qscale, HD));
