@@ -155,5 +155,9 @@ def test_design_step_seq_L224(cuda):
     # edge or glycine rule moves most of the 15-bin histogram instead
     live = int((m1 > 0).sum()) ** 2
     assert flips["n"] <= 0.02 * live, f"{flips['n']} distogram bins differ"
+    # the first pass's atoms (one trunk pass and the structure module) at the
+    # activation bar; the recycled pass compounds two passes' roundings
+    fa = flips["atoms"]
+    assert fa["max_rel"] <= 2e-2 and fa["rel_l2"] <= 2e-2 and fa["cos"] >= 0.9999, fa
     assert not bad, f"outside the bars: {bad}"
     _say(f"  total {time.time() - t0:.0f}s")
