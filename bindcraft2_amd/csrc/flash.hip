@@ -2021,7 +2021,7 @@ static void attn_bwd_t(hipStream_t st, const AttnBwdArgs& b0) {
     });
   }
 dkv_done:
-  if (b.dbias && a.bias && !one_chunk) {
+  if (b.dbias && a.bias && !one_chunk && !b.dbias_deferred) {
     if (!b.dbias_part) throw std::runtime_error("attention bwd: missing dbias scratch");
     const long n = (long)a.H * a.N * a.N;
     KTimed kt(timer_name(4, a), st);

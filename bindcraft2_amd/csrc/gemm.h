@@ -767,7 +767,9 @@ struct ALoadRelu16 {
 //   g = gs * gamma * (dy + sum_h dbias[h][m] wb[c][h]),  xhat = (x[src] - mean) * rstd,
 // src = ln_src_row(m, nt) (the transposed orientation when nt > 0), gs =
 // *gmul (the module's inverse cotangent scale; 1 when null).  dres may alias
-// out.  16 lanes per row (a DPP row), 8 channels each.
+// out.  16 lanes per row (a DPP row), 8 channels each.  dbias may be given as
+// dbias_nch partials [nch][H][M], added here in chunk order (the attention
+// backward's deferred reduction; the same sums as its reduction kernel).
 template <int H>
 struct EpiLnBwd : EpiRows {
   static constexpr bool kRowBlock = true;
@@ -776,11 +778,12 @@ struct EpiLnBwd : EpiRows {
   float* out;
   long M;
   int nt;
+  int dbias_nch = 1;
   EpiLnBwd(const float* x_, const float* g_, const float* mu_, const float* rs_, const float* dres_,
            float* out_, long M_, int nt_, const float* dbias_ = nullptr, const float* wb_ = nullptr,
-           const float* gmul_ = nullptr)
+           const float* gmul_ = nullptr, int dbias_nch_ = 1)
       : x(x_), gamma(g_), mean(mu_), rstd(rs_), dres(dres_), dbias(dbias_), wb(wb_), gmul(gmul_),
-        out(out_), M(M_), nt(nt_) {}
+        out(out_), M(M_), nt(nt_), dbias_nch(dbias_nch_) {}
   __device__ __forceinline__ void row(int, int, int, const float (&)[8]) const {}
   template <int WM>
   __device__ __forceinline__ void block(int, long mb, const float* T, int ldt, int tid) const {
@@ -821,11 +824,46 @@ struct EpiLnBwd : EpiRows {
         ld_f8(x + src[q] * C + c0, xv[q]);
         ld_f8(dres + src[q] * C + c0, dr[q]);
         if constexpr (H > 0) {
+          if (dbias_nch == 1) {
 #pragma unroll
-          for (int h = 0; h < H; ++h) db[q][h] = dbias[(long)h * M + m];
+            for (int h = 0; h < H; ++h) db[q][h] = dbias[(long)h * M + m];
+          } else if constexpr (G * H != 16) {
+#pragma unroll
+            for (int h = 0; h < H; ++h) {
+              float s = 0.f;
+              for (int c = 0; c < dbias_nch; ++c) s += dbias[((long)c * H + h) * M + m];
+              db[q][h] = s;
+            }
+          }
         }
         mu[q] = mean[m];
         rs[q] = rstd[m];
+      }
+      if constexpr (H > 0 && G * H == 16) {
+        if (dbias_nch > 1) {
+          // lane c0 / 8 = 4 q + h of the row group adds the partials of
+          // (row q, head h) in chunk order, eight loads in flight; the row
+          // group then shares the 16 sums
+          const int own = (tid & 15), oq = own / H, oh = own % H;
+          const long om = min(mb + r0 + 16 * oq + lr, M - 1);
+          const float* p = dbias + (long)oh * M + om;
+          const long cs = (long)H * M;
+          float s = 0.f;
+          int c = 0;
+          for (; c + 8 <= dbias_nch; c += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = p[(c + u) * cs];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) s += v[u];
+          }
+          for (; c < dbias_nch; ++c) s += p[c * cs];
+          const int base = tid & 48;  // the row group's first lane in the wave
+#pragma unroll
+          for (int q = 0; q < G; ++q)
+#pragma unroll
+            for (int h = 0; h < H; ++h) db[q][h] = __shfl(s, base + q * H + h, 64);
+        }
       }
 #pragma unroll
       for (int q = 0; q < G; ++q) {

@@ -107,6 +107,10 @@ struct AttnBwdArgs {
   // dO, nDsum and the gate gradient already written by the caller (the
   // d(og) GEMM's EpiGateBwd epilogue); dog is then not read
   bool gate_done = false;
+  // the caller adds the attn_bwd_nchunk partials itself (in chunk order, as
+  // the reduction would): no reduction launch; with one chunk the partial is
+  // dbias itself
+  bool dbias_deferred = false;
 };
 void attn_bwd(hipStream_t st, const AttnBwdArgs& a);
 int attn_bwd_nchunk(int R, int rows_per_chunk);

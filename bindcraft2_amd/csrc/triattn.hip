@@ -283,6 +283,7 @@ void triattn_bwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
   a.o = sv.o; a.og = nullptr; a.ldo = HD;
   a.lse = sv.lse;
   b.scale = 1.f / std::sqrt((float)w.D);
+  b.dbias_deferred = C == 128 && H == 4;  // the dX product's epilogue adds the partials
   attn_bwd(st, b);
 
   GemmArgs g2;
@@ -290,11 +291,13 @@ void triattn_bwd(hipStream_t st, const TriAttnW& w, bool per_column, int N,
   g2.A = b.dqkvg; g2.a_sm = 4L * HD; g2.a_sk = 1;
   g2.B = w.wqkvg; g2.b_sn = 4L * HD; g2.b_sk = 1;
   if (C == 128 && H == 4) {
-    // the input LayerNorm's backward (with the pair-bias projection's term)
-    // and the residual add in the epilogue
+    // the input LayerNorm's backward (with the pair-bias projection's term,
+    // its per-chunk partials added in the epilogue: attn_bwd launched no
+    // reduction) and the residual add in the epilogue
+    const float* dbp = nch == 1 ? b.dbias : b.dbias_part;
     gemm<128, 128>(st, g2,
                    EpiLnBwd<4>(pair_in, w.ln_g, sv.mean, sv.rstd, dout, din, M, per_column ? N : 0,
-                               b.dbias, w.w2d, sc + 1),
+                               dbp, w.w2d, sc + 1, nch),
                    BC2N_TN(C, "triattn.gemm_dx_ln"));
     return;
   }
