@@ -90,6 +90,16 @@ struct epi_row_block : std::false_type {};
 template <class E>
 struct epi_row_block<E, std::void_t<decltype(E::kRowBlock)>> : std::bool_constant<E::kRowBlock> {};
 
+// A row-block epilogue with kProRowFloats > 0 also has a prologue:
+// prologue<BM>(m0, pro, tid) fills pro[BM][kProRowFloats] (LDS) for the
+// tile's rows while the first operand tiles load, and block() then takes
+// pro + (mb - m0) * kProRowFloats as its last argument.
+template <class E, class = void>
+struct epi_pro_floats : std::integral_constant<int, 0> {};
+template <class E>
+struct epi_pro_floats<E, std::void_t<decltype(E::kProRowFloats)>>
+    : std::integral_constant<int, E::kProRowFloats> {};
+
 // Base of every epilogue: row mode only.
 struct EpiRows {
   static constexpr bool kHasCol = false;
@@ -292,7 +302,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi, AL al = 
     for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int nk = g.K / BK;
+  constexpr int PRO = epi_pro_floats<Epi>::value;
+  __shared__ float pro[PRO > 0 ? BM * PRO : 1];
   gload(0);
+  if constexpr (PRO > 0) epi.template prologue<BM>(m0, pro, tid);
   sstore(0);
   __syncthreads();
   const int fr = lane & 15, fk = (lane >> 4) * 8;
@@ -359,7 +372,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi, AL al = 
       }
     };
     if constexpr (epi_row_block<Epi>::value) {
-      epi.template block<WM>(b, mb, T, LDT, tid);
+      if constexpr (PRO > 0) epi.template block<WM>(b, mb, T, LDT, tid, pro + (mb - m0) * PRO);
+      else epi.template block<WM>(b, mb, T, LDT, tid);
     } else if (colm) {
       for (int it = tid; it < BN * (WM / 8); it += 256) {
         const int c = it % BN, rg = it / BN;
@@ -779,14 +793,58 @@ struct EpiLnBwd : EpiRows {
   long M;
   int nt;
   int dbias_nch = 1;
+  // the bias term's per-row head sums, made in the GEMM's prologue
+  static constexpr int kProRowFloats = H;
   EpiLnBwd(const float* x_, const float* g_, const float* mu_, const float* rs_, const float* dres_,
            float* out_, long M_, int nt_, const float* dbias_ = nullptr, const float* wb_ = nullptr,
            const float* gmul_ = nullptr, int dbias_nch_ = 1)
       : x(x_), gamma(g_), mean(mu_), rstd(rs_), dres(dres_), dbias(dbias_), wb(wb_), gmul(gmul_),
         out(out_), M(M_), nt(nt_), dbias_nch(dbias_nch_) {}
   __device__ __forceinline__ void row(int, int, int, const float (&)[8]) const {}
+  // pro[r][h] = dbias of row m0 + r, head h: the partials added in chunk
+  // order, eight loads in flight (the sums of the attention backward's
+  // reduction kernel); rows past M take row M - 1's
+  template <int BM>
+  __device__ __forceinline__ void prologue(long m0, float* pro, int tid) const {
+    if constexpr (H > 0) {
+      static_assert(BM * H % 256 == 0, "whole sums a thread");
+      constexpr int PT = BM * H / 256;
+      const long cs = (long)H * M;
+      float s[PT];
+      const float* p[PT];
+#pragma unroll
+      for (int i = 0; i < PT; ++i) {
+        const int e = tid + 256 * i, r = e / H, h = e % H;
+        p[i] = dbias + (long)h * M + min(m0 + r, M - 1);
+        s[i] = 0.f;
+      }
+      if (dbias_nch == 1) {
+#pragma unroll
+        for (int i = 0; i < PT; ++i) s[i] = *p[i];
+      } else {
+        int c = 0;
+        for (; c + 8 <= dbias_nch; c += 8) {
+          float v[PT][8];
+#pragma unroll
+          for (int i = 0; i < PT; ++i)
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[i][u] = p[i][(c + u) * cs];
+#pragma unroll
+          for (int i = 0; i < PT; ++i)
+#pragma unroll
+            for (int u = 0; u < 8; ++u) s[i] += v[i][u];
+        }
+        for (; c < dbias_nch; ++c)
+#pragma unroll
+          for (int i = 0; i < PT; ++i) s[i] += p[i][c * cs];
+      }
+#pragma unroll
+      for (int i = 0; i < PT; ++i) pro[tid + 256 * i] = s[i];
+    }
+  }
   template <int WM>
-  __device__ __forceinline__ void block(int, long mb, const float* T, int ldt, int tid) const {
+  __device__ __forceinline__ void block(int, long mb, const float* T, int ldt, int tid,
+                                        const float* pro = nullptr) const {
     const int lr = tid >> 4, c0 = (tid & 15) * 8;
     float gm[8];
     ld_f8(gamma + c0, gm);
@@ -824,12 +882,13 @@ struct EpiLnBwd : EpiRows {
         ld_f8(x + src[q] * C + c0, xv[q]);
         ld_f8(dres + src[q] * C + c0, dr[q]);
         if constexpr (H > 0) {
-          if (dbias_nch == 1) {
 #pragma unroll
-            for (int h = 0; h < H; ++h) db[q][h] = dbias[(long)h * M + m];
-          } else if constexpr (G * H != 16) {
-#pragma unroll
-            for (int h = 0; h < H; ++h) {
+          for (int h = 0; h < H; ++h) {
+            if (pro) {
+              db[q][h] = pro[(r0 + 16 * q + lr) * H + h];
+            } else if (dbias_nch == 1) {
+              db[q][h] = dbias[(long)h * M + m];
+            } else {
               float s = 0.f;
               for (int c = 0; c < dbias_nch; ++c) s += dbias[((long)c * H + h) * M + m];
               db[q][h] = s;
@@ -838,32 +897,6 @@ struct EpiLnBwd : EpiRows {
         }
         mu[q] = mean[m];
         rs[q] = rstd[m];
-      }
-      if constexpr (H > 0 && G * H == 16) {
-        if (dbias_nch > 1) {
-          // lane c0 / 8 = 4 q + h of the row group adds the partials of
-          // (row q, head h) in chunk order, eight loads in flight; the row
-          // group then shares the 16 sums
-          const int own = (tid & 15), oq = own / H, oh = own % H;
-          const long om = min(mb + r0 + 16 * oq + lr, M - 1);
-          const float* p = dbias + (long)oh * M + om;
-          const long cs = (long)H * M;
-          float s = 0.f;
-          int c = 0;
-          for (; c + 8 <= dbias_nch; c += 8) {
-            float v[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = p[(c + u) * cs];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) s += v[u];
-          }
-          for (; c < dbias_nch; ++c) s += p[c * cs];
-          const int base = tid & 48;  // the row group's first lane in the wave
-#pragma unroll
-          for (int q = 0; q < G; ++q)
-#pragma unroll
-            for (int h = 0; h < H; ++h) db[q][h] = __shfl(s, base + q * H + h, 64);
-        }
       }
 #pragma unroll
       for (int q = 0; q < G; ++q) {
