@@ -109,6 +109,9 @@ def kernel_model(name, n):
         "trimul.gemm_proj": (gemm(c, 5 * c), m * (2 * c + 4 * c + 2 * c + 4)),
         "trimul.proj_bwd": (gemm(c, 4 * c), m * (2 * c + 4 * c + 4 + 8 * c)),
         "trimul.gemm_out": (gemm(c, c), m * (2 * c + 2 * c + 4 * c + 2 * c + 4 * c)),
+        # centre norm + output projection in one kernel (C = 128): T read (f32),
+        # statistics, then the output epilogue's traffic
+        "trimul.ln_out": (gemm(c, c), m * (4 * c + 8 + 2 * c + 4 * c + 2 * c + 4 * c)),
         "trimul.gemm_dout": (gemm(c, c), m * (4 * c + 2 * c + 2 * c + 4 * c + 2 * c)),
         "trimul.gemm_dx": (gemm(5 * c, c), m * (10 * c + 4 * c)),
         # recompute GEMM + d(cat) + dX GEMM + LayerNorm backward: xn, d(left|right),
@@ -311,6 +314,7 @@ def traffic_of(kernel, n):
            "trans.fused_fwd": r"^fused<.*EpiResidualRows|fused_kernel.*EpiResidualRows",
            "trans.fused_bwd": r"^fused<.*EpiLnBwd|fused_kernel.*EpiLnBwd",
            "trimul.gemm_out": r"EpiTrimulOut",
+           "trimul.ln_out": r"EpiTrimulOut",
            "triattn.gemm_dx_ln": r"EpiLnBwd<4>|EpiLnBwdILi4E",
            "trimul.contract_fwd": rf"contract(_kernel)?(<{nb}, .*float>|ILi{nb}E.*fEE)",
            "trimul.contract_bwd": rf"contract(_kernel)?(<{nb}, .*_Float16>|ILi{nb}E.*DF16_EE)"}.get(kernel)

@@ -36,7 +36,10 @@ struct Args {
 };
 
 // LN = false: no LayerNorm; the binary16 rows are read from a.xn as they are.
-template <int H, bool FAST, class Epi, bool LN = true>
+// CM: the input is channel-major ([C][M], trimul's contraction output) and
+// the LayerNorm is the centre norm's (ln_fwd_cm: eight lanes a row with 16
+// consecutive channels each, the same sums in the same order), no xn.
+template <int H, bool FAST, class Epi, bool LN = true, bool CM = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void kernel(Args a,
                                                                                            Epi epi) {
   __shared__ __align__(16) h16 xs[BM * LDX];
@@ -64,6 +67,63 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     for (int p = 0; p < RT; ++p) {
       const int r = p * 16 + w * 4 + lr;
       st8(xs + r * LDX + c0, m0 + r < M ? ob[p] : h16x8{});
+    }
+  } else if constexpr (CM) {
+    // the [C][BM] tile through T (rows past M read as zero), then the rows
+    static_assert(H == 0 && BM % 4 == 0, "centre norm: no bias heads");
+    load_b(0);
+    for (int i = tid; i < C * (BM / 4); i += 256) {
+      const int c = i / (BM / 4), q = (i % (BM / 4)) * 4;
+      const long m = m0 + q;
+      float4 v4 = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (m < M) v4 = *reinterpret_cast<const float4*>(a.x + (long)c * M + m);  // M % 4 == 0
+      T[(q + 0) * LDT + c] = v4.x;
+      T[(q + 1) * LDT + c] = v4.y;
+      T[(q + 2) * LDT + c] = v4.z;
+      T[(q + 3) * LDT + c] = v4.w;
+    }
+    __syncthreads();
+    constexpr int P = 8, CPL = C / P;  // lanes and channels a row
+#pragma unroll
+    for (int rb = 0; rb < BM; rb += 256 / P) {
+      const int r = rb + tid / P, part = tid % P;
+      if (r < BM) {  // whole 8-lane groups
+        const long m = m0 + r;
+        float v[CPL];
+        float s = 0.f, s2 = 0.f;
+#pragma unroll
+        for (int e = 0; e < CPL; ++e) {
+          v[e] = T[r * LDT + part * CPL + e];
+          s += v[e];
+          s2 += v[e] * v[e];
+        }
+        s = group_sum<P>(s);
+        const float mu = s / C;
+        float var;
+        if (FAST) {
+          var = group_sum<P>(s2) / C - mu * mu;
+        } else {
+          float d2 = 0.f;
+#pragma unroll
+          for (int e = 0; e < CPL; ++e) { const float d = v[e] - mu; d2 += d * d; }
+          var = group_sum<P>(d2) / C;
+        }
+        const float rs = rsqrtf(var + LN_EPS);
+#pragma unroll
+        for (int e0 = 0; e0 < CPL; e0 += 8) {
+          h16x8 ob;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int c = part * CPL + e0 + e;
+            ob[e] = (h16)((v[e0 + e] - mu) * rs * a.g[c] + a.b[c]);
+          }
+          st8(xs + r * LDX + part * CPL + e0, m < M ? ob : h16x8{});
+        }
+        if (part == 0 && m < M) {
+          a.mean[m] = mu;
+          a.rstd[m] = rs;
+        }
+      }
     }
   } else {
     const int lr = lane >> 4, c0 = l16 * 8;
@@ -204,6 +264,15 @@ void launch(hipStream_t st, const Args& a, const Epi& epi) {
     throw std::runtime_error("LayerNorm-projection: shape");
   const dim3 grid((unsigned)((a.M + BM - 1) / BM));
   hipLaunchKernelGGL((kernel<H, FAST, Epi>), grid, dim3(256), 0, st, a, epi);
+}
+// The centre norm of a channel-major input (a.x = [C][M] f32, the statistics
+// to a.mean / a.rstd) fused with the product; FAST: the one-pass variance.
+template <bool FAST, class Epi>
+void launch_cm(hipStream_t st, const Args& a, const Epi& epi) {
+  if (a.M <= 0 || a.M % 8 != 0 || a.nout % 128 != 0 || !a.x || !a.W || !a.mean || !a.rstd)
+    throw std::runtime_error("centre-norm projection: shape");
+  const dim3 grid((unsigned)((a.M + BM - 1) / BM));
+  hipLaunchKernelGGL((kernel<0, FAST, Epi, true, true>), grid, dim3(256), 0, st, a, epi);
 }
 // The same product without the LayerNorm: rows = a.xn (binary16 [M][128]).
 template <class Epi>

@@ -635,11 +635,21 @@ void trimul_fwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
     gemm<128, 128>(st, g1, proj, BC2N_TN(C, "trimul.gemm_proj"));
   }
   contraction_fwd(st, outgoing, N, I, sv.left, sv.right, sv.T);
+  const EpiTrimulOut out(pair_in, pair_out, w.bo, sv.gout, sv.osave, tbl, N, C);
+  if (w.wo_frag && I == lnproj::C) {
+    // the centre norm and the output projection in one kernel: the normalised
+    // rows stay on chip (the same statistics and binary16 rows as ln_fwd_cm)
+    lnproj::Args la{};
+    la.M = M; la.nout = C; la.x = sv.T; la.g = w.cn_g; la.b = w.cn_b;
+    la.mean = sv.cmean; la.rstd = sv.crstd; la.W = w.wo_frag;
+    KTimed kt(BC2N_TN(C, "trimul.ln_out"), st);
+    lnproj::launch_cm<true>(st, la, out);
+    return;
+  }
   {
     KTimed kt(BC2N_TN(C, "trimul.ln_center"), st);
     ln_fwd_cm(st, sv.T, M, I, w.cn_g, w.cn_b, tn, sv.cmean, sv.crstd, true);
   }
-  const EpiTrimulOut out(pair_in, pair_out, w.bo, sv.gout, sv.osave, tbl, N, C);
   if (w.wo_frag) {
     lnproj::Args la{};
     la.M = M; la.nout = C; la.xn = tn; la.W = w.wo_frag;
