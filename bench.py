@@ -113,6 +113,9 @@ def kernel_model(name, n):
         # statistics, then the output epilogue's traffic
         "trimul.ln_out": (gemm(c, c), m * (4 * c + 8 + 2 * c + 4 * c + 2 * c + 4 * c)),
         "trimul.gemm_dout": (gemm(c, c), m * (4 * c + 2 * c + 2 * c + 4 * c + 2 * c)),
+        # with the centre norm's backward in its epilogue: dout, g_out, o read,
+        # d(cat)'s gating columns written, T and the statistics read, dT written
+        "trimul.gemm_dout_ln": (gemm(c, c), m * (4 * c + 2 * c + 2 * c + 2 * c + 4 * c + 8 + 2 * c)),
         "trimul.gemm_dx": (gemm(5 * c, c), m * (10 * c + 4 * c)),
         # recompute GEMM + d(cat) + dX GEMM + LayerNorm backward: xn, d(left|right),
         # d(cat)'s gating columns, mask, x, dout read, din written, LN stats

@@ -206,6 +206,73 @@ struct ALoadTrimulOut {
   }
 };
 
+// The centre LayerNorm's backward fused into the d(tn) product as its
+// row-block epilogue (I = 128): each staged half tile of d(tn) rows is the dy
+// of ln_bwd_cm, normalised with the same arithmetic in the same order (eight
+// lanes a row, 16 consecutive channels each, the x values read from the
+// channel-major T), and written channel-major in binary16 through the tile,
+// so d(tn) never reaches memory.
+struct EpiCmLnBwd : EpiRows {
+  static constexpr bool kRowBlock = true;
+  static constexpr int C = 128, P = 8, CPL = C / P;
+  const float *x, *gamma, *mean, *rstd;  // x: channel-major [C][M]
+  h16* dx;                               // channel-major [C][M]
+  long M;
+  __device__ __forceinline__ void row(int, int, int, const float (&)[8]) const {}
+  template <int WM>
+  __device__ __forceinline__ void block(int, long mb, const float* T, int ldt, int tid) const {
+    static_assert(WM % (256 / P) == 0 && WM % 4 == 0, "rows a pass");
+    float* Tw = const_cast<float*>(T);  // the kernel's own staging tile
+#pragma unroll
+    for (int rb = 0; rb < WM; rb += 256 / P) {
+      const int r = rb + tid / P, part = tid % P;
+      const long m = mb + r;
+      const bool live = m < M;
+      const float mu = live ? mean[m] : 0.f, rs = live ? rstd[m] : 0.f;
+      float xv[CPL];
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) xv[e] = live ? x[(long)(part * CPL + e) * M + m] : 0.f;
+      float xh[CPL], g[CPL];
+      float sg = 0.f, sgx = 0.f;
+#pragma unroll
+      for (int e0 = 0; e0 < CPL; e0 += 4) {
+        float4 d = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (live) d = *reinterpret_cast<const float4*>(T + r * ldt + part * CPL + e0);
+        const float dv[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int e = e0 + k, c = part * CPL + e;
+          xh[e] = (xv[e] - mu) * rs;
+          g[e] = dv[k] * gamma[c];
+          sg += g[e];
+          sgx += g[e] * xh[e];
+        }
+      }
+      sg = group_sum<P>(sg) / C;
+      sgx = group_sum<P>(sgx) / C;
+      // each thread rewrites exactly the 16 values it read
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) {
+        const int c = part * CPL + e;
+        Tw[r * ldt + c] = rs * (g[e] - sg - xh[e] * sgx);
+      }
+    }
+    __syncthreads();
+    for (int i = tid; i < C * (WM / 4); i += 256) {
+      const int c = i / (WM / 4), q = (i % (WM / 4)) * 4;
+      const long mm = mb + q;
+      if (mm < M) {
+        h16x4 o;
+        o[0] = f2h_sat(T[(q + 0) * ldt + c]);
+        o[1] = f2h_sat(T[(q + 1) * ldt + c]);
+        o[2] = f2h_sat(T[(q + 2) * ldt + c]);
+        o[3] = f2h_sat(T[(q + 3) * ldt + c]);
+        *reinterpret_cast<h16x4*>(dx + (long)c * M + mm) = o;
+      }
+    }
+  }
+};
+
 // ---------------------------------------------------------------------------
 // The backward's tail in one kernel (C = I = 128):
 //
@@ -705,9 +772,15 @@ void trimul_bwd(hipStream_t st, const TriMulW& w, bool outgoing, int N, const fl
   // 64-row tiles: with N = K = 128 a 128-row grid leaves most workgroup
   // slots empty (392 workgroups at 224 tokens); the 128 x 128 B operand is
   // cheap to re-read
-  gemm<64, 128>(st, g1, EpiStore<float>{dtn, I, 0, nullptr, I}, BC2N_TN(C, "trimul.gemm_dout"),
-                ALoadTrimulOut{dout, tbl, sv.gout, sv.osave, dcat, C, ldcat, off, N, sc});
-  {
+  const ALoadTrimulOut aload{dout, tbl, sv.gout, sv.osave, dcat, C, ldcat, off, N, sc};
+  if (I == EpiCmLnBwd::C && M % 4 == 0) {
+    // the centre norm's backward in the epilogue: dT straight from d(tn)
+    EpiCmLnBwd ep;
+    ep.x = sv.T; ep.gamma = w.cn_g; ep.mean = sv.cmean; ep.rstd = sv.crstd; ep.dx = dT; ep.M = M;
+    gemm<64, 128>(st, g1, ep, BC2N_TN(C, "trimul.gemm_dout_ln"), aload);
+  } else {
+    gemm<64, 128>(st, g1, EpiStore<float>{dtn, I, 0, nullptr, I}, BC2N_TN(C, "trimul.gemm_dout"),
+                  aload);
     KTimed kt(BC2N_TN(C, "trimul.ln_center_bwd"), st);
     ln_bwd_cm(st, dtn, sv.T, M, I, w.cn_g, sv.cmean, sv.crstd, dT);
   }
