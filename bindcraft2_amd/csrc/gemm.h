@@ -29,6 +29,10 @@ namespace bc2n {
 
 struct GemmArgs {
   int M = 0, N = 0, K = 0, batch = 1;
+  // > 0 (the sliced launch): the accumulators fold into the result every
+  // kslice of K, in order, giving the bits of a split-K launch of kslice
+  // slices summed by gemm_splitk_epi, on a grid of the tiles alone
+  int kslice = 0;
   const h16* A = nullptr;
   long a_sm = 0, a_sk = 0, a_sb = 0;  // element strides; a_sm==1 or a_sk==1
   const h16* B = nullptr;
@@ -206,8 +210,10 @@ struct GemmSmem {
   static constexpr int BYTES = AB > T ? AB : T;
 };
 
-template <int BM, int BN, int BK, bool AK, bool BKC, class Epi, class AL = ALoadDirect>
+template <int BM, int BN, int BK, bool AK, bool BKC, class Epi, class AL = ALoadDirect,
+          bool SLICED = false>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi, AL al = AL{}) {
+  static_assert(!SLICED || BK == 32, "the sliced launch folds at 32-deep steps");
   using SM = GemmSmem<BM, BN, BK>;
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int TM = WM / 16, TN = WN / 16;
@@ -318,6 +324,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi, AL al = 
     for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int nk = g.K / BK;
+  f32x4 total[SLICED ? TM : 1][SLICED ? TN : 1];  // the slices' running sum
   constexpr int PRO = epi_pro_floats<Epi>::value;
   __shared__ float pro[PRO > 0 ? BM * PRO : 1];
   typename epi_preload<Epi>::type pl;
@@ -352,6 +359,21 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi, AL al = 
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = mfma16x16x32(af[i], bfr[j], acc[i][j]);
     }
+    if constexpr (SLICED) {
+      // a slice ends: its partial joins the running sum (the first one as
+      // it is, as gemm_splitk_epi starts from partial 0) and restarts at 0
+      const int spk = g.kslice / 32;
+      if ((kt + 1) % spk == 0) {
+        const bool first = kt + 1 == spk;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) {
+            total[i][j] = first ? acc[i][j] : total[i][j] + acc[i][j];
+            acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+          }
+      }
+    }
     if constexpr (SM::NBUF == 2) {
       if (kt + 1 < nk) sstore(buf ^ 1);
     } else if (kt + 1 < nk) {
@@ -359,6 +381,13 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi, AL al = 
       sstore(0);
     }
     __syncthreads();
+  }
+
+  if constexpr (SLICED) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = total[i][j];
   }
 
   // ---- epilogue: stage half a tile (the rows of one wave row) per pass
@@ -453,6 +482,22 @@ void gemm_launch(hipStream_t st, const GemmArgs& g, const Epi& epi, const AL& al
 #undef BC2N_GEMM_LAUNCH
 }
 
+// The sliced launch (g.kslice > 0, a multiple of 32 dividing K): 32-deep
+// steps, a grid of the tiles alone.
+template <int BM, int BN, class Epi, class AL>
+void gemm_launch_sliced(hipStream_t st, const GemmArgs& g, const Epi& epi, const AL& al) {
+  const bool ak = (g.a_sk == 1), bk = (g.b_sk == 1);
+  const int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
+  dim3 grid(xcd_grid((long)tiles * g.batch)), block(256);
+#define BC2N_GEMM_SLICED(AKV, BKCV) \
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, 32, AKV, BKCV, Epi, AL, true>), grid, block, 0, st, g, epi, al)
+  if (ak && bk) BC2N_GEMM_SLICED(true, true);
+  else if (ak) BC2N_GEMM_SLICED(true, false);
+  else if (bk) BC2N_GEMM_SLICED(false, true);
+  else BC2N_GEMM_SLICED(false, false);
+#undef BC2N_GEMM_SLICED
+}
+
 // Split K for a grid of a few tiles and a long K (the MSA track's S x N-row
 // products at S = 1: e.g. 224 x 256 over K = 1024 is 4 tiles of 128 x 128,
 // each a chain of 8 dependent K steps): the K slices run as the batch
@@ -544,6 +589,16 @@ void gemm(hipStream_t st, const GemmArgs& g, const Epi& epi, const char* name = 
       while (split > 1 && kb % split != 0) --split;
       if (split > 1) {
         const int kslice = g.K / split;
+        if (lane() != 0) {
+          // the side lane runs beside the pair track, the critical path: the
+          // same sums on a grid of the tiles alone (no extra workgroups, no
+          // partials through memory, no reduction launch) take less of the
+          // chip from it; the bits are those of the split launch
+          GemmArgs gk = g;
+          gk.kslice = kslice;
+          gemm_launch_sliced<BM, BN>(st, gk, epi, al);
+          return;
+        }
         GemmArgs gs = g;
         gs.K = kslice;
         gs.batch = split;
