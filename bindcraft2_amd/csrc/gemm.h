@@ -104,22 +104,6 @@ template <class E>
 struct epi_pro_floats<E, std::void_t<decltype(E::kProRowFloats)>>
     : std::integral_constant<int, E::kProRowFloats> {};
 
-// A row-block epilogue with a Preload type reads its own operands into
-// registers before the K loop (preload<BM>(m0, pl, tid), issued behind the
-// first operand tiles), and block() then takes (pl, pass) as its last
-// arguments: the epilogue's loads wait behind the products, not after them.
-struct NoPreload {};
-template <class E, class = void>
-struct epi_preload {
-  static constexpr bool value = false;
-  using type = NoPreload;
-};
-template <class E>
-struct epi_preload<E, std::void_t<typename E::Preload>> {
-  static constexpr bool value = true;
-  using type = typename E::Preload;
-};
-
 // Base of every epilogue: row mode only.
 struct EpiRows {
   static constexpr bool kHasCol = false;
@@ -210,9 +194,18 @@ struct GemmSmem {
   static constexpr int BYTES = AB > T ? AB : T;
 };
 
+// An epilogue may ask for a minimum occupancy (kMinWaves waves per SIMD: the
+// register budget the compiler then keeps to), e.g. to fit a grid in one round.
+template <class E, class = void>
+struct epi_min_waves : std::integral_constant<int, 1> {};
+template <class E>
+struct epi_min_waves<E, std::void_t<decltype(E::kMinWaves)>>
+    : std::integral_constant<int, E::kMinWaves> {};
+
 template <int BM, int BN, int BK, bool AK, bool BKC, class Epi, class AL = ALoadDirect,
           bool SLICED = false>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi, AL al = AL{}) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(epi_min_waves<Epi>::value)))
+void gemm_kernel(GemmArgs g, Epi epi, AL al = AL{}) {
   static_assert(!SLICED || BK == 32, "the sliced launch folds at 32-deep steps");
   using SM = GemmSmem<BM, BN, BK>;
   constexpr int WM = BM / 2, WN = BN / 2;
@@ -327,10 +320,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi, AL al = 
   f32x4 total[SLICED ? TM : 1][SLICED ? TN : 1];  // the slices' running sum
   constexpr int PRO = epi_pro_floats<Epi>::value;
   __shared__ float pro[PRO > 0 ? BM * PRO : 1];
-  typename epi_preload<Epi>::type pl;
   gload(0);
   if constexpr (PRO > 0) epi.template prologue<BM>(m0, pro, tid);
-  if constexpr (epi_preload<Epi>::value) epi.template preload<BM>(m0, pl, tid);
   sstore(0);
   __syncthreads();
   const int fr = lane & 15, fk = (lane >> 4) * 8;
@@ -420,7 +411,6 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, Epi epi, AL al = 
     };
     if constexpr (epi_row_block<Epi>::value) {
       if constexpr (PRO > 0) epi.template block<WM>(b, mb, T, LDT, tid, pro + (mb - m0) * PRO);
-      else if constexpr (epi_preload<Epi>::value) epi.template block<WM>(b, mb, T, LDT, tid, pl, pass);
       else epi.template block<WM>(b, mb, T, LDT, tid);
     } else if (colm) {
       for (int it = tid; it < BN * (WM / 8); it += 256) {

@@ -214,45 +214,27 @@ struct ALoadTrimulOut {
 // so d(tn) never reaches memory.
 struct EpiCmLnBwd : EpiRows {
   static constexpr bool kRowBlock = true;
+  // four waves a SIMD: the 64-row grid (784 workgroups at 224 tokens) in one
+  // round of 1024 slots (three would leave 16 workgroups for a second round)
+  static constexpr int kMinWaves = 4;
   static constexpr int C = 128, P = 8, CPL = C / P;
   const float *x, *gamma, *mean, *rstd;  // x: channel-major [C][M]
   h16* dx;                               // channel-major [C][M]
   long M;
-  // 64-row tiles: two 32-row passes, one row (of eight lanes) a thread each;
-  // its x values and statistics load before the GEMM's K loop
-  static constexpr int WMP = 256 / P;
-  struct Preload {
-    float xv[2][CPL], mu[2], rs[2];
-  };
-  template <int BM>
-  __device__ __forceinline__ void preload(long m0, Preload& pl, int tid) const {
-    static_assert(BM == 2 * WMP, "64-row tiles");
-    const int part = tid % P;
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const long m = m0 + p * WMP + tid / P;
-      const bool live = m < M;
-#pragma unroll
-      for (int e = 0; e < CPL; ++e) pl.xv[p][e] = live ? x[(long)(part * CPL + e) * M + m] : 0.f;
-      pl.mu[p] = live ? mean[m] : 0.f;
-      pl.rs[p] = live ? rstd[m] : 0.f;
-    }
-  }
+  static constexpr int WMP = 256 / P;  // rows a pass: one (of eight lanes) a thread
   __device__ __forceinline__ void row(int, int, int, const float (&)[8]) const {}
   template <int WM>
-  __device__ __forceinline__ void block(int, long mb, const float* T, int ldt, int tid,
-                                        const Preload& pl, int pass) const {
+  __device__ __forceinline__ void block(int, long mb, const float* T, int ldt, int tid) const {
     static_assert(WM == WMP, "one 32-row pass a call");
     float* Tw = const_cast<float*>(T);  // the kernel's own staging tile
     {
       const int r = tid / P, part = tid % P;
       const long m = mb + r;
       const bool live = m < M;
-      // selects, not an index: a runtime index would put pl in scratch memory
-      const float mu = pass ? pl.mu[1] : pl.mu[0], rs = pass ? pl.rs[1] : pl.rs[0];
+      const float mu = live ? mean[m] : 0.f, rs = live ? rstd[m] : 0.f;
       float xv[CPL];
 #pragma unroll
-      for (int e = 0; e < CPL; ++e) xv[e] = pass ? pl.xv[1][e] : pl.xv[0][e];
+      for (int e = 0; e < CPL; ++e) xv[e] = live ? x[(long)(part * CPL + e) * M + m] : 0.f;
       float xh[CPL], g[CPL];
       float sg = 0.f, sgx = 0.f;
 #pragma unroll
